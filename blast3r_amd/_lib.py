@@ -1,0 +1,133 @@
+"""ctypes binding of libba_hip.so (declarations in include/ba_hip.h).
+
+The library is loaded lazily on first use and never replaced by a Python or
+CPU implementation: if it is missing the call raises RuntimeError, exactly like
+the reference's stub module does when its extension is not compiled
+(src/blast3r/extensions/cujac/__init__.py:7-16).
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, 'libba_hip.so')
+
+_lib = None
+_lock = threading.Lock()
+
+c_int = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_f = ctypes.c_float
+c_d = ctypes.c_double
+c_p = ctypes.c_void_p
+
+
+class BaHuber(ctypes.Structure):
+    _fields_ = [('weight_z', c_f), ('pnorm', c_f), ('max_pix_err', c_f), ('huber_delta', c_f),
+                ('w_pts_null', c_f), ('is_depth_log', c_int)]
+
+
+class BaLayout(ctypes.Structure):
+    _fields_ = [('d', c_int), ('C', c_int), ('off_tau', c_int), ('off_zcf', c_int), ('hasK', c_int), ('hasP', c_int),
+                ('hasZ', c_int), ('no_grad_f_from_rz', c_int), ('optim_Z0', c_int), ('optim_Z_1st_cam', c_int),
+                ('wmin', c_f), ('wmax', c_f), ('dampen', c_d), ('adaptive', c_int), ('x_off', c_int)]
+
+
+_LIN_FIELDS = [
+    ('infos', c_p), ('n_imgs', c_int),
+    ('chunk_obs', c_p), ('chunk_meta', c_p), ('slot_info', c_p),
+    ('ct_pid', c_p), ('ct_first', c_p), ('ct_m', c_p), ('ct_mask', c_p),
+    ('b_chunk_ptr', c_p), ('b_imgs', c_p), ('b_nimgs', c_p), ('b_slot_ptr', c_p), ('slot_pair', c_p),
+    ('L', c_int),
+    ('s_pix', c_p), ('s_std', c_p), ('s_dep', c_p), ('s_pid', c_p), ('s_img', c_p),
+    ('K', c_p), ('P_rig2cam', c_p), ('P_rig2cam_stride', c_i64), ('P_w2rig', c_p), ('z_coefs', c_p), ('pts3d', c_p),
+    ('enK', c_p), ('enP', c_p), ('enZ', c_p), ('enX', c_p),
+    ('hp', BaHuber), ('lay', BaLayout),
+    ('Hpp', c_p), ('gp', c_p), ('chunk_max', c_p), ('lam_p', c_p),
+    ('partials', c_p), ('img_partials', c_p),
+    ('dc', c_p), ('umap', c_p), ('dX', c_p), ('dX64', c_p),
+    ('n_chunks', c_i64), ('n_batches', c_i64), ('n_pairs', c_i64),
+    ('pair_ptr', c_p), ('pair_src', c_p), ('img_ptr', c_p), ('img_src', c_p),
+    ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p),
+    ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
+]
+
+
+class BaLinArgs(ctypes.Structure):
+    _fields_ = _LIN_FIELDS
+
+
+class BaPcgArgs(ctypes.Structure):
+    _fields_ = [('n_u', c_i64), ('n_imgs', c_int), ('d', c_int), ('umap', c_p), ('inv_ptr', c_p), ('inv_src', c_p),
+                ('leaf', c_p), ('row_ptr', c_p), ('row_ent', c_p), ('pair_i1', c_p), ('pair_i2', c_p),
+                ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dampen', c_d), ('adaptive', c_int),
+                ('maxiter', c_int), ('tol', c_d),
+                ('rhs', c_p), ('diagA', c_p), ('damp', c_p), ('x', c_p), ('xbest', c_p), ('r', c_p), ('z', c_p),
+                ('p', c_p), ('Ap', c_p), ('y_img', c_p), ('partials', c_p), ('state', c_p), ('istate', c_p)]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    'ba_last_error': (ctypes.c_char_p, []),
+    'ba_version': (c_int, []),
+    'ba_residuals': (c_int, [c_p, c_int, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int,
+                             c_f, c_f, c_f, c_f, c_f, c_p, c_p]),
+    'ba_jacobians': (c_int, [c_p, c_int, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_int,
+                             c_p, c_p, c_p, c_p]),
+    'ba_chol3x3_solve': (c_int, [c_p, c_p, c_p, c_i64, c_d, c_int, c_p]),
+    'ba_blockcoo_matvec': (c_int, [c_p, c_int, c_int, c_p, c_p, c_int, c_i64, c_p, c_p, c_i64, c_i64, c_int, c_int,
+                                   c_p]),
+    'ba_einsum_bki_bkj': (c_int, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_int, c_int, c_int, c_int, c_p]),
+    'ba_exp_se3': (c_int, [c_p, c_p, c_i64, c_p]),
+    'ba_plan_create': (c_p, [c_p, c_int, c_p, c_i64, c_int, c_int, c_int, c_i64]),
+    'ba_plan_query': (c_int, [c_p, c_p, c_p]),
+    'ba_plan_export': (c_int, [c_p, c_int, c_p]),
+    'ba_plan_destroy': (None, [c_p]),
+    'ba_plan_last_error': (ctypes.c_char_p, []),
+    'ba_linearize_schur': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
+    'ba_backsubstitute': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
+    'ba_pcg_solve': (c_int, [ctypes.POINTER(BaPcgArgs), c_p]),
+    'ba_pcg_partials_size': (c_i64, [c_i64]),
+    'ba_apply_update': (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_f, c_f, c_int, c_int, c_int, c_int, c_i64,
+                                c_p, c_p, c_p, c_p, c_p]),
+    'ba_objective_workspace_bytes': (c_i64, [c_i64]),
+    'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib():
+    """The loaded library (raises RuntimeError when it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f'libba_hip.so is not built ({LIB_PATH}); run `python -m blast3r_amd.build` '
+                                   'or __graft_entry__.build()')
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGS.items():
+                f = getattr(L, name)
+                f.restype = res
+                f.argtypes = args
+            _lib = L
+    return _lib
+
+
+def check(status):
+    if status != 0:
+        msg = lib().ba_last_error()
+        raise RuntimeError((msg or b'libba_hip error').decode())
+
+
+def stream_ptr(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    """Raw device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())

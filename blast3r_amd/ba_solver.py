@@ -1,0 +1,364 @@
+"""MI355X ``GaussNewtonSolver``: drop-in for src/blast3r/inference/ba_solver.py:20-248 (``bs``).
+
+Same constructor, same ``compute_jacobians`` / ``solve_delta`` /
+``unpack_delta_inplace`` signatures, same unknown order
+[foc (n_cams x 2) | tau (n_nodes x 6) | zcf (n_imgs x C) | pts (n_tracks x 3)]
+(bs:119, bs:229), same fp32 delta (bs:182).  What changes is how the step is
+computed: ``compute_jacobians`` returns a light handle instead of materialised
+fp64 Jacobian blocks, and ``solve_delta`` runs the fused HIP path
+
+    ba_linearize_schur   J, J^T W r, H_pp, camera-pair blocks of S, rhs (fp64, on chip)
+    ba_pcg_solve         the reference's Jacobi-PCG (bs:184-206, :1197-1238) on the explicit S
+    ba_backsubstitute    delta_p = H_pp^-1 (g_p - H_pc delta_c)
+
+with no host synchronisation between them.
+"""
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
+from .plan import get_plan
+
+N_FOC = 2   # focal columns (bs:11)
+N_TAU = 6   # pose columns (bs:12)
+
+
+class Param:
+    """bs:15-18."""
+    def __init__(self, n):
+        self.n = self.true_n = n
+        self.true_idxs = None
+
+
+class Linearization:
+    """What ``compute_jacobians`` hands to ``solve_delta``: the inputs of the fused kernels.
+
+    ``shape`` is the shape the reference's J would have (bs:119), so callers that
+    assert on it keep working.
+    """
+    def __init__(self, solver, **kw):
+        self.__dict__.update(kw)
+        self.solver = solver
+
+    @property
+    def shape(self):
+        s = self.solver
+        return (3 * s.n_kpts, s.cams.n * N_FOC + s.nodes.n * N_TAU + s.imgs.n * s.n_zcf + s.tracks.n * 3)
+
+
+def _flag(status, name, count):
+    """Normalise an optim_* flag: returns (enabled_group, uint8 mask or None, kept indices or None)."""
+    if status is True:
+        return True, None, None
+    if status is False:
+        return False, None, None
+    if isinstance(status, torch.Tensor):
+        if status.dtype != torch.bool or status.shape != (count,):
+            raise ValueError(f'bad {name}={status}')
+        idxs = status.nonzero().squeeze(-1)
+        if len(idxs) == 0:
+            return False, None, None     # all columns removed -> zero matrix (bs:91-92)
+        return True, status.to(torch.uint8).contiguous(), idxs
+    raise ValueError(f'bad {name}={status}')
+
+
+class GaussNewtonSolver:
+    """Bundle-adjustment Gauss-Newton step on MI355X (bs:20-248)."""
+
+    def __init__(self, n_cams, n_nodes, n_imgs, n_tracks, device, no_grad_f_from_rz=False, dampen=1e-12,
+                 adaptive_dampen=True, dtype=torch.float32, solver='pcg', pcg_tol=1e-6, pcg_maxiter=300,
+                 plan_options=None):
+        self.cams = Param(n_cams)
+        self.nodes = Param(n_nodes)
+        self.imgs = Param(n_imgs)
+        self.tracks = Param(n_tracks)
+        self.device = torch.device(device)
+        # the fused path always linearises and reduces in fp64 (the reference's solver dtype,
+        # engine.py:490); `dtype` is accepted for signature compatibility.
+        self.dtype = dtype
+        self.dampen = dampen
+        self.adaptive_dampen = adaptive_dampen
+        self.no_grad_f_from_rz = no_grad_f_from_rz
+        if solver != 'pcg':
+            raise ValueError(f'unknown reduced solver {solver!r} (supported: "pcg")')
+        self.solver = solver
+        self.pcg_tol = pcg_tol
+        self.pcg_maxiter = pcg_maxiter
+        self.plan_options = dict(plan_options or {})
+        self.last = {}
+
+    # ------------------------------------------------------------------ bs:34-40
+    def compute_jacobians(self, rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d_std, pix2d_dep, is_depth_log,
+                          optim_Z_1st_cam=True, optim_Z0=True, optim_K=True, optim_Z=True, optim_P=True, optim_X=True,
+                          pix2d=None, hp=None):
+        assert rigs.shape == (3, self.imgs.n)
+        self.n_kpts = int(pids.shape[0])
+        self.n_zcf = int(z_coefs.shape[1])
+        assert pix2d_dep.shape == (self.n_kpts, self.n_zcf)
+        en = {}
+        en['K'] = _flag(optim_K, 'optim_K', self.cams.n)
+        en['P'] = _flag(optim_P, 'optim_P', self.nodes.n)
+        en['Z'] = _flag(optim_Z, 'optim_Z', self.imgs.n)
+        en['X'] = _flag(optim_X, 'optim_X', self.tracks.n)
+        for key, par in (('K', self.cams), ('P', self.nodes), ('Z', self.imgs), ('X', self.tracks)):
+            if en[key][2] is not None:              # column compaction (bs:86-104)
+                par.n = len(en[key][2])
+                par.true_idxs = en[key][2]
+        return Linearization(self, rigs=rigs, K=K, P_rig2cam=P_rig2cam, P_w2rig=P_w2rig, z_coefs=z_coefs,
+                             pts3d=pts3d, pids=pids, pix2d_std=pix2d_std, pix2d_dep=pix2d_dep, pix2d=pix2d,
+                             is_depth_log=bool(is_depth_log), optim_Z_1st_cam=bool(optim_Z_1st_cam),
+                             optim_Z0=bool(optim_Z0), en=en, hp=hp)
+
+    # ------------------------------------------------------------------ unknown maps
+    def _unknown_maps(self, J, lay, plan):
+        """Image-level parameter -> unknown index (-1 inactive), its inverse CSR and leaf ids.
+
+        Unknowns follow the reference order [foc | tau | zcf] over the compacted
+        entities; groups whose optim flag is False keep their (decoupled) unknowns,
+        like the reference's ZerosMat leaves (bs:510-517).
+        """
+        d, C = lay['d'], self.n_zcf
+        n_imgs = self.imgs.true_n
+        cam_ids, node_ids = plan.cam_ids, plan.node_ids
+
+        def compact(key, par):
+            m = np.arange(par.true_n)
+            if J.en[key][2] is not None:
+                keep = np.full(par.true_n, -1, dtype=np.int64)
+                idx = J.en[key][2].cpu().numpy()
+                keep[idx] = np.arange(len(idx))
+                m = keep
+            return m
+
+        cam_map, node_map, img_map = compact('K', self.cams), compact('P', self.nodes), compact('Z', self.imgs)
+        nf, nt, nz = self.cams.n * N_FOC, self.nodes.n * N_TAU, self.imgs.n * C
+        umap = np.full((n_imgs, max(d, 1)), -1, dtype=np.int64)
+        col = 0
+        if lay['hasK']:
+            c = cam_map[cam_ids]
+            for k in range(2):
+                umap[:, col + k] = np.where(c >= 0, c * 2 + k, -1)
+            col += 2
+        if lay['hasP']:
+            n = node_map[node_ids]
+            for k in range(6):
+                umap[:, col + k] = np.where(n >= 0, nf + n * 6 + k, -1)
+            col += 6
+        if lay['hasZ']:
+            im = img_map[np.arange(n_imgs)]
+            for k in range(C):
+                umap[:, col + k] = np.where(im >= 0, nf + nt + im * C + k, -1)
+            col += C
+        n_u = nf + nt + nz
+        flat = umap.reshape(-1)
+        valid = np.nonzero(flat >= 0)[0]
+        order = np.argsort(flat[valid], kind='stable')
+        src = valid[order]
+        counts = np.bincount(flat[valid], minlength=n_u) if n_u else np.zeros(0, np.int64)
+        inv_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        leaf = np.zeros(n_u, dtype=np.int32)
+        leaf[nf:nf + nt] = 1
+        leaf[nf + nt:] = 2
+        # a group switched off entirely is a zero leaf damped by dampen * I (non-adaptive)
+        if not lay['hasK']:
+            leaf[:nf] += 3
+        if not lay['hasP']:
+            leaf[nf:nf + nt] += 3
+        if not lay['hasZ']:
+            leaf[nf + nt:] += 3
+        dev = self.device
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        return dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
+                    leaf=t(leaf if n_u else np.zeros(1)))
+
+    # ------------------------------------------------------------------ bs:110-182
+    def solve_delta(self, J, residuals, w_pts, clamp_w=(1e-6, 1e6), z_prior=None):
+        """Solve (J^T W J + damping) delta = J^T W r by Schur reduction; returns fp32 delta."""
+        assert isinstance(J, Linearization)
+        assert J.shape == (3 * self.n_kpts, self.cams.n * N_FOC + self.nodes.n * N_TAU + self.imgs.n * self.n_zcf +
+                           self.tracks.n * 3)
+        assert residuals.shape == (self.n_kpts, 3)
+        assert w_pts.shape in ((self.n_kpts, 1), (self.n_kpts, 3))
+        dev = self.device
+        C = self.n_zcf
+        en = J.en
+        hasK, hasP, hasZ = en['K'][0], en['P'][0], en['Z'][0]
+        d = 2 * hasK + 6 * hasP + C * hasZ
+        lay = dict(d=d, hasK=hasK, hasP=hasP, hasZ=hasZ)
+        plan = get_plan(J.rigs, J.pids, self.tracks.true_n, device=dev, **self.plan_options)
+        sc = plan.scalars
+        T = self.tracks.true_n
+        s_pix, s_std, s_dep = plan.slot_data(J.pix2d if J.pix2d is not None else J.pix2d_std, J.pix2d_std,
+                                             J.pix2d_dep)
+        ws = plan.workspace
+        n_imgs = self.imgs.true_n
+        Hpp = ws('Hpp', (max(T, 1), 6), torch.float64)
+        gp = ws('gp', (max(T, 1), 3), torch.float64)
+        chunk_max = ws('chunk_max', (max(sc['n_chunks'], 1),), torch.float64)
+        lam_p = ws('lam_p', (1,), torch.float64)
+        dd = max(d, 1)
+        partials = ws('partials', (max(sc['n_slots'], 1), dd, dd), torch.float64)
+        img_partials = ws('img_partials', (max(sc['n_batches'], 1), plan.L, 2, dd), torch.float64)
+        S_pairs = torch.empty((max(sc['n_pairs'], 1), dd, dd), dtype=torch.float64, device=dev)
+        e_img = torch.empty((n_imgs, dd), dtype=torch.float64, device=dev)
+        dg_img = torch.empty((n_imgs, dd), dtype=torch.float64, device=dev)
+
+        a = BaLinArgs()
+        pd = plan.dev
+        a.infos = ptr(J.rigs.contiguous())
+        a.n_imgs = n_imgs
+        for name in ('chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr',
+                     'b_imgs', 'b_nimgs', 'b_slot_ptr', 'slot_pair', 'pair_ptr', 'pair_src', 'img_ptr', 'img_src'):
+            setattr(a, name, ptr(pd[name]))
+        a.L = plan.L
+        a.s_pix, a.s_std, a.s_dep = ptr(s_pix), ptr(s_std), ptr(s_dep)
+        a.s_pid, a.s_img = ptr(pd['s_pid']), ptr(pd['s_img'])
+        a.K, a.P_rig2cam, a.P_rig2cam_stride = ptr(J.K), ptr(J.P_rig2cam), J.P_rig2cam.stride(0)
+        a.P_w2rig, a.z_coefs, a.pts3d = ptr(J.P_w2rig), ptr(J.z_coefs), ptr(J.pts3d)
+        a.enK, a.enP, a.enZ, a.enX = (ptr(en[k][1]) for k in ('K', 'P', 'Z', 'X'))
+        hp = J.hp or {}
+        a.hp.weight_z = float(hp.get('weight_z', 1.0))
+        a.hp.pnorm = float(hp.get('pnorm', 1.0))
+        a.hp.max_pix_err = float(hp.get('max_pix_err', 100.0))
+        a.hp.huber_delta = float(hp.get('huber_delta', 0.5))
+        a.hp.w_pts_null = float(hp.get('w_pts_null', 1e-16))
+        a.hp.is_depth_log = int(J.is_depth_log)
+        L_ = a.lay
+        L_.d, L_.C = d, C
+        L_.off_tau, L_.off_zcf = 2 * hasK, 2 * hasK + 6 * hasP
+        L_.hasK, L_.hasP, L_.hasZ = int(hasK), int(hasP), int(hasZ)
+        L_.no_grad_f_from_rz = int(bool(self.no_grad_f_from_rz))
+        L_.optim_Z0, L_.optim_Z_1st_cam = int(J.optim_Z0), int(J.optim_Z_1st_cam)
+        L_.wmin, L_.wmax = float(clamp_w[0]), float(clamp_w[1])
+        L_.dampen = float(self.dampen)
+        L_.adaptive = int(bool(self.adaptive_dampen))
+        L_.x_off = int(not en['X'][0])
+        a.Hpp, a.gp, a.chunk_max, a.lam_p = ptr(Hpp), ptr(gp), ptr(chunk_max), ptr(lam_p)
+        a.partials, a.img_partials = ptr(partials), ptr(img_partials)
+        a.n_chunks, a.n_batches, a.n_pairs = sc['n_chunks'], sc['n_batches'], sc['n_pairs']
+        a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
+        # residuals / weights: recompute in-kernel when they are this step's own objective output,
+        # otherwise read the caller's tensors (bs:123-128 semantics)
+        W = w_pts.expand(-1, 3)
+        own = getattr(residuals, '_ba_state', None)
+        if own is None or own != _param_state(J) or J.pix2d is None:
+            a.r_in, a.w_in = ptr(residuals), ptr(W)
+            a.r_s0, a.r_s1 = residuals.stride(0), residuals.stride(1)
+            a.w_s0, a.w_s1 = W.stride(0), W.stride(1)
+        st = stream_ptr(dev)
+        if d > 0:
+            check(lib().ba_linearize_schur(a, st))
+        else:
+            S_pairs.zero_(); e_img.zero_(); dg_img.zero_()
+        if z_prior is not None:
+            self._add_z_prior(z_prior, lay, plan, S_pairs, e_img, dg_img)
+
+        # reduced solve
+        um = self._unknown_maps(J, lay, plan)
+        n_u = um['n_u']
+        x = torch.zeros(max(n_u, 1), dtype=torch.float64, device=dev)
+        istate = torch.zeros(8, dtype=torch.int32, device=dev)
+        if n_u > 0 and d > 0:
+            pa = BaPcgArgs()
+            pa.n_u, pa.n_imgs, pa.d = n_u, n_imgs, d
+            pa.umap, pa.inv_ptr, pa.inv_src, pa.leaf = ptr(um['umap']), ptr(um['inv_ptr']), ptr(um['inv_src']), ptr(
+                um['leaf'])
+            pa.row_ptr, pa.row_ent = ptr(pd['row_ptr']), ptr(pd['row_ent'])
+            pa.pair_i1, pa.pair_i2 = ptr(pd['pair_i1']), ptr(pd['pair_i2'])
+            pa.S_pairs, pa.e_img, pa.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
+            pa.dampen, pa.adaptive = float(self.dampen), int(bool(self.adaptive_dampen))
+            pa.maxiter, pa.tol = int(self.pcg_maxiter), float(self.pcg_tol)
+            vec = lambda name: ws('pcg_' + name, (n_u,), torch.float64)
+            rhs, diagA, damp = vec('rhs'), vec('diagA'), vec('damp')
+            xbest, r, z, p, Ap = vec('xbest'), vec('r'), vec('z'), vec('p'), vec('Ap')
+            y_img = ws('pcg_y', (n_imgs * d,), torch.float64)
+            part = ws('pcg_part', (int(lib().ba_pcg_partials_size(n_u)),), torch.float64)
+            state = ws('pcg_state', (16,), torch.float64)
+            pa.rhs, pa.diagA, pa.damp, pa.x, pa.xbest = ptr(rhs), ptr(diagA), ptr(damp), ptr(x), ptr(xbest)
+            pa.r, pa.z, pa.p, pa.Ap, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(Ap), ptr(y_img)
+            pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
+            check(lib().ba_pcg_solve(pa, st))
+            self.last.update(rhs=rhs, diagA=diagA, damp=damp)
+        # back-substitution for the points
+        dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
+        if en['X'][0] and sc['n_chunks'] > 0:
+            a.dc = ptr(x)
+            a.umap = ptr(um['umap'])
+            a.dX = ptr(dX)
+            a.dX64 = None
+            check(lib().ba_backsubstitute(a, st))
+        self.last.update(S_pairs=S_pairs, e_img=e_img, dg_img=dg_img, unknowns=um, lay=lay, plan=plan, x=x,
+                         istate=istate, Hpp=Hpp, gp=gp, lam_p=lam_p)
+        dc = x[:n_u].to(torch.float32)
+        dXa = dX[:T]
+        if en['X'][2] is not None:
+            dXa = dXa[en['X'][2]]
+        return torch.cat([dc, dXa.reshape(-1)])
+
+    def _add_z_prior(self, z_prior, lay, plan, S_pairs, e_img, dg_img):
+        """Tangent-prior terms on the z-coefficient blocks before damping (bs:141-173)."""
+        H_z, g_z = z_prior
+        if H_z is None or g_z is None:
+            return
+        if not lay['hasZ']:
+            raise TypeError('Unsupported JTJ.A type for z_prior: z-coefficients are not optimised')
+        C = self.n_zcf
+        o = lay['d'] - C
+        H_z = H_z.to(torch.float64)
+        g_z = g_z.to(torch.float64)
+        assert g_z.shape == (self.imgs.n, C) and H_z.shape == (self.imgs.n, C, C)
+        diag_pairs = plan.dev['pair_i1'] == plan.dev['pair_i2']
+        pid = torch.nonzero(diag_pairs).squeeze(-1)
+        img = plan.dev['pair_i1'][pid].long()
+        S_pairs[pid, o:, o:] += H_z[img]
+        e_img[:, o:] += g_z
+        dg_img[:, o:] += H_z.diagonal(dim1=-1, dim2=-2)
+
+    # ------------------------------------------------------------------ bs:228-248
+    def unpack_delta_inplace(self, delta):
+        sizes = [self.cams.n * N_FOC, self.nodes.n * N_TAU, self.imgs.n * self.n_zcf, self.tracks.n * 3]
+        cum_sizes = torch.tensor(sizes, dtype=torch.int).cumsum(dim=0)
+        assert delta.shape == (cum_sizes[-1],)
+        dK, dP, dZ, dX = delta.tensor_split(cum_sizes[:-1])
+
+        def expand(deriv, param, np_):
+            deriv = deriv.view(param.n, np_)
+            if param.true_idxs is not None:
+                deriv2 = deriv.new_zeros((param.true_n, np_))
+                deriv2[param.true_idxs] = deriv
+                return deriv2
+            return deriv
+
+        return (expand(dK, self.cams, N_FOC), expand(dP, self.nodes, N_TAU), expand(dZ, self.imgs, self.n_zcf),
+                expand(dX, self.tracks, 3))
+
+    # ------------------------------------------------------------------ inspection helpers
+    def reduced_system_dense(self):
+        """Dense S (reference unknown order, damped) and rhs of the last solve_delta (for tests)."""
+        last = self.last
+        um, lay, plan = last['unknowns'], last['lay'], last['plan']
+        n_u, d = um['n_u'], lay['d']
+        S_img_pairs = last['S_pairs']
+        umap = um['umap'].long()
+        S = torch.zeros((n_u, n_u), dtype=torch.float64, device=self.device)
+        i1 = plan.dev['pair_i1'].long()[:plan.scalars['n_pairs']]
+        i2 = plan.dev['pair_i2'].long()[:plan.scalars['n_pairs']]
+        for p in range(len(i1)):
+            r = umap[i1[p]]
+            c = umap[i2[p]]
+            blk = S_img_pairs[p]
+            mr, mc = r >= 0, c >= 0
+            sub = blk[mr][:, mc]
+            S.index_put_((r[mr][:, None].expand(-1, int(mc.sum())), c[mc][None, :].expand(int(mr.sum()), -1)), sub,
+                         accumulate=True)
+            if i1[p] != i2[p]:
+                S.index_put_((c[mc][:, None].expand(-1, int(mr.sum())), r[mr][None, :].expand(int(mc.sum()), -1)),
+                             sub.T, accumulate=True)
+        S += torch.diag(last['damp'])
+        return S, last['rhs']
+
+
+def _param_state(J):
+    """Identity of the parameter tensors a residual evaluation was computed from."""
+    return tuple((t.data_ptr(), t._version) for t in (J.K, J.P_w2rig, J.z_coefs, J.pts3d, J.pix2d_dep, J.pids))

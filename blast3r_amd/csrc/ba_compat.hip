@@ -1,0 +1,326 @@
+// Operator-level entry points with the semantics of the reference cujac module
+// (src/blast3r/extensions/cujac/sfm_jacobian_rigs.cu, ".cu" below; Python
+// aliases in src/blast3r/extensions/cujac/__init__.py:18-22, :56-58).
+// These let the reference's own solver run on MI355X unchanged; the fused
+// linearize + Schur path lives in ba_schur.hip.
+#include <hip/hip_runtime.h>
+#include <cmath>
+#include <string>
+
+#include "ba_common.h"
+#include "ba_error.h"
+
+namespace ba {
+static thread_local std::string g_err;
+void set_error(const std::string& msg) { g_err = msg; }
+void clear_error() { g_err.clear(); }
+}  // namespace ba
+
+using namespace ba;
+
+extern "C" const char* ba_last_error(void) { return ba::g_err.c_str(); }
+extern "C" int ba_version(void) { return 1; }
+
+static inline hipStream_t S(void* s) { return (hipStream_t)s; }
+static inline unsigned nblk(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// ----------------------------------------------------------------------------- residuals
+__global__ void __launch_bounds__(256) k_residuals(const int* __restrict__ infos, int n_imgs, const float* __restrict__ K,
+                                                   const float* __restrict__ Prc, int64_t prc_stride,
+                                                   const float* __restrict__ Pwr, const float* __restrict__ zc,
+                                                   const float* __restrict__ pts, const int* __restrict__ pids,
+                                                   const float* __restrict__ pix, const float* __restrict__ sd,
+                                                   const float* __restrict__ dep, int64_t n_obs, int C, HuberParams hp,
+                                                   float* __restrict__ out) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_obs) return;
+    int img = obs_image(infos, n_imgs, (int)idx);
+    int node = infos[n_imgs + img];
+    int cam = infos[2 * n_imgs + img];
+    int pid = pids[idx];
+    CamF cp;
+    load_cam(cp, K, Prc, prc_stride, Pwr, cam, node);
+    float X[3] = {pts[3 * (int64_t)pid], pts[3 * (int64_t)pid + 1], pts[3 * (int64_t)pid + 2]};
+    float g = 0.f;
+    for (int c = 0; c < C; ++c) g += zc[(int64_t)img * C + c] * dep[idx * C + c];
+    float2 uv = reinterpret_cast<const float2*>(pix)[idx];
+    float2 sv = reinterpret_cast<const float2*>(sd)[idx];
+    ResOut o;
+    eval_residual(cp, X, uv.x, uv.y, sv.x, sv.y, g, hp, o);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) out[i * n_obs + idx] = o.r[i];
+    if (hp.pnorm > 0.f) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            out[(3 + i) * n_obs + idx] = o.err[i];
+            out[(6 + i) * n_obs + idx] = o.w[i];
+        }
+    }
+}
+
+// Replaces residuals_with_rigs (.cu:1048-1101).  out is (n_out, n_obs) fp32, n_out = 9 if
+// pnorm > 0 else 3; every element is written (rows with z <= 1e-3 get zeros, .cu:212).
+extern "C" int ba_residuals(const int32_t* infos, int32_t n_imgs, const float* K, const float* P_rig2cam,
+                            int64_t P_rig2cam_stride, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                            const int32_t* pids, const float* pix2d, const float* pix2d_std, const float* pix2d_dep,
+                            int64_t n_obs, int32_t C, int32_t is_depth_log, float weight_z, float pnorm,
+                            float max_pix_err, float huber_delta, float w_pts_null, float* out, void* stream) {
+    clear_error();
+    BA_REQUIRE(pnorm == -1.f || (pnorm > 0.f && pnorm <= 2.f), "pnorm must be in {-1} U ]0,2]");
+    BA_REQUIRE(n_imgs > 0 && C >= 0 && n_obs >= 0, "bad sizes");
+    if (n_obs == 0) return BA_OK;
+    HuberParams hp{weight_z, pnorm, max_pix_err, huber_delta, w_pts_null, is_depth_log};
+    hipLaunchKernelGGL(k_residuals, dim3(nblk(n_obs, 256)), dim3(256), 0, S(stream), infos, n_imgs, K, P_rig2cam,
+                       P_rig2cam_stride, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std, pix2d_dep, n_obs, C, hp, out);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// ----------------------------------------------------------------------------- jacobians
+template <typename T>
+__global__ void __launch_bounds__(256) k_jacobians(const int* __restrict__ infos, int n_imgs, const float* __restrict__ K,
+                                                   const float* __restrict__ Prc, int64_t prc_stride,
+                                                   const float* __restrict__ Pwr, const float* __restrict__ zc,
+                                                   const float* __restrict__ pts, const int* __restrict__ pids,
+                                                   const float* __restrict__ sd, const float* __restrict__ dep,
+                                                   int64_t n_obs, int C, int is_depth_log, T* __restrict__ Jcam,
+                                                   T* __restrict__ Jz, T* __restrict__ Jp) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_obs) return;
+    int img = obs_image(infos, n_imgs, (int)idx);
+    int node = infos[n_imgs + img];
+    int cam = infos[2 * n_imgs + img];
+    int pid = pids[idx];
+    CamF cp;
+    load_cam(cp, K, Prc, prc_stride, Pwr, cam, node);
+    float X[3] = {pts[3 * (int64_t)pid], pts[3 * (int64_t)pid + 1], pts[3 * (int64_t)pid + 2]};
+    double g = 0.0;   // Tfloat guidance (.cu:466-468): float products accumulated in double
+    for (int c = 0; c < C; ++c) {
+        float pr = zc[(int64_t)img * C + c] * dep[idx * C + c];
+        g += (double)pr;
+    }
+    float2 sv = reinterpret_cast<const float2*>(sd)[idx];
+    JacOut J;
+    eval_jacobian(cp, X, sv.x, sv.y, g, is_depth_log, J);
+#pragma unroll
+    for (int k = 0; k < 24; ++k) Jcam[idx * 24 + k] = (T)J.Jcam[k];
+    for (int c = 0; c < C; ++c) Jz[idx * C + c] = J.valid ? (T)(J.zscale * (double)dep[idx * C + c]) : (T)0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) Jp[idx * 9 + k] = (T)J.Jp[k];
+}
+
+// Replaces jacobians_with_rigs (.cu:1105-1148): J_cam (N,3,8), J_zcf (N,1,C), J_pts (N,3,3),
+// fp64 when float64 != 0 else fp32; every element is written.
+extern "C" int ba_jacobians(const int32_t* infos, int32_t n_imgs, const float* K, const float* P_rig2cam,
+                            int64_t P_rig2cam_stride, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                            const int32_t* pids, const float* pix2d_std, const float* pix2d_dep, int64_t n_obs,
+                            int32_t C, int32_t is_depth_log, int32_t float64, void* J_cam, void* J_zcf, void* J_pts,
+                            void* stream) {
+    clear_error();
+    BA_REQUIRE(n_imgs > 0 && C >= 0 && n_obs >= 0, "bad sizes");
+    if (n_obs == 0) return BA_OK;
+    if (float64)
+        hipLaunchKernelGGL(k_jacobians<double>, dim3(nblk(n_obs, 256)), dim3(256), 0, S(stream), infos, n_imgs, K,
+                           P_rig2cam, P_rig2cam_stride, P_w2rig, z_coefs, pts3d, pids, pix2d_std, pix2d_dep, n_obs, C,
+                           is_depth_log, (double*)J_cam, (double*)J_zcf, (double*)J_pts);
+    else
+        hipLaunchKernelGGL(k_jacobians<float>, dim3(nblk(n_obs, 256)), dim3(256), 0, S(stream), infos, n_imgs, K,
+                           P_rig2cam, P_rig2cam_stride, P_w2rig, z_coefs, pts3d, pids, pix2d_std, pix2d_dep, n_obs, C,
+                           is_depth_log, (float*)J_cam, (float*)J_zcf, (float*)J_pts);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// ----------------------------------------------------------------------------- chol3x3
+template <typename T>
+__device__ __forceinline__ T bsqrt(T x) { return sqrt(x); }
+template <>
+__device__ __forceinline__ float bsqrt<float>(float x) { return sqrtf(x); }
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_chol3x3(const T* __restrict__ A, const T* __restrict__ b, T* __restrict__ y,
+                                                 int64_t n, T jitter) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const T* a = A + i * 9;
+    T a00 = a[0] + jitter, a11 = a[4] + jitter, a22 = a[8] + jitter;     // .cu:578-595
+    T a01 = (a[1] + a[3]) * T(0.5), a02 = (a[2] + a[6]) * T(0.5), a12 = (a[5] + a[7]) * T(0.5);
+    a00 = a00 > T(0) ? a00 : a00 + jitter;                               // .cu:600
+    T l00 = bsqrt(a00);
+    T l10 = a01 / l00, l20 = a02 / l00;
+    T t11 = a11 - l10 * l10;
+    t11 = t11 > T(0) ? t11 : t11 + jitter;
+    T l11 = bsqrt(t11);
+    T l21 = (a12 - l10 * l20) / l11;
+    T t22 = a22 - l20 * l20 - l21 * l21;
+    t22 = t22 > T(0) ? t22 : t22 + jitter;
+    T l22 = bsqrt(t22);
+    const T* r = b + i * 3;
+    T z0 = r[0] / l00;                                                   // .cu:621-628
+    T z1 = (r[1] - l10 * z0) / l11;
+    T z2 = (r[2] - l20 * z0 - l21 * z1) / l22;
+    T x2 = z2 / l22;
+    T x1 = (z1 - l21 * x2) / l11;
+    T x0 = (z0 - l10 * x1 - l20 * x2) / l00;
+    y[i * 3 + 0] = x0; y[i * 3 + 1] = x1; y[i * 3 + 2] = x2;
+}
+
+// Replaces chol3x3_solve (.cu:1151-1169). dtype: 0 fp32, 1 fp64.
+extern "C" int ba_chol3x3_solve(const void* blocks, const void* rhs, void* out, int64_t n, double jitter, int32_t dtype,
+                                void* stream) {
+    clear_error();
+    BA_REQUIRE(n >= 0, "bad size");
+    if (n == 0) return BA_OK;
+    if (dtype == 1)
+        hipLaunchKernelGGL(k_chol3x3<double>, dim3(nblk(n, 256)), dim3(256), 0, S(stream), (const double*)blocks,
+                           (const double*)rhs, (double*)out, n, jitter);
+    else
+        hipLaunchKernelGGL(k_chol3x3<float>, dim3(nblk(n, 256)), dim3(256), 0, S(stream), (const float*)blocks,
+                           (const float*)rhs, (float*)out, n, (float)jitter);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// ----------------------------------------------------------------------------- block-COO matvec
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) k_bcoo(const T* __restrict__ blocks, int bh, int bw, const I* __restrict__ rows,
+                                              const I* __restrict__ cols, int64_t n, const T* __restrict__ x,
+                                              T* __restrict__ y, int transpose) {
+    int per = transpose ? bw : bh;
+    int64_t total = n * per;
+    for (int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tid < total;
+         tid += (int64_t)blockDim.x * gridDim.x) {
+        int64_t bi = tid / per;
+        int lo = (int)(tid - bi * per);
+        int64_t rb = (int64_t)rows[bi], cb = (int64_t)cols[bi];
+        const T* A = blocks + bi * (int64_t)bh * bw;
+        T acc = T(0);
+        if (!transpose) {
+            for (int c = 0; c < bw; ++c) acc += A[lo * bw + c] * x[cb * bw + c];
+            atomicAdd(y + rb * bh + lo, acc);
+        } else {
+            for (int r = 0; r < bh; ++r) acc += A[r * bw + lo] * x[rb * bh + r];
+            atomicAdd(y + cb * bw + lo, acc);
+        }
+    }
+}
+
+// Replaces blockcoo_matvec (.cu:1171-1219) for any block shape.  y (out_len) is zero-filled here.
+extern "C" int ba_blockcoo_matvec(const void* blocks, int32_t bh, int32_t bw, const void* row_idx, const void* col_idx,
+                                  int32_t index_int64, int64_t n_blocks, const void* x, void* y, int64_t HB1,
+                                  int64_t WB1, int32_t transpose, int32_t dtype, void* stream) {
+    clear_error();
+    BA_REQUIRE(bh > 0 && bw > 0 && n_blocks >= 0, "bad block shape");
+    int64_t out_len = transpose ? WB1 * bw : HB1 * bh;
+    BA_HIP(hipMemsetAsync(y, 0, out_len * (dtype == 1 ? 8 : 4), S(stream)));
+    if (n_blocks == 0) return BA_OK;
+    int64_t total = n_blocks * (transpose ? bw : bh);
+    unsigned g = nblk(total, 256);
+#define BA_BCOO(T, I) \
+    hipLaunchKernelGGL((k_bcoo<T, I>), dim3(g), dim3(256), 0, S(stream), (const T*)blocks, bh, bw, (const I*)row_idx, \
+                       (const I*)col_idx, n_blocks, (const T*)x, (T*)y, transpose)
+    if (dtype == 1) { if (index_int64) BA_BCOO(double, int64_t); else BA_BCOO(double, int32_t); }
+    else            { if (index_int64) BA_BCOO(float, int64_t);  else BA_BCOO(float, int32_t); }
+#undef BA_BCOO
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// ----------------------------------------------------------------------------- einsum bki,bkj->bij
+template <typename T>
+__global__ void __launch_bounds__(256) k_einsum(const T* __restrict__ L, int64_t l_bs, int64_t l_ks,
+                                                const T* __restrict__ R, int64_t r_bs, int64_t r_ks,
+                                                T* __restrict__ out, int64_t B, int K, int I, int J) {
+    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t total = B * I * J;
+    if (tid >= total) return;
+    int64_t b = tid / (I * J);
+    int ij = (int)(tid - b * I * J);
+    int i = ij / J, j = ij - (ij / J) * J;
+    const T* lb = L + b * l_bs;
+    const T* rb = R + b * r_bs;
+    T acc = T(0);
+    for (int k = 0; k < K; ++k) acc += lb[k * l_ks + i] * rb[k * r_ks + j];
+    out[tid] = acc;
+}
+
+// Replaces fused_einsum_bki_bkj (.cu:1222-1250) for every (I, J, K): the reference dispatch
+// list (.cu:969-1007) lacks (C,6,1) for C=5, which the pose/depth-coefficient cross term needs.
+extern "C" int ba_einsum_bki_bkj(const void* left, int64_t l_bs, int64_t l_ks, const void* right, int64_t r_bs,
+                                 int64_t r_ks, void* out, int64_t B, int32_t K, int32_t I, int32_t J, int32_t dtype,
+                                 void* stream) {
+    clear_error();
+    BA_REQUIRE(B >= 0 && K >= 0 && I > 0 && J > 0, "bad sizes");
+    int64_t total = B * I * J;
+    if (total == 0) return BA_OK;
+    if (dtype == 1)
+        hipLaunchKernelGGL(k_einsum<double>, dim3(nblk(total, 256)), dim3(256), 0, S(stream), (const double*)left, l_bs,
+                           l_ks, (const double*)right, r_bs, r_ks, (double*)out, B, K, I, J);
+    else
+        hipLaunchKernelGGL(k_einsum<float>, dim3(nblk(total, 256)), dim3(256), 0, S(stream), (const float*)left, l_bs,
+                           l_ks, (const float*)right, r_bs, r_ks, (float*)out, B, K, I, J);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// ----------------------------------------------------------------------------- SE(3) exponential
+// Closed form: R = I + A [w]x + B [w]x^2, t = (I + B [w]x + Cc [w]x^2) v, with
+// A = sin(th)/th, B = (1-cos th)/th^2, Cc = (th - sin th)/th^3 (Taylor series below 1e-4 rad),
+// evaluated in fp64 and rounded once to fp32.  Same map as torch.matrix_exp of the hat matrix
+// (cujac/__init__.py:43-58).
+__device__ __forceinline__ void se3_exp(const double xi[6], double Rt[12]) {
+    double wx = xi[0], wy = xi[1], wz = xi[2];
+    double th2 = wx * wx + wy * wy + wz * wz;
+    double th = sqrt(th2);
+    double A, B, Cc;
+    if (th < 1e-4) {
+        A = 1.0 - th2 / 6.0 + th2 * th2 / 120.0;
+        B = 0.5 - th2 / 24.0 + th2 * th2 / 720.0;
+        Cc = 1.0 / 6.0 - th2 / 120.0 + th2 * th2 / 5040.0;
+    } else {
+        double s = sin(th), c = cos(th);
+        A = s / th;
+        B = (1.0 - c) / th2;
+        Cc = (th - s) / (th2 * th);
+    }
+    double W[9] = {0, -wz, wy, wz, 0, -wx, -wy, wx, 0};
+    double W2[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) {
+            double s = 0;
+            for (int k = 0; k < 3; ++k) s += W[3 * r + k] * W[3 * k + c];
+            W2[3 * r + c] = s;
+        }
+    for (int r = 0; r < 3; ++r) {
+        double t = 0;
+        for (int c = 0; c < 3; ++c) {
+            double I = (r == c) ? 1.0 : 0.0;
+            Rt[4 * r + c] = I + A * W[3 * r + c] + B * W2[3 * r + c];
+            double V = I + B * W[3 * r + c] + Cc * W2[3 * r + c];
+            t += V * xi[3 + c];
+        }
+        Rt[4 * r + 3] = t;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_exp_se3(const float* __restrict__ xi, float* __restrict__ out, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    double x[6];
+    for (int k = 0; k < 6; ++k) x[k] = xi[i * 6 + k];
+    double Rt[12];
+    se3_exp(x, Rt);
+    float* o = out + i * 16;
+    for (int k = 0; k < 12; ++k) o[k] = (float)Rt[k];
+    o[12] = 0.f; o[13] = 0.f; o[14] = 0.f; o[15] = 1.f;
+}
+
+// Replaces exp_se3 (cujac/__init__.py:56-58): xi (B,6) = [w | v] -> (B,4,4) fp32.
+extern "C" int ba_exp_se3(const float* xi, float* out, int64_t n, void* stream) {
+    clear_error();
+    BA_REQUIRE(n >= 0, "bad size");
+    if (n == 0) return BA_OK;
+    hipLaunchKernelGGL(k_exp_se3, dim3(nblk(n, 256)), dim3(256), 0, S(stream), xi, out, n);
+    BA_LAUNCHED();
+    return BA_OK;
+}

@@ -1,0 +1,49 @@
+// Constants shared by the plan builder (host C++) and the fused kernels (HIP).
+#pragma once
+
+#define BA_CHUNK 128          // observation slots per chunk (one slot per lane in the per-observation phases)
+#define BA_MAX_LOCAL 16       // images a batch may touch (bit mask in 32 bits, local ids in 8 bits)
+#define BA_WAVES 4            // waves per workgroup of the fused Schur kernel
+#define BA_SLOTS_PER_WAVE 24  // camera-pair accumulators held in registers by one wave
+#define BA_MAX_SLOTS (BA_WAVES * BA_SLOTS_PER_WAVE)
+
+// plan arrays (all int32)
+enum {
+    BA_PA_CHUNK_OBS = 0,
+    BA_PA_CHUNK_META,
+    BA_PA_SLOT_INFO,
+    BA_PA_CT_PID,
+    BA_PA_CT_FIRST,
+    BA_PA_CT_M,
+    BA_PA_CT_MASK,
+    BA_PA_B_CHUNK_PTR,
+    BA_PA_B_IMGS,
+    BA_PA_B_NIMGS,
+    BA_PA_B_SLOT_PTR,
+    BA_PA_SLOT_PAIR,
+    BA_PA_SLOT_GPAIR,
+    BA_PA_PAIR_I1,
+    BA_PA_PAIR_I2,
+    BA_PA_PAIR_PTR,
+    BA_PA_PAIR_SRC,
+    BA_PA_ROW_PTR,
+    BA_PA_ROW_ENT,
+    BA_PA_IMG_PTR,
+    BA_PA_IMG_SRC,
+    BA_PLAN_NARRAYS
+};
+
+// plan scalars (int64)
+enum {
+    BA_PS_N_CHUNKS = 0,
+    BA_PS_N_BATCHES,
+    BA_PS_N_SLOTS,
+    BA_PS_N_PAIRS,
+    BA_PS_N_CTRACKS,
+    BA_PS_L,
+    BA_PS_CHUNK,
+    BA_PS_MAX_SLOTS_USED,
+    BA_PS_MAX_CHUNKS_PER_BATCH,
+    BA_PS_N_PAIR_TERMS,
+    BA_PLAN_NSCALARS
+};

@@ -1,0 +1,265 @@
+// LM step helpers on the device: parameter update and the line-search objective.
+//
+//   ba_apply_update  K <- clip(K - s dK, 100), P <- exp_se3(-s dP) P, z <- z - s dZ, X <- X - s dX
+//                    (src/blast3r/inference/engine.py:310-313, :347-354; cujac/__init__.py:56-58)
+//   ba_objective     loss = mean(err) (engine.py:268) and reproj_score = mean of the lowest
+//                    80% of ||r[:, :2]|| (engine.py:357-361), the latter by an exact radix
+//                    select on the fp32 bit patterns instead of a full sort.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <cmath>
+
+#include "ba_common.h"
+#include "ba_error.h"
+
+namespace ba {
+
+__device__ __forceinline__ void se3_exp_local(const double xi[6], double Rt[12]) {
+    double wx = xi[0], wy = xi[1], wz = xi[2];
+    double th2 = wx * wx + wy * wy + wz * wz;
+    double th = sqrt(th2);
+    double A, B, Cc;
+    if (th < 1e-4) {
+        A = 1.0 - th2 / 6.0 + th2 * th2 / 120.0;
+        B = 0.5 - th2 / 24.0 + th2 * th2 / 720.0;
+        Cc = 1.0 / 6.0 - th2 / 120.0 + th2 * th2 / 5040.0;
+    } else {
+        double s = sin(th), c = cos(th);
+        A = s / th;
+        B = (1.0 - c) / th2;
+        Cc = (th - s) / (th2 * th);
+    }
+    double W[9] = {0, -wz, wy, wz, 0, -wx, -wy, wx, 0};
+    double W2[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) {
+            double s = 0;
+            for (int k = 0; k < 3; ++k) s += W[3 * r + k] * W[3 * k + c];
+            W2[3 * r + c] = s;
+        }
+    for (int r = 0; r < 3; ++r) {
+        double t = 0;
+        for (int c = 0; c < 3; ++c) {
+            double I = (r == c) ? 1.0 : 0.0;
+            Rt[4 * r + c] = I + A * W[3 * r + c] + B * W2[3 * r + c];
+            t += (I + B * W[3 * r + c] + Cc * W2[3 * r + c]) * xi[3 + c];
+        }
+        Rt[4 * r + 3] = t;
+    }
+}
+
+// one thread per camera / node / image / track item, flattened
+__global__ void __launch_bounds__(256) k_apply_update(const float* __restrict__ K, const float* __restrict__ P,
+                                                      const float* __restrict__ Z, const float* __restrict__ X,
+                                                      const float* __restrict__ dK, const float* __restrict__ dP,
+                                                      const float* __restrict__ dZ, const float* __restrict__ dX,
+                                                      float scale, float min_f, int n_cams, int n_nodes, int n_imgs,
+                                                      int C, int64_t n_tracks, float* __restrict__ Ko,
+                                                      float* __restrict__ Po, float* __restrict__ Zo,
+                                                      float* __restrict__ Xo) {
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n_cams) {
+        const float* k = K + t * 9;
+        float* o = Ko + t * 9;
+        for (int e = 0; e < 9; ++e) o[e] = k[e];
+        float fx = k[0] - dK[2 * t] * scale, fy = k[4] - dK[2 * t + 1] * scale;   // update_K (engine.py:347-354)
+        o[0] = fx < min_f ? min_f : fx;
+        o[4] = fy < min_f ? min_f : fy;
+        return;
+    }
+    t -= n_cams;
+    if (t < n_nodes) {
+        double xi[6], Rt[12];
+        for (int e = 0; e < 6; ++e) xi[e] = -(double)(dP[6 * t + e] * scale);
+        se3_exp_local(xi, Rt);
+        float E[16];
+        for (int e = 0; e < 12; ++e) E[e] = (float)Rt[e];
+        E[12] = 0.f; E[13] = 0.f; E[14] = 0.f; E[15] = 1.f;
+        const float* p = P + t * 16;
+        float* o = Po + t * 16;
+        for (int r = 0; r < 4; ++r)
+            for (int c = 0; c < 4; ++c) {
+                float s = 0.f;
+                for (int k = 0; k < 4; ++k) s += E[4 * r + k] * p[4 * k + c];
+                o[4 * r + c] = s;
+            }
+        return;
+    }
+    t -= n_nodes;
+    if (t < (int64_t)n_imgs * C) { Zo[t] = Z[t] - dZ[t] * scale; return; }
+    t -= (int64_t)n_imgs * C;
+    if (t < 3 * n_tracks) { Xo[t] = X[t] - dX[t] * scale; }
+}
+
+// ------------------------------------------------------------------ objective
+#define OBJ_T 256
+
+__global__ void k_obj_init(uint32_t* __restrict__ hist, uint32_t* __restrict__ sel, uint32_t k) {
+    hist[threadIdx.x] = 0;
+    if (threadIdx.x == 0) { sel[0] = 0; sel[1] = 0; sel[2] = k; sel[3] = 0; }
+}
+
+__global__ void __launch_bounds__(OBJ_T) k_obj_prep(const float* __restrict__ res, int64_t n, int has_err,
+                                                   uint32_t* __restrict__ ebits, double* __restrict__ part) {
+    __shared__ double sh[OBJ_T];
+    int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x;
+    double s = 0.0;
+    if (i < n) {
+        float r0 = res[i], r1 = res[n + i];
+        float e = sqrtf(r0 * r0 + r1 * r1);
+        ebits[i] = __float_as_uint(e);
+        if (has_err) s = (double)res[3 * n + i] + (double)res[4 * n + i] + (double)res[5 * n + i];
+    }
+    sh[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = OBJ_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
+}
+
+// histogram of the next 8 bits among values whose higher bits equal the prefix
+__global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__ ebits, int64_t n,
+                                                   const uint32_t* __restrict__ sel, int shift,
+                                                   uint32_t* __restrict__ hist) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    uint32_t prefix = sel[0], pmask = sel[1];
+    for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
+        uint32_t b = ebits[i];
+        if ((b & pmask) == prefix) atomicAdd(&h[(b >> shift) & 0xffu], 1u);
+    }
+    __syncthreads();
+    if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+}
+
+// pick the bin holding the k-th smallest (k in sel[2], 1-based); clear hist for the next pass
+__global__ void k_obj_pick(uint32_t* __restrict__ hist, uint32_t* __restrict__ sel, int shift) {
+    if (threadIdx.x != 0) return;
+    uint32_t k = sel[2];
+    uint32_t cum = 0;
+    int b = 0;
+    for (; b < 256; ++b) {
+        if (cum + hist[b] >= k) break;
+        cum += hist[b];
+    }
+    if (b > 255) b = 255;
+    sel[0] |= (uint32_t)b << shift;
+    sel[1] |= 0xffu << shift;
+    sel[2] = k - cum;
+    for (int q = 0; q < 256; ++q) hist[q] = 0;
+}
+
+__global__ void __launch_bounds__(OBJ_T) k_obj_below(const uint32_t* __restrict__ ebits, int64_t n,
+                                                    const uint32_t* __restrict__ sel, double* __restrict__ psum,
+                                                    uint32_t* __restrict__ pcnt) {
+    __shared__ double sh[OBJ_T];
+    __shared__ uint32_t sc[OBJ_T];
+    uint32_t T = sel[0];
+    double s = 0.0;
+    uint32_t c = 0;
+    int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x;
+    if (i < n) {
+        uint32_t b = ebits[i];
+        if (b < T) { s = (double)__uint_as_float(b); c = 1; }
+    }
+    sh[threadIdx.x] = s; sc[threadIdx.x] = c;
+    __syncthreads();
+    for (int w = OBJ_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) { sh[threadIdx.x] += sh[threadIdx.x + w]; sc[threadIdx.x] += sc[threadIdx.x + w]; }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) { psum[blockIdx.x] = sh[0]; pcnt[blockIdx.x] = sc[0]; }
+}
+
+__global__ void __launch_bounds__(OBJ_T) k_obj_final(const double* __restrict__ lpart, const double* __restrict__ psum,
+                                                    const uint32_t* __restrict__ pcnt, int nb, int64_t n,
+                                                    int64_t n80, const uint32_t* __restrict__ sel, int has_err,
+                                                    float* __restrict__ out) {
+    __shared__ double sh[OBJ_T], sl[OBJ_T];
+    __shared__ uint64_t sc[OBJ_T];
+    double s = 0.0, l = 0.0;
+    uint64_t c = 0;
+    for (int b = threadIdx.x; b < nb; b += OBJ_T) { s += psum[b]; l += lpart[b]; c += pcnt[b]; }
+    sh[threadIdx.x] = s; sl[threadIdx.x] = l; sc[threadIdx.x] = c;
+    __syncthreads();
+    for (int w = OBJ_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) {
+            sh[threadIdx.x] += sh[threadIdx.x + w]; sl[threadIdx.x] += sl[threadIdx.x + w]; sc[threadIdx.x] += sc[threadIdx.x + w];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float T = __uint_as_float(sel[0]);
+        double tot = sh[0] + (double)(n80 - (int64_t)sc[0]) * (double)T;
+        out[0] = has_err ? (float)(sl[0] / (3.0 * (double)n)) : NAN;
+        out[1] = n80 > 0 ? (float)(tot / (double)n80) : NAN;
+    }
+}
+
+}  // namespace ba
+
+using namespace ba;
+
+static inline unsigned nbk(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// Replaces the update block of lm_step (engine.py:310-313): one launch for every parameter group.
+extern "C" int ba_apply_update(const float* K, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                               const float* dK, const float* dP, const float* dZ, const float* dX, float scale,
+                               float min_f, int32_t n_cams, int32_t n_nodes, int32_t n_imgs, int32_t C,
+                               int64_t n_tracks, float* K_out, float* P_out, float* z_out, float* X_out,
+                               void* stream) {
+    clear_error();
+    int64_t total = (int64_t)n_cams + n_nodes + (int64_t)n_imgs * C + 3 * n_tracks;
+    if (total == 0) return BA_OK;
+    hipLaunchKernelGGL(k_apply_update, dim3(nbk(total, 256)), dim3(256), 0, (hipStream_t)stream, K, P_w2rig, z_coefs,
+                       pts3d, dK, dP, dZ, dX, scale, min_f, n_cams, n_nodes, n_imgs, C, n_tracks, K_out, P_out, z_out,
+                       X_out);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+extern "C" int64_t ba_objective_workspace_bytes(int64_t n_obs) {
+    int64_t nb = (n_obs + OBJ_T - 1) / OBJ_T;
+    if (nb < 1) nb = 1;
+    return 4 * n_obs + 8 * nb * 2 + 4 * nb + 4 * 256 + 4 * 4 + 64;
+}
+
+// loss = mean(err) and reproj_score from the (9 or 3, n_obs) residual buffer; out[0] = loss,
+// out[1] = reproj_score (fp32, device).  Workspace of ba_objective_workspace_bytes(n_obs).
+extern "C" int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out,
+                            void* stream) {
+    clear_error();
+    hipStream_t st = (hipStream_t)stream;
+    int64_t nb = (n_obs + OBJ_T - 1) / OBJ_T;
+    if (nb < 1) nb = 1;
+    char* w = (char*)workspace;
+    uint32_t* ebits = (uint32_t*)w; w += 4 * n_obs;
+    w = (char*)(((uintptr_t)w + 7) & ~(uintptr_t)7);
+    double* lpart = (double*)w; w += 8 * nb;
+    double* psum = (double*)w; w += 8 * nb;
+    uint32_t* pcnt = (uint32_t*)w; w += 4 * nb;
+    uint32_t* hist = (uint32_t*)w; w += 4 * 256;
+    uint32_t* sel = (uint32_t*)w;
+    int64_t n80 = n_obs * 80 / 100;
+    hipLaunchKernelGGL(k_obj_init, dim3(1), dim3(256), 0, st, hist, sel, (uint32_t)(n80 > 0 ? n80 : 1));
+    if (n_obs > 0) {
+        hipLaunchKernelGGL(k_obj_prep, dim3((unsigned)nb), dim3(OBJ_T), 0, st, res, n_obs, has_err, ebits, lpart);
+        unsigned hb = (unsigned)(nb < 1024 ? nb : 1024);
+        for (int pass = 0; pass < 4; ++pass) {
+            int shift = 24 - 8 * pass;
+            hipLaunchKernelGGL(k_obj_hist, dim3(hb), dim3(OBJ_T), 0, st, ebits, n_obs, sel, shift, hist);
+            hipLaunchKernelGGL(k_obj_pick, dim3(1), dim3(64), 0, st, hist, sel, shift);
+        }
+        hipLaunchKernelGGL(k_obj_below, dim3((unsigned)nb), dim3(OBJ_T), 0, st, ebits, n_obs, sel, psum, pcnt);
+    } else {
+        hipLaunchKernelGGL(k_obj_prep, dim3(1), dim3(OBJ_T), 0, st, res, (int64_t)0, has_err, ebits, lpart);
+        hipLaunchKernelGGL(k_obj_below, dim3(1), dim3(OBJ_T), 0, st, ebits, (int64_t)0, sel, psum, pcnt);
+    }
+    hipLaunchKernelGGL(k_obj_final, dim3(1), dim3(OBJ_T), 0, st, lpart, psum, pcnt, (int)nb, n_obs, n80, sel, has_err,
+                       out);
+    BA_LAUNCHED();
+    return BA_OK;
+}

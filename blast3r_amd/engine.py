@@ -1,0 +1,264 @@
+"""MI355X LM driver: drop-in for src/blast3r/inference/engine.py (``en``) on the BA path.
+
+``lm_step`` and ``bundle_adjustment`` keep the reference signatures, defaults,
+return values and control flow (en:206-334, en:405-503).  The numerical work
+runs in libba_hip.so: residuals (ba_residuals), the fused linearize + Schur +
+PCG + back-substitution step (GaussNewtonSolver), the parameter update
+(ba_apply_update) and the line-search objective with an exact radix-select
+reproj_score (ba_objective).
+"""
+from collections import namedtuple
+
+import torch
+
+from . import cujac
+from ._lib import check, lib, ptr, stream_ptr
+from .ba_solver import GaussNewtonSolver, _param_state
+
+BA_Status = namedtuple('BA_Status', 'init_loss, init_residuals, new_loss, new_residuals')
+
+STEP_SCHEDULE = [0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0]     # en:309
+
+
+def shape_of(tensor, is_contiguous=True):
+    """en:340-344."""
+    assert tensor.dtype in (torch.float32, torch.int32)
+    if is_contiguous:
+        assert tensor.is_contiguous()
+    assert tensor.isfinite().all()
+    return tensor.shape
+
+
+def update_K(K0, delta_focal, min_f=100):
+    """en:347-354."""
+    dfx, dfy = delta_focal.T
+    K = K0.clone()
+    K[:, 0, 0] -= dfx
+    K[:, 1, 1] -= dfy
+    K[:, 0, 0].clip_(min=min_f)
+    K[:, 1, 1].clip_(min=min_f)
+    return K
+
+
+def reproj_score(res):
+    """Mean of the lowest 80% of ||r[:, :2]|| (en:357-361); device radix select, no sort."""
+    n = res.shape[0]
+    buf = res[:, :2].T.contiguous() if not (res.stride(0) == 1) else None
+    base = buf if buf is not None else res.T   # (k, n) with unit stride along n
+    return _objective(base, n, has_err=False)[1]
+
+
+def _objective(res_kn, n, has_err):
+    """(loss, reproj) as 0-d device tensors from a (>=3 or 2, n) SoA buffer with unit inner stride."""
+    dev = res_kn.device
+    if res_kn.stride(1) != 1 or (res_kn.shape[0] > 1 and res_kn.stride(0) != n):
+        res_kn = res_kn.contiguous()
+    ws = torch.empty(int(lib().ba_objective_workspace_bytes(n)), dtype=torch.uint8, device=dev)
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    check(lib().ba_objective(ptr(res_kn), n, int(has_err), ptr(ws), ptr(out), stream_ptr(dev)))
+    return out[0], out[1]
+
+
+def iter_on(*iterators):
+    """en:364-383."""
+    iterable = lambda it: isinstance(it, (tuple, list))
+    max_len = 1
+    for it in iterators:
+        if iterable(it):
+            max_len = max(max_len, len(it))
+    new_iterators = []
+    for it in iterators:
+        if iterable(it):
+            assert len(it) in (1, max_len), f'missing {max_len - len(it)} values for parameter={it}'
+            new_iterators.append(it[0] if len(it) == 1 else it)
+        else:
+            new_iterators.append(it)
+    for step in range(max_len):
+        yield tuple(it[step] if iterable(it) else it for it in new_iterators)
+
+
+def used_depth_channels(n_zcfs, n_channels, depth_mode):
+    """en:386-402."""
+    phases = n_zcfs if isinstance(n_zcfs, (list, tuple)) else [n_zcfs]
+    used = 0
+    for n in phases:
+        if n is None:
+            return n_channels
+        if depth_mode[:3] == 'log' and not (n == 2 or n == n_channels):
+            n += 1
+        used = max(used, n)
+    return min(used, n_channels)
+
+
+def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
+            K, P_rig2cam, P_w2rig, z_coefs, pts3d,
+            depth_mode='log',
+            pnorm=1,
+            clip_pix_err=100,
+            huber_delta=0.5,
+            min_reproj=0.01,
+            dampen=1e-12,
+            min_loss_delta=1e-4,
+            weight_z=1,
+            log_depth_maps=None, conf=None, pts3d_ref=None, weight_tan=0.0, tan_stride=4,
+            normalize_tangents=True,
+            optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True, verbose_steps=False,
+            **ba_options):
+    """Levenberg-Marquardt step (en:206-334) on MI355X.  Returns (update, BA_Status)."""
+    assert depth_mode in ('lin', 'log')
+    is_depth_log = depth_mode == 'log'
+    if weight_tan > 0:
+        raise NotImplementedError('the dense tangent prior (weight_tan > 0) is not part of the MI355X path; '
+                                  'pass z_prior to GaussNewtonSolver.solve_delta instead')
+    n_imgs = rigs.shape[1]
+    assert shape_of(rigs) == (3, n_imgs)
+    n_cams = len(K)
+    assert shape_of(K) == (n_cams, 3, 3)
+    assert shape_of(P_rig2cam, is_contiguous=False) == (n_cams, 4, 4)
+    n_nodes = len(P_w2rig)
+    assert shape_of(P_w2rig) == (n_nodes, 4, 4)
+    n_zcf = z_coefs.shape[1]
+    assert shape_of(z_coefs) == (n_imgs, n_zcf)
+    n_tracks = len(pts3d)
+    assert shape_of(pts3d) == (n_tracks, 3)
+    n_obs = len(pids)
+    assert shape_of(pids) == (n_obs,)
+    assert shape_of(pix2d) == (n_obs, 2)
+    assert shape_of(pix2d_std) == (n_obs, 2)
+    assert shape_of(pix2d_dep) == (n_obs, n_zcf), f'expected pix2d_dep of shape {(n_obs, n_zcf)}, got {shape_of(pix2d_dep)}'
+    assert 0 <= weight_z <= 10
+    assert n_obs >= n_tracks, 'there must be more 2d kpts than tracks'
+    assert huber_delta >= 0.1
+
+    w_null = 1e-16
+
+    def objective(K, P_w2rig, pts3d, z_coefs):
+        out = cujac.compute_residuals_with_rigs(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std,
+                                                pix2d_dep, is_depth_log, weight_z, pnorm, clip_pix_err, huber_delta,
+                                                w_null)
+        buf = out.T                                               # (9, n) buffer
+        residuals_, err_, w_pts_ = out.view(-1, 3, 3).unbind(dim=1)
+        loss, reproj = _objective(buf, n_obs, has_err=pnorm > 0)
+        return loss, residuals_, w_pts_, reproj
+
+    init_loss, init_residuals, w_pts, _ = objective(K, P_w2rig, pts3d, z_coefs)
+
+    hp = dict(weight_z=weight_z, pnorm=pnorm, max_pix_err=clip_pix_err, huber_delta=huber_delta, w_pts_null=w_null)
+    jac = GaussNewtonSolver(n_cams, n_nodes, n_imgs, n_tracks, pts3d.device, dampen=dampen, **ba_options)
+    J = jac.compute_jacobians(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d_std, pix2d_dep,
+                              optim_K=optim_K, optim_Z=optim_Z, optim_Z0=optim_Z0, optim_P=optim_P, optim_X=optim_X,
+                              is_depth_log=is_depth_log, pix2d=pix2d, hp=hp)
+    init_residuals._ba_state = _param_state(J)
+    delta = jac.solve_delta(J, init_residuals, w_pts)
+    delta_K, delta_P, delta_zcf, delta_pts = jac.unpack_delta_inplace(delta)
+
+    update = dict()
+    dKc = delta_K.contiguous()
+    dPc = delta_P.contiguous()
+    dZc = delta_zcf.contiguous()
+    dXc = delta_pts.contiguous()
+    scale = 1.0
+    last_a = 1
+    dev = pts3d.device
+    for a in STEP_SCHEDULE:
+        Kn = torch.empty_like(K)
+        Pn = torch.empty_like(P_w2rig)
+        Zn = torch.empty_like(z_coefs)
+        Xn = torch.empty_like(pts3d)
+        check(lib().ba_apply_update(ptr(K), ptr(P_w2rig), ptr(z_coefs), ptr(pts3d), ptr(dKc), ptr(dPc), ptr(dZc),
+                                    ptr(dXc), float(scale), 100.0, n_cams, n_nodes, n_imgs, n_zcf, n_tracks,
+                                    ptr(Kn), ptr(Pn), ptr(Zn), ptr(Xn), stream_ptr(dev)))
+        update['K'], update['P_w2rig'], update['z_coefs'], update['pts3d'] = Kn, Pn, Zn, Xn
+        new_loss, new_residuals, _, new_reproj_t = objective(**update)
+        vals = torch.stack([new_loss, init_loss, new_reproj_t]).cpu()
+        if torch.isnan(vals[0]):
+            print('Warning: loss is NaN')
+            new_loss = init_loss
+        new_loss = new_loss + min_loss_delta
+        new_reproj = float(vals[2])
+        degenerate = new_reproj < min_reproj
+        if degenerate:
+            print(f'Rejecting step: reprojection residual collapsed to {new_reproj:.2e}')
+        if float(new_loss) < float(vals[1]) and not degenerate:
+            break
+        scale = scale * (a / last_a)       # delta *= a/last_a (en:330): every slice scaled together
+        last_a = a
+    else:
+        print('Warning: loss is not decreasing')
+    return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals)
+
+
+def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
+                      max_iters=1000,
+                      pnorm=0.5,
+                      optim_P=True,
+                      optim_Z=True,
+                      optim_Z0=True,
+                      optim_K=True,
+                      optim_X=True,
+                      weight_z=0.1,
+                      dense_depth=None,
+                      dense_conf=None,
+                      dense_pts3d_ref=None,
+                      tangent_reg=0.0,
+                      tan_stride=4,
+                      normalize_tangents=True,
+                      n_zcfs=None,
+                      no_Jfz=False,
+                      max_n_phases=-1,
+                      device='cuda',
+                      verbose=True,
+                      **other_lm_kwargs):
+    """Main bundle-adjustment loop (en:405-503)."""
+    trk = track_data.to(device)
+    rig = rigs_data.to(device)
+    if z_coefs is None:
+        z_coefs = rig.z_coefs_from_scale(trk)
+    original_pix2d_dep = trk.pix2d_dep
+    assert pts3d is not None, 'the 3D points must be initialized before bundle adjustment'
+    pts3d = pts3d.to(device)
+    variables = dict(K=rig.K, P_rig2cam=rig.P_rig2cam, P_w2rig=rig.P_w2rig, z_coefs=z_coefs, pts3d=pts3d)
+    phase_num = 0
+    for pnorm, max_iters, optim_K, optim_P, optim_Z, optim_X, weight_z, n_zcfs, tangent_reg in \
+            iter_on(pnorm, max_iters, optim_K, optim_P, optim_Z, optim_X, weight_z, n_zcfs, tangent_reg):
+        phase_num += 1
+        if phase_num > (max_n_phases % 1000):
+            break
+        if n_zcfs is not None:
+            z_coefs = variables['z_coefs']
+            optim_Z0 = True
+            if rig.depth_mode[:3] == 'log':
+                optim_Z0 = (n_zcfs == 2) or (n_zcfs == original_pix2d_dep.shape[1])
+                n_zcfs += not optim_Z0
+            trk.pix2d_dep = original_pix2d_dep[:, :n_zcfs].contiguous()
+            if n_zcfs < z_coefs.shape[1]:
+                assert n_zcfs >= 1
+                variables['z_coefs'] = z_coefs[:, :n_zcfs].contiguous()
+            elif n_zcfs > z_coefs.shape[1]:
+                assert trk.pix2d_dep.shape[1] == n_zcfs, 'not enough multi-depthmaps in the original data'
+                variables['z_coefs'] = torch.cat((z_coefs, z_coefs.new_zeros((len(z_coefs), n_zcfs - z_coefs.shape[1]))),
+                                                 dim=1).contiguous()
+        if verbose:
+            print(f"Starting phase {phase_num}, with {variables['z_coefs'].shape[1]} z-coefs.")
+        it = 0
+        while it < max_iters:
+            update, status = lm_step(rig.infos(trk), trk.pids, trk.pix2d, trk.pix2d_std, trk.pix2d_dep, **variables,
+                                     weight_tan=tangent_reg, tan_stride=tan_stride,
+                                     normalize_tangents=normalize_tangents,
+                                     optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P, optim_X=optim_X,
+                                     optim_Z0=optim_Z0, pnorm=pnorm, weight_z=weight_z, no_grad_f_from_rz=no_Jfz,
+                                     depth_mode=rig.depth_mode, dampen=1e-12, adaptive_dampen=True,
+                                     dtype=torch.float64, **other_lm_kwargs)
+            if verbose:
+                reproj_before = float(reproj_score(status.init_residuals))
+                reproj_after = float(reproj_score(status.new_residuals))
+                avg_focal = float((update['K'][:, 0, 0].mean() + update['K'][:, 1, 1].mean()) / 2)
+                print(f"Loss at iter={it}: {float(status.init_loss):.3f} --> {float(status.new_loss):.3f}, "
+                      f"reproj_score: {reproj_before:.3f} --> reproj_after={reproj_after:.3f}, avg_focal={avg_focal:.2f}")
+            if status.new_loss >= status.init_loss:
+                break
+            variables.update(update)
+            it += 1
+    trk.pix2d_dep = original_pix2d_dep
+    pts3d = variables.pop('pts3d')
+    return rigs_data.update(**variables), pts3d

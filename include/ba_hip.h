@@ -1,0 +1,164 @@
+/*
+ * libba_hip.so -- C ABI of the MI355X bundle-adjustment linearize + Schur path.
+ *
+ * Drop-in boundary for the reference's native module `ba_with_rigs_cuda_kernels`
+ * (src/blast3r/extensions/cujac/sfm_jacobian_rigs.cu, pybind table at :1254-1275,
+ * Python aliases at src/blast3r/extensions/cujac/__init__.py:18-22) and for the
+ * solver work the reference does in PyTorch (src/blast3r/inference/ba_solver.py).
+ *
+ * Conventions for every entry point:
+ *   - returns 0 on success, nonzero on error; ba_last_error() holds a message
+ *     (thread-local), the Python layer raises RuntimeError with it;
+ *   - all pointers are device pointers unless the name says host; the caller
+ *     owns every buffer (the library allocates no caller-visible memory);
+ *   - `stream` is a hipStream_t; work is enqueued asynchronously and never
+ *     synchronised, like the reference's getCurrentCUDAStream launches (.cu:293);
+ *   - entry points are stateless and reentrant; calls that share output or
+ *     workspace buffers must not overlap.
+ */
+#ifndef BA_HIP_H
+#define BA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ misc */
+const char* ba_last_error(void);
+int ba_version(void);
+
+/* ------------------------------------------------------------------ operator-level (cujac) API */
+
+/* residuals_with_rigs (sfm_jacobian_rigs.cu:1048-1101, kernel :129-259).
+ * out: (n_out, n_obs) fp32 with n_out = 9 when pnorm > 0 else 3, rows
+ * [r0 r1 r2 | err0 err1 err2 | w0 w1 w2]; every element is written. */
+int ba_residuals(const int32_t* infos, int32_t n_imgs, const float* K, const float* P_rig2cam,
+                 int64_t P_rig2cam_stride, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                 const int32_t* pids, const float* pix2d, const float* pix2d_std, const float* pix2d_dep,
+                 int64_t n_obs, int32_t C, int32_t is_depth_log, float weight_z, float pnorm,
+                 float max_pix_err, float huber_delta, float w_pts_null, float* out, void* stream);
+
+/* jacobians_with_rigs (sfm_jacobian_rigs.cu:1105-1148, kernel :323-509).
+ * J_cam (n_obs,3,8), J_zcf (n_obs,1,C), J_pts (n_obs,3,3): fp64 if float64 else fp32. */
+int ba_jacobians(const int32_t* infos, int32_t n_imgs, const float* K, const float* P_rig2cam,
+                 int64_t P_rig2cam_stride, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                 const int32_t* pids, const float* pix2d_std, const float* pix2d_dep, int64_t n_obs, int32_t C,
+                 int32_t is_depth_log, int32_t float64, void* J_cam, void* J_zcf, void* J_pts, void* stream);
+
+/* chol3x3_solve (sfm_jacobian_rigs.cu:1151-1169, kernel :560-634). dtype 0 = fp32, 1 = fp64. */
+int ba_chol3x3_solve(const void* blocks, const void* rhs, void* out, int64_t n, double jitter, int32_t dtype,
+                     void* stream);
+
+/* blockcoo_matvec (sfm_jacobian_rigs.cu:1171-1219); any (bh, bw); y is zero-filled by the call. */
+int ba_blockcoo_matvec(const void* blocks, int32_t bh, int32_t bw, const void* row_idx, const void* col_idx,
+                       int32_t index_int64, int64_t n_blocks, const void* x, void* y, int64_t HB1, int64_t WB1,
+                       int32_t transpose, int32_t dtype, void* stream);
+
+/* fused_einsum_bki_bkj (sfm_jacobian_rigs.cu:1222-1250); any (I, J, K), strides in elements. */
+int ba_einsum_bki_bkj(const void* left, int64_t l_bs, int64_t l_ks, const void* right, int64_t r_bs, int64_t r_ks,
+                      void* out, int64_t B, int32_t K, int32_t I, int32_t J, int32_t dtype, void* stream);
+
+/* exp_se3 (cujac/__init__.py:56-58): xi (n,6) = [w|v] -> (n,4,4) fp32. */
+int ba_exp_se3(const float* xi, float* out, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------ structure plan (host) */
+/* Built once per observation structure; replaces the per-iteration torch.unique /
+ * index bookkeeping of ba_solver.py:51-56, :877-909, :968-974.  Host pointers. */
+void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
+                     int32_t n_tracks, int32_t max_local_imgs, int32_t max_slots, int64_t max_batch_obs);
+int ba_plan_query(const void* plan, int64_t* scalars, int64_t* array_sizes);
+int ba_plan_export(const void* plan, int32_t which, int32_t* host_dst);
+void ba_plan_destroy(void* plan);
+const char* ba_plan_last_error(void);
+
+/* ------------------------------------------------------------------ fused linearize + Schur */
+typedef struct {
+    float weight_z, pnorm, max_pix_err, huber_delta, w_pts_null;
+    int32_t is_depth_log;
+} ba_huber;
+
+typedef struct {
+    int32_t d, C, off_tau, off_zcf, hasK, hasP, hasZ;     /* image-level block layout [foc|tau|zcf] */
+    int32_t no_grad_f_from_rz, optim_Z0, optim_Z_1st_cam;  /* ba_solver.py:38-39, :59-60 */
+    float wmin, wmax;                                       /* clamp_w (ba_solver.py:123-124) */
+    double dampen;                                          /* 1e-12 (engine.py:490) */
+    int32_t adaptive, x_off;                                /* adaptive_dampen; optim_X is False */
+} ba_layout;
+
+typedef struct {
+    /* structure */
+    const int32_t* infos; int32_t n_imgs;
+    const int32_t *chunk_obs, *chunk_meta, *slot_info;
+    const int32_t *ct_pid, *ct_first, *ct_m, *ct_mask;
+    const int32_t *b_chunk_ptr, *b_imgs, *b_nimgs, *b_slot_ptr, *slot_pair;
+    int32_t L;
+    /* observations in plan slot order */
+    const float *s_pix, *s_std, *s_dep;
+    const int32_t *s_pid, *s_img;
+    /* parameters */
+    const float* K; const float* P_rig2cam; int64_t P_rig2cam_stride; const float* P_w2rig;
+    const float* z_coefs; const float* pts3d;
+    /* optional uint8 enable masks per cam / node / image / track (NULL = all on) */
+    const uint8_t *enK, *enP, *enZ, *enX;
+    ba_huber hp;
+    ba_layout lay;
+    /* per-track fp64 state: H_pp upper (n_tracks,6), g_p (n_tracks,3) */
+    double *Hpp, *gp;
+    double *chunk_max;   /* (n_chunks) scratch */
+    double *lam_p;       /* (1) point-leaf damping value, written by ba_linearize_schur */
+    /* partial blocks: (n_slots, d, d) and (n_batches, L, 2, d) scratch */
+    double *partials, *img_partials;
+    /* back-substitution inputs/outputs */
+    const double* dc; const int32_t* umap; float* dX; double* dX64;
+    /* sizes and reductions */
+    int64_t n_chunks, n_batches, n_pairs;
+    const int32_t *pair_ptr, *pair_src, *img_ptr, *img_src;
+    /* outputs: image-pair blocks of S (n_pairs,d,d), rhs (n_imgs,d), diag(H_cc) (n_imgs,d) */
+    double *S_pairs, *e_img, *dg_img;
+    /* optional given residuals / IRLS weights, element (obs, k) at r_in[obs*r_s0 + k*r_s1]
+     * (the `residuals`, `w_pts` arguments of solve_delta, ba_solver.py:110); NULL = recompute */
+    const float *r_in, *w_in;
+    int64_t r_s0, r_s1, w_s0, w_s1;
+} ba_lin_args;
+
+/* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.
+ * Requires d <= 16 and C <= 24. */
+int ba_linearize_schur(const ba_lin_args* args, void* stream);
+
+/* Stage 4b: delta_p = (H_pp + lam_p I)^-1 (g_p - H_pc delta_c) per track, written to dX
+ * (n_tracks,3) fp32 (and dX64 if not NULL); dc is the reduced solution, umap the
+ * (n_imgs, d) image-parameter -> unknown index map (-1 = inactive). */
+int ba_backsubstitute(const ba_lin_args* args, void* stream);
+
+/* ------------------------------------------------------------------ reduced system (PCG) */
+typedef struct {
+    int64_t n_u;                       /* active unknowns */
+    int32_t n_imgs, d;
+    const int32_t *umap;               /* (n_imgs, d) -> unknown or -1 */
+    const int32_t *inv_ptr, *inv_src;  /* unknown -> list of image-level entries (i*d + j) */
+    const int32_t *leaf;               /* (n_u) 0 foc, 1 tau, 2 zcf */
+    const int32_t *row_ptr, *row_ent;  /* image rows of the pair structure: (pair << 1) | transposed */
+    const int32_t *pair_i1, *pair_i2;
+    const double *S_pairs, *e_img, *dg_img;
+    double dampen; int32_t adaptive;
+    int32_t maxiter; double tol;
+    /* workspace (fp64 unless noted) */
+    double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *Ap, *y_img;
+    double *partials;                  /* 3 * n_blocks */
+    double *state;                     /* 16 doubles */
+    int32_t *istate;                   /* 8 ints: done, k, converged, best_k, ... */
+} ba_pcg_args;
+
+/* Builds the unknown-level rhs, diag(A) with per-leaf damping (ba_solver.py:575-582,
+ * :1188-1191) and runs Jacobi-PCG (ba_solver.py:184-206, :1197-1238) on
+ * S = P^T S_img P + damping, entirely on the device.  The solution is left in x
+ * (converged) or xbest; istate[2] = converged, istate[1] = iterations. */
+int ba_pcg_solve(const ba_pcg_args* args, void* stream);
+int64_t ba_pcg_partials_size(int64_t n_u);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BA_HIP_H */

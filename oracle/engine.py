@@ -1,0 +1,117 @@
+"""Oracle restatement of the reference LM step (test infrastructure only).
+
+Follows ``lm_step`` (src/blast3r/inference/engine.py:206-334, abbreviated ``en``)
+on CPU with the oracle kernels and solver: objective = mean Huber error
+(en:263-278), linearisation + Schur solve (en:284-303), update of K, P, z, X
+(en:310-313, en:347-354, cujac/__init__.py:56-58) and the step-halving line
+search over a in [0.5, 0.25, 0.125, 1/64, 1/512, 1/4096, 0] with the
+min_loss_delta and reproj_score tests (en:308-333, en:357-361).  The tangent
+prior (en:15-179) is dormant in the reference (tangent_reg = 0.0, en:418) and is
+not restated.
+"""
+from collections import namedtuple
+
+import torch
+
+from . import kernels as K_
+from .solver import Problem, build_normal_equations, solve_reduced_pcg, solve_reduced_direct, unpack_delta
+
+BA_Status = namedtuple('BA_Status', 'init_loss, init_residuals, new_loss, new_residuals')
+
+STEP_SCHEDULE = [0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0]      # en:309
+
+
+def update_K(K0, delta_focal, min_f=100):
+    """en:347-354."""
+    dfx, dfy = delta_focal.T
+    K = K0.clone()
+    K[:, 0, 0] -= dfx
+    K[:, 1, 1] -= dfy
+    K[:, 0, 0].clip_(min=min_f)
+    K[:, 1, 1].clip_(min=min_f)
+    return K
+
+
+def reproj_score(res):
+    """Mean of the lowest 80% of ||r[:, :2]|| (en:357-361)."""
+    e = res[:, :2].norm(dim=-1).sort().values
+    n80 = len(e) * 80 // 100
+    return e[:n80].mean()
+
+
+def objective(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std, pix2d_dep,
+              is_depth_log, weight_z, pnorm, clip_pix_err, huber_delta):
+    """en:263-278 without the tangent prior."""
+    out = K_.residuals_with_rigs(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std,
+                                 pix2d_dep, is_depth_log, weight_z, pnorm, clip_pix_err, huber_delta)
+    res, err, w = out.reshape(-1, 3, 3).unbind(dim=1)
+    return err.mean(), res, w
+
+
+def linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d,
+                        residuals, w_pts, is_depth_log=True, optim_K=True, optim_Z=True, optim_P=True,
+                        optim_X=True, optim_Z0=True, optim_Z_1st_cam=True, no_grad_f_from_rz=False,
+                        dampen=1e-12, adaptive_dampen=True, dtype=torch.float64, solver='pcg',
+                        pcg_tol=1e-6, pcg_maxiter=300):
+    """compute_jacobians + solve_delta + unpack (bs:34-40, bs:110-248). Returns (dK, dP, dZ, dX, info)."""
+    J_cam, J_zcf, J_pts = K_.jacobians_with_rigs(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d_std,
+                                                 pix2d_dep, is_depth_log, float64=(dtype == torch.float64))
+    if not optim_Z_1st_cam:                                                           # bs:38
+        J_zcf[0, 0, 0] = 0
+    if not optim_Z0:                                                                  # bs:39
+        J_zcf[:, 0, 0:1] = 0
+    prob = Problem(rigs, pids, len(K), len(P_w2rig), len(pts3d), z_coefs.shape[1])
+    ne, g, params = build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=optim_K,
+                                           optim_P=optim_P, optim_Z=optim_Z, optim_X=optim_X,
+                                           no_grad_f_from_rz=no_grad_f_from_rz, dampen=dampen,
+                                           adaptive_dampen=adaptive_dampen)
+    info = dict(ne=ne, g=g, params=params)
+    if solver == 'pcg':
+        delta, niter, conv = solve_reduced_pcg(ne, g, tol=pcg_tol, maxiter=pcg_maxiter)
+        info.update(niter=niter, converged=conv)
+    else:
+        delta = solve_reduced_direct(ne, g)
+    delta = delta.to(torch.float32)                                                   # bs:182
+    info['delta'] = delta
+    return unpack_delta(delta, params, z_coefs.shape[1]) + (info,)
+
+
+def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d, depth_mode='log',
+            pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12, min_loss_delta=1e-4,
+            weight_z=1, optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True,
+            no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float64, solver='pcg', verbose=False):
+    """en:206-334 on CPU. Returns (update dict, BA_Status, info)."""
+    assert depth_mode in ('lin', 'log')
+    is_depth_log = depth_mode == 'log'
+    obj = lambda K, P_w2rig, pts3d, z_coefs: objective(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d,
+                                                       pix2d_std, pix2d_dep, is_depth_log, weight_z, pnorm,
+                                                       clip_pix_err, huber_delta)
+    init_loss, init_residuals, w_pts = obj(K, P_w2rig, pts3d, z_coefs)
+    dK, dP, dZ, dX, info = linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs,
+                                               pts3d, init_residuals, w_pts, is_depth_log=is_depth_log,
+                                               optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P, optim_X=optim_X,
+                                               optim_Z0=optim_Z0, no_grad_f_from_rz=no_grad_f_from_rz,
+                                               dampen=dampen, adaptive_dampen=adaptive_dampen, dtype=dtype,
+                                               solver=solver)
+    update = {}
+    last_a = 1.0
+    scale = 1.0
+    trials = 0
+    for a in STEP_SCHEDULE:
+        trials += 1
+        update['K'] = update_K(K, dK * scale)
+        update['P_w2rig'] = K_.exp_se3(-(dP * scale)) @ P_w2rig
+        update['z_coefs'] = z_coefs - dZ * scale
+        update['pts3d'] = pts3d - dX * scale
+        new_loss, new_residuals, _ = obj(**update)
+        if new_loss.isnan():
+            new_loss = init_loss
+        new_loss = new_loss + min_loss_delta
+        degenerate = float(reproj_score(new_residuals)) < min_reproj
+        if new_loss < init_loss and not degenerate:
+            break
+        scale = scale * (a / last_a)     # delta *= a / last_a (en:330) applied to every slice
+        last_a = a
+    info['trials'] = trials
+    info['scale'] = scale
+    return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals), info

@@ -1,0 +1,237 @@
+"""GPU parity: libba_hip.so against the CPU oracle on identical seeded inputs.
+
+Tolerances (norm-wise relative, ||gpu - oracle|| / ||oracle||):
+  * fp32 residuals / Huber errors / weights: 1e-5 (the reference computes them in fp32)
+  * fp64 Jacobian blocks: 1e-9 (same fp64 formula from the same fp32 inputs)
+  * reduced-system blocks S, rhs, point blocks: 1e-5 (fp64, differences come from the
+    fp32 residual/weight rounding of logf/powf on either side)
+  * PCG step and LM update: 1e-4 on delta and on J.delta (the north-star step tolerance)
+"""
+import pytest
+import torch
+
+from blast3r_amd import cujac
+from blast3r_amd.ba_solver import GaussNewtonSolver
+from blast3r_amd import engine as gpu_engine
+from blast3r_amd.synthetic import make_problem
+from oracle import kernels as ok
+from oracle import solver as osol
+from oracle import engine as oeng
+from tests.helpers import rel_err, tiny_problem, opts
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda:0'
+
+
+def _gpu(p):
+    return p.to(DEV)
+
+
+def _oracle_res(p, pnorm=1.0, **kw):
+    o = opts(p)
+    o.update(kw)
+    return ok.residuals_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], pnorm, o['clip_pix_err'],
+                                  o['huber_delta'])
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 32, 2000), (2, 40, 3000), (4, 30, 2000)])
+def test_residuals_parity(cfg, nf, nt):
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    ref = _oracle_res(p)
+    assert out.shape == ref.shape == (p.n_obs, 9)
+    assert out.stride() == (1, p.n_obs)                    # transposed SoA view (.cu:1100)
+    for sl in (slice(0, 3), slice(3, 6), slice(6, 9)):
+        assert rel_err(out[:, sl], ref[:, sl]) < 1e-5
+    # pnorm = -1 -> 3 outputs only
+    out3 = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                             g.pix2d, g.pix2d_std, g.pix2d_dep, True)
+    assert out3.shape == (p.n_obs, 3)
+    assert rel_err(out3, ref[:, :3]) < 1e-5
+
+
+def test_residuals_invalid_depth_rows_are_zero():
+    p = tiny_problem()
+    P = p.P_w2rig.clone()
+    P[0, 2, 3] -= 100.0           # push every point of image 0 behind the camera
+    p.P_w2rig = P
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta']).cpu()
+    n0 = int(p.infos[0, 0])
+    assert n0 > 0 and torch.all(out[:n0] == 0)
+    assert torch.any(out[n0:] != 0)
+
+
+@pytest.mark.parametrize('float64', [True, False])
+def test_jacobians_parity(float64):
+    p = make_problem(0, n_frames=10, n_tracks=500)
+    g = _gpu(p)
+    Jg = cujac.compute_jacobians_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                           g.pix2d_std, g.pix2d_dep, True, float64=float64)
+    Jr = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d_std,
+                                p.pix2d_dep, True, float64=float64)
+    tol = 1e-9 if float64 else 1e-5
+    for a, b in zip(Jg, Jr):
+        assert a.dtype == b.dtype and a.shape == b.shape
+        assert rel_err(a, b) < tol
+
+
+def test_compat_ops():
+    torch.manual_seed(0)
+    # chol3x3_solve
+    A = torch.randn(100, 3, 5, dtype=torch.float64)
+    H = A @ A.transpose(1, 2)
+    b = torch.randn(100, 3, dtype=torch.float64)
+    for dt in (torch.float64, torch.float32):
+        x = cujac.chol3x3_solve(H.to(DEV, dt), b.to(DEV, dt)).cpu()
+        assert rel_err(x, ok.chol3x3_solve(H.to(dt), b.to(dt))) < (1e-12 if dt == torch.float64 else 1e-4)
+    # blockcoo_matvec, both orientations and index dtypes
+    blocks = torch.randn(50, 3, 6, dtype=torch.float64)
+    rows = torch.randint(0, 7, (50,))
+    cols = torch.randint(0, 9, (50,))
+    for idt in (torch.int32, torch.int64):
+        for tr in (False, True):
+            x = torch.randn(7 * 3 if tr else 9 * 6, dtype=torch.float64)
+            y = cujac.blockcoo_matvec(blocks.to(DEV), rows.to(DEV, idt), cols.to(DEV, idt), x.to(DEV), 7, 9, tr)
+            yr = ok.blockcoo_matvec(blocks, rows, cols, x, 7, 9, tr)
+            assert rel_err(y, yr) < 1e-12
+    # fused_einsum_bki_bkj including the (5, 6, 1) case missing from the reference dispatch
+    for (I, J, K) in [(5, 6, 1), (3, 6, 3), (9, 9, 1), (2, 6, 3), (17, 17, 1)]:
+        L = torch.randn(40, K, I, dtype=torch.float64)
+        R = torch.randn(40, K, J, dtype=torch.float64)
+        assert rel_err(cujac.fused_einsum_bki_bkj(L.to(DEV), R.to(DEV)), ok.fused_einsum_bki_bkj(L, R)) < 1e-12
+    # exp_se3 against torch.matrix_exp of the hat matrix (fp32)
+    xi = torch.randn(64, 6) * torch.tensor([0.3, 0.3, 0.3, 1.0, 1.0, 1.0])
+    xi[:4, :3] *= 1e-6
+    assert rel_err(cujac.exp_se3(xi.to(DEV)), ok.exp_se3(xi)) < 1e-6
+
+
+def _oracle_ne(p, **flags):
+    o = opts(p)
+    loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'],
+                                  o['huber_delta'])
+    Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                        p.pix2d_std, p.pix2d_dep, True, float64=True)
+    if not flags.get('optim_Z0', True):
+        Jz[:, 0, 0] = 0
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    f = {k: v for k, v in flags.items() if k in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'no_grad_f_from_rz')}
+    ne, gvec, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, **f)
+    return ne, gvec, params, (Jc, Jz, Jp), res, w
+
+
+def _gpu_solver(p, **flags):
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
+                           no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False))
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    fl = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in flags.items()
+          if k in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'optim_Z0')}
+    J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                             g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **fl)
+    delta = gs.solve_delta(J, res, w)
+    return gs, delta, g
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 8, 200), (2, 20, 400)])
+def test_reduced_system_parity(cfg, nf, nt):
+    """S = H_cc - H_cp H_pp^-1 H_pc (damped, reference unknown order) and rhs against the oracle."""
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    ne, gvec, params, _, _, _ = _oracle_ne(p)
+    S_ref = osol.dense_schur(ne)
+    rhs_ref = osol.reduced_rhs(ne, gvec)
+    gs, delta, _ = _gpu_solver(p)
+    S, rhs = gs.reduced_system_dense()
+    assert S.shape == S_ref.shape
+    assert rel_err(S, S_ref) < 1e-5
+    assert rel_err(rhs, rhs_ref) < 1e-5
+    assert rel_err(S, S.T) < 1e-12                     # symmetric by construction
+    # point blocks and their damping
+    T = p.n_tracks
+    H = gs.last['Hpp'][:T].cpu()
+    Hr = ne.leaves['pts'] - float(gs.last['lam_p'].cpu()) * torch.eye(3, dtype=torch.float64)
+    iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
+    Hr6 = torch.stack([Hr[:, i, j] for i, j in iu], 1)
+    assert rel_err(H, Hr6) < 1e-5
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (2, 24, 800)])
+def test_pcg_step_parity(cfg, nf, nt):
+    """delta from the device PCG against the oracle restatement of _pcg (same iterations)."""
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    ne, gvec, params, (Jc, Jz, Jp), res, w = _oracle_ne(p)
+    d_ref, it_ref, conv_ref = osol.solve_reduced_pcg(ne, gvec)
+    gs, delta, _ = _gpu_solver(p)
+    ist = gs.last['istate'].cpu()
+    assert int(ist[3]) == int(conv_ref)
+    if conv_ref:
+        assert abs(int(ist[2]) - it_ref) <= 2
+    d_ref32 = d_ref.to(torch.float32)
+    assert rel_err(delta, d_ref32) < 1e-4
+    # gauge-invariant check: the predicted residual change J.delta
+    from oracle.dense import dense_jacobian
+    Jd = dense_jacobian(Jc, Jz, Jp, p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks)
+    sW = w.clamp(1e-6, 1e6).reshape(-1).double().sqrt()
+    assert rel_err(sW[:, None] * Jd @ delta.cpu().double(), sW[:, None] * Jd @ d_ref) < 1e-4
+
+
+def test_solver_flags_parity():
+    """optim_K / optim_P off (depth stitching), optim_X off, tensor masks, optim_Z0 off."""
+    p = make_problem(4, n_frames=10, n_tracks=300)
+    cases = [dict(optim_K=False, optim_P=False),
+             dict(optim_X=False),
+             dict(optim_Z0=False),
+             dict(no_grad_f_from_rz=True),
+             dict(optim_P=torch.tensor([True] * 5 + [False] * 5)),
+             dict(optim_Z=torch.tensor([False] * 3 + [True] * 7))]
+    for flags in cases:
+        ne, gvec, params, _, _, _ = _oracle_ne(p, **flags)
+        d_ref, _, _ = osol.solve_reduced_pcg(ne, gvec)
+        gs, delta, _ = _gpu_solver(p, **flags)
+        assert delta.shape == d_ref.shape, flags
+        assert rel_err(delta, d_ref.to(torch.float32)) < 1e-4, flags
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 30, 1500), (4, 20, 800)])
+def test_lm_step_parity(cfg, nf, nt):
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+              optim_P=o['optim_P'])
+    up_r, st_r, info = oeng.lm_step(**p.lm_inputs(), **kw)
+    g = _gpu(p)
+    up_g, st_g = gpu_engine.lm_step(**g.lm_inputs(), **kw)
+    assert abs(float(st_g.init_loss) - float(st_r.init_loss)) <= 1e-5 * abs(float(st_r.init_loss))
+    assert abs(float(st_g.new_loss) - float(st_r.new_loss)) <= 1e-4 * abs(float(st_r.new_loss))
+    for k in ('K', 'z_coefs', 'pts3d', 'P_w2rig'):
+        assert rel_err(up_g[k] - g.lm_inputs()[k] if k != 'P_w2rig' else up_g[k], (up_r[k] - p.lm_inputs()[k])
+                       if k != 'P_w2rig' else up_r[k]) < 1e-3, k
+    assert rel_err(st_g.new_residuals, st_r.new_residuals) < 1e-4
+
+
+def test_objective_reproj_exact():
+    p = make_problem(0, n_frames=12, n_tracks=1000)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    r = gpu_engine.reproj_score(out[:, :3])
+    ref = oeng.reproj_score(out[:, :3].cpu())
+    assert abs(float(r) - float(ref)) <= 1e-6 * abs(float(ref))
+    loss, _ = gpu_engine._objective(out.T, p.n_obs, True)
+    assert abs(float(loss) - float(out[:, 3:6].cpu().double().mean())) <= 1e-6 * float(loss)

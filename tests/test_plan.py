@@ -1,0 +1,178 @@
+"""Structure plan (host C++ in libba_hip.so, no GPU needed) and a CPU emulation of the
+fused Schur data flow driven by the plan's metadata.
+
+The emulation takes per-observation blocks from the oracle (fp64), accumulates
+them exactly the way k_schur / k_pair_reduce route them (batch slots, local
+orientation, transposition flags, deterministic CSR order) and must reproduce the
+oracle's dense Schur complement: this pins the plan metadata independently of the
+GPU arithmetic.
+"""
+import numpy as np
+import pytest
+import torch
+
+from blast3r_amd.plan import BAPlan
+from blast3r_amd.synthetic import make_problem
+from oracle import kernels as ok
+from oracle import solver as osol
+from oracle import engine as oeng
+from tests.helpers import rel_err, opts
+
+
+def _plan(p, **kw):
+    return BAPlan(p.infos, p.pids, p.n_tracks, device='cpu', **kw)
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 6, 60, {}), (0, 32, 3000, {}), (1, 40, 4000, {}), (2, 60, 6000, {}),
+                                          (2, 60, 6000, dict(max_batch_obs=500)), (0, 12, 500, dict(max_slots=40))])
+def test_plan_invariants(cfg, nf, nt, kw):
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    pl = _plan(p, **kw)
+    h, sc = pl.host, pl.scalars
+    CH = 128
+    obs = h['chunk_obs']
+    assert obs.size == sc['n_chunks'] * CH
+    # every observation exactly once
+    seen = np.sort(obs[obs >= 0])
+    assert np.array_equal(seen, np.arange(p.n_obs))
+    pids = p.pids.numpy()
+    img = pl.obs_img
+    meta = h['chunk_meta'].reshape(-1, 4)
+    slot_pair = h['slot_pair']
+    for ck in range(sc['n_chunks']):
+        b, f, n, used = meta[ck]
+        imgs = h['b_imgs'][b * pl.L:(b + 1) * pl.L]
+        info = h['slot_info'][ck * CH:(ck + 1) * CH]
+        o = obs[ck * CH:(ck + 1) * CH]
+        assert np.all(o[used:] == -1) and np.all(o[:used] >= 0)
+        covered = set()
+        for t in range(n):
+            first, m, pid, mask = h['ct_first'][f + t], h['ct_m'][f + t], h['ct_pid'][f + t], h['ct_mask'][f + t]
+            tob = o[first:first + m]
+            assert np.all(pids[tob] == pid)
+            assert m == np.sum(pids == pid)                 # whole track inside one chunk
+            li = info[first:first + m] & 0xff
+            assert np.all(imgs[li] == img[tob])
+            assert mask == np.bitwise_or.reduce(1 << li)
+            assert np.all((info[first:first + m] >> 8) & 0xff == t)
+            lead = info[first:first + m] >> 16
+            assert np.all(img[o[lead]] == img[tob])        # leader shares the image
+            ls = sorted(set(li.tolist()))
+            covered |= {(min(x, y), max(x, y)) for x in ls for y in ls}
+        slots = {(s & 0xff, (s >> 8) & 0xff) for s in slot_pair[h['b_slot_ptr'][b]:h['b_slot_ptr'][b + 1]]}
+        assert covered <= slots
+        assert len(slots) <= 96
+    # every slot appears exactly once among the pair sources, with the right orientation flag
+    src = h['pair_src']
+    assert np.array_equal(np.sort(src >> 1), np.arange(sc['n_slots']))
+    for q in range(sc['n_pairs']):
+        i1, i2 = h['pair_i1'][q], h['pair_i2'][q]
+        assert i1 <= i2
+        for e in src[h['pair_ptr'][q]:h['pair_ptr'][q + 1]]:
+            s = e >> 1
+            b = np.searchsorted(h['b_slot_ptr'], s, side='right') - 1
+            a, c = slot_pair[s] & 0xff, (slot_pair[s] >> 8) & 0xff
+            ga, gc = h['b_imgs'][b * pl.L + a], h['b_imgs'][b * pl.L + c]
+            assert (min(ga, gc), max(ga, gc)) == (i1, i2)
+            assert (e & 1) == int(ga > gc)
+
+
+def test_plan_errors():
+    p = make_problem(0, n_frames=8, n_tracks=50)
+    with pytest.raises(RuntimeError, match='max_local_imgs'):
+        BAPlan(p.infos, p.pids, p.n_tracks, device='cpu', max_local_imgs=2)
+    bad = p.pids.clone()
+    bad[0] = p.n_tracks + 3
+    with pytest.raises(RuntimeError, match='pid out of range'):
+        BAPlan(p.infos, bad, p.n_tracks, device='cpu')
+
+
+def _chol3(H, lam, jit=1e-12):
+    """chol3x3 rules (.cu:560-634) on a (T,3,3) batch, returns lower factors."""
+    A = H + (lam + jit) * torch.eye(3, dtype=H.dtype)
+    return torch.linalg.cholesky(A)
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 10, 300), (2, 30, 600)])
+def test_schur_emulation_matches_oracle(cfg, nf, nt):
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = opts(p)
+    loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'],
+                                  o['huber_delta'])
+    Jc8, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                         p.pix2d_std, p.pix2d_dep, True, float64=True)
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    ne, gvec, params = osol.build_normal_equations(prob, Jc8, Jz, Jp, res, w)
+    S_ref = osol.dense_schur(ne)
+
+    C = p.C
+    d = 8 + C
+    N = p.n_obs
+    W = w.clamp(1e-6, 1e6)
+    sW = torch.sqrt(W).double()
+    Jc = torch.zeros((N, 3, d), dtype=torch.float64)
+    Jc[:, :, :8] = Jc8
+    Jc[:, 2, 8:] = Jz[:, 0]
+    Jc = Jc * sW[:, :, None]
+    Jpw = Jp * sW[:, :, None]
+    H = torch.zeros((p.n_tracks, 3, 3), dtype=torch.float64)
+    H.index_add_(0, p.pids.long(), Jpw.transpose(1, 2) @ Jpw)
+    lam = 1e-12 * H.diagonal(dim1=-1, dim2=-2).abs().max()
+    Lf = _chol3(H, lam)
+    Hcp = Jc.transpose(1, 2) @ Jpw                                      # (N, d, 3)
+    V = torch.linalg.solve_triangular(Lf[p.pids.long()], Hcp.transpose(1, 2), upper=False).transpose(1, 2)
+
+    pl = _plan(p)
+    h, sc = pl.host, pl.scalars
+    partial = np.zeros((sc['n_slots'], d, d))
+    obs = h['chunk_obs']
+    meta = h['chunk_meta'].reshape(-1, 4)
+    Vn, Jn = V.numpy(), Jc.numpy()
+    for b in range(sc['n_batches']):
+        s0, s1 = h['b_slot_ptr'][b], h['b_slot_ptr'][b + 1]
+        for ck in range(h['b_chunk_ptr'][b], h['b_chunk_ptr'][b + 1]):
+            _, f, n, used = meta[ck]
+            info = h['slot_info'][ck * 128:(ck + 1) * 128]
+            ob = obs[ck * 128:(ck + 1) * 128]
+            for s in range(s0, s1):
+                a, c = h['slot_pair'][s] & 0xff, (h['slot_pair'][s] >> 8) & 0xff
+                for t in range(n):
+                    mask = h['ct_mask'][f + t]
+                    if not ((mask >> a) & 1 and (mask >> c) & 1):
+                        continue
+                    first, m = h['ct_first'][f + t], h['ct_m'][f + t]
+                    li = info[first:first + m] & 0xff
+                    Va = Vn[ob[first:first + m][li == a]].sum(0)
+                    Vc = Vn[ob[first:first + m][li == c]].sum(0)
+                    partial[s] -= Va @ Vc.T
+                if a == c:
+                    sel = ob[(np.arange(128) < used) & ((info & 0xff) == a)]
+                    partial[s] += np.einsum('nri,nrj->ij', Jn[sel], Jn[sel])
+    S_pairs = np.zeros((sc['n_pairs'], d, d))
+    for q in range(sc['n_pairs']):
+        for e in h['pair_src'][h['pair_ptr'][q]:h['pair_ptr'][q + 1]]:
+            S_pairs[q] += partial[e >> 1].T if (e & 1) else partial[e >> 1]
+    # image-level -> reference unknown order (mono focal, no rigs)
+    nf_, nt_ = 2 * len(p.K), 6 * len(p.P_w2rig)
+    cam, node = p.infos[2].long().numpy(), p.infos[1].long().numpy()
+    n_c = nf_ + nt_ + C * p.n_imgs
+    um = np.zeros((p.n_imgs, d), dtype=np.int64)
+    for i in range(p.n_imgs):
+        um[i, :2] = cam[i] * 2 + np.arange(2)
+        um[i, 2:8] = nf_ + node[i] * 6 + np.arange(6)
+        um[i, 8:] = nf_ + nt_ + i * C + np.arange(C)
+    S = np.zeros((n_c, n_c))
+    for q in range(sc['n_pairs']):
+        i1, i2 = h['pair_i1'][q], h['pair_i2'][q]
+        np.add.at(S, (um[i1][:, None], um[i2][None, :]), S_pairs[q])
+        if i1 != i2:
+            np.add.at(S, (um[i2][:, None], um[i1][None, :]), S_pairs[q].T)
+    dg = np.diag(S_ref.numpy() - S)        # the damping is the only remaining difference
+    Sd = torch.from_numpy(S) + torch.diag(torch.from_numpy(dg))
+    assert rel_err(Sd, S_ref) < 1e-10
+    # the difference is a per-leaf constant 1e-12 * max|diag(H_cc leaf)|
+    for name, sl in (('foc', slice(0, nf_)), ('tau', slice(nf_, nf_ + nt_)), ('zcf', slice(nf_ + nt_, n_c))):
+        leaf = ne.leaves[name]
+        lam_leaf = float(leaf.diagonal(dim1=-1, dim2=-2).abs().max()) * 1e-12
+        assert np.allclose(dg[sl], lam_leaf, rtol=1e-2, atol=0)   # rounding noise ~1e-16 * |S_ii|
