@@ -1,0 +1,178 @@
+"""Benchmark of the bundle-adjustment linearize + Schur path on one MI355X.
+
+A "step" is one fused linearize + Schur-reduce pass (ba_linearize_schur: point
+blocks, camera-pair Schur blocks, rhs, deterministic reductions) over the whole
+synthetic problem, inputs resident in HBM.  The default workload is benchmark
+config 2: 1024 frames, 1M tracks on contiguous windows of 4..12 frames
+(~8M observations), log-depth with K=4 channels (C=5 z-coefficients), focal +
+pose + depth coefficients + points optimised.
+
+Prints one JSON line: value = observations per second of the linearize + Schur
+pass; LM iterations per second of the full lm_step are reported beside it, as
+are the roofline of the dominant kernel (k_schur, timed with events on its own
+launch stream) and the CPU oracle timed on a bounded sample of the same
+workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--config', type=int, default=2)
+    ap.add_argument('--frames', type=int, default=None)
+    ap.add_argument('--tracks', type=int, default=None)
+    ap.add_argument('--lm-steps', type=int, default=3)
+    ap.add_argument('--cpu-baseline', type=int, default=1)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one MI355X: multi-GPU runs are not part of this build '
+              '(the path would shard by track with one all-reduce of the reduced system; see DESIGN.md)',
+              file=sys.stderr)
+        sys.exit(2)
+
+    from blast3r_amd import cujac
+    from blast3r_amd._lib import check, lib
+    from blast3r_amd.ba_solver import GaussNewtonSolver
+    from blast3r_amd import engine
+    from blast3r_amd.synthetic import make_problem
+
+    dev = torch.device('cuda:0')
+    t0 = time.time()
+    prob = make_problem(args.config, n_frames=args.frames, n_tracks=args.tracks)
+    log(f'[bench] generated cfg {args.config}: {prob.n_imgs} frames, {prob.n_tracks} tracks, {prob.n_obs} obs, '
+        f'C={prob.C} in {time.time() - t0:.1f}s')
+    g = prob.to(dev)
+    o = prob.options
+    hp = dict(weight_z=o['weight_z'], pnorm=o['pnorm'], max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d,
+                                            g.pix2d_std, g.pix2d_dep, True, hp['weight_z'], hp['pnorm'],
+                                            hp['max_pix_err'], hp['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev)
+    J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                             g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
+    from blast3r_amd.ba_solver import _param_state
+    res._ba_state = _param_state(J)
+    t0 = time.time()
+    ctx = gs.prepare(J, res, w)
+    torch.cuda.synchronize()
+    log(f'[bench] plan + slot data in {time.time() - t0:.1f}s: {ctx["plan"].scalars}')
+    a, st = ctx['args'], ctx['stream']
+    L = lib()
+
+    def step(ev=None):
+        check(L.ba_linearize_stage(a, 0, st))
+        if ev is not None:
+            ev[0].record()
+        check(L.ba_linearize_stage(a, 1, st))
+        if ev is not None:
+            ev[1].record()
+        check(L.ba_linearize_stage(a, 2, st))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    schur_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / args.steps
+    n_obs = prob.n_obs
+    value = n_obs / (ms_step * 1e-3)
+    log(f'[bench] linearize+Schur {ms_step:.3f} ms/step, k_schur {schur_ms:.3f} ms -> {value:.4g} obs/s')
+
+    # roofline of the dominant kernel (k_schur)
+    sc = ctx['plan'].scalars
+    d, C = ctx['lay']['d'], prob.C
+    T = prob.n_tracks
+    bytes_alg = n_obs * (20 + 4 * C) + T * (12 + 72) + sc['n_slots'] * d * d * 8 + sc['n_batches'] * 16 * 2 * d * 8
+    flops_pairs = (sc['n_pair_terms'] + n_obs) * 6 * d * d
+    achieved_tf = flops_pairs / (schur_ms * 1e-3) / 1e12
+    achieved_gbs = bytes_alg / (schur_ms * 1e-3) / 1e9
+
+    # full LM iterations
+    lm_ms = None
+    if args.lm_steps > 0:
+        kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
+                  optim_P=o['optim_P'])
+        engine.lm_step(**g.lm_inputs(), **kw)          # warm (plan cached after this)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.lm_steps):
+            engine.lm_step(**g.lm_inputs(), **kw)
+        torch.cuda.synchronize()
+        lm_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
+        log(f'[bench] lm_step {lm_ms:.2f} ms')
+
+    cpu = None
+    if args.cpu_baseline:
+        cpu = cpu_baseline(args.config)
+        log(f'[bench] cpu baseline {cpu}')
+
+    line = {
+        'metric': 'BA linearize+Schur obs/sec & LM iters/sec at 1024 frames; % HBM roofline',
+        'value': value, 'unit': 'obs/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'ms_per_step': ms_step, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f64',
+        'data': 'synthetic (seeded generator, benchmark config %d)' % args.config,
+        'config': {'workload': f'cfg{args.config}: {prob.n_imgs} frames, {T} tracks, {n_obs} observations, '
+                               f'C={C}, d={d} image-level parameters', 'frames': prob.n_imgs, 'tracks': T,
+                   'observations': n_obs, 'C': C},
+        'lm_iters_per_s': (1e3 / lm_ms) if lm_ms else None,
+        'lm_ms_per_iter': lm_ms,
+        'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
+                     'frac': achieved_tf / 78.6, 'traffic': None, 'kernel': 'k_schur',
+                     'kernel_ms': schur_ms, 'flops_per_launch': flops_pairs},
+        'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
+                         'bytes_per_launch': bytes_alg, 'kernel': 'k_schur'},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(cfg, budget_obs=600_000):
+    """Oracle (torch-CPU restatement of the reference's linearisation + normal equations +
+    Schur rhs) on a bounded sample of the same configuration, timed on this host."""
+    import oracle.kernels as ok
+    import oracle.solver as osol
+    import oracle.engine as oeng
+    from blast3r_amd.synthetic import make_problem
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    frames = {0: 32, 1: 64, 2: 128, 3: 256, 4: 128}[cfg]
+    tracks = {0: 20_000, 1: 50_000, 2: 75_000, 3: 40_000, 4: 75_000}[cfg]
+    p = make_problem(cfg, n_frames=frames, n_tracks=tracks)
+    o = p.options
+    t0 = time.perf_counter()
+    loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], o['pnorm'], o['clip_pix_err'],
+                                  o['huber_delta'])
+    Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                        p.pix2d_std, p.pix2d_dep, True, float64=True)
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_K=o['optim_K'], optim_P=o['optim_P'])
+    rhs = osol.reduced_rhs(ne, g)
+    dt = time.perf_counter() - t0
+    return {'value': p.n_obs / dt, 'unit': 'obs/s', 'cores': threads, 'kind': 'port',
+            'sample': f'cfg{cfg} scaled to {frames} frames / {tracks} tracks ({p.n_obs} obs): residuals, fp64 '
+                      f'Jacobians, normal equations and Schur rhs in the oracle, {dt:.2f} s'}
+
+
+if __name__ == '__main__':
+    main()

@@ -87,6 +87,7 @@ _SIGS = {
     'ba_plan_destroy': (None, [c_p]),
     'ba_plan_last_error': (ctypes.c_char_p, []),
     'ba_linearize_schur': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
+    'ba_linearize_stage': (c_int, [ctypes.POINTER(BaLinArgs), c_int, c_p]),
     'ba_backsubstitute': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
     'ba_pcg_solve': (c_int, [ctypes.POINTER(BaPcgArgs), c_p]),
     'ba_pcg_partials_size': (c_i64, [c_i64]),

@@ -175,6 +175,18 @@ class GaussNewtonSolver:
     # ------------------------------------------------------------------ bs:110-182
     def solve_delta(self, J, residuals, w_pts, clamp_w=(1e-6, 1e6), z_prior=None):
         """Solve (J^T W J + damping) delta = J^T W r by Schur reduction; returns fp32 delta."""
+        ctx = self.prepare(J, residuals, w_pts, clamp_w)
+        st = ctx['stream']
+        if ctx['lay']['d'] > 0:
+            check(lib().ba_linearize_schur(ctx['args'], st))
+        else:
+            ctx['S_pairs'].zero_(); ctx['e_img'].zero_(); ctx['dg_img'].zero_()
+        if z_prior is not None:
+            self._add_z_prior(z_prior, ctx['lay'], ctx['plan'], ctx['S_pairs'], ctx['e_img'], ctx['dg_img'])
+        return self.reduce_and_backsubstitute(J, ctx)
+
+    def prepare(self, J, residuals, w_pts, clamp_w=(1e-6, 1e6)):
+        """Plan, workspaces and the ba_lin_args of one linearisation (no kernel launched)."""
         assert isinstance(J, Linearization)
         assert J.shape == (3 * self.n_kpts, self.cams.n * N_FOC + self.nodes.n * N_TAU + self.imgs.n * self.n_zcf +
                            self.tracks.n * 3)
@@ -246,15 +258,18 @@ class GaussNewtonSolver:
             a.r_in, a.w_in = ptr(residuals), ptr(W)
             a.r_s0, a.r_s1 = residuals.stride(0), residuals.stride(1)
             a.w_s0, a.w_s1 = W.stride(0), W.stride(1)
-        st = stream_ptr(dev)
-        if d > 0:
-            check(lib().ba_linearize_schur(a, st))
-        else:
-            S_pairs.zero_(); e_img.zero_(); dg_img.zero_()
-        if z_prior is not None:
-            self._add_z_prior(z_prior, lay, plan, S_pairs, e_img, dg_img)
+        return dict(args=a, stream=stream_ptr(dev), lay=lay, plan=plan, S_pairs=S_pairs, e_img=e_img, dg_img=dg_img,
+                    Hpp=Hpp, gp=gp, lam_p=lam_p, keep=(s_pix, s_std, s_dep, W, residuals))
 
-        # reduced solve
+    def reduce_and_backsubstitute(self, J, ctx):
+        """Device PCG on the reduced system and point back-substitution; returns fp32 delta."""
+        a, st, lay, plan = ctx['args'], ctx['stream'], ctx['lay'], ctx['plan']
+        S_pairs, e_img, dg_img = ctx['S_pairs'], ctx['e_img'], ctx['dg_img']
+        Hpp, gp, lam_p = ctx['Hpp'], ctx['gp'], ctx['lam_p']
+        dev, d, sc, pd, ws = self.device, lay['d'], plan.scalars, plan.dev, plan.workspace
+        en = J.en
+        T = self.tracks.true_n
+        n_imgs = self.imgs.true_n
         um = self._unknown_maps(J, lay, plan)
         n_u = um['n_u']
         x = torch.zeros(max(n_u, 1), dtype=torch.float64, device=dev)

@@ -541,7 +541,18 @@ static inline unsigned nblk(int64_t n, int t) { return (unsigned)((n + t - 1) / 
         else                          { constexpr int HK_ = 0, HP_ = 0; __VA_ARGS__; } \
     } while (0)
 
+extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream);
+
 extern "C" int ba_linearize_schur(const ba_lin_args* args, void* stream) {
+    for (int s = 0; s < 3; ++s) {
+        int rc = ba_linearize_stage(args, s, stream);
+        if (rc) return rc;
+    }
+    return BA_OK;
+}
+
+// stage 0: point blocks + damping value; 1: camera-pair batches; 2: deterministic reductions
+extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
     const ba_lin_args& a = *args;
@@ -552,16 +563,19 @@ extern "C" int ba_linearize_schur(const ba_lin_args* args, void* stream) {
                "inconsistent image-level layout");
     BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "fused path supports at most 24 z-coefficient columns");
     BA_REQUIRE(a.L >= 1 && a.L <= BA_MAX_LOCAL, "bad plan L");
-    if (a.n_chunks == 0) {
+    if (stage == 0 && a.n_chunks == 0) {
         BA_HIP(hipMemsetAsync(a.lam_p, 0, sizeof(double), st));
-    } else {
+    } else if (stage == 0) {
         BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0, st, a));
         BA_LAUNCHED();
     }
-    hipLaunchKernelGGL(k_lam_reduce, dim3(1), dim3(256), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen, a.lay.adaptive,
-                       a.lay.x_off, a.lam_p);
-    BA_LAUNCHED();
-    if (a.n_batches > 0) {
+    if (stage == 0) {
+        hipLaunchKernelGGL(k_lam_reduce, dim3(1), dim3(256), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen,
+                           a.lay.adaptive, a.lay.x_off, a.lam_p);
+        BA_LAUNCHED();
+        return BA_OK;
+    }
+    if (stage == 1 && a.n_batches > 0) {
         size_t lds = (size_t)BA_CHUNK * 8 * a.lay.d * sizeof(double);
         BA_DISPATCH_KP(a.lay, {
             BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -570,6 +584,7 @@ extern "C" int ba_linearize_schur(const ba_lin_args* args, void* stream) {
         });
         BA_LAUNCHED();
     }
+    if (stage == 1) return BA_OK;
     int d = a.lay.d;
     if (a.n_pairs > 0) {
         hipLaunchKernelGGL(k_pair_reduce, dim3(nblk(a.n_pairs * d * d, 256)), dim3(256), 0, st, a.pair_ptr, a.pair_src,

@@ -127,6 +127,10 @@ typedef struct {
  * Requires d <= 16 and C <= 24. */
 int ba_linearize_schur(const ba_lin_args* args, void* stream);
 
+/* The same work split in its three launch groups (callers that time the camera-pair
+ * kernel on its own): 0 point blocks + damping, 1 camera-pair batches, 2 reductions. */
+int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream);
+
 /* Stage 4b: delta_p = (H_pp + lam_p I)^-1 (g_p - H_pc delta_c) per track, written to dX
  * (n_tracks,3) fp32 (and dX64 if not NULL); dc is the reduced solution, umap the
  * (n_imgs, d) image-parameter -> unknown index map (-1 = inactive). */

@@ -191,14 +191,16 @@ def test_pcg_step_parity(cfg, nf, nt):
 
 def test_solver_flags_parity():
     """optim_K / optim_P off (depth stitching), optim_X off, tensor masks, optim_Z0 off."""
-    p = make_problem(4, n_frames=10, n_tracks=300)
-    cases = [dict(optim_K=False, optim_P=False),
-             dict(optim_X=False),
-             dict(optim_Z0=False),
-             dict(no_grad_f_from_rz=True),
-             dict(optim_P=torch.tensor([True] * 5 + [False] * 5)),
-             dict(optim_Z=torch.tensor([False] * 3 + [True] * 7))]
-    for flags in cases:
+    p4 = make_problem(4, n_frames=10, n_tracks=300)
+    p0 = make_problem(0, n_frames=10, n_tracks=300)
+    cases = [(p4, dict(optim_K=False, optim_P=False)),
+             (p0, dict(optim_X=False)),
+             (p0, dict(optim_Z0=False)),
+             (p0, dict(no_grad_f_from_rz=True)),
+             (p0, dict(optim_K=False)),
+             (p0, dict(optim_P=torch.tensor([True] * 5 + [False] * 5))),
+             (p0, dict(optim_Z=torch.tensor([False] * 3 + [True] * 7)))]
+    for p, flags in cases:
         ne, gvec, params, _, _, _ = _oracle_ne(p, **flags)
         d_ref, _, _ = osol.solve_reduced_pcg(ne, gvec)
         gs, delta, _ = _gpu_solver(p, **flags)
