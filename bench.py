@@ -36,6 +36,8 @@ def main():
     ap.add_argument('--tracks', type=int, default=None)
     ap.add_argument('--lm-steps', type=int, default=3)
     ap.add_argument('--cpu-baseline', type=int, default=1)
+    ap.add_argument('--copy-probe', action='store_true',
+                    help='run one 256 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: multi-GPU runs are not part of this build '
@@ -97,6 +99,13 @@ def main():
     n_obs = prob.n_obs
     value = n_obs / (ms_step * 1e-3)
     log(f'[bench] linearize+Schur {ms_step:.3f} ms/step, k_schur {schur_ms:.3f} ms -> {value:.4g} obs/s')
+
+    if args.copy_probe:
+        src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     # roofline of the dominant kernel (k_schur)
     sc = ctx['plan'].scalars

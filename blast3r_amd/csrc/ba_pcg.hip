@@ -42,18 +42,23 @@ __device__ __forceinline__ double sum_partials(const double* __restrict__ part, 
     return block_sum(v, sh);
 }
 
-// unknown-level rhs and diag(H_cc) from the image-level vectors
+// unknown-level rhs and diag(H_cc) from the image-level vectors; one wave per unknown so that
+// shared unknowns (one focal pair for every image of a camera) reduce in parallel
 __global__ void __launch_bounds__(PCG_T) k_unk_setup(ba_pcg_args a) {
-    int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);
     if (u >= a.n_u) return;
     double e = 0.0, g = 0.0;
-    for (int q = a.inv_ptr[u]; q < a.inv_ptr[u + 1]; ++q) {
+    for (int q = a.inv_ptr[u] + lane; q < a.inv_ptr[u + 1]; q += 64) {
         int src = a.inv_src[q];
         e += a.e_img[src];
         g += a.dg_img[src];
     }
-    a.rhs[u] = e;
-    a.diagA[u] = g;
+    for (int off = 32; off > 0; off >>= 1) {
+        e += __shfl_down(e, off);
+        g += __shfl_down(g, off);
+    }
+    if (lane == 0) { a.rhs[u] = e; a.diagA[u] = g; }
 }
 
 // per-leaf damping (BlockDiagMat.dampen_, ba_solver.py:575-582) and the Jacobi preconditioner.
@@ -119,50 +124,64 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
     }
 }
 
-// y_img[i][j] = sum over pair blocks of image row i of S_blk (j, :) . x_img
+// y_img[i][j] = sum over the pair blocks of image row i of S_blk(j, :) . x_img; one wave per
+// image: lane (g, j) takes output row j of every 4th block of the row, then the 4 groups add up
 __global__ void __launch_bounds__(PCG_T) k_spmv_img(ba_pcg_args a, const double* __restrict__ xin, int k) {
     if (a.istate[IS_DONE0 + (k & 1)]) return;
-    int64_t t = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+    const int lane = threadIdx.x & 63, grp = lane >> 4, j = lane & 15;
+    const int i = blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);
+    if (i >= a.n_imgs) return;
     const int d = a.d;
-    if (t >= (int64_t)a.n_imgs * d) return;
-    int i = (int)(t / d), j = (int)(t - (t / d) * d);
     double acc = 0.0;
-    for (int q = a.row_ptr[i]; q < a.row_ptr[i + 1]; ++q) {
-        int ent = a.row_ent[q];
-        int p = ent >> 1, tr = ent & 1;
-        int i2 = tr ? a.pair_i1[p] : a.pair_i2[p];
-        const double* blk = a.S_pairs + (int64_t)p * d * d;
-        const int* um = a.umap + (int64_t)i2 * d;
-        for (int j2 = 0; j2 < d; ++j2) {
-            int u2 = um[j2];
-            if (u2 >= 0) acc += (tr ? blk[j2 * d + j] : blk[j * d + j2]) * xin[u2];
+    if (j < d) {
+        for (int q = a.row_ptr[i] + grp; q < a.row_ptr[i + 1]; q += 4) {
+            int ent = a.row_ent[q];
+            int p = ent >> 1, tr = ent & 1;
+            int i2 = tr ? a.pair_i1[p] : a.pair_i2[p];
+            const double* blk = a.S_pairs + (int64_t)p * d * d;
+            const int* um = a.umap + (int64_t)i2 * d;
+            for (int j2 = 0; j2 < d; ++j2) {
+                int u2 = um[j2];
+                if (u2 >= 0) acc += (tr ? blk[j2 * d + j] : blk[j * d + j2]) * xin[u2];
+            }
         }
     }
-    a.y_img[t] = acc;
+    acc += __shfl_down(acc, 32);
+    acc += __shfl_down(acc, 16);
+    if (grp == 0 && j < d) a.y_img[(int64_t)i * d + j] = acc;
 }
 
-// Ap[u] = sum of image-level rows mapping to u + damp[u] p[u]; partial of p.Ap
+// Ap[u] = sum of the image-level rows mapping to u + damp[u] p[u] (one wave per unknown);
+// per-block partial of p.Ap
 __global__ void __launch_bounds__(PCG_T) k_spmv_unk(ba_pcg_args a, int k) {
-    __shared__ double sh[PCG_T];
+    __shared__ double sh[PCG_T / 64];
     if (a.istate[IS_DONE0 + (k & 1)]) return;
-    int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + w;
+    double s = 0.0;
+    if (u < a.n_u)
+        for (int q = a.inv_ptr[u] + lane; q < a.inv_ptr[u + 1]; q += 64) s += a.y_img[a.inv_src[q]];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off);
     double pap = 0.0;
-    if (u < a.n_u) {
-        double s = 0.0;
-        for (int q = a.inv_ptr[u]; q < a.inv_ptr[u + 1]; ++q) s += a.y_img[a.inv_src[q]];
+    if (lane == 0 && u < a.n_u) {
         s += a.damp[u] * a.p[u];
         a.Ap[u] = s;
         pap = a.p[u] * s;
     }
-    double bs = block_sum(pap, sh);
-    if (threadIdx.x == 0) a.partials[3 * blockIdx.x + 2] = bs;
+    if (lane == 0) sh[w] = pap;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int q = 0; q < PCG_T / 64; ++q) t += sh[q];
+        a.partials[3 * blockIdx.x + 2] = t;
+    }
 }
 
 // alpha = rz / max(p.Ap, 1e-32); x += alpha p; r -= alpha Ap; z = M^-1 r; partials r.r, r.z
-__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int nb, int k) {
+__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int nb, int nbw, int k) {
     __shared__ double sh[PCG_T];
     if (a.istate[IS_DONE0 + (k & 1)]) return;
-    double pap = sum_partials(a.partials, nb, 2, sh);
+    double pap = sum_partials(a.partials, nbw, 2, sh);
     double denom = pap > 1e-32 ? pap : 1e-32;
     double alpha = a.state[ST_RZ0 + (k & 1)] / denom;
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
@@ -223,7 +242,8 @@ using namespace ba;
 
 static inline unsigned nb_of(int64_t n) { return (unsigned)((n + PCG_T - 1) / PCG_T); }
 
-extern "C" int64_t ba_pcg_partials_size(int64_t n_u) { return 3 * (int64_t)nb_of(n_u < 1 ? 1 : n_u); }
+// partial sums: 3 per block of the widest launch (one wave per unknown)
+extern "C" int64_t ba_pcg_partials_size(int64_t n_u) { return 3 * (((n_u < 1 ? 1 : n_u) + 3) / 4) + 3; }
 
 extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     clear_error();
@@ -233,16 +253,17 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.maxiter >= 0, "bad sizes");
     if (a.n_u == 0) return BA_OK;
     const unsigned nb = nb_of(a.n_u);
-    const unsigned nbi = nb_of((int64_t)a.n_imgs * a.d);
-    hipLaunchKernelGGL(k_unk_setup, dim3(nb), dim3(PCG_T), 0, st, a);
+    const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown
+    const unsigned nbi = (unsigned)((a.n_imgs + PCG_T / 64 - 1) / (PCG_T / 64));     // wave per image
+    hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_leaf_damp, dim3(1), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
     BA_LAUNCHED();
     for (int it = 0; it < a.maxiter; ++it) {
         hipLaunchKernelGGL(k_spmv_img, dim3(nbi), dim3(PCG_T), 0, st, a, (const double*)a.p, it);
-        hipLaunchKernelGGL(k_spmv_unk, dim3(nb), dim3(PCG_T), 0, st, a, it);
-        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, it);
+        hipLaunchKernelGGL(k_spmv_unk, dim3(nbw), dim3(PCG_T), 0, st, a, it);
+        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, (int)nbw, it);
         hipLaunchKernelGGL(k_pcg_dir, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, it);
     }
     hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);

@@ -300,6 +300,8 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __shared__ CamF sCam[BA_MAX_LOCAL];
     __shared__ float sZc[BA_MAX_LOCAL * BA_MAX_C];
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
+    __shared__ unsigned char sLa[BA_MAX_SLOTS], sLb[BA_MAX_SLOTS];
+    __shared__ double sVec[BA_MAX_LOCAL * 2 * 16];       // per local image: rhs (d) | diag(H_cc) (d)
 
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -318,11 +320,18 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
     }
 
+    for (int q = tid; q < ns; q += BA_WAVES * 64) {
+        const int pr = a.slot_pair[s0 + q];
+        sLa[q] = (unsigned char)(pr & 0xff);
+        sLb[q] = (unsigned char)((pr >> 8) & 0xff);
+    }
+    for (int q = tid; q < BA_MAX_LOCAL * 2 * 16; q += BA_WAVES * 64) sVec[q] = 0.0;
+
     dbl4 acc[BA_SLOTS_PER_WAVE];
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) acc[q] = dbl4{0.0, 0.0, 0.0, 0.0};
-    const int va = tid >> 4, vj = tid & 15;       // per-image vector entry owned by this thread
-    double accE = 0.0, accD = 0.0;
+    // K-element of this lane in the three MFMAs of a 4-track group: k = 4*mm + lane/16
+    const int mi = lane & 15, kk = lane >> 4;
 
     const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
     for (int ck = c_begin; ck < c_end; ++ck) {
@@ -384,34 +393,59 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         }
         __syncthreads();
 
-        // camera-pair tiles owned by this wave
+        // camera-pair tiles: groups of 4 chunk tracks outermost, so that every owned slot the group
+        // covers gets its 3 MFMAs back to back on independent accumulators
+        for (int t0 = 0; t0 < n_ct; t0 += 4) {
+            const unsigned gm0 = sMask[t0];
+            const unsigned gm1 = t0 + 1 < n_ct ? sMask[t0 + 1] : 0u;
+            const unsigned gm2 = t0 + 2 < n_ct ? sMask[t0 + 2] : 0u;
+            const unsigned gm3 = t0 + 3 < n_ct ? sMask[t0 + 3] : 0u;
 #pragma unroll
-        for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-            const int sl = wave + BA_WAVES * q;
-            if (sl < ns) {
-                const int pr = a.slot_pair[s0 + sl];
-                const int la = pr & 0xff, lb = (pr >> 8) & 0xff;
-                bool c0 = lane < n_ct && ((sMask[lane] >> la) & 1u) && ((sMask[lane] >> lb) & 1u);
-                bool c1 = lane + 64 < n_ct && ((sMask[lane + 64] >> la) & 1u) && ((sMask[lane + 64] >> lb) & 1u);
-                uint64_t m0 = __ballot(c0), m1 = __ballot(c1);
-                mfma_items<false>(acc[q], m0, m1, sV, sRow, sRow, BA_MAX_LOCAL, la, lb, d, -1.0, lane);
-                if (la == lb) {
-                    int i0 = sInfo[lane], i1 = sInfo[lane + 64];
-                    bool o0 = i0 >= 0 && (i0 & 0xff) == la;
-                    bool o1 = i1 >= 0 && (i1 & 0xff) == la;
-                    uint64_t n0 = __ballot(o0), n1 = __ballot(o1);
-                    mfma_items<true>(acc[q], n0, n1, sJ, nullptr, nullptr, 0, la, la, d, 1.0, lane);
+            for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
+                const int sl = wave + BA_WAVES * q;
+                if (sl < ns) {
+                    const int la = sLa[sl], lb = sLb[sl];
+                    const unsigned cov = ((gm0 >> la) & (gm0 >> lb) & 1u) | (((gm1 >> la) & (gm1 >> lb) & 1u) << 1) |
+                                         (((gm2 >> la) & (gm2 >> lb) & 1u) << 2) |
+                                         (((gm3 >> la) & (gm3 >> lb) & 1u) << 3);
+                    if (cov) {
+#pragma unroll
+                        for (int mm = 0; mm < 3; ++mm) {
+                            const int kq = 4 * mm + kk, tq = kq / 3, gcomp = kq - 3 * tq;
+                            const bool on = ((cov >> tq) & 1u) && mi < d;
+                            const int t = t0 + tq < BA_CHUNK ? t0 + tq : BA_CHUNK - 1;
+                            const int ra = sRow[t * BA_MAX_LOCAL + la], rb = sRow[t * BA_MAX_LOCAL + lb];
+                            const double A = on ? -sV[(ra * 3 + gcomp) * d + mi] : 0.0;
+                            const double B = on ? sV[(rb * 3 + gcomp) * d + mi] : 0.0;
+                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
+                        }
+                    }
                 }
             }
         }
-        // per-image rhs and diag(H_cc)
-        if (va < nimg && vj < d) {
-            for (int s = 0; s < BA_CHUNK; ++s) {
-                int info = sInfo[s];
-                if (info >= 0 && (info & 0xff) == va) {
-                    accE += sE[s * d + vj];
-                    accD += sD[s * d + vj];
+        // diagonal slots: + J_c^T J_c of every observation in the image, and the image's rhs and
+        // diag(H_cc) contributions (each image has exactly one diagonal slot, owned by one wave)
+#pragma unroll
+        for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
+            const int sl = wave + BA_WAVES * q;
+            if (sl < ns && sLa[sl] == sLb[sl]) {
+                const int la = sLa[sl];
+                int i0 = sInfo[lane], i1 = sInfo[lane + 64];
+                bool o0 = i0 >= 0 && (i0 & 0xff) == la;
+                bool o1 = i1 >= 0 && (i1 & 0xff) == la;
+                uint64_t n0 = __ballot(o0), n1 = __ballot(o1);
+                if (lane < d) {
+                    double e = sVec[la * 32 + lane], g = sVec[la * 32 + 16 + lane];
+                    uint64_t c0 = n0, c1 = n1;
+                    while (c0 | c1) {
+                        int s = pop_lowest(c0, c1);
+                        e += sE[s * d + lane];
+                        g += sD[s * d + lane];
+                    }
+                    sVec[la * 32 + lane] = e;
+                    sVec[la * 32 + 16 + lane] = g;
                 }
+                mfma_items<true>(acc[q], n0, n1, sJ, nullptr, nullptr, 0, la, la, d, 1.0, lane);
             }
         }
     }
@@ -431,10 +465,14 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             }
         }
     }
-    if (va < nimg && vj < d) {
-        double* o = a.img_partials + ((int64_t)batch * a.L + va) * 2 * d;
-        o[vj] = accE;
-        o[d + vj] = accD;
+    __syncthreads();
+    {
+        const int va = tid >> 4, vj = tid & 15;
+        if (va < nimg && vj < d) {
+            double* o = a.img_partials + ((int64_t)batch * a.L + va) * 2 * d;
+            o[vj] = sVec[va * 32 + vj];
+            o[d + vj] = sVec[va * 32 + 16 + vj];
+        }
     }
 }
 

@@ -79,7 +79,8 @@ def linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig,
 def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d, depth_mode='log',
             pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12, min_loss_delta=1e-4,
             weight_z=1, optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True,
-            no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float64, solver='pcg', verbose=False):
+            no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float64, solver='pcg', verbose=False,
+            pcg_tol=1e-6, pcg_maxiter=300):
     """en:206-334 on CPU. Returns (update dict, BA_Status, info)."""
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
@@ -92,7 +93,7 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_co
                                                optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P, optim_X=optim_X,
                                                optim_Z0=optim_Z0, no_grad_f_from_rz=no_grad_f_from_rz,
                                                dampen=dampen, adaptive_dampen=adaptive_dampen, dtype=dtype,
-                                               solver=solver)
+                                               solver=solver, pcg_tol=pcg_tol, pcg_maxiter=pcg_maxiter)
     update = {}
     last_a = 1.0
     scale = 1.0
