@@ -143,7 +143,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             while (k < cur_tracks.size()) {
                 int t = cur_tracks[k];
                 int m = (int)(tptr[t + 1] - tptr[t]);
-                if (used + m > BA_CHUNK) break;
+                if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
                 uint32_t mask = 0;
                 int last_img = -1, leader = -1;
                 for (int j = 0; j < m; ++j) {

@@ -6,6 +6,7 @@
 #define BA_WAVES 4            // waves per workgroup of the fused Schur kernel
 #define BA_SLOTS_PER_WAVE 24  // camera-pair accumulators held in registers by one wave
 #define BA_MAX_SLOTS (BA_WAVES * BA_SLOTS_PER_WAVE)
+#define BA_MAX_CT 64          // tracks per chunk (coverage bit masks in 64 bits)
 
 // plan arrays (all int32)
 enum {

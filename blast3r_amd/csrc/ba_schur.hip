@@ -26,11 +26,29 @@ typedef ba_layout LinLayout;
 typedef ba_lin_args LinArgs;
 
 // ----------------------------------------------------------------------------- per observation
+#define BA_PRE_C 8          // depth-guidance channels held in registers (further channels are read from memory)
+#define BA_BLK 129          // doubles per observation block in LDS: 8 rows x 16 columns + 1 pad (spreads banks)
+
+// Depth-guidance channels of one observation: the first BA_PRE_C in registers, the rest in memory.
+// Every access uses a compile-time channel index, so the register part never spills.
+struct DepSrc {
+    float r[BA_PRE_C];
+    const float* g;
+    __device__ __forceinline__ float operator()(int c) const { return c < BA_PRE_C ? r[c] : g[c]; }
+};
+
+__device__ __forceinline__ void load_dep(DepSrc& s, const float* g, int C) {
+    s.g = g;
+#pragma unroll
+    for (int c = 0; c < BA_PRE_C; ++c) s.r[c] = c < C ? g[c] : 0.f;
+}
+
 struct ObsLin {
-    double Jc[3][16];     // sqrt(W)-weighted camera rows in the image-level layout [foc|tau|zcf]
+    double Jc[3][16];     // sqrt(W)-weighted camera rows in the image-level layout [foc|tau|zcf], 0 beyond d
     double Jp[3][3];      // sqrt(W)-weighted point rows
-    double gJ[16];        // J_c^T (W r)
-    double gP[3];         // J_p^T (W r)
+    double Wr[3];         // W*r formed in fp32, widened
+    double Rs[3];         // W*r / sqrt(W): the residual that pairs with the weighted rows in J_c^T W r
+    double gP[3];         // J_p^T (W r)  (point gradient; only when requested)
 };
 
 __device__ __forceinline__ float clampw(float w, float lo, float hi) {
@@ -38,12 +56,11 @@ __device__ __forceinline__ float clampw(float w, float lo, float hi) {
     return w < lo ? lo : (w > hi ? hi : w);
 }
 
-template <int HK, int HP>
+template <int HK, int HP, bool GRAD_P>
 __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __restrict__ zc_img, const float X[3],
-                                              float2 uv, float2 sv, const float* __restrict__ dep,
-                                              const HuberParams& hp, const LinLayout& lay, bool enK, bool enP,
-                                              bool enZ, bool enX, bool first_obs, const float* given_r,
-                                              const float* given_w, ObsLin& L) {
+                                              float2 uv, float2 sv, const DepSrc& dep, const HuberParams& hp,
+                                              const LinLayout& lay, bool enK, bool enP, bool enZ, bool enX,
+                                              bool first_obs, const float* given_r, const float* given_w, ObsLin& L) {
     constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
     const int C = lay.C;
     ResOut ro;
@@ -54,21 +71,26 @@ __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __res
     } else {
         // residual and weights in fp32 (residuals_with_rigs, .cu:129-259)
         float gf = 0.f;
-        for (int c = 0; c < C; ++c) gf += zc_img[c] * dep[c];
+#pragma unroll
+        for (int c = 0; c < BA_MAX_C; ++c)
+            if (c < C) gf += zc_img[c] * dep(c);
         eval_residual(cp, X, uv.x, uv.y, sv.x, sv.y, gf, hp, ro);
     }
     // Jacobian in fp64 (.cu:323-509); guidance = float products summed in double
     double gd = 0.0;
-    for (int c = 0; c < C; ++c) { float pr = zc_img[c] * dep[c]; gd += (double)pr; }
+#pragma unroll
+    for (int c = 0; c < BA_MAX_C; ++c)
+        if (c < C) { float pr = zc_img[c] * dep(c); gd += (double)pr; }
     JacOut J;
     eval_jacobian(cp, X, sv.x, sv.y, gd, hp.is_depth_log, J);
     // W = clamp(w), g uses (W*r) in fp32 cast to fp64, J *= sqrt(W) with sqrt in fp32 (ba_solver.py:123-132)
-    double Wr[3], sW[3];
+    double sW[3];
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         float W = clampw(ro.w[r], lay.wmin, lay.wmax);
-        Wr[r] = (double)(W * ro.r[r]);
+        L.Wr[r] = (double)(W * ro.r[r]);
         sW[r] = (double)sqrtf(W);
+        L.Rs[r] = L.Wr[r] * (1.0 / sW[r]);
     }
     const double mK = enK ? 1.0 : 0.0, mP = enP ? 1.0 : 0.0;
     const bool zon = lay.hasZ && enZ && J.valid;
@@ -86,18 +108,17 @@ __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __res
             u2 = J.Jcam[18 + (j - OT)] * mP;
         } else {
             const int c = j - OZ;
-            if (zon && c < C && !(c == 0 && z0off)) u2 = J.zscale * (double)dep[c];
+            if (zon && c < C && !(c == 0 && z0off)) u2 = J.zscale * (double)dep(c);
         }
-        L.gJ[j] = u0 * Wr[0] + u1 * Wr[1] + u2 * Wr[2];
         L.Jc[0][j] = u0 * sW[0];
         L.Jc[1][j] = u1 * sW[1];
         L.Jc[2][j] = u2 * sW[2];
     }
-    bool xon = enX && !lay.x_off;
+    const bool xon = enX && !lay.x_off;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         double jp0 = xon ? J.Jp[k] : 0.0, jp1 = xon ? J.Jp[3 + k] : 0.0, jp2 = xon ? J.Jp[6 + k] : 0.0;
-        L.gP[k] = jp0 * Wr[0] + jp1 * Wr[1] + jp2 * Wr[2];
+        if (GRAD_P) L.gP[k] = jp0 * L.Wr[0] + jp1 * L.Wr[1] + jp2 * L.Wr[2];
         L.Jp[0][k] = jp0 * sW[0];
         L.Jp[1][k] = jp1 * sW[1];
         L.Jp[2][k] = jp2 * sW[2];
@@ -151,7 +172,8 @@ __device__ __forceinline__ void load_obs_ctx(const LinArgs& a, int img, ObsCtx& 
     c.enZ = a.enZ ? a.enZ[img] != 0 : true;
 }
 
-template <int HK, int HP>
+// Linearise the observation in plan slot `slot`, reading every input from memory.
+template <int HK, int HP, bool GRAD_P>
 __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, int obs, const ObsCtx& c, ObsLin& L,
                                                int& pid) {
     pid = a.s_pid[slot];
@@ -159,6 +181,8 @@ __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, i
     float2 uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
     float2 sv = reinterpret_cast<const float2*>(a.s_std)[slot];
     bool enX = a.enX ? a.enX[pid] != 0 : true;
+    DepSrc dep;
+    load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
     float gr[3], gw[3];
     if (a.r_in) {
 #pragma unroll
@@ -167,8 +191,8 @@ __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, i
             gw[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
         }
     }
-    linearize_obs<HK, HP>(c.cp, c.zc, X, uv, sv, a.s_dep + slot * a.lay.C, a.hp, a.lay, c.enK, c.enP, c.enZ, enX,
-                          obs == 0, a.r_in ? gr : nullptr, a.r_in ? gw : nullptr, L);
+    linearize_obs<HK, HP, GRAD_P>(c.cp, c.zc, X, uv, sv, dep, a.hp, a.lay, c.enK, c.enP, c.enZ, enX, obs == 0,
+                                  a.r_in ? gr : nullptr, a.r_in ? gw : nullptr, L);
 }
 
 // ----------------------------------------------------------------------------- point blocks
@@ -187,7 +211,7 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
         load_obs_ctx(a, a.s_img[slot], ctx);
         ObsLin L;
         int pid;
-        linearize_slot<HK, HP>(a, slot, obs, ctx, L, pid);
+        linearize_slot<HK, HP, true>(a, slot, obs, ctx, L, pid);
         // J_pts gram (ba_solver.py:911-924) and J_pts^T W r
         const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
 #pragma unroll
@@ -241,73 +265,112 @@ __global__ void __launch_bounds__(256) k_lam_reduce(const double* __restrict__ c
 }
 
 // ----------------------------------------------------------------------------- camera-pair blocks
-__device__ __forceinline__ int pop_lowest(uint64_t& m0, uint64_t& m1) {
-    if (m0) { int b = __builtin_ctzll(m0); m0 &= m0 - 1; return b; }
-    int b = __builtin_ctzll(m1); m1 &= m1 - 1; return 64 + b;
+//
+// k_schur: one workgroup (4 waves) per batch.  Per chunk of 128 observation slots:
+//   A1  waves 0-1, lane per slot: linearise; write the weighted camera rows J_c (rows 4-6 of the
+//       slot's LDS block, column 15 = W r / sqrt(W)); wave 2, lane per chunk track: Cholesky factor of the
+//       damped point block, its reciprocal pivots and w = L^-1 g_p; coverage masks by ballot.
+//   A2  waves 0-1: V = J_c^T J_p L^-T (rows 0-2 of the block, column 15 = w for the first
+//       observation of the track in the image, else 0); several observations of one track in one
+//       image are then summed into the first one.
+//   B   every wave, for each camera-pair slot it owns (accumulator in registers):
+//         off-diagonal (a,b):  acc += V_ta^T V_tb        one 16x16x4 fp64 MFMA per covering track
+//         diagonal (a,a):      acc += V_ta^T V_ta        per covering track
+//                              acc -= J_o^T J_o          per observation o in image a
+//       Rows 3 and 7 of a block are zero, so every MFMA reads 4 whole block rows with a uniform
+//       base address.  The partial block is -acc; column 15 of a diagonal tile then holds
+//       sum J_c^T W r - V w = the image's rhs term, and diag(J_c^T J_c) is summed from the
+//       squared B operands of the J MFMAs.
+// Observation inputs for the next chunk are fetched during the current one (two levels:
+// slot streams first, then the gathers that depend on them).
+
+__device__ __forceinline__ uint64_t uni64(uint64_t x) {
+    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ int sel4(int q, int v0, int v1, int v2, int v3) {
-    return q == 0 ? v0 : (q == 1 ? v1 : (q == 2 ? v2 : v3));
+struct ObsPre {                 // one observation slot, fetched a chunk ahead
+    int info, obs, pid, enX;
+    float2 uv, sv;
+    float dep[BA_PRE_C];
+    float X[3];
+    float gr[3], gw[3];
+};
+
+struct TrkPre {                 // one chunk track, fetched a chunk ahead
+    int n_ct, pid, mask;
+    double H[6], g[3];
+};
+
+__device__ __forceinline__ void obs_pre_l1(const LinArgs& a, int64_t slot, int C, ObsPre& p) {
+    p.info = a.slot_info[slot];
+    p.obs = a.chunk_obs[slot];
+    p.pid = a.s_pid[slot];
+    p.uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
+    p.sv = reinterpret_cast<const float2*>(a.s_std)[slot];
+    const float* dg = a.s_dep + slot * C;
+#pragma unroll
+    for (int c = 0; c < BA_PRE_C; ++c) p.dep[c] = c < C ? dg[c] : 0.f;
 }
 
-// One 16x16 fp64 tile: acc += sign * X_a^T X_b over K-elements (group item, component).
-// Items come 4 at a time from a uniform bit mask; item q maps to LDS rows (ra, rb).
-template <bool DIAG_J>
-__device__ __forceinline__ void mfma_items(dbl4& acc, uint64_t m0, uint64_t m1, const double* __restrict__ X,
-                                           const unsigned char* __restrict__ rowsA, const unsigned char* __restrict__ rowsB,
-                                           int rstride, int la, int lb, int d, double sign, int lane) {
-    int cnt = __builtin_popcountll(m0) + __builtin_popcountll(m1);
-    const int i = lane & 15;
-    const int kk = lane >> 4;
-    for (int g = 0; g < cnt; g += 4) {
-        int nt = cnt - g < 4 ? cnt - g : 4;
-        int it[4];
+__device__ __forceinline__ void obs_pre_l2(const LinArgs& a, ObsPre& p) {
+    const int64_t pid = p.info >= 0 ? p.pid : 0;
+    p.X[0] = a.pts3d[3 * pid]; p.X[1] = a.pts3d[3 * pid + 1]; p.X[2] = a.pts3d[3 * pid + 2];
+    p.enX = a.enX ? a.enX[pid] : 1;
+    if (a.r_in) {
+        const int64_t o = p.info >= 0 ? p.obs : 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) it[q] = (q < nt) ? pop_lowest(m0, m1) : 0;
-        int ra[4], rb[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (DIAG_J) { ra[q] = it[q]; rb[q] = it[q]; }
-            else { ra[q] = rowsA[it[q] * rstride + la]; rb[q] = rowsB[it[q] * rstride + lb]; }
-        }
-        int nk = 3 * nt;
-#pragma unroll
-        for (int mm = 0; mm < 3; ++mm) {
-            if (4 * mm >= nk) break;
-            int k = 4 * mm + kk;
-            int q = k / 3, comp = k - 3 * (k / 3);
-            bool ok = (k < nk) && (i < d);
-            int rowa = sel4(q, ra[0], ra[1], ra[2], ra[3]);
-            int rowb = sel4(q, rb[0], rb[1], rb[2], rb[3]);
-            double A = ok ? sign * X[(rowa * 3 + comp) * d + i] : 0.0;
-            double B = ok ? X[(rowb * 3 + comp) * d + i] : 0.0;
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc, 0, 0, 0);
+        for (int k = 0; k < 3; ++k) {
+            p.gr[k] = a.r_in[o * a.r_s0 + k * a.r_s1];
+            p.gw[k] = a.w_in[o * a.w_s0 + k * a.w_s1];
         }
     }
 }
 
+__device__ __forceinline__ void trk_pre_l1(const LinArgs& a, int ck, int lane, TrkPre& p) {
+    const int first_ct = a.chunk_meta[4 * ck + 1];
+    p.n_ct = a.chunk_meta[4 * ck + 2];
+    p.pid = lane < p.n_ct ? a.ct_pid[first_ct + lane] : -1;
+    p.mask = lane < p.n_ct ? a.ct_mask[first_ct + lane] : 0;
+}
+
+__device__ __forceinline__ void trk_pre_l2(const LinArgs& a, TrkPre& p) {
+    const int64_t pid = p.pid >= 0 ? p.pid : 0;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) p.H[k] = a.Hpp[6 * pid + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) p.g[k] = a.gp[3 * pid + k];
+}
+
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
-    extern __shared__ double dyn[];
-    const int d = a.lay.d, C = a.lay.C;
-    double* sV = dyn;                                 // [CHUNK][3][d]  V = H_cp L^-T per observation
-    double* sJ = sV + BA_CHUNK * 3 * d;               // [CHUNK][3][d]  weighted J_c rows
-    double* sE = sJ + BA_CHUNK * 3 * d;               // [CHUNK][d]     rhs contribution
-    double* sD = sE + BA_CHUNK * d;                   // [CHUNK][d]     diag(J_c^T J_c) contribution
+    extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks
+    __shared__ double sTrk[BA_MAX_CT][12];               // per chunk track: L (6) | 1/pivots (3) | L^-1 g_p (3)
+    __shared__ double sDv[BA_MAX_LOCAL][16];             // per local image: diag(J_c^T J_c)
+    __shared__ uint64_t sTm[BA_MAX_LOCAL];               // chunk tracks covering each local image
+    __shared__ uint64_t sIm[BA_MAX_LOCAL][2];            // slots observed in each local image
+    __shared__ uint64_t sLm[BA_MAX_LOCAL][2];            // ... first slot of a (track, image) run
     __shared__ int sInfo[BA_CHUNK];
-    __shared__ unsigned sMask[BA_CHUNK];
-    __shared__ unsigned char sRow[BA_CHUNK * BA_MAX_LOCAL];
+    __shared__ unsigned char sRowT[BA_MAX_LOCAL * BA_MAX_CT];   // (image, track) -> first slot
     __shared__ CamF sCam[BA_MAX_LOCAL];
     __shared__ float sZc[BA_MAX_LOCAL * BA_MAX_C];
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
-    __shared__ unsigned char sLa[BA_MAX_SLOTS], sLb[BA_MAX_SLOTS];
-    __shared__ double sVec[BA_MAX_LOCAL * 2 * 16];       // per local image: rhs (d) | diag(H_cc) (d)
+    __shared__ int sPair[BA_MAX_SLOTS];
+    __shared__ int sDup[2];
 
+    const int d = a.lay.d, C = a.lay.C;
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
     const double lam = a.lam_p[0];
+    const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
+
+    ObsPre pre;
+    TrkPre tpre;
+    if (tid < BA_CHUNK) obs_pre_l1(a, (int64_t)c_begin * BA_CHUNK + tid, C, pre);
+    else if (wave == 2) trk_pre_l1(a, c_begin, lane, tpre);
 
     // local image parameters
     if (tid < nimg) {
@@ -319,160 +382,233 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         sEn[3 * tid + 1] = a.enP ? a.enP[node] : 1;
         sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
     }
-
-    for (int q = tid; q < ns; q += BA_WAVES * 64) {
-        const int pr = a.slot_pair[s0 + q];
-        sLa[q] = (unsigned char)(pr & 0xff);
-        sLb[q] = (unsigned char)((pr >> 8) & 0xff);
-    }
-    for (int q = tid; q < BA_MAX_LOCAL * 2 * 16; q += BA_WAVES * 64) sVec[q] = 0.0;
+    // the pair of slot q: (a | b << 8), -1 past the batch's slots
+    for (int q = tid; q < BA_MAX_SLOTS; q += BA_WAVES * 64) sPair[q] = q < ns ? a.slot_pair[s0 + q] : -1;
+    for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
+    if (tid < BA_CHUNK) obs_pre_l2(a, pre);
+    else if (wave == 2) trk_pre_l2(a, tpre);
+    __syncthreads();
 
     dbl4 acc[BA_SLOTS_PER_WAVE];
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) acc[q] = dbl4{0.0, 0.0, 0.0, 0.0};
-    // K-element of this lane in the three MFMAs of a 4-track group: k = 4*mm + lane/16
-    const int mi = lane & 15, kk = lane >> 4;
+    // MFMA operand element of this lane inside a 4-row group: row lane/16, column lane%16
+    const int loff = (lane >> 4) * 16 + (lane & 15);
 
-    const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
     for (int ck = c_begin; ck < c_end; ++ck) {
-        __syncthreads();    // previous chunk fully consumed; local params visible
-        const int first_ct = a.chunk_meta[4 * ck + 1], n_ct = a.chunk_meta[4 * ck + 2];
-        if (tid < BA_CHUNK) {
-            const int64_t slot = (int64_t)ck * BA_CHUNK + tid;
-            const int info = a.slot_info[slot];
-            sInfo[tid] = info;
-            if (info >= 0) {
-                const int li = info & 0xff, ctr = (info >> 8) & 0xff, leader = info >> 16;
-                const int obs = a.chunk_obs[slot];
-                ObsCtx ctx;
-                ctx.cp = sCam[li];
-                ctx.zc = sZc + li * BA_MAX_C;
-                ctx.enK = sEn[3 * li] != 0; ctx.enP = sEn[3 * li + 1] != 0; ctx.enZ = sEn[3 * li + 2] != 0;
-                ObsLin L;
-                int pid;
-                linearize_slot<HK, HP>(a, slot, obs, ctx, L, pid);
-                double H[6], g[3], Lf[6];
-#pragma unroll
-                for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * (int64_t)pid + k];
-#pragma unroll
-                for (int k = 0; k < 3; ++k) g[k] = a.gp[3 * (int64_t)pid + k];
-                chol3_factor(H, lam, Lf);
-                double P[3][3], w[3];
-#pragma unroll
-                for (int r = 0; r < 3; ++r) chol3_fwd(Lf, L.Jp[r], P[r]);    // P = Jp L^-T (row-wise)
-                chol3_fwd(Lf, g, w);                                          // w = L^-1 g_p
-                double* v = sV + tid * 3 * d;
-                double* jj = sJ + tid * 3 * d;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    if (j < d) {
-                        double v0 = L.Jc[0][j] * P[0][0] + L.Jc[1][j] * P[1][0] + L.Jc[2][j] * P[2][0];
-                        double v1 = L.Jc[0][j] * P[0][1] + L.Jc[1][j] * P[1][1] + L.Jc[2][j] * P[2][1];
-                        double v2 = L.Jc[0][j] * P[0][2] + L.Jc[1][j] * P[1][2] + L.Jc[2][j] * P[2][2];
-                        v[0 * d + j] = v0; v[1 * d + j] = v1; v[2 * d + j] = v2;
-                        jj[0 * d + j] = L.Jc[0][j]; jj[1 * d + j] = L.Jc[1][j]; jj[2 * d + j] = L.Jc[2][j];
-                        sE[tid * d + j] = L.gJ[j] - (v0 * w[0] + v1 * w[1] + v2 * w[2]);
-                        sD[tid * d + j] = L.Jc[0][j] * L.Jc[0][j] + L.Jc[1][j] * L.Jc[1][j] + L.Jc[2][j] * L.Jc[2][j];
-                    }
-                }
-                if (leader == tid) sRow[ctr * BA_MAX_LOCAL + li] = (unsigned char)tid;
-            }
+        if (ck != c_begin) __syncthreads();    // the previous chunk's blocks are consumed
+        const ObsPre cur = pre;
+        const TrkPre tcur = tpre;
+        const bool more = ck + 1 < c_end;
+        if (more) {
+            if (tid < BA_CHUNK) obs_pre_l1(a, (int64_t)(ck + 1) * BA_CHUNK + tid, C, pre);
+            else if (wave == 2) trk_pre_l1(a, ck + 1, lane, tpre);
         }
-        if (tid < n_ct) sMask[tid] = (unsigned)a.ct_mask[first_ct + tid];
-        __syncthreads();
-        // several observations of one track in one image: sum their V into the leader row
+
+        // ---------------- A1
+        const int info = cur.info;
+        const bool valid = tid < BA_CHUNK && info >= 0;
+        const int li = info & 0xff, ct = (info >> 8) & 0xff, leader = info >> 16;
         if (tid < BA_CHUNK) {
-            int info = sInfo[tid];
-            if (info >= 0 && (info >> 16) == tid) {
-                for (int f = tid + 1; f < BA_CHUNK; ++f) {
-                    int fi = sInfo[f];
-                    if (fi < 0 || (fi >> 16) != tid) break;
-                    for (int e = 0; e < 3 * d; ++e) sV[tid * 3 * d + e] += sV[f * 3 * d + e];
+            sInfo[tid] = info;
+            if (valid) {
+                ObsLin L;
+                DepSrc dep;
+#pragma unroll
+                for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = cur.dep[c];
+                dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + tid) * C;
+                const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
+                linearize_obs<HK, HP, false>(sCam[li], sZc + li * BA_MAX_C, cur.X, cur.uv, cur.sv, dep, a.hp, a.lay,
+                                             eK, eP, eZ, cur.enX != 0, cur.obs == 0, a.r_in ? cur.gr : nullptr,
+                                             a.r_in ? cur.gw : nullptr, L);
+                double* blk = sBlk + tid * BA_BLK;
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+#pragma unroll
+                    for (int j = 0; j < 15; ++j) blk[64 + 16 * r + j] = j < d ? L.Jc[r][j] : 0.0;
+                    blk[64 + 16 * r + 15] = L.Rs[r];
                 }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) blk[112 + j] = 0.0;
+                // J_p waits in row 0 until A2 overwrites the row with V
+#pragma unroll
+                for (int r = 0; r < 3; ++r)
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) blk[3 * r + k] = L.Jp[r][k];
+                if (leader == tid) sRowT[li * BA_MAX_CT + ct] = (unsigned char)tid;
             }
+            uint64_t im = 0, lm = 0;
+#pragma unroll
+            for (int m = 0; m < BA_MAX_LOCAL; ++m) {
+                const uint64_t b = __ballot(valid && li == m);
+                const uint64_t bl = __ballot(valid && li == m && leader == tid);
+                if (lane == m) { im = b; lm = bl; }
+            }
+            if (lane < BA_MAX_LOCAL) { sIm[lane][wave] = im; sLm[lane][wave] = lm; }
+            const uint64_t dup = __ballot(valid && leader != tid);
+            if (lane == 0) sDup[wave] = dup != 0;
+        } else if (wave == 2) {
+            if (lane < tcur.n_ct) {
+                double Lf[6];
+                chol3_factor(tcur.H, lam, Lf);
+                const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
+                const double w0 = tcur.g[0] * r0;
+                const double w1 = (tcur.g[1] - Lf[1] * w0) * r1;
+                const double w2 = (tcur.g[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
+                double* T = sTrk[lane];
+#pragma unroll
+                for (int k = 0; k < 6; ++k) T[k] = Lf[k];
+                T[6] = r0; T[7] = r1; T[8] = r2; T[9] = w0; T[10] = w1; T[11] = w2;
+            }
+            uint64_t tm = 0;
+#pragma unroll
+            for (int m = 0; m < BA_MAX_LOCAL; ++m) {
+                const uint64_t b = __ballot((tcur.mask >> m) & 1);
+                if (lane == m) tm = b;
+            }
+            if (lane < BA_MAX_LOCAL) sTm[lane] = tm;
         }
         __syncthreads();
 
-        // camera-pair tiles: groups of 4 chunk tracks outermost, so that every owned slot the group
-        // covers gets its 3 MFMAs back to back on independent accumulators
-        for (int t0 = 0; t0 < n_ct; t0 += 4) {
-            const unsigned gm0 = sMask[t0];
-            const unsigned gm1 = t0 + 1 < n_ct ? sMask[t0 + 1] : 0u;
-            const unsigned gm2 = t0 + 2 < n_ct ? sMask[t0 + 2] : 0u;
-            const unsigned gm3 = t0 + 3 < n_ct ? sMask[t0 + 3] : 0u;
+        // ---------------- A2: V = J_c^T P with P = J_p L^-T
+        if (valid) {
+            const double* T = sTrk[ct];
+            const double l10 = T[1], l20 = T[2], l21 = T[4], r0 = T[6], r1 = T[7], r2 = T[8];
+            double* blk = sBlk + tid * BA_BLK;
+            double P[3][3];
 #pragma unroll
-            for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-                const int sl = wave + BA_WAVES * q;
-                if (sl < ns) {
-                    const int la = sLa[sl], lb = sLb[sl];
-                    const unsigned cov = ((gm0 >> la) & (gm0 >> lb) & 1u) | (((gm1 >> la) & (gm1 >> lb) & 1u) << 1) |
-                                         (((gm2 >> la) & (gm2 >> lb) & 1u) << 2) |
-                                         (((gm3 >> la) & (gm3 >> lb) & 1u) << 3);
-                    if (cov) {
+            for (int r = 0; r < 3; ++r) {
+                P[r][0] = blk[3 * r] * r0;
+                P[r][1] = (blk[3 * r + 1] - l10 * P[r][0]) * r1;
+                P[r][2] = (blk[3 * r + 2] - l20 * P[r][0] - l21 * P[r][1]) * r2;
+            }
+            const bool lead = leader == tid;
+            double V[3][16];
 #pragma unroll
-                        for (int mm = 0; mm < 3; ++mm) {
-                            const int kq = 4 * mm + kk, tq = kq / 3, gcomp = kq - 3 * tq;
-                            const bool on = ((cov >> tq) & 1u) && mi < d;
-                            const int t = t0 + tq < BA_CHUNK ? t0 + tq : BA_CHUNK - 1;
-                            const int ra = sRow[t * BA_MAX_LOCAL + la], rb = sRow[t * BA_MAX_LOCAL + lb];
-                            const double A = on ? -sV[(ra * 3 + gcomp) * d + mi] : 0.0;
-                            const double B = on ? sV[(rb * 3 + gcomp) * d + mi] : 0.0;
-                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
-                        }
-                    }
+            for (int j = 0; j < 15; ++j) {
+                const double j0 = blk[64 + j], j1 = blk[80 + j], j2 = blk[96 + j];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) V[c][j] = j < d ? j0 * P[0][c] + j1 * P[1][c] + j2 * P[2][c] : 0.0;
+            }
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+#pragma unroll
+                for (int j = 0; j < 15; ++j) blk[16 * c + j] = V[c][j];
+                blk[16 * c + 15] = lead ? T[9 + c] : 0.0;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) blk[48 + j] = 0.0;
+        }
+        if (more) {
+            if (tid < BA_CHUNK) obs_pre_l2(a, pre);
+            else if (wave == 2) trk_pre_l2(a, tpre);
+        }
+        __syncthreads();
+        if (sDup[0] | sDup[1]) {
+            // several observations of one track in one image: V of the run is summed into its first slot
+            if (tid < BA_CHUNK && valid && leader == tid) {
+                double* dst = sBlk + tid * BA_BLK;
+                for (int f = tid + 1; f < BA_CHUNK; ++f) {
+                    const int fi = sInfo[f];
+                    if (fi < 0 || (fi >> 16) != tid) break;
+                    const double* src = sBlk + f * BA_BLK;
+#pragma unroll
+                    for (int c = 0; c < 3; ++c)
+#pragma unroll
+                        for (int j = 0; j < 15; ++j) dst[16 * c + j] += src[16 * c + j];
                 }
             }
+            __syncthreads();
         }
-        // diagonal slots: + J_c^T J_c of every observation in the image, and the image's rhs and
-        // diag(H_cc) contributions (each image has exactly one diagonal slot, owned by one wave)
+
+        // ---------------- B: camera-pair tiles
 #pragma unroll
         for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-            const int sl = wave + BA_WAVES * q;
-            if (sl < ns && sLa[sl] == sLb[sl]) {
-                const int la = sLa[sl];
-                int i0 = sInfo[lane], i1 = sInfo[lane + 64];
-                bool o0 = i0 >= 0 && (i0 & 0xff) == la;
-                bool o1 = i1 >= 0 && (i1 & 0xff) == la;
-                uint64_t n0 = __ballot(o0), n1 = __ballot(o1);
-                if (lane < d) {
-                    double e = sVec[la * 32 + lane], g = sVec[la * 32 + 16 + lane];
-                    uint64_t c0 = n0, c1 = n1;
-                    while (c0 | c1) {
-                        int s = pop_lowest(c0, c1);
-                        e += sE[s * d + lane];
-                        g += sD[s * d + lane];
+            const int pq = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
+            if (pq >= 0) {
+                const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
+                if (la != lb) {
+                    uint64_t cov = uni64(sTm[la] & sTm[lb]);
+                    if (cov) {
+                        const int rA = sRowT[la * BA_MAX_CT + lane], rB = sRowT[lb * BA_MAX_CT + lane];
+                        // operands of the next covering track are read while the current MFMA runs
+                        int t = __builtin_ctzll(cov);
+                        cov &= cov - 1;
+                        double A = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                        double B = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                        while (cov) {
+                            t = __builtin_ctzll(cov);
+                            cov &= cov - 1;
+                            const double A2 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                            const double B2 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
+                            A = A2;
+                            B = B2;
+                        }
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
                     }
-                    sVec[la * 32 + lane] = e;
-                    sVec[la * 32 + 16 + lane] = g;
+                } else {
+                    // J rows (block offset 64) of every observation in the image, then V rows (offset 0)
+                    // of every (track, image) run, each list walked with the next operand read ahead
+                    // of the current MFMA
+                    double dsq = 0.0;
+                    auto walk = [&](uint64_t w0, uint64_t w1, const int roff, const bool jrows) {
+                        auto pop = [&]() {
+                            int o;
+                            if (w0) { o = __builtin_ctzll(w0); w0 &= w0 - 1; }
+                            else    { o = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; }
+                            return o * BA_BLK + roff + loff;
+                        };
+                        if (!(w0 | w1)) return;
+                        double B = sBlk[pop()];
+                        while (w0 | w1) {
+                            const double B2 = sBlk[pop()];
+                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jrows ? -B : B, B, acc[q], 0, 0, 0);
+                            if (jrows) dsq += B * B;
+                            B = B2;
+                        }
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jrows ? -B : B, B, acc[q], 0, 0, 0);
+                        if (jrows) dsq += B * B;
+                    };
+                    walk(uni64(sIm[la][0]), uni64(sIm[la][1]), 64, true);
+                    walk(uni64(sLm[la][0]), uni64(sLm[la][1]), 0, false);
+                    dsq += __shfl_xor(dsq, 16);
+                    dsq += __shfl_xor(dsq, 32);
+                    if (lane < 16) sDv[la][lane] += dsq;
                 }
-                mfma_items<true>(acc[q], n0, n1, sJ, nullptr, nullptr, 0, la, la, d, 1.0, lane);
             }
         }
     }
 
-    // flush this batch's partial blocks (row-major d x d, local orientation)
+    // flush this batch's partial blocks (-acc, row-major d x d, local orientation);
+    // v_mfma_f64_16x16x4f64 accumulator layout: lane l, element v holds D[4v + l/16][l%16]
+    const int jc = lane & 15;
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-        const int sl = wave + BA_WAVES * q;
-        if (sl < ns) {
+        const int pq = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
+        if (pq >= 0) {
+            const int sl = wave + BA_WAVES * q;
             double* P = a.partials + (int64_t)(s0 + sl) * d * d;
-            // v_mfma_f64_16x16x4f64 accumulator layout: lane l, element v holds D[4v + l/16][l%16]
-            const int j = lane & 15;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                int i = 4 * v + (lane >> 4);
-                if (i < d && j < d) P[i * d + j] = acc[q][v];
+                const int i = 4 * v + (lane >> 4);
+                if (i < d && jc < d) P[i * d + jc] = -acc[q][v];
+            }
+            const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
+            if (la == lb && jc == 15) {
+                double* o = a.img_partials + ((int64_t)batch * a.L + la) * 2 * d;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = 4 * v + (lane >> 4);
+                    if (i < d) o[i] = -acc[q][v];
+                }
             }
         }
     }
     __syncthreads();
     {
         const int va = tid >> 4, vj = tid & 15;
-        if (va < nimg && vj < d) {
-            double* o = a.img_partials + ((int64_t)batch * a.L + va) * 2 * d;
-            o[vj] = sVec[va * 32 + vj];
-            o[d + vj] = sVec[va * 32 + 16 + vj];
-        }
+        if (va < nimg && vj < d) a.img_partials[((int64_t)batch * a.L + va) * 2 * d + d + vj] = sDv[va][vj];
     }
 }
 
@@ -526,7 +662,7 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         load_obs_ctx(a, img, ctx);
         ObsLin L;
         int pid;
-        linearize_slot<HK, HP>(a, slot, obs, ctx, L, pid);
+        linearize_slot<HK, HP, false>(a, slot, obs, ctx, L, pid);
         double t[3] = {0.0, 0.0, 0.0};
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -595,7 +731,7 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
     BA_REQUIRE(args != nullptr, "null args");
     const ba_lin_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
-    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 16, "fused path supports 1 <= d <= 16 image-level parameters");
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 15, "fused path supports 1 <= d <= 15 image-level parameters");
     BA_REQUIRE(a.lay.off_tau == 2 * a.lay.hasK && a.lay.off_zcf == a.lay.off_tau + 6 * a.lay.hasP &&
                    a.lay.d == a.lay.off_zcf + (a.lay.hasZ ? a.lay.C : 0),
                "inconsistent image-level layout");
@@ -614,7 +750,7 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
         return BA_OK;
     }
     if (stage == 1 && a.n_batches > 0) {
-        size_t lds = (size_t)BA_CHUNK * 8 * a.lay.d * sizeof(double);
+        size_t lds = (size_t)BA_CHUNK * BA_BLK * sizeof(double);
         BA_DISPATCH_KP(a.lay, {
             BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds));
@@ -639,7 +775,7 @@ extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
     const ba_lin_args& a = *args;
-    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 16, "fused path supports 1 <= d <= 16 image-level parameters");
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 15, "fused path supports 1 <= d <= 15 image-level parameters");
     if (a.n_chunks == 0) return BA_OK;
     hipStream_t st = (hipStream_t)stream;
     BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_backsub<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0, st, a));

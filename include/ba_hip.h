@@ -124,7 +124,7 @@ typedef struct {
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.
- * Requires d <= 16 and C <= 24. */
+ * Requires d <= 15 and C <= 24. */
 int ba_linearize_schur(const ba_lin_args* args, void* stream);
 
 /* The same work split in its three launch groups (callers that time the camera-pair
