@@ -205,9 +205,11 @@ class GaussNewtonSolver:
                                              J.pix2d_dep)
         ws = plan.workspace
         n_imgs = self.imgs.true_n
-        Hpp = ws('Hpp', (max(T, 1), 6), torch.float64)
-        gp = ws('gp', (max(T, 1), 3), torch.float64)
-        chunk_max = ws('chunk_max', (max(sc['n_chunks'], 1),), torch.float64)
+        n_ct = sc['n_ctracks']
+        Hpp = ws('Hpp', (max(n_ct, 1), 6), torch.float64)          # chunk-track order
+        gp = ws('gp', (max(n_ct, 1), 3), torch.float64)
+        ct_pt = ws('ct_pt', (max(n_ct, 1), 4), torch.float32)
+        chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), torch.float64)
         lam_p = ws('lam_p', (1,), torch.float64)
         dd = max(d, 1)
         partials = ws('partials', (max(sc['n_slots'], 1), dd, dd), torch.float64)
@@ -247,6 +249,7 @@ class GaussNewtonSolver:
         L_.adaptive = int(bool(self.adaptive_dampen))
         L_.x_off = int(not en['X'][0])
         a.Hpp, a.gp, a.chunk_max, a.lam_p = ptr(Hpp), ptr(gp), ptr(chunk_max), ptr(lam_p)
+        a.ct_pt, a.n_ctracks = ptr(ct_pt), n_ct
         a.partials, a.img_partials = ptr(partials), ptr(img_partials)
         a.n_chunks, a.n_batches, a.n_pairs = sc['n_chunks'], sc['n_batches'], sc['n_pairs']
         a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
@@ -349,6 +352,20 @@ class GaussNewtonSolver:
                 expand(dX, self.tracks, 3))
 
     # ------------------------------------------------------------------ inspection helpers
+    def point_blocks(self):
+        """H_pp upper (n_tracks,6) and g_p (n_tracks,3) of the last solve_delta in track-id order
+        (the device keeps them in chunk-track order); tracks without observations hold zeros."""
+        last = self.last
+        plan = last['plan']
+        n_ct = plan.scalars['n_ctracks']
+        T = self.tracks.true_n
+        pid = plan.dev['ct_pid'][:n_ct].long()
+        H = torch.zeros((T, 6), dtype=torch.float64, device=self.device)
+        g = torch.zeros((T, 3), dtype=torch.float64, device=self.device)
+        H[pid] = last['Hpp'][:n_ct]
+        g[pid] = last['gp'][:n_ct]
+        return H, g
+
     def reduced_system_dense(self):
         """Dense S (reference unknown order, damped) and rhs of the last solve_delta (for tests)."""
         last = self.last

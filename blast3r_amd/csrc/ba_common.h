@@ -105,104 +105,134 @@ __device__ __forceinline__ void eval_residual(const CamF& cp, const float X[3], 
 }
 
 // ---------------------------------------------------------------- Jacobian (fp64)
-// Jcam: 3x8 row-major [fx, fy, wx, wy, wz, vx, vy, vz]; Jz: C entries of row 2; Jp: 3x3.
-struct JacOut {
-    double Jcam[24];
-    double Jp[9];
-    double fbar;         // d r2 / d zcf_c = fbar * dep_c (log mode)
-    double zscale;       // lin mode: fbar / g (or 0); log mode: fbar
+// Every Jacobian entry of one observation is formed from a small core (.cu:323-509):
+//   Jpr = d(proj)/d X_cam * R_cr, rows scaled by 1/std           (.cu:415-441)
+//   tau block of row r = Jpr_r @ [-skew(Xr) | I]                 (.cu:444-458)
+//   points block       = Jpr @ R_rw                              (.cu:463)
+//   focal columns: Xc0/z/s0, Xc1/z/s1, and for row 2 J_k_f, gated on g > 0 and rounded to fp32
+//   (.cu:473-489).
+struct JacCore {
+    double Xr[3];
+    double Jpr[9];
+    double fx_col, fy_col;   // row 0 column fx, row 1 column fy
+    double jkf;              // row 2, both focal columns
+    double fbar;             // d r2 / d zcf_c = fbar * dep_c (log mode)
+    double zscale;           // lin mode: fbar / g (or 0); log mode: fbar
     bool valid;
 };
 
-__device__ __forceinline__ void eval_jacobian(const CamF& cp, const float Xf[3], float su, float sv, double guidance,
-                                              int is_depth_log, JacOut& J) {
+__device__ __forceinline__ void eval_jac_core(const CamF& cp, const float Xf[3], float su, float sv, double guidance,
+                                              int is_depth_log, JacCore& J) {
     double X[3] = {Xf[0], Xf[1], Xf[2]};
-    double Rrw[9], trw[3], Rcr[9], tcr[3];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) { Rrw[k] = cp.Rrw[k]; Rcr[k] = cp.Rcr[k]; }
-#pragma unroll
-    for (int k = 0; k < 3; ++k) { trw[k] = cp.trw[k]; tcr[k] = cp.tcr[k]; }
-    double fx = cp.fx, fy = cp.fy, cx = cp.cx, cy = cp.cy;
-    double Xr[3], Xc[3];
+    double Xc[3];
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         double s = 0.0;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) s += Rrw[3 * r + k] * X[k];
-        Xr[r] = s + trw[r];
+        for (int k = 0; k < 3; ++k) s += (double)cp.Rrw[3 * r + k] * X[k];
+        J.Xr[r] = s + (double)cp.trw[r];
     }
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         double s = 0.0;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) s += Rcr[3 * r + k] * Xr[k];
-        Xc[r] = s + tcr[r];
+        for (int k = 0; k < 3; ++k) s += (double)cp.Rcr[3 * r + k] * J.Xr[k];
+        Xc[r] = s + (double)cp.tcr[r];
     }
-    double p0 = fx * Xc[0] + cx * Xc[2];
-    double p1 = fy * Xc[1] + cy * Xc[2];
-    double z = Xc[2];
+    const double fx = cp.fx, fy = cp.fy, cx = cp.cx, cy = cp.cy;
+    const double p0 = fx * Xc[0] + cx * Xc[2];
+    const double p1 = fy * Xc[1] + cy * Xc[2];
+    const double z = Xc[2];
     J.valid = z > 1e-3;
     if (!J.valid) {
 #pragma unroll
-        for (int k = 0; k < 24; ++k) J.Jcam[k] = 0.0;
-#pragma unroll
-        for (int k = 0; k < 9; ++k) J.Jp[k] = 0.0;
-        J.fbar = 0.0; J.zscale = 0.0;
+        for (int k = 0; k < 9; ++k) J.Jpr[k] = 0.0;
+        J.fx_col = J.fy_col = J.jkf = J.fbar = J.zscale = 0.0;
         return;
     }
-    double inv_z = 1.0 / z;
-    double inv_z2 = inv_z * inv_z;
-    double avg_focal = 0.5 * (fx + fy);
-    double s0 = su, s1 = sv;
-    // d(proj)/d X_cam, rows scaled by 1/std (.cu:415-435)
+    const double inv_z = 1.0 / z;
+    const double inv_z2 = inv_z * inv_z;
+    const double avg_focal = 0.5 * (fx + fy);
+    const double s0 = su, s1 = sv;
     double Jpc[9];
     Jpc[0] = fx * inv_z / s0;  Jpc[1] = 0.0;             Jpc[2] = (cx * inv_z - p0 * inv_z2) / s0;
     Jpc[3] = 0.0;              Jpc[4] = fy * inv_z / s1; Jpc[5] = (cy * inv_z - p1 * inv_z2) / s1;
     Jpc[6] = 0.0;              Jpc[7] = 0.0;             Jpc[8] = -avg_focal * inv_z;
-    double Jpr[9];   // (.cu:441)
 #pragma unroll
     for (int r = 0; r < 3; ++r)
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             double s = 0.0;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) s += Jpc[3 * r + k] * Rcr[3 * k + c];
-            Jpr[3 * r + c] = s;
+            for (int k = 0; k < 3; ++k) s += Jpc[3 * r + k] * (double)cp.Rcr[3 * k + c];
+            J.Jpr[3 * r + c] = s;
         }
-    // tau block = Jpr @ [-skew(Xr) | I] (.cu:444-458)
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-        double a0 = Jpr[3 * r + 0], a1 = Jpr[3 * r + 1], a2 = Jpr[3 * r + 2];
-        J.Jcam[8 * r + 2] = -a1 * Xr[2] + a2 * Xr[1];
-        J.Jcam[8 * r + 3] = a0 * Xr[2] - a2 * Xr[0];
-        J.Jcam[8 * r + 4] = -a0 * Xr[1] + a1 * Xr[0];
-        J.Jcam[8 * r + 5] = a0;
-        J.Jcam[8 * r + 6] = a1;
-        J.Jcam[8 * r + 7] = a2;
-    }
-    // points (.cu:463)
-#pragma unroll
-    for (int r = 0; r < 3; ++r)
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            double s = 0.0;
-#pragma unroll
-            for (int k = 0; k < 3; ++k) s += Jpr[3 * r + k] * Rrw[3 * k + c];
-            J.Jp[3 * r + c] = s;
-        }
-    // focal columns (.cu:473-489): J_k_f gated on g > 0 and rounded to fp32
-    J.Jcam[0] = Xc[0] * inv_z / s0;  J.Jcam[1] = 0.0;
-    J.Jcam[8] = 0.0;                 J.Jcam[9] = Xc[1] * inv_z / s1;
+    J.fx_col = Xc[0] * inv_z / s0;
+    J.fy_col = Xc[1] * inv_z / s1;
     float jkf = 0.0f;
     if (guidance > 0) {
         if (is_depth_log) jkf = (float)(0.5 * (guidance + log(inv_z)));
         else              jkf = (float)(0.5 * log(guidance * inv_z));
     }
-    J.Jcam[16] = (double)jkf;
-    J.Jcam[17] = (double)jkf;
+    J.jkf = (double)jkf;
     J.fbar = avg_focal;
     if (is_depth_log) J.zscale = avg_focal;
     else              J.zscale = (guidance != 0) ? avg_focal / guidance : 0.0;
+}
+
+// tau column k (0..5: w_x, w_y, w_z, v_x, v_y, v_z) of residual row r
+__device__ __forceinline__ double jac_tau(const JacCore& J, int r, int k) {
+    const double a0 = J.Jpr[3 * r], a1 = J.Jpr[3 * r + 1], a2 = J.Jpr[3 * r + 2];
+    switch (k) {
+        case 0: return -a1 * J.Xr[2] + a2 * J.Xr[1];
+        case 1: return a0 * J.Xr[2] - a2 * J.Xr[0];
+        case 2: return -a0 * J.Xr[1] + a1 * J.Xr[0];
+        case 3: return a0;
+        case 4: return a1;
+        default: return a2;
+    }
+}
+
+// focal column k (0 = fx, 1 = fy) of residual row r
+__device__ __forceinline__ double jac_foc(const JacCore& J, int r, int k) {
+    if (r == 0) return k == 0 ? J.fx_col : 0.0;
+    if (r == 1) return k == 1 ? J.fy_col : 0.0;
+    return J.jkf;
+}
+
+// point column c of residual row r
+__device__ __forceinline__ double jac_pts(const JacCore& J, const CamF& cp, int r, int c) {
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s += J.Jpr[3 * r + k] * (double)cp.Rrw[3 * k + c];
+    return s;
+}
+
+// Full blocks, for the operator-level jacobians_with_rigs.
+// Jcam: 3x8 row-major [fx, fy, wx, wy, wz, vx, vy, vz]; Jp: 3x3.
+struct JacOut {
+    double Jcam[24];
+    double Jp[9];
+    double fbar, zscale;
+    bool valid;
+};
+
+__device__ __forceinline__ void eval_jacobian(const CamF& cp, const float Xf[3], float su, float sv, double guidance,
+                                              int is_depth_log, JacOut& O) {
+    JacCore J;
+    eval_jac_core(cp, Xf, su, sv, guidance, is_depth_log, J);
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        O.Jcam[8 * r + 0] = jac_foc(J, r, 0);
+        O.Jcam[8 * r + 1] = jac_foc(J, r, 1);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) O.Jcam[8 * r + 2 + k] = jac_tau(J, r, k);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) O.Jp[3 * r + c] = jac_pts(J, cp, r, c);
+    }
+    O.fbar = J.fbar;
+    O.zscale = J.zscale;
+    O.valid = J.valid;
 }
 
 }  // namespace ba

@@ -45,7 +45,10 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     g_plan_err.clear();
     if (n_imgs <= 0 || n_obs < 0 || n_tracks < 0) { g_plan_err = "bad sizes"; return nullptr; }
     if (max_local_imgs < 1 || max_local_imgs > BA_MAX_LOCAL) { g_plan_err = "max_local_imgs out of range"; return nullptr; }
-    if (max_slots < 1) { g_plan_err = "max_slots must be >= 1"; return nullptr; }
+    if (max_slots < 1 || max_slots > BA_MAX_SLOTS) {
+        g_plan_err = "max_slots must be in [1, " + std::to_string(BA_MAX_SLOTS) + "]";
+        return nullptr;
+    }
     if (n_obs >= (int64_t)1 << 30) { g_plan_err = "more than 2^30 observations"; return nullptr; }
     if ((int64_t)cum_nkpts[n_imgs - 1] != n_obs) { g_plan_err = "infos[0][-1] != number of observations"; return nullptr; }
     for (int i = 1; i < n_imgs; ++i)

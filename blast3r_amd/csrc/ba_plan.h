@@ -3,8 +3,12 @@
 
 #define BA_CHUNK 128          // observation slots per chunk (one slot per lane in the per-observation phases)
 #define BA_MAX_LOCAL 16       // images a batch may touch (bit mask in 32 bits, local ids in 8 bits)
-#define BA_WAVES 4            // waves per workgroup of the fused Schur kernel
-#define BA_SLOTS_PER_WAVE 24  // camera-pair accumulators held in registers by one wave
+#ifndef BA_WAVES
+#define BA_WAVES 8            // waves per workgroup of the fused Schur kernel (two per SIMD)
+#endif
+#ifndef BA_SLOTS_PER_WAVE
+#define BA_SLOTS_PER_WAVE 12  // camera-pair accumulators held in registers by one wave
+#endif
 #define BA_MAX_SLOTS (BA_WAVES * BA_SLOTS_PER_WAVE)
 #define BA_MAX_CT 64          // tracks per chunk (coverage bit masks in 64 bits)
 

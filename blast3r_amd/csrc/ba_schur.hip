@@ -43,8 +43,14 @@ __device__ __forceinline__ void load_dep(DepSrc& s, const float* g, int C) {
     for (int c = 0; c < BA_PRE_C; ++c) s.r[c] = c < C ? g[c] : 0.f;
 }
 
+// The sqrt(W)-weighted camera rows (image-level layout [foc|tau|zcf], columns 0..15, zero beyond d)
+// are handed element by element to a sink (r, j, value) as they are formed, so no caller holds all
+// of them in registers at once.
+struct NoSink {
+    __device__ __forceinline__ void operator()(int, int, double) const {}
+};
+
 struct ObsLin {
-    double Jc[3][16];     // sqrt(W)-weighted camera rows in the image-level layout [foc|tau|zcf], 0 beyond d
     double Jp[3][3];      // sqrt(W)-weighted point rows
     double Wr[3];         // W*r formed in fp32, widened
     double Rs[3];         // W*r / sqrt(W): the residual that pairs with the weighted rows in J_c^T W r
@@ -56,18 +62,23 @@ __device__ __forceinline__ float clampw(float w, float lo, float hi) {
     return w < lo ? lo : (w > hi ? hi : w);
 }
 
-template <int HK, int HP, bool GRAD_P>
+// Residuals and IRLS weights handed over by the caller (the `residuals`, `w_pts` of solve_delta)
+struct GivenRW {
+    float r[3], w[3];
+};
+
+template <int HK, int HP, bool GRAD_P, class JcSink>
 __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __restrict__ zc_img, const float X[3],
                                               float2 uv, float2 sv, const DepSrc& dep, const HuberParams& hp,
                                               const LinLayout& lay, bool enK, bool enP, bool enZ, bool enX,
-                                              bool first_obs, const float* given_r, const float* given_w, ObsLin& L) {
+                                              bool first_obs, bool given, const GivenRW& grw, ObsLin& L,
+                                              JcSink&& sink) {
     constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
     const int C = lay.C;
     ResOut ro;
-    if (given_r) {
-        // residuals and weights handed to solve_delta by the caller
+    if (given) {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) { ro.r[k] = given_r[k]; ro.w[k] = given_w[k]; }
+        for (int k = 0; k < 3; ++k) { ro.r[k] = grw.r[k]; ro.w[k] = grw.w[k]; }
     } else {
         // residual and weights in fp32 (residuals_with_rigs, .cu:129-259)
         float gf = 0.f;
@@ -81,8 +92,8 @@ __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __res
 #pragma unroll
     for (int c = 0; c < BA_MAX_C; ++c)
         if (c < C) { float pr = zc_img[c] * dep(c); gd += (double)pr; }
-    JacOut J;
-    eval_jacobian(cp, X, sv.x, sv.y, gd, hp.is_depth_log, J);
+    JacCore J;
+    eval_jac_core(cp, X, sv.x, sv.y, gd, hp.is_depth_log, J);
     // W = clamp(w), g uses (W*r) in fp32 cast to fp64, J *= sqrt(W) with sqrt in fp32 (ba_solver.py:123-132)
     double sW[3];
 #pragma unroll
@@ -95,33 +106,35 @@ __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __res
     const double mK = enK ? 1.0 : 0.0, mP = enP ? 1.0 : 0.0;
     const bool zon = lay.hasZ && enZ && J.valid;
     const bool z0off = !lay.optim_Z0 || (first_obs && !lay.optim_Z_1st_cam);      // ba_solver.py:38-39
+    // camera rows, formed element by element from the core
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        double u0 = 0.0, u1 = 0.0, u2 = 0.0;
-        if (j < OT) {
-            u0 = J.Jcam[j] * mK;
-            u1 = J.Jcam[8 + j] * mK;
-            u2 = lay.no_grad_f_from_rz ? 0.0 : J.Jcam[16 + j] * mK;             // ba_solver.py:59-60
-        } else if (j < OZ) {
-            u0 = J.Jcam[2 + (j - OT)] * mP;
-            u1 = J.Jcam[10 + (j - OT)] * mP;
-            u2 = J.Jcam[18 + (j - OT)] * mP;
-        } else {
-            const int c = j - OZ;
-            if (zon && c < C && !(c == 0 && z0off)) u2 = J.zscale * (double)dep(c);
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            double u = 0.0;
+            if (j < OT) {
+                u = (r == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(J, r, j) * mK;     // ba_solver.py:59-60
+            } else if (j < OZ) {
+                u = jac_tau(J, r, j - OT) * mP;
+            } else if (r == 2) {
+                const int c = j - OZ;
+                if (zon && c < C && !(c == 0 && z0off)) u = J.zscale * (double)dep(c);
+            }
+            sink(r, j, u * sW[r]);
         }
-        L.Jc[0][j] = u0 * sW[0];
-        L.Jc[1][j] = u1 * sW[1];
-        L.Jc[2][j] = u2 * sW[2];
     }
     const bool xon = enX && !lay.x_off;
+    double jp[3][3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) jp[r][k] = xon ? jac_pts(J, cp, r, k) : 0.0;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        double jp0 = xon ? J.Jp[k] : 0.0, jp1 = xon ? J.Jp[3 + k] : 0.0, jp2 = xon ? J.Jp[6 + k] : 0.0;
-        if (GRAD_P) L.gP[k] = jp0 * L.Wr[0] + jp1 * L.Wr[1] + jp2 * L.Wr[2];
-        L.Jp[0][k] = jp0 * sW[0];
-        L.Jp[1][k] = jp1 * sW[1];
-        L.Jp[2][k] = jp2 * sW[2];
+        if (GRAD_P) L.gP[k] = jp[0][k] * L.Wr[0] + jp[1][k] * L.Wr[1] + jp[2][k] * L.Wr[2];
+        L.Jp[0][k] = jp[0][k] * sW[0];
+        L.Jp[1][k] = jp[1][k] * sW[1];
+        L.Jp[2][k] = jp[2][k] * sW[2];
     }
 }
 
@@ -173,9 +186,9 @@ __device__ __forceinline__ void load_obs_ctx(const LinArgs& a, int img, ObsCtx& 
 }
 
 // Linearise the observation in plan slot `slot`, reading every input from memory.
-template <int HK, int HP, bool GRAD_P>
+template <int HK, int HP, bool GRAD_P, class JcSink>
 __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, int obs, const ObsCtx& c, ObsLin& L,
-                                               int& pid) {
+                                               int& pid, JcSink&& sink) {
     pid = a.s_pid[slot];
     float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
     float2 uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
@@ -183,19 +196,21 @@ __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, i
     bool enX = a.enX ? a.enX[pid] != 0 : true;
     DepSrc dep;
     load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
-    float gr[3], gw[3];
+    GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
     if (a.r_in) {
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
-            gr[k] = a.r_in[(int64_t)obs * a.r_s0 + k * a.r_s1];
-            gw[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
+            grw.r[k] = a.r_in[(int64_t)obs * a.r_s0 + k * a.r_s1];
+            grw.w[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
         }
     }
     linearize_obs<HK, HP, GRAD_P>(c.cp, c.zc, X, uv, sv, dep, a.hp, a.lay, c.enK, c.enP, c.enZ, enX, obs == 0,
-                                  a.r_in ? gr : nullptr, a.r_in ? gw : nullptr, L);
+                                  a.r_in != nullptr, grw, L, sink);
 }
 
 // ----------------------------------------------------------------------------- point blocks
+// One chunk per block.  Writes, per chunk track (index first_ct + t), H_pp upper, g_p, the point
+// with its enable flag, and the chunk's largest point-block diagonal (for the damping value).
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     __shared__ double sh[BA_CHUNK][9];
@@ -211,7 +226,7 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
         load_obs_ctx(a, a.s_img[slot], ctx);
         ObsLin L;
         int pid;
-        linearize_slot<HK, HP, true>(a, slot, obs, ctx, L, pid);
+        linearize_slot<HK, HP, true>(a, slot, obs, ctx, L, pid, NoSink());
         // J_pts gram (ba_solver.py:911-924) and J_pts^T W r
         const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
 #pragma unroll
@@ -227,7 +242,8 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
     double mx = 0.0;
     if (tid < n_ct) {
-        int f = a.ct_first[first_ct + tid], m = a.ct_m[first_ct + tid], pid = a.ct_pid[first_ct + tid];
+        const int64_t ct = first_ct + tid;
+        const int f = a.ct_first[ct], m = a.ct_m[ct], pid = a.ct_pid[ct];
         double s[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k) s[k] = 0.0;
@@ -235,9 +251,11 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
 #pragma unroll
             for (int k = 0; k < 9; ++k) s[k] += sh[f + q][k];
 #pragma unroll
-        for (int k = 0; k < 6; ++k) a.Hpp[6 * (int64_t)pid + k] = s[k];
+        for (int k = 0; k < 6; ++k) a.Hpp[6 * ct + k] = s[k];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) a.gp[3 * (int64_t)pid + k] = s[6 + k];
+        for (int k = 0; k < 3; ++k) a.gp[3 * ct + k] = s[6 + k];
+        const float* X = a.pts3d + 3 * (int64_t)pid;
+        reinterpret_cast<float4*>(a.ct_pt)[ct] = make_float4(X[0], X[1], X[2], (a.enX ? a.enX[pid] != 0 : true) ? 1.f : 0.f);
         mx = fmax(fmax(fabs(s[0]), fabs(s[3])), fabs(s[5]));
     }
     smax[tid] = mx;
@@ -249,27 +267,36 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     if (tid == 0) a.chunk_max[chunk] = smax[0];
 }
 
-// lam_p = dampen * max diag over all tracks (BlockDiagMat.dampen_, ba_solver.py:575-582)
-__global__ void __launch_bounds__(256) k_lam_reduce(const double* __restrict__ cmax, int64_t n, double dampen,
-                                                    int adaptive, int x_off, double* __restrict__ out) {
+// lam_p = dampen * max diag over all tracks (BlockDiagMat.dampen_, ba_solver.py:575-582).
+// The maximum of non-negative doubles is the maximum of their bit patterns, so blocks combine with
+// an integer atomic max into word n of cmax (cleared by k_lam_clear); the result is order-free.
+__global__ void k_lam_clear(double* __restrict__ cmax, int64_t n) { cmax[n] = 0.0; }
+
+__global__ void __launch_bounds__(256) k_lam_reduce(double* __restrict__ cmax, int64_t n) {
     __shared__ double s[256];
     double m = 0.0;
-    for (int64_t i = threadIdx.x; i < n; i += 256) m = fmax(m, cmax[i]);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) m = fmax(m, cmax[i]);
     s[threadIdx.x] = m;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if ((int)threadIdx.x < w) s[threadIdx.x] = fmax(s[threadIdx.x], s[threadIdx.x + w]);
         __syncthreads();
     }
-    if (threadIdx.x == 0) out[0] = (adaptive && !x_off) ? dampen * s[0] : dampen;
+    if (threadIdx.x == 0)
+        atomicMax(reinterpret_cast<unsigned long long*>(cmax + n), (unsigned long long)__double_as_longlong(s[0]));
+}
+
+__global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double dampen, int adaptive, int x_off,
+                            double* __restrict__ out) {
+    out[0] = (adaptive && !x_off) ? dampen * cmax[n] : dampen;
 }
 
 // ----------------------------------------------------------------------------- camera-pair blocks
 //
-// k_schur: one workgroup (4 waves) per batch.  Per chunk of 128 observation slots:
+// k_schur: one workgroup (8 waves, two per SIMD) per batch.  Per chunk of 128 observation slots:
 //   A1  waves 0-1, lane per slot: linearise; write the weighted camera rows J_c (rows 4-6 of the
-//       slot's LDS block, column 15 = W r / sqrt(W)); wave 2, lane per chunk track: Cholesky factor of the
-//       damped point block, its reciprocal pivots and w = L^-1 g_p; coverage masks by ballot.
+//       slot's LDS block, column 15 = W r / sqrt(W)); wave 2, lane per chunk track: Cholesky factor
+//       of the damped point block, its reciprocal pivots and w = L^-1 g_p; coverage masks by ballot.
 //   A2  waves 0-1: V = J_c^T J_p L^-T (rows 0-2 of the block, column 15 = w for the first
 //       observation of the track in the image, else 0); several observations of one track in one
 //       image are then summed into the first one.
@@ -281,8 +308,8 @@ __global__ void __launch_bounds__(256) k_lam_reduce(const double* __restrict__ c
 //       base address.  The partial block is -acc; column 15 of a diagonal tile then holds
 //       sum J_c^T W r - V w = the image's rhs term, and diag(J_c^T J_c) is summed from the
 //       squared B operands of the J MFMAs.
-// Observation inputs for the next chunk are fetched during the current one (two levels:
-// slot streams first, then the gathers that depend on them).
+// The next chunk's inputs (slot streams, and the chunk-track state written by k_track_pp) are
+// fetched while the current chunk's MFMAs run; every fetch is a single level (no gathers).
 
 __device__ __forceinline__ uint64_t uni64(uint64_t x) {
     uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
@@ -291,22 +318,29 @@ __device__ __forceinline__ uint64_t uni64(uint64_t x) {
 }
 
 struct ObsPre {                 // one observation slot, fetched a chunk ahead
-    int info, obs, pid, enX;
+    int info, obs;
     float2 uv, sv;
     float dep[BA_PRE_C];
-    float X[3];
-    float gr[3], gw[3];
 };
 
 struct TrkPre {                 // one chunk track, fetched a chunk ahead
-    int n_ct, pid, mask;
     double H[6], g[3];
+    float4 X;
+    int mask, n_ct;
 };
 
-__device__ __forceinline__ void obs_pre_l1(const LinArgs& a, int64_t slot, int C, ObsPre& p) {
+// per chunk track in LDS: the fetched state, then (after the factorisation) the factor
+struct TrkStage {
+    double L[6];                // H_pp upper, replaced by the Cholesky factor
+    double w[3];                // g_p, replaced by L^-1 g_p
+    double rp[3];               // reciprocal pivots
+    float4 X;                   // point, enable flag
+    int mask, pad;
+};
+
+__device__ __forceinline__ void obs_fetch(const LinArgs& a, int64_t slot, int C, ObsPre& p) {
     p.info = a.slot_info[slot];
     p.obs = a.chunk_obs[slot];
-    p.pid = a.s_pid[slot];
     p.uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
     p.sv = reinterpret_cast<const float2*>(a.s_std)[slot];
     const float* dg = a.s_dep + slot * C;
@@ -314,39 +348,32 @@ __device__ __forceinline__ void obs_pre_l1(const LinArgs& a, int64_t slot, int C
     for (int c = 0; c < BA_PRE_C; ++c) p.dep[c] = c < C ? dg[c] : 0.f;
 }
 
-__device__ __forceinline__ void obs_pre_l2(const LinArgs& a, ObsPre& p) {
-    const int64_t pid = p.info >= 0 ? p.pid : 0;
-    p.X[0] = a.pts3d[3 * pid]; p.X[1] = a.pts3d[3 * pid + 1]; p.X[2] = a.pts3d[3 * pid + 2];
-    p.enX = a.enX ? a.enX[pid] : 1;
-    if (a.r_in) {
-        const int64_t o = p.info >= 0 ? p.obs : 0;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            p.gr[k] = a.r_in[o * a.r_s0 + k * a.r_s1];
-            p.gw[k] = a.w_in[o * a.w_s0 + k * a.w_s1];
-        }
-    }
-}
-
-__device__ __forceinline__ void trk_pre_l1(const LinArgs& a, int ck, int lane, TrkPre& p) {
-    const int first_ct = a.chunk_meta[4 * ck + 1];
+__device__ __forceinline__ void trk_fetch(const LinArgs& a, int ck, int first_ct, int lane, TrkPre& p) {
     p.n_ct = a.chunk_meta[4 * ck + 2];
-    p.pid = lane < p.n_ct ? a.ct_pid[first_ct + lane] : -1;
-    p.mask = lane < p.n_ct ? a.ct_mask[first_ct + lane] : 0;
+    int64_t ct = (int64_t)first_ct + lane;
+    ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
+    p.mask = a.ct_mask[ct];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) p.H[k] = a.Hpp[6 * ct + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) p.g[k] = a.gp[3 * ct + k];
+    p.X = reinterpret_cast<const float4*>(a.ct_pt)[ct];
 }
 
-__device__ __forceinline__ void trk_pre_l2(const LinArgs& a, TrkPre& p) {
-    const int64_t pid = p.pid >= 0 ? p.pid : 0;
+__device__ __forceinline__ void trk_stage(const TrkPre& p, TrkStage& s) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) p.H[k] = a.Hpp[6 * pid + k];
+    for (int k = 0; k < 6; ++k) s.L[k] = p.H[k];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) p.g[k] = a.gp[3 * pid + k];
+    for (int k = 0; k < 3; ++k) s.w[k] = p.g[k];
+    s.X = p.X;
+    s.mask = p.mask;
 }
 
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks
-    __shared__ double sTrk[BA_MAX_CT][12];               // per chunk track: L (6) | 1/pivots (3) | L^-1 g_p (3)
+    __shared__ TrkStage sTS[BA_MAX_CT];                  // per chunk track
+    __shared__ ObsPre sPre[BA_CHUNK];                    // per observation slot
     __shared__ double sDv[BA_MAX_LOCAL][16];             // per local image: diag(J_c^T J_c)
     __shared__ uint64_t sTm[BA_MAX_LOCAL];               // chunk tracks covering each local image
     __shared__ uint64_t sIm[BA_MAX_LOCAL][2];            // slots observed in each local image
@@ -358,35 +385,43 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
     __shared__ int sPair[BA_MAX_SLOTS];
     __shared__ int sDup[2];
+    __shared__ int sNct;
 
     const int d = a.lay.d, C = a.lay.C;
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const bool obs_lane = tid < BA_CHUNK;                // waves 0-1: one observation slot per lane
+    const bool trk_wave = wave == 2;                     // wave 2: one chunk track per lane
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
     const double lam = a.lam_p[0];
     const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
+    int first_ct = a.chunk_meta[4 * c_begin + 1];
 
-    ObsPre pre;
-    TrkPre tpre;
-    if (tid < BA_CHUNK) obs_pre_l1(a, (int64_t)c_begin * BA_CHUNK + tid, C, pre);
-    else if (wave == 2) trk_pre_l1(a, c_begin, lane, tpre);
-
-    // local image parameters
-    if (tid < nimg) {
-        int img = a.b_imgs[(int64_t)batch * a.L + tid];
-        int node = a.infos[a.n_imgs + img], cam = a.infos[2 * a.n_imgs + img];
-        load_cam(sCam[tid], a.K, a.P_rig2cam, a.P_rig2cam_stride, a.P_w2rig, cam, node);
-        for (int c = 0; c < C; ++c) sZc[tid * BA_MAX_C + c] = a.z_coefs[(int64_t)img * C + c];
-        sEn[3 * tid + 0] = a.enK ? a.enK[cam] : 1;
-        sEn[3 * tid + 1] = a.enP ? a.enP[node] : 1;
-        sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
+    {
+        ObsPre pre;
+        TrkPre tpre;
+        if (obs_lane) obs_fetch(a, (int64_t)c_begin * BA_CHUNK + tid, C, pre);
+        else if (trk_wave) trk_fetch(a, c_begin, first_ct, lane, tpre);
+        // local image parameters
+        if (tid < nimg) {
+            int img = a.b_imgs[(int64_t)batch * a.L + tid];
+            int node = a.infos[a.n_imgs + img], cam = a.infos[2 * a.n_imgs + img];
+            load_cam(sCam[tid], a.K, a.P_rig2cam, a.P_rig2cam_stride, a.P_w2rig, cam, node);
+            for (int c = 0; c < C; ++c) sZc[tid * BA_MAX_C + c] = a.z_coefs[(int64_t)img * C + c];
+            sEn[3 * tid + 0] = a.enK ? a.enK[cam] : 1;
+            sEn[3 * tid + 1] = a.enP ? a.enP[node] : 1;
+            sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
+        }
+        // the pair of slot q: (a | b << 8), -1 past the batch's slots
+        for (int q = tid; q < BA_MAX_SLOTS; q += BA_WAVES * 64) sPair[q] = q < ns ? a.slot_pair[s0 + q] : -1;
+        for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
+        if (obs_lane) sPre[tid] = pre;
+        else if (trk_wave) {
+            trk_stage(tpre, sTS[lane]);
+            if (lane == 0) sNct = tpre.n_ct;
+        }
     }
-    // the pair of slot q: (a | b << 8), -1 past the batch's slots
-    for (int q = tid; q < BA_MAX_SLOTS; q += BA_WAVES * 64) sPair[q] = q < ns ? a.slot_pair[s0 + q] : -1;
-    for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
-    if (tid < BA_CHUNK) obs_pre_l2(a, pre);
-    else if (wave == 2) trk_pre_l2(a, tpre);
     __syncthreads();
 
     dbl4 acc[BA_SLOTS_PER_WAVE];
@@ -396,38 +431,42 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     const int loff = (lane >> 4) * 16 + (lane & 15);
 
     for (int ck = c_begin; ck < c_end; ++ck) {
-        if (ck != c_begin) __syncthreads();    // the previous chunk's blocks are consumed
-        const ObsPre cur = pre;
-        const TrkPre tcur = tpre;
-        const bool more = ck + 1 < c_end;
-        if (more) {
-            if (tid < BA_CHUNK) obs_pre_l1(a, (int64_t)(ck + 1) * BA_CHUNK + tid, C, pre);
-            else if (wave == 2) trk_pre_l1(a, ck + 1, lane, tpre);
-        }
+        if (ck != c_begin) __syncthreads();    // previous chunk consumed; this chunk's inputs staged
+        const int n_ct = sNct;
 
         // ---------------- A1
-        const int info = cur.info;
-        const bool valid = tid < BA_CHUNK && info >= 0;
+        const int info = obs_lane ? sPre[tid].info : -1;
+        const bool valid = info >= 0;
         const int li = info & 0xff, ct = (info >> 8) & 0xff, leader = info >> 16;
-        if (tid < BA_CHUNK) {
+        if (obs_lane) {
             sInfo[tid] = info;
             if (valid) {
+                const ObsPre& pr = sPre[tid];
                 ObsLin L;
                 DepSrc dep;
 #pragma unroll
-                for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = cur.dep[c];
+                for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = pr.dep[c];
                 dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + tid) * C;
-                const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
-                linearize_obs<HK, HP, false>(sCam[li], sZc + li * BA_MAX_C, cur.X, cur.uv, cur.sv, dep, a.hp, a.lay,
-                                             eK, eP, eZ, cur.enX != 0, cur.obs == 0, a.r_in ? cur.gr : nullptr,
-                                             a.r_in ? cur.gw : nullptr, L);
-                double* blk = sBlk + tid * BA_BLK;
+                const float4 Xt = sTS[ct].X;
+                const float X[3] = {Xt.x, Xt.y, Xt.z};
+                const int obs = pr.obs;
+                GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
+                if (a.r_in) {
 #pragma unroll
-                for (int r = 0; r < 3; ++r) {
-#pragma unroll
-                    for (int j = 0; j < 15; ++j) blk[64 + 16 * r + j] = j < d ? L.Jc[r][j] : 0.0;
-                    blk[64 + 16 * r + 15] = L.Rs[r];
+                    for (int k = 0; k < 3; ++k) {
+                        grw.r[k] = a.r_in[(int64_t)obs * a.r_s0 + k * a.r_s1];
+                        grw.w[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
+                    }
                 }
+                const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
+                double* blk = sBlk + tid * BA_BLK;
+                linearize_obs<HK, HP, false>(sCam[li], sZc + li * BA_MAX_C, X, pr.uv, pr.sv, dep, a.hp, a.lay, eK, eP,
+                                             eZ, Xt.w != 0.f, obs == 0, a.r_in != nullptr, grw,
+                                             L, [&](int r, int j, double v) {
+                                                 if (j < 15) blk[64 + 16 * r + j] = j < d ? v : 0.0;
+                                             });
+#pragma unroll
+                for (int r = 0; r < 3; ++r) blk[64 + 16 * r + 15] = L.Rs[r];
 #pragma unroll
                 for (int j = 0; j < 16; ++j) blk[112 + j] = 0.0;
                 // J_p waits in row 0 until A2 overwrites the row with V
@@ -447,33 +486,37 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             if (lane < BA_MAX_LOCAL) { sIm[lane][wave] = im; sLm[lane][wave] = lm; }
             const uint64_t dup = __ballot(valid && leader != tid);
             if (lane == 0) sDup[wave] = dup != 0;
-        } else if (wave == 2) {
-            if (lane < tcur.n_ct) {
-                double Lf[6];
-                chol3_factor(tcur.H, lam, Lf);
-                const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
-                const double w0 = tcur.g[0] * r0;
-                const double w1 = (tcur.g[1] - Lf[1] * w0) * r1;
-                const double w2 = (tcur.g[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
-                double* T = sTrk[lane];
+        } else if (trk_wave) {
+            TrkStage& T = sTS[lane];
+            const int mask = T.mask;
+            if (lane < n_ct) {
+                double H[6], Lf[6];
 #pragma unroll
-                for (int k = 0; k < 6; ++k) T[k] = Lf[k];
-                T[6] = r0; T[7] = r1; T[8] = r2; T[9] = w0; T[10] = w1; T[11] = w2;
+                for (int k = 0; k < 6; ++k) H[k] = T.L[k];
+                chol3_factor(H, lam, Lf);
+                const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
+                const double w0 = T.w[0] * r0;
+                const double w1 = (T.w[1] - Lf[1] * w0) * r1;
+                const double w2 = (T.w[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
+#pragma unroll
+                for (int k = 0; k < 6; ++k) T.L[k] = Lf[k];
+                T.rp[0] = r0; T.rp[1] = r1; T.rp[2] = r2;
+                T.w[0] = w0; T.w[1] = w1; T.w[2] = w2;
             }
             uint64_t tm = 0;
 #pragma unroll
             for (int m = 0; m < BA_MAX_LOCAL; ++m) {
-                const uint64_t b = __ballot((tcur.mask >> m) & 1);
+                const uint64_t b = __ballot(lane < n_ct && ((mask >> m) & 1));
                 if (lane == m) tm = b;
             }
             if (lane < BA_MAX_LOCAL) sTm[lane] = tm;
         }
         __syncthreads();
 
-        // ---------------- A2: V = J_c^T P with P = J_p L^-T
+        // ---------------- A2: V = J_c^T P with P = J_p L^-T, column by column
         if (valid) {
-            const double* T = sTrk[ct];
-            const double l10 = T[1], l20 = T[2], l21 = T[4], r0 = T[6], r1 = T[7], r2 = T[8];
+            const TrkStage& T = sTS[ct];
+            const double l10 = T.L[1], l20 = T.L[2], l21 = T.L[4], r0 = T.rp[0], r1 = T.rp[1], r2 = T.rp[2];
             double* blk = sBlk + tid * BA_BLK;
             double P[3][3];
 #pragma unroll
@@ -483,30 +526,21 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 P[r][2] = (blk[3 * r + 2] - l20 * P[r][0] - l21 * P[r][1]) * r2;
             }
             const bool lead = leader == tid;
-            double V[3][16];
 #pragma unroll
             for (int j = 0; j < 15; ++j) {
                 const double j0 = blk[64 + j], j1 = blk[80 + j], j2 = blk[96 + j];
 #pragma unroll
-                for (int c = 0; c < 3; ++c) V[c][j] = j < d ? j0 * P[0][c] + j1 * P[1][c] + j2 * P[2][c] : 0.0;
+                for (int c = 0; c < 3; ++c) blk[16 * c + j] = j < d ? j0 * P[0][c] + j1 * P[1][c] + j2 * P[2][c] : 0.0;
             }
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-#pragma unroll
-                for (int j = 0; j < 15; ++j) blk[16 * c + j] = V[c][j];
-                blk[16 * c + 15] = lead ? T[9 + c] : 0.0;
-            }
+            for (int c = 0; c < 3; ++c) blk[16 * c + 15] = lead ? T.w[c] : 0.0;
 #pragma unroll
             for (int j = 0; j < 16; ++j) blk[48 + j] = 0.0;
-        }
-        if (more) {
-            if (tid < BA_CHUNK) obs_pre_l2(a, pre);
-            else if (wave == 2) trk_pre_l2(a, tpre);
         }
         __syncthreads();
         if (sDup[0] | sDup[1]) {
             // several observations of one track in one image: V of the run is summed into its first slot
-            if (tid < BA_CHUNK && valid && leader == tid) {
+            if (valid && leader == tid) {
                 double* dst = sBlk + tid * BA_BLK;
                 for (int f = tid + 1; f < BA_CHUNK; ++f) {
                     const int fi = sInfo[f];
@@ -521,61 +555,125 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             __syncthreads();
         }
 
+        // next chunk's inputs: fetched into registers now, staged into LDS after the MFMAs
+        const bool more = ck + 1 < c_end;
+        ObsPre pre;
+        TrkPre tpre;
+        if (more) {
+            if (obs_lane) {
+                obs_fetch(a, (int64_t)(ck + 1) * BA_CHUNK + tid, C, pre);
+            } else if (trk_wave) {
+                first_ct += n_ct;
+                trk_fetch(a, ck + 1, first_ct, lane, tpre);
+            }
+        }
+
         // ---------------- B: camera-pair tiles
+        // coverage masks and first-slot rows of every owned off-diagonal slot, read together
+        int pqs[BA_SLOTS_PER_WAVE];
+        uint64_t covs[BA_SLOTS_PER_WAVE];
+        int rAs[BA_SLOTS_PER_WAVE], rBs[BA_SLOTS_PER_WAVE];
 #pragma unroll
         for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
             const int pq = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
-            if (pq >= 0) {
-                const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
-                if (la != lb) {
-                    uint64_t cov = uni64(sTm[la] & sTm[lb]);
-                    if (cov) {
-                        const int rA = sRowT[la * BA_MAX_CT + lane], rB = sRowT[lb * BA_MAX_CT + lane];
-                        // operands of the next covering track are read while the current MFMA runs
-                        int t = __builtin_ctzll(cov);
-                        cov &= cov - 1;
-                        double A = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                        double B = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
-                        while (cov) {
-                            t = __builtin_ctzll(cov);
-                            cov &= cov - 1;
-                            const double A2 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                            const double B2 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
-                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
-                            A = A2;
-                            B = B2;
-                        }
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A, B, acc[q], 0, 0, 0);
-                    }
-                } else {
-                    // J rows (block offset 64) of every observation in the image, then V rows (offset 0)
-                    // of every (track, image) run, each list walked with the next operand read ahead
-                    // of the current MFMA
-                    double dsq = 0.0;
-                    auto walk = [&](uint64_t w0, uint64_t w1, const int roff, const bool jrows) {
-                        auto pop = [&]() {
-                            int o;
-                            if (w0) { o = __builtin_ctzll(w0); w0 &= w0 - 1; }
-                            else    { o = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; }
-                            return o * BA_BLK + roff + loff;
-                        };
-                        if (!(w0 | w1)) return;
-                        double B = sBlk[pop()];
-                        while (w0 | w1) {
-                            const double B2 = sBlk[pop()];
-                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jrows ? -B : B, B, acc[q], 0, 0, 0);
-                            if (jrows) dsq += B * B;
-                            B = B2;
-                        }
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jrows ? -B : B, B, acc[q], 0, 0, 0);
-                        if (jrows) dsq += B * B;
+            const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
+            pqs[q] = pq;
+            covs[q] = 0;
+            rAs[q] = rBs[q] = 0;
+            if (pq >= 0 && la != lb) {
+                covs[q] = sTm[la] & sTm[lb];
+                rAs[q] = sRowT[la * BA_MAX_CT + lane];
+                rBs[q] = sRowT[lb * BA_MAX_CT + lane];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
+            const int pq = pqs[q];
+            if (pq < 0) continue;
+            const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
+            if (la != lb) {
+                uint64_t cov = uni64(covs[q]);
+                if (cov) {
+                    const int rA = rAs[q], rB = rBs[q];
+                    // operands are read two MFMAs ahead of their use, into two register sets; the
+                    // reads are unconditional (an exhausted list re-reads its last track) so the
+                    // loop body is straight-line and each wait covers only the older pair
+                    int t = 0;
+                    auto adv = [&]() {
+                        if (cov) { t = __builtin_ctzll(cov); cov &= cov - 1; }
                     };
-                    walk(uni64(sIm[la][0]), uni64(sIm[la][1]), 64, true);
-                    walk(uni64(sLm[la][0]), uni64(sLm[la][1]), 0, false);
-                    dsq += __shfl_xor(dsq, 16);
-                    dsq += __shfl_xor(dsq, 32);
-                    if (lane < 16) sDv[la][lane] += dsq;
+                    adv();
+                    double A0 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                    double B0 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                    bool h1 = cov != 0;
+                    adv();
+                    double A1 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                    double B1 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                    for (;;) {
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A0, B0, acc[q], 0, 0, 0);
+                        if (!h1) break;
+                        const bool h0 = cov != 0;
+                        adv();
+                        A0 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                        B0 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A1, B1, acc[q], 0, 0, 0);
+                        if (!h0) break;
+                        h1 = cov != 0;
+                        adv();
+                        A1 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
+                        B1 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                    }
                 }
+            } else {
+                // J rows (block offset 64) of every observation in the image, subtracted (A = -B) and
+                // feeding diag(J_c^T J_c); then V rows (offset 0) of every (track, image) run.  Each
+                // list is walked like the off-diagonal one, two MFMAs of read-ahead.
+                double dsq = 0.0;
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const bool jr = part == 0;
+                    uint64_t w0 = uni64(jr ? sIm[la][0] : sLm[la][0]);
+                    uint64_t w1 = uni64(jr ? sIm[la][1] : sLm[la][1]);
+                    if (!(w0 | w1)) continue;
+                    const int roff = (jr ? 64 : 0) + loff;
+                    int o = 0;
+                    auto adv = [&]() {
+                        if (w0) { o = __builtin_ctzll(w0); w0 &= w0 - 1; }
+                        else if (w1) { o = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; }
+                    };
+                    auto step = [&](double B) {
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jr ? -B : B, B, acc[q], 0, 0, 0);
+                        if (jr) dsq += B * B;
+                    };
+                    adv();
+                    double B0 = sBlk[o * BA_BLK + roff];
+                    bool h1 = (w0 | w1) != 0;
+                    adv();
+                    double B1 = sBlk[o * BA_BLK + roff];
+                    for (;;) {
+                        step(B0);
+                        if (!h1) break;
+                        const bool h0 = (w0 | w1) != 0;
+                        adv();
+                        B0 = sBlk[o * BA_BLK + roff];
+                        step(B1);
+                        if (!h0) break;
+                        h1 = (w0 | w1) != 0;
+                        adv();
+                        B1 = sBlk[o * BA_BLK + roff];
+                    }
+                }
+                dsq += __shfl_xor(dsq, 16);
+                dsq += __shfl_xor(dsq, 32);
+                if (lane < 16) sDv[la][lane] += dsq;
+            }
+        }
+        // stage the next chunk's inputs (A1 and A2 of this chunk are past, so the arrays are free)
+        if (more) {
+            if (obs_lane) sPre[tid] = pre;
+            else if (trk_wave) {
+                trk_stage(tpre, sTS[lane]);
+                if (lane == 0) sNct = tpre.n_ct;
             }
         }
     }
@@ -662,16 +760,15 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         load_obs_ctx(a, img, ctx);
         ObsLin L;
         int pid;
-        linearize_slot<HK, HP, false>(a, slot, obs, ctx, L, pid);
-        double t[3] = {0.0, 0.0, 0.0};
+        // t = J_c delta_c, with delta_c of this image gathered through the unknown map
+        double xs[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            if (j < d) {
-                int u = a.umap[(int64_t)img * d + j];
-                double x = u >= 0 ? a.dc[u] : 0.0;
-                t[0] += L.Jc[0][j] * x; t[1] += L.Jc[1][j] * x; t[2] += L.Jc[2][j] * x;
-            }
+            const int u = j < d ? a.umap[(int64_t)img * d + j] : -1;
+            xs[j] = u >= 0 ? a.dc[u] : 0.0;
         }
+        double t[3] = {0.0, 0.0, 0.0};
+        linearize_slot<HK, HP, false>(a, slot, obs, ctx, L, pid, [&](int r, int j, double v) { t[r] += v * xs[j]; });
 #pragma unroll
         for (int k = 0; k < 3; ++k) y[k] = L.Jp[0][k] * t[0] + L.Jp[1][k] * t[1] + L.Jp[2][k] * t[2];
     }
@@ -679,14 +776,15 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
     __syncthreads();
     const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
     if (tid < n_ct) {
-        int f = a.ct_first[first_ct + tid], m = a.ct_m[first_ct + tid], pid = a.ct_pid[first_ct + tid];
+        const int64_t ctk = first_ct + tid;
+        int f = a.ct_first[ctk], m = a.ct_m[ctk], pid = a.ct_pid[ctk];
         double s[3] = {0.0, 0.0, 0.0};
         for (int q = 0; q < m; ++q) { s[0] += sh[f + q][0]; s[1] += sh[f + q][1]; s[2] += sh[f + q][2]; }
         double H[6], Lf[6], b[3], z[3], x[3];
 #pragma unroll
-        for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * (int64_t)pid + k];
+        for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * ctk + k];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) b[k] = a.gp[3 * (int64_t)pid + k] - s[k];
+        for (int k = 0; k < 3; ++k) b[k] = a.gp[3 * ctk + k] - s[k];
         chol3_factor(H, a.lam_p[0], Lf);
         chol3_fwd(Lf, b, z);
         chol3_bwd(Lf, z, x);
@@ -737,15 +835,17 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
                "inconsistent image-level layout");
     BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "fused path supports at most 24 z-coefficient columns");
     BA_REQUIRE(a.L >= 1 && a.L <= BA_MAX_LOCAL, "bad plan L");
-    if (stage == 0 && a.n_chunks == 0) {
-        BA_HIP(hipMemsetAsync(a.lam_p, 0, sizeof(double), st));
-    } else if (stage == 0) {
-        BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0, st, a));
-        BA_LAUNCHED();
-    }
     if (stage == 0) {
-        hipLaunchKernelGGL(k_lam_reduce, dim3(1), dim3(256), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen,
-                           a.lay.adaptive, a.lay.x_off, a.lam_p);
+        hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks);
+        if (a.n_chunks > 0) {
+            BA_REQUIRE(a.n_ctracks >= 1 && a.ct_pt != nullptr, "chunk-track state missing");
+            BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0,
+                                                     st, a));
+            const int64_t nb = a.n_chunks < 256 * 256 ? (a.n_chunks + 255) / 256 : 256;
+            hipLaunchKernelGGL(k_lam_reduce, dim3((unsigned)nb), dim3(256), 0, st, a.chunk_max, a.n_chunks);
+        }
+        hipLaunchKernelGGL(k_lam_final, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen, a.lay.adaptive,
+                           a.lay.x_off, a.lam_p);
         BA_LAUNCHED();
         return BA_OK;
     }

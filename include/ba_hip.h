@@ -104,9 +104,10 @@ typedef struct {
     const uint8_t *enK, *enP, *enZ, *enX;
     ba_huber hp;
     ba_layout lay;
-    /* per-track fp64 state: H_pp upper (n_tracks,6), g_p (n_tracks,3) */
+    /* per-track state in chunk-track order (the plan's ct_* arrays): H_pp upper (n_ctracks,6) and
+     * g_p (n_ctracks,3) in fp64, the point and its enable flag (n_ctracks,4) in fp32 */
     double *Hpp, *gp;
-    double *chunk_max;   /* (n_chunks) scratch */
+    double *chunk_max;   /* (n_chunks + 1) scratch */
     double *lam_p;       /* (1) point-leaf damping value, written by ba_linearize_schur */
     /* partial blocks: (n_slots, d, d) and (n_batches, L, 2, d) scratch */
     double *partials, *img_partials;
@@ -121,6 +122,8 @@ typedef struct {
      * (the `residuals`, `w_pts` arguments of solve_delta, ba_solver.py:110); NULL = recompute */
     const float *r_in, *w_in;
     int64_t r_s0, r_s1, w_s0, w_s1;
+    float* ct_pt;         /* (n_ctracks,4) scratch written by stage 0: x, y, z, enable */
+    int64_t n_ctracks;
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.

@@ -162,7 +162,7 @@ def test_reduced_system_parity(cfg, nf, nt):
     assert rel_err(S, S.T) < 1e-12                     # symmetric by construction
     # point blocks and their damping
     T = p.n_tracks
-    H = gs.last['Hpp'][:T].cpu()
+    H = gs.point_blocks()[0].cpu()
     Hr = ne.leaves['pts'] - float(gs.last['lam_p'].cpu()) * torch.eye(3, dtype=torch.float64)
     iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
     Hr6 = torch.stack([Hr[:, i, j] for i, j in iu], 1)
