@@ -52,7 +52,7 @@ _LIN_FIELDS = [
     ('pair_ptr', c_p), ('pair_src', c_p), ('img_ptr', c_p), ('img_src', c_p),
     ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p),
     ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
-    ('ct_pt', c_p), ('n_ctracks', c_i64),
+    ('ct_pt', c_p), ('n_ctracks', c_i64), ('core', c_p),
 ]
 
 

@@ -10,7 +10,8 @@
 //                  in fp64 MFMA tiles held in registers, plus rhs and diag(H_cc) per image
 //   k_pair_reduce  per image pair: deterministic sum of the batch partials
 //   k_backsub      per chunk: delta_p = H_pp^-1 (g_p - H_pc delta_c)
-// Every per-observation quantity is recomputed from the inputs (no J is stored).
+// The expensive per-observation work (residual, IRLS weight, Jacobian core) is done once, in
+// k_track_pp, and kept as a 160-byte record per observation; the weighted rows are re-formed from it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -28,6 +29,7 @@ typedef ba_lin_args LinArgs;
 // ----------------------------------------------------------------------------- per observation
 #define BA_PRE_C 8          // depth-guidance channels held in registers (further channels are read from memory)
 #define BA_BLK 129          // doubles per observation block in LDS: 8 rows x 16 columns + 1 pad (spreads banks)
+#define BA_CORE 20          // doubles per observation in the linearisation record
 
 // Depth-guidance channels of one observation: the first BA_PRE_C in registers, the rest in memory.
 // Every access uses a compile-time channel index, so the register part never spills.
@@ -50,13 +52,6 @@ struct NoSink {
     __device__ __forceinline__ void operator()(int, int, double) const {}
 };
 
-struct ObsLin {
-    double Jp[3][3];      // sqrt(W)-weighted point rows
-    double Wr[3];         // W*r formed in fp32, widened
-    double Rs[3];         // W*r / sqrt(W): the residual that pairs with the weighted rows in J_c^T W r
-    double gP[3];         // J_p^T (W r)  (point gradient; only when requested)
-};
-
 __device__ __forceinline__ float clampw(float w, float lo, float hi) {
     // torch.clamp semantics: NaN propagates
     return w < lo ? lo : (w > hi ? hi : w);
@@ -67,13 +62,17 @@ struct GivenRW {
     float r[3], w[3];
 };
 
-template <int HK, int HP, bool GRAD_P, class JcSink>
-__device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __restrict__ zc_img, const float X[3],
-                                              float2 uv, float2 sv, const DepSrc& dep, const HuberParams& hp,
-                                              const LinLayout& lay, bool enK, bool enP, bool enZ, bool enX,
-                                              bool first_obs, bool given, const GivenRW& grw, ObsLin& L,
-                                              JcSink&& sink) {
-    constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
+// Everything the weighted rows of one observation are formed from.
+struct ObsCore {
+    JacCore J;
+    double sW[3];         // sqrt(W), W = clamp(w), sqrt in fp32 (ba_solver.py:123-132)
+    double Wr[3];         // W*r formed in fp32, widened (ba_solver.py:128)
+    double Rs[3];         // W*r / sqrt(W): the residual that pairs with the weighted rows in J^T W r
+};
+
+__device__ __forceinline__ void obs_core(const CamF& cp, const float* __restrict__ zc_img, const float X[3], float2 uv,
+                                         float2 sv, const DepSrc& dep, const HuberParams& hp, const LinLayout& lay,
+                                         bool given, const GivenRW& grw, ObsCore& o) {
     const int C = lay.C;
     ResOut ro;
     if (given) {
@@ -92,49 +91,96 @@ __device__ __forceinline__ void linearize_obs(const CamF& cp, const float* __res
 #pragma unroll
     for (int c = 0; c < BA_MAX_C; ++c)
         if (c < C) { float pr = zc_img[c] * dep(c); gd += (double)pr; }
-    JacCore J;
-    eval_jac_core(cp, X, sv.x, sv.y, gd, hp.is_depth_log, J);
-    // W = clamp(w), g uses (W*r) in fp32 cast to fp64, J *= sqrt(W) with sqrt in fp32 (ba_solver.py:123-132)
-    double sW[3];
+    eval_jac_core(cp, X, sv.x, sv.y, gd, hp.is_depth_log, o.J);
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         float W = clampw(ro.w[r], lay.wmin, lay.wmax);
-        L.Wr[r] = (double)(W * ro.r[r]);
-        sW[r] = (double)sqrtf(W);
-        L.Rs[r] = L.Wr[r] * (1.0 / sW[r]);
+        o.Wr[r] = (double)(W * ro.r[r]);
+        o.sW[r] = (double)sqrtf(W);
+        o.Rs[r] = o.Wr[r] * (1.0 / o.sW[r]);
     }
+}
+
+// The linearisation record of one observation slot, written by the point-block pass and read by
+// the camera-pair and back-substitution passes: chunk-blocked structure of arrays, field f of slot
+// (chunk, t) at rec[(chunk * BA_CORE + f) * BA_CHUNK + t] (coalesced per field).
+//   0-2 X_rig | 3-11 Jpr | 12 d r0/d fx | 13 d r1/d fy | 14 zscale | 15-17 W r / sqrt(W)
+//   18 (J_k_f, sqrt(W_0)) | 19 (sqrt(W_1), sqrt(W_2))  as fp32 pairs (both are fp32 values)
+__device__ __forceinline__ void core_store(double* __restrict__ rec, int t, const ObsCore& o) {
+    auto put = [&](int f, double v) { rec[f * BA_CHUNK + t] = v; };
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put(k, o.J.Xr[k]);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) put(3 + k, o.J.Jpr[k]);
+    put(12, o.J.fx_col);
+    put(13, o.J.fy_col);
+    put(14, o.J.zscale);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put(15 + k, o.Rs[k]);
+    float2* p = reinterpret_cast<float2*>(rec);
+    p[18 * BA_CHUNK + t] = make_float2((float)o.J.jkf, (float)o.sW[0]);
+    p[19 * BA_CHUNK + t] = make_float2((float)o.sW[1], (float)o.sW[2]);
+}
+
+__device__ __forceinline__ void core_load(const double* __restrict__ rec, int t, ObsCore& o) {
+    auto get = [&](int f) { return rec[f * BA_CHUNK + t]; };
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o.J.Xr[k] = get(k);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) o.J.Jpr[k] = get(3 + k);
+    o.J.fx_col = get(12);
+    o.J.fy_col = get(13);
+    o.J.zscale = get(14);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o.Rs[k] = get(15 + k);
+    const float2* p = reinterpret_cast<const float2*>(rec);
+    const float2 a = p[18 * BA_CHUNK + t], b = p[19 * BA_CHUNK + t];
+    o.J.jkf = a.x;
+    o.sW[0] = a.y; o.sW[1] = b.x; o.sW[2] = b.y;
+}
+
+// Weighted camera rows, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60).
+template <int HK, int HP, class JcSink>
+__device__ __forceinline__ void emit_jc(const ObsCore& o, const LinLayout& lay, bool enK, bool enP, bool enZ,
+                                        bool first_obs, const DepSrc& dep, JcSink&& sink) {
+    constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
+    const int C = lay.C;
     const double mK = enK ? 1.0 : 0.0, mP = enP ? 1.0 : 0.0;
-    const bool zon = lay.hasZ && enZ && J.valid;
-    const bool z0off = !lay.optim_Z0 || (first_obs && !lay.optim_Z_1st_cam);      // ba_solver.py:38-39
-    // camera rows, formed element by element from the core
+    const bool zon = lay.hasZ && enZ;                 // an invalid observation has zscale = 0
+    const bool z0off = !lay.optim_Z0 || (first_obs && !lay.optim_Z_1st_cam);
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             double u = 0.0;
             if (j < OT) {
-                u = (r == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(J, r, j) * mK;     // ba_solver.py:59-60
+                u = (r == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(o.J, r, j) * mK;
             } else if (j < OZ) {
-                u = jac_tau(J, r, j - OT) * mP;
+                u = jac_tau(o.J, r, j - OT) * mP;
             } else if (r == 2) {
                 const int c = j - OZ;
-                if (zon && c < C && !(c == 0 && z0off)) u = J.zscale * (double)dep(c);
+                if (zon && c < C && !(c == 0 && z0off)) u = o.J.zscale * (double)dep(c);
             }
-            sink(r, j, u * sW[r]);
+            sink(r, j, u * o.sW[r]);
         }
     }
-    const bool xon = enX && !lay.x_off;
+}
+
+// Weighted point rows Jp (3x3) and, when asked, the point gradient J_p^T (W r) (unweighted rows).
+template <bool GRAD_P>
+__device__ __forceinline__ void point_rows(const ObsCore& o, const CamF& cp, bool xon, double Jp[3][3],
+                                           double gP[3]) {
     double jp[3][3];
 #pragma unroll
     for (int r = 0; r < 3; ++r)
 #pragma unroll
-        for (int k = 0; k < 3; ++k) jp[r][k] = xon ? jac_pts(J, cp, r, k) : 0.0;
+        for (int k = 0; k < 3; ++k) jp[r][k] = xon ? jac_pts(o.J, cp, r, k) : 0.0;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        if (GRAD_P) L.gP[k] = jp[0][k] * L.Wr[0] + jp[1][k] * L.Wr[1] + jp[2][k] * L.Wr[2];
-        L.Jp[0][k] = jp[0][k] * sW[0];
-        L.Jp[1][k] = jp[1][k] * sW[1];
-        L.Jp[2][k] = jp[2][k] * sW[2];
+        if (GRAD_P) gP[k] = jp[0][k] * o.Wr[0] + jp[1][k] * o.Wr[1] + jp[2][k] * o.Wr[2];
+        Jp[0][k] = jp[0][k] * o.sW[0];
+        Jp[1][k] = jp[1][k] * o.sW[1];
+        Jp[2][k] = jp[2][k] * o.sW[2];
     }
 }
 
@@ -185,17 +231,12 @@ __device__ __forceinline__ void load_obs_ctx(const LinArgs& a, int img, ObsCtx& 
     c.enZ = a.enZ ? a.enZ[img] != 0 : true;
 }
 
-// Linearise the observation in plan slot `slot`, reading every input from memory.
-template <int HK, int HP, bool GRAD_P, class JcSink>
-__device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, int obs, const ObsCtx& c, ObsLin& L,
-                                               int& pid, JcSink&& sink) {
-    pid = a.s_pid[slot];
+// Core of the observation in plan slot `slot`, every input gathered from memory.
+__device__ __forceinline__ void obs_core_slot(const LinArgs& a, int64_t slot, int obs, const ObsCtx& c, int pid,
+                                              const DepSrc& dep, ObsCore& o) {
     float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
     float2 uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
     float2 sv = reinterpret_cast<const float2*>(a.s_std)[slot];
-    bool enX = a.enX ? a.enX[pid] != 0 : true;
-    DepSrc dep;
-    load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
     GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
     if (a.r_in) {
 #pragma unroll
@@ -204,13 +245,14 @@ __device__ __forceinline__ void linearize_slot(const LinArgs& a, int64_t slot, i
             grw.w[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
         }
     }
-    linearize_obs<HK, HP, GRAD_P>(c.cp, c.zc, X, uv, sv, dep, a.hp, a.lay, c.enK, c.enP, c.enZ, enX, obs == 0,
-                                  a.r_in != nullptr, grw, L, sink);
+    obs_core(c.cp, c.zc, X, uv, sv, dep, a.hp, a.lay, a.r_in != nullptr, grw, o);
 }
 
 // ----------------------------------------------------------------------------- point blocks
-// One chunk per block.  Writes, per chunk track (index first_ct + t), H_pp upper, g_p, the point
-// with its enable flag, and the chunk's largest point-block diagonal (for the damping value).
+// One chunk per block.  Linearises every observation (residual, weights, Jacobian) once per LM
+// iteration and writes its linearisation record; writes, per chunk track (index first_ct + t),
+// H_pp upper, g_p, the point with its enable flag, and the chunk's largest point-block diagonal
+// (for the damping value).
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     __shared__ double sh[BA_CHUNK][9];
@@ -224,17 +266,23 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     if (obs >= 0) {
         ObsCtx ctx;
         load_obs_ctx(a, a.s_img[slot], ctx);
-        ObsLin L;
-        int pid;
-        linearize_slot<HK, HP, true>(a, slot, obs, ctx, L, pid, NoSink());
+        const int pid = a.s_pid[slot];
+        DepSrc dep;
+        load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
+        ObsCore o;
+        obs_core_slot(a, slot, obs, ctx, pid, dep, o);
+        core_store(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
+        const bool xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
+        double Jp[3][3], gP[3];
+        point_rows<true>(o, ctx.cp, xon, Jp, gP);
         // J_pts gram (ba_solver.py:911-924) and J_pts^T W r
         const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
 #pragma unroll
         for (int q = 0; q < 6; ++q) {
             int i = pr[q][0], j = pr[q][1];
-            c[q] = L.Jp[0][i] * L.Jp[0][j] + L.Jp[1][i] * L.Jp[1][j] + L.Jp[2][i] * L.Jp[2][j];
+            c[q] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
         }
-        c[6] = L.gP[0]; c[7] = L.gP[1]; c[8] = L.gP[2];
+        c[6] = gP[0]; c[7] = gP[1]; c[8] = gP[2];
     }
 #pragma unroll
     for (int k = 0; k < 9; ++k) sh[tid][k] = c[k];
@@ -294,9 +342,10 @@ __global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double d
 // ----------------------------------------------------------------------------- camera-pair blocks
 //
 // k_schur: one workgroup (8 waves, two per SIMD) per batch.  Per chunk of 128 observation slots:
-//   A1  waves 0-1, lane per slot: linearise; write the weighted camera rows J_c (rows 4-6 of the
-//       slot's LDS block, column 15 = W r / sqrt(W)); wave 2, lane per chunk track: Cholesky factor
-//       of the damped point block, its reciprocal pivots and w = L^-1 g_p; coverage masks by ballot.
+//   A1  waves 0-1, lane per slot: form the weighted camera rows J_c from the slot's linearisation
+//       record (rows 4-6 of the slot's LDS block, column 15 = W r / sqrt(W)) and the point rows;
+//       wave 2, lane per chunk track: Cholesky factor of the damped point block, its reciprocal
+//       pivots and w = L^-1 g_p; coverage masks by ballot.
 //   A2  waves 0-1: V = J_c^T J_p L^-T (rows 0-2 of the block, column 15 = w for the first
 //       observation of the track in the image, else 0); several observations of one track in one
 //       image are then summed into the first one.
@@ -319,7 +368,6 @@ __device__ __forceinline__ uint64_t uni64(uint64_t x) {
 
 struct ObsPre {                 // one observation slot, fetched a chunk ahead
     int info, obs;
-    float2 uv, sv;
     float dep[BA_PRE_C];
 };
 
@@ -341,8 +389,6 @@ struct TrkStage {
 __device__ __forceinline__ void obs_fetch(const LinArgs& a, int64_t slot, int C, ObsPre& p) {
     p.info = a.slot_info[slot];
     p.obs = a.chunk_obs[slot];
-    p.uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
-    p.sv = reinterpret_cast<const float2*>(a.s_std)[slot];
     const float* dg = a.s_dep + slot * C;
 #pragma unroll
     for (int c = 0; c < BA_PRE_C; ++c) p.dep[c] = c < C ? dg[c] : 0.f;
@@ -381,7 +427,6 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __shared__ int sInfo[BA_CHUNK];
     __shared__ unsigned char sRowT[BA_MAX_LOCAL * BA_MAX_CT];   // (image, track) -> first slot
     __shared__ CamF sCam[BA_MAX_LOCAL];
-    __shared__ float sZc[BA_MAX_LOCAL * BA_MAX_C];
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
     __shared__ int sPair[BA_MAX_SLOTS];
     __shared__ int sDup[2];
@@ -408,7 +453,6 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             int img = a.b_imgs[(int64_t)batch * a.L + tid];
             int node = a.infos[a.n_imgs + img], cam = a.infos[2 * a.n_imgs + img];
             load_cam(sCam[tid], a.K, a.P_rig2cam, a.P_rig2cam_stride, a.P_w2rig, cam, node);
-            for (int c = 0; c < C; ++c) sZc[tid * BA_MAX_C + c] = a.z_coefs[(int64_t)img * C + c];
             sEn[3 * tid + 0] = a.enK ? a.enK[cam] : 1;
             sEn[3 * tid + 1] = a.enP ? a.enP[node] : 1;
             sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
@@ -442,38 +486,28 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             sInfo[tid] = info;
             if (valid) {
                 const ObsPre& pr = sPre[tid];
-                ObsLin L;
                 DepSrc dep;
 #pragma unroll
                 for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = pr.dep[c];
                 dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + tid) * C;
-                const float4 Xt = sTS[ct].X;
-                const float X[3] = {Xt.x, Xt.y, Xt.z};
-                const int obs = pr.obs;
-                GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
-                if (a.r_in) {
-#pragma unroll
-                    for (int k = 0; k < 3; ++k) {
-                        grw.r[k] = a.r_in[(int64_t)obs * a.r_s0 + k * a.r_s1];
-                        grw.w[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
-                    }
-                }
+                ObsCore o;
+                core_load(a.core + (int64_t)ck * BA_CORE * BA_CHUNK, tid, o);
                 const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
                 double* blk = sBlk + tid * BA_BLK;
-                linearize_obs<HK, HP, false>(sCam[li], sZc + li * BA_MAX_C, X, pr.uv, pr.sv, dep, a.hp, a.lay, eK, eP,
-                                             eZ, Xt.w != 0.f, obs == 0, a.r_in != nullptr, grw,
-                                             L, [&](int r, int j, double v) {
-                                                 if (j < 15) blk[64 + 16 * r + j] = j < d ? v : 0.0;
-                                             });
+                emit_jc<HK, HP>(o, a.lay, eK, eP, eZ, pr.obs == 0, dep, [&](int r, int j, double v) {
+                    if (j < 15) blk[64 + 16 * r + j] = j < d ? v : 0.0;
+                });
 #pragma unroll
-                for (int r = 0; r < 3; ++r) blk[64 + 16 * r + 15] = L.Rs[r];
+                for (int r = 0; r < 3; ++r) blk[64 + 16 * r + 15] = o.Rs[r];
 #pragma unroll
                 for (int j = 0; j < 16; ++j) blk[112 + j] = 0.0;
                 // J_p waits in row 0 until A2 overwrites the row with V
+                double Jp[3][3], gP[3];
+                point_rows<false>(o, sCam[li], sTS[ct].X.w != 0.f && !a.lay.x_off, Jp, gP);
 #pragma unroll
                 for (int r = 0; r < 3; ++r)
 #pragma unroll
-                    for (int k = 0; k < 3; ++k) blk[3 * r + k] = L.Jp[r][k];
+                    for (int k = 0; k < 3; ++k) blk[3 * r + k] = Jp[r][k];
                 if (leader == tid) sRowT[li * BA_MAX_CT + ct] = (unsigned char)tid;
             }
             uint64_t im = 0, lm = 0;
@@ -758,8 +792,11 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         const int img = a.s_img[slot];
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
-        ObsLin L;
-        int pid;
+        const int pid = a.s_pid[slot];
+        DepSrc dep;
+        load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
+        ObsCore o;
+        core_load(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
         double xs[16];
 #pragma unroll
@@ -768,9 +805,13 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
             xs[j] = u >= 0 ? a.dc[u] : 0.0;
         }
         double t[3] = {0.0, 0.0, 0.0};
-        linearize_slot<HK, HP, false>(a, slot, obs, ctx, L, pid, [&](int r, int j, double v) { t[r] += v * xs[j]; });
+        emit_jc<HK, HP>(o, a.lay, ctx.enK, ctx.enP, ctx.enZ, obs == 0, dep,
+                        [&](int r, int j, double v) { t[r] += v * xs[j]; });
+        const bool xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
+        double Jp[3][3], gP[3];
+        point_rows<false>(o, ctx.cp, xon, Jp, gP);
 #pragma unroll
-        for (int k = 0; k < 3; ++k) y[k] = L.Jp[0][k] * t[0] + L.Jp[1][k] * t[1] + L.Jp[2][k] * t[2];
+        for (int k = 0; k < 3; ++k) y[k] = Jp[0][k] * t[0] + Jp[1][k] * t[1] + Jp[2][k] * t[2];
     }
     sh[tid][0] = y[0]; sh[tid][1] = y[1]; sh[tid][2] = y[2];
     __syncthreads();

@@ -124,6 +124,7 @@ typedef struct {
     int64_t r_s0, r_s1, w_s0, w_s1;
     float* ct_pt;         /* (n_ctracks,4) scratch written by stage 0: x, y, z, enable */
     int64_t n_ctracks;
+    double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0) */
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.
