@@ -627,74 +627,63 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
             if (la != lb) {
                 uint64_t cov = uni64(covs[q]);
-                if (cov) {
-                    const int rA = rAs[q], rB = rBs[q];
-                    // operands are read two MFMAs ahead of their use, into two register sets; the
-                    // reads are unconditional (an exhausted list re-reads its last track) so the
-                    // loop body is straight-line and each wait covers only the older pair
-                    int t = 0;
-                    auto adv = [&]() {
-                        if (cov) { t = __builtin_ctzll(cov); cov &= cov - 1; }
-                    };
-                    adv();
-                    double A0 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                    double B0 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
-                    bool h1 = cov != 0;
-                    adv();
-                    double A1 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                    double B1 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
-                    for (;;) {
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A0, B0, acc[q], 0, 0, 0);
-                        if (!h1) break;
-                        const bool h0 = cov != 0;
-                        adv();
-                        A0 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                        B0 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A1, B1, acc[q], 0, 0, 0);
-                        if (!h0) break;
-                        h1 = cov != 0;
-                        adv();
-                        A1 = sBlk[__builtin_amdgcn_readlane(rA, t) * BA_BLK + loff];
-                        B1 = sBlk[__builtin_amdgcn_readlane(rB, t) * BA_BLK + loff];
+                const int rA = rAs[q], rB = rBs[q];
+                // covering tracks in groups of four: the eight operand reads of a group are issued
+                // together, then its four MFMAs run as they arrive (a short group re-reads its first
+                // track with B = 0, adding exact zeros)
+                while (cov) {
+                    int t[4];
+                    int n = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if (cov) { t[k] = __builtin_ctzll(cov); cov &= cov - 1; ++n; }
+                        else t[k] = t[0];
                     }
+                    double A[4], B[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        A[k] = sBlk[__builtin_amdgcn_readlane(rA, t[k]) * BA_BLK + loff];
+                        B[k] = sBlk[__builtin_amdgcn_readlane(rB, t[k]) * BA_BLK + loff];
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[k], k < n ? B[k] : 0.0, acc[q], 0, 0, 0);
+                    // keep the group's LDS reads ahead of its MFMAs (the scheduler would otherwise
+                    // pair each read with its MFMA to save registers, serialising on LDS latency)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 }
             } else {
                 // J rows (block offset 64) of every observation in the image, subtracted (A = -B) and
-                // feeding diag(J_c^T J_c); then V rows (offset 0) of every (track, image) run.  Each
-                // list is walked like the off-diagonal one, two MFMAs of read-ahead.
+                // feeding diag(J_c^T J_c); then V rows (offset 0) of every (track, image) run; both
+                // lists in groups of four like the off-diagonal tracks
                 double dsq = 0.0;
 #pragma unroll
                 for (int part = 0; part < 2; ++part) {
                     const bool jr = part == 0;
                     uint64_t w0 = uni64(jr ? sIm[la][0] : sLm[la][0]);
                     uint64_t w1 = uni64(jr ? sIm[la][1] : sLm[la][1]);
-                    if (!(w0 | w1)) continue;
                     const int roff = (jr ? 64 : 0) + loff;
-                    int o = 0;
-                    auto adv = [&]() {
-                        if (w0) { o = __builtin_ctzll(w0); w0 &= w0 - 1; }
-                        else if (w1) { o = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; }
-                    };
-                    auto step = [&](double B) {
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jr ? -B : B, B, acc[q], 0, 0, 0);
-                        if (jr) dsq += B * B;
-                    };
-                    adv();
-                    double B0 = sBlk[o * BA_BLK + roff];
-                    bool h1 = (w0 | w1) != 0;
-                    adv();
-                    double B1 = sBlk[o * BA_BLK + roff];
-                    for (;;) {
-                        step(B0);
-                        if (!h1) break;
-                        const bool h0 = (w0 | w1) != 0;
-                        adv();
-                        B0 = sBlk[o * BA_BLK + roff];
-                        step(B1);
-                        if (!h0) break;
-                        h1 = (w0 | w1) != 0;
-                        adv();
-                        B1 = sBlk[o * BA_BLK + roff];
+                    while (w0 | w1) {
+                        int o[4];
+                        int n = 0;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            if (w0) { o[k] = __builtin_ctzll(w0); w0 &= w0 - 1; ++n; }
+                            else if (w1) { o[k] = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; ++n; }
+                            else o[k] = o[0];
+                        }
+                        double B[4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) B[k] = sBlk[o[k] * BA_BLK + roff];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const double b = k < n ? B[k] : 0.0;
+                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jr ? -b : b, b, acc[q], 0, 0, 0);
+                            if (jr) dsq += b * b;
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                     }
                 }
                 dsq += __shfl_xor(dsq, 16);
