@@ -37,7 +37,7 @@ def main():
     ap.add_argument('--lm-steps', type=int, default=3)
     ap.add_argument('--cpu-baseline', type=int, default=1)
     ap.add_argument('--copy-probe', action='store_true',
-                    help='run one 256 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
+                    help='run a 256 MiB fill and a 256 MiB kernel copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: multi-GPU runs are not part of this build '
@@ -101,20 +101,27 @@ def main():
     log(f'[bench] linearize+Schur {ms_step:.3f} ms/step, k_schur {schur_ms:.3f} ms -> {value:.4g} obs/s')
 
     if args.copy_probe:
+        # byte-counter calibration: a fill (writes 256 MiB) and a kernel copy (reads 256 MiB,
+        # writes 256 MiB); tensor copy_ may go to a DMA engine, so the copy is an elementwise kernel
         src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
 
-    # roofline of the dominant kernel (k_schur)
+    # roofline of the dominant kernel (k_schur): fp64 MFMA-bound.  Algorithmic flops per launch =
+    # 6 d^2 per (track, image pair) term and per observation (the J_c^T J_c term), d = image-level
+    # parameters; algorithmic bytes of the whole linearize + Schur pass = per observation
+    # pid 4 + pix 8 + std 8 + dep 4C, per track point 12 + H_pp^-1 24 + g_p 12, per reduced
+    # block d^2 fp64 written once, per image g_c d fp64.
     sc = ctx['plan'].scalars
     d, C = ctx['lay']['d'], prob.C
     T = prob.n_tracks
-    bytes_alg = n_obs * (20 + 4 * C) + T * (12 + 72) + sc['n_slots'] * d * d * 8 + sc['n_batches'] * 16 * 2 * d * 8
+    bytes_alg = n_obs * (20 + 4 * C) + T * 48 + sc['n_pairs'] * d * d * 8 + prob.n_imgs * d * 8
     flops_pairs = (sc['n_pair_terms'] + n_obs) * 6 * d * d
     achieved_tf = flops_pairs / (schur_ms * 1e-3) / 1e12
-    achieved_gbs = bytes_alg / (schur_ms * 1e-3) / 1e9
+    achieved_gbs = bytes_alg / (ms_step * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(args.config)
 
     # full LM iterations
     lm_ms = None
@@ -146,26 +153,39 @@ def main():
         'lm_iters_per_s': (1e3 / lm_ms) if lm_ms else None,
         'lm_ms_per_iter': lm_ms,
         'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
-                     'frac': achieved_tf / 78.6, 'traffic': None, 'kernel': 'k_schur',
-                     'kernel_ms': schur_ms, 'flops_per_launch': flops_pairs},
+                     'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': 'k_schur',
+                     'kernel_ms': schur_ms, 'flops_per_launch': flops_pairs, 'traffic_source': traffic_src},
         'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
-                         'bytes_per_launch': bytes_alg, 'kernel': 'k_schur'},
+                         'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)'},
         'cpu_baseline': cpu,
     }
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(cfg, budget_obs=600_000):
+def measured_traffic(cfg):
+    """HBM bytes per k_schur launch from the committed rocprofv3 PMC summary of this workload
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a plain copy of known size),
+    or None when no summary for this configuration is present."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', f'k_schur_cfg{cfg}_pmc.json')
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec['hbm_bytes_per_launch'], os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
+
+
+def cpu_baseline(cfg):
     """Oracle (torch-CPU restatement of the reference's linearisation + normal equations +
     Schur rhs) on a bounded sample of the same configuration, timed on this host."""
     import oracle.kernels as ok
     import oracle.solver as osol
     import oracle.engine as oeng
     from blast3r_amd.synthetic import make_problem
-    threads = os.cpu_count() or 1
+    threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    frames = {0: 32, 1: 64, 2: 128, 3: 256, 4: 128}[cfg]
-    tracks = {0: 20_000, 1: 50_000, 2: 75_000, 3: 40_000, 4: 75_000}[cfg]
+    # about a quarter of the frames and tracks of the configuration (10-30 s of CPU work)
+    frames = {0: 32, 1: 128, 2: 256, 3: 512, 4: 256}[cfg]
+    tracks = {0: 20_000, 1: 100_000, 2: 250_000, 3: 200_000, 4: 250_000}[cfg]
     p = make_problem(cfg, n_frames=frames, n_tracks=tracks)
     o = p.options
     t0 = time.perf_counter()

@@ -166,6 +166,28 @@ typedef struct {
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);
 int64_t ba_pcg_partials_size(int64_t n_u);
 
+/* ------------------------------------------------------------------ LM step (update + line search) */
+
+/* One trial of the lm_step update (engine.py:310-313, :347-354, cujac/__init__.py:56-58):
+ *   K_out = K with fx, fy <- max(f - scale*dK, min_f)     dK (n_cams,2)
+ *   P_out = exp_se3(-scale*dP) @ P_w2rig                   dP (n_nodes,6) = [w|v]
+ *   z_out = z_coefs - scale*dZ                             dZ (n_imgs,C)
+ *   X_out = pts3d - scale*dX                               dX (n_tracks,3)
+ * fp32 in and out; the outputs may not alias the inputs. */
+int ba_apply_update(const float* K, const float* P_w2rig, const float* z_coefs, const float* pts3d,
+                    const float* dK, const float* dP, const float* dZ, const float* dX, float scale, float min_f,
+                    int32_t n_cams, int32_t n_nodes, int32_t n_imgs, int32_t C, int64_t n_tracks, float* K_out,
+                    float* P_out, float* z_out, float* X_out, void* stream);
+
+/* Bytes of device workspace ba_objective needs for n_obs observations. */
+int64_t ba_objective_workspace_bytes(int64_t n_obs);
+
+/* Line-search objective of lm_step (engine.py:263-278, :357-361) from the residual buffer of
+ * ba_residuals (has_err != 0: (9,n_obs) rows r|err|w; else (3,n_obs) rows r):
+ *   out[0] = mean(err) (fp32 result of an fp64 sum), out[1] = reproj_score = mean of the lowest
+ *   80% of ||(r0,r1)|| (exact selection on the fp32 values, no sort).  out is device memory. */
+int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,296 @@
+"""CPU pins of the oracle: each restated function is checked against something other than its
+own formula (closed forms, special cases, torch.func autodiff, dense linear algebra, the
+reference's own `_pcg` vectors), chosen so that a dropped term, a sign or index error or a
+transposed operand fails.  Tolerances are stated per assertion.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.dense as od
+import oracle.engine as oe
+import oracle.kernels as ok
+import oracle.solver as osol
+from helpers import rel_err, tiny_problem
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# ----------------------------------------------------------------------------- residuals (A3)
+def _one_obs(X, pix=(259.0, 191.0), std=(1.0, 2.0), dep=None, zc=None, f=500.0):
+    K = torch.tensor([[[f, 0, 256.0], [0, f, 192.0], [0, 0, 1]]])
+    eye = torch.eye(4).view(1, 4, 4)
+    dep = torch.tensor([dep if dep is not None else [0.0, 1.0, 0.0]])
+    zc = torch.tensor([zc if zc is not None else [1.0, 0.0, 0.0]])
+    return dict(infos=torch.tensor([[1], [0], [0]], dtype=torch.int32), K=K, P_rig2c=eye.expand(1, 4, 4),
+                P_w2rig=eye.clone(), z_coefs=zc, pts3d=torch.tensor([X]), pids=torch.tensor([0], dtype=torch.int32),
+                pix2d=torch.tensor([pix]), pix2d_std=torch.tensor([std]), pix2d_dep=dep)
+
+
+def _res(d, **kw):
+    a = dict(is_depth_log=True, weight_z=1.0, pnorm=1.0, max_pix_err=100.0, huber_delta=2.0, w_pts_null=1e-16)
+    a.update(kw)
+    return ok.residuals_with_rigs(d['infos'], d['K'], d['P_rig2c'], d['P_w2rig'], d['z_coefs'], d['pts3d'], d['pids'],
+                                  d['pix2d'], d['pix2d_std'], d['pix2d_dep'], **a)[0]
+
+
+def test_residual_on_axis_point_and_huber_pnorm1():
+    """Identity pose, point on the optical axis projects to (cx, cy); pnorm = 1 is textbook Huber/IRLS:
+    err = r^2 / (2 delta) (|r| <= delta) or |r| - delta / 2, w = 1 / max(|r|, delta)."""
+    z = 5.0
+    d = _one_obs([0.0, 0.0, z], dep=[math.log(z) + 0.01, 1.0, 0.0], zc=[1.0, 0.003, 0.0])
+    out = _res(d)
+    r0, r1 = (256.0 - 259.0) / 1.0, (192.0 - 191.0) / 2.0
+    r2 = 500.0 * 0.013                                          # fbar (g - ln z), g = ln z + 0.013
+    assert torch.allclose(out[:3], torch.tensor([r0, r1, r2]), rtol=1e-5, atol=1e-4)
+    delta = 2.0
+    huber = lambda r: r * r / (2 * delta) if abs(r) <= delta else abs(r) - delta / 2
+    assert torch.allclose(out[3:6], torch.tensor([huber(r0), huber(r1), huber(r2)]), rtol=1e-5)
+    assert torch.allclose(out[6:9], torch.tensor([1 / max(abs(r), delta) for r in (r0, r1, r2)]), rtol=1e-6)
+
+
+def test_residual_clip_weight_z_and_invalid_depth():
+    """|r| clipped at M: err = wz (M - delta/2), w = w_null (no wz); weight_z scales row 2 only;
+    a point behind the camera (z <= 1e-3) gives all-zero rows."""
+    d = _one_obs([0.0, 0.0, 5.0], pix=(256.0 + 150.0, 192.0), dep=[math.log(5.0) + 0.5, 1.0, 0.0])
+    out = _res(d, weight_z=0.25)
+    assert out[0].item() == pytest.approx(-150.0, rel=1e-6)
+    assert out[3].item() == pytest.approx(100.0 - 1.0, rel=1e-6)          # clipped, pnorm 1
+    assert out[6].item() == pytest.approx(1e-16, rel=1e-6)                # w_null
+    r2 = 500.0 * 0.5
+    assert out[2].item() == pytest.approx(r2, rel=1e-5)
+    assert out[5].item() == pytest.approx(0.25 * (100.0 - 1.0), rel=1e-5)  # clipped and scaled by weight_z
+    assert out[8].item() == pytest.approx(1e-16, rel=1e-6)
+    behind = _res(_one_obs([0.0, 0.0, -2.0]))
+    assert torch.count_nonzero(behind) == 0
+
+
+def test_residual_pnorm2_and_lin_mode():
+    """pnorm = 2: a = p delta^(p-2) / 2 = 1 and b = 0, so err = r^2 on both sides of delta and w = 1;
+    lin depth mode r2 = fbar ln(g / z)."""
+    z = 4.0
+    d = _one_obs([0.0, 0.0, z], dep=[2.0 * z, 1.0, 0.0], zc=[1.0, 0.0, 0.0])
+    out = _res(d, pnorm=2.0, is_depth_log=False)
+    r2 = 500.0 * math.log(2.0)
+    assert out[2].item() == pytest.approx(r2, rel=1e-5)
+    assert out[3].item() == pytest.approx(out[0].item() ** 2, rel=1e-5)
+    assert out[4].item() == pytest.approx(out[1].item() ** 2, rel=1e-5)
+    assert torch.allclose(out[6:8], torch.ones(2))
+    nores = _res(d, pnorm=-1.0)                                   # pnorm -1: residual rows only
+    assert nores.shape == (3,)
+
+
+# ----------------------------------------------------------------------------- Jacobians (A4)
+def _jac_inputs(p):
+    return (p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d_std, p.pix2d_dep)
+
+
+def test_jacobians_match_autodiff():
+    """Camera pose (left perturbation), points, z-coefficients and the r0/r1 focal columns equal
+    torch.func derivatives of an independent fp64 residual; the r2 focal column equals
+    d r2 / d f rounded to fp32 where g > 0 (the reference's J_k_f quirk)."""
+    p = tiny_problem(0, n_frames=6, n_tracks=50)
+    Jc, Jz, Jp = ok.jacobians_with_rigs(*_jac_inputs(p), True, float64=True)
+    af, at, az, ax = od.autodiff_jacobians(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                           p.pix2d_std, p.pix2d_dep, True)
+    assert rel_err(Jp, ax) < 1e-12
+    assert rel_err(Jc[:, :, 2:], at) < 1e-12
+    assert rel_err(Jz[:, 0], az[:, 2]) < 1e-12 and torch.count_nonzero(az[:, :2]) == 0
+    assert rel_err(Jc[:, :2, :2], af[:, :2]) < 1e-12
+    g_pos = (p.z_coefs[ok.obs_to_img(p.infos, len(p.pids))] * p.pix2d_dep).sum(1) > 0
+    assert bool(g_pos.all())
+    assert rel_err(Jc[:, 2, :2], af[:, 2]) < 1e-7                      # fp32-rounded column
+
+
+def test_jacobian_focal_gate_for_negative_guidance():
+    """J_k_f = 0 when g <= 0 even though the true derivative is not (reference quirk, .cu:481-489)."""
+    p = tiny_problem(0, n_frames=5, n_tracks=30)
+    dep = p.pix2d_dep.clone()
+    dep[:, 0] -= 10.0                                               # log-depth channel shifted below 0
+    Jc, _, _ = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d_std,
+                                      dep, True, float64=True)
+    af, _, _, _ = od.autodiff_jacobians(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                        p.pix2d_std, dep, True)
+    assert torch.count_nonzero(Jc[:, 2, :2]) == 0
+    assert torch.count_nonzero(af[:, 2]) > 0
+
+
+# ----------------------------------------------------------------------------- small operators (A8, A6, A9, A14)
+def test_chol3x3_solve_matches_linalg_and_jitter_rules():
+    g = torch.Generator().manual_seed(3)
+    M = torch.randn(200, 3, 3, generator=g, dtype=torch.float64)
+    A = M @ M.transpose(1, 2) + 0.1 * torch.eye(3, dtype=torch.float64)
+    b = torch.randn(200, 3, generator=g, dtype=torch.float64)
+    x = ok.chol3x3_solve(A, b)
+    ref = torch.linalg.solve(A + 1e-12 * torch.eye(3, dtype=torch.float64), b.unsqueeze(-1)).squeeze(-1)
+    assert rel_err(x, ref) < 1e-10
+    # off-diagonals are averaged: an asymmetric block solves like its symmetric part
+    Aa = A.clone()
+    Aa[:, 0, 1] += 0.05
+    Aa[:, 1, 0] -= 0.05
+    assert rel_err(ok.chol3x3_solve(Aa, b), x) < 1e-10
+    # singular (rank-1) blocks: non-positive pivots get the jitter, the result stays finite
+    v = torch.randn(10, 3, 1, generator=g, dtype=torch.float64)
+    S = v @ v.transpose(1, 2)
+    assert torch.isfinite(ok.chol3x3_solve(S, b[:10])).all()
+
+
+def test_blockcoo_matvec_against_dense_assembly():
+    g = torch.Generator().manual_seed(4)
+    nb, bh, bw, HB1, WB1 = 70, 3, 6, 9, 11
+    blocks = torch.randn(nb, bh, bw, generator=g, dtype=torch.float64)
+    rows = torch.randint(0, HB1, (nb,), generator=g)
+    cols = torch.randint(0, WB1, (nb,), generator=g)          # duplicates included
+    D = torch.zeros(HB1 * bh, WB1 * bw, dtype=torch.float64)
+    for k in range(nb):
+        D[rows[k] * bh:(rows[k] + 1) * bh, cols[k] * bw:(cols[k] + 1) * bw] += blocks[k]
+    x = torch.randn(WB1 * bw, generator=g, dtype=torch.float64)
+    y = ok.blockcoo_matvec(blocks, rows, cols, x.view(WB1, bw), HB1, WB1).reshape(-1)
+    assert rel_err(y, D @ x) < 1e-12
+    xt = torch.randn(HB1 * bh, generator=g, dtype=torch.float64)
+    yt = ok.blockcoo_matvec(blocks, rows, cols, xt.view(HB1, bh), HB1, WB1, transpose_blocks=True).reshape(-1)
+    assert rel_err(yt, D.T @ xt) < 1e-12
+
+
+def test_fused_einsum_is_batched_transpose_product():
+    g = torch.Generator().manual_seed(5)
+    L = torch.randn(20, 3, 5, generator=g, dtype=torch.float64)
+    R = torch.randn(20, 3, 7, generator=g, dtype=torch.float64)
+    out = ok.fused_einsum_bki_bkj(L, R)
+    ref = torch.stack([L[b].T @ R[b] for b in range(20)])
+    assert rel_err(out, ref) < 1e-14
+
+
+def test_exp_se3_closed_forms():
+    """Rotation about z by theta (Rodrigues) and a pure translation."""
+    th = 0.7
+    xi = torch.tensor([[0.0, 0.0, th, 0.0, 0.0, 0.0], [0.0, 0.0, 0.0, 1.0, -2.0, 0.5]])
+    T = ok.exp_se3(xi)
+    Rz = torch.tensor([[math.cos(th), -math.sin(th), 0.0], [math.sin(th), math.cos(th), 0.0], [0.0, 0.0, 1.0]])
+    assert torch.allclose(T[0, :3, :3], Rz, atol=1e-6) and torch.allclose(T[0, :3, 3], torch.zeros(3), atol=1e-7)
+    assert torch.allclose(T[1, :3, :3], torch.eye(3)) and torch.allclose(T[1, :3, 3], xi[1, 3:], atol=1e-7)
+    assert torch.allclose(T[:, 3], torch.tensor([0.0, 0.0, 0.0, 1.0]).expand(2, 4))
+
+
+def test_update_K_and_reproj_score():
+    K = torch.tensor([[[300.0, 0, 1], [0, 120.0, 2], [0, 0, 1]]])
+    Kn = oe.update_K(K, torch.tensor([[50.0, 40.0]]))
+    assert Kn[0, 0, 0].item() == 250.0 and Kn[0, 1, 1].item() == 100.0      # clip at 100 (engine.py:352-353)
+    Kc = oe.update_K(K, torch.tensor([[0.0, 30.0]]))
+    assert Kc[0, 1, 1].item() == 100.0
+    r = torch.zeros(10, 3)
+    r[:, 0] = torch.arange(10.0)                                           # norms 0..9
+    assert oe.reproj_score(r).item() == pytest.approx(sum(range(8)) / 8)   # lowest 80% = 8 values
+
+
+# ----------------------------------------------------------------------------- normal equations and Schur (A5-A12)
+def _system(p, **flags):
+    o = p.options
+    _, res, w = oe.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d, p.pix2d_std,
+                             p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'], o['huber_delta'])
+    Jc, Jz, Jp = ok.jacobians_with_rigs(*_jac_inputs(p), True, float64=True)
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, **flags)
+    Jd = od.dense_jacobian(Jc, Jz, Jp, p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks)
+    sizes = (2 * len(p.K), 6 * len(p.P_w2rig), p.C * p.n_imgs, 3 * p.n_tracks)
+    Hd, gd = od.dense_normal_equations(Jd, res, w, sizes)
+    return ne, g, Hd, gd, Jd
+
+
+def test_normal_equations_match_dense_products():
+    p = tiny_problem(0, n_frames=5, n_tracks=40)
+    ne, g, Hd, gd, _ = _system(p)
+    n_c = ne.sizes['n_c']
+    # 1e-7: the reference forms W*r in fp32 and scales J by an fp32 sqrt(W) (ba_solver.py:128-132);
+    # the dense products here use W in fp64, so the two differ by fp32 rounding only
+    assert rel_err(g, gd) < 1e-7
+    assert rel_err(osol.dense_A(ne), Hd[:n_c, :n_c]) < 1e-7
+    Hpp = torch.block_diag(*ne.leaves['pts'])
+    assert rel_err(Hpp, Hd[n_c:, n_c:]) < 1e-7
+    # cross blocks through the operators: B y = H_cp y
+    y = torch.randn(Hd.shape[0] - n_c, dtype=torch.float64)
+    assert rel_err(osol._B_matvec(ne, y), Hd[:n_c, n_c:] @ y) < 1e-7
+
+
+def test_schur_identity_symmetry_psd_and_gauge():
+    """Reduced solve + back-substitution equals the dense solve of the damped system; S is symmetric
+    PSD; the seven similarity directions lie in its (near-)nullspace (damping 1e-12 max diag)."""
+    p = tiny_problem(0, n_frames=5, n_tracks=40)
+    ne, g, Hd, gd, Jd = _system(p)
+    n_c = ne.sizes['n_c']
+    d_red = osol.solve_reduced_direct(ne, g)
+    d_full = torch.linalg.solve(Hd, gd)
+    assert rel_err(Jd @ d_red, Jd @ d_full) < 1e-6                  # equal up to the (damped) gauge span
+    S = osol.dense_schur(ne)
+    assert rel_err(S, S.T) < 1e-12
+    ev = torch.linalg.eigvalsh(0.5 * (S + S.T))
+    assert ev.min().item() > -1e-9 * ev.max().item()
+    B = od.similarity_gauge_basis(p.P_w2rig, p.pts3d, p.n_imgs, len(p.K), p.C)
+    assert rel_err(Jd @ B, torch.zeros(Jd.shape[0], 7, dtype=torch.float64)) < 1e-6 * Jd.norm() * B.norm()
+    Sv = S @ B[:n_c]
+    assert float(Sv.norm()) < 1e-6 * float(S.norm()) * float(B[:n_c].norm())
+
+
+def test_converged_pcg_equals_direct_solve():
+    p = tiny_problem(0, n_frames=5, n_tracks=40)
+    ne, g, _, _, Jd = _system(p)
+    d_pcg, it, conv = osol.solve_reduced_pcg(ne, g, tol=1e-13, maxiter=5000)
+    d_dir = osol.solve_reduced_direct(ne, g)
+    assert rel_err(Jd @ d_pcg, Jd @ d_dir) < 1e-6
+
+
+# ----------------------------------------------------------------------------- PCG control flow (A10)
+@pytest.mark.parametrize('case', ['converges', 'maxiter_hit', 'ill_conditioned', 'indefinite', 'zero_rhs'])
+def test_pcg_against_reference_vectors(case):
+    """Iterate sequence, stopping rule and best-so-far choice against the reference `_pcg`
+    (vectors from tests/golden/make_pcg_golden.py)."""
+    z = np.load(os.path.join(HERE, 'golden', 'pcg_golden.npz'))
+    A = torch.from_numpy(z[f'{case}/A'])
+    b = torch.from_numpy(z[f'{case}/b'])
+    d = A.diagonal().clamp(min=1e-12)
+    x, k, conv = osol.pcg(lambda v: A @ v, b, M_mv=lambda v: v / d, tol=float(z[f'{case}/tol']),
+                          maxiter=int(z[f'{case}/maxiter']))
+    assert int(k) == int(z[f'{case}/iters']) and bool(conv) == bool(z[f'{case}/converged'])
+    xr = torch.from_numpy(z[f'{case}/x'])
+    assert rel_err(x, xr) < 1e-12 if xr.norm() > 0 else float(x.norm()) == 0.0
+
+
+# ----------------------------------------------------------------------------- the LM step (A14)
+def test_oracle_lm_step_decreases_loss_and_follows_schedule():
+    p = tiny_problem(0, n_frames=6, n_tracks=80)
+    o = p.options
+    up, st, info = oe.lm_step(**p.lm_inputs(), weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'])
+    assert float(st.new_loss) < float(st.init_loss)
+    assert info['scale'] in [1.0, 0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0.0]
+
+
+# ----------------------------------------------------------------------------- the C ABI library
+def _header_functions():
+    import re
+    names = []
+    for fn in sorted(os.listdir(os.path.join(HERE, '..', 'include'))):
+        if fn.endswith('.h'):
+            text = open(os.path.join(HERE, '..', 'include', fn)).read()
+            text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+            names += re.findall(r'^[A-Za-z_][\w\s\*]*?\b(ba_\w+)\s*\(', text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    """libba_hip.so loads without a GPU and exports every function include/*.h declares; the
+    Python binding knows the signature of each (no compute call is made here)."""
+    import ctypes
+    from blast3r_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from blast3r_amd.build import build
+        build()
+    so = ctypes.CDLL(_lib.LIB_PATH)
+    names = _header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(so, n)]
+    assert not missing, missing
+    unbound = [n for n in names if n not in _lib._SIGS]
+    assert not unbound, unbound
