@@ -66,7 +66,8 @@ class BaPcgArgs(ctypes.Structure):
                 ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dampen', c_d), ('adaptive', c_int),
                 ('maxiter', c_int), ('tol', c_d),
                 ('rhs', c_p), ('diagA', c_p), ('damp', c_p), ('x', c_p), ('xbest', c_p), ('r', c_p), ('z', c_p),
-                ('p', c_p), ('Ap', c_p), ('y_img', c_p), ('partials', c_p), ('state', c_p), ('istate', c_p)]
+                ('p', c_p), ('Ap', c_p), ('y_img', c_p), ('partials', c_p), ('state', c_p), ('istate', c_p),
+                ('S_rows', c_p), ('n_row_ent', c_i64)]
 
 
 # name -> (restype, argtypes)

@@ -68,7 +68,7 @@ class GaussNewtonSolver:
 
     def __init__(self, n_cams, n_nodes, n_imgs, n_tracks, device, no_grad_f_from_rz=False, dampen=1e-12,
                  adaptive_dampen=True, dtype=torch.float32, solver='pcg', pcg_tol=1e-6, pcg_maxiter=300,
-                 plan_options=None):
+                 plan_options=None, use_graph=True):
         self.cams = Param(n_cams)
         self.nodes = Param(n_nodes)
         self.imgs = Param(n_imgs)
@@ -86,6 +86,7 @@ class GaussNewtonSolver:
         self.pcg_tol = pcg_tol
         self.pcg_maxiter = pcg_maxiter
         self.plan_options = dict(plan_options or {})
+        self.use_graph = bool(use_graph)        # replay the PCG launches from a captured graph
         self.last = {}
 
     # ------------------------------------------------------------------ bs:34-40
@@ -120,6 +121,14 @@ class GaussNewtonSolver:
         """
         d, C = lay['d'], self.n_zcf
         n_imgs = self.imgs.true_n
+        ident = lambda t: None if t is None else (t.data_ptr(), t._version, tuple(t.shape))
+        key = (d, C, lay['hasK'], lay['hasP'], lay['hasZ'], self.cams.n, self.nodes.n, self.imgs.n, n_imgs,
+               ident(J.en['K'][2]), ident(J.en['P'][2]), ident(J.en['Z'][2]))
+        cache = plan.__dict__.setdefault('_umaps', {})
+        if key in cache:
+            return cache[key]
+        if len(cache) > 8:
+            cache.clear()
         cam_ids, node_ids = plan.cam_ids, plan.node_ids
 
         def compact(key, par):
@@ -169,8 +178,10 @@ class GaussNewtonSolver:
             leaf[nf + nt:] += 3
         dev = self.device
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
-        return dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
-                    leaf=t(leaf if n_u else np.zeros(1)))
+        out = dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
+                   leaf=t(leaf if n_u else np.zeros(1)))
+        cache[key] = out
+        return out
 
     # ------------------------------------------------------------------ bs:110-182
     def solve_delta(self, J, residuals, w_pts, clamp_w=(1e-6, 1e6), z_prior=None):
@@ -215,9 +226,10 @@ class GaussNewtonSolver:
         dd = max(d, 1)
         partials = ws('partials', (max(sc['n_slots'], 1), dd, dd), torch.float64)
         img_partials = ws('img_partials', (max(sc['n_batches'], 1), plan.L, 2, dd), torch.float64)
-        S_pairs = torch.empty((max(sc['n_pairs'], 1), dd, dd), dtype=torch.float64, device=dev)
-        e_img = torch.empty((n_imgs, dd), dtype=torch.float64, device=dev)
-        dg_img = torch.empty((n_imgs, dd), dtype=torch.float64, device=dev)
+        # outputs live in the plan's workspace: fixed addresses across LM steps (graph replay)
+        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), torch.float64)
+        e_img = ws('e_img', (n_imgs, dd), torch.float64)
+        dg_img = ws('dg_img', (n_imgs, dd), torch.float64)
 
         a = BaLinArgs()
         pd = plan.dev
@@ -276,8 +288,12 @@ class GaussNewtonSolver:
         n_imgs = self.imgs.true_n
         um = self._unknown_maps(J, lay, plan)
         n_u = um['n_u']
-        x = torch.zeros(max(n_u, 1), dtype=torch.float64, device=dev)
-        istate = torch.zeros(8, dtype=torch.int32, device=dev)
+        if n_u > 0 and d > 0:
+            x = ws('pcg_x', (n_u,), torch.float64)
+            istate = ws('pcg_istate', (8,), torch.int32)
+        else:
+            x = torch.zeros(max(n_u, 1), dtype=torch.float64, device=dev)
+            istate = torch.zeros(8, dtype=torch.int32, device=dev)
         if n_u > 0 and d > 0:
             pa = BaPcgArgs()
             pa.n_u, pa.n_imgs, pa.d = n_u, n_imgs, d
@@ -297,7 +313,10 @@ class GaussNewtonSolver:
             pa.rhs, pa.diagA, pa.damp, pa.x, pa.xbest = ptr(rhs), ptr(diagA), ptr(damp), ptr(x), ptr(xbest)
             pa.r, pa.z, pa.p, pa.Ap, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(Ap), ptr(y_img)
             pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
-            check(lib().ba_pcg_solve(pa, st))
+            n_ent = int(plan.host['row_ptr'][-1]) if len(plan.host['row_ptr']) else 0
+            S_rows = ws('pcg_S_rows', (max(n_ent, 1), d, d), torch.float64)
+            pa.S_rows, pa.n_row_ent = ptr(S_rows), n_ent
+            self._run_pcg(pa, plan, st)
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
         # back-substitution for the points
         dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
@@ -314,6 +333,25 @@ class GaussNewtonSolver:
         if en['X'][2] is not None:
             dXa = dXa[en['X'][2]]
         return torch.cat([dc, dXa.reshape(-1)])
+
+    def _run_pcg(self, pa, plan, st):
+        """ba_pcg_solve, replayed from a HIP graph (captured once per argument set and kept with the
+        plan) so that its ~4 x maxiter launches cost one graph launch."""
+        if not self.use_graph:
+            check(lib().ba_pcg_solve(pa, st))
+            return
+        graphs = plan.__dict__.setdefault('_pcg_graphs', {})
+        key = bytes(pa)
+        g = graphs.get(key)
+        if g is None:
+            if len(graphs) > 4:
+                graphs.clear()
+            g = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize(self.device)
+            with torch.cuda.graph(g):
+                check(lib().ba_pcg_solve(pa, stream_ptr(self.device)))
+            graphs[key] = g
+        g.replay()
 
     def _add_z_prior(self, z_prior, lay, plan, S_pairs, e_img, dg_img):
         """Tangent-prior terms on the z-coefficient blocks before damping (bs:141-173)."""

@@ -19,8 +19,8 @@ namespace ba {
 #define PCG_T 256
 
 enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_LEAF = 8 };
-// istate: done flag of iteration k lives in IS_DONE0 + (k & 1) so that the kernel writing the
-// flag for k+1 never races with blocks of the same launch still reading the flag for k.
+// istate: IS_DONE0 / IS_DONE1 done flags (double-buffered by iteration parity), IS_K iterations,
+// IS_CONV converged, IS_BESTK best iterate, IS_USEBEST the best iterate is returned.
 enum { IS_DONE0 = 0, IS_DONE1 = 1, IS_K = 2, IS_CONV = 3, IS_BESTK = 4, IS_USEBEST = 5 };
 
 __device__ __forceinline__ double block_sum(double v, double* sh) {
@@ -124,31 +124,63 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
     }
 }
 
-// y_img[i][j] = sum over the pair blocks of image row i of S_blk(j, :) . x_img; one wave per
-// image: lane (g, j) takes output row j of every 4th block of the row, then the 4 groups add up
-__global__ void __launch_bounds__(PCG_T) k_spmv_img(ba_pcg_args a, const double* __restrict__ xin, int k) {
+// Image-row copies of the pair blocks, column-major: entry q of image row i (pair p, flag tr) holds
+// B = S(i, i2) with B[j][j2] at S_rows[q][j2 * d + j], so that the SpMV's lanes (one per output
+// row j) read each column of a block contiguously.  S(i, i2) is S_p for tr = 0 and S_p^T for tr = 1.
+__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent) {
+    const int d = a.d, dd = d * d;
+    const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+    if (tid >= n_ent * dd) return;
+    const int64_t q = tid / dd;
+    const int e = (int)(tid - q * dd);
+    const int j2 = e / d, j = e - (e / d) * d;
+    const int ent = a.row_ent[q];
+    const int64_t p = ent >> 1;
+    const double* S = a.S_pairs + p * dd;
+    a.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
+}
+
+// ----------------------------------------------------------------------------- one CG iteration
+// Four launches per iteration; a launch whose iteration is past the stopping point returns at
+// once (the done flag of iteration k lives in IS_DONE0 + (k & 1), so the kernel that writes the
+// flag for k + 1 never races with blocks of the same launch reading the flag for k).
+
+// y_img[i][j] = sum over the blocks of image row i of S(i, i2)[j, :] . p(i2): one workgroup per
+// image row; its 16 lane groups (one lane per output row j) take every 16th block of the row, and
+// the group sums are added in LDS in a fixed order.  The 16 unknown indices of a block, then the 16
+// values, are read as independent loads.
+__global__ void __launch_bounds__(PCG_T) k_spmv_img(ba_pcg_args a, int k) {
+    __shared__ double sh[PCG_T];
     if (a.istate[IS_DONE0 + (k & 1)]) return;
-    const int lane = threadIdx.x & 63, grp = lane >> 4, j = lane & 15;
-    const int i = blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);
-    if (i >= a.n_imgs) return;
-    const int d = a.d;
+    const int i = blockIdx.x;
+    const int grp = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int d = a.d, dd = d * d;
     double acc = 0.0;
     if (j < d) {
-        for (int q = a.row_ptr[i] + grp; q < a.row_ptr[i + 1]; q += 4) {
-            int ent = a.row_ent[q];
-            int p = ent >> 1, tr = ent & 1;
-            int i2 = tr ? a.pair_i1[p] : a.pair_i2[p];
-            const double* blk = a.S_pairs + (int64_t)p * d * d;
+        for (int q = a.row_ptr[i] + grp; q < a.row_ptr[i + 1]; q += PCG_T / 16) {
+            const int ent = a.row_ent[q];
+            const int pr = ent >> 1;
+            const int i2 = (ent & 1) ? a.pair_i1[pr] : a.pair_i2[pr];
+            const double* B = a.S_rows + (int64_t)q * dd;
             const int* um = a.umap + (int64_t)i2 * d;
-            for (int j2 = 0; j2 < d; ++j2) {
-                int u2 = um[j2];
-                if (u2 >= 0) acc += (tr ? blk[j2 * d + j] : blk[j * d + j2]) * xin[u2];
-            }
+            int u2[16];
+#pragma unroll
+            for (int j2 = 0; j2 < 16; ++j2) u2[j2] = j2 < d ? um[j2] : -1;
+            double xv[16];
+#pragma unroll
+            for (int j2 = 0; j2 < 16; ++j2) xv[j2] = u2[j2] >= 0 ? a.p[u2[j2]] : 0.0;
+#pragma unroll
+            for (int j2 = 0; j2 < 16; ++j2)
+                if (j2 < d) acc += B[j2 * d + j] * xv[j2];
         }
     }
-    acc += __shfl_down(acc, 32);
-    acc += __shfl_down(acc, 16);
-    if (grp == 0 && j < d) a.y_img[(int64_t)i * d + j] = acc;
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16 && j < d) {
+        double t = 0.0;
+        for (int g = 0; g < PCG_T / 16; ++g) t += sh[16 * g + j];
+        a.y_img[(int64_t)i * d + j] = t;
+    }
 }
 
 // Ap[u] = sum of the image-level rows mapping to u + damp[u] p[u] (one wave per unknown);
@@ -199,7 +231,7 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int nb, int
 }
 
 // best-so-far bookkeeping, stopping test, beta and the new search direction
-// k counts from 0; the reference numbers the same iteration k+1.
+// (ba_solver.py:1222-1236); k counts from 0, the reference numbers the same iteration k + 1.
 __global__ void __launch_bounds__(PCG_T) k_pcg_dir(ba_pcg_args a, int nb, int k) {
     __shared__ double sh[PCG_T];
     if (a.istate[IS_DONE0 + (k & 1)]) {
@@ -250,18 +282,22 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(args != nullptr, "null args");
     const ba_pcg_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
-    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.maxiter >= 0, "bad sizes");
+    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16 && a.maxiter >= 0, "bad sizes");
     if (a.n_u == 0) return BA_OK;
     const unsigned nb = nb_of(a.n_u);
     const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown
-    const unsigned nbi = (unsigned)((a.n_imgs + PCG_T / 64 - 1) / (PCG_T / 64));     // wave per image
+    const int64_t n_ent = a.n_row_ent;
+    BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr, "image-row block workspace missing");
+    if (n_ent > 0)
+        hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * a.d * a.d + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
+                           n_ent);
     hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_leaf_damp, dim3(1), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
     BA_LAUNCHED();
     for (int it = 0; it < a.maxiter; ++it) {
-        hipLaunchKernelGGL(k_spmv_img, dim3(nbi), dim3(PCG_T), 0, st, a, (const double*)a.p, it);
+        hipLaunchKernelGGL(k_spmv_img, dim3((unsigned)a.n_imgs), dim3(PCG_T), 0, st, a, it);
         hipLaunchKernelGGL(k_spmv_unk, dim3(nbw), dim3(PCG_T), 0, st, a, it);
         hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, (int)nbw, it);
         hipLaunchKernelGGL(k_pcg_dir, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, it);

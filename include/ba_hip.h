@@ -156,13 +156,17 @@ typedef struct {
     double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *Ap, *y_img;
     double *partials;                  /* 3 * n_blocks */
     double *state;                     /* 16 doubles */
-    int32_t *istate;                   /* 8 ints: done, k, converged, best_k, ... */
+    int32_t *istate;                   /* 8 ints: [0], [1] done flags, [2] iterations, [3] converged,
+                                          [4] best iteration, [5] best iterate returned */
+    double *S_rows;                    /* (n_row_ent, d, d): the pair blocks copied per image row */
+    int64_t n_row_ent;                 /* row_ptr[n_imgs] */
 } ba_pcg_args;
 
 /* Builds the unknown-level rhs, diag(A) with per-leaf damping (ba_solver.py:575-582,
  * :1188-1191) and runs Jacobi-PCG (ba_solver.py:184-206, :1197-1238) on
- * S = P^T S_img P + damping, entirely on the device.  The solution is left in x
- * (converged) or xbest; istate[2] = converged, istate[1] = iterations. */
+ * S = P^T S_img P + damping, entirely on the device (four launches per iteration, no host
+ * synchronisation).  The result (the converged iterate, else the best one) is left in x;
+ * istate holds the loop's outcome. */
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);
 int64_t ba_pcg_partials_size(int64_t n_u);
 

@@ -189,6 +189,37 @@ def test_pcg_step_parity(cfg, nf, nt):
     assert rel_err(sW[:, None] * Jd @ delta.cpu().double(), sW[:, None] * Jd @ d_ref) < 1e-4
 
 
+def test_pcg_graph_replay_matches_eager():
+    """The PCG replayed from its captured HIP graph equals the eager launches bit for bit on every
+    replay, with the program's own eager work and synchronisations between the replays."""
+    p = make_problem(0, n_frames=12, n_tracks=600)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+
+    def solve(use_graph):
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, use_graph=use_graph)
+        J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, pix2d=g.pix2d, hp=hp)
+        d = gs.solve_delta(J, res, w)
+        return d.clone(), gs.last['istate'].clone()
+
+    d_e, ist_e = solve(False)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        d_g, ist_g = solve(True)
+        torch.cuda.synchronize()
+        y = torch.randn(4096, device=DEV)
+        assert float((y * y).sum()) > 0                     # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(ist_g, ist_e), rep
+        assert torch.equal(d_g, d_e), rep
+
+
 def test_solver_flags_parity():
     """optim_K / optim_P off (depth stitching), optim_X off, tensor masks, optim_Z0 off."""
     p4 = make_problem(4, n_frames=10, n_tracks=300)
