@@ -36,6 +36,8 @@ def main():
     ap.add_argument('--tracks', type=int, default=None)
     ap.add_argument('--lm-steps', type=int, default=3)
     ap.add_argument('--cpu-baseline', type=int, default=1)
+    ap.add_argument('--sampling', type=int, default=1,
+                    help='also time the F-sampling kernel on maps of the configuration (1 = yes)')
     ap.add_argument('--copy-probe', action='store_true',
                     help='run a 256 MiB fill and a 256 MiB kernel copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
@@ -137,6 +139,8 @@ def main():
         lm_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
         log(f'[bench] lm_step {lm_ms:.2f} ms')
 
+    smp = bench_sampling(prob, g, dev, args.steps, args.warmup) if args.sampling else None
+
     cpu = None
     if args.cpu_baseline:
         cpu = cpu_baseline(args.config)
@@ -158,8 +162,65 @@ def main():
         'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
                          'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)'},
         'cpu_baseline': cpu,
+        'f_sampling': smp,
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_sampling(prob, g, dev, steps, warmup):
+    """F sampling (ba_sample_depth) at the configuration's size: one (384, 512, C) fp32 map per
+    frame (C = K + 1 channels with the ones channel stacked, as the reference's maps are) and the
+    configuration's observations.  Algorithmic bytes per observation: pixel 8 + four texels 16 C
+    read + row 4 C written.  Beside it, the reference's own call sequence on the same GPU (one
+    torch grid_sample per frame, geometry.py:183-196)."""
+    import torch.nn.functional as F
+    from blast3r_amd.sampling import sample_depth_maps
+    H, W, C = 384, 512, prob.C
+    gen = torch.Generator(device=dev).manual_seed(5)
+    maps = torch.rand((prob.n_imgs, H, W, C), device=dev, generator=gen)
+    cum = g.infos[0].contiguous()
+    pix = g.pix2d.contiguous()
+    out = torch.empty((prob.n_obs, C), device=dev)
+    for _ in range(warmup):
+        sample_depth_maps(maps, cum, pix, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sample_depth_maps(maps, cum, pix, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # the reference's loop (one grid_sample per frame) on the same inputs, for comparison
+    cum_h = [0] + g.infos[0].tolist()
+    scale = pix.new_tensor([2 / W, 2 / H])
+
+    def ref_loop():
+        res = []
+        for i in range(prob.n_imgs):
+            p = pix[cum_h[i]:cum_h[i + 1]].reshape(1, 1, -1, 2)
+            r = F.grid_sample(maps[i:i + 1].permute(0, 3, 1, 2), p * scale - 1, mode='bilinear',
+                              padding_mode='border', align_corners=False)
+            res.append(r.permute(0, 2, 3, 1).reshape(-1, C))
+        return torch.cat(res)
+
+    ref_loop()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        ref_loop()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3 / 3
+    bytes_alg = prob.n_obs * (8 + 16 * C + 4 * C)
+    gbs = bytes_alg / (ms * 1e-3) / 1e9
+    log(f'[bench] F sampling {ms:.3f} ms ({prob.n_obs / (ms * 1e-3):.4g} obs/s, {gbs:.0f} GB/s algorithmic); '
+        f'torch grid_sample per frame {ref_ms:.2f} ms')
+    del maps
+    return {'kernel': 'k_sample', 'ms': ms, 'obs_per_s': prob.n_obs / (ms * 1e-3),
+            'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
+                         'bytes_per_launch': bytes_alg},
+            'maps': f'{prob.n_imgs} x {H} x {W} x {C} fp32 (uniform random values)',
+            'torch_grid_sample_per_frame_ms': ref_ms}
 
 
 def measured_traffic(cfg):

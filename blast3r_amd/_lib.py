@@ -70,6 +70,12 @@ class BaPcgArgs(ctypes.Structure):
                 ('S_rows', c_p), ('n_row_ent', c_i64)]
 
 
+class BaSampleArgs(ctypes.Structure):
+    _fields_ = [('map_addr', c_p), ('map_hw', c_p), ('H', c_int), ('W', c_int), ('Cm', c_int), ('pix_stride', c_int),
+                ('insert_ones', c_int),
+                ('cum_nppi', c_p), ('n_imgs', c_i64), ('pix2d', c_p), ('n_obs', c_i64), ('out', c_p)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     'ba_last_error': (ctypes.c_char_p, []),
@@ -97,6 +103,7 @@ _SIGS = {
                                 c_p, c_p, c_p, c_p, c_p]),
     'ba_objective_workspace_bytes': (c_i64, [c_i64]),
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
+    'ba_sample_depth': (c_int, [ctypes.POINTER(BaSampleArgs), c_p]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -191,8 +191,18 @@ __global__ void __launch_bounds__(PCG_T) k_spmv_unk(ba_pcg_args a, int k) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + w;
     double s = 0.0;
-    if (u < a.n_u)
-        for (int q = a.inv_ptr[u] + lane; q < a.inv_ptr[u + 1]; q += 64) s += a.y_img[a.inv_src[q]];
+    if (u < a.n_u) {
+        // a shared unknown (one focal pair for every image of a camera) has a long list: its
+        // entries are read 8 per lane at a time as independent loads
+        const int q0 = a.inv_ptr[u], q1 = a.inv_ptr[u + 1];
+        for (int q = q0 + lane; q < q1; q += 64 * 8) {
+            int src[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) src[t] = q + 64 * t < q1 ? a.inv_src[q + 64 * t] : -1;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
+        }
+    }
     for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off);
     double pap = 0.0;
     if (lane == 0 && u < a.n_u) {

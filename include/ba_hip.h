@@ -192,6 +192,33 @@ int64_t ba_objective_workspace_bytes(int64_t n_obs);
  *   80% of ||(r0,r1)|| (exact selection on the fp32 values, no sort).  out is device memory. */
 int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out, void* stream);
 
+/* ------------------------------------------------------------------ F sampling */
+
+/* Multi-depth values at the observations (replaces the per-image bilinear_sampling calls of
+ * gather_data_from_dense_tracks, src/blast3r/inference/tracks.py:865-872, and
+ * src/blast3r/utils/geometry.py:167-198: grid_sample bilinear, padding 'border',
+ * align_corners=False, pixel (i, j) centred at (i + .5, j + .5)).
+ * Observation o belongs to image img(o) = upper bound of o in cum_nppi (image-major order,
+ * rigs.py:50-51); its row of out is the bilinear sample of that image's map at pix2d[o]. */
+typedef struct {
+    const int64_t* map_addr;   /* (n_imgs,) device addresses of the maps, each (H, W, Cm) fp32 row-major */
+    const int32_t* map_hw;     /* (n_imgs, 2) per-image H, W; null when every map is H x W */
+    int32_t H, W;              /* map size when map_hw is null */
+    int32_t Cm;                /* channels sampled per map, 1..1024 */
+    int32_t pix_stride;        /* floats from one pixel to the next (rows are W * pix_stride apart);
+                                  0 means Cm.  A channel slice of a wider map, e.g. raw[..., 2:], is
+                                  sampled in place with map_addr at its first channel */
+    int32_t insert_ones;       /* 1: out column 1 is a sampled constant-one channel and map channel c >= 1
+                                  goes to column c + 1 (the stack [F0, 1, F1, ...] of multidepth.py:53-54) */
+    const int32_t* cum_nppi;   /* (n_imgs,) inclusive cumulative observation counts (infos row 0) */
+    int64_t n_imgs;
+    const float* pix2d;        /* (n_obs, 2) pixel coordinates x, y */
+    int64_t n_obs;
+    float* out;                /* (n_obs, Cm + insert_ones) fp32 */
+} ba_sample_args;
+
+int ba_sample_depth(const ba_sample_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
