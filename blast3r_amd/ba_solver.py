@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
+from ._lib import PCG_LONG_LIST, BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
 from .plan import get_plan
 
 N_FOC = 2   # focal columns (bs:11)
@@ -178,8 +178,10 @@ class GaussNewtonSolver:
             leaf[nf + nt:] += 3
         dev = self.device
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        long_u = np.nonzero(counts > PCG_LONG_LIST)[0]
         out = dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
-                   leaf=t(leaf if n_u else np.zeros(1)))
+                   leaf=t(leaf if n_u else np.zeros(1)), long_u=t(long_u if len(long_u) else np.zeros(1)),
+                   n_long=len(long_u))
         cache[key] = out
         return out
 
@@ -306,7 +308,8 @@ class GaussNewtonSolver:
             pa.maxiter, pa.tol = int(self.pcg_maxiter), float(self.pcg_tol)
             vec = lambda name: ws('pcg_' + name, (n_u,), torch.float64)
             rhs, diagA, damp = vec('rhs'), vec('diagA'), vec('damp')
-            xbest, r, z, p, Ap = vec('xbest'), vec('r'), vec('z'), vec('p'), vec('Ap')
+            xbest, r, z, Ap = vec('xbest'), vec('r'), vec('z'), vec('Ap')
+            p = ws('pcg_p2', (2 * n_u,), torch.float64)
             y_img = ws('pcg_y', (n_imgs * d,), torch.float64)
             part = ws('pcg_part', (int(lib().ba_pcg_partials_size(n_u)),), torch.float64)
             state = ws('pcg_state', (16,), torch.float64)
@@ -316,6 +319,8 @@ class GaussNewtonSolver:
             n_ent = int(plan.host['row_ptr'][-1]) if len(plan.host['row_ptr']) else 0
             S_rows = ws('pcg_S_rows', (max(n_ent, 1), d, d), torch.float64)
             pa.S_rows, pa.n_row_ent = ptr(S_rows), n_ent
+            pa.row_u = ptr(ws('pcg_row_u', (max(n_ent, 1) * 16,), torch.int32))
+            pa.long_u, pa.n_long = ptr(um['long_u']), um['n_long']
             self._run_pcg(pa, plan, st)
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
         # back-substitution for the points

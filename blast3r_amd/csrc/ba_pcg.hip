@@ -17,29 +17,46 @@
 namespace ba {
 
 #define PCG_T 256
+#define PCG_ST 512          // threads of the image-row SpMV: 32 groups of 16 lanes
 
-enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_LEAF = 8 };
-// istate: IS_DONE0 / IS_DONE1 done flags (double-buffered by iteration parity), IS_K iterations,
+// state (fp64): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
+// both in slot n & 1; ST_BETA the beta of the current direction; ST_LEAF.. the camera-leaf damping.
+enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_BETA = 5, ST_LEAF = 8 };
+// istate: IS_DONE0 / IS_DONE1 "stopped before update n" in slot n & 1, IS_K iterations run,
 // IS_CONV converged, IS_BESTK best iterate, IS_USEBEST the best iterate is returned.
 enum { IS_DONE0 = 0, IS_DONE1 = 1, IS_K = 2, IS_CONV = 3, IS_BESTK = 4, IS_USEBEST = 5 };
 
-__device__ __forceinline__ double block_sum(double v, double* sh) {
-    sh[threadIdx.x] = v;
-    __syncthreads();
-    for (int w = PCG_T / 2; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
-        __syncthreads();
-    }
-    double r = sh[0];
-    __syncthreads();
-    return r;
+// search direction of update n: p_n = z_n + beta_n p_{n-1} (ba_solver.py:1235), written as one
+// fused multiply-add so that every kernel that forms it gets the same bits
+__device__ __forceinline__ double pdir(double z, double pold, double beta) { return fma(beta, pold, z); }
+
+// Sum over the 64 lanes of a wave; every lane gets the same bits (each butterfly step adds the
+// same two values in either lane, and fp addition commutes).
+__device__ __forceinline__ double wave_sum(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
 }
 
-// Sum of n block partials at stride 3 (deterministic, identical in every block).
+// Sum over a block of NT threads in a fixed order (waves by butterfly, then the wave sums in wave
+// order); every thread gets the result.  sh holds at least NT / 64 doubles.
+template <int NT>
+__device__ __forceinline__ double block_sum(double v, double* sh) {
+    v = wave_sum(v);
+    __syncthreads();                                  // sh may still be read by a previous call
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int k = 0; k < NT / 64; ++k) t += sh[k];
+    return t;
+}
+
+// Sum of n block partials at stride 3 (deterministic, identical in every block of NT threads).
+template <int NT>
 __device__ __forceinline__ double sum_partials(const double* __restrict__ part, int nb, int which, double* sh) {
     double v = 0.0;
-    for (int b = threadIdx.x; b < nb; b += PCG_T) v += part[3 * b + which];
-    return block_sum(v, sh);
+    for (int b = threadIdx.x; b < nb; b += NT) v += part[3 * b + which];
+    return block_sum<NT>(v, sh);
 }
 
 // unknown-level rhs and diag(H_cc) from the image-level vectors; one wave per unknown so that
@@ -94,7 +111,7 @@ __global__ void __launch_bounds__(PCG_T) k_leaf_damp(ba_pcg_args a) {
     }
 }
 
-// x = 0, r = b, z = M^-1 r, p = z; partials of b.b and r.z
+// x = 0, r = b, z = M^-1 r, p_{-1} = 0 (so that p_0 = z_0); partials of b.b and r.z
 __global__ void __launch_bounds__(PCG_T) k_pcg_init(ba_pcg_args a) {
     __shared__ double sh[PCG_T];
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
@@ -102,22 +119,23 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init(ba_pcg_args a) {
     if (u < a.n_u) {
         double b = a.rhs[u];
         double z = b / a.diagA[u];
-        a.x[u] = 0.0; a.xbest[u] = 0.0; a.r[u] = b; a.z[u] = z; a.p[u] = z;
+        a.x[u] = 0.0; a.xbest[u] = 0.0; a.r[u] = b; a.z[u] = z; a.p[a.n_u + u] = 0.0;
         bb = b * b; rz = b * z;
     }
-    double s0 = block_sum(bb, sh), s1 = block_sum(rz, sh);
+    double s0 = block_sum<PCG_T>(bb, sh), s1 = block_sum<PCG_T>(rz, sh);
     if (threadIdx.x == 0) { a.partials[3 * blockIdx.x + 0] = s0; a.partials[3 * blockIdx.x + 1] = s1; }
 }
 
 __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
     __shared__ double sh[PCG_T];
-    double bb = sum_partials(a.partials, nb, 0, sh);
-    double rz = sum_partials(a.partials, nb, 1, sh);
+    double bb = sum_partials<PCG_T>(a.partials, nb, 0, sh);
+    double rz = sum_partials<PCG_T>(a.partials, nb, 1, sh);
     if (threadIdx.x == 0) {
         double bn = sqrt(bb);
         a.state[ST_BNORM] = bn > 1e-12 ? bn : 1e-12;    // torch.norm(b).clamp(min=1e-12)
         a.state[ST_RZ0] = rz;
         a.state[ST_BEST0] = INFINITY; a.state[ST_BEST1] = INFINITY;
+        a.state[ST_BETA] = 0.0;
         a.istate[IS_DONE0] = a.maxiter <= 0; a.istate[IS_DONE1] = 0; a.istate[IS_K] = 0; a.istate[IS_CONV] = 0;
         a.istate[IS_BESTK] = 0;
         a.istate[IS_USEBEST] = 1;
@@ -127,74 +145,151 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
 // Image-row copies of the pair blocks, column-major: entry q of image row i (pair p, flag tr) holds
 // B = S(i, i2) with B[j][j2] at S_rows[q][j2 * d + j], so that the SpMV's lanes (one per output
 // row j) read each column of a block contiguously.  S(i, i2) is S_p for tr = 0 and S_p^T for tr = 1.
-__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent) {
+// row_u[q][j2] = umap[i2][j2] (-1 past d): the unknowns the block multiplies.  One thread per
+// (entry, element), max(d^2, 16) elements per entry.
+__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int per) {
     const int d = a.d, dd = d * d;
     const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    if (tid >= n_ent * dd) return;
-    const int64_t q = tid / dd;
-    const int e = (int)(tid - q * dd);
-    const int j2 = e / d, j = e - (e / d) * d;
+    if (tid >= n_ent * per) return;
+    const int64_t q = tid / per;
+    const int e = (int)(tid - q * per);
     const int ent = a.row_ent[q];
     const int64_t p = ent >> 1;
-    const double* S = a.S_pairs + p * dd;
-    a.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
+    if (e < dd) {
+        const int j2 = e / d, j = e - (e / d) * d;
+        const double* S = a.S_pairs + p * dd;
+        a.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
+    }
+    if (e < 16) {
+        const int i2 = (ent & 1) ? a.pair_i1[p] : a.pair_i2[p];
+        a.row_u[q * 16 + e] = e < d ? a.umap[(int64_t)i2 * d + e] : -1;
+    }
 }
 
 // ----------------------------------------------------------------------------- one CG iteration
-// Four launches per iteration; a launch whose iteration is past the stopping point returns at
-// once (the done flag of iteration k lives in IS_DONE0 + (k & 1), so the kernel that writes the
-// flag for k + 1 never races with blocks of the same launch reading the flag for k).
+// Iteration n (n = 0 .. maxiter - 1; the reference numbers it n + 1, ba_solver.py:1216-1236) is three
+// launches:
+//   k_pcg_spmv(n)    the stopping decisions after update n - 1 (every block forms them from the same
+//                    partial sums, so they agree without a grid barrier), the best-so-far copy, then
+//                    y_img = S_img p_n with p_n formed on the fly from z and p_{n-1};
+//   k_pcg_gather(n)  Ap = P^T y_img + damp p_n and the partials of p.Ap;
+//   k_pcg_update(n)  alpha, x, r, z, the stored p_n, and the partials of r.r and r.z.
+// p is double-buffered (p_n in slot n & 1).  A launch after the stopping point returns at once: the
+// flag "stopped before update n" lives in IS_DONE0 + (n & 1) and is written by k_pcg_spmv(n - 1).
 
-// y_img[i][j] = sum over the blocks of image row i of S(i, i2)[j, :] . p(i2): one workgroup per
-// image row; its 16 lane groups (one lane per output row j) take every 16th block of the row, and
-// the group sums are added in LDS in a fixed order.  The 16 unknown indices of a block, then the 16
-// values, are read as independent loads.
-__global__ void __launch_bounds__(PCG_T) k_spmv_img(ba_pcg_args a, int k) {
-    __shared__ double sh[PCG_T];
-    if (a.istate[IS_DONE0 + (k & 1)]) return;
+// y_img[i][j] = sum over the blocks of image row i of S(i, i2)[j, :] . p(i2): one workgroup of
+// PCG_ST threads per image row; its 32 lane groups (one lane per row j) take every 32nd block of
+// the row.  Lane j2 of a group forms p_n at the block's column unknown j2 and the group shares the
+// 16 values by shuffles; the group sums are added in LDS in a fixed order.  The operands of the
+// first pass are requested before the scalar decisions, which only need the partial sums.
+__global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int nb) {
+    __shared__ double sh[PCG_ST];
+    if (a.istate[IS_DONE0 + (n & 1)]) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.istate[IS_DONE0 + ((n + 1) & 1)] = 1;
+        return;
+    }
     const int i = blockIdx.x;
     const int grp = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int d = a.d, dd = d * d;
-    double acc = 0.0;
-    if (j < d) {
-        for (int q = a.row_ptr[i] + grp; q < a.row_ptr[i + 1]; q += PCG_T / 16) {
-            const int ent = a.row_ent[q];
-            const int pr = ent >> 1;
-            const int i2 = (ent & 1) ? a.pair_i1[pr] : a.pair_i2[pr];
-            const double* B = a.S_rows + (int64_t)q * dd;
-            const int* um = a.umap + (int64_t)i2 * d;
-            int u2[16];
+    const int q0 = a.row_ptr[i], q1 = a.row_ptr[i + 1];
+    const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
+    auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[16]) {
+        const bool live = q < q1;
+        u = live ? a.row_u[(int64_t)q * 16 + j] : -1;
+        zv = 0.0; pv = 0.0;
+        if (u >= 0) { zv = a.z[u]; pv = pold[u]; }
+        const double* B = a.S_rows + (int64_t)q * dd;
 #pragma unroll
-            for (int j2 = 0; j2 < 16; ++j2) u2[j2] = j2 < d ? um[j2] : -1;
-            double xv[16];
+        for (int j2 = 0; j2 < 16; ++j2) bcol[j2] = (live && j < d && j2 < d) ? B[j2 * d + j] : 0.0;
+    };
+    auto mac = [&](int u, double zv, double pv, double beta, const double (&bcol)[16], double acc) {
+        const double xj = u >= 0 ? pdir(zv, pv, beta) : 0.0;
 #pragma unroll
-            for (int j2 = 0; j2 < 16; ++j2) xv[j2] = u2[j2] >= 0 ? a.p[u2[j2]] : 0.0;
-#pragma unroll
-            for (int j2 = 0; j2 < 16; ++j2)
-                if (j2 < d) acc += B[j2 * d + j] * xv[j2];
+        for (int j2 = 0; j2 < 16; ++j2) acc += bcol[j2] * __shfl(xj, j2, 16);
+        return acc;
+    };
+    int u;
+    double zv, pv, bcol[16];
+    load(q0 + grp, u, zv, pv, bcol);
+
+    double beta = 0.0;
+    if (n >= 1) {
+        // end of update n - 1 (ba_solver.py:1222-1236)
+        const double rr = sum_partials<PCG_ST>(a.partials, nb, 0, sh);
+        const double rz_new = sum_partials<PCG_ST>(a.partials, nb, 1, sh);
+        const double rnorm = sqrt(rr);
+        const double best = a.state[ST_BEST0 + ((n - 1) & 1)];
+        const bool improved = rnorm < best;
+        const bool conv = rnorm <= a.tol * a.state[ST_BNORM];
+        const bool bad = !isfinite(rz_new);
+        const bool stop = conv || bad || n >= a.maxiter;
+        const double rz_old = a.state[ST_RZ0 + ((n - 1) & 1)];
+        beta = rz_new / (rz_old > 1e-32 ? rz_old : 1e-32);
+        if (improved)                                    // best_so_far = r_norm, x, k
+            for (int64_t v = (int64_t)blockIdx.x * PCG_ST + threadIdx.x; v < a.n_u; v += (int64_t)gridDim.x * PCG_ST)
+                a.xbest[v] = a.x[v];
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.state[ST_BEST0 + (n & 1)] = improved ? rnorm : best;
+            if (improved) a.istate[IS_BESTK] = n;
+            a.state[ST_RZ0 + (n & 1)] = rz_new;
+            a.state[ST_BETA] = beta;
+            a.istate[IS_K] = n;
+            if (conv) { a.istate[IS_CONV] = 1; a.istate[IS_USEBEST] = 0; }
+            a.istate[IS_DONE0 + ((n + 1) & 1)] = stop;
         }
+        if (stop) return;
+    } else if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.istate[IS_DONE0 + 1] = 0;
     }
+    double acc = mac(u, zv, pv, beta, bcol, 0.0);
+    for (int qb = q0 + PCG_ST / 16; qb < q1; qb += PCG_ST / 16) {     // rows longer than 32 blocks
+        load(qb + grp, u, zv, pv, bcol);
+        acc = mac(u, zv, pv, beta, bcol, acc);
+    }
+    __syncthreads();
     sh[threadIdx.x] = acc;
     __syncthreads();
     if (threadIdx.x < 16 && j < d) {
         double t = 0.0;
-        for (int g = 0; g < PCG_T / 16; ++g) t += sh[16 * g + j];
+        for (int g = 0; g < PCG_ST / 16; ++g) t += sh[16 * g + j];
         a.y_img[(int64_t)i * d + j] = t;
     }
 }
 
-// Ap[u] = sum of the image-level rows mapping to u + damp[u] p[u] (one wave per unknown);
-// per-block partial of p.Ap
-__global__ void __launch_bounds__(PCG_T) k_spmv_unk(ba_pcg_args a, int k) {
+// Ap[u] = sum of the image-level rows mapping to u + damp[u] p_n[u], and per-block partials of p.Ap.
+// Blocks [0, nb) take one unknown per thread (lists of at most BA_PCG_LONG_LIST entries); blocks
+// [nb, nb + nlb) take one of the long_u unknowns per wave (a focal pair shared by every image of a
+// camera has one entry per image), reading 8 entries per lane at a time as independent loads.
+__global__ void __launch_bounds__(PCG_T) k_pcg_gather(ba_pcg_args a, int n, int nb) {
     __shared__ double sh[PCG_T / 64];
-    if (a.istate[IS_DONE0 + (k & 1)]) return;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + w;
-    double s = 0.0;
-    if (u < a.n_u) {
-        // a shared unknown (one focal pair for every image of a camera) has a long list: its
-        // entries are read 8 per lane at a time as independent loads
-        const int q0 = a.inv_ptr[u], q1 = a.inv_ptr[u + 1];
+    if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
+    const double beta = a.state[ST_BETA];
+    const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
+    double pap = 0.0;
+    if ((int)blockIdx.x < nb) {
+        const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+        if (u < a.n_u) {
+            const int q0 = a.inv_ptr[u], q1 = a.inv_ptr[u + 1];
+            if (q1 - q0 <= BA_PCG_LONG_LIST) {
+                double s = 0.0;
+                for (int q = q0; q < q1; ++q) s += a.y_img[a.inv_src[q]];
+                const double pn = pdir(a.z[u], pold[u], beta);
+                s += a.damp[u] * pn;
+                a.Ap[u] = s;
+                pap = pn * s;
+            }
+        }
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int64_t k = (int64_t)(blockIdx.x - nb) * (PCG_T / 64) + (threadIdx.x >> 6);
+        int64_t u = -1;
+        int q0 = 0, q1 = 0;
+        if (k < a.n_long) {
+            u = a.long_u[k];
+            q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1];
+            if (q1 - q0 <= BA_PCG_LONG_LIST) { u = -1; q1 = q0; }   // not long: the thread pass owns it
+        }
+        double s = 0.0;
         for (int q = q0 + lane; q < q1; q += 64 * 8) {
             int src[8];
 #pragma unroll
@@ -202,74 +297,46 @@ __global__ void __launch_bounds__(PCG_T) k_spmv_unk(ba_pcg_args a, int k) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
         }
+        s = wave_sum(s);
+        if (lane == 0 && u >= 0) {
+            const double pn = pdir(a.z[u], pold[u], beta);
+            s += a.damp[u] * pn;
+            a.Ap[u] = s;
+            pap = pn * s;
+        }
     }
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off);
-    double pap = 0.0;
-    if (lane == 0 && u < a.n_u) {
-        s += a.damp[u] * a.p[u];
-        a.Ap[u] = s;
-        pap = a.p[u] * s;
-    }
-    if (lane == 0) sh[w] = pap;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (int q = 0; q < PCG_T / 64; ++q) t += sh[q];
-        a.partials[3 * blockIdx.x + 2] = t;
-    }
+    const double t = block_sum<PCG_T>(pap, sh);
+    if (threadIdx.x == 0) a.partials[3 * blockIdx.x + 2] = t;
 }
 
-// alpha = rz / max(p.Ap, 1e-32); x += alpha p; r -= alpha Ap; z = M^-1 r; partials r.r, r.z
-__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int nb, int nbw, int k) {
-    __shared__ double sh[PCG_T];
-    if (a.istate[IS_DONE0 + (k & 1)]) return;
-    double pap = sum_partials(a.partials, nbw, 2, sh);
-    double denom = pap > 1e-32 ? pap : 1e-32;
-    double alpha = a.state[ST_RZ0 + (k & 1)] / denom;
-    int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+// alpha = rz / max(p.Ap, 1e-32); x += alpha p; r -= alpha Ap; z = M^-1 r (ba_solver.py:1217-1228);
+// p_n stored in slot n & 1; partials r.r, r.z
+__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int ngb, int n) {
+    __shared__ double sh[PCG_T / 64];
+    if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
+    const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
+    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, apu = 0.0, du = 1.0;
+    if (u < a.n_u) {                                   // operands first, then the reduction
+        zu = a.z[u]; pu = a.p[(int64_t)((n + 1) & 1) * a.n_u + u]; xu = a.x[u]; ru = a.r[u]; apu = a.Ap[u];
+        du = a.diagA[u];
+    }
+    const double pap = sum_partials<PCG_T>(a.partials, ngb, 2, sh);
+    const double denom = pap > 1e-32 ? pap : 1e-32;
+    const double alpha = a.state[ST_RZ0 + (n & 1)] / denom;
+    const double beta = a.state[ST_BETA];
     double rr = 0.0, rz = 0.0;
     if (u < a.n_u) {
-        double x = a.x[u] + alpha * a.p[u];
-        double r = a.r[u] - alpha * a.Ap[u];
-        double z = r / a.diagA[u];
+        const double pn = pdir(zu, pu, beta);
+        a.p[(int64_t)(n & 1) * a.n_u + u] = pn;
+        const double x = xu + alpha * pn;
+        const double r = ru - alpha * apu;
+        const double z = r / du;
         a.x[u] = x; a.r[u] = r; a.z[u] = z;
         rr = r * r; rz = r * z;
     }
-    __syncthreads();
-    double s0 = block_sum(rr, sh), s1 = block_sum(rz, sh);
+    const double s0 = block_sum<PCG_T>(rr, sh);
+    const double s1 = block_sum<PCG_T>(rz, sh);
     if (threadIdx.x == 0) { a.partials[3 * blockIdx.x + 0] = s0; a.partials[3 * blockIdx.x + 1] = s1; }
-}
-
-// best-so-far bookkeeping, stopping test, beta and the new search direction
-// (ba_solver.py:1222-1236); k counts from 0, the reference numbers the same iteration k + 1.
-__global__ void __launch_bounds__(PCG_T) k_pcg_dir(ba_pcg_args a, int nb, int k) {
-    __shared__ double sh[PCG_T];
-    if (a.istate[IS_DONE0 + (k & 1)]) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) a.istate[IS_DONE0 + ((k + 1) & 1)] = 1;
-        return;
-    }
-    double rr = sum_partials(a.partials, nb, 0, sh);
-    double rz_new = sum_partials(a.partials, nb, 1, sh);
-    double rnorm = sqrt(rr);
-    double best = a.state[ST_BEST0 + (k & 1)];
-    bool improved = rnorm < best;
-    int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    if (improved && u < a.n_u) a.xbest[u] = a.x[u];
-    bool conv = rnorm <= a.tol * a.state[ST_BNORM];
-    bool bad = !isfinite(rz_new);
-    double rz_old = a.state[ST_RZ0 + (k & 1)];
-    double beta = rz_new / (rz_old > 1e-32 ? rz_old : 1e-32);
-    if (!conv && !bad && u < a.n_u) a.p[u] = a.z[u] + beta * a.p[u];
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        a.state[ST_BEST0 + ((k + 1) & 1)] = improved ? rnorm : best;
-        if (improved) a.istate[IS_BESTK] = k + 1;
-        a.state[ST_RZ0 + ((k + 1) & 1)] = rz_new;
-        a.istate[IS_K] = k + 1;
-        int done = 0;
-        if (conv) { done = 1; a.istate[IS_CONV] = 1; a.istate[IS_USEBEST] = 0; }
-        else if (bad || k + 1 >= a.maxiter) { done = 1; }
-        a.istate[IS_DONE0 + ((k + 1) & 1)] = done;
-    }
 }
 
 // result: x if converged else the best iterate
@@ -284,8 +351,12 @@ using namespace ba;
 
 static inline unsigned nb_of(int64_t n) { return (unsigned)((n + PCG_T - 1) / PCG_T); }
 
-// partial sums: 3 per block of the widest launch (one wave per unknown)
-extern "C" int64_t ba_pcg_partials_size(int64_t n_u) { return 3 * (((n_u < 1 ? 1 : n_u) + 3) / 4) + 3; }
+// partial sums: 3 per block of the widest launch (the gather: one thread per unknown plus one
+// wave per long unknown)
+extern "C" int64_t ba_pcg_partials_size(int64_t n_u) {
+    const int64_t m = n_u < 1 ? 1 : n_u;
+    return 3 * ((m + PCG_T - 1) / PCG_T + (m + 3) / 4 + 1) + 3;
+}
 
 extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     clear_error();
@@ -293,25 +364,29 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     const ba_pcg_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
     BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16 && a.maxiter >= 0, "bad sizes");
+    BA_REQUIRE(a.n_long >= 0 && a.n_long <= a.n_u && (a.n_long == 0 || a.long_u != nullptr), "bad long-list unknowns");
     if (a.n_u == 0) return BA_OK;
     const unsigned nb = nb_of(a.n_u);
-    const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown
+    const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown (setup)
+    const unsigned ngb = nb + (unsigned)((a.n_long + PCG_T / 64 - 1) / (PCG_T / 64));  // gather blocks
     const int64_t n_ent = a.n_row_ent;
-    BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr, "image-row block workspace missing");
+    BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
+    const int per = a.d * a.d > 16 ? a.d * a.d : 16;
     if (n_ent > 0)
-        hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * a.d * a.d + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
-                           n_ent);
+        hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
+                           n_ent, per);
     hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_leaf_damp, dim3(1), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
     BA_LAUNCHED();
     for (int it = 0; it < a.maxiter; ++it) {
-        hipLaunchKernelGGL(k_spmv_img, dim3((unsigned)a.n_imgs), dim3(PCG_T), 0, st, a, it);
-        hipLaunchKernelGGL(k_spmv_unk, dim3(nbw), dim3(PCG_T), 0, st, a, it);
-        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, (int)nbw, it);
-        hipLaunchKernelGGL(k_pcg_dir, dim3(nb), dim3(PCG_T), 0, st, a, (int)nb, it);
+        hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+        hipLaunchKernelGGL(k_pcg_gather, dim3(ngb), dim3(PCG_T), 0, st, a, it, (int)nb);
+        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)ngb, it);
     }
+    // the decisions after the last update (no SpMV follows them)
+    hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, a.maxiter, (int)nb);
     hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);
     BA_LAUNCHED();
     return BA_OK;

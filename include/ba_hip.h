@@ -152,7 +152,7 @@ typedef struct {
     const double *S_pairs, *e_img, *dg_img;
     double dampen; int32_t adaptive;
     int32_t maxiter; double tol;
-    /* workspace (fp64 unless noted) */
+    /* workspace (fp64 unless noted); p holds 2 * n_u (the search direction, double-buffered) */
     double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *Ap, *y_img;
     double *partials;                  /* 3 * n_blocks */
     double *state;                     /* 16 doubles */
@@ -160,11 +160,17 @@ typedef struct {
                                           [4] best iteration, [5] best iterate returned */
     double *S_rows;                    /* (n_row_ent, d, d): the pair blocks copied per image row */
     int64_t n_row_ent;                 /* row_ptr[n_imgs] */
+    int32_t *row_u;                    /* (n_row_ent, 16) workspace: the unknowns each image-row block multiplies */
+    const int32_t *long_u;             /* the unknowns whose inv list has more than BA_PCG_LONG_LIST entries,
+                                          every one of them (e.g. a focal pair shared by many images) */
+    int64_t n_long;
 } ba_pcg_args;
+
+#define BA_PCG_LONG_LIST 32
 
 /* Builds the unknown-level rhs, diag(A) with per-leaf damping (ba_solver.py:575-582,
  * :1188-1191) and runs Jacobi-PCG (ba_solver.py:184-206, :1197-1238) on
- * S = P^T S_img P + damping, entirely on the device (four launches per iteration, no host
+ * S = P^T S_img P + damping, entirely on the device (three launches per iteration, no host
  * synchronisation).  The result (the converged iterate, else the best one) is left in x;
  * istate holds the loop's outcome. */
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);
