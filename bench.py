@@ -139,7 +139,7 @@ def main():
         lm_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
         log(f'[bench] lm_step {lm_ms:.2f} ms')
 
-    smp = bench_sampling(prob, g, dev, args.steps, args.warmup) if args.sampling else None
+    smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
 
     cpu = None
     if args.cpu_baseline:
@@ -167,27 +167,30 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_sampling(prob, g, dev, steps, warmup):
+def bench_sampling(prob, g, dev, steps, warmup, cfg):
     """F sampling (ba_sample_depth) at the configuration's size: one (384, 512, C) fp32 map per
     frame (C = K + 1 channels with the ones channel stacked, as the reference's maps are) and the
     configuration's observations.  Algorithmic bytes per observation: pixel 8 + four texels 16 C
     read + row 4 C written.  Beside it, the reference's own call sequence on the same GPU (one
     torch grid_sample per frame, geometry.py:183-196)."""
     import torch.nn.functional as F
-    from blast3r_amd.sampling import sample_depth_maps
+    import ctypes
+    from blast3r_amd._lib import check, lib, stream_ptr
+    from blast3r_amd.sampling import prepare_sample
     H, W, C = 384, 512, prob.C
     gen = torch.Generator(device=dev).manual_seed(5)
     maps = torch.rand((prob.n_imgs, H, W, C), device=dev, generator=gen)
     cum = g.infos[0].contiguous()
     pix = g.pix2d.contiguous()
-    out = torch.empty((prob.n_obs, C), device=dev)
+    a, out, keep = prepare_sample(maps, cum, pix)
+    L, st = lib(), stream_ptr(dev)
     for _ in range(warmup):
-        sample_depth_maps(maps, cum, pix, out=out)
+        check(L.ba_sample_depth(ctypes.byref(a), st))
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
-        sample_depth_maps(maps, cum, pix, out=out)
+        check(L.ba_sample_depth(ctypes.byref(a), st))
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
@@ -213,21 +216,22 @@ def bench_sampling(prob, g, dev, steps, warmup):
     ref_ms = (time.perf_counter() - t0) * 1e3 / 3
     bytes_alg = prob.n_obs * (8 + 16 * C + 4 * C)
     gbs = bytes_alg / (ms * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(cfg, 'k_sample')
     log(f'[bench] F sampling {ms:.3f} ms ({prob.n_obs / (ms * 1e-3):.4g} obs/s, {gbs:.0f} GB/s algorithmic); '
         f'torch grid_sample per frame {ref_ms:.2f} ms')
     del maps
     return {'kernel': 'k_sample', 'ms': ms, 'obs_per_s': prob.n_obs / (ms * 1e-3),
             'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
-                         'bytes_per_launch': bytes_alg},
+                         'bytes_per_launch': bytes_alg, 'traffic': traffic, 'traffic_source': traffic_src},
             'maps': f'{prob.n_imgs} x {H} x {W} x {C} fp32 (uniform random values)',
             'torch_grid_sample_per_frame_ms': ref_ms}
 
 
-def measured_traffic(cfg):
-    """HBM bytes per k_schur launch from the committed rocprofv3 PMC summary of this workload
+def measured_traffic(cfg, kernel='k_schur'):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary of this workload
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a plain copy of known size),
     or None when no summary for this configuration is present."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', f'k_schur_cfg{cfg}_pmc.json')
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', f'{kernel}_cfg{cfg}_pmc.json')
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
@@ -235,33 +239,37 @@ def measured_traffic(cfg):
     return rec['hbm_bytes_per_launch'], os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
 
 
-def cpu_baseline(cfg):
-    """Oracle (torch-CPU restatement of the reference's linearisation + normal equations +
-    Schur rhs) on a bounded sample of the same configuration, timed on this host."""
+def cpu_baseline(cfg, reps=3):
+    """Oracle (torch-CPU restatement of the reference's linearisation + normal equations + Schur
+    rhs) on the full configuration, timed on this host over `reps` passes (about 10-30 s of CPU
+    work at configuration 2)."""
     import oracle.kernels as ok
     import oracle.solver as osol
     import oracle.engine as oeng
     from blast3r_amd.synthetic import make_problem
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    # about a quarter of the frames and tracks of the configuration (10-30 s of CPU work)
-    frames = {0: 32, 1: 128, 2: 256, 3: 512, 4: 256}[cfg]
-    tracks = {0: 20_000, 1: 100_000, 2: 250_000, 3: 200_000, 4: 250_000}[cfg]
-    p = make_problem(cfg, n_frames=frames, n_tracks=tracks)
+    p = make_problem(cfg)
     o = p.options
-    t0 = time.perf_counter()
-    loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
-                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], o['pnorm'], o['clip_pix_err'],
-                                  o['huber_delta'])
-    Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
-                                        p.pix2d_std, p.pix2d_dep, True, float64=True)
-    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
-    ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_K=o['optim_K'], optim_P=o['optim_P'])
-    rhs = osol.reduced_rhs(ne, g)
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                      p.pix2d_std, p.pix2d_dep, True, o['weight_z'], o['pnorm'], o['clip_pix_err'],
+                                      o['huber_delta'])
+        Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                            p.pix2d_std, p.pix2d_dep, True, float64=True)
+        prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+        ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_K=o['optim_K'],
+                                                    optim_P=o['optim_P'])
+        osol.reduced_rhs(ne, g)
+        times.append(time.perf_counter() - t0)
+        del Jc, Jz, Jp, ne, g, params
+    dt = sum(times) / len(times)
     return {'value': p.n_obs / dt, 'unit': 'obs/s', 'cores': threads, 'kind': 'port',
-            'sample': f'cfg{cfg} scaled to {frames} frames / {tracks} tracks ({p.n_obs} obs): residuals, fp64 '
-                      f'Jacobians, normal equations and Schur rhs in the oracle, {dt:.2f} s'}
+            'sample': f'the full cfg{cfg} workload ({p.n_imgs} frames, '
+                      f'{p.n_tracks} tracks, {p.n_obs} obs), {reps} passes of residuals, fp64 Jacobians, normal '
+                      f'equations and Schur rhs in the oracle: {sum(times):.1f} s in total, {dt:.2f} s per pass'}
 
 
 if __name__ == '__main__':

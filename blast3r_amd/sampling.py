@@ -15,7 +15,7 @@ import torch
 from ._lib import BaSampleArgs, check, lib, stream_ptr
 from .data import ObservedTracks
 
-__all__ = ['sample_depth_maps', 'bilinear_sampling', 'gather_data_from_dense_tracks', 'DEPTH_MODES']
+__all__ = ['prepare_sample', 'sample_depth_maps', 'bilinear_sampling', 'gather_data_from_dense_tracks', 'DEPTH_MODES']
 
 DEPTH_MODES = ('log_multidepth', 'linear_multidepth')
 
@@ -35,57 +35,72 @@ def _map_geometry(m, C):
     return H, W, ps
 
 
-def sample_depth_maps(maps, cum_nppi, pix2d, insert_ones=False, out=None):
-    """Bilinear samples of per-image maps at image-major observations.
-
-    maps       list of (H_i, W_i, Cm) fp32 device tensors, one per image (or one (n_imgs, H, W, Cm)
-               tensor); channel slices of wider maps (``raw[..., 2:]``) are read in place
-    cum_nppi   (n_imgs,) int32 inclusive cumulative observation counts (``infos`` row 0)
-    pix2d      (n_obs, 2) fp32 pixel coordinates
-    insert_ones  also sample a constant-one channel at output column 1 (the stack of
-               src/blast3r/inference/multidepth.py:53-54)
-    returns    (n_obs, Cm + insert_ones) fp32
-    """
-    if isinstance(maps, torch.Tensor):
-        maps = list(maps.unbind(0)) if maps.dim() == 4 else [maps]
-    if len(maps) == 0:
-        raise ValueError('no maps')
+def prepare_sample(maps, cum_nppi, pix2d, insert_ones=False, out=None):
+    """Argument block of ba_sample_depth for sample_depth_maps (same arguments); returns
+    (args, out, keep) where keep holds the device tensors args points into."""
+    stacked = isinstance(maps, torch.Tensor) and maps.dim() == 4
+    if isinstance(maps, torch.Tensor) and not stacked:
+        maps = [maps]
     dev = pix2d.device
     if dev.type != 'cuda':
         raise RuntimeError('sample_depth_maps needs device tensors (the sampling runs in libba_hip.so)')
-    C = maps[0].shape[-1]
-    geo = []
-    for m in maps:
+    views = list(maps.unbind(0)) if stacked else list(maps)
+    if len(views) == 0:
+        raise ValueError('no maps')
+    C = views[0].shape[-1]
+    for m in views:
         if m.dtype != torch.float32 or m.device != dev:
             raise ValueError('maps must be fp32 tensors on the device of pix2d')
-        geo.append(_map_geometry(m, C))
+    if stacked:
+        geo = [_map_geometry(views[0], C)]
+        if len(views) > 1 and maps.stride(0) <= 0:
+            raise ValueError('stacked maps need a positive image stride')
+    else:
+        geo = [_map_geometry(m, C) for m in views]
     pix2d = pix2d.contiguous()
     if pix2d.dtype != torch.float32 or pix2d.dim() != 2 or pix2d.shape[1] != 2:
         raise ValueError('pix2d must be (n_obs, 2) fp32')
     cum_nppi = cum_nppi.to(device=dev, dtype=torch.int32).contiguous()
-    if len(cum_nppi) != len(maps):
-        raise ValueError(f'{len(maps)} maps for {len(cum_nppi)} images')
+    if len(cum_nppi) != len(views):
+        raise ValueError(f'{len(views)} maps for {len(cum_nppi)} images')
     n_obs = pix2d.shape[0]
     co = C + int(bool(insert_ones))
     if out is None:
         out = torch.empty((n_obs, co), dtype=torch.float32, device=dev)
     elif out.shape != (n_obs, co) or not out.is_contiguous() or out.dtype != torch.float32:
         raise ValueError(f'out must be a contiguous ({n_obs}, {co}) fp32 tensor')
-    if n_obs == 0:
-        return out
     pss = {g[2] for g in geo}
     if len(pss) != 1:
         raise ValueError('maps must share one pixel stride')
     hw = {(g[0], g[1]) for g in geo}
-    addr = torch.tensor([m.data_ptr() for m in maps], dtype=torch.int64).to(dev, non_blocking=False)
+    if stacked:                                   # image i at base + i * stride, formed on the device
+        addr = maps.data_ptr() + torch.arange(len(views), dtype=torch.int64, device=dev) * (maps.stride(0) * 4)
+    else:
+        addr = torch.tensor([m.data_ptr() for m in views], dtype=torch.int64).to(dev)
     map_hw = None
     if len(hw) > 1:
         map_hw = torch.tensor([[g[0], g[1]] for g in geo], dtype=torch.int32).to(dev)
     H, W = next(iter(hw)) if len(hw) == 1 else (0, 0)
     a = BaSampleArgs(map_addr=addr.data_ptr(), map_hw=None if map_hw is None else map_hw.data_ptr(), H=H, W=W, Cm=C,
                      pix_stride=pss.pop(), insert_ones=int(bool(insert_ones)), cum_nppi=cum_nppi.data_ptr(),
-                     n_imgs=len(maps), pix2d=pix2d.data_ptr(), n_obs=n_obs, out=out.data_ptr())
-    check(lib().ba_sample_depth(ctypes.byref(a), stream_ptr(dev)))
+                     n_imgs=len(views), pix2d=pix2d.data_ptr(), n_obs=n_obs, out=out.data_ptr())
+    return a, out, (addr, map_hw, cum_nppi, pix2d, maps)
+
+
+def sample_depth_maps(maps, cum_nppi, pix2d, insert_ones=False, out=None):
+    """Bilinear samples of per-image maps at image-major observations.
+
+    maps       list of (H_i, W_i, Cm) fp32 device tensors, one per image, or one (n_imgs, H, W, Cm)
+               tensor; channel slices of wider maps (``raw[..., 2:]``) are read in place
+    cum_nppi   (n_imgs,) int32 inclusive cumulative observation counts (``infos`` row 0)
+    pix2d      (n_obs, 2) fp32 pixel coordinates
+    insert_ones  also sample a constant-one channel at output column 1 (the stack of
+               src/blast3r/inference/multidepth.py:53-54)
+    returns    (n_obs, Cm + insert_ones) fp32
+    """
+    a, out, keep = prepare_sample(maps, cum_nppi, pix2d, insert_ones, out)
+    if a.n_obs > 0:
+        check(lib().ba_sample_depth(ctypes.byref(a), stream_ptr(pix2d.device)))
     return out
 
 
@@ -114,7 +129,7 @@ def bilinear_sampling(depth, pix2d, mode='bilinear', padding_mode='border'):
     maps = depth.reshape(B, *depth.shape[nb:])
     pts = pix2d.reshape(B * P, 2)
     cum = torch.arange(1, B + 1, dtype=torch.int32, device=dev) * P
-    res = sample_depth_maps(list(maps.unbind(0)), cum, pts).view(*batch_dims, *pix_shape, depth.shape[-1])
+    res = sample_depth_maps(maps, cum, pts).view(*batch_dims, *pix_shape, depth.shape[-1])
     return res.cpu().numpy() if to_numpy else res
 
 

@@ -6,7 +6,7 @@ as vectorised torch-CPU code.  Precision follows the reference: the residual
 kernel is fp32 end to end (``.cu:129-259``), the Jacobian kernel computes in the
 output dtype (fp64 on the solver path, ``.cu:323-509``) from fp32 inputs.
 
-Pinning (see tests/test_oracle_kernels.py):
+Pinning (see tests/test_oracle.py):
   * residuals: fp64 closed form of the projection, identity-pose on-axis point,
     z <= 1e-3 rows, textbook Huber/IRLS for pnorm=1, clip -> w_null.
   * jacobians: torch.autograd of an independent fp64 residual under the left

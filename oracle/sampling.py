@@ -14,7 +14,7 @@ Restates, in numpy fp32:
     ascending within an image, and the per-view samples concatenated;
   * the channel stack [F0, 1, F1, ...] of src/blast3r/inference/multidepth.py:53-54.
 
-Pinning (tests/test_oracle.py): bit-for-bit equality with torch CPU ``F.grid_sample`` called the
+Pinning (tests/test_sampling.py): bit-for-bit equality with torch CPU ``F.grid_sample`` called the
 way geometry.py calls it, on random and smooth maps with points inside, on and beyond the border;
 fma32 against exact rational arithmetic on cases built to round on a tie; pixel centres of
 power-of-two maps return the texel exactly; an affine map is reproduced exactly in the interior

@@ -17,7 +17,7 @@ structure, without the reference's sparse-matrix class hierarchy:
     (bs:184-206, bs:1197-1238), or a dense direct solve of the same S;
   * back-substitution delta_p = D^-1 (g_p - C delta_c) and fp32 output (bs:182, bs:203).
 
-Pinning (tests/test_oracle_solver.py): every block against a materialised dense
+Pinning (tests/test_oracle.py): every block against a materialised dense
 J (``oracle.dense``): dense J^T W J and J^T W r, the Schur identity (full dense
 solve == reduced solve + back-substitution), symmetry and PSD of S, the 7-DoF
 similarity gauge in ker S, and converged PCG == direct solve.
