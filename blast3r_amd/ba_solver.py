@@ -238,7 +238,8 @@ class GaussNewtonSolver:
         a.infos = ptr(J.rigs.contiguous())
         a.n_imgs = n_imgs
         for name in ('chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr',
-                     'b_imgs', 'b_nimgs', 'b_slot_ptr', 'slot_pair', 'pair_ptr', 'pair_src', 'img_ptr', 'img_src'):
+                     'b_imgs', 'b_nimgs', 'b_slot_ptr', 'slot_pair', 'pair_ptr', 'pair_src', 'img_ptr', 'img_src',
+                     'chunk_slots', 'chunk_ent', 'chunk_eptr', 'b_pos_slot'):
             setattr(a, name, ptr(pd[name]))
         a.L = plan.L
         a.s_pix, a.s_std, a.s_dep = ptr(s_pix), ptr(s_std), ptr(s_dep)

@@ -114,6 +114,12 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     auto& b_slot_ptr = P->v[BA_PA_B_SLOT_PTR];    // n_batches + 1
     auto& slot_pair = P->v[BA_PA_SLOT_PAIR];      // per slot: a | b << 8  (a <= b local)
     auto& slot_gpair = P->v[BA_PA_SLOT_GPAIR];    // per slot: global pair id
+    auto& chunk_slots = P->v[BA_PA_CHUNK_SLOTS];  // n_chunks * BA_MAX_SLOTS
+    auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 16-bit entries, two per word
+    auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks
+    auto& b_pos_slot = P->v[BA_PA_B_POS_SLOT];    // n_batches * BA_MAX_SLOTS
+    std::vector<uint16_t> ents;                   // all chunks' entries (packed into chunk_ent at the end)
+    bool list_overflow = false;
 
     std::vector<int32_t> cur_imgs;
     std::vector<uint8_t> cur_pairs((size_t)max_local_imgs * max_local_imgs, 0);
@@ -131,7 +137,6 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             for (int a = 0; a <= b; ++a)
                 if (cur_pairs[a * max_local_imgs + b]) slot_pair.push_back(a | (b << 8));
         b_slot_ptr.push_back((int32_t)slot_pair.size());
-        (void)slot0;
         // chunks: pack tracks in order
         int ch_first_track = 0;
         size_t k = 0;
@@ -170,8 +175,98 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             chunk_meta.push_back(ntr);
             chunk_meta.push_back(used);
             (void)chunk; (void)ch_first_track;
+
+            // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
+            // first observation of each covering track in a with the one in b (chunk-track order);
+            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order), then
+            // the V rows of the first observation of each (track, image) run in a (slot order)
+            {
+                std::vector<int16_t> lead((size_t)ntr * BA_MAX_LOCAL, -1);
+                for (int sidx = 0; sidx < used; ++sidx) {
+                    const int inf = slot_info[base + sidx];
+                    lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
+                }
+                const size_t e0 = ents.size();
+                chunk_eptr.push_back((int32_t)(e0 / 8));
+                const int nsl = (int)slot_pair.size() - slot0;
+                for (int q = 0; q < BA_MAX_SLOTS; ++q) {
+                    if (q >= nsl) { chunk_slots.push_back(0); continue; }
+                    const int a = slot_pair[slot0 + q] & 0xff, bq = (slot_pair[slot0 + q] >> 8) & 0xff;
+                    const size_t off = ents.size() - e0;
+                    auto ent = [&](int sa, int sb, int kind) {
+                        ents.push_back((uint16_t)(sa | (sb << 7) | (kind << 14)));
+                    };
+                    if (a != bq) {
+                        for (int tt = 0; tt < ntr; ++tt) {
+                            const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
+                            if (la_ >= 0 && lb_ >= 0) ent(la_, lb_, BA_ENT_V);
+                        }
+                    } else {
+                        for (int sidx = 0; sidx < used; ++sidx)
+                            if ((slot_info[base + sidx] & 0xff) == a) ent(sidx, sidx, BA_ENT_J);
+                        for (int sidx = 0; sidx < used; ++sidx) {
+                            const int inf = slot_info[base + sidx];
+                            if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx, sidx, BA_ENT_V);
+                        }
+                    }
+                    while ((ents.size() - e0 - off) % 4) ent(0, 0, BA_ENT_PAD);
+                    const size_t len = ents.size() - e0 - off;
+                    chunk_slots.push_back((int32_t)(off | (len << 16)));
+                }
+                if (ents.size() - e0 > BA_LIST_CAP) list_overflow = true;
+                while ((ents.size() - e0) % 8) ents.push_back(0);
+            }
         }
         b_chunk_ptr.push_back((int32_t)(chunk_meta.size() / 4));
+        // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
+        // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
+        // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
+        // decreasing total work and each goes where the summed per-chunk maxima grow least.
+        {
+            const int nsl = (int)slot_pair.size() - slot0;
+            const int c0 = b_chunk_ptr[b_chunk_ptr.size() - 2], nc = b_chunk_ptr.back() - c0;
+            std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
+            std::vector<int64_t> tot(nsl, 0);
+            for (int c = 0; c < nc; ++c)
+                for (int q = 0; q < nsl; ++q) {
+                    const int len = chunk_slots[(size_t)(c0 + c) * BA_MAX_SLOTS + q] >> 16;
+                    wk[(size_t)c * nsl + q] = 3 * (len / 4);
+                    tot[q] += wk[(size_t)c * nsl + q];
+                }
+            std::vector<int> order(nsl);
+            std::iota(order.begin(), order.end(), 0);
+            std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return tot[x] > tot[y]; });
+            constexpr int NS = 4, WPS = BA_WAVES / NS;
+            std::vector<int64_t> ls((size_t)nc * NS, 0), lw((size_t)nc * BA_WAVES, 0), ms(nc, 0), mw(nc, 0);
+            int cnt[BA_WAVES] = {0};
+            const size_t pbase = b_pos_slot.size();
+            b_pos_slot.resize(pbase + BA_MAX_SLOTS, -1);
+            for (int q : order) {
+                int best = -1;
+                int64_t best_cost = 0;
+                for (int w = 0; w < BA_WAVES; ++w) {
+                    if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
+                    const int sd = w % NS;
+                    int64_t cost = 0;
+                    for (int c = 0; c < nc; ++c) {
+                        const int64_t x = wk[(size_t)c * nsl + q];
+                        cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
+                    }
+                    if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
+                }
+                b_pos_slot[pbase + best + BA_WAVES * cnt[best]] = q;
+                cnt[best]++;
+                const int sd = best % NS;
+                for (int c = 0; c < nc; ++c) {
+                    const int64_t x = wk[(size_t)c * nsl + q];
+                    ls[(size_t)c * NS + sd] += x;
+                    lw[(size_t)c * BA_WAVES + best] += x;
+                    ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
+                    mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
+                }
+            }
+            (void)WPS;
+        }
         for (int a = 0; a < max_local_imgs; ++a)
             b_imgs.push_back(a < (int)cur_imgs.size() ? cur_imgs[a] : -1);
         b_nimgs.push_back((int32_t)cur_imgs.size());
@@ -236,6 +331,17 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
 
     // ------------------------------------------------------------ global pairs
     int n_batches = (int)b_nimgs.size();
+    if (list_overflow) {
+        g_plan_err = "a chunk needs more than BA_LIST_CAP MFMA entries";
+        delete P;
+        return nullptr;
+    }
+    // two entries per word, and one chunk's worth of padding so that a full-capacity copy of the
+    // last chunk's list stays inside the array
+    ents.resize(ents.size() + BA_LIST_CAP, 0);
+    if (ents.size() % 2) ents.push_back(0);
+    chunk_ent.resize(ents.size() / 2);
+    std::memcpy(chunk_ent.data(), ents.data(), ents.size() * sizeof(uint16_t));
     int64_t n_slots = (int64_t)slot_pair.size();
     std::vector<int64_t> keys(n_slots);
     std::vector<uint8_t> swapped(n_slots, 0);

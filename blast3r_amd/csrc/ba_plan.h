@@ -4,10 +4,10 @@
 #define BA_CHUNK 128          // observation slots per chunk (one slot per lane in the per-observation phases)
 #define BA_MAX_LOCAL 16       // images a batch may touch (bit mask in 32 bits, local ids in 8 bits)
 #ifndef BA_WAVES
-#define BA_WAVES 8            // waves per workgroup of the fused Schur kernel (two per SIMD)
+#define BA_WAVES 16           // waves per workgroup of the fused Schur kernel (four per SIMD)
 #endif
 #ifndef BA_SLOTS_PER_WAVE
-#define BA_SLOTS_PER_WAVE 12  // camera-pair accumulators held in registers by one wave
+#define BA_SLOTS_PER_WAVE 6   // camera-pair accumulators held in registers by one wave
 #endif
 #define BA_MAX_SLOTS (BA_WAVES * BA_SLOTS_PER_WAVE)
 #define BA_MAX_CT 64          // tracks per chunk (coverage bit masks in 64 bits)
@@ -35,8 +35,20 @@ enum {
     BA_PA_ROW_ENT,
     BA_PA_IMG_PTR,
     BA_PA_IMG_SRC,
+    BA_PA_CHUNK_SLOTS,      // per chunk, BA_MAX_SLOTS words: entry offset | padded entry count << 16
+    BA_PA_CHUNK_ENT,        // MFMA entries of every chunk, 16 bits each (two per word), see below
+    BA_PA_CHUNK_EPTR,       // per chunk: first entry, in units of 8 entries (16 bytes)
+    BA_PA_B_POS_SLOT,       // per batch, BA_MAX_SLOTS words: the batch slot at Schur-kernel place
+                            // wave + BA_WAVES * k, or -1 (places balanced by work)
     BA_PLAN_NARRAYS
 };
+
+// MFMA entry of a camera-pair slot: A slot (7 bits) | B slot (7 bits) << 7 | kind << 14, where the
+// slots index the chunk's observation blocks and kind is BA_ENT_V (the V rows of A and B),
+// BA_ENT_J (the J rows of A = B, A negated) or BA_ENT_PAD (the zero block).  Each slot's list is
+// padded to a multiple of 4 entries; a chunk holds at most BA_LIST_CAP entries.
+enum { BA_ENT_V = 0, BA_ENT_J = 1, BA_ENT_PAD = 2 };
+#define BA_LIST_CAP 1536
 
 // plan scalars (int64)
 enum {

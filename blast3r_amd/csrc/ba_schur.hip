@@ -28,8 +28,17 @@ typedef ba_lin_args LinArgs;
 
 // ----------------------------------------------------------------------------- per observation
 #define BA_PRE_C 8          // depth-guidance channels held in registers (further channels are read from memory)
-#define BA_BLK 129          // doubles per observation block in LDS: 8 rows x 16 columns + 1 pad (spreads banks)
+#define BA_BLK 97           // doubles per observation block in LDS: 6 rows x 16 columns + 1 pad (spreads banks)
+#define BA_JROW 48          // first J row of a block (rows 0-2 hold V, rows 3-5 the weighted camera rows J_c)
+#define BA_ZERO (BA_CHUNK * BA_BLK)   // a zero block (3 rows) after the chunk's blocks, for padding entries
+// The MFMA entry lists come from the plan (16-bit entries, see ba_plan.h): one entry per (track,
+// image pair) of an off-diagonal slot, per observation and per (track, image) run of a diagonal
+// slot.  A chunk holds at most 128 observations of tracks spanning at most 16 images, so it has at
+// most 128 * 17 / 2 pair-and-run entries plus 128 observation entries, plus 3 of padding per slot.
+static_assert(BA_CHUNK * (BA_MAX_LOCAL + 1) / 2 + BA_CHUNK + 3 * BA_MAX_SLOTS <= BA_LIST_CAP, "entry list capacity");
+static_assert(BA_LIST_CAP * 2 % 1024 == 0 && BA_MAX_SLOTS % 4 == 0, "list copies are whole 16-byte lanes");
 #define BA_CORE 20          // doubles per observation in the linearisation record
+static_assert(BA_CORE * BA_CHUNK % 256 == 0, "a chunk's record block is copied 256 doubles at a time");
 
 // Depth-guidance channels of one observation: the first BA_PRE_C in registers, the rest in memory.
 // Every access uses a compile-time channel index, so the register part never spills.
@@ -139,31 +148,44 @@ __device__ __forceinline__ void core_load(const double* __restrict__ rec, int t,
     o.sW[0] = a.y; o.sW[1] = b.x; o.sW[2] = b.y;
 }
 
-// Weighted camera rows, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60).
-template <int HK, int HP, class JcSink>
-__device__ __forceinline__ void emit_jc(const ObsCore& o, const LinLayout& lay, bool enK, bool enP, bool enZ,
-                                        bool first_obs, const DepSrc& dep, JcSink&& sink) {
+// Weighted camera row R, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60).
+template <int HK, int HP, int R, class RowSink>
+__device__ __forceinline__ void emit_jc_row(const ObsCore& o, const LinLayout& lay, bool enK, bool enP, bool enZ,
+                                            bool first_obs, const DepSrc& dep, RowSink&& sink) {
     constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
     const int C = lay.C;
     const double mK = enK ? 1.0 : 0.0, mP = enP ? 1.0 : 0.0;
     const bool zon = lay.hasZ && enZ;                 // an invalid observation has zscale = 0
     const bool z0off = !lay.optim_Z0 || (first_obs && !lay.optim_Z_1st_cam);
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            double u = 0.0;
-            if (j < OT) {
-                u = (r == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(o.J, r, j) * mK;
-            } else if (j < OZ) {
-                u = jac_tau(o.J, r, j - OT) * mP;
-            } else if (r == 2) {
-                const int c = j - OZ;
-                if (zon && c < C && !(c == 0 && z0off)) u = o.J.zscale * (double)dep(c);
-            }
-            sink(r, j, u * o.sW[r]);
+    for (int j = 0; j < 16; ++j) {
+        double u = 0.0;
+        if (j < OT) {
+            u = (R == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(o.J, R, j) * mK;
+        } else if (j < OZ) {
+            u = jac_tau(o.J, R, j - OT) * mP;
+        } else if (R == 2) {
+            const int c = j - OZ;
+            if (zon && c < C && !(c == 0 && z0off)) u = o.J.zscale * (double)dep(c);
         }
+        sink(j, u * o.sW[R]);
     }
+}
+
+// All three weighted camera rows; sink(r, j, value).
+template <int HK, int HP, class JcSink>
+__device__ __forceinline__ void emit_jc(const ObsCore& o, const LinLayout& lay, bool enK, bool enP, bool enZ,
+                                        bool first_obs, const DepSrc& dep, JcSink&& sink) {
+    emit_jc_row<HK, HP, 0>(o, lay, enK, enP, enZ, first_obs, dep, [&](int j, double v) { sink(0, j, v); });
+    emit_jc_row<HK, HP, 1>(o, lay, enK, enP, enZ, first_obs, dep, [&](int j, double v) { sink(1, j, v); });
+    emit_jc_row<HK, HP, 2>(o, lay, enK, enP, enZ, first_obs, dep, [&](int j, double v) { sink(2, j, v); });
+}
+
+// Weighted point row R of Jp.
+template <int R>
+__device__ __forceinline__ void point_row(const ObsCore& o, const CamF& cp, bool xon, double Jp[3]) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) Jp[k] = (xon ? jac_pts(o.J, cp, R, k) : 0.0) * o.sW[R];
 }
 
 // Weighted point rows Jp (3x3) and, when asked, the point gradient J_p^T (W r) (unweighted rows).
@@ -341,24 +363,27 @@ __global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double d
 
 // ----------------------------------------------------------------------------- camera-pair blocks
 //
-// k_schur: one workgroup (8 waves, two per SIMD) per batch.  Per chunk of 128 observation slots:
-//   A1  waves 0-1, lane per slot: form the weighted camera rows J_c from the slot's linearisation
-//       record (rows 4-6 of the slot's LDS block, column 15 = W r / sqrt(W)) and the point rows;
-//       wave 2, lane per chunk track: Cholesky factor of the damped point block, its reciprocal
-//       pivots and w = L^-1 g_p; coverage masks by ballot.
-//   A2  waves 0-1: V = J_c^T J_p L^-T (rows 0-2 of the block, column 15 = w for the first
-//       observation of the track in the image, else 0); several observations of one track in one
-//       image are then summed into the first one.
-//   B   every wave, for each camera-pair slot it owns (accumulator in registers):
-//         off-diagonal (a,b):  acc += V_ta^T V_tb        one 16x16x4 fp64 MFMA per covering track
+// k_schur: one workgroup (16 waves, four per SIMD) per batch.  Per chunk of 128 observation slots:
+//   A1  waves 0-5, lane per (slot, row r): row r of the weighted camera rows J_c from the slot's
+//       linearisation record (rows 3-5 of the slot's LDS block, column 15 = W r / sqrt(W)) and row
+//       r of the point rows J_p; wave 6, lane per chunk track: Cholesky factor of the damped point
+//       block, its reciprocal pivots and w = L^-1 g_p.
+//   A2  waves 0-5, lane per (slot, column c): column c of V = J_c^T J_p L^-T (row c of the block,
+//       column 15 = w for the first observation of the track in the image, else 0); several
+//       observations of one track in one image are then summed into the first one.
+//   B   every wave, for each camera-pair slot it owns (accumulator in registers), over the slot's
+//       entry list (built by the planner once per structure):
+//         off-diagonal (a,b):  acc += V_ta^T V_tb        per covering track t
 //         diagonal (a,a):      acc += V_ta^T V_ta        per covering track
 //                              acc -= J_o^T J_o          per observation o in image a
-//       Rows 3 and 7 of a block are zero, so every MFMA reads 4 whole block rows with a uniform
-//       base address.  The partial block is -acc; column 15 of a diagonal tile then holds
-//       sum J_c^T W r - V w = the image's rhs term, and diag(J_c^T J_c) is summed from the
-//       squared B operands of the J MFMAs.
-// The next chunk's inputs (slot streams, and the chunk-track state written by k_track_pp) are
-// fetched while the current chunk's MFMAs run; every fetch is a single level (no gathers).
+//       The entries of a slot are taken four at a time along the MFMA's K dimension: lane group k
+//       of a 16x16x4 fp64 MFMA reads row c of entry k's blocks, and one MFMA per row c = 0..2
+//       sums c over four entries.  The partial block is -acc; column 15 of a diagonal tile then
+//       holds sum J_c^T W r - V w = the image's rhs term, and diag(J_c^T J_c) is summed from the
+//       squared B operands of the J entries.
+// The next chunk's inputs (its linearisation records, slot streams, the chunk-track state written by
+// k_track_pp, its entry list) are copied into LDS while the current chunk's MFMAs run.  Four waves
+// per SIMD keep four independent accumulation chains in flight on each MFMA pipe.
 
 __device__ __forceinline__ uint64_t uni64(uint64_t x) {
     uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
@@ -366,77 +391,100 @@ __device__ __forceinline__ uint64_t uni64(uint64_t x) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-struct ObsPre {                 // one observation slot, fetched a chunk ahead
-    int info, obs;
-    float dep[BA_PRE_C];
-};
-
-struct TrkPre {                 // one chunk track, fetched a chunk ahead
-    double H[6], g[3];
-    float4 X;
-    int mask, n_ct;
-};
-
-// per chunk track in LDS: the fetched state, then (after the factorisation) the factor
+// per chunk track in LDS, written by the factorisation
 struct TrkStage {
-    double L[6];                // H_pp upper, replaced by the Cholesky factor
-    double w[3];                // g_p, replaced by L^-1 g_p
+    double L[6];                // Cholesky factor of the damped point block (upper storage order)
+    double w[3];                // L^-1 g_p
     double rp[3];               // reciprocal pivots
-    float4 X;                   // point, enable flag
-    int mask, pad;
 };
 
-__device__ __forceinline__ void obs_fetch(const LinArgs& a, int64_t slot, int C, ObsPre& p) {
-    p.info = a.slot_info[slot];
-    p.obs = a.chunk_obs[slot];
-    const float* dg = a.s_dep + slot * C;
-#pragma unroll
-    for (int c = 0; c < BA_PRE_C; ++c) p.dep[c] = c < C ? dg[c] : 0.f;
+// The next chunk's inputs are copied straight into LDS staging arrays while the current chunk's
+// MFMAs run (global_load_lds: lane l of the issuing wave writes dst + 4 l or dst + 16 l; dst is
+// uniform),
+// so no registers hold them across the MFMA phase.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glob_void;
+__device__ __forceinline__ void dma4_to_lds(const void* src, void* wave_dst) {
+    __builtin_amdgcn_global_load_lds((glob_void*)src, (lds_void*)wave_dst, 4, 0, 0);
+}
+__device__ __forceinline__ void dma16_to_lds(const void* src, void* wave_dst) {
+    __builtin_amdgcn_global_load_lds((glob_void*)src, (lds_void*)wave_dst, 16, 0, 0);
 }
 
-__device__ __forceinline__ void trk_fetch(const LinArgs& a, int ck, int first_ct, int lane, TrkPre& p) {
-    p.n_ct = a.chunk_meta[4 * ck + 2];
-    int64_t ct = (int64_t)first_ct + lane;
-    ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
-    p.mask = a.ct_mask[ct];
-#pragma unroll
-    for (int k = 0; k < 6; ++k) p.H[k] = a.Hpp[6 * ct + k];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) p.g[k] = a.gp[3 * ct + k];
-    p.X = reinterpret_cast<const float4*>(a.ct_pt)[ct];
-}
+struct Staging {                // one chunk's inputs, laid out as the copies write them
+    double rec[BA_CORE * BA_CHUNK];         // the chunk's linearisation records (field-major, as in memory)
+    int info[BA_CHUNK];                     // slot_info per slot
+    int obs[BA_CHUNK];                      // chunk_obs per slot
+    float dep[BA_PRE_C][BA_CHUNK];          // depth guidance channels c < min(C, BA_PRE_C)
+    double H[3][BA_MAX_CT][2];              // H_pp upper of each chunk track, 16 bytes per copy
+    int g[6][BA_MAX_CT];                    // g_p, as 6 dwords
+    float4 X[BA_MAX_CT];                    // point, enable flag
+};
 
-__device__ __forceinline__ void trk_stage(const TrkPre& p, TrkStage& s) {
+// waves 0-1: the slots of chunk ck; wave 2: its chunk tracks (first_ct ..), n_ct; wave 3: its entry list
+__device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* sNct,
+                                            uint16_t (*lists)[BA_LIST_CAP], int (*tabs)[BA_MAX_SLOTS], int ck,
+                                            int first_ct, int C, int wave, int lane) {
+    if (wave < 2) {
+        const int w = __builtin_amdgcn_readfirstlane(wave);
+        const int64_t slot = (int64_t)ck * BA_CHUNK + 64 * w + lane;
+        // the record block: BA_CORE * BA_CHUNK doubles, 16 bytes per lane per copy
+        const double* rec = a.core + (int64_t)ck * BA_CORE * BA_CHUNK;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) s.L[k] = p.H[k];
+        for (int i = 0; i < BA_CORE * BA_CHUNK / 256; ++i)
+            dma16_to_lds(rec + 256 * i + 128 * w + 2 * lane, S.rec + 256 * i + 128 * w);
+        dma4_to_lds(a.slot_info + slot, S.info + 64 * w);
+        dma4_to_lds(a.chunk_obs + slot, S.obs + 64 * w);
 #pragma unroll
-    for (int k = 0; k < 3; ++k) s.w[k] = p.g[k];
-    s.X = p.X;
-    s.mask = p.mask;
+        for (int c = 0; c < BA_PRE_C; ++c)
+            if (c < C) dma4_to_lds(a.s_dep + slot * C + c, &S.dep[c][64 * w]);
+    } else if (wave == 2) {
+        int64_t ct = (int64_t)first_ct + lane;
+        ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) dma16_to_lds(a.Hpp + 6 * ct + 2 * k, &S.H[k][0][0]);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) dma4_to_lds(reinterpret_cast<const int*>(a.gp + 3 * ct) + k, S.g[k]);
+        dma16_to_lds(a.ct_pt + 4 * ct, S.X);
+        if (lane == 0) *sNct = a.chunk_meta[4 * ck + 2];
+    } else if (wave == 3) {
+        // the chunk's MFMA entry list (a full-capacity copy; the plan pads its array for it) and
+        // its slot table, into buffer ck & 1
+        const char* src = reinterpret_cast<const char*>(a.chunk_ent) + (int64_t)a.chunk_eptr[ck] * 16;
+        char* dst = reinterpret_cast<char*>(lists[ck & 1]);
+#pragma unroll
+        for (int i = 0; i < BA_LIST_CAP * 2 / 1024; ++i) dma16_to_lds(src + 1024 * i + 16 * lane, dst + 1024 * i);
+        if (lane < BA_MAX_SLOTS / 4)
+            dma16_to_lds(a.chunk_slots + (int64_t)ck * BA_MAX_SLOTS + 4 * lane, tabs[ck & 1]);
+    }
 }
 
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
-    extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks
+    extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks + zero block
     __shared__ TrkStage sTS[BA_MAX_CT];                  // per chunk track
-    __shared__ ObsPre sPre[BA_CHUNK];                    // per observation slot
+    __shared__ Staging sSt;                              // this chunk's inputs (the next chunk's, in phase B)
+    __shared__ double sJp[BA_CHUNK][9];                  // weighted point rows J_p of each slot
     __shared__ double sDv[BA_MAX_LOCAL][16];             // per local image: diag(J_c^T J_c)
-    __shared__ uint64_t sTm[BA_MAX_LOCAL];               // chunk tracks covering each local image
-    __shared__ uint64_t sIm[BA_MAX_LOCAL][2];            // slots observed in each local image
-    __shared__ uint64_t sLm[BA_MAX_LOCAL][2];            // ... first slot of a (track, image) run
     __shared__ int sInfo[BA_CHUNK];
-    __shared__ unsigned char sRowT[BA_MAX_LOCAL * BA_MAX_CT];   // (image, track) -> first slot
     __shared__ CamF sCam[BA_MAX_LOCAL];
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
-    __shared__ int sPair[BA_MAX_SLOTS];
+    __shared__ int sPair[BA_MAX_SLOTS];                  // per kernel place: the slot's pair, -1 if none
+    __shared__ int sQ[BA_MAX_SLOTS];                     // per kernel place: the batch slot
+    __shared__ uint16_t sList[2][BA_LIST_CAP];           // MFMA entry lists (chunk ck in buffer ck & 1)
+    __shared__ int sSlotTab[2][BA_MAX_SLOTS];            // per slot: entry offset | padded count << 16
     __shared__ int sDup[2];
     __shared__ int sNct;
 
     const int d = a.lay.d, C = a.lay.C;
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const bool obs_lane = tid < BA_CHUNK;                // waves 0-1: one observation slot per lane
-    const bool trk_wave = wave == 2;                     // wave 2: one chunk track per lane
+    // phase A roles: waves 0-5 take one (slot, row) each (slot tid % 128, row tid / 128), wave 6 the
+    // chunk tracks
+    const bool row_lane = tid < 3 * BA_CHUNK;
+    const int t = tid & (BA_CHUNK - 1), rr = tid >> 7;
+    const bool trk_wave = wave == 6;
+    static_assert(BA_WAVES >= 7, "phase A needs seven waves");
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
     const double lam = a.lam_p[0];
@@ -444,10 +492,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     int first_ct = a.chunk_meta[4 * c_begin + 1];
 
     {
-        ObsPre pre;
-        TrkPre tpre;
-        if (obs_lane) obs_fetch(a, (int64_t)c_begin * BA_CHUNK + tid, C, pre);
-        else if (trk_wave) trk_fetch(a, c_begin, first_ct, lane, tpre);
+        stage_chunk(a, sSt, &sNct, sList, sSlotTab, c_begin, first_ct, C, wave, lane);
         // local image parameters
         if (tid < nimg) {
             int img = a.b_imgs[(int64_t)batch * a.L + tid];
@@ -457,246 +502,184 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             sEn[3 * tid + 1] = a.enP ? a.enP[node] : 1;
             sEn[3 * tid + 2] = a.enZ ? a.enZ[img] : 1;
         }
-        // the pair of slot q: (a | b << 8), -1 past the batch's slots
-        for (int q = tid; q < BA_MAX_SLOTS; q += BA_WAVES * 64) sPair[q] = q < ns ? a.slot_pair[s0 + q] : -1;
-        for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
-        if (obs_lane) sPre[tid] = pre;
-        else if (trk_wave) {
-            trk_stage(tpre, sTS[lane]);
-            if (lane == 0) sNct = tpre.n_ct;
+        // kernel place p = wave + BA_WAVES * k holds batch slot sQ[p] with pair (a | b << 8), or -1
+        for (int p = tid; p < BA_MAX_SLOTS; p += BA_WAVES * 64) {
+            const int q = a.b_pos_slot[(int64_t)batch * BA_MAX_SLOTS + p];
+            sQ[p] = q;
+            sPair[p] = q >= 0 && q < ns ? a.slot_pair[s0 + q] : -1;
         }
+        for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
+        for (int q = tid; q < 48; q += BA_WAVES * 64) sBlk[BA_ZERO + q] = 0.0;
     }
     __syncthreads();
 
     dbl4 acc[BA_SLOTS_PER_WAVE];
+    int my_pq[BA_SLOTS_PER_WAVE], my_q[BA_SLOTS_PER_WAVE];       // this wave's slots: pair, batch slot
 #pragma unroll
-    for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) acc[q] = dbl4{0.0, 0.0, 0.0, 0.0};
-    // MFMA operand element of this lane inside a 4-row group: row lane/16, column lane%16
-    const int loff = (lane >> 4) * 16 + (lane & 15);
+    for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
+        acc[q] = dbl4{0.0, 0.0, 0.0, 0.0};
+        my_pq[q] = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
+        my_q[q] = __builtin_amdgcn_readfirstlane(sQ[wave + BA_WAVES * q]);
+    }
+    // MFMA operand element of this lane: K index lane/16 (the entry), column lane%16
+    const int kq = lane >> 4, l15 = lane & 15;
 
     for (int ck = c_begin; ck < c_end; ++ck) {
         if (ck != c_begin) __syncthreads();    // previous chunk consumed; this chunk's inputs staged
         const int n_ct = sNct;
 
         // ---------------- A1
-        const int info = obs_lane ? sPre[tid].info : -1;
+        const int info = row_lane ? sSt.info[t] : -1;
         const bool valid = info >= 0;
         const int li = info & 0xff, ct = (info >> 8) & 0xff, leader = info >> 16;
-        if (obs_lane) {
-            sInfo[tid] = info;
+        if (row_lane) {
+            if (rr == 0) sInfo[t] = info;
             if (valid) {
-                const ObsPre& pr = sPre[tid];
-                DepSrc dep;
-#pragma unroll
-                for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = pr.dep[c];
-                dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + tid) * C;
                 ObsCore o;
-                core_load(a.core + (int64_t)ck * BA_CORE * BA_CHUNK, tid, o);
+                core_load(sSt.rec, t, o);
                 const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
-                double* blk = sBlk + tid * BA_BLK;
-                emit_jc<HK, HP>(o, a.lay, eK, eP, eZ, pr.obs == 0, dep, [&](int r, int j, double v) {
-                    if (j < 15) blk[64 + 16 * r + j] = j < d ? v : 0.0;
-                });
+                const bool first = sSt.obs[t] == 0, xon = sSt.X[ct].w != 0.f && !a.lay.x_off;
+                double* blk = sBlk + t * BA_BLK + BA_JROW + 16 * rr;
+                auto sink = [&](int j, double v) { if (j < 15) blk[j] = j < d ? v : 0.0; };
+                double jp[3];
+                DepSrc dep;
+                if (rr == 0) {
+                    emit_jc_row<HK, HP, 0>(o, a.lay, eK, eP, eZ, first, dep, sink);
+                    blk[15] = o.Rs[0];
+                    point_row<0>(o, sCam[li], xon, jp);
+                } else if (rr == 1) {
+                    emit_jc_row<HK, HP, 1>(o, a.lay, eK, eP, eZ, first, dep, sink);
+                    blk[15] = o.Rs[1];
+                    point_row<1>(o, sCam[li], xon, jp);
+                } else {
 #pragma unroll
-                for (int r = 0; r < 3; ++r) blk[64 + 16 * r + 15] = o.Rs[r];
+                    for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = c < C ? sSt.dep[c][t] : 0.f;
+                    dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + t) * C;
+                    emit_jc_row<HK, HP, 2>(o, a.lay, eK, eP, eZ, first, dep, sink);
+                    blk[15] = o.Rs[2];
+                    point_row<2>(o, sCam[li], xon, jp);
+                }
 #pragma unroll
-                for (int j = 0; j < 16; ++j) blk[112 + j] = 0.0;
-                // J_p waits in row 0 until A2 overwrites the row with V
-                double Jp[3][3], gP[3];
-                point_rows<false>(o, sCam[li], sTS[ct].X.w != 0.f && !a.lay.x_off, Jp, gP);
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-#pragma unroll
-                    for (int k = 0; k < 3; ++k) blk[3 * r + k] = Jp[r][k];
-                if (leader == tid) sRowT[li * BA_MAX_CT + ct] = (unsigned char)tid;
+                for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
             }
-            uint64_t im = 0, lm = 0;
-#pragma unroll
-            for (int m = 0; m < BA_MAX_LOCAL; ++m) {
-                const uint64_t b = __ballot(valid && li == m);
-                const uint64_t bl = __ballot(valid && li == m && leader == tid);
-                if (lane == m) { im = b; lm = bl; }
+            if (rr == 0) {
+                const uint64_t dup = __ballot(valid && leader != t);
+                if (lane == 0) sDup[wave] = dup != 0;
             }
-            if (lane < BA_MAX_LOCAL) { sIm[lane][wave] = im; sLm[lane][wave] = lm; }
-            const uint64_t dup = __ballot(valid && leader != tid);
-            if (lane == 0) sDup[wave] = dup != 0;
         } else if (trk_wave) {
             TrkStage& T = sTS[lane];
-            const int mask = T.mask;
             if (lane < n_ct) {
-                double H[6], Lf[6];
+                double H[6], Lf[6], gv[3];
 #pragma unroll
-                for (int k = 0; k < 6; ++k) H[k] = T.L[k];
+                for (int k = 0; k < 6; ++k) H[k] = sSt.H[k >> 1][lane][k & 1];
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+                    gv[k] = __hiloint2double(sSt.g[2 * k + 1][lane], sSt.g[2 * k][lane]);
                 chol3_factor(H, lam, Lf);
                 const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
-                const double w0 = T.w[0] * r0;
-                const double w1 = (T.w[1] - Lf[1] * w0) * r1;
-                const double w2 = (T.w[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
+                const double w0 = gv[0] * r0;
+                const double w1 = (gv[1] - Lf[1] * w0) * r1;
+                const double w2 = (gv[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
 #pragma unroll
                 for (int k = 0; k < 6; ++k) T.L[k] = Lf[k];
                 T.rp[0] = r0; T.rp[1] = r1; T.rp[2] = r2;
                 T.w[0] = w0; T.w[1] = w1; T.w[2] = w2;
             }
-            uint64_t tm = 0;
-#pragma unroll
-            for (int m = 0; m < BA_MAX_LOCAL; ++m) {
-                const uint64_t b = __ballot(lane < n_ct && ((mask >> m) & 1));
-                if (lane == m) tm = b;
-            }
-            if (lane < BA_MAX_LOCAL) sTm[lane] = tm;
         }
         __syncthreads();
 
-        // ---------------- A2: V = J_c^T P with P = J_p L^-T, column by column
-        if (valid) {
+        // ---------------- A2: V = J_c^T P with P = J_p L^-T; lane (slot, rr) forms column c = rr
+        if (row_lane && valid) {
+            const int c = rr;
             const TrkStage& T = sTS[ct];
             const double l10 = T.L[1], l20 = T.L[2], l21 = T.L[4], r0 = T.rp[0], r1 = T.rp[1], r2 = T.rp[2];
-            double* blk = sBlk + tid * BA_BLK;
-            double P[3][3];
+            double Pc[3];
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
-                P[r][0] = blk[3 * r] * r0;
-                P[r][1] = (blk[3 * r + 1] - l10 * P[r][0]) * r1;
-                P[r][2] = (blk[3 * r + 2] - l20 * P[r][0] - l21 * P[r][1]) * r2;
+                const double p0 = sJp[t][3 * r] * r0;
+                const double p1 = (sJp[t][3 * r + 1] - l10 * p0) * r1;
+                const double p2 = (sJp[t][3 * r + 2] - l20 * p0 - l21 * p1) * r2;
+                Pc[r] = c == 0 ? p0 : (c == 1 ? p1 : p2);
             }
-            const bool lead = leader == tid;
+            double* blk = sBlk + t * BA_BLK;
 #pragma unroll
             for (int j = 0; j < 15; ++j) {
-                const double j0 = blk[64 + j], j1 = blk[80 + j], j2 = blk[96 + j];
-#pragma unroll
-                for (int c = 0; c < 3; ++c) blk[16 * c + j] = j < d ? j0 * P[0][c] + j1 * P[1][c] + j2 * P[2][c] : 0.0;
+                const double j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
+                blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : 0.0;
             }
-#pragma unroll
-            for (int c = 0; c < 3; ++c) blk[16 * c + 15] = lead ? T.w[c] : 0.0;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) blk[48 + j] = 0.0;
+            blk[16 * c + 15] = leader == t ? T.w[c] : 0.0;
         }
         __syncthreads();
         if (sDup[0] | sDup[1]) {
             // several observations of one track in one image: V of the run is summed into its first slot
-            if (valid && leader == tid) {
-                double* dst = sBlk + tid * BA_BLK;
-                for (int f = tid + 1; f < BA_CHUNK; ++f) {
+            if (row_lane && valid && leader == t) {             // lane (slot, rr): V row rr
+                double* dst = sBlk + t * BA_BLK + 16 * rr;
+                for (int f = t + 1; f < BA_CHUNK; ++f) {
                     const int fi = sInfo[f];
-                    if (fi < 0 || (fi >> 16) != tid) break;
-                    const double* src = sBlk + f * BA_BLK;
+                    if (fi < 0 || (fi >> 16) != t) break;
+                    const double* src = sBlk + f * BA_BLK + 16 * rr;
 #pragma unroll
-                    for (int c = 0; c < 3; ++c)
-#pragma unroll
-                        for (int j = 0; j < 15; ++j) dst[16 * c + j] += src[16 * c + j];
+                    for (int j = 0; j < 15; ++j) dst[j] += src[j];
                 }
             }
             __syncthreads();
         }
 
-        // next chunk's inputs: fetched into registers now, staged into LDS after the MFMAs
-        const bool more = ck + 1 < c_end;
-        ObsPre pre;
-        TrkPre tpre;
-        if (more) {
-            if (obs_lane) {
-                obs_fetch(a, (int64_t)(ck + 1) * BA_CHUNK + tid, C, pre);
-            } else if (trk_wave) {
-                first_ct += n_ct;
-                trk_fetch(a, ck + 1, first_ct, lane, tpre);
-            }
+        // next chunk's inputs: copied into the staging arrays while the MFMAs run (this chunk's A1,
+        // the only reader of the staging arrays, is past)
+        if (ck + 1 < c_end) {
+            first_ct += n_ct;
+            stage_chunk(a, sSt, &sNct, sList, sSlotTab, ck + 1, first_ct, C, wave, lane);
         }
 
         // ---------------- B: camera-pair tiles
-        // coverage masks and first-slot rows of every owned off-diagonal slot, read together
-        int pqs[BA_SLOTS_PER_WAVE];
-        uint64_t covs[BA_SLOTS_PER_WAVE];
-        int rAs[BA_SLOTS_PER_WAVE], rBs[BA_SLOTS_PER_WAVE];
+        // one group of four entries: lane group kq reads row c of its entry's A and B blocks (the
+        // descriptor of the next group is requested before this group's operands), then one MFMA
+        // per row c; a diagonal slot's J entries negate A and feed diag(J_c^T J_c)
+        auto run_slot = [&](const uint16_t* L, int ng, dbl4 acc_in, bool diag, double& dsq) -> dbl4 {
+            dbl4 acc_l = acc_in;
+            uint32_t dn = ng > 0 ? L[kq] : 0u;
+            for (int g = 0; g < ng; ++g) {
+                const uint32_t dsc = dn;
+                if (g + 1 < ng) dn = L[4 * (g + 1) + kq];
+                const uint32_t kind = dsc >> 14;
+                const int roff = kind == BA_ENT_J ? BA_JROW : 0;
+                const int ia = (kind == BA_ENT_PAD ? BA_ZERO : (int)(dsc & 127u) * BA_BLK + roff) + l15;
+                const int ib = (kind == BA_ENT_PAD ? BA_ZERO : (int)((dsc >> 7) & 127u) * BA_BLK + roff) + l15;
+                double A[3], B[3];
 #pragma unroll
-        for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-            const int pq = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
-            const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
-            pqs[q] = pq;
-            covs[q] = 0;
-            rAs[q] = rBs[q] = 0;
-            if (pq >= 0 && la != lb) {
-                covs[q] = sTm[la] & sTm[lb];
-                rAs[q] = sRowT[la * BA_MAX_CT + lane];
-                rBs[q] = sRowT[lb * BA_MAX_CT + lane];
+                for (int c = 0; c < 3; ++c) { A[c] = sBlk[ia + 16 * c]; B[c] = sBlk[ib + 16 * c]; }
+                if (diag) {
+                    const uint64_t sgn = (uint64_t)(kind == BA_ENT_J) << 63;
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        if (sgn) dsq += B[c] * B[c];
+                        A[c] = __longlong_as_double(__double_as_longlong(A[c]) ^ (long long)sgn);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < 3; ++c) acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], B[c], acc_l, 0, 0, 0);
+                // keep the group's LDS reads ahead of its MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, 7, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
             }
-        }
+            return acc_l;
+        };
 #pragma unroll
         for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-            const int pq = pqs[q];
+            const int pq = my_pq[q];
             if (pq < 0) continue;
             const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
+            const int tab = __builtin_amdgcn_readfirstlane(sSlotTab[ck & 1][my_q[q]]);
+            const int off = tab & 0xffff, ng = (tab >> 16) >> 2;
+            double dsq = 0.0;
             if (la != lb) {
-                uint64_t cov = uni64(covs[q]);
-                const int rA = rAs[q], rB = rBs[q];
-                // covering tracks in groups of four: the eight operand reads of a group are issued
-                // together, then its four MFMAs run as they arrive (a short group re-reads its first
-                // track with B = 0, adding exact zeros)
-                while (cov) {
-                    int t[4];
-                    int n = 0;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        if (cov) { t[k] = __builtin_ctzll(cov); cov &= cov - 1; ++n; }
-                        else t[k] = t[0];
-                    }
-                    double A[4], B[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        A[k] = sBlk[__builtin_amdgcn_readlane(rA, t[k]) * BA_BLK + loff];
-                        B[k] = sBlk[__builtin_amdgcn_readlane(rB, t[k]) * BA_BLK + loff];
-                    }
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[k], k < n ? B[k] : 0.0, acc[q], 0, 0, 0);
-                    // keep the group's LDS reads ahead of its MFMAs (the scheduler would otherwise
-                    // pair each read with its MFMA to save registers, serialising on LDS latency)
-                    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-                }
+                acc[q] = run_slot(sList[ck & 1] + off, ng, acc[q], false, dsq);
             } else {
-                // J rows (block offset 64) of every observation in the image, subtracted (A = -B) and
-                // feeding diag(J_c^T J_c); then V rows (offset 0) of every (track, image) run; both
-                // lists in groups of four like the off-diagonal tracks
-                double dsq = 0.0;
-#pragma unroll
-                for (int part = 0; part < 2; ++part) {
-                    const bool jr = part == 0;
-                    uint64_t w0 = uni64(jr ? sIm[la][0] : sLm[la][0]);
-                    uint64_t w1 = uni64(jr ? sIm[la][1] : sLm[la][1]);
-                    const int roff = (jr ? 64 : 0) + loff;
-                    while (w0 | w1) {
-                        int o[4];
-                        int n = 0;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            if (w0) { o[k] = __builtin_ctzll(w0); w0 &= w0 - 1; ++n; }
-                            else if (w1) { o[k] = 64 + __builtin_ctzll(w1); w1 &= w1 - 1; ++n; }
-                            else o[k] = o[0];
-                        }
-                        double B[4];
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) B[k] = sBlk[o[k] * BA_BLK + roff];
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const double b = k < n ? B[k] : 0.0;
-                            acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(jr ? -b : b, b, acc[q], 0, 0, 0);
-                            if (jr) dsq += b * b;
-                        }
-                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-                    }
-                }
+                acc[q] = run_slot(sList[ck & 1] + off, ng, acc[q], true, dsq);
                 dsq += __shfl_xor(dsq, 16);
                 dsq += __shfl_xor(dsq, 32);
                 if (lane < 16) sDv[la][lane] += dsq;
-            }
-        }
-        // stage the next chunk's inputs (A1 and A2 of this chunk are past, so the arrays are free)
-        if (more) {
-            if (obs_lane) sPre[tid] = pre;
-            else if (trk_wave) {
-                trk_stage(tpre, sTS[lane]);
-                if (lane == 0) sNct = tpre.n_ct;
             }
         }
     }
@@ -706,9 +689,9 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     const int jc = lane & 15;
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-        const int pq = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
+        const int pq = my_pq[q];
         if (pq >= 0) {
-            const int sl = wave + BA_WAVES * q;
+            const int sl = my_q[q];
             double* P = a.partials + (int64_t)(s0 + sl) * d * d;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -880,7 +863,7 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
         return BA_OK;
     }
     if (stage == 1 && a.n_batches > 0) {
-        size_t lds = (size_t)BA_CHUNK * BA_BLK * sizeof(double);
+        size_t lds = ((size_t)BA_CHUNK * BA_BLK + 48) * sizeof(double);
         BA_DISPATCH_KP(a.lay, {
             BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds));

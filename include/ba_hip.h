@@ -125,6 +125,8 @@ typedef struct {
     float* ct_pt;         /* (n_ctracks,4) scratch written by stage 0: x, y, z, enable */
     int64_t n_ctracks;
     double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0) */
+    const int32_t *chunk_slots, *chunk_ent, *chunk_eptr;   /* plan: MFMA entry lists of every chunk */
+    const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.

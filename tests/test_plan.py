@@ -77,6 +77,70 @@ def test_plan_invariants(cfg, nf, nt, kw):
             assert (e & 1) == int(ga > gc)
 
 
+@pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 6, 60, {}), (0, 32, 3000, {}), (2, 60, 6000, {}),
+                                          (0, 12, 500, dict(max_slots=40))])
+def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
+    """The per-chunk MFMA entry lists equal an independent reconstruction from slot_info: per
+    off-diagonal slot (a, b) one V entry per covering chunk track (chunk-track order) joining the
+    first observations of its runs in a and b; per diagonal slot (a, a) one J entry per observation
+    in a, then one V entry per (track, image) run in a (slot order); padding to a multiple of 4 with
+    PAD entries; at most BA_LIST_CAP (1536) entries per chunk."""
+    V, J, PAD, CAP, MS = 0, 1, 2, 1536, 96
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    pl = _plan(p, **kw)
+    h = pl.host
+    ents = h['chunk_ent'].view(np.uint16)
+    meta = h['chunk_meta'].reshape(-1, 4)
+    n_chunks = len(meta)
+    assert ents.size >= 8 * int(h['chunk_eptr'][-1]) + CAP if n_chunks else True
+    total_real = 0
+    for ck in range(n_chunks):
+        batch, first_ct, n_ct, used = meta[ck]
+        info = h['slot_info'][ck * 128:(ck + 1) * 128]
+        lead = {}
+        for sidx in range(used):
+            li, t, ld = info[sidx] & 0xff, (info[sidx] >> 8) & 0xff, info[sidx] >> 16
+            lead.setdefault((t, li), ld)
+            assert lead[(t, li)] == ld
+        s0, s1 = h['b_slot_ptr'][batch], h['b_slot_ptr'][batch + 1]
+        base = 8 * int(h['chunk_eptr'][ck])
+        tab = h['chunk_slots'][ck * MS:(ck + 1) * MS]
+        end = 0
+        for q in range(MS):
+            off, ln = int(tab[q]) & 0xffff, int(tab[q]) >> 16
+            if q >= s1 - s0:
+                assert tab[q] == 0
+                continue
+            pq = h['slot_pair'][s0 + q]
+            a, b = pq & 0xff, (pq >> 8) & 0xff
+            want = []
+            if a != b:
+                for t in range(n_ct):
+                    if (t, a) in lead and (t, b) in lead:
+                        want.append(lead[(t, a)] | lead[(t, b)] << 7 | V << 14)
+            else:
+                want += [sidx | sidx << 7 | J << 14 for sidx in range(used) if info[sidx] & 0xff == a]
+                want += [sidx | sidx << 7 | V << 14 for sidx in range(used)
+                         if info[sidx] & 0xff == a and info[sidx] >> 16 == sidx]
+            total_real += len(want)
+            want += [PAD << 14] * (-len(want) % 4)
+            assert ln == len(want) and ln % 4 == 0
+            assert off == end
+            assert np.array_equal(ents[base + off:base + off + ln], np.array(want, dtype=np.uint16))
+            end += ln
+        assert end <= CAP
+    # every pair term and every observation once: sum over tracks of m(m+1)/2 plus n_obs
+    assert total_real == pl.scalars['n_pair_terms'] + p.n_obs
+    # kernel places: every batch slot at exactly one place, at most 6 places used per wave (16 waves)
+    pos = h['b_pos_slot'].reshape(-1, MS)
+    for b in range(len(pos)):
+        ns = h['b_slot_ptr'][b + 1] - h['b_slot_ptr'][b]
+        used = pos[b][pos[b] >= 0]
+        assert np.array_equal(np.sort(used), np.arange(ns))
+        per_wave = np.bincount(np.nonzero(pos[b] >= 0)[0] % 16, minlength=16)
+        assert per_wave.max() <= 6
+
+
 def test_plan_errors():
     p = make_problem(0, n_frames=8, n_tracks=50)
     with pytest.raises(RuntimeError, match='max_local_imgs'):
