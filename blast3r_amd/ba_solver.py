@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import PCG_LONG_LIST, BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
+from ._lib import PCG_BLOCK, PCG_LONG_LIST, BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
 from .plan import get_plan
 
 N_FOC = 2   # focal columns (bs:11)
@@ -179,9 +179,13 @@ class GaussNewtonSolver:
         dev = self.device
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
         long_u = np.nonzero(counts > PCG_LONG_LIST)[0]
+        nblk = (n_u + PCG_BLOCK - 1) // PCG_BLOCK
+        long_ptr = np.searchsorted(long_u, np.arange(nblk + 1) * PCG_BLOCK).astype(np.int32)
+        long_idx = np.full(max(n_u, 1), -1, dtype=np.int32)
+        long_idx[long_u] = np.arange(len(long_u)) - long_ptr[long_u // PCG_BLOCK]
         out = dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
                    leaf=t(leaf if n_u else np.zeros(1)), long_u=t(long_u if len(long_u) else np.zeros(1)),
-                   n_long=len(long_u))
+                   n_long=len(long_u), long_ptr=t(long_ptr), long_idx=t(long_idx))
         cache[key] = out
         return out
 
@@ -309,19 +313,21 @@ class GaussNewtonSolver:
             pa.maxiter, pa.tol = int(self.pcg_maxiter), float(self.pcg_tol)
             vec = lambda name: ws('pcg_' + name, (n_u,), torch.float64)
             rhs, diagA, damp = vec('rhs'), vec('diagA'), vec('damp')
-            xbest, r, z, Ap = vec('xbest'), vec('r'), vec('z'), vec('Ap')
+            xbest, r, z = vec('xbest'), vec('r'), vec('z')
             p = ws('pcg_p2', (2 * n_u,), torch.float64)
             y_img = ws('pcg_y', (n_imgs * d,), torch.float64)
             part = ws('pcg_part', (int(lib().ba_pcg_partials_size(n_u)),), torch.float64)
             state = ws('pcg_state', (16,), torch.float64)
             pa.rhs, pa.diagA, pa.damp, pa.x, pa.xbest = ptr(rhs), ptr(diagA), ptr(damp), ptr(x), ptr(xbest)
-            pa.r, pa.z, pa.p, pa.Ap, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(Ap), ptr(y_img)
+            pa.r, pa.z, pa.p, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(y_img)
+            pa.img_part = ptr(ws('pcg_img_part', (n_imgs,), torch.float64))
             pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
             n_ent = int(plan.host['row_ptr'][-1]) if len(plan.host['row_ptr']) else 0
             S_rows = ws('pcg_S_rows', (max(n_ent, 1), d, d), torch.float64)
             pa.S_rows, pa.n_row_ent = ptr(S_rows), n_ent
             pa.row_u = ptr(ws('pcg_row_u', (max(n_ent, 1) * 16,), torch.int32))
             pa.long_u, pa.n_long = ptr(um['long_u']), um['n_long']
+            pa.long_ptr, pa.long_idx = ptr(um['long_ptr']), ptr(um['long_idx'])
             self._run_pcg(pa, plan, st)
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
         # back-substitution for the points

@@ -18,6 +18,9 @@ namespace ba {
 
 #define PCG_T 256
 #define PCG_ST 512          // threads of the image-row SpMV: 32 groups of 16 lanes
+// Block partials of the update launch (nb blocks): r.r and r.z, PCG_NP per block.
+#define PCG_NP 2
+enum { PT_RR = 0, PT_RZ = 1 };
 
 // state (fp64): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
 // both in slot n & 1; ST_BETA the beta of the current direction; ST_LEAF.. the camera-leaf damping.
@@ -51,12 +54,33 @@ __device__ __forceinline__ double block_sum(double v, double* sh) {
     return t;
 }
 
-// Sum of n block partials at stride 3 (deterministic, identical in every block of NT threads).
+// K block sums at once with two barriers; v[k] becomes the sum of every thread's v[k], in the
+// same order as block_sum.  sh holds at least K * NT / 64 doubles.
+template <int NT, int K>
+__device__ __forceinline__ void block_sums(double (&v)[K], double* sh) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = wave_sum(v[k]);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int k = 0; k < K; ++k) sh[k * (NT / 64) + (threadIdx.x >> 6)] = v[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) t += sh[k * (NT / 64) + w];
+        v[k] = t;
+    }
+}
+
+// Sums of r.r and r.z over the nb block partials (deterministic, identical in every block of NT
+// threads); sh holds at least 2 * NT / 64 doubles.
 template <int NT>
-__device__ __forceinline__ double sum_partials(const double* __restrict__ part, int nb, int which, double* sh) {
-    double v = 0.0;
-    for (int b = threadIdx.x; b < nb; b += NT) v += part[3 * b + which];
-    return block_sum<NT>(v, sh);
+__device__ __forceinline__ void sum_partials(const double* __restrict__ part, int nb, double (&rs)[2], double* sh) {
+    rs[0] = 0.0; rs[1] = 0.0;
+    for (int b = threadIdx.x; b < nb; b += NT) { rs[0] += part[PCG_NP * b + PT_RR]; rs[1] += part[PCG_NP * b + PT_RZ]; }
+    block_sums<NT, 2>(rs, sh);
 }
 
 // unknown-level rhs and diag(H_cc) from the image-level vectors; one wave per unknown so that
@@ -115,21 +139,22 @@ __global__ void __launch_bounds__(PCG_T) k_leaf_damp(ba_pcg_args a) {
 __global__ void __launch_bounds__(PCG_T) k_pcg_init(ba_pcg_args a) {
     __shared__ double sh[PCG_T];
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    double bb = 0.0, rz = 0.0;
+    double t[2] = {0.0, 0.0};
     if (u < a.n_u) {
         double b = a.rhs[u];
         double z = b / a.diagA[u];
         a.x[u] = 0.0; a.xbest[u] = 0.0; a.r[u] = b; a.z[u] = z; a.p[a.n_u + u] = 0.0;
-        bb = b * b; rz = b * z;
+        t[0] = b * b; t[1] = b * z;
     }
-    double s0 = block_sum<PCG_T>(bb, sh), s1 = block_sum<PCG_T>(rz, sh);
-    if (threadIdx.x == 0) { a.partials[3 * blockIdx.x + 0] = s0; a.partials[3 * blockIdx.x + 1] = s1; }
+    block_sums<PCG_T, 2>(t, sh);
+    if (threadIdx.x == 0) { a.partials[PCG_NP * blockIdx.x + PT_RR] = t[0]; a.partials[PCG_NP * blockIdx.x + PT_RZ] = t[1]; }
 }
 
 __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
     __shared__ double sh[PCG_T];
-    double bb = sum_partials<PCG_T>(a.partials, nb, 0, sh);
-    double rz = sum_partials<PCG_T>(a.partials, nb, 1, sh);
+    double rs[2];
+    sum_partials<PCG_T>(a.partials, nb, rs, sh);
+    const double bb = rs[0], rz = rs[1];
     if (threadIdx.x == 0) {
         double bn = sqrt(bb);
         a.state[ST_BNORM] = bn > 1e-12 ? bn : 1e-12;    // torch.norm(b).clamp(min=1e-12)
@@ -167,13 +192,17 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 }
 
 // ----------------------------------------------------------------------------- one CG iteration
-// Iteration n (n = 0 .. maxiter - 1; the reference numbers it n + 1, ba_solver.py:1216-1236) is three
+// Iteration n (n = 0 .. maxiter - 1; the reference numbers it n + 1, ba_solver.py:1216-1236) is two
 // launches:
 //   k_pcg_spmv(n)    the stopping decisions after update n - 1 (every block forms them from the same
 //                    partial sums, so they agree without a grid barrier), the best-so-far copy, then
-//                    y_img = S_img p_n with p_n formed on the fly from z and p_{n-1};
-//   k_pcg_gather(n)  Ap = P^T y_img + damp p_n and the partials of p.Ap;
-//   k_pcg_update(n)  alpha, x, r, z, the stored p_n, and the partials of r.r and r.z.
+//                    y_img = S_img p_n with p_n formed on the fly from z and p_{n-1}, and per image
+//                    row i a partial of p.Ap = sum_e p_u(e) y_e + sum_u damp_u p_u^2 (e over the
+//                    image-level entries, u over the unknowns, the block of row i taking
+//                    u = i, i + n_imgs, ...: A p = P^T y_img + damp p);
+//   k_pcg_update(n)  alpha, A p of the block's unknowns (one thread per short inverse list, one
+//                    wave per long one), x, r, z, the stored p_n, and the block partials of r.r
+//                    and r.z.
 // p is double-buffered (p_n in slot n & 1).  A launch after the stopping point returns at once: the
 // flag "stopped before update n" lives in IS_DONE0 + (n & 1) and is written by k_pcg_spmv(n - 1).
 
@@ -184,10 +213,7 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 // first pass are requested before the scalar decisions, which only need the partial sums.
 __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int nb) {
     __shared__ double sh[PCG_ST];
-    if (a.istate[IS_DONE0 + (n & 1)]) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) a.istate[IS_DONE0 + ((n + 1) & 1)] = 1;
-        return;
-    }
+    __shared__ double sDamp[PCG_ST / 64];
     const int i = blockIdx.x;
     const int grp = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int d = a.d, dd = d * d;
@@ -210,13 +236,22 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     };
     int u;
     double zv, pv, bcol[16];
-    load(q0 + grp, u, zv, pv, bcol);
+    load(q0 + grp, u, zv, pv, bcol);                 // requested before the done flag is known
+    // damping term of the unknowns v = i + k n_imgs (thread k): its first operands are requested now
+    const int64_t v0 = i + (int64_t)threadIdx.x * a.n_imgs;
+    double dz = 0.0, dpo = 0.0, dd0 = 0.0;
+    if (v0 < a.n_u) { dz = a.z[v0]; dpo = pold[v0]; dd0 = a.damp[v0]; }
+    if (a.istate[IS_DONE0 + (n & 1)]) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.istate[IS_DONE0 + ((n + 1) & 1)] = 1;
+        return;
+    }
 
     double beta = 0.0;
     if (n >= 1) {
         // end of update n - 1 (ba_solver.py:1222-1236)
-        const double rr = sum_partials<PCG_ST>(a.partials, nb, 0, sh);
-        const double rz_new = sum_partials<PCG_ST>(a.partials, nb, 1, sh);
+        double rs[2];
+        sum_partials<PCG_ST>(a.partials, nb, rs, sh);
+        const double rr = rs[0], rz_new = rs[1];
         const double rnorm = sqrt(rr);
         const double best = a.state[ST_BEST0 + ((n - 1) & 1)];
         const bool improved = rnorm < best;
@@ -241,6 +276,16 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     } else if (blockIdx.x == 0 && threadIdx.x == 0) {
         a.istate[IS_DONE0 + 1] = 0;
     }
+    double dsum = 0.0;
+    {
+        const double pv0 = pdir(dz, dpo, beta);
+        dsum = dd0 * pv0 * pv0;
+        for (int64_t v = v0 + (int64_t)PCG_ST * a.n_imgs; v < a.n_u; v += (int64_t)PCG_ST * a.n_imgs) {
+            const double pv2 = pdir(a.z[v], pold[v], beta);
+            dsum += a.damp[v] * pv2 * pv2;
+        }
+        dsum = wave_sum(dsum);
+    }
     double acc = mac(u, zv, pv, beta, bcol, 0.0);
     for (int qb = q0 + PCG_ST / 16; qb < q1; qb += PCG_ST / 16) {     // rows longer than 32 blocks
         load(qb + grp, u, zv, pv, bcol);
@@ -248,95 +293,86 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     }
     __syncthreads();
     sh[threadIdx.x] = acc;
+    if ((threadIdx.x & 63) == 0) sDamp[threadIdx.x >> 6] = dsum;
     __syncthreads();
-    if (threadIdx.x < 16 && j < d) {
-        double t = 0.0;
-        for (int g = 0; g < PCG_ST / 16; ++g) t += sh[16 * g + j];
-        a.y_img[(int64_t)i * d + j] = t;
+    // y of this image row; the row's share of p.Ap: sum_e p_u(e) y_e over its entries (one wave,
+    // 16 rows at most) plus the damping sum of its unknowns
+    if (threadIdx.x < 64) {
+        double part = 0.0;
+        if (j < d && threadIdx.x < 16) {
+            double t = 0.0;
+            for (int g = 0; g < PCG_ST / 16; ++g) t += sh[16 * g + j];
+            a.y_img[(int64_t)i * d + j] = t;
+            const int uo = a.umap[(int64_t)i * d + j];
+            if (uo >= 0) part = pdir(a.z[uo], pold[uo], beta) * t;
+        }
+        part = wave_sum(part);
+        if (threadIdx.x == 0) {
+            double dt = 0.0;
+#pragma unroll
+            for (int w = 0; w < PCG_ST / 64; ++w) dt += sDamp[w];
+            a.img_part[i] = part + dt;
+        }
     }
 }
 
-// Ap[u] = sum of the image-level rows mapping to u + damp[u] p_n[u], and per-block partials of p.Ap.
-// Blocks [0, nb) take one unknown per thread (lists of at most BA_PCG_LONG_LIST entries); blocks
-// [nb, nb + nlb) take one of the long_u unknowns per wave (a focal pair shared by every image of a
-// camera has one entry per image), reading 8 entries per lane at a time as independent loads.
-__global__ void __launch_bounds__(PCG_T) k_pcg_gather(ba_pcg_args a, int n, int nb) {
-    __shared__ double sh[PCG_T / 64];
+// alpha = rz / max(p.Ap, 1e-32); x += alpha p; r -= alpha Ap; z = M^-1 r (ba_solver.py:1217-1228);
+// p_n stored in slot n & 1; block partials r.r, r.z.  A p of
+// unknown u is the sum of the image-level rows mapping to u plus damp[u] p_n[u]: one thread sums a
+// list of at most BA_PCG_LONG_LIST entries; the block's long lists (a focal pair shared by every
+// image of a camera) are summed first, one wave each, 8 entries per lane in flight, into LDS.
+__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
+    __shared__ double sh[2 * (PCG_T / 64)];
+    __shared__ double sLong[PCG_T];
     if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
-    const double beta = a.state[ST_BETA];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
     const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
-    double pap = 0.0;
-    if ((int)blockIdx.x < nb) {
-        const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-        if (u < a.n_u) {
-            const int q0 = a.inv_ptr[u], q1 = a.inv_ptr[u + 1];
-            if (q1 - q0 <= BA_PCG_LONG_LIST) {
-                double s = 0.0;
-                for (int q = q0; q < q1; ++q) s += a.y_img[a.inv_src[q]];
-                const double pn = pdir(a.z[u], pold[u], beta);
-                s += a.damp[u] * pn;
-                a.Ap[u] = s;
-                pap = pn * s;
-            }
-        }
-    } else {
-        const int lane = threadIdx.x & 63;
-        const int64_t k = (int64_t)(blockIdx.x - nb) * (PCG_T / 64) + (threadIdx.x >> 6);
-        int64_t u = -1;
-        int q0 = 0, q1 = 0;
-        if (k < a.n_long) {
-            u = a.long_u[k];
-            q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1];
-            if (q1 - q0 <= BA_PCG_LONG_LIST) { u = -1; q1 = q0; }   // not long: the thread pass owns it
-        }
+    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, du = 1.0, dmp = 0.0;
+    int q0 = 0, q1 = 0, li = -1;
+    if (u < a.n_u) {                                   // operands first, then the reductions
+        zu = a.z[u]; pu = pold[u]; xu = a.x[u]; ru = a.r[u]; du = a.diagA[u]; dmp = a.damp[u];
+        q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1]; li = a.long_idx[u];
+    }
+    const int lk0 = a.long_ptr[blockIdx.x], lk1 = a.long_ptr[blockIdx.x + 1];
+    for (int k = lk0 + w; k < lk1; k += PCG_T / 64) {
+        const int v = a.long_u[k];
+        const int b0 = a.inv_ptr[v], b1 = a.inv_ptr[v + 1];
         double s = 0.0;
-        for (int q = q0 + lane; q < q1; q += 64 * 8) {
+        for (int q = b0 + lane; q < b1; q += 64 * 8) {
             int src[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) src[t] = q + 64 * t < q1 ? a.inv_src[q + 64 * t] : -1;
+            for (int t = 0; t < 8; ++t) src[t] = q + 64 * t < b1 ? a.inv_src[q + 64 * t] : -1;
 #pragma unroll
             for (int t = 0; t < 8; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
         }
         s = wave_sum(s);
-        if (lane == 0 && u >= 0) {
-            const double pn = pdir(a.z[u], pold[u], beta);
-            s += a.damp[u] * pn;
-            a.Ap[u] = s;
-            pap = pn * s;
-        }
+        if (lane == 0) sLong[k - lk0] = s;
     }
-    const double t = block_sum<PCG_T>(pap, sh);
-    if (threadIdx.x == 0) a.partials[3 * blockIdx.x + 2] = t;
-}
-
-// alpha = rz / max(p.Ap, 1e-32); x += alpha p; r -= alpha Ap; z = M^-1 r (ba_solver.py:1217-1228);
-// p_n stored in slot n & 1; partials r.r, r.z
-__global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int ngb, int n) {
-    __shared__ double sh[PCG_T / 64];
-    if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
-    const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, apu = 0.0, du = 1.0;
-    if (u < a.n_u) {                                   // operands first, then the reduction
-        zu = a.z[u]; pu = a.p[(int64_t)((n + 1) & 1) * a.n_u + u]; xu = a.x[u]; ru = a.r[u]; apu = a.Ap[u];
-        du = a.diagA[u];
-    }
-    const double pap = sum_partials<PCG_T>(a.partials, ngb, 2, sh);
+    // the short lists: y_img is complete at launch, so these sums need nothing from the reductions
+    double ys = 0.0;
+    if (li < 0)
+        for (int q = q0; q < q1; ++q) ys += a.y_img[a.inv_src[q]];
+    const double beta = a.state[ST_BETA];
+    double sums[1] = {0.0};
+    for (int b = threadIdx.x; b < a.n_imgs; b += PCG_T) sums[0] += a.img_part[b];
+    block_sums<PCG_T, 1>(sums, sh);                    // p.Ap (its barriers also publish sLong)
+    const double pap = sums[0];
     const double denom = pap > 1e-32 ? pap : 1e-32;
     const double alpha = a.state[ST_RZ0 + (n & 1)] / denom;
-    const double beta = a.state[ST_BETA];
-    double rr = 0.0, rz = 0.0;
+    double t[PCG_NP] = {0.0, 0.0};
     if (u < a.n_u) {
         const double pn = pdir(zu, pu, beta);
+        const double apu = (li >= 0 ? sLong[li] : ys) + dmp * pn;
         a.p[(int64_t)(n & 1) * a.n_u + u] = pn;
         const double x = xu + alpha * pn;
         const double r = ru - alpha * apu;
         const double z = r / du;
         a.x[u] = x; a.r[u] = r; a.z[u] = z;
-        rr = r * r; rz = r * z;
+        t[PT_RR] = r * r; t[PT_RZ] = r * z;
     }
-    const double s0 = block_sum<PCG_T>(rr, sh);
-    const double s1 = block_sum<PCG_T>(rz, sh);
-    if (threadIdx.x == 0) { a.partials[3 * blockIdx.x + 0] = s0; a.partials[3 * blockIdx.x + 1] = s1; }
+    block_sums<PCG_T, PCG_NP>(t, sh);
+    if (threadIdx.x < PCG_NP) a.partials[PCG_NP * blockIdx.x + threadIdx.x] = threadIdx.x == 0 ? t[0] : t[1];
 }
 
 // result: x if converged else the best iterate
@@ -351,11 +387,10 @@ using namespace ba;
 
 static inline unsigned nb_of(int64_t n) { return (unsigned)((n + PCG_T - 1) / PCG_T); }
 
-// partial sums: 3 per block of the widest launch (the gather: one thread per unknown plus one
-// wave per long unknown)
+// partial sums: PCG_NP per block of the update launch (one thread per unknown)
 extern "C" int64_t ba_pcg_partials_size(int64_t n_u) {
     const int64_t m = n_u < 1 ? 1 : n_u;
-    return 3 * ((m + PCG_T - 1) / PCG_T + (m + 3) / 4 + 1) + 3;
+    return PCG_NP * ((m + PCG_T - 1) / PCG_T);
 }
 
 extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
@@ -364,11 +399,12 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     const ba_pcg_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
     BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16 && a.maxiter >= 0, "bad sizes");
-    BA_REQUIRE(a.n_long >= 0 && a.n_long <= a.n_u && (a.n_long == 0 || a.long_u != nullptr), "bad long-list unknowns");
+    BA_REQUIRE(a.n_long >= 0 && a.n_long <= a.n_u && a.long_ptr != nullptr && a.long_idx != nullptr &&
+                   (a.n_long == 0 || a.long_u != nullptr) && a.img_part != nullptr,
+               "bad long-list unknowns or image partials");
     if (a.n_u == 0) return BA_OK;
     const unsigned nb = nb_of(a.n_u);
     const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown (setup)
-    const unsigned ngb = nb + (unsigned)((a.n_long + PCG_T / 64 - 1) / (PCG_T / 64));  // gather blocks
     const int64_t n_ent = a.n_row_ent;
     BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
     const int per = a.d * a.d > 16 ? a.d * a.d : 16;
@@ -382,8 +418,7 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_LAUNCHED();
     for (int it = 0; it < a.maxiter; ++it) {
         hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
-        hipLaunchKernelGGL(k_pcg_gather, dim3(ngb), dim3(PCG_T), 0, st, a, it, (int)nb);
-        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, (int)ngb, it);
+        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, it);
     }
     // the decisions after the last update (no SpMV follows them)
     hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, a.maxiter, (int)nb);

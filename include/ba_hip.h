@@ -155,7 +155,7 @@ typedef struct {
     double dampen; int32_t adaptive;
     int32_t maxiter; double tol;
     /* workspace (fp64 unless noted); p holds 2 * n_u (the search direction, double-buffered) */
-    double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *Ap, *y_img;
+    double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img;
     double *partials;                  /* 3 * n_blocks */
     double *state;                     /* 16 doubles */
     int32_t *istate;                   /* 8 ints: [0], [1] done flags, [2] iterations, [3] converged,
@@ -164,15 +164,19 @@ typedef struct {
     int64_t n_row_ent;                 /* row_ptr[n_imgs] */
     int32_t *row_u;                    /* (n_row_ent, 16) workspace: the unknowns each image-row block multiplies */
     const int32_t *long_u;             /* the unknowns whose inv list has more than BA_PCG_LONG_LIST entries,
-                                          every one of them (e.g. a focal pair shared by many images) */
+                                          every one of them, ascending (e.g. a focal pair shared by many images) */
     int64_t n_long;
+    const int32_t *long_ptr;           /* (ceil(n_u / 256) + 1): long_u[long_ptr[b] .. long_ptr[b + 1]) lie in
+                                          [256 b, 256 b + 256) */
+    const int32_t *long_idx;           /* (n_u): k - long_ptr[u / 256] for u = long_u[k], else -1 */
+    double *img_part;                  /* (n_imgs) workspace: per image row partial of p.Ap */
 } ba_pcg_args;
 
 #define BA_PCG_LONG_LIST 32
 
 /* Builds the unknown-level rhs, diag(A) with per-leaf damping (ba_solver.py:575-582,
  * :1188-1191) and runs Jacobi-PCG (ba_solver.py:184-206, :1197-1238) on
- * S = P^T S_img P + damping, entirely on the device (three launches per iteration, no host
+ * S = P^T S_img P + damping, entirely on the device (two launches per iteration, no host
  * synchronisation).  The result (the converged iterate, else the best one) is left in x;
  * istate holds the loop's outcome. */
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);

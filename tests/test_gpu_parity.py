@@ -213,12 +213,14 @@ def _device_pcg_dense(A, b, tol, maxiter, d):
                 pair_i1=t([q[0] for q in pairs], i32), pair_i2=t([q[1] for q in pairs], i32),
                 S_pairs=t(S_pairs, f64), e_img=t(b, f64), dg_img=t(np.diag(A), f64))
     n_ent = int(row_ptr[-1])
-    for name, size in dict(rhs=n, diagA=n, damp=n, x=n, xbest=n, r=n, z=n, p=2 * n, Ap=n, y_img=n,
+    for name, size in dict(rhs=n, diagA=n, damp=n, x=n, xbest=n, r=n, z=n, p=2 * n, y_img=n, img_part=m,
                            partials=int(lib().ba_pcg_partials_size(n)), state=16, S_rows=n_ent * d * d).items():
         keep[name] = torch.zeros(size, dtype=f64, device=DEV)
     keep['istate'] = torch.zeros(8, dtype=i32, device=DEV)
     keep['row_u'] = torch.zeros(n_ent * 16, dtype=i32, device=DEV)
     keep['long_u'] = torch.zeros(1, dtype=i32, device=DEV)
+    keep['long_ptr'] = torch.zeros((n + 255) // 256 + 1, dtype=i32, device=DEV)
+    keep['long_idx'] = torch.full((n,), -1, dtype=i32, device=DEV)
     pa = BaPcgArgs()
     pa.n_u, pa.n_imgs, pa.d = n, m, d
     pa.dampen, pa.adaptive, pa.maxiter, pa.tol = 0.0, 0, int(maxiter), float(tol)
