@@ -81,6 +81,22 @@ class BaSampleArgs(ctypes.Structure):
                 ('cum_nppi', c_p), ('n_imgs', c_i64), ('pix2d', c_p), ('n_obs', c_i64), ('out', c_p)]
 
 
+class BaObsSet(ctypes.Structure):
+    _fields_ = [('pids', c_p), ('pix2d', c_p), ('pix2d_std', c_p), ('pix2d_dep', c_p), ('nppi', c_p), ('n_imgs', c_i64)]
+
+
+class BaGatherArgs(ctypes.Structure):
+    _fields_ = [('a', BaObsSet), ('b', BaObsSet), ('sel_a', c_p), ('sel_b', c_p), ('pid_shift_b', c_int), ('C', c_int),
+                ('n_out', c_i64), ('n_rows', c_i64), ('pids', c_p), ('pix2d', c_p), ('pix2d_std', c_p),
+                ('pix2d_dep', c_p), ('nppi', c_p), ('total', c_p), ('workspace', c_p)]
+
+
+class BaRemoveArgs(ctypes.Structure):
+    _fields_ = [('in_', BaObsSet), ('n_rows', c_i64), ('n_tracks', c_i64), ('C', c_int), ('bad_int64', c_int),
+                ('bad', c_p), ('n_bad', c_i64), ('pids', c_p), ('pix2d', c_p), ('pix2d_std', c_p), ('pix2d_dep', c_p),
+                ('nppi', c_p), ('old_to_keep', c_p), ('counts', c_p), ('workspace', c_p)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     'ba_last_error': (ctypes.c_char_p, []),
@@ -109,6 +125,11 @@ _SIGS = {
     'ba_objective_workspace_bytes': (c_i64, [c_i64]),
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
     'ba_sample_depth': (c_int, [ctypes.POINTER(BaSampleArgs), c_p]),
+    'ba_tracks_gather': (c_int, [ctypes.POINTER(BaGatherArgs), c_p]),
+    'ba_tracks_remove': (c_int, [ctypes.POINTER(BaRemoveArgs), c_p]),
+    'ba_tracks_to_dense': (c_int, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p]),
+    'ba_tracks_img_id': (c_int, [c_p, c_i64, c_i64, c_p, c_p, c_p]),
+    'ba_tracks_workspace_bytes': (c_i64, [c_i64, c_i64, c_i64]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -2,13 +2,20 @@
 
 Follows src/blast3r/inference/rigs.py:15-94 (camera / node / image ids, K,
 P_rig2cam, P_w2rig, z_coefs, the ``infos`` CSR at :50-51, z-coefficient
-initialisation at :69-94) and src/blast3r/inference/tracks.py:19-57
-(image-major observations).  Pose initialisation, matching and retrieval are
-not part of the BA path and are not included.
+initialisation at :69-94) and src/blast3r/inference/tracks.py:19-127
+(image-major observations and the structure edits of the online pipeline:
+``old | new``, ``tracks[idx]``, ``remove``, ``to_dense``, ``img_id``).  The edits
+that build a new observation set run in libba_hip.so (``ba_tracks_*``) on the
+tensors' device; CPU-resident sets support the views (``tracks[i]``) and ``to``
+only.  Pose initialisation, matching and retrieval are not part of the BA path
+and are not included.
 """
+import ctypes
 from dataclasses import dataclass
 
 import torch
+
+from ._lib import BaGatherArgs, BaObsSet, BaRemoveArgs, check, lib, ptr, stream_ptr
 
 
 def _to(x, device):
@@ -78,6 +85,27 @@ class RigsData:
         return self.z_coefs
 
 
+def _need_device(*ts):
+    dev = ts[0].device
+    if dev.type != 'cuda' or any(t.device != dev for t in ts):
+        raise RuntimeError('this ObservedTracks operation runs in libba_hip.so: move the tracks to the GPU first')
+    return dev
+
+
+def _obs_set(t):
+    """ba_obs_set of an ObservedTracks (int32 pids / nppi, contiguous fp32 rows) + the tensors it points into."""
+    pids = t.pids.to(torch.int32).contiguous()
+    nppi = t.nppi.to(device=pids.device, dtype=torch.int32).contiguous()
+    pix, std, dep = (x.to(torch.float32).contiguous() for x in (t.pix2d, t.pix2d_std, t.pix2d_dep))
+    keep = (pids, nppi, pix, std, dep)
+    return BaObsSet(ptr(pids), ptr(pix), ptr(std), ptr(dep), ptr(nppi), int(len(nppi))), keep
+
+
+def _workspace(dev, n_rows, n_tracks, n_imgs):
+    n = int(lib().ba_tracks_workspace_bytes(int(n_rows), int(n_tracks), int(n_imgs)))
+    return torch.empty(n, dtype=torch.uint8, device=dev)
+
+
 @dataclass
 class ObservedTracks:
     n_imgs: int
@@ -88,11 +116,15 @@ class ObservedTracks:
     pix2d_std: torch.Tensor   # (n_kpts, 2)
     pix2d_dep: torch.Tensor   # (n_kpts, n_zcf)
     depth_mode: str
+    img_slices: list = None   # rows of each image, from nppi (tracks.py:31, :51-54)
 
     def __post_init__(self):
         assert self.n_imgs == len(self.nppi)
         assert len(self.pids) == len(self.pix2d) == len(self.pix2d_std) == len(self.pix2d_dep)
-        assert self.n_kpts == int(self.nppi.sum())
+        cum = torch.cumsum(self.nppi.detach().to('cpu', torch.int64), dim=-1).tolist()
+        assert self.n_kpts == (cum[-1] if cum else 0)
+        if self.img_slices is None:
+            self.img_slices = [slice(int(i), int(j)) for i, j in zip([0] + cum[:-1], cum)]
 
     @property
     def n_kpts(self):
@@ -107,6 +139,124 @@ class ObservedTracks:
         if self.device == str(torch.device(device)):
             return self
         return ObservedTracks(**{k: _to(v, device) for k, v in vars(self).items()})
+
+    @property
+    def img_id(self):
+        """tracks.py:45-49: image index of every row (int64); coinciding delimiters (empty images)
+        count once, as in the reference."""
+        dev = _need_device(self.pids, self.nppi)
+        n = self.n_kpts
+        if self.n_imgs > 1 and self.img_slices[-2].stop >= n and n > 0:
+            raise IndexError('img_id: an image delimiter falls past the last row (trailing empty images)')
+        out = torch.empty(n, dtype=torch.int64, device=dev)
+        nppi = self.nppi.to(torch.int32).contiguous()
+        ws = _workspace(dev, n, 0, self.n_imgs)
+        check(lib().ba_tracks_img_id(ptr(nppi), self.n_imgs, n, ptr(out), ptr(ws), stream_ptr(dev)))
+        return out
+
+    def _gather(self, sel_a, other=None, sel_b=None, shift=0, n_rows=None, nppi_dtype=None):
+        dev = _need_device(self.pids, self.nppi, *(() if other is None else (other.pids,)))
+        C = self.pix2d_dep.shape[1]
+        sa, keep_a = _obs_set(self)
+        sb, keep_b = (_obs_set(other) if other is not None else (BaObsSet(), ()))
+        n_out = len(sel_a) if sel_a is not None else len(sel_b)
+        sel_a = None if sel_a is None else sel_a.to(device=dev, dtype=torch.int32).contiguous()
+        sel_b = None if sel_b is None else sel_b.to(device=dev, dtype=torch.int32).contiguous()
+        out = dict(pids=torch.empty(n_rows, dtype=torch.int32, device=dev),
+                   pix2d=torch.empty((n_rows, 2), dtype=torch.float32, device=dev),
+                   pix2d_std=torch.empty((n_rows, 2), dtype=torch.float32, device=dev),
+                   pix2d_dep=torch.empty((n_rows, C), dtype=torch.float32, device=dev))
+        nppi = torch.empty(n_out, dtype=torch.int32, device=dev)
+        total = torch.empty(1, dtype=torch.int64, device=dev)
+        n_img_ws = max(n_out, self.n_imgs, other.n_imgs if other is not None else 0)
+        ws = _workspace(dev, n_rows, 0, n_img_ws)
+        a = BaGatherArgs(a=sa, b=sb, sel_a=ptr(sel_a), sel_b=ptr(sel_b), pid_shift_b=int(shift), C=C, n_out=n_out,
+                         n_rows=n_rows, pids=ptr(out['pids']), pix2d=ptr(out['pix2d']), pix2d_std=ptr(out['pix2d_std']),
+                         pix2d_dep=ptr(out['pix2d_dep']), nppi=ptr(nppi), total=ptr(total), workspace=ptr(ws))
+        check(lib().ba_tracks_gather(ctypes.byref(a), stream_ptr(dev)))
+        if int(total) != n_rows:
+            raise RuntimeError(f'observation gather: expected {n_rows} rows, the selection has {int(total)}')
+        if nppi_dtype is not None:
+            nppi = nppi.to(nppi_dtype)
+        return nppi, out
+
+    def __getitem__(self, idx):
+        """tracks.py:66-79: an int gives a one-image view (no copy); an index tensor gathers images."""
+        if isinstance(idx, int):
+            sl = self.img_slices[idx]
+            return ObservedTracks(1, self.n_tracks, self.nppi[idx:idx + 1], self.pids[sl], self.pix2d[sl],
+                                  self.pix2d_std[sl], self.pix2d_dep[sl], self.depth_mode)
+        if isinstance(idx, torch.Tensor):
+            sel = idx.to('cpu', torch.int64)
+            n_rows = int(sum(self.img_slices[int(i)].stop - self.img_slices[int(i)].start for i in sel))
+            nppi, out = self._gather(sel, n_rows=n_rows, nppi_dtype=self.nppi.dtype)
+            return ObservedTracks(len(sel), self.n_tracks, nppi, depth_mode=self.depth_mode, **out)
+        raise TypeError(f'bad index type {type(idx)}')
+
+    def __ror__(self, left):
+        assert left is None
+        return self
+
+    def __or__(self, trks):
+        """tracks.py:84-102: append the next image's tracks; per image, old rows then new rows (new
+        track ids shifted by the old n_tracks)."""
+        assert self.n_imgs + 1 == trks.n_imgs
+        assert self.depth_mode == trks.depth_mode
+        if self.n_tracks == 0:
+            return trks
+        assert self.pix2d_dep.shape[1] == trks.pix2d_dep.shape[1]
+        dev = self.pids.device
+        sel_a = torch.cat([torch.arange(self.n_imgs, dtype=torch.int32), torch.tensor([-1], dtype=torch.int32)])
+        sel_b = torch.arange(trks.n_imgs, dtype=torch.int32)
+        nppi, out = self._gather(sel_a.to(dev), other=trks, sel_b=sel_b.to(dev), shift=self.n_tracks,
+                                 n_rows=self.n_kpts + trks.n_kpts, nppi_dtype=trks.nppi.dtype)
+        return ObservedTracks(trks.n_imgs, self.n_tracks + trks.n_tracks, nppi, depth_mode=self.depth_mode, **out)
+
+    def to_dense(self, n_imgs=None):
+        """tracks.py:104-114: (n_tracks, n_imgs, 2) view, NaN where a track is not observed."""
+        if n_imgs is None:
+            n_imgs = self.n_imgs
+        else:
+            assert n_imgs >= self.n_imgs
+        dev = _need_device(self.pids, self.nppi, self.pix2d)
+        res = torch.empty((n_imgs, self.n_tracks, 2), dtype=torch.float32, device=dev)
+        pids = self.pids.to(torch.int32).contiguous()
+        pix = self.pix2d.to(torch.float32).contiguous()
+        nppi = self.nppi.to(torch.int32).contiguous()
+        ws = _workspace(dev, self.n_kpts, 0, self.n_imgs)
+        check(lib().ba_tracks_to_dense(ptr(pids), ptr(pix), ptr(nppi), self.n_imgs, self.n_kpts, self.n_tracks, n_imgs,
+                                       ptr(res), ptr(ws), stream_ptr(dev)))
+        return res.transpose(0, 1)
+
+    def remove(self, bad_track_idxs):
+        """tracks.py:116-127: drop the rows of the listed tracks, renumber the remaining tracks by
+        rank; returns (tracks, old_to_keep)."""
+        if len(bad_track_idxs) == 0:
+            return self, torch.zeros((0,), dtype=self.pids.dtype, device=self.pids.device)
+        dev = _need_device(self.pids, self.nppi)
+        bad = torch.as_tensor(bad_track_idxs, device=dev)
+        if bad.dtype not in (torch.int32, torch.int64):
+            bad = bad.to(torch.int64)
+        bad = bad.contiguous().view(-1)
+        s, keep = _obs_set(self)
+        n, T, C = self.n_kpts, self.n_tracks, self.pix2d_dep.shape[1]
+        out = dict(pids=torch.empty(n, dtype=torch.int32, device=dev),
+                   pix2d=torch.empty((n, 2), dtype=torch.float32, device=dev),
+                   pix2d_std=torch.empty((n, 2), dtype=torch.float32, device=dev),
+                   pix2d_dep=torch.empty((n, C), dtype=torch.float32, device=dev))
+        nppi = torch.empty(self.n_imgs, dtype=torch.int32, device=dev)
+        old_to_keep = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
+        counts = torch.empty(2, dtype=torch.int64, device=dev)
+        ws = _workspace(dev, n, T, self.n_imgs)
+        a = BaRemoveArgs(in_=s, n_rows=n, n_tracks=T, C=C, bad_int64=int(bad.dtype == torch.int64), bad=ptr(bad),
+                         n_bad=len(bad), pids=ptr(out['pids']), pix2d=ptr(out['pix2d']), pix2d_std=ptr(out['pix2d_std']),
+                         pix2d_dep=ptr(out['pix2d_dep']), nppi=ptr(nppi), old_to_keep=ptr(old_to_keep),
+                         counts=ptr(counts), workspace=ptr(ws))
+        check(lib().ba_tracks_remove(ctypes.byref(a), stream_ptr(dev)))
+        n_keep, n_rows = (int(v) for v in counts.cpu())
+        out = {k: v[:n_rows] for k, v in out.items()}
+        res = ObservedTracks(self.n_imgs, n_keep, nppi, depth_mode=self.depth_mode, **out)
+        return res, old_to_keep[:n_keep].to(self.pids.dtype)
 
 
 def from_problem(prob):

@@ -105,6 +105,25 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
             optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True, verbose_steps=False,
             **ba_options):
     """Levenberg-Marquardt step (en:206-334) on MI355X.  Returns (update, BA_Status)."""
+    update, status, _ = _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d,
+                                 depth_mode=depth_mode, pnorm=pnorm, clip_pix_err=clip_pix_err,
+                                 huber_delta=huber_delta, min_reproj=min_reproj, dampen=dampen,
+                                 min_loss_delta=min_loss_delta, weight_z=weight_z, log_depth_maps=log_depth_maps,
+                                 conf=conf, pts3d_ref=pts3d_ref, weight_tan=weight_tan, tan_stride=tan_stride,
+                                 normalize_tangents=normalize_tangents, optim_K=optim_K, optim_Z=optim_Z,
+                                 optim_P=optim_P, optim_X=optim_X, optim_Z0=optim_Z0, **ba_options)
+    return update, status
+
+
+def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d,
+             depth_mode='log', pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12,
+             min_loss_delta=1e-4, weight_z=1, log_depth_maps=None, conf=None, pts3d_ref=None, weight_tan=0.0,
+             tan_stride=4, normalize_tangents=True, optim_K=True, optim_Z=True, optim_P=True, optim_X=True,
+             optim_Z0=True, init_eval=None, **ba_options):
+    """lm_step, plus the objective of the last evaluated trial (loss before min_loss_delta, residuals,
+    w_pts) as a third result.  init_eval, when given, is that triple for (K, P_w2rig, z_coefs, pts3d)
+    under the same hyper-parameters: the evaluation at the start of the step (en:281) is then taken
+    from it instead of being recomputed (same inputs, same kernels, so the same values)."""
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
     if weight_tan > 0:
@@ -141,7 +160,10 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
         loss, reproj = _objective(buf, n_obs, has_err=pnorm > 0)
         return loss, residuals_, w_pts_, reproj
 
-    init_loss, init_residuals, w_pts, _ = objective(K, P_w2rig, pts3d, z_coefs)
+    if init_eval is not None:
+        init_loss, init_residuals, w_pts = init_eval
+    else:
+        init_loss, init_residuals, w_pts, _ = objective(K, P_w2rig, pts3d, z_coefs)
 
     hp = dict(weight_z=weight_z, pnorm=pnorm, max_pix_err=clip_pix_err, huber_delta=huber_delta, w_pts_null=w_null)
     jac = GaussNewtonSolver(n_cams, n_nodes, n_imgs, n_tracks, pts3d.device, dampen=dampen, **ba_options)
@@ -169,7 +191,8 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
                                     ptr(dXc), float(scale), 100.0, n_cams, n_nodes, n_imgs, n_zcf, n_tracks,
                                     ptr(Kn), ptr(Pn), ptr(Zn), ptr(Xn), stream_ptr(dev)))
         update['K'], update['P_w2rig'], update['z_coefs'], update['pts3d'] = Kn, Pn, Zn, Xn
-        new_loss, new_residuals, _, new_reproj_t = objective(**update)
+        new_loss, new_residuals, new_w, new_reproj_t = objective(**update)
+        last_eval = (new_loss, new_residuals, new_w)
         vals = torch.stack([new_loss, init_loss, new_reproj_t]).cpu()
         if torch.isnan(vals[0]):
             print('Warning: loss is NaN')
@@ -185,7 +208,7 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
         last_a = a
     else:
         print('Warning: loss is not decreasing')
-    return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals)
+    return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals), last_eval
 
 
 def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
@@ -241,14 +264,17 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
         if verbose:
             print(f"Starting phase {phase_num}, with {variables['z_coefs'].shape[1]} z-coefs.")
         it = 0
+        carry = None          # objective at `variables`, from the trial that produced them
+        infos = rig.infos(trk)
         while it < max_iters:
-            update, status = lm_step(rig.infos(trk), trk.pids, trk.pix2d, trk.pix2d_std, trk.pix2d_dep, **variables,
-                                     weight_tan=tangent_reg, tan_stride=tan_stride,
-                                     normalize_tangents=normalize_tangents,
-                                     optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P, optim_X=optim_X,
-                                     optim_Z0=optim_Z0, pnorm=pnorm, weight_z=weight_z, no_grad_f_from_rz=no_Jfz,
-                                     depth_mode=rig.depth_mode, dampen=1e-12, adaptive_dampen=True,
-                                     dtype=torch.float64, **other_lm_kwargs)
+            update, status, last_eval = _lm_step(infos, trk.pids, trk.pix2d, trk.pix2d_std, trk.pix2d_dep,
+                                                 **variables, weight_tan=tangent_reg, tan_stride=tan_stride,
+                                                 normalize_tangents=normalize_tangents,
+                                                 optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P,
+                                                 optim_X=optim_X, optim_Z0=optim_Z0, pnorm=pnorm,
+                                                 weight_z=weight_z, no_grad_f_from_rz=no_Jfz,
+                                                 depth_mode=rig.depth_mode, dampen=1e-12, adaptive_dampen=True,
+                                                 dtype=torch.float64, init_eval=carry, **other_lm_kwargs)
             if verbose:
                 reproj_before = float(reproj_score(status.init_residuals))
                 reproj_after = float(reproj_score(status.new_residuals))
@@ -258,6 +284,10 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
             if status.new_loss >= status.init_loss:
                 break
             variables.update(update)
+            # the next step starts where this trial ended: reuse its objective (en:281 would recompute
+            # it from the same parameters).  The tangent prior term depends on the step's K, so with
+            # the prior on the start-of-step objective is evaluated afresh.
+            carry = last_eval if not tangent_reg > 0 else None
             it += 1
     trk.pix2d_dep = original_pix2d_dep
     pts3d = variables.pop('pts3d')

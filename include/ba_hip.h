@@ -231,6 +231,85 @@ typedef struct {
 
 int ba_sample_depth(const ba_sample_args* args, void* stream);
 
+/* ------------------------------------------------------------------ observation structure (layout builder) */
+
+/* One image-major observation set (ObservedTracks, src/blast3r/inference/tracks.py:19-57):
+ * rows of image i follow those of image i - 1; nppi[i] rows per image. */
+typedef struct {
+    const int32_t* pids;       /* (n_rows,) track ids */
+    const float* pix2d;        /* (n_rows, 2) */
+    const float* pix2d_std;    /* (n_rows, 2) */
+    const float* pix2d_dep;    /* (n_rows, C) */
+    const int32_t* nppi;       /* (n_imgs,) rows per image */
+    int64_t n_imgs;
+} ba_obs_set;
+
+/* Image-wise gather.  Output image j holds the rows of image sel_a[j] of set a, then the rows of
+ * image sel_b[j] of set b with pid_shift_b added to their track ids (-1 or an index past the set's
+ * images selects nothing).  Replaces `old | new` (tracks.py:84-102: sel_a[j] = j for the old images,
+ * -1 for the new last one, sel_b[j] = j, shift = old n_tracks) and `tracks[idx]` for an index tensor
+ * (tracks.py:66-74: sel_a = idx, sel_b = null).  Output buffers hold n_rows rows, the total the
+ * caller expects; *total (device, may be null) receives the total the selection really has, and
+ * rows past n_rows are not written. */
+typedef struct {
+    ba_obs_set a, b;
+    const int32_t* sel_a;      /* (n_out,) or null */
+    const int32_t* sel_b;      /* (n_out,) or null (then set b is not read) */
+    int32_t pid_shift_b;
+    int32_t C;                 /* depth channels of both sets */
+    int64_t n_out;             /* output images */
+    int64_t n_rows;
+    int32_t* pids;             /* outputs: (n_rows,), (n_rows, 2), (n_rows, 2), (n_rows, C), (n_out,) */
+    float* pix2d;
+    float* pix2d_std;
+    float* pix2d_dep;
+    int32_t* nppi;
+    int64_t* total;
+    void* workspace;           /* ba_tracks_workspace_bytes(n_rows, 0, max(n_out, images of a and b)) */
+} ba_gather_args;
+
+int ba_tracks_gather(const ba_gather_args* args, void* stream);
+
+/* Track removal (ObservedTracks.remove, tracks.py:116-127): rows whose track id is listed in bad
+ * (int32 or int64 ids, any order, repeats allowed; ids matching no row are ignored, as torch.isin)
+ * are dropped; the remaining rows keep their order, nppi counts them per image, and each kept
+ * track is renumbered by its rank among the tracks that still have a row (torch.unique's sorted
+ * values and inverse).  old_to_keep[k] = old id of new track k.  counts (device) = {tracks kept,
+ * rows kept}; the outputs are sized for the input (every row / track kept). */
+typedef struct {
+    ba_obs_set in;
+    int64_t n_rows;            /* rows of the input set */
+    int64_t n_tracks;
+    int32_t C;
+    int32_t bad_int64;         /* bad holds int64 ids (else int32) */
+    const void* bad;
+    int64_t n_bad;
+    int32_t* pids;             /* outputs: (n_rows,), (n_rows, 2), (n_rows, 2), (n_rows, C), (n_imgs,), (n_tracks,), (2,) */
+    float* pix2d;
+    float* pix2d_std;
+    float* pix2d_dep;
+    int32_t* nppi;
+    int32_t* old_to_keep;
+    int64_t* counts;
+    void* workspace;           /* ba_tracks_workspace_bytes(n_rows, n_tracks, n_imgs) */
+} ba_remove_args;
+
+int ba_tracks_remove(const ba_remove_args* args, void* stream);
+
+/* ObservedTracks.to_dense(n_imgs_out) (tracks.py:104-114): out (n_imgs_out, n_tracks, 2) fp32 is
+ * NaN except out[i, pids[o]] = pix2d[o] for the rows o of image i (the caller views it transposed). */
+int ba_tracks_to_dense(const int32_t* pids, const float* pix2d, const int32_t* nppi, int64_t n_imgs, int64_t n_rows,
+                       int64_t n_tracks, int64_t n_imgs_out, float* out, void* workspace, void* stream);
+
+/* ObservedTracks.img_id (tracks.py:45-49): out[o] = number of distinct delimiters cumsum(nppi)[:-1]
+ * at or before row o (int64).  Delimiters that coincide (empty images) count once, as in the
+ * reference's assignment res[delims] = 1; the caller rejects a delimiter equal to n_rows, which the
+ * reference's indexing rejects. */
+int ba_tracks_img_id(const int32_t* nppi, int64_t n_imgs, int64_t n_rows, int64_t* out, void* workspace, void* stream);
+
+/* Workspace of the four calls above (bytes). */
+int64_t ba_tracks_workspace_bytes(int64_t n_rows, int64_t n_tracks, int64_t n_imgs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,9 +5,10 @@ on CPU with the oracle kernels and solver: objective = mean Huber error
 (en:263-278), linearisation + Schur solve (en:284-303), update of K, P, z, X
 (en:310-313, en:347-354, cujac/__init__.py:56-58) and the step-halving line
 search over a in [0.5, 0.25, 0.125, 1/64, 1/512, 1/4096, 0] with the
-min_loss_delta and reproj_score tests (en:308-333, en:357-361).  The tangent
-prior (en:15-179) is dormant in the reference (tangent_reg = 0.0, en:418) and is
-not restated.
+min_loss_delta and reproj_score tests (en:308-333, en:357-361).
+``bundle_adjustment`` restates the phase loop of en:405-503 (per-phase options,
+z-coefficient add/remove, stop on no decrease).  The tangent prior (en:15-179)
+is restated separately in ``oracle.tangent``.
 """
 from collections import namedtuple
 
@@ -116,3 +117,65 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_co
     info['trials'] = trials
     info['scale'] = scale
     return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals), info
+
+
+def iter_on(*iterators):
+    """en:364-383: per-phase values; scalars repeat, lists give one value per phase."""
+    iterable = lambda it: isinstance(it, (tuple, list))
+    n = max([len(it) for it in iterators if iterable(it)] + [1])
+    its = []
+    for it in iterators:
+        if iterable(it):
+            assert len(it) in (1, n)
+            its.append(it[0] if len(it) == 1 else it)
+        else:
+            its.append(it)
+    for k in range(n):
+        yield tuple(it[k] if iterable(it) else it for it in its)
+
+
+def bundle_adjustment(rigs_data, track_data, pts3d, z_coefs=None, max_iters=1000, pnorm=0.5, optim_P=True,
+                      optim_Z=True, optim_Z0=True, optim_K=True, optim_X=True, weight_z=0.1, n_zcfs=None,
+                      no_Jfz=False, max_n_phases=-1, **lm_kwargs):
+    """en:405-503 on CPU with the oracle lm_step (no tangent prior).
+
+    rigs_data needs K, P_rig2cam, P_w2rig, z_coefs, depth_mode, infos(tracks), z_coefs_from_scale(tracks);
+    track_data needs pids, pix2d, pix2d_std, pix2d_dep.  Returns (dict of the optimised K, P_w2rig,
+    z_coefs, pts3d, number of accepted steps per phase)."""
+    trk, rig = track_data, rigs_data
+    if z_coefs is None:
+        z_coefs = rig.z_coefs_from_scale(trk)
+    dep0 = trk.pix2d_dep
+    var = dict(K=rig.K, P_w2rig=rig.P_w2rig, z_coefs=z_coefs, pts3d=pts3d)
+    steps = []
+    phase = 0
+    dep = dep0             # the reference narrows track_data.pix2d_dep in place; it persists across phases
+    for pnorm, max_iters, optim_K, optim_P, optim_Z, optim_X, weight_z, n_zcfs in \
+            iter_on(pnorm, max_iters, optim_K, optim_P, optim_Z, optim_X, weight_z, n_zcfs):
+        phase += 1
+        if phase > (max_n_phases % 1000):                                       # en:447
+            break
+        if n_zcfs is not None:                                                  # en:451-471
+            optim_Z0 = True
+            if rig.depth_mode[:3] == 'log':
+                optim_Z0 = (n_zcfs == 2) or (n_zcfs == dep0.shape[1])
+                n_zcfs += not optim_Z0
+            dep = dep0[:, :n_zcfs].contiguous()
+            zc = var['z_coefs']
+            if n_zcfs < zc.shape[1]:
+                var['z_coefs'] = zc[:, :n_zcfs].contiguous()
+            elif n_zcfs > zc.shape[1]:
+                var['z_coefs'] = torch.cat((zc, zc.new_zeros((len(zc), n_zcfs - zc.shape[1]))), dim=1).contiguous()
+        infos = rig.infos(trk)
+        k = 0
+        while k < max_iters:                                                    # en:476-497
+            up, st, _ = lm_step(infos, trk.pids, trk.pix2d, trk.pix2d_std, dep, var['K'], rig.P_rig2cam,
+                                var['P_w2rig'], var['z_coefs'], var['pts3d'], depth_mode=rig.depth_mode,
+                                pnorm=pnorm, weight_z=weight_z, optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P,
+                                optim_X=optim_X, optim_Z0=optim_Z0, no_grad_f_from_rz=no_Jfz, **lm_kwargs)
+            if st.new_loss >= st.init_loss:
+                break
+            var.update(up)
+            k += 1
+        steps.append(k)
+    return var, steps

@@ -349,6 +349,65 @@ def test_lm_step_parity(cfg, nf, nt):
         assert rel_err(got, ref) <= max(1e-4, 4 * spread), (k, rel_err(got, ref), spread)
 
 
+def _ba_inputs(p, dev):
+    from blast3r_amd.data import from_problem
+    rig, trk, X = from_problem(p)
+    return rig.to(dev), trk.to(dev), X.to(dev)
+
+
+def test_bundle_adjustment_reuses_trial_objective_exactly():
+    """bundle_adjustment starts each step from the objective its accepted trial already evaluated
+    (instead of evaluating it again, en:281); the parameters it returns equal, bit for bit, those of
+    a chain of lm_step calls that each evaluate their own start."""
+    p = make_problem(0, n_frames=8, n_tracks=200)
+    o = p.options
+    rig, trk, X = _ba_inputs(p, DEV)
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'])
+    rig_out, X_out = gpu_engine.bundle_adjustment(rig, trk, X, z_coefs=p.z_coefs.to(DEV), max_iters=4, pnorm=1.0,
+                                                  verbose=False, **kw)
+    var = dict(K=rig.K, P_rig2cam=rig.P_rig2cam, P_w2rig=rig.P_w2rig, z_coefs=p.z_coefs.to(DEV), pts3d=X)
+    infos = rig.infos(trk)
+    n_acc = 0
+    for _ in range(4):
+        up, st = gpu_engine.lm_step(infos, trk.pids, trk.pix2d, trk.pix2d_std, trk.pix2d_dep, **var, pnorm=1.0,
+                                    depth_mode='log', dampen=1e-12, adaptive_dampen=True, dtype=torch.float64, **kw)
+        if st.new_loss >= st.init_loss:
+            break
+        var.update(up)
+        n_acc += 1
+    assert n_acc >= 2
+    for k, got in (('K', rig_out.K), ('P_w2rig', rig_out.P_w2rig), ('z_coefs', rig_out.z_coefs), ('pts3d', X_out)):
+        assert torch.equal(got, var[k]), k
+
+
+def test_bundle_adjustment_parity():
+    """Two phases (pnorm 1 then 0.5; n_zcfs 3 -> first coefficient frozen, 4 columns) against the
+    oracle's bundle_adjustment.  As for lm_step, the reference's PCG tolerance fixes each step only
+    up to a spread, measured here between the oracle at tol 1e-6 and at 1e-10: the GPU parameters
+    must agree with the oracle's to max(1e-4, 4 * spread) relative."""
+    from blast3r_amd.data import from_problem
+    p = make_problem(0, n_frames=8, n_tracks=300)
+    o = p.options
+    kw = dict(max_iters=[2, 2], pnorm=[1.0, 0.5], n_zcfs=[3, None], weight_z=o['weight_z'],
+              huber_delta=o['huber_delta'])
+    rig_c, trk_c, X_c = from_problem(p)
+    var_r, steps_r = oeng.bundle_adjustment(rig_c, trk_c, X_c, z_coefs=p.z_coefs.clone(), **kw)
+    var_t, _ = oeng.bundle_adjustment(rig_c, trk_c, X_c, z_coefs=p.z_coefs.clone(), pcg_tol=1e-10,
+                                      pcg_maxiter=5000, **kw)
+    rig, trk, X = _ba_inputs(p, DEV)
+    rig_out, X_out = gpu_engine.bundle_adjustment(rig, trk, X, z_coefs=p.z_coefs.to(DEV), verbose=False, **kw)
+    assert torch.equal(trk.pix2d_dep, p.pix2d_dep.to(DEV))            # restored after the phases
+    got = dict(K=rig_out.K, P_w2rig=rig_out.P_w2rig, z_coefs=rig_out.z_coefs, pts3d=X_out)
+    assert got['z_coefs'].shape == var_r['z_coefs'].shape == (p.z_coefs.shape[0], 4)
+    assert torch.equal(got['z_coefs'][:, 0].cpu(), p.z_coefs[:, 0])
+    x0 = dict(K=p.K, P_w2rig=p.P_w2rig, z_coefs=p.z_coefs[:, :4], pts3d=p.pts3d)
+    for k in ('K', 'P_w2rig', 'z_coefs', 'pts3d'):
+        ref, tight = var_r[k] - x0[k], var_t[k] - x0[k]
+        spread = rel_err(ref, tight) if ref.norm() > 0 else 0.0
+        err = rel_err(got[k].cpu() - x0[k], ref) if ref.norm() > 0 else float((got[k].cpu() - x0[k]).abs().max())
+        assert err <= max(1e-4, 4 * spread), (k, err, spread, steps_r)
+
+
 def test_objective_reproj_exact():
     p = make_problem(0, n_frames=12, n_tracks=1000)
     g = _gpu(p)

@@ -267,6 +267,30 @@ def test_oracle_lm_step_decreases_loss_and_follows_schedule():
     assert info['scale'] in [1.0, 0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0.0]
 
 
+
+def test_oracle_bundle_adjustment_phases():
+    """en:405-503: a phase with n_zcfs=3 in log mode keeps the first coefficient frozen
+    (optim_Z0 = False, n_zcfs + 1 = 4 columns, en:455-458) and the loss falls across accepted steps;
+    a second phase (n_zcfs=None) keeps the narrowed depth channels and z-coefficients."""
+    from blast3r_amd.data import from_problem
+    p = tiny_problem(0, n_frames=6, n_tracks=80)
+    o = p.options
+    rig, trk, X = from_problem(p)
+    z0 = p.z_coefs.clone()
+    var, steps = oe.bundle_adjustment(rig, trk, X, z_coefs=z0, max_iters=[2, 1], pnorm=[1.0, 0.5], n_zcfs=[3, None],
+                                      weight_z=o['weight_z'], huber_delta=o['huber_delta'])
+    assert var['z_coefs'].shape == (p.z_coefs.shape[0], 4)
+    assert steps[0] >= 1 and len(steps) == 2
+    assert torch.equal(var['z_coefs'][:, 0], p.z_coefs[:, 0])              # frozen column, exactly
+    assert torch.equal(trk.pix2d_dep, p.pix2d_dep)                         # input not modified
+    l0, _, _ = oe.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs[:, :4].contiguous(), X, p.pids, p.pix2d,
+                            p.pix2d_std, p.pix2d_dep[:, :4].contiguous(), True, o['weight_z'], 1.0, 100,
+                            o['huber_delta'])
+    l1, _, _ = oe.objective(p.infos, var['K'], p.P_rig2cam, var['P_w2rig'], var['z_coefs'], var['pts3d'], p.pids,
+                            p.pix2d, p.pix2d_std, p.pix2d_dep[:, :4].contiguous(), True, o['weight_z'], 1.0, 100,
+                            o['huber_delta'])
+    assert float(l1) < float(l0)
+
 # ----------------------------------------------------------------------------- the C ABI library
 def _header_functions():
     import re

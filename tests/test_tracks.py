@@ -1,0 +1,174 @@
+"""ObservedTracks structure edits (tracks.py:19-127): oracle pins on the CPU, then the device
+operations of blast3r_amd.data against the oracle, bit-exact (integer and copied fp32 data)."""
+import pytest
+import torch
+
+import oracle.tracks as otr
+from blast3r_amd.data import ObservedTracks
+
+DEV = 'cuda'
+
+
+def _random_set(seed, n_imgs, n_tracks, C=5, empty=(), max_per_img=40):
+    """Image-major set; a track is seen at most once per image (as a real track)."""
+    g = torch.Generator().manual_seed(seed)
+    nppi, pids = [], []
+    for i in range(n_imgs):
+        m = 0 if i in empty else int(torch.randint(1, min(max_per_img, n_tracks) + 1, (1,), generator=g))
+        pids.append(torch.randperm(n_tracks, generator=g)[:m].to(torch.int32))
+        nppi.append(m)
+    pids = torch.cat(pids) if pids else torch.zeros(0, dtype=torch.int32)
+    n = len(pids)
+    return (torch.tensor(nppi, dtype=torch.int32), pids, torch.rand((n, 2), generator=g) * 500,
+            torch.rand((n, 2), generator=g) + 0.5, torch.randn((n, C), generator=g))
+
+
+# ----------------------------------------------------------------------------- oracle pins (CPU)
+def test_oracle_img_id_closed_form_and_empty_images():
+    nppi = torch.tensor([3, 1, 4, 2], dtype=torch.int32)
+    assert torch.equal(otr.img_id(nppi, 10), torch.repeat_interleave(torch.arange(4), nppi.long()))
+    # an empty image: its delimiter coincides with the next one and counts once (known answer)
+    assert otr.img_id(torch.tensor([2, 0, 3], dtype=torch.int32), 5).tolist() == [0, 0, 1, 1, 1]
+
+
+def test_oracle_merge_is_side_by_side_in_dense_form():
+    old = _random_set(1, 5, 30)
+    new = _random_set(2, 6, 20)
+    m = otr.merge(old, 30, new)
+    assert m[0].tolist() == [int(a) + int(b) for a, b in zip(old[0].tolist() + [0], new[0].tolist())]
+    dense = otr.to_dense(m, 50)
+    ref = torch.cat([otr.to_dense(old, 30, n_imgs=6), otr.to_dense(new, 20)], dim=0)
+    assert torch.equal(torch.nan_to_num(dense, nan=-1.0), torch.nan_to_num(ref, nan=-1.0))
+    # rows of image j: the old rows first, then the new ones (pid >= 30)
+    sl = otr.img_slices(m[0])
+    for j in range(6):
+        p = m[1][sl[j]]
+        k = int(old[0][j]) if j < 5 else 0
+        assert bool((p[:k] < 30).all()) and bool((p[k:] >= 30).all())
+
+
+def test_oracle_remove_is_a_column_selection_of_the_dense_form():
+    obs = _random_set(3, 7, 40, empty=(2,))
+    bad = torch.tensor([5, 5, 17, 39, 99])                   # repeats and an id matching no row
+    (nppi, pids, pix, std, dep), keep = otr.remove(obs, bad)
+    present = torch.unique(obs[1])
+    expect = present[~torch.isin(present, bad)]
+    assert torch.equal(keep.long(), expect.long())
+    d0 = otr.to_dense(obs, 40)
+    d1 = otr.to_dense((nppi, pids, pix, std, dep), len(keep))
+    assert torch.equal(torch.nan_to_num(d1, nan=-1.0), torch.nan_to_num(d0[keep.long()], nan=-1.0))
+    assert int(nppi.sum()) == len(pids) and int(nppi[2]) == 0
+
+
+def test_oracle_select_matches_one_image_views():
+    obs = _random_set(4, 6, 25, empty=(1,))
+    idx = torch.tensor([4, 1, 4, 0])
+    s = otr.select(obs, idx)
+    sl = otr.img_slices(obs[0])
+    for k in range(1, 5):
+        assert torch.equal(s[k], torch.cat([obs[k][sl[int(i)]] for i in idx]))
+    assert s[0].tolist() == [int(obs[0][int(i)]) for i in idx]
+
+
+# ----------------------------------------------------------------------------- device vs oracle
+def _dev_tracks(obs, n_tracks):
+    nppi, pids, pix, std, dep = obs
+    return ObservedTracks(len(nppi), n_tracks, nppi.to(DEV), pids.to(DEV), pix.to(DEV), std.to(DEV), dep.to(DEV),
+                          'log_multidepth')
+
+
+def _same(t, obs):
+    for got, ref in zip((t.nppi, t.pids, t.pix2d, t.pix2d_std, t.pix2d_dep), obs):
+        assert got.dtype == ref.dtype and torch.equal(got.cpu(), ref), (got.dtype, ref.dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('seed,n_old,T_old,T_new,empty', [(10, 5, 30, 20, ()), (11, 9, 200, 150, (0, 3)),
+                                                          (12, 1, 8, 8, ())])
+def test_merge_matches_oracle(seed, n_old, T_old, T_new, empty):
+    old = _random_set(seed, n_old, T_old, empty=empty)
+    new = _random_set(seed + 100, n_old + 1, T_new, empty=empty)
+    got = _dev_tracks(old, T_old) | _dev_tracks(new, T_new)
+    assert got.n_imgs == n_old + 1 and got.n_tracks == T_old + T_new
+    _same(got, otr.merge(old, T_old, new))
+    assert (None | got) is got
+
+
+@pytest.mark.gpu
+def test_merge_with_no_old_tracks_returns_new():
+    new = _dev_tracks(_random_set(13, 4, 10), 10)
+    old = _dev_tracks((torch.zeros(3, dtype=torch.int32), torch.zeros(0, dtype=torch.int32), torch.zeros((0, 2)),
+                       torch.zeros((0, 2)), torch.zeros((0, 5))), 0)
+    assert (old | new) is new
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('bad_kind', ['int64', 'int32', 'tuple', 'all_but_one'])
+def test_remove_matches_oracle(bad_kind):
+    obs = _random_set(20, 8, 60, empty=(5,))
+    if bad_kind == 'all_but_one':
+        bad = torch.arange(1, 60)
+    else:
+        bad = torch.tensor([3, 3, 59, 0, 1000, -4])
+    ref, keep_r = otr.remove(obs, bad)
+    arg = {'int64': bad, 'int32': bad.to(torch.int32), 'tuple': tuple(bad.tolist()),
+           'all_but_one': bad.to(DEV)}[bad_kind]
+    t, keep = _dev_tracks(obs, 60).remove(arg)
+    assert t.n_tracks == len(keep_r)
+    assert keep.dtype == keep_r.dtype and torch.equal(keep.cpu(), keep_r)
+    _same(t, ref)
+
+
+@pytest.mark.gpu
+def test_remove_nothing_and_everything():
+    obs = _random_set(21, 4, 12)
+    t0 = _dev_tracks(obs, 12)
+    same, keep = t0.remove(())
+    assert same is t0 and keep.shape == (0,)
+    t, keep = t0.remove(torch.arange(12))
+    assert t.n_tracks == 0 and t.n_kpts == 0 and keep.numel() == 0 and t.nppi.tolist() == [0, 0, 0, 0]
+
+
+@pytest.mark.gpu
+def test_select_to_dense_img_id_match_oracle():
+    obs = _random_set(30, 7, 50, empty=(2, 3))
+    t = _dev_tracks(obs, 50)
+    idx = torch.tensor([6, 2, 0, 6, 4])
+    s = t[idx.to(DEV)]
+    _same(s, otr.select(obs, idx))
+    v = t[4]                                                    # one-image view
+    sl = otr.img_slices(obs[0])[4]
+    assert v.n_imgs == 1 and torch.equal(v.pids.cpu(), obs[1][sl])
+    for n_imgs in (None, 9):
+        d = t.to_dense(n_imgs)
+        r = otr.to_dense(obs, 50, n_imgs)
+        assert d.shape == r.shape and torch.equal(torch.nan_to_num(d.cpu(), nan=-7.0), torch.nan_to_num(r, nan=-7.0))
+    iid = t.img_id
+    assert iid.dtype == torch.int64 and torch.equal(iid.cpu(), otr.img_id(obs[0], len(obs[1])).to(torch.int64))
+
+
+@pytest.mark.gpu
+def test_merge_at_pipeline_size():
+    """Merge at config-2 scale (8M rows kept, one new image) against the per-image slices."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    n_imgs, T = 1024, 1_000_000
+    nppi = torch.randint(7000, 8600, (n_imgs,), device=DEV, dtype=torch.int32)
+    n = int(nppi.sum())
+    old = ObservedTracks(n_imgs, T, nppi, torch.randint(0, T, (n,), device=DEV, dtype=torch.int32, generator=g),
+                         torch.rand((n, 2), device=DEV, generator=g), torch.rand((n, 2), device=DEV, generator=g),
+                         torch.rand((n, 5), device=DEV, generator=g), 'log_multidepth')
+    nppi_n = torch.zeros(n_imgs + 1, dtype=torch.int32, device=DEV)
+    nppi_n[-12:] = 500
+    m = int(nppi_n.sum())
+    new = ObservedTracks(n_imgs + 1, 1000, nppi_n, torch.randint(0, 1000, (m,), device=DEV, dtype=torch.int32,
+                                                                generator=g),
+                         torch.rand((m, 2), device=DEV, generator=g), torch.rand((m, 2), device=DEV, generator=g),
+                         torch.rand((m, 5), device=DEV, generator=g), 'log_multidepth')
+    got = old | new
+    for j in (0, 511, n_imgs - 12, n_imgs - 1, n_imgs):
+        so = old.img_slices[j] if j < n_imgs else slice(0, 0)
+        sn = new.img_slices[j]
+        sg = got.img_slices[j]
+        assert torch.equal(got.pids[sg], torch.cat([old.pids[so], new.pids[sn] + T]))
+        assert torch.equal(got.pix2d_dep[sg], torch.cat([old.pix2d_dep[so], new.pix2d_dep[sn]]))
+    assert torch.equal(got.nppi[:-1], nppi + nppi_n[:-1])
