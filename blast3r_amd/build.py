@@ -38,7 +38,7 @@ def build(verbose=False, jobs=None):
         obj = os.path.join(objdir, src + '.o')
         objs.append(obj)
         if src.endswith('.cpp'):
-            cmd = ['g++', '-O3', '-std=c++17', '-fPIC', '-I', os.path.join(ROOT, 'include'), '-I', CSRC, '-c', path,
+            cmd = ['g++', '-O3', '-std=c++17', '-fPIC', '-pthread', '-I', os.path.join(ROOT, 'include'), '-I', CSRC, '-c', path,
                    '-o', obj]
         else:
             cmd = [hipcc] + HIPCC_FLAGS + ['-c', path, '-o', obj]
@@ -57,7 +57,7 @@ def build(verbose=False, jobs=None):
         msg = '\n'.join(f'--- {s}\n{t}' for s, t in failed)
         raise RuntimeError(f'HIP build failed:\n{msg}')
     tmp = LIB + '.tmp'
-    cmd = [hipcc, '-shared', f'--offload-arch={ARCH}', '-fPIC', '-o', tmp] + objs
+    cmd = [hipcc, '-shared', f'--offload-arch={ARCH}', '-fPIC', '-pthread', '-o', tmp] + objs
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if r.returncode != 0:
         raise RuntimeError('link failed:\n' + r.stdout.decode(errors='replace'))

@@ -15,10 +15,12 @@
 //     global image pair (i1 <= i2) to its slots in batch order, so the final
 //     reduction is a deterministic sum.
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "ba_plan.h"
@@ -37,6 +39,23 @@ struct Plan {
 }  // namespace ba
 
 using namespace ba;
+
+// Runs fn(begin, end) over [0, n) on up to 16 host threads (contiguous ranges).
+template <typename F>
+static void parallel_for(int64_t n, F fn, int64_t min_per_thread = 65536) {
+    unsigned nth = std::thread::hardware_concurrency();
+    nth = std::max(1u, std::min(nth == 0 ? 1u : nth, 16u));
+    nth = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nth, n / std::max<int64_t>(1, min_per_thread)));
+    if (nth <= 1) { fn((int64_t)0, n); return; }
+    std::vector<std::thread> pool;
+    const int64_t step = (n + nth - 1) / nth;
+    for (unsigned w = 1; w < nth; ++w) {
+        const int64_t b = w * step, e = std::min(n, b + step);
+        if (b < e) pool.emplace_back(fn, b, e);
+    }
+    fn((int64_t)0, std::min(n, step));
+    for (auto& th : pool) th.join();
+}
 
 extern "C" const char* ba_plan_last_error(void) { return g_plan_err.c_str(); }
 
@@ -57,50 +76,323 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     Plan* P = new Plan();
     P->n_imgs = n_imgs; P->n_obs = n_obs; P->n_tracks = n_tracks; P->L = max_local_imgs; P->max_slots = max_slots;
 
-    // observation -> image, and per-track observation lists sorted by (image, obs)
+    // observation -> image, and per-track observation lists in observation (= image) order
     std::vector<int32_t> img(n_obs);
-    for (int i = 0, o = 0; i < n_imgs; ++i)
-        for (; o < cum_nkpts[i]; ++o) img[o] = i;
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i)
+            for (int64_t o = i ? cum_nkpts[i - 1] : 0; o < cum_nkpts[i]; ++o) img[o] = (int32_t)i;
+    }, 1);
+    std::vector<int32_t> tcnt(n_tracks, 0);
+    std::atomic<bool> bad_pid(false);
+    parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
+        for (int64_t o = o0; o < o1; ++o) {
+            const int32_t t = pids[o];
+            if (t < 0 || t >= n_tracks) { bad_pid = true; continue; }
+            __atomic_fetch_add(&tcnt[t], 1, __ATOMIC_RELAXED);
+        }
+    });
+    if (bad_pid) { g_plan_err = "pid out of range"; delete P; return nullptr; }
     std::vector<int64_t> tptr(n_tracks + 1, 0);
-    for (int64_t o = 0; o < n_obs; ++o) {
-        int32_t t = pids[o];
-        if (t < 0 || t >= n_tracks) { g_plan_err = "pid out of range"; delete P; return nullptr; }
-        tptr[t + 1]++;
-    }
-    for (int t = 0; t < n_tracks; ++t) tptr[t + 1] += tptr[t];
+    for (int t = 0; t < n_tracks; ++t) tptr[t + 1] = tptr[t] + tcnt[t];
     std::vector<int32_t> tobs(n_obs);
     {
         std::vector<int64_t> fill(tptr.begin(), tptr.end() - 1);
-        for (int64_t o = 0; o < n_obs; ++o) tobs[fill[pids[o]]++] = (int32_t)o;   // image-major input: already sorted by image
+        parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
+            for (int64_t o = o0; o < o1; ++o) tobs[__atomic_fetch_add(&fill[pids[o]], 1, __ATOMIC_RELAXED)] = (int32_t)o;
+        });
+        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {        // each list back in observation order
+            for (int64_t t = t0; t < t1; ++t) std::sort(tobs.begin() + tptr[t], tobs.begin() + tptr[t + 1]);
+        });
     }
-    // distinct images per track
+    // distinct images per track (observations of a track are in image order)
     std::vector<int32_t> tmin(n_tracks, INT32_MAX), tmax(n_tracks, -1), tdist(n_tracks, 0);
-    for (int t = 0; t < n_tracks; ++t) {
-        int last = -1;
-        for (int64_t k = tptr[t]; k < tptr[t + 1]; ++k) {
-            int i = img[tobs[k]];
-            if (i != last) { tdist[t]++; last = i; }
-            tmin[t] = std::min(tmin[t], i);
-            tmax[t] = std::max(tmax[t], i);
+    std::atomic<int32_t> worst_m(0), worst_d(0);
+    parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {
+        int32_t wm = 0, wd = 0;
+        for (int64_t t = t0; t < t1; ++t) {
+            int last = -1;
+            for (int64_t k = tptr[t]; k < tptr[t + 1]; ++k) {
+                const int i = img[tobs[k]];
+                if (i != last) { tdist[t]++; last = i; }
+                tmin[t] = std::min(tmin[t], i);
+                tmax[t] = std::max(tmax[t], i);
+            }
+            wm = std::max<int32_t>(wm, (int32_t)(tptr[t + 1] - tptr[t]));
+            wd = std::max(wd, tdist[t]);
         }
-        int64_t m = tptr[t + 1] - tptr[t];
-        if (m > BA_CHUNK) { g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")"; delete P; return nullptr; }
-        if (tdist[t] > max_local_imgs) {
-            g_plan_err = "a track spans more images (" + std::to_string(tdist[t]) + ") than max_local_imgs (" +
-                         std::to_string(max_local_imgs) + ")";
-            delete P; return nullptr;
-        }
+        int32_t c = worst_m.load();
+        while (wm > c && !worst_m.compare_exchange_weak(c, wm)) {}
+        c = worst_d.load();
+        while (wd > c && !worst_d.compare_exchange_weak(c, wd)) {}
+    });
+    if (worst_m.load() > BA_CHUNK) {
+        g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")";
+        delete P; return nullptr;
     }
+    if (worst_d.load() > max_local_imgs) {
+        g_plan_err = "a track spans more images (" + std::to_string(worst_d.load()) + ") than max_local_imgs (" +
+                     std::to_string(max_local_imgs) + ")";
+        delete P; return nullptr;
+    }
+    // observed tracks ordered by (first image, last image, track id): two stable counting sorts
     std::vector<int32_t> order;
-    order.reserve(n_tracks);
-    for (int t = 0; t < n_tracks; ++t) if (tptr[t + 1] > tptr[t]) order.push_back(t);
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
-        if (tmin[a] != tmin[b]) return tmin[a] < tmin[b];
-        if (tmax[a] != tmax[b]) return tmax[a] < tmax[b];
-        return a < b;
+    {
+        std::vector<int32_t> tmp;
+        tmp.reserve(n_tracks);
+        std::vector<int64_t> cnt(n_imgs + 1, 0);
+        for (int t = 0; t < n_tracks; ++t) if (tptr[t + 1] > tptr[t]) cnt[tmax[t] + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        int64_t n_obs_tracks = cnt[n_imgs];
+        tmp.resize(n_obs_tracks);
+        for (int t = 0; t < n_tracks; ++t) if (tptr[t + 1] > tptr[t]) tmp[cnt[tmax[t]]++] = t;
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (int t : tmp) cnt[tmin[t] + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        order.resize(n_obs_tracks);
+        for (int t : tmp) order[cnt[tmin[t]]++] = t;
+    }
+    // distinct image list of each track, laid out in `order`
+    std::vector<int64_t> oimg_ptr(order.size() + 1, 0);
+    for (size_t k = 0; k < order.size(); ++k) oimg_ptr[k + 1] = oimg_ptr[k] + tdist[order[k]];
+    std::vector<int32_t> oimg(oimg_ptr.back());
+    parallel_for((int64_t)order.size(), [&](int64_t k0, int64_t k1) {
+        for (int64_t k = k0; k < k1; ++k) {
+            const int t = order[k];
+            int64_t q = oimg_ptr[k];
+            int last = -1;
+            for (int64_t j = tptr[t]; j < tptr[t + 1]; ++j) {
+                const int i = img[tobs[j]];
+                if (i != last) { oimg[q++] = i; last = i; }
+            }
+        }
     });
 
     // ------------------------------------------------------------ greedy batching
+    // Pass 1 (sequential): tracks are taken in order and a batch is closed when the next track
+    // would exceed max_local_imgs images, max_slots pairs or max_batch_obs observations, so every
+    // batch is a contiguous range of `order`.  Pass 2 (parallel over batches): chunks, MFMA entry
+    // lists and wave placement of each batch.  Pass 3: concatenation in batch order.
+    struct BatchDesc {
+        int32_t k0, k1;                    // range of `order`
+        std::vector<int32_t> imgs;         // local image -> global image
+        std::vector<uint32_t> rows;        // rows[a] bit b: local pair (a, b), a <= b, is touched
+    };
+    std::vector<BatchDesc> batches;
+    {
+        std::vector<int32_t> cur_imgs;
+        std::vector<uint32_t> rows(max_local_imgs, 0);
+        std::vector<int32_t> limg_of(n_imgs, -1);
+        int cur_nslots = 0, k_begin = 0, n_cur = 0;
+        int64_t cur_obs = 0;
+        auto close = [&](int k_end) {
+            if (n_cur == 0) return;
+            batches.push_back(BatchDesc{k_begin, k_end, cur_imgs, rows});
+            for (int i : cur_imgs) limg_of[i] = -1;
+            cur_imgs.clear();
+            std::fill(rows.begin(), rows.end(), 0u);
+            cur_nslots = 0; cur_obs = 0; n_cur = 0; k_begin = k_end;
+        };
+        for (int kk = 0; kk < (int)order.size(); ++kk) {
+            const int t = order[kk];
+            const int32_t* timgs = oimg.data() + oimg_ptr[kk];
+            const int nti = (int)(oimg_ptr[kk + 1] - oimg_ptr[kk]);
+            const int m = (int)(tptr[t + 1] - tptr[t]);
+            for (int attempt = 0; attempt < 2; ++attempt) {
+                // local ids of the track's images (images not yet local get provisional ids)
+                const int n_loc = (int)cur_imgs.size();
+                int prov = n_loc;
+                uint32_t M = 0;
+                for (int q = 0; q < nti; ++q) {
+                    const int l = limg_of[timgs[q]];
+                    M |= 1u << (l >= 0 ? l : prov++);
+                }
+                bool ok = prov <= max_local_imgs &&
+                          (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || n_cur == 0);
+                int add_slots = 0;
+                if (ok) {
+                    // local pairs (x <= y) within M that no earlier track of the batch touched
+                    for (uint32_t r = M; r; r &= r - 1) {
+                        const int x = __builtin_ctz(r);
+                        add_slots += __builtin_popcount(M & ~((1u << x) - 1u) & ~rows[x]);
+                    }
+                    ok = cur_nslots + add_slots <= max_slots;
+                }
+                if (!ok) {
+                    if (n_cur == 0) {
+                        g_plan_err = "a single track needs more pair slots than max_slots";
+                        delete P; return nullptr;
+                    }
+                    close(kk);
+                    continue;
+                }
+                for (int q = 0; q < nti; ++q)
+                    if (limg_of[timgs[q]] < 0) { limg_of[timgs[q]] = (int)cur_imgs.size(); cur_imgs.push_back(timgs[q]); }
+                for (uint32_t r = M; r; r &= r - 1) {
+                    const int x = __builtin_ctz(r);
+                    rows[x] |= M & ~((1u << x) - 1u);
+                }
+                cur_nslots += add_slots;
+                cur_obs += m;
+                n_cur++;
+                break;
+            }
+        }
+        close((int)order.size());
+    }
+
+    // Pass 2: one batch's arrays, with chunk-track ids and entry offsets local to the batch
+    struct BatchOut {
+        std::vector<int32_t> chunk_obs, slot_info, chunk_meta, ct_pid, ct_first, ct_m, ct_mask, slot_pair,
+            chunk_slots, chunk_eptr, pos_slot;
+        std::vector<uint16_t> ents;
+        bool overflow = false;
+    };
+    const int n_batches = (int)batches.size();
+    std::vector<BatchOut> outs(n_batches);
+    auto build_batch = [&](int batch, std::vector<int32_t>& limg_of) {
+        const BatchDesc& bd = batches[batch];
+        BatchOut& R = outs[batch];
+        for (int a = 0; a < (int)bd.imgs.size(); ++a) limg_of[bd.imgs[a]] = a;
+        // local pair slots in (b, a) order
+        for (int b = 0; b < (int)bd.imgs.size(); ++b)
+            for (int a = 0; a <= b; ++a)
+                if ((bd.rows[a] >> b) & 1u) R.slot_pair.push_back(a | (b << 8));
+        const int nsl = (int)R.slot_pair.size();
+        std::vector<int16_t> lead;
+        int k = bd.k0;
+        while (k < bd.k1) {                                   // chunks: tracks packed whole, in order
+            int used = 0, ntr = 0;
+            const size_t base = R.chunk_obs.size();
+            R.chunk_obs.resize(base + BA_CHUNK, -1);
+            R.slot_info.resize(base + BA_CHUNK, -1);
+            const int first_ct = (int)R.ct_pid.size();
+            while (k < bd.k1) {
+                const int t = order[k];
+                const int m = (int)(tptr[t + 1] - tptr[t]);
+                if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
+                uint32_t mask = 0;
+                int last_img = -1, leader = -1;
+                for (int j = 0; j < m; ++j) {
+                    const int o = tobs[tptr[t] + j];
+                    const int lim = limg_of[img[o]];
+                    if (img[o] != last_img) { leader = used + j; last_img = img[o]; }
+                    mask |= 1u << lim;
+                    R.chunk_obs[base + used + j] = o;
+                    R.slot_info[base + used + j] = lim | (ntr << 8) | (leader << 16);
+                }
+                R.ct_pid.push_back(t);
+                R.ct_first.push_back(used);
+                R.ct_m.push_back(m);
+                R.ct_mask.push_back((int32_t)mask);
+                used += m;
+                ntr++;
+                k++;
+            }
+            R.chunk_meta.push_back(batch);
+            R.chunk_meta.push_back(first_ct);
+            R.chunk_meta.push_back(ntr);
+            R.chunk_meta.push_back(used);
+
+            // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
+            // first observation of each covering track in a with the one in b (chunk-track order);
+            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order), then
+            // the V rows of the first observation of each (track, image) run in a (slot order)
+            lead.assign((size_t)ntr * BA_MAX_LOCAL, -1);
+            for (int sidx = 0; sidx < used; ++sidx) {
+                const int inf = R.slot_info[base + sidx];
+                lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
+            }
+            const size_t e0 = R.ents.size();
+            R.chunk_eptr.push_back((int32_t)(e0 / 8));
+            auto ent = [&](int sa, int sb, int kind) { R.ents.push_back((uint16_t)(sa | (sb << 7) | (kind << 14))); };
+            for (int q = 0; q < BA_MAX_SLOTS; ++q) {
+                if (q >= nsl) { R.chunk_slots.push_back(0); continue; }
+                const int a = R.slot_pair[q] & 0xff, bq = (R.slot_pair[q] >> 8) & 0xff;
+                const size_t off = R.ents.size() - e0;
+                if (a != bq) {
+                    for (int tt = 0; tt < ntr; ++tt) {
+                        const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
+                        if (la_ >= 0 && lb_ >= 0) ent(la_, lb_, BA_ENT_V);
+                    }
+                } else {
+                    for (int sidx = 0; sidx < used; ++sidx)
+                        if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx, sidx, BA_ENT_J);
+                    for (int sidx = 0; sidx < used; ++sidx) {
+                        const int inf = R.slot_info[base + sidx];
+                        if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx, sidx, BA_ENT_V);
+                    }
+                }
+                while ((R.ents.size() - e0 - off) % 4) ent(0, 0, BA_ENT_PAD);
+                const size_t len = R.ents.size() - e0 - off;
+                R.chunk_slots.push_back((int32_t)(off | (len << 16)));
+            }
+            if (R.ents.size() - e0 > BA_LIST_CAP) R.overflow = true;
+            while ((R.ents.size() - e0) % 8) R.ents.push_back(0);
+        }
+        // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
+        // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
+        // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
+        // decreasing total work and each goes where the summed per-chunk maxima grow least.
+        {
+            const int nc = (int)(R.chunk_meta.size() / 4);
+            std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
+            std::vector<int64_t> tot(nsl, 0);
+            for (int c = 0; c < nc; ++c)
+                for (int q = 0; q < nsl; ++q) {
+                    const int len = R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q] >> 16;
+                    wk[(size_t)c * nsl + q] = 3 * (len / 4);
+                    tot[q] += wk[(size_t)c * nsl + q];
+                }
+            std::vector<int> sorder(nsl);
+            std::iota(sorder.begin(), sorder.end(), 0);
+            std::stable_sort(sorder.begin(), sorder.end(), [&](int x, int y) { return tot[x] > tot[y]; });
+            constexpr int NS = 4;
+            std::vector<int64_t> ls((size_t)nc * NS, 0), lw((size_t)nc * BA_WAVES, 0), ms(nc, 0), mw(nc, 0);
+            int cnt[BA_WAVES] = {0};
+            R.pos_slot.assign(BA_MAX_SLOTS, -1);
+            for (int q : sorder) {
+                int best = -1;
+                int64_t best_cost = 0;
+                for (int w = 0; w < BA_WAVES; ++w) {
+                    if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
+                    const int sd = w % NS;
+                    int64_t cost = 0;
+                    for (int c = 0; c < nc; ++c) {
+                        const int64_t x = wk[(size_t)c * nsl + q];
+                        cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
+                    }
+                    if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
+                }
+                R.pos_slot[best + BA_WAVES * cnt[best]] = q;
+                cnt[best]++;
+                const int sd = best % NS;
+                for (int c = 0; c < nc; ++c) {
+                    const int64_t x = wk[(size_t)c * nsl + q];
+                    ls[(size_t)c * NS + sd] += x;
+                    lw[(size_t)c * BA_WAVES + best] += x;
+                    ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
+                    mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
+                }
+            }
+        }
+        for (int i : bd.imgs) limg_of[i] = -1;
+    };
+    {
+        unsigned nth = std::thread::hardware_concurrency();
+        nth = std::max(1u, std::min(nth == 0 ? 1u : nth, 16u));
+        nth = (unsigned)std::min<int64_t>(nth, std::max(1, n_batches));
+        std::atomic<int> next(0);
+        auto work = [&]() {
+            std::vector<int32_t> limg_of(n_imgs, -1);
+            for (int b = next++; b < n_batches; b = next++) build_batch(b, limg_of);
+        };
+        std::vector<std::thread> pool;
+        for (unsigned w = 1; w < nth; ++w) pool.emplace_back(work);
+        work();
+        for (auto& th : pool) th.join();
+    }
+
+    // Pass 3: concatenation in batch order
     auto& chunk_obs = P->v[BA_PA_CHUNK_OBS];      // n_chunks * BA_CHUNK obs index or -1
     auto& chunk_meta = P->v[BA_PA_CHUNK_META];    // n_chunks * 4: batch, first ctrack, n ctracks, n slots used
     auto& slot_info = P->v[BA_PA_SLOT_INFO];      // n_chunks * BA_CHUNK: local img | ctrack<<8 | leader_slot<<16 (-1 pad)
@@ -118,230 +410,76 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 16-bit entries, two per word
     auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks
     auto& b_pos_slot = P->v[BA_PA_B_POS_SLOT];    // n_batches * BA_MAX_SLOTS
-    std::vector<uint16_t> ents;                   // all chunks' entries (packed into chunk_ent at the end)
     bool list_overflow = false;
-
-    std::vector<int32_t> cur_imgs;
-    std::vector<uint8_t> cur_pairs((size_t)max_local_imgs * max_local_imgs, 0);
-    int cur_nslots = 0;
-    int64_t cur_obs = 0;
-    std::vector<int32_t> cur_tracks;
-    std::vector<int32_t> limg_of(n_imgs, -1);
-
-    auto flush_batch = [&]() {
-        if (cur_tracks.empty()) return;
-        int batch = (int)b_nimgs.size();
-        // local pair slots in (b, a) order
-        int slot0 = (int)slot_pair.size();
-        for (int b = 0; b < (int)cur_imgs.size(); ++b)
-            for (int a = 0; a <= b; ++a)
-                if (cur_pairs[a * max_local_imgs + b]) slot_pair.push_back(a | (b << 8));
-        b_slot_ptr.push_back((int32_t)slot_pair.size());
-        // chunks: pack tracks in order
-        int ch_first_track = 0;
-        size_t k = 0;
-        while (k < cur_tracks.size()) {
-            int used = 0;
-            int ntr = 0;
-            int chunk = (int)(chunk_meta.size() / 4);
-            size_t base = chunk_obs.size();
-            chunk_obs.resize(base + BA_CHUNK, -1);
-            slot_info.resize(base + BA_CHUNK, -1);
-            int first_ct = (int)ct_pid.size();
-            while (k < cur_tracks.size()) {
-                int t = cur_tracks[k];
-                int m = (int)(tptr[t + 1] - tptr[t]);
-                if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
-                uint32_t mask = 0;
-                int last_img = -1, leader = -1;
-                for (int j = 0; j < m; ++j) {
-                    int o = tobs[tptr[t] + j];
-                    int li = limg_of[img[o]];
-                    if (img[o] != last_img) { leader = used + j; last_img = img[o]; }
-                    mask |= 1u << li;
-                    chunk_obs[base + used + j] = o;
-                    slot_info[base + used + j] = li | (ntr << 8) | (leader << 16);
-                }
-                ct_pid.push_back(t);
-                ct_first.push_back(used);
-                ct_m.push_back(m);
-                ct_mask.push_back((int32_t)mask);
-                used += m;
-                ntr++;
-                k++;
-            }
-            chunk_meta.push_back(batch);
-            chunk_meta.push_back(first_ct);
-            chunk_meta.push_back(ntr);
-            chunk_meta.push_back(used);
-            (void)chunk; (void)ch_first_track;
-
-            // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
-            // first observation of each covering track in a with the one in b (chunk-track order);
-            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order), then
-            // the V rows of the first observation of each (track, image) run in a (slot order)
-            {
-                std::vector<int16_t> lead((size_t)ntr * BA_MAX_LOCAL, -1);
-                for (int sidx = 0; sidx < used; ++sidx) {
-                    const int inf = slot_info[base + sidx];
-                    lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
-                }
-                const size_t e0 = ents.size();
-                chunk_eptr.push_back((int32_t)(e0 / 8));
-                const int nsl = (int)slot_pair.size() - slot0;
-                for (int q = 0; q < BA_MAX_SLOTS; ++q) {
-                    if (q >= nsl) { chunk_slots.push_back(0); continue; }
-                    const int a = slot_pair[slot0 + q] & 0xff, bq = (slot_pair[slot0 + q] >> 8) & 0xff;
-                    const size_t off = ents.size() - e0;
-                    auto ent = [&](int sa, int sb, int kind) {
-                        ents.push_back((uint16_t)(sa | (sb << 7) | (kind << 14)));
-                    };
-                    if (a != bq) {
-                        for (int tt = 0; tt < ntr; ++tt) {
-                            const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
-                            if (la_ >= 0 && lb_ >= 0) ent(la_, lb_, BA_ENT_V);
-                        }
-                    } else {
-                        for (int sidx = 0; sidx < used; ++sidx)
-                            if ((slot_info[base + sidx] & 0xff) == a) ent(sidx, sidx, BA_ENT_J);
-                        for (int sidx = 0; sidx < used; ++sidx) {
-                            const int inf = slot_info[base + sidx];
-                            if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx, sidx, BA_ENT_V);
-                        }
-                    }
-                    while ((ents.size() - e0 - off) % 4) ent(0, 0, BA_ENT_PAD);
-                    const size_t len = ents.size() - e0 - off;
-                    chunk_slots.push_back((int32_t)(off | (len << 16)));
-                }
-                if (ents.size() - e0 > BA_LIST_CAP) list_overflow = true;
-                while ((ents.size() - e0) % 8) ents.push_back(0);
-            }
-        }
-        b_chunk_ptr.push_back((int32_t)(chunk_meta.size() / 4));
-        // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
-        // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
-        // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
-        // decreasing total work and each goes where the summed per-chunk maxima grow least.
-        {
-            const int nsl = (int)slot_pair.size() - slot0;
-            const int c0 = b_chunk_ptr[b_chunk_ptr.size() - 2], nc = b_chunk_ptr.back() - c0;
-            std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
-            std::vector<int64_t> tot(nsl, 0);
-            for (int c = 0; c < nc; ++c)
-                for (int q = 0; q < nsl; ++q) {
-                    const int len = chunk_slots[(size_t)(c0 + c) * BA_MAX_SLOTS + q] >> 16;
-                    wk[(size_t)c * nsl + q] = 3 * (len / 4);
-                    tot[q] += wk[(size_t)c * nsl + q];
-                }
-            std::vector<int> order(nsl);
-            std::iota(order.begin(), order.end(), 0);
-            std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return tot[x] > tot[y]; });
-            constexpr int NS = 4, WPS = BA_WAVES / NS;
-            std::vector<int64_t> ls((size_t)nc * NS, 0), lw((size_t)nc * BA_WAVES, 0), ms(nc, 0), mw(nc, 0);
-            int cnt[BA_WAVES] = {0};
-            const size_t pbase = b_pos_slot.size();
-            b_pos_slot.resize(pbase + BA_MAX_SLOTS, -1);
-            for (int q : order) {
-                int best = -1;
-                int64_t best_cost = 0;
-                for (int w = 0; w < BA_WAVES; ++w) {
-                    if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
-                    const int sd = w % NS;
-                    int64_t cost = 0;
-                    for (int c = 0; c < nc; ++c) {
-                        const int64_t x = wk[(size_t)c * nsl + q];
-                        cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
-                    }
-                    if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
-                }
-                b_pos_slot[pbase + best + BA_WAVES * cnt[best]] = q;
-                cnt[best]++;
-                const int sd = best % NS;
-                for (int c = 0; c < nc; ++c) {
-                    const int64_t x = wk[(size_t)c * nsl + q];
-                    ls[(size_t)c * NS + sd] += x;
-                    lw[(size_t)c * BA_WAVES + best] += x;
-                    ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
-                    mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
-                }
-            }
-            (void)WPS;
-        }
-        for (int a = 0; a < max_local_imgs; ++a)
-            b_imgs.push_back(a < (int)cur_imgs.size() ? cur_imgs[a] : -1);
-        b_nimgs.push_back((int32_t)cur_imgs.size());
-        for (int i : cur_imgs) limg_of[i] = -1;
-        cur_imgs.clear();
-        std::fill(cur_pairs.begin(), cur_pairs.end(), 0);
-        cur_nslots = 0;
-        cur_obs = 0;
-        cur_tracks.clear();
-    };
-
-    b_chunk_ptr.push_back(0);
-    b_slot_ptr.push_back(0);
-    std::vector<int32_t> timgs;
-    for (int t : order) {
-        timgs.clear();
-        for (int64_t k = tptr[t]; k < tptr[t + 1]; ++k) {
-            int i = img[tobs[k]];
-            if (timgs.empty() || timgs.back() != i) timgs.push_back(i);
-        }
-        int m = (int)(tptr[t + 1] - tptr[t]);
-        for (int attempt = 0; attempt < 2; ++attempt) {
-            // new images and new pairs this track would add
-            int new_imgs = 0;
-            for (int i : timgs) if (limg_of[i] < 0) new_imgs++;
-            bool ok = (int)cur_imgs.size() + new_imgs <= max_local_imgs &&
-                      (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || cur_tracks.empty());
-            int add_slots = 0;
-            if (ok) {
-                // count pairs not yet touched (images not yet local get provisional ids)
-                int prov = (int)cur_imgs.size();
-                std::vector<int> li(timgs.size());
-                for (size_t q = 0; q < timgs.size(); ++q) li[q] = limg_of[timgs[q]] >= 0 ? limg_of[timgs[q]] : prov++;
-                for (size_t p = 0; p < li.size(); ++p)
-                    for (size_t q = p; q < li.size(); ++q) {
-                        int a = std::min(li[p], li[q]), b = std::max(li[p], li[q]);
-                        if (a >= (int)cur_imgs.size() || b >= (int)cur_imgs.size() || !cur_pairs[a * max_local_imgs + b]) add_slots++;
-                    }
-                ok = cur_nslots + add_slots <= max_slots;
-            }
-            if (!ok) {
-                if (cur_tracks.empty()) {
-                    g_plan_err = "a single track needs more pair slots than max_slots";
-                    delete P; return nullptr;
-                }
-                flush_batch();
-                continue;
-            }
-            for (int i : timgs) if (limg_of[i] < 0) { limg_of[i] = (int)cur_imgs.size(); cur_imgs.push_back(i); }
-            for (size_t p = 0; p < timgs.size(); ++p)
-                for (size_t q = p; q < timgs.size(); ++q) {
-                    int a = std::min(limg_of[timgs[p]], limg_of[timgs[q]]);
-                    int b = std::max(limg_of[timgs[p]], limg_of[timgs[q]]);
-                    if (!cur_pairs[a * max_local_imgs + b]) { cur_pairs[a * max_local_imgs + b] = 1; cur_nslots++; }
-                }
-            cur_obs += m;
-            cur_tracks.push_back(t);
-            break;
-        }
+    // offsets of each batch in the concatenated arrays, then a parallel copy
+    std::vector<int64_t> o_ch(n_batches + 1, 0), o_ct(n_batches + 1, 0), o_sl(n_batches + 1, 0), o_en(n_batches + 1, 0);
+    for (int b = 0; b < n_batches; ++b) {
+        o_ch[b + 1] = o_ch[b] + (int64_t)outs[b].chunk_meta.size() / 4;
+        o_ct[b + 1] = o_ct[b] + (int64_t)outs[b].ct_pid.size();
+        o_sl[b + 1] = o_sl[b] + (int64_t)outs[b].slot_pair.size();
+        o_en[b + 1] = o_en[b] + (int64_t)outs[b].ents.size();
+        list_overflow |= outs[b].overflow;
     }
-    flush_batch();
+    auto& slot_src = P->v[BA_PA_SLOT_SRC];
+    auto& s_pid = P->v[BA_PA_S_PID];
+    auto& s_img = P->v[BA_PA_S_IMG];
+    chunk_obs.resize(o_ch[n_batches] * BA_CHUNK); slot_info.resize(o_ch[n_batches] * BA_CHUNK);
+    slot_src.resize(o_ch[n_batches] * BA_CHUNK); s_pid.resize(o_ch[n_batches] * BA_CHUNK);
+    s_img.resize(o_ch[n_batches] * BA_CHUNK);
+    chunk_meta.resize(o_ch[n_batches] * 4); chunk_slots.resize(o_ch[n_batches] * BA_MAX_SLOTS);
+    chunk_eptr.resize(o_ch[n_batches]);
+    for (auto* v : {&ct_pid, &ct_first, &ct_m, &ct_mask}) v->resize(o_ct[n_batches]);
+    slot_pair.resize(o_sl[n_batches]);
+    // entries two per word, and one chunk's worth of zero padding so that a full-capacity copy of
+    // the last chunk's list stays inside the array
+    chunk_ent.assign((size_t)((o_en[n_batches] + BA_LIST_CAP + 1) / 2), 0);
+    uint16_t* ents = reinterpret_cast<uint16_t*>(chunk_ent.data());
+    b_pos_slot.resize((size_t)n_batches * BA_MAX_SLOTS);
+    parallel_for(n_batches, [&](int64_t b0, int64_t b1) {
+        for (int64_t b = b0; b < b1; ++b) {
+            BatchOut& R = outs[b];
+            const int32_t ct0 = (int32_t)o_ct[b], e8 = (int32_t)(o_en[b] / 8);
+            std::copy(R.chunk_obs.begin(), R.chunk_obs.end(), chunk_obs.begin() + o_ch[b] * BA_CHUNK);
+            for (size_t q = 0; q < R.chunk_obs.size(); ++q) {
+                const int32_t o = R.chunk_obs[q];
+                const size_t d = (size_t)o_ch[b] * BA_CHUNK + q;
+                slot_src[d] = o >= 0 ? o : 0;
+                s_pid[d] = o >= 0 ? pids[o] : 0;
+                s_img[d] = o >= 0 ? img[o] : 0;
+            }
+            std::copy(R.slot_info.begin(), R.slot_info.end(), slot_info.begin() + o_ch[b] * BA_CHUNK);
+            for (size_t c = 0; c < R.chunk_meta.size(); c += 4) {
+                int32_t* d = chunk_meta.data() + o_ch[b] * 4 + c;
+                d[0] = R.chunk_meta[c]; d[1] = R.chunk_meta[c + 1] + ct0; d[2] = R.chunk_meta[c + 2]; d[3] = R.chunk_meta[c + 3];
+            }
+            std::copy(R.ct_pid.begin(), R.ct_pid.end(), ct_pid.begin() + o_ct[b]);
+            std::copy(R.ct_first.begin(), R.ct_first.end(), ct_first.begin() + o_ct[b]);
+            std::copy(R.ct_m.begin(), R.ct_m.end(), ct_m.begin() + o_ct[b]);
+            std::copy(R.ct_mask.begin(), R.ct_mask.end(), ct_mask.begin() + o_ct[b]);
+            std::copy(R.slot_pair.begin(), R.slot_pair.end(), slot_pair.begin() + o_sl[b]);
+            std::copy(R.chunk_slots.begin(), R.chunk_slots.end(), chunk_slots.begin() + o_ch[b] * BA_MAX_SLOTS);
+            for (size_t c = 0; c < R.chunk_eptr.size(); ++c) chunk_eptr[o_ch[b] + c] = R.chunk_eptr[c] + e8;
+            std::copy(R.ents.begin(), R.ents.end(), ents + o_en[b]);
+            std::copy(R.pos_slot.begin(), R.pos_slot.end(), b_pos_slot.begin() + b * BA_MAX_SLOTS);
+            R = BatchOut();                                    // release as we go
+        }
+    }, 1);
+    for (int b = 0; b <= n_batches; ++b) {
+        b_chunk_ptr.push_back((int32_t)o_ch[b]);
+        b_slot_ptr.push_back((int32_t)o_sl[b]);
+    }
+    for (int b = 0; b < n_batches; ++b) {
+        for (int a = 0; a < max_local_imgs; ++a)
+            b_imgs.push_back(a < (int)batches[b].imgs.size() ? batches[b].imgs[a] : -1);
+        b_nimgs.push_back((int32_t)batches[b].imgs.size());
+    }
 
     // ------------------------------------------------------------ global pairs
-    int n_batches = (int)b_nimgs.size();
     if (list_overflow) {
         g_plan_err = "a chunk needs more than BA_LIST_CAP MFMA entries";
         delete P;
         return nullptr;
     }
-    // two entries per word, and one chunk's worth of padding so that a full-capacity copy of the
-    // last chunk's list stays inside the array
-    ents.resize(ents.size() + BA_LIST_CAP, 0);
-    if (ents.size() % 2) ents.push_back(0);
-    chunk_ent.resize(ents.size() / 2);
-    std::memcpy(chunk_ent.data(), ents.data(), ents.size() * sizeof(uint16_t));
     int64_t n_slots = (int64_t)slot_pair.size();
     std::vector<int64_t> keys(n_slots);
     std::vector<uint8_t> swapped(n_slots, 0);

@@ -40,6 +40,9 @@ enum {
     BA_PA_CHUNK_EPTR,       // per chunk: first entry, in units of 8 entries (16 bytes)
     BA_PA_B_POS_SLOT,       // per batch, BA_MAX_SLOTS words: the batch slot at Schur-kernel place
                             // wave + BA_WAVES * k, or -1 (places balanced by work)
+    BA_PA_SLOT_SRC,         // per chunk slot: its observation, 0 for an empty slot (a gather index)
+    BA_PA_S_PID,            // per chunk slot: track id of its observation (0 when empty)
+    BA_PA_S_IMG,            // per chunk slot: image of its observation (0 when empty)
     BA_PLAN_NARRAYS
 };
 

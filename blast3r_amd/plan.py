@@ -20,7 +20,7 @@ from ._lib import check, lib
 ARRAYS = ['chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr', 'b_imgs',
           'b_nimgs', 'b_slot_ptr', 'slot_pair', 'slot_gpair', 'pair_i1', 'pair_i2', 'pair_ptr', 'pair_src',
           'row_ptr', 'row_ent', 'img_ptr', 'img_src', 'chunk_slots', 'chunk_ent', 'chunk_eptr',
-          'b_pos_slot']
+          'b_pos_slot', 'slot_src', 's_pid', 's_img']
 SCALARS = ['n_chunks', 'n_batches', 'n_slots', 'n_pairs', 'n_ctracks', 'L', 'chunk', 'max_slots_used',
            'max_chunks_per_batch', 'n_pair_terms']
 CHUNK = 128
@@ -34,10 +34,10 @@ class BAPlan:
     def __init__(self, infos, pids, n_tracks, device=None, max_local_imgs=MAX_LOCAL, max_slots=MAX_SLOTS,
                  max_batch_obs=0):
         device = device or pids.device
-        cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32))
+        cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
         self.node_ids = np.ascontiguousarray(infos[1].detach().cpu().numpy().astype(np.int64))
         self.cam_ids = np.ascontiguousarray(infos[2].detach().cpu().numpy().astype(np.int64))
-        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32))
+        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
         self.n_imgs = int(cum.shape[0])
         self.n_obs = int(p.shape[0])
         self.n_tracks = int(n_tracks)
@@ -53,7 +53,7 @@ class BAPlan:
             self.scalars = {k: int(v) for k, v in zip(SCALARS, sc)}
             self.host = {}
             for i, name in enumerate(ARRAYS):
-                arr = np.zeros(int(sz[i]), dtype=np.int32)
+                arr = np.empty(int(sz[i]), dtype=np.int32)
                 check(L.ba_plan_export(h, i, arr.ctypes.data_as(ctypes.c_void_p)))
                 self.host[name] = arr
         finally:
@@ -64,19 +64,16 @@ class BAPlan:
             if self.dev[k].numel() == 0:
                 self.dev[k] = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.L = int(max_local_imgs)
-        obs = self.host['chunk_obs']
-        valid = obs >= 0
-        safe = np.where(valid, obs, 0).astype(np.int64)
-        img = np.searchsorted(cum[:-1], np.arange(self.n_obs), side='right').astype(np.int32) if self.n_obs else \
-            np.zeros(0, np.int32)
-        self.obs_img = img
-        self.slot_index = torch.from_numpy(safe).to(self.device)
-        self.dev['s_pid'] = torch.from_numpy(np.where(valid, p[safe] if self.n_obs else 0, 0).astype(np.int32)).to(
-            self.device) if obs.size else torch.zeros(1, dtype=torch.int32, device=self.device)
-        self.dev['s_img'] = torch.from_numpy(np.where(valid, img[safe] if self.n_obs else 0, 0).astype(np.int32)).to(
-            self.device) if obs.size else torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._cum = cum
+        self.slot_index = self.dev['slot_src'] if self.host['slot_src'].size else self.dev['slot_src'][:0]
         self._slot_cache = {}
         self._ws = {}
+
+    @property
+    def obs_img(self):
+        """Image of every observation (host array)."""
+        counts = np.diff(np.concatenate([[0], self._cum.astype(np.int64)]))
+        return np.repeat(np.arange(self.n_imgs, dtype=np.int32), counts)
 
     # ------------------------------------------------------------------ data
     def slot_data(self, pix2d, pix2d_std, pix2d_dep):
