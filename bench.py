@@ -38,6 +38,8 @@ def main():
     ap.add_argument('--cpu-baseline', type=int, default=1)
     ap.add_argument('--sampling', type=int, default=1,
                     help='also time the F-sampling kernel on maps of the configuration (1 = yes)')
+    ap.add_argument('--layout', type=int, default=1,
+                    help='also time the observation-structure edits (old | new merge, remove, plan rebuild)')
     ap.add_argument('--copy-probe', action='store_true',
                     help='run a 256 MiB fill and a 256 MiB kernel copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
@@ -140,6 +142,7 @@ def main():
         log(f'[bench] lm_step {lm_ms:.2f} ms')
 
     smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
+    lay = bench_layout(prob, g, dev, args.steps, args.warmup) if args.layout else None
 
     cpu = None
     if args.cpu_baseline:
@@ -163,8 +166,83 @@ def main():
                          'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)'},
         'cpu_baseline': cpu,
         'f_sampling': smp,
+        'layout': lay,
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_layout(prob, g, dev, steps, warmup):
+    """Observation-structure edits of the online pipeline at the configuration's size: `old | new`
+    (tracks.py:84-102) with old = every observation of the configuration and new = one more frame
+    whose 1000 tracks are seen in the last 12 frames, then `remove` of 1% of the tracks
+    (tracks.py:116-127) and the rebuild of the structure plan for the merged set.  The bare gather
+    launch sequence (ba_tracks_gather) is timed with events on its stream; algorithmic bytes per
+    output row: one row read and written, 2 (4 + 8 + 8 + 4 C)."""
+    import ctypes
+    from blast3r_amd._lib import BaGatherArgs, check, lib, ptr, stream_ptr
+    from blast3r_amd.data import ObservedTracks, _obs_set, _workspace
+    from blast3r_amd.plan import BAPlan
+    C, n_imgs, T = prob.C, prob.n_imgs, prob.n_tracks
+    cum = g.infos[0].long()
+    nppi = torch.diff(torch.cat([cum.new_zeros(1), cum])).to(torch.int32)
+    old = ObservedTracks(n_imgs, T, nppi, g.pids, g.pix2d, g.pix2d_std, g.pix2d_dep, 'log_multidepth')
+    gen = torch.Generator(device=dev).manual_seed(11)
+    nppi_n = torch.zeros(n_imgs + 1, dtype=torch.int32, device=dev)
+    nppi_n[-12:] = 1000 * 8 // 12
+    m = int(nppi_n.sum())
+    new = ObservedTracks(n_imgs + 1, 1000, nppi_n,
+                         torch.randint(0, 1000, (m,), device=dev, dtype=torch.int32, generator=gen),
+                         torch.rand((m, 2), device=dev, generator=gen) * 500, torch.ones((m, 2), device=dev),
+                         torch.rand((m, C), device=dev, generator=gen), 'log_multidepth')
+    # the bare launch sequence, arguments prepared once
+    sa, ka = _obs_set(old)
+    sb, kb = _obs_set(new)
+    n_rows = old.n_kpts + new.n_kpts
+    out = [torch.empty(n_rows, dtype=torch.int32, device=dev), torch.empty((n_rows, 2), device=dev),
+           torch.empty((n_rows, 2), device=dev), torch.empty((n_rows, C), device=dev),
+           torch.empty(n_imgs + 1, dtype=torch.int32, device=dev), torch.empty(1, dtype=torch.int64, device=dev)]
+    sel_a = torch.cat([torch.arange(n_imgs, dtype=torch.int32), torch.tensor([-1], dtype=torch.int32)]).to(dev)
+    sel_b = torch.arange(n_imgs + 1, dtype=torch.int32, device=dev)
+    ws = _workspace(dev, n_rows, 0, n_imgs + 1)
+    a = BaGatherArgs(a=sa, b=sb, sel_a=ptr(sel_a), sel_b=ptr(sel_b), pid_shift_b=T, C=C, n_out=n_imgs + 1,
+                     n_rows=n_rows, pids=ptr(out[0]), pix2d=ptr(out[1]), pix2d_std=ptr(out[2]), pix2d_dep=ptr(out[3]),
+                     nppi=ptr(out[4]), total=ptr(out[5]), workspace=ptr(ws))
+    L, st = lib(), stream_ptr(dev)
+    for _ in range(warmup):
+        check(L.ba_tracks_gather(ctypes.byref(a), st))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        check(L.ba_tracks_gather(ctypes.byref(a), st))
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gbs = n_rows * 2 * (20 + 4 * C) / (ms * 1e-3) / 1e9
+    # the Python operations, outputs allocated per call (host waits for the row count, as the reference)
+    t0 = time.perf_counter()
+    merged = old | new
+    torch.cuda.synchronize()
+    merge_ms = (time.perf_counter() - t0) * 1e3
+    bad = torch.randperm(T + 1000, device=dev, generator=gen)[:(T + 1000) // 100]
+    merged.remove(bad)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    kept, _ = merged.remove(bad)
+    torch.cuda.synchronize()
+    remove_ms = (time.perf_counter() - t0) * 1e3
+    infos = torch.stack([torch.cumsum(kept.nppi.long(), 0), torch.arange(n_imgs + 1, device=dev),
+                         torch.zeros(n_imgs + 1, dtype=torch.long, device=dev)]).to(torch.int32)
+    t0 = time.perf_counter()
+    BAPlan(infos, kept.pids, kept.n_tracks)
+    torch.cuda.synchronize()
+    plan_s = time.perf_counter() - t0
+    log(f'[bench] layout: gather {ms:.3f} ms ({gbs:.0f} GB/s algorithmic, {n_rows} rows); old | new {merge_ms:.2f} ms, '
+        f'remove 1% {remove_ms:.2f} ms, plan rebuild {plan_s:.3f} s')
+    return {'gather_ms': ms, 'rows': n_rows, 'bytes_per_row': 2 * (20 + 4 * C),
+            'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
+                         'kernel': 'ba_tracks_gather (k_gather_rows + offsets)'},
+            'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s}
 
 
 def bench_sampling(prob, g, dev, steps, warmup, cfg):
