@@ -97,6 +97,14 @@ class BaRemoveArgs(ctypes.Structure):
                 ('nppi', c_p), ('old_to_keep', c_p), ('counts', c_p), ('workspace', c_p)]
 
 
+class BaTangentArgs(ctypes.Structure):
+    _fields_ = [('depth_addr', c_p), ('ref_addr', c_p), ('map_hw', c_p), ('H', c_int), ('W', c_int),
+                ('depth_pix_stride', c_int), ('ref_pix_stride', c_int), ('K', c_p), ('cam_ids', c_p), ('z_coefs', c_p),
+                ('n_imgs', c_i64), ('C', c_int), ('tan_stride', c_int), ('normalize', c_int), ('optim_Z0', c_int),
+                ('fp64', c_int), ('compute_gn', c_int), ('weight', c_d), ('eps', c_d), ('loss', c_p), ('g_z', c_p),
+                ('H_z', c_p), ('workspace', c_p), ('workspace_bytes', c_i64)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     'ba_last_error': (ctypes.c_char_p, []),
@@ -130,6 +138,10 @@ _SIGS = {
     'ba_tracks_to_dense': (c_int, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p]),
     'ba_tracks_img_id': (c_int, [c_p, c_i64, c_i64, c_p, c_p, c_p]),
     'ba_tracks_workspace_bytes': (c_i64, [c_i64, c_i64, c_i64]),
+    'ba_tangent_prior': (c_int, [ctypes.POINTER(BaTangentArgs), c_p]),
+    'ba_tangent_workspace_bytes': (c_i64, [c_i64, c_int, c_int, c_int, c_int, c_int, c_int]),
+    'ba_planar_confidence': (c_int, [c_p, c_int, c_int, c_f, c_p, c_p]),
+    'ba_add_z_prior': (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_p]),
 }
 
 EXPORTED = tuple(_SIGS)

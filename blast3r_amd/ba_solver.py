@@ -374,15 +374,27 @@ class GaussNewtonSolver:
             raise TypeError('Unsupported JTJ.A type for z_prior: z-coefficients are not optimised')
         C = self.n_zcf
         o = lay['d'] - C
-        H_z = H_z.to(torch.float64)
-        g_z = g_z.to(torch.float64)
+        H_z = H_z.to(device=S_pairs.device, dtype=torch.float64).contiguous()
+        g_z = g_z.to(device=S_pairs.device, dtype=torch.float64).contiguous()
         assert g_z.shape == (self.imgs.n, C) and H_z.shape == (self.imgs.n, C, C)
-        diag_pairs = plan.dev['pair_i1'] == plan.dev['pair_i2']
-        pid = torch.nonzero(diag_pairs).squeeze(-1)
-        img = plan.dev['pair_i1'][pid].long()
-        S_pairs[pid, o:, o:] += H_z[img]
-        e_img[:, o:] += g_z
-        dg_img[:, o:] += H_z.diagonal(dim1=-1, dim2=-2)
+        if len(e_img) != self.imgs.n:          # compacted images: the rows of the optimised ones
+            idx = torch.as_tensor(self.imgs.true_idxs, device=S_pairs.device).long()
+            gf = torch.zeros((len(e_img), C), dtype=torch.float64, device=S_pairs.device)
+            Hf = torch.zeros((len(e_img), C, C), dtype=torch.float64, device=S_pairs.device)
+            gf[idx], Hf[idx] = g_z, H_z
+            g_z, H_z = gf, Hf
+        diag = plan.workspace_cache.get('diag_pair')
+        if diag is None:                       # the (i, i) block of each image, once per structure
+            n_imgs = len(e_img)
+            i1, i2 = plan.dev['pair_i1'][:plan.scalars['n_pairs']], plan.dev['pair_i2'][:plan.scalars['n_pairs']]
+            pid = torch.nonzero(i1 == i2).squeeze(-1)
+            diag = torch.full((n_imgs,), -1, dtype=torch.int32, device=S_pairs.device)
+            diag[i1[pid].long()] = pid.to(torch.int32)
+            if bool((diag < 0).any()):
+                raise ValueError('z_prior: an image without observations has no block in the reduced system')
+            plan.workspace_cache['diag_pair'] = diag
+        check(lib().ba_add_z_prior(ptr(S_pairs), ptr(diag), ptr(e_img), ptr(dg_img), ptr(H_z), ptr(g_z), len(e_img),
+                                   lay['d'], C, stream_ptr(S_pairs.device)))
 
     # ------------------------------------------------------------------ bs:228-248
     def unpack_delta_inplace(self, delta):

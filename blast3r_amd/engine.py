@@ -5,7 +5,8 @@ return values and control flow (en:206-334, en:405-503).  The numerical work
 runs in libba_hip.so: residuals (ba_residuals), the fused linearize + Schur +
 PCG + back-substitution step (GaussNewtonSolver), the parameter update
 (ba_apply_update) and the line-search objective with an exact radix-select
-reproj_score (ba_objective).
+reproj_score (ba_objective), and the dense tangent prior (ba_tangent_prior, en:15-200) when
+weight_tan > 0.
 """
 from collections import namedtuple
 
@@ -14,6 +15,7 @@ import torch
 from . import cujac
 from ._lib import check, lib, ptr, stream_ptr
 from .ba_solver import GaussNewtonSolver, _param_state
+from .tangent import confident_in_planar_regions, dense_tangent_prior_terms as _dense_tangent_prior_terms
 
 BA_Status = namedtuple('BA_Status', 'init_loss, init_residuals, new_loss, new_residuals')
 
@@ -127,8 +129,7 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
     if weight_tan > 0:
-        raise NotImplementedError('the dense tangent prior (weight_tan > 0) is not part of the MI355X path; '
-                                  'pass z_prior to GaussNewtonSolver.solve_delta instead')
+        assert is_depth_log, 'tangent prior currently only implemented for depth_mode="log"'
     n_imgs = rigs.shape[1]
     assert shape_of(rigs) == (3, n_imgs)
     n_cams = len(K)
@@ -150,6 +151,9 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
     assert huber_delta >= 0.1
 
     w_null = 1e-16
+    K_tan = K.detach()          # the prior treats the intrinsics as constant within the step (en:250-252)
+    tan_kw = dict(weight_tan=float(weight_tan), tan_stride=int(tan_stride), optim_Z0=optim_Z0,
+                  normalize_tangents=bool(normalize_tangents))
 
     def objective(K, P_w2rig, pts3d, z_coefs):
         out = cujac.compute_residuals_with_rigs(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std,
@@ -158,6 +162,10 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
         buf = out.T                                               # (9, n) buffer
         residuals_, err_, w_pts_ = out.view(-1, 3, 3).unbind(dim=1)
         loss, reproj = _objective(buf, n_obs, has_err=pnorm > 0)
+        if weight_tan > 0:                                        # en:270-277
+            tan_loss, _, _ = _dense_tangent_prior_terms(rigs, K_tan, z_coefs, log_depth_maps, conf, pts3d_ref,
+                                                        dtype=loss.dtype, compute_gn=False, **tan_kw)
+            loss = loss + tan_loss
         return loss, residuals_, w_pts_, reproj
 
     if init_eval is not None:
@@ -171,7 +179,12 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
                               optim_K=optim_K, optim_Z=optim_Z, optim_Z0=optim_Z0, optim_P=optim_P, optim_X=optim_X,
                               is_depth_log=is_depth_log, pix2d=pix2d, hp=hp)
     init_residuals._ba_state = _param_state(J)
-    delta = jac.solve_delta(J, init_residuals, w_pts)
+    z_prior = None
+    if weight_tan > 0:                                            # en:288-298: GN terms on z_coefs only
+        _, g_z, H_z = _dense_tangent_prior_terms(rigs, K_tan, z_coefs, log_depth_maps, conf, pts3d_ref,
+                                                 dtype=jac.dtype, compute_gn=True, **tan_kw)
+        z_prior = (H_z, g_z)
+    delta = jac.solve_delta(J, init_residuals, w_pts, z_prior=z_prior)
     delta_K, delta_P, delta_zcf, delta_pts = jac.unpack_delta_inplace(delta)
 
     update = dict()
@@ -235,6 +248,8 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
     """Main bundle-adjustment loop (en:405-503)."""
     trk = track_data.to(device)
     rig = rigs_data.to(device)
+    todev = lambda x: None if x is None else (x.to(device) if isinstance(x, torch.Tensor) else [t.to(device) for t in x])
+    dense_depth, dense_conf, dense_pts3d_ref = todev(dense_depth), todev(dense_conf), todev(dense_pts3d_ref)
     if z_coefs is None:
         z_coefs = rig.z_coefs_from_scale(trk)
     original_pix2d_dep = trk.pix2d_dep
@@ -247,6 +262,7 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
         phase_num += 1
         if phase_num > (max_n_phases % 1000):
             break
+        dense_depth_use = dense_depth
         if n_zcfs is not None:
             z_coefs = variables['z_coefs']
             optim_Z0 = True
@@ -254,6 +270,11 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
                 optim_Z0 = (n_zcfs == 2) or (n_zcfs == original_pix2d_dep.shape[1])
                 n_zcfs += not optim_Z0
             trk.pix2d_dep = original_pix2d_dep[:, :n_zcfs].contiguous()
+            if dense_depth is not None:                       # en:460-464
+                assert len(dense_depth) == rig.n_imgs, 'log_depth_maps must be n_imgs x (H, W, C)'
+                assert all(d.shape[-1] >= n_zcfs for d in dense_depth), \
+                    'not enough dense depth channels for the requested n_zcfs'
+                dense_depth_use = [d[..., :n_zcfs] for d in dense_depth]
             if n_zcfs < z_coefs.shape[1]:
                 assert n_zcfs >= 1
                 variables['z_coefs'] = z_coefs[:, :n_zcfs].contiguous()
@@ -268,7 +289,9 @@ def bundle_adjustment(rigs_data, track_data, pts3d=None, z_coefs=None,
         infos = rig.infos(trk)
         while it < max_iters:
             update, status, last_eval = _lm_step(infos, trk.pids, trk.pix2d, trk.pix2d_std, trk.pix2d_dep,
-                                                 **variables, weight_tan=tangent_reg, tan_stride=tan_stride,
+                                                 **variables, log_depth_maps=dense_depth_use, conf=dense_conf,
+                                                 pts3d_ref=dense_pts3d_ref, weight_tan=tangent_reg,
+                                                 tan_stride=tan_stride,
                                                  normalize_tangents=normalize_tangents,
                                                  optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P,
                                                  optim_X=optim_X, optim_Z0=optim_Z0, pnorm=pnorm,

@@ -68,6 +68,7 @@ class BAPlan:
         self.slot_index = self.dev['slot_src'] if self.host['slot_src'].size else self.dev['slot_src'][:0]
         self._slot_cache = {}
         self._ws = {}
+        self.workspace_cache = {}      # derived per-structure arrays (e.g. each image's diagonal block)
 
     @property
     def obs_img(self):

@@ -310,6 +310,61 @@ int ba_tracks_img_id(const int32_t* nppi, int64_t n_imgs, int64_t n_rows, int64_
 /* Workspace of the four calls above (bytes). */
 int64_t ba_tracks_workspace_bytes(int64_t n_rows, int64_t n_tracks, int64_t n_imgs);
 
+/* ------------------------------------------------------------------ dense tangent prior */
+
+/* _dense_tangent_prior_terms (src/blast3r/inference/engine.py:15-179) for every image at once:
+ * the combined log-depth exp(min(sum_c z_c L_c, 80)) of the image's maps and its reference
+ * pointmap, both sampled at rows / columns s//2 + s k, give unit-tangent residuals along rows and
+ * columns weighted by the planar confidence of the pointmap's depth (engine.py:182-200).
+ *   loss (1,): sum over images of weight * mean(w r^2) per direction, in the working precision;
+ *   g_z (n_imgs, C), H_z (n_imgs, C, C): Gauss-Newton terms w.r.t. z_coefs (compute_gn), with
+ *   column / row 0 zeroed when optim_Z0 is 0.
+ * Images whose subsampled width or channel count is below 2 contribute nothing (engine.py:75).
+ * fp64 selects the working precision (the reference's dtype argument); the pointmap tangents and
+ * the confidence stay fp32 either way, as in the reference; sums are fp64. */
+typedef struct {
+    const int64_t* depth_addr; /* (n_imgs,) device address of each image's log-depth map (H_i, W_i, >= C) fp32,
+                                  pixels depth_pix_stride floats apart, rows W_i pixels apart; channel c at +c */
+    const int64_t* ref_addr;   /* (n_imgs,) address of each image's reference pointmap (H_i, W_i, 3) fp32,
+                                  pixels ref_pix_stride floats apart */
+    const int32_t* map_hw;     /* (n_imgs, 2) per-image H_i, W_i, or null when every map is H x W */
+    int32_t H, W;              /* the map size, or the largest H_i and W_i when map_hw is given */
+    int32_t depth_pix_stride;
+    int32_t ref_pix_stride;
+    const float* K;            /* (n_cams, 3, 3) */
+    const int32_t* cam_ids;    /* (n_imgs,) camera of each image (rigs row 2) */
+    const float* z_coefs;      /* (n_imgs, C) */
+    int64_t n_imgs;            /* 1..65535 */
+    int32_t C;                 /* z-coefficients (channels used), <= 16 with compute_gn */
+    int32_t tan_stride;
+    int32_t normalize;         /* normalize_tangents */
+    int32_t optim_Z0;
+    int32_t fp64;              /* working precision of loss / g_z / H_z: 0 fp32, 1 fp64 */
+    int32_t compute_gn;
+    double weight;             /* weight_tan */
+    double eps;
+    void* loss;
+    void* g_z;
+    void* H_z;
+    void* workspace;
+    int64_t workspace_bytes;   /* >= ba_tangent_workspace_bytes(n_imgs, C, H, W, tan_stride, normalize, compute_gn) */
+} ba_tangent_args;
+
+int ba_tangent_prior(const ba_tangent_args* args, void* stream);
+int64_t ba_tangent_workspace_bytes(int64_t n_imgs, int32_t C, int32_t H, int32_t W, int32_t tan_stride,
+                                   int32_t normalize, int32_t compute_gn);
+
+/* confident_in_planar_regions (engine.py:182-200) of one (H, W) fp32 map: exp(-alpha (lx^2 + ly^2)) with
+ * lx, ly the row / column Laplacians (one-sided at the borders) divided by the 3x3 minimum
+ * (at least 1e-12). */
+int ba_planar_confidence(const float* D0, int32_t H, int32_t W, float alpha, float* out, void* stream);
+
+/* z_prior injection (ba_solver.py:141-173) into the image-level reduced system before damping:
+ * S_pairs[diag_pair[i]][o + c][o + d] += H_z[i][c][d], e_img[i][o + c] += g_z[i][c],
+ * dg_img[i][o + c] += H_z[i][c][c], for the n_imgs images (fp64 arrays, d x d blocks, o = d - C). */
+int ba_add_z_prior(double* S_pairs, const int32_t* diag_pair, double* e_img, double* dg_img, const double* H_z,
+                   const double* g_z, int64_t n_imgs, int32_t d, int32_t C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

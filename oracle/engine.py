@@ -15,6 +15,7 @@ from collections import namedtuple
 import torch
 
 from . import kernels as K_
+from . import tangent as T_
 from .solver import Problem, build_normal_equations, solve_reduced_pcg, solve_reduced_direct, unpack_delta
 
 BA_Status = namedtuple('BA_Status', 'init_loss, init_residuals, new_loss, new_residuals')
@@ -53,7 +54,7 @@ def linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig,
                         residuals, w_pts, is_depth_log=True, optim_K=True, optim_Z=True, optim_P=True,
                         optim_X=True, optim_Z0=True, optim_Z_1st_cam=True, no_grad_f_from_rz=False,
                         dampen=1e-12, adaptive_dampen=True, dtype=torch.float64, solver='pcg',
-                        pcg_tol=1e-6, pcg_maxiter=300):
+                        pcg_tol=1e-6, pcg_maxiter=300, z_prior=None):
     """compute_jacobians + solve_delta + unpack (bs:34-40, bs:110-248). Returns (dK, dP, dZ, dX, info)."""
     J_cam, J_zcf, J_pts = K_.jacobians_with_rigs(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d_std,
                                                  pix2d_dep, is_depth_log, float64=(dtype == torch.float64))
@@ -65,7 +66,7 @@ def linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig,
     ne, g, params = build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=optim_K,
                                            optim_P=optim_P, optim_Z=optim_Z, optim_X=optim_X,
                                            no_grad_f_from_rz=no_grad_f_from_rz, dampen=dampen,
-                                           adaptive_dampen=adaptive_dampen)
+                                           adaptive_dampen=adaptive_dampen, z_prior=z_prior)
     info = dict(ne=ne, g=g, params=params)
     if solver == 'pcg':
         delta, niter, conv = solve_reduced_pcg(ne, g, tol=pcg_tol, maxiter=pcg_maxiter)
@@ -81,20 +82,36 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_co
             pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12, min_loss_delta=1e-4,
             weight_z=1, optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True,
             no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float64, solver='pcg', verbose=False,
-            pcg_tol=1e-6, pcg_maxiter=300):
+            pcg_tol=1e-6, pcg_maxiter=300, log_depth_maps=None, conf=None, pts3d_ref=None, weight_tan=0.0,
+            tan_stride=4, normalize_tangents=True):
     """en:206-334 on CPU. Returns (update dict, BA_Status, info)."""
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
-    obj = lambda K, P_w2rig, pts3d, z_coefs: objective(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d,
-                                                       pix2d_std, pix2d_dep, is_depth_log, weight_z, pnorm,
-                                                       clip_pix_err, huber_delta)
+    K_tan = K.detach()
+    tan_kw = dict(weight_tan=float(weight_tan), tan_stride=int(tan_stride), optim_Z0=optim_Z0,
+                  normalize_tangents=bool(normalize_tangents))
+
+    def obj(K, P_w2rig, pts3d, z_coefs):
+        loss, res, w = objective(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std, pix2d_dep,
+                                 is_depth_log, weight_z, pnorm, clip_pix_err, huber_delta)
+        if weight_tan > 0:                                                        # en:270-277
+            loss = loss + T_.tangent_prior_terms(rigs[2], K_tan, z_coefs, log_depth_maps, pts3d_ref, dtype=loss.dtype,
+                                                 compute_gn=False, **tan_kw)[0]
+        return loss, res, w
+
     init_loss, init_residuals, w_pts = obj(K, P_w2rig, pts3d, z_coefs)
+    z_prior = None
+    if weight_tan > 0:                                                            # en:288-298
+        _, g_z, H_z = T_.tangent_prior_terms(rigs[2], K_tan, z_coefs, log_depth_maps, pts3d_ref, dtype=dtype,
+                                             compute_gn=True, **tan_kw)
+        z_prior = (H_z, g_z)
     dK, dP, dZ, dX, info = linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs,
                                                pts3d, init_residuals, w_pts, is_depth_log=is_depth_log,
                                                optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P, optim_X=optim_X,
                                                optim_Z0=optim_Z0, no_grad_f_from_rz=no_grad_f_from_rz,
                                                dampen=dampen, adaptive_dampen=adaptive_dampen, dtype=dtype,
-                                               solver=solver, pcg_tol=pcg_tol, pcg_maxiter=pcg_maxiter)
+                                               solver=solver, pcg_tol=pcg_tol, pcg_maxiter=pcg_maxiter,
+                                               z_prior=z_prior)
     update = {}
     last_a = 1.0
     scale = 1.0

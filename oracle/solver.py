@@ -121,8 +121,11 @@ def _enable(status, blocks, cols, param, ent_of_obs):
 
 def build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=True, optim_P=True,
                            optim_Z=True, optim_X=True, no_grad_f_from_rz=False, clamp_w=(1e-6, 1e6),
-                           dampen=1e-12, adaptive_dampen=True):
+                           dampen=1e-12, adaptive_dampen=True, z_prior=None):
     """g = J^T W r and damped J^T W J (bs:42-70, bs:110-177), blocks kept separate.
+
+    z_prior = (H_z, g_z) adds the tangent-prior terms to the z-coefficient blocks and gradient
+    before damping (bs:141-173); a switched-off z block becomes H_z (bs:163-164).
 
     Returns (NormalEquations, g, params) where g is the fp64 gradient in the
     (compacted) unknown order and params the four ``_Param`` counters.
@@ -158,6 +161,9 @@ def build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=
         g[off_t:off_z].view(-1, 6).index_add_(0, c_tau, torch.einsum('nki,nk->ni', J_tau, Wr))
     if not zz:
         g[off_z:n_c].view(-1, C).index_add_(0, c_zcf, Jz * Wr[:, 2:3])
+    if z_prior is not None:                                        # bs:150-155
+        assert z_prior[1].shape == (imgs.n, C)
+        g[off_z:n_c] += z_prior[1].to(dt).reshape(-1)
     if not zp:
         g[n_c:].view(-1, 3).index_add_(0, c_pts, torch.einsum('nki,nk->ni', Jp, Wr))
 
@@ -171,7 +177,14 @@ def build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=
     ne = NormalEquations()
     ne.sizes = dict(n_f=n_f, n_t=n_t, n_z=n_z, n_p=n_p, n_c=n_c, C=C)
 
-    def gram_leaf(name, Jb, cols, n_ent, b, is_zero):
+    def gram_leaf(name, Jb, cols, n_ent, b, is_zero, extra=None):
+        if is_zero and extra is not None:                          # ZerosMat replaced by H_z (bs:163-164)
+            blocks = extra.to(dt).clone()
+            val = dampen
+            if adaptive_dampen:
+                val = val * blocks.diagonal(dim1=-1, dim2=-2).abs().max() if n_ent else val
+            ne.leaves[name] = blocks + val * torch.eye(b, dtype=dt)
+            return
         if is_zero:                                                # ZerosMat.dampen_ (bs:510-517)
             blocks = torch.zeros((n_ent, b, b), dtype=dt)
             blocks += dampen * torch.eye(b, dtype=dt)
@@ -179,6 +192,8 @@ def build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=
             per = torch.einsum('nki,nkj->nij', Jb, Jb) if Jb.ndim == 3 else Jb[:, :, None] * Jb[:, None, :]
             blocks = torch.zeros((n_ent, b, b), dtype=dt)
             blocks.index_add_(0, cols, per)                          # bs:919-924
+            if extra is not None:                                    # bs:157-158, before damping
+                blocks += extra.to(dt)
             val = dampen
             if adaptive_dampen:                                      # bs:579-581
                 val = val * blocks.diagonal(dim1=-1, dim2=-2).abs().max() if n_ent else val
@@ -187,7 +202,7 @@ def build_normal_equations(prob, J_cam, J_zcf, J_pts, residuals, w_pts, optim_K=
 
     gram_leaf('foc', J_foc, c_foc, cams.n, 2, zf)
     gram_leaf('tau', J_tau, c_tau, nodes.n, 6, zt)
-    gram_leaf('zcf', Jz, c_zcf, imgs.n, C, zz)
+    gram_leaf('zcf', Jz, c_zcf, imgs.n, C, zz, None if z_prior is None else z_prior[0])
     gram_leaf('pts', Jp, c_pts, trks.n, 3, zp)
     ne.leaf_offsets = dict(foc=0, tau=off_t, zcf=off_z, pts=n_c)
 
