@@ -40,6 +40,8 @@ def main():
                     help='also time the F-sampling kernel on maps of the configuration (1 = yes)')
     ap.add_argument('--layout', type=int, default=1,
                     help='also time the observation-structure edits (old | new merge, remove, plan rebuild)')
+    ap.add_argument('--tangent', type=int, default=1,
+                    help='also time the dense tangent prior on maps of the configuration (1 = yes)')
     ap.add_argument('--copy-probe', action='store_true',
                     help='run a 256 MiB fill and a 256 MiB kernel copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
@@ -143,6 +145,7 @@ def main():
 
     smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
     lay = bench_layout(prob, g, dev, args.steps, args.warmup) if args.layout else None
+    tan = bench_tangent(prob, g, dev, args.steps, args.warmup) if args.tangent else None
 
     cpu = None
     if args.cpu_baseline:
@@ -167,6 +170,7 @@ def main():
         'cpu_baseline': cpu,
         'f_sampling': smp,
         'layout': lay,
+        'tangent_prior': tan,
     }
     print(json.dumps(line), flush=True)
 
@@ -243,6 +247,61 @@ def bench_layout(prob, g, dev, steps, warmup):
             'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
                          'kernel': 'ba_tracks_gather (k_gather_rows + offsets)'},
             'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s}
+
+
+def bench_tangent(prob, g, dev, steps, warmup):
+    """Dense tangent prior (ba_tangent_prior) at the configuration's size: one (384, 512, C) log-depth
+    map and one (384, 512, 3) reference pointmap per frame, stride 4 (engine.py defaults): the
+    fp32 loss of every line-search objective and the fp64 Gauss-Newton terms of every step.  The
+    bare launch sequences are timed with events on their stream.  Algorithmic bytes: the sampled
+    pixels' C + 3 floats (the kernel reads each once; the cache lines around them come along)."""
+    import ctypes
+    from blast3r_amd._lib import BaTangentArgs, check, lib, ptr, stream_ptr
+    H, W, C, s = 384, 512, prob.C, 4
+    n = prob.n_imgs
+    gen = torch.Generator(device=dev).manual_seed(13)
+    yy, xx = torch.meshgrid(torch.arange(H, device=dev, dtype=torch.float32),
+                            torch.arange(W, device=dev, dtype=torch.float32), indexing='ij')
+    plane = 3.0 + 0.004 * xx + 0.003 * yy
+    maps = torch.empty((n, H, W, C), device=dev)
+    maps[..., 0] = torch.log(plane)
+    maps[..., 1:] = 0.05 * torch.rand((n, H, W, C - 1), device=dev, generator=gen)
+    Kc = g.K[0]
+    ray = torch.stack([(xx + 0.5 - Kc[0, 2]) / Kc[0, 0], (yy + 0.5 - Kc[1, 2]) / Kc[1, 1], torch.ones_like(xx)], -1)
+    refs = (ray * plane[..., None]).expand(n, H, W, 3).contiguous()
+    cam_ids = g.infos[2].to(torch.int32).contiguous()
+    Kd = g.K.contiguous()
+    zc = g.z_coefs.contiguous()
+    dep_addr = maps.data_ptr() + torch.arange(n, device=dev, dtype=torch.int64) * (H * W * C * 4)
+    ref_addr = refs.data_ptr() + torch.arange(n, device=dev, dtype=torch.int64) * (H * W * 3 * 4)
+    L, st = lib(), stream_ptr(dev)
+    res = {}
+    for name, gn, fp64 in (('loss_fp32', 0, 0), ('gauss_newton_fp64', 1, 1)):
+        loss = torch.empty((), dtype=torch.float64 if fp64 else torch.float32, device=dev)
+        gz = torch.empty((n, C), dtype=torch.float64, device=dev)
+        hz = torch.empty((n, C, C), dtype=torch.float64, device=dev)
+        nb = int(L.ba_tangent_workspace_bytes(n, C, H, W, s, 1, gn))
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        a = BaTangentArgs(depth_addr=ptr(dep_addr), ref_addr=ptr(ref_addr), map_hw=None, H=H, W=W,
+                          depth_pix_stride=C, ref_pix_stride=3, K=ptr(Kd), cam_ids=ptr(cam_ids), z_coefs=ptr(zc),
+                          n_imgs=n, C=C, tan_stride=s, normalize=1, optim_Z0=1, fp64=fp64, compute_gn=gn, weight=0.5,
+                          eps=1e-4, loss=ptr(loss), g_z=ptr(gz), H_z=ptr(hz), workspace=ptr(ws), workspace_bytes=nb)
+        for _ in range(warmup):
+            check(L.ba_tangent_prior(ctypes.byref(a), st))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            check(L.ba_tangent_prior(ctypes.byref(a), st))
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        pts = n * ((H - s // 2 + s - 1) // s) * ((W - s // 2 + s - 1) // s)
+        gbs = pts * 4 * (C + 3) / (ms * 1e-3) / 1e9
+        res[name] = {'ms': ms, 'grid_points': pts, 'algorithmic_GBps': gbs}
+    log(f"[bench] tangent prior: loss {res['loss_fp32']['ms']:.3f} ms, GN terms {res['gauss_newton_fp64']['ms']:.3f} ms "
+        f"({res['loss_fp32']['grid_points']} grid points, {n} maps of {H}x{W}x{C})")
+    return res
 
 
 def bench_sampling(prob, g, dev, steps, warmup, cfg):

@@ -366,15 +366,23 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
     }
 }
 
-// per image: sum of the tile partials in tile order; g_z, H_z (symmetric, in T) and the loss sums
+// per image: sum of the tile partials in tile order; g_z, H_z (symmetric, in T) and the image's
+// two loss terms weight * mean(w r^2) (x, y; 0 where the reference adds nothing), in T
 template <typename T>
 __global__ void __launch_bounds__(TG_T) k_tan_reduce(ba_tangent_args a, const double* __restrict__ part, int n_tiles,
-                                                      int n_acc, double* __restrict__ img_loss) {
+                                                      int n_acc, T* __restrict__ img_loss) {
     const int img = blockIdx.x, C = a.C;
     for (int j = threadIdx.x; j < n_acc; j += TG_T) {
         double s = 0.0;
         for (int t = 0; t < n_tiles; ++t) s += part[((int64_t)img * n_tiles + t) * n_acc + j];
-        if (j < 2) { img_loss[2 * img + j] = s; continue; }
+        if (j < 2) {
+            const TgImage m = tg_image(a, img);
+            const int64_t np = j == 0 ? (int64_t)(m.Hs - 1) * m.Ws : (int64_t)m.Hs * (m.Ws - 1);
+            T term = 0;
+            if (m.Ws >= 2 && C >= 2 && np > 0) term = (T)a.weight * (T)(s / (3.0 * (double)np));
+            img_loss[2 * img + j] = term;
+            continue;
+        }
         if (!a.compute_gn) continue;
         if (j < 2 + C) {
             const int c = j - 2;
@@ -393,20 +401,22 @@ __global__ void __launch_bounds__(TG_T) k_tan_reduce(ba_tangent_args a, const do
     }
 }
 
-// tan_loss = sum over images, in image order, of weight * mean(w r^2) for x then y (engine.py:132-135)
+// tan_loss = the images' terms added one by one in image order, x then y (engine.py:132-135): the
+// terms are staged through LDS in coalesced chunks and one thread adds them in order
 template <typename T>
-__global__ void k_tan_loss(ba_tangent_args a, const double* __restrict__ img_loss) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+__global__ void __launch_bounds__(TG_T) k_tan_loss(ba_tangent_args a, const T* __restrict__ img_loss) {
+    __shared__ T sT[2 * 1024];
     T loss = 0;
-    const T wt = (T)a.weight;
-    for (int64_t img = 0; img < a.n_imgs; ++img) {
-        const TgImage m = tg_image(a, (int)img);
-        if (m.Ws < 2 || a.C < 2) continue;
-        const int64_t nx = (int64_t)(m.Hs - 1) * m.Ws, ny = (int64_t)m.Hs * (m.Ws - 1);
-        if (nx > 0) loss = loss + wt * (T)(img_loss[2 * img] / (3.0 * (double)nx));
-        if (ny > 0) loss = loss + wt * (T)(img_loss[2 * img + 1] / (3.0 * (double)ny));
+    const int64_t n = 2 * a.n_imgs;
+    for (int64_t c0 = 0; c0 < n; c0 += 2 * 1024) {
+        const int64_t m = n - c0 < 2 * 1024 ? n - c0 : 2 * 1024;
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < m; i += TG_T) sT[i] = img_loss[c0 + i];
+        __syncthreads();
+        if (threadIdx.x == 0)
+            for (int64_t i = 0; i < m; ++i) loss = loss + sT[i];
     }
-    *static_cast<T*>(a.loss) = loss;
+    if (threadIdx.x == 0) *static_cast<T*>(a.loss) = loss;
 }
 
 // planar confidence of one (H, W) fp32 map (engine.py:182-200)
@@ -478,7 +488,13 @@ static void launch_all(const ba_tangent_args& a, const TgLayout& L, char* ws, hi
         hipLaunchKernelGGL(k_tan_median<T>, dim3((unsigned)a.n_imgs), dim3(TG_T), 0, st, a, (uint64_t*)(ws + L.off_keys),
                            L.key_stride, (double*)(ws + L.off_scale));
     if (a.compute_gn) {
-        if (a.C <= 8) {
+        if (a.C <= 4) {
+            if (a.normalize) launch_tiles<T, 4, true, true>(a, L, ws, st);
+            else launch_tiles<T, 4, true, false>(a, L, ws, st);
+        } else if (a.C <= 6) {
+            if (a.normalize) launch_tiles<T, 6, true, true>(a, L, ws, st);
+            else launch_tiles<T, 6, true, false>(a, L, ws, st);
+        } else if (a.C <= 8) {
             if (a.normalize) launch_tiles<T, 8, true, true>(a, L, ws, st);
             else launch_tiles<T, 8, true, false>(a, L, ws, st);
         } else if (a.C <= 12) {
@@ -493,8 +509,8 @@ static void launch_all(const ba_tangent_args& a, const TgLayout& L, char* ws, hi
         else launch_tiles<T, 1, false, false>(a, L, ws, st);
     }
     hipLaunchKernelGGL(k_tan_reduce<T>, dim3((unsigned)a.n_imgs), dim3(TG_T), 0, st, a, (const double*)(ws + L.off_part),
-                       L.n_tiles, L.n_acc, (double*)(ws + L.off_loss));
-    hipLaunchKernelGGL(k_tan_loss<T>, dim3(1), dim3(64), 0, st, a, (const double*)(ws + L.off_loss));
+                       L.n_tiles, L.n_acc, (T*)(ws + L.off_loss));
+    hipLaunchKernelGGL(k_tan_loss<T>, dim3(1), dim3(TG_T), 0, st, a, (const T*)(ws + L.off_loss));
 }
 
 extern "C" int ba_tangent_prior(const ba_tangent_args* args, void* stream) {
