@@ -148,8 +148,9 @@ __device__ __forceinline__ void core_load(const double* __restrict__ rec, int t,
     o.sW[0] = a.y; o.sW[1] = b.x; o.sW[2] = b.y;
 }
 
-// Weighted camera row R, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60).
-template <int HK, int HP, int R, class RowSink>
+// Weighted camera row R, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60);
+// only the columns j in [JLO, JHI) are formed.
+template <int HK, int HP, int R, int JLO = 0, int JHI = 16, class RowSink>
 __device__ __forceinline__ void emit_jc_row(const ObsCore& o, const LinLayout& lay, bool enK, bool enP, bool enZ,
                                             bool first_obs, const DepSrc& dep, RowSink&& sink) {
     constexpr int OT = 2 * HK, OZ = OT + 6 * HP;     // image-level columns [foc | tau | zcf]
@@ -158,7 +159,7 @@ __device__ __forceinline__ void emit_jc_row(const ObsCore& o, const LinLayout& l
     const bool zon = lay.hasZ && enZ;                 // an invalid observation has zscale = 0
     const bool z0off = !lay.optim_Z0 || (first_obs && !lay.optim_Z_1st_cam);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = JLO; j < JHI; ++j) {
         double u = 0.0;
         if (j < OT) {
             u = (R == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(o.J, R, j) * mK;
@@ -366,8 +367,10 @@ __global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double d
 // k_schur: one workgroup (16 waves, four per SIMD) per batch.  Per chunk of 128 observation slots:
 //   A1  waves 0-5, lane per (slot, row r): row r of the weighted camera rows J_c from the slot's
 //       linearisation record (rows 3-5 of the slot's LDS block, column 15 = W r / sqrt(W)) and row
-//       r of the point rows J_p; wave 6, lane per chunk track: Cholesky factor of the damped point
-//       block, its reciprocal pivots and w = L^-1 g_p.
+//       r of the point rows J_p, except the z-coefficient columns of row 2 (the depth row), which
+//       waves 6-7 form, lane per slot; wave 8, lane per chunk track: Cholesky factor of the damped
+//       point block, its reciprocal pivots and w = L^-1 g_p.  (Waves w and w + 4 share a SIMD:
+//       this spreads phase A evenly over the four.)
 //   A2  waves 0-5, lane per (slot, column c): column c of V = J_c^T J_p L^-T (row c of the block,
 //       column 15 = w for the first observation of the track in the image, else 0); several
 //       observations of one track in one image are then summed into the first one.
@@ -479,12 +482,12 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     const int d = a.lay.d, C = a.lay.C;
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // phase A roles: waves 0-5 take one (slot, row) each (slot tid % 128, row tid / 128), wave 6 the
-    // chunk tracks
-    const bool row_lane = tid < 3 * BA_CHUNK;
+    // phase A roles: waves 0-5 take one (slot, row) each (slot tid % 128, row tid / 128), waves 6-7
+    // the z-coefficient columns of row 2 (rr = 3), wave 8 the chunk tracks
+    const bool row_lane = tid < 4 * BA_CHUNK;
     const int t = tid & (BA_CHUNK - 1), rr = tid >> 7;
-    const bool trk_wave = wave == 6;
-    static_assert(BA_WAVES >= 7, "phase A needs seven waves");
+    const bool trk_wave = wave == 8;
+    static_assert(BA_WAVES >= 9, "phase A needs nine waves");
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
     const double lam = a.lam_p[0];
@@ -551,16 +554,21 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                     emit_jc_row<HK, HP, 1>(o, a.lay, eK, eP, eZ, first, dep, sink);
                     blk[15] = o.Rs[1];
                     point_row<1>(o, sCam[li], xon, jp);
-                } else {
+                } else if (rr == 2) {
+                    emit_jc_row<HK, HP, 2, 0, 2 * HK + 6 * HP>(o, a.lay, eK, eP, eZ, first, dep, sink);
+                    blk[15] = o.Rs[2];
+                    point_row<2>(o, sCam[li], xon, jp);
+                } else {                                   // rr = 3: row 2's z-coefficient columns
+                    double* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
+                    auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? v : 0.0; };
 #pragma unroll
                     for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = c < C ? sSt.dep[c][t] : 0.f;
                     dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + t) * C;
-                    emit_jc_row<HK, HP, 2>(o, a.lay, eK, eP, eZ, first, dep, sink);
-                    blk[15] = o.Rs[2];
-                    point_row<2>(o, sCam[li], xon, jp);
+                    emit_jc_row<HK, HP, 2, 2 * HK + 6 * HP, 15>(o, a.lay, eK, eP, eZ, first, dep, sink2);
                 }
+                if (rr < 3)
 #pragma unroll
-                for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
+                    for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
             }
             if (rr == 0) {
                 const uint64_t dup = __ballot(valid && leader != t);
@@ -589,7 +597,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         __syncthreads();
 
         // ---------------- A2: V = J_c^T P with P = J_p L^-T; lane (slot, rr) forms column c = rr
-        if (row_lane && valid) {
+        if (row_lane && rr < 3 && valid) {
             const int c = rr;
             const TrkStage& T = sTS[ct];
             const double l10 = T.L[1], l20 = T.L[2], l21 = T.L[4], r0 = T.rp[0], r1 = T.rp[1], r2 = T.rp[2];
@@ -612,7 +620,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         __syncthreads();
         if (sDup[0] | sDup[1]) {
             // several observations of one track in one image: V of the run is summed into its first slot
-            if (row_lane && valid && leader == t) {             // lane (slot, rr): V row rr
+            if (row_lane && rr < 3 && valid && leader == t) {   // lane (slot, rr): V row rr
                 double* dst = sBlk + t * BA_BLK + 16 * rr;
                 for (int f = t + 1; f < BA_CHUNK; ++f) {
                     const int fi = sInfo[f];
