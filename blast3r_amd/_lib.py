@@ -53,7 +53,7 @@ _LIN_FIELDS = [
     ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p),
     ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
     ('ct_pt', c_p), ('n_ctracks', c_i64), ('core', c_p),
-    ('chunk_slots', c_p), ('chunk_ent', c_p), ('chunk_eptr', c_p), ('b_pos_slot', c_p),
+    ('chunk_slots', c_p), ('chunk_ent', c_p), ('chunk_eptr', c_p), ('b_pos_slot', c_p), ('pfac', c_p),
 ]
 
 

@@ -226,6 +226,7 @@ class GaussNewtonSolver:
         Hpp = ws('Hpp', (max(n_ct, 1), 6), torch.float64)          # chunk-track order
         gp = ws('gp', (max(n_ct, 1), 3), torch.float64)
         ct_pt = ws('ct_pt', (max(n_ct, 1), 4), torch.float32)
+        pfac = ws('pfac', (max(n_ct, 1), 12), torch.float64)
         core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)   # linearisation records
         chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), torch.float64)
         lam_p = ws('lam_p', (1,), torch.float64)
@@ -269,7 +270,7 @@ class GaussNewtonSolver:
         L_.adaptive = int(bool(self.adaptive_dampen))
         L_.x_off = int(not en['X'][0])
         a.Hpp, a.gp, a.chunk_max, a.lam_p = ptr(Hpp), ptr(gp), ptr(chunk_max), ptr(lam_p)
-        a.ct_pt, a.n_ctracks, a.core = ptr(ct_pt), n_ct, ptr(core)
+        a.ct_pt, a.n_ctracks, a.core, a.pfac = ptr(ct_pt), n_ct, ptr(core), ptr(pfac)
         a.partials, a.img_partials = ptr(partials), ptr(img_partials)
         a.n_chunks, a.n_batches, a.n_pairs = sc['n_chunks'], sc['n_batches'], sc['n_pairs']
         a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)

@@ -362,15 +362,38 @@ __global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double d
     out[0] = (adaptive && !x_off) ? dampen * cmax[n] : dampen;
 }
 
+// Point factors of every chunk track once the damping value is known: L = chol(H_pp + lam_p I) with
+// the chol3x3_solve rules, w = L^-1 g_p and the reciprocal pivots, 12 doubles per chunk track
+// (L0..L5 | w0 w1 w2 | 1/L0 1/L3 1/L5), read by the camera-pair kernel two doubles per copy.
+__global__ void __launch_bounds__(256) k_point_factor(const double* __restrict__ Hpp, const double* __restrict__ gp,
+                                                      const double* __restrict__ lam_p, int64_t n_ct,
+                                                      double* __restrict__ pf) {
+    const int64_t ct = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (ct >= n_ct) return;
+    double H[6], Lf[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) H[k] = Hpp[6 * ct + k];
+    chol3_factor(H, lam_p[0], Lf);
+    const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
+    const double g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
+    const double w0 = g0 * r0;
+    const double w1 = (g1 - Lf[1] * w0) * r1;
+    const double w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
+    double* o = pf + 12 * ct;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) o[k] = Lf[k];
+    o[6] = w0; o[7] = w1; o[8] = w2;
+    o[9] = r0; o[10] = r1; o[11] = r2;
+}
+
 // ----------------------------------------------------------------------------- camera-pair blocks
 //
 // k_schur: one workgroup (16 waves, four per SIMD) per batch.  Per chunk of 128 observation slots:
 //   A1  waves 0-5, lane per (slot, row r): row r of the weighted camera rows J_c from the slot's
 //       linearisation record (rows 3-5 of the slot's LDS block, column 15 = W r / sqrt(W)) and row
 //       r of the point rows J_p, except the z-coefficient columns of row 2 (the depth row), which
-//       waves 6-7 form, lane per slot; wave 8, lane per chunk track: Cholesky factor of the damped
-//       point block, its reciprocal pivots and w = L^-1 g_p.  (Waves w and w + 4 share a SIMD:
-//       this spreads phase A evenly over the four.)
+//       waves 6-7 form, lane per slot (waves w and w + 4 share a SIMD: this spreads phase A evenly
+//       over the four).  The point blocks' Cholesky factors come precomputed (k_point_factor).
 //   A2  waves 0-5, lane per (slot, column c): column c of V = J_c^T J_p L^-T (row c of the block,
 //       column 15 = w for the first observation of the track in the image, else 0); several
 //       observations of one track in one image are then summed into the first one.
@@ -394,13 +417,6 @@ __device__ __forceinline__ uint64_t uni64(uint64_t x) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// per chunk track in LDS, written by the factorisation
-struct TrkStage {
-    double L[6];                // Cholesky factor of the damped point block (upper storage order)
-    double w[3];                // L^-1 g_p
-    double rp[3];               // reciprocal pivots
-};
-
 // The next chunk's inputs are copied straight into LDS staging arrays while the current chunk's
 // MFMAs run (global_load_lds: lane l of the issuing wave writes dst + 4 l or dst + 16 l; dst is
 // uniform),
@@ -419,8 +435,7 @@ struct Staging {                // one chunk's inputs, laid out as the copies wr
     int info[BA_CHUNK];                     // slot_info per slot
     int obs[BA_CHUNK];                      // chunk_obs per slot
     float dep[BA_PRE_C][BA_CHUNK];          // depth guidance channels c < min(C, BA_PRE_C)
-    double H[3][BA_MAX_CT][2];              // H_pp upper of each chunk track, 16 bytes per copy
-    int g[6][BA_MAX_CT];                    // g_p, as 6 dwords
+    double pf[6][BA_MAX_CT][2];             // point factors of each chunk track (L | w | 1/pivots), 16 bytes per copy
     float4 X[BA_MAX_CT];                    // point, enable flag
 };
 
@@ -445,9 +460,7 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
         int64_t ct = (int64_t)first_ct + lane;
         ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) dma16_to_lds(a.Hpp + 6 * ct + 2 * k, &S.H[k][0][0]);
-#pragma unroll
-        for (int k = 0; k < 6; ++k) dma4_to_lds(reinterpret_cast<const int*>(a.gp + 3 * ct) + k, S.g[k]);
+        for (int k = 0; k < 6; ++k) dma16_to_lds(a.pfac + 12 * ct + 2 * k, &S.pf[k][0][0]);
         dma16_to_lds(a.ct_pt + 4 * ct, S.X);
         if (lane == 0) *sNct = a.chunk_meta[4 * ck + 2];
     } else if (wave == 3) {
@@ -465,7 +478,6 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
 template <int HK, int HP>
 __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks + zero block
-    __shared__ TrkStage sTS[BA_MAX_CT];                  // per chunk track
     __shared__ Staging sSt;                              // this chunk's inputs (the next chunk's, in phase B)
     __shared__ double sJp[BA_CHUNK][9];                  // weighted point rows J_p of each slot
     __shared__ double sDv[BA_MAX_LOCAL][16];             // per local image: diag(J_c^T J_c)
@@ -483,14 +495,12 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     const int batch = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // phase A roles: waves 0-5 take one (slot, row) each (slot tid % 128, row tid / 128), waves 6-7
-    // the z-coefficient columns of row 2 (rr = 3), wave 8 the chunk tracks
+    // the z-coefficient columns of row 2 (rr = 3)
     const bool row_lane = tid < 4 * BA_CHUNK;
     const int t = tid & (BA_CHUNK - 1), rr = tid >> 7;
-    const bool trk_wave = wave == 8;
-    static_assert(BA_WAVES >= 9, "phase A needs nine waves");
+    static_assert(BA_WAVES >= 8, "phase A needs eight waves");
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
-    const double lam = a.lam_p[0];
     const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
     int first_ct = a.chunk_meta[4 * c_begin + 1];
 
@@ -537,7 +547,19 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         const int li = info & 0xff, ct = (info >> 8) & 0xff, leader = info >> 16;
         if (row_lane) {
             if (rr == 0) sInfo[t] = info;
-            if (valid) {
+            if (valid && rr == 3) {                        // row 2's z-coefficient columns: zscale, sqrt(W_2)
+                ObsCore o;
+                o.J.zscale = sSt.rec[14 * BA_CHUNK + t];
+                o.sW[2] = reinterpret_cast<const float2*>(sSt.rec)[19 * BA_CHUNK + t].y;
+                const bool eZ = sEn[3 * li + 2] != 0, first = sSt.obs[t] == 0;
+                double* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
+                auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? v : 0.0; };
+                DepSrc dep;
+#pragma unroll
+                for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = c < C ? sSt.dep[c][t] : 0.f;
+                dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + t) * C;
+                emit_jc_row<HK, HP, 2, 2 * HK + 6 * HP, 15>(o, a.lay, true, true, eZ, first, dep, sink2);
+            } else if (valid) {
                 ObsCore o;
                 core_load(sSt.rec, t, o);
                 const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
@@ -554,44 +576,17 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                     emit_jc_row<HK, HP, 1>(o, a.lay, eK, eP, eZ, first, dep, sink);
                     blk[15] = o.Rs[1];
                     point_row<1>(o, sCam[li], xon, jp);
-                } else if (rr == 2) {
+                } else {
                     emit_jc_row<HK, HP, 2, 0, 2 * HK + 6 * HP>(o, a.lay, eK, eP, eZ, first, dep, sink);
                     blk[15] = o.Rs[2];
                     point_row<2>(o, sCam[li], xon, jp);
-                } else {                                   // rr = 3: row 2's z-coefficient columns
-                    double* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
-                    auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? v : 0.0; };
-#pragma unroll
-                    for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = c < C ? sSt.dep[c][t] : 0.f;
-                    dep.g = a.s_dep + ((int64_t)ck * BA_CHUNK + t) * C;
-                    emit_jc_row<HK, HP, 2, 2 * HK + 6 * HP, 15>(o, a.lay, eK, eP, eZ, first, dep, sink2);
                 }
-                if (rr < 3)
 #pragma unroll
-                    for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
+                for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
             }
             if (rr == 0) {
                 const uint64_t dup = __ballot(valid && leader != t);
                 if (lane == 0) sDup[wave] = dup != 0;
-            }
-        } else if (trk_wave) {
-            TrkStage& T = sTS[lane];
-            if (lane < n_ct) {
-                double H[6], Lf[6], gv[3];
-#pragma unroll
-                for (int k = 0; k < 6; ++k) H[k] = sSt.H[k >> 1][lane][k & 1];
-#pragma unroll
-                for (int k = 0; k < 3; ++k)
-                    gv[k] = __hiloint2double(sSt.g[2 * k + 1][lane], sSt.g[2 * k][lane]);
-                chol3_factor(H, lam, Lf);
-                const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
-                const double w0 = gv[0] * r0;
-                const double w1 = (gv[1] - Lf[1] * w0) * r1;
-                const double w2 = (gv[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
-#pragma unroll
-                for (int k = 0; k < 6; ++k) T.L[k] = Lf[k];
-                T.rp[0] = r0; T.rp[1] = r1; T.rp[2] = r2;
-                T.w[0] = w0; T.w[1] = w1; T.w[2] = w2;
             }
         }
         __syncthreads();
@@ -599,8 +594,10 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         // ---------------- A2: V = J_c^T P with P = J_p L^-T; lane (slot, rr) forms column c = rr
         if (row_lane && rr < 3 && valid) {
             const int c = rr;
-            const TrkStage& T = sTS[ct];
-            const double l10 = T.L[1], l20 = T.L[2], l21 = T.L[4], r0 = T.rp[0], r1 = T.rp[1], r2 = T.rp[2];
+            const double (*F)[BA_MAX_CT][2] = sSt.pf;          // element i of track ct at F[i / 2][ct][i % 2]
+            const double l10 = F[0][ct][1], l20 = F[1][ct][0], l21 = F[2][ct][0];
+            const double r0 = F[4][ct][1], r1 = F[5][ct][0], r2 = F[5][ct][1];
+            const double wc = c == 0 ? F[3][ct][0] : (c == 1 ? F[3][ct][1] : F[4][ct][0]);
             double Pc[3];
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
@@ -615,7 +612,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 const double j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
                 blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : 0.0;
             }
-            blk[16 * c + 15] = leader == t ? T.w[c] : 0.0;
+            blk[16 * c + 15] = leader == t ? wc : 0.0;
         }
         __syncthreads();
         if (sDup[0] | sDup[1]) {
@@ -867,6 +864,11 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
         }
         hipLaunchKernelGGL(k_lam_final, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen, a.lay.adaptive,
                            a.lay.x_off, a.lam_p);
+        if (a.n_chunks > 0) {
+            BA_REQUIRE(a.pfac != nullptr, "point-factor scratch missing");
+            hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
+                               a.n_ctracks, a.pfac);
+        }
         BA_LAUNCHED();
         return BA_OK;
     }

@@ -127,6 +127,8 @@ typedef struct {
     double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0) */
     const int32_t *chunk_slots, *chunk_ent, *chunk_eptr;   /* plan: MFMA entry lists of every chunk */
     const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
+    double* pfac;         /* (n_ctracks,12) scratch written by stage 0: Cholesky factor L of H_pp + lam_p I
+                             (upper storage), w = L^-1 g_p, reciprocal pivots */
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.
