@@ -245,7 +245,8 @@ def bench_layout(prob, g, dev, steps, warmup):
         f'remove 1% {remove_ms:.2f} ms, plan rebuild {plan_s:.3f} s')
     return {'gather_ms': ms, 'rows': n_rows, 'bytes_per_row': 2 * (20 + 4 * C),
             'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
-                         'kernel': 'ba_tracks_gather (k_gather_rows + offsets)'},
+                         'kernel': 'ba_tracks_gather (k_gather_rows + offsets)',
+                         'traffic': measured_traffic(2, 'k_gather_rows')[0] if prob.n_imgs == 1024 else None},
             'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s}
 
 
@@ -298,7 +299,8 @@ def bench_tangent(prob, g, dev, steps, warmup):
         ms = e0.elapsed_time(e1) / steps
         pts = n * ((H - s // 2 + s - 1) // s) * ((W - s // 2 + s - 1) // s)
         gbs = pts * 4 * (C + 3) / (ms * 1e-3) / 1e9
-        res[name] = {'ms': ms, 'grid_points': pts, 'algorithmic_GBps': gbs}
+        traffic = measured_traffic(2, 'k_tan_tile_gn' if gn else 'k_tan_tile_loss')[0] if n == 1024 else None
+        res[name] = {'ms': ms, 'grid_points': pts, 'algorithmic_GBps': gbs, 'traffic_per_launch': traffic}
     log(f"[bench] tangent prior: loss {res['loss_fp32']['ms']:.3f} ms, GN terms {res['gauss_newton_fp64']['ms']:.3f} ms "
         f"({res['loss_fp32']['grid_points']} grid points, {n} maps of {H}x{W}x{C})")
     return res
