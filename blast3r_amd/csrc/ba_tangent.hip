@@ -11,7 +11,9 @@
 // Gauss-Newton terms g = sum scale w J^T r, H = sum scale w J^T J w.r.t. the image's
 // z-coefficients, scale = weight / (3 n_pairs) of the direction.
 //
-// Layout: one workgroup per (image, tile of TG_TR x TG_TC pair origins).  The tile's points and
+// Layout: one workgroup per (image, tile of TR x TG_TC pair origins; TR = 16 rows for the loss alone,
+// 8 with the Gauss-Newton terms, 4 with more than 8 coefficients; each thread takes TR x TG_TC / 256
+// origins).  The tile's points and
 // the row / column after it are computed once into LDS (X, X0, Cw, the channel values), the depth
 // halo the planar confidence needs is staged before that; each thread then takes one origin and
 // its x and y pairs.  The derivative of a pair difference is rank two in the channel values:
@@ -34,13 +36,13 @@
 namespace ba {
 
 #define TG_T 256
-#define TG_TR 4
-#define TG_TC 64
-#define TG_RR (TG_TR + 1)
+#define TG_TC 64                // tile columns (pair origins)
 #define TG_RC (TG_TC + 1)
-#define TG_HR (TG_TR + 3)
 #define TG_HC (TG_TC + 3)
 #define TG_CMAX 16
+// tile rows: 16 for the loss alone, 8 with the Gauss-Newton terms, 4 with more than 8 coefficients
+// (the channel values then fill LDS)
+template <int CMAX, bool GN> struct TgRows { static constexpr int TR = !GN ? 16 : (CMAX > 8 ? 4 : 8); };
 
 static inline int64_t tg_div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline int64_t tg_align(int64_t b) { return (b + 255) & ~int64_t(255); }
@@ -189,6 +191,7 @@ template <typename T, int CMAX, bool GN, bool NORM>
 __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const double* __restrict__ scale,
                                                     double* __restrict__ part, int n_tc, int n_acc) {
     constexpr int E = CMAX * (CMAX + 1) / 2;
+    constexpr int TG_TR = TgRows<CMAX, GN>::TR, TG_RR = TG_TR + 1, TG_HR = TG_TR + 3;
     __shared__ float sD0[TG_HR][TG_HC];
     __shared__ T sX[3][TG_RR * TG_RC];
     __shared__ float sX0[3][TG_RR * TG_RC];
@@ -264,11 +267,13 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
 #pragma unroll
         for (int e = 0; e < E; ++e) Hacc[e] = 0.0;
     }
-    const int tr = threadIdx.x / TG_TC, tc = threadIdx.x - tr * TG_TC;
-    const int gr = tr0 + tr, gc = tc0 + tc;
-    const int p = tr * TG_RC + tc;
     const float eps_f = (float)a.eps;
     const T eps_t = (T)a.eps;
+#pragma unroll 1
+    for (int po = threadIdx.x; po < TG_TR * TG_TC; po += TG_T) {
+    const int tr = po / TG_TC, tc = po - tr * TG_TC;
+    const int gr = tr0 + tr, gc = tc0 + tc;
+    const int p = tr * TG_RC + tc;
 #pragma unroll 1
     for (int dir = 0; dir < 2; ++dir) {
         const bool ok = dir == 0 ? (gr + 1 < m.Hs && gc < m.Ws) : (gr < m.Hs && gc + 1 < m.Ws);
@@ -329,6 +334,7 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
                 for (int d2 = c; d2 < CMAX; ++d2) Hacc[c * CMAX - c * (c - 1) / 2 + (d2 - c)] += s1 * al[d2] + s2 * be[d2];
             }
         }
+    }
     }
     // block sums in a fixed order: waves by butterfly, then the wave sums in wave order
     auto bsum = [&](double v) -> double {
@@ -453,10 +459,15 @@ struct TgLayout {
     int64_t off_scale, off_keys, off_part, off_loss, total;
 };
 
+// tile rows of the kernel instantiation chosen for C (see launch_all)
+static int tg_tile_rows(int C, int compute_gn) {
+    return !compute_gn ? TgRows<1, false>::TR : (C > 8 ? TgRows<16, true>::TR : TgRows<8, true>::TR);
+}
+
 static TgLayout tg_layout(int64_t n_imgs, int C, int H, int W, int s, int normalize, int compute_gn) {
     TgLayout L;
     const int Hs = grid_len(H, s), Ws = grid_len(W, s);
-    L.n_tr = (int)tg_div_up(Hs > 0 ? Hs : 1, TG_TR);
+    L.n_tr = (int)tg_div_up(Hs > 0 ? Hs : 1, tg_tile_rows(C, compute_gn));
     L.n_tc = (int)tg_div_up(Ws > 0 ? Ws : 1, TG_TC);
     L.n_tiles = L.n_tr * L.n_tc;
     L.n_acc = 2 + (compute_gn ? C + C * (C + 1) / 2 : 0);
