@@ -5,7 +5,10 @@ Tolerances (norm-wise relative, ||gpu - oracle|| / ||oracle||):
   * fp64 Jacobian blocks: 1e-9 (same fp64 formula from the same fp32 inputs)
   * reduced-system blocks S, rhs, point blocks: 1e-5 (fp64, differences come from the
     fp32 residual/weight rounding of logf/powf on either side)
-  * PCG step and LM update: 1e-4 on delta and on J.delta (the north-star step tolerance)
+  * PCG step and LM update: 1e-4 on delta and on J.delta (the north-star step tolerance), widened
+    to 5x the oracle's own spread under a change of summation order where the system's conditioning
+    leaves the stopped PCG's step that loose (test_pcg_step_parity), and to 4x the spread between
+    tol 1e-6 and a tightly converged solve for lm_step
 """
 import pytest
 import torch
@@ -129,6 +132,11 @@ def _oracle_ne(p, **flags):
     return ne, gvec, params, (Jc, Jz, Jp), res, w
 
 
+def _cfg_flags(p):
+    """The configuration's own optimisation flags (config 4 keeps K and P fixed)."""
+    return {k: p.options[k] for k in ('optim_K', 'optim_P') if not p.options.get(k, True)}
+
+
 def _gpu_solver(p, **flags):
     g = _gpu(p)
     o = opts(p)
@@ -147,14 +155,14 @@ def _gpu_solver(p, **flags):
     return gs, delta, g
 
 
-@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 8, 200), (2, 20, 400)])
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 8, 200), (1, 32, 400), (2, 20, 400), (3, 24, 600), (4, 12, 300)])
 def test_reduced_system_parity(cfg, nf, nt):
     """S = H_cc - H_cp H_pp^-1 H_pc (damped, reference unknown order) and rhs against the oracle."""
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
-    ne, gvec, params, _, _, _ = _oracle_ne(p)
+    ne, gvec, params, _, _, _ = _oracle_ne(p, **_cfg_flags(p))
     S_ref = osol.dense_schur(ne)
     rhs_ref = osol.reduced_rhs(ne, gvec)
-    gs, delta, _ = _gpu_solver(p)
+    gs, delta, _ = _gpu_solver(p, **_cfg_flags(p))
     S, rhs = gs.reduced_system_dense()
     assert S.shape == S_ref.shape
     assert rel_err(S, S_ref) < 1e-5
@@ -169,24 +177,54 @@ def test_reduced_system_parity(cfg, nf, nt):
     assert rel_err(H, Hr6) < 1e-5
 
 
-@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (2, 24, 800)])
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (1, 32, 400), (2, 24, 800), (3, 24, 600),
+                                        (4, 12, 300)])
 def test_pcg_step_parity(cfg, nf, nt):
-    """delta from the device PCG against the oracle restatement of _pcg (same iterations)."""
+    """delta from the device PCG against the oracle restatement of _pcg (same iterations).
+
+    A PCG stopped at ||r|| <= 1e-6 ||b|| (or at maxiter) fixes the step only up to its rounding on an
+    ill-conditioned system.  The oracle's own sensitivity is measured by running the same iteration
+    with the operator applied as a dense matrix (same mathematics, another summation order, also its
+    symmetrised form): the device step must agree with the oracle to max(1e-4, 5 x that spread) on
+    delta and on J.delta.  A converged device solve must meet the stopping test on the oracle's S
+    (to 2x, since it stopped on its own rounding of S) within 5% of the oracle's iteration count (at
+    least 2: config 4's oracle count moves between 151 and 155 with the summation order); one stopped
+    at maxiter must reach the oracle's reduced residual.  On well-conditioned cases (configs 0, 2, 3)
+    the spread is below 1e-5 and the bar is the plain 1e-4; config 1 stops at maxiter (condition
+    number ~1e11) and config 4's step moves by ~5e-3 between summation orders.
+    """
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
-    ne, gvec, params, (Jc, Jz, Jp), res, w = _oracle_ne(p)
+    fl = _cfg_flags(p)
+    ne, gvec, params, (Jc, Jz, Jp), res, w = _oracle_ne(p, **fl)
     d_ref, it_ref, conv_ref = osol.solve_reduced_pcg(ne, gvec)
-    gs, delta, _ = _gpu_solver(p)
+    gs, delta, _ = _gpu_solver(p, **fl)
     ist = gs.last['istate'].cpu()
     assert int(ist[3]) == int(conv_ref)
-    if conv_ref:
-        assert abs(int(ist[2]) - it_ref) <= 2
-    d_ref32 = d_ref.to(torch.float32)
-    assert rel_err(delta, d_ref32) < 1e-4
-    # gauge-invariant check: the predicted residual change J.delta
     from oracle.dense import dense_jacobian
     Jd = dense_jacobian(Jc, Jz, Jp, p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks)
     sW = w.clamp(1e-6, 1e6).reshape(-1).double().sqrt()
-    assert rel_err(sW[:, None] * Jd @ delta.cpu().double(), sW[:, None] * Jd @ d_ref) < 1e-4
+    Jdelta = lambda d: sW[:, None] * Jd @ d.cpu().double()
+    # the oracle's spread under a change of summation order of the same operator
+    n_c = ne.sizes['n_c']
+    S = osol.dense_schur(ne)
+    rhs = osol.reduced_rhs(ne, gvec)
+    diagA = osol.A_diag(ne).clamp(min=1e-12)
+    alts = []
+    for Sx in (S, 0.5 * (S + S.T)):
+        dc, _, _ = osol.pcg(lambda v: Sx @ v, rhs, M_mv=lambda v: v / diagA, tol=1e-6, maxiter=300)
+        alts.append(torch.cat([dc, osol._D_solve(ne, gvec[n_c:] - osol._C_matvec(ne, dc))]))
+    tol_d = max([1e-4] + [5 * rel_err(d, d_ref) for d in alts])
+    tol_j = max([1e-4] + [5 * rel_err(Jdelta(d), Jdelta(d_ref)) for d in alts])
+    red = lambda dc: float((rhs - S @ dc).norm() / rhs.norm())
+    if conv_ref:
+        assert abs(int(ist[2]) - it_ref) <= max(2, 0.05 * it_ref), (int(ist[2]), it_ref)
+        assert red(delta[:n_c].cpu().double()) <= 2e-6
+    else:
+        r_ref = max([red(d_ref[:n_c])] + [red(d[:n_c]) for d in alts])
+        assert red(delta[:n_c].cpu().double()) <= 1.5 * r_ref
+    assert rel_err(delta, d_ref.to(torch.float32)) < tol_d, (rel_err(delta, d_ref.to(torch.float32)), tol_d)
+    # gauge-invariant check: the predicted residual change J.delta
+    assert rel_err(Jdelta(delta), Jdelta(d_ref)) < tol_j
 
 
 def _device_pcg_dense(A, b, tol, maxiter, d):
@@ -312,7 +350,7 @@ def test_solver_flags_parity():
         assert rel_err(delta, d_ref.to(torch.float32)) < 1e-4, flags
 
 
-@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 30, 1500), (4, 20, 800)])
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800)])
 def test_lm_step_parity(cfg, nf, nt):
     """Full lm_step against the oracle.
 
