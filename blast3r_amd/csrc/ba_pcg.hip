@@ -17,9 +17,13 @@
 namespace ba {
 
 #define PCG_T 256
-#define PCG_ST 512          // threads of the image-row SpMV: 32 groups of 16 lanes
+// threads of the image-row SpMV: 8 groups of 16 lanes.  Two waves per row keep every row of a
+// 1024-image system resident at once (the kernel needs ~112 VGPRs: 4 waves per SIMD).
+#define PCG_ST 128
 // Block partials of the update launch (nb blocks): r.r and r.z, PCG_NP per block.
 #define PCG_NP 2
+#define PCG_LF 16           // entries of a long inverse list each lane has in flight
+#define PCG_IPF 4           // image partials of p.Ap each update thread requests at launch
 enum { PT_RR = 0, PT_RZ = 1 };
 
 // state (fp64): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
@@ -207,18 +211,30 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 // flag "stopped before update n" lives in IS_DONE0 + (n & 1) and is written by k_pcg_spmv(n - 1).
 
 // y_img[i][j] = sum over the blocks of image row i of S(i, i2)[j, :] . p(i2): one workgroup of
-// PCG_ST threads per image row; its 32 lane groups (one lane per row j) take every 32nd block of
-// the row.  Lane j2 of a group forms p_n at the block's column unknown j2 and the group shares the
+// PCG_ST threads per image row; its PCG_ST / 16 lane groups (one lane per row j) take every
+// (PCG_ST / 16)-th block of the row.  Lane j2 of a group forms p_n at the block's column unknown j2 and the group shares the
 // 16 values by shuffles; the group sums are added in LDS in a fixed order.  The operands of the
-// first pass are requested before the scalar decisions, which only need the partial sums.
+// first pass, the row's own unknowns and the partial sums are requested before any of them is used.
 __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int nb) {
     __shared__ double sh[PCG_ST];
     __shared__ double sDamp[PCG_ST / 64];
     const int i = blockIdx.x;
     const int grp = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int d = a.d, dd = d * d;
-    const int q0 = a.row_ptr[i], q1 = a.row_ptr[i + 1];
     const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
+    // operands that depend on nothing are requested first: each thread's first block partials of
+    // update n - 1, the scalar state, and (threads 0..d-1) the row's own unknowns with z and p_{n-1}
+    double pr0 = 0.0, pr1 = 0.0;
+    if (threadIdx.x < nb) { pr0 = a.partials[PCG_NP * threadIdx.x + PT_RR]; pr1 = a.partials[PCG_NP * threadIdx.x + PT_RZ]; }
+    const double best = a.state[ST_BEST0 + ((n - 1) & 1)], rz_old = a.state[ST_RZ0 + ((n - 1) & 1)];
+    const double bnorm = a.state[ST_BNORM];
+    int uo = -1;
+    double zo = 0.0, po = 0.0;
+    if (threadIdx.x < 16 && j < d) {
+        uo = a.umap[(int64_t)i * d + j];
+        if (uo >= 0) { zo = a.z[uo]; po = pold[uo]; }
+    }
+    const int q0 = a.row_ptr[i], q1 = a.row_ptr[i + 1];
     auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[16]) {
         const bool live = q < q1;
         u = live ? a.row_u[(int64_t)q * 16 + j] : -1;
@@ -249,16 +265,16 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     double beta = 0.0;
     if (n >= 1) {
         // end of update n - 1 (ba_solver.py:1222-1236)
-        double rs[2];
-        sum_partials<PCG_ST>(a.partials, nb, rs, sh);
+        double rs[2] = {0.0, 0.0};
+        if (threadIdx.x < nb) { rs[0] += pr0; rs[1] += pr1; }     // the order of sum_partials
+        for (int b = threadIdx.x + PCG_ST; b < nb; b += PCG_ST) { rs[0] += a.partials[PCG_NP * b + PT_RR]; rs[1] += a.partials[PCG_NP * b + PT_RZ]; }
+        block_sums<PCG_ST, 2>(rs, sh);
         const double rr = rs[0], rz_new = rs[1];
         const double rnorm = sqrt(rr);
-        const double best = a.state[ST_BEST0 + ((n - 1) & 1)];
         const bool improved = rnorm < best;
-        const bool conv = rnorm <= a.tol * a.state[ST_BNORM];
+        const bool conv = rnorm <= a.tol * bnorm;
         const bool bad = !isfinite(rz_new);
         const bool stop = conv || bad || n >= a.maxiter;
-        const double rz_old = a.state[ST_RZ0 + ((n - 1) & 1)];
         beta = rz_new / (rz_old > 1e-32 ? rz_old : 1e-32);
         if (improved)                                    // best_so_far = r_norm, x, k
             for (int64_t v = (int64_t)blockIdx.x * PCG_ST + threadIdx.x; v < a.n_u; v += (int64_t)gridDim.x * PCG_ST)
@@ -287,7 +303,7 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
         dsum = wave_sum(dsum);
     }
     double acc = mac(u, zv, pv, beta, bcol, 0.0);
-    for (int qb = q0 + PCG_ST / 16; qb < q1; qb += PCG_ST / 16) {     // rows longer than 32 blocks
+    for (int qb = q0 + PCG_ST / 16; qb < q1; qb += PCG_ST / 16) {     // the row's further blocks
         load(qb + grp, u, zv, pv, bcol);
         acc = mac(u, zv, pv, beta, bcol, acc);
     }
@@ -303,8 +319,7 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
             double t = 0.0;
             for (int g = 0; g < PCG_ST / 16; ++g) t += sh[16 * g + j];
             a.y_img[(int64_t)i * d + j] = t;
-            const int uo = a.umap[(int64_t)i * d + j];
-            if (uo >= 0) part = pdir(a.z[uo], pold[uo], beta) * t;
+            if (uo >= 0) part = pdir(zo, po, beta) * t;
         }
         part = wave_sum(part);
         if (threadIdx.x == 0) {
@@ -324,6 +339,14 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
 __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
     __shared__ double sh[2 * (PCG_T / 64)];
     __shared__ double sLong[PCG_T];
+    // requested first: the image partials of p.Ap (the first PCG_IPF of each thread) and the scalars
+    double ipf[PCG_IPF];
+#pragma unroll
+    for (int k = 0; k < PCG_IPF; ++k) {
+        const int b = threadIdx.x + k * PCG_T;
+        ipf[k] = b < a.n_imgs ? a.img_part[b] : 0.0;
+    }
+    const double beta = a.state[ST_BETA], rz = a.state[ST_RZ0 + (n & 1)];
     if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
@@ -339,12 +362,12 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
         const int v = a.long_u[k];
         const int b0 = a.inv_ptr[v], b1 = a.inv_ptr[v + 1];
         double s = 0.0;
-        for (int q = b0 + lane; q < b1; q += 64 * 8) {
-            int src[8];
+        for (int q = b0 + lane; q < b1; q += 64 * PCG_LF) {
+            int src[PCG_LF];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) src[t] = q + 64 * t < b1 ? a.inv_src[q + 64 * t] : -1;
+            for (int t = 0; t < PCG_LF; ++t) src[t] = q + 64 * t < b1 ? a.inv_src[q + 64 * t] : -1;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
+            for (int t = 0; t < PCG_LF; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
         }
         s = wave_sum(s);
         if (lane == 0) sLong[k - lk0] = s;
@@ -353,13 +376,15 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
     double ys = 0.0;
     if (li < 0)
         for (int q = q0; q < q1; ++q) ys += a.y_img[a.inv_src[q]];
-    const double beta = a.state[ST_BETA];
     double sums[1] = {0.0};
-    for (int b = threadIdx.x; b < a.n_imgs; b += PCG_T) sums[0] += a.img_part[b];
+#pragma unroll
+    for (int k = 0; k < PCG_IPF; ++k)
+        if (threadIdx.x + k * PCG_T < a.n_imgs) sums[0] += ipf[k];
+    for (int b = threadIdx.x + PCG_IPF * PCG_T; b < a.n_imgs; b += PCG_T) sums[0] += a.img_part[b];
     block_sums<PCG_T, 1>(sums, sh);                    // p.Ap (its barriers also publish sLong)
     const double pap = sums[0];
     const double denom = pap > 1e-32 ? pap : 1e-32;
-    const double alpha = a.state[ST_RZ0 + (n & 1)] / denom;
+    const double alpha = rz / denom;
     double t[PCG_NP] = {0.0, 0.0};
     if (u < a.n_u) {
         const double pn = pdir(zu, pu, beta);

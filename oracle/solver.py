@@ -275,8 +275,11 @@ def A_diag(ne):
     return torch.cat([ne.leaves[n].diagonal(dim1=-1, dim2=-2).reshape(-1) for n in ('foc', 'tau', 'zcf')])
 
 
-def pcg(A_mv, b, M_mv=None, x0=None, tol=1e-6, maxiter=200):
-    """Restates ``_pcg`` (bs:1197-1238): returns (x, iters, converged)."""
+def pcg(A_mv, b, M_mv=None, x0=None, tol=1e-6, maxiter=200, history=None):
+    """Restates ``_pcg`` (bs:1197-1238): returns (x, iters, converged).
+
+    ``history``, a list, receives the iterate after every update (x after k updates at index k - 1).
+    """
     x = torch.zeros_like(b) if x0 is None else x0.clone()
     r = b - A_mv(x)
     z = M_mv(r) if M_mv is not None else r
@@ -290,6 +293,8 @@ def pcg(A_mv, b, M_mv=None, x0=None, tol=1e-6, maxiter=200):
         alpha = rz_old / denom
         x = x + alpha * p
         r = r - alpha * Ap
+        if history is not None:
+            history.append(x)
         r_norm = r.norm()
         if r_norm < best[0]:
             best = (r_norm, x, k)

@@ -6,9 +6,9 @@ Tolerances (norm-wise relative, ||gpu - oracle|| / ||oracle||):
   * reduced-system blocks S, rhs, point blocks: 1e-5 (fp64, differences come from the
     fp32 residual/weight rounding of logf/powf on either side)
   * PCG step and LM update: 1e-4 on delta and on J.delta (the north-star step tolerance), widened
-    to 5x the oracle's own spread under a change of summation order where the system's conditioning
-    leaves the stopped PCG's step that loose (test_pcg_step_parity), and to 4x the spread between
-    tol 1e-6 and a tightly converged solve for lm_step
+    where the system's conditioning makes CG amplify rounding: to 5x the move of the oracle's own
+    iterate under 1e-15 perturbations (test_pcg_step_parity), and to 4x the spread between tol
+    1e-6 and a tightly converged solve for lm_step
 """
 import pytest
 import torch
@@ -180,18 +180,18 @@ def test_reduced_system_parity(cfg, nf, nt):
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (1, 32, 400), (2, 24, 800), (3, 24, 600),
                                         (4, 12, 300)])
 def test_pcg_step_parity(cfg, nf, nt):
-    """delta from the device PCG against the oracle restatement of _pcg (same iterations).
+    """delta from the device PCG against the oracle restatement of _pcg.
 
-    A PCG stopped at ||r|| <= 1e-6 ||b|| (or at maxiter) fixes the step only up to its rounding on an
-    ill-conditioned system.  The oracle's own sensitivity is measured by running the same iteration
-    with the operator applied as a dense matrix (same mathematics, another summation order, also its
-    symmetrised form): the device step must agree with the oracle to max(1e-4, 5 x that spread) on
-    delta and on J.delta.  A converged device solve must meet the stopping test on the oracle's S
-    (to 2x, since it stopped on its own rounding of S) within 5% of the oracle's iteration count (at
-    least 2: config 4's oracle count moves between 151 and 155 with the summation order); one stopped
-    at maxiter must reach the oracle's reduced residual.  On well-conditioned cases (configs 0, 2, 3)
-    the spread is below 1e-5 and the bar is the plain 1e-4; config 1 stops at maxiter (condition
-    number ~1e11) and config 4's step moves by ~5e-3 between summation orders.
+    The device's iterate (after k updates: the converged one, else the best so far) is compared
+    with the oracle's iterate after the same k updates.  On an ill-conditioned system CG amplifies
+    rounding: perturbing b by 1e-15 relative moves the oracle's own k-th iterate by ~1e-3 on
+    configs 1 and 4 (condition numbers ~1e11).  So the bar is max(1e-4, 5x the largest such move
+    over four perturbed oracle runs: three of b, one applying S as a dense matrix) on delta and on
+    J.delta; on well-conditioned cases (configs 0, 2, 3) that is the plain 1e-4.  The stopping
+    decisions are checked separately: the same converged flag, a converged count within 5% of the
+    oracle's (at least 2: config 4's moves between 151 and 156 under those perturbations), the
+    stopping test met on the oracle's S (to 2x: the device stops on its own rounding of S), and a
+    run stopped at maxiter reaching the oracle's reduced residual.
     """
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
     fl = _cfg_flags(p)
@@ -204,27 +204,38 @@ def test_pcg_step_parity(cfg, nf, nt):
     Jd = dense_jacobian(Jc, Jz, Jp, p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks)
     sW = w.clamp(1e-6, 1e6).reshape(-1).double().sqrt()
     Jdelta = lambda d: sW[:, None] * Jd @ d.cpu().double()
-    # the oracle's spread under a change of summation order of the same operator
     n_c = ne.sizes['n_c']
     S = osol.dense_schur(ne)
     rhs = osol.reduced_rhs(ne, gvec)
     diagA = osol.A_diag(ne).clamp(min=1e-12)
-    alts = []
-    for Sx in (S, 0.5 * (S + S.T)):
-        dc, _, _ = osol.pcg(lambda v: Sx @ v, rhs, M_mv=lambda v: v / diagA, tol=1e-6, maxiter=300)
-        alts.append(torch.cat([dc, osol._D_solve(ne, gvec[n_c:] - osol._C_matvec(ne, dc))]))
-    tol_d = max([1e-4] + [5 * rel_err(d, d_ref) for d in alts])
-    tol_j = max([1e-4] + [5 * rel_err(Jdelta(d), Jdelta(d_ref)) for d in alts])
+    M = lambda v: v / diagA
     red = lambda dc: float((rhs - S @ dc).norm() / rhs.norm())
     if conv_ref:
         assert abs(int(ist[2]) - it_ref) <= max(2, 0.05 * it_ref), (int(ist[2]), it_ref)
         assert red(delta[:n_c].cpu().double()) <= 2e-6
     else:
-        r_ref = max([red(d_ref[:n_c])] + [red(d[:n_c]) for d in alts])
-        assert red(delta[:n_c].cpu().double()) <= 1.5 * r_ref
-    assert rel_err(delta, d_ref.to(torch.float32)) < tol_d, (rel_err(delta, d_ref.to(torch.float32)), tol_d)
+        assert red(delta[:n_c].cpu().double()) <= 1.5 * red(d_ref[:n_c])
+    # the oracle's iterate after the device's k updates, and its sensitivity to rounding there
+    k = int(ist[2]) if conv_ref else int(ist[4])
+    assert k >= 1
+    full = lambda dc: torch.cat([dc, osol._D_solve(ne, gvec[n_c:] - osol._C_matvec(ne, dc))])
+
+    def kth(A_mv, b):
+        hist = []
+        osol.pcg(A_mv, b, M_mv=M, tol=0.0, maxiter=k, history=hist)
+        return full(hist[k - 1])
+
+    ref_k = kth(lambda v: osol.S_matvec(ne, v), rhs)
+    gen = torch.Generator().manual_seed(cfg)
+    alts = [kth(lambda v: S @ v, rhs)]
+    for _ in range(3):
+        e = 1 + 1e-15 * torch.randn(rhs.shape, generator=gen, dtype=rhs.dtype)
+        alts.append(kth(lambda v: osol.S_matvec(ne, v), rhs * e))
+    tol_d = max([1e-4] + [5 * rel_err(d, ref_k) for d in alts])
+    tol_j = max([1e-4] + [5 * rel_err(Jdelta(d), Jdelta(ref_k)) for d in alts])
+    assert rel_err(delta, ref_k.to(torch.float32)) < tol_d, (rel_err(delta, ref_k.to(torch.float32)), tol_d)
     # gauge-invariant check: the predicted residual change J.delta
-    assert rel_err(Jdelta(delta), Jdelta(d_ref)) < tol_j
+    assert rel_err(Jdelta(delta), Jdelta(ref_k)) < tol_j
 
 
 def _device_pcg_dense(A, b, tol, maxiter, d):
