@@ -5,6 +5,8 @@
 //   ba_objective     loss = mean(err) (engine.py:268) and reproj_score = mean of the lowest
 //                    80% of ||r[:, :2]|| (engine.py:357-361), the latter by an exact radix
 //                    select on the fp32 bit patterns instead of a full sort.
+//   ba_nonfinite_flags  the `tensor.isfinite().all()` input checks of lm_step (engine.py:340-344)
+//                    for every fp32 input in one launch.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <cmath>
@@ -199,11 +201,74 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_final(const double* __restrict__ 
     }
 }
 
+// ------------------------------------------------------------------ input checks
+struct NfSpans {
+    const float* p[BA_NONFINITE_MAX_SPANS];
+    int64_t n[BA_NONFINITE_MAX_SPANS];
+};
+
+__global__ void __launch_bounds__(64) k_nf_clear(int32_t* flags, int n) {
+    if ((int)threadIdx.x < n) flags[threadIdx.x] = 0;
+}
+
+// blockIdx.y = span; every block strides over its span, 16-byte loads where the span's first element is
+// 16-byte aligned (the 0-3 leading elements before that boundary and the tail are read singly).  A
+// non-finite value (exponent bits all ones) sets the span's flag; every writer stores the same 1.
+#define NF_T 256
+__global__ void __launch_bounds__(NF_T) k_nonfinite(NfSpans sp, int32_t* flags) {
+    const int t = blockIdx.y;
+    const float* __restrict__ p = sp.p[t];
+    const int64_t n = sp.n[t];
+    const uint32_t E = 0x7f800000u;
+    const int64_t mis = (int64_t)(((16 - ((uintptr_t)p & 15)) & 15) >> 2);   // elements before the 16-byte boundary
+    const int64_t lead = mis < n ? mis : n;
+    bool bad = false;
+    const int64_t gtid = (int64_t)blockIdx.x * NF_T + threadIdx.x, gstride = (int64_t)gridDim.x * NF_T;
+    if (((uintptr_t)p & 3) == 0) {
+        const int64_t nv = (n - lead) >> 2;
+        const uint4* __restrict__ v = (const uint4*)(p + lead);
+        for (int64_t k = gtid; k < nv; k += gstride) {
+            const uint4 q = v[k];
+            bad |= ((q.x & E) == E) | ((q.y & E) == E) | ((q.z & E) == E) | ((q.w & E) == E);
+        }
+        for (int64_t k = gtid; k < lead; k += gstride) bad |= (__float_as_uint(p[k]) & E) == E;
+        for (int64_t k = lead + 4 * nv + gtid; k < n; k += gstride) bad |= (__float_as_uint(p[k]) & E) == E;
+    } else {
+        for (int64_t k = gtid; k < n; k += gstride) bad |= (__float_as_uint(p[k]) & E) == E;
+    }
+    if (bad) flags[t] = 1;
+}
+
 }  // namespace ba
 
 using namespace ba;
 
 static inline unsigned nbk(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// flags[t] = 1 when ptrs[t][0 .. counts[t]) holds a NaN or an infinity (fp32), else 0.
+extern "C" int ba_nonfinite_flags(const float* const* ptrs, const int64_t* counts, int32_t n_spans, int32_t* flags,
+                                  void* stream) {
+    clear_error();
+    BA_REQUIRE(n_spans >= 0 && n_spans <= BA_NONFINITE_MAX_SPANS, "ba_nonfinite_flags: 0 to 16 arrays");
+    BA_REQUIRE(n_spans == 0 || (ptrs != nullptr && counts != nullptr && flags != nullptr), "null argument");
+    if (n_spans == 0) return BA_OK;
+    NfSpans sp{};
+    int64_t most = 0;
+    for (int t = 0; t < n_spans; ++t) {
+        BA_REQUIRE(counts[t] >= 0 && (counts[t] == 0 || ptrs[t] != nullptr), "bad array");
+        sp.p[t] = ptrs[t];
+        sp.n[t] = counts[t];
+        most = counts[t] > most ? counts[t] : most;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_nf_clear, dim3(1), dim3(64), 0, st, flags, (int)n_spans);
+    // enough blocks to stream the largest array at full bandwidth: 4 floats per thread per pass
+    int64_t nbx = (most / 4 + NF_T - 1) / NF_T;
+    nbx = nbx < 1 ? 1 : (nbx > 2048 ? 2048 : nbx);
+    hipLaunchKernelGGL(k_nonfinite, dim3((unsigned)nbx, (unsigned)n_spans), dim3(NF_T), 0, st, sp, flags);
+    BA_LAUNCHED();
+    return BA_OK;
+}
 
 // Replaces the update block of lm_step (engine.py:310-313): one launch for every parameter group.
 extern "C" int ba_apply_update(const float* K, const float* P_w2rig, const float* z_coefs, const float* pts3d,

@@ -10,6 +10,8 @@ weight_tan > 0.
 """
 from collections import namedtuple
 
+import ctypes
+
 import torch
 
 from . import cujac
@@ -22,13 +24,36 @@ BA_Status = namedtuple('BA_Status', 'init_loss, init_residuals, new_loss, new_re
 STEP_SCHEDULE = [0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0]     # en:309
 
 
-def shape_of(tensor, is_contiguous=True):
-    """en:340-344."""
+def shape_of(tensor, is_contiguous=True, check_finite=True):
+    """en:340-344.  check_finite=False leaves the isfinite assertion to a later batched
+    _assert_finite over all inputs (lm_step)."""
     assert tensor.dtype in (torch.float32, torch.int32)
     if is_contiguous:
         assert tensor.is_contiguous()
-    assert tensor.isfinite().all()
+    if check_finite:
+        _assert_finite(tensor)
     return tensor.shape
+
+
+def _assert_finite(*tensors):
+    """``assert t.isfinite().all()`` for every tensor (en:343), one launch and one host read for all
+    device fp32 inputs (ba_nonfinite_flags); int32 tensors are finite by type."""
+    floats = [t for t in tensors if t.dtype != torch.int32]
+    dev = [t for t in floats if t.is_cuda]
+    for t in floats:
+        if not t.is_cuda:
+            assert t.isfinite().all()
+    if not dev:
+        return
+    views = [t if t.is_contiguous() else t.contiguous() for t in dev]
+    for k in range(0, len(views), 16):
+        part = views[k:k + 16]
+        n = len(part)
+        ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in part])
+        counts = (ctypes.c_int64 * n)(*[t.numel() for t in part])
+        flags = torch.empty(n, dtype=torch.int32, device=part[0].device)
+        check(lib().ba_nonfinite_flags(ptrs, counts, n, ptr(flags), stream_ptr(part[0].device)))
+        assert not bool(flags.cpu().any()), 'non-finite input'
 
 
 def update_K(K0, delta_focal, min_f=100):
@@ -131,21 +156,25 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
     if weight_tan > 0:
         assert is_depth_log, 'tangent prior currently only implemented for depth_mode="log"'
     n_imgs = rigs.shape[1]
-    assert shape_of(rigs) == (3, n_imgs)
+    # en:219-233; the isfinite part of every shape_of runs once for all inputs below
+    chk = dict(check_finite=False)
+    assert shape_of(rigs, **chk) == (3, n_imgs)
     n_cams = len(K)
-    assert shape_of(K) == (n_cams, 3, 3)
-    assert shape_of(P_rig2cam, is_contiguous=False) == (n_cams, 4, 4)
+    assert shape_of(K, **chk) == (n_cams, 3, 3)
+    assert shape_of(P_rig2cam, is_contiguous=False, **chk) == (n_cams, 4, 4)
     n_nodes = len(P_w2rig)
-    assert shape_of(P_w2rig) == (n_nodes, 4, 4)
+    assert shape_of(P_w2rig, **chk) == (n_nodes, 4, 4)
     n_zcf = z_coefs.shape[1]
-    assert shape_of(z_coefs) == (n_imgs, n_zcf)
+    assert shape_of(z_coefs, **chk) == (n_imgs, n_zcf)
     n_tracks = len(pts3d)
-    assert shape_of(pts3d) == (n_tracks, 3)
+    assert shape_of(pts3d, **chk) == (n_tracks, 3)
     n_obs = len(pids)
-    assert shape_of(pids) == (n_obs,)
-    assert shape_of(pix2d) == (n_obs, 2)
-    assert shape_of(pix2d_std) == (n_obs, 2)
-    assert shape_of(pix2d_dep) == (n_obs, n_zcf), f'expected pix2d_dep of shape {(n_obs, n_zcf)}, got {shape_of(pix2d_dep)}'
+    assert shape_of(pids, **chk) == (n_obs,)
+    assert shape_of(pix2d, **chk) == (n_obs, 2)
+    assert shape_of(pix2d_std, **chk) == (n_obs, 2)
+    assert shape_of(pix2d_dep, **chk) == (n_obs, n_zcf), \
+        f'expected pix2d_dep of shape {(n_obs, n_zcf)}, got {shape_of(pix2d_dep, **chk)}'
+    _assert_finite(K, P_rig2cam, P_w2rig, z_coefs, pts3d, pix2d, pix2d_std, pix2d_dep)
     assert 0 <= weight_z <= 10
     assert n_obs >= n_tracks, 'there must be more 2d kpts than tracks'
     assert huber_delta >= 0.1
@@ -206,16 +235,22 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
         update['K'], update['P_w2rig'], update['z_coefs'], update['pts3d'] = Kn, Pn, Zn, Xn
         new_loss, new_residuals, new_w, new_reproj_t = objective(**update)
         last_eval = (new_loss, new_residuals, new_w)
-        vals = torch.stack([new_loss, init_loss, new_reproj_t]).cpu()
+        # one read for every decision: the sums + min_loss_delta are formed on the device, as the
+        # reference forms them, so the comparison sees the same fp32 values
+        vals = torch.stack([new_loss, init_loss, new_reproj_t, new_loss + min_loss_delta,
+                            init_loss + min_loss_delta]).cpu()
         if torch.isnan(vals[0]):
             print('Warning: loss is NaN')
             new_loss = init_loss
+            new_loss_h = vals[4]
+        else:
+            new_loss_h = vals[3]
         new_loss = new_loss + min_loss_delta
         new_reproj = float(vals[2])
         degenerate = new_reproj < min_reproj
         if degenerate:
             print(f'Rejecting step: reprojection residual collapsed to {new_reproj:.2e}')
-        if float(new_loss) < float(vals[1]) and not degenerate:
+        if float(new_loss_h) < float(vals[1]) and not degenerate:
             break
         scale = scale * (a / last_a)       # delta *= a/last_a (en:330): every slice scaled together
         last_a = a

@@ -109,17 +109,26 @@ _cache = {}
 
 def get_plan(infos, pids, n_tracks, **kw):
     """Plan for this structure: reused while the same pids tensor (unmodified) and the same
-    per-image counts / node / cam ids come back, rebuilt otherwise."""
-    meta = infos.detach().cpu().numpy().tobytes()
+    per-image counts / node / cam ids come back, rebuilt otherwise.  The ids are compared by
+    content unless the very infos tensor of the cached plan comes back unmodified (torch's version
+    counter), which needs no device-to-host read."""
     key = (int(n_tracks), tuple(pids.shape), tuple(sorted(kw.items())))
     with _cache_lock:
         for ent in _cache.get(id(pids), []):
-            ref, version, k, m, plan = ent
+            ref, version, k, m, iref, iversion, plan = ent
+            if ref() is pids and version == pids._version and k == key and iref() is infos and \
+                    iversion == infos._version:
+                return plan
+    meta = infos.detach().cpu().numpy().tobytes()
+    with _cache_lock:
+        for ent in _cache.get(id(pids), []):
+            ref, version, k, m, iref, iversion, plan = ent
             if ref() is pids and version == pids._version and k == key and m == meta:
                 return plan
     plan = BAPlan(infos, pids, n_tracks, **kw)
     with _cache_lock:
         if sum(len(v) for v in _cache.values()) > 8:
             _cache.clear()
-        _cache.setdefault(id(pids), []).append((weakref.ref(pids), pids._version, key, meta, plan))
+        _cache.setdefault(id(pids), []).append((weakref.ref(pids), pids._version, key, meta, weakref.ref(infos),
+                                                infos._version, plan))
     return plan

@@ -206,6 +206,13 @@ int64_t ba_objective_workspace_bytes(int64_t n_obs);
  *   80% of ||(r0,r1)|| (exact selection on the fp32 values, no sort).  out is device memory. */
 int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out, void* stream);
 
+/* lm_step's input checks, `assert tensor.isfinite().all()` on every input (engine.py:340-344), for up
+ * to BA_NONFINITE_MAX_SPANS fp32 arrays in one launch: flags[t] (device, int32) = 1 when
+ * ptrs[t][0 .. counts[t]) holds a NaN or an infinity, else 0.  int32 inputs are finite by type. */
+#define BA_NONFINITE_MAX_SPANS 16
+int ba_nonfinite_flags(const float* const* ptrs, const int64_t* counts, int32_t n_spans, int32_t* flags,
+                       void* stream);
+
 /* ------------------------------------------------------------------ F sampling */
 
 /* Multi-depth values at the observations (replaces the per-image bilinear_sampling calls of

@@ -469,3 +469,55 @@ def test_objective_reproj_exact():
     assert abs(float(r) - float(ref)) <= 1e-6 * abs(float(ref))
     loss, _ = gpu_engine._objective(out.T, p.n_obs, True)
     assert abs(float(loss) - float(out[:, 3:6].cpu().double().mean())) <= 1e-6 * float(loss)
+
+
+def test_nonfinite_flags_match_torch_isfinite():
+    """ba_nonfinite_flags (the batched isfinite assertions of lm_step, en:340-344) against
+    torch.isfinite on spans of every alignment and size, with NaN / +-inf at the edges and inside."""
+    import ctypes
+    from blast3r_amd._lib import check, lib, stream_ptr
+    base = torch.randn(3_000_011, device=DEV)
+    cases = []
+    for off, n in [(0, 0), (0, 1), (1, 1), (2, 3), (3, 5), (1, 17), (0, 64), (5, 1000), (7, 1_000_003),
+                   (0, 3_000_000), (2, 2_999_999)]:
+        for where in (None, 'first', 'last', 'mid'):
+            if where is not None and n == 0:
+                continue
+            cases.append((off, n, where))
+    vals = [float('nan'), float('inf'), float('-inf')]
+    for start in range(0, len(cases), 16):
+        part = cases[start:start + 16]
+        views = []
+        for j, (off, n, where) in enumerate(part):
+            t = base[off:off + n].clone() if n else base[:0]
+            if n and where is not None:
+                i = {'first': 0, 'last': n - 1, 'mid': n // 2}[where]
+                t[i] = vals[j % 3]
+            # the same values at the case's offset inside a fresh buffer (alignment as in the case)
+            buf = torch.randn(off + n + 4, device=DEV)
+            buf[off:off + n] = t
+            views.append(buf[off:off + n])
+        m = len(views)
+        ptrs = (ctypes.c_void_p * m)(*[v.data_ptr() for v in views])
+        counts = (ctypes.c_int64 * m)(*[v.numel() for v in views])
+        flags = torch.full((m,), 7, dtype=torch.int32, device=DEV)
+        check(lib().ba_nonfinite_flags(ptrs, counts, m, flags.data_ptr(), stream_ptr(DEV)))
+        want = torch.tensor([0 if v.isfinite().all() else 1 for v in views], dtype=torch.int32)
+        assert torch.equal(flags.cpu(), want), part
+
+
+def test_lm_step_rejects_nonfinite_inputs():
+    """lm_step asserts isfinite on its inputs before any work (en:340-344)."""
+    p = make_problem(0, n_frames=6, n_tracks=60)
+    o = p.options
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0)
+    g = _gpu(p)
+    gpu_engine.lm_step(**g.lm_inputs(), **kw)                  # finite inputs pass
+    for name, idx, v in [('pix2d_dep', (3, 1), float('nan')), ('K', (0, 0, 0), float('inf')),
+                         ('pts3d', (-1, 2), float('-inf')), ('pix2d_std', (0, 0), float('nan'))]:
+        inp = g.lm_inputs()
+        bad = inp[name].clone()
+        bad[idx] = v
+        inp[name] = bad
+        with pytest.raises(AssertionError):
+            gpu_engine.lm_step(**inp, **kw)
