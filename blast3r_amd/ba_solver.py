@@ -227,6 +227,7 @@ class GaussNewtonSolver:
         gp = ws('gp', (max(n_ct, 1), 3), torch.float64)
         ct_pt = ws('ct_pt', (max(n_ct, 1), 4), torch.float32)
         pfac = ws('pfac', (max(n_ct, 1), 12), torch.float64)
+        work_ctr = ws('work_ctr', (1,), torch.int32)
         core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)   # linearisation records
         chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), torch.float64)
         lam_p = ws('lam_p', (1,), torch.float64)
@@ -244,7 +245,7 @@ class GaussNewtonSolver:
         a.n_imgs = n_imgs
         for name in ('chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr',
                      'b_imgs', 'b_nimgs', 'b_slot_ptr', 'slot_pair', 'pair_ptr', 'pair_src', 'img_ptr', 'img_src',
-                     'chunk_slots', 'chunk_ent', 'chunk_eptr', 'b_pos_slot'):
+                     'chunk_slots', 'chunk_ent', 'chunk_eptr', 'b_pos_slot', 'b_order'):
             setattr(a, name, ptr(pd[name]))
         a.L = plan.L
         a.s_pix, a.s_std, a.s_dep = ptr(s_pix), ptr(s_std), ptr(s_dep)
@@ -271,6 +272,7 @@ class GaussNewtonSolver:
         L_.x_off = int(not en['X'][0])
         a.Hpp, a.gp, a.chunk_max, a.lam_p = ptr(Hpp), ptr(gp), ptr(chunk_max), ptr(lam_p)
         a.ct_pt, a.n_ctracks, a.core, a.pfac = ptr(ct_pt), n_ct, ptr(core), ptr(pfac)
+        a.work_ctr = ptr(work_ctr)
         a.partials, a.img_partials = ptr(partials), ptr(img_partials)
         a.n_chunks, a.n_batches, a.n_pairs = sc['n_chunks'], sc['n_batches'], sc['n_pairs']
         a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)

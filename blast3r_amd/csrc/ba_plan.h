@@ -43,6 +43,7 @@ enum {
     BA_PA_SLOT_SRC,         // per chunk slot: its observation, 0 for an empty slot (a gather index)
     BA_PA_S_PID,            // per chunk slot: track id of its observation (0 when empty)
     BA_PA_S_IMG,            // per chunk slot: image of its observation (0 when empty)
+    BA_PA_B_ORDER,          // the batches in Schur-kernel dispatch order (estimated cost, decreasing)
     BA_PLAN_NARRAYS
 };
 

@@ -490,15 +490,32 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __shared__ int sSlotTab[2][BA_MAX_SLOTS];            // per slot: entry offset | padded count << 16
     __shared__ int sDup[2];
     __shared__ int sNct;
+    __shared__ int sNext;
 
     const int d = a.lay.d, C = a.lay.C;
-    const int batch = blockIdx.x;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    static_assert(BA_WAVES >= 8, "phase A needs eight waves");
+
+    // Work queue: with a counter, each workgroup (one per CU) takes the next batch of the dispatch
+    // order until none is left, so a CU that finishes early starts the next batch at once (the
+    // hardware dispatcher hands each XCD its workgroups in launch order, and one long batch
+    // then holds back every later workgroup of its XCD).  Without one, workgroup b takes batch b.
+    for (int bq = blockIdx.x;;) {
+    // the lane indices are re-derived for every batch (through an opaque copy of the thread id), so
+    // that nothing computed from them is hoisted out of this loop and kept live across the inner ones
+    int tid_ = threadIdx.x;
+    asm volatile("" : "+v"(tid_));
+    const int tid = tid_, wave = tid >> 6, lane = tid & 63;
     // phase A roles: waves 0-5 take one (slot, row) each (slot tid % 128, row tid / 128), waves 6-7
     // the z-coefficient columns of row 2 (rr = 3)
     const bool row_lane = tid < 4 * BA_CHUNK;
     const int t = tid & (BA_CHUNK - 1), rr = tid >> 7;
-    static_assert(BA_WAVES >= 8, "phase A needs eight waves");
+    if (a.work_ctr != nullptr) {
+        if (tid == 0) sNext = atomicAdd(a.work_ctr, 1);
+        __syncthreads();
+        bq = sNext;
+    }
+    if (bq >= a.n_batches) break;
+    const int batch = a.b_order != nullptr ? a.b_order[bq] : bq;             // most expensive first
     const int nimg = a.b_nimgs[batch];
     const int s0 = a.b_slot_ptr[batch], ns = a.b_slot_ptr[batch + 1] - s0;
     const int c_begin = a.b_chunk_ptr[batch], c_end = a.b_chunk_ptr[batch + 1];
@@ -719,7 +736,12 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         const int va = tid >> 4, vj = tid & 15;
         if (va < nimg && vj < d) a.img_partials[((int64_t)batch * a.L + va) * 2 * d + d + vj] = sDv[va][vj];
     }
+    if (a.work_ctr == nullptr) break;
+    __syncthreads();                     // this batch's LDS fully read before the next one is staged
+    }
 }
+
+__global__ void k_ctr_clear(int* ctr) { *ctr = 0; }
 
 // ----------------------------------------------------------------------------- reductions
 __global__ void __launch_bounds__(256) k_pair_reduce(const int* __restrict__ pair_ptr, const int* __restrict__ pair_src,
@@ -874,10 +896,19 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
     }
     if (stage == 1 && a.n_batches > 0) {
         size_t lds = ((size_t)BA_CHUNK * BA_BLK + 48) * sizeof(double);
+        // one workgroup per CU (the kernel's LDS allows one) pulling batches from the work queue
+        unsigned grid = (unsigned)a.n_batches;
+        if (a.work_ctr != nullptr) {
+            int dev = 0, n_cu = 0;
+            BA_HIP(hipGetDevice(&dev));
+            BA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+            if (n_cu > 0 && (int64_t)n_cu < a.n_batches) grid = (unsigned)n_cu;
+            hipLaunchKernelGGL(k_ctr_clear, dim3(1), dim3(1), 0, st, a.work_ctr);
+        }
         BA_DISPATCH_KP(a.lay, {
             BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds));
-            hipLaunchKernelGGL((k_schur<HK_, HP_>), dim3((unsigned)a.n_batches), dim3(BA_WAVES * 64), lds, st, a);
+            hipLaunchKernelGGL((k_schur<HK_, HP_>), dim3(grid), dim3(BA_WAVES * 64), lds, st, a);
         });
         BA_LAUNCHED();
     }

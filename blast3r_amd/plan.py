@@ -20,7 +20,7 @@ from ._lib import check, lib
 ARRAYS = ['chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr', 'b_imgs',
           'b_nimgs', 'b_slot_ptr', 'slot_pair', 'slot_gpair', 'pair_i1', 'pair_i2', 'pair_ptr', 'pair_src',
           'row_ptr', 'row_ent', 'img_ptr', 'img_src', 'chunk_slots', 'chunk_ent', 'chunk_eptr',
-          'b_pos_slot', 'slot_src', 's_pid', 's_img']
+          'b_pos_slot', 'slot_src', 's_pid', 's_img', 'b_order']
 SCALARS = ['n_chunks', 'n_batches', 'n_slots', 'n_pairs', 'n_ctracks', 'L', 'chunk', 'max_slots_used',
            'max_chunks_per_batch', 'n_pair_terms']
 CHUNK = 128

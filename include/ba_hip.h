@@ -129,6 +129,9 @@ typedef struct {
     const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
     double* pfac;         /* (n_ctracks,12) scratch written by stage 0: Cholesky factor L of H_pp + lam_p I
                              (upper storage), w = L^-1 g_p, reciprocal pivots */
+    const int32_t* b_order;  /* plan: batches in dispatch order (most expensive first); NULL = 0, 1, ... */
+    int32_t* work_ctr;       /* 1 int of device scratch: the camera-pair kernel's batch queue (one
+                                workgroup per CU); NULL = one workgroup per batch */
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.

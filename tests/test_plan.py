@@ -141,6 +141,30 @@ def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
         assert per_wave.max() <= 6
 
 
+def test_plan_dispatch_order():
+    """b_order is a permutation of the batches, most expensive first: greedy list scheduling of the
+    batches (one per machine at a time, as the Schur kernel's workgroups on the CUs) in that order
+    finishes no later than in plan order, by chunk count, on several machine counts."""
+    import heapq
+    p = make_problem(2, n_frames=400, n_tracks=120000)
+    pl = _plan(p)
+    h = pl.host
+    nb = pl.scalars['n_batches']
+    order = h['b_order']
+    assert np.array_equal(np.sort(order), np.arange(nb))
+    cost = np.diff(h['b_chunk_ptr']).astype(np.float64)
+    assert cost[order[0]] >= np.percentile(cost, 90)
+
+    def makespan(seq, m):
+        heap = [0.0] * m
+        for b in seq:
+            heapq.heappush(heap, heapq.heappop(heap) + cost[b])
+        return max(heap)
+
+    for m in (nb // 8, nb // 4, nb // 3):
+        assert makespan(order, m) <= makespan(np.arange(nb), m)
+
+
 def test_plan_errors():
     p = make_problem(0, n_frames=8, n_tracks=50)
     with pytest.raises(RuntimeError, match='max_local_imgs'):
