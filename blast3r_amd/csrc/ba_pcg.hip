@@ -428,6 +428,12 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
                    (a.n_long == 0 || a.long_u != nullptr) && a.img_part != nullptr,
                "bad long-list unknowns or image partials");
     if (a.n_u == 0) return BA_OK;
+    {
+        const void* need[] = {a.umap, a.inv_ptr, a.inv_src, a.leaf, a.row_ptr, a.row_ent, a.pair_i1, a.pair_i2,
+                              a.S_pairs, a.e_img, a.dg_img, a.rhs, a.diagA, a.damp, a.x, a.xbest, a.r, a.z, a.p,
+                              a.y_img, a.partials, a.state, a.istate};
+        for (const void* q : need) BA_REQUIRE(q != nullptr, "null pointer in ba_pcg_args");
+    }
     const unsigned nb = nb_of(a.n_u);
     const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown (setup)
     const int64_t n_ent = a.n_row_ent;

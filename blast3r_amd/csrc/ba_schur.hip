@@ -277,23 +277,42 @@ __device__ __forceinline__ void obs_core_slot(const LinArgs& a, int64_t slot, in
 // H_pp upper, g_p, the point with its enable flag, and the chunk's largest point-block diagonal
 // (for the damping value).
 template <int HK, int HP>
-__global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
+__global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 waves per SIMD: 96 VGPRs, no spills
     __shared__ double sh[BA_CHUNK][9];
     __shared__ double smax[BA_CHUNK];
     const int chunk = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = (int64_t)chunk * BA_CHUNK + tid;
+    // Everything that depends only on the slot or the chunk is requested at once (an empty slot
+    // holds gather index 0 in the slot arrays, so every lane's reads are valid), then what those
+    // give: the image's camera and pose, the point; then the chunk track of this lane.
     const int obs = a.chunk_obs[slot];
+    const int img = a.s_img[slot], pid = a.s_pid[slot];
+    const float2 uv = reinterpret_cast<const float2*>(a.s_pix)[slot];
+    const float2 sv = reinterpret_cast<const float2*>(a.s_std)[slot];
+    DepSrc dep;
+    load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
+    const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
+    int64_t ct = first_ct + (tid < n_ct ? tid : 0);
+    ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
+    const int ct_f = a.ct_first[ct], ct_m = a.ct_m[ct], ct_pid = a.ct_pid[ct];
+    const float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
     double c[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) c[k] = 0.0;
     if (obs >= 0) {
         ObsCtx ctx;
-        load_obs_ctx(a, a.s_img[slot], ctx);
-        const int pid = a.s_pid[slot];
-        DepSrc dep;
-        load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
+        load_obs_ctx(a, img, ctx);
+        GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
+        if (a.r_in) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                grw.r[k] = a.r_in[(int64_t)obs * a.r_s0 + k * a.r_s1];
+                grw.w[k] = a.w_in[(int64_t)obs * a.w_s0 + k * a.w_s1];
+            }
+        }
         ObsCore o;
-        obs_core_slot(a, slot, obs, ctx, pid, dep, o);
+        float Xo[3] = {X[0], X[1], X[2]};
+        obs_core(ctx.cp, ctx.zc, Xo, uv, sv, dep, a.hp, a.lay, a.r_in != nullptr, grw, o);
         core_store(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         const bool xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
         double Jp[3][3], gP[3];
@@ -309,12 +328,12 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < 9; ++k) sh[tid][k] = c[k];
+    const float* Xc = a.pts3d + 3 * (int64_t)ct_pid;
+    const float4 cpt = make_float4(Xc[0], Xc[1], Xc[2], (a.enX ? a.enX[ct_pid] != 0 : true) ? 1.f : 0.f);
     __syncthreads();
-    const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
     double mx = 0.0;
     if (tid < n_ct) {
-        const int64_t ct = first_ct + tid;
-        const int f = a.ct_first[ct], m = a.ct_m[ct], pid = a.ct_pid[ct];
+        const int f = ct_f, m = ct_m;
         double s[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k) s[k] = 0.0;
@@ -325,8 +344,7 @@ __global__ void __launch_bounds__(BA_CHUNK) k_track_pp(LinArgs a) {
         for (int k = 0; k < 6; ++k) a.Hpp[6 * ct + k] = s[k];
 #pragma unroll
         for (int k = 0; k < 3; ++k) a.gp[3 * ct + k] = s[6 + k];
-        const float* X = a.pts3d + 3 * (int64_t)pid;
-        reinterpret_cast<float4*>(a.ct_pt)[ct] = make_float4(X[0], X[1], X[2], (a.enX ? a.enX[pid] != 0 : true) ? 1.f : 0.f);
+        reinterpret_cast<float4*>(a.ct_pt)[ct] = cpt;
         mx = fmax(fmax(fabs(s[0]), fabs(s[3])), fabs(s[5]));
     }
     smax[tid] = mx;
@@ -784,16 +802,26 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
     __shared__ double sh[BA_CHUNK][3];
     const int chunk = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = (int64_t)chunk * BA_CHUNK + tid;
+    // slot- and chunk-only inputs first (as in k_track_pp): the observation's slot data, and this
+    // lane's chunk track with its point block and gradient
     const int obs = a.chunk_obs[slot];
+    const int img = a.s_img[slot], pid = a.s_pid[slot];
     const int d = a.lay.d;
+    DepSrc dep;
+    load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
+    const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
+    int64_t ctk = first_ct + (tid < n_ct ? tid : 0);
+    ctk = ctk < a.n_ctracks ? ctk : a.n_ctracks - 1;
+    const int ct_f = a.ct_first[ctk], ct_m = a.ct_m[ctk], ct_pid = a.ct_pid[ctk];
+    double H[6], gpt[3];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * ctk + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) gpt[k] = a.gp[3 * ctk + k];
     double y[3] = {0.0, 0.0, 0.0};
     if (obs >= 0) {
-        const int img = a.s_img[slot];
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
-        const int pid = a.s_pid[slot];
-        DepSrc dep;
-        load_dep(dep, a.s_dep + slot * a.lay.C, a.lay.C);
         ObsCore o;
         core_load(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
@@ -814,17 +842,13 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
     }
     sh[tid][0] = y[0]; sh[tid][1] = y[1]; sh[tid][2] = y[2];
     __syncthreads();
-    const int first_ct = a.chunk_meta[4 * chunk + 1], n_ct = a.chunk_meta[4 * chunk + 2];
     if (tid < n_ct) {
-        const int64_t ctk = first_ct + tid;
-        int f = a.ct_first[ctk], m = a.ct_m[ctk], pid = a.ct_pid[ctk];
+        const int f = ct_f, m = ct_m, pid = ct_pid;
         double s[3] = {0.0, 0.0, 0.0};
         for (int q = 0; q < m; ++q) { s[0] += sh[f + q][0]; s[1] += sh[f + q][1]; s[2] += sh[f + q][2]; }
-        double H[6], Lf[6], b[3], z[3], x[3];
+        double Lf[6], b[3], z[3], x[3];
 #pragma unroll
-        for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * ctk + k];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) b[k] = a.gp[3 * ctk + k] - s[k];
+        for (int k = 0; k < 3; ++k) b[k] = gpt[k] - s[k];
         chol3_factor(H, a.lam_p[0], Lf);
         chol3_fwd(Lf, b, z);
         chol3_bwd(Lf, z, x);
@@ -863,6 +887,37 @@ extern "C" int ba_linearize_schur(const ba_lin_args* args, void* stream) {
     return BA_OK;
 }
 
+// The first pointer a stage (0, 1, 2) or the back-substitution (3) dereferences that the caller left
+// NULL, or nullptr when all are set (the optional ones: enable masks, r_in / w_in, dX64, b_order,
+// work_ctr).
+static const char* missing_pointer(const ba_lin_args& a, int stage) {
+    const bool C = a.lay.C > 0;
+#define BA_NEED(cond, p) do { if ((cond) && (p) == nullptr) return "null pointer " #p; } while (0)
+    BA_NEED(stage != 2, a.infos);
+    BA_NEED(stage != 2, a.chunk_obs); BA_NEED(stage != 2, a.chunk_meta);
+    BA_NEED(stage != 2, a.ct_pid); BA_NEED(stage != 2, a.ct_first); BA_NEED(stage != 2, a.ct_m);
+    BA_NEED(stage != 2 && C, a.s_dep);
+    BA_NEED(stage != 2, a.s_pid); BA_NEED(stage != 2, a.s_img);
+    BA_NEED(stage != 2, a.K); BA_NEED(stage != 2, a.P_rig2cam); BA_NEED(stage != 2, a.P_w2rig);
+    BA_NEED(stage != 2 && C, a.z_coefs);
+    BA_NEED(stage != 2, a.Hpp); BA_NEED(stage != 2, a.gp); BA_NEED(stage != 2, a.lam_p);
+    BA_NEED(stage != 2, a.core);
+    BA_NEED(stage == 0, a.s_pix); BA_NEED(stage == 0, a.s_std); BA_NEED(stage == 0, a.pts3d);
+    BA_NEED(stage == 0, a.chunk_max); BA_NEED(stage == 0, a.ct_pt); BA_NEED(stage == 0, a.pfac);
+    BA_NEED(stage == 0 && a.r_in != nullptr, a.w_in);
+    BA_NEED(stage == 1, a.slot_info); BA_NEED(stage == 1, a.b_chunk_ptr); BA_NEED(stage == 1, a.b_imgs);
+    BA_NEED(stage == 1, a.b_nimgs); BA_NEED(stage == 1, a.b_slot_ptr); BA_NEED(stage == 1, a.slot_pair);
+    BA_NEED(stage == 1, a.chunk_slots); BA_NEED(stage == 1, a.chunk_ent); BA_NEED(stage == 1, a.chunk_eptr);
+    BA_NEED(stage == 1, a.b_pos_slot); BA_NEED(stage == 1, a.ct_pt); BA_NEED(stage == 1, a.pfac);
+    BA_NEED(stage == 1, a.partials); BA_NEED(stage == 1, a.img_partials);
+    BA_NEED(stage == 2, a.pair_ptr); BA_NEED(stage == 2, a.pair_src); BA_NEED(stage == 2, a.img_ptr);
+    BA_NEED(stage == 2, a.img_src); BA_NEED(stage == 2, a.partials); BA_NEED(stage == 2, a.img_partials);
+    BA_NEED(stage == 2, a.S_pairs); BA_NEED(stage == 2, a.e_img); BA_NEED(stage == 2, a.dg_img);
+    BA_NEED(stage == 3, a.dc); BA_NEED(stage == 3, a.umap); BA_NEED(stage == 3, a.dX);
+#undef BA_NEED
+    return nullptr;
+}
+
 // stage 0: point blocks + damping value; 1: camera-pair batches; 2: deterministic reductions
 extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream) {
     clear_error();
@@ -875,6 +930,11 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
                "inconsistent image-level layout");
     BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "fused path supports at most 24 z-coefficient columns");
     BA_REQUIRE(a.L >= 1 && a.L <= BA_MAX_LOCAL, "bad plan L");
+    BA_REQUIRE(stage >= 0 && stage <= 2, "stage must be 0, 1 or 2");
+    if (a.n_chunks > 0) {
+        const char* miss = missing_pointer(a, stage);
+        BA_REQUIRE(miss == nullptr, miss);
+    }
     if (stage == 0) {
         hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks);
         if (a.n_chunks > 0) {
@@ -931,6 +991,9 @@ extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
     const ba_lin_args& a = *args;
     BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 15, "fused path supports 1 <= d <= 15 image-level parameters");
     if (a.n_chunks == 0) return BA_OK;
+    BA_REQUIRE(a.n_ctracks >= 1, "chunk-track state missing");
+    const char* miss = missing_pointer(a, 3);
+    BA_REQUIRE(miss == nullptr, miss);
     hipStream_t st = (hipStream_t)stream;
     BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_backsub<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0, st, a));
     BA_LAUNCHED();

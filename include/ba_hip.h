@@ -161,7 +161,7 @@ typedef struct {
     int32_t maxiter; double tol;
     /* workspace (fp64 unless noted); p holds 2 * n_u (the search direction, double-buffered) */
     double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img;
-    double *partials;                  /* 3 * n_blocks */
+    double *partials;                  /* ba_pcg_partials_size(n_u) doubles */
     double *state;                     /* 16 doubles */
     int32_t *istate;                   /* 8 ints: [0], [1] done flags, [2] iterations, [3] converged,
                                           [4] best iteration, [5] best iterate returned */

@@ -318,3 +318,29 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     unbound = [n for n in names if n not in _lib._SIGS]
     assert not unbound, unbound
+
+
+def test_entry_points_reject_null_pointers_without_a_gpu():
+    """The fused-pass, back-substitution and PCG entry points name a NULL pointer they would
+    dereference and return an error before any device call (so they run here, without a GPU)."""
+    import ctypes
+    from blast3r_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from blast3r_amd.build import build
+        build()
+    L = _lib.lib()
+    a = _lib.BaLinArgs()
+    a.lay.d, a.lay.C, a.lay.off_tau, a.lay.off_zcf, a.lay.hasK, a.lay.hasP, a.lay.hasZ = 13, 5, 2, 8, 1, 1, 1
+    a.L, a.n_chunks, a.n_batches, a.n_pairs, a.n_ctracks, a.n_imgs = 16, 1, 1, 1, 1, 1
+    for stage in (0, 1, 2):
+        assert L.ba_linearize_stage(ctypes.byref(a), stage, None) != 0
+        assert b'null pointer' in L.ba_last_error(), stage
+    assert L.ba_backsubstitute(ctypes.byref(a), None) != 0
+    assert b'null pointer' in L.ba_last_error()
+    assert L.ba_linearize_stage(ctypes.byref(a), 7, None) != 0
+    pa = _lib.BaPcgArgs()
+    pa.n_u, pa.n_imgs, pa.d, pa.maxiter = 4, 1, 4, 10
+    n = (ctypes.c_int32 * 8)()
+    pa.long_ptr, pa.long_idx, pa.img_part = ctypes.addressof(n), ctypes.addressof(n), ctypes.addressof(n)
+    assert L.ba_pcg_solve(ctypes.byref(pa), None) != 0
+    assert b'null pointer' in L.ba_last_error()
