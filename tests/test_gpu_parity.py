@@ -521,3 +521,48 @@ def test_lm_step_rejects_nonfinite_inputs():
         inp[name] = bad
         with pytest.raises(AssertionError):
             gpu_engine.lm_step(**inp, **kw)
+
+
+def test_schur_work_queue_is_deterministic():
+    """The camera-pair kernel's batch queue (one workgroup per CU taking batches in the planner's
+    cost order) writes every batch's partial blocks to fixed places: the reduced system (S blocks,
+    rhs, diag) is bit-identical to one workgroup per batch in plan order, on a plan with more
+    batches than CUs (so workgroups take several batches), over repeated runs."""
+    import ctypes
+    from blast3r_amd._lib import check, lib
+    p = make_problem(2, n_frames=100, n_tracks=20000)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
+                           plan_options=dict(max_batch_obs=400))
+    J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                             g.pix2d_dep, True, pix2d=g.pix2d, hp=hp)
+    ctx = gs.prepare(J, res, w)
+    a, st = ctx['args'], ctx['stream']
+    assert ctx['plan'].scalars['n_batches'] > torch.cuda.get_device_properties(0).multi_processor_count
+    assert a.work_ctr and a.b_order
+
+    def run():
+        check(lib().ba_linearize_schur(ctypes.byref(a), st))
+        torch.cuda.synchronize()
+        return [ctx[k].clone() for k in ('S_pairs', 'e_img', 'dg_img')]
+
+    ref = None
+    for mode in ('queue', 'per_batch', 'plan_order', 'queue'):
+        a.work_ctr = ptr_of(ctx, 'work_ctr') if mode == 'queue' else None
+        a.b_order = ctx['plan'].dev['b_order'].data_ptr() if mode != 'plan_order' else None
+        got = run()
+        if ref is None:
+            ref = got
+            continue
+        for x, y in zip(got, ref):
+            assert torch.equal(x, y), mode
+
+
+def ptr_of(ctx, name):
+    return ctx['plan'].workspace(name, (1,), torch.int32).data_ptr()
