@@ -351,16 +351,26 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
     const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
-    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, du = 1.0, dmp = 0.0;
-    int q0 = 0, q1 = 0, li = -1;
+    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, du = 1.0, dmp = 0.0, y1 = 0.0;
+    int q0 = 0, q1 = 0, li = -1, s1 = -1;
     if (u < a.n_u) {                                   // operands first, then the reductions
         zu = a.z[u]; pu = pold[u]; xu = a.x[u]; ru = a.r[u]; du = a.diagA[u]; dmp = a.damp[u];
-        q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1]; li = a.long_idx[u];
+        li = a.long_idx[u];
+        if (a.src1 != nullptr) {                       // a one-entry list resolved ahead
+            s1 = a.src1[u];
+            if (s1 >= 0) y1 = a.y_img[s1];
+        }
+        if (s1 < 0) { q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1]; }
     }
     const int lk0 = a.long_ptr[blockIdx.x], lk1 = a.long_ptr[blockIdx.x + 1];
     for (int k = lk0 + w; k < lk1; k += PCG_T / 64) {
-        const int v = a.long_u[k];
-        const int b0 = a.inv_ptr[v], b1 = a.inv_ptr[v + 1];
+        int b0, b1;
+        if (a.long_rng != nullptr) {
+            b0 = a.long_rng[2 * k]; b1 = a.long_rng[2 * k + 1];
+        } else {
+            const int v = a.long_u[k];
+            b0 = a.inv_ptr[v]; b1 = a.inv_ptr[v + 1];
+        }
         double s = 0.0;
         for (int q = b0 + lane; q < b1; q += 64 * PCG_LF) {
             int src[PCG_LF];
@@ -374,7 +384,9 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
     }
     // the short lists: y_img is complete at launch, so these sums need nothing from the reductions
     double ys = 0.0;
-    if (li < 0)
+    if (s1 >= 0)
+        ys = 0.0 + y1;                                 // the same sum as the one-entry loop below
+    else if (li < 0)
         for (int q = q0; q < q1; ++q) ys += a.y_img[a.inv_src[q]];
     double sums[1] = {0.0};
 #pragma unroll

@@ -175,6 +175,10 @@ typedef struct {
                                           [256 b, 256 b + 256) */
     const int32_t *long_idx;           /* (n_u): k - long_ptr[u / 256] for u = long_u[k], else -1 */
     double *img_part;                  /* (n_imgs) workspace: per image row partial of p.Ap */
+    /* optional (NULL = follow inv_ptr / inv_src): the lists pre-resolved, one dependent load fewer */
+    const int32_t *src1;               /* (n_u): the only entry of u's inv list when it has exactly one,
+                                          else -1 */
+    const int32_t *long_rng;           /* (2 n_long): the inv-list bounds of long_u[k] */
 } ba_pcg_args;
 
 #define BA_PCG_LONG_LIST 32
