@@ -160,13 +160,28 @@ struct GatherWs {
     const int32_t* off_a;
     const int32_t* off_b;
     const int32_t* out_off;
+    const int32_t* blk_seg;
 };
 
-// one thread per output row; C depth channels copied per row
+// blk_seg[b] = the output image holding row b * TR_T (the first row of block b of k_gather_rows), for
+// the blocks whose first row is below min(total, n_rows): one thread per output image writes the
+// blocks that start inside its rows
+__global__ void __launch_bounds__(TR_T) k_block_seg(const int32_t* __restrict__ out_off, int64_t n_out, int64_t n_rows,
+                                                     int32_t* __restrict__ blk_seg) {
+    const int64_t j = (int64_t)blockIdx.x * TR_T + threadIdx.x;
+    if (j >= n_out) return;
+    const int64_t s = out_off[j], e = out_off[j + 1] < n_rows ? out_off[j + 1] : n_rows;
+    for (int64_t b = (s + TR_T - 1) / TR_T; b * TR_T < e; ++b) blk_seg[b] = (int32_t)j;
+}
+
+// one thread per output row; C depth channels copied per row.  The row's image is found from its
+// block's first image by stepping forward (a block of rows spans few images), not by a binary
+// search of all the offsets: one dependent load instead of about log2(n_out).
 __global__ void __launch_bounds__(TR_T) k_gather_rows(ba_gather_args a, GatherWs w) {
     const int64_t o = (int64_t)blockIdx.x * TR_T + threadIdx.x;
     if (o >= a.n_rows || o >= w.out_off[a.n_out]) return;
-    const int64_t j = find_segment(w.out_off, a.n_out, o);
+    int64_t j = w.blk_seg[blockIdx.x];
+    while (w.out_off[j + 1] <= o) ++j;
     int64_t k = o - w.out_off[j];
     const int32_t ia = a.sel_a ? a.sel_a[j] : -1;
     const int32_t na = (ia >= 0 && ia < a.a.n_imgs) ? a.a.nppi[ia] : 0;
@@ -333,8 +348,12 @@ extern "C" int ba_tracks_gather(const ba_gather_args* args, void* stream) {
     if (a.n_out > 0) hipLaunchKernelGGL(k_gather_counts, dim3(grid_of(a.n_out)), dim3(TR_T), 0, st, a, cnt);
     scan_i32(cnt, a.n_out, out_off, bsum, st);
     hipLaunchKernelGGL(k_copy_counts, dim3(grid_of(a.n_out)), dim3(TR_T), 0, st, cnt, a.n_out, a.nppi, out_off, a.total);
-    if (a.n_rows > 0 && a.n_out > 0)
-        hipLaunchKernelGGL(k_gather_rows, dim3(grid_of(a.n_rows)), dim3(TR_T), 0, st, a, GatherWs{off_a, off_b, out_off});
+    if (a.n_rows > 0 && a.n_out > 0) {
+        // r0 (n_rows + 1 ints, unused by the gather) holds the per-block first image
+        hipLaunchKernelGGL(k_block_seg, dim3(grid_of(a.n_out)), dim3(TR_T), 0, st, out_off, a.n_out, a.n_rows, r0);
+        hipLaunchKernelGGL(k_gather_rows, dim3(grid_of(a.n_rows)), dim3(TR_T), 0, st, a,
+                           GatherWs{off_a, off_b, out_off, r0});
+    }
     BA_LAUNCHED();
     return BA_OK;
 }
