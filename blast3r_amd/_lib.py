@@ -70,7 +70,8 @@ class BaPcgArgs(ctypes.Structure):
                 ('rhs', c_p), ('diagA', c_p), ('damp', c_p), ('x', c_p), ('xbest', c_p), ('r', c_p), ('z', c_p),
                 ('p', c_p), ('y_img', c_p), ('partials', c_p), ('state', c_p), ('istate', c_p),
                 ('S_rows', c_p), ('n_row_ent', c_i64), ('row_u', c_p), ('long_u', c_p), ('n_long', c_i64),
-                ('long_ptr', c_p), ('long_idx', c_p), ('img_part', c_p), ('src1', c_p), ('long_rng', c_p)]
+                ('long_ptr', c_p), ('long_idx', c_p), ('img_part', c_p), ('src1', c_p), ('long_rng', c_p),
+                ('row_cap', c_int)]
 
 PCG_LONG_LIST = 32          # BA_PCG_LONG_LIST in include/ba_hip.h
 PCG_BLOCK = 256             # unknowns per block of the PCG update launch (long_ptr granularity)

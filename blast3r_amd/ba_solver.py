@@ -330,10 +330,16 @@ class GaussNewtonSolver:
             pa.r, pa.z, pa.p, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(y_img)
             pa.img_part = ptr(ws('pcg_img_part', (n_imgs,), torch.float64))
             pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
-            n_ent = int(plan.host['row_ptr'][-1]) if len(plan.host['row_ptr']) else 0
-            S_rows = ws('pcg_S_rows', (max(n_ent, 1), d, d), torch.float64)
-            pa.S_rows, pa.n_row_ent = ptr(S_rows), n_ent
-            pa.row_u = ptr(ws('pcg_row_u', (max(n_ent, 1) * 16,), torch.int32))
+            rp = plan.host['row_ptr']
+            n_ent = int(rp[-1]) if len(rp) else 0
+            # rows at a fixed capacity (the SpMV then needs no row_ptr load) when that pads by <= 25%
+            longest = int(np.diff(rp).max()) if len(rp) > 1 else 0
+            cap = -(-longest // 8) * 8
+            row_cap = cap if 0 < cap and n_imgs * cap <= 1.25 * n_ent else 0
+            n_blk = n_imgs * row_cap if row_cap else n_ent
+            S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float64)
+            pa.S_rows, pa.n_row_ent, pa.row_cap = ptr(S_rows), n_ent, row_cap
+            pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * 16,), torch.int32))
             pa.long_u, pa.n_long = ptr(um['long_u']), um['n_long']
             pa.long_ptr, pa.long_idx = ptr(um['long_ptr']), ptr(um['long_idx'])
             pa.src1, pa.long_rng = ptr(um['src1']), ptr(um['long_rng'])

@@ -180,9 +180,19 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
     const int d = a.d, dd = d * d;
     const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
     if (tid >= n_ent * per) return;
-    const int64_t q = tid / per;
+    const int64_t q = tid / per;                       // destination block
     const int e = (int)(tid - q * per);
-    const int ent = a.row_ent[q];
+    int64_t qs = q;                                    // its source entry of row_ent
+    if (a.row_cap > 0) {                               // fixed capacity: row i at [i cap, (i + 1) cap)
+        const int64_t i = q / a.row_cap, k = q - i * a.row_cap;
+        qs = a.row_ptr[i] + k;
+        if (qs >= a.row_ptr[i + 1]) {                  // past the row's end: a zero block, no unknowns
+            if (e < dd) a.S_rows[q * dd + e] = 0.0;
+            if (e < 16) a.row_u[q * 16 + e] = -1;
+            return;
+        }
+    }
+    const int ent = a.row_ent[qs];
     const int64_t p = ent >> 1;
     if (e < dd) {
         const int j2 = e / d, j = e - (e / d) * d;
@@ -234,7 +244,9 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
         uo = a.umap[(int64_t)i * d + j];
         if (uo >= 0) { zo = a.z[uo]; po = pold[uo]; }
     }
-    const int q0 = a.row_ptr[i], q1 = a.row_ptr[i + 1];
+    // the row's blocks: from the fixed capacity when set (no load on this chain), else from row_ptr
+    const int q0 = a.row_cap > 0 ? i * a.row_cap : a.row_ptr[i];
+    const int q1 = a.row_cap > 0 ? q0 + a.row_cap : a.row_ptr[i + 1];
     auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[16]) {
         const bool live = q < q1;
         u = live ? a.row_u[(int64_t)q * 16 + j] : -1;
@@ -448,7 +460,8 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     }
     const unsigned nb = nb_of(a.n_u);
     const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));        // wave per unknown (setup)
-    const int64_t n_ent = a.n_row_ent;
+    BA_REQUIRE(a.row_cap >= 0 && a.row_cap % (PCG_ST / 16) == 0, "row_cap must be a multiple of 8");
+    const int64_t n_ent = a.row_cap > 0 ? (int64_t)a.n_imgs * a.row_cap : a.n_row_ent;
     BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
     const int per = a.d * a.d > 16 ? a.d * a.d : 16;
     if (n_ent > 0)

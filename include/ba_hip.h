@@ -179,6 +179,10 @@ typedef struct {
     const int32_t *src1;               /* (n_u): the only entry of u's inv list when it has exactly one,
                                           else -1 */
     const int32_t *long_rng;           /* (2 n_long): the inv-list bounds of long_u[k] */
+    int32_t row_cap;                   /* 0: S_rows / row_u hold row i's blocks at [row_ptr[i], row_ptr[i+1]);
+                                          > 0 (a multiple of 8, at least every row's length): at
+                                          [i row_cap, (i+1) row_cap), the rest zero blocks with unknown -1,
+                                          and S_rows / row_u sized for n_imgs * row_cap blocks */
 } ba_pcg_args;
 
 #define BA_PCG_LONG_LIST 32
