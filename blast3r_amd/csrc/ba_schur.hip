@@ -389,24 +389,24 @@ __global__ void __launch_bounds__(256) k_point_factor(const double* __restrict__
     const int64_t ct = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (ct >= n_ct) return;
     double H[6], Lf[6];
+    const double2* h2 = reinterpret_cast<const double2*>(Hpp + 6 * ct);      // 16-byte aligned rows
 #pragma unroll
-    for (int k = 0; k < 6; ++k) H[k] = Hpp[6 * ct + k];
+    for (int k = 0; k < 3; ++k) { const double2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
     chol3_factor(H, lam_p[0], Lf);
     const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
     const double g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
     const double w0 = g0 * r0;
     const double w1 = (g1 - Lf[1] * w0) * r1;
     const double w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
-    double* o = pf + 12 * ct;
-#pragma unroll
-    for (int k = 0; k < 6; ++k) o[k] = Lf[k];
-    o[6] = w0; o[7] = w1; o[8] = w2;
-    o[9] = r0; o[10] = r1; o[11] = r2;
+    double2* o = reinterpret_cast<double2*>(pf + 12 * ct);
+    o[0] = make_double2(Lf[0], Lf[1]); o[1] = make_double2(Lf[2], Lf[3]); o[2] = make_double2(Lf[4], Lf[5]);
+    o[3] = make_double2(w0, w1); o[4] = make_double2(w2, r0); o[5] = make_double2(r1, r2);
 }
 
 // ----------------------------------------------------------------------------- camera-pair blocks
 //
-// k_schur: one workgroup (16 waves, four per SIMD) per batch.  Per chunk of 128 observation slots:
+// k_schur: one workgroup (16 waves, four per SIMD) per CU, taking batches from a work queue.  Per
+// chunk of 128 observation slots:
 //   A1  waves 0-5, lane per (slot, row r): row r of the weighted camera rows J_c from the slot's
 //       linearisation record (rows 3-5 of the slot's LDS block, column 15 = W r / sqrt(W)) and row
 //       r of the point rows J_p, except the z-coefficient columns of row 2 (the depth row), which
@@ -948,6 +948,7 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
                            a.lay.x_off, a.lam_p);
         if (a.n_chunks > 0) {
             BA_REQUIRE(a.pfac != nullptr, "point-factor scratch missing");
+            BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
             hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
                                a.n_ctracks, a.pfac);
         }

@@ -106,7 +106,7 @@ typedef struct {
     ba_layout lay;
     /* per-track state in chunk-track order (the plan's ct_* arrays): H_pp upper (n_ctracks,6) and
      * g_p (n_ctracks,3) in fp64, the point and its enable flag (n_ctracks,4) in fp32 */
-    double *Hpp, *gp;
+    double *Hpp, *gp;    /* Hpp 16-byte aligned */
     double *chunk_max;   /* (n_chunks + 1) scratch */
     double *lam_p;       /* (1) point-leaf damping value, written by ba_linearize_schur */
     /* partial blocks: (n_slots, d, d) and (n_batches, L, 2, d) scratch */
@@ -127,7 +127,7 @@ typedef struct {
     double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0) */
     const int32_t *chunk_slots, *chunk_ent, *chunk_eptr;   /* plan: MFMA entry lists of every chunk */
     const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
-    double* pfac;         /* (n_ctracks,12) scratch written by stage 0: Cholesky factor L of H_pp + lam_p I
+    double* pfac;         /* (n_ctracks,12) 16-byte aligned scratch written by stage 0: Cholesky factor L of H_pp + lam_p I
                              (upper storage), w = L^-1 g_p, reciprocal pivots */
     const int32_t* b_order;  /* plan: batches in dispatch order (most expensive first); NULL = 0, 1, ... */
     int32_t* work_ctr;       /* 1 int of device scratch: the camera-pair kernel's batch queue (one
