@@ -152,6 +152,8 @@ def main():
         cpu = cpu_baseline(args.config)
         log(f'[bench] cpu baseline {cpu}')
 
+    triad = stream_triad(dev)
+    log(f'[bench] STREAM triad (fp64, 3 x 1 GiB): {triad:.0f} GB/s achievable')
     line = {
         'metric': 'BA linearize+Schur obs/sec & LM iters/sec at 1024 frames; % HBM roofline',
         'value': value, 'unit': 'obs/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
@@ -166,7 +168,8 @@ def main():
                      'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': 'k_schur',
                      'kernel_ms': schur_ms, 'flops_per_launch': flops_pairs, 'traffic_source': traffic_src},
         'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
-                         'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)'},
+                         'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)',
+                         'achievable_triad': triad},
         'cpu_baseline': cpu,
         'f_sampling': smp,
         'layout': lay,
@@ -248,6 +251,30 @@ def bench_layout(prob, g, dev, steps, warmup):
                          'kernel': 'ba_tracks_gather (k_gather_rows + offsets)',
                          'traffic': measured_traffic(2, 'k_gather_rows')[0] if prob.n_imgs == 1024 else None},
             'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s}
+
+
+def stream_triad(dev, n=1 << 27, reps=10):
+    """Achievable HBM bandwidth: ba_stream_triad (a = b + s c, fp64) over three 1 GiB arrays, the best
+    of `reps` launches timed with events on the launch stream; 24 bytes moved per element."""
+    from blast3r_amd._lib import check, lib, stream_ptr
+    a = torch.empty(n, dtype=torch.float64, device=dev)
+    b = torch.ones(n, dtype=torch.float64, device=dev)
+    c = torch.full((n,), 2.0, dtype=torch.float64, device=dev)
+    L, st = lib(), stream_ptr(dev)
+    stream = torch.cuda.current_stream(dev)
+    best = None
+    for r in range(reps + 2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        check(L.ba_stream_triad(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0.5, n, st))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if r >= 2:
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+    assert float(a[0]) == 2.0 and float(a[-1]) == 2.0
+    del a, b, c
+    return 24 * n / (best * 1e-3) / 1e9
 
 
 def bench_tangent(prob, g, dev, steps, warmup):

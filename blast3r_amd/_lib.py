@@ -135,6 +135,7 @@ _SIGS = {
     'ba_objective_workspace_bytes': (c_i64, [c_i64]),
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
     'ba_nonfinite_flags': (c_int, [c_p, c_p, c_int, c_p, c_p]),
+    'ba_stream_triad': (c_int, [c_p, c_p, c_p, ctypes.c_double, c_i64, c_p]),
     'ba_sample_depth': (c_int, [ctypes.POINTER(BaSampleArgs), c_p]),
     'ba_tracks_gather': (c_int, [ctypes.POINTER(BaGatherArgs), c_p]),
     'ba_tracks_remove': (c_int, [ctypes.POINTER(BaRemoveArgs), c_p]),

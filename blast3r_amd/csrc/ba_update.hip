@@ -7,6 +7,8 @@
 //                    select on the fp32 bit patterns instead of a full sort.
 //   ba_nonfinite_flags  the `tensor.isfinite().all()` input checks of lm_step (engine.py:340-344)
 //                    for every fp32 input in one launch.
+//   ba_stream_triad  a = b + s c in fp64 (STREAM triad): the achievable HBM bandwidth that the
+//                    benchmark reports beside the roofline fractions (no counterpart in the reference).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <cmath>
@@ -239,11 +241,39 @@ __global__ void __launch_bounds__(NF_T) k_nonfinite(NfSpans sp, int32_t* flags) 
     if (bad) flags[t] = 1;
 }
 
+// ------------------------------------------------------------------ STREAM triad
+__global__ void __launch_bounds__(256) k_triad(double* __restrict__ a, const double* __restrict__ b,
+                                               const double* __restrict__ c, double s, int64_t n) {
+    const int64_t n2 = n >> 1;
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x, gs = (int64_t)gridDim.x * 256;
+    for (int64_t i = g; i < n2; i += gs) {
+        const double2 x = reinterpret_cast<const double2*>(b)[i], y = reinterpret_cast<const double2*>(c)[i];
+        reinterpret_cast<double2*>(a)[i] = make_double2(x.x + s * y.x, x.y + s * y.y);
+    }
+    if (g == 0 && (n & 1)) a[n - 1] = b[n - 1] + s * c[n - 1];
+}
+
 }  // namespace ba
 
 using namespace ba;
 
 static inline unsigned nbk(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// a[i] = b[i] + s * c[i], i < n (fp64, 16-byte aligned arrays)
+extern "C" int ba_stream_triad(double* a, const double* b, const double* c, double s, int64_t n, void* stream) {
+    clear_error();
+    BA_REQUIRE(n >= 0, "bad size");
+    if (n == 0) return BA_OK;
+    BA_REQUIRE(a && b && c, "null array");
+    BA_REQUIRE((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0, "arrays must be 16-byte aligned");
+    // a large grid with few elements per thread streams best (measured on MI355X over 3 x 1 GiB:
+    // 5.5 TB/s at 65536 blocks against 4.6-5.0 TB/s at 2048-16384 blocks or with unrolled loads)
+    int64_t nb = (n / 2 + 255) / 256;
+    nb = nb < 1 ? 1 : (nb > 65536 ? 65536 : nb);
+    hipLaunchKernelGGL(k_triad, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, a, b, c, s, n);
+    BA_LAUNCHED();
+    return BA_OK;
+}
 
 // flags[t] = 1 when ptrs[t][0 .. counts[t]) holds a NaN or an infinity (fp32), else 0.
 extern "C" int ba_nonfinite_flags(const float* const* ptrs, const int64_t* counts, int32_t n_spans, int32_t* flags,

@@ -224,6 +224,11 @@ int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspa
 int ba_nonfinite_flags(const float* const* ptrs, const int64_t* counts, int32_t n_spans, int32_t* flags,
                        void* stream);
 
+/* Measurement helper with no counterpart in the reference: STREAM triad a = b + s c over n fp64
+ * values (16-byte aligned device arrays), whose bandwidth the benchmark reports as the achievable
+ * HBM figure beside the roofline fractions. */
+int ba_stream_triad(double* a, const double* b, const double* c, double s, int64_t n, void* stream);
+
 /* ------------------------------------------------------------------ F sampling */
 
 /* Multi-depth values at the observations (replaces the per-image bilinear_sampling calls of

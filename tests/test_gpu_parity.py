@@ -566,3 +566,21 @@ def test_schur_work_queue_is_deterministic():
 
 def ptr_of(ctx, name):
     return ctx['plan'].workspace(name, (1,), torch.int32).data_ptr()
+
+
+def test_stream_triad():
+    """ba_stream_triad (the benchmark's achievable-bandwidth probe) computes a = b + s c exactly
+    (one fp64 multiply-add per element, as torch's b + s * c rounds it) for even and odd sizes,
+    and rejects arrays that are not 16-byte aligned."""
+    from blast3r_amd._lib import lib, stream_ptr
+    for n in (1, 2, 7, 1000, 262145):
+        b = torch.randn(n + 2, dtype=torch.float64, device=DEV)
+        c = torch.randn(n + 2, dtype=torch.float64, device=DEV)
+        a = torch.full((n + 2,), 7.0, dtype=torch.float64, device=DEV)
+        assert lib().ba_stream_triad(a.data_ptr(), b.data_ptr(), c.data_ptr(), 0.25, n, stream_ptr(DEV)) == 0
+        torch.cuda.synchronize()
+        ref = torch.addcmul(b[:n], c[:n], torch.tensor(0.25, dtype=torch.float64, device=DEV))
+        assert torch.allclose(a[:n], ref, rtol=1e-15, atol=0), n
+        assert torch.all(a[n:] == 7.0)                        # nothing written past n
+    x = torch.zeros(8, dtype=torch.float64, device=DEV)
+    assert lib().ba_stream_triad(x.data_ptr() + 8, x.data_ptr(), x.data_ptr(), 1.0, 4, stream_ptr(DEV)) != 0
