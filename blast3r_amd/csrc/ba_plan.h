@@ -3,12 +3,8 @@
 
 #define BA_CHUNK 128          // observation slots per chunk (one slot per lane in the per-observation phases)
 #define BA_MAX_LOCAL 16       // images a batch may touch (bit mask in 32 bits, local ids in 8 bits)
-#ifndef BA_WAVES
 #define BA_WAVES 16           // waves per workgroup of the fused Schur kernel (four per SIMD)
-#endif
-#ifndef BA_SLOTS_PER_WAVE
 #define BA_SLOTS_PER_WAVE 6   // camera-pair accumulators held in registers by one wave
-#endif
 #define BA_MAX_SLOTS (BA_WAVES * BA_SLOTS_PER_WAVE)
 #define BA_MAX_CT 64          // tracks per chunk (coverage bit masks in 64 bits)
 
