@@ -97,6 +97,7 @@ __global__ void __launch_bounds__(256) k_apply_update(const float* __restrict__ 
 
 // ------------------------------------------------------------------ objective
 #define OBJ_T 256
+#define OBJ_NBMAX 2048
 
 __global__ void k_obj_init(uint32_t* __restrict__ hist, uint32_t* __restrict__ sel, uint32_t k) {
     hist[threadIdx.x] = 0;
@@ -106,13 +107,12 @@ __global__ void k_obj_init(uint32_t* __restrict__ hist, uint32_t* __restrict__ s
 __global__ void __launch_bounds__(OBJ_T) k_obj_prep(const float* __restrict__ res, int64_t n, int has_err,
                                                    uint32_t* __restrict__ ebits, double* __restrict__ part) {
     __shared__ double sh[OBJ_T];
-    int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x;
     double s = 0.0;
-    if (i < n) {
+    for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
         float r0 = res[i], r1 = res[n + i];
         float e = sqrtf(r0 * r0 + r1 * r1);
         ebits[i] = __float_as_uint(e);
-        if (has_err) s = (double)res[3 * n + i] + (double)res[4 * n + i] + (double)res[5 * n + i];
+        if (has_err) s += (double)res[3 * n + i] + (double)res[4 * n + i] + (double)res[5 * n + i];
     }
     sh[threadIdx.x] = s;
     __syncthreads();
@@ -123,20 +123,28 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_prep(const float* __restrict__ re
     if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
 }
 
-// histogram of the next 8 bits among values whose higher bits equal the prefix
+// histogram of the next 8 bits among values whose higher bits equal the prefix.  The values cluster
+// in few bins (the top byte is the exponent), so each block keeps 8 sub-histograms (lane & 7; rows
+// 257 words apart, so a bin's copies lie in different LDS banks) to spread the atomic increments.
+#define OBJ_SUBH 8
 __global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__ ebits, int64_t n,
                                                    const uint32_t* __restrict__ sel, int shift,
                                                    uint32_t* __restrict__ hist) {
-    __shared__ uint32_t h[256];
-    h[threadIdx.x] = 0;
+    __shared__ uint32_t h[OBJ_SUBH][257];
+#pragma unroll
+    for (int k = 0; k < OBJ_SUBH; ++k) h[k][threadIdx.x] = 0;
     __syncthreads();
     uint32_t prefix = sel[0], pmask = sel[1];
+    uint32_t* mine = h[threadIdx.x & (OBJ_SUBH - 1)];
     for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
         uint32_t b = ebits[i];
-        if ((b & pmask) == prefix) atomicAdd(&h[(b >> shift) & 0xffu], 1u);
+        if ((b & pmask) == prefix) atomicAdd(&mine[(b >> shift) & 0xffu], 1u);
     }
     __syncthreads();
-    if (h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+    uint32_t t = 0;
+#pragma unroll
+    for (int k = 0; k < OBJ_SUBH; ++k) t += h[k][threadIdx.x];
+    if (t) atomicAdd(&hist[threadIdx.x], t);
 }
 
 // pick the bin holding the k-th smallest (k in sel[2], 1-based); clear hist for the next pass
@@ -164,10 +172,9 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_below(const uint32_t* __restrict_
     uint32_t T = sel[0];
     double s = 0.0;
     uint32_t c = 0;
-    int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x;
-    if (i < n) {
+    for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
         uint32_t b = ebits[i];
-        if (b < T) { s = (double)__uint_as_float(b); c = 1; }
+        if (b < T) { s += (double)__uint_as_float(b); c += 1; }
     }
     sh[threadIdx.x] = s; sc[threadIdx.x] = c;
     __syncthreads();
@@ -339,22 +346,25 @@ extern "C" int ba_objective(const float* res, int64_t n_obs, int32_t has_err, vo
     uint32_t* hist = (uint32_t*)w; w += 4 * 256;
     uint32_t* sel = (uint32_t*)w;
     int64_t n80 = n_obs * 80 / 100;
+    // the per-block partials of prep and below: at most OBJ_NBMAX blocks (grid-stride loops), so the
+    // one-block final sum stays short
+    const int64_t nbp = nb < OBJ_NBMAX ? nb : OBJ_NBMAX;
     hipLaunchKernelGGL(k_obj_init, dim3(1), dim3(256), 0, st, hist, sel, (uint32_t)(n80 > 0 ? n80 : 1));
     if (n_obs > 0) {
-        hipLaunchKernelGGL(k_obj_prep, dim3((unsigned)nb), dim3(OBJ_T), 0, st, res, n_obs, has_err, ebits, lpart);
+        hipLaunchKernelGGL(k_obj_prep, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, res, n_obs, has_err, ebits, lpart);
         unsigned hb = (unsigned)(nb < 1024 ? nb : 1024);
         for (int pass = 0; pass < 4; ++pass) {
             int shift = 24 - 8 * pass;
             hipLaunchKernelGGL(k_obj_hist, dim3(hb), dim3(OBJ_T), 0, st, ebits, n_obs, sel, shift, hist);
             hipLaunchKernelGGL(k_obj_pick, dim3(1), dim3(64), 0, st, hist, sel, shift);
         }
-        hipLaunchKernelGGL(k_obj_below, dim3((unsigned)nb), dim3(OBJ_T), 0, st, ebits, n_obs, sel, psum, pcnt);
+        hipLaunchKernelGGL(k_obj_below, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, ebits, n_obs, sel, psum, pcnt);
     } else {
         hipLaunchKernelGGL(k_obj_prep, dim3(1), dim3(OBJ_T), 0, st, res, (int64_t)0, has_err, ebits, lpart);
         hipLaunchKernelGGL(k_obj_below, dim3(1), dim3(OBJ_T), 0, st, ebits, (int64_t)0, sel, psum, pcnt);
     }
-    hipLaunchKernelGGL(k_obj_final, dim3(1), dim3(OBJ_T), 0, st, lpart, psum, pcnt, (int)nb, n_obs, n80, sel, has_err,
-                       out);
+    hipLaunchKernelGGL(k_obj_final, dim3(1), dim3(OBJ_T), 0, st, lpart, psum, pcnt, n_obs > 0 ? (int)nbp : 1, n_obs,
+                       n80, sel, has_err, out);
     BA_LAUNCHED();
     return BA_OK;
 }
