@@ -350,6 +350,10 @@ class GaussNewtonSolver:
         if en['X'][0] and sc['n_chunks'] > 0:
             a.dc = ptr(x)
             a.umap = ptr(um['umap'])
+            if 'umap_pad' not in um:                   # -1 -> the appended zero, once per structure
+                um['umap_pad'] = torch.where(um['umap'] >= 0, um['umap'], x.numel()).long().view(-1)
+            dc_img = torch.nn.functional.pad(x, (0, 1))[um['umap_pad']]
+            a.dc_img = ptr(dc_img)                     # delta_c at image level (one load fewer per obs)
             a.dX = ptr(dX)
             a.dX64 = None
             check(lib().ba_backsubstitute(a, st))

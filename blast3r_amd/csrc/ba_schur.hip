@@ -826,10 +826,15 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         core_load(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
         double xs[16];
+        if (a.dc_img != nullptr) {                     // image-level copy: one load fewer
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int u = j < d ? a.umap[(int64_t)img * d + j] : -1;
-            xs[j] = u >= 0 ? a.dc[u] : 0.0;
+            for (int j = 0; j < 16; ++j) xs[j] = j < d ? a.dc_img[(int64_t)img * d + j] : 0.0;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int u = j < d ? a.umap[(int64_t)img * d + j] : -1;
+                xs[j] = u >= 0 ? a.dc[u] : 0.0;
+            }
         }
         double t[3] = {0.0, 0.0, 0.0};
         emit_jc<HK, HP>(o, a.lay, ctx.enK, ctx.enP, ctx.enZ, obs == 0, dep,
@@ -913,7 +918,8 @@ static const char* missing_pointer(const ba_lin_args& a, int stage) {
     BA_NEED(stage == 2, a.pair_ptr); BA_NEED(stage == 2, a.pair_src); BA_NEED(stage == 2, a.img_ptr);
     BA_NEED(stage == 2, a.img_src); BA_NEED(stage == 2, a.partials); BA_NEED(stage == 2, a.img_partials);
     BA_NEED(stage == 2, a.S_pairs); BA_NEED(stage == 2, a.e_img); BA_NEED(stage == 2, a.dg_img);
-    BA_NEED(stage == 3, a.dc); BA_NEED(stage == 3, a.umap); BA_NEED(stage == 3, a.dX);
+    BA_NEED(stage == 3 && a.dc_img == nullptr, a.dc); BA_NEED(stage == 3 && a.dc_img == nullptr, a.umap);
+    BA_NEED(stage == 3, a.dX);
 #undef BA_NEED
     return nullptr;
 }

@@ -132,6 +132,8 @@ typedef struct {
     const int32_t* b_order;  /* plan: batches in dispatch order (most expensive first); NULL = 0, 1, ... */
     int32_t* work_ctr;       /* 1 int of device scratch: the camera-pair kernel's batch queue (one
                                 workgroup per CU); NULL = one workgroup per batch */
+    const double* dc_img;    /* optional (n_imgs, d): delta_c at image level (dc[umap], 0 where umap is
+                                -1), read by the back-substitution instead of dc through umap */
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.
