@@ -412,8 +412,9 @@ __global__ void __launch_bounds__(256) k_point_factor(const double* __restrict__
 //       r of the point rows J_p, except the z-coefficient columns of row 2 (the depth row), which
 //       waves 6-7 form, lane per slot (waves w and w + 4 share a SIMD: this spreads phase A evenly
 //       over the four).  The point blocks' Cholesky factors come precomputed (k_point_factor).
-//   A2  waves 0-5, lane per (slot, column c): column c of V = J_c^T J_p L^-T (row c of the block,
-//       column 15 = w for the first observation of the track in the image, else 0); several
+//   A2  waves 0-11, lane per (slot, column c, half h): column c of V = J_c^T J_p L^-T at the image-level
+//       columns [8h, 8h + 8) (row c of the block, column 15 = w for the first observation of the track
+//       in the image, else 0); several
 //       observations of one track in one image are then summed into the first one.
 //   B   every wave, for each camera-pair slot it owns (accumulator in registers), over the slot's
 //       entry list (built by the planner once per structure):
@@ -626,28 +627,39 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         }
         __syncthreads();
 
-        // ---------------- A2: V = J_c^T P with P = J_p L^-T; lane (slot, rr) forms column c = rr
-        if (row_lane && rr < 3 && valid) {
-            const int c = rr;
-            const double (*F)[BA_MAX_CT][2] = sSt.pf;          // element i of track ct at F[i / 2][ct][i % 2]
-            const double l10 = F[0][ct][1], l20 = F[1][ct][0], l21 = F[2][ct][0];
-            const double r0 = F[4][ct][1], r1 = F[5][ct][0], r2 = F[5][ct][1];
-            const double wc = c == 0 ? F[3][ct][0] : (c == 1 ? F[3][ct][1] : F[4][ct][0]);
-            double Pc[3];
+        // ---------------- A2: V = J_c^T P with P = J_p L^-T; waves 0-11, lane (slot t, task q = tid / 128)
+        // forms column c = q % 3 of V at the image-level columns [8h, 8h + 8), h = q / 3 (h = 1 also
+        // writes column 15, the rhs term); the slot's status comes from sInfo (written in A1)
+        if (tid < 6 * BA_CHUNK) {
+            const int info2 = sInfo[t];
+            if (info2 >= 0) {
+                const int q = tid >> 7, c = q % 3, h = q / 3;
+                const int ct2 = (info2 >> 8) & 0xff, leader2 = info2 >> 16;
+                const double (*F)[BA_MAX_CT][2] = sSt.pf;      // element i of track ct at F[i / 2][ct][i % 2]
+                const double l10 = F[0][ct2][1], l20 = F[1][ct2][0], l21 = F[2][ct2][0];
+                const double r0 = F[4][ct2][1], r1 = F[5][ct2][0], r2 = F[5][ct2][1];
+                double Pc[3];
 #pragma unroll
-            for (int r = 0; r < 3; ++r) {
-                const double p0 = sJp[t][3 * r] * r0;
-                const double p1 = (sJp[t][3 * r + 1] - l10 * p0) * r1;
-                const double p2 = (sJp[t][3 * r + 2] - l20 * p0 - l21 * p1) * r2;
-                Pc[r] = c == 0 ? p0 : (c == 1 ? p1 : p2);
-            }
-            double* blk = sBlk + t * BA_BLK;
+                for (int r = 0; r < 3; ++r) {
+                    const double p0 = sJp[t][3 * r] * r0;
+                    const double p1 = (sJp[t][3 * r + 1] - l10 * p0) * r1;
+                    const double p2 = (sJp[t][3 * r + 2] - l20 * p0 - l21 * p1) * r2;
+                    Pc[r] = c == 0 ? p0 : (c == 1 ? p1 : p2);
+                }
+                double* blk = sBlk + t * BA_BLK;
 #pragma unroll
-            for (int j = 0; j < 15; ++j) {
-                const double j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
-                blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : 0.0;
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int j = 8 * h + jj;
+                    if (j < 15) {
+                        const double j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
+                        blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : 0.0;
+                    }
+                }
+                if (h == 1) {
+                    const double wc = c == 0 ? F[3][ct2][0] : (c == 1 ? F[3][ct2][1] : F[4][ct2][0]);
+                    blk[16 * c + 15] = leader2 == t ? wc : 0.0;
+                }
             }
-            blk[16 * c + 15] = leader == t ? wc : 0.0;
         }
         __syncthreads();
         if (sDup[0] | sDup[1]) {
