@@ -429,13 +429,15 @@ def test_bundle_adjustment_reuses_trial_objective_exactly():
         assert torch.equal(got, var[k]), k
 
 
-def test_bundle_adjustment_parity():
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 20, 600), (3, 20, 500)])
+def test_bundle_adjustment_parity(cfg, nf, nt):
     """Two phases (pnorm 1 then 0.5; n_zcfs 3 -> first coefficient frozen, 4 columns) against the
-    oracle's bundle_adjustment.  As for lm_step, the reference's PCG tolerance fixes each step only
-    up to a spread, measured here between the oracle at tol 1e-6 and at 1e-10: the GPU parameters
-    must agree with the oracle's to max(1e-4, 4 * spread) relative."""
+    oracle's bundle_adjustment, on a circle (config 0), forward motion (config 2) and random
+    neighbours with a camera per frame (config 3).  As for lm_step, the reference's PCG tolerance
+    fixes each step only up to a spread, measured here between the oracle at tol 1e-6 and at 1e-10:
+    the GPU parameters must agree with the oracle's to max(1e-4, 4 * spread) relative."""
     from blast3r_amd.data import from_problem
-    p = make_problem(0, n_frames=8, n_tracks=300)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
     o = p.options
     kw = dict(max_iters=[2, 2], pnorm=[1.0, 0.5], n_zcfs=[3, None], weight_z=o['weight_z'],
               huber_delta=o['huber_delta'])
