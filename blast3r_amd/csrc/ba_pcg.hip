@@ -28,7 +28,8 @@ enum { PT_RR = 0, PT_RZ = 1 };
 
 // state (fp64): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
 // both in slot n & 1; ST_BETA the beta of the current direction; ST_LEAF.. the camera-leaf damping.
-enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_BETA = 5, ST_LEAF = 8 };
+// ST_LEAFMAX.. (3 words): the per-leaf maxima of |diag(A)| as bit patterns, accumulated by k_leaf_max.
+enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_BETA = 5, ST_LEAF = 8, ST_LEAFMAX = 11 };
 // istate: IS_DONE0 / IS_DONE1 "stopped before update n" in slot n & 1, IS_K iterations run,
 // IS_CONV converged, IS_BESTK best iterate, IS_USEBEST the best iterate is returned.
 enum { IS_DONE0 = 0, IS_DONE1 = 1, IS_K = 2, IS_CONV = 3, IS_BESTK = 4, IS_USEBEST = 5 };
@@ -91,6 +92,8 @@ __device__ __forceinline__ void sum_partials(const double* __restrict__ part, in
 // shared unknowns (one focal pair for every image of a camera) reduce in parallel
 __global__ void __launch_bounds__(PCG_T) k_unk_setup(ba_pcg_args a) {
     const int lane = threadIdx.x & 63;
+    if (blockIdx.x == 0 && threadIdx.x < 3)                  // k_leaf_max's accumulators
+        reinterpret_cast<unsigned long long*>(a.state)[ST_LEAFMAX + threadIdx.x] = 0ull;
     int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);
     if (u >= a.n_u) return;
     double e = 0.0, g = 0.0;
@@ -109,32 +112,49 @@ __global__ void __launch_bounds__(PCG_T) k_unk_setup(ba_pcg_args a) {
 // per-leaf damping (BlockDiagMat.dampen_, ba_solver.py:575-582) and the Jacobi preconditioner.
 // leaf ids 0..2 = foc, tau, zcf; 3..5 = the same groups switched off (a zero matrix damped by
 // dampen * I, ZerosMat.dampen_, ba_solver.py:510-517).
-__global__ void __launch_bounds__(PCG_T) k_leaf_damp(ba_pcg_args a) {
-    __shared__ double sh[PCG_T];
+// Two launches over every block of unknowns: the per-leaf maxima (fmax within a block; across blocks
+// an integer max of the bit patterns, which orders non-negative doubles as their values, so the
+// result does not depend on the order; a block whose maximum is NaN contributes nothing, as fmax
+// ignores NaN), then the damping and the clamped preconditioner diagonal per unknown.
+__global__ void __launch_bounds__(PCG_T) k_leaf_max(ba_pcg_args a) {
+    __shared__ double sh[3][PCG_T];
     double m[3] = {0.0, 0.0, 0.0};
-    for (int64_t u = threadIdx.x; u < a.n_u; u += PCG_T) {
-        int l = a.leaf[u];
+    for (int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x; u < a.n_u; u += (int64_t)gridDim.x * PCG_T) {
+        const int l = a.leaf[u];
         if (l < 3) m[l] = fmax(m[l], fabs(a.diagA[u]));
     }
-    double lam[6];
-    for (int l = 0; l < 3; ++l) {
-        sh[threadIdx.x] = m[l];
-        __syncthreads();
-        for (int w = PCG_T / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w) sh[threadIdx.x] = fmax(sh[threadIdx.x], sh[threadIdx.x + w]);
-            __syncthreads();
-        }
-        lam[l] = a.adaptive ? a.dampen * sh[0] : a.dampen;
-        lam[l + 3] = a.dampen;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) sh[l][threadIdx.x] = m[l];
+    __syncthreads();
+    for (int w = PCG_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w)
+#pragma unroll
+            for (int l = 0; l < 3; ++l) sh[l][threadIdx.x] = fmax(sh[l][threadIdx.x], sh[l][threadIdx.x + w]);
         __syncthreads();
     }
-    for (int64_t u = threadIdx.x; u < a.n_u; u += PCG_T) {
+    if (threadIdx.x < 3) {
+        const double v = sh[threadIdx.x][0];
+        if (!isnan(v))
+            atomicMax(reinterpret_cast<unsigned long long*>(a.state) + ST_LEAFMAX + threadIdx.x,
+                      (unsigned long long)__double_as_longlong(v));
+    }
+}
+
+__global__ void __launch_bounds__(PCG_T) k_leaf_damp(ba_pcg_args a) {
+    double lam[6];
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        const double mx = __longlong_as_double(reinterpret_cast<const long long*>(a.state)[ST_LEAFMAX + l]);
+        lam[l] = a.adaptive ? a.dampen * mx : a.dampen;
+        lam[l + 3] = a.dampen;
+    }
+    for (int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x; u < a.n_u; u += (int64_t)gridDim.x * PCG_T) {
         double dmp = lam[a.leaf[u]];
         a.damp[u] = dmp;
         double dA = a.diagA[u] + dmp;
         a.diagA[u] = dA > 1e-12 ? dA : 1e-12;          // diagA.clamp(min=1e-12) (ba_solver.py:191-192)
     }
-    if (threadIdx.x == 0) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
         for (int l = 0; l < 3; ++l) a.state[ST_LEAF + l] = lam[l];
     }
 }
@@ -468,7 +488,8 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
         hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
                            n_ent, per);
     hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_leaf_damp, dim3(1), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
     BA_LAUNCHED();
