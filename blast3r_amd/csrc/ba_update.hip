@@ -148,20 +148,46 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__
 }
 
 // pick the bin holding the k-th smallest (k in sel[2], 1-based); clear hist for the next pass
-__global__ void k_obj_pick(uint32_t* __restrict__ hist, uint32_t* __restrict__ sel, int shift) {
-    if (threadIdx.x != 0) return;
-    uint32_t k = sel[2];
-    uint32_t cum = 0;
-    int b = 0;
-    for (; b < 256; ++b) {
-        if (cum + hist[b] >= k) break;
-        cum += hist[b];
+// One wave: lane l holds bins 4l .. 4l + 3; an inclusive scan of the lane sums finds the lane, then
+// the bin, where the running count first reaches k (the same bin and count as a sequential walk;
+// when no bin reaches k: bin 255 with the full count, as that walk leaves them).
+__global__ void __launch_bounds__(64) k_obj_pick(uint32_t* __restrict__ hist, uint32_t* __restrict__ sel, int shift) {
+    const int l = threadIdx.x;
+    const uint32_t k = sel[2];
+    uint32_t h[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[q] = hist[4 * l + q];
+    const uint32_t s = h[0] + h[1] + h[2] + h[3];
+    uint32_t inc = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t t = __shfl_up(inc, off);
+        if (l >= off) inc += t;
     }
-    if (b > 255) b = 255;
-    sel[0] |= (uint32_t)b << shift;
-    sel[1] |= 0xffu << shift;
-    sel[2] = k - cum;
-    for (int q = 0; q < 256; ++q) hist[q] = 0;
+    const uint64_t ball = __ballot(inc >= k);
+    int b = 255;
+    uint32_t cum = __shfl(inc, 63);
+    if (ball) {
+        const int L = __ffsll((unsigned long long)ball) - 1;
+        uint32_t c = __shfl(inc - s, L);
+        uint32_t hl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hl[q] = __shfl(h[q], L);
+        int q = 0;
+        for (; q < 3; ++q) {
+            if (c + hl[q] >= k) break;
+            c += hl[q];
+        }
+        b = 4 * L + q;
+        cum = c;
+    }
+    if (l == 0) {
+        sel[0] |= (uint32_t)b << shift;
+        sel[1] |= 0xffu << shift;
+        sel[2] = k - cum;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hist[4 * l + q] = 0;
 }
 
 __global__ void __launch_bounds__(OBJ_T) k_obj_below(const uint32_t* __restrict__ ebits, int64_t n,
