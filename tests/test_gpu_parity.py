@@ -586,3 +586,39 @@ def test_stream_triad():
         assert torch.all(a[n:] == 7.0)                        # nothing written past n
     x = torch.zeros(8, dtype=torch.float64, device=DEV)
     assert lib().ba_stream_triad(x.data_ptr() + 8, x.data_ptr(), x.data_ptr(), 1.0, 4, stream_ptr(DEV)) != 0
+
+
+def test_backsubstitute_image_level_delta_matches_unknown_map():
+    """ba_backsubstitute gives the same point steps, bit for bit, whether it reads delta_c at image
+    level (dc_img) or through the unknown map (dc, umap), and with a masked parameter group."""
+    import ctypes
+    from blast3r_amd._lib import check, lib, ptr
+    p = make_problem(2, n_frames=20, n_tracks=600)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    for flags in ({}, dict(optim_P=False)):
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV)
+        J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
+        gs.solve_delta(J, res, w)
+        x, um, d = gs.last['x'], gs.last['unknowns'], gs.last['lay']['d']
+        ctx = gs.prepare(J, res, w)                    # the same workspace, records of this linearisation
+        a, st = ctx['args'], ctx['stream']
+        check(lib().ba_linearize_stage(ctypes.byref(a), 0, st))
+        umap = um['umap'].view(p.n_imgs, d).long()
+        dc_img = torch.where(umap >= 0, x[umap.clamp(min=0)], torch.zeros((), dtype=x.dtype, device=DEV))
+        outs = []
+        for use_img in (True, False):
+            dX = torch.zeros((p.n_tracks, 3), dtype=torch.float32, device=DEV)
+            a.dc, a.umap, a.dX, a.dX64 = ptr(x), ptr(um['umap']), ptr(dX), None
+            a.dc_img = ptr(dc_img) if use_img else None
+            check(lib().ba_backsubstitute(ctypes.byref(a), st))
+            torch.cuda.synchronize()
+            outs.append(dX)
+        assert torch.equal(outs[0], outs[1]), flags
+        assert outs[0].abs().sum() > 0
