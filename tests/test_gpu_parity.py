@@ -622,3 +622,53 @@ def test_backsubstitute_image_level_delta_matches_unknown_map():
             outs.append(dX)
         assert torch.equal(outs[0], outs[1]), flags
         assert outs[0].abs().sum() > 0
+
+
+def test_reduced_system_full_config2_against_oracle():
+    """The benchmark's own size (config 2: 1024 frames, 1 M tracks, 8.0 M observations): the reduced
+    rhs, the point blocks and S v for seeded v against the oracle's normal equations at the same
+    size (the oracle's pass takes a few seconds on the host's threads), to the 1e-5 bar."""
+    import os
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    p = make_problem(2)
+    assert p.n_imgs == 1024 and p.n_tracks == 1_000_000
+    print(f'[full cfg2] {p.n_obs} observations', flush=True)
+    gs, _, _ = _gpu_solver(p)
+    last = gs.last
+    um, d, plan = last['unknowns'], last['lay']['d'], last['plan']
+    rhs = last['rhs'].cpu()
+    H = gs.point_blocks()[0].cpu()
+    n_pairs = plan.scalars['n_pairs']
+    B = last['S_pairs'][:n_pairs].view(n_pairs, d, d)
+    i1 = plan.dev['pair_i1'][:n_pairs].long()
+    i2 = plan.dev['pair_i2'][:n_pairs].long()
+    umap = um['umap'].long().view(p.n_imgs, d)
+    valid = umap >= 0
+    n_u = int(um['n_u'])
+
+    def s_matvec(v):                                  # S_u v = P^T S_img P v + damp v
+        v = v.to(DEV)
+        v_img = torch.where(valid, v[umap.clamp(min=0)], torch.zeros((), dtype=v.dtype, device=DEV))
+        y_img = torch.zeros_like(v_img)
+        y_img.index_add_(0, i1, torch.bmm(B, v_img[i2].unsqueeze(2)).squeeze(2))
+        off = i1 != i2
+        Bt = B[off].transpose(1, 2).contiguous()
+        y_img.index_add_(0, i2[off], torch.bmm(Bt, v_img[i1[off]].unsqueeze(2)).squeeze(2))
+        y = torch.zeros(n_u, dtype=v.dtype, device=DEV)
+        y.index_add_(0, umap[valid], y_img[valid])
+        return (y + last['damp'] * v).cpu()
+
+    ne, gvec, _, _, _, _ = _oracle_ne(p)
+    print('[full cfg2] oracle normal equations built', flush=True)
+    assert rel_err(rhs, osol.reduced_rhs(ne, gvec)) < 1e-5
+    Hr = ne.leaves['pts'] - float(last['lam_p'].cpu()) * torch.eye(3, dtype=torch.float64)
+    iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
+    assert rel_err(H, torch.stack([Hr[:, i, j] for i, j in iu], 1)) < 1e-5
+    gen = torch.Generator().manual_seed(7)
+    for k in range(3):
+        v = torch.randn(n_u, dtype=torch.float64, generator=gen)
+        assert rel_err(s_matvec(v), osol.S_matvec(ne, v)) < 1e-5, k
+    # S v is symmetric: u.(S v) = v.(S u)
+    u = torch.randn(n_u, dtype=torch.float64, generator=gen)
+    a, b = torch.dot(u, s_matvec(v)), torch.dot(v, s_matvec(u))
+    assert abs(a - b) <= 1e-10 * (abs(a) + abs(b))
