@@ -672,3 +672,30 @@ def test_reduced_system_full_config2_against_oracle():
     u = torch.randn(n_u, dtype=torch.float64, generator=gen)
     a, b = torch.dot(u, s_matvec(v)), torch.dot(v, s_matvec(u))
     assert abs(a - b) <= 1e-10 * (abs(a) + abs(b))
+
+
+def test_lm_step_full_config2_objective_consistency():
+    """One lm_step at the benchmark's full config-2 size: its initial loss equals the oracle
+    objective at the inputs, and its post-step loss equals the oracle objective evaluated at the
+    parameters it returned (1e-5), so the device objective, update and line search agree with the
+    reference's arithmetic at that size; the step keeps every parameter finite."""
+    import os
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    p = make_problem(2)
+    o = p.options
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+              optim_P=o['optim_P'])
+    print(f'[full cfg2 lm_step] {p.n_obs} observations', flush=True)
+    up_g, st_g = gpu_engine.lm_step(**_gpu(p).lm_inputs(), **kw)
+    up = {k: v.cpu() for k, v in up_g.items()}
+    for k in ('K', 'z_coefs', 'pts3d', 'P_w2rig'):
+        assert torch.isfinite(up[k]).all(), k
+
+    def obj(K, P_w2rig, z_coefs, pts3d):
+        return float(oeng.objective(p.infos, K, p.P_rig2cam, P_w2rig, z_coefs, pts3d, p.pids, p.pix2d, p.pix2d_std,
+                                    p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'], o['huber_delta'])[0])
+    l0 = obj(p.K, p.P_w2rig, p.z_coefs, p.pts3d)
+    assert abs(float(st_g.init_loss) - l0) <= 1e-5 * abs(l0)
+    l1 = obj(up['K'], up['P_w2rig'], up['z_coefs'], up['pts3d'])
+    assert abs(float(st_g.new_loss) - (l1 + 1e-4)) <= 1e-5 * l1
+    print(f'[full cfg2 lm_step] loss {l0:.6g} -> {l1:.6g}', flush=True)
