@@ -181,5 +181,10 @@ def stream_ptr(device=None):
 
 
 def ptr(t):
-    """Raw device pointer of a tensor (None -> NULL)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Raw device pointer of a tensor (None -> NULL); a host tensor raises instead of handing a
+    host address to a kernel."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RuntimeError(f'expected a device tensor for a kernel argument, got one on {t.device}')
+    return ctypes.c_void_p(t.data_ptr())

@@ -47,8 +47,12 @@ class Linearization:
         return (3 * s.n_kpts, s.cams.n * N_FOC + s.nodes.n * N_TAU + s.imgs.n * s.n_zcf + s.tracks.n * 3)
 
 
-def _flag(status, name, count):
-    """Normalise an optim_* flag: returns (enabled_group, uint8 mask or None, kept indices or None)."""
+def _flag(status, name, count, device):
+    """Normalise an optim_* flag: returns (enabled_group, uint8 mask or None, kept indices or None).
+
+    A mask tensor must live on the solver's device: the kernels read it there.  The reference
+    indexes the mask with the device's per-observation ids (bs:98), which raises RuntimeError for a
+    host mask unless every entry is False (then it returns the zero matrix first, bs:91-92)."""
     if status is True:
         return True, None, None
     if status is False:
@@ -59,6 +63,9 @@ def _flag(status, name, count):
         idxs = status.nonzero().squeeze(-1)
         if len(idxs) == 0:
             return False, None, None     # all columns removed -> zero matrix (bs:91-92)
+        if status.device != device:
+            raise RuntimeError(f'{name}: indices should be either on cpu or on the same device as the indexed '
+                               f'tensor (mask on {status.device}, observations on {device})')
         return True, status.to(torch.uint8).contiguous(), idxs
     raise ValueError(f'bad {name}={status}')
 
@@ -98,10 +105,11 @@ class GaussNewtonSolver:
         self.n_zcf = int(z_coefs.shape[1])
         assert pix2d_dep.shape == (self.n_kpts, self.n_zcf)
         en = {}
-        en['K'] = _flag(optim_K, 'optim_K', self.cams.n)
-        en['P'] = _flag(optim_P, 'optim_P', self.nodes.n)
-        en['Z'] = _flag(optim_Z, 'optim_Z', self.imgs.n)
-        en['X'] = _flag(optim_X, 'optim_X', self.tracks.n)
+        dev = pids.device
+        en['K'] = _flag(optim_K, 'optim_K', self.cams.n, dev)
+        en['P'] = _flag(optim_P, 'optim_P', self.nodes.n, dev)
+        en['Z'] = _flag(optim_Z, 'optim_Z', self.imgs.n, dev)
+        en['X'] = _flag(optim_X, 'optim_X', self.tracks.n, dev)
         for key, par in (('K', self.cams), ('P', self.nodes), ('Z', self.imgs), ('X', self.tracks)):
             if en[key][2] is not None:              # column compaction (bs:86-104)
                 par.n = len(en[key][2])
@@ -121,9 +129,12 @@ class GaussNewtonSolver:
         """
         d, C = lay['d'], self.n_zcf
         n_imgs = self.imgs.true_n
-        ident = lambda t: None if t is None else (t.data_ptr(), t._version, tuple(t.shape))
+        # masks are keyed by content: a new mask tensor may reuse a freed one's address and version
+        host_idx = {k: (None if J.en[k][2] is None else J.en[k][2].cpu().numpy().astype(np.int64))
+                    for k in ('K', 'P', 'Z')}
+        ident = lambda a: None if a is None else (len(a), a.tobytes())
         key = (d, C, lay['hasK'], lay['hasP'], lay['hasZ'], self.cams.n, self.nodes.n, self.imgs.n, n_imgs,
-               ident(J.en['K'][2]), ident(J.en['P'][2]), ident(J.en['Z'][2]))
+               ident(host_idx['K']), ident(host_idx['P']), ident(host_idx['Z']))
         cache = plan.__dict__.setdefault('_umaps', {})
         if key in cache:
             return cache[key]
@@ -133,9 +144,9 @@ class GaussNewtonSolver:
 
         def compact(key, par):
             m = np.arange(par.true_n)
-            if J.en[key][2] is not None:
+            if host_idx[key] is not None:
                 keep = np.full(par.true_n, -1, dtype=np.int64)
-                idx = J.en[key][2].cpu().numpy()
+                idx = host_idx[key]
                 keep[idx] = np.arange(len(idx))
                 m = keep
             return m

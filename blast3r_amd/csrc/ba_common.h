@@ -78,7 +78,8 @@ __device__ __forceinline__ void eval_residual(const CamF& cp, const float X[3], 
         Xc[r] = s + cp.tcr[r];
     }
     float z = Xc[2];
-    o.valid = z > 1e-3f;
+    // .cu:212 compares the fp32 depth with the double literal 1e-3: z = 1e-3f (just above 1e-3) is kept
+    o.valid = (double)z > 1e-3;
 #pragma unroll
     for (int i = 0; i < 3; ++i) { o.r[i] = 0.f; o.err[i] = 0.f; o.w[i] = 0.f; }
     if (!o.valid) return;

@@ -117,6 +117,53 @@ def used_depth_channels(n_zcfs, n_channels, depth_mode):
     return min(used, n_channels)
 
 
+def line_search(trial, init_loss, min_loss_delta, min_reproj):
+    """The step-halving loop of lm_step (en:308-333), on 0-d loss tensors.
+
+    trial(scale) evaluates the update at `scale` times the step and returns (loss, reproj_score,
+    payload); the scales tried are 1, then the running product of a / last_a over the schedule
+    (en:330 scales every slice of delta in place).  A trial is accepted when loss + min_loss_delta <
+    init_loss and reproj_score >= min_reproj.  A NaN loss takes the reference's aliasing
+    (en:317-319: `new_loss = init_loss; new_loss += min_loss_delta` adds min_loss_delta to init_loss
+    itself): init_loss grows by min_loss_delta for the rest of the step and is returned so.  All
+    comparisons use the fp32 sums formed on the loss's device, read with one copy per trial.
+    Returns a dict: scale, scales (every scale tried), init_loss, new_loss (with min_loss_delta),
+    trial_loss (the last trial's objective as evaluated), payload, accepted."""
+    scale = 1.0
+    last_a = 1
+    scales = []
+    accepted = False
+    for a in STEP_SCHEDULE:
+        scales.append(scale)
+        trial_loss, reproj_t, payload = trial(scale)
+        # one read for every decision: the sums + min_loss_delta are formed on the device, as the
+        # reference forms them, so the comparison sees the same fp32 values
+        plus = trial_loss + min_loss_delta
+        init_plus = init_loss + min_loss_delta
+        vals = torch.stack([t.reshape(()).to(torch.float32) for t in (trial_loss, init_loss, reproj_t, plus,
+                                                                       init_plus)]).cpu()
+        if torch.isnan(vals[0]):
+            print('Warning: loss is NaN')
+            init_loss = new_loss = init_plus     # en:317-319: new_loss aliases init_loss, += adds to both
+            lhs, rhs = float(vals[4]), float(vals[4])
+        else:
+            new_loss = plus
+            lhs, rhs = float(vals[3]), float(vals[1])
+        new_reproj = float(vals[2])
+        degenerate = new_reproj < min_reproj
+        if degenerate:
+            print(f'Rejecting step: reprojection residual collapsed to {new_reproj:.2e}')
+        if lhs < rhs and not degenerate:
+            accepted = True
+            break
+        scale = scale * (a / last_a)       # delta *= a/last_a (en:330): every slice scaled together
+        last_a = a
+    else:
+        print('Warning: loss is not decreasing')
+    return dict(scale=scales[-1], scales=scales, init_loss=init_loss, new_loss=new_loss, trial_loss=trial_loss,
+                payload=payload, accepted=accepted)
+
+
 def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep,
             K, P_rig2cam, P_w2rig, z_coefs, pts3d,
             depth_mode='log',
@@ -146,11 +193,13 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
              depth_mode='log', pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12,
              min_loss_delta=1e-4, weight_z=1, log_depth_maps=None, conf=None, pts3d_ref=None, weight_tan=0.0,
              tan_stride=4, normalize_tangents=True, optim_K=True, optim_Z=True, optim_P=True, optim_X=True,
-             optim_Z0=True, init_eval=None, **ba_options):
+             optim_Z0=True, init_eval=None, info=None, **ba_options):
     """lm_step, plus the objective of the last evaluated trial (loss before min_loss_delta, residuals,
     w_pts) as a third result.  init_eval, when given, is that triple for (K, P_w2rig, z_coefs, pts3d)
     under the same hyper-parameters: the evaluation at the start of the step (en:281) is then taken
-    from it instead of being recomputed (same inputs, same kernels, so the same values)."""
+    from it instead of being recomputed (same inputs, same kernels, so the same values).  info, when
+    a dict, receives the accepted step scale, the scales tried, the fp32 step delta, the PCG's
+    istate and the solver (for inspection; nothing else reads it)."""
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
     if weight_tan > 0:
@@ -216,15 +265,13 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
     delta = jac.solve_delta(J, init_residuals, w_pts, z_prior=z_prior)
     delta_K, delta_P, delta_zcf, delta_pts = jac.unpack_delta_inplace(delta)
 
-    update = dict()
     dKc = delta_K.contiguous()
     dPc = delta_P.contiguous()
     dZc = delta_zcf.contiguous()
     dXc = delta_pts.contiguous()
-    scale = 1.0
-    last_a = 1
     dev = pts3d.device
-    for a in STEP_SCHEDULE:
+
+    def trial(scale):
         Kn = torch.empty_like(K)
         Pn = torch.empty_like(P_w2rig)
         Zn = torch.empty_like(z_coefs)
@@ -232,30 +279,19 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
         check(lib().ba_apply_update(ptr(K), ptr(P_w2rig), ptr(z_coefs), ptr(pts3d), ptr(dKc), ptr(dPc), ptr(dZc),
                                     ptr(dXc), float(scale), 100.0, n_cams, n_nodes, n_imgs, n_zcf, n_tracks,
                                     ptr(Kn), ptr(Pn), ptr(Zn), ptr(Xn), stream_ptr(dev)))
-        update['K'], update['P_w2rig'], update['z_coefs'], update['pts3d'] = Kn, Pn, Zn, Xn
-        new_loss, new_residuals, new_w, new_reproj_t = objective(**update)
-        last_eval = (new_loss, new_residuals, new_w)
-        # one read for every decision: the sums + min_loss_delta are formed on the device, as the
-        # reference forms them, so the comparison sees the same fp32 values
-        vals = torch.stack([new_loss, init_loss, new_reproj_t, new_loss + min_loss_delta,
-                            init_loss + min_loss_delta]).cpu()
-        if torch.isnan(vals[0]):
-            print('Warning: loss is NaN')
-            new_loss = init_loss
-            new_loss_h = vals[4]
-        else:
-            new_loss_h = vals[3]
-        new_loss = new_loss + min_loss_delta
-        new_reproj = float(vals[2])
-        degenerate = new_reproj < min_reproj
-        if degenerate:
-            print(f'Rejecting step: reprojection residual collapsed to {new_reproj:.2e}')
-        if float(new_loss_h) < float(vals[1]) and not degenerate:
-            break
-        scale = scale * (a / last_a)       # delta *= a/last_a (en:330): every slice scaled together
-        last_a = a
-    else:
-        print('Warning: loss is not decreasing')
+        update = dict(K=Kn, P_w2rig=Pn, z_coefs=Zn, pts3d=Xn)
+        new_loss, new_residuals, new_w, new_reproj = objective(**update)
+        return new_loss, new_reproj, (update, new_residuals, new_w)
+
+    ls = line_search(trial, init_loss, min_loss_delta, min_reproj)
+    update, new_residuals, new_w = ls['payload']
+    if info is not None:
+        ist = jac.last.get('istate')
+        info.update(scale=ls['scale'], scales=ls['scales'], trials=len(ls['scales']), delta=delta,
+                    pcg_istate=None if ist is None else ist.clone(), solver=jac)
+    # the objective of the last trial, before min_loss_delta (what the next step starts from)
+    last_eval = (ls['trial_loss'], new_residuals, new_w)
+    init_loss, new_loss = ls['init_loss'], ls['new_loss']
     return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals), last_eval
 
 

@@ -79,9 +79,11 @@ class BAPlan:
     # ------------------------------------------------------------------ data
     def slot_data(self, pix2d, pix2d_std, pix2d_dep):
         """pix2d, pix2d_std, pix2d_dep permuted into slot order (cached per tensor version)."""
-        key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (pix2d, pix2d_std, pix2d_dep))
-        hit = self._slot_cache.get('key')
-        if hit == key:
+        # identity by weak reference (a new tensor may reuse a freed one's address with version 0)
+        ts = (pix2d, pix2d_std, pix2d_dep)
+        key = tuple((t._version, tuple(t.shape), t.data_ptr()) for t in ts)
+        refs = self._slot_cache.get('refs')
+        if refs is not None and self._slot_cache['key'] == key and all(r() is t for r, t in zip(refs, ts)):
             return self._slot_cache['val']
         if self.slot_index.numel():
             val = (pix2d.index_select(0, self.slot_index).contiguous(),
@@ -90,7 +92,7 @@ class BAPlan:
         else:
             val = (torch.zeros((1, 2), device=self.device), torch.ones((1, 2), device=self.device),
                    torch.zeros((1, max(1, pix2d_dep.shape[1])), device=self.device))
-        self._slot_cache = {'key': key, 'val': val}
+        self._slot_cache = {'key': key, 'refs': tuple(weakref.ref(t) for t in ts), 'val': val}
         return val
 
     def workspace(self, name, shape, dtype):
@@ -107,6 +109,17 @@ _cache_lock = threading.Lock()
 _cache = {}
 
 
+def _prune():
+    """Drop plans whose pids tensor is gone: they can no longer be looked up, and each holds its
+    workspaces (GB-scale at large sizes)."""
+    for k in list(_cache):
+        live = [ent for ent in _cache[k] if ent[0]() is not None]
+        if live:
+            _cache[k] = live
+        else:
+            del _cache[k]
+
+
 def get_plan(infos, pids, n_tracks, **kw):
     """Plan for this structure: reused while the same pids tensor (unmodified) and the same
     per-image counts / node / cam ids come back, rebuilt otherwise.  The ids are compared by
@@ -121,6 +134,7 @@ def get_plan(infos, pids, n_tracks, **kw):
                 return plan
     meta = infos.detach().cpu().numpy().tobytes()
     with _cache_lock:
+        _prune()
         for ent in _cache.get(id(pids), []):
             ref, version, k, m, iref, iversion, plan = ent
             if ref() is pids and version == pids._version and k == key and m == meta:

@@ -41,6 +41,38 @@ def reproj_score(res):
     return e[:n80].mean()
 
 
+def line_search(trial, init_loss, min_loss_delta=1e-4, min_reproj=0.01):
+    """The trial loop of en:305-333.  trial(scale) returns (loss, reproj_score, payload) for the update
+    at `scale` times the step (en:310-313 with delta scaled in place by a / last_a, en:330).
+
+    Written with the reference's in-place tensor operations: after a NaN loss `new_loss = init_loss`
+    makes both names one tensor and `new_loss += min_loss_delta` (en:317-319) adds min_loss_delta to
+    init_loss itself, which every later comparison and the returned status see.  The caller's tensor
+    is cloned first, so only this step's init_loss changes, as in the reference where it is a fresh
+    result of objective().  Returns dict(scale, scales, init_loss, new_loss, payload, accepted)."""
+    init_loss = init_loss.clone()
+    last_a = 1
+    scale = 1.0
+    scales = []
+    accepted = False
+    for a in STEP_SCHEDULE:
+        scales.append(scale)
+        new_loss, reproj, payload = trial(scale)
+        new_loss = new_loss.clone()
+        if new_loss.isnan():                                                    # en:316-318
+            new_loss = init_loss
+        new_loss += min_loss_delta                                              # en:319
+        new_reproj = float(reproj)                                              # en:324
+        degenerate = new_reproj < min_reproj
+        if new_loss < init_loss and not degenerate:                             # en:328
+            accepted = True
+            break
+        scale = scale * (a / last_a)     # delta *= a / last_a (en:330) applied to every slice
+        last_a = a
+    return dict(scale=scales[-1], scales=scales, init_loss=init_loss, new_loss=new_loss, payload=payload,
+                accepted=accepted)
+
+
 def objective(rigs, K, P_rig2cam, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std, pix2d_dep,
               is_depth_log, weight_z, pnorm, clip_pix_err, huber_delta):
     """en:263-278 without the tangent prior."""
@@ -112,25 +144,16 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_co
                                                dampen=dampen, adaptive_dampen=adaptive_dampen, dtype=dtype,
                                                solver=solver, pcg_tol=pcg_tol, pcg_maxiter=pcg_maxiter,
                                                z_prior=z_prior)
-    update = {}
-    last_a = 1.0
-    scale = 1.0
-    trials = 0
-    for a in STEP_SCHEDULE:
-        trials += 1
-        update['K'] = update_K(K, dK * scale)
-        update['P_w2rig'] = K_.exp_se3(-(dP * scale)) @ P_w2rig
-        update['z_coefs'] = z_coefs - dZ * scale
-        update['pts3d'] = pts3d - dX * scale
+    def trial(scale):
+        update = dict(K=update_K(K, dK * scale), P_w2rig=K_.exp_se3(-(dP * scale)) @ P_w2rig,
+                      z_coefs=z_coefs - dZ * scale, pts3d=pts3d - dX * scale)
         new_loss, new_residuals, _ = obj(**update)
-        if new_loss.isnan():
-            new_loss = init_loss
-        new_loss = new_loss + min_loss_delta
-        degenerate = float(reproj_score(new_residuals)) < min_reproj
-        if new_loss < init_loss and not degenerate:
-            break
-        scale = scale * (a / last_a)     # delta *= a / last_a (en:330) applied to every slice
-        last_a = a
+        return new_loss, reproj_score(new_residuals), (update, new_residuals)
+
+    ls = line_search(trial, init_loss, min_loss_delta, min_reproj)
+    update, new_residuals = ls['payload']
+    init_loss, new_loss = ls['init_loss'], ls['new_loss']
+    trials, scale = len(ls['scales']), ls['scale']
     info['trials'] = trials
     info['scale'] = scale
     return update, BA_Status(init_loss, init_residuals, new_loss, new_residuals), info

@@ -63,7 +63,7 @@ def residuals_with_rigs(infos, K, P_rig2c, P_w2rig, z_coefs, pts3d, pids, pix2d,
     X_rig = torch.einsum('nij,nj->ni', Pwr[:, :3, :3], X) + Pwr[:, :3, 3]          # .cu:203
     X_cam = torch.einsum('nij,nj->ni', Prc[:, :3, :3], X_rig) + Prc[:, :3, 3]      # .cu:208
     z = X_cam[:, 2]
-    valid = z > 1e-3                                                                  # .cu:212
+    valid = z.double() > 1e-3         # .cu:212: the fp32 depth against the double literal (1e-3f is kept)
     fx, cx, fy, cy = Kc[:, 0, 0], Kc[:, 0, 2], Kc[:, 1, 1], Kc[:, 1, 2]
     zs = torch.where(valid, z, torch.ones_like(z))
     p0 = (fx * X_cam[:, 0] + cx * X_cam[:, 2]) / zs                                  # .cu:217
@@ -119,7 +119,7 @@ def jacobians_with_rigs(infos, K, P_rig2c, P_w2rig, z_coefs, pts3d, pids, pix2d_
     p0 = fx * X_cam[:, 0] + cx * X_cam[:, 2]                                          # .cu:403
     p1 = fy * X_cam[:, 1] + cy * X_cam[:, 2]
     z = X_cam[:, 2]
-    valid = z > 1e-3                                                                  # .cu:408
+    valid = z.double() > 1e-3         # .cu:408: Tfloat depth against the double literal
     zs = torch.where(valid, z, torch.ones_like(z))
     inv_z = 1.0 / zs                                                                  # .cu:411
     inv_z2 = inv_z * inv_z

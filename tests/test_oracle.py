@@ -68,6 +68,27 @@ def test_residual_clip_weight_z_and_invalid_depth():
     assert torch.count_nonzero(behind) == 0
 
 
+def test_depth_threshold_is_a_double_comparison():
+    """.cu:212 and :408 test `z <= 1e-3` with a float (or double) z against the double literal
+    1e-3.  float32(1e-3) = 0.0010000000475 lies above it, so a point at exactly z = 1e-3f keeps its
+    residual and Jacobian rows; the next float below (0.00099999993) drops them.  An fp32
+    comparison (z > 1e-3f) would drop the first one too."""
+    z_keep = float(np.float32(1e-3))
+    z_drop = float(np.nextafter(np.float32(1e-3), np.float32(0)))
+    assert z_keep > 1e-3 > z_drop
+    for z, kept in ((z_keep, True), (z_drop, False)):
+        d = _one_obs([0.0, 0.0, z])
+        assert float(d['pts3d'][0, 2]) == z
+        out = _res(d)
+        assert bool(torch.count_nonzero(out) > 0) == kept, z
+        assert out[0].item() == (pytest.approx(-3.0, rel=1e-6) if kept else 0.0)     # (cx - u) / std
+        for f64 in (True, False):
+            Jc, Jz, Jp = ok.jacobians_with_rigs(d['infos'], d['K'], d['P_rig2c'], d['P_w2rig'], d['z_coefs'],
+                                                d['pts3d'], d['pids'], d['pix2d_std'], d['pix2d_dep'], True,
+                                                float64=f64)
+            assert bool(torch.count_nonzero(Jp) > 0) == kept, (z, f64)
+
+
 def test_residual_pnorm2_and_lin_mode():
     """pnorm = 2: a = p delta^(p-2) / 2 = 1 and b = 0, so err = r^2 on both sides of delta and w = 1;
     lin depth mode r2 = fbar ln(g / z)."""
@@ -265,6 +286,54 @@ def test_oracle_lm_step_decreases_loss_and_follows_schedule():
     up, st, info = oe.lm_step(**p.lm_inputs(), weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'])
     assert float(st.new_loss) < float(st.init_loss)
     assert info['scale'] in [1.0, 0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0.0]
+
+
+# Known answers for the acceptance rule of en:305-333, worked out by hand from the reference text:
+# trials are evaluated at scales 1, 1/2, 1/4, 1/8, 1/64, 1/512, 1/4096 (delta *= a / last_a over
+# [0.5, 0.25, 0.125, 1/64, 1/512, 1/4096, 0]); a trial is taken when loss + 1e-4 < init_loss (fp32)
+# and reproj >= 0.01; a NaN loss is replaced by init_loss and `+= 1e-4` then lands on init_loss
+# itself (en:317-319), so init_loss grows by 1e-4 for the rest of the step.
+_F = lambda x: float(torch.tensor(x, dtype=torch.float32))
+_ALL_SCALES = [1.0, 0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096]
+_LS_CASES = {
+    # name: ([(loss, reproj) per trial], accepted scale, trials, init_loss after, new_loss, accepted)
+    'first_trial': ([(0.9, 1.0)], 1.0, 1, 1.0, _F(_F(0.9) + _F(1e-4)), True),
+    'margin_rejects': ([(0.99995, 1.0), (0.9998, 1.0)], 0.5, 2, 1.0, _F(_F(0.9998) + _F(1e-4)), True),
+    'reproj_collapse': ([(0.5, 0.001), (0.6, 0.02)], 0.5, 2, 1.0, _F(_F(0.6) + _F(1e-4)), True),
+    # NaN, then 0.99995: 0.99995 + 1e-4 = 1.00005 < 1.0001 (the aliased init_loss) is taken;
+    # without the aliasing it would be rejected and the third trial (0.9) taken at scale 1/4
+    'nan_aliases_init': ([(float('nan'), 1.0), (0.99995, 1.0), (0.9, 1.0)], 0.5, 2, _F(_F(1.0) + _F(1e-4)),
+                         _F(_F(0.99995) + _F(1e-4)), True),
+    'two_nans': ([(float('nan'), 1.0), (float('nan'), 1.0), (1.00005, 1.0)], 0.25, 3,
+                 _F(_F(_F(1.0) + _F(1e-4)) + _F(1e-4)), _F(_F(1.00005) + _F(1e-4)), True),
+    'none_decreases': ([(1.5, 1.0)] * 7, 1 / 4096, 7, 1.0, _F(_F(1.5) + _F(1e-4)), False),
+}
+
+
+@pytest.mark.parametrize('name', sorted(_LS_CASES))
+@pytest.mark.parametrize('impl', ['oracle', 'device_engine_host_logic'])
+def test_line_search_acceptance_known_answers(name, impl):
+    """Both line searches (the oracle restatement and the device engine's host-side decision loop, fed
+    CPU tensors here) against the hand-worked outcomes above: the scales tried, the accepted scale,
+    the init_loss after NaN aliasing and the returned new_loss."""
+    from blast3r_amd import engine as de
+    seq, scale, n_trials, init_after, new_loss, accepted = _LS_CASES[name]
+    calls = []
+
+    def trial(s):
+        loss, reproj = seq[len(calls)]
+        calls.append(s)
+        return torch.tensor(loss, dtype=torch.float32), torch.tensor(reproj, dtype=torch.float32), len(calls)
+
+    init = torch.tensor(1.0, dtype=torch.float32)
+    fn = oe.line_search if impl == 'oracle' else de.line_search
+    out = fn(trial, init, 1e-4, 0.01)
+    assert calls == _ALL_SCALES[:n_trials]
+    assert out['scale'] == scale and out['scales'] == calls
+    assert out['accepted'] == accepted and out['payload'] == n_trials
+    assert float(out['init_loss']) == init_after
+    assert float(out['new_loss']) == new_loss
+    assert float(init) == 1.0                                   # the caller's tensor is left alone
 
 
 

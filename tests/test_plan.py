@@ -264,3 +264,23 @@ def test_schur_emulation_matches_oracle(cfg, nf, nt):
         leaf = ne.leaves[name]
         lam_leaf = float(leaf.diagonal(dim1=-1, dim2=-2).abs().max()) * 1e-12
         assert np.allclose(dg[sl], lam_leaf, rtol=1e-2, atol=0)   # rounding noise ~1e-16 * |S_ii|
+
+
+def test_host_mask_for_device_observations_raises():
+    """A mask tensor on another device than the observations raises RuntimeError before any launch
+    (the kernels would read it at its address on their own device; the reference's indexing at
+    ba_solver.py:98 raises for it too), except an all-False mask, which the reference turns into the
+    zero matrix first (ba_solver.py:91-92).  A host tensor handed to a kernel argument raises."""
+    from blast3r_amd import _lib
+    from blast3r_amd.ba_solver import _flag
+    dev = torch.device('cuda:0')
+    with pytest.raises(RuntimeError, match='optim_P'):
+        _flag(torch.tensor([True, False, True]), 'optim_P', 3, dev)
+    assert _flag(torch.tensor([False, False, False]), 'optim_P', 3, dev) == (False, None, None)
+    en, mask, idx = _flag(torch.tensor([True, False, True]), 'optim_P', 3, torch.device('cpu'))
+    assert en and mask.dtype == torch.uint8 and idx.tolist() == [0, 2]
+    with pytest.raises(ValueError):
+        _flag(torch.tensor([1, 0, 1]), 'optim_P', 3, dev)
+    with pytest.raises(RuntimeError, match='device tensor'):
+        _lib.ptr(torch.zeros(4))
+    assert _lib.ptr(None) is None

@@ -225,7 +225,9 @@ def test_device_planar_confidence_matches_oracle():
 @pytest.mark.gpu
 def test_lm_step_with_tangent_prior_parity():
     """lm_step with weight_tan > 0 (prior loss in every objective, GN terms added to the z blocks)
-    against the oracle lm_step with the same prior; tolerances as in test_lm_step_parity, the
+    against the oracle with the same prior, checked as test_lm_step_parity checks a step: the step
+    delta against the oracle's PCG iterate after the same number of updates (1e-4), the oracle's
+    line search on the device's delta (same scales, loss and parameters within 1e-5); the
     start-of-step loss (Huber mean + prior) to 1e-4."""
     from blast3r_amd.synthetic import make_problem
     from blast3r_amd import engine as gpu_engine
@@ -249,16 +251,21 @@ def test_lm_step_with_tangent_prior_parity():
         refs.append((ray * plane[..., None]).float())
     kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, weight_tan=0.5, tan_stride=4)
     conf = [torch.ones(1)] * n_imgs
-    up_r, st_r, _ = oeng.lm_step(**p.lm_inputs(), log_depth_maps=maps, conf=conf, pts3d_ref=refs, **kw)
-    up_c, st_c, _ = oeng.lm_step(**p.lm_inputs(), log_depth_maps=maps, conf=conf, pts3d_ref=refs, pcg_tol=1e-10,
-                                 pcg_maxiter=5000, **kw)
+    import oracle.tangent as T_
+    from tests.step_checks import check_line_search, check_step_delta, device_system, oracle_system
+    tan_kw = dict(weight_tan=0.5, tan_stride=4, optim_Z0=True, normalize_tangents=True)
+    prior = lambda zc, gn, dt: T_.tangent_prior_terms(p.infos[2], p.K, zc, maps, refs, dtype=dt, compute_gn=gn,
+                                                      **tan_kw)
+    extra = lambda zc: prior(zc, False, torch.float32)[0]
+    _, g_z, H_z = prior(p.z_coefs, True, torch.float64)
     gp = p.to(DEV)
-    up_g, st_g = gpu_engine.lm_step(**gp.lm_inputs(), log_depth_maps=[m.to(DEV) for m in maps], conf=conf,
-                                    pts3d_ref=[r.to(DEV) for r in refs], dtype=torch.float64, **kw)
-    assert abs(float(st_g.init_loss) - float(st_r.init_loss)) <= 1e-4 * abs(float(st_r.init_loss))
-    for k in ('K', 'z_coefs', 'pts3d', 'P_w2rig'):
-        ref = up_r[k] - p.lm_inputs()[k]
-        conv = up_c[k] - p.lm_inputs()[k]
-        spread = rel_err(ref, conv) if ref.norm() > 0 else 0.0
-        got = up_g[k].cpu() - p.lm_inputs()[k]
-        assert rel_err(got, ref) <= max(1e-4, 4 * spread), (k, rel_err(got, ref), spread)
+    info = {}
+    up_g, st_g, _ = gpu_engine._lm_step(**gp.lm_inputs(), log_depth_maps=[m.to(DEV) for m in maps], conf=conf,
+                                        pts3d_ref=[r.to(DEV) for r in refs], dtype=torch.float64, info=info, **kw)
+    inp = p.lm_inputs()
+    hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
+    sysd = oracle_system(inp, hp, {}, z_prior=(H_z, g_z), extra_loss=extra)
+    assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-4 * abs(float(sysd['loss']))
+    check_step_delta(sysd, info['delta'], info['pcg_istate'].cpu(), seed=9,
+                     reduced=device_system(info['solver']))
+    check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g, extra_loss=extra)
