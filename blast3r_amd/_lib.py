@@ -134,6 +134,7 @@ _SIGS = {
                                 c_p, c_p, c_p, c_p, c_p]),
     'ba_objective_workspace_bytes': (c_i64, [c_i64]),
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
+    'ba_objective_noalloc': (c_int, [c_p, c_i64, c_int, c_p, c_p]),
     'ba_nonfinite_flags': (c_int, [c_p, c_p, c_int, c_p, c_p]),
     'ba_stream_triad': (c_int, [c_p, c_p, c_p, ctypes.c_double, c_i64, c_p]),
     'ba_sample_depth': (c_int, [ctypes.POINTER(BaSampleArgs), c_p]),

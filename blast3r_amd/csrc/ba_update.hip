@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <cmath>
+#include <mutex>
 
 #include "ba_common.h"
 #include "ba_error.h"
@@ -104,14 +105,20 @@ __global__ void k_obj_init(uint32_t* __restrict__ hist, uint32_t* __restrict__ s
     if (threadIdx.x == 0) { sel[0] = 0; sel[1] = 0; sel[2] = k; sel[3] = 0; }
 }
 
+// the selection key of observation i: the bit pattern of ||(r0, r1)|| (non-negative, so the pattern
+// orders as the value).  Every kernel forms it through this one function, so a key stored by
+// k_obj_prep and a key recomputed from res (ebits == nullptr) are the same bits.
+__device__ __forceinline__ uint32_t obj_key(const float* __restrict__ res, int64_t n, int64_t i) {
+    const float r0 = res[i], r1 = res[n + i];
+    return __float_as_uint(sqrtf(r0 * r0 + r1 * r1));
+}
+
 __global__ void __launch_bounds__(OBJ_T) k_obj_prep(const float* __restrict__ res, int64_t n, int has_err,
                                                    uint32_t* __restrict__ ebits, double* __restrict__ part) {
     __shared__ double sh[OBJ_T];
     double s = 0.0;
     for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
-        float r0 = res[i], r1 = res[n + i];
-        float e = sqrtf(r0 * r0 + r1 * r1);
-        ebits[i] = __float_as_uint(e);
+        if (ebits) ebits[i] = obj_key(res, n, i);
         if (has_err) s += (double)res[3 * n + i] + (double)res[4 * n + i] + (double)res[5 * n + i];
     }
     sh[threadIdx.x] = s;
@@ -127,8 +134,8 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_prep(const float* __restrict__ re
 // in few bins (the top byte is the exponent), so each block keeps 8 sub-histograms (lane & 7; rows
 // 257 words apart, so a bin's copies lie in different LDS banks) to spread the atomic increments.
 #define OBJ_SUBH 8
-__global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__ ebits, int64_t n,
-                                                   const uint32_t* __restrict__ sel, int shift,
+__global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__ ebits, const float* __restrict__ res,
+                                                   int64_t n, const uint32_t* __restrict__ sel, int shift,
                                                    uint32_t* __restrict__ hist) {
     __shared__ uint32_t h[OBJ_SUBH][257];
 #pragma unroll
@@ -137,7 +144,7 @@ __global__ void __launch_bounds__(OBJ_T) k_obj_hist(const uint32_t* __restrict__
     uint32_t prefix = sel[0], pmask = sel[1];
     uint32_t* mine = h[threadIdx.x & (OBJ_SUBH - 1)];
     for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
-        uint32_t b = ebits[i];
+        uint32_t b = ebits ? ebits[i] : obj_key(res, n, i);
         if ((b & pmask) == prefix) atomicAdd(&mine[(b >> shift) & 0xffu], 1u);
     }
     __syncthreads();
@@ -190,16 +197,16 @@ __global__ void __launch_bounds__(64) k_obj_pick(uint32_t* __restrict__ hist, ui
     for (int q = 0; q < 4; ++q) hist[4 * l + q] = 0;
 }
 
-__global__ void __launch_bounds__(OBJ_T) k_obj_below(const uint32_t* __restrict__ ebits, int64_t n,
-                                                    const uint32_t* __restrict__ sel, double* __restrict__ psum,
-                                                    uint32_t* __restrict__ pcnt) {
+__global__ void __launch_bounds__(OBJ_T) k_obj_below(const uint32_t* __restrict__ ebits, const float* __restrict__ res,
+                                                    int64_t n, const uint32_t* __restrict__ sel,
+                                                    double* __restrict__ psum, uint32_t* __restrict__ pcnt) {
     __shared__ double sh[OBJ_T];
     __shared__ uint32_t sc[OBJ_T];
     uint32_t T = sel[0];
     double s = 0.0;
     uint32_t c = 0;
     for (int64_t i = (int64_t)blockIdx.x * OBJ_T + threadIdx.x; i < n; i += (int64_t)gridDim.x * OBJ_T) {
-        uint32_t b = ebits[i];
+        uint32_t b = ebits ? ebits[i] : obj_key(res, n, i);
         if (b < T) { s += (double)__uint_as_float(b); c += 1; }
     }
     sh[threadIdx.x] = s; sc[threadIdx.x] = c;
@@ -355,12 +362,77 @@ extern "C" int64_t ba_objective_workspace_bytes(int64_t n_obs) {
     return 4 * n_obs + 8 * nb * 2 + 4 * nb + 4 * 256 + 4 * 4 + 64;
 }
 
+namespace ba {
+
+// The launch sequence of ba_objective.  ebits (4 bytes per observation) keeps each observation's
+// key between the passes; when it is null the passes recompute the key from res instead.  lpart,
+// psum (fp64) and pcnt hold one partial per block of the grid-stride passes (at most OBJ_NBMAX),
+// hist 256 counters, sel 4 words; k_obj_init clears hist and sel, every partial is written before
+// it is read.
+static int objective_launch(const float* res, int64_t n_obs, int32_t has_err, uint32_t* ebits, double* lpart,
+                            double* psum, uint32_t* pcnt, uint32_t* hist, uint32_t* sel, float* out, hipStream_t st) {
+    int64_t nb = (n_obs + OBJ_T - 1) / OBJ_T;
+    if (nb < 1) nb = 1;
+    int64_t n80 = n_obs * 80 / 100;
+    BA_REQUIRE(n80 <= (int64_t)UINT32_MAX, "ba_objective: the 80% rank of n_obs must fit 32 bits "
+                                          "(n_obs <= 5368709119)");
+    // the per-block partials of prep and below: at most OBJ_NBMAX blocks (grid-stride loops), so the
+    // one-block final sum stays short
+    const int64_t nbp = nb < OBJ_NBMAX ? nb : OBJ_NBMAX;
+    hipLaunchKernelGGL(k_obj_init, dim3(1), dim3(256), 0, st, hist, sel, (uint32_t)(n80 > 0 ? n80 : 1));
+    if (n_obs > 0) {
+        hipLaunchKernelGGL(k_obj_prep, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, res, n_obs, has_err, ebits, lpart);
+        unsigned hb = (unsigned)(nb < 1024 ? nb : 1024);
+        for (int pass = 0; pass < 4; ++pass) {
+            int shift = 24 - 8 * pass;
+            hipLaunchKernelGGL(k_obj_hist, dim3(hb), dim3(OBJ_T), 0, st, ebits, res, n_obs, sel, shift, hist);
+            hipLaunchKernelGGL(k_obj_pick, dim3(1), dim3(64), 0, st, hist, sel, shift);
+        }
+        hipLaunchKernelGGL(k_obj_below, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, ebits, res, n_obs, sel, psum, pcnt);
+    } else {
+        hipLaunchKernelGGL(k_obj_prep, dim3(1), dim3(OBJ_T), 0, st, res, (int64_t)0, has_err, ebits, lpart);
+        hipLaunchKernelGGL(k_obj_below, dim3(1), dim3(OBJ_T), 0, st, ebits, res, (int64_t)0, sel, psum, pcnt);
+    }
+    hipLaunchKernelGGL(k_obj_final, dim3(1), dim3(OBJ_T), 0, st, lpart, psum, pcnt, n_obs > 0 ? (int)nbp : 1, n_obs,
+                       n80, sel, has_err, out);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+// Scratch of ba_objective_noalloc: the fixed-size part of the objective's workspace (the per-block
+// partials, histogram and selection state; no per-observation keys), one copy per GPU for the life
+// of the process.  Host code never uses the symbol itself: each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+#define OBJ_SCRATCH_BYTES (OBJ_NBMAX * (8 + 8 + 4) + 256 * 4 + 4 * 4)
+static __device__ __align__(256) unsigned char scratch[(OBJ_SCRATCH_BYTES + 255) / 256 * 256];
+
+#define OBJ_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[OBJ_MAX_DEVICES];
+
+static int scratch_of_current_device(unsigned char** out) {
+    int dev = -1;
+    BA_HIP(hipGetDevice(&dev));
+    BA_REQUIRE(dev >= 0 && dev < OBJ_MAX_DEVICES, "ba_objective_noalloc: device index beyond 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        BA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        BA_REQUIRE(p != nullptr, "ba_objective_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = (unsigned char*)g_scratch_ptr[dev];
+    return BA_OK;
+}
+
+}  // namespace ba
+
 // loss = mean(err) and reproj_score from the (9 or 3, n_obs) residual buffer; out[0] = loss,
 // out[1] = reproj_score (fp32, device).  Workspace of ba_objective_workspace_bytes(n_obs).
 extern "C" int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out,
                             void* stream) {
     clear_error();
-    hipStream_t st = (hipStream_t)stream;
+    BA_REQUIRE(n_obs >= 0, "ba_objective: n_obs < 0");
     int64_t nb = (n_obs + OBJ_T - 1) / OBJ_T;
     if (nb < 1) nb = 1;
     char* w = (char*)workspace;
@@ -371,26 +443,22 @@ extern "C" int ba_objective(const float* res, int64_t n_obs, int32_t has_err, vo
     uint32_t* pcnt = (uint32_t*)w; w += 4 * nb;
     uint32_t* hist = (uint32_t*)w; w += 4 * 256;
     uint32_t* sel = (uint32_t*)w;
-    int64_t n80 = n_obs * 80 / 100;
-    // the per-block partials of prep and below: at most OBJ_NBMAX blocks (grid-stride loops), so the
-    // one-block final sum stays short
-    const int64_t nbp = nb < OBJ_NBMAX ? nb : OBJ_NBMAX;
-    hipLaunchKernelGGL(k_obj_init, dim3(1), dim3(256), 0, st, hist, sel, (uint32_t)(n80 > 0 ? n80 : 1));
-    if (n_obs > 0) {
-        hipLaunchKernelGGL(k_obj_prep, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, res, n_obs, has_err, ebits, lpart);
-        unsigned hb = (unsigned)(nb < 1024 ? nb : 1024);
-        for (int pass = 0; pass < 4; ++pass) {
-            int shift = 24 - 8 * pass;
-            hipLaunchKernelGGL(k_obj_hist, dim3(hb), dim3(OBJ_T), 0, st, ebits, n_obs, sel, shift, hist);
-            hipLaunchKernelGGL(k_obj_pick, dim3(1), dim3(64), 0, st, hist, sel, shift);
-        }
-        hipLaunchKernelGGL(k_obj_below, dim3((unsigned)nbp), dim3(OBJ_T), 0, st, ebits, n_obs, sel, psum, pcnt);
-    } else {
-        hipLaunchKernelGGL(k_obj_prep, dim3(1), dim3(OBJ_T), 0, st, res, (int64_t)0, has_err, ebits, lpart);
-        hipLaunchKernelGGL(k_obj_below, dim3(1), dim3(OBJ_T), 0, st, ebits, (int64_t)0, sel, psum, pcnt);
-    }
-    hipLaunchKernelGGL(k_obj_final, dim3(1), dim3(OBJ_T), 0, st, lpart, psum, pcnt, n_obs > 0 ? (int)nbp : 1, n_obs,
-                       n80, sel, has_err, out);
-    BA_LAUNCHED();
-    return BA_OK;
+    return objective_launch(res, n_obs, has_err, ebits, lpart, psum, pcnt, hist, sel, out, (hipStream_t)stream);
+}
+
+// ba_objective with no workspace argument and no allocation: the passes recompute each key from res
+// and keep their partials in the library's per-GPU scratch array.  Calls that overlap on one GPU
+// share that array and race; the results equal ba_objective's bit for bit.
+extern "C" int ba_objective_noalloc(const float* res, int64_t n_obs, int32_t has_err, float* out, void* stream) {
+    clear_error();
+    BA_REQUIRE(n_obs >= 0, "ba_objective_noalloc: n_obs < 0");
+    unsigned char* sp = nullptr;
+    int rc = scratch_of_current_device(&sp);
+    if (rc != BA_OK) return rc;
+    double* lpart = (double*)sp;
+    double* psum = lpart + OBJ_NBMAX;
+    uint32_t* pcnt = (uint32_t*)(psum + OBJ_NBMAX);
+    uint32_t* hist = pcnt + OBJ_NBMAX;
+    uint32_t* sel = hist + 256;
+    return objective_launch(res, n_obs, has_err, nullptr, lpart, psum, pcnt, hist, sel, out, (hipStream_t)stream);
 }

@@ -219,6 +219,16 @@ int64_t ba_objective_workspace_bytes(int64_t n_obs);
  *   80% of ||(r0,r1)|| (exact selection on the fp32 values, no sort).  out is device memory. */
 int ba_objective(const float* res, int64_t n_obs, int32_t has_err, void* workspace, float* out, void* stream);
 
+/* ba_objective without a workspace argument and without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The passes recompute each observation's
+ * key from res instead of storing it, and keep their partial sums (at most 2048 blocks) in a static
+ * per-GPU scratch array of 42 KB, so every n_obs fits (up to the 32-bit rank limit that
+ * ba_objective shares: n_obs <= 5368709119, rejected with an error beyond).  Outputs equal
+ * ba_objective's bit for bit.  All calls on one GPU share its scratch array: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialised by the caller. */
+int ba_objective_noalloc(const float* res, int64_t n_obs, int32_t has_err, float* out, void* stream);
+
 /* lm_step's input checks, `assert tensor.isfinite().all()` on every input (engine.py:340-344), for up
  * to BA_NONFINITE_MAX_SPANS fp32 arrays in one launch: flags[t] (device, int32) = 1 when
  * ptrs[t][0 .. counts[t]) holds a NaN or an infinity, else 0.  int32 inputs are finite by type. */
