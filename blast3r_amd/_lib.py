@@ -73,6 +73,13 @@ class BaPcgArgs(ctypes.Structure):
                 ('long_ptr', c_p), ('long_idx', c_p), ('img_part', c_p), ('src1', c_p), ('long_rng', c_p),
                 ('row_cap', c_int)]
 
+class BaCholArgs(ctypes.Structure):
+    _fields_ = [('mode', c_int), ('A', c_p), ('lda', c_i64), ('Linv', c_p), ('pair_idx', c_p), ('kind', c_p),
+                ('shared_u', c_p), ('n_shared', c_int), ('w', c_int), ('db', c_int), ('bcol', c_p), ('bpos', c_p),
+                ('n_pairs', c_i64), ('info', c_p),
+                ('work', c_p)]
+
+
 PCG_LONG_LIST = 32          # BA_PCG_LONG_LIST in include/ba_hip.h
 PCG_BLOCK = 256             # unknowns per block of the PCG update launch (long_ptr granularity)
 
@@ -135,6 +142,10 @@ _SIGS = {
     'ba_objective_workspace_bytes': (c_i64, [c_i64]),
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
     'ba_objective_noalloc': (c_int, [c_p, c_i64, c_int, c_p, c_p]),
+    'ba_chol_dense_lda': (c_i64, [c_i64]),
+    'ba_chol_band_lds_bytes': (c_i64, [c_int, c_int, c_int]),
+    'ba_chol_work_doubles': (c_i64, [c_int, c_i64, c_int, c_int, c_int, c_int]),
+    'ba_reduced_solve': (c_int, [ctypes.POINTER(BaPcgArgs), ctypes.POINTER(BaCholArgs), c_p]),
     'ba_nonfinite_flags': (c_int, [c_p, c_p, c_int, c_p, c_p]),
     'ba_stream_triad': (c_int, [c_p, c_p, c_p, ctypes.c_double, c_i64, c_p]),
     'ba_sample_depth': (c_int, [ctypes.POINTER(BaSampleArgs), c_p]),

@@ -75,7 +75,7 @@ class GaussNewtonSolver:
 
     def __init__(self, n_cams, n_nodes, n_imgs, n_tracks, device, no_grad_f_from_rz=False, dampen=1e-12,
                  adaptive_dampen=True, dtype=torch.float32, solver='pcg', pcg_tol=1e-6, pcg_maxiter=300,
-                 plan_options=None, use_graph=True):
+                 plan_options=None, use_graph=True, cholesky_layout='auto'):
         self.cams = Param(n_cams)
         self.nodes = Param(n_nodes)
         self.imgs = Param(n_imgs)
@@ -87,9 +87,15 @@ class GaussNewtonSolver:
         self.dampen = dampen
         self.adaptive_dampen = adaptive_dampen
         self.no_grad_f_from_rz = no_grad_f_from_rz
-        if solver != 'pcg':
-            raise ValueError(f'unknown reduced solver {solver!r} (supported: "pcg")')
+        if solver not in ('pcg', 'cholesky'):
+            raise ValueError(f'unknown reduced solver {solver!r} (supported: "pcg", "cholesky")')
         self.solver = solver
+        # solver='cholesky': 'banded' when every image pair lies within w images, the window of w + 1 images
+        # fits one workgroup's LDS ((w + 1) d <= 160, ~132 at d = 11) and at most 8 unknowns are shared by
+        # several images, else 'dense' ('auto' picks)
+        if cholesky_layout not in ('auto', 'dense', 'banded'):
+            raise ValueError(f'unknown cholesky_layout {cholesky_layout!r}')
+        self.cholesky_layout = cholesky_layout
         self.pcg_tol = pcg_tol
         self.pcg_maxiter = pcg_maxiter
         self.plan_options = dict(plan_options or {})
@@ -198,7 +204,10 @@ class GaussNewtonSolver:
         one = np.nonzero(counts == 1)[0]
         src1[one] = src[inv_ptr[one]]
         long_rng = np.stack([inv_ptr[long_u], inv_ptr[long_u + 1]], 1).reshape(-1) if len(long_u) else np.zeros(2)
+        kind = np.where(counts == 0, 0, np.where(counts == 1, 1, 2)) if n_u else np.zeros(1)
+        shared_u = np.nonzero(counts >= 2)[0] if n_u else np.zeros(0)
         out = dict(n_u=n_u, umap=t(umap), inv_ptr=t(inv_ptr), inv_src=t(src if len(src) else np.zeros(1)),
+                   kind=t(kind), shared_u=t(shared_u if len(shared_u) else np.zeros(1)), n_shared=len(shared_u),
                    leaf=t(leaf if n_u else np.zeros(1)), long_u=t(long_u if len(long_u) else np.zeros(1)),
                    n_long=len(long_u), long_ptr=t(long_ptr), long_idx=t(long_idx), src1=t(src1),
                    long_rng=t(long_rng))
@@ -341,20 +350,13 @@ class GaussNewtonSolver:
             pa.r, pa.z, pa.p, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(y_img)
             pa.img_part = ptr(ws('pcg_img_part', (n_imgs,), torch.float64))
             pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
-            rp = plan.host['row_ptr']
-            n_ent = int(rp[-1]) if len(rp) else 0
-            # rows at a fixed capacity (the SpMV then needs no row_ptr load) when that pads by <= 25%
-            longest = int(np.diff(rp).max()) if len(rp) > 1 else 0
-            cap = -(-longest // 8) * 8
-            row_cap = cap if 0 < cap and n_imgs * cap <= 1.25 * n_ent else 0
-            n_blk = n_imgs * row_cap if row_cap else n_ent
-            S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float64)
-            pa.S_rows, pa.n_row_ent, pa.row_cap = ptr(S_rows), n_ent, row_cap
-            pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * 16,), torch.int32))
             pa.long_u, pa.n_long = ptr(um['long_u']), um['n_long']
             pa.long_ptr, pa.long_idx = ptr(um['long_ptr']), ptr(um['long_idx'])
             pa.src1, pa.long_rng = ptr(um['src1']), ptr(um['long_rng'])
-            self._run_pcg(pa, plan, st)
+            self.last['direct'] = None
+            if not (self.solver == 'cholesky' and self._run_direct(pa, plan, st, n_imgs, um)):
+                self._pcg_rows(pa, plan, d, n_imgs)
+                self._run_pcg(pa, plan, st)
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
         # back-substitution for the points
         dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
@@ -375,6 +377,73 @@ class GaussNewtonSolver:
         if en['X'][2] is not None:
             dXa = dXa[en['X'][2]]
         return torch.cat([dc, dXa.reshape(-1)])
+
+    @staticmethod
+    def _pcg_rows(pa, plan, d, n_imgs):
+        """The PCG's image-row copies of the pair blocks (workspace fields of ba_pcg_args)."""
+        ws = plan.workspace
+        rp = plan.host['row_ptr']
+        n_ent = int(rp[-1]) if len(rp) else 0
+        # rows at a fixed capacity (the SpMV then needs no row_ptr load) when that pads by <= 25%
+        longest = int(np.diff(rp).max()) if len(rp) > 1 else 0
+        cap = -(-longest // 8) * 8
+        row_cap = cap if 0 < cap and n_imgs * cap <= 1.25 * n_ent else 0
+        n_blk = n_imgs * row_cap if row_cap else n_ent
+        S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float64)
+        pa.S_rows, pa.n_row_ent, pa.row_cap = ptr(S_rows), n_ent, row_cap
+        pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * 16,), torch.int32))
+
+    def _run_direct(self, pa, plan, st, n_imgs, um):
+        """ba_reduced_solve (L L^T of the damped reduced system, banded or dense).  Returns False, after
+        recording it in last['direct'], when a pivot was not positive: the caller then runs the device
+        PCG."""
+        L = lib()
+        ws = plan.workspace
+        d = pa.d
+        n_p = plan.scalars['n_pairs']
+        pidx = plan.workspace_cache.get('pair_idx')
+        if pidx is None:                       # pair id of every image pair (i <= j), once per structure
+            i1 = plan.dev['pair_i1'][:n_p].long()
+            i2 = plan.dev['pair_i2'][:n_p].long()
+            pidx = torch.full((n_imgs * n_imgs,), -1, dtype=torch.int32, device=self.device)
+            pidx[i1 * n_imgs + i2] = torch.arange(n_p, dtype=torch.int32, device=self.device)
+            plan.workspace_cache['pair_idx'] = pidx
+            h1, h2 = plan.host['pair_i1'][:n_p], plan.host['pair_i2'][:n_p]
+            plan.workspace_cache['band_w'] = int((h2 - h1).max()) if n_p else 0
+        w = max(1, min(plan.workspace_cache['band_w'], max(n_imgs - 1, 0)))
+        ns = um['n_shared']
+        if 'bcol' not in um:                   # band columns: image-level columns local in some image
+            kind = um['kind'].cpu().numpy()
+            umh = um['umap'].cpu().numpy()
+            loc = (umh >= 0) & (kind[np.clip(umh, 0, None)] == 1)
+            bcol = np.nonzero(loc.any(0))[0]
+            bpos = np.full(d, -1, dtype=np.int64)
+            bpos[bcol] = np.arange(len(bcol))
+            um['bcol'] = torch.as_tensor(bcol if len(bcol) else np.zeros(1), dtype=torch.int32, device=self.device)
+            um['bpos'] = torch.as_tensor(bpos, dtype=torch.int32, device=self.device)
+            um['db'] = len(bcol)
+        db = um['db']
+        layout = self.cholesky_layout
+        if layout == 'auto':
+            fits = db >= 1 and n_imgs >= 2 and (w + 1) * db <= 160 and ns <= 8 and \
+                int(L.ba_chol_band_lds_bytes(db, w, ns)) <= 160 * 1024
+            layout = 'banded' if fits else 'dense'
+        mode = 1 if layout == 'banded' else 0
+        lda = int(L.ba_chol_dense_lda(pa.n_u))
+        nwork = int(L.ba_chol_work_doubles(mode, pa.n_u, n_imgs, db if mode else d, w, ns))
+        info = ws('chol_info', (1,), torch.int32)
+        ca = _lib.BaCholArgs(mode=mode, lda=lda, pair_idx=ptr(pidx), kind=ptr(um['kind']),
+                             shared_u=ptr(um['shared_u']), n_shared=ns, w=w, db=db, bcol=ptr(um['bcol']),
+                             bpos=ptr(um['bpos']), n_pairs=n_p, info=ptr(info),
+                             work=ptr(ws('chol_work', (nwork,), torch.float64)))
+        if mode == 0:
+            ca.A = ptr(ws('chol_A', (lda, lda), torch.float64))
+            ca.Linv = ptr(ws('chol_Linv', (lda // 64, 64, 64), torch.float64))
+        check(L.ba_reduced_solve(pa, ca, st))
+        bad = int(info.cpu())                  # one read per solve
+        self.last['direct'] = dict(layout=layout, w=w, db=db, n_shared=ns,
+                                   first_bad_pivot=None if bad == 2 ** 31 - 1 else bad)
+        return bad == 2 ** 31 - 1
 
     def _run_pcg(self, pa, plan, st):
         """ba_pcg_solve, replayed from a HIP graph (captured once per argument set and kept with the

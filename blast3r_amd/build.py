@@ -10,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libba_hip.so')
-SOURCES = ['ba_compat.hip', 'ba_schur.hip', 'ba_pcg.hip', 'ba_update.hip', 'ba_sample.hip', 'ba_tracks.hip', 'ba_tangent.hip',
+SOURCES = ['ba_compat.hip', 'ba_schur.hip', 'ba_pcg.hip', 'ba_chol.hip', 'ba_update.hip', 'ba_sample.hip', 'ba_tracks.hip', 'ba_tangent.hip',
            'ba_plan.cpp']
 ARCH = os.environ.get('BA_OFFLOAD_ARCH', 'gfx950')
 

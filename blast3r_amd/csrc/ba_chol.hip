@@ -1,0 +1,869 @@
+// Direct solve of the reduced camera system (north-star stage 4: "the reduced-system Cholesky solve
+// on the same GPU").  The reference's only definition of a direct reduced solve is
+// GaussNewtonSolver._solve_dense_S (src/blast3r/inference/ba_solver.py:208-226): S = A - B D^-1 C,
+// rhs = g_c - B D^-1 g_p, delta_c = torch.linalg.solve(S, rhs).  Here S_u = P^T S_img P + diag(damp)
+// (the image-pair blocks of ba_linearize_schur mapped onto the reference's unknowns, with the per-leaf
+// damping of ba_solver.py:575-582) is symmetric positive definite, so it is factored S_u = L L^T
+// (fp64) and solved by two triangular sweeps; delta_c lands in the same x as the PCG's, so the
+// back-substitution that follows is unchanged.
+//
+// Two layouts:
+//   dense   S_u assembled as a full lower triangle (n_u padded to 64), factored by right-looking
+//           64-column panels: the diagonal tile and its inverse in LDS (one workgroup), the panel
+//           below as A_ik L_kk^-T and the trailing update A_ij -= L_ik L_jk^T as 64 x 64 tiles of
+//           v_mfma_f64_16x16x4f64; the triangular sweeps go block by block.  Any structure.
+//   banded  the image-level blocks of a block-banded structure (every image pair within w images)
+//           with the unknowns shared by several images (a mono camera's focal pair) as a dense
+//           border: one workgroup walks the images, keeping the w + 1 active block rows in LDS,
+//           and runs both sweeps in the same launch.  Work ~ n_imgs (w d)^2 d instead of n_u^3.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <cmath>
+
+#include "ba_common.h"
+#include "ba_error.h"
+
+namespace ba {
+int unknown_setup(const ba_pcg_args& a, hipStream_t st);   // ba_pcg.hip
+
+#define CH_T 256
+#define CH_NB 64
+#define CH_LD (CH_NB + 1)
+
+typedef double dbl4 __attribute__((ext_vector_type(4)));
+
+// ba_chol_args plus the banded layout's arrays, carved out of the caller's work buffer
+struct ChArgs {
+    int32_t mode;
+    double* A;
+    int64_t lda;
+    double* Linv;
+    const int32_t* pair_idx;
+    const int32_t* kind;
+    const int32_t* shared_u;
+    int32_t n_shared;
+    int32_t w;
+    int32_t db;                 // banded: block size (the image-level columns that are local somewhere)
+    const int32_t* bcol;        // banded: (db) image-level column of each band column
+    const int32_t* bpos;        // banded: (d) band column of each image-level column, or -1
+    int32_t* info;
+    double *Ab, *Bfull, *Cb, *bl, *Lcol, *Lbord, *yv, *xl;
+};
+
+// ------------------------------------------------------------------ assembly
+// Unknown classes (host-built from the inverse lists): kind 1 = local (exactly one image-level entry,
+// e.g. a pose or z-coefficient), 2 = shared (several entries: a mono camera's focal pair, a rig node),
+// 0 = isolated (none: a group switched off, a zero leaf damped by dampen * I).
+//
+// S_img(a, b) for image-level entries a = (i, r), b = (j, c): the pair block of images (i, j).
+__device__ __forceinline__ double s_img(const ba_pcg_args& a, const int32_t* __restrict__ pair_idx, int i, int r,
+                                        int j, int c) {
+    const int d = a.d;
+    if (i <= j) {
+        const int p = pair_idx[(int64_t)i * a.n_imgs + j];
+        return p >= 0 ? a.S_pairs[((int64_t)p * d + r) * d + c] : 0.0;
+    }
+    const int p = pair_idx[(int64_t)j * a.n_imgs + i];
+    return p >= 0 ? a.S_pairs[((int64_t)p * d + c) * d + r] : 0.0;
+}
+
+// S_u(s, v) for a shared unknown s and a local one v = entry (j, cv): the sum over the pairs of image
+// row j of B[cv][r] over the entries (i, r) of the other image that carry s (B = S(j, i)).
+__device__ double shared_local(const ba_pcg_args& a, int s, int j, int cv) {
+    const int d = a.d;
+    double val = 0.0;
+    for (int q = a.row_ptr[j]; q < a.row_ptr[j + 1]; ++q) {
+        const int ent = a.row_ent[q];
+        const int p = ent >> 1, tr = ent & 1;
+        const int i = tr ? a.pair_i1[p] : a.pair_i2[p];
+        const double* S = a.S_pairs + (int64_t)p * d * d;
+        for (int r = 0; r < d; ++r)
+            if (a.umap[(int64_t)i * d + r] == s) val += tr ? S[r * d + cv] : S[cv * d + r];
+    }
+    return val;
+}
+
+// dense: S_u[u][v] for v <= u where neither is shared (the identity on the padding rows n_u .. N, the
+// damping alone on an isolated unknown), one thread per (u, v)
+__global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c, int64_t N) {
+    const int64_t u = blockIdx.y;
+    const int64_t v = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (v > u || u >= N) return;
+    double val = 0.0;
+    if (u < a.n_u && v < a.n_u) {
+        const int ku = c.kind[u], kv = c.kind[v];
+        if (ku == 2 || kv == 2) return;                 // k_shared_local / k_shared_shared
+        if (ku == 1 && kv == 1) {
+            const int ea = a.inv_src[a.inv_ptr[u]], eb = a.inv_src[a.inv_ptr[v]];
+            const int ia = ea / a.d, ib = eb / a.d;
+            val = s_img(a, c.pair_idx, ia, ea - ia * a.d, ib, eb - ib * a.d);
+        }
+        if (u == v) val += a.damp[u];
+    } else if (u == v) {
+        val = 1.0;
+    }
+    c.A[u * c.lda + v] = val;
+}
+
+// S_u(s, v) for every shared s (blockIdx.y) and every local v: written to the dense matrix (mode 0)
+// or to the border rows Bfull[s][entry of v] (mode 1)
+__global__ void __launch_bounds__(CH_T) k_shared_local(ba_pcg_args a, ChArgs c, int mode) {
+    const int64_t v = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    const int sb = blockIdx.y;
+    if (v >= a.n_u || c.kind[v] != 1) return;
+    const int s = c.shared_u[sb];
+    const int e = a.inv_src[a.inv_ptr[v]];
+    const int j = e / a.d, cv = e - j * a.d;
+    const double val = shared_local(a, s, j, cv);
+    if (mode == 0) {
+        const int64_t r = s > v ? s : v, q = s > v ? v : s;
+        c.A[r * c.lda + q] = val;
+    } else {
+        c.Bfull[(int64_t)sb * a.n_imgs * c.db + (int64_t)j * c.db + c.bpos[cv]] = val;
+    }
+}
+
+// S_u(s1, s2) for shared s2 <= s1 (by list position): one workgroup per pair summing every pair
+// block's entries that carry (s1, s2), in a fixed order; the damping on the diagonal.
+__global__ void __launch_bounds__(CH_T) k_shared_shared(ba_pcg_args a, ChArgs c, int mode, int64_t n_pairs) {
+    __shared__ double sh[CH_T];
+    const int b1 = blockIdx.x, b2 = blockIdx.y;
+    if (b2 > b1) return;
+    const int s1 = c.shared_u[b1], s2 = c.shared_u[b2];
+    const int d = a.d;
+    double val = 0.0;
+    for (int64_t p = threadIdx.x; p < n_pairs; p += CH_T) {
+        const int i1 = a.pair_i1[p], i2 = a.pair_i2[p];
+        const double* S = a.S_pairs + p * d * d;
+        for (int r = 0; r < d; ++r) {
+            const int u1 = a.umap[(int64_t)i1 * d + r];
+            for (int q = 0; q < d; ++q) {
+                const int u2 = a.umap[(int64_t)i2 * d + q];
+                if (u1 == s1 && u2 == s2) val += S[r * d + q];
+                if (i1 != i2 && u2 == s1 && u1 == s2) val += S[r * d + q];
+            }
+        }
+    }
+    sh[threadIdx.x] = val;
+    __syncthreads();
+    for (int w = CH_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        double t = sh[0] + (s1 == s2 ? a.damp[s1] : 0.0);
+        if (mode == 0) {
+            const int64_t r = s1 > s2 ? s1 : s2, q = s1 > s2 ? s2 : s1;
+            c.A[r * c.lda + q] = t;
+        } else {
+            c.Cb[b1 * c.n_shared + b2] = t;
+            c.Cb[b2 * c.n_shared + b1] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ dense panel factor
+// Diagonal tile k: L_kk = chol(A_kk) in place and Linv_k = L_kk^-1 (64 x 64, row-major, compact).
+// A pivot that is not positive (S_u not positive definite in fp64) is recorded in info (the first
+// such global column + 1, by atomicMin) and replaced by 1 so that the sweep stays finite.
+__global__ void __launch_bounds__(CH_T) k_potrf_tile(double* __restrict__ A, int64_t lda, int k,
+                                                     double* __restrict__ Linv, int32_t* __restrict__ info) {
+    __shared__ double T[CH_NB][CH_LD];
+    __shared__ double X[CH_NB][CH_LD];
+    const int t = threadIdx.x;
+    const int64_t o = (int64_t)k * CH_NB;
+    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
+        const int r = e / CH_NB, q = e - r * CH_NB;
+        T[r][q] = q <= r ? A[(o + r) * lda + o + q] : 0.0;
+        X[r][q] = r == q ? 1.0 : 0.0;
+    }
+    __syncthreads();
+    for (int j = 0; j < CH_NB; ++j) {
+        if (t == 0) {
+            double dj = T[j][j];
+            if (!(dj > 0.0)) {
+                atomicMin(info, (int32_t)(o + j + 1));
+                dj = 1.0;
+            }
+            T[j][j] = sqrt(dj);
+        }
+        __syncthreads();
+        const double piv = T[j][j];
+        if (t > j && t < CH_NB) T[t][j] /= piv;
+        __syncthreads();
+        // trailing update of the lower triangle right of column j: thread (row r, column group g)
+        {
+            const int r = t & (CH_NB - 1), g = t >> 6;
+            if (r > j) {
+                const double lr = T[r][j];
+                for (int q = j + 1 + g; q <= r; q += CH_T / CH_NB) T[r][q] -= lr * T[q][j];
+            }
+        }
+        __syncthreads();
+    }
+    // X = L^-1 by elimination on [L | I]: normalise row j, then remove column j from the rows below
+    for (int j = 0; j < CH_NB; ++j) {
+        const double piv = T[j][j];
+        if (t <= j) X[j][t] /= piv;
+        __syncthreads();
+        {
+            const int r = t & (CH_NB - 1), g = t >> 6;
+            if (r > j) {
+                const double lr = T[r][j];
+                for (int q = g; q <= j; q += CH_T / CH_NB) X[r][q] -= lr * X[j][q];
+            }
+        }
+        __syncthreads();
+    }
+    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
+        const int r = e / CH_NB, q = e - r * CH_NB;
+        if (q <= r) A[(o + r) * lda + o + q] = T[r][q];
+        Linv[(int64_t)k * CH_NB * CH_NB + e] = q <= r ? X[r][q] : 0.0;
+    }
+}
+
+// ------------------------------------------------------------------ dense 64 x 64 tile products
+// mode 0 (panel): tile (k + 1 + blockIdx.x, k) <- A_ik Linv_k^T.
+// mode 1 (trailing update): tile (i, j), k < j <= i, from the triangular index blockIdx.x:
+//   A_ij -= L_ik L_jk^T (the diagonal tiles keep their upper part).
+// Four waves, each a 32 x 32 quadrant as 2 x 2 tiles of v_mfma_f64_16x16x4f64 over K = 64; the
+// operands are staged in LDS (rows padded to 65 doubles).  Accumulator layout: lane l, element v
+// holds D[4 v + l / 16][l % 16]; operand lane l holds row l % 16, k = l / 16 of its 16 x 4 slice.
+__global__ void __launch_bounds__(CH_T) k_tile_nt(double* __restrict__ A, int64_t lda, int k, int mode,
+                                                  const double* __restrict__ Linv) {
+    __shared__ double sa[CH_NB][CH_LD];
+    __shared__ double sb[CH_NB][CH_LD];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    int ti, tj;
+    if (mode == 0) {
+        ti = k + 1 + (int)blockIdx.x;
+        tj = k;
+    } else {
+        const int64_t q = blockIdx.x;
+        int i = (int)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
+        while ((int64_t)(i + 1) * (i + 2) / 2 <= q) ++i;
+        while ((int64_t)i * (i + 1) / 2 > q) --i;
+        const int j = (int)(q - (int64_t)i * (i + 1) / 2);
+        ti = k + 1 + i;
+        tj = k + 1 + j;
+    }
+    const int64_t ro = (int64_t)ti * CH_NB, co = (int64_t)tj * CH_NB, ko = (int64_t)k * CH_NB;
+    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
+        const int r = e / CH_NB, q = e - r * CH_NB;
+        sa[r][q] = A[(ro + r) * lda + ko + q];
+        sb[r][q] = mode == 0 ? Linv[(int64_t)k * CH_NB * CH_NB + e] : A[(co + r) * lda + ko + q];
+    }
+    __syncthreads();
+    const int qi = (wave >> 1) * 32, qj = (wave & 1) * 32;
+    const int l16 = lane & 15, lk = lane >> 4;
+    dbl4 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = (dbl4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll 4
+    for (int kk = 0; kk < CH_NB / 4; ++kk) {
+        double av[2], bv[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) av[mi] = sa[qi + 16 * mi + l16][4 * kk + lk];
+#pragma unroll
+        for (int nj = 0; nj < 2; ++nj) bv[nj] = sb[qj + 16 * nj + l16][4 * kk + lk];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int nj = 0; nj < 2; ++nj)
+                acc[mi][nj] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mi], bv[nj], acc[mi][nj], 0, 0, 0);
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = qi + 16 * mi + 4 * v + lk, q = qj + 16 * nj + l16;
+                double* dst = A + (ro + r) * lda + co + q;
+                if (mode == 0) {
+                    *dst = acc[mi][nj][v];
+                } else if (ti != tj || q <= r) {
+                    *dst = *dst - acc[mi][nj][v];
+                }
+            }
+}
+
+// ------------------------------------------------------------------ dense triangular sweeps
+// Forward, block k (right-looking): y_k = Linv_k b_k; every workgroup forms y_k itself from b_k (read
+// only in this launch), workgroup 0 stores it, workgroup w >= 1 updates b_i -= L_ik y_k for the tile
+// i = k + w.  b is the working copy of the rhs (padded with zeros), y the result.
+__global__ void __launch_bounds__(CH_NB) k_fwd_block(const double* __restrict__ A, int64_t lda, int k,
+                                                     const double* __restrict__ Linv, double* __restrict__ b,
+                                                     double* __restrict__ y) {
+    __shared__ double sy[CH_NB];
+    __shared__ double sbk[CH_NB];
+    const int t = threadIdx.x;
+    const int64_t ko = (int64_t)k * CH_NB;
+    sbk[t] = b[ko + t];
+    __syncthreads();
+    const double* Li = Linv + (int64_t)k * CH_NB * CH_NB + t * CH_NB;
+    double s = 0.0;
+    for (int q = 0; q <= t; ++q) s += Li[q] * sbk[q];
+    sy[t] = s;
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        y[ko + t] = s;
+        return;
+    }
+    const int64_t ro = ko + (int64_t)blockIdx.x * CH_NB;
+    const double* Lr = A + (ro + t) * lda + ko;
+    double acc = 0.0;
+    for (int q = 0; q < CH_NB; ++q) acc += Lr[q] * sy[q];
+    b[ro + t] -= acc;
+}
+
+// Backward, block k (right-looking on L^T): x_k = Linv_k^T y_k; workgroup 0 stores it, workgroup
+// w >= 1 updates y_i -= L_ki^T x_k for the tile i = w - 1 < k.
+__global__ void __launch_bounds__(CH_NB) k_bwd_block(const double* __restrict__ A, int64_t lda, int k,
+                                                     const double* __restrict__ Linv, double* __restrict__ y,
+                                                     double* __restrict__ x) {
+    __shared__ double sx[CH_NB];
+    __shared__ double syk[CH_NB];
+    const int t = threadIdx.x;
+    const int64_t ko = (int64_t)k * CH_NB;
+    syk[t] = y[ko + t];
+    __syncthreads();
+    const double* Lb = Linv + (int64_t)k * CH_NB * CH_NB;
+    double s = 0.0;
+    for (int r = t; r < CH_NB; ++r) s += Lb[r * CH_NB + t] * syk[r];
+    sx[t] = s;
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        x[ko + t] = s;
+        return;
+    }
+    const int64_t io = (int64_t)(blockIdx.x - 1) * CH_NB;
+    double acc = 0.0;
+    for (int r = 0; r < CH_NB; ++r) acc += A[(ko + r) * lda + io + t] * sx[r];
+    y[io + t] -= acc;
+}
+
+__global__ void __launch_bounds__(CH_T) k_copy_pad(const double* __restrict__ src, int64_t n, int64_t N,
+                                                   double* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (i < N) dst[i] = i < n ? src[i] : 0.0;
+}
+
+// unknowns that no image-level entry carries (a parameter group switched off: a zero leaf damped by
+// dampen * I, ba_solver.py:510-517) are decoupled: x_u = rhs_u / damp_u (the rhs is zero there)
+__global__ void __launch_bounds__(CH_T) k_isolated(ba_pcg_args a, const double* __restrict__ xs) {
+    const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (u >= a.n_u) return;
+    a.x[u] = a.inv_ptr[u + 1] > a.inv_ptr[u] ? xs[u] : a.rhs[u] / a.damp[u];
+}
+
+__global__ void k_chol_status(ba_pcg_args a, const int32_t* __restrict__ info) {
+    if (threadIdx.x == 0 && a.istate) {
+        a.istate[0] = 1; a.istate[1] = 1;
+        a.istate[2] = 0;                     // no iterations
+        a.istate[3] = info[0] == 0x7fffffff; // "converged": the factorisation found every pivot positive
+        a.istate[4] = 0; a.istate[5] = 0;
+    }
+}
+
+__global__ void k_info_init(int32_t* info) {
+    if (threadIdx.x == 0) info[0] = 0x7fffffff;
+}
+
+
+// ------------------------------------------------------------------ banded layout
+// Unknown order of the banded factor: the local unknowns image by image (entry (i, c) at i d + c;
+// an entry that is inactive or carries a shared unknown is an identity row there), then the n_s
+// shared unknowns (the border).  Every image pair (i, j) of the structure has |i - j| <= w, so the
+// factor of the local part is block-banded with w sub-diagonal blocks.
+#define CB_T 512
+#define CB_MAXD 16
+#define CB_MAXM 160
+#define CB_MAXS 8
+#define CB_PF 5                 // new-row entries per thread: (16 x 160) / 512
+#define CB_NX 6                 // staged backward entries per thread: (160 + 8) x 16 / 512
+#define CB_PK(r, c) ((r) * ((r) + 1) / 2 + (c))
+
+// Ab[i][k] (db x db) = the local block of S_u at images (i, i - k), k = 0..w (zero for i - k < 0), in
+// band columns (the image-level columns that carry a local unknown in some image: a mono camera's focal
+// columns, shared by every image, are left out), the damping on a local diagonal entry, 1 on a
+// non-local one; bl[i db + r] = the local rhs entries; the border rows Bfull cleared.
+__global__ void __launch_bounds__(CH_T) k_band_assemble(ba_pcg_args a, ChArgs c) {
+    const int d = a.d, db = c.db, w1 = c.w + 1;
+    const int64_t e = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    const int64_t per = (int64_t)w1 * db * db;
+    if (e >= (int64_t)a.n_imgs * per) return;
+    const int i = (int)(e / per);
+    int rem = (int)(e - (int64_t)i * per);
+    const int k = rem / (db * db);
+    rem -= k * db * db;
+    const int r = rem / db, q = rem - r * db;
+    const int j = i - k;
+    const int cr = c.bcol[r], cq = c.bcol[q];
+    double val = 0.0;
+    const int ua = a.umap[(int64_t)i * d + cr];
+    const bool la = ua >= 0 && c.kind[ua] == 1;
+    if (j >= 0) {
+        const int ub = a.umap[(int64_t)j * d + cq];
+        const bool lb = ub >= 0 && c.kind[ub] == 1;
+        if (la && lb) val = s_img(a, c.pair_idx, i, cr, j, cq);
+        if (k == 0 && r == q) val = la ? val + a.damp[ua] : 1.0;
+    }
+    c.Ab[e] = val;
+    if (k == 0 && q == 0) {
+        c.bl[(int64_t)i * db + r] = la ? a.rhs[ua] : 0.0;
+        // border couplings: k_shared_local (launched next) writes those of the local entries; the
+        // other entries are identity rows, uncoupled
+        for (int b = 0; b < c.n_shared; ++b) c.Bfull[(int64_t)b * a.n_imgs * db + (int64_t)i * db + r] = 0.0;
+    }
+}
+
+// LDS of k_band_solve (dynamic): two packed lower triangles of the window (M (M + 1) / 2 doubles
+// each), two copies of the border rows (n_s x M), the corner (n_s^2), two copies of the rhs window (M),
+// the border rhs (n_s), the diagonal block's y / reciprocal pivots (2 x 16) and x_b (n_s).
+__host__ __device__ inline int64_t band_lds_doubles(int M, int ns) {
+    return (int64_t)M * (M + 1) + 2 * (int64_t)ns * M + (int64_t)ns * ns + 2 * M + ns + 2 * CB_MAXD + ns;
+}
+
+// One workgroup factors the banded system and runs both triangular sweeps.  LDS holds the active
+// window: block rows i .. i + w of the local part as a packed lower triangle (M = (w + 1) d rows), the
+// border rows restricted to those columns, the corner and the rhs window, in two copies: each step
+// reads one and writes the next, so the window moves down an image as a side effect of its update.
+// Per image i:
+//   1. wave 0 factors the diagonal block in registers (lane r holds row r; the columns' values move by
+//      lane shuffles), keeps the reciprocal pivots, and forms y_i = L_ii^-1 b_i (the forward sweep
+//      rides along);
+//   2. one thread per panel row (and per border row) solves its row against L_ii^T, stores it to the
+//      factor, and subtracts its share of y_i from the rhs window;
+//   3. the trailing window takes - P P^T as 16 x 16 tiles of v_mfma_f64_16x16x4f64 (K = d padded to a
+//      multiple of 4), written one image up into the other copy; the border rows and the corner
+//      their own products; the next image's block row, border columns and rhs (prefetched into
+//      registers at the start of the step) fill the last rows of the other copy.
+// Then thread 0 factors the corner, and the backward sweep walks the images in reverse, reading each
+// column panel of L (prefetched one step ahead) against the solved x of the following images.
+__global__ void __launch_bounds__(CB_T) k_band_solve(ba_pcg_args a, ChArgs c) {
+    extern __shared__ double lds[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int d = c.db, w1 = c.w + 1, M = w1 * d, Md = M - d, ns = c.n_shared, n_imgs = a.n_imgs;
+    const int64_t nl = (int64_t)n_imgs * d;
+    const int PK = M * (M + 1) / 2;
+    double* Wbuf[2] = {lds, lds + PK};
+    double* Bbuf[2] = {lds + 2 * PK, lds + 2 * PK + ns * M};
+    double* Cw = lds + 2 * PK + 2 * ns * M;
+    double* bwbuf[2] = {Cw + ns * ns, Cw + ns * ns + M};
+    double* bw = bwbuf[0];
+    double* bb = bwbuf[1] + M;
+    double* yd = bb + ns;
+    double* rp = yd + CB_MAXD;
+    double* xb = rp + CB_MAXD;
+    // block (image ir, image ic) entry (r, q) of the local part, identity past the last image
+    auto band_at = [&](int ir, int ic, int r, int q) -> double {
+        if (ir >= n_imgs) return (ir == ic && r == q) ? 1.0 : 0.0;
+        return c.Ab[(((int64_t)ir * w1 + (ir - ic)) * d + r) * d + q];
+    };
+    auto row_of = [&](int e) -> int {          // the packed row of index e
+        int r = (int)((sqrt(8.0 * e + 1.0) - 1.0) * 0.5);
+        while (CB_PK(r + 1, 0) <= e) ++r;
+        while (CB_PK(r, 0) > e) --r;
+        return r;
+    };
+    // ---- initial window: images 0 .. w
+    for (int e = t; e < PK; e += CB_T) {
+        const int r = row_of(e), q = e - CB_PK(r, 0);
+        Wbuf[0][e] = band_at(r / d, q / d, r % d, q % d);
+    }
+    for (int e = t; e < ns * M; e += CB_T) {
+        const int bq = e % M;
+        Bbuf[0][e] = bq < nl ? c.Bfull[(int64_t)(e / M) * nl + bq] : 0.0;
+    }
+    for (int e = t; e < ns * ns; e += CB_T) Cw[e] = c.Cb[e];
+    for (int e = t; e < M; e += CB_T) bw[e] = e < nl ? c.bl[e] : 0.0;
+    if (t < ns) bb[t] = a.rhs[c.shared_u[t]];
+    // this thread's entries of the window's last block row (new rows Md .. M - 1, packed order)
+    const int n_new = PK - CB_PK(Md, 0);
+    int nr_r[CB_PF], nr_q[CB_PF];
+#pragma unroll
+    for (int k = 0; k < CB_PF; ++k) {
+        const int e = t + k * CB_T;
+        nr_r[k] = -1; nr_q[k] = 0;
+        if (e < n_new) {
+            const int g = CB_PK(Md, 0) + e;
+            nr_r[k] = row_of(g);
+            nr_q[k] = g - CB_PK(nr_r[k], 0);
+        }
+    }
+    // this wave's tiles of the trailing window
+    const int n16 = (Md + 15) >> 4, ntile = n16 * (n16 + 1) / 2, nk = (d + 3) >> 2;
+    const int l16 = lane & 15, lk = lane >> 4;
+    __syncthreads();
+    for (int i = 0; i < n_imgs; ++i) {
+        double* W = Wbuf[i & 1];
+        double* Wn = Wbuf[(i + 1) & 1];
+        double* Bw = Bbuf[i & 1];
+        double* Bn = Bbuf[(i + 1) & 1];
+        bw = bwbuf[i & 1];
+        double* bwn = bwbuf[(i + 1) & 1];
+        // prefetch the block row of image i + w + 1 (the last rows of the next window)
+        const int inew = i + w1;
+        double pf[CB_PF], pfb = 0.0, pfr = 0.0;
+#pragma unroll
+        for (int k = 0; k < CB_PF; ++k)
+            pf[k] = nr_r[k] >= 0 ? band_at(inew, i + 1 + nr_q[k] / d, nr_r[k] - Md, nr_q[k] % d) : 0.0;
+        if (t < ns * d) {
+            const int q = t % d;
+            pfb = (int64_t)inew * d + q < nl ? c.Bfull[(int64_t)(t / d) * nl + (int64_t)inew * d + q] : 0.0;
+        }
+        if (t < d) pfr = (int64_t)inew * d + t < nl ? c.bl[(int64_t)inew * d + t] : 0.0;
+
+        // 1. diagonal block (wave 0): L_ii in registers, reciprocal pivots, y_i = L_ii^-1 b_i
+        if (wave == 0) {
+            double row[CB_MAXD];
+#pragma unroll
+            for (int q = 0; q < CB_MAXD; ++q) row[q] = (lane < d && q <= lane) ? W[CB_PK(lane, q)] : 0.0;
+            double rinv = 0.0;
+#pragma unroll
+            for (int j = 0; j < CB_MAXD; ++j) {
+                if (j < d) {
+                    double pj = __shfl(row[j], j);
+                    if (!(pj > 0.0)) {
+                        if (lane == 0) atomicMin(c.info, (int32_t)((int64_t)i * d + j + 1));
+                        pj = 1.0;
+                    }
+                    const double ljj = sqrt(pj), rj = 1.0 / ljj;
+                    if (lane == j) { row[j] = ljj; rinv = rj; }
+                    else if (lane > j) row[j] = row[j] * rj;
+                    const double lj = row[j];
+#pragma unroll
+                    for (int q = j + 1; q < CB_MAXD; ++q) {
+                        const double lqj = __shfl(lj, q);
+                        if (q < d && lane >= q && lane < d) row[q] -= lj * lqj;
+                    }
+                }
+            }
+            double acc = lane < d ? bw[lane] : 0.0, y = 0.0;
+#pragma unroll
+            for (int m = 0; m < CB_MAXD; ++m) {
+                if (m < d) {
+                    if (lane == m) y = acc * rinv;
+                    const double ym = __shfl(y, m);
+                    if (lane > m) acc -= row[m] * ym;
+                }
+            }
+            if (lane < d) {
+                double* Lc = c.Lcol + ((int64_t)i * M + lane) * d;
+#pragma unroll
+                for (int q = 0; q < CB_MAXD; ++q)
+                    if (q < d) Lc[q] = q <= lane ? row[q] : 0.0;
+                rp[lane] = rinv;
+                yd[lane] = y;
+                c.yv[(int64_t)i * d + lane] = y;
+            }
+            // L_ii for the panel rows of step 2 (read from W: rows 0..d-1 are not read by anything else)
+            if (lane < d) {
+#pragma unroll
+                for (int q = 0; q < CB_MAXD; ++q)
+                    if (q <= lane) W[CB_PK(lane, q)] = row[q];
+            }
+        }
+        __syncthreads();
+        // 2. panel rows and border rows against L_ii^T; their share of y_i leaves the rhs window
+        if (t < Md + ns) {
+            const bool pr = t < Md;
+            const int r = d + t, b = t - Md;
+            double x[CB_MAXD];
+            double dot = 0.0;
+#pragma unroll
+            for (int q = 0; q < CB_MAXD; ++q) {
+                x[q] = 0.0;
+                if (q < d) {
+                    double v = pr ? W[CB_PK(r, q)] : Bw[b * M + q];
+#pragma unroll
+                    for (int m = 0; m < CB_MAXD; ++m)
+                        if (m < q) v -= x[m] * W[CB_PK(q, m)];
+                    x[q] = v * rp[q];
+                    dot += x[q] * yd[q];
+                }
+            }
+            double* dst = pr ? c.Lcol + ((int64_t)i * M + r) * d : c.Lbord + ((int64_t)i * ns + b) * d;
+            double* wrow = pr ? W + CB_PK(r, 0) : Bw + b * M;
+#pragma unroll
+            for (int q = 0; q < CB_MAXD; ++q)
+                if (q < d) { wrow[q] = x[q]; dst[q] = x[q]; }
+            if (pr) bw[r] -= dot;
+            else bb[b] -= dot;
+        }
+        __syncthreads();
+        // 3. next window = trailing window - P P^T (one image up), border rows and corner, new last rows
+        for (int tile = wave; tile < ntile; tile += CB_T / 64) {
+            int ti = (int)((sqrt(8.0 * tile + 1.0) - 1.0) * 0.5);
+            while ((ti + 1) * (ti + 2) / 2 <= tile) ++ti;
+            while (ti * (ti + 1) / 2 > tile) --ti;
+            const int tj = tile - ti * (ti + 1) / 2;
+            const int ra = 16 * ti + l16, rb = 16 * tj + l16;
+            dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+            for (int kk = 0; kk < nk; ++kk) {
+                const int k = 4 * kk + lk;
+                const double av = (ra < Md && k < d) ? W[CB_PK(d + ra, k)] : 0.0;
+                const double bv = (rb < Md && k < d) ? W[CB_PK(d + rb, k)] : 0.0;
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * ti + 4 * v + lk, q = 16 * tj + l16;
+                if (r < Md && q <= r) Wn[CB_PK(r, q)] = W[CB_PK(d + r, d + q)] - acc[v];
+            }
+        }
+        for (int e = t; e < ns * Md + ns * ns; e += CB_T) {
+            if (e < ns * Md) {
+                const int b = e / Md, q = e - b * Md;
+                double sum = 0.0;
+                for (int m = 0; m < d; ++m) sum += Bw[b * M + m] * W[CB_PK(d + q, m)];
+                Bn[b * M + q] = Bw[b * M + d + q] - sum;
+            } else {
+                const int f = e - ns * Md, b1 = f / ns, b2 = f - b1 * ns;
+                double sum = 0.0;
+                for (int m = 0; m < d; ++m) sum += Bw[b1 * M + m] * Bw[b2 * M + m];
+                Cw[f] -= sum;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < CB_PF; ++k)
+            if (nr_r[k] >= 0) Wn[CB_PK(nr_r[k], nr_q[k])] = pf[k];
+        if (t < ns * d) Bn[(t / d) * M + Md + t % d] = pfb;
+        // the rhs window moves down one image (its entries d.. took this step's share in step 2)
+        if (t < Md) bwn[t] = bw[t + d];
+        if (t < d) bwn[Md + t] = pfr;
+        __syncthreads();
+    }
+    bw = bwbuf[n_imgs & 1];
+    // ---- border: factor the corner in place, finish the forward sweep, start the backward one
+    if (t == 0) {
+        for (int r = 0; r < ns; ++r)
+            for (int q = 0; q <= r; ++q) {
+                double v = Cw[r * ns + q];
+                for (int m = 0; m < q; ++m) v -= Cw[r * ns + m] * Cw[q * ns + m];
+                if (r == q) {
+                    if (!(v > 0.0)) {
+                        atomicMin(c.info, (int32_t)(nl + r + 1));
+                        v = 1.0;
+                    }
+                    Cw[r * ns + r] = sqrt(v);
+                } else {
+                    Cw[r * ns + q] = v / Cw[q * ns + q];
+                }
+            }
+        for (int r = 0; r < ns; ++r) {
+            double v = bb[r];
+            for (int m = 0; m < r; ++m) v -= Cw[r * ns + m] * bb[m];
+            bb[r] = v / Cw[r * ns + r];
+        }
+        for (int r = ns - 1; r >= 0; --r) {
+            double v = bb[r];
+            for (int m = r + 1; m < ns; ++m) v -= Cw[m * ns + r] * xb[m];
+            xb[r] = v / Cw[r * ns + r];
+        }
+        for (int r = 0; r < ns; ++r) a.x[c.shared_u[r]] = xb[r];
+    }
+    // backward sweep: x_i = L_ii^-T (y_i - sum_r L(r, i)^T x_r - L_b,i^T x_b).  xw holds x of the
+    // window's images circularly (image j at slot j mod (w + 1)); images past the last one stay zero
+    // (their panel rows of L are zero anyway).  The column panel of L (M x d) and the border rows
+    // (n_s x d) of image i are staged in LDS (two slots over the free window buffers, w >= 1), the
+    // next image's loaded into registers while this one is used.  Wave g forms the dots of columns g and
+    // g + 8; wave 0 holds column q of L_ii in lane q, so the back substitution only broadcasts x_m.
+    double* xw = bw;                          // the rhs window is free now
+    const int slot_sz = M * d + ns * d, n_sl = (slot_sz + CB_T - 1) / CB_T;
+    double* Lp[2] = {lds, lds + slot_sz};     // over the window buffers (2 slot_sz <= M (M + 1) + 2 ns M)
+    __syncthreads();
+    if (t < M) xw[t] = 0.0;
+    auto stage_val = [&](int i, int e) -> double {
+        if (e < M * d) return c.Lcol[(int64_t)i * M * d + e];
+        return c.Lbord[(int64_t)i * ns * d + (e - M * d)];
+    };
+    for (int e = t; e < slot_sz; e += CB_T) Lp[(n_imgs - 1) & 1][e] = stage_val(n_imgs - 1, e);
+    __syncthreads();
+    const int g = t >> 6;                     // column group: columns g, g + 8
+    int rq[3], rm[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int r = d + lane + 64 * k;
+        rq[k] = r / d;
+        rm[k] = r - rq[k] * d;
+    }
+    for (int i = n_imgs - 1; i >= 0; --i) {
+        double nx[CB_NX];
+#pragma unroll
+        for (int k = 0; k < CB_NX; ++k) {
+            const int e = t + k * CB_T;
+            nx[k] = (i >= 1 && k < n_sl && e < slot_sz) ? stage_val(i - 1, e) : 0.0;
+        }
+        const double* P = Lp[i & 1];
+        // columns g and g + 8 of this image's panel against the solved x of the following images
+#pragma unroll
+        for (int h = 0; h < CB_MAXD; h += CB_T / 64) {
+            const int col = g + h;
+            double sum = 0.0;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                const int r = d + lane + 64 * k;
+                if (col < d && r < M) sum += P[r * d + col] * xw[((i + rq[k]) % w1) * d + rm[k]];
+            }
+            if (col < d && lane < ns) sum += P[M * d + lane * d + col] * xb[lane];
+            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            if (col < d && lane == 0) yd[col] = c.yv[(int64_t)i * d + col] - sum;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            double lc[CB_MAXD];
+#pragma unroll
+            for (int m = 0; m < CB_MAXD; ++m) lc[m] = (lane < d && m < d && m >= lane) ? P[m * d + lane] : 0.0;
+            double acc = lane < d ? yd[lane] : 0.0, xv = 0.0;
+#pragma unroll
+            for (int m = CB_MAXD - 1; m >= 0; --m) {
+                if (m < d) {
+                    if (lane == m) xv = acc / lc[m];
+                    const double xm = __shfl(xv, m);
+                    if (lane < m) acc -= lc[m] * xm;
+                }
+            }
+            if (lane < d) {
+                xw[(i % w1) * d + lane] = xv;
+                c.xl[(int64_t)i * d + lane] = xv;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < CB_NX; ++k) {
+            const int e = t + k * CB_T;
+            if (i >= 1 && k < n_sl && e < slot_sz) Lp[(i - 1) & 1][e] = nx[k];
+        }
+        __syncthreads();
+    }
+}
+
+// x of the local unknowns from the banded solution (shared ones were written by k_band_solve);
+// isolated unknowns: rhs / damp
+__global__ void __launch_bounds__(CH_T) k_band_scatter(ba_pcg_args a, ChArgs c) {
+    const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (u >= a.n_u) return;
+    const int k = c.kind[u];
+    if (k == 1) {
+        const int e = a.inv_src[a.inv_ptr[u]], i = e / a.d;
+        a.x[u] = c.xl[(int64_t)i * c.db + c.bpos[e - i * a.d]];
+    }
+    else if (k == 0) a.x[u] = a.rhs[u] / a.damp[u];
+}
+
+}  // namespace ba
+
+using namespace ba;
+
+extern "C" int64_t ba_chol_dense_lda(int64_t n_u) {
+    const int64_t m = n_u < 1 ? 1 : n_u;
+    return (m + CH_NB - 1) / CH_NB * CH_NB;
+}
+
+extern "C" int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_imgs, int32_t d, int32_t w,
+                                        int32_t n_shared) {
+    // banded: d is the band block size db
+    if (mode == 0) return 3 * ba_chol_dense_lda(n_u);
+    const int64_t M = (int64_t)(w + 1) * d, nl = (int64_t)n_imgs * d;
+    return (int64_t)n_imgs * (w + 1) * d * d + (int64_t)n_shared * nl + (int64_t)n_shared * n_shared + nl +
+           (int64_t)n_imgs * M * d + (int64_t)n_imgs * n_shared * d + 2 * nl;
+}
+
+extern "C" int64_t ba_chol_band_lds_bytes(int32_t d, int32_t w, int32_t n_shared) {
+    return band_lds_doubles((w + 1) * d, n_shared) * (int64_t)sizeof(double);
+}
+
+extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* cargs, void* stream) {
+    clear_error();
+    BA_REQUIRE(args != nullptr && cargs != nullptr, "ba_reduced_solve: null args");
+    const ba_pcg_args& a = *args;
+    const ba_chol_args& ca = *cargs;
+    hipStream_t st = (hipStream_t)stream;
+    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16, "ba_reduced_solve: bad sizes");
+    if (a.n_u == 0) return BA_OK;
+    {
+        const void* need[] = {a.umap, a.inv_ptr, a.inv_src, a.leaf, a.S_pairs, a.e_img, a.dg_img, a.rhs, a.diagA,
+                              a.damp, a.x, a.state, a.row_ptr, a.row_ent, a.pair_i1, a.pair_i2, ca.pair_idx, ca.info,
+                              ca.work, ca.kind};
+        for (const void* q : need) BA_REQUIRE(q != nullptr, "ba_reduced_solve: null pointer in the arguments");
+    }
+    BA_REQUIRE(ca.n_shared >= 0 && (ca.n_shared == 0 || ca.shared_u != nullptr),
+               "ba_reduced_solve: shared unknowns missing");
+    ChArgs c{};
+    c.mode = ca.mode; c.A = ca.A; c.lda = ca.lda; c.Linv = ca.Linv; c.pair_idx = ca.pair_idx; c.kind = ca.kind;
+    c.shared_u = ca.shared_u; c.n_shared = ca.n_shared; c.w = ca.w; c.info = ca.info;
+    c.db = ca.db; c.bcol = ca.bcol; c.bpos = ca.bpos;
+    const int64_t n_pairs = ca.n_pairs;
+    int rc = unknown_setup(a, st);
+    if (rc != BA_OK) return rc;
+    hipLaunchKernelGGL(k_info_init, dim3(1), dim3(64), 0, st, c.info);
+    const unsigned nbu = (unsigned)((a.n_u + CH_T - 1) / CH_T);
+    if (ca.mode == 1) {
+        BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.bcol != nullptr && ca.bpos != nullptr,
+                   "ba_reduced_solve: banded layout needs db, bcol, bpos");
+        const int d = ca.db, M = (ca.w + 1) * d;
+        BA_REQUIRE(ca.w >= 0 && M <= CB_MAXM && ca.n_shared <= CB_MAXS,
+                   "ba_reduced_solve: the banded layout needs (w + 1) d <= 160 and at most 8 shared unknowns");
+        const int64_t nl = (int64_t)a.n_imgs * d;
+        double* w = ca.work;
+        c.Ab = w; w += (int64_t)a.n_imgs * (ca.w + 1) * d * d;
+        c.Bfull = w; w += (int64_t)ca.n_shared * nl;
+        c.Cb = w; w += (int64_t)ca.n_shared * ca.n_shared;
+        c.bl = w; w += nl;
+        c.Lcol = w; w += (int64_t)a.n_imgs * M * d;
+        c.Lbord = w; w += (int64_t)a.n_imgs * ca.n_shared * d;
+        c.yv = w; w += nl;
+        c.xl = w;
+        const int64_t nab = (int64_t)a.n_imgs * (ca.w + 1) * d * d;
+        hipLaunchKernelGGL(k_band_assemble, dim3((unsigned)((nab + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
+        if (ca.n_shared > 0) {
+            hipLaunchKernelGGL(k_shared_local, dim3(nbu, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 1);
+            hipLaunchKernelGGL(k_shared_shared, dim3((unsigned)ca.n_shared, (unsigned)ca.n_shared), dim3(CH_T), 0,
+                               st, a, c, 1, n_pairs);
+        }
+        const size_t lds_bytes = (size_t)band_lds_doubles(M, ca.n_shared) * sizeof(double);
+        BA_REQUIRE(lds_bytes <= 160 * 1024, "ba_reduced_solve: the banded window does not fit LDS (use mode 0)");
+        BA_HIP(hipFuncSetAttribute((const void*)k_band_solve, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds_bytes));
+        hipLaunchKernelGGL(k_band_solve, dim3(1), dim3(CB_T), lds_bytes, st, a, c);
+        hipLaunchKernelGGL(k_band_scatter, dim3(nbu), dim3(CH_T), 0, st, a, c);
+        hipLaunchKernelGGL(k_chol_status, dim3(1), dim3(64), 0, st, a, c.info);
+        BA_LAUNCHED();
+        return BA_OK;
+    }
+    BA_REQUIRE(ca.mode == 0, "ba_reduced_solve: unknown mode");
+    const int64_t N = ba_chol_dense_lda(a.n_u);
+    BA_REQUIRE(c.A != nullptr && c.lda >= N && c.Linv != nullptr, "ba_reduced_solve: dense workspace missing");
+    const int nt = (int)(N / CH_NB);
+    double* b = ca.work;
+    double* y = b + N;
+    double* xs = y + N;
+    hipLaunchKernelGGL(k_dense_assemble, dim3((unsigned)((N + CH_T - 1) / CH_T), (unsigned)N), dim3(CH_T), 0, st, a,
+                       c, N);
+    if (ca.n_shared > 0) {
+        hipLaunchKernelGGL(k_shared_local, dim3(nbu, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 0);
+        hipLaunchKernelGGL(k_shared_shared, dim3((unsigned)ca.n_shared, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a,
+                           c, 0, n_pairs);
+    }
+    for (int k = 0; k < nt; ++k) {
+        hipLaunchKernelGGL(k_potrf_tile, dim3(1), dim3(CH_T), 0, st, c.A, c.lda, k, c.Linv, c.info);
+        const int below = nt - 1 - k;
+        if (below > 0) {
+            hipLaunchKernelGGL(k_tile_nt, dim3((unsigned)below), dim3(CH_T), 0, st, c.A, c.lda, k, 0, c.Linv);
+            const int64_t tri = (int64_t)below * (below + 1) / 2;
+            hipLaunchKernelGGL(k_tile_nt, dim3((unsigned)tri), dim3(CH_T), 0, st, c.A, c.lda, k, 1, c.Linv);
+        }
+    }
+    hipLaunchKernelGGL(k_copy_pad, dim3((unsigned)((N + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a.rhs, a.n_u, N, b);
+    for (int k = 0; k < nt; ++k)
+        hipLaunchKernelGGL(k_fwd_block, dim3((unsigned)(nt - k)), dim3(CH_NB), 0, st, c.A, c.lda, k, c.Linv, b, y);
+    for (int k = nt - 1; k >= 0; --k)
+        hipLaunchKernelGGL(k_bwd_block, dim3((unsigned)(k + 1)), dim3(CH_NB), 0, st, c.A, c.lda, k, c.Linv, y, xs);
+    hipLaunchKernelGGL(k_isolated, dim3(nbu), dim3(CH_T), 0, st, a, xs);
+    hipLaunchKernelGGL(k_chol_status, dim3(1), dim3(64), 0, st, a, c.info);
+    BA_LAUNCHED();
+    return BA_OK;
+}

@@ -462,6 +462,21 @@ extern "C" int64_t ba_pcg_partials_size(int64_t n_u) {
     return PCG_NP * ((m + PCG_T - 1) / PCG_T);
 }
 
+namespace ba {
+// The unknown-level rhs, damping and preconditioner diagonal (the first part of ba_pcg_solve), for
+// the direct solve that shares them: rhs = P^T e_img, damp per leaf, diagA = clamp(P^T dg_img + damp).
+int unknown_setup(const ba_pcg_args& a, hipStream_t st) {
+    if (a.n_u == 0) return BA_OK;
+    const unsigned nb = nb_of(a.n_u);
+    const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));
+    hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+}  // namespace ba
+
 extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");

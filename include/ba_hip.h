@@ -197,6 +197,45 @@ typedef struct {
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);
 int64_t ba_pcg_partials_size(int64_t n_u);
 
+/* ------------------------------------------------------------------ reduced system (direct solve) */
+/* Direct solve of S_u delta_c = rhs with S_u = P^T S_img P + diag(damp), the system ba_pcg_solve
+ * iterates on.  Replaces the reference's explicit-Schur solve GaussNewtonSolver._solve_dense_S
+ * (ba_solver.py:208-226: S = A - B D^-1 C, torch.linalg.solve(S, rhs) at :220).  S_u is symmetric
+ * positive definite (fp64, damped), so it is factored L L^T: densely (mode 0, any structure), or, when
+ * every image pair lies within w images and few unknowns are shared, as a block band of width w with
+ * the shared unknowns as a dense border (mode 1, one workgroup). */
+typedef struct {
+    int32_t mode;                /* 0: dense (any structure); 1: banded with a dense border */
+    double* A;                   /* dense: (lda, lda) workspace; the lower triangle of S_u, then L */
+    int64_t lda;                 /* dense: ba_chol_dense_lda(n_u) (n_u rounded up to 64) */
+    double* Linv;                /* dense: (lda / 64, 64, 64) inverses of the diagonal tiles of L */
+    const int32_t* pair_idx;     /* (n_imgs, n_imgs): the pair id of images (i, j), i <= j, or -1 */
+    const int32_t* kind;         /* (n_u): 1 local (one image-level entry), 2 shared (several: a mono
+                                    camera's focal pair, a rig node), 0 isolated (none) */
+    const int32_t* shared_u;     /* (n_shared): the shared unknowns */
+    int32_t n_shared;            /* banded: at most 8 */
+    int32_t w;                   /* banded: every image pair (i, j) has |i - j| <= w (>= 1); (w + 1) db <= 160
+                                    and ba_chol_band_lds_bytes(db, w, n_shared) <= 160 KB */
+    int32_t db;                  /* banded: block size, the number of image-level columns that carry a
+                                    local unknown in some image (a mono camera's focal pair is left out) */
+    const int32_t* bcol;         /* banded: (db) image-level column of each band column */
+    const int32_t* bpos;         /* banded: (d) band column of each image-level column, or -1 */
+    int64_t n_pairs;             /* image pairs of the structure (pair_i1 / pair_i2 of ba_pcg_args) */
+    int32_t* info;               /* (1): INT32_MAX when every pivot was positive, else the first column
+                                    (1-based) whose pivot was not (replaced by 1 to keep the sweep finite) */
+    double* work;                /* ba_chol_work_doubles(mode, n_u, n_imgs, d (db when banded), w, n_shared) */
+} ba_chol_args;
+
+int64_t ba_chol_dense_lda(int64_t n_u);
+/* LDS bytes of the banded layout's workgroup (d = db); mode 1 requires at most 160 KB */
+int64_t ba_chol_band_lds_bytes(int32_t d, int32_t w, int32_t n_shared);
+int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_imgs, int32_t d, int32_t w, int32_t n_shared);
+
+/* Uses every field of ba_pcg_args that the unknown-level setup of ba_pcg_solve uses (umap, inv lists,
+ * leaf, S_pairs, e_img, dg_img, dampen / adaptive, rhs, diagA, damp, state) and writes delta_c to
+ * args->x, like the PCG; istate (if set) reports 0 iterations and "converged" = every pivot positive. */
+int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* chol, void* stream);
+
 /* ------------------------------------------------------------------ LM step (update + line search) */
 
 /* One trial of the lm_step update (engine.py:310-313, :347-354, cujac/__init__.py:56-58):

@@ -770,3 +770,54 @@ def test_lm_step_full_config2_line_search():
     ls = _check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g)
     print(f'[full cfg2 lm_step] loss {float(l0):.6g} -> {float(ls["new_loss"]):.6g} at scale {ls["scale"]}',
           flush=True)
+
+
+@pytest.mark.parametrize('layout', ['dense', 'auto'])
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800),
+                                        (2, 70, 3000)])
+def test_reduced_solve_cholesky_parity(cfg, nf, nt, layout):
+    """solver='cholesky' (ba_reduced_solve, dense L L^T of the damped reduced system on the device)
+    against the oracle's direct solve of the reference's explicit Schur system (solve_reduced_direct,
+    ba_solver.py:208-226): the device's own system is solved to a relative residual of 1e-10, and the
+    full step agrees with the oracle's on sqrt(W) J delta to 1e-6, widened only by 5x the oracle's own
+    move when its fp32 inputs are rounded differently.  layout 'auto' takes the banded factor wherever
+    the structure allows it (configs 0, 2 and 4 here: every image pair within (w + 1) d <= 160), the
+    dense one elsewhere; 'dense' forces the dense one."""
+    from tests.step_checks import oracle_system, rounded_differently, weighted_jdelta, device_system
+    print(f'cholesky parity cfg {cfg} ({nf} frames, {nt} tracks), layout {layout}', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    flags = _cfg_flags(p)
+    g = _gpu(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, solver='cholesky',
+                           cholesky_layout=layout)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                             g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
+    delta = gs.solve_delta(J, res, w)
+    assert gs.last['direct'] is not None and gs.last['direct']['first_bad_pivot'] is None
+    ist = gs.last['istate'].cpu()
+    assert int(ist[2]) == 0 and int(ist[3]) == 1
+    S_dev, rhs_dev, _ = device_system(gs)
+    n_c = S_dev.shape[0]
+    x = gs.last['x'][:n_c].cpu()
+    res_rel = float((S_dev @ x - rhs_dev).norm() / rhs_dev.norm())
+    hpo = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=o['clip_pix_err'])
+    sysd = oracle_system(p.lm_inputs(), hpo, flags)
+    ref = osol.solve_reduced_direct(sysd['ne'], sysd['g'])
+    jd_ref = weighted_jdelta(sysd, ref)
+    gen = torch.Generator().manual_seed(cfg)
+    moves = []
+    for _ in range(2):
+        alt = rounded_differently(sysd, gen)
+        moves.append(rel_err(weighted_jdelta(sysd, osol.solve_reduced_direct(alt['ne'], alt['g'])), jd_ref))
+    bar = max([1e-6] + [5 * m for m in moves])
+    e_j = rel_err(weighted_jdelta(sysd, delta), jd_ref)
+    print(f'  n_u {n_c} {gs.last["direct"]}: device residual {res_rel:.1e}; sqrt(W) J delta {e_j:.2e} (bar {bar:.1e}); '
+          f'delta {rel_err(delta, ref.to(torch.float32)):.2e}', flush=True)
+    assert res_rel <= 1e-10
+    assert e_j <= bar, (e_j, bar)
