@@ -73,6 +73,21 @@ class BaPcgArgs(ctypes.Structure):
                 ('long_ptr', c_p), ('long_idx', c_p), ('img_part', c_p), ('src1', c_p), ('long_rng', c_p),
                 ('row_cap', c_int)]
 
+class BaPmArgs(ctypes.Structure):
+    _fields_ = [('infos', c_p), ('n_imgs', c_int), ('n_tracks', c_int),
+                ('run_ptr', c_p), ('run_obs', c_p), ('run_trk', c_p), ('run_img', c_p), ('img_run_ptr', c_p),
+                ('trk_run_ptr', c_p), ('trk_run', c_p), ('trk_obs_ptr', c_p), ('trk_obs', c_p), ('obs_img', c_p),
+                ('pair_i1', c_p), ('pair_i2', c_p), ('diag_pair', c_p), ('term_ptr', c_p), ('term', c_p),
+                ('n_obs', c_i64), ('n_runs', c_i64), ('n_pairs', c_i64),
+                ('pids', c_p), ('pix2d', c_p), ('pix2d_std', c_p), ('pix2d_dep', c_p),
+                ('K', c_p), ('P_rig2cam', c_p), ('P_rig2cam_stride', c_i64), ('P_w2rig', c_p), ('z_coefs', c_p),
+                ('pts3d', c_p), ('enK', c_p), ('enP', c_p), ('enZ', c_p), ('enX', c_p),
+                ('hp', BaHuber), ('lay', BaLayout),
+                ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
+                ('pobs', c_p), ('Hpp', c_p), ('gp', c_p), ('tmax', c_p), ('lam_p', c_p), ('pfac', c_p), ('V', c_p),
+                ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dc_img', c_p), ('dX', c_p), ('dX64', c_p)]
+
+
 class BaCholArgs(ctypes.Structure):
     _fields_ = [('mode', c_int), ('A', c_p), ('lda', c_i64), ('Linv', c_p), ('pair_idx', c_p), ('kind', c_p),
                 ('shared_u', c_p), ('n_shared', c_int), ('w', c_int), ('db', c_int), ('bcol', c_p), ('bpos', c_p),
@@ -132,6 +147,7 @@ _SIGS = {
     'ba_plan_export': (c_int, [c_p, c_int, c_p]),
     'ba_plan_destroy': (None, [c_p]),
     'ba_plan_last_error': (ctypes.c_char_p, []),
+    'ba_abi_sizeof': (c_i64, [ctypes.c_char_p]),
     'ba_linearize_schur': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
     'ba_linearize_stage': (c_int, [ctypes.POINTER(BaLinArgs), c_int, c_p]),
     'ba_backsubstitute': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
@@ -143,6 +159,12 @@ _SIGS = {
     'ba_objective': (c_int, [c_p, c_i64, c_int, c_p, c_p, c_p]),
     'ba_objective_noalloc': (c_int, [c_p, c_i64, c_int, c_p, c_p]),
     'ba_chol_dense_lda': (c_i64, [c_i64]),
+    'ba_pm_plan_create': (c_p, [c_p, c_int, c_p, c_i64, c_int]),
+    'ba_pm_plan_query': (c_int, [c_p, c_p, c_p]),
+    'ba_pm_plan_export': (c_int, [c_p, c_int, c_p]),
+    'ba_pm_plan_destroy': (None, [c_p]),
+    'ba_pm_linearize_schur': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
+    'ba_pm_backsubstitute': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
     'ba_chol_band_lds_bytes': (c_i64, [c_int, c_int, c_int]),
     'ba_chol_work_doubles': (c_i64, [c_int, c_i64, c_int, c_int, c_int, c_int]),
     'ba_reduced_solve': (c_int, [ctypes.POINTER(BaPcgArgs), ctypes.POINTER(BaCholArgs), c_p]),
@@ -163,6 +185,21 @@ _SIGS = {
 EXPORTED = tuple(_SIGS)
 
 
+ABI_STRUCTS = {'ba_huber': BaHuber, 'ba_layout': BaLayout, 'ba_lin_args': BaLinArgs, 'ba_pm_args': BaPmArgs,
+               'ba_pcg_args': BaPcgArgs, 'ba_chol_args': BaCholArgs, 'ba_sample_args': BaSampleArgs,
+               'ba_obs_set': BaObsSet, 'ba_gather_args': BaGatherArgs, 'ba_remove_args': BaRemoveArgs,
+               'ba_tangent_args': BaTangentArgs}
+
+
+def _check_abi(L):
+    """Every argument struct here has the library's size (a field missing on one side would hand
+    the kernels shifted pointers)."""
+    bad = [(n, ctypes.sizeof(cls), int(L.ba_abi_sizeof(n.encode()))) for n, cls in ABI_STRUCTS.items()
+           if ctypes.sizeof(cls) != int(L.ba_abi_sizeof(n.encode()))]
+    if bad:
+        raise RuntimeError(f'libba_hip.so struct layout differs from the Python binding: {bad}')
+
+
 def lib():
     """The loaded library (raises RuntimeError when it has not been built)."""
     global _lib
@@ -178,6 +215,7 @@ def lib():
                 f = getattr(L, name)
                 f.restype = res
                 f.argtypes = args
+            _check_abi(L)
             _lib = L
     return _lib
 

@@ -75,7 +75,7 @@ class GaussNewtonSolver:
 
     def __init__(self, n_cams, n_nodes, n_imgs, n_tracks, device, no_grad_f_from_rz=False, dampen=1e-12,
                  adaptive_dampen=True, dtype=torch.float32, solver='pcg', pcg_tol=1e-6, pcg_maxiter=300,
-                 plan_options=None, use_graph=True, cholesky_layout='auto'):
+                 plan_options=None, use_graph=True, cholesky_layout='auto', path='auto'):
         self.cams = Param(n_cams)
         self.nodes = Param(n_nodes)
         self.imgs = Param(n_imgs)
@@ -99,6 +99,12 @@ class GaussNewtonSolver:
         self.pcg_tol = pcg_tol
         self.pcg_maxiter = pcg_maxiter
         self.plan_options = dict(plan_options or {})
+        # linearize + Schur: 'batched' (chunk batches, d <= 15, tracks within 13 images and 128
+        # observations, fastest on banded structures), 'pairmajor' (any track length, d <= 32, any
+        # co-visibility), 'auto' (batched where it applies and pays, else pair-major)
+        if path not in ('auto', 'batched', 'pairmajor'):
+            raise ValueError(f'unknown path {path!r}')
+        self.path = path
         self.use_graph = bool(use_graph)        # replay the PCG launches from a captured graph
         self.last = {}
 
@@ -220,7 +226,10 @@ class GaussNewtonSolver:
         ctx = self.prepare(J, residuals, w_pts, clamp_w)
         st = ctx['stream']
         if ctx['lay']['d'] > 0:
-            check(lib().ba_linearize_schur(ctx['args'], st))
+            if ctx['path'] == 'pairmajor':
+                check(lib().ba_pm_linearize_schur(ctx['args'], st))
+            else:
+                check(lib().ba_linearize_schur(ctx['args'], st))
         else:
             ctx['S_pairs'].zero_(); ctx['e_img'].zero_(); ctx['dg_img'].zero_()
         if z_prior is not None:
@@ -240,8 +249,22 @@ class GaussNewtonSolver:
         hasK, hasP, hasZ = en['K'][0], en['P'][0], en['Z'][0]
         d = 2 * hasK + 6 * hasP + C * hasZ
         lay = dict(d=d, hasK=hasK, hasP=hasP, hasZ=hasZ)
-        plan = get_plan(J.rigs, J.pids, self.tracks.true_n, device=dev, **self.plan_options)
+        plan = None
+        if self.path == 'pairmajor' or d > 15:
+            return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
+        try:
+            plan = get_plan(J.rigs, J.pids, self.tracks.true_n, device=dev, **self.plan_options)
+        except RuntimeError as e:
+            # the batched planner's limits (a track longer than a chunk or spanning more images than a
+            # batch holds): the pair-major path has none
+            if self.path == 'batched' or 'track' not in str(e):
+                raise
+            return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         sc = plan.scalars
+        if self.path == 'auto' and sc['n_chunks'] >= 256 and sc['n_batches'] * 2 > sc['n_chunks']:
+            # batches that hardly share image pairs (random co-visibility): every chunk would write its
+            # own partial blocks; the pair-major path writes each pair block once
+            return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         T = self.tracks.true_n
         s_pix, s_std, s_dep = plan.slot_data(J.pix2d if J.pix2d is not None else J.pix2d_std, J.pix2d_std,
                                              J.pix2d_dep)
@@ -310,7 +333,79 @@ class GaussNewtonSolver:
             a.r_s0, a.r_s1 = residuals.stride(0), residuals.stride(1)
             a.w_s0, a.w_s1 = W.stride(0), W.stride(1)
         return dict(args=a, stream=stream_ptr(dev), lay=lay, plan=plan, S_pairs=S_pairs, e_img=e_img, dg_img=dg_img,
-                    Hpp=Hpp, gp=gp, lam_p=lam_p, keep=(s_pix, s_std, s_dep, W, residuals))
+                    Hpp=Hpp, gp=gp, lam_p=lam_p, keep=(s_pix, s_std, s_dep, W, residuals), path='batched')
+
+    def _layout_args(self, L_, J, lay, clamp_w):
+        C = self.n_zcf
+        en = J.en
+        L_.d, L_.C = lay['d'], C
+        L_.off_tau, L_.off_zcf = 2 * lay['hasK'], 2 * lay['hasK'] + 6 * lay['hasP']
+        L_.hasK, L_.hasP, L_.hasZ = int(lay['hasK']), int(lay['hasP']), int(lay['hasZ'])
+        L_.no_grad_f_from_rz = int(bool(self.no_grad_f_from_rz))
+        L_.optim_Z0, L_.optim_Z_1st_cam = int(J.optim_Z0), int(J.optim_Z_1st_cam)
+        L_.wmin, L_.wmax = float(clamp_w[0]), float(clamp_w[1])
+        L_.dampen = float(self.dampen)
+        L_.adaptive = int(bool(self.adaptive_dampen))
+        L_.x_off = int(not en['X'][0])
+
+    @staticmethod
+    def _huber_args(h, J):
+        hp = J.hp or {}
+        h.weight_z = float(hp.get('weight_z', 1.0))
+        h.pnorm = float(hp.get('pnorm', 1.0))
+        h.max_pix_err = float(hp.get('max_pix_err', 100.0))
+        h.huber_delta = float(hp.get('huber_delta', 0.5))
+        h.w_pts_null = float(hp.get('w_pts_null', 1e-16))
+        h.is_depth_log = int(J.is_depth_log)
+
+    def _prepare_pm(self, J, residuals, w_pts, clamp_w, lay):
+        """Plan, workspaces and the ba_pm_args of one pair-major linearisation (no kernel launched)."""
+        dev = self.device
+        d = lay['d']
+        if d > 32:
+            raise ValueError(f'{d} image-level parameters: the reduced system supports at most 32')
+        plan = get_plan(J.rigs, J.pids, self.tracks.true_n, kind='pairmajor', device=dev)
+        sc, pd, ws = plan.scalars, plan.dev, plan.workspace
+        T = self.tracks.true_n
+        n_imgs = self.imgs.true_n
+        n_obs = int(J.pids.shape[0])
+        dp = 16 if d <= 16 else 32
+        dd = max(d, 1)
+        a = _lib.BaPmArgs()
+        a.infos = ptr(J.rigs.contiguous())
+        a.n_imgs, a.n_tracks = n_imgs, T
+        for name in ('run_ptr', 'run_obs', 'run_trk', 'run_img', 'img_run_ptr', 'trk_run_ptr', 'trk_run',
+                     'trk_obs_ptr', 'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'diag_pair', 'term_ptr', 'term'):
+            setattr(a, name, ptr(pd[name]))
+        a.n_obs, a.n_runs, a.n_pairs = n_obs, sc['n_runs'], sc['n_pairs']
+        pix = J.pix2d if J.pix2d is not None else J.pix2d_std
+        a.pids, a.pix2d, a.pix2d_std, a.pix2d_dep = ptr(J.pids), ptr(pix), ptr(J.pix2d_std), ptr(J.pix2d_dep)
+        a.K, a.P_rig2cam, a.P_rig2cam_stride = ptr(J.K), ptr(J.P_rig2cam), J.P_rig2cam.stride(0)
+        a.P_w2rig, a.z_coefs, a.pts3d = ptr(J.P_w2rig), ptr(J.z_coefs), ptr(J.pts3d)
+        en = J.en
+        a.enK, a.enP, a.enZ, a.enX = (ptr(en[k][1]) for k in ('K', 'P', 'Z', 'X'))
+        self._huber_args(a.hp, J)
+        self._layout_args(a.lay, J, lay, clamp_w)
+        Hpp = ws('Hpp', (max(T, 1), 6), torch.float64)
+        gp = ws('gp', (max(T, 1), 3), torch.float64)
+        lam_p = ws('lam_p', (1,), torch.float64)
+        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), torch.float64)
+        e_img = ws('e_img', (n_imgs, dd), torch.float64)
+        dg_img = ws('dg_img', (n_imgs, dd), torch.float64)
+        a.pobs = ptr(ws('pobs', (max(n_obs, 1), 9), torch.float64))
+        a.Hpp, a.gp, a.lam_p = ptr(Hpp), ptr(gp), ptr(lam_p)
+        a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), torch.float64))
+        a.pfac = ptr(ws('pfac', (max(T, 1), 12), torch.float64))
+        a.V = ptr(ws('V', (max(sc['n_runs'], 1), 3, dp), torch.float64))
+        a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
+        W = w_pts.expand(-1, 3)
+        own = getattr(residuals, '_ba_state', None)
+        if own is None or own != _param_state(J) or J.pix2d is None:
+            a.r_in, a.w_in = ptr(residuals), ptr(W)
+            a.r_s0, a.r_s1 = residuals.stride(0), residuals.stride(1)
+            a.w_s0, a.w_s1 = W.stride(0), W.stride(1)
+        return dict(args=a, stream=stream_ptr(dev), lay=lay, plan=plan, S_pairs=S_pairs, e_img=e_img, dg_img=dg_img,
+                    Hpp=Hpp, gp=gp, lam_p=lam_p, keep=(W, residuals), path='pairmajor')
 
     def reduce_and_backsubstitute(self, J, ctx):
         """Device PCG on the reduced system and point back-substitution; returns fp32 delta."""
@@ -360,18 +455,22 @@ class GaussNewtonSolver:
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
         # back-substitution for the points
         dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
-        if en['X'][0] and sc['n_chunks'] > 0:
-            a.dc = ptr(x)
-            a.umap = ptr(um['umap'])
+        pm = ctx['path'] == 'pairmajor'
+        if en['X'][0] and (sc['n_runs'] > 0 if pm else sc['n_chunks'] > 0):
             if 'umap_pad' not in um:                   # -1 -> the appended zero, once per structure
                 um['umap_pad'] = torch.where(um['umap'] >= 0, um['umap'], x.numel()).long().view(-1)
             dc_img = torch.nn.functional.pad(x, (0, 1))[um['umap_pad']]
             a.dc_img = ptr(dc_img)                     # delta_c at image level (one load fewer per obs)
             a.dX = ptr(dX)
             a.dX64 = None
-            check(lib().ba_backsubstitute(a, st))
+            if pm:
+                check(lib().ba_pm_backsubstitute(a, st))
+            else:
+                a.dc = ptr(x)
+                a.umap = ptr(um['umap'])
+                check(lib().ba_backsubstitute(a, st))
         self.last.update(S_pairs=S_pairs, e_img=e_img, dg_img=dg_img, unknowns=um, lay=lay, plan=plan, x=x,
-                         istate=istate, Hpp=Hpp, gp=gp, lam_p=lam_p)
+                         istate=istate, Hpp=Hpp, gp=gp, lam_p=lam_p, path=ctx['path'])
         dc = x[:n_u].to(torch.float32)
         dXa = dX[:T]
         if en['X'][2] is not None:
@@ -391,7 +490,8 @@ class GaussNewtonSolver:
         n_blk = n_imgs * row_cap if row_cap else n_ent
         S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float64)
         pa.S_rows, pa.n_row_ent, pa.row_cap = ptr(S_rows), n_ent, row_cap
-        pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * 16,), torch.int32))
+        gw = 16 if d <= 16 else 32                     # row_u entries per block (the SpMV's lanes per group)
+        pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * gw,), torch.int32))
 
     def _run_direct(self, pa, plan, st, n_imgs, um):
         """ba_reduced_solve (L L^T of the damped reduced system, banded or dense).  Returns False, after
@@ -425,7 +525,7 @@ class GaussNewtonSolver:
         db = um['db']
         layout = self.cholesky_layout
         if layout == 'auto':
-            fits = db >= 1 and n_imgs >= 2 and (w + 1) * db <= 160 and ns <= 8 and \
+            fits = 1 <= db <= 16 and n_imgs >= 2 and (w + 1) * db <= 160 and ns <= 8 and \
                 int(L.ba_chol_band_lds_bytes(db, w, ns)) <= 160 * 1024
             layout = 'banded' if fits else 'dense'
         mode = 1 if layout == 'banded' else 0
@@ -519,8 +619,10 @@ class GaussNewtonSolver:
         (the device keeps them in chunk-track order); tracks without observations hold zeros."""
         last = self.last
         plan = last['plan']
-        n_ct = plan.scalars['n_ctracks']
         T = self.tracks.true_n
+        if last.get('path') == 'pairmajor':         # kept in track order
+            return last['Hpp'][:T].clone(), last['gp'][:T].clone()
+        n_ct = plan.scalars['n_ctracks']
         pid = plan.dev['ct_pid'][:n_ct].long()
         H = torch.zeros((T, 6), dtype=torch.float64, device=self.device)
         g = torch.zeros((T, 3), dtype=torch.float64, device=self.device)

@@ -782,7 +782,7 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     const ba_pcg_args& a = *args;
     const ba_chol_args& ca = *cargs;
     hipStream_t st = (hipStream_t)stream;
-    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16, "ba_reduced_solve: bad sizes");
+    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 32, "ba_reduced_solve: bad sizes (1 <= d <= 32)");
     if (a.n_u == 0) return BA_OK;
     {
         const void* need[] = {a.umap, a.inv_ptr, a.inv_src, a.leaf, a.S_pairs, a.e_img, a.dg_img, a.rhs, a.diagA,
@@ -802,8 +802,8 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     hipLaunchKernelGGL(k_info_init, dim3(1), dim3(64), 0, st, c.info);
     const unsigned nbu = (unsigned)((a.n_u + CH_T - 1) / CH_T);
     if (ca.mode == 1) {
-        BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.bcol != nullptr && ca.bpos != nullptr,
-                   "ba_reduced_solve: banded layout needs db, bcol, bpos");
+        BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.db <= CB_MAXD && ca.bcol != nullptr && ca.bpos != nullptr,
+                   "ba_reduced_solve: the banded layout needs db <= 16, bcol, bpos");
         const int d = ca.db, M = (ca.w + 1) * d;
         BA_REQUIRE(ca.w >= 0 && M <= CB_MAXM && ca.n_shared <= CB_MAXS,
                    "ba_reduced_solve: the banded layout needs (w + 1) d <= 160 and at most 8 shared unknowns");

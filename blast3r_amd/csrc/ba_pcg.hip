@@ -194,9 +194,9 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
 // Image-row copies of the pair blocks, column-major: entry q of image row i (pair p, flag tr) holds
 // B = S(i, i2) with B[j][j2] at S_rows[q][j2 * d + j], so that the SpMV's lanes (one per output
 // row j) read each column of a block contiguously.  S(i, i2) is S_p for tr = 0 and S_p^T for tr = 1.
-// row_u[q][j2] = umap[i2][j2] (-1 past d): the unknowns the block multiplies.  One thread per
-// (entry, element), max(d^2, 16) elements per entry.
-__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int per) {
+// row_u[q][j2] = umap[i2][j2] (-1 past d, gw entries per block: 16 for d <= 16, else 32): the unknowns
+// the block multiplies.  One thread per (entry, element), max(d^2, gw) elements per entry.
+__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int per, int gw) {
     const int d = a.d, dd = d * d;
     const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
     if (tid >= n_ent * per) return;
@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
         qs = a.row_ptr[i] + k;
         if (qs >= a.row_ptr[i + 1]) {                  // past the row's end: a zero block, no unknowns
             if (e < dd) a.S_rows[q * dd + e] = 0.0;
-            if (e < 16) a.row_u[q * 16 + e] = -1;
+            if (e < gw) a.row_u[q * gw + e] = -1;
             return;
         }
     }
@@ -219,9 +219,9 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
         const double* S = a.S_pairs + p * dd;
         a.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
     }
-    if (e < 16) {
+    if (e < gw) {
         const int i2 = (ent & 1) ? a.pair_i1[p] : a.pair_i2[p];
-        a.row_u[q * 16 + e] = e < d ? a.umap[(int64_t)i2 * d + e] : -1;
+        a.row_u[q * gw + e] = e < d ? a.umap[(int64_t)i2 * d + e] : -1;
     }
 }
 
@@ -245,11 +245,12 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 // (PCG_ST / 16)-th block of the row.  Lane j2 of a group forms p_n at the block's column unknown j2 and the group shares the
 // 16 values by shuffles; the group sums are added in LDS in a fixed order.  The operands of the
 // first pass, the row's own unknowns and the partial sums are requested before any of them is used.
+template <int GW>
 __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int nb) {
     __shared__ double sh[PCG_ST];
     __shared__ double sDamp[PCG_ST / 64];
     const int i = blockIdx.x;
-    const int grp = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int grp = threadIdx.x / GW, j = threadIdx.x % GW;
     const int d = a.d, dd = d * d;
     const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
     // operands that depend on nothing are requested first: each thread's first block partials of
@@ -260,30 +261,30 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     const double bnorm = a.state[ST_BNORM];
     int uo = -1;
     double zo = 0.0, po = 0.0;
-    if (threadIdx.x < 16 && j < d) {
+    if (threadIdx.x < GW && j < d) {
         uo = a.umap[(int64_t)i * d + j];
         if (uo >= 0) { zo = a.z[uo]; po = pold[uo]; }
     }
     // the row's blocks: from the fixed capacity when set (no load on this chain), else from row_ptr
     const int q0 = a.row_cap > 0 ? i * a.row_cap : a.row_ptr[i];
     const int q1 = a.row_cap > 0 ? q0 + a.row_cap : a.row_ptr[i + 1];
-    auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[16]) {
+    auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[GW]) {
         const bool live = q < q1;
-        u = live ? a.row_u[(int64_t)q * 16 + j] : -1;
+        u = live ? a.row_u[(int64_t)q * GW + j] : -1;
         zv = 0.0; pv = 0.0;
         if (u >= 0) { zv = a.z[u]; pv = pold[u]; }
         const double* B = a.S_rows + (int64_t)q * dd;
 #pragma unroll
-        for (int j2 = 0; j2 < 16; ++j2) bcol[j2] = (live && j < d && j2 < d) ? B[j2 * d + j] : 0.0;
+        for (int j2 = 0; j2 < GW; ++j2) bcol[j2] = (live && j < d && j2 < d) ? B[j2 * d + j] : 0.0;
     };
-    auto mac = [&](int u, double zv, double pv, double beta, const double (&bcol)[16], double acc) {
+    auto mac = [&](int u, double zv, double pv, double beta, const double (&bcol)[GW], double acc) {
         const double xj = u >= 0 ? pdir(zv, pv, beta) : 0.0;
 #pragma unroll
-        for (int j2 = 0; j2 < 16; ++j2) acc += bcol[j2] * __shfl(xj, j2, 16);
+        for (int j2 = 0; j2 < GW; ++j2) acc += bcol[j2] * __shfl(xj, j2, GW);
         return acc;
     };
     int u;
-    double zv, pv, bcol[16];
+    double zv, pv, bcol[GW];
     load(q0 + grp, u, zv, pv, bcol);                 // requested before the done flag is known
     // damping term of the unknowns v = i + k n_imgs (thread k): its first operands are requested now
     const int64_t v0 = i + (int64_t)threadIdx.x * a.n_imgs;
@@ -335,7 +336,7 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
         dsum = wave_sum(dsum);
     }
     double acc = mac(u, zv, pv, beta, bcol, 0.0);
-    for (int qb = q0 + PCG_ST / 16; qb < q1; qb += PCG_ST / 16) {     // the row's further blocks
+    for (int qb = q0 + PCG_ST / GW; qb < q1; qb += PCG_ST / GW) {     // the row's further blocks
         load(qb + grp, u, zv, pv, bcol);
         acc = mac(u, zv, pv, beta, bcol, acc);
     }
@@ -347,9 +348,9 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     // 16 rows at most) plus the damping sum of its unknowns
     if (threadIdx.x < 64) {
         double part = 0.0;
-        if (j < d && threadIdx.x < 16) {
+        if (j < d && threadIdx.x < GW) {
             double t = 0.0;
-            for (int g = 0; g < PCG_ST / 16; ++g) t += sh[16 * g + j];
+            for (int g = 0; g < PCG_ST / GW; ++g) t += sh[GW * g + j];
             a.y_img[(int64_t)i * d + j] = t;
             if (uo >= 0) part = pdir(zo, po, beta) * t;
         }
@@ -482,7 +483,7 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(args != nullptr, "null args");
     const ba_pcg_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
-    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 16 && a.maxiter >= 0, "bad sizes");
+    BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 32 && a.maxiter >= 0, "bad sizes (1 <= d <= 32)");
     BA_REQUIRE(a.n_long >= 0 && a.n_long <= a.n_u && a.long_ptr != nullptr && a.long_idx != nullptr &&
                    (a.n_long == 0 || a.long_u != nullptr) && a.img_part != nullptr,
                "bad long-list unknowns or image partials");
@@ -498,22 +499,27 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(a.row_cap >= 0 && a.row_cap % (PCG_ST / 16) == 0, "row_cap must be a multiple of 8");
     const int64_t n_ent = a.row_cap > 0 ? (int64_t)a.n_imgs * a.row_cap : a.n_row_ent;
     BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
-    const int per = a.d * a.d > 16 ? a.d * a.d : 16;
+    const int gw = a.d <= 16 ? 16 : 32;               // lanes per block row group of the SpMV (row_u stride)
+    const int per = a.d * a.d > gw ? a.d * a.d : gw;
     if (n_ent > 0)
         hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
-                           n_ent, per);
+                           n_ent, per, gw);
     hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
     hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
     BA_LAUNCHED();
+    auto spmv = [&](int it) {
+        if (gw == 16) hipLaunchKernelGGL(k_pcg_spmv<16>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+        else          hipLaunchKernelGGL(k_pcg_spmv<32>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+    };
     for (int it = 0; it < a.maxiter; ++it) {
-        hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+        spmv(it);
         hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, it);
     }
     // the decisions after the last update (no SpMV follows them)
-    hipLaunchKernelGGL(k_pcg_spmv, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, a.maxiter, (int)nb);
+    spmv(a.maxiter);
     hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);
     BA_LAUNCHED();
     return BA_OK;

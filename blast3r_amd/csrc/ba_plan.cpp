@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "ba_plan.h"
+#include "ba_hip.h"
 
 namespace ba {
 
@@ -58,6 +59,17 @@ static void parallel_for(int64_t n, F fn, int64_t min_per_thread = 65536) {
 }
 
 extern "C" const char* ba_plan_last_error(void) { return g_plan_err.c_str(); }
+
+extern "C" int64_t ba_abi_sizeof(const char* name) {
+    if (!name) return -1;
+    const std::string n(name);
+#define BA_SZ(T) if (n == #T) return (int64_t)sizeof(T)
+    BA_SZ(ba_huber); BA_SZ(ba_layout); BA_SZ(ba_lin_args); BA_SZ(ba_pm_args); BA_SZ(ba_pcg_args);
+    BA_SZ(ba_chol_args); BA_SZ(ba_sample_args); BA_SZ(ba_obs_set); BA_SZ(ba_gather_args); BA_SZ(ba_remove_args);
+    BA_SZ(ba_tangent_args);
+#undef BA_SZ
+    return -1;
+}
 
 extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
                                 int32_t n_tracks, int32_t max_local_imgs, int32_t max_slots, int64_t max_batch_obs) {
@@ -597,3 +609,217 @@ extern "C" int ba_plan_export(const void* plan, int32_t which, int32_t* dst) {
 }
 
 extern "C" void ba_plan_destroy(void* plan) { delete (Plan*)plan; }
+
+// ---------------------------------------------------------------------------- pair-major plan
+namespace ba {
+struct PmPlan {
+    std::vector<int32_t> v[BA_PM_NARRAYS];
+    int64_t scalars[BA_PM_NSCALARS] = {0};
+};
+}  // namespace ba
+
+extern "C" void* ba_pm_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
+                                   int32_t n_tracks) {
+    g_plan_err.clear();
+    if (n_imgs <= 0 || n_obs < 0 || n_tracks < 0) { g_plan_err = "bad sizes"; return nullptr; }
+    if (n_obs >= (int64_t)1 << 30) { g_plan_err = "more than 2^30 observations"; return nullptr; }
+    if ((int64_t)cum_nkpts[n_imgs - 1] != n_obs) { g_plan_err = "infos[0][-1] != number of observations"; return nullptr; }
+    for (int i = 1; i < n_imgs; ++i)
+        if (cum_nkpts[i] < cum_nkpts[i - 1]) { g_plan_err = "infos[0] must be non-decreasing"; return nullptr; }
+    for (int64_t o = 0; o < n_obs; ++o)
+        if (pids[o] < 0 || pids[o] >= n_tracks) { g_plan_err = "pid out of range"; return nullptr; }
+    PmPlan* P = new PmPlan();
+    auto& obs_img = P->v[BA_PM_OBS_IMG];
+    obs_img.assign(n_obs, 0);
+    auto obs0 = [&](int64_t i) -> int64_t { return i ? cum_nkpts[i - 1] : 0; };
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i)
+            for (int64_t o = obs0(i); o < cum_nkpts[i]; ++o) obs_img[o] = (int32_t)i;
+    }, 1);
+    // runs: per image, the observations grouped by track id (stable), one run per distinct track
+    auto& run_obs = P->v[BA_PM_RUN_OBS];
+    run_obs.resize(n_obs);
+    std::vector<int32_t> img_nruns(n_imgs, 0);
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i) {
+            const int64_t b = obs0(i), e = cum_nkpts[i];
+            std::iota(run_obs.begin() + b, run_obs.begin() + e, (int32_t)b);
+            std::stable_sort(run_obs.begin() + b, run_obs.begin() + e,
+                             [&](int32_t x, int32_t y) { return pids[x] < pids[y]; });
+            int32_t n = 0;
+            for (int64_t k = b; k < e; ++k)
+                if (k == b || pids[run_obs[k]] != pids[run_obs[k - 1]]) ++n;
+            img_nruns[i] = n;
+        }
+    }, 1);
+    auto& img_run_ptr = P->v[BA_PM_IMG_RUN_PTR];
+    img_run_ptr.assign(n_imgs + 1, 0);
+    for (int i = 0; i < n_imgs; ++i) img_run_ptr[i + 1] = img_run_ptr[i] + img_nruns[i];
+    const int64_t n_runs = img_run_ptr[n_imgs];
+    auto& run_ptr = P->v[BA_PM_RUN_PTR];
+    auto& run_trk = P->v[BA_PM_RUN_TRK];
+    auto& run_img = P->v[BA_PM_RUN_IMG];
+    run_ptr.assign(n_runs + 1, 0);
+    run_trk.assign(n_runs, 0);
+    run_img.assign(n_runs, 0);
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i) {
+            int64_t r = img_run_ptr[i];
+            const int64_t b = obs0(i), e = cum_nkpts[i];
+            for (int64_t k = b; k < e; ++k)
+                if (k == b || pids[run_obs[k]] != pids[run_obs[k - 1]]) {
+                    run_ptr[r] = (int32_t)k;
+                    run_trk[r] = pids[run_obs[k]];
+                    run_img[r] = (int32_t)i;
+                    ++r;
+                }
+        }
+    }, 1);
+    run_ptr[n_runs] = (int32_t)n_obs;
+    // runs and observations of each track in image order (runs are visited image by image)
+    auto& trk_run_ptr = P->v[BA_PM_TRK_RUN_PTR];
+    auto& trk_run = P->v[BA_PM_TRK_RUN];
+    auto& trk_obs_ptr = P->v[BA_PM_TRK_OBS_PTR];
+    auto& trk_obs = P->v[BA_PM_TRK_OBS];
+    trk_run_ptr.assign(n_tracks + 1, 0);
+    trk_obs_ptr.assign(n_tracks + 1, 0);
+    for (int64_t r = 0; r < n_runs; ++r) {
+        trk_run_ptr[run_trk[r] + 1]++;
+        trk_obs_ptr[run_trk[r] + 1] += run_ptr[r + 1] - run_ptr[r];
+    }
+    for (int t = 0; t < n_tracks; ++t) {
+        trk_run_ptr[t + 1] += trk_run_ptr[t];
+        trk_obs_ptr[t + 1] += trk_obs_ptr[t];
+    }
+    trk_run.assign(n_runs, 0);
+    trk_obs.assign(n_obs, 0);
+    {
+        std::vector<int32_t> fr(trk_run_ptr.begin(), trk_run_ptr.end() - 1), fo(trk_obs_ptr.begin(), trk_obs_ptr.end() - 1);
+        for (int64_t r = 0; r < n_runs; ++r) {
+            const int t = run_trk[r];
+            trk_run[fr[t]++] = (int32_t)r;
+            for (int k = run_ptr[r]; k < run_ptr[r + 1]; ++k) trk_obs[fo[t]++] = run_obs[k];
+        }
+    }
+    int64_t max_tr = 0;
+    for (int t = 0; t < n_tracks; ++t) max_tr = std::max<int64_t>(max_tr, trk_run_ptr[t + 1] - trk_run_ptr[t]);
+    // co-visible images after each image: for each run of image a, the later runs of its track
+    std::vector<std::vector<int32_t>> nb(n_imgs);
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t a = i0; a < i1; ++a) {
+            auto& L = nb[a];
+            for (int r = img_run_ptr[a]; r < img_run_ptr[a + 1]; ++r) {
+                const int t = run_trk[r];
+                for (int q = trk_run_ptr[t]; q < trk_run_ptr[t + 1]; ++q) {
+                    const int b = run_img[trk_run[q]];
+                    if (b > a) L.push_back(b);
+                }
+            }
+            std::sort(L.begin(), L.end());
+            L.erase(std::unique(L.begin(), L.end()), L.end());
+        }
+    }, 1);
+    // pairs: (a, a) for every image with runs, then (a, b) for b in nb[a]
+    std::vector<int64_t> pbase(n_imgs + 1, 0);
+    for (int a = 0; a < n_imgs; ++a)
+        pbase[a + 1] = pbase[a] + (img_nruns[a] > 0 ? 1 : 0) + (int64_t)nb[a].size();
+    const int64_t n_pairs = pbase[n_imgs];
+    if (n_pairs >= ((int64_t)1 << 30)) { g_plan_err = "too many image pairs"; delete P; return nullptr; }
+    auto& pair_i1 = P->v[BA_PM_PAIR_I1];
+    auto& pair_i2 = P->v[BA_PM_PAIR_I2];
+    auto& diag_pair = P->v[BA_PM_DIAG_PAIR];
+    pair_i1.assign(n_pairs, 0);
+    pair_i2.assign(n_pairs, 0);
+    diag_pair.assign(n_imgs, -1);
+    for (int a = 0; a < n_imgs; ++a) {
+        int64_t q = pbase[a];
+        if (img_nruns[a] > 0) { diag_pair[a] = (int32_t)q; pair_i1[q] = a; pair_i2[q] = a; ++q; }
+        for (int32_t b : nb[a]) { pair_i1[q] = a; pair_i2[q] = b; ++q; }
+    }
+    // terms of the off-diagonal pairs of row a, in run order of image a then track order
+    std::vector<int64_t> tcnt(n_pairs + 1, 0);
+    auto pair_of = [&](int a, int b) -> int64_t {
+        const auto& L = nb[a];
+        const int64_t k = std::lower_bound(L.begin(), L.end(), b) - L.begin();
+        return pbase[a] + (img_nruns[a] > 0 ? 1 : 0) + k;
+    };
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t a = i0; a < i1; ++a)
+            for (int r = img_run_ptr[a]; r < img_run_ptr[a + 1]; ++r) {
+                const int t = run_trk[r];
+                for (int q = trk_run_ptr[t]; q < trk_run_ptr[t + 1]; ++q) {
+                    const int b = run_img[trk_run[q]];
+                    if (b > a) tcnt[pair_of((int)a, b) + 1]++;
+                }
+            }
+    }, 1);
+    for (int64_t p = 0; p < n_pairs; ++p) tcnt[p + 1] += tcnt[p];
+    const int64_t n_terms = tcnt[n_pairs];
+    if (n_terms >= ((int64_t)1 << 30)) { g_plan_err = "too many pair terms"; delete P; return nullptr; }
+    auto& term_ptr = P->v[BA_PM_TERM_PTR];
+    auto& term = P->v[BA_PM_TERM];
+    term_ptr.assign(n_pairs + 1, 0);
+    for (int64_t p = 0; p <= n_pairs; ++p) term_ptr[p] = (int32_t)tcnt[p];
+    term.assign(2 * n_terms, 0);
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        std::vector<int64_t> fill;
+        for (int64_t a = i0; a < i1; ++a) {
+            const int64_t p0 = pbase[a], p1 = pbase[a + 1];
+            fill.assign(tcnt.begin() + p0, tcnt.begin() + p1);
+            for (int r = img_run_ptr[a]; r < img_run_ptr[a + 1]; ++r) {
+                const int t = run_trk[r];
+                for (int q = trk_run_ptr[t]; q < trk_run_ptr[t + 1]; ++q) {
+                    const int rb = trk_run[q], b = run_img[rb];
+                    if (b > a) {
+                        const int64_t k = fill[pair_of((int)a, b) - p0]++;
+                        term[2 * k] = r;
+                        term[2 * k + 1] = rb;
+                    }
+                }
+            }
+        }
+    }, 1);
+    int64_t max_terms = 0;
+    for (int64_t p = 0; p < n_pairs; ++p) max_terms = std::max<int64_t>(max_terms, tcnt[p + 1] - tcnt[p]);
+    // image rows of the symmetric pair structure, as in the batched plan
+    auto& row_ptr = P->v[BA_PM_ROW_PTR];
+    auto& row_ent = P->v[BA_PM_ROW_ENT];
+    {
+        std::vector<int32_t> cnt(n_imgs + 1, 0);
+        for (int64_t p = 0; p < n_pairs; ++p) {
+            cnt[pair_i1[p] + 1]++;
+            if (pair_i2[p] != pair_i1[p]) cnt[pair_i2[p] + 1]++;
+        }
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        row_ptr.assign(cnt.begin(), cnt.end());
+        row_ent.assign(cnt[n_imgs], 0);
+        std::vector<int32_t> fill(cnt.begin(), cnt.end() - 1);
+        for (int64_t p = 0; p < n_pairs; ++p) {
+            row_ent[fill[pair_i1[p]]++] = (int32_t)(p << 1);
+            if (pair_i2[p] != pair_i1[p]) row_ent[fill[pair_i2[p]]++] = (int32_t)((p << 1) | 1);
+        }
+    }
+    P->scalars[BA_PMS_N_RUNS] = n_runs;
+    P->scalars[BA_PMS_N_PAIRS] = n_pairs;
+    P->scalars[BA_PMS_N_TERMS] = n_terms;
+    P->scalars[BA_PMS_MAX_TERMS] = max_terms;
+    P->scalars[BA_PMS_MAX_TRACK_RUNS] = max_tr;
+    return P;
+}
+
+extern "C" int ba_pm_plan_query(const void* plan, int64_t* scalars, int64_t* array_sizes) {
+    const PmPlan* P = (const PmPlan*)plan;
+    if (!P) return 1;
+    for (int k = 0; k < BA_PM_NSCALARS; ++k) scalars[k] = P->scalars[k];
+    for (int k = 0; k < BA_PM_NARRAYS; ++k) array_sizes[k] = (int64_t)P->v[k].size();
+    return 0;
+}
+
+extern "C" int ba_pm_plan_export(const void* plan, int32_t which, int32_t* dst) {
+    const PmPlan* P = (const PmPlan*)plan;
+    if (!P || which < 0 || which >= BA_PM_NARRAYS) return 1;
+    if (!P->v[which].empty()) std::memcpy(dst, P->v[which].data(), P->v[which].size() * sizeof(int32_t));
+    return 0;
+}
+
+extern "C" void ba_pm_plan_destroy(void* plan) { delete (PmPlan*)plan; }

@@ -64,3 +64,29 @@ enum {
     BA_PS_N_PAIR_TERMS,
     BA_PLAN_NSCALARS
 };
+
+// ---------------------------------------------------------------------------- pair-major plan
+// Structure of the pair-major linearize + Schur path (no chunks or batches, so no limit on track
+// length, image-level width up to 32 or co-visibility pattern).  A run is the set of observations of
+// one track in one image; runs are numbered image by image, by track id within an image.
+enum {
+    BA_PM_RUN_PTR = 0,      // (n_runs + 1): run r's observations are run_obs[run_ptr[r] .. run_ptr[r + 1])
+    BA_PM_RUN_OBS,          // (n_obs): observation ids grouped by run (the identity when an image's rows are pid-sorted)
+    BA_PM_RUN_TRK,          // (n_runs): track of run r
+    BA_PM_RUN_IMG,          // (n_runs): image of run r
+    BA_PM_IMG_RUN_PTR,      // (n_imgs + 1): runs of image i are img_run_ptr[i] .. img_run_ptr[i + 1]
+    BA_PM_TRK_RUN_PTR,      // (n_tracks + 1)
+    BA_PM_TRK_RUN,          // (n_runs): runs of each track in image order
+    BA_PM_TRK_OBS_PTR,      // (n_tracks + 1)
+    BA_PM_TRK_OBS,          // (n_obs): observations of each track in image order
+    BA_PM_OBS_IMG,          // (n_obs): image of each observation
+    BA_PM_PAIR_I1,          // (n_pairs): image pairs (i1 <= i2) ordered by (i1, i2): the diagonal pair of every
+    BA_PM_PAIR_I2,          //   image with observations and every co-visible pair
+    BA_PM_ROW_PTR,          // (n_imgs + 1) image rows of the pair structure, as the batched plan's
+    BA_PM_ROW_ENT,          // (pair << 1) | transposed
+    BA_PM_DIAG_PAIR,        // (n_imgs): pair id of (i, i), or -1
+    BA_PM_TERM_PTR,         // (n_pairs + 1): terms of off-diagonal pair p (none for a diagonal pair)
+    BA_PM_TERM,             // (2 n_terms): (run in i1, run in i2) of one track, per term
+    BA_PM_NARRAYS
+};
+enum { BA_PMS_N_RUNS = 0, BA_PMS_N_PAIRS, BA_PMS_N_TERMS, BA_PMS_MAX_TERMS, BA_PMS_MAX_TRACK_RUNS, BA_PM_NSCALARS };

@@ -1018,3 +1018,427 @@ extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
     BA_LAUNCHED();
     return BA_OK;
 }
+
+// ============================================================================= pair-major path
+// The reduced system built per run, per image and per image pair instead of per chunk batch (no
+// limit on track length, up to 32 image-level parameters, any co-visibility), over the plan of
+// ba_pm_plan_create.  Every sum runs in a fixed order, so the result does not depend on scheduling.
+namespace ba {
+
+#define PM_T 256
+#define PM_OB 64            // observations (or runs) staged per round of k_pm_image: 3 rows each
+
+typedef ba_pm_args PmArgs;
+
+__device__ __forceinline__ void pm_ctx(const PmArgs& a, int img, ObsCtx& c) {
+    const int node = a.infos[a.n_imgs + img];
+    const int cam = a.infos[2 * a.n_imgs + img];
+    load_cam(c.cp, a.K, a.P_rig2cam, a.P_rig2cam_stride, a.P_w2rig, cam, node);
+    c.zc = a.z_coefs + (int64_t)img * a.lay.C;
+    c.enK = a.enK ? a.enK[cam] != 0 : true;
+    c.enP = a.enP ? a.enP[node] != 0 : true;
+    c.enZ = a.enZ ? a.enZ[img] != 0 : true;
+}
+
+// linearisation of observation o (residual or the caller's, weights, Jacobian core)
+__device__ __forceinline__ void pm_core(const PmArgs& a, int o, const ObsCtx& c, ObsCore& oc, DepSrc& dep,
+                                        bool& xon) {
+    const int pid = a.pids[o];
+    float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
+    const float2 uv = reinterpret_cast<const float2*>(a.pix2d)[o];
+    const float2 sv = reinterpret_cast<const float2*>(a.pix2d_std)[o];
+    load_dep(dep, a.pix2d_dep + (int64_t)o * a.lay.C, a.lay.C);
+    GivenRW grw = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
+    if (a.r_in) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            grw.r[k] = a.r_in[(int64_t)o * a.r_s0 + k * a.r_s1];
+            grw.w[k] = a.w_in[(int64_t)o * a.w_s0 + k * a.w_s1];
+        }
+    }
+    obs_core(c.cp, c.zc, X, uv, sv, dep, a.hp, a.lay, a.r_in != nullptr, grw, oc);
+    xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
+}
+
+// per observation: J_p^T J_p (upper 6) and J_p^T W r (3)
+__global__ void __launch_bounds__(PM_T) k_pm_obs(PmArgs a) {
+    const int64_t o = (int64_t)blockIdx.x * PM_T + threadIdx.x;
+    if (o >= a.n_obs) return;
+    ObsCtx c;
+    pm_ctx(a, a.obs_img[o], c);
+    ObsCore oc;
+    DepSrc dep;
+    bool xon;
+    pm_core(a, (int)o, c, oc, dep, xon);
+    double Jp[3][3], gP[3];
+    point_rows<true>(oc, c.cp, xon, Jp, gP);
+    const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
+    double* q = a.pobs + 9 * o;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const int i = pr[k][0], j = pr[k][1];
+        q[k] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
+    }
+    q[6] = gP[0]; q[7] = gP[1]; q[8] = gP[2];
+}
+
+// per track: H_pp and g_p summed over its observations in image order; the block's largest diagonal
+__global__ void __launch_bounds__(PM_T) k_pm_track(PmArgs a) {
+    __shared__ double sm[PM_T];
+    const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
+    double m = 0.0;
+    if (t < a.n_tracks) {
+        double h[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) h[k] = 0.0;
+        for (int q = a.trk_obs_ptr[t]; q < a.trk_obs_ptr[t + 1]; ++q) {
+            const double* s = a.pobs + 9 * (int64_t)a.trk_obs[q];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) h[k] += s[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 6; ++k) a.Hpp[6 * t + k] = h[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) a.gp[3 * t + k] = h[6 + k];
+        m = fmax(fabs(h[0]), fmax(fabs(h[3]), fabs(h[5])));
+    }
+    sm[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = PM_T / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) sm[threadIdx.x] = fmax(sm[threadIdx.x], sm[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) a.tmax[blockIdx.x] = sm[0];
+}
+
+// per run (track t, image i), columns [16 H, 16 H + 16): U = sum over the run's observations of
+// J_c^T J_p (weighted rows), V = U L^-T (forward substitution of each row against L)
+template <int HK, int HP, int H>
+__global__ void __launch_bounds__(PM_T) k_pm_runs(PmArgs a, int dp) {
+    const int64_t r = (int64_t)blockIdx.x * PM_T + threadIdx.x;
+    if (r >= a.n_runs) return;
+    const int t = a.run_trk[r];
+    ObsCtx c;
+    pm_ctx(a, a.run_img[r], c);
+    double U[16][3];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) U[j][k] = 0.0;
+    for (int q = a.run_ptr[r]; q < a.run_ptr[r + 1]; ++q) {
+        const int o = a.run_obs[q];
+        ObsCore oc;
+        DepSrc dep;
+        bool xon;
+        pm_core(a, o, c, oc, dep, xon);
+        double Jp[3][3], gP[3];
+        point_rows<false>(oc, c.cp, xon, Jp, gP);
+        const bool first = o == 0;
+        emit_jc_row<HK, HP, 0, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[0][k];
+        });
+        emit_jc_row<HK, HP, 1, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[1][k];
+        });
+        emit_jc_row<HK, HP, 2, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[2][k];
+        });
+    }
+    const double* pf = a.pfac + 12 * (int64_t)t;
+    const double L1 = pf[1], L2 = pf[2], L4 = pf[4], r0 = pf[9], r1 = pf[10], r2 = pf[11];
+    double* Vr = a.V + r * 3 * dp + 16 * H;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const double v0 = U[j][0] * r0;
+        const double v1 = (U[j][1] - L1 * v0) * r1;
+        const double v2 = (U[j][2] - L2 * v0 - L4 * v1) * r2;
+        Vr[j] = v0; Vr[dp + j] = v1; Vr[2 * dp + j] = v2;
+    }
+}
+
+// per image i (one workgroup): S_ii = sum_o J_c^T J_c - sum_t V_ti V_ti^T, rhs_i = sum_o J_c^T W r -
+// sum_t V_ti (L_t^-1 g_p,t), diag(H_cc)_i = sum_o |J_c|^2 by columns.  The rows are staged in LDS
+// (PM_OB observations or runs, three rows each, per round); the four waves take every fourth group of
+// four rows into v_mfma_f64_16x16x4f64 tiles (the lower tiles of a DP x DP block), then the wave
+// partials are added in wave order.
+template <int HK, int HP, int DP>
+__global__ void __launch_bounds__(PM_T) k_pm_image(PmArgs a) {
+    constexpr int NR = 3 * PM_OB, NT = DP / 16, NTL = NT * (NT + 1) / 2;
+    __shared__ double X[NR][DP + 1];
+    __shared__ double bv[NR];
+    const int i = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int d = a.lay.d;
+    const int o0 = i ? a.infos[i - 1] : 0, o1 = a.infos[i];
+    const int r0 = a.img_run_ptr[i], r1 = a.img_run_ptr[i + 1];
+    dbl4 acc[NTL];
+#pragma unroll
+    for (int q = 0; q < NTL; ++q) acc[q] = (dbl4){0.0, 0.0, 0.0, 0.0};
+    double e_acc = 0.0, g_acc = 0.0;
+    ObsCtx c;
+    pm_ctx(a, i, c);
+    const int nro = (o1 - o0 + PM_OB - 1) / PM_OB, nrr = (r1 - r0 + PM_OB - 1) / PM_OB;
+    for (int round = 0; round < nro + nrr; ++round) {
+        const bool vrows = round >= nro;
+        if (t < PM_OB) {
+            if (!vrows) {
+                const int o = o0 + round * PM_OB + t;
+                if (o < o1) {
+                    ObsCore oc;
+                    DepSrc dep;
+                    bool xon;
+                    pm_core(a, o, c, oc, dep, xon);
+                    const bool first = o == 0;
+                    emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * t][j] = v; });
+                    emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * t + 1][j] = v; });
+                    emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * t + 2][j] = v; });
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) bv[3 * t + k] = oc.Rs[k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) {
+                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = 0.0;
+                        bv[3 * t + k] = 0.0;
+                    }
+                }
+            } else {
+                const int r = r0 + (round - nro) * PM_OB + t;
+                if (r < r1) {
+                    const double* Vr = a.V + (int64_t)r * 3 * DP;
+                    const double* pf = a.pfac + 12 * (int64_t)a.run_trk[r];
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) {
+                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = Vr[k * DP + j];
+                        bv[3 * t + k] = pf[6 + k];
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) {
+                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = 0.0;
+                        bv[3 * t + k] = 0.0;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const double sg = vrows ? -1.0 : 1.0;
+        for (int kk = wave; kk < NR / 4; kk += PM_T / 64) {
+            const int row = 4 * kk + (lane >> 4), col = lane & 15;
+            double av[NT], bw[NT];
+#pragma unroll
+            for (int h = 0; h < NT; ++h) { av[h] = sg * X[row][16 * h + col]; bw[h] = X[row][16 * h + col]; }
+            int q = 0;
+#pragma unroll
+            for (int hi = 0; hi < NT; ++hi)
+#pragma unroll
+                for (int hj = 0; hj <= hi; ++hj) {
+                    acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[hi], bw[hj], acc[q], 0, 0, 0);
+                    ++q;
+                }
+        }
+        if (t < DP) {
+            for (int row = 0; row < NR; ++row) {
+                const double x = X[row][t];
+                e_acc += sg * x * bv[row];
+                if (!vrows) g_acc += x * x;
+            }
+        }
+        __syncthreads();
+    }
+    // wave partials -> LDS (over X), summed in wave order
+    double* part = &X[0][0];
+    constexpr int TS = 256;                          // doubles per 16 x 16 tile
+#pragma unroll
+    for (int q = 0; q < NTL; ++q)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[(wave * NTL + q) * TS + (4 * v + (lane >> 4)) * 16 + (lane & 15)] = acc[q][v];
+    __syncthreads();
+    const int pd = a.diag_pair[i];
+    if (pd >= 0) {
+        double* S = a.S_pairs + (int64_t)pd * d * d;
+        for (int e = t; e < NTL * TS; e += PM_T) {
+            const int q = e / TS, w = e - q * TS, ri = w >> 4, cj = w & 15;
+            int hi = 0, hj = 0, qq = 0;
+#pragma unroll
+            for (int x = 0; x < NT; ++x)
+#pragma unroll
+                for (int y = 0; y <= x; ++y) { if (qq == q) { hi = x; hj = y; } ++qq; }
+            double s = 0.0;
+#pragma unroll
+            for (int wv = 0; wv < PM_T / 64; ++wv) s += part[(wv * NTL + q) * TS + w];
+            const int rr = 16 * hi + ri, cc = 16 * hj + cj;
+            if (rr < d && cc < d && (hi != hj || cc <= rr)) {
+                S[rr * d + cc] = s;
+                S[cc * d + rr] = s;
+            }
+        }
+    }
+    if (t < d) {
+        a.e_img[(int64_t)i * d + t] = e_acc;
+        a.dg_img[(int64_t)i * d + t] = g_acc;
+    }
+}
+
+// per off-diagonal image pair (one wave): S_ij = - sum over the pair's terms of V_ti V_tj^T; the
+// operands of the next term are requested before this term's MFMAs
+template <int DP>
+__global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
+    constexpr int NT = DP / 16;
+    const int lane = threadIdx.x & 63;
+    const int64_t p = (int64_t)blockIdx.x * (PM_T / 64) + (threadIdx.x >> 6);
+    if (p >= a.n_pairs) return;
+    const int i1 = a.pair_i1[p], i2 = a.pair_i2[p];
+    if (i1 == i2) return;
+    const int d = a.lay.d;
+    const int k = lane >> 4, c = lane & 15;
+    dbl4 acc[NT][NT];
+#pragma unroll
+    for (int x = 0; x < NT; ++x)
+#pragma unroll
+        for (int y = 0; y < NT; ++y) acc[x][y] = (dbl4){0.0, 0.0, 0.0, 0.0};
+    const int q0 = a.term_ptr[p], q1 = a.term_ptr[p + 1];
+    auto load = [&](int q, double (&A)[NT], double (&B)[NT]) {
+        const int ra = a.term[2 * (int64_t)q], rb = a.term[2 * (int64_t)q + 1];
+#pragma unroll
+        for (int h = 0; h < NT; ++h) {
+            A[h] = k < 3 ? a.V[(int64_t)ra * 3 * DP + k * DP + 16 * h + c] : 0.0;
+            B[h] = k < 3 ? a.V[(int64_t)rb * 3 * DP + k * DP + 16 * h + c] : 0.0;
+        }
+    };
+    double A[NT], B[NT], An[NT], Bn[NT];
+    if (q0 < q1) load(q0, A, B);
+    for (int q = q0; q < q1; ++q) {
+        if (q + 1 < q1) load(q + 1, An, Bn);
+#pragma unroll
+        for (int x = 0; x < NT; ++x)
+#pragma unroll
+            for (int y = 0; y < NT; ++y) acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[x], B[y], acc[x][y], 0, 0, 0);
+#pragma unroll
+        for (int h = 0; h < NT; ++h) { A[h] = An[h]; B[h] = Bn[h]; }
+    }
+    double* S = a.S_pairs + p * d * d;
+#pragma unroll
+    for (int x = 0; x < NT; ++x)
+#pragma unroll
+        for (int y = 0; y < NT; ++y)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int rr = 16 * x + 4 * v + (lane >> 4), cc = 16 * y + (lane & 15);
+                if (rr < d && cc < d) S[rr * d + cc] = -acc[x][y][v];
+            }
+}
+
+// per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i))
+template <int DP>
+__global__ void __launch_bounds__(PM_T) k_pm_backsub(PmArgs a) {
+    const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
+    if (t >= a.n_tracks) return;
+    const int d = a.lay.d;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0;
+    for (int q = a.trk_run_ptr[t]; q < a.trk_run_ptr[t + 1]; ++q) {
+        const int r = a.trk_run[q];
+        const double* Vr = a.V + (int64_t)r * 3 * DP;
+        const double* dc = a.dc_img + (int64_t)a.run_img[r] * d;
+        for (int j = 0; j < d; ++j) {
+            const double x = dc[j];
+            s0 += Vr[j] * x; s1 += Vr[DP + j] * x; s2 += Vr[2 * DP + j] * x;
+        }
+    }
+    const double* pf = a.pfac + 12 * t;
+    const double z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
+    const double x2 = z2 * pf[11];
+    const double x1 = (z1 - pf[4] * x2) * pf[10];
+    const double x0 = (z0 - pf[1] * x1 - pf[2] * x2) * pf[9];
+    a.dX[3 * t] = (float)x0; a.dX[3 * t + 1] = (float)x1; a.dX[3 * t + 2] = (float)x2;
+    if (a.dX64) { a.dX64[3 * t] = x0; a.dX64[3 * t + 1] = x1; a.dX64[3 * t + 2] = x2; }
+}
+
+static const char* pm_missing(const ba_pm_args& a, bool backsub) {
+#define BA_NEED(cond, p) do { if ((cond) && (p) == nullptr) return "null pointer " #p; } while (0)
+    const bool C = a.lay.C > 0;
+    BA_NEED(true, a.trk_run_ptr); BA_NEED(true, a.trk_run); BA_NEED(true, a.run_img); BA_NEED(true, a.V);
+    BA_NEED(true, a.pfac);
+    BA_NEED(backsub, a.dc_img); BA_NEED(backsub, a.dX);
+    if (backsub) return nullptr;
+    BA_NEED(true, a.infos); BA_NEED(true, a.run_ptr); BA_NEED(true, a.run_obs); BA_NEED(true, a.run_trk);
+    BA_NEED(true, a.img_run_ptr); BA_NEED(true, a.trk_obs_ptr); BA_NEED(true, a.trk_obs); BA_NEED(true, a.obs_img);
+    BA_NEED(true, a.pair_i1); BA_NEED(true, a.pair_i2); BA_NEED(true, a.diag_pair); BA_NEED(true, a.term_ptr);
+    BA_NEED(true, a.term); BA_NEED(true, a.pids); BA_NEED(true, a.pix2d); BA_NEED(true, a.pix2d_std);
+    BA_NEED(C, a.pix2d_dep); BA_NEED(true, a.K); BA_NEED(true, a.P_rig2cam); BA_NEED(true, a.P_w2rig);
+    BA_NEED(C, a.z_coefs); BA_NEED(true, a.pts3d); BA_NEED(a.r_in != nullptr, a.w_in);
+    BA_NEED(true, a.pobs); BA_NEED(true, a.Hpp); BA_NEED(true, a.gp); BA_NEED(true, a.tmax); BA_NEED(true, a.lam_p);
+    BA_NEED(true, a.S_pairs); BA_NEED(true, a.e_img); BA_NEED(true, a.dg_img);
+#undef BA_NEED
+    return nullptr;
+}
+
+}  // namespace ba
+
+extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
+    clear_error();
+    BA_REQUIRE(args != nullptr, "null args");
+    const ba_pm_args& a = *args;
+    hipStream_t st = (hipStream_t)stream;
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 32, "pair-major path supports 1 <= d <= 32 image-level parameters");
+    BA_REQUIRE(a.lay.off_tau == 2 * a.lay.hasK && a.lay.off_zcf == a.lay.off_tau + 6 * a.lay.hasP &&
+                   a.lay.d == a.lay.off_zcf + (a.lay.hasZ ? a.lay.C : 0),
+               "inconsistent image-level layout");
+    BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "at most 24 z-coefficient columns");
+    BA_REQUIRE(a.n_imgs >= 1 && a.n_tracks >= 0 && a.n_obs >= 0 && a.n_runs >= 0 && a.n_pairs >= 0, "bad sizes");
+    const char* miss = pm_missing(a, false);
+    BA_REQUIRE(miss == nullptr, miss);
+    BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
+    const int64_t nbt = (a.n_tracks + PM_T - 1) / PM_T;
+    hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.tmax, nbt);
+    if (a.n_obs > 0) hipLaunchKernelGGL(k_pm_obs, dim3(nblk(a.n_obs, PM_T)), dim3(PM_T), 0, st, a);
+    if (a.n_tracks > 0) {
+        hipLaunchKernelGGL(k_pm_track, dim3((unsigned)nbt), dim3(PM_T), 0, st, a);
+        const int64_t nb = nbt < 256 * 256 ? (nbt + 255) / 256 : 256;
+        hipLaunchKernelGGL(k_lam_reduce, dim3((unsigned)nb), dim3(256), 0, st, a.tmax, nbt);
+    }
+    hipLaunchKernelGGL(k_lam_final, dim3(1), dim3(1), 0, st, a.tmax, nbt, a.lay.dampen, a.lay.adaptive, a.lay.x_off,
+                       a.lam_p);
+    if (a.n_tracks > 0)
+        hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
+                           (int64_t)a.n_tracks, a.pfac);
+    const bool wide = a.lay.d > 16;
+    const int dp = wide ? 32 : 16;
+    if (a.n_runs > 0) {
+        BA_DISPATCH_KP(a.lay, {
+            hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 0>), dim3(nblk(a.n_runs, PM_T)), dim3(PM_T), 0, st, a, dp);
+            if (wide)
+                hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 1>), dim3(nblk(a.n_runs, PM_T)), dim3(PM_T), 0, st, a, dp);
+        });
+    }
+    BA_DISPATCH_KP(a.lay, {
+        if (wide) hipLaunchKernelGGL((k_pm_image<HK_, HP_, 32>), dim3((unsigned)a.n_imgs), dim3(PM_T), 0, st, a);
+        else      hipLaunchKernelGGL((k_pm_image<HK_, HP_, 16>), dim3((unsigned)a.n_imgs), dim3(PM_T), 0, st, a);
+    });
+    if (a.n_pairs > 0) {
+        const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
+        if (wide) hipLaunchKernelGGL(k_pm_pairs<32>, dim3(g), dim3(PM_T), 0, st, a);
+        else      hipLaunchKernelGGL(k_pm_pairs<16>, dim3(g), dim3(PM_T), 0, st, a);
+    }
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
+extern "C" int ba_pm_backsubstitute(const ba_pm_args* args, void* stream) {
+    clear_error();
+    BA_REQUIRE(args != nullptr, "null args");
+    const ba_pm_args& a = *args;
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 32, "pair-major path supports 1 <= d <= 32 image-level parameters");
+    if (a.n_tracks == 0) return BA_OK;
+    const char* miss = pm_missing(a, true);
+    BA_REQUIRE(miss == nullptr, miss);
+    hipStream_t st = (hipStream_t)stream;
+    if (a.lay.d > 16) hipLaunchKernelGGL(k_pm_backsub<32>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+    else              hipLaunchKernelGGL(k_pm_backsub<16>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+    BA_LAUNCHED();
+    return BA_OK;
+}

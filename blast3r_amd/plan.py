@@ -104,6 +104,54 @@ class BAPlan:
         return t[:n].view(shape) if n else t[:0]
 
 
+PM_ARRAYS = ['run_ptr', 'run_obs', 'run_trk', 'run_img', 'img_run_ptr', 'trk_run_ptr', 'trk_run', 'trk_obs_ptr',
+             'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'row_ptr', 'row_ent', 'diag_pair', 'term_ptr', 'term']
+PM_SCALARS = ['n_runs', 'n_pairs', 'n_terms', 'max_terms', 'max_track_runs']
+
+
+class PMPlan:
+    """Device-resident pair-major plan for one (infos, pids) structure (ba_pm_plan_create): runs (the
+    observations of one track in one image), the tracks' runs and observations in image order, and
+    the image pairs with their (run, run) terms.  No limit on track length or co-visibility."""
+    kind = 'pairmajor'
+
+    def __init__(self, infos, pids, n_tracks, device=None):
+        device = device or pids.device
+        cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
+        self.node_ids = np.ascontiguousarray(infos[1].detach().cpu().numpy().astype(np.int64))
+        self.cam_ids = np.ascontiguousarray(infos[2].detach().cpu().numpy().astype(np.int64))
+        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
+        self.n_imgs = int(cum.shape[0])
+        self.n_obs = int(p.shape[0])
+        self.n_tracks = int(n_tracks)
+        L = lib()
+        h = L.ba_pm_plan_create(cum.ctypes.data_as(ctypes.c_void_p), self.n_imgs, p.ctypes.data_as(ctypes.c_void_p),
+                                self.n_obs, self.n_tracks)
+        if not h:
+            raise RuntimeError('pair-major structure plan failed: ' + (L.ba_plan_last_error() or b'').decode())
+        try:
+            sc = np.zeros(len(PM_SCALARS), dtype=np.int64)
+            sz = np.zeros(len(PM_ARRAYS), dtype=np.int64)
+            check(L.ba_pm_plan_query(h, sc.ctypes.data_as(ctypes.c_void_p), sz.ctypes.data_as(ctypes.c_void_p)))
+            self.scalars = {k: int(v) for k, v in zip(PM_SCALARS, sc)}
+            self.host = {}
+            for i, name in enumerate(PM_ARRAYS):
+                arr = np.empty(int(sz[i]), dtype=np.int32)
+                check(L.ba_pm_plan_export(h, i, arr.ctypes.data_as(ctypes.c_void_p)))
+                self.host[name] = arr
+        finally:
+            L.ba_pm_plan_destroy(h)
+        self.device = torch.device(device)
+        self.dev = {k: torch.from_numpy(v).to(self.device) for k, v in self.host.items()}
+        for k in PM_ARRAYS:     # never hand a null pointer to a kernel for an empty array
+            if self.dev[k].numel() == 0:
+                self.dev[k] = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._ws = {}
+        self.workspace_cache = {}
+
+    workspace = BAPlan.workspace
+
+
 # ---------------------------------------------------------------------- cache
 _cache_lock = threading.Lock()
 _cache = {}
@@ -120,12 +168,12 @@ def _prune():
             del _cache[k]
 
 
-def get_plan(infos, pids, n_tracks, **kw):
-    """Plan for this structure: reused while the same pids tensor (unmodified) and the same
-    per-image counts / node / cam ids come back, rebuilt otherwise.  The ids are compared by
+def get_plan(infos, pids, n_tracks, kind='batched', **kw):
+    """Plan for this structure (kind 'batched': BAPlan, 'pairmajor': PMPlan): reused while the same
+    pids tensor (unmodified) and the same per-image counts / node / cam ids come back, rebuilt otherwise.  The ids are compared by
     content unless the very infos tensor of the cached plan comes back unmodified (torch's version
     counter), which needs no device-to-host read."""
-    key = (int(n_tracks), tuple(pids.shape), tuple(sorted(kw.items())))
+    key = (int(n_tracks), tuple(pids.shape), kind, tuple(sorted(kw.items())))
     with _cache_lock:
         for ent in _cache.get(id(pids), []):
             ref, version, k, m, iref, iversion, plan = ent
@@ -139,7 +187,7 @@ def get_plan(infos, pids, n_tracks, **kw):
             ref, version, k, m, iref, iversion, plan = ent
             if ref() is pids and version == pids._version and k == key and m == meta:
                 return plan
-    plan = BAPlan(infos, pids, n_tracks, **kw)
+    plan = PMPlan(infos, pids, n_tracks, **kw) if kind == 'pairmajor' else BAPlan(infos, pids, n_tracks, **kw)
     with _cache_lock:
         if sum(len(v) for v in _cache.values()) > 8:
             _cache.clear()

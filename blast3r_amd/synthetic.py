@@ -296,9 +296,16 @@ def _sample_tracks(rng, cfg, P, f_img, T, mmin, mmax, neigh=None):
     return frames, tids, X
 
 
-def make_problem(cfg=0, n_frames=None, n_tracks=None, seed=None, huber_delta=2.0, dtype=torch.float32):
-    """Build one benchmark configuration (optionally scaled down in frames/tracks)."""
+def make_problem(cfg=0, n_frames=None, n_tracks=None, seed=None, huber_delta=2.0, dtype=torch.float32,
+                 n_channels=None, track_len=None):
+    """Build one benchmark configuration (optionally scaled down in frames/tracks).  n_channels (K_F,
+    giving C = K_F + 1 z-coefficients) and track_len (min, max images per track) override the
+    configuration's own values, for the wide and long-track cases of the tests."""
     spec = dict(_SPEC[cfg])
+    if n_channels is not None:
+        spec['KF'] = int(n_channels)
+    if track_len is not None:
+        spec['mmin'], spec['mmax'] = int(track_len[0]), int(track_len[1])
     F = int(n_frames or spec['F'])
     T = int(n_tracks or spec['T'])
     rng = np.random.Generator(np.random.PCG64(1000 + cfg if seed is None else seed))

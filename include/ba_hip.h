@@ -28,6 +28,9 @@ extern "C" {
 /* ------------------------------------------------------------------ misc */
 const char* ba_last_error(void);
 int ba_version(void);
+/* sizeof(name) for every argument struct below ("ba_lin_args", ...), -1 for an unknown name: lets a
+ * binding check its own struct layout against the library's before the first launch.  Host only. */
+int64_t ba_abi_sizeof(const char* name);
 
 /* ------------------------------------------------------------------ operator-level (cujac) API */
 
@@ -149,10 +152,61 @@ int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream);
  * (n_imgs, d) image-parameter -> unknown index map (-1 = inactive). */
 int ba_backsubstitute(const ba_lin_args* args, void* stream);
 
+/* ------------------------------------------------------------------ pair-major linearize + Schur */
+/* The same reduced system as ba_linearize_schur (S blocks per image pair, rhs and diag(H_cc) per
+ * image, point blocks per track), built without chunks or batches, so that tracks of any length, up
+ * to 32 image-level parameters and any co-visibility pattern are handled (the batched path needs
+ * d <= 15, tracks within 13 images and 128 observations, and is slow on random co-visibility).
+ * Structure from ba_pm_plan_create (host); a run is the observations of one track in one image:
+ *   per observation       J_p^T J_p and J_p^T W r                        (pobs)
+ *   per track             H_pp, g_p in image order; the point-leaf damping; L, L^-1 g_p
+ *   per run (t, i)        V_ti = (sum J_c^T J_p) L^-T                   (V, 3 x dp per run)
+ *   per image i           S_ii = sum J_c^T J_c - sum_t V_ti V_ti^T, rhs and diag(H_cc)
+ *   per image pair (i, j) S_ij = - sum_t V_ti V_tj^T over the pair's terms (one wave, MFMA)
+ * Replaces the same reference work as ba_linearize_schur (ba_solver.py:110-206). */
+void* ba_pm_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
+                        int32_t n_tracks);
+int ba_pm_plan_query(const void* plan, int64_t* scalars, int64_t* array_sizes);
+int ba_pm_plan_export(const void* plan, int32_t which, int32_t* host_dst);
+void ba_pm_plan_destroy(void* plan);
+
+typedef struct {
+    /* structure: the pair-major plan's arrays (device) */
+    const int32_t* infos; int32_t n_imgs; int32_t n_tracks;
+    const int32_t *run_ptr, *run_obs, *run_trk, *run_img, *img_run_ptr, *trk_run_ptr, *trk_run, *trk_obs_ptr,
+        *trk_obs, *obs_img, *pair_i1, *pair_i2, *diag_pair, *term_ptr, *term;
+    int64_t n_obs, n_runs, n_pairs;
+    /* observations in their own (image-major) order */
+    const int32_t* pids; const float *pix2d, *pix2d_std, *pix2d_dep;
+    /* parameters */
+    const float* K; const float* P_rig2cam; int64_t P_rig2cam_stride; const float* P_w2rig;
+    const float* z_coefs; const float* pts3d;
+    const uint8_t *enK, *enP, *enZ, *enX;    /* optional enable masks (NULL = all on) */
+    ba_huber hp;
+    ba_layout lay;                           /* d <= 32 */
+    const float *r_in, *w_in;                /* optional given residuals / weights, as in ba_lin_args */
+    int64_t r_s0, r_s1, w_s0, w_s1;
+    /* workspace */
+    double* pobs;                            /* (n_obs, 9) */
+    double *Hpp, *gp;                        /* (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
+    double* tmax;                            /* (ceil(n_tracks / 256) + 1) */
+    double* lam_p;                           /* (1) point-leaf damping value */
+    double* pfac;                            /* (n_tracks, 12) 16-byte aligned: L, L^-1 g_p, reciprocal pivots */
+    double* V;                               /* (n_runs, 3, dp), dp = 16 for d <= 16 else 32 */
+    /* outputs: (n_pairs, d, d), (n_imgs, d), (n_imgs, d) */
+    double *S_pairs, *e_img, *dg_img;
+    /* back-substitution: delta_c at image level (n_imgs, d), point steps (n_tracks, 3) */
+    const double* dc_img; float* dX; double* dX64;
+} ba_pm_args;
+
+int ba_pm_linearize_schur(const ba_pm_args* args, void* stream);
+/* delta_p = L^-T (L^-1 g_p - sum_i V_ti^T delta_c(i)) per track (= (H_pp + lam_p I)^-1 (g_p - H_pc delta_c)) */
+int ba_pm_backsubstitute(const ba_pm_args* args, void* stream);
+
 /* ------------------------------------------------------------------ reduced system (PCG) */
 typedef struct {
     int64_t n_u;                       /* active unknowns */
-    int32_t n_imgs, d;
+    int32_t n_imgs, d;                 /* d <= 32 */
     const int32_t *umap;               /* (n_imgs, d) -> unknown or -1 */
     const int32_t *inv_ptr, *inv_src;  /* unknown -> list of image-level entries (i*d + j) */
     const int32_t *leaf;               /* (n_u) 0 foc, 1 tau, 2 zcf */
@@ -169,7 +223,8 @@ typedef struct {
                                           [4] best iteration, [5] best iterate returned */
     double *S_rows;                    /* (n_row_ent, d, d): the pair blocks copied per image row */
     int64_t n_row_ent;                 /* row_ptr[n_imgs] */
-    int32_t *row_u;                    /* (n_row_ent, 16) workspace: the unknowns each image-row block multiplies */
+    int32_t *row_u;                    /* (n_row_ent, 16 if d <= 16 else 32) workspace: the unknowns each image-row
+                                          block multiplies */
     const int32_t *long_u;             /* the unknowns whose inv list has more than BA_PCG_LONG_LIST entries,
                                           every one of them, ascending (e.g. a focal pair shared by many images) */
     int64_t n_long;

@@ -164,7 +164,7 @@ def _cfg_flags(p):
     return {k: p.options[k] for k in ('optim_K', 'optim_P') if not p.options.get(k, True)}
 
 
-def _gpu_solver(p, **flags):
+def _gpu_solver(p, path='auto', **flags):
     g = _gpu(p)
     o = opts(p)
     out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
@@ -172,7 +172,7 @@ def _gpu_solver(p, **flags):
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
     gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
-                           no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False))
+                           no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False), path=path)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     fl = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in flags.items()
           if k in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'optim_Z0')}
@@ -182,14 +182,34 @@ def _gpu_solver(p, **flags):
     return gs, delta, g
 
 
+# pair-major path cases: every configuration, image-level width 17 (config 4 with 16 depth channels,
+# focal and pose fixed) and 25 (config 2 with 16 depth channels), tracks spanning 20 to 30 images
+PM_CASES = [(0, 6, 60, {}), (1, 32, 400, {}), (2, 24, 800, {}), (3, 24, 600, {}), (4, 12, 300, {}),
+            (4, 12, 200, dict(n_channels=16)), (2, 16, 300, dict(n_channels=16)),
+            (2, 40, 300, dict(track_len=(20, 30)))]
+PM_IDS = ['cfg0', 'cfg1', 'cfg2', 'cfg3', 'cfg4', 'd17', 'd25', 'long']
+
+
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 8, 200), (1, 32, 400), (2, 20, 400), (3, 24, 600), (4, 12, 300)])
 def test_reduced_system_parity(cfg, nf, nt):
     """S = H_cc - H_cp H_pp^-1 H_pc (damped, reference unknown order) and rhs against the oracle."""
-    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    _check_reduced_system(make_problem(cfg, n_frames=nf, n_tracks=nt), 'auto')
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', PM_CASES, ids=PM_IDS)
+def test_reduced_system_parity_pairmajor(cfg, nf, nt, kw):
+    """The pair-major linearize + Schur path against the oracle, as the batched path."""
+    print(f'pair-major reduced system cfg {cfg} {kw}', flush=True)
+    _check_reduced_system(make_problem(cfg, n_frames=nf, n_tracks=nt, **kw), 'pairmajor')
+
+
+def _check_reduced_system(p, path):
     ne, gvec, params, _, _, _ = _oracle_ne(p, **_cfg_flags(p))
     S_ref = osol.dense_schur(ne)
     rhs_ref = osol.reduced_rhs(ne, gvec)
-    gs, delta, _ = _gpu_solver(p, **_cfg_flags(p))
+    gs, delta, _ = _gpu_solver(p, path=path, **_cfg_flags(p))
+    if path == 'pairmajor':
+        assert gs.last['path'] == 'pairmajor'
     S, rhs = gs.reduced_system_dense()
     assert S.shape == S_ref.shape
     assert rel_err(S, S_ref) < 1e-5
@@ -207,6 +227,16 @@ def test_reduced_system_parity(cfg, nf, nt):
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (1, 32, 400), (2, 24, 800), (3, 24, 600),
                                         (4, 12, 300)])
 def test_pcg_step_parity(cfg, nf, nt):
+    _check_pcg_step(make_problem(cfg, n_frames=nf, n_tracks=nt), 'auto', cfg)
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', PM_CASES, ids=PM_IDS)
+def test_pcg_step_parity_pairmajor(cfg, nf, nt, kw):
+    print(f'pair-major PCG step cfg {cfg} {kw}', flush=True)
+    _check_pcg_step(make_problem(cfg, n_frames=nf, n_tracks=nt, **kw), 'pairmajor', cfg)
+
+
+def _check_pcg_step(p, path, cfg):
     """delta from the device PCG against the oracle restatement of _pcg.
 
     The device's iterate (after k updates: the converged one, else the best so far) is compared
@@ -220,11 +250,11 @@ def test_pcg_step_parity(cfg, nf, nt):
     stopping test met on the oracle's S (to 2x: the device stops on its own rounding of S), and a
     run stopped at maxiter reaching the oracle's reduced residual.
     """
-    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
     fl = _cfg_flags(p)
     ne, gvec, params, (Jc, Jz, Jp), res, w = _oracle_ne(p, **fl)
     d_ref, it_ref, conv_ref = osol.solve_reduced_pcg(ne, gvec)
-    gs, delta, _ = _gpu_solver(p, **fl)
+    gs, delta, _ = _gpu_solver(p, path=path, **fl)
+    assert gs.last['path'] == path or path == 'auto'
     ist = gs.last['istate'].cpu()
     assert int(ist[3]) == int(conv_ref)
     from oracle.dense import dense_jacobian
@@ -425,14 +455,27 @@ def test_lm_step_parity(cfg, nf, nt):
     (1e-4 on delta and on sqrt(W) J delta), then the oracle's line search on that same delta: the same
     scales tried and accepted, loss and updated parameters within 1e-5."""
     print(f'lm_step parity cfg {cfg} ({nf} frames, {nt} tracks)', flush=True)
-    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    _check_lm_step(make_problem(cfg, n_frames=nf, n_tracks=nt), cfg, {})
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', [PM_CASES[i] for i in (2, 3, 5, 6, 7)],
+                         ids=[PM_IDS[i] for i in (2, 3, 5, 6, 7)])
+def test_lm_step_parity_pairmajor(cfg, nf, nt, kw):
+    """lm_step on the pair-major path (forced), same bars as the batched path."""
+    print(f'pair-major lm_step parity cfg {cfg} {kw}', flush=True)
+    _check_lm_step(make_problem(cfg, n_frames=nf, n_tracks=nt, **kw), cfg, dict(path='pairmajor'))
+
+
+def _check_lm_step(p, cfg, solver_kw):
     o = p.options
     kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
-              optim_P=o['optim_P'])
+              optim_P=o['optim_P'], **solver_kw)
     hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
     g = _gpu(p)
     info = {}
     up_g, st_g, _ = gpu_engine._lm_step(**g.lm_inputs(), **kw, info=info)
+    if solver_kw.get('path') == 'pairmajor':
+        assert info['solver'].last['path'] == 'pairmajor'
     inp = p.lm_inputs()
     sysd = _oracle_system(inp, hp, dict(optim_K=o['optim_K'], optim_P=o['optim_P']))
     assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-5 * abs(float(sysd['loss']))
@@ -474,6 +517,23 @@ def test_bundle_adjustment_reuses_trial_objective_exactly():
 
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 20, 600), (3, 20, 500)])
 def test_bundle_adjustment_parity(cfg, nf, nt, monkeypatch):
+    _check_bundle_adjustment(make_problem(cfg, n_frames=nf, n_tracks=nt), cfg, [3, None], monkeypatch)
+
+
+@pytest.mark.parametrize('case', ['d25', 'long'])
+def test_bundle_adjustment_parity_wide_and_long(case, monkeypatch):
+    """Two phases with n_zcfs [1, 17] on 17 depth channels (image-level width 9, batched path, then
+    25, pair-major path), and two phases on tracks spanning 20 to 30 images (pair-major path), with
+    the same step-by-step checks."""
+    if case == 'd25':
+        p = make_problem(2, n_frames=16, n_tracks=300, n_channels=16)
+        _check_bundle_adjustment(p, 20, [1, 17], monkeypatch, paths={'batched', 'pairmajor'})
+    else:
+        p = make_problem(2, n_frames=40, n_tracks=300, track_len=(20, 30))
+        _check_bundle_adjustment(p, 21, [3, None], monkeypatch, paths={'pairmajor'})
+
+
+def _check_bundle_adjustment(p, cfg, n_zcfs, monkeypatch, paths=None):
     """Two phases (pnorm 1 then 0.5; n_zcfs 3 -> first coefficient frozen, 4 columns) on a circle
     (config 0), forward motion (config 2) and random neighbours with a camera per frame (config 3),
     replayed step by step against the oracle: every lm_step bundle_adjustment takes is checked where
@@ -481,12 +541,11 @@ def test_bundle_adjustment_parity(cfg, nf, nt, monkeypatch):
     initial loss, step delta (1e-4, rounding-sensitivity bound only) and the oracle's line search on
     that delta (same scales, loss and parameters within 1e-5); the phase loop then stops where the
     oracle's loss test says (en:496-497) and the z-coefficients keep their frozen column."""
-    from blast3r_amd.data import from_problem
-    print(f'bundle_adjustment parity cfg {cfg}', flush=True)
-    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    print(f'bundle_adjustment parity case {cfg} n_zcfs {n_zcfs}', flush=True)
     o = p.options
-    kw = dict(max_iters=[2, 2], pnorm=[1.0, 0.5], n_zcfs=[3, None], weight_z=o['weight_z'],
+    kw = dict(max_iters=[2, 2], pnorm=[1.0, 0.5], n_zcfs=n_zcfs, weight_z=o['weight_z'],
               huber_delta=o['huber_delta'])
+    n_last = n_zcfs[-1] or n_zcfs[0] + 1
     steps = []
     real = gpu_engine._lm_step
 
@@ -503,9 +562,12 @@ def test_bundle_adjustment_parity(cfg, nf, nt, monkeypatch):
     rig, trk, X = _ba_inputs(p, DEV)
     rig_out, X_out = gpu_engine.bundle_adjustment(rig, trk, X, z_coefs=p.z_coefs.to(DEV), verbose=False, **kw)
     assert torch.equal(trk.pix2d_dep, p.pix2d_dep.to(DEV))            # restored after the phases
-    assert rig_out.z_coefs.shape == (p.z_coefs.shape[0], 4)
-    assert torch.equal(rig_out.z_coefs[:, 0].cpu(), p.z_coefs[:, 0])
+    assert rig_out.z_coefs.shape == (p.z_coefs.shape[0], n_last)
+    if n_zcfs[-1] is None:                                              # the last phase keeps column 0 frozen
+        assert torch.equal(rig_out.z_coefs[:, 0].cpu(), p.z_coefs[:, 0])
     assert len(steps) >= 3
+    if paths is not None:
+        assert {info['solver'].last['path'] for _, _, info, _ in steps} == paths
     accepted = 0
     for n, (inp, k, info, (up_g, st_g, _)) in enumerate(steps):
         hp = dict(weight_z=k['weight_z'], huber_delta=k.get('huber_delta', o['huber_delta']), pnorm=k['pnorm'],

@@ -387,6 +387,15 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     unbound = [n for n in names if n not in _lib._SIGS]
     assert not unbound, unbound
+    # every argument struct the header declares has a ctypes mirror of the library's size
+    hdr = open(os.path.join(os.path.dirname(_lib.LIB_PATH), '..', 'include', 'ba_hip.h')).read()
+    import re
+    structs = set(re.findall(r'}\s*(ba_\w+)\s*;', hdr))
+    assert structs == set(_lib.ABI_STRUCTS), structs ^ set(_lib.ABI_STRUCTS)
+    L = _lib.lib()
+    for n, cls in _lib.ABI_STRUCTS.items():
+        assert L.ba_abi_sizeof(n.encode()) == ctypes.sizeof(cls), n
+    assert L.ba_abi_sizeof(b'no_such_struct') == -1
 
 
 def test_entry_points_reject_null_pointers_without_a_gpu():

@@ -284,3 +284,168 @@ def test_host_mask_for_device_observations_raises():
     with pytest.raises(RuntimeError, match='device tensor'):
         _lib.ptr(torch.zeros(4))
     assert _lib.ptr(None) is None
+
+
+# ------------------------------------------------------------------ pair-major plan
+def _pm_brute(cum, pids, n_tracks):
+    """The pair-major structure restated with Python dicts: runs = (image, track) groups in image
+    order then track order, observations in their original order inside a run."""
+    n_imgs = len(cum)
+    img = np.repeat(np.arange(n_imgs), np.diff(np.concatenate([[0], cum])))
+    runs = {}
+    for o in range(len(pids)):
+        runs.setdefault((int(img[o]), int(pids[o])), []).append(o)
+    keys = sorted(runs)
+    rid = {k: r for r, k in enumerate(keys)}
+    trk_runs = {t: [rid[k] for k in keys if k[1] == t] for t in range(n_tracks)}
+    pairs = sorted({(i, i) for i, _ in keys} |
+                   {(keys[a][0], keys[b][0]) for t in range(n_tracks) for a in trk_runs[t] for b in trk_runs[t]
+                    if keys[a][0] < keys[b][0]})
+    terms = {q: [(a, b) for t in range(n_tracks) for a in trk_runs[t] for b in trk_runs[t]
+                 if (keys[a][0], keys[b][0]) == q] for q in pairs if q[0] != q[1]}
+    return img, keys, runs, trk_runs, pairs, terms
+
+
+@pytest.mark.parametrize('case', ['cfg0', 'dups', 'long', 'empty_imgs'])
+def test_pm_plan_matches_brute_force(case):
+    from blast3r_amd.plan import PMPlan
+    rng = np.random.default_rng(7)
+    if case == 'cfg0':
+        p = make_problem(0, n_frames=8, n_tracks=60)
+        cum, pids, T = p.infos[0].numpy(), p.pids.numpy(), p.n_tracks
+        infos = p.infos
+    else:
+        n_imgs, T = (12, 40) if case != 'long' else (30, 10)
+        counts = rng.integers(0, 25, n_imgs) if case == 'empty_imgs' else rng.integers(5, 25, n_imgs)
+        if case == 'empty_imgs':
+            counts[[0, 4, 11]] = 0
+        cum = np.cumsum(counts).astype(np.int32)
+        pids = rng.integers(0, T, int(cum[-1])).astype(np.int32)     # repeats inside an image: runs of >1
+        infos = torch.stack([torch.from_numpy(cum), torch.arange(n_imgs, dtype=torch.int32),
+                             torch.zeros(n_imgs, dtype=torch.int32)])
+    pl = PMPlan(infos, torch.from_numpy(np.asarray(pids, dtype=np.int32)), T, device='cpu')
+    h, sc = pl.host, pl.scalars
+    img, keys, runs, trk_runs, pairs, terms = _pm_brute(np.asarray(cum), np.asarray(pids), T)
+    n_runs = len(keys)
+    assert sc['n_runs'] == n_runs and sc['n_pairs'] == len(pairs)
+    assert np.array_equal(h['obs_img'], img)
+    assert np.array_equal(h['run_trk'], [k[1] for k in keys]) and np.array_equal(h['run_img'], [k[0] for k in keys])
+    for r, k in enumerate(keys):
+        assert h['run_obs'][h['run_ptr'][r]:h['run_ptr'][r + 1]].tolist() == runs[k]
+    assert h['run_ptr'][-1] == len(pids)
+    for i in range(len(cum)):
+        assert h['img_run_ptr'][i + 1] - h['img_run_ptr'][i] == sum(k[0] == i for k in keys)
+    for t in range(T):
+        assert h['trk_run'][h['trk_run_ptr'][t]:h['trk_run_ptr'][t + 1]].tolist() == trk_runs[t]
+        assert h['trk_obs'][h['trk_obs_ptr'][t]:h['trk_obs_ptr'][t + 1]].tolist() == \
+            [o for r in trk_runs[t] for o in runs[keys[r]]]
+    assert sc['max_track_runs'] == max(len(v) for v in trk_runs.values())
+    assert list(zip(h['pair_i1'].tolist(), h['pair_i2'].tolist())) == pairs
+    for i in range(len(cum)):
+        dp = h['diag_pair'][i]
+        assert (dp == pairs.index((i, i))) if (i, i) in pairs else dp == -1
+    n_terms = 0
+    for q, pr in enumerate(pairs):
+        tt = h['term'][2 * h['term_ptr'][q]:2 * h['term_ptr'][q + 1]].reshape(-1, 2)
+        if pr[0] == pr[1]:
+            assert len(tt) == 0
+        else:
+            assert [tuple(x) for x in tt.tolist()] == terms[pr]
+            n_terms += len(tt)
+    assert sc['n_terms'] == n_terms
+    # rows: every pair once in the row of each of its images, the transposed flag on the second image
+    for i in range(len(cum)):
+        ent = h['row_ent'][h['row_ptr'][i]:h['row_ptr'][i + 1]]
+        want = [(q << 1) | int(pr[0] != i) for q, pr in enumerate(pairs) if i in pr]
+        assert ent.tolist() == want
+
+
+def test_pm_plan_errors():
+    from blast3r_amd.plan import PMPlan
+    p = make_problem(0, n_frames=8, n_tracks=50)
+    bad = p.pids.clone()
+    bad[0] = p.n_tracks + 3
+    with pytest.raises(RuntimeError, match='pid out of range'):
+        PMPlan(p.infos, bad, p.n_tracks, device='cpu')
+    inf = p.infos.clone()
+    inf[0, -1] += 1
+    with pytest.raises(RuntimeError, match='number of observations'):
+        PMPlan(inf, p.pids, p.n_tracks, device='cpu')
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 6, 60, {}), (2, 30, 200, dict(track_len=(20, 30))),
+                                          (4, 12, 150, dict(n_channels=16))])
+def test_pm_schur_emulation_matches_oracle(cfg, nf, nt, kw):
+    """The pair-major data flow (per-run V = sum of the run's J_c^T J_p times L^-T, per-image
+    diagonal blocks from the J rows and the runs' V, per-pair blocks from the term lists) on the
+    oracle's per-observation blocks reproduces the oracle's dense Schur complement."""
+    from blast3r_amd.plan import PMPlan
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt, **kw)
+    o = opts(p)
+    loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'],
+                                  o['huber_delta'])
+    Jc8, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                         p.pix2d_std, p.pix2d_dep, True, float64=True)
+    fl = {k: False for k in ('optim_K', 'optim_P') if not p.options.get(k, True)}
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    ne, gvec, params = osol.build_normal_equations(prob, Jc8, Jz, Jp, res, w, **fl)
+    S_ref = osol.dense_schur(ne)
+    C = p.C
+    hasK, hasP = 'optim_K' not in fl, 'optim_P' not in fl
+    cols = ([0, 1] if hasK else []) + (list(range(2, 8)) if hasP else [])
+    d = len(cols) + C
+    N = p.n_obs
+    sW = torch.sqrt(w.clamp(1e-6, 1e6)).double()
+    Jc = torch.zeros((N, 3, d), dtype=torch.float64)
+    Jc[:, :, :len(cols)] = Jc8[:, :, cols]
+    Jc[:, 2, len(cols):] = Jz[:, 0]
+    Jc = Jc * sW[:, :, None]
+    Jpw = Jp * sW[:, :, None]
+    H = torch.zeros((p.n_tracks, 3, 3), dtype=torch.float64)
+    H.index_add_(0, p.pids.long(), Jpw.transpose(1, 2) @ Jpw)
+    lam = 1e-12 * H.diagonal(dim1=-1, dim2=-2).abs().max()
+    Lf = _chol3(H, lam)
+    pl = PMPlan(p.infos, p.pids, p.n_tracks, device='cpu')
+    h, sc = pl.host, pl.scalars
+    Jn = Jc.numpy()
+    Hcp = (Jc.transpose(1, 2) @ Jpw).numpy()                                # (N, d, 3)
+    Vr = np.zeros((sc['n_runs'], d, 3))
+    for r in range(sc['n_runs']):
+        ob = h['run_obs'][h['run_ptr'][r]:h['run_ptr'][r + 1]]
+        Lt = Lf[h['run_trk'][r]].numpy()
+        Vr[r] = np.linalg.solve(Lt, Hcp[ob].sum(0).T).T                      # (sum J_c^T J_p) L^-T
+    S_pairs = np.zeros((sc['n_pairs'], d, d))
+    for i in range(p.n_imgs):
+        q = h['diag_pair'][i]
+        if q < 0:
+            continue
+        r0, r1 = h['img_run_ptr'][i], h['img_run_ptr'][i + 1]
+        ob = h['run_obs'][h['run_ptr'][r0]:h['run_ptr'][r1]]
+        S_pairs[q] = np.einsum('nri,nrj->ij', Jn[ob], Jn[ob]) - np.einsum('rik,rjk->ij', Vr[r0:r1], Vr[r0:r1])
+    for q in range(sc['n_pairs']):
+        for a, b in h['term'][2 * h['term_ptr'][q]:2 * h['term_ptr'][q + 1]].reshape(-1, 2):
+            S_pairs[q] -= Vr[a] @ Vr[b].T
+    nf_, nt_ = 2 * len(p.K), 6 * len(p.P_w2rig)        # a switched-off leaf keeps its (zero) columns
+    cam, node = p.infos[2].long().numpy(), p.infos[1].long().numpy()
+    n_c = nf_ + nt_ + C * p.n_imgs
+    um = np.zeros((p.n_imgs, d), dtype=np.int64)
+    for i in range(p.n_imgs):
+        c = 0
+        if hasK:
+            um[i, :2] = cam[i] * 2 + np.arange(2); c = 2
+        if hasP:
+            um[i, c:c + 6] = nf_ + node[i] * 6 + np.arange(6); c += 6
+        um[i, c:] = nf_ + nt_ + i * C + np.arange(C)
+    S = np.zeros((n_c, n_c))
+    for q in range(sc['n_pairs']):
+        i1, i2 = h['pair_i1'][q], h['pair_i2'][q]
+        np.add.at(S, (um[i1][:, None], um[i2][None, :]), S_pairs[q])
+        if i1 != i2:
+            np.add.at(S, (um[i2][:, None], um[i1][None, :]), S_pairs[q].T)
+    S_ref = S_ref.clone()
+    assert S.shape == tuple(S_ref.shape)
+    dg = np.diag(S_ref.numpy() - S).copy()
+    assert rel_err(torch.from_numpy(S) + torch.diag(torch.from_numpy(dg)), S_ref) < 1e-10
+    on = np.concatenate([np.full(nf_, hasK), np.full(nt_, hasP), np.ones(C * p.n_imgs, bool)])
+    assert np.all(np.abs(dg[on]) <= 1e-9 * np.abs(np.diag(S_ref.numpy())).max())   # only the 1e-12 damping differs
