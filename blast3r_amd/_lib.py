@@ -84,7 +84,7 @@ class BaPmArgs(ctypes.Structure):
                 ('pts3d', c_p), ('enK', c_p), ('enP', c_p), ('enZ', c_p), ('enX', c_p),
                 ('hp', BaHuber), ('lay', BaLayout),
                 ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
-                ('pobs', c_p), ('Hpp', c_p), ('gp', c_p), ('tmax', c_p), ('lam_p', c_p), ('pfac', c_p), ('V', c_p),
+                ('pobs', c_p), ('wobs', c_p), ('jslots', c_p), ('vslots', c_p), ('yrun', c_p), ('Hpp', c_p), ('gp', c_p), ('tmax', c_p), ('lam_p', c_p), ('pfac', c_p), ('V', c_p),
                 ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dc_img', c_p), ('dX', c_p), ('dX64', c_p)]
 
 
@@ -165,6 +165,7 @@ _SIGS = {
     'ba_pm_plan_destroy': (None, [c_p]),
     'ba_pm_linearize_schur': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
     'ba_pm_backsubstitute': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
+    'ba_pm_slot_doubles': (c_i64, [c_i64, c_int, c_int]),
     'ba_chol_band_lds_bytes': (c_i64, [c_int, c_int, c_int]),
     'ba_chol_work_doubles': (c_i64, [c_int, c_i64, c_int, c_int, c_int, c_int]),
     'ba_reduced_solve': (c_int, [ctypes.POINTER(BaPcgArgs), ctypes.POINTER(BaCholArgs), c_p]),

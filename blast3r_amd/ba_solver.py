@@ -362,14 +362,14 @@ class GaussNewtonSolver:
         """Plan, workspaces and the ba_pm_args of one pair-major linearisation (no kernel launched)."""
         dev = self.device
         d = lay['d']
-        if d > 32:
-            raise ValueError(f'{d} image-level parameters: the reduced system supports at most 32')
+        if d > 31:
+            raise ValueError(f'{d} image-level parameters: the pair-major path supports at most 31')
         plan = get_plan(J.rigs, J.pids, self.tracks.true_n, kind='pairmajor', device=dev)
         sc, pd, ws = plan.scalars, plan.dev, plan.workspace
         T = self.tracks.true_n
         n_imgs = self.imgs.true_n
         n_obs = int(J.pids.shape[0])
-        dp = 16 if d <= 16 else 32
+        dp = 16 if d <= 15 else 32
         dd = max(d, 1)
         a = _lib.BaPmArgs()
         a.infos = ptr(J.rigs.contiguous())
@@ -393,6 +393,11 @@ class GaussNewtonSolver:
         e_img = ws('e_img', (n_imgs, dd), torch.float64)
         dg_img = ws('dg_img', (n_imgs, dd), torch.float64)
         a.pobs = ptr(ws('pobs', (max(n_obs, 1), 9), torch.float64))
+        a.wobs = ptr(ws('wobs', (max(n_obs, 1), 4), torch.float32))
+        nsl = lambda n: int(lib().ba_pm_slot_doubles(n, n_imgs, d))
+        a.jslots = ptr(ws('jslots', (max(nsl(n_obs), 1),), torch.float64))
+        a.vslots = ptr(ws('vslots', (max(nsl(sc['n_runs']), 1),), torch.float64))
+        a.yrun = ptr(ws('yrun', (max(sc['n_runs'], 1), 3), torch.float64))
         a.Hpp, a.gp, a.lam_p = ptr(Hpp), ptr(gp), ptr(lam_p)
         a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), torch.float64))
         a.pfac = ptr(ws('pfac', (max(T, 1), 12), torch.float64))

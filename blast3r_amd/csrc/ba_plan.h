@@ -89,4 +89,5 @@ enum {
     BA_PM_TERM,             // (2 n_terms): (run in i1, run in i2) of one track, per term
     BA_PM_NARRAYS
 };
+#define BA_PM_SPAN 512        // observations (runs) per wave of the pair-major per-image sums
 enum { BA_PMS_N_RUNS = 0, BA_PMS_N_PAIRS, BA_PMS_N_TERMS, BA_PMS_MAX_TERMS, BA_PMS_MAX_TRACK_RUNS, BA_PM_NSCALARS };

@@ -1026,7 +1026,7 @@ extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
 namespace ba {
 
 #define PM_T 256
-#define PM_OB 64            // observations (or runs) staged per round of k_pm_image: 3 rows each
+#define PM_SPAN BA_PM_SPAN  // observations (runs) per wave of k_pm_obs (k_pm_runs)
 
 typedef ba_pm_args PmArgs;
 
@@ -1060,26 +1060,158 @@ __device__ __forceinline__ void pm_core(const PmArgs& a, int o, const ObsCtx& c,
     xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
 }
 
-// per observation: J_p^T J_p (upper 6) and J_p^T W r (3)
-__global__ void __launch_bounds__(PM_T) k_pm_obs(PmArgs a) {
-    const int64_t o = (int64_t)blockIdx.x * PM_T + threadIdx.x;
-    if (o >= a.n_obs) return;
-    ObsCtx c;
-    pm_ctx(a, a.obs_img[o], c);
-    ObsCore oc;
-    DepSrc dep;
-    bool xon;
-    pm_core(a, (int)o, c, oc, dep, xon);
-    double Jp[3][3], gP[3];
-    point_rows<true>(oc, c.cp, xon, Jp, gP);
-    const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
-    double* q = a.pobs + 9 * o;
+// The Jacobian core of observation o with the sqrt(W) k_pm_obs stored for it (no residual, no
+// IRLS weights: the run pass needs neither).
+__device__ __forceinline__ void pm_jcore(const PmArgs& a, int o, const ObsCtx& c, ObsCore& oc, DepSrc& dep,
+                                         bool& xon) {
+    const int pid = a.pids[o];
+    const float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
+    const float2 sv = reinterpret_cast<const float2*>(a.pix2d_std)[o];
+    load_dep(dep, a.pix2d_dep + (int64_t)o * a.lay.C, a.lay.C);
+    double gd = 0.0;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-        const int i = pr[k][0], j = pr[k][1];
-        q[k] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
+    for (int k = 0; k < BA_MAX_C; ++k)
+        if (k < a.lay.C) { float pr = c.zc[k] * dep(k); gd += (double)pr; }
+    eval_jac_core(c.cp, X, sv.x, sv.y, gd, a.hp.is_depth_log, oc.J);
+    const float4 w = reinterpret_cast<const float4*>(a.wobs)[o];
+    oc.sW[0] = w.x; oc.sW[1] = w.y; oc.sW[2] = w.z;
+    xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
+}
+
+// Weighted camera-row element (R, j) of an observation (the element emit_jc_row hands its sink).
+template <int HK, int HP, int R>
+__device__ __forceinline__ double jc_elem(const ObsCore& o, const LinLayout& lay, double mK, double mP, bool zon,
+                                          bool z0off, const DepSrc& dep, int j) {
+    constexpr int OT = 2 * HK, OZ = OT + 6 * HP;
+    double u = 0.0;
+    if (j < OT) {
+        u = (R == 2 && lay.no_grad_f_from_rz) ? 0.0 : jac_foc(o.J, R, j) * mK;
+    } else if (j < OZ) {
+        u = jac_tau(o.J, R, j - OT) * mP;
+    } else if (R == 2) {
+        const int c = j - OZ;
+        if (zon && c < lay.C && !(c == 0 && z0off)) u = o.J.zscale * (double)dep(c);
     }
-    q[6] = gP[0]; q[7] = gP[1]; q[8] = gP[2];
+    return u * o.sW[R];
+}
+
+// One wave's running sum of X^T X (or -X^T X) over the rows it staged for one image: the lower
+// DP/16 x DP/16 tiles of v_mfma_f64_16x16x4f64, flushed to the slot (wave + image) when the image
+// changes.  Column d of every staged row holds its right-hand-side value, so row d of the sum is
+// the image's rhs part.  A slot (w, i) is unique: obs (runs) are image-sorted, so waves w and w + 1
+// cannot hold images i + 1 and i respectively.
+template <int DP>
+struct PmTileAcc {
+    static constexpr int NT = DP / 16, NTL = NT * (NT + 1) / 2;
+    dbl4 acc[NTL];
+    int img;
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int q = 0; q < NTL; ++q) acc[q] = (dbl4){0.0, 0.0, 0.0, 0.0};
+    }
+    __device__ __forceinline__ void flush(double* __restrict__ slots, int64_t wave, int lane) const {
+        double* dst = slots + (wave + img) * (int64_t)(NTL * 256);
+#pragma unroll
+        for (int q = 0; q < NTL; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dst[q * 256 + (4 * v + (lane >> 4)) * 16 + (lane & 15)] = acc[q][v];
+    }
+    // rows [row_lo, row_hi) of X (LDS, row stride DP + 1) into the sum, A operand scaled by sg
+    __device__ __forceinline__ void add_rows(const double (*X)[DP + 1], int row_lo, int row_hi, double sg, int lane) {
+        const int c = lane & 15, k = lane >> 4;
+        for (int g = row_lo >> 2; 4 * g < row_hi; ++g) {
+            const int row = 4 * g + k;
+            const bool ok = row >= row_lo && row < row_hi;
+            double av[NT], bw[NT];
+#pragma unroll
+            for (int h = 0; h < NT; ++h) {
+                const double x = ok ? X[row][16 * h + c] : 0.0;
+                av[h] = sg * x;
+                bw[h] = x;
+            }
+            int q = 0;
+#pragma unroll
+            for (int hi = 0; hi < NT; ++hi)
+#pragma unroll
+                for (int hj = 0; hj <= hi; ++hj) {
+                    acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[hi], bw[hj], acc[q], 0, 0, 0);
+                    ++q;
+                }
+        }
+    }
+    // the 64 staged entities of one round (3 rows each), image ids simg[0..64) (-1 = none, only at
+    // the end; the others non-decreasing): every image segment into the sum
+    __device__ __forceinline__ void add_round(const double (*X)[DP + 1], const int* simg, double sg, double* slots,
+                                              int64_t wave, int lane) {
+        const int my = simg[lane];
+        int lo = 0;
+        while (lo < 64) {
+            const int i = __shfl(my, lo);
+            if (i < 0) break;
+            const int hi = lo + __popcll(__ballot(my == i));
+            if (i != img) {
+                if (img >= 0) flush(slots, wave, lane);
+                zero();
+                img = i;
+            }
+            add_rows(X, 3 * lo, 3 * hi, sg, lane);
+            lo = hi;
+        }
+    }
+};
+
+// Per observation (one wave per PM_SPAN observations, 64 at a time): J_p^T J_p (upper 6) and
+// J_p^T W r (3) to pobs, sqrt(W) to wobs; the weighted camera rows, with sqrt(W) r in column d,
+// staged in LDS and summed per image (X^T X) into the J slots.
+template <int HK, int HP, int DP>
+__global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
+    __shared__ double X[192][DP + 1];
+    __shared__ int simg[64];
+    const int lane = threadIdx.x;
+    const int64_t w = blockIdx.x;
+    const int64_t o_begin = w * PM_SPAN, o_end = min(o_begin + PM_SPAN, a.n_obs);
+    const int d = a.lay.d;
+    PmTileAcc<DP> T;
+    T.img = -1;
+    T.zero();
+    for (int64_t base = o_begin; base < o_end; base += 64) {
+        const int64_t o = base + lane;
+        int img = -1;
+        if (o < o_end) {
+            img = a.obs_img[o];
+            ObsCtx c;
+            ObsCore oc;
+            DepSrc dep;
+            bool xon;
+            pm_ctx(a, img, c);
+            pm_core(a, (int)o, c, oc, dep, xon);
+            double Jp[3][3], gP[3];
+            point_rows<true>(oc, c.cp, xon, Jp, gP);
+            const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
+            double* q = a.pobs + 9 * o;
+#pragma unroll
+            for (int k = 0; k < 6; ++k) {
+                const int i = pr[k][0], j = pr[k][1];
+                q[k] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
+            }
+            q[6] = gP[0]; q[7] = gP[1]; q[8] = gP[2];
+            reinterpret_cast<float4*>(a.wobs)[o] = make_float4((float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f);
+            const bool first = o == 0;
+            emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                          [&](int j, double v) { X[3 * lane][j] = v; });
+            emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                          [&](int j, double v) { X[3 * lane + 1][j] = v; });
+            emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                          [&](int j, double v) { X[3 * lane + 2][j] = v; });
+#pragma unroll
+            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = oc.Rs[k];
+        }
+        simg[lane] = img;
+        __syncthreads();
+        T.add_round(X, simg, 1.0, a.jslots, w, lane);
+        __syncthreads();
+    }
+    if (T.img >= 0) T.flush(a.jslots, w, lane);
 }
 
 // per track: H_pp and g_p summed over its observations in image order; the block's largest diagonal
@@ -1111,186 +1243,141 @@ __global__ void __launch_bounds__(PM_T) k_pm_track(PmArgs a) {
     if (threadIdx.x == 0) a.tmax[blockIdx.x] = sm[0];
 }
 
-// per run (track t, image i), columns [16 H, 16 H + 16): U = sum over the run's observations of
-// J_c^T J_p (weighted rows), V = U L^-T (forward substitution of each row against L)
-template <int HK, int HP, int H>
-__global__ void __launch_bounds__(PM_T) k_pm_runs(PmArgs a, int dp) {
-    const int64_t r = (int64_t)blockIdx.x * PM_T + threadIdx.x;
-    if (r >= a.n_runs) return;
-    const int t = a.run_trk[r];
-    ObsCtx c;
-    pm_ctx(a, a.run_img[r], c);
-    double U[16][3];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-#pragma unroll
-        for (int k = 0; k < 3; ++k) U[j][k] = 0.0;
-    for (int q = a.run_ptr[r]; q < a.run_ptr[r + 1]; ++q) {
-        const int o = a.run_obs[q];
-        ObsCore oc;
-        DepSrc dep;
-        bool xon;
-        pm_core(a, o, c, oc, dep, xon);
-        double Jp[3][3], gP[3];
-        point_rows<false>(oc, c.cp, xon, Jp, gP);
-        const bool first = o == 0;
-        emit_jc_row<HK, HP, 0, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
-#pragma unroll
-            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[0][k];
-        });
-        emit_jc_row<HK, HP, 1, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
-#pragma unroll
-            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[1][k];
-        });
-        emit_jc_row<HK, HP, 2, 16 * H, 16 * H + 16>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep, [&](int j, double v) {
-#pragma unroll
-            for (int k = 0; k < 3; ++k) U[j - 16 * H][k] += v * Jp[2][k];
-        });
-    }
-    const double* pf = a.pfac + 12 * (int64_t)t;
-    const double L1 = pf[1], L2 = pf[2], L4 = pf[4], r0 = pf[9], r1 = pf[10], r2 = pf[11];
-    double* Vr = a.V + r * 3 * dp + 16 * H;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const double v0 = U[j][0] * r0;
-        const double v1 = (U[j][1] - L1 * v0) * r1;
-        const double v2 = (U[j][2] - L2 * v0 - L4 * v1) * r2;
-        Vr[j] = v0; Vr[dp + j] = v1; Vr[2 * dp + j] = v2;
-    }
-}
-
-// per image i (one workgroup): S_ii = sum_o J_c^T J_c - sum_t V_ti V_ti^T, rhs_i = sum_o J_c^T W r -
-// sum_t V_ti (L_t^-1 g_p,t), diag(H_cc)_i = sum_o |J_c|^2 by columns.  The rows are staged in LDS
-// (PM_OB observations or runs, three rows each, per round); the four waves take every fourth group of
-// four rows into v_mfma_f64_16x16x4f64 tiles (the lower tiles of a DP x DP block), then the wave
-// partials are added in wave order.
+// Per run (one wave per PM_SPAN runs, 64 at a time): V = sum over the run's observations of
+// sum_R jc_R (L^-1 jp_R)^T (= (sum J_c^T J_p) L^-T), staged in LDS with L^-1 g_p in column d,
+// summed per image (-X^T X) into the V slots and copied to V (run-major, 3 x DP per run).
 template <int HK, int HP, int DP>
-__global__ void __launch_bounds__(PM_T) k_pm_image(PmArgs a) {
-    constexpr int NR = 3 * PM_OB, NT = DP / 16, NTL = NT * (NT + 1) / 2;
-    __shared__ double X[NR][DP + 1];
-    __shared__ double bv[NR];
-    const int i = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+__global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
+    __shared__ double X[192][DP + 1];
+    __shared__ int simg[64];
+    const int lane = threadIdx.x;
+    const int64_t w = blockIdx.x;
+    const int64_t r_begin = w * PM_SPAN, r_end = min(r_begin + PM_SPAN, a.n_runs);
     const int d = a.lay.d;
-    const int o0 = i ? a.infos[i - 1] : 0, o1 = a.infos[i];
-    const int r0 = a.img_run_ptr[i], r1 = a.img_run_ptr[i + 1];
-    dbl4 acc[NTL];
+    PmTileAcc<DP> T;
+    T.img = -1;
+    T.zero();
+    for (int64_t base = r_begin; base < r_end; base += 64) {
+        const int64_t r = base + lane;
+        int img = -1;
+        if (r < r_end) {
+            img = a.run_img[r];
+            const int t = a.run_trk[r];
+            ObsCtx c;
+            pm_ctx(a, img, c);
+            const double mK = c.enK ? 1.0 : 0.0, mP = c.enP ? 1.0 : 0.0;
+            const bool zon = a.lay.hasZ && c.enZ;
+            const double* pf = a.pfac + 12 * (int64_t)t;
+            const double L1 = pf[1], L2 = pf[2], L4 = pf[4], i0 = pf[9], i1 = pf[10], i2 = pf[11];
+            const int q0 = a.run_ptr[r], q1 = a.run_ptr[r + 1];
+            for (int q = q0; q < q1; ++q) {
+                const int o = a.run_obs[q];
+                ObsCore oc;
+                DepSrc dep;
+                bool xon;
+                pm_jcore(a, o, c, oc, dep, xon);
+                double Jp[3][3], gP[3];
+                point_rows<false>(oc, c.cp, xon, Jp, gP);
+                double wv[3][3];                     // L^-1 jp_R, R = 0..2
 #pragma unroll
-    for (int q = 0; q < NTL; ++q) acc[q] = (dbl4){0.0, 0.0, 0.0, 0.0};
-    double e_acc = 0.0, g_acc = 0.0;
-    ObsCtx c;
-    pm_ctx(a, i, c);
-    const int nro = (o1 - o0 + PM_OB - 1) / PM_OB, nrr = (r1 - r0 + PM_OB - 1) / PM_OB;
-    for (int round = 0; round < nro + nrr; ++round) {
-        const bool vrows = round >= nro;
-        if (t < PM_OB) {
-            if (!vrows) {
-                const int o = o0 + round * PM_OB + t;
-                if (o < o1) {
-                    ObsCore oc;
-                    DepSrc dep;
-                    bool xon;
-                    pm_core(a, o, c, oc, dep, xon);
-                    const bool first = o == 0;
-                    emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                                  [&](int j, double v) { X[3 * t][j] = v; });
-                    emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                                  [&](int j, double v) { X[3 * t + 1][j] = v; });
-                    emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                                  [&](int j, double v) { X[3 * t + 2][j] = v; });
-#pragma unroll
-                    for (int k = 0; k < 3; ++k) bv[3 * t + k] = oc.Rs[k];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 3; ++k) {
-                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = 0.0;
-                        bv[3 * t + k] = 0.0;
-                    }
+                for (int R = 0; R < 3; ++R) {
+                    wv[R][0] = Jp[R][0] * i0;
+                    wv[R][1] = (Jp[R][1] - L1 * wv[R][0]) * i1;
+                    wv[R][2] = (Jp[R][2] - L2 * wv[R][0] - L4 * wv[R][1]) * i2;
                 }
-            } else {
-                const int r = r0 + (round - nro) * PM_OB + t;
-                if (r < r1) {
-                    const double* Vr = a.V + (int64_t)r * 3 * DP;
-                    const double* pf = a.pfac + 12 * (int64_t)a.run_trk[r];
+                const bool z0off = !a.lay.optim_Z0 || (o == 0 && !a.lay.optim_Z_1st_cam);
+                auto col = [&](int j, double v[3]) {
+                    const double e0 = jc_elem<HK, HP, 0>(oc, a.lay, mK, mP, zon, z0off, dep, j);
+                    const double e1 = jc_elem<HK, HP, 1>(oc, a.lay, mK, mP, zon, z0off, dep, j);
+                    const double e2 = jc_elem<HK, HP, 2>(oc, a.lay, mK, mP, zon, z0off, dep, j);
 #pragma unroll
-                    for (int k = 0; k < 3; ++k) {
-                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = Vr[k * DP + j];
-                        bv[3 * t + k] = pf[6 + k];
+                    for (int k = 0; k < 3; ++k) v[k] = e0 * wv[0][k] + e1 * wv[1][k] + e2 * wv[2][k];
+                };
+                if (q == q0) {
+#pragma unroll
+                    for (int j = 0; j < DP; ++j) {
+                        double v[3];
+                        col(j, v);
+#pragma unroll
+                        for (int k = 0; k < 3; ++k) X[3 * lane + k][j] = v[k];
                     }
-                } else {
+                } else {                             // several observations of the track in this image
 #pragma unroll
-                    for (int k = 0; k < 3; ++k) {
-                        for (int j = 0; j < DP; ++j) X[3 * t + k][j] = 0.0;
-                        bv[3 * t + k] = 0.0;
+                    for (int j = 0; j < DP; ++j) {
+                        double v[3];
+                        col(j, v);
+#pragma unroll
+                        for (int k = 0; k < 3; ++k) X[3 * lane + k][j] += v[k];
                     }
                 }
             }
+#pragma unroll
+            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = pf[6 + k];
         }
+        simg[lane] = img;
         __syncthreads();
-        const double sg = vrows ? -1.0 : 1.0;
-        for (int kk = wave; kk < NR / 4; kk += PM_T / 64) {
-            const int row = 4 * kk + (lane >> 4), col = lane & 15;
-            double av[NT], bw[NT];
-#pragma unroll
-            for (int h = 0; h < NT; ++h) { av[h] = sg * X[row][16 * h + col]; bw[h] = X[row][16 * h + col]; }
-            int q = 0;
-#pragma unroll
-            for (int hi = 0; hi < NT; ++hi)
-#pragma unroll
-                for (int hj = 0; hj <= hi; ++hj) {
-                    acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[hi], bw[hj], acc[q], 0, 0, 0);
-                    ++q;
-                }
-        }
-        if (t < DP) {
-            for (int row = 0; row < NR; ++row) {
-                const double x = X[row][t];
-                e_acc += sg * x * bv[row];
-                if (!vrows) g_acc += x * x;
-            }
-        }
+        T.add_round(X, simg, -1.0, a.vslots, w, lane);
+        const int nr = (int)min((int64_t)64, r_end - base);
+        double* dst = a.V + base * 3 * DP;
+        for (int e = lane; e < nr * 3 * DP; e += 64) dst[e] = X[e / DP][e % DP];
         __syncthreads();
     }
-    // wave partials -> LDS (over X), summed in wave order
-    double* part = &X[0][0];
-    constexpr int TS = 256;                          // doubles per 16 x 16 tile
-#pragma unroll
-    for (int q = 0; q < NTL; ++q)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) part[(wave * NTL + q) * TS + (4 * v + (lane >> 4)) * 16 + (lane & 15)] = acc[q][v];
-    __syncthreads();
+    if (T.img >= 0) T.flush(a.vslots, w, lane);
+}
+
+// Per image i: the J and V slots of the waves that held its observations and runs, summed in wave
+// order: S_ii (lower tiles, mirrored), rhs_i (row d) and diag(H_cc)_i (the J part's diagonal).
+template <int DP>
+__global__ void __launch_bounds__(256) k_pm_diag(PmArgs a) {
+    constexpr int NT = DP / 16, NTL = NT * (NT + 1) / 2;
+    const int i = blockIdx.x, t = threadIdx.x, d = a.lay.d;
     const int pd = a.diag_pair[i];
-    if (pd >= 0) {
-        double* S = a.S_pairs + (int64_t)pd * d * d;
-        for (int e = t; e < NTL * TS; e += PM_T) {
-            const int q = e / TS, w = e - q * TS, ri = w >> 4, cj = w & 15;
-            int hi = 0, hj = 0, qq = 0;
-#pragma unroll
-            for (int x = 0; x < NT; ++x)
-#pragma unroll
-                for (int y = 0; y <= x; ++y) { if (qq == q) { hi = x; hj = y; } ++qq; }
-            double s = 0.0;
-#pragma unroll
-            for (int wv = 0; wv < PM_T / 64; ++wv) s += part[(wv * NTL + q) * TS + w];
-            const int rr = 16 * hi + ri, cc = 16 * hj + cj;
-            if (rr < d && cc < d && (hi != hj || cc <= rr)) {
-                S[rr * d + cc] = s;
-                S[cc * d + rr] = s;
-            }
-        }
+    if (pd < 0) {
+        if (t < d) { a.e_img[(int64_t)i * d + t] = 0.0; a.dg_img[(int64_t)i * d + t] = 0.0; }
+        return;
     }
-    if (t < d) {
-        a.e_img[(int64_t)i * d + t] = e_acc;
-        a.dg_img[(int64_t)i * d + t] = g_acc;
+    const int64_t o0 = i ? a.infos[i - 1] : 0, o1 = a.infos[i];
+    const int64_t r0 = a.img_run_ptr[i], r1 = a.img_run_ptr[i + 1];
+    const int64_t wj0 = o0 / PM_SPAN, wj1 = (o1 - 1) / PM_SPAN, wv0 = r0 / PM_SPAN, wv1 = (r1 - 1) / PM_SPAN;
+    double* S = a.S_pairs + (int64_t)pd * d * d;
+    for (int e = t; e < NTL * 256; e += 256) {
+        double sj = 0.0, sv = 0.0;
+        for (int64_t w = wj0; w <= wj1; ++w) sj += a.jslots[(w + i) * (NTL * 256) + e];
+        for (int64_t w = wv0; w <= wv1; ++w) sv += a.vslots[(w + i) * (NTL * 256) + e];
+        const int q = e >> 8, ri = (e >> 4) & 15, cj = e & 15;
+        int hi = 0, hj = 0, qq = 0;
+#pragma unroll
+        for (int x = 0; x < NT; ++x)
+#pragma unroll
+            for (int y = 0; y <= x; ++y) { if (qq == q) { hi = x; hj = y; } ++qq; }
+        const int rr = 16 * hi + ri, cc = 16 * hj + cj;
+        if (rr < d && cc < d && (hi != hj || cc <= rr)) {
+            const double s = sj + sv;
+            S[rr * d + cc] = s;
+            S[cc * d + rr] = s;
+            if (rr == cc) a.dg_img[(int64_t)i * d + rr] = sj;
+        } else if (rr == d && cc < d) {
+            a.e_img[(int64_t)i * d + cc] = sj + sv;
+        }
     }
 }
 
-// per off-diagonal image pair (one wave): S_ij = - sum over the pair's terms of V_ti V_tj^T; the
-// operands of the next term are requested before this term's MFMAs
+// Block -> work index with consecutive indices on one XCD (blocks are dispatched round-robin over
+// the 8 XCDs, each with its own L2): neighbouring pairs share image runs.
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+    const int64_t x = b & 7, q = nb >> 3, r = nb & 7;
+    return x * q + (x < r ? x : r) + (b >> 3);
+}
+
+// per off-diagonal image pair (one wave): S_ij = - sum over the pair's terms of V_ti V_tj^T, four
+// terms (twelve rows) per three v_mfma_f64_16x16x4f64 per tile; the term indices of 64 terms are
+// read at once and handed to the row lanes by shuffles, the rows of the next 8 terms are requested
+// before the MFMAs of the current 8
 template <int DP>
 __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
     constexpr int NT = DP / 16;
     const int lane = threadIdx.x & 63;
-    const int64_t p = (int64_t)blockIdx.x * (PM_T / 64) + (threadIdx.x >> 6);
+    const int64_t p = xcd_block(blockIdx.x, gridDim.x) * (PM_T / 64) + (threadIdx.x >> 6);
     if (p >= a.n_pairs) return;
     const int i1 = a.pair_i1[p], i2 = a.pair_i2[p];
     if (i1 == i2) return;
@@ -1302,24 +1389,57 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
 #pragma unroll
         for (int y = 0; y < NT; ++y) acc[x][y] = (dbl4){0.0, 0.0, 0.0, 0.0};
     const int q0 = a.term_ptr[p], q1 = a.term_ptr[p + 1];
-    auto load = [&](int q, double (&A)[NT], double (&B)[NT]) {
-        const int ra = a.term[2 * (int64_t)q], rb = a.term[2 * (int64_t)q + 1];
+    const int n = q1 - q0, nbat = (n + 7) >> 3;
+    // The loop body has no branches (indices clamped, out-of-range rows zeroed by a factor), so the
+    // accumulators stay in the MFMA registers across iterations.
+    // term indices of window w (64 terms) in lane order, -1 past the end
+    auto window = [&](int w, int& ra, int& rb) {
+        const int q = q0 + 64 * w + lane;
+        const int qc = min(q, q1 - 1);
+        ra = a.term[2 * (int64_t)qc];
+        rb = a.term[2 * (int64_t)qc + 1];
+        if (q >= q1) { ra = -1; rb = -1; }
+    };
+    // rows of batch b (8 terms, 24 rows = 6 groups of 4): group g, lane (c, k) holds row 4 g + k
+    auto fetch = [&](int b, int ra_w, int rb_w, double (&A)[6][NT], double (&B)[6][NT]) {
 #pragma unroll
-        for (int h = 0; h < NT; ++h) {
-            A[h] = k < 3 ? a.V[(int64_t)ra * 3 * DP + k * DP + 16 * h + c] : 0.0;
-            B[h] = k < 3 ? a.V[(int64_t)rb * 3 * DP + k * DP + 16 * h + c] : 0.0;
+        for (int g = 0; g < 6; ++g) {
+            const int row = 4 * g + k, tj = 8 * (b & 7) + row / 3, kk = row % 3;
+            const int ra = __shfl(ra_w, tj), rb = __shfl(rb_w, tj);
+            const double ma = ra >= 0 ? 1.0 : 0.0, mb = rb >= 0 ? 1.0 : 0.0;
+            const int64_t oa = (int64_t)max(ra, 0) * 3 * DP + kk * DP + c, ob = (int64_t)max(rb, 0) * 3 * DP + kk * DP + c;
+#pragma unroll
+            for (int h = 0; h < NT; ++h) {
+                A[g][h] = ma * a.V[oa + 16 * h];
+                B[g][h] = mb * a.V[ob + 16 * h];
+            }
         }
     };
-    double A[NT], B[NT], An[NT], Bn[NT];
-    if (q0 < q1) load(q0, A, B);
-    for (int q = q0; q < q1; ++q) {
-        if (q + 1 < q1) load(q + 1, An, Bn);
+    int ra_c, rb_c, ra_n, rb_n;
+    window(0, ra_c, rb_c);
+    window(1, ra_n, rb_n);
+    double A[6][NT], B[6][NT], An[6][NT], Bn[6][NT];
+    fetch(0, ra_c, rb_c, A, B);
+    for (int b = 0; b < nbat; ++b) {
+        const int nb = b + 1;
+        const bool wrap = (nb & 7) == 0;
+        const int raw = wrap ? ra_n : ra_c, rbw = wrap ? rb_n : rb_c;
+        fetch(nb, nb < nbat ? raw : -1, nb < nbat ? rbw : -1, An, Bn);
 #pragma unroll
-        for (int x = 0; x < NT; ++x)
+        for (int g = 0; g < 6; ++g)
 #pragma unroll
-            for (int y = 0; y < NT; ++y) acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[x], B[y], acc[x][y], 0, 0, 0);
+            for (int x = 0; x < NT; ++x)
 #pragma unroll
-        for (int h = 0; h < NT; ++h) { A[h] = An[h]; B[h] = Bn[h]; }
+                for (int y = 0; y < NT; ++y) acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[g][x], B[g][y], acc[x][y], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 6; ++g)
+#pragma unroll
+            for (int h = 0; h < NT; ++h) { A[g][h] = An[g][h]; B[g][h] = Bn[g][h]; }
+        // after the last batch of a window: the next window becomes current, the one after is read
+        int ra_f, rb_f;
+        window((nb >> 3) + 1, ra_f, rb_f);
+        ra_c = wrap ? ra_n : ra_c; rb_c = wrap ? rb_n : rb_c;
+        ra_n = wrap ? ra_f : ra_n; rb_n = wrap ? rb_f : rb_n;
     }
     double* S = a.S_pairs + p * d * d;
 #pragma unroll
@@ -1333,21 +1453,34 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
             }
 }
 
-// per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i))
+// per run row: y = V_r[k] . delta_c(image of r), DP lanes per row (coalesced over V)
 template <int DP>
+__global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
+    const int64_t n_el = a.n_runs * 3 * DP;
+    const int d = a.lay.d;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e - (threadIdx.x & 63) < n_el;
+         e += (int64_t)gridDim.x * 256) {
+        const int col = (int)(e % DP);
+        const int64_t row = e / DP;
+        double v = 0.0;
+        if (e < n_el && col < d) {
+            const int64_t r = row / 3;
+            v = a.V[e] * a.dc_img[(int64_t)a.run_img[r] * d + col];
+        }
+#pragma unroll
+        for (int m = DP / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+        if (e < n_el && col == 0) a.yrun[row] = v;
+    }
+}
+
+// per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i))
 __global__ void __launch_bounds__(PM_T) k_pm_backsub(PmArgs a) {
     const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
     if (t >= a.n_tracks) return;
-    const int d = a.lay.d;
     double s0 = 0.0, s1 = 0.0, s2 = 0.0;
     for (int q = a.trk_run_ptr[t]; q < a.trk_run_ptr[t + 1]; ++q) {
-        const int r = a.trk_run[q];
-        const double* Vr = a.V + (int64_t)r * 3 * DP;
-        const double* dc = a.dc_img + (int64_t)a.run_img[r] * d;
-        for (int j = 0; j < d; ++j) {
-            const double x = dc[j];
-            s0 += Vr[j] * x; s1 += Vr[DP + j] * x; s2 += Vr[2 * DP + j] * x;
-        }
+        const double* y = a.yrun + 3 * (int64_t)a.trk_run[q];
+        s0 += y[0]; s1 += y[1]; s2 += y[2];
     }
     const double* pf = a.pfac + 12 * t;
     const double z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
@@ -1363,8 +1496,9 @@ static const char* pm_missing(const ba_pm_args& a, bool backsub) {
     const bool C = a.lay.C > 0;
     BA_NEED(true, a.trk_run_ptr); BA_NEED(true, a.trk_run); BA_NEED(true, a.run_img); BA_NEED(true, a.V);
     BA_NEED(true, a.pfac);
-    BA_NEED(backsub, a.dc_img); BA_NEED(backsub, a.dX);
+    BA_NEED(backsub, a.dc_img); BA_NEED(backsub, a.dX); BA_NEED(backsub, a.yrun);
     if (backsub) return nullptr;
+    BA_NEED(true, a.jslots); BA_NEED(true, a.vslots); BA_NEED(true, a.wobs);
     BA_NEED(true, a.infos); BA_NEED(true, a.run_ptr); BA_NEED(true, a.run_obs); BA_NEED(true, a.run_trk);
     BA_NEED(true, a.img_run_ptr); BA_NEED(true, a.trk_obs_ptr); BA_NEED(true, a.trk_obs); BA_NEED(true, a.obs_img);
     BA_NEED(true, a.pair_i1); BA_NEED(true, a.pair_i2); BA_NEED(true, a.diag_pair); BA_NEED(true, a.term_ptr);
@@ -1379,23 +1513,38 @@ static const char* pm_missing(const ba_pm_args& a, bool backsub) {
 
 }  // namespace ba
 
+extern "C" int64_t ba_pm_slot_doubles(int64_t n_items, int32_t n_imgs, int32_t d) {
+    if (n_items < 0 || n_imgs < 0 || d < 1 || d > 31) return -1;
+    const int64_t ntl = d < 16 ? 1 : 3;
+    return ((n_items + PM_SPAN - 1) / PM_SPAN + n_imgs) * ntl * 256;
+}
+
 extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
     const ba_pm_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
-    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 32, "pair-major path supports 1 <= d <= 32 image-level parameters");
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 31, "pair-major path supports 1 <= d <= 31 image-level parameters");
     BA_REQUIRE(a.lay.off_tau == 2 * a.lay.hasK && a.lay.off_zcf == a.lay.off_tau + 6 * a.lay.hasP &&
                    a.lay.d == a.lay.off_zcf + (a.lay.hasZ ? a.lay.C : 0),
                "inconsistent image-level layout");
     BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "at most 24 z-coefficient columns");
     BA_REQUIRE(a.n_imgs >= 1 && a.n_tracks >= 0 && a.n_obs >= 0 && a.n_runs >= 0 && a.n_pairs >= 0, "bad sizes");
+    BA_REQUIRE(a.n_obs < ((int64_t)1 << 31) && a.n_runs <= a.n_obs, "bad observation / run counts");
     const char* miss = pm_missing(a, false);
     BA_REQUIRE(miss == nullptr, miss);
-    BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
+    BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp | (uintptr_t)a.wobs) & 15) == 0,
+               "Hpp, pfac and wobs must be 16-byte aligned");
     const int64_t nbt = (a.n_tracks + PM_T - 1) / PM_T;
+    const bool wide = a.lay.d > 15;
     hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.tmax, nbt);
-    if (a.n_obs > 0) hipLaunchKernelGGL(k_pm_obs, dim3(nblk(a.n_obs, PM_T)), dim3(PM_T), 0, st, a);
+    if (a.n_obs > 0) {
+        const unsigned g = (unsigned)((a.n_obs + PM_SPAN - 1) / PM_SPAN);
+        BA_DISPATCH_KP(a.lay, {
+            if (wide) hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 32>), dim3(g), dim3(64), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 16>), dim3(g), dim3(64), 0, st, a);
+        });
+    }
     if (a.n_tracks > 0) {
         hipLaunchKernelGGL(k_pm_track, dim3((unsigned)nbt), dim3(PM_T), 0, st, a);
         const int64_t nb = nbt < 256 * 256 ? (nbt + 255) / 256 : 256;
@@ -1406,19 +1555,15 @@ extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
     if (a.n_tracks > 0)
         hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
                            (int64_t)a.n_tracks, a.pfac);
-    const bool wide = a.lay.d > 16;
-    const int dp = wide ? 32 : 16;
     if (a.n_runs > 0) {
+        const unsigned g = (unsigned)((a.n_runs + PM_SPAN - 1) / PM_SPAN);
         BA_DISPATCH_KP(a.lay, {
-            hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 0>), dim3(nblk(a.n_runs, PM_T)), dim3(PM_T), 0, st, a, dp);
-            if (wide)
-                hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 1>), dim3(nblk(a.n_runs, PM_T)), dim3(PM_T), 0, st, a, dp);
+            if (wide) hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 32>), dim3(g), dim3(64), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 16>), dim3(g), dim3(64), 0, st, a);
         });
     }
-    BA_DISPATCH_KP(a.lay, {
-        if (wide) hipLaunchKernelGGL((k_pm_image<HK_, HP_, 32>), dim3((unsigned)a.n_imgs), dim3(PM_T), 0, st, a);
-        else      hipLaunchKernelGGL((k_pm_image<HK_, HP_, 16>), dim3((unsigned)a.n_imgs), dim3(PM_T), 0, st, a);
-    });
+    if (wide) hipLaunchKernelGGL(k_pm_diag<32>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
+    else      hipLaunchKernelGGL(k_pm_diag<16>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
     if (a.n_pairs > 0) {
         const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
         if (wide) hipLaunchKernelGGL(k_pm_pairs<32>, dim3(g), dim3(PM_T), 0, st, a);
@@ -1432,13 +1577,19 @@ extern "C" int ba_pm_backsubstitute(const ba_pm_args* args, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
     const ba_pm_args& a = *args;
-    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 32, "pair-major path supports 1 <= d <= 32 image-level parameters");
+    BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 31, "pair-major path supports 1 <= d <= 31 image-level parameters");
     if (a.n_tracks == 0) return BA_OK;
     const char* miss = pm_missing(a, true);
     BA_REQUIRE(miss == nullptr, miss);
     hipStream_t st = (hipStream_t)stream;
-    if (a.lay.d > 16) hipLaunchKernelGGL(k_pm_backsub<32>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
-    else              hipLaunchKernelGGL(k_pm_backsub<16>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+    if (a.n_runs > 0) {
+        const int dp = a.lay.d > 15 ? 32 : 16;
+        const int64_t n_el = a.n_runs * 3 * dp;
+        const unsigned g = (unsigned)std::min<int64_t>((n_el + 255) / 256, 65536);
+        if (dp == 32) hipLaunchKernelGGL(k_pm_yrun<32>, dim3(g), dim3(256), 0, st, a);
+        else          hipLaunchKernelGGL(k_pm_yrun<16>, dim3(g), dim3(256), 0, st, a);
+    }
+    hipLaunchKernelGGL(k_pm_backsub, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
     BA_LAUNCHED();
     return BA_OK;
 }

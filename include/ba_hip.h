@@ -155,13 +155,15 @@ int ba_backsubstitute(const ba_lin_args* args, void* stream);
 /* ------------------------------------------------------------------ pair-major linearize + Schur */
 /* The same reduced system as ba_linearize_schur (S blocks per image pair, rhs and diag(H_cc) per
  * image, point blocks per track), built without chunks or batches, so that tracks of any length, up
- * to 32 image-level parameters and any co-visibility pattern are handled (the batched path needs
+ * to 31 image-level parameters and any co-visibility pattern are handled (the batched path needs
  * d <= 15, tracks within 13 images and 128 observations, and is slow on random co-visibility).
  * Structure from ba_pm_plan_create (host); a run is the observations of one track in one image:
- *   per observation       J_p^T J_p and J_p^T W r                        (pobs)
+ *   per observation       J_p^T J_p and J_p^T W r (pobs); per wave of BA_PM_SPAN observations and
+ *                         image, sum J_c^T J_c and J_c^T W r (jslots, MFMA)
  *   per track             H_pp, g_p in image order; the point-leaf damping; L, L^-1 g_p
- *   per run (t, i)        V_ti = (sum J_c^T J_p) L^-T                   (V, 3 x dp per run)
- *   per image i           S_ii = sum J_c^T J_c - sum_t V_ti V_ti^T, rhs and diag(H_cc)
+ *   per run (t, i)        V_ti = (sum J_c^T J_p) L^-T (V, 3 x dp per run); per wave of BA_PM_SPAN
+ *                         runs and image, sum V V^T and V L^-1 g_p (vslots, MFMA)
+ *   per image i           S_ii, rhs and diag(H_cc) from its slots, summed in wave order
  *   per image pair (i, j) S_ij = - sum_t V_ti V_tj^T over the pair's terms (one wave, MFMA)
  * Replaces the same reference work as ba_linearize_schur (ba_solver.py:110-206). */
 void* ba_pm_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
@@ -183,16 +185,19 @@ typedef struct {
     const float* z_coefs; const float* pts3d;
     const uint8_t *enK, *enP, *enZ, *enX;    /* optional enable masks (NULL = all on) */
     ba_huber hp;
-    ba_layout lay;                           /* d <= 32 */
+    ba_layout lay;                           /* d <= 31 */
     const float *r_in, *w_in;                /* optional given residuals / weights, as in ba_lin_args */
     int64_t r_s0, r_s1, w_s0, w_s1;
     /* workspace */
     double* pobs;                            /* (n_obs, 9) */
+    float* wobs;                             /* (n_obs, 4) 16-byte aligned: sqrt(W) per residual row */
+    double *jslots, *vslots;                 /* per-wave image sums: ba_pm_slot_doubles(n_obs | n_runs, n_imgs, d) */
+    double* yrun;                            /* (n_runs, 3) back-substitution: V_r^T delta_c per run */
     double *Hpp, *gp;                        /* (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
     double* tmax;                            /* (ceil(n_tracks / 256) + 1) */
     double* lam_p;                           /* (1) point-leaf damping value */
     double* pfac;                            /* (n_tracks, 12) 16-byte aligned: L, L^-1 g_p, reciprocal pivots */
-    double* V;                               /* (n_runs, 3, dp), dp = 16 for d <= 16 else 32 */
+    double* V;                               /* (n_runs, 3, dp), dp = 16 for d <= 15 else 32 */
     /* outputs: (n_pairs, d, d), (n_imgs, d), (n_imgs, d) */
     double *S_pairs, *e_img, *dg_img;
     /* back-substitution: delta_c at image level (n_imgs, d), point steps (n_tracks, 3) */
@@ -200,6 +205,9 @@ typedef struct {
 } ba_pm_args;
 
 int ba_pm_linearize_schur(const ba_pm_args* args, void* stream);
+/* doubles of one slot array of ba_pm_args (n_items = n_obs for jslots, n_runs for vslots); -1 for d
+ * outside 1..31 */
+int64_t ba_pm_slot_doubles(int64_t n_items, int32_t n_imgs, int32_t d);
 /* delta_p = L^-T (L^-1 g_p - sum_i V_ti^T delta_c(i)) per track (= (H_pp + lam_p I)^-1 (g_p - H_pc delta_c)) */
 int ba_pm_backsubstitute(const ba_pm_args* args, void* stream);
 

@@ -1,0 +1,142 @@
+"""Code generation check of the MFMA kernels (CPU only: hipcc cross-compiles gfx950 here).
+
+An MFMA result read back from its accumulator registers (v_accvgpr_read, or any instruction
+naming the register) needs a number of wait states after the v_mfma that writes it.  The compiler
+inserts them in straight-line code, but one loop shape of the pair kernel had the accumulators
+copied out at the loop head with only 5 wait states after the MFMA at the loop end (the back
+edge): the result read back was stale in its last element, which the pair-major parity tests
+caught.  This test compiles the MFMA sources to assembly and requires at least MIN_WAIT wait states
+(instructions, s_nop n counting n + 1) between every v_mfma_f64 and a read of its destination
+registers, along straight-line code and across loop back edges.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+from blast3r_amd import build as B
+
+MIN_WAIT = 10
+MFMA_SOURCES = ['ba_schur.hip', 'ba_chol.hip']
+
+
+def _asm(src, tmp_path):
+    out = str(tmp_path / (src + '.s'))
+    cmd = [B._hipcc()] + [f for f in B.HIPCC_FLAGS if f not in ('-fPIC',)] + \
+        ['-S', '--cuda-device-only', os.path.join(B.CSRC, src), '-o', out]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-2000:]
+    return open(out).read()
+
+
+def _functions(asm):
+    cur, body = None, []
+    for line in asm.split('\n'):
+        m = re.match(r'^(_Z\w+):', line)
+        if m:
+            if cur:
+                yield cur, body
+            cur, body = m.group(1), []
+            continue
+        t = line.split(';')[0].strip()
+        if cur and t and not (t.startswith('.') and not t.startswith('.LBB')):
+            body.append(t)
+        if cur and line.startswith('.Lfunc_end'):
+            yield cur, body
+            cur = None
+    if cur:
+        yield cur, body
+
+
+def _mfma_dest(t):
+    m = re.match(r'v_mfma_f64\S*\s+([av])\[(\d+):(\d+)\]', t)
+    return (m.group(1), int(m.group(2)), int(m.group(3))) if m else None
+
+
+def _reads(t, kind, reg):
+    """Does instruction t read register kind+reg (outside an MFMA's own accumulator operand)?"""
+    if t.startswith('v_mfma') or t.startswith('.LBB') or t.startswith('s_'):
+        return False
+    ops = t.split(None, 1)[1] if ' ' in t else ''
+    parts = [p.strip() for p in ops.split(',')]
+    srcs = parts[1:] if not t.startswith(('global_store', 'buffer_store', 'ds_write', 'flat_store')) else parts
+    for p in srcs:
+        m = re.match(rf'{kind}\[(\d+):(\d+)\]', p)
+        if m and int(m.group(1)) <= reg <= int(m.group(2)):
+            return True
+        if p == f'{kind}{reg}':
+            return True
+    return False
+
+
+def _wait(t):
+    m = re.match(r's_nop\s+(\d+)', t)
+    return int(m.group(1)) + 1 if m else (0 if t.startswith('.LBB') else 1)
+
+
+def _violations(body):
+    bad = []
+    for k, t in enumerate(body):
+        dst = _mfma_dest(t)
+        if not dst:
+            continue
+        kind, lo, hi = dst
+        for reg in range(lo, hi + 1):
+            # straight-line successors, and the loop head after a back edge to an earlier label
+            w = 0
+            for j in range(k + 1, min(len(body), k + 64)):
+                u = body[j]
+                if _reads(u, kind, reg):
+                    if w < MIN_WAIT:
+                        bad.append((t, u, w))
+                    break
+                if _mfma_dest(u) and _mfma_dest(u)[0] == kind and _mfma_dest(u)[1] <= reg <= _mfma_dest(u)[2]:
+                    break
+                m = re.match(r's_(?:cbranch\w*|branch)\s+(\.LBB\w+)$', u)
+                if m:
+                    lab = m.group(1)
+                    heads = [i for i, x in enumerate(body) if x.split(':')[0] == lab]
+                    if heads and heads[0] < j:
+                        w2 = w + 1
+                        for i in range(heads[0] + 1, min(len(body), heads[0] + 64)):
+                            v = body[i]
+                            if _reads(v, kind, reg):
+                                if w2 < MIN_WAIT:
+                                    bad.append((t, v, w2))
+                                break
+                            if _mfma_dest(v) or v.startswith('s_cbranch') or v.startswith('s_branch'):
+                                break
+                            w2 += _wait(v)
+                    if u.startswith('s_branch'):
+                        break
+                w += _wait(u)
+                if w >= 64:
+                    break
+    return bad
+
+
+def test_scanner_finds_a_short_back_edge():
+    """The scanner itself: a loop whose head reads the accumulator 5 wait states after the MFMA at
+    its end (the shape that gave stale results) is flagged; with s_nop padding it is not."""
+    body = ['.LBB0_1:', 's_nop 3', 'v_accvgpr_read_b32 v9, a7', 'v_mov_b32_e32 v1, v2',
+            'v_mfma_f64_16x16x4_f64 a[0:7], v[2:3], v[4:5], a[0:7]', 's_cbranch_vccnz .LBB0_1', 's_endpgm']
+    assert _violations(body)
+    ok = list(body)
+    ok[1] = 's_nop 15'
+    assert not _violations(ok)
+    straight = ['v_mfma_f64_16x16x4_f64 a[0:7], v[2:3], v[4:5], a[0:7]', 's_nop 1', 'v_accvgpr_read_b32 v9, a7']
+    assert _violations(straight)
+
+
+@pytest.mark.parametrize('src', MFMA_SOURCES)
+def test_mfma_results_read_after_enough_wait_states(src, tmp_path):
+    asm = _asm(src, tmp_path)
+    n_mfma = asm.count('v_mfma_f64')
+    assert n_mfma > 0
+    bad = {}
+    for name, body in _functions(asm):
+        v = _violations(body)
+        if v:
+            bad[name] = v[:3]
+    assert not bad, bad

@@ -182,12 +182,13 @@ def _gpu_solver(p, path='auto', **flags):
     return gs, delta, g
 
 
-# pair-major path cases: every configuration, image-level width 17 (config 4 with 16 depth channels,
-# focal and pose fixed) and 25 (config 2 with 16 depth channels), tracks spanning 20 to 30 images
+# pair-major path cases: every configuration, image-level width 16 and 17 (config 4 with 15 and 16
+# depth channels, focal and pose fixed) and 25 (config 2 with 16 depth channels), tracks spanning 20
+# to 30 images
 PM_CASES = [(0, 6, 60, {}), (1, 32, 400, {}), (2, 24, 800, {}), (3, 24, 600, {}), (4, 12, 300, {}),
             (4, 12, 200, dict(n_channels=16)), (2, 16, 300, dict(n_channels=16)),
-            (2, 40, 300, dict(track_len=(20, 30)))]
-PM_IDS = ['cfg0', 'cfg1', 'cfg2', 'cfg3', 'cfg4', 'd17', 'd25', 'long']
+            (2, 40, 300, dict(track_len=(20, 30))), (4, 12, 200, dict(n_channels=15))]
+PM_IDS = ['cfg0', 'cfg1', 'cfg2', 'cfg3', 'cfg4', 'd17', 'd25', 'long', 'd16']
 
 
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 8, 200), (1, 32, 400), (2, 20, 400), (3, 24, 600), (4, 12, 300)])
@@ -246,7 +247,8 @@ def _check_pcg_step(p, path, cfg):
     over four perturbed oracle runs: three of b, one applying S as a dense matrix) on delta and on
     J.delta; on well-conditioned cases (configs 0, 2, 3) that is the plain 1e-4.  The stopping
     decisions are checked separately: the same converged flag, a converged count within 5% of the
-    oracle's (at least 2: config 4's moves between 151 and 156 under those perturbations), the
+    oracle's (at least 2: config 4's moves between 151 and 156 under those perturbations; twice the
+    largest move of the oracle's own count under those perturbations where that is larger), the
     stopping test met on the oracle's S (to 2x: the device stops on its own rounding of S), and a
     run stopped at maxiter reaching the oracle's reduced residual.
     """
@@ -268,7 +270,17 @@ def _check_pcg_step(p, path, cfg):
     M = lambda v: v / diagA
     red = lambda dc: float((rhs - S @ dc).norm() / rhs.norm())
     if conv_ref:
-        assert abs(int(ist[2]) - it_ref) <= max(2, 0.05 * it_ref), (int(ist[2]), it_ref)
+        # the oracle's own count under the same rounding perturbations as below (a 1e-15 relative
+        # change of b moves it from 249 to 275 on the width-16 case, condition number ~1e19)
+        gen = torch.Generator().manual_seed(1000 + cfg)
+        spread = 0
+        for A_mv, b in [(lambda v: S @ v, rhs)] + [
+                (lambda v: osol.S_matvec(ne, v), rhs * (1 + 1e-15 * torch.randn(rhs.shape, generator=gen,
+                                                                                 dtype=rhs.dtype)))
+                for _ in range(3)]:
+            _, it_alt, conv_alt = osol.pcg(A_mv, b, M_mv=M, tol=1e-6, maxiter=300)
+            spread = max(spread, abs(it_alt - it_ref) if conv_alt else 300)
+        assert abs(int(ist[2]) - it_ref) <= max(2, 0.05 * it_ref, 2 * spread), (int(ist[2]), it_ref, spread)
         assert red(delta[:n_c].cpu().double()) <= 2e-6
     else:
         assert red(delta[:n_c].cpu().double()) <= 1.5 * red(d_ref[:n_c])
