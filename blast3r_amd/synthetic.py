@@ -147,17 +147,19 @@ class _FieldBank:
         gh, gw = H_IMG // self.STRIDE, W_IMG // self.STRIDE
         ys = (np.arange(gh) + 0.5) * self.STRIDE
         xs = (np.arange(gw) + 0.5) * self.STRIDE
-        gx, gy = np.meshgrid(xs, ys)
-        pts = np.stack([gx.ravel(), gy.ravel()], 1)                        # (G, 2)
         self.grid = np.zeros((n_frames, n_ch, gh, gw), dtype=np.float32)
         for f0 in range(0, n_frames, 64):
             f1 = min(n_frames, f0 + 64)
             om = rng.normal(0.0, 1.0 / ell, size=(f1 - f0, n_ch, self.N_FEAT, 2))
             ph = rng.uniform(0, 2 * np.pi, size=(f1 - f0, n_ch, self.N_FEAT))
-            arg = np.einsum('fcrk,gk->fcrg', om, pts) + ph[..., None]
-            val = sigma * np.sqrt(2.0 / self.N_FEAT) * np.cos(arg).sum(2)
-            self.grid[f0:f1] = val.reshape(f1 - f0, n_ch, gh, gw).astype(np.float32)
+            # cos(w_x x + w_y y + ph) on the separable lattice = Re(e^{i (w_y y + ph)} e^{i w_x x}):
+            # a sum over features of outer products, one complex matrix product per (frame, channel)
+            ey = np.exp(1j * (om[..., 1, None] * ys + ph[..., None]))          # (f, c, r, gh)
+            ex = np.exp(1j * (om[..., 0, None] * xs))                           # (f, c, r, gw)
+            val = sigma * np.sqrt(2.0 / self.N_FEAT) * np.matmul(ey.transpose(0, 1, 3, 2), ex).real
+            self.grid[f0:f1] = val.astype(np.float32)
         self.gh, self.gw = gh, gw
+        self.grid_hwc = np.ascontiguousarray(self.grid.transpose(0, 2, 3, 1))   # channel-last for gathers
 
     def sample(self, frame, uv):
         """Bilinear sample of every channel at pixels uv (n,2) of frames (n,) -> (n, n_ch)."""
@@ -169,11 +171,11 @@ class _FieldBank:
         y0 = np.minimum(np.floor(y).astype(np.int64), self.gh - 2)
         ax = (x - x0)[:, None]
         ay = (y - y0)[:, None]
-        g = self.grid
-        v00 = g[frame, :, y0, x0]
-        v01 = g[frame, :, y0, x0 + 1]
-        v10 = g[frame, :, y0 + 1, x0]
-        v11 = g[frame, :, y0 + 1, x0 + 1]
+        g = self.grid_hwc
+        v00 = g[frame, y0, x0]
+        v01 = g[frame, y0, x0 + 1]
+        v10 = g[frame, y0 + 1, x0]
+        v11 = g[frame, y0 + 1, x0 + 1]
         return ((1 - ay) * ((1 - ax) * v00 + ax * v01) + ay * ((1 - ax) * v10 + ax * v11)).astype(np.float32)
 
 

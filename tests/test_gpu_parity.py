@@ -766,17 +766,21 @@ def test_backsubstitute_image_level_delta_matches_unknown_map():
         assert outs[0].abs().sum() > 0
 
 
-def test_reduced_system_full_config2_against_oracle():
-    """The benchmark's own size (config 2: 1024 frames, 1 M tracks, 8.0 M observations): the reduced
-    rhs, the point blocks and S v for seeded v against the oracle's normal equations at the same
-    size (the oracle's pass takes a few seconds on the host's threads), to the 1e-5 bar."""
+@pytest.mark.parametrize('cfg,path', [(2, 'auto'), (2, 'pairmajor'), (3, 'auto')])
+def test_reduced_system_full_size_against_oracle(cfg, path):
+    """Full benchmark sizes (config 2: 1024 frames, 1 M tracks, 8.0 M observations, on the batched
+    and the pair-major path; config 3: 4096 frames with a camera each, 3 M tracks on random
+    neighbours, 22.5 M observations, where the pair-major path is chosen): the reduced rhs, the
+    point blocks and S v for seeded v against the oracle's normal equations at the same size (the
+    oracle's pass takes seconds on the host's threads), to the 1e-5 bar."""
     import os
     torch.set_num_threads(min(16, os.cpu_count() or 1))
-    p = make_problem(2)
-    assert p.n_imgs == 1024 and p.n_tracks == 1_000_000
-    print(f'[full cfg2] {p.n_obs} observations', flush=True)
-    gs, _, _ = _gpu_solver(p)
+    p = make_problem(cfg)
+    assert (p.n_imgs, p.n_tracks) == ((1024, 1_000_000) if cfg == 2 else (4096, 3_000_000))
+    print(f'[full cfg{cfg} {path}] {p.n_obs} observations', flush=True)
+    gs, _, _ = _gpu_solver(p, path=path)
     last = gs.last
+    assert last['path'] == ('batched' if (cfg, path) == (2, 'auto') else 'pairmajor')
     um, d, plan = last['unknowns'], last['lay']['d'], last['plan']
     rhs = last['rhs'].cpu()
     H = gs.point_blocks()[0].cpu()
@@ -801,7 +805,7 @@ def test_reduced_system_full_config2_against_oracle():
         return (y + last['damp'] * v).cpu()
 
     ne, gvec, _, _, _, _ = _oracle_ne(p)
-    print('[full cfg2] oracle normal equations built', flush=True)
+    print(f'[full cfg{cfg}] oracle normal equations built', flush=True)
     assert rel_err(rhs, osol.reduced_rhs(ne, gvec)) < 1e-5
     Hr = ne.leaves['pts'] - float(last['lam_p'].cpu()) * torch.eye(3, dtype=torch.float64)
     iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
