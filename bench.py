@@ -10,8 +10,10 @@ pose + depth coefficients + points optimised.
 Prints one JSON line: value = observations per second of the linearize + Schur
 pass; LM iterations per second of the full lm_step are reported beside it, as
 are the roofline of the dominant kernel (k_schur, timed with events on its own
-launch stream) and the CPU oracle timed on a bounded sample of the same
-workload.
+launch stream), the pass's algorithmic bytes against its counter traffic (the
+committed rocprofv3 summaries under profiles/), the pair-major path on config 3
+(random co-visibility, 22.5 M observations) and the CPU oracle on the same
+workload (fp64 and fp32 passes, one lm_step with a capped PCG).
 """
 import argparse
 import json
@@ -42,6 +44,8 @@ def main():
                     help='also time the observation-structure edits (old | new merge, remove, plan rebuild)')
     ap.add_argument('--tangent', type=int, default=1,
                     help='also time the dense tangent prior on maps of the configuration (1 = yes)')
+    ap.add_argument('--pm-config', type=int, default=3,
+                    help='also time the pair-major path on this configuration at full size (-1 = no)')
     ap.add_argument('--copy-probe', action='store_true',
                     help='run a 256 MiB fill and a 256 MiB kernel copy (calibrates FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
@@ -115,19 +119,15 @@ def main():
         torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
 
-    # roofline of the dominant kernel (k_schur): fp64 MFMA-bound.  Algorithmic flops per launch =
-    # 6 d^2 per (track, image pair) term and per observation (the J_c^T J_c term), d = image-level
-    # parameters; algorithmic bytes of the whole linearize + Schur pass = per observation
-    # pid 4 + pix 8 + std 8 + dep 4C, per track point 12 + H_pp^-1 24 + g_p 12, per reduced
-    # block d^2 fp64 written once, per image g_c d fp64.
+    # roofline of the dominant kernel (k_schur): fp64 MFMA-bound; algorithmic bytes of the pass
     sc = ctx['plan'].scalars
     d, C = ctx['lay']['d'], prob.C
     T = prob.n_tracks
-    bytes_alg = n_obs * (20 + 4 * C) + T * 48 + sc['n_pairs'] * d * d * 8 + prob.n_imgs * d * 8
-    flops_pairs = (sc['n_pair_terms'] + n_obs) * 6 * d * d
-    achieved_tf = flops_pairs / (schur_ms * 1e-3) / 1e12
-    achieved_gbs = bytes_alg / (ms_step * 1e-3) / 1e9
+    alg = algorithmic_counts(prob, ctx['lay'], sc['n_pair_terms'], sc['n_pairs'])
+    achieved_tf = alg['flops_dense'] / (schur_ms * 1e-3) / 1e12
+    achieved_gbs = alg['bytes'] / (ms_step * 1e-3) / 1e9
     traffic, traffic_src = measured_traffic(args.config)
+    pass_traffic = pass_counter_traffic(args.config)
 
     # full LM iterations
     lm_ms = None
@@ -147,9 +147,11 @@ def main():
     lay = bench_layout(prob, g, dev, args.steps, args.warmup) if args.layout else None
     tan = bench_tangent(prob, g, dev, args.steps, args.warmup) if args.tangent else None
 
+    pm = bench_pairmajor(args.pm_config, dev, args.steps, args.warmup) if args.pm_config >= 0 else None
+
     cpu = None
     if args.cpu_baseline:
-        cpu = cpu_baseline(args.config)
+        cpu = cpu_baseline(args.config, prob)
         log(f'[bench] cpu baseline {cpu}')
 
     triad = stream_triad(dev)
@@ -166,10 +168,20 @@ def main():
         'lm_ms_per_iter': lm_ms,
         'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
                      'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': 'k_schur',
-                     'kernel_ms': schur_ms, 'flops_per_launch': flops_pairs, 'traffic_source': traffic_src},
+                     'kernel_ms': schur_ms, 'flops_per_launch': alg['flops_dense'], 'd_alg': alg['d_alg'],
+                     'pair_terms': sc['n_pair_terms'],
+                     'flops_rule': '6 d_alg^2 per pair of observations of a track (sum over tracks of m(m+1)/2)',
+                     'structured_flops_per_launch': alg['flops_structured'],
+                     'structured_achieved': alg['flops_structured'] / (schur_ms * 1e-3) / 1e12,
+                     'structured_rule': alg['structured_rule'], 'traffic_source': traffic_src},
         'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
-                         'bytes_per_step': bytes_alg, 'scope': 'linearize + Schur pass (all stage kernels)',
-                         'achievable_triad': triad},
+                         'bytes_per_step': alg['bytes'], 'bytes_rule': alg['bytes_rule'],
+                         'scope': 'linearize + Schur pass (all stage kernels)', 'achievable_triad': triad,
+                         'pass_counter_traffic': pass_traffic['bytes'] if pass_traffic else None,
+                         'pass_counter_traffic_over_alg': (pass_traffic['bytes'] / alg['bytes']) if pass_traffic
+                         else None,
+                         'pass_counter_kernels': pass_traffic['kernels'] if pass_traffic else None},
+        'pairmajor': pm,
         'cpu_baseline': cpu,
         'f_sampling': smp,
         'layout': lay,
@@ -393,6 +405,128 @@ def bench_sampling(prob, g, dev, steps, warmup, cfg):
             'torch_grid_sample_per_frame_ms': ref_ms}
 
 
+def algorithmic_counts(prob, lay, n_pair_terms, n_pairs):
+    """Algorithmic flops and bytes of one linearize + Schur pass.
+
+    d_alg is the per-image block the reduced system needs: 6 pose + C depth coefficients + 2 focal
+    parameters when every image has its own camera; a focal shared by all images (mono) is a border
+    of 2 unknowns accumulated per track, not per image pair, so it is not in d_alg.
+      dense flops: 6 d_alg^2 per pair of observations of one track (S_ij -= V_i V_j^T with V d x 3),
+        summed over tracks as m(m+1)/2 pairs;
+      structured flops: the same products with the depth-coefficient block of V of rank one (the
+        z-coefficient Jacobian is dep_c times one row): per pair 2 x (3*36 pose-pose + 2*(18 + 6C)
+        pose-depth + (3 + C^2) depth-depth [+ per-image focal: 12 + 2*36 + 2*(6 + 2C)]) MACs for
+        the enabled blocks;
+      bytes: per observation pid 4 + pix 8 + std 8 + dep 4C read, per track point 12 + H_pp^-1 24
+        + g_p 12, per reduced block 4 d_alg^2 written once, per image 4 d_alg."""
+    C = prob.C
+    hasP, hasZ = bool(lay['hasP']), bool(lay['hasZ'])
+    per_image_K = bool(lay['hasK']) and len(prob.K) == prob.n_imgs and prob.n_imgs > 1
+    d_alg = 6 * hasP + C * hasZ + 2 * per_image_K
+    mac = 0
+    if hasP:
+        mac += 3 * 36
+    if hasP and hasZ:
+        mac += 2 * (18 + 6 * C)
+    if hasZ:
+        mac += 3 + C * C
+    if per_image_K:
+        mac += 12 + (2 * 36 if hasP else 0) + (2 * (6 + 2 * C) if hasZ else 0)
+    return {'d_alg': d_alg,
+            'flops_dense': n_pair_terms * 6 * d_alg * d_alg,
+            'flops_structured': n_pair_terms * 2 * mac,
+            'structured_rule': f'{2 * mac} flops per pair (rank-one depth block; pose {hasP}, depth {hasZ}, '
+                               f'per-image focal {per_image_K})',
+            'bytes': prob.n_obs * (20 + 4 * C) + prob.n_tracks * 48 + n_pairs * 4 * d_alg * d_alg
+            + prob.n_imgs * 4 * d_alg,
+            'bytes_rule': 'N (20 + 4C) + T 48 + N_blk 4 d_alg^2 + F 4 d_alg'}
+
+
+PASS_KERNELS = ['k_track_pp', 'k_point_factor', 'k_schur', 'k_pair_reduce', 'k_img_reduce']
+
+
+def pass_counter_traffic(cfg):
+    """HBM bytes of one batched linearize + Schur pass from the committed counter summaries of its
+    kernels (None unless every one is present)."""
+    tot, kernels = 0, {}
+    for k in PASS_KERNELS:
+        b, _ = measured_traffic(cfg, k)
+        if b is None:
+            return None
+        tot += b
+        kernels[k] = b
+    return {'bytes': tot, 'kernels': kernels}
+
+
+def bench_pairmajor(cfg, dev, steps, warmup):
+    """The pair-major linearize + Schur pass (ba_pm_linearize_schur) on configuration `cfg` at full
+    size, inputs resident: observations per second of the pass (HIP events around the launches on
+    their stream) and one full lm_step.  Configuration 3 (random co-visibility) is where the solver
+    chooses this path."""
+    from blast3r_amd import cujac, engine
+    from blast3r_amd._lib import check, lib
+    from blast3r_amd.ba_solver import GaussNewtonSolver, _param_state
+    from blast3r_amd.synthetic import make_problem
+    t0 = time.time()
+    prob = make_problem(cfg)
+    g = prob.to(dev)
+    o = prob.options
+    hp = dict(weight_z=o['weight_z'], pnorm=o['pnorm'], max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d,
+                                            g.pix2d_std, g.pix2d_dep, True, hp['weight_z'], hp['pnorm'],
+                                            hp['max_pix_err'], hp['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, path='pairmajor')
+    J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                             g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
+    res._ba_state = _param_state(J)
+    ctx = gs.prepare(J, res, w)
+    torch.cuda.synchronize()
+    sc = ctx['plan'].scalars
+    log(f'[bench] pair-major cfg {cfg}: {prob.n_obs} obs, generated + planned in {time.time() - t0:.1f}s: {sc}')
+    a, st = ctx['args'], ctx['stream']
+    L = lib()
+    for _ in range(warmup):
+        check(L.ba_pm_linearize_schur(a, st))
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        check(L.ba_pm_linearize_schur(a, st))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
+              optim_P=o['optim_P'])
+    engine.lm_step(**g.lm_inputs(), **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_lm = 2
+    for _ in range(n_lm):
+        engine.lm_step(**g.lm_inputs(), **kw)
+    torch.cuda.synchronize()
+    lm_ms = (time.perf_counter() - t0) * 1e3 / n_lm
+    alg = algorithmic_counts(prob, ctx['lay'], sc['n_terms'] + prob.n_obs, sc['n_pairs'])
+    v_bytes = sc['n_terms'] * 2 * 3 * (16 if ctx['lay']['d'] <= 15 else 32) * 8
+    pairs_traffic, src = measured_traffic(cfg, 'k_pm_pairs')
+    log(f'[bench] pair-major cfg {cfg}: linearize+Schur {ms:.3f} ms -> {prob.n_obs / (ms * 1e-3):.4g} obs/s; '
+        f'lm_step {lm_ms:.2f} ms')
+    res = {'config': f'cfg{cfg}: {prob.n_imgs} frames, {prob.n_tracks} tracks, {prob.n_obs} observations, C={prob.C}, '
+                     f'd={ctx["lay"]["d"]}',
+           'ms_per_step': ms, 'obs_per_s': prob.n_obs / (ms * 1e-3), 'lm_ms_per_iter': lm_ms,
+           'lm_iters_per_s': 1e3 / lm_ms, 'runs': sc['n_runs'], 'pairs': sc['n_pairs'], 'pair_terms': sc['n_terms'],
+           'hbm_roofline': {'achieved': alg['bytes'] / (ms * 1e-3) / 1e9, 'peak': 8000.0, 'unit': 'GB/s',
+                            'frac': alg['bytes'] / (ms * 1e-3) / 1e9 / 8000.0, 'bytes_per_step': alg['bytes'],
+                            'bytes_rule': alg['bytes_rule']},
+           'k_pm_pairs': {'bound': 'hbm', 'v_bytes_per_launch': v_bytes,
+                          'v_rule': 'two V rows (3 x dp fp64) read per pair term',
+                          'traffic': pairs_traffic, 'traffic_source': src}}
+    del gs, J, ctx, g, prob
+    torch.cuda.empty_cache()
+    return res
+
+
 def measured_traffic(cfg, kernel='k_schur'):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary of this workload
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a plain copy of known size),
@@ -405,37 +539,81 @@ def measured_traffic(cfg, kernel='k_schur'):
     return rec['hbm_bytes_per_launch'], os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
 
 
-def cpu_baseline(cfg, reps=3):
-    """Oracle (torch-CPU restatement of the reference's linearisation + normal equations + Schur
-    rhs) on the full configuration, timed on this host over `reps` passes (about 10-30 s of CPU
-    work at configuration 2)."""
+def host_cpu():
+    """Model name and logical CPU count of this host (the CPU baseline's machine)."""
+    model = None
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'model': model, 'logical_cpus': os.cpu_count()}
+
+
+CPU_PCG_CAP = 5
+
+
+def cpu_baseline(cfg, prob=None):
+    """The oracle (torch-CPU restatement of the reference's path) on the full configuration, on this
+    host's CPU share (OMP_NUM_THREADS when set, as on the GPU boxes, else every logical CPU):
+      * value: observations per second of one linearize + Schur-rhs pass in fp64 (residuals, fp64
+        Jacobians, normal equations, reduced rhs), the reference's solver dtype;
+      * fp32: the same pass with fp32 Jacobians and normal equations;
+      * lm_step: one full oracle lm_step (objective, linearisation, Schur, PCG capped at CPU_PCG_CAP
+        iterations, back-substitution, line search) -- LM iterations per second at that cap, and the
+        time of one PCG iteration (one S v product of the Schur operator plus the vector work), from
+        which the 300-iteration step is estimated.
+    About 20-60 s of CPU work at configuration 2."""
     import oracle.kernels as ok
     import oracle.solver as osol
     import oracle.engine as oeng
     from blast3r_amd.synthetic import make_problem
-    threads = min(16, os.cpu_count() or 1)
+    threads = int(os.environ.get('OMP_NUM_THREADS') or 0) or (os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    p = make_problem(cfg)
+    p = prob if prob is not None else make_problem(cfg)
     o = p.options
-    times = []
-    for _ in range(reps):
+
+    def npass(float64):
         t0 = time.perf_counter()
         loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
                                       p.pix2d_std, p.pix2d_dep, True, o['weight_z'], o['pnorm'], o['clip_pix_err'],
                                       o['huber_delta'])
         Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
-                                            p.pix2d_std, p.pix2d_dep, True, float64=True)
-        prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
-        ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_K=o['optim_K'],
-                                                    optim_P=o['optim_P'])
-        osol.reduced_rhs(ne, g)
-        times.append(time.perf_counter() - t0)
-        del Jc, Jz, Jp, ne, g, params
-    dt = sum(times) / len(times)
-    return {'value': p.n_obs / dt, 'unit': 'obs/s', 'cores': threads, 'kind': 'port',
-            'sample': f'the full cfg{cfg} workload ({p.n_imgs} frames, '
-                      f'{p.n_tracks} tracks, {p.n_obs} obs), {reps} passes of residuals, fp64 Jacobians, normal '
-                      f'equations and Schur rhs in the oracle: {sum(times):.1f} s in total, {dt:.2f} s per pass'}
+                                            p.pix2d_std, p.pix2d_dep, True, float64=float64)
+        pr = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+        ne, g, params = osol.build_normal_equations(pr, Jc, Jz, Jp, res, w, optim_K=o['optim_K'], optim_P=o['optim_P'])
+        rhs = osol.reduced_rhs(ne, g)
+        dt = time.perf_counter() - t0
+        return dt, ne, rhs
+
+    dt64, ne, rhs = npass(True)
+    # one PCG iteration's operator: S v plus the preconditioner and vector updates
+    v = torch.randn(rhs.shape[0], dtype=torch.float64)
+    t0 = time.perf_counter()
+    osol.S_matvec(ne, v)
+    t_mv = time.perf_counter() - t0
+    del ne
+    dt32, ne32, _ = npass(False)
+    del ne32
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], clip_pix_err=o['clip_pix_err'],
+              optim_K=o['optim_K'], optim_P=o['optim_P'])
+    t0 = time.perf_counter()
+    _, st, info = oeng.lm_step(**p.lm_inputs(), **kw, pcg_maxiter=CPU_PCG_CAP)
+    t_lm = time.perf_counter() - t0
+    est300 = t_lm + (300 - CPU_PCG_CAP) * t_mv
+    return {'value': p.n_obs / dt64, 'unit': 'obs/s', 'cores': threads, 'kind': 'port',
+            'sample': f'the full cfg{cfg} workload ({p.n_imgs} frames, {p.n_tracks} tracks, {p.n_obs} obs): one '
+                      f'fp64 pass of residuals, Jacobians, normal equations and Schur rhs in the oracle ({dt64:.2f} s), '
+                      f'the fp32 variant ({dt32:.2f} s), one S v product ({t_mv:.2f} s) and one oracle lm_step with '
+                      f'PCG capped at {CPU_PCG_CAP} iterations ({t_lm:.2f} s, {info["trials"]} line-search trials)',
+            'host': host_cpu(), 'threads': threads,
+            'fp32_obs_per_s': p.n_obs / dt32,
+            'lm_step_s_at_pcg_cap': t_lm, 'pcg_cap': CPU_PCG_CAP, 'lm_iters_per_s_at_pcg_cap': 1.0 / t_lm,
+            'pcg_iteration_s': t_mv, 'lm_step_s_estimated_300_pcg': est300,
+            'lm_iters_per_s_estimated_300_pcg': 1.0 / est300}
 
 
 if __name__ == '__main__':

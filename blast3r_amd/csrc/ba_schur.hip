@@ -1411,7 +1411,7 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
 #pragma unroll
             for (int h = 0; h < NT; ++h) {
                 A[g][h] = ma * a.V[oa + 16 * h];
-                B[g][h] = mb * a.V[ob + 16 * h];
+                B[g][h] = mb * __builtin_nontemporal_load(a.V + ob + 16 * h);
             }
         }
     };
