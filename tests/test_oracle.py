@@ -236,6 +236,32 @@ def test_normal_equations_match_dense_products():
     assert rel_err(osol._B_matvec(ne, y), Hd[:n_c, n_c:] @ y) < 1e-7
 
 
+def test_track_mask_drops_the_disabled_tracks_columns():
+    """A tensor optim_X (per track) gives the normal equations of the dense Jacobian with the
+    disabled tracks' point columns deleted and the enabled ones kept in order (the per-track
+    reading of enable(), ba_solver.py:72-108, for a track mask)."""
+    p = tiny_problem(0, n_frames=5, n_tracks=40)
+    mask = torch.arange(p.n_tracks) % 3 != 0
+    o = p.options
+    _, res, w = oe.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d, p.pix2d_std,
+                             p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'], o['huber_delta'])
+    Jc, Jz, Jp = ok.jacobians_with_rigs(*_jac_inputs(p), True, float64=True)
+    prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
+    ne, g, params = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_X=mask)
+    Jd = od.dense_jacobian(Jc, Jz, Jp, p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks)
+    n_c = 2 * len(p.K) + 6 * len(p.P_w2rig) + p.C * p.n_imgs
+    en = torch.nonzero(mask).squeeze(-1)
+    keep = torch.cat([torch.arange(n_c), (n_c + 3 * en[:, None] + torch.arange(3)).reshape(-1)])
+    sizes = (2 * len(p.K), 6 * len(p.P_w2rig), p.C * p.n_imgs, 3 * len(en))
+    Hd, gd = od.dense_normal_equations(Jd[:, keep], res, w, sizes)
+    assert ne.sizes['n_c'] == n_c and g.shape == gd.shape
+    assert rel_err(g, gd) < 1e-7
+    assert rel_err(osol.dense_A(ne), Hd[:n_c, :n_c]) < 1e-7
+    assert rel_err(torch.block_diag(*ne.leaves['pts']), Hd[n_c:, n_c:]) < 1e-7
+    y = torch.randn(3 * len(en), dtype=torch.float64)
+    assert rel_err(osol._B_matvec(ne, y), Hd[:n_c, n_c:] @ y) < 1e-7
+
+
 def test_schur_identity_symmetry_psd_and_gauge():
     """Reduced solve + back-substitution equals the dense solve of the damped system; S is symmetric
     PSD; the seven similarity directions lie in its (near-)nullspace (damping 1e-12 max diag)."""
