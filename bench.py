@@ -44,6 +44,8 @@ def main():
                     help='also time the observation-structure edits (old | new merge, remove, plan rebuild)')
     ap.add_argument('--tangent', type=int, default=1,
                     help='also time the dense tangent prior on maps of the configuration (1 = yes)')
+    ap.add_argument('--reduced-solve', type=int, default=1,
+                    help='also time the reduced-system Cholesky (ba_reduced_solve, dense and banded) on the config')
     ap.add_argument('--pm-config', type=int, default=3,
                     help='also time the pair-major path on this configuration at full size (-1 = no)')
     ap.add_argument('--copy-probe', action='store_true',
@@ -143,6 +145,7 @@ def main():
         lm_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
         log(f'[bench] lm_step {lm_ms:.2f} ms')
 
+    red = bench_reduced_solve(prob, g, dev, args.warmup) if args.reduced_solve else None
     smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
     lay = bench_layout(prob, g, dev, args.steps, args.warmup) if args.layout else None
     tan = bench_tangent(prob, g, dev, args.steps, args.warmup) if args.tangent else None
@@ -182,6 +185,7 @@ def main():
                          else None,
                          'pass_counter_kernels': pass_traffic['kernels'] if pass_traffic else None},
         'pairmajor': pm,
+        'reduced_solve': red,
         'cpu_baseline': cpu,
         'f_sampling': smp,
         'layout': lay,
@@ -537,6 +541,66 @@ def measured_traffic(cfg, kernel='k_schur'):
     with open(path) as f:
         rec = json.load(f)
     return rec['hbm_bytes_per_launch'], os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
+
+
+def bench_reduced_solve(prob, g, dev, warmup, reps=5):
+    """The reduced-system Cholesky (ba_reduced_solve, solver='cholesky') on the configuration's
+    damped reduced system, dense and banded layouts: the bare launch sequence (assembly of S_u from
+    the image-pair blocks, factorisation, both triangular sweeps) timed with events on its stream,
+    beside the device PCG's solve.  fp64 flops: dense n^3/3 + 2 n^2; banded n b^2 + 4 n b with b the
+    scalar bandwidth (w + 1) d_band."""
+    from blast3r_amd._lib import check, lib
+    from blast3r_amd.ba_solver import GaussNewtonSolver
+    o = prob.options
+    hp = dict(weight_z=o['weight_z'], pnorm=o['pnorm'], max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    from blast3r_amd import cujac
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d,
+                                            g.pix2d_std, g.pix2d_dep, True, hp['weight_z'], hp['pnorm'],
+                                            hp['max_pix_err'], hp['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    L = lib()
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    result = {}
+    for layout in ('banded', 'dense'):
+        gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, solver='cholesky',
+                               cholesky_layout=layout)
+        J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
+        try:
+            gs.solve_delta(J, res, w)
+        except RuntimeError as e:
+            result[layout] = {'error': str(e)}
+            continue
+        info = gs.last['direct']
+        if info is None or info.get('first_bad_pivot') is not None or info['layout'] != layout:
+            result[layout] = {'error': f'not run as {layout}: {info}'}
+            continue
+        pa, ca = gs.last['direct_call']
+        for _ in range(warmup):
+            check(L.ba_reduced_solve(pa, ca, st))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            check(L.ba_reduced_solve(pa, ca, st))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        n = int(pa.n_u)
+        if layout == 'dense':
+            flops = n ** 3 / 3 + 2 * n * n
+        else:
+            b = (info['w'] + 1) * info['db']
+            flops = n * b * b + 4 * n * b
+        result[layout] = {'ms': ms, 'unknowns': n, 'flops': flops, 'achieved_tflops': flops / (ms * 1e-3) / 1e12,
+                          'frac_of_fp64_peak': flops / (ms * 1e-3) / 1e12 / 78.6, 'w': info['w'], 'd_band': info['db'],
+                          'shared': info['n_shared']}
+        log(f'[bench] reduced solve ({layout}): {ms:.2f} ms for {n} unknowns, '
+            f'{flops / (ms * 1e-3) / 1e12:.2f} TFLOP/s fp64')
+        del gs, J
+    torch.cuda.empty_cache()
+    return result
 
 
 def host_cpu():

@@ -545,6 +545,7 @@ class GaussNewtonSolver:
             ca.A = ptr(ws('chol_A', (lda, lda), torch.float64))
             ca.Linv = ptr(ws('chol_Linv', (lda // 64, 64, 64), torch.float64))
         check(L.ba_reduced_solve(pa, ca, st))
+        self.last['direct_call'] = (pa, ca)    # kept for re-timing the bare launch sequence
         bad = int(info.cpu())                  # one read per solve
         self.last['direct'] = dict(layout=layout, w=w, db=db, n_shared=ns,
                                    first_bad_pivot=None if bad == 2 ** 31 - 1 else bad)
