@@ -86,15 +86,24 @@ def main():
     log(f'[bench] plan + slot data in {time.time() - t0:.1f}s: {ctx["plan"].scalars}')
     a, st = ctx['args'], ctx['stream']
     L = lib()
+    pm_path = ctx['path'] == 'pairmajor'          # config 3 (random co-visibility) or d > 15
 
     def step(ev=None):
-        check(L.ba_linearize_stage(a, 0, st))
+        # events bracket the dominant kernel: k_schur (batched stage 1) or k_pm_pairs (pair-major stage 1)
+        if pm_path:
+            check(L.ba_pm_linearize_stage(a, 0, st))
+        else:
+            check(L.ba_linearize_stage(a, 0, st))
         if ev is not None:
             ev[0].record()
-        check(L.ba_linearize_stage(a, 1, st))
+        if pm_path:
+            check(L.ba_pm_linearize_stage(a, 1, st))
+        else:
+            check(L.ba_linearize_stage(a, 1, st))
         if ev is not None:
             ev[1].record()
-        check(L.ba_linearize_stage(a, 2, st))
+        if not pm_path:
+            check(L.ba_linearize_stage(a, 2, st))
 
     for _ in range(args.warmup):
         step()
@@ -110,7 +119,9 @@ def main():
     schur_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / args.steps
     n_obs = prob.n_obs
     value = n_obs / (ms_step * 1e-3)
-    log(f'[bench] linearize+Schur {ms_step:.3f} ms/step, k_schur {schur_ms:.3f} ms -> {value:.4g} obs/s')
+    kname = 'k_pm_pairs' if pm_path else 'k_schur'
+    log(f'[bench] linearize+Schur {ms_step:.3f} ms/step ({ctx["path"]} path), {kname} {schur_ms:.3f} ms -> '
+        f'{value:.4g} obs/s')
 
     if args.copy_probe:
         # byte-counter calibration: a fill (writes 256 MiB) and a kernel copy (reads 256 MiB,
@@ -125,11 +136,16 @@ def main():
     sc = ctx['plan'].scalars
     d, C = ctx['lay']['d'], prob.C
     T = prob.n_tracks
-    alg = algorithmic_counts(prob, ctx['lay'], sc['n_pair_terms'], sc['n_pairs'])
-    achieved_tf = alg['flops_dense'] / (schur_ms * 1e-3) / 1e12
+    # pair terms: every pair of observations of a track, self pairs included (batched k_schur forms
+    # them all); the pair-major k_pm_pairs forms the off-diagonal ones (its runs pass the rest)
+    pair_terms = sc['n_terms'] + n_obs if pm_path else sc['n_pair_terms']
+    kernel_terms = sc['n_terms'] if pm_path else sc['n_pair_terms']
+    alg = algorithmic_counts(prob, ctx['lay'], pair_terms, sc['n_pairs'])
+    kalg = algorithmic_counts(prob, ctx['lay'], kernel_terms, sc['n_pairs'])
+    achieved_tf = kalg['flops_dense'] / (schur_ms * 1e-3) / 1e12
     achieved_gbs = alg['bytes'] / (ms_step * 1e-3) / 1e9
-    traffic, traffic_src = measured_traffic(args.config)
-    pass_traffic = pass_counter_traffic(args.config)
+    traffic, traffic_src = measured_traffic(args.config, kname)
+    pass_traffic = pass_counter_traffic(args.config, PM_PASS_KERNELS if pm_path else PASS_KERNELS)
 
     # full LM iterations
     lm_ms = None
@@ -165,18 +181,20 @@ def main():
         'ms_per_step': ms_step, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f64',
         'data': 'synthetic (seeded generator, benchmark config %d)' % args.config,
         'config': {'workload': f'cfg{args.config}: {prob.n_imgs} frames, {T} tracks, {n_obs} observations, '
-                               f'C={C}, d={d} image-level parameters', 'frames': prob.n_imgs, 'tracks': T,
-                   'observations': n_obs, 'C': C},
+                               f'C={C}, d={d} image-level parameters, {ctx["path"]} path', 'frames': prob.n_imgs,
+                   'tracks': T, 'observations': n_obs, 'C': C, 'path': ctx['path']},
         'lm_iters_per_s': (1e3 / lm_ms) if lm_ms else None,
         'lm_ms_per_iter': lm_ms,
         'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
-                     'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': 'k_schur',
-                     'kernel_ms': schur_ms, 'flops_per_launch': alg['flops_dense'], 'd_alg': alg['d_alg'],
-                     'pair_terms': sc['n_pair_terms'],
-                     'flops_rule': '6 d_alg^2 per pair of observations of a track (sum over tracks of m(m+1)/2)',
-                     'structured_flops_per_launch': alg['flops_structured'],
-                     'structured_achieved': alg['flops_structured'] / (schur_ms * 1e-3) / 1e12,
-                     'structured_rule': alg['structured_rule'], 'traffic_source': traffic_src},
+                     'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': kname,
+                     'kernel_ms': schur_ms, 'flops_per_launch': kalg['flops_dense'], 'd_alg': kalg['d_alg'],
+                     'pair_terms': kernel_terms,
+                     'flops_rule': ('6 d_alg^2 per pair of observations of a track in two images (the off-diagonal '
+                                    'terms)' if pm_path else
+                                    '6 d_alg^2 per pair of observations of a track (sum over tracks of m(m+1)/2)'),
+                     'structured_flops_per_launch': kalg['flops_structured'],
+                     'structured_achieved': kalg['flops_structured'] / (schur_ms * 1e-3) / 1e12,
+                     'structured_rule': kalg['structured_rule'], 'traffic_source': traffic_src},
         'hbm_roofline': {'achieved': achieved_gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': achieved_gbs / 8000.0,
                          'bytes_per_step': alg['bytes'], 'bytes_rule': alg['bytes_rule'],
                          'scope': 'linearize + Schur pass (all stage kernels)', 'achievable_triad': triad,
@@ -447,13 +465,14 @@ def algorithmic_counts(prob, lay, n_pair_terms, n_pairs):
 
 
 PASS_KERNELS = ['k_track_pp', 'k_point_factor', 'k_schur', 'k_pair_reduce', 'k_img_reduce']
+PM_PASS_KERNELS = ['k_pm_obs', 'k_pm_track', 'k_point_factor', 'k_pm_runs', 'k_pm_diag', 'k_pm_pairs']
 
 
-def pass_counter_traffic(cfg):
-    """HBM bytes of one batched linearize + Schur pass from the committed counter summaries of its
-    kernels (None unless every one is present)."""
+def pass_counter_traffic(cfg, kernels_of_pass=PASS_KERNELS):
+    """HBM bytes of one linearize + Schur pass from the committed counter summaries of its kernels
+    (None unless every one is present)."""
     tot, kernels = 0, {}
-    for k in PASS_KERNELS:
+    for k in kernels_of_pass:
         b, _ = measured_traffic(cfg, k)
         if b is None:
             return None

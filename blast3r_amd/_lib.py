@@ -164,6 +164,7 @@ _SIGS = {
     'ba_pm_plan_export': (c_int, [c_p, c_int, c_p]),
     'ba_pm_plan_destroy': (None, [c_p]),
     'ba_pm_linearize_schur': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
+    'ba_pm_linearize_stage': (c_int, [ctypes.POINTER(BaPmArgs), c_int, c_p]),
     'ba_pm_backsubstitute': (c_int, [ctypes.POINTER(BaPmArgs), c_p]),
     'ba_pm_slot_doubles': (c_i64, [c_i64, c_int, c_int]),
     'ba_chol_band_lds_bytes': (c_i64, [c_int, c_int, c_int]),

@@ -1519,9 +1519,10 @@ extern "C" int64_t ba_pm_slot_doubles(int64_t n_items, int32_t n_imgs, int32_t d
     return ((n_items + PM_SPAN - 1) / PM_SPAN + n_imgs) * ntl * 256;
 }
 
-extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
+extern "C" int ba_pm_linearize_stage(const ba_pm_args* args, int stage, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
+    BA_REQUIRE(stage == 0 || stage == 1, "stage must be 0 (observations, tracks, runs, images) or 1 (pairs)");
     const ba_pm_args& a = *args;
     hipStream_t st = (hipStream_t)stream;
     BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 31, "pair-major path supports 1 <= d <= 31 image-level parameters");
@@ -1537,6 +1538,15 @@ extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
                "Hpp, pfac and wobs must be 16-byte aligned");
     const int64_t nbt = (a.n_tracks + PM_T - 1) / PM_T;
     const bool wide = a.lay.d > 15;
+    if (stage == 1) {
+        if (a.n_pairs > 0) {
+            const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
+            if (wide) hipLaunchKernelGGL(k_pm_pairs<32>, dim3(g), dim3(PM_T), 0, st, a);
+            else      hipLaunchKernelGGL(k_pm_pairs<16>, dim3(g), dim3(PM_T), 0, st, a);
+        }
+        BA_LAUNCHED();
+        return BA_OK;
+    }
     hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.tmax, nbt);
     if (a.n_obs > 0) {
         const unsigned g = (unsigned)((a.n_obs + PM_SPAN - 1) / PM_SPAN);
@@ -1564,13 +1574,13 @@ extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
     }
     if (wide) hipLaunchKernelGGL(k_pm_diag<32>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
     else      hipLaunchKernelGGL(k_pm_diag<16>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
-    if (a.n_pairs > 0) {
-        const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
-        if (wide) hipLaunchKernelGGL(k_pm_pairs<32>, dim3(g), dim3(PM_T), 0, st, a);
-        else      hipLaunchKernelGGL(k_pm_pairs<16>, dim3(g), dim3(PM_T), 0, st, a);
-    }
     BA_LAUNCHED();
     return BA_OK;
+}
+
+extern "C" int ba_pm_linearize_schur(const ba_pm_args* args, void* stream) {
+    const int rc = ba_pm_linearize_stage(args, 0, stream);
+    return rc != BA_OK ? rc : ba_pm_linearize_stage(args, 1, stream);
 }
 
 extern "C" int ba_pm_backsubstitute(const ba_pm_args* args, void* stream) {

@@ -205,6 +205,9 @@ typedef struct {
 } ba_pm_args;
 
 int ba_pm_linearize_schur(const ba_pm_args* args, void* stream);
+/* the same in two launches sequences: stage 0 = observations, tracks, damping, point factors, runs and
+ * per-image blocks; stage 1 = the off-diagonal pair blocks (k_pm_pairs), for timing them apart */
+int ba_pm_linearize_stage(const ba_pm_args* args, int stage, void* stream);
 /* doubles of one slot array of ba_pm_args (n_items = n_obs for jslots, n_runs for vslots); -1 for d
  * outside 1..31 */
 int64_t ba_pm_slot_doubles(int64_t n_items, int32_t n_imgs, int32_t d);
