@@ -256,7 +256,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     struct BatchOut {
         std::vector<int32_t> chunk_obs, slot_info, chunk_meta, ct_pid, ct_first, ct_m, ct_mask, slot_pair,
             chunk_slots, chunk_eptr, pos_slot;
-        std::vector<uint16_t> ents;
+        std::vector<uint32_t> ents;
         bool overflow = false;
     };
     const int n_batches = (int)batches.size();
@@ -307,39 +307,44 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
 
             // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
             // first observation of each covering track in a with the one in b (chunk-track order);
-            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order), then
-            // the V rows of the first observation of each (track, image) run in a (slot order)
+            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order, padded
+            // to whole groups), then the V rows of the first observation of each (track, image) run
+            // in a (slot order)
             lead.assign((size_t)ntr * BA_MAX_LOCAL, -1);
             for (int sidx = 0; sidx < used; ++sidx) {
                 const int inf = R.slot_info[base + sidx];
                 lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
             }
             const size_t e0 = R.ents.size();
-            R.chunk_eptr.push_back((int32_t)(e0 / 8));
-            auto ent = [&](int sa, int sb, int kind) { R.ents.push_back((uint16_t)(sa | (sb << 7) | (kind << 14))); };
+            R.chunk_eptr.push_back((int32_t)(e0 / 4));
+            auto ent = [&](int oa, int ob) { R.ents.push_back((uint32_t)oa | ((uint32_t)ob << 16)); };
+            auto pad = [&](size_t from) { while ((R.ents.size() - from) % 4) ent(BA_ZERO, BA_ZERO); };
             for (int q = 0; q < BA_MAX_SLOTS; ++q) {
                 if (q >= nsl) { R.chunk_slots.push_back(0); continue; }
                 const int a = R.slot_pair[q] & 0xff, bq = (R.slot_pair[q] >> 8) & 0xff;
                 const size_t off = R.ents.size() - e0;
+                int njg = 0;
                 if (a != bq) {
                     for (int tt = 0; tt < ntr; ++tt) {
                         const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
-                        if (la_ >= 0 && lb_ >= 0) ent(la_, lb_, BA_ENT_V);
+                        if (la_ >= 0 && lb_ >= 0) ent(la_ * BA_BLK, lb_ * BA_BLK);
                     }
                 } else {
                     for (int sidx = 0; sidx < used; ++sidx)
-                        if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx, sidx, BA_ENT_J);
+                        if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx * BA_BLK + BA_JROW, sidx * BA_BLK + BA_JROW);
+                    pad(e0 + off);
+                    njg = (int)((R.ents.size() - e0 - off) / 4);
                     for (int sidx = 0; sidx < used; ++sidx) {
                         const int inf = R.slot_info[base + sidx];
-                        if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx, sidx, BA_ENT_V);
+                        if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx * BA_BLK, sidx * BA_BLK);
                     }
                 }
-                while ((R.ents.size() - e0 - off) % 4) ent(0, 0, BA_ENT_PAD);
+                pad(e0 + off);
                 const size_t len = R.ents.size() - e0 - off;
-                R.chunk_slots.push_back((int32_t)(off | (len << 16)));
+                R.chunk_slots.push_back(BA_TAB(off, len / 4, njg));
             }
             if (R.ents.size() - e0 > BA_LIST_CAP) R.overflow = true;
-            while ((R.ents.size() - e0) % 8) R.ents.push_back(0);
+            while ((R.ents.size() - e0) % 4) R.ents.push_back(0);
         }
         // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
         // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
@@ -351,8 +356,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             std::vector<int64_t> tot(nsl, 0);
             for (int c = 0; c < nc; ++c)
                 for (int q = 0; q < nsl; ++q) {
-                    const int len = R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q] >> 16;
-                    wk[(size_t)c * nsl + q] = 3 * (len / 4);
+                    wk[(size_t)c * nsl + q] = 3 * BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]);
                     tot[q] += wk[(size_t)c * nsl + q];
                 }
             std::vector<int> sorder(nsl);
@@ -419,7 +423,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     auto& slot_pair = P->v[BA_PA_SLOT_PAIR];      // per slot: a | b << 8  (a <= b local)
     auto& slot_gpair = P->v[BA_PA_SLOT_GPAIR];    // per slot: global pair id
     auto& chunk_slots = P->v[BA_PA_CHUNK_SLOTS];  // n_chunks * BA_MAX_SLOTS
-    auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 16-bit entries, two per word
+    auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 32-bit entries
     auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks
     auto& b_pos_slot = P->v[BA_PA_B_POS_SLOT];    // n_batches * BA_MAX_SLOTS
     bool list_overflow = false;
@@ -442,15 +446,15 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     chunk_eptr.resize(o_ch[n_batches]);
     for (auto* v : {&ct_pid, &ct_first, &ct_m, &ct_mask}) v->resize(o_ct[n_batches]);
     slot_pair.resize(o_sl[n_batches]);
-    // entries two per word, and one chunk's worth of zero padding so that a full-capacity copy of
-    // the last chunk's list stays inside the array
-    chunk_ent.assign((size_t)((o_en[n_batches] + BA_LIST_CAP + 1) / 2), 0);
-    uint16_t* ents = reinterpret_cast<uint16_t*>(chunk_ent.data());
+    // the entries, and one chunk's worth of zero padding so that a full-capacity copy of the last
+    // chunk's list stays inside the array
+    chunk_ent.assign((size_t)(o_en[n_batches] + BA_LIST_CAP), 0);
+    uint32_t* ents = reinterpret_cast<uint32_t*>(chunk_ent.data());
     b_pos_slot.resize((size_t)n_batches * BA_MAX_SLOTS);
     parallel_for(n_batches, [&](int64_t b0, int64_t b1) {
         for (int64_t b = b0; b < b1; ++b) {
             BatchOut& R = outs[b];
-            const int32_t ct0 = (int32_t)o_ct[b], e8 = (int32_t)(o_en[b] / 8);
+            const int32_t ct0 = (int32_t)o_ct[b], e4 = (int32_t)(o_en[b] / 4);
             std::copy(R.chunk_obs.begin(), R.chunk_obs.end(), chunk_obs.begin() + o_ch[b] * BA_CHUNK);
             for (size_t q = 0; q < R.chunk_obs.size(); ++q) {
                 const int32_t o = R.chunk_obs[q];
@@ -470,7 +474,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             std::copy(R.ct_mask.begin(), R.ct_mask.end(), ct_mask.begin() + o_ct[b]);
             std::copy(R.slot_pair.begin(), R.slot_pair.end(), slot_pair.begin() + o_sl[b]);
             std::copy(R.chunk_slots.begin(), R.chunk_slots.end(), chunk_slots.begin() + o_ch[b] * BA_MAX_SLOTS);
-            for (size_t c = 0; c < R.chunk_eptr.size(); ++c) chunk_eptr[o_ch[b] + c] = R.chunk_eptr[c] + e8;
+            for (size_t c = 0; c < R.chunk_eptr.size(); ++c) chunk_eptr[o_ch[b] + c] = R.chunk_eptr[c] + e4;
             std::copy(R.ents.begin(), R.ents.end(), ents + o_en[b]);
             std::copy(R.pos_slot.begin(), R.pos_slot.end(), b_pos_slot.begin() + b * BA_MAX_SLOTS);
             R = BatchOut();                                    // release as we go

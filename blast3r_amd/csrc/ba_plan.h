@@ -31,9 +31,9 @@ enum {
     BA_PA_ROW_ENT,
     BA_PA_IMG_PTR,
     BA_PA_IMG_SRC,
-    BA_PA_CHUNK_SLOTS,      // per chunk, BA_MAX_SLOTS words: entry offset | padded entry count << 16
-    BA_PA_CHUNK_ENT,        // MFMA entries of every chunk, 16 bits each (two per word), see below
-    BA_PA_CHUNK_EPTR,       // per chunk: first entry, in units of 8 entries (16 bytes)
+    BA_PA_CHUNK_SLOTS,      // per chunk, BA_MAX_SLOTS slot table words (BA_TAB, below)
+    BA_PA_CHUNK_ENT,        // MFMA entries of every chunk, 32 bits each, see below
+    BA_PA_CHUNK_EPTR,       // per chunk: first entry, in units of 4 entries (16 bytes)
     BA_PA_B_POS_SLOT,       // per batch, BA_MAX_SLOTS words: the batch slot at Schur-kernel place
                             // wave + BA_WAVES * k, or -1 (places balanced by work)
     BA_PA_SLOT_SRC,         // per chunk slot: its observation, 0 for an empty slot (a gather index)
@@ -43,12 +43,25 @@ enum {
     BA_PLAN_NARRAYS
 };
 
-// MFMA entry of a camera-pair slot: A slot (7 bits) | B slot (7 bits) << 7 | kind << 14, where the
-// slots index the chunk's observation blocks and kind is BA_ENT_V (the V rows of A and B),
-// BA_ENT_J (the J rows of A = B, A negated) or BA_ENT_PAD (the zero block).  Each slot's list is
-// padded to a multiple of 4 entries; a chunk holds at most BA_LIST_CAP entries.
-enum { BA_ENT_V = 0, BA_ENT_J = 1, BA_ENT_PAD = 2 };
+// Per-chunk LDS layout of the Schur kernel's observation blocks: slot s holds its V rows (3 x 16
+// doubles) at s * BA_BLK and its weighted camera rows J_c at s * BA_BLK + BA_JROW; a zero block of
+// 3 x 16 doubles follows the last slot at BA_ZERO.
+#define BA_BLK 97           // doubles per observation block: 6 rows x 16 columns + 1 pad (spreads banks)
+#define BA_JROW 48          // first J row of a block
+#define BA_ZERO (BA_CHUNK * BA_BLK)
+
+// MFMA entry of a camera-pair slot (32 bits): the LDS offsets, in doubles, of its A rows and its B
+// rows, A | B << 16: V rows of two observations (an off-diagonal term, or a run's own V on a
+// diagonal slot), the J rows of one observation (A = B) on a diagonal slot, or the zero block
+// (padding).  Each slot's list is padded to a multiple of 4 entries (one MFMA group); on a diagonal
+// slot the J entries come first, padded to whole groups of their own, so that every group is of one
+// kind (J groups negate A).  A chunk holds at most BA_LIST_CAP entries.
 #define BA_LIST_CAP 1536
+// slot table word of a chunk: entry offset | groups << 12 | J groups << 21
+#define BA_TAB(off, ng, njg) ((int32_t)(off) | ((int32_t)(ng) << 12) | ((int32_t)(njg) << 21))
+#define BA_TAB_OFF(t) ((t) & 0xfff)
+#define BA_TAB_NG(t) (((t) >> 12) & 0x1ff)
+#define BA_TAB_NJG(t) (((t) >> 21) & 0x3f)
 
 // plan scalars (int64)
 enum {

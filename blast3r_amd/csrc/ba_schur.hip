@@ -28,15 +28,12 @@ typedef ba_lin_args LinArgs;
 
 // ----------------------------------------------------------------------------- per observation
 #define BA_PRE_C 8          // depth-guidance channels held in registers (further channels are read from memory)
-#define BA_BLK 97           // doubles per observation block in LDS: 6 rows x 16 columns + 1 pad (spreads banks)
-#define BA_JROW 48          // first J row of a block (rows 0-2 hold V, rows 3-5 the weighted camera rows J_c)
-#define BA_ZERO (BA_CHUNK * BA_BLK)   // a zero block (3 rows) after the chunk's blocks, for padding entries
-// The MFMA entry lists come from the plan (16-bit entries, see ba_plan.h): one entry per (track,
-// image pair) of an off-diagonal slot, per observation and per (track, image) run of a diagonal
-// slot.  A chunk holds at most 128 observations of tracks spanning at most 16 images, so it has at
-// most 128 * 17 / 2 pair-and-run entries plus 128 observation entries, plus 3 of padding per slot.
-static_assert(BA_CHUNK * (BA_MAX_LOCAL + 1) / 2 + BA_CHUNK + 3 * BA_MAX_SLOTS <= BA_LIST_CAP, "entry list capacity");
-static_assert(BA_LIST_CAP * 2 % 1024 == 0 && BA_MAX_SLOTS % 4 == 0, "list copies are whole 16-byte lanes");
+// The MFMA entry lists come from the plan (32-bit entries holding the LDS offsets of the A and B
+// rows, see ba_plan.h): one entry per (track, image pair) of an off-diagonal slot, per observation
+// and per (track, image) run of a diagonal slot.  The planner rejects a chunk that would need more
+// than BA_LIST_CAP entries; the kernel copies whole lists of that capacity.
+static_assert(BA_LIST_CAP * 4 % 1024 == 0 && BA_MAX_SLOTS % 4 == 0, "list copies are whole 16-byte lanes");
+static_assert(BA_ZERO + 48 < 65536 && BA_LIST_CAP < 4096, "entry offsets fit their fields");
 #define BA_CORE 20          // doubles per observation in the linearisation record
 static_assert(BA_CORE * BA_CHUNK % 256 == 0, "a chunk's record block is copied 256 doubles at a time");
 
@@ -449,6 +446,44 @@ __device__ __forceinline__ void dma16_to_lds(const void* src, void* wave_dst) {
     __builtin_amdgcn_global_load_lds((glob_void*)src, (lds_void*)wave_dst, 16, 0, 0);
 }
 
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// LDS reads of the MFMA phase, issued from inline asm.  The next chunk's inputs are being copied
+// into LDS (global_load_lds) while the MFMA phase runs, and the compiler cannot tell that these
+// reads touch other arrays, so a read it issued itself would first wait for the whole copy
+// (vmcnt 0).  lds_rd* issue reads the compiler does not wait for; lds_wait waits for every
+// outstanding LDS read (lgkmcnt 0, so the count never depends on what else is in flight) and
+// passes the values through, so nothing can read (or copy) a destination register before its data
+// has arrived.  The "; ba_pf" / "; ba_pw" tags let the code-generation test check exactly that in
+// the compiled kernel.
+__device__ __forceinline__ uint32_t lds_rd_u32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 ; ba_pf" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_rd3(uint32_t addr, double (&v)[3]) {
+    asm volatile("ds_read_b64 %0, %1 ; ba_pf" : "=v"(v[0]) : "v"(addr));
+    asm volatile("ds_read_b64 %0, %1 offset:128 ; ba_pf" : "=v"(v[1]) : "v"(addr));
+    asm volatile("ds_read_b64 %0, %1 offset:256 ; ba_pf" : "=v"(v[2]) : "v"(addr));
+}
+__device__ __forceinline__ void lds_wait(uint32_t& a) {
+    asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw" : "+v"(a));
+}
+__device__ __forceinline__ void lds_wait(double (&A)[3], uint32_t& d) {
+    asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(d));
+}
+__device__ __forceinline__ void lds_wait(double (&A)[3], double (&B)[3], uint32_t& d) {
+    asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw"
+                 : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(d));
+}
+// LDS f64 atomic add (no return) at a byte address, also outside the compiler's view of LDS.
+__device__ __forceinline__ void lds_add_f64(uint32_t addr, double v) {
+    asm volatile("ds_add_f64 %0, %1 ; ba_pa" : : "v"(addr), "v"(v) : "memory");
+}
+
 struct Staging {                // one chunk's inputs, laid out as the copies write them
     double rec[BA_CORE * BA_CHUNK];         // the chunk's linearisation records (field-major, as in memory)
     int info[BA_CHUNK];                     // slot_info per slot
@@ -460,7 +495,7 @@ struct Staging {                // one chunk's inputs, laid out as the copies wr
 
 // waves 0-1: the slots of chunk ck; wave 2: its chunk tracks (first_ct ..), n_ct; wave 3: its entry list
 __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* sNct,
-                                            uint16_t (*lists)[BA_LIST_CAP], int (*tabs)[BA_MAX_SLOTS], int ck,
+                                            uint32_t (*lists)[BA_LIST_CAP], int (*tabs)[BA_MAX_SLOTS], int ck,
                                             int first_ct, int C, int wave, int lane) {
     if (wave < 2) {
         const int w = __builtin_amdgcn_readfirstlane(wave);
@@ -488,7 +523,7 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
         const char* src = reinterpret_cast<const char*>(a.chunk_ent) + (int64_t)a.chunk_eptr[ck] * 16;
         char* dst = reinterpret_cast<char*>(lists[ck & 1]);
 #pragma unroll
-        for (int i = 0; i < BA_LIST_CAP * 2 / 1024; ++i) dma16_to_lds(src + 1024 * i + 16 * lane, dst + 1024 * i);
+        for (int i = 0; i < BA_LIST_CAP * 4 / 1024; ++i) dma16_to_lds(src + 1024 * i + 16 * lane, dst + 1024 * i);
         if (lane < BA_MAX_SLOTS / 4)
             dma16_to_lds(a.chunk_slots + (int64_t)ck * BA_MAX_SLOTS + 4 * lane, tabs[ck & 1]);
     }
@@ -505,7 +540,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
     __shared__ int sPair[BA_MAX_SLOTS];                  // per kernel place: the slot's pair, -1 if none
     __shared__ int sQ[BA_MAX_SLOTS];                     // per kernel place: the batch slot
-    __shared__ uint16_t sList[2][BA_LIST_CAP];           // MFMA entry lists (chunk ck in buffer ck & 1)
+    __shared__ uint32_t sList[2][BA_LIST_CAP];           // MFMA entry lists (chunk ck in buffer ck & 1)
     __shared__ int sSlotTab[2][BA_MAX_SLOTS];            // per slot: entry offset | padded count << 16
     __shared__ int sDup[2];
     __shared__ int sNct;
@@ -685,53 +720,67 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         }
 
         // ---------------- B: camera-pair tiles
-        // one group of four entries: lane group kq reads row c of its entry's A and B blocks (the
-        // descriptor of the next group is requested before this group's operands), then one MFMA
-        // per row c; a diagonal slot's J entries negate A and feed diag(J_c^T J_c)
-        auto run_slot = [&](const uint16_t* L, int ng, dbl4 acc_in, bool diag, double& dsq) -> dbl4 {
-            dbl4 acc_l = acc_in;
-            uint32_t dn = ng > 0 ? L[kq] : 0u;
-            for (int g = 0; g < ng; ++g) {
-                const uint32_t dsc = dn;
-                if (g + 1 < ng) dn = L[4 * (g + 1) + kq];
-                const uint32_t kind = dsc >> 14;
-                const int roff = kind == BA_ENT_J ? BA_JROW : 0;
-                const int ia = (kind == BA_ENT_PAD ? BA_ZERO : (int)(dsc & 127u) * BA_BLK + roff) + l15;
-                const int ib = (kind == BA_ENT_PAD ? BA_ZERO : (int)((dsc >> 7) & 127u) * BA_BLK + roff) + l15;
+        // one group of four entries: lane group kq reads row c of its entry's A and B rows (the
+        // entry holds their LDS offsets), then one MFMA per row c; the next group's entry is read
+        // with this group's operands.  A diagonal slot starts with its J groups (A = B = the J rows
+        // of one observation each, A negated by the MFMA's modifier, and their squares summed into
+        // diag(J_c^T J_c)), then its V groups.  Every LDS read here goes through lds_rd* (above).
+        const uint32_t lane_base = lds_addr(sBlk) + 8u * (uint32_t)l15;
+        auto run_v = [&](uint32_t Lb, int g0, int g1, dbl4 acc_l) -> dbl4 {
+            if (g0 >= g1) return acc_l;
+            uint32_t e = lds_rd_u32(Lb + 16u * (uint32_t)g0);
+            lds_wait(e);
+            for (int g = g0; g < g1; ++g) {
                 double A[3], B[3];
-#pragma unroll
-                for (int c = 0; c < 3; ++c) { A[c] = sBlk[ia + 16 * c]; B[c] = sBlk[ib + 16 * c]; }
-                if (diag) {
-                    const uint64_t sgn = (uint64_t)(kind == BA_ENT_J) << 63;
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        if (sgn) dsq += B[c] * B[c];
-                        A[c] = __longlong_as_double(__double_as_longlong(A[c]) ^ (long long)sgn);
-                    }
-                }
+                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
+                lds_rd3(lane_base + 8u * (e >> 16), B);
+                uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, g1 - 1));
+                lds_wait(A, B, en);
 #pragma unroll
                 for (int c = 0; c < 3; ++c) acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], B[c], acc_l, 0, 0, 0);
-                // keep the group's LDS reads ahead of its MFMAs
-                __builtin_amdgcn_sched_group_barrier(0x100, 7, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                e = en;
             }
             return acc_l;
         };
+        auto run_j = [&](uint32_t Lb, int ng, dbl4 acc_l, double& dsq) -> dbl4 {
+            if (ng <= 0) return acc_l;
+            uint32_t e = lds_rd_u32(Lb);
+            lds_wait(e);
+            for (int g = 0; g < ng; ++g) {
+                double A[3];
+                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
+                uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, ng - 1));
+                lds_wait(A, en);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    dsq += A[c] * A[c];
+                    acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], A[c], acc_l, 0, 0, 1);   // neg:[1,0,0]
+                }
+                e = en;
+            }
+            return acc_l;
+        };
+        const uint32_t tab_base = lds_addr(sSlotTab[ck & 1]), list_base = lds_addr(sList[ck & 1]) + 4u * (uint32_t)kq;
 #pragma unroll
         for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
             const int pq = my_pq[q];
             if (pq < 0) continue;
             const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
-            const int tab = __builtin_amdgcn_readfirstlane(sSlotTab[ck & 1][my_q[q]]);
-            const int off = tab & 0xffff, ng = (tab >> 16) >> 2;
-            double dsq = 0.0;
+            uint32_t tv = lds_rd_u32(tab_base + 4u * (uint32_t)my_q[q]);
+            lds_wait(tv);
+            const int tab = __builtin_amdgcn_readfirstlane((int)tv);
+            const uint32_t Lb = list_base + 4u * (uint32_t)BA_TAB_OFF(tab);
+            const int ng = BA_TAB_NG(tab);
             if (la != lb) {
-                acc[q] = run_slot(sList[ck & 1] + off, ng, acc[q], false, dsq);
+                acc[q] = run_v(Lb, 0, ng, acc[q]);
             } else {
-                acc[q] = run_slot(sList[ck & 1] + off, ng, acc[q], true, dsq);
+                const int njg = BA_TAB_NJG(tab);
+                double dsq = 0.0;
+                acc[q] = run_j(Lb, njg, acc[q], dsq);
+                acc[q] = run_v(Lb, njg, ng, acc[q]);
                 dsq += __shfl_xor(dsq, 16);
                 dsq += __shfl_xor(dsq, 32);
-                if (lane < 16) sDv[la][lane] += dsq;
+                if (lane < 16) lds_add_f64(lds_addr(&sDv[la][lane]), dsq);
             }
         }
     }

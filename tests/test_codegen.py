@@ -140,3 +140,76 @@ def test_mfma_results_read_after_enough_wait_states(src, tmp_path):
         if v:
             bad[name] = v[:3]
     assert not bad, bad
+
+
+def _vregs(text):
+    """VGPRs named in an instruction's operand text (v5, v[4:7])."""
+    regs = set()
+    for m in re.finditer(r'\bv\[(\d+):(\d+)\]|\bv(\d+)\b', text):
+        if m.group(3) is not None:
+            regs.add(int(m.group(3)))
+        else:
+            regs.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return regs
+
+
+def _lds_asm_violations(lines):
+    """LDS reads tagged `ba_pf` are issued from inline asm, so the compiler does not wait for them:
+    no instruction may name one of their destination registers before the next `ba_pw` wait (an
+    `s_waitcnt lgkmcnt(0)`), and none may still be pending at a label or branch."""
+    bad, pending = [], {}
+    for ln in lines:
+        t = ln.strip()
+        if not t or t.startswith(';') or (t.startswith('.') and not t.startswith('.LBB')):
+            continue
+        if t.endswith('ba_pw'):
+            if not t.startswith('s_waitcnt lgkmcnt(0)'):
+                bad.append(('wait is not lgkmcnt(0)', t))
+            pending = {}
+            continue
+        if pending and (t.startswith('.LBB') or t.startswith(('s_branch', 's_cbranch', 's_endpgm', 's_setpc'))):
+            bad.append(('read pending at ' + t.split()[0], sorted(pending)))
+            pending = {}
+            continue
+        parts = t.split(';')[0].split(None, 1)
+        ops = parts[1] if len(parts) > 1 else ''
+        hit = _vregs(ops) & set(pending)
+        if hit:
+            bad.append((t, {r: pending[r] for r in sorted(hit)}))
+        if t.endswith('ba_pf'):
+            for r in _vregs(ops.split(',')[0]):
+                pending[r] = t
+    return bad
+
+
+def test_lds_asm_scanner_flags_an_early_use():
+    ok = ['ds_read_b64 v[8:9], v0 ; ba_pf', 's_waitcnt lgkmcnt(0) ; ba_pw',
+          'v_mfma_f64_16x16x4_f64 v[58:65], v[8:9], v[6:7], v[58:65]']
+    assert not _lds_asm_violations(ok)
+    early = ['ds_read_b64 v[8:9], v0 ; ba_pf', 'v_mov_b64_e32 v[4:5], v[8:9]', 's_waitcnt lgkmcnt(0) ; ba_pw']
+    assert _lds_asm_violations(early)
+    crossing = ['ds_read_b64 v[8:9], v0 ; ba_pf', 's_cbranch_scc0 .LBB0_1', 's_waitcnt lgkmcnt(0) ; ba_pw']
+    assert _lds_asm_violations(crossing)
+    clobber = ['ds_read_b64 v[8:9], v0 ; ba_pf', 'ds_read_b64 v[8:9], v1 ; ba_pf', 's_waitcnt lgkmcnt(0) ; ba_pw']
+    assert _lds_asm_violations(clobber)
+    weak = ['ds_read_b64 v[8:9], v0 ; ba_pf', 's_waitcnt lgkmcnt(1) ; ba_pw']
+    assert _lds_asm_violations(weak)
+
+
+def test_schur_asm_lds_reads_untouched_until_their_wait(tmp_path):
+    """The MFMA phase of k_schur reads LDS through inline asm (so that the compiler does not make it
+    wait for the next chunk's global_load_lds copies); in the compiled kernel every such read's
+    destination is left alone until the explicit lgkmcnt(0) wait that follows it."""
+    asm = _asm('ba_schur.hip', tmp_path)
+    assert asm.count('ba_pf') > 0 and asm.count('ba_pw') > 0
+    funcs, cur = {}, None
+    for line in asm.split('\n'):
+        m = re.match(r'^(_Z\w+):', line)
+        if m:
+            cur = m.group(1)
+            funcs[cur] = []
+            continue
+        if cur:
+            funcs[cur].append(line)
+    bad = {name: v[:3] for name, lines in funcs.items() for v in [_lds_asm_violations(lines)] if v}
+    assert not bad, bad

@@ -80,19 +80,24 @@ def test_plan_invariants(cfg, nf, nt, kw):
 @pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 6, 60, {}), (0, 32, 3000, {}), (2, 60, 6000, {}),
                                           (0, 12, 500, dict(max_slots=40))])
 def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
-    """The per-chunk MFMA entry lists equal an independent reconstruction from slot_info: per
-    off-diagonal slot (a, b) one V entry per covering chunk track (chunk-track order) joining the
-    first observations of its runs in a and b; per diagonal slot (a, a) one J entry per observation
-    in a, then one V entry per (track, image) run in a (slot order); padding to a multiple of 4 with
-    PAD entries; at most BA_LIST_CAP (1536) entries per chunk."""
-    V, J, PAD, CAP, MS = 0, 1, 2, 1536, 96
+    """The per-chunk MFMA entry lists equal an independent reconstruction from slot_info.  An entry
+    holds the LDS offsets (in doubles) of its A rows and B rows, A | B << 16, with observation slot s
+    at s * 97 (V rows) and s * 97 + 48 (J rows) and a zero block at 128 * 97.  Per off-diagonal
+    slot (a, b): one V entry per covering chunk track (chunk-track order) joining the first
+    observations of its runs in a and b; per diagonal slot (a, a): one J entry per observation in a
+    (slot order), padded to a multiple of 4 with zero-block entries, then one V entry per (track,
+    image) run in a (slot order); each list padded to a multiple of 4; at most BA_LIST_CAP (1536)
+    entries per chunk.  The slot table word is offset | groups << 12 | J groups << 21."""
+    BLK, JROW, CAP, MS = 97, 48, 1536, 96
+    ZERO = 128 * BLK
+    PAD = ZERO | ZERO << 16
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
     pl = _plan(p, **kw)
     h = pl.host
-    ents = h['chunk_ent'].view(np.uint16)
+    ents = h['chunk_ent'].view(np.uint32)
     meta = h['chunk_meta'].reshape(-1, 4)
     n_chunks = len(meta)
-    assert ents.size >= 8 * int(h['chunk_eptr'][-1]) + CAP if n_chunks else True
+    assert ents.size >= 4 * int(h['chunk_eptr'][-1]) + CAP if n_chunks else True
     total_real = 0
     for ck in range(n_chunks):
         batch, first_ct, n_ct, used = meta[ck]
@@ -103,31 +108,36 @@ def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
             lead.setdefault((t, li), ld)
             assert lead[(t, li)] == ld
         s0, s1 = h['b_slot_ptr'][batch], h['b_slot_ptr'][batch + 1]
-        base = 8 * int(h['chunk_eptr'][ck])
+        base = 4 * int(h['chunk_eptr'][ck])
         tab = h['chunk_slots'][ck * MS:(ck + 1) * MS]
         end = 0
         for q in range(MS):
-            off, ln = int(tab[q]) & 0xffff, int(tab[q]) >> 16
+            off, ng, njg = int(tab[q]) & 0xfff, (int(tab[q]) >> 12) & 0x1ff, (int(tab[q]) >> 21) & 0x3f
             if q >= s1 - s0:
                 assert tab[q] == 0
                 continue
             pq = h['slot_pair'][s0 + q]
             a, b = pq & 0xff, (pq >> 8) & 0xff
-            want = []
+            want, n_real, want_njg = [], 0, 0
             if a != b:
                 for t in range(n_ct):
                     if (t, a) in lead and (t, b) in lead:
-                        want.append(lead[(t, a)] | lead[(t, b)] << 7 | V << 14)
+                        want.append(lead[(t, a)] * BLK | (lead[(t, b)] * BLK) << 16)
+                n_real = len(want)
             else:
-                want += [sidx | sidx << 7 | J << 14 for sidx in range(used) if info[sidx] & 0xff == a]
-                want += [sidx | sidx << 7 | V << 14 for sidx in range(used)
-                         if info[sidx] & 0xff == a and info[sidx] >> 16 == sidx]
-            total_real += len(want)
-            want += [PAD << 14] * (-len(want) % 4)
-            assert ln == len(want) and ln % 4 == 0
+                js = [sidx * BLK + JROW for sidx in range(used) if info[sidx] & 0xff == a]
+                want += [o | o << 16 for o in js]
+                want += [PAD] * (-len(want) % 4)
+                want_njg = len(want) // 4
+                vs = [sidx * BLK for sidx in range(used) if info[sidx] & 0xff == a and info[sidx] >> 16 == sidx]
+                want += [o | o << 16 for o in vs]
+                n_real = len(js) + len(vs)
+            total_real += n_real
+            want += [PAD] * (-len(want) % 4)
+            assert 4 * ng == len(want) and njg == want_njg
             assert off == end
-            assert np.array_equal(ents[base + off:base + off + ln], np.array(want, dtype=np.uint16))
-            end += ln
+            assert np.array_equal(ents[base + off:base + off + 4 * ng], np.array(want, dtype=np.uint32))
+            end += 4 * ng
         assert end <= CAP
     # every pair term and every observation once: sum over tracks of m(m+1)/2 plus n_obs
     assert total_real == pl.scalars['n_pair_terms'] + p.n_obs
