@@ -424,7 +424,7 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     auto& slot_gpair = P->v[BA_PA_SLOT_GPAIR];    // per slot: global pair id
     auto& chunk_slots = P->v[BA_PA_CHUNK_SLOTS];  // n_chunks * BA_MAX_SLOTS
     auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 32-bit entries
-    auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks
+    auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks + 1
     auto& b_pos_slot = P->v[BA_PA_B_POS_SLOT];    // n_batches * BA_MAX_SLOTS
     bool list_overflow = false;
     // offsets of each batch in the concatenated arrays, then a parallel copy
@@ -443,7 +443,8 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     slot_src.resize(o_ch[n_batches] * BA_CHUNK); s_pid.resize(o_ch[n_batches] * BA_CHUNK);
     s_img.resize(o_ch[n_batches] * BA_CHUNK);
     chunk_meta.resize(o_ch[n_batches] * 4); chunk_slots.resize(o_ch[n_batches] * BA_MAX_SLOTS);
-    chunk_eptr.resize(o_ch[n_batches]);
+    chunk_eptr.resize(o_ch[n_batches] + 1);
+    chunk_eptr[o_ch[n_batches]] = (int32_t)(o_en[n_batches] / 4);
     for (auto* v : {&ct_pid, &ct_first, &ct_m, &ct_mask}) v->resize(o_ct[n_batches]);
     slot_pair.resize(o_sl[n_batches]);
     // the entries, and one chunk's worth of zero padding so that a full-capacity copy of the last

@@ -33,7 +33,7 @@ enum {
     BA_PA_IMG_SRC,
     BA_PA_CHUNK_SLOTS,      // per chunk, BA_MAX_SLOTS slot table words (BA_TAB, below)
     BA_PA_CHUNK_ENT,        // MFMA entries of every chunk, 32 bits each, see below
-    BA_PA_CHUNK_EPTR,       // per chunk: first entry, in units of 4 entries (16 bytes)
+    BA_PA_CHUNK_EPTR,       // per chunk, and one past the last: first entry, in units of 4 entries (16 bytes)
     BA_PA_B_POS_SLOT,       // per batch, BA_MAX_SLOTS words: the batch slot at Schur-kernel place
                             // wave + BA_WAVES * k, or -1 (places balanced by work)
     BA_PA_SLOT_SRC,         // per chunk slot: its observation, 0 for an empty slot (a gather index)

@@ -518,12 +518,15 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
         dma16_to_lds(a.ct_pt + 4 * ct, S.X);
         if (lane == 0) *sNct = a.chunk_meta[4 * ck + 2];
     } else if (wave == 3) {
-        // the chunk's MFMA entry list (a full-capacity copy; the plan pads its array for it) and
-        // its slot table, into buffer ck & 1
-        const char* src = reinterpret_cast<const char*>(a.chunk_ent) + (int64_t)a.chunk_eptr[ck] * 16;
+        // the chunk's MFMA entry list, in whole 1 KB pieces (the plan pads its array for a copy of
+        // full capacity), and its slot table, into buffer ck & 1
+        const int ep0 = a.chunk_eptr[ck], ep1 = a.chunk_eptr[ck + 1];
+        const char* src = reinterpret_cast<const char*>(a.chunk_ent) + (int64_t)ep0 * 16;
         char* dst = reinterpret_cast<char*>(lists[ck & 1]);
+        const int nbytes = __builtin_amdgcn_readfirstlane((ep1 - ep0) * 16);
 #pragma unroll
-        for (int i = 0; i < BA_LIST_CAP * 4 / 1024; ++i) dma16_to_lds(src + 1024 * i + 16 * lane, dst + 1024 * i);
+        for (int i = 0; i < BA_LIST_CAP * 4 / 1024; ++i)
+            if (1024 * i < nbytes) dma16_to_lds(src + 1024 * i + 16 * lane, dst + 1024 * i);
         if (lane < BA_MAX_SLOTS / 4)
             dma16_to_lds(a.chunk_slots + (int64_t)ck * BA_MAX_SLOTS + 4 * lane, tabs[ck & 1]);
     }

@@ -97,7 +97,8 @@ def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
     ents = h['chunk_ent'].view(np.uint32)
     meta = h['chunk_meta'].reshape(-1, 4)
     n_chunks = len(meta)
-    assert ents.size >= 4 * int(h['chunk_eptr'][-1]) + CAP if n_chunks else True
+    assert len(h['chunk_eptr']) == n_chunks + 1
+    assert ents.size >= 4 * int(h['chunk_eptr'][-1]) + CAP
     total_real = 0
     for ck in range(n_chunks):
         batch, first_ct, n_ct, used = meta[ck]
@@ -139,6 +140,8 @@ def test_plan_mfma_entry_lists(cfg, nf, nt, kw):
             assert np.array_equal(ents[base + off:base + off + 4 * ng], np.array(want, dtype=np.uint32))
             end += 4 * ng
         assert end <= CAP
+        # the kernel copies the chunk's list up to the next chunk's first entry
+        assert end <= 4 * int(h['chunk_eptr'][ck + 1] - h['chunk_eptr'][ck])
     # every pair term and every observation once: sum over tracks of m(m+1)/2 plus n_obs
     assert total_real == pl.scalars['n_pair_terms'] + p.n_obs
     # kernel places: every batch slot at exactly one place, at most 6 places used per wave (16 waves)
