@@ -26,6 +26,17 @@ __device__ __forceinline__ int obs_image(const int* __restrict__ cum, int n_imgs
     return a;
 }
 
+// ---------------------------------------------------------------- XCD-aware block order
+// The dispatcher hands workgroup b to XCD b mod 8 (MI355X: 8 XCDs, one L2 each).  xcd_block maps
+// the hardware id onto a logical id so that each XCD takes one contiguous range of logical blocks,
+// in order: neighbouring blocks that read the same data (one image's map, one image's tiles) then
+// share an L2 instead of fetching it into all eight.  A bijection on [0, nb) for any nb.
+#define BA_N_XCD 8
+__device__ __forceinline__ unsigned xcd_block(unsigned b, unsigned nb) {
+    const unsigned x = b % BA_N_XCD, k = b / BA_N_XCD, q = nb / BA_N_XCD, r = nb % BA_N_XCD;
+    return x * q + (x < r ? x : r) + k;
+}
+
 // ---------------------------------------------------------------- camera parameters
 struct CamF {           // fp32 view of the parameters an observation needs
     float fx, fy, cx, cy;

@@ -19,7 +19,9 @@
 //
 // Memory: observations are image-major, so the blocks of one image gather from one map (a few MB,
 // resident in L2 / MALL while they run); each block stages its output rows in LDS and writes them
-// as one contiguous run.
+// as one contiguous run.  (Laying the blocks out so that each XCD takes a contiguous range of them
+// cut the fetched bytes from 2.72 to 2.04 GB per launch at config 2 but took 4% longer: the kernel
+// is bound by its gathers' latency, not by the bytes.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -28,6 +28,7 @@
 #include <stdint.h>
 #include <cmath>
 
+#include "ba_common.h"
 #include "ba_error.h"
 #include "ba_hip.h"
 
@@ -198,7 +199,9 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
     __shared__ float sCw[TG_RR * TG_RC];
     __shared__ float sL[GN ? CMAX : 1][TG_RR * TG_RC];
     __shared__ double sRed[TG_T / 64];
-    const int img = blockIdx.y, tile = blockIdx.x;
+    // an image's tiles on one XCD, so that the halo rows neighbouring tiles share are fetched into one L2
+    const unsigned lb = xcd_block(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x * gridDim.y);
+    const int img = (int)(lb / gridDim.x), tile = (int)(lb % gridDim.x);
     const TgImage m = tg_image(a, img);
     const int tr0 = (tile / n_tc) * TG_TR, tc0 = (tile % n_tc) * TG_TC;
     double* out = part + ((int64_t)img * gridDim.x + tile) * n_acc;
