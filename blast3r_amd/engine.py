@@ -35,25 +35,34 @@ def shape_of(tensor, is_contiguous=True, check_finite=True):
     return tensor.shape
 
 
-def _assert_finite(*tensors):
-    """``assert t.isfinite().all()`` for every tensor (en:343), one launch and one host read for all
-    device fp32 inputs (ba_nonfinite_flags); int32 tensors are finite by type."""
+def _nonfinite_flag(*tensors):
+    """The isfinite check of every tensor (en:343) for the device fp32 inputs, launched without a
+    host read: returns a 0-d device bool (True when a value is non-finite), or None when no input is
+    on the device.  Host inputs are asserted at once; int32 tensors are finite by type."""
     floats = [t for t in tensors if t.dtype != torch.int32]
     dev = [t for t in floats if t.is_cuda]
     for t in floats:
         if not t.is_cuda:
             assert t.isfinite().all()
     if not dev:
-        return
+        return None
     views = [t if t.is_contiguous() else t.contiguous() for t in dev]
+    flags = torch.empty(len(views), dtype=torch.int32, device=views[0].device)
     for k in range(0, len(views), 16):
         part = views[k:k + 16]
         n = len(part)
         ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in part])
         counts = (ctypes.c_int64 * n)(*[t.numel() for t in part])
-        flags = torch.empty(n, dtype=torch.int32, device=part[0].device)
-        check(lib().ba_nonfinite_flags(ptrs, counts, n, ptr(flags), stream_ptr(part[0].device)))
-        assert not bool(flags.cpu().any()), 'non-finite input'
+        check(lib().ba_nonfinite_flags(ptrs, counts, n, ptr(flags[k:k + n]), stream_ptr(part[0].device)))
+    return flags.any()
+
+
+def _assert_finite(*tensors):
+    """``assert t.isfinite().all()`` for every tensor (en:343), one launch and one host read for all
+    device fp32 inputs (ba_nonfinite_flags)."""
+    f = _nonfinite_flag(*tensors)
+    if f is not None:
+        assert not bool(f.cpu()), 'non-finite input'
 
 
 def update_K(K0, delta_focal, min_f=100):
@@ -117,7 +126,7 @@ def used_depth_channels(n_zcfs, n_channels, depth_mode):
     return min(used, n_channels)
 
 
-def line_search(trial, init_loss, min_loss_delta, min_reproj):
+def line_search(trial, init_loss, min_loss_delta, min_reproj, nonfinite=None):
     """The step-halving loop of lm_step (en:308-333), on 0-d loss tensors.
 
     trial(scale) evaluates the update at `scale` times the step and returns (loss, reproj_score,
@@ -127,6 +136,9 @@ def line_search(trial, init_loss, min_loss_delta, min_reproj):
     (en:317-319: `new_loss = init_loss; new_loss += min_loss_delta` adds min_loss_delta to init_loss
     itself): init_loss grows by min_loss_delta for the rest of the step and is returned so.  All
     comparisons use the fp32 sums formed on the loss's device, read with one copy per trial.
+    nonfinite, when given, is lm_step's input check (a 0-d device bool): it travels with the first
+    trial's values, and the step raises there, before any decision, as the reference raises at its
+    start (en:343).
     Returns a dict: scale, scales (every scale tried), init_loss, new_loss (with min_loss_delta),
     trial_loss (the last trial's objective as evaluated), payload, accepted."""
     scale = 1.0
@@ -140,8 +152,13 @@ def line_search(trial, init_loss, min_loss_delta, min_reproj):
         # reference forms them, so the comparison sees the same fp32 values
         plus = trial_loss + min_loss_delta
         init_plus = init_loss + min_loss_delta
-        vals = torch.stack([t.reshape(()).to(torch.float32) for t in (trial_loss, init_loss, reproj_t, plus,
-                                                                       init_plus)]).cpu()
+        items = [trial_loss, init_loss, reproj_t, plus, init_plus]
+        if nonfinite is not None:
+            items.append(nonfinite)
+        vals = torch.stack([t.reshape(()).to(torch.float32) for t in items]).cpu()
+        if nonfinite is not None:
+            assert not bool(vals[5]), 'non-finite input'
+            nonfinite = None
         if torch.isnan(vals[0]):
             print('Warning: loss is NaN')
             init_loss = new_loss = init_plus     # en:317-319: new_loss aliases init_loss, += adds to both
@@ -223,7 +240,9 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
     assert shape_of(pix2d_std, **chk) == (n_obs, 2)
     assert shape_of(pix2d_dep, **chk) == (n_obs, n_zcf), \
         f'expected pix2d_dep of shape {(n_obs, n_zcf)}, got {shape_of(pix2d_dep, **chk)}'
-    _assert_finite(K, P_rig2cam, P_w2rig, z_coefs, pts3d, pix2d, pix2d_std, pix2d_dep)
+    # the isfinite assertions (en:343): launched here, read with the first line-search trial (one host
+    # round trip fewer; nothing the step does before that depends on the answer)
+    nonfinite = _nonfinite_flag(K, P_rig2cam, P_w2rig, z_coefs, pts3d, pix2d, pix2d_std, pix2d_dep)
     assert 0 <= weight_z <= 10
     assert n_obs >= n_tracks, 'there must be more 2d kpts than tracks'
     assert huber_delta >= 0.1
@@ -283,7 +302,7 @@ def _lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_c
         new_loss, new_residuals, new_w, new_reproj = objective(**update)
         return new_loss, new_reproj, (update, new_residuals, new_w)
 
-    ls = line_search(trial, init_loss, min_loss_delta, min_reproj)
+    ls = line_search(trial, init_loss, min_loss_delta, min_reproj, nonfinite=nonfinite)
     update, new_residuals, new_w = ls['payload']
     if info is not None:
         ist = jac.last.get('istate')

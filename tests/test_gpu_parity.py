@@ -656,7 +656,8 @@ def test_nonfinite_flags_match_torch_isfinite():
 
 
 def test_lm_step_rejects_nonfinite_inputs():
-    """lm_step asserts isfinite on its inputs before any work (en:340-344)."""
+    """lm_step asserts isfinite on its inputs (en:340-344): the check is launched at the start of the
+    step and read with the first line-search trial, before any decision is taken."""
     p = make_problem(0, n_frames=6, n_tracks=60)
     o = p.options
     kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0)
