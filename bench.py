@@ -564,10 +564,13 @@ def measured_traffic(cfg, kernel='k_schur'):
 
 def bench_reduced_solve(prob, g, dev, warmup, reps=5):
     """The reduced-system Cholesky (ba_reduced_solve, solver='cholesky') on the configuration's
-    damped reduced system, dense and banded layouts: the bare launch sequence (assembly of S_u from
-    the image-pair blocks, factorisation, both triangular sweeps) timed with events on its stream,
-    beside the device PCG's solve.  fp64 flops: dense n^3/3 + 2 n^2; banded n b^2 + 4 n b with b the
-    scalar bandwidth (w + 1) d_band."""
+    damped reduced system, banded (block cyclic reduction where it applies), banded by one workgroup, and
+    dense layouts: the bare launch sequence (assembly of S_u from the image-pair blocks, factorisation,
+    both triangular sweeps) timed with events on its stream, beside the device PCG's solve.  fp64 flops:
+    dense n^3/3 + 2 n^2; banded n b^2 + 4 n b with b the scalar bandwidth (w + 1) d_band (the band
+    factor's own count: the cyclic reduction issues more, 128^3 x ~7 per super-block and level).
+    Beside them, the reference's own call (torch.linalg.solve, ba_solver.py:220) on the same dense S_u
+    (rebuilt as L L^T from the dense factor) on the same GPU."""
     from blast3r_amd._lib import check, lib
     from blast3r_amd.ba_solver import GaussNewtonSolver
     o = prob.options
@@ -581,7 +584,7 @@ def bench_reduced_solve(prob, g, dev, warmup, reps=5):
     stream = torch.cuda.current_stream(dev)
     st = stream.cuda_stream
     result = {}
-    for layout in ('banded', 'dense'):
+    for layout in ('banded', 'banded_sequential', 'dense'):
         gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, solver='cholesky',
                                cholesky_layout=layout)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
@@ -614,9 +617,28 @@ def bench_reduced_solve(prob, g, dev, warmup, reps=5):
             flops = n * b * b + 4 * n * b
         result[layout] = {'ms': ms, 'unknowns': n, 'flops': flops, 'achieved_tflops': flops / (ms * 1e-3) / 1e12,
                           'frac_of_fp64_peak': flops / (ms * 1e-3) / 1e12 / 78.6, 'w': info['w'], 'd_band': info['db'],
-                          'shared': info['n_shared']}
+                          'shared': info['n_shared'], 'superblocks': info.get('superblocks', 0)}
         log(f'[bench] reduced solve ({layout}): {ms:.2f} ms for {n} unknowns, '
-            f'{flops / (ms * 1e-3) / 1e12:.2f} TFLOP/s fp64')
+            f'{flops / (ms * 1e-3) / 1e12:.2f} TFLOP/s fp64' +
+            (f', {info["superblocks"]} super-blocks' if info.get('superblocks') else ''))
+        if layout == 'dense':
+            # the reference's call on the same system: S_u = L L^T from the factor just computed
+            Lt = torch.tril(gs.last['direct_A'][:n, :n])
+            S = Lt @ Lt.T
+            rhs = torch.randn(n, 1, dtype=torch.float64, device=dev)
+            for _ in range(max(1, warmup)):
+                torch.linalg.solve(S, rhs)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(reps):
+                torch.linalg.solve(S, rhs)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms_t = e0.elapsed_time(e1) / reps
+            result['torch_linalg_solve'] = {'ms': ms_t, 'unknowns': n,
+                                            'call': 'torch.linalg.solve(S, rhs), ba_solver.py:220'}
+            log(f'[bench] reference call torch.linalg.solve on the same {n} x {n} S_u: {ms_t:.2f} ms')
+            del S, Lt
         del gs, J
     torch.cuda.empty_cache()
     return result

@@ -169,6 +169,7 @@ _SIGS = {
     'ba_pm_slot_doubles': (c_i64, [c_i64, c_int, c_int]),
     'ba_chol_band_lds_bytes': (c_i64, [c_int, c_int, c_int]),
     'ba_chol_work_doubles': (c_i64, [c_int, c_i64, c_int, c_int, c_int, c_int]),
+    'ba_chol_band_superblocks': (c_int, [c_int, c_int, c_int, c_int]),
     'ba_reduced_solve': (c_int, [ctypes.POINTER(BaPcgArgs), ctypes.POINTER(BaCholArgs), c_p]),
     'ba_nonfinite_flags': (c_int, [c_p, c_p, c_int, c_p, c_p]),
     'ba_stream_triad': (c_int, [c_p, c_p, c_p, ctypes.c_double, c_i64, c_p]),

@@ -90,10 +90,12 @@ class GaussNewtonSolver:
         if solver not in ('pcg', 'cholesky'):
             raise ValueError(f'unknown reduced solver {solver!r} (supported: "pcg", "cholesky")')
         self.solver = solver
-        # solver='cholesky': 'banded' when every image pair lies within w images, the window of w + 1 images
-        # fits one workgroup's LDS ((w + 1) d <= 160, ~132 at d = 11) and at most 8 unknowns are shared by
-        # several images, else 'dense' ('auto' picks)
-        if cholesky_layout not in ('auto', 'dense', 'banded'):
+        # solver='cholesky': 'banded' when every image pair lies within w images and few unknowns are shared
+        # by several images: block cyclic reduction over super-blocks of 128 unknowns when w d <= 128 and
+        # at most 15 are shared, else one workgroup walking the images when its window of w + 1 images
+        # fits LDS ((w + 1) d <= 160) and at most 8 are shared; 'banded_sequential' forces the
+        # one-workgroup walk; 'dense' any structure ('auto' picks banded where it applies)
+        if cholesky_layout not in ('auto', 'dense', 'banded', 'banded_sequential'):
             raise ValueError(f'unknown cholesky_layout {cholesky_layout!r}')
         self.cholesky_layout = cholesky_layout
         self.pcg_tol = pcg_tol
@@ -529,11 +531,14 @@ class GaussNewtonSolver:
             um['db'] = len(bcol)
         db = um['db']
         layout = self.cholesky_layout
+        seq_fits = 1 <= db <= 16 and n_imgs >= 2 and (w + 1) * db <= 160 and ns <= 8 and \
+            int(L.ba_chol_band_lds_bytes(db, w, ns)) <= 160 * 1024
+        nsb = int(L.ba_chol_band_superblocks(db, w, ns, n_imgs)) if db >= 1 and n_imgs >= 2 else 0
         if layout == 'auto':
-            fits = 1 <= db <= 16 and n_imgs >= 2 and (w + 1) * db <= 160 and ns <= 8 and \
-                int(L.ba_chol_band_lds_bytes(db, w, ns)) <= 160 * 1024
-            layout = 'banded' if fits else 'dense'
-        mode = 1 if layout == 'banded' else 0
+            layout = 'banded' if nsb > 0 or seq_fits else 'dense'
+        mode = {'dense': 0, 'banded': 1, 'banded_sequential': 2}[layout]
+        if mode == 2:
+            nsb = 0
         lda = int(L.ba_chol_dense_lda(pa.n_u))
         nwork = int(L.ba_chol_work_doubles(mode, pa.n_u, n_imgs, db if mode else d, w, ns))
         info = ws('chol_info', (1,), torch.int32)
@@ -541,13 +546,15 @@ class GaussNewtonSolver:
                              shared_u=ptr(um['shared_u']), n_shared=ns, w=w, db=db, bcol=ptr(um['bcol']),
                              bpos=ptr(um['bpos']), n_pairs=n_p, info=ptr(info),
                              work=ptr(ws('chol_work', (nwork,), torch.float64)))
+        self.last['direct_A'] = None
         if mode == 0:
-            ca.A = ptr(ws('chol_A', (lda, lda), torch.float64))
+            self.last['direct_A'] = ws('chol_A', (lda, lda), torch.float64)   # S_u's lower triangle, then L
+            ca.A = ptr(self.last['direct_A'])
             ca.Linv = ptr(ws('chol_Linv', (lda // 64, 64, 64), torch.float64))
         check(L.ba_reduced_solve(pa, ca, st))
         self.last['direct_call'] = (pa, ca)    # kept for re-timing the bare launch sequence
         bad = int(info.cpu())                  # one read per solve
-        self.last['direct'] = dict(layout=layout, w=w, db=db, n_shared=ns,
+        self.last['direct'] = dict(layout=layout, w=w, db=db, n_shared=ns, superblocks=nsb if mode == 1 else 0,
                                    first_bad_pivot=None if bad == 2 ** 31 - 1 else bad)
         return bad == 2 ** 31 - 1
 

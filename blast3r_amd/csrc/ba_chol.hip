@@ -14,8 +14,13 @@
 //           v_mfma_f64_16x16x4f64; the triangular sweeps go block by block.  Any structure.
 //   banded  the image-level blocks of a block-banded structure (every image pair within w images)
 //           with the unknowns shared by several images (a mono camera's focal pair) as a dense
-//           border: one workgroup walks the images, keeping the w + 1 active block rows in LDS,
-//           and runs both sweeps in the same launch.  Work ~ n_imgs (w d)^2 d instead of n_u^3.
+//           border.  When s >= w images fit a super-block of 128 unknowns, the super-blocks form a
+//           block-tridiagonal system, solved by block cyclic reduction: each level eliminates every
+//           other remaining super-block in parallel (a 128 x 128 L L^T and L^-1 per super-block in
+//           LDS, then batched MFMA products for the neighbours' Schur updates), ~log2(n_imgs / s)
+//           levels; the border enters as extra right-hand sides.  Otherwise one workgroup walks the
+//           images, keeping the w + 1 active block rows in LDS, and runs both sweeps in the same
+//           launch.  Work ~ n_imgs (w d)^2 d instead of n_u^3.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <cmath>
@@ -48,6 +53,9 @@ struct ChArgs {
     const int32_t* bpos;        // banded: (d) band column of each image-level column, or -1
     int32_t* info;
     double *Ab, *Bfull, *Cb, *bl, *Lcol, *Lbord, *yv, *xl;
+    // banded by block cyclic reduction: nsb super-blocks of s images (CR_MP unknowns each, padded)
+    int32_t nsb, s;
+    double *crD, *crE, *crR, *crL, *crGa, *crGb, *crY, *crX, *crXb;
 };
 
 // ------------------------------------------------------------------ assembly
@@ -754,6 +762,451 @@ __global__ void __launch_bounds__(CH_T) k_band_scatter(ba_pcg_args a, ChArgs c) 
     else if (k == 0) a.x[u] = a.rhs[u] / a.damp[u];
 }
 
+// ------------------------------------------------------------------ banded layout, block cyclic reduction
+// Super-block I holds the local unknowns of images I s .. I s + s - 1 (entry (i, r) at (i - I s) db + r),
+// padded to CR_MP with identity rows; images past the last one are identity rows too.  Since s >= w, only
+// neighbouring super-blocks couple: S = tridiag(E_I (block (I, I - 1)), D_I, E_{I+1}^T).
+//
+// Level h = 1, 2, 4, ...: the remaining super-blocks are I = h - 1 (mod h); those at I = h - 1 (mod 2h)
+// are eliminated, each against its remaining neighbours a = I - h and b = I + h (when they exist):
+//   D_I = L L^T,  Ga = L^-1 E_I,  Gb = L^-1 E_b^T,  Y_I = L^-1 R_I
+//   D_a -= Ga^T Ga,  D_b -= Gb^T Gb,  E_b <- -Gb^T Ga (b now couples to a),  R_a -= Ga^T Y_I,  R_b -= Gb^T Y_I
+// and, levels in reverse, X_I = L^-T (Y_I - Ga X_a - Gb X_b).  This is L L^T of S in the odd-even
+// order of the super-blocks, so it is as stable as the sequential factor.  R carries CR_NR right-hand
+// sides: the local rhs, then the border columns (the couplings of the n_s shared unknowns), so that
+// X = S_loc^-1 [b | B] and the border is solved from its n_s x n_s Schur complement.
+#define CR_MP 128                       // unknowns per super-block
+#define CR_MP2 (CR_MP * CR_MP)
+#define CR_NR 16                        // right-hand sides per super-block (n_s <= 15)
+#define CR_T 512                        // threads of the super-block factor
+#define CR_LD (CR_MP + 1)               // LDS row pitch of the factor
+#define CR_LDS_DOUBLES (CR_MP * CR_LD + 8 * 256 + 16)
+
+// images per super-block, or 0 when the cyclic reduction does not apply (a super-block of s >= w images
+// must fit CR_MP unknowns, the border CR_NR - 1 columns)
+__host__ __device__ inline int cr_images(int db, int w, int ns) {
+    if (db < 1 || w < 1 || ns < 0 || ns > CR_NR - 1 || w * db > CR_MP) return 0;
+    const int s = CR_MP / db;
+    return s > w ? s : w;
+}
+
+__global__ void __launch_bounds__(CH_T) k_cr_assemble(ba_pcg_args a, ChArgs c) {
+    const int64_t e = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (e >= (int64_t)c.nsb * CR_MP2) return;
+    const int I = (int)(e / CR_MP2);
+    const int rem = (int)(e - (int64_t)I * CR_MP2);
+    const int u = rem / CR_MP, v = rem - u * CR_MP;
+    const int db = c.db, w = c.w, w1 = c.w + 1, n = a.n_imgs, m = c.s * db;
+    const int iu = I * c.s + u / db, ru = u % db;
+    auto band = [&](int i, int k, int r, int q) { return c.Ab[(((int64_t)i * w1 + k) * db + r) * db + q]; };
+    double dv = u == v ? 1.0 : 0.0;       // padding and images past the last one: identity
+    if (u < m && v < m && iu < n) {
+        const int iv = I * c.s + v / db, rv = v % db;
+        if (iv < n) {
+            dv = 0.0;
+            if (iu >= iv) {
+                if (iu - iv <= w) dv = band(iu, iu - iv, ru, rv);
+            } else if (iv - iu <= w) {
+                dv = band(iv, iv - iu, rv, ru);
+            }
+        }
+    }
+    c.crD[e] = dv;
+    double ev = 0.0;                      // block (I, I - 1)
+    if (I >= 1 && u < m && v < m && iu < n) {
+        const int iv = (I - 1) * c.s + v / db, k = iu - iv;
+        if (k <= w) ev = band(iu, k, ru, v % db);
+    }
+    c.crE[e] = ev;
+    if (v < CR_NR) {
+        double rv = 0.0;
+        if (u < m && iu < n) {
+            if (v == 0) rv = c.bl[(int64_t)iu * db + ru];
+            else if (v <= c.n_shared) rv = c.Bfull[(int64_t)(v - 1) * n * db + (int64_t)iu * db + ru];
+        }
+        c.crR[((int64_t)I * CR_MP + u) * CR_NR + v] = rv;
+    }
+}
+
+// acc[mi][nj] += A B over k in [kb, ke) (multiples of 4) for the 16 x 16 tiles (16 mi, 16 nj) of a wave:
+// fa(r, k) = A[r][k], fb(k, c) = B[k][c] relative to the wave's corner (v_mfma_f64_16x16x4f64 operand lane
+// l: row / column l % 16, k = l / 16; accumulator element v of lane l: row 4 v + l / 16, column l % 16)
+template <int NI, int NJ, class FA, class FB>
+__device__ __forceinline__ void cr_mma(dbl4 (&acc)[NI][NJ], int kb, int ke, FA fa, FB fb, int l16, int lk) {
+#pragma unroll 4
+    for (int k = kb; k < ke; k += 4) {
+        double av[NI], bv[NJ];
+#pragma unroll
+        for (int mi = 0; mi < NI; ++mi) av[mi] = fa(16 * mi + l16, k + lk);
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) bv[nj] = fb(k + lk, 16 * nj + l16);
+#pragma unroll
+        for (int mi = 0; mi < NI; ++mi)
+#pragma unroll
+            for (int nj = 0; nj < NJ; ++nj)
+                acc[mi][nj] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mi], bv[nj], acc[mi][nj], 0, 0, 0);
+    }
+}
+
+template <int NI, int NJ>
+__device__ __forceinline__ void cr_zero(dbl4 (&acc)[NI][NJ]) {
+#pragma unroll
+    for (int mi = 0; mi < NI; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = (dbl4){0.0, 0.0, 0.0, 0.0};
+}
+
+// One workgroup per eliminated super-block I = (2 blockIdx.x + 1) h - 1: D_I = L L^T in LDS by 16-column
+// panels (wave 0 factors and inverts the 16 x 16 diagonal block with lane shuffles; the panel below and
+// the trailing blocks are MFMA products), then L^-1 in place by block columns from the right
+// (L^-1_ij = - sum_{k = j+1..i} L^-1_ik L_kj L_jj^-1), written to crL[I] (lower; zero above).
+__global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
+    extern __shared__ double lds[];
+    double* S = lds;                          // [CR_MP][CR_LD]
+    double* Inv = lds + CR_MP * CR_LD;        // [8][16][16] inverses of the diagonal blocks
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int l16 = lane & 15, lk = lane >> 4;
+    const int I = (2 * (int)blockIdx.x + 1) * h - 1;
+    const double* D = c.crD + (int64_t)I * CR_MP2;
+    for (int e = t; e < CR_MP2; e += CR_T) {
+        const int r = e / CR_MP, q = e - r * CR_MP;
+        S[r * CR_LD + q] = q <= r ? D[e] : 0.0;
+    }
+    __syncthreads();
+    for (int p = 0; p < 8; ++p) {
+        double* B = S + 16 * p * CR_LD + 16 * p;
+        if (wave == 0) {
+            // lane r (mod 16) holds row r of the diagonal block
+            const int r = l16;
+            double row[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) row[q] = q <= r ? B[r * CR_LD + q] : 0.0;
+            double rinv = 0.0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                double pj = __shfl(row[j], j);
+                if (!(pj > 0.0)) {
+                    if (lane == 0) atomicMin(c.info, (int32_t)(I * CR_MP + 16 * p + j + 1));
+                    pj = 1.0;
+                }
+                const double rs = rsqrt(pj);
+                if (r == j) {
+                    row[j] = pj * rs;
+                    rinv = rs;
+                } else if (r > j) {
+                    row[j] *= rs;
+                }
+                const double lj = row[j];
+#pragma unroll
+                for (int q = j + 1; q < 16; ++q) {
+                    const double lqj = __shfl(lj, q);
+                    if (r >= q) row[q] -= lj * lqj;
+                }
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    if (q <= r) B[r * CR_LD + q] = row[q];
+            }
+            // lane c (mod 16) forms column c of L_pp^-1 by forward substitution (rows read back from LDS)
+            double x[16];
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const double ri = __shfl(rinv, rr);
+                double sum = 0.0;
+#pragma unroll
+                for (int mm = 0; mm < rr; ++mm) sum += B[rr * CR_LD + mm] * x[mm];
+                x[rr] = rr == l16 ? ri : (rr > l16 ? -ri * sum : 0.0);
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) Inv[p * 256 + rr * 16 + l16] = x[rr];
+            }
+        }
+        __syncthreads();
+        // panel: L_ip = A_ip L_pp^-T for the block rows below
+        if (wave < 7 - p) {
+            double* Ab = S + 16 * (p + 1 + wave) * CR_LD + 16 * p;
+            const double* Ip = Inv + p * 256;
+            dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(Ab[l16 * CR_LD + 4 * kk + lk], Ip[l16 * 16 + 4 * kk + lk],
+                                                           acc, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) Ab[(4 * v + lk) * CR_LD + l16] = acc[v];
+        }
+        __syncthreads();
+        // trailing blocks (ib, jb), p < jb <= ib: A_ij -= L_ip L_jp^T
+        int tc = 0;
+        for (int ib = p + 1; ib < 8; ++ib)
+            for (int jb = p + 1; jb <= ib; ++jb, ++tc) {
+                if ((tc & 7) != wave) continue;
+                const double* Li = S + 16 * ib * CR_LD + 16 * p;
+                const double* Lj = S + 16 * jb * CR_LD + 16 * p;
+                dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(Li[l16 * CR_LD + 4 * kk + lk],
+                                                               Lj[l16 * CR_LD + 4 * kk + lk], acc, 0, 0, 0);
+                double* C = S + 16 * ib * CR_LD + 16 * jb;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) C[(4 * v + lk) * CR_LD + l16] -= acc[v];
+            }
+        __syncthreads();
+    }
+    // L^-1 in place, block columns from the right
+    for (int j = 7; j >= 0; --j) {
+        const double* Ij = Inv + j * 256;
+        if (j < 7) {
+            // W_k = L_kj L_jj^-1 over L_kj
+            if (wave < 7 - j) {
+                double* Lk = S + 16 * (j + 1 + wave) * CR_LD + 16 * j;
+                dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(Lk[l16 * CR_LD + 4 * kk + lk],
+                                                               Ij[(4 * kk + lk) * 16 + l16], acc, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) Lk[(4 * v + lk) * CR_LD + l16] = acc[v];
+            }
+            __syncthreads();
+            // L^-1_ij = - sum_{k = j+1..i} L^-1_ik W_k
+            dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+            const int ib = j + 1 + wave;
+            if (wave < 7 - j) {
+                for (int k = j + 1; k <= ib; ++k) {
+                    const double* Lik = S + 16 * ib * CR_LD + 16 * k;
+                    const double* Wk = S + 16 * k * CR_LD + 16 * j;
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(Lik[l16 * CR_LD + 4 * kk + lk],
+                                                                   Wk[(4 * kk + lk) * CR_LD + l16], acc, 0, 0, 0);
+                }
+            }
+            __syncthreads();
+            if (wave < 7 - j) {
+                double* Q = S + 16 * ib * CR_LD + 16 * j;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) Q[(4 * v + lk) * CR_LD + l16] = -acc[v];
+            }
+        }
+        if (t < 256) S[(16 * j + (t >> 4)) * CR_LD + 16 * j + (t & 15)] = Ij[t];
+        __syncthreads();
+    }
+    double* Lo = c.crL + (int64_t)I * CR_MP2;
+    for (int e = t; e < CR_MP2; e += CR_T) {
+        const int r = e / CR_MP, q = e - r * CR_MP;
+        Lo[e] = q <= r ? S[r * CR_LD + q] : 0.0;
+    }
+}
+
+// Ga = L^-1 E_I (blockIdx.y 0-3: rows 32 y ..), Gb = L^-1 E_b^T (4-7), Y_I = L^-1 R_I (8) for the eliminated
+// super-block I = (2 blockIdx.x + 1) h - 1; wave w takes columns 32 w .. (rows 32 w .. of Y)
+__global__ void __launch_bounds__(256) k_cr_elim(ChArgs c, int h) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
+    const int I = (2 * (int)blockIdx.x + 1) * h - 1, y = blockIdx.y;
+    const double* Li = c.crL + (int64_t)I * CR_MP2;
+    if (y < 8) {
+        const bool left = y < 4;
+        const int nb = left ? I - h : I + h;
+        if (nb < 0 || nb >= c.nsb) return;
+        const int r0 = 32 * (y & 3), c0 = 32 * wave;
+        const double* La = Li + (int64_t)r0 * CR_MP;
+        auto fa = [&](int r, int k) { return La[r * CR_MP + k]; };
+        dbl4 acc[2][2];
+        cr_zero(acc);
+        if (left) {
+            const double* E = c.crE + (int64_t)I * CR_MP2 + c0;
+            cr_mma(acc, 0, r0 + 32, fa, [&](int k, int q) { return E[k * CR_MP + q]; }, l16, lk);
+        } else {
+            const double* E = c.crE + (int64_t)nb * CR_MP2 + (int64_t)c0 * CR_MP;
+            cr_mma(acc, 0, r0 + 32, fa, [&](int k, int q) { return E[q * CR_MP + k]; }, l16, lk);
+        }
+        double* G = (left ? c.crGa : c.crGb) + (int64_t)I * CR_MP2 + (int64_t)r0 * CR_MP + c0;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) G[(16 * mi + 4 * v + lk) * CR_MP + 16 * nj + l16] = acc[mi][nj][v];
+    } else {
+        const int r0 = 32 * wave;
+        const double* La = Li + (int64_t)r0 * CR_MP;
+        const double* R = c.crR + (int64_t)I * CR_MP * CR_NR;
+        dbl4 acc[2][1];
+        cr_zero(acc);
+        cr_mma(acc, 0, r0 + 32, [&](int r, int k) { return La[r * CR_MP + k]; },
+               [&](int k, int q) { return R[k * CR_NR + q]; }, l16, lk);
+        double* Y = c.crY + ((int64_t)I * CR_MP + r0) * CR_NR;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) Y[(16 * mi + 4 * v + lk) * CR_NR + l16] = acc[mi][0][v];
+    }
+}
+
+// Schur updates of the remaining super-block K = (2 blockIdx.x + 2) h - 1 from its eliminated neighbours
+// p = K - h and q = K + h (if any): D_K (blockIdx.y 0-3), the new coupling E_K = -Gb_p^T Ga_p to p - h
+// (4-7, when p - h exists), R_K (8)
+__global__ void __launch_bounds__(256) k_cr_update(ChArgs c, int h) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
+    const int K = (2 * (int)blockIdx.x + 2) * h - 1, y = blockIdx.y;
+    const int p = K - h, q = K + h;
+    const bool hq = q < c.nsb;
+    const double* Gbp = c.crGb + (int64_t)p * CR_MP2;
+    const double* Gaq = c.crGa + (int64_t)q * CR_MP2;
+    if (y < 8) {
+        const bool dblk = y < 4;
+        if (!dblk && p - h < 0) return;
+        const int r0 = 32 * (y & 3), c0 = 32 * wave;
+        dbl4 acc[2][2];
+        cr_zero(acc);
+        cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gbp[k * CR_MP + r0 + r]; },
+               [&](int k, int cc) { return (dblk ? Gbp : c.crGa + (int64_t)p * CR_MP2)[k * CR_MP + c0 + cc]; },
+               l16, lk);
+        if (dblk && hq)
+            cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gaq[k * CR_MP + r0 + r]; },
+                   [&](int k, int cc) { return Gaq[k * CR_MP + c0 + cc]; }, l16, lk);
+        double* O = (dblk ? c.crD : c.crE) + (int64_t)K * CR_MP2 + (int64_t)r0 * CR_MP + c0;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    double* o = O + (16 * mi + 4 * v + lk) * CR_MP + 16 * nj + l16;
+                    *o = dblk ? *o - acc[mi][nj][v] : -acc[mi][nj][v];
+                }
+    } else {
+        const int r0 = 32 * wave;
+        const double* Yp = c.crY + (int64_t)p * CR_MP * CR_NR;
+        const double* Yq = c.crY + (int64_t)q * CR_MP * CR_NR;
+        dbl4 acc[2][1];
+        cr_zero(acc);
+        cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gbp[k * CR_MP + r0 + r]; },
+               [&](int k, int cc) { return Yp[k * CR_NR + cc]; }, l16, lk);
+        if (hq)
+            cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gaq[k * CR_MP + r0 + r]; },
+                   [&](int k, int cc) { return Yq[k * CR_NR + cc]; }, l16, lk);
+        double* R = c.crR + ((int64_t)K * CR_MP + r0) * CR_NR;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) R[(16 * mi + 4 * v + lk) * CR_NR + l16] -= acc[mi][0][v];
+    }
+}
+
+// back substitution of the super-blocks eliminated at level h: X_I = L^-T (Y_I - Ga X_a - Gb X_b)
+__global__ void __launch_bounds__(256) k_cr_back(ChArgs c, int h) {
+    __shared__ double sT[CR_MP][CR_NR + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
+    const int I = (2 * (int)blockIdx.x + 1) * h - 1, a = I - h, b = I + h;
+    const int r0 = 32 * wave;
+    dbl4 acc[2][1];
+    cr_zero(acc);
+    if (a >= 0) {
+        const double* G = c.crGa + (int64_t)I * CR_MP2 + (int64_t)r0 * CR_MP;
+        const double* X = c.crX + (int64_t)a * CR_MP * CR_NR;
+        cr_mma(acc, 0, CR_MP, [&](int r, int k) { return G[r * CR_MP + k]; },
+               [&](int k, int q) { return X[k * CR_NR + q]; }, l16, lk);
+    }
+    if (b < c.nsb) {
+        const double* G = c.crGb + (int64_t)I * CR_MP2 + (int64_t)r0 * CR_MP;
+        const double* X = c.crX + (int64_t)b * CR_MP * CR_NR;
+        cr_mma(acc, 0, CR_MP, [&](int r, int k) { return G[r * CR_MP + k]; },
+               [&](int k, int q) { return X[k * CR_NR + q]; }, l16, lk);
+    }
+    const double* Y = c.crY + (int64_t)I * CR_MP * CR_NR;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r = r0 + 16 * mi + 4 * v + lk;
+            sT[r][l16] = Y[r * CR_NR + l16] - acc[mi][0][v];
+        }
+    __syncthreads();
+    const double* Li = c.crL + (int64_t)I * CR_MP2;
+    cr_zero(acc);
+    cr_mma(acc, r0, CR_MP, [&](int r, int k) { return Li[k * CR_MP + r0 + r]; },
+           [&](int k, int q) { return sT[k][q]; }, l16, lk);
+    double* X = c.crX + ((int64_t)I * CR_MP + r0) * CR_NR;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) X[(16 * mi + 4 * v + lk) * CR_NR + l16] = acc[mi][0][v];
+}
+
+// X of local entry u = i db + r (image i) and right-hand side col
+__device__ __forceinline__ double cr_x(const ChArgs& c, int64_t u, int col) {
+    const int i = (int)(u / c.db), r = (int)(u - (int64_t)i * c.db);
+    const int I = i / c.s;
+    return c.crX[((int64_t)I * CR_MP + (i - I * c.s) * c.db + r) * CR_NR + col];
+}
+
+// border: the corner's Schur complement C - B^T S_loc^-1 B and rhs b_s - B^T S_loc^-1 b_loc, reduced in a
+// fixed order (per thread, then the waves' lanes, then the waves), factored and solved by thread 0
+__global__ void __launch_bounds__(1024) k_cr_border(ba_pcg_args a, ChArgs c) {
+    __shared__ double part[CR_NR - 1][CR_NR][16];
+    __shared__ double Cc[(CR_NR - 1) * (CR_NR - 1)], rb[CR_NR - 1], xb[CR_NR - 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, ns = c.n_shared;
+    const int64_t nl = (int64_t)a.n_imgs * c.db;
+    for (int b1 = 0; b1 < ns; ++b1)
+        for (int col = 0; col <= ns; ++col) {
+            double s = 0.0;
+            for (int64_t u = t; u < nl; u += 1024) s += c.Bfull[(int64_t)b1 * nl + u] * cr_x(c, u, col);
+            for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+            if (lane == 0) part[b1][col][wave] = s;
+        }
+    __syncthreads();
+    if (t == 0) {
+        for (int b1 = 0; b1 < ns; ++b1)
+            for (int col = 0; col <= ns; ++col) {
+                double s = 0.0;
+                for (int w = 0; w < 16; ++w) s += part[b1][col][w];
+                if (col == 0) rb[b1] = a.rhs[c.shared_u[b1]] - s;
+                else Cc[b1 * ns + col - 1] = c.Cb[b1 * ns + col - 1] - s;
+            }
+        for (int r = 0; r < ns; ++r)
+            for (int q = 0; q <= r; ++q) {
+                double v = Cc[r * ns + q];
+                for (int m = 0; m < q; ++m) v -= Cc[r * ns + m] * Cc[q * ns + m];
+                if (r == q) {
+                    if (!(v > 0.0)) {
+                        atomicMin(c.info, (int32_t)(nl + r + 1));
+                        v = 1.0;
+                    }
+                    Cc[r * ns + r] = sqrt(v);
+                } else {
+                    Cc[r * ns + q] = v / Cc[q * ns + q];
+                }
+            }
+        for (int r = 0; r < ns; ++r) {
+            double v = rb[r];
+            for (int m = 0; m < r; ++m) v -= Cc[r * ns + m] * rb[m];
+            rb[r] = v / Cc[r * ns + r];
+        }
+        for (int r = ns - 1; r >= 0; --r) {
+            double v = rb[r];
+            for (int m = r + 1; m < ns; ++m) v -= Cc[m * ns + r] * xb[m];
+            xb[r] = v / Cc[r * ns + r];
+        }
+        for (int r = 0; r < ns; ++r) {
+            a.x[c.shared_u[r]] = xb[r];
+            c.crXb[r] = xb[r];
+        }
+    }
+}
+
+// the local solution: x_loc = S_loc^-1 b_loc - S_loc^-1 B x_s
+__global__ void __launch_bounds__(CH_T) k_cr_local(ba_pcg_args a, ChArgs c) {
+    const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    if (u >= (int64_t)a.n_imgs * c.db) return;
+    double v = cr_x(c, u, 0);
+    for (int b = 0; b < c.n_shared; ++b) v -= cr_x(c, u, 1 + b) * c.crXb[b];
+    c.xl[u] = v;
+}
+
 }  // namespace ba
 
 using namespace ba;
@@ -768,8 +1221,17 @@ extern "C" int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_img
     // banded: d is the band block size db
     if (mode == 0) return 3 * ba_chol_dense_lda(n_u);
     const int64_t M = (int64_t)(w + 1) * d, nl = (int64_t)n_imgs * d;
-    return (int64_t)n_imgs * (w + 1) * d * d + (int64_t)n_shared * nl + (int64_t)n_shared * n_shared + nl +
-           (int64_t)n_imgs * M * d + (int64_t)n_imgs * n_shared * d + 2 * nl;
+    int64_t n = (int64_t)n_imgs * (w + 1) * d * d + (int64_t)n_shared * nl + (int64_t)n_shared * n_shared + nl +
+                (int64_t)n_imgs * M * d + (int64_t)n_imgs * n_shared * d + 2 * nl;
+    const int32_t nsb = mode == 1 ? ba_chol_band_superblocks(d, w, n_shared, n_imgs) : 0;
+    if (nsb > 0) n += (int64_t)nsb * (5 * CR_MP2 + 3 * CR_MP * CR_NR) + CR_NR;
+    return n;
+}
+
+extern "C" int32_t ba_chol_band_superblocks(int32_t d, int32_t w, int32_t n_shared, int32_t n_imgs) {
+    const int s = cr_images(d, w, n_shared);
+    if (s == 0 || n_imgs < 1) return 0;
+    return (n_imgs + s - 1) / s;
 }
 
 extern "C" int64_t ba_chol_band_lds_bytes(int32_t d, int32_t w, int32_t n_shared) {
@@ -801,12 +1263,14 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     if (rc != BA_OK) return rc;
     hipLaunchKernelGGL(k_info_init, dim3(1), dim3(64), 0, st, c.info);
     const unsigned nbu = (unsigned)((a.n_u + CH_T - 1) / CH_T);
-    if (ca.mode == 1) {
-        BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.db <= CB_MAXD && ca.bcol != nullptr && ca.bpos != nullptr,
-                   "ba_reduced_solve: the banded layout needs db <= 16, bcol, bpos");
+    if (ca.mode == 1 || ca.mode == 2) {
+        BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.bcol != nullptr && ca.bpos != nullptr,
+                   "ba_reduced_solve: the banded layout needs 1 <= db <= d, bcol, bpos");
         const int d = ca.db, M = (ca.w + 1) * d;
-        BA_REQUIRE(ca.w >= 0 && M <= CB_MAXM && ca.n_shared <= CB_MAXS,
-                   "ba_reduced_solve: the banded layout needs (w + 1) d <= 160 and at most 8 shared unknowns");
+        const int s_cr = ca.mode == 1 ? cr_images(d, ca.w, ca.n_shared) : 0;
+        BA_REQUIRE(ca.w >= 1 && (s_cr > 0 || (d <= CB_MAXD && M <= CB_MAXM && ca.n_shared <= CB_MAXS)),
+                   "ba_reduced_solve: the banded layout needs w >= 1 and either w db <= 128 with at most 15 shared "
+                   "unknowns (mode 1) or db <= 16, (w + 1) db <= 160 and at most 8 shared unknowns");
         const int64_t nl = (int64_t)a.n_imgs * d;
         double* w = ca.work;
         c.Ab = w; w += (int64_t)a.n_imgs * (ca.w + 1) * d * d;
@@ -816,13 +1280,52 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
         c.Lcol = w; w += (int64_t)a.n_imgs * M * d;
         c.Lbord = w; w += (int64_t)a.n_imgs * ca.n_shared * d;
         c.yv = w; w += nl;
-        c.xl = w;
+        c.xl = w; w += nl;
+        if (s_cr > 0) {
+            c.s = s_cr;
+            c.nsb = (a.n_imgs + s_cr - 1) / s_cr;
+            const int64_t big = (int64_t)c.nsb * CR_MP2, rhs = (int64_t)c.nsb * CR_MP * CR_NR;
+            c.crD = w; w += big;
+            c.crE = w; w += big;
+            c.crL = w; w += big;
+            c.crGa = w; w += big;
+            c.crGb = w; w += big;
+            c.crR = w; w += rhs;
+            c.crY = w; w += rhs;
+            c.crX = w; w += rhs;
+            c.crXb = w;
+        }
         const int64_t nab = (int64_t)a.n_imgs * (ca.w + 1) * d * d;
         hipLaunchKernelGGL(k_band_assemble, dim3((unsigned)((nab + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
         if (ca.n_shared > 0) {
             hipLaunchKernelGGL(k_shared_local, dim3(nbu, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 1);
             hipLaunchKernelGGL(k_shared_shared, dim3((unsigned)ca.n_shared, (unsigned)ca.n_shared), dim3(CH_T), 0,
                                st, a, c, 1, n_pairs);
+        }
+        if (s_cr > 0) {
+            const int nsb = c.nsb;
+            const int64_t big = (int64_t)nsb * CR_MP2;
+            hipLaunchKernelGGL(k_cr_assemble, dim3((unsigned)((big + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
+            const size_t cr_lds = (size_t)CR_LDS_DOUBLES * sizeof(double);
+            BA_HIP(hipFuncSetAttribute((const void*)k_cr_factor, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)cr_lds));
+            int levels = 0;
+            for (int h = 1; h <= nsb; h *= 2, ++levels) {
+                const int n_elim = (nsb / h + 1) / 2, n_kept = nsb / (2 * h);
+                hipLaunchKernelGGL(k_cr_factor, dim3((unsigned)n_elim), dim3(CR_T), cr_lds, st, c, h);
+                hipLaunchKernelGGL(k_cr_elim, dim3((unsigned)n_elim, 9), dim3(256), 0, st, c, h);
+                if (n_kept > 0) hipLaunchKernelGGL(k_cr_update, dim3((unsigned)n_kept, 9), dim3(256), 0, st, c, h);
+            }
+            for (int l = levels - 1; l >= 0; --l) {
+                const int h = 1 << l;
+                hipLaunchKernelGGL(k_cr_back, dim3((unsigned)((nsb / h + 1) / 2)), dim3(256), 0, st, c, h);
+            }
+            if (ca.n_shared > 0) hipLaunchKernelGGL(k_cr_border, dim3(1), dim3(1024), 0, st, a, c);
+            hipLaunchKernelGGL(k_cr_local, dim3((unsigned)((nl + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
+            hipLaunchKernelGGL(k_band_scatter, dim3(nbu), dim3(CH_T), 0, st, a, c);
+            hipLaunchKernelGGL(k_chol_status, dim3(1), dim3(64), 0, st, a, c.info);
+            BA_LAUNCHED();
+            return BA_OK;
         }
         const size_t lds_bytes = (size_t)band_lds_doubles(M, ca.n_shared) * sizeof(double);
         BA_REQUIRE(lds_bytes <= 160 * 1024, "ba_reduced_solve: the banded window does not fit LDS (use mode 0)");

@@ -269,9 +269,12 @@ int64_t ba_pcg_partials_size(int64_t n_u);
  * (ba_solver.py:208-226: S = A - B D^-1 C, torch.linalg.solve(S, rhs) at :220).  S_u is symmetric
  * positive definite (fp64, damped), so it is factored L L^T: densely (mode 0, any structure), or, when
  * every image pair lies within w images and few unknowns are shared, as a block band of width w with
- * the shared unknowns as a dense border (mode 1, one workgroup). */
+ * the shared unknowns as a dense border (mode 1: by block cyclic reduction over super-blocks of
+ * 128 unknowns when w db <= 128 and n_shared <= 15, else by one workgroup walking the images;
+ * mode 2: always the one-workgroup walk). */
 typedef struct {
-    int32_t mode;                /* 0: dense (any structure); 1: banded with a dense border */
+    int32_t mode;                /* 0: dense (any structure); 1: banded with a dense border (cyclic reduction
+                                    where it applies); 2: banded, one workgroup */
     double* A;                   /* dense: (lda, lda) workspace; the lower triangle of S_u, then L */
     int64_t lda;                 /* dense: ba_chol_dense_lda(n_u) (n_u rounded up to 64) */
     double* Linv;                /* dense: (lda / 64, 64, 64) inverses of the diagonal tiles of L */
@@ -279,9 +282,10 @@ typedef struct {
     const int32_t* kind;         /* (n_u): 1 local (one image-level entry), 2 shared (several: a mono
                                     camera's focal pair, a rig node), 0 isolated (none) */
     const int32_t* shared_u;     /* (n_shared): the shared unknowns */
-    int32_t n_shared;            /* banded: at most 8 */
-    int32_t w;                   /* banded: every image pair (i, j) has |i - j| <= w (>= 1); (w + 1) db <= 160
-                                    and ba_chol_band_lds_bytes(db, w, n_shared) <= 160 KB */
+    int32_t n_shared;            /* banded: at most 15 (cyclic reduction) or 8 (one workgroup) */
+    int32_t w;                   /* banded: every image pair (i, j) has |i - j| <= w (>= 1); cyclic reduction:
+                                    w db <= 128; one workgroup: (w + 1) db <= 160 and
+                                    ba_chol_band_lds_bytes(db, w, n_shared) <= 160 KB */
     int32_t db;                  /* banded: block size, the number of image-level columns that carry a
                                     local unknown in some image (a mono camera's focal pair is left out) */
     const int32_t* bcol;         /* banded: (db) image-level column of each band column */
@@ -296,6 +300,9 @@ int64_t ba_chol_dense_lda(int64_t n_u);
 /* LDS bytes of the banded layout's workgroup (d = db); mode 1 requires at most 160 KB */
 int64_t ba_chol_band_lds_bytes(int32_t d, int32_t w, int32_t n_shared);
 int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_imgs, int32_t d, int32_t w, int32_t n_shared);
+/* super-blocks of mode 1's cyclic reduction for this structure (d = db), or 0 when mode 1 runs the
+ * one-workgroup factor (no counterpart in the reference: a layout query) */
+int32_t ba_chol_band_superblocks(int32_t d, int32_t w, int32_t n_shared, int32_t n_imgs);
 
 /* Uses every field of ba_pcg_args that the unknown-level setup of ba_pcg_solve uses (umap, inv lists,
  * leaf, S_pairs, e_img, dg_img, dampen / adaptive, rhs, diagA, damp, state) and writes delta_c to

@@ -856,17 +856,21 @@ def test_lm_step_full_config2_line_search():
           flush=True)
 
 
-@pytest.mark.parametrize('layout', ['dense', 'auto'])
-@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800),
-                                        (2, 70, 3000)])
+_CHOL_CASES = [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800), (2, 70, 3000)]
+
+
+@pytest.mark.parametrize('cfg,nf,nt,layout', [c + (l,) for l in ('dense', 'auto') for c in _CHOL_CASES] +
+                         [c + ('banded_sequential',) for c in _CHOL_CASES if c[0] in (0, 2, 4)] +
+                         [(2, 150, 4000, 'auto')])
 def test_reduced_solve_cholesky_parity(cfg, nf, nt, layout):
-    """solver='cholesky' (ba_reduced_solve, dense L L^T of the damped reduced system on the device)
-    against the oracle's direct solve of the reference's explicit Schur system (solve_reduced_direct,
+    """solver='cholesky' (ba_reduced_solve, L L^T of the damped reduced system on the device) against
+    the oracle's direct solve of the reference's explicit Schur system (solve_reduced_direct,
     ba_solver.py:208-226): the device's own system is solved to a relative residual of 1e-10, and the
     full step agrees with the oracle's on sqrt(W) J delta to 1e-6, widened only by 5x the oracle's own
     move when its fp32 inputs are rounded differently.  layout 'auto' takes the banded factor wherever
-    the structure allows it (configs 0, 2 and 4 here: every image pair within (w + 1) d <= 160), the
-    dense one elsewhere; 'dense' forces the dense one."""
+    the structure allows it (configs 0, 2 and 4 here: every image pair within w images), by block cyclic
+    reduction over super-blocks (checked to have run, on several levels at 70 and 150 frames), the dense
+    one elsewhere; 'dense' forces the dense one, 'banded_sequential' the one-workgroup banded walk."""
     from tests.step_checks import oracle_system, rounded_differently, weighted_jdelta, device_system
     print(f'cholesky parity cfg {cfg} ({nf} frames, {nt} tracks), layout {layout}', flush=True)
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
@@ -884,6 +888,10 @@ def test_reduced_solve_cholesky_parity(cfg, nf, nt, layout):
                              g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
     delta = gs.solve_delta(J, res, w)
     assert gs.last['direct'] is not None and gs.last['direct']['first_bad_pivot'] is None
+    if layout == 'auto' and cfg == 2:
+        assert gs.last['direct']['layout'] == 'banded' and gs.last['direct']['superblocks'] >= (5 if nf >= 70 else 1)
+    if layout == 'banded_sequential':
+        assert gs.last['direct']['layout'] == 'banded_sequential' and gs.last['direct']['superblocks'] == 0
     ist = gs.last['istate'].cpu()
     assert int(ist[2]) == 0 and int(ist[3]) == 1
     S_dev, rhs_dev, _ = device_system(gs)
