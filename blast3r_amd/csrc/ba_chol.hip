@@ -56,6 +56,8 @@ struct ChArgs {
     // banded by block cyclic reduction: nsb super-blocks of s images (CR_MP unknowns each, padded)
     int32_t nsb, s;
     double *crD, *crE, *crR, *crL, *crGa, *crGb, *crY, *crX, *crXb;
+    double* ss_part;            // (n_shared (n_shared + 1), 64) partial sums: the shared-shared entries, then
+                                // the border products of the cyclic reduction
 };
 
 // ------------------------------------------------------------------ assembly
@@ -75,22 +77,6 @@ __device__ __forceinline__ double s_img(const ba_pcg_args& a, const int32_t* __r
     return p >= 0 ? a.S_pairs[((int64_t)p * d + c) * d + r] : 0.0;
 }
 
-// S_u(s, v) for a shared unknown s and a local one v = entry (j, cv): the sum over the pairs of image
-// row j of B[cv][r] over the entries (i, r) of the other image that carry s (B = S(j, i)).
-__device__ double shared_local(const ba_pcg_args& a, int s, int j, int cv) {
-    const int d = a.d;
-    double val = 0.0;
-    for (int q = a.row_ptr[j]; q < a.row_ptr[j + 1]; ++q) {
-        const int ent = a.row_ent[q];
-        const int p = ent >> 1, tr = ent & 1;
-        const int i = tr ? a.pair_i1[p] : a.pair_i2[p];
-        const double* S = a.S_pairs + (int64_t)p * d * d;
-        for (int r = 0; r < d; ++r)
-            if (a.umap[(int64_t)i * d + r] == s) val += tr ? S[r * d + cv] : S[cv * d + r];
-    }
-    return val;
-}
-
 // dense: S_u[u][v] for v <= u where neither is shared (the identity on the padding rows n_u .. N, the
 // damping alone on an isolated unknown), one thread per (u, v)
 __global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c, int64_t N) {
@@ -100,7 +86,7 @@ __global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c
     double val = 0.0;
     if (u < a.n_u && v < a.n_u) {
         const int ku = c.kind[u], kv = c.kind[v];
-        if (ku == 2 || kv == 2) return;                 // k_shared_local / k_shared_shared
+        if (ku == 2 || kv == 2) return;                 // k_shared_local / k_shared_part
         if (ku == 1 && kv == 1) {
             const int ea = a.inv_src[a.inv_ptr[u]], eb = a.inv_src[a.inv_ptr[v]];
             const int ia = ea / a.d, ib = eb / a.d;
@@ -113,16 +99,29 @@ __global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c
     c.A[u * c.lda + v] = val;
 }
 
-// S_u(s, v) for every shared s (blockIdx.y) and every local v: written to the dense matrix (mode 0)
-// or to the border rows Bfull[s][entry of v] (mode 1)
+// S_u(s, v) for every shared s (blockIdx.y) and every local v (one wave each; lane l sums the pairs l, l + 64, ..
+// of v's image row, the lanes are summed in a fixed tree): written to the dense matrix (mode 0) or to the
+// border rows Bfull[s][entry of v] (mode 1)
 __global__ void __launch_bounds__(CH_T) k_shared_local(ba_pcg_args a, ChArgs c, int mode) {
-    const int64_t v = (int64_t)blockIdx.x * CH_T + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int64_t v = (int64_t)blockIdx.x * (CH_T / 64) + (threadIdx.x >> 6);
     const int sb = blockIdx.y;
     if (v >= a.n_u || c.kind[v] != 1) return;
     const int s = c.shared_u[sb];
+    const int d = a.d;
     const int e = a.inv_src[a.inv_ptr[v]];
-    const int j = e / a.d, cv = e - j * a.d;
-    const double val = shared_local(a, s, j, cv);
+    const int j = e / d, cv = e - j * d;
+    double val = 0.0;
+    for (int q = a.row_ptr[j] + lane; q < a.row_ptr[j + 1]; q += 64) {
+        const int ent = a.row_ent[q];
+        const int p = ent >> 1, tr = ent & 1;
+        const int i = tr ? a.pair_i1[p] : a.pair_i2[p];
+        const double* S = a.S_pairs + (int64_t)p * d * d;
+        for (int r = 0; r < d; ++r)
+            if (a.umap[(int64_t)i * d + r] == s) val += tr ? S[r * d + cv] : S[cv * d + r];
+    }
+    for (int off = 32; off > 0; off >>= 1) val += __shfl_xor(val, off);
+    if (lane != 0) return;
     if (mode == 0) {
         const int64_t r = s > v ? s : v, q = s > v ? v : s;
         c.A[r * c.lda + q] = val;
@@ -131,20 +130,24 @@ __global__ void __launch_bounds__(CH_T) k_shared_local(ba_pcg_args a, ChArgs c, 
     }
 }
 
-// S_u(s1, s2) for shared s2 <= s1 (by list position): one workgroup per pair summing every pair
-// block's entries that carry (s1, s2), in a fixed order; the damping on the diagonal.
-__global__ void __launch_bounds__(CH_T) k_shared_shared(ba_pcg_args a, ChArgs c, int mode, int64_t n_pairs) {
-    __shared__ double sh[CH_T];
-    const int b1 = blockIdx.x, b2 = blockIdx.y;
+// S_u(s1, s2) for shared s2 <= s1 (by list position): every pair block's entries that carry (s1, s2),
+// summed by block (b1 n_s + b2, chunk) over a fixed slice of the image pairs (pair p goes to chunk
+// (p / CH_T) mod SS_CHUNKS), then over the chunks in order by k_shared_sum, with the damping on the diagonal
+#define SS_CHUNKS 64
+__global__ void __launch_bounds__(CH_T) k_shared_part(ba_pcg_args a, ChArgs c, int64_t n_pairs) {
+    __shared__ double sh[CH_T / 64];
+    const int ns = c.n_shared;
+    const int b1 = (int)blockIdx.x / ns, b2 = (int)blockIdx.x - b1 * ns;
     if (b2 > b1) return;
     const int s1 = c.shared_u[b1], s2 = c.shared_u[b2];
     const int d = a.d;
     double val = 0.0;
-    for (int64_t p = threadIdx.x; p < n_pairs; p += CH_T) {
+    for (int64_t p = (int64_t)blockIdx.y * CH_T + threadIdx.x; p < n_pairs; p += (int64_t)SS_CHUNKS * CH_T) {
         const int i1 = a.pair_i1[p], i2 = a.pair_i2[p];
         const double* S = a.S_pairs + p * d * d;
         for (int r = 0; r < d; ++r) {
             const int u1 = a.umap[(int64_t)i1 * d + r];
+            if (u1 != s1 && u1 != s2) continue;
             for (int q = 0; q < d; ++q) {
                 const int u2 = a.umap[(int64_t)i2 * d + q];
                 if (u1 == s1 && u2 == s2) val += S[r * d + q];
@@ -152,21 +155,33 @@ __global__ void __launch_bounds__(CH_T) k_shared_shared(ba_pcg_args a, ChArgs c,
             }
         }
     }
-    sh[threadIdx.x] = val;
+    for (int off = 32; off > 0; off >>= 1) val += __shfl_xor(val, off);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = val;
     __syncthreads();
-    for (int w = CH_T / 2; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
-        __syncthreads();
-    }
     if (threadIdx.x == 0) {
-        double t = sh[0] + (s1 == s2 ? a.damp[s1] : 0.0);
-        if (mode == 0) {
-            const int64_t r = s1 > s2 ? s1 : s2, q = s1 > s2 ? s2 : s1;
-            c.A[r * c.lda + q] = t;
-        } else {
-            c.Cb[b1 * c.n_shared + b2] = t;
-            c.Cb[b2 * c.n_shared + b1] = t;
-        }
+        double t = 0.0;
+        for (int w = 0; w < CH_T / 64; ++w) t += sh[w];
+        c.ss_part[(int64_t)blockIdx.x * SS_CHUNKS + blockIdx.y] = t;
+    }
+}
+
+// written to the dense matrix (mode 0) or to the corner Cb (mode 1)
+__global__ void __launch_bounds__(CH_T) k_shared_sum(ba_pcg_args a, ChArgs c, int mode) {
+    const int ns = c.n_shared;
+    const int e = (int)(blockIdx.x * CH_T + threadIdx.x);
+    if (e >= ns * ns) return;
+    const int b1 = e / ns, b2 = e - b1 * ns;
+    if (b2 > b1) return;
+    double t = 0.0;
+    for (int k = 0; k < SS_CHUNKS; ++k) t += c.ss_part[(int64_t)e * SS_CHUNKS + k];
+    const int s1 = c.shared_u[b1], s2 = c.shared_u[b2];
+    if (s1 == s2) t += a.damp[s1];
+    if (mode == 0) {
+        const int64_t r = s1 > s2 ? s1 : s2, q = s1 > s2 ? s2 : s1;
+        c.A[r * c.lda + q] = t;
+    } else {
+        c.Cb[b1 * ns + b2] = t;
+        c.Cb[b2 * ns + b1] = t;
     }
 }
 
@@ -828,37 +843,95 @@ __global__ void __launch_bounds__(CH_T) k_cr_assemble(ba_pcg_args a, ChArgs c) {
     }
 }
 
-// acc[mi][nj] += A B over k in [kb, ke) (multiples of 4) for the 16 x 16 tiles (16 mi, 16 nj) of a wave:
-// fa(r, k) = A[r][k], fb(k, c) = B[k][c] relative to the wave's corner (v_mfma_f64_16x16x4f64 operand lane
-// l: row / column l % 16, k = l / 16; accumulator element v of lane l: row 4 v + l / 16, column l % 16)
-template <int NI, int NJ, class FA, class FB>
-__device__ __forceinline__ void cr_mma(dbl4 (&acc)[NI][NJ], int kb, int ke, FA fa, FB fb, int l16, int lk) {
-#pragma unroll 4
-    for (int k = kb; k < ke; k += 4) {
-        double av[NI], bv[NJ];
+// acc += A B over k in [kb, ke) (multiples of 16) for one 16 x 16 tile of a wave: fa(r, k) = A[r][k],
+// fb(k, c) = B[k][c] relative to the tile's corner (v_mfma_f64_16x16x4f64 operand lane l: row / column
+// l % 16, k = l / 16; accumulator element v of lane l: row 4 v + l / 16, column l % 16).  The operands of
+// 16 k are loaded before their MFMAs.
+template <class FA, class FB>
+__device__ __forceinline__ void cr_mma(dbl4& acc, int kb, int ke, FA fa, FB fb, int l16, int lk) {
+    for (int k = kb; k < ke; k += 16) {
+        double av[4], bv[4];
 #pragma unroll
-        for (int mi = 0; mi < NI; ++mi) av[mi] = fa(16 * mi + l16, k + lk);
+        for (int kk = 0; kk < 4; ++kk) {
+            av[kk] = fa(l16, k + 4 * kk + lk);
+            bv[kk] = fb(k + 4 * kk + lk, l16);
+        }
 #pragma unroll
-        for (int nj = 0; nj < NJ; ++nj) bv[nj] = fb(k + lk, 16 * nj + l16);
-#pragma unroll
-        for (int mi = 0; mi < NI; ++mi)
-#pragma unroll
-            for (int nj = 0; nj < NJ; ++nj)
-                acc[mi][nj] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mi], bv[nj], acc[mi][nj], 0, 0, 0);
+        for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[kk], bv[kk], acc, 0, 0, 0);
     }
 }
 
-template <int NI, int NJ>
-__device__ __forceinline__ void cr_zero(dbl4 (&acc)[NI][NJ]) {
+// lane src's v in every lane (src uniform)
+__device__ __forceinline__ double lane_bcast(double v, int src) {
+    const int2 b = __builtin_bit_cast(int2, v);
+    return __builtin_bit_cast(double, make_int2(__builtin_amdgcn_readlane(b.x, src), __builtin_amdgcn_readlane(b.y, src)));
+}
+
+// 1 / sqrt(x) for x > 0: the hardware estimate refined by two Newton steps y (3 - x y^2) / 2
+__device__ __forceinline__ double rsqrt_nr(double x) {
+    double y = __builtin_amdgcn_rsq(x);
+    const double hx = 0.5 * x;
+    y = y * fma(-hx * y, y, 1.5);
+    y = y * fma(-hx * y, y, 1.5);
+    return y;
+}
+
+// Diagonal block p of the super-block factor, by wave 0: L_pp and L_pp^-1 (to Inv[p]; the block of S keeps
+// L_pp below its diagonal and garbage above).  Lane r (mod 16) holds row r.  Step j sends the unscaled
+// column j through LDS (Inv[p] serves as staging) while the pivot's reciprocal square root is formed, and
+// updates row r by a_rj a_qj / a_jj; entries above the diagonal take updates too (no predication) and are
+// never read.  A pivot that is not positive is recorded in info and replaced by 1.
+__device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __restrict__ Inv, int p, int lane,
+                                              int32_t* __restrict__ info, int32_t pos0) {
+    const int r = lane & 15;
+    double* B = S + 16 * p * CR_LD + 16 * p;
+    double* col = Inv + p * 256;
+    double row[16];
 #pragma unroll
-    for (int mi = 0; mi < NI; ++mi)
+    for (int q = 0; q < 16; ++q) row[q] = q <= r ? B[r * CR_LD + q] : 0.0;
+    double rinv = 0.0;
 #pragma unroll
-        for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = (dbl4){0.0, 0.0, 0.0, 0.0};
+    for (int j = 0; j < 16; ++j) {
+        if (j < 15 && lane < 16) col[16 * j + r] = row[j];      // a wave's LDS accesses complete in order
+        double pj = lane_bcast(row[j], j);
+        if (!(pj > 0.0)) {
+            if (lane == 0) atomicMin(info, pos0 + j + 1);
+            pj = 1.0;
+        }
+        const double rs = rsqrt_nr(pj);
+        if (j < 15) {
+            const double tj = row[j] * (rs * rs);
+#pragma unroll
+            for (int q = j + 1; q < 16; ++q) row[q] = fma(-tj, col[16 * j + q], row[q]);
+        }
+        row[j] = r == j ? pj * rs : row[j] * rs;
+        rinv = r == j ? rs : rinv;
+    }
+    // the factored rows through LDS (B); lane c (mod 16) forms column c of L_pp^-1 by forward substitution,
+    // reading the rows at uniform addresses
+    if (lane < 16) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) B[r * CR_LD + q] = row[q];
+    }
+    double x[16];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+        const double ri = lane_bcast(rinv, rr);
+        double sum = 0.0;
+#pragma unroll
+        for (int mm = 0; mm < rr; ++mm) sum = fma(B[rr * CR_LD + mm], x[mm], sum);
+        x[rr] = rr == r ? ri : (rr > r ? -ri * sum : 0.0);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) col[rr * 16 + r] = x[rr];
+    }
 }
 
 // One workgroup per eliminated super-block I = (2 blockIdx.x + 1) h - 1: D_I = L L^T in LDS by 16-column
-// panels (wave 0 factors and inverts the 16 x 16 diagonal block with lane shuffles; the panel below and
-// the trailing blocks are MFMA products), then L^-1 in place by block columns from the right
+// panels (wave 0 factors and inverts the 16 x 16 diagonal block; the panel below and the trailing blocks
+// are MFMA products; wave 0 takes the next diagonal block's trailing update first and factors it while
+// the other waves finish the trailing blocks), then L^-1 in place by block columns from the right
 // (L^-1_ij = - sum_{k = j+1..i} L^-1_ik L_kj L_jj^-1), written to crL[I] (lower; zero above).
 __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
     extern __shared__ double lds[];
@@ -873,57 +946,9 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
         S[r * CR_LD + q] = q <= r ? D[e] : 0.0;
     }
     __syncthreads();
-    for (int p = 0; p < 8; ++p) {
-        double* B = S + 16 * p * CR_LD + 16 * p;
-        if (wave == 0) {
-            // lane r (mod 16) holds row r of the diagonal block
-            const int r = l16;
-            double row[16];
-#pragma unroll
-            for (int q = 0; q < 16; ++q) row[q] = q <= r ? B[r * CR_LD + q] : 0.0;
-            double rinv = 0.0;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                double pj = __shfl(row[j], j);
-                if (!(pj > 0.0)) {
-                    if (lane == 0) atomicMin(c.info, (int32_t)(I * CR_MP + 16 * p + j + 1));
-                    pj = 1.0;
-                }
-                const double rs = rsqrt(pj);
-                if (r == j) {
-                    row[j] = pj * rs;
-                    rinv = rs;
-                } else if (r > j) {
-                    row[j] *= rs;
-                }
-                const double lj = row[j];
-#pragma unroll
-                for (int q = j + 1; q < 16; ++q) {
-                    const double lqj = __shfl(lj, q);
-                    if (r >= q) row[q] -= lj * lqj;
-                }
-            }
-            if (lane < 16) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    if (q <= r) B[r * CR_LD + q] = row[q];
-            }
-            // lane c (mod 16) forms column c of L_pp^-1 by forward substitution (rows read back from LDS)
-            double x[16];
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const double ri = __shfl(rinv, rr);
-                double sum = 0.0;
-#pragma unroll
-                for (int mm = 0; mm < rr; ++mm) sum += B[rr * CR_LD + mm] * x[mm];
-                x[rr] = rr == l16 ? ri : (rr > l16 ? -ri * sum : 0.0);
-            }
-            if (lane < 16) {
-#pragma unroll
-                for (int rr = 0; rr < 16; ++rr) Inv[p * 256 + rr * 16 + l16] = x[rr];
-            }
-        }
-        __syncthreads();
+    if (wave == 0) cr_diag_block(S, Inv, 0, lane, c.info, I * CR_MP);
+    __syncthreads();
+    for (int p = 0; p < 7; ++p) {
         // panel: L_ip = A_ip L_pp^-T for the block rows below
         if (wave < 7 - p) {
             double* Ab = S + 16 * (p + 1 + wave) * CR_LD + 16 * p;
@@ -937,11 +962,13 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
             for (int v = 0; v < 4; ++v) Ab[(4 * v + lk) * CR_LD + l16] = acc[v];
         }
         __syncthreads();
-        // trailing blocks (ib, jb), p < jb <= ib: A_ij -= L_ip L_jp^T
+        // trailing blocks (ib, jb), p < jb <= ib: A_ij -= L_ip L_jp^T; wave 0 takes (p + 1, p + 1) and then
+        // factors it, waves 1-7 the others
         int tc = 0;
         for (int ib = p + 1; ib < 8; ++ib)
-            for (int jb = p + 1; jb <= ib; ++jb, ++tc) {
-                if ((tc & 7) != wave) continue;
+            for (int jb = p + 1; jb <= ib; ++jb) {
+                const bool mine = (ib == p + 1) ? wave == 0 : (wave != 0 && tc++ % 7 == wave - 1);
+                if (!mine) continue;
                 const double* Li = S + 16 * ib * CR_LD + 16 * p;
                 const double* Lj = S + 16 * jb * CR_LD + 16 * p;
                 dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
@@ -953,6 +980,7 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) C[(4 * v + lk) * CR_LD + l16] -= acc[v];
             }
+        if (wave == 0) cr_diag_block(S, Inv, p + 1, lane, c.info, I * CR_MP + 16 * (p + 1));
         __syncthreads();
     }
     // L^-1 in place, block columns from the right
@@ -1001,54 +1029,46 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
     }
 }
 
-// Ga = L^-1 E_I (blockIdx.y 0-3: rows 32 y ..), Gb = L^-1 E_b^T (4-7), Y_I = L^-1 R_I (8) for the eliminated
-// super-block I = (2 blockIdx.x + 1) h - 1; wave w takes columns 32 w .. (rows 32 w .. of Y)
+// Ga = L^-1 E_I, Gb = L^-1 E_b^T and Y_I = L^-1 R_I for the eliminated super-block I = (2 blockIdx.x + 1) h - 1,
+// one 16 x 16 tile per wave: blockIdx.y 0-15 Ga (tile row y / 2, tile columns 4 (y % 2) + wave), 16-31 Gb,
+// 32-33 Y (tile row 4 (y - 32) + wave)
 __global__ void __launch_bounds__(256) k_cr_elim(ChArgs c, int h) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
     const int I = (2 * (int)blockIdx.x + 1) * h - 1, y = blockIdx.y;
     const double* Li = c.crL + (int64_t)I * CR_MP2;
-    if (y < 8) {
-        const bool left = y < 4;
+    dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+    if (y < 32) {
+        const bool left = y < 16;
         const int nb = left ? I - h : I + h;
         if (nb < 0 || nb >= c.nsb) return;
-        const int r0 = 32 * (y & 3), c0 = 32 * wave;
+        const int r0 = 16 * ((y & 15) >> 1), c0 = 16 * (4 * (y & 1) + wave);
         const double* La = Li + (int64_t)r0 * CR_MP;
         auto fa = [&](int r, int k) { return La[r * CR_MP + k]; };
-        dbl4 acc[2][2];
-        cr_zero(acc);
         if (left) {
             const double* E = c.crE + (int64_t)I * CR_MP2 + c0;
-            cr_mma(acc, 0, r0 + 32, fa, [&](int k, int q) { return E[k * CR_MP + q]; }, l16, lk);
+            cr_mma(acc, 0, r0 + 16, fa, [&](int k, int q) { return E[k * CR_MP + q]; }, l16, lk);
         } else {
             const double* E = c.crE + (int64_t)nb * CR_MP2 + (int64_t)c0 * CR_MP;
-            cr_mma(acc, 0, r0 + 32, fa, [&](int k, int q) { return E[q * CR_MP + k]; }, l16, lk);
+            cr_mma(acc, 0, r0 + 16, fa, [&](int k, int q) { return E[q * CR_MP + k]; }, l16, lk);
         }
         double* G = (left ? c.crGa : c.crGb) + (int64_t)I * CR_MP2 + (int64_t)r0 * CR_MP + c0;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) G[(16 * mi + 4 * v + lk) * CR_MP + 16 * nj + l16] = acc[mi][nj][v];
+        for (int v = 0; v < 4; ++v) G[(4 * v + lk) * CR_MP + l16] = acc[v];
     } else {
-        const int r0 = 32 * wave;
+        const int r0 = 16 * (4 * (y - 32) + wave);
         const double* La = Li + (int64_t)r0 * CR_MP;
         const double* R = c.crR + (int64_t)I * CR_MP * CR_NR;
-        dbl4 acc[2][1];
-        cr_zero(acc);
-        cr_mma(acc, 0, r0 + 32, [&](int r, int k) { return La[r * CR_MP + k]; },
+        cr_mma(acc, 0, r0 + 16, [&](int r, int k) { return La[r * CR_MP + k]; },
                [&](int k, int q) { return R[k * CR_NR + q]; }, l16, lk);
         double* Y = c.crY + ((int64_t)I * CR_MP + r0) * CR_NR;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) Y[(16 * mi + 4 * v + lk) * CR_NR + l16] = acc[mi][0][v];
+        for (int v = 0; v < 4; ++v) Y[(4 * v + lk) * CR_NR + l16] = acc[v];
     }
 }
 
 // Schur updates of the remaining super-block K = (2 blockIdx.x + 2) h - 1 from its eliminated neighbours
-// p = K - h and q = K + h (if any): D_K (blockIdx.y 0-3), the new coupling E_K = -Gb_p^T Ga_p to p - h
-// (4-7, when p - h exists), R_K (8)
+// p = K - h and q = K + h (if any), one 16 x 16 tile per wave: D_K (blockIdx.y 0-15), the new coupling
+// E_K = -Gb_p^T Ga_p to p - h (16-31, when p - h exists), R_K (32-33)
 __global__ void __launch_bounds__(256) k_cr_update(ChArgs c, int h) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
     const int K = (2 * (int)blockIdx.x + 2) * h - 1, y = blockIdx.y;
@@ -1056,34 +1076,27 @@ __global__ void __launch_bounds__(256) k_cr_update(ChArgs c, int h) {
     const bool hq = q < c.nsb;
     const double* Gbp = c.crGb + (int64_t)p * CR_MP2;
     const double* Gaq = c.crGa + (int64_t)q * CR_MP2;
-    if (y < 8) {
-        const bool dblk = y < 4;
+    dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+    if (y < 32) {
+        const bool dblk = y < 16;
         if (!dblk && p - h < 0) return;
-        const int r0 = 32 * (y & 3), c0 = 32 * wave;
-        dbl4 acc[2][2];
-        cr_zero(acc);
+        const int r0 = 16 * ((y & 15) >> 1), c0 = 16 * (4 * (y & 1) + wave);
+        const double* Bm = dblk ? Gbp : c.crGa + (int64_t)p * CR_MP2;
         cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gbp[k * CR_MP + r0 + r]; },
-               [&](int k, int cc) { return (dblk ? Gbp : c.crGa + (int64_t)p * CR_MP2)[k * CR_MP + c0 + cc]; },
-               l16, lk);
+               [&](int k, int cc) { return Bm[k * CR_MP + c0 + cc]; }, l16, lk);
         if (dblk && hq)
             cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gaq[k * CR_MP + r0 + r]; },
                    [&](int k, int cc) { return Gaq[k * CR_MP + c0 + cc]; }, l16, lk);
         double* O = (dblk ? c.crD : c.crE) + (int64_t)K * CR_MP2 + (int64_t)r0 * CR_MP + c0;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    double* o = O + (16 * mi + 4 * v + lk) * CR_MP + 16 * nj + l16;
-                    *o = dblk ? *o - acc[mi][nj][v] : -acc[mi][nj][v];
-                }
+        for (int v = 0; v < 4; ++v) {
+            double* o = O + (4 * v + lk) * CR_MP + l16;
+            *o = dblk ? *o - acc[v] : -acc[v];
+        }
     } else {
-        const int r0 = 32 * wave;
+        const int r0 = 16 * (4 * (y - 32) + wave);
         const double* Yp = c.crY + (int64_t)p * CR_MP * CR_NR;
         const double* Yq = c.crY + (int64_t)q * CR_MP * CR_NR;
-        dbl4 acc[2][1];
-        cr_zero(acc);
         cr_mma(acc, 0, CR_MP, [&](int r, int k) { return Gbp[k * CR_MP + r0 + r]; },
                [&](int k, int cc) { return Yp[k * CR_NR + cc]; }, l16, lk);
         if (hq)
@@ -1091,20 +1104,18 @@ __global__ void __launch_bounds__(256) k_cr_update(ChArgs c, int h) {
                    [&](int k, int cc) { return Yq[k * CR_NR + cc]; }, l16, lk);
         double* R = c.crR + ((int64_t)K * CR_MP + r0) * CR_NR;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) R[(16 * mi + 4 * v + lk) * CR_NR + l16] -= acc[mi][0][v];
+        for (int v = 0; v < 4; ++v) R[(4 * v + lk) * CR_NR + l16] -= acc[v];
     }
 }
 
-// back substitution of the super-blocks eliminated at level h: X_I = L^-T (Y_I - Ga X_a - Gb X_b)
-__global__ void __launch_bounds__(256) k_cr_back(ChArgs c, int h) {
+// back substitution of the super-blocks eliminated at level h: X_I = L^-T (Y_I - Ga X_a - Gb X_b), wave w
+// the rows 16 w ..
+__global__ void __launch_bounds__(512) k_cr_back(ChArgs c, int h) {
     __shared__ double sT[CR_MP][CR_NR + 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lk = lane >> 4;
     const int I = (2 * (int)blockIdx.x + 1) * h - 1, a = I - h, b = I + h;
-    const int r0 = 32 * wave;
-    dbl4 acc[2][1];
-    cr_zero(acc);
+    const int r0 = 16 * wave;
+    dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
     if (a >= 0) {
         const double* G = c.crGa + (int64_t)I * CR_MP2 + (int64_t)r0 * CR_MP;
         const double* X = c.crX + (int64_t)a * CR_MP * CR_NR;
@@ -1119,22 +1130,18 @@ __global__ void __launch_bounds__(256) k_cr_back(ChArgs c, int h) {
     }
     const double* Y = c.crY + (int64_t)I * CR_MP * CR_NR;
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int r = r0 + 16 * mi + 4 * v + lk;
-            sT[r][l16] = Y[r * CR_NR + l16] - acc[mi][0][v];
-        }
+    for (int v = 0; v < 4; ++v) {
+        const int r = r0 + 4 * v + lk;
+        sT[r][l16] = Y[r * CR_NR + l16] - acc[v];
+    }
     __syncthreads();
     const double* Li = c.crL + (int64_t)I * CR_MP2;
-    cr_zero(acc);
+    acc = (dbl4){0.0, 0.0, 0.0, 0.0};
     cr_mma(acc, r0, CR_MP, [&](int r, int k) { return Li[k * CR_MP + r0 + r]; },
            [&](int k, int q) { return sT[k][q]; }, l16, lk);
     double* X = c.crX + ((int64_t)I * CR_MP + r0) * CR_NR;
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) X[(16 * mi + 4 * v + lk) * CR_NR + l16] = acc[mi][0][v];
+    for (int v = 0; v < 4; ++v) X[(4 * v + lk) * CR_NR + l16] = acc[v];
 }
 
 // X of local entry u = i db + r (image i) and right-hand side col
@@ -1144,57 +1151,67 @@ __device__ __forceinline__ double cr_x(const ChArgs& c, int64_t u, int col) {
     return c.crX[((int64_t)I * CR_MP + (i - I * c.s) * c.db + r) * CR_NR + col];
 }
 
-// border: the corner's Schur complement C - B^T S_loc^-1 B and rhs b_s - B^T S_loc^-1 b_loc, reduced in a
-// fixed order (per thread, then the waves' lanes, then the waves), factored and solved by thread 0
-__global__ void __launch_bounds__(1024) k_cr_border(ba_pcg_args a, ChArgs c) {
-    __shared__ double part[CR_NR - 1][CR_NR][16];
-    __shared__ double Cc[(CR_NR - 1) * (CR_NR - 1)], rb[CR_NR - 1], xb[CR_NR - 1];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, ns = c.n_shared;
+// border: the corner's Schur complement C - B^T S_loc^-1 B and rhs b_s - B^T S_loc^-1 b_loc.  k_cr_bpart sums
+// B[b1] . X[:, col] over a fixed slice of the local entries (block (chunk, b1 (n_s + 1) + col)), lanes and
+// waves in a fixed tree; k_cr_border adds the chunks in order, factors the corner and solves (thread 0).
+#define BP_CHUNKS 64
+static_assert(BP_CHUNKS <= SS_CHUNKS, "the border products share the shared-shared partial-sum buffer");
+__global__ void __launch_bounds__(CH_T) k_cr_bpart(ba_pcg_args a, ChArgs c) {
+    __shared__ double sh[CH_T / 64];
+    const int ns = c.n_shared, combo = blockIdx.y, b1 = combo / (ns + 1), col = combo - b1 * (ns + 1);
+    const int64_t nl = (int64_t)a.n_imgs * c.db;
+    double s = 0.0;
+    for (int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x; u < nl; u += (int64_t)BP_CHUNKS * CH_T)
+        s += c.Bfull[(int64_t)b1 * nl + u] * cr_x(c, u, col);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < CH_T / 64; ++w) t += sh[w];
+        c.ss_part[(int64_t)combo * BP_CHUNKS + blockIdx.x] = t;
+    }
+}
+
+__global__ void k_cr_border(ba_pcg_args a, ChArgs c) {
+    double Cc[(CR_NR - 1) * (CR_NR - 1)], rb[CR_NR - 1], xb[CR_NR - 1];
+    if (threadIdx.x != 0) return;
+    const int ns = c.n_shared;
     const int64_t nl = (int64_t)a.n_imgs * c.db;
     for (int b1 = 0; b1 < ns; ++b1)
         for (int col = 0; col <= ns; ++col) {
             double s = 0.0;
-            for (int64_t u = t; u < nl; u += 1024) s += c.Bfull[(int64_t)b1 * nl + u] * cr_x(c, u, col);
-            for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-            if (lane == 0) part[b1][col][wave] = s;
+            for (int k = 0; k < BP_CHUNKS; ++k) s += c.ss_part[(int64_t)(b1 * (ns + 1) + col) * BP_CHUNKS + k];
+            if (col == 0) rb[b1] = a.rhs[c.shared_u[b1]] - s;
+            else Cc[b1 * ns + col - 1] = c.Cb[b1 * ns + col - 1] - s;
         }
-    __syncthreads();
-    if (t == 0) {
-        for (int b1 = 0; b1 < ns; ++b1)
-            for (int col = 0; col <= ns; ++col) {
-                double s = 0.0;
-                for (int w = 0; w < 16; ++w) s += part[b1][col][w];
-                if (col == 0) rb[b1] = a.rhs[c.shared_u[b1]] - s;
-                else Cc[b1 * ns + col - 1] = c.Cb[b1 * ns + col - 1] - s;
-            }
-        for (int r = 0; r < ns; ++r)
-            for (int q = 0; q <= r; ++q) {
-                double v = Cc[r * ns + q];
-                for (int m = 0; m < q; ++m) v -= Cc[r * ns + m] * Cc[q * ns + m];
-                if (r == q) {
-                    if (!(v > 0.0)) {
-                        atomicMin(c.info, (int32_t)(nl + r + 1));
-                        v = 1.0;
-                    }
-                    Cc[r * ns + r] = sqrt(v);
-                } else {
-                    Cc[r * ns + q] = v / Cc[q * ns + q];
+    for (int r = 0; r < ns; ++r)
+        for (int q = 0; q <= r; ++q) {
+            double v = Cc[r * ns + q];
+            for (int m = 0; m < q; ++m) v -= Cc[r * ns + m] * Cc[q * ns + m];
+            if (r == q) {
+                if (!(v > 0.0)) {
+                    atomicMin(c.info, (int32_t)(nl + r + 1));
+                    v = 1.0;
                 }
+                Cc[r * ns + r] = sqrt(v);
+            } else {
+                Cc[r * ns + q] = v / Cc[q * ns + q];
             }
-        for (int r = 0; r < ns; ++r) {
-            double v = rb[r];
-            for (int m = 0; m < r; ++m) v -= Cc[r * ns + m] * rb[m];
-            rb[r] = v / Cc[r * ns + r];
         }
-        for (int r = ns - 1; r >= 0; --r) {
-            double v = rb[r];
-            for (int m = r + 1; m < ns; ++m) v -= Cc[m * ns + r] * xb[m];
-            xb[r] = v / Cc[r * ns + r];
-        }
-        for (int r = 0; r < ns; ++r) {
-            a.x[c.shared_u[r]] = xb[r];
-            c.crXb[r] = xb[r];
-        }
+    for (int r = 0; r < ns; ++r) {
+        double v = rb[r];
+        for (int m = 0; m < r; ++m) v -= Cc[r * ns + m] * rb[m];
+        rb[r] = v / Cc[r * ns + r];
+    }
+    for (int r = ns - 1; r >= 0; --r) {
+        double v = rb[r];
+        for (int m = r + 1; m < ns; ++m) v -= Cc[m * ns + r] * xb[m];
+        xb[r] = v / Cc[r * ns + r];
+    }
+    for (int r = 0; r < ns; ++r) {
+        a.x[c.shared_u[r]] = xb[r];
+        c.crXb[r] = xb[r];
     }
 }
 
@@ -1219,13 +1236,14 @@ extern "C" int64_t ba_chol_dense_lda(int64_t n_u) {
 extern "C" int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_imgs, int32_t d, int32_t w,
                                         int32_t n_shared) {
     // banded: d is the band block size db
-    if (mode == 0) return 3 * ba_chol_dense_lda(n_u);
+    const int64_t ss = (int64_t)n_shared * (n_shared + 1) * SS_CHUNKS;     // also BP_CHUNKS per border product
+    if (mode == 0) return 3 * ba_chol_dense_lda(n_u) + ss;
     const int64_t M = (int64_t)(w + 1) * d, nl = (int64_t)n_imgs * d;
     int64_t n = (int64_t)n_imgs * (w + 1) * d * d + (int64_t)n_shared * nl + (int64_t)n_shared * n_shared + nl +
                 (int64_t)n_imgs * M * d + (int64_t)n_imgs * n_shared * d + 2 * nl;
     const int32_t nsb = mode == 1 ? ba_chol_band_superblocks(d, w, n_shared, n_imgs) : 0;
     if (nsb > 0) n += (int64_t)nsb * (5 * CR_MP2 + 3 * CR_MP * CR_NR) + CR_NR;
-    return n;
+    return n + ss;
 }
 
 extern "C" int32_t ba_chol_band_superblocks(int32_t d, int32_t w, int32_t n_shared, int32_t n_imgs) {
@@ -1263,6 +1281,7 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     if (rc != BA_OK) return rc;
     hipLaunchKernelGGL(k_info_init, dim3(1), dim3(64), 0, st, c.info);
     const unsigned nbu = (unsigned)((a.n_u + CH_T - 1) / CH_T);
+    const unsigned nbw = (unsigned)((a.n_u + CH_T / 64 - 1) / (CH_T / 64));     // one wave per unknown
     if (ca.mode == 1 || ca.mode == 2) {
         BA_REQUIRE(ca.db >= 1 && ca.db <= a.d && ca.bcol != nullptr && ca.bpos != nullptr,
                    "ba_reduced_solve: the banded layout needs 1 <= db <= d, bcol, bpos");
@@ -1293,14 +1312,17 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
             c.crR = w; w += rhs;
             c.crY = w; w += rhs;
             c.crX = w; w += rhs;
-            c.crXb = w;
+            c.crXb = w; w += CR_NR;
         }
+        c.ss_part = w;
         const int64_t nab = (int64_t)a.n_imgs * (ca.w + 1) * d * d;
         hipLaunchKernelGGL(k_band_assemble, dim3((unsigned)((nab + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
         if (ca.n_shared > 0) {
-            hipLaunchKernelGGL(k_shared_local, dim3(nbu, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 1);
-            hipLaunchKernelGGL(k_shared_shared, dim3((unsigned)ca.n_shared, (unsigned)ca.n_shared), dim3(CH_T), 0,
-                               st, a, c, 1, n_pairs);
+            hipLaunchKernelGGL(k_shared_local, dim3(nbw, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 1);
+            hipLaunchKernelGGL(k_shared_part, dim3((unsigned)(ca.n_shared * ca.n_shared), SS_CHUNKS), dim3(CH_T), 0,
+                               st, a, c, n_pairs);
+            hipLaunchKernelGGL(k_shared_sum, dim3((unsigned)((ca.n_shared * ca.n_shared + CH_T - 1) / CH_T)),
+                               dim3(CH_T), 0, st, a, c, 1);
         }
         if (s_cr > 0) {
             const int nsb = c.nsb;
@@ -1313,14 +1335,18 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
             for (int h = 1; h <= nsb; h *= 2, ++levels) {
                 const int n_elim = (nsb / h + 1) / 2, n_kept = nsb / (2 * h);
                 hipLaunchKernelGGL(k_cr_factor, dim3((unsigned)n_elim), dim3(CR_T), cr_lds, st, c, h);
-                hipLaunchKernelGGL(k_cr_elim, dim3((unsigned)n_elim, 9), dim3(256), 0, st, c, h);
-                if (n_kept > 0) hipLaunchKernelGGL(k_cr_update, dim3((unsigned)n_kept, 9), dim3(256), 0, st, c, h);
+                hipLaunchKernelGGL(k_cr_elim, dim3((unsigned)n_elim, 34), dim3(256), 0, st, c, h);
+                if (n_kept > 0) hipLaunchKernelGGL(k_cr_update, dim3((unsigned)n_kept, 34), dim3(256), 0, st, c, h);
             }
             for (int l = levels - 1; l >= 0; --l) {
                 const int h = 1 << l;
-                hipLaunchKernelGGL(k_cr_back, dim3((unsigned)((nsb / h + 1) / 2)), dim3(256), 0, st, c, h);
+                hipLaunchKernelGGL(k_cr_back, dim3((unsigned)((nsb / h + 1) / 2)), dim3(512), 0, st, c, h);
             }
-            if (ca.n_shared > 0) hipLaunchKernelGGL(k_cr_border, dim3(1), dim3(1024), 0, st, a, c);
+            if (ca.n_shared > 0) {
+                hipLaunchKernelGGL(k_cr_bpart, dim3(BP_CHUNKS, (unsigned)(ca.n_shared * (ca.n_shared + 1))), dim3(CH_T),
+                                   0, st, a, c);
+                hipLaunchKernelGGL(k_cr_border, dim3(1), dim3(64), 0, st, a, c);
+            }
             hipLaunchKernelGGL(k_cr_local, dim3((unsigned)((nl + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a, c);
             hipLaunchKernelGGL(k_band_scatter, dim3(nbu), dim3(CH_T), 0, st, a, c);
             hipLaunchKernelGGL(k_chol_status, dim3(1), dim3(64), 0, st, a, c.info);
@@ -1344,12 +1370,15 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     double* b = ca.work;
     double* y = b + N;
     double* xs = y + N;
+    c.ss_part = xs + N;
     hipLaunchKernelGGL(k_dense_assemble, dim3((unsigned)((N + CH_T - 1) / CH_T), (unsigned)N), dim3(CH_T), 0, st, a,
                        c, N);
     if (ca.n_shared > 0) {
-        hipLaunchKernelGGL(k_shared_local, dim3(nbu, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 0);
-        hipLaunchKernelGGL(k_shared_shared, dim3((unsigned)ca.n_shared, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a,
-                           c, 0, n_pairs);
+        hipLaunchKernelGGL(k_shared_local, dim3(nbw, (unsigned)ca.n_shared), dim3(CH_T), 0, st, a, c, 0);
+        hipLaunchKernelGGL(k_shared_part, dim3((unsigned)(ca.n_shared * ca.n_shared), SS_CHUNKS), dim3(CH_T), 0, st,
+                           a, c, n_pairs);
+        hipLaunchKernelGGL(k_shared_sum, dim3((unsigned)((ca.n_shared * ca.n_shared + CH_T - 1) / CH_T)), dim3(CH_T),
+                           0, st, a, c, 0);
     }
     for (int k = 0; k < nt; ++k) {
         hipLaunchKernelGGL(k_potrf_tile, dim3(1), dim3(CH_T), 0, st, c.A, c.lda, k, c.Linv, c.info);
