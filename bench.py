@@ -148,7 +148,7 @@ def main():
     pass_traffic = pass_counter_traffic(args.config, PM_PASS_KERNELS if pm_path else PASS_KERNELS)
 
     # full LM iterations
-    lm_ms = None
+    lm_ms = lm_ms_direct = None
     if args.lm_steps > 0:
         kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
                   optim_P=o['optim_P'])
@@ -160,6 +160,16 @@ def main():
         torch.cuda.synchronize()
         lm_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
         log(f'[bench] lm_step {lm_ms:.2f} ms')
+        # the same step with the reduced system solved directly (solver='cholesky': the reference's
+        # _solve_dense_S, ba_solver.py:208-226, in place of its default _solve_CG)
+        engine.lm_step(**g.lm_inputs(), **kw, solver='cholesky')
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.lm_steps):
+            engine.lm_step(**g.lm_inputs(), **kw, solver='cholesky')
+        torch.cuda.synchronize()
+        lm_ms_direct = (time.perf_counter() - t0) * 1e3 / args.lm_steps
+        log(f'[bench] lm_step with the direct reduced solve {lm_ms_direct:.2f} ms')
 
     red = bench_reduced_solve(prob, g, dev, args.warmup) if args.reduced_solve else None
     smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
@@ -184,6 +194,7 @@ def main():
                                f'C={C}, d={d} image-level parameters, {ctx["path"]} path', 'frames': prob.n_imgs,
                    'tracks': T, 'observations': n_obs, 'C': C, 'path': ctx['path']},
         'lm_iters_per_s': (1e3 / lm_ms) if lm_ms else None,
+        'lm_iters_per_s_direct_solve': (1e3 / lm_ms_direct) if lm_ms_direct else None,
         'lm_ms_per_iter': lm_ms,
         'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
                      'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': kname,

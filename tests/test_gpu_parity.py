@@ -483,6 +483,42 @@ def test_lm_step_parity_pairmajor(cfg, nf, nt, kw):
     _check_lm_step(make_problem(cfg, n_frames=nf, n_tracks=nt, **kw), cfg, dict(path='pairmajor'))
 
 
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 70, 3000), (4, 20, 800)])
+def test_lm_step_direct_solve_parity(cfg, nf, nt):
+    """lm_step with solver='cholesky' (the reference's _solve_dense_S, ba_solver.py:208-226, in place of its
+    default _solve_CG; banded by cyclic reduction on configs 2 and 4): the step delta against the oracle's
+    direct solve on sqrt(W) J delta to 1e-6 (widened only by 5x the oracle's own move when its fp32 inputs
+    are rounded differently), then the oracle's line search on that same delta: the same scales tried and
+    accepted, loss and updated parameters within 1e-5."""
+    from tests.step_checks import rounded_differently, weighted_jdelta
+    print(f'lm_step (direct solve) parity cfg {cfg} ({nf} frames, {nt} tracks)', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+              optim_P=o['optim_P'], solver='cholesky')
+    hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
+    g = _gpu(p)
+    info = {}
+    up_g, st_g, _ = gpu_engine._lm_step(**g.lm_inputs(), **kw, info=info)
+    direct = info['solver'].last['direct']
+    assert direct is not None and direct['first_bad_pivot'] is None
+    if cfg in (2, 4):
+        assert direct['layout'] == 'banded' and direct['superblocks'] >= 1
+    inp = p.lm_inputs()
+    sysd = _oracle_system(inp, hp, dict(optim_K=o['optim_K'], optim_P=o['optim_P']))
+    assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-5 * abs(float(sysd['loss']))
+    ref = osol.solve_reduced_direct(sysd['ne'], sysd['g'])
+    jd_ref = weighted_jdelta(sysd, ref)
+    gen = torch.Generator().manual_seed(cfg)
+    moves = [rel_err(weighted_jdelta(sysd, osol.solve_reduced_direct(alt['ne'], alt['g'])), jd_ref)
+             for alt in (rounded_differently(sysd, gen) for _ in range(2))]
+    bar = max([1e-6] + [5 * m for m in moves])
+    e_j = rel_err(weighted_jdelta(sysd, info['delta']), jd_ref)
+    print(f'  {direct}: sqrt(W) J delta {e_j:.2e} (bar {bar:.1e})', flush=True)
+    assert e_j <= bar, (e_j, bar)
+    _check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g)
+
+
 def _check_lm_step(p, cfg, solver_kw):
     o = p.options
     kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
