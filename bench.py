@@ -227,7 +227,8 @@ def bench_layout(prob, g, dev, steps, warmup):
     """Observation-structure edits of the online pipeline at the configuration's size: `old | new`
     (tracks.py:84-102) with old = every observation of the configuration and new = one more frame
     whose 1000 tracks are seen in the last 12 frames, then `remove` of 1% of the tracks
-    (tracks.py:116-127) and the rebuild of the structure plan for the merged set.  The bare gather
+    (tracks.py:116-127) and the rebuild of the structure plan for the merged set; the plan of `old | new`
+    made from the old set's plan (ba_plan_append, wall clock with the device copies).  The bare gather
     launch sequence (ba_tracks_gather) is timed with events on its stream; algorithmic bytes per
     output row: one row read and written, 2 (4 + 8 + 8 + 4 C)."""
     import ctypes
@@ -276,6 +277,20 @@ def bench_layout(prob, g, dev, steps, warmup):
     merged = old | new
     torch.cuda.synchronize()
     merge_ms = (time.perf_counter() - t0) * 1e3
+    # the structure plan of the merged set, made from the old set's plan (ba_plan_append), as the solver's
+    # next lm_step makes it: the old plan is the one the pass above used
+    from blast3r_amd.plan import get_plan
+    get_plan(g.infos, g.pids, T, device=dev)
+    infos_m = torch.stack([torch.cumsum(merged.nppi.long(), 0), torch.arange(n_imgs + 1, device=dev),
+                           torch.zeros(n_imgs + 1, dtype=torch.long, device=dev)]).to(torch.int32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan_m = get_plan(infos_m, merged.pids, merged.n_tracks, device=dev)
+    torch.cuda.synchronize()
+    append_ms = (time.perf_counter() - t0) * 1e3
+    appended = plan_m.stable_prefix is not None
+    kept_frac = plan_m.stable_prefix['chunk_ent'] / max(1, plan_m.sizes['chunk_ent']) if appended else 0.0
+    del plan_m
     bad = torch.randperm(T + 1000, device=dev, generator=gen)[:(T + 1000) // 100]
     merged.remove(bad)
     torch.cuda.synchronize()
@@ -290,12 +305,14 @@ def bench_layout(prob, g, dev, steps, warmup):
     torch.cuda.synchronize()
     plan_s = time.perf_counter() - t0
     log(f'[bench] layout: gather {ms:.3f} ms ({gbs:.0f} GB/s algorithmic, {n_rows} rows); old | new {merge_ms:.2f} ms, '
-        f'remove 1% {remove_ms:.2f} ms, plan rebuild {plan_s:.3f} s')
+        f'plan of old | new {append_ms:.2f} ms ({"appended, " if appended else "full, "}{kept_frac:.3f} of the MFMA '
+        f'entries kept), remove 1% {remove_ms:.2f} ms, plan rebuild {plan_s:.3f} s')
     return {'gather_ms': ms, 'rows': n_rows, 'bytes_per_row': 2 * (20 + 4 * C),
             'roofline': {'bound': 'hbm', 'achieved': gbs, 'peak': 8000.0, 'unit': 'GB/s', 'frac': gbs / 8000.0,
                          'kernel': 'ba_tracks_gather (k_gather_rows + offsets)',
                          'traffic': measured_traffic(2, 'k_gather_rows')[0] if prob.n_imgs == 1024 else None},
-            'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s}
+            'merge_call_ms': merge_ms, 'remove_call_ms': remove_ms, 'plan_rebuild_s': plan_s,
+            'plan_append_ms': append_ms, 'plan_appended': appended, 'plan_append_kept_frac': kept_frac}
 
 
 def stream_triad(dev, n=1 << 27, reps=10):

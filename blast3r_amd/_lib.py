@@ -147,6 +147,10 @@ _SIGS = {
     'ba_plan_export': (c_int, [c_p, c_int, c_p]),
     'ba_plan_destroy': (None, [c_p]),
     'ba_plan_last_error': (ctypes.c_char_p, []),
+    'ba_plan_append': (c_p, [c_p, c_p, c_int, c_p, c_i64, c_int]),
+    'ba_plan_array': (c_p, [c_p, c_int]),
+    'ba_plan_stable': (c_int, [c_p, c_p, c_p]),
+    'ba_plan_shift_ids': (c_int, [c_p, c_p, c_p, c_i64, c_p]),
     'ba_abi_sizeof': (c_i64, [ctypes.c_char_p]),
     'ba_linearize_schur': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
     'ba_linearize_stage': (c_int, [ctypes.POINTER(BaLinArgs), c_int, c_p]),

@@ -30,11 +30,48 @@ namespace ba {
 
 static std::string g_plan_err;
 
+// a batch: a contiguous range of the track order, its images and its touched local pairs
+struct BatchDesc {
+    int32_t k0, k1;                    // range of `order`
+    std::vector<int32_t> imgs;         // local image -> global image
+    std::vector<uint32_t> rows;        // rows[a] bit b: local pair (a, b), a <= b, is touched
+};
+
+// What the planner keeps of a structure so that an appended one (old | new: per image, the old
+// observations, then the new tracks' ones) is planned by redoing only the batches it changes.
+// Observations are kept as (image, position in the image's block), which an append does not move.
+struct PlanState {
+    std::vector<int64_t> base;                 // n_imgs + 1: first observation of each image, then n_obs
+    std::vector<int64_t> tptr;                 // n_tracks + 1
+    std::vector<int32_t> tob_img, tob_pos;     // each track's observations, in observation order
+    std::vector<int32_t> tmin, tmax, tdist;    // per track: first and last image, distinct images
+    std::vector<int32_t> order;                // observed tracks by (first image, last image, track id)
+    std::vector<int64_t> oimg_ptr;             // per position of `order`: its distinct images in oimg
+    std::vector<int32_t> oimg;
+    std::vector<BatchDesc> batches;
+    std::vector<int64_t> o_ch, o_ct, o_sl, o_en;   // per batch (and one past the last): first chunk,
+                                                   // chunk track, slot and MFMA entry
+    int64_t ncov = 0;                          // sum over tracks of m (m + 1) / 2, m distinct images
+};
+
 struct Plan {
     int32_t n_imgs = 0, n_tracks = 0, L = 0, max_slots = 0;
-    int64_t n_obs = 0;
+    int64_t n_obs = 0, max_batch_obs = 0;
     std::vector<int32_t> v[BA_PLAN_NARRAYS];
     int64_t scalars[BA_PLAN_NSCALARS] = {0};
+    PlanState st;
+    // for a plan made by ba_plan_append: per array, the leading elements equal to the parent plan's (the
+    // observation ids of chunk_obs / slot_src after adding shift[image]); per image, that shift
+    int64_t stable[BA_PLAN_NARRAYS] = {0};
+    std::vector<int32_t> shift;
+};
+
+// one batch's arrays, with chunk-track ids and entry offsets local to the batch
+struct BatchOut {
+    std::vector<int32_t> chunk_obs, slot_info, s_pid, s_img, chunk_meta, ct_pid, ct_first, ct_m, ct_mask, slot_pair,
+        chunk_slots, chunk_eptr, pos_slot;
+    std::vector<uint32_t> ents;
+    bool overflow = false;
 };
 
 }  // namespace ba
@@ -58,357 +95,283 @@ static void parallel_for(int64_t n, F fn, int64_t min_per_thread = 65536) {
     for (auto& th : pool) th.join();
 }
 
-extern "C" const char* ba_plan_last_error(void) { return g_plan_err.c_str(); }
-
-extern "C" int64_t ba_abi_sizeof(const char* name) {
-    if (!name) return -1;
-    const std::string n(name);
-#define BA_SZ(T) if (n == #T) return (int64_t)sizeof(T)
-    BA_SZ(ba_huber); BA_SZ(ba_layout); BA_SZ(ba_lin_args); BA_SZ(ba_pm_args); BA_SZ(ba_pcg_args);
-    BA_SZ(ba_chol_args); BA_SZ(ba_sample_args); BA_SZ(ba_obs_set); BA_SZ(ba_gather_args); BA_SZ(ba_remove_args);
-    BA_SZ(ba_tangent_args);
-#undef BA_SZ
-    return -1;
+static bool tracks_ok(const PlanState& S, int64_t t0, int64_t t1, int L) {
+    int32_t worst_m = 0, worst_d = 0;
+    for (int64_t t = t0; t < t1; ++t) {
+        worst_m = std::max<int32_t>(worst_m, (int32_t)(S.tptr[t + 1] - S.tptr[t]));
+        worst_d = std::max(worst_d, S.tdist[t]);
+    }
+    if (worst_m > BA_CHUNK) {
+        g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")";
+        return false;
+    }
+    if (worst_d > L) {
+        g_plan_err = "a track spans more images (" + std::to_string(worst_d) + ") than max_local_imgs (" +
+                     std::to_string(L) + ")";
+        return false;
+    }
+    return true;
 }
 
-extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
-                                int32_t n_tracks, int32_t max_local_imgs, int32_t max_slots, int64_t max_batch_obs) {
-    g_plan_err.clear();
-    if (n_imgs <= 0 || n_obs < 0 || n_tracks < 0) { g_plan_err = "bad sizes"; return nullptr; }
-    if (max_local_imgs < 1 || max_local_imgs > BA_MAX_LOCAL) { g_plan_err = "max_local_imgs out of range"; return nullptr; }
-    if (max_slots < 1 || max_slots > BA_MAX_SLOTS) {
-        g_plan_err = "max_slots must be in [1, " + std::to_string(BA_MAX_SLOTS) + "]";
-        return nullptr;
-    }
-    if (n_obs >= (int64_t)1 << 30) { g_plan_err = "more than 2^30 observations"; return nullptr; }
-    if ((int64_t)cum_nkpts[n_imgs - 1] != n_obs) { g_plan_err = "infos[0][-1] != number of observations"; return nullptr; }
-    for (int i = 1; i < n_imgs; ++i)
-        if (cum_nkpts[i] < cum_nkpts[i - 1]) { g_plan_err = "infos[0] must be non-decreasing"; return nullptr; }
-
-    Plan* P = new Plan();
-    P->n_imgs = n_imgs; P->n_obs = n_obs; P->n_tracks = n_tracks; P->L = max_local_imgs; P->max_slots = max_slots;
-
-    // observation -> image, and per-track observation lists in observation (= image) order
-    std::vector<int32_t> img(n_obs);
-    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
-        for (int64_t i = i0; i < i1; ++i)
-            for (int64_t o = i ? cum_nkpts[i - 1] : 0; o < cum_nkpts[i]; ++o) img[o] = (int32_t)i;
-    }, 1);
-    std::vector<int32_t> tcnt(n_tracks, 0);
-    std::atomic<bool> bad_pid(false);
-    parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
-        for (int64_t o = o0; o < o1; ++o) {
-            const int32_t t = pids[o];
-            if (t < 0 || t >= n_tracks) { bad_pid = true; continue; }
-            __atomic_fetch_add(&tcnt[t], 1, __ATOMIC_RELAXED);
-        }
-    });
-    if (bad_pid) { g_plan_err = "pid out of range"; delete P; return nullptr; }
-    std::vector<int64_t> tptr(n_tracks + 1, 0);
-    for (int t = 0; t < n_tracks; ++t) tptr[t + 1] = tptr[t] + tcnt[t];
-    std::vector<int32_t> tobs(n_obs);
-    {
-        std::vector<int64_t> fill(tptr.begin(), tptr.end() - 1);
-        parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
-            for (int64_t o = o0; o < o1; ++o) tobs[__atomic_fetch_add(&fill[pids[o]], 1, __ATOMIC_RELAXED)] = (int32_t)o;
-        });
-        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {        // each list back in observation order
-            for (int64_t t = t0; t < t1; ++t) std::sort(tobs.begin() + tptr[t], tobs.begin() + tptr[t + 1]);
-        });
-    }
-    // distinct images per track (observations of a track are in image order)
-    std::vector<int32_t> tmin(n_tracks, INT32_MAX), tmax(n_tracks, -1), tdist(n_tracks, 0);
-    std::atomic<int32_t> worst_m(0), worst_d(0);
-    parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {
-        int32_t wm = 0, wd = 0;
-        for (int64_t t = t0; t < t1; ++t) {
-            int last = -1;
-            for (int64_t k = tptr[t]; k < tptr[t + 1]; ++k) {
-                const int i = img[tobs[k]];
-                if (i != last) { tdist[t]++; last = i; }
-                tmin[t] = std::min(tmin[t], i);
-                tmax[t] = std::max(tmax[t], i);
+// first / last / distinct images of tracks [t0, t1) from their observation lists
+static void track_extent(PlanState& S, int64_t t0, int64_t t1) {
+    parallel_for(t1 - t0, [&](int64_t a, int64_t b) {
+        for (int64_t t = t0 + a; t < t0 + b; ++t) {
+            int last = -1, mn = INT32_MAX, mx = -1, nd = 0;
+            for (int64_t k = S.tptr[t]; k < S.tptr[t + 1]; ++k) {
+                const int i = S.tob_img[k];
+                if (i != last) { nd++; last = i; }
+                mn = std::min(mn, i);
+                mx = std::max(mx, i);
             }
-            wm = std::max<int32_t>(wm, (int32_t)(tptr[t + 1] - tptr[t]));
-            wd = std::max(wd, tdist[t]);
+            S.tmin[t] = mn; S.tmax[t] = mx; S.tdist[t] = nd;
         }
-        int32_t c = worst_m.load();
-        while (wm > c && !worst_m.compare_exchange_weak(c, wm)) {}
-        c = worst_d.load();
-        while (wd > c && !worst_d.compare_exchange_weak(c, wd)) {}
     });
-    if (worst_m.load() > BA_CHUNK) {
-        g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")";
-        delete P; return nullptr;
-    }
-    if (worst_d.load() > max_local_imgs) {
-        g_plan_err = "a track spans more images (" + std::to_string(worst_d.load()) + ") than max_local_imgs (" +
-                     std::to_string(max_local_imgs) + ")";
-        delete P; return nullptr;
-    }
-    // observed tracks ordered by (first image, last image, track id): two stable counting sorts
-    std::vector<int32_t> order;
-    {
-        std::vector<int32_t> tmp;
-        tmp.reserve(n_tracks);
-        std::vector<int64_t> cnt(n_imgs + 1, 0);
-        for (int t = 0; t < n_tracks; ++t) if (tptr[t + 1] > tptr[t]) cnt[tmax[t] + 1]++;
-        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
-        int64_t n_obs_tracks = cnt[n_imgs];
-        tmp.resize(n_obs_tracks);
-        for (int t = 0; t < n_tracks; ++t) if (tptr[t + 1] > tptr[t]) tmp[cnt[tmax[t]]++] = t;
-        std::fill(cnt.begin(), cnt.end(), 0);
-        for (int t : tmp) cnt[tmin[t] + 1]++;
-        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
-        order.resize(n_obs_tracks);
-        for (int t : tmp) order[cnt[tmin[t]]++] = t;
-    }
-    // distinct image list of each track, laid out in `order`
-    std::vector<int64_t> oimg_ptr(order.size() + 1, 0);
-    for (size_t k = 0; k < order.size(); ++k) oimg_ptr[k + 1] = oimg_ptr[k] + tdist[order[k]];
-    std::vector<int32_t> oimg(oimg_ptr.back());
-    parallel_for((int64_t)order.size(), [&](int64_t k0, int64_t k1) {
-        for (int64_t k = k0; k < k1; ++k) {
-            const int t = order[k];
-            int64_t q = oimg_ptr[k];
+}
+
+// distinct image lists of the order positions [k_begin, end)
+static void order_images(PlanState& S, int64_t k_begin) {
+    const int64_t n = (int64_t)S.order.size();
+    S.oimg_ptr.resize(n + 1);
+    for (int64_t k = k_begin; k < n; ++k) S.oimg_ptr[k + 1] = S.oimg_ptr[k] + S.tdist[S.order[k]];
+    S.oimg.resize(S.oimg_ptr[n]);
+    parallel_for(n - k_begin, [&](int64_t a, int64_t b) {
+        for (int64_t k = k_begin + a; k < k_begin + b; ++k) {
+            const int t = S.order[k];
+            int64_t q = S.oimg_ptr[k];
             int last = -1;
-            for (int64_t j = tptr[t]; j < tptr[t + 1]; ++j) {
-                const int i = img[tobs[j]];
-                if (i != last) { oimg[q++] = i; last = i; }
+            for (int64_t j = S.tptr[t]; j < S.tptr[t + 1]; ++j) {
+                const int i = S.tob_img[j];
+                if (i != last) { S.oimg[q++] = i; last = i; }
             }
         }
     });
+}
 
-    // ------------------------------------------------------------ greedy batching
-    // Pass 1 (sequential): tracks are taken in order and a batch is closed when the next track
-    // would exceed max_local_imgs images, max_slots pairs or max_batch_obs observations, so every
-    // batch is a contiguous range of `order`.  Pass 2 (parallel over batches): chunks, MFMA entry
-    // lists and wave placement of each batch.  Pass 3: concatenation in batch order.
-    struct BatchDesc {
-        int32_t k0, k1;                    // range of `order`
-        std::vector<int32_t> imgs;         // local image -> global image
-        std::vector<uint32_t> rows;        // rows[a] bit b: local pair (a, b), a <= b, is touched
+// Greedy batching from order position k_begin (with an empty batch there): tracks are taken in order and a
+// batch is closed when the next track would exceed L images, max_slots pairs or max_batch_obs observations,
+// so every batch is a contiguous range of `order`.  Appends to S.batches.
+static bool greedy(PlanState& S, int64_t k_begin, int n_imgs, int L, int max_slots, int64_t max_batch_obs) {
+    std::vector<int32_t> cur_imgs;
+    std::vector<uint32_t> rows(L, 0);
+    std::vector<int32_t> limg_of(n_imgs, -1);
+    int cur_nslots = 0, n_cur = 0;
+    int64_t k_open = k_begin, cur_obs = 0;
+    auto close = [&](int64_t k_end) {
+        if (n_cur == 0) return;
+        S.batches.push_back(BatchDesc{(int32_t)k_open, (int32_t)k_end, cur_imgs, rows});
+        for (int i : cur_imgs) limg_of[i] = -1;
+        cur_imgs.clear();
+        std::fill(rows.begin(), rows.end(), 0u);
+        cur_nslots = 0; cur_obs = 0; n_cur = 0; k_open = k_end;
     };
-    std::vector<BatchDesc> batches;
-    {
-        std::vector<int32_t> cur_imgs;
-        std::vector<uint32_t> rows(max_local_imgs, 0);
-        std::vector<int32_t> limg_of(n_imgs, -1);
-        int cur_nslots = 0, k_begin = 0, n_cur = 0;
-        int64_t cur_obs = 0;
-        auto close = [&](int k_end) {
-            if (n_cur == 0) return;
-            batches.push_back(BatchDesc{k_begin, k_end, cur_imgs, rows});
-            for (int i : cur_imgs) limg_of[i] = -1;
-            cur_imgs.clear();
-            std::fill(rows.begin(), rows.end(), 0u);
-            cur_nslots = 0; cur_obs = 0; n_cur = 0; k_begin = k_end;
-        };
-        for (int kk = 0; kk < (int)order.size(); ++kk) {
-            const int t = order[kk];
-            const int32_t* timgs = oimg.data() + oimg_ptr[kk];
-            const int nti = (int)(oimg_ptr[kk + 1] - oimg_ptr[kk]);
-            const int m = (int)(tptr[t + 1] - tptr[t]);
-            for (int attempt = 0; attempt < 2; ++attempt) {
-                // local ids of the track's images (images not yet local get provisional ids)
-                const int n_loc = (int)cur_imgs.size();
-                int prov = n_loc;
-                uint32_t M = 0;
-                for (int q = 0; q < nti; ++q) {
-                    const int l = limg_of[timgs[q]];
-                    M |= 1u << (l >= 0 ? l : prov++);
-                }
-                bool ok = prov <= max_local_imgs &&
-                          (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || n_cur == 0);
-                int add_slots = 0;
-                if (ok) {
-                    // local pairs (x <= y) within M that no earlier track of the batch touched
-                    for (uint32_t r = M; r; r &= r - 1) {
-                        const int x = __builtin_ctz(r);
-                        add_slots += __builtin_popcount(M & ~((1u << x) - 1u) & ~rows[x]);
-                    }
-                    ok = cur_nslots + add_slots <= max_slots;
-                }
-                if (!ok) {
-                    if (n_cur == 0) {
-                        g_plan_err = "a single track needs more pair slots than max_slots";
-                        delete P; return nullptr;
-                    }
-                    close(kk);
-                    continue;
-                }
-                for (int q = 0; q < nti; ++q)
-                    if (limg_of[timgs[q]] < 0) { limg_of[timgs[q]] = (int)cur_imgs.size(); cur_imgs.push_back(timgs[q]); }
+    const int64_t n = (int64_t)S.order.size();
+    for (int64_t kk = k_begin; kk < n; ++kk) {
+        const int t = S.order[kk];
+        const int32_t* timgs = S.oimg.data() + S.oimg_ptr[kk];
+        const int nti = (int)(S.oimg_ptr[kk + 1] - S.oimg_ptr[kk]);
+        const int m = (int)(S.tptr[t + 1] - S.tptr[t]);
+        for (int attempt = 0; attempt < 2; ++attempt) {
+            // local ids of the track's images (images not yet local get provisional ids)
+            const int n_loc = (int)cur_imgs.size();
+            int prov = n_loc;
+            uint32_t M = 0;
+            for (int q = 0; q < nti; ++q) {
+                const int l = limg_of[timgs[q]];
+                M |= 1u << (l >= 0 ? l : prov++);
+            }
+            bool ok = prov <= L && (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || n_cur == 0);
+            int add_slots = 0;
+            if (ok) {
+                // local pairs (x <= y) within M that no earlier track of the batch touched
                 for (uint32_t r = M; r; r &= r - 1) {
                     const int x = __builtin_ctz(r);
-                    rows[x] |= M & ~((1u << x) - 1u);
+                    add_slots += __builtin_popcount(M & ~((1u << x) - 1u) & ~rows[x]);
                 }
-                cur_nslots += add_slots;
-                cur_obs += m;
-                n_cur++;
-                break;
+                ok = cur_nslots + add_slots <= max_slots;
             }
+            if (!ok) {
+                if (n_cur == 0) {
+                    g_plan_err = "a single track needs more pair slots than max_slots";
+                    return false;
+                }
+                close(kk);
+                continue;
+            }
+            for (int q = 0; q < nti; ++q)
+                if (limg_of[timgs[q]] < 0) { limg_of[timgs[q]] = (int)cur_imgs.size(); cur_imgs.push_back(timgs[q]); }
+            for (uint32_t r = M; r; r &= r - 1) {
+                const int x = __builtin_ctz(r);
+                rows[x] |= M & ~((1u << x) - 1u);
+            }
+            cur_nslots += add_slots;
+            cur_obs += m;
+            n_cur++;
+            break;
         }
-        close((int)order.size());
     }
+    close(n);
+    return true;
+}
 
-    // Pass 2: one batch's arrays, with chunk-track ids and entry offsets local to the batch
-    struct BatchOut {
-        std::vector<int32_t> chunk_obs, slot_info, chunk_meta, ct_pid, ct_first, ct_m, ct_mask, slot_pair,
-            chunk_slots, chunk_eptr, pos_slot;
-        std::vector<uint32_t> ents;
-        bool overflow = false;
-    };
-    const int n_batches = (int)batches.size();
-    std::vector<BatchOut> outs(n_batches);
-    auto build_batch = [&](int batch, std::vector<int32_t>& limg_of) {
-        const BatchDesc& bd = batches[batch];
-        BatchOut& R = outs[batch];
-        for (int a = 0; a < (int)bd.imgs.size(); ++a) limg_of[bd.imgs[a]] = a;
-        // local pair slots in (b, a) order
-        for (int b = 0; b < (int)bd.imgs.size(); ++b)
-            for (int a = 0; a <= b; ++a)
-                if ((bd.rows[a] >> b) & 1u) R.slot_pair.push_back(a | (b << 8));
-        const int nsl = (int)R.slot_pair.size();
-        std::vector<int16_t> lead;
-        int k = bd.k0;
-        while (k < bd.k1) {                                   // chunks: tracks packed whole, in order
-            int used = 0, ntr = 0;
-            const size_t base = R.chunk_obs.size();
-            R.chunk_obs.resize(base + BA_CHUNK, -1);
-            R.slot_info.resize(base + BA_CHUNK, -1);
-            const int first_ct = (int)R.ct_pid.size();
-            while (k < bd.k1) {
-                const int t = order[k];
-                const int m = (int)(tptr[t + 1] - tptr[t]);
-                if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
-                uint32_t mask = 0;
-                int last_img = -1, leader = -1;
-                for (int j = 0; j < m; ++j) {
-                    const int o = tobs[tptr[t] + j];
-                    const int lim = limg_of[img[o]];
-                    if (img[o] != last_img) { leader = used + j; last_img = img[o]; }
-                    mask |= 1u << lim;
-                    R.chunk_obs[base + used + j] = o;
-                    R.slot_info[base + used + j] = lim | (ntr << 8) | (leader << 16);
-                }
-                R.ct_pid.push_back(t);
-                R.ct_first.push_back(used);
-                R.ct_m.push_back(m);
-                R.ct_mask.push_back((int32_t)mask);
-                used += m;
-                ntr++;
-                k++;
+// One batch's chunks, MFMA entry lists and wave placement (chunk-track ids and entry offsets local to it).
+static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& limg_of, BatchOut& R) {
+    const BatchDesc& bd = S.batches[batch];
+    for (int a = 0; a < (int)bd.imgs.size(); ++a) limg_of[bd.imgs[a]] = a;
+    // local pair slots in (b, a) order
+    for (int b = 0; b < (int)bd.imgs.size(); ++b)
+        for (int a = 0; a <= b; ++a)
+            if ((bd.rows[a] >> b) & 1u) R.slot_pair.push_back(a | (b << 8));
+    const int nsl = (int)R.slot_pair.size();
+    std::vector<int16_t> lead;
+    int k = bd.k0;
+    while (k < bd.k1) {                                   // chunks: tracks packed whole, in order
+        int used = 0, ntr = 0;
+        const size_t base = R.chunk_obs.size();
+        R.chunk_obs.resize(base + BA_CHUNK, -1);
+        R.slot_info.resize(base + BA_CHUNK, -1);
+        R.s_pid.resize(base + BA_CHUNK, 0);
+        R.s_img.resize(base + BA_CHUNK, 0);
+        const int first_ct = (int)R.ct_pid.size();
+        while (k < bd.k1) {
+            const int t = S.order[k];
+            const int m = (int)(S.tptr[t + 1] - S.tptr[t]);
+            if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
+            uint32_t mask = 0;
+            int last_img = -1, leader = -1;
+            for (int j = 0; j < m; ++j) {
+                const int i = S.tob_img[S.tptr[t] + j];
+                const int lim = limg_of[i];
+                if (i != last_img) { leader = used + j; last_img = i; }
+                mask |= 1u << lim;
+                R.chunk_obs[base + used + j] = (int32_t)(S.base[i] + S.tob_pos[S.tptr[t] + j]);
+                R.slot_info[base + used + j] = lim | (ntr << 8) | (leader << 16);
+                R.s_pid[base + used + j] = t;
+                R.s_img[base + used + j] = i;
             }
-            R.chunk_meta.push_back(batch);
-            R.chunk_meta.push_back(first_ct);
-            R.chunk_meta.push_back(ntr);
-            R.chunk_meta.push_back(used);
-
-            // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
-            // first observation of each covering track in a with the one in b (chunk-track order);
-            // a diagonal slot (a, a) lists the J rows of every observation in a (slot order, padded
-            // to whole groups), then the V rows of the first observation of each (track, image) run
-            // in a (slot order)
-            lead.assign((size_t)ntr * BA_MAX_LOCAL, -1);
-            for (int sidx = 0; sidx < used; ++sidx) {
-                const int inf = R.slot_info[base + sidx];
-                lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
-            }
-            const size_t e0 = R.ents.size();
-            R.chunk_eptr.push_back((int32_t)(e0 / 4));
-            auto ent = [&](int oa, int ob) { R.ents.push_back((uint32_t)oa | ((uint32_t)ob << 16)); };
-            auto pad = [&](size_t from) { while ((R.ents.size() - from) % 4) ent(BA_ZERO, BA_ZERO); };
-            for (int q = 0; q < BA_MAX_SLOTS; ++q) {
-                if (q >= nsl) { R.chunk_slots.push_back(0); continue; }
-                const int a = R.slot_pair[q] & 0xff, bq = (R.slot_pair[q] >> 8) & 0xff;
-                const size_t off = R.ents.size() - e0;
-                int njg = 0;
-                if (a != bq) {
-                    for (int tt = 0; tt < ntr; ++tt) {
-                        const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
-                        if (la_ >= 0 && lb_ >= 0) ent(la_ * BA_BLK, lb_ * BA_BLK);
-                    }
-                } else {
-                    for (int sidx = 0; sidx < used; ++sidx)
-                        if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx * BA_BLK + BA_JROW, sidx * BA_BLK + BA_JROW);
-                    pad(e0 + off);
-                    njg = (int)((R.ents.size() - e0 - off) / 4);
-                    for (int sidx = 0; sidx < used; ++sidx) {
-                        const int inf = R.slot_info[base + sidx];
-                        if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx * BA_BLK, sidx * BA_BLK);
-                    }
-                }
-                pad(e0 + off);
-                const size_t len = R.ents.size() - e0 - off;
-                R.chunk_slots.push_back(BA_TAB(off, len / 4, njg));
-            }
-            if (R.ents.size() - e0 > BA_LIST_CAP) R.overflow = true;
-            while ((R.ents.size() - e0) % 4) R.ents.push_back(0);
+            R.ct_pid.push_back(t);
+            R.ct_first.push_back(used);
+            R.ct_m.push_back(m);
+            R.ct_mask.push_back((int32_t)mask);
+            used += m;
+            ntr++;
+            k++;
         }
-        // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
-        // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
-        // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
-        // decreasing total work and each goes where the summed per-chunk maxima grow least.
-        {
-            const int nc = (int)(R.chunk_meta.size() / 4);
-            std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
-            std::vector<int64_t> tot(nsl, 0);
-            for (int c = 0; c < nc; ++c)
-                for (int q = 0; q < nsl; ++q) {
-                    wk[(size_t)c * nsl + q] = 3 * BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]);
-                    tot[q] += wk[(size_t)c * nsl + q];
+        R.chunk_meta.push_back(batch);
+        R.chunk_meta.push_back(first_ct);
+        R.chunk_meta.push_back(ntr);
+        R.chunk_meta.push_back(used);
+
+        // MFMA entry lists of the chunk, slot by slot: an off-diagonal slot (a, b) pairs the
+        // first observation of each covering track in a with the one in b (chunk-track order);
+        // a diagonal slot (a, a) lists the J rows of every observation in a (slot order, padded
+        // to whole groups), then the V rows of the first observation of each (track, image) run
+        // in a (slot order)
+        lead.assign((size_t)ntr * BA_MAX_LOCAL, -1);
+        for (int sidx = 0; sidx < used; ++sidx) {
+            const int inf = R.slot_info[base + sidx];
+            lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
+        }
+        const size_t e0 = R.ents.size();
+        R.chunk_eptr.push_back((int32_t)(e0 / 4));
+        auto ent = [&](int oa, int ob) { R.ents.push_back((uint32_t)oa | ((uint32_t)ob << 16)); };
+        auto pad = [&](size_t from) { while ((R.ents.size() - from) % 4) ent(BA_ZERO, BA_ZERO); };
+        for (int q = 0; q < BA_MAX_SLOTS; ++q) {
+            if (q >= nsl) { R.chunk_slots.push_back(0); continue; }
+            const int a = R.slot_pair[q] & 0xff, bq = (R.slot_pair[q] >> 8) & 0xff;
+            const size_t off = R.ents.size() - e0;
+            int njg = 0;
+            if (a != bq) {
+                for (int tt = 0; tt < ntr; ++tt) {
+                    const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
+                    if (la_ >= 0 && lb_ >= 0) ent(la_ * BA_BLK, lb_ * BA_BLK);
                 }
-            std::vector<int> sorder(nsl);
-            std::iota(sorder.begin(), sorder.end(), 0);
-            std::stable_sort(sorder.begin(), sorder.end(), [&](int x, int y) { return tot[x] > tot[y]; });
-            constexpr int NS = 4;
-            std::vector<int64_t> ls((size_t)nc * NS, 0), lw((size_t)nc * BA_WAVES, 0), ms(nc, 0), mw(nc, 0);
-            int cnt[BA_WAVES] = {0};
-            R.pos_slot.assign(BA_MAX_SLOTS, -1);
-            for (int q : sorder) {
-                int best = -1;
-                int64_t best_cost = 0;
-                for (int w = 0; w < BA_WAVES; ++w) {
-                    if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
-                    const int sd = w % NS;
-                    int64_t cost = 0;
-                    for (int c = 0; c < nc; ++c) {
-                        const int64_t x = wk[(size_t)c * nsl + q];
-                        cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
-                    }
-                    if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
+            } else {
+                for (int sidx = 0; sidx < used; ++sidx)
+                    if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx * BA_BLK + BA_JROW, sidx * BA_BLK + BA_JROW);
+                pad(e0 + off);
+                njg = (int)((R.ents.size() - e0 - off) / 4);
+                for (int sidx = 0; sidx < used; ++sidx) {
+                    const int inf = R.slot_info[base + sidx];
+                    if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx * BA_BLK, sidx * BA_BLK);
                 }
-                R.pos_slot[best + BA_WAVES * cnt[best]] = q;
-                cnt[best]++;
-                const int sd = best % NS;
+            }
+            pad(e0 + off);
+            const size_t len = R.ents.size() - e0 - off;
+            R.chunk_slots.push_back(BA_TAB(off, len / 4, njg));
+        }
+        if (R.ents.size() - e0 > BA_LIST_CAP) R.overflow = true;
+        while ((R.ents.size() - e0) % 4) R.ents.push_back(0);
+    }
+    // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
+    // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
+    // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
+    // decreasing total work and each goes where the summed per-chunk maxima grow least.
+    {
+        const int nc = (int)(R.chunk_meta.size() / 4);
+        std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
+        std::vector<int64_t> tot(nsl, 0);
+        for (int c = 0; c < nc; ++c)
+            for (int q = 0; q < nsl; ++q) {
+                wk[(size_t)c * nsl + q] = 3 * BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]);
+                tot[q] += wk[(size_t)c * nsl + q];
+            }
+        std::vector<int> sorder(nsl);
+        std::iota(sorder.begin(), sorder.end(), 0);
+        std::stable_sort(sorder.begin(), sorder.end(), [&](int x, int y) { return tot[x] > tot[y]; });
+        constexpr int NS = 4;
+        std::vector<int64_t> ls((size_t)nc * NS, 0), lw((size_t)nc * BA_WAVES, 0), ms(nc, 0), mw(nc, 0);
+        int cnt[BA_WAVES] = {0};
+        R.pos_slot.assign(BA_MAX_SLOTS, -1);
+        for (int q : sorder) {
+            int best = -1;
+            int64_t best_cost = 0;
+            for (int w = 0; w < BA_WAVES; ++w) {
+                if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
+                const int sd = w % NS;
+                int64_t cost = 0;
                 for (int c = 0; c < nc; ++c) {
                     const int64_t x = wk[(size_t)c * nsl + q];
-                    ls[(size_t)c * NS + sd] += x;
-                    lw[(size_t)c * BA_WAVES + best] += x;
-                    ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
-                    mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
+                    cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
                 }
+                if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
+            }
+            R.pos_slot[best + BA_WAVES * cnt[best]] = q;
+            cnt[best]++;
+            const int sd = best % NS;
+            for (int c = 0; c < nc; ++c) {
+                const int64_t x = wk[(size_t)c * nsl + q];
+                ls[(size_t)c * NS + sd] += x;
+                lw[(size_t)c * BA_WAVES + best] += x;
+                ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
+                mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
             }
         }
-        for (int i : bd.imgs) limg_of[i] = -1;
-    };
+    }
+    for (int i : bd.imgs) limg_of[i] = -1;
+}
+
+// Batches [b0, n_batches): their arrays (built in parallel) replace whatever the plan's batch-ordered arrays
+// hold from batch b0 on; then the arrays that depend on every batch (dispatch order, global pairs, image rows,
+// per-image partial sources) and the scalars.
+static bool emit(Plan* P, int b0) {
+    PlanState& S = P->st;
+    const int n_batches = (int)S.batches.size(), L = P->L, n_imgs = P->n_imgs;
+    std::vector<BatchOut> outs(n_batches - b0);
     {
         unsigned nth = std::thread::hardware_concurrency();
         nth = std::max(1u, std::min(nth == 0 ? 1u : nth, 16u));
-        nth = (unsigned)std::min<int64_t>(nth, std::max(1, n_batches));
-        std::atomic<int> next(0);
+        nth = (unsigned)std::min<int64_t>(nth, std::max(1, n_batches - b0));
+        std::atomic<int> next(b0);
         auto work = [&]() {
             std::vector<int32_t> limg_of(n_imgs, -1);
-            for (int b = next++; b < n_batches; b = next++) build_batch(b, limg_of);
+            for (int b = next++; b < n_batches; b = next++) build_batch(S, b, limg_of, outs[b - b0]);
         };
         std::vector<std::thread> pool;
         for (unsigned w = 1; w < nth; ++w) pool.emplace_back(work);
         work();
         for (auto& th : pool) th.join();
     }
-
-    // Pass 3: concatenation in batch order
     auto& chunk_obs = P->v[BA_PA_CHUNK_OBS];      // n_chunks * BA_CHUNK obs index or -1
     auto& chunk_meta = P->v[BA_PA_CHUNK_META];    // n_chunks * 4: batch, first ctrack, n ctracks, n slots used
     auto& slot_info = P->v[BA_PA_SLOT_INFO];      // n_chunks * BA_CHUNK: local img | ctrack<<8 | leader_slot<<16 (-1 pad)
@@ -426,45 +389,60 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     auto& chunk_ent = P->v[BA_PA_CHUNK_ENT];      // 32-bit entries
     auto& chunk_eptr = P->v[BA_PA_CHUNK_EPTR];    // n_chunks + 1
     auto& b_pos_slot = P->v[BA_PA_B_POS_SLOT];    // n_batches * BA_MAX_SLOTS
-    bool list_overflow = false;
-    // offsets of each batch in the concatenated arrays, then a parallel copy
-    std::vector<int64_t> o_ch(n_batches + 1, 0), o_ct(n_batches + 1, 0), o_sl(n_batches + 1, 0), o_en(n_batches + 1, 0);
-    for (int b = 0; b < n_batches; ++b) {
-        o_ch[b + 1] = o_ch[b] + (int64_t)outs[b].chunk_meta.size() / 4;
-        o_ct[b + 1] = o_ct[b] + (int64_t)outs[b].ct_pid.size();
-        o_sl[b + 1] = o_sl[b] + (int64_t)outs[b].slot_pair.size();
-        o_en[b + 1] = o_en[b] + (int64_t)outs[b].ents.size();
-        list_overflow |= outs[b].overflow;
-    }
     auto& slot_src = P->v[BA_PA_SLOT_SRC];
     auto& s_pid = P->v[BA_PA_S_PID];
     auto& s_img = P->v[BA_PA_S_IMG];
-    chunk_obs.resize(o_ch[n_batches] * BA_CHUNK); slot_info.resize(o_ch[n_batches] * BA_CHUNK);
-    slot_src.resize(o_ch[n_batches] * BA_CHUNK); s_pid.resize(o_ch[n_batches] * BA_CHUNK);
-    s_img.resize(o_ch[n_batches] * BA_CHUNK);
-    chunk_meta.resize(o_ch[n_batches] * 4); chunk_slots.resize(o_ch[n_batches] * BA_MAX_SLOTS);
-    chunk_eptr.resize(o_ch[n_batches] + 1);
-    chunk_eptr[o_ch[n_batches]] = (int32_t)(o_en[n_batches] / 4);
+    bool list_overflow = false;
+    // offsets of each batch in the concatenated arrays, then a parallel copy
+    S.o_ch.resize(n_batches + 1); S.o_ct.resize(n_batches + 1); S.o_sl.resize(n_batches + 1); S.o_en.resize(n_batches + 1);
+    if (b0 == 0) { S.o_ch[0] = S.o_ct[0] = S.o_sl[0] = S.o_en[0] = 0; }
+    for (int b = b0; b < n_batches; ++b) {
+        const BatchOut& R = outs[b - b0];
+        S.o_ch[b + 1] = S.o_ch[b] + (int64_t)R.chunk_meta.size() / 4;
+        S.o_ct[b + 1] = S.o_ct[b] + (int64_t)R.ct_pid.size();
+        S.o_sl[b + 1] = S.o_sl[b] + (int64_t)R.slot_pair.size();
+        S.o_en[b + 1] = S.o_en[b] + (int64_t)R.ents.size();
+        list_overflow |= R.overflow;
+    }
+    if (list_overflow) {
+        g_plan_err = "a chunk needs more than BA_LIST_CAP MFMA entries";
+        return false;
+    }
+    const auto& o_ch = S.o_ch;
+    const auto& o_ct = S.o_ct;
+    const auto& o_sl = S.o_sl;
+    const auto& o_en = S.o_en;
+    const int64_t nch = o_ch[n_batches];
+    if (b0 == 0) {
+        // room for appended structures (ba_plan_append grows these arrays in place)
+        auto room = [](std::vector<int32_t>& v, int64_t n) { v.reserve((size_t)(n + n / 8 + 4096)); };
+        for (auto* v : {&chunk_obs, &slot_info, &slot_src, &s_pid, &s_img}) room(*v, nch * BA_CHUNK);
+        room(chunk_meta, nch * 4); room(chunk_slots, nch * BA_MAX_SLOTS); room(chunk_eptr, nch + 1);
+        room(chunk_ent, o_en[n_batches] + BA_LIST_CAP);
+        for (auto* v : {&ct_pid, &ct_first, &ct_m, &ct_mask}) room(*v, o_ct[n_batches]);
+    }
+    for (auto* v : {&chunk_obs, &slot_info, &slot_src, &s_pid, &s_img}) v->resize(nch * BA_CHUNK);
+    chunk_meta.resize(nch * 4); chunk_slots.resize(nch * BA_MAX_SLOTS);
+    chunk_eptr.resize(nch + 1);
+    chunk_eptr[nch] = (int32_t)(o_en[n_batches] / 4);
     for (auto* v : {&ct_pid, &ct_first, &ct_m, &ct_mask}) v->resize(o_ct[n_batches]);
     slot_pair.resize(o_sl[n_batches]);
     // the entries, and one chunk's worth of zero padding so that a full-capacity copy of the last
     // chunk's list stays inside the array
-    chunk_ent.assign((size_t)(o_en[n_batches] + BA_LIST_CAP), 0);
+    chunk_ent.resize((size_t)o_en[b0]);
+    chunk_ent.resize((size_t)(o_en[n_batches] + BA_LIST_CAP), 0);
     uint32_t* ents = reinterpret_cast<uint32_t*>(chunk_ent.data());
     b_pos_slot.resize((size_t)n_batches * BA_MAX_SLOTS);
-    parallel_for(n_batches, [&](int64_t b0, int64_t b1) {
-        for (int64_t b = b0; b < b1; ++b) {
-            BatchOut& R = outs[b];
+    parallel_for(n_batches - b0, [&](int64_t q0, int64_t q1) {
+        for (int64_t b = b0 + q0; b < b0 + q1; ++b) {
+            BatchOut& R = outs[b - b0];
             const int32_t ct0 = (int32_t)o_ct[b], e4 = (int32_t)(o_en[b] / 4);
-            std::copy(R.chunk_obs.begin(), R.chunk_obs.end(), chunk_obs.begin() + o_ch[b] * BA_CHUNK);
-            for (size_t q = 0; q < R.chunk_obs.size(); ++q) {
-                const int32_t o = R.chunk_obs[q];
-                const size_t d = (size_t)o_ch[b] * BA_CHUNK + q;
-                slot_src[d] = o >= 0 ? o : 0;
-                s_pid[d] = o >= 0 ? pids[o] : 0;
-                s_img[d] = o >= 0 ? img[o] : 0;
-            }
-            std::copy(R.slot_info.begin(), R.slot_info.end(), slot_info.begin() + o_ch[b] * BA_CHUNK);
+            const size_t c0 = (size_t)o_ch[b] * BA_CHUNK;
+            std::copy(R.chunk_obs.begin(), R.chunk_obs.end(), chunk_obs.begin() + c0);
+            for (size_t q = 0; q < R.chunk_obs.size(); ++q) slot_src[c0 + q] = R.chunk_obs[q] >= 0 ? R.chunk_obs[q] : 0;
+            std::copy(R.s_pid.begin(), R.s_pid.end(), s_pid.begin() + c0);
+            std::copy(R.s_img.begin(), R.s_img.end(), s_img.begin() + c0);
+            std::copy(R.slot_info.begin(), R.slot_info.end(), slot_info.begin() + c0);
             for (size_t c = 0; c < R.chunk_meta.size(); c += 4) {
                 int32_t* d = chunk_meta.data() + o_ch[b] * 4 + c;
                 d[0] = R.chunk_meta[c]; d[1] = R.chunk_meta[c + 1] + ct0; d[2] = R.chunk_meta[c + 2]; d[3] = R.chunk_meta[c + 3];
@@ -481,14 +459,16 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
             R = BatchOut();                                    // release as we go
         }
     }, 1);
-    for (int b = 0; b <= n_batches; ++b) {
+    b_chunk_ptr.resize(b0); b_slot_ptr.resize(b0);
+    for (int b = b0; b <= n_batches; ++b) {
         b_chunk_ptr.push_back((int32_t)o_ch[b]);
         b_slot_ptr.push_back((int32_t)o_sl[b]);
     }
-    for (int b = 0; b < n_batches; ++b) {
-        for (int a = 0; a < max_local_imgs; ++a)
-            b_imgs.push_back(a < (int)batches[b].imgs.size() ? batches[b].imgs[a] : -1);
-        b_nimgs.push_back((int32_t)batches[b].imgs.size());
+    b_imgs.resize((size_t)b0 * L); b_nimgs.resize(b0);
+    for (int b = b0; b < n_batches; ++b) {
+        for (int a = 0; a < L; ++a)
+            b_imgs.push_back(a < (int)S.batches[b].imgs.size() ? S.batches[b].imgs[a] : -1);
+        b_nimgs.push_back((int32_t)S.batches[b].imgs.size());
     }
     // Dispatch order of the Schur kernel's workgroups (one batch per CU at a time): most expensive
     // first, so that the last ones to start are short (longest-processing-time-first list
@@ -505,28 +485,34 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     }
 
     // ------------------------------------------------------------ global pairs
-    if (list_overflow) {
-        g_plan_err = "a chunk needs more than BA_LIST_CAP MFMA entries";
-        delete P;
-        return nullptr;
-    }
     int64_t n_slots = (int64_t)slot_pair.size();
     std::vector<int64_t> keys(n_slots);
     std::vector<uint8_t> swapped(n_slots, 0);
     for (int b = 0; b < n_batches; ++b)
         for (int s = b_slot_ptr[b]; s < b_slot_ptr[b + 1]; ++s) {
             int a = slot_pair[s] & 0xff, c = (slot_pair[s] >> 8) & 0xff;
-            int64_t i1 = b_imgs[(int64_t)b * max_local_imgs + a], i2 = b_imgs[(int64_t)b * max_local_imgs + c];
+            int64_t i1 = b_imgs[(int64_t)b * L + a], i2 = b_imgs[(int64_t)b * L + c];
             if (i1 > i2) { std::swap(i1, i2); swapped[s] = 1; }
             keys[s] = i1 * n_imgs + i2;
         }
+    // slots by key (i1, i2), stable: counting sorts by i2, then by i1
     std::vector<int64_t> perm(n_slots);
-    std::iota(perm.begin(), perm.end(), 0);
-    std::stable_sort(perm.begin(), perm.end(), [&](int64_t a, int64_t b) { return keys[a] < keys[b]; });
+    {
+        std::vector<int64_t> tmp(n_slots), cnt(n_imgs + 1);
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (int64_t q = 0; q < n_slots; ++q) cnt[keys[q] % n_imgs + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        for (int64_t q = 0; q < n_slots; ++q) tmp[cnt[keys[q] % n_imgs]++] = q;
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (int64_t q = 0; q < n_slots; ++q) cnt[keys[q] / n_imgs + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        for (int64_t q : tmp) perm[cnt[keys[q] / n_imgs]++] = q;
+    }
     auto& pair_i1 = P->v[BA_PA_PAIR_I1];
     auto& pair_i2 = P->v[BA_PA_PAIR_I2];
     auto& pair_ptr = P->v[BA_PA_PAIR_PTR];
     auto& pair_src = P->v[BA_PA_PAIR_SRC];
+    pair_i1.clear(); pair_i2.clear(); pair_ptr.clear(); pair_src.clear();
     slot_gpair.assign(n_slots, -1);
     pair_ptr.push_back(0);
     for (int64_t q = 0; q < n_slots; ++q) {
@@ -568,14 +554,14 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     {
         std::vector<int32_t> cnt(n_imgs + 1, 0);
         for (int b = 0; b < n_batches; ++b)
-            for (int a = 0; a < b_nimgs[b]; ++a) cnt[b_imgs[(int64_t)b * max_local_imgs + a] + 1]++;
+            for (int a = 0; a < b_nimgs[b]; ++a) cnt[b_imgs[(int64_t)b * L + a] + 1]++;
         for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
         img_ptr.assign(cnt.begin(), cnt.end());
         img_src.assign(cnt[n_imgs], 0);
         std::vector<int32_t> fill(cnt.begin(), cnt.end() - 1);
         for (int b = 0; b < n_batches; ++b)
             for (int a = 0; a < b_nimgs[b]; ++a)
-                img_src[fill[b_imgs[(int64_t)b * max_local_imgs + a]]++] = b * max_local_imgs + a;
+                img_src[fill[b_imgs[(int64_t)b * L + a]]++] = b * L + a;
     }
 
     int64_t max_slots_used = 0, max_chunks = 0;
@@ -583,18 +569,275 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
         max_slots_used = std::max<int64_t>(max_slots_used, b_slot_ptr[b + 1] - b_slot_ptr[b]);
         max_chunks = std::max<int64_t>(max_chunks, b_chunk_ptr[b + 1] - b_chunk_ptr[b]);
     }
-    P->scalars[BA_PS_N_CHUNKS] = (int64_t)(chunk_meta.size() / 4);
+    P->scalars[BA_PS_N_CHUNKS] = nch;
     P->scalars[BA_PS_N_BATCHES] = n_batches;
     P->scalars[BA_PS_N_SLOTS] = n_slots;
     P->scalars[BA_PS_N_PAIRS] = n_pairs;
     P->scalars[BA_PS_N_CTRACKS] = (int64_t)ct_pid.size();
-    P->scalars[BA_PS_L] = max_local_imgs;
+    P->scalars[BA_PS_L] = L;
     P->scalars[BA_PS_CHUNK] = BA_CHUNK;
     P->scalars[BA_PS_MAX_SLOTS_USED] = max_slots_used;
     P->scalars[BA_PS_MAX_CHUNKS_PER_BATCH] = max_chunks;
-    int64_t ncov = 0;
-    for (int t = 0; t < n_tracks; ++t) ncov += (int64_t)tdist[t] * (tdist[t] + 1) / 2;
-    P->scalars[BA_PS_N_PAIR_TERMS] = ncov;
+    P->scalars[BA_PS_N_PAIR_TERMS] = S.ncov;
+    return true;
+}
+
+extern "C" const char* ba_plan_last_error(void) { return g_plan_err.c_str(); }
+extern "C" int64_t ba_abi_sizeof(const char* name) {
+    if (!name) return -1;
+    const std::string n(name);
+#define BA_SZ(T) if (n == #T) return (int64_t)sizeof(T)
+    BA_SZ(ba_huber); BA_SZ(ba_layout); BA_SZ(ba_lin_args); BA_SZ(ba_pm_args); BA_SZ(ba_pcg_args);
+    BA_SZ(ba_chol_args); BA_SZ(ba_sample_args); BA_SZ(ba_obs_set); BA_SZ(ba_gather_args); BA_SZ(ba_remove_args);
+    BA_SZ(ba_tangent_args);
+#undef BA_SZ
+    return -1;
+}
+
+extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
+                                int32_t n_tracks, int32_t max_local_imgs, int32_t max_slots, int64_t max_batch_obs) {
+    g_plan_err.clear();
+    if (n_imgs <= 0 || n_obs < 0 || n_tracks < 0) { g_plan_err = "bad sizes"; return nullptr; }
+    if (max_local_imgs < 1 || max_local_imgs > BA_MAX_LOCAL) { g_plan_err = "max_local_imgs out of range"; return nullptr; }
+    if (max_slots < 1 || max_slots > BA_MAX_SLOTS) {
+        g_plan_err = "max_slots must be in [1, " + std::to_string(BA_MAX_SLOTS) + "]";
+        return nullptr;
+    }
+    if (n_obs >= (int64_t)1 << 30) { g_plan_err = "more than 2^30 observations"; return nullptr; }
+    if ((int64_t)cum_nkpts[n_imgs - 1] != n_obs) { g_plan_err = "infos[0][-1] != number of observations"; return nullptr; }
+    for (int i = 1; i < n_imgs; ++i)
+        if (cum_nkpts[i] < cum_nkpts[i - 1]) { g_plan_err = "infos[0] must be non-decreasing"; return nullptr; }
+
+    Plan* P = new Plan();
+    P->n_imgs = n_imgs; P->n_obs = n_obs; P->n_tracks = n_tracks; P->L = max_local_imgs; P->max_slots = max_slots;
+    P->max_batch_obs = max_batch_obs;
+    PlanState& S = P->st;
+    S.base.resize(n_imgs + 1);
+    S.base[0] = 0;
+    for (int i = 0; i < n_imgs; ++i) S.base[i + 1] = cum_nkpts[i];
+
+    // observation -> image, and per-track observation lists in observation (= image) order
+    std::vector<int32_t> img(n_obs);
+    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i)
+            for (int64_t o = S.base[i]; o < S.base[i + 1]; ++o) img[o] = (int32_t)i;
+    }, 1);
+    std::vector<int32_t> tcnt(n_tracks, 0);
+    std::atomic<bool> bad_pid(false);
+    parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
+        for (int64_t o = o0; o < o1; ++o) {
+            const int32_t t = pids[o];
+            if (t < 0 || t >= n_tracks) { bad_pid = true; continue; }
+            __atomic_fetch_add(&tcnt[t], 1, __ATOMIC_RELAXED);
+        }
+    });
+    if (bad_pid) { g_plan_err = "pid out of range"; delete P; return nullptr; }
+    S.tptr.assign(n_tracks + 1, 0);
+    for (int t = 0; t < n_tracks; ++t) S.tptr[t + 1] = S.tptr[t] + tcnt[t];
+    {
+        std::vector<int32_t> tobs(n_obs);
+        std::vector<int64_t> fill(S.tptr.begin(), S.tptr.end() - 1);
+        parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
+            for (int64_t o = o0; o < o1; ++o) tobs[__atomic_fetch_add(&fill[pids[o]], 1, __ATOMIC_RELAXED)] = (int32_t)o;
+        });
+        S.tob_img.reserve((size_t)(n_obs + n_obs / 8 + 4096));
+        S.tob_pos.reserve((size_t)(n_obs + n_obs / 8 + 4096));
+        S.tob_img.resize(n_obs);
+        S.tob_pos.resize(n_obs);
+        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {        // each list back in observation order
+            for (int64_t t = t0; t < t1; ++t) {
+                std::sort(tobs.begin() + S.tptr[t], tobs.begin() + S.tptr[t + 1]);
+                for (int64_t k = S.tptr[t]; k < S.tptr[t + 1]; ++k) {
+                    const int32_t o = tobs[k], i = img[o];
+                    S.tob_img[k] = i;
+                    S.tob_pos[k] = (int32_t)(o - S.base[i]);
+                }
+            }
+        });
+    }
+    // room for appended tracks (ba_plan_append grows the per-track state in place)
+    const size_t t_room = (size_t)n_tracks + n_tracks / 8 + 4096;
+    for (auto* v : {&S.tmin, &S.tmax, &S.tdist}) v->reserve(t_room);
+    S.tptr.reserve(t_room + 1);
+    S.tmin.assign(n_tracks, INT32_MAX); S.tmax.assign(n_tracks, -1); S.tdist.assign(n_tracks, 0);
+    track_extent(S, 0, n_tracks);
+    if (!tracks_ok(S, 0, n_tracks, max_local_imgs)) { delete P; return nullptr; }
+    // observed tracks ordered by (first image, last image, track id): two stable counting sorts
+    {
+        std::vector<int32_t> tmp;
+        tmp.reserve(n_tracks);
+        std::vector<int64_t> cnt(n_imgs + 1, 0);
+        for (int t = 0; t < n_tracks; ++t) if (S.tptr[t + 1] > S.tptr[t]) cnt[S.tmax[t] + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        int64_t n_obs_tracks = cnt[n_imgs];
+        tmp.resize(n_obs_tracks);
+        for (int t = 0; t < n_tracks; ++t) if (S.tptr[t + 1] > S.tptr[t]) tmp[cnt[S.tmax[t]]++] = t;
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (int t : tmp) cnt[S.tmin[t] + 1]++;
+        for (int i = 0; i < n_imgs; ++i) cnt[i + 1] += cnt[i];
+        S.order.reserve(t_room);
+        S.order.resize(n_obs_tracks);
+        for (int t : tmp) S.order[cnt[S.tmin[t]]++] = t;
+    }
+    S.oimg_ptr.reserve(t_room + 1);
+    S.oimg.reserve((size_t)(n_obs + n_obs / 8 + 4096));
+    S.oimg_ptr.assign(1, 0);
+    order_images(S, 0);
+    S.ncov = 0;
+    for (int t = 0; t < n_tracks; ++t) S.ncov += (int64_t)S.tdist[t] * (S.tdist[t] + 1) / 2;
+    if (!greedy(S, 0, n_imgs, max_local_imgs, max_slots, max_batch_obs) || !emit(P, 0)) { delete P; return nullptr; }
+    return P;
+}
+
+// Plan of prev's structure with new tracks appended (tracks.py:84-102): n_imgs_new = prev's n_imgs + 1;
+// image i keeps prev's observations and then gets add_cnt[i] new ones, whose track ids (add_pids, image by
+// image) are n_tracks_prev .. n_tracks_new - 1.  Byte-identical to ba_plan_create on the merged structure:
+// tracks keep their (first image, last image, id) order, so the batches that close before the first new
+// track's place are the same and only the later ones are planned again; the earlier chunks keep their
+// arrays with observation ids shifted by the new observations inserted before them (shift, per image).
+// On success prev is consumed (destroyed); on failure it is left as it was.
+extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_imgs_new, const int32_t* add_pids,
+                                int64_t n_add, int32_t n_tracks_new) {
+    g_plan_err.clear();
+    Plan* Q = (Plan*)prev;
+    if (!Q || Q->st.tptr.empty()) { g_plan_err = "no plan state to append to"; return nullptr; }
+    const int n_old = Q->n_imgs, T_old = Q->n_tracks;
+    if (n_imgs_new != n_old + 1 || n_tracks_new < T_old || n_add < 0) { g_plan_err = "not an append"; return nullptr; }
+    int64_t tot = 0;
+    for (int i = 0; i < n_imgs_new; ++i) {
+        if (add_cnt[i] < 0) { g_plan_err = "negative count"; return nullptr; }
+        tot += add_cnt[i];
+    }
+    if (tot != n_add || Q->n_obs + n_add >= ((int64_t)1 << 30)) { g_plan_err = "bad appended counts"; return nullptr; }
+    for (int64_t q = 0; q < n_add; ++q)
+        if (add_pids[q] < T_old || add_pids[q] >= n_tracks_new) { g_plan_err = "appended pid out of range"; return nullptr; }
+    // the new tracks' lists (image by image, so in observation order)
+    const int T_new = n_tracks_new, T_add = T_new - T_old;
+    std::vector<int64_t> nptr(T_add + 1, 0);
+    for (int64_t q = 0; q < n_add; ++q) nptr[add_pids[q] - T_old + 1]++;
+    for (int t = 0; t < T_add; ++t) nptr[t + 1] += nptr[t];
+    for (int t = 0; t < T_add; ++t)
+        if (nptr[t + 1] - nptr[t] > BA_CHUNK) {
+            g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")";
+            return nullptr;
+        }
+    std::vector<int32_t> n_img(n_add), n_pos(n_add);
+    {
+        std::vector<int64_t> fill(nptr.begin(), nptr.end() - 1);
+        int64_t q = 0;
+        for (int i = 0; i < n_imgs_new; ++i) {
+            const int64_t old_cnt = i < n_old ? Q->st.base[i + 1] - Q->st.base[i] : 0;
+            for (int j = 0; j < add_cnt[i]; ++j, ++q) {
+                const int64_t d = fill[add_pids[q] - T_old]++;
+                n_img[d] = i;
+                n_pos[d] = (int32_t)(old_cnt + j);
+            }
+        }
+    }
+    // the new tracks' extents and their limits, before touching prev
+    std::vector<int32_t> dn(T_add, 0), mn(T_add, INT32_MAX), mx(T_add, -1);
+    int32_t worst_d = 0;
+    for (int t = 0; t < T_add; ++t) {
+        int last = -1;
+        for (int64_t k = nptr[t]; k < nptr[t + 1]; ++k) {
+            const int i = n_img[k];
+            if (i != last) { dn[t]++; last = i; }
+            mn[t] = std::min(mn[t], i);
+            mx[t] = std::max(mx[t], i);
+        }
+        worst_d = std::max(worst_d, dn[t]);
+    }
+    if (worst_d > Q->L) {
+        g_plan_err = "a track spans more images (" + std::to_string(worst_d) + ") than max_local_imgs (" +
+                     std::to_string(Q->L) + ")";
+        return nullptr;
+    }
+    // new tracks in (first image, last image, id) order, merged into the old order
+    std::vector<int32_t> nord;
+    for (int t = 0; t < T_add; ++t) if (nptr[t + 1] > nptr[t]) nord.push_back(T_old + t);
+    auto key_new = [&](int32_t t) { return std::make_tuple(mn[t - T_old], mx[t - T_old], t); };
+    std::stable_sort(nord.begin(), nord.end(), [&](int32_t x, int32_t y) { return key_new(x) < key_new(y); });
+
+    // ---- from here on prev is consumed
+    Plan* P = Q;
+    PlanState& S = P->st;
+    const int64_t n_obs_new = P->n_obs + n_add;
+    std::vector<int64_t> base_old = S.base;
+    S.base.resize(n_imgs_new + 1);
+    {
+        int64_t acc = 0;
+        for (int i = 0; i <= n_imgs_new; ++i) {
+            const int64_t cnt_old = i < n_old ? base_old[i + 1] - base_old[i] : 0;
+            S.base[i] = acc;
+            if (i < n_imgs_new) acc += cnt_old + add_cnt[i];
+        }
+    }
+    P->shift.assign(n_imgs_new, 0);
+    for (int i = 0; i < n_old; ++i) P->shift[i] = (int32_t)(S.base[i] - base_old[i]);
+    S.tptr.resize(T_new + 1);
+    for (int t = 0; t < T_add; ++t) S.tptr[T_old + t + 1] = S.tptr[T_old] + nptr[t + 1];
+    S.tob_img.insert(S.tob_img.end(), n_img.begin(), n_img.end());
+    S.tob_pos.insert(S.tob_pos.end(), n_pos.begin(), n_pos.end());
+    S.tmin.insert(S.tmin.end(), mn.begin(), mn.end());
+    S.tmax.insert(S.tmax.end(), mx.begin(), mx.end());
+    S.tdist.insert(S.tdist.end(), dn.begin(), dn.end());
+    for (int t = 0; t < T_add; ++t) S.ncov += (int64_t)dn[t] * (dn[t] + 1) / 2;
+    auto key = [&](int32_t t) { return std::make_tuple(S.tmin[t], S.tmax[t], t); };
+    // first place of a new track in the merged order; the batches decided before it stay
+    int64_t kstar = (int64_t)S.order.size();
+    if (!nord.empty())
+        kstar = std::lower_bound(S.order.begin(), S.order.end(), nord[0],
+                                 [&](int32_t a, int32_t b) { return key(a) < key(b); }) - S.order.begin();
+    int b_star = 0;
+    {
+        const int nb = (int)S.batches.size();
+        while (b_star < nb && S.batches[b_star].k1 < kstar) ++b_star;
+    }
+    const int64_t k_re = b_star < (int)S.batches.size() ? S.batches[b_star].k0 : (int64_t)S.order.size();
+    {
+        std::vector<int32_t> tail;
+        tail.reserve(S.order.size() - kstar + nord.size());
+        std::merge(S.order.begin() + kstar, S.order.end(), nord.begin(), nord.end(), std::back_inserter(tail),
+                   [&](int32_t a, int32_t b) { return key(a) < key(b); });
+        S.order.resize(kstar);
+        S.order.insert(S.order.end(), tail.begin(), tail.end());
+    }
+    S.oimg_ptr.resize(k_re + 1);
+    order_images(S, k_re);
+    S.batches.resize(b_star);
+    P->n_imgs = n_imgs_new; P->n_obs = n_obs_new; P->n_tracks = T_new;
+    // what stays: the arrays of batches [0, b_star), observation ids shifted
+    const int64_t c_keep = S.o_ch[b_star] * BA_CHUNK;
+    for (int k = 0; k < BA_PLAN_NARRAYS; ++k) P->stable[k] = 0;
+    P->stable[BA_PA_CHUNK_OBS] = P->stable[BA_PA_SLOT_INFO] = P->stable[BA_PA_SLOT_SRC] = c_keep;
+    P->stable[BA_PA_S_PID] = P->stable[BA_PA_S_IMG] = c_keep;
+    P->stable[BA_PA_CHUNK_META] = S.o_ch[b_star] * 4;
+    P->stable[BA_PA_CHUNK_SLOTS] = S.o_ch[b_star] * BA_MAX_SLOTS;
+    P->stable[BA_PA_CHUNK_EPTR] = S.o_ch[b_star];
+    P->stable[BA_PA_CHUNK_ENT] = S.o_en[b_star];
+    for (int k : {BA_PA_CT_PID, BA_PA_CT_FIRST, BA_PA_CT_M, BA_PA_CT_MASK}) P->stable[k] = S.o_ct[b_star];
+    P->stable[BA_PA_SLOT_PAIR] = S.o_sl[b_star];
+    P->stable[BA_PA_B_CHUNK_PTR] = P->stable[BA_PA_B_SLOT_PTR] = b_star + 1;
+    P->stable[BA_PA_B_IMGS] = (int64_t)b_star * P->L;
+    P->stable[BA_PA_B_NIMGS] = b_star;
+    P->stable[BA_PA_B_POS_SLOT] = (int64_t)b_star * BA_MAX_SLOTS;
+    {
+        auto& co = P->v[BA_PA_CHUNK_OBS];
+        auto& ss = P->v[BA_PA_SLOT_SRC];
+        const auto& si = P->v[BA_PA_S_IMG];
+        const int32_t* sh = P->shift.data();
+        parallel_for(c_keep, [&](int64_t q0, int64_t q1) {
+            for (int64_t q = q0; q < q1; ++q) {
+                const int32_t d = sh[si[q]];
+                ss[q] += d;
+                if (co[q] >= 0) co[q] += d;
+            }
+        });
+    }
+    if (!greedy(S, k_re, n_imgs_new, P->L, P->max_slots, P->max_batch_obs) || !emit(P, b_star)) {
+        delete P;        // prev was consumed
+        return nullptr;
+    }
     return P;
 }
 
@@ -614,6 +857,25 @@ extern "C" int ba_plan_export(const void* plan, int32_t which, int32_t* dst) {
 }
 
 extern "C" void ba_plan_destroy(void* plan) { delete (Plan*)plan; }
+
+// the plan's array `which` in place (valid until the plan is destroyed or appended to)
+extern "C" const int32_t* ba_plan_array(const void* plan, int32_t which) {
+    const Plan* P = (const Plan*)plan;
+    if (!P || which < 0 || which >= BA_PLAN_NARRAYS) return nullptr;
+    return P->v[which].data();
+}
+
+// a plan made by ba_plan_append: per array, the leading elements equal to the parent's (after the shift of
+// chunk_obs / slot_src); per image, the shift of the parent's observation ids (0 for a plan made by
+// ba_plan_create, whose stable lengths are all 0)
+extern "C" int ba_plan_stable(const void* plan, int64_t* stable, int32_t* shift) {
+    const Plan* P = (const Plan*)plan;
+    if (!P) return 1;
+    for (int k = 0; k < BA_PLAN_NARRAYS; ++k) stable[k] = P->stable[k];
+    if (shift)
+        for (int i = 0; i < P->n_imgs; ++i) shift[i] = i < (int)P->shift.size() ? P->shift[i] : 0;
+    return 0;
+}
 
 // ---------------------------------------------------------------------------- pair-major plan
 namespace ba {

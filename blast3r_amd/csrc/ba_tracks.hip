@@ -431,3 +431,21 @@ extern "C" int ba_tracks_img_id(const int32_t* nppi, int64_t n_imgs, int64_t n_r
     BA_LAUNCHED();
     return BA_OK;
 }
+
+// ------------------------------------------------------------------ structure plan after an append
+// ids[q] += shift[img[q]] for q < n: the observation ids of a structure plan's chunk slots (chunk_obs, slot_src)
+// after ba_plan_append inserted the new tracks' observations into the image blocks (img: each slot's image, 0 for
+// an empty slot; shift[0] = 0, so an empty slot's -1 or 0 stays)
+__global__ void __launch_bounds__(TR_T) k_plan_shift_ids(int32_t* __restrict__ ids, const int32_t* __restrict__ img,
+                                                       const int32_t* __restrict__ shift, int64_t n) {
+    const int64_t q = (int64_t)blockIdx.x * TR_T + threadIdx.x;
+    if (q < n) ids[q] += shift[img[q]];
+}
+
+extern "C" int ba_plan_shift_ids(int32_t* ids, const int32_t* img, const int32_t* shift, int64_t n, void* stream) {
+    clear_error();
+    BA_REQUIRE(n >= 0 && (n == 0 || (ids != nullptr && img != nullptr && shift != nullptr)), "bad arguments");
+    if (n > 0) hipLaunchKernelGGL(k_plan_shift_ids, dim3(grid_of(n)), dim3(TR_T), 0, (hipStream_t)stream, ids, img, shift, n);
+    BA_LAUNCHED();
+    return BA_OK;
+}

@@ -16,6 +16,7 @@ from dataclasses import dataclass
 import torch
 
 from ._lib import BaGatherArgs, BaObsSet, BaRemoveArgs, check, lib, ptr, stream_ptr
+from .plan import note_append
 
 
 def _to(x, device):
@@ -210,7 +211,11 @@ class ObservedTracks:
         sel_b = torch.arange(trks.n_imgs, dtype=torch.int32)
         nppi, out = self._gather(sel_a.to(dev), other=trks, sel_b=sel_b.to(dev), shift=self.n_tracks,
                                  n_rows=self.n_kpts + trks.n_kpts, nppi_dtype=trks.nppi.dtype)
-        return ObservedTracks(trks.n_imgs, self.n_tracks + trks.n_tracks, nppi, depth_mode=self.depth_mode, **out)
+        res = ObservedTracks(trks.n_imgs, self.n_tracks + trks.n_tracks, nppi, depth_mode=self.depth_mode, **out)
+        # the solver's structure plan of the result can then be made from this set's (only the batches the
+        # new tracks reach are planned again)
+        note_append(res.pids, self.pids, self.n_tracks, trks.nppi, trks.pids)
+        return res
 
     def to_dense(self, n_imgs=None):
         """tracks.py:104-114: (n_tracks, n_imgs, 2) view, NaN where a track is not observed."""

@@ -14,7 +14,7 @@ import weakref
 import numpy as np
 import torch
 
-from ._lib import check, lib
+from ._lib import check, lib, stream_ptr
 
 # array / scalar ids (ba_plan.h)
 ARRAYS = ['chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr', 'b_imgs',
@@ -28,47 +28,126 @@ MAX_LOCAL = 16
 MAX_SLOTS = 96
 
 
+class _HostArrays:
+    """A plan's arrays on the host, exported on first use (from the host plan while it lives, else from
+    the device)."""
+
+    def __init__(self, plan):
+        self._plan = weakref.ref(plan)
+        self._d = {}
+
+    def __getitem__(self, name):
+        if name not in self._d:
+            pl = self._plan()
+            n = pl.sizes[name]
+            self._d[name] = pl._host_view(ARRAYS.index(name), n).copy() if pl._h else pl.dev[name][:n].cpu().numpy()
+        return self._d[name]
+
+    def __contains__(self, name):
+        return name in ARRAYS
+
+    def keys(self):
+        return list(ARRAYS)
+
+
 class BAPlan:
-    """Device-resident plan for one (infos, pids) structure."""
+    """Device-resident plan for one (infos, pids) structure.  The host planner's state is kept (`_h`) so
+    that the structure `old | new` can be planned from this one (BAPlan.appended), until that is done once."""
 
     def __init__(self, infos, pids, n_tracks, device=None, max_local_imgs=MAX_LOCAL, max_slots=MAX_SLOTS,
-                 max_batch_obs=0):
+                 max_batch_obs=0, _parent=None, _added=None):
         device = device or pids.device
         cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
         self.node_ids = np.ascontiguousarray(infos[1].detach().cpu().numpy().astype(np.int64))
         self.cam_ids = np.ascontiguousarray(infos[2].detach().cpu().numpy().astype(np.int64))
-        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
         self.n_imgs = int(cum.shape[0])
-        self.n_obs = int(p.shape[0])
+        self.n_obs = int(pids.shape[0])
         self.n_tracks = int(n_tracks)
+        self.options = dict(max_local_imgs=int(max_local_imgs), max_slots=int(max_slots), max_batch_obs=int(max_batch_obs))
         L = lib()
-        h = L.ba_plan_create(cum.ctypes.data_as(ctypes.c_void_p), self.n_imgs, p.ctypes.data_as(ctypes.c_void_p),
-                             self.n_obs, self.n_tracks, int(max_local_imgs), int(max_slots), int(max_batch_obs))
+        if _parent is None:
+            p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
+            h = L.ba_plan_create(cum.ctypes.data_as(ctypes.c_void_p), self.n_imgs, p.ctypes.data_as(ctypes.c_void_p),
+                                 self.n_obs, self.n_tracks, int(max_local_imgs), int(max_slots), int(max_batch_obs))
+        else:
+            add_cnt, add_pids = _added
+            h = L.ba_plan_append(ctypes.c_void_p(_parent._h), add_cnt.ctypes.data_as(ctypes.c_void_p), self.n_imgs,
+                                 add_pids.ctypes.data_as(ctypes.c_void_p), int(add_pids.shape[0]), self.n_tracks)
         if not h:
             raise RuntimeError('structure plan failed: ' + (L.ba_plan_last_error() or b'').decode())
-        try:
-            sc = np.zeros(len(SCALARS), dtype=np.int64)
-            sz = np.zeros(len(ARRAYS), dtype=np.int64)
-            check(L.ba_plan_query(h, sc.ctypes.data_as(ctypes.c_void_p), sz.ctypes.data_as(ctypes.c_void_p)))
-            self.scalars = {k: int(v) for k, v in zip(SCALARS, sc)}
-            self.host = {}
-            for i, name in enumerate(ARRAYS):
-                arr = np.empty(int(sz[i]), dtype=np.int32)
-                check(L.ba_plan_export(h, i, arr.ctypes.data_as(ctypes.c_void_p)))
-                self.host[name] = arr
-        finally:
-            L.ba_plan_destroy(h)
+        if _parent is not None:
+            _parent._h = None                  # consumed by ba_plan_append
+        self._h = h
+        sc = np.zeros(len(SCALARS), dtype=np.int64)
+        sz = np.zeros(len(ARRAYS), dtype=np.int64)
+        check(L.ba_plan_query(h, sc.ctypes.data_as(ctypes.c_void_p), sz.ctypes.data_as(ctypes.c_void_p)))
+        self.scalars = {k: int(v) for k, v in zip(SCALARS, sc)}
+        stable = np.zeros(len(ARRAYS), dtype=np.int64)
+        shift = np.zeros(max(self.n_imgs, 1), dtype=np.int32)
+        check(L.ba_plan_stable(h, stable.ctypes.data_as(ctypes.c_void_p), shift.ctypes.data_as(ctypes.c_void_p)))
         self.device = torch.device(device)
-        self.dev = {k: torch.from_numpy(v).to(self.device) for k, v in self.host.items()}
-        for k in ARRAYS:     # never hand a null pointer to a kernel for an empty array
-            if self.dev[k].numel() == 0:
-                self.dev[k] = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.dev = {}
+        self.sizes = {name: int(sz[i]) for i, name in enumerate(ARRAYS)}
+        for i, name in enumerate(ARRAYS):
+            n, keep = int(sz[i]), int(stable[i]) if _parent is not None else 0
+            host = self._host_view(i, n)
+            t = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
+            if n == 0:
+                t.zero_()                      # never hand a null pointer to a kernel for an empty array
+            if keep:
+                t[:keep].copy_(_parent.dev[name][:keep])
+            if n > keep:
+                t[keep:n].copy_(torch.from_numpy(host[keep:n]))
+            self.dev[name] = t[:n] if n else t
+        if _parent is not None and shift.any():
+            # the kept chunks' observation ids, brought to the merged structure's numbering
+            sh = torch.from_numpy(shift).to(self.device)
+            for name in ('chunk_obs', 'slot_src'):
+                keep = int(stable[ARRAYS.index(name)])
+                if self.device.type == 'cuda':
+                    check(L.ba_plan_shift_ids(ctypes.c_void_p(self.dev[name].data_ptr()),
+                                              ctypes.c_void_p(self.dev['s_img'].data_ptr()),
+                                              ctypes.c_void_p(sh.data_ptr()), keep, stream_ptr(self.device)))
+                else:
+                    self.dev[name][:keep] += sh[self.dev['s_img'][:keep].long()]
+        self.stable_prefix = {name: int(stable[i]) for i, name in enumerate(ARRAYS)} if _parent is not None else None
+        self.host = _HostArrays(self)
         self.L = int(max_local_imgs)
         self._cum = cum
-        self.slot_index = self.dev['slot_src'] if self.host['slot_src'].size else self.dev['slot_src'][:0]
+        self.slot_index = self.dev['slot_src'] if self.sizes['slot_src'] else self.dev['slot_src'][:0]
         self._slot_cache = {}
         self._ws = {}
         self.workspace_cache = {}      # derived per-structure arrays (e.g. each image's diagonal block)
+
+    def _host_view(self, which, n):
+        """Array `which` of the host plan, in place (numpy view; valid while the host plan lives)."""
+        if n == 0:
+            return np.zeros(0, dtype=np.int32)
+        addr = lib().ba_plan_array(ctypes.c_void_p(self._h), which)
+        return np.ctypeslib.as_array((ctypes.c_int32 * n).from_address(addr))
+
+    @property
+    def appendable(self):
+        return self._h is not None
+
+    @classmethod
+    def appended(cls, parent, infos, pids, n_tracks, add_cnt, add_pids):
+        """Plan of `parent`'s structure with one image and new tracks appended (`old | new`): add_cnt
+        (n_imgs + 1,) new observations per image, add_pids their track ids, image by image.  Equal to
+        BAPlan(infos, pids, n_tracks), array for array; consumes the parent's host state."""
+        if parent._h is None:
+            raise RuntimeError('the parent plan was already appended to')
+        return cls(infos, pids, n_tracks, device=parent.device, _parent=parent,
+                   _added=(np.ascontiguousarray(add_cnt, dtype=np.int32), np.ascontiguousarray(add_pids, dtype=np.int32)),
+                   **parent.options)
+
+    def __del__(self):
+        h, self._h = getattr(self, '_h', None), None
+        if h:
+            try:
+                lib().ba_plan_destroy(ctypes.c_void_p(h))
+            except Exception:
+                pass
 
     @property
     def obs_img(self):
@@ -168,9 +247,54 @@ def _prune():
             del _cache[k]
 
 
+_lineage = {}
+
+
+def note_append(pids, parent_pids, parent_n_tracks, add_nppi, add_pids):
+    """Records that the structure with track ids `pids` is `old | new` of the one with `parent_pids`
+    (tracks.py:84-102): add_nppi (n_imgs + 1,) new observations per image, add_pids the new tracks' ids
+    (before the shift by parent_n_tracks), image by image; device tensors, read only if a plan is needed."""
+    with _cache_lock:
+        for k in [k for k, v in _lineage.items() if v[0]() is None]:
+            del _lineage[k]
+        _lineage[id(pids)] = (weakref.ref(pids), pids._version, weakref.ref(parent_pids), parent_pids._version,
+                              int(parent_n_tracks), add_nppi, add_pids)
+
+
+def _appended_plan(infos, pids, n_tracks, key):
+    """The batched plan of `pids` from its parent's cached plan, when the lineage says it is an append."""
+    with _cache_lock:
+        lin = _lineage.get(id(pids))
+        if lin is None or lin[0]() is not pids or lin[1] != pids._version:
+            return None
+        parent_pids = lin[2]()
+        if parent_pids is None or lin[3] != parent_pids._version:
+            return None
+        parent = None
+        for ent in _cache.get(id(parent_pids), []):
+            ref, version, k, m, iref, iversion, plan = ent
+            if ref() is parent_pids and version == parent_pids._version and k[2:] == key[2:] and \
+                    isinstance(plan, BAPlan) and plan.appendable:
+                parent = plan
+    if parent is None:
+        return None
+    add_nppi = lin[5].detach().cpu().numpy().astype(np.int64)
+    cum = infos[0].detach().cpu().numpy().astype(np.int64)
+    old_cnt = np.diff(np.concatenate([[0], parent._cum.astype(np.int64)]))
+    if len(cum) != parent.n_imgs + 1 or len(add_nppi) != len(cum) or \
+            not np.array_equal(cum, np.cumsum(np.concatenate([old_cnt, [0]]) + add_nppi)):
+        return None
+    add_pids = lin[6].detach().cpu().numpy().astype(np.int64) + lin[4]
+    try:
+        return BAPlan.appended(parent, infos, pids, n_tracks, add_nppi, add_pids)
+    except RuntimeError:
+        return None
+
+
 def get_plan(infos, pids, n_tracks, kind='batched', **kw):
     """Plan for this structure (kind 'batched': BAPlan, 'pairmajor': PMPlan): reused while the same
-    pids tensor (unmodified) and the same per-image counts / node / cam ids come back, rebuilt otherwise.  The ids are compared by
+    pids tensor (unmodified) and the same per-image counts / node / cam ids come back, rebuilt otherwise
+    (a batched plan from its parent's, when note_append recorded the structure as `old | new` of a cached one).  The ids are compared by
     content unless the very infos tensor of the cached plan comes back unmodified (torch's version
     counter), which needs no device-to-host read."""
     key = (int(n_tracks), tuple(pids.shape), kind, tuple(sorted(kw.items())))
@@ -187,7 +311,11 @@ def get_plan(infos, pids, n_tracks, kind='batched', **kw):
             ref, version, k, m, iref, iversion, plan = ent
             if ref() is pids and version == pids._version and k == key and m == meta:
                 return plan
-    plan = PMPlan(infos, pids, n_tracks, **kw) if kind == 'pairmajor' else BAPlan(infos, pids, n_tracks, **kw)
+    plan = None
+    if kind == 'batched':
+        plan = _appended_plan(infos, pids, n_tracks, key)
+    if plan is None:
+        plan = PMPlan(infos, pids, n_tracks, **kw) if kind == 'pairmajor' else BAPlan(infos, pids, n_tracks, **kw)
     with _cache_lock:
         if sum(len(v) for v in _cache.values()) > 8:
             _cache.clear()

@@ -75,6 +75,21 @@ int ba_plan_query(const void* plan, int64_t* scalars, int64_t* array_sizes);
 int ba_plan_export(const void* plan, int32_t which, int32_t* host_dst);
 void ba_plan_destroy(void* plan);
 const char* ba_plan_last_error(void);
+/* The plan of prev's structure with one image and new tracks appended (`old | new`, tracks.py:84-102:
+ * per image, prev's observations, then add_cnt[i] of the new tracks, whose ids add_pids lists image by
+ * image); byte-identical to ba_plan_create on the merged structure, but only the batches from the first
+ * new track's place in the track order on are planned again.  prev is consumed on success (no counterpart
+ * in the reference, which rebuilds its structure with torch.unique on every iteration, ba_solver.py:877-909). */
+void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_imgs_new, const int32_t* add_pids, int64_t n_add,
+                     int32_t n_tracks_new);
+/* array `which` of the plan in place (host memory, valid until the plan is destroyed or appended to) */
+const int32_t* ba_plan_array(const void* plan, int32_t which);
+/* per array, the leading elements equal to the parent plan's (chunk_obs / slot_src after adding shift[image]);
+ * per image (n_imgs of the plan), that shift.  All 0 for a plan made by ba_plan_create. */
+int ba_plan_stable(const void* plan, int64_t* stable, int32_t* shift);
+/* device: ids[q] += shift[img[q]], q < n (a device copy of a parent plan's chunk_obs / slot_src brought to the
+ * appended structure's observation ids; no counterpart in the reference) */
+int ba_plan_shift_ids(int32_t* ids, const int32_t* img, const int32_t* shift, int64_t n, void* stream);
 
 /* ------------------------------------------------------------------ fused linearize + Schur */
 typedef struct {

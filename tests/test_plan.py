@@ -462,3 +462,82 @@ def test_pm_schur_emulation_matches_oracle(cfg, nf, nt, kw):
     assert rel_err(torch.from_numpy(S) + torch.diag(torch.from_numpy(dg)), S_ref) < 1e-10
     on = np.concatenate([np.full(nf_, hasK), np.full(nt_, hasP), np.ones(C * p.n_imgs, bool)])
     assert np.all(np.abs(dg[on]) <= 1e-9 * np.abs(np.diag(S_ref.numpy())).max())   # only the 1e-12 damping differs
+
+
+def _online_steps(p, steps):
+    """The structures an online pipeline builds with `old | new` (tracks.py:84-102) from problem p:
+    S_k holds the tracks whose last image is <= k, numbered by (last image, id), and within an image the
+    rows of earlier steps come first, so S_k = S_(k-1) | (the tracks ending at image k).  Yields
+    (infos, pids, n_tracks, add_cnt, add_pids) for k = n_imgs - steps .. n_imgs - 1 (add_* None first)."""
+    cum = p.infos[0].numpy().astype(np.int64)
+    n_imgs = len(cum)
+    obs_img = np.repeat(np.arange(n_imgs), np.diff(np.concatenate([[0], cum])))
+    pids = p.pids.numpy().astype(np.int64)
+    T = p.n_tracks
+    tmax = np.full(T, -1)
+    np.maximum.at(tmax, pids, obs_img)
+    rank = np.empty(T, dtype=np.int64)
+    rank[np.lexsort((np.arange(T), tmax))] = np.arange(T)
+    prev = None
+    for k in range(n_imgs - steps, n_imgs):
+        sel = tmax[pids] <= k
+        oi, pp, tm = obs_img[sel], rank[pids[sel]], tmax[pids[sel]]
+        o = np.lexsort((np.arange(len(oi)), tm, oi))
+        nppi = np.bincount(oi, minlength=k + 1)
+        infos = torch.stack([torch.from_numpy(np.cumsum(nppi)), torch.arange(k + 1), torch.zeros(k + 1, dtype=torch.long)])
+        pk = torch.from_numpy(pp[o].astype(np.int32))
+        Tk = int((tmax <= k).sum())
+        add = None
+        if prev is not None:
+            old_cnt = np.concatenate([prev[0], [0]])
+            starts = np.concatenate([[0], np.cumsum(nppi)[:-1]])
+            add_pids = np.concatenate([pp[o][starts[i] + old_cnt[i]: starts[i] + nppi[i]] for i in range(k + 1)])
+            add = (nppi - old_cnt, add_pids)
+        yield infos.to(torch.int32), pk, Tk, add
+        prev = (nppi, Tk)
+
+
+@pytest.mark.parametrize('cfg,nf,nt,steps,kw', [(2, 30, 1500, 6, {}), (0, 12, 400, 5, {}), (4, 20, 800, 5, {}),
+                                                (2, 40, 2500, 4, dict(max_batch_obs=400)),
+                                                (1, 40, 4000, 4, {}), (0, 6, 200, 5, dict(max_slots=40))])
+def test_plan_append_equals_full_rebuild(cfg, nf, nt, steps, kw):
+    """BAPlan.appended (ba_plan_append: `old | new` planned from the old structure's plan, only the batches
+    from the first new track's place on planned again) equals a full BAPlan of the merged structure, every
+    array and scalar, byte for byte, over a chain of appends; and reuses the old arrays' prefix."""
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    plan = None
+    kept = []
+    for infos, pk, Tk, add in _online_steps(p, steps):
+        full = BAPlan(infos, pk, Tk, device='cpu', **kw)
+        if plan is None:
+            plan = full
+            continue
+        child = BAPlan.appended(plan, infos, pk, Tk, add[0], add[1])
+        assert not plan.appendable and child.appendable
+        assert child.scalars == full.scalars
+        for name in full.sizes:
+            assert child.sizes[name] == full.sizes[name], name
+            assert torch.equal(child.dev[name], full.dev[name]), name
+            assert np.array_equal(child.host[name], full.host[name]), name
+        kept.append(child.stable_prefix['chunk_ent'] / max(1, full.sizes['chunk_ent']))
+        plan = child
+    print(f'cfg {cfg}: fraction of MFMA entries kept per append {np.round(kept, 3)}')
+
+
+def test_plan_append_rejects_non_appends():
+    """An appended id below the old track count, or an image count that is not one more, is refused and
+    leaves the parent plan appendable (the caller then plans the structure in full)."""
+    p = make_problem(2, n_frames=20, n_tracks=800)
+    steps = list(_online_steps(p, 2))
+    parent = BAPlan(*steps[0][:3], device='cpu')
+    infos, pk, Tk, (add_cnt, add_pids) = steps[1]
+    bad = add_pids.copy()
+    bad[0] = 0
+    with pytest.raises(RuntimeError, match='appended pid out of range'):
+        BAPlan.appended(parent, infos, pk, Tk, add_cnt, bad)
+    with pytest.raises(RuntimeError, match='not an append'):
+        BAPlan.appended(parent, infos[:, :-1], pk, Tk, add_cnt[:-1], add_pids)
+    assert parent.appendable
+    child = BAPlan.appended(parent, infos, pk, Tk, add_cnt, add_pids)
+    full = BAPlan(infos, pk, Tk, device='cpu')
+    assert all(torch.equal(child.dev[n], full.dev[n]) for n in full.sizes)

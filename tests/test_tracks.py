@@ -172,3 +172,68 @@ def test_merge_at_pipeline_size():
         assert torch.equal(got.pids[sg], torch.cat([old.pids[so], new.pids[sn] + T]))
         assert torch.equal(got.pix2d_dep[sg], torch.cat([old.pix2d_dep[so], new.pix2d_dep[sn]]))
     assert torch.equal(got.nppi[:-1], nppi + nppi_n[:-1])
+
+
+@pytest.mark.gpu
+def test_merge_then_plan_is_an_append_equal_to_a_full_plan():
+    """`old | new` records its lineage; the solver's plan for the merged structure is then made from the old
+    structure's cached plan by ba_plan_append (only the batches from the first new track on planned again),
+    and equals a full plan of the merged structure on every device array, bit for bit; an LM step on the
+    merged structure gives the same result on either plan."""
+    import numpy as np
+    from blast3r_amd import engine, plan as bplan
+    from blast3r_amd.plan import BAPlan, get_plan
+    from blast3r_amd.synthetic import make_problem
+    p = make_problem(2, n_frames=40, n_tracks=2500)
+    n = p.n_imgs
+    cum = p.infos[0].numpy().astype(np.int64)
+    obs_img = np.repeat(np.arange(n), np.diff(np.concatenate([[0], cum])))
+    pids = p.pids.numpy().astype(np.int64)
+    T = p.n_tracks
+    tmax = np.full(T, -1)
+    np.maximum.at(tmax, pids, obs_img)
+    rank = np.empty(T, dtype=np.int64)
+    rank[np.lexsort((np.arange(T), tmax))] = np.arange(T)
+    T_old = int((tmax < n - 1).sum())
+    # old: the tracks ending before the last image, over images 0 .. n-2; new: the others, over all images
+    def part(sel, n_imgs, shift, n_tracks):
+        oi = obs_img[sel]
+        o = np.lexsort((np.arange(len(oi)), oi))
+        idx = torch.from_numpy(np.nonzero(sel)[0][o])
+        nppi = torch.from_numpy(np.bincount(oi, minlength=n_imgs).astype(np.int32))
+        return ObservedTracks(n_imgs, n_tracks, nppi.to(DEV),
+                              torch.from_numpy((rank[pids[idx.numpy()]] - shift).astype(np.int32)).to(DEV),
+                              p.pix2d[idx].to(DEV), p.pix2d_std[idx].to(DEV), p.pix2d_dep[idx].to(DEV), 'log_multidepth')
+    old = part(tmax[pids] < n - 1, n - 1, 0, T_old)
+    new = part(tmax[pids] == n - 1, n, T_old, T - T_old)
+    merged = old | new
+    assert merged.n_tracks == T
+
+    def infos_of(trk, k):
+        return torch.stack([torch.cumsum(trk.nppi.long(), 0), p.infos[1, :k].to(DEV).long(),
+                            p.infos[2, :k].to(DEV).long()]).to(torch.int32)
+    inf_old, inf_new = infos_of(old, n - 1), infos_of(merged, n)
+    get_plan(inf_old, old.pids, old.n_tracks, device=torch.device(DEV))
+    plan_new = get_plan(inf_new, merged.pids, merged.n_tracks, device=torch.device(DEV))
+    assert plan_new.stable_prefix is not None, 'the merged structure was planned in full'
+    full = BAPlan(inf_new, merged.pids, merged.n_tracks, device=DEV)
+    for name in full.sizes:
+        assert torch.equal(plan_new.dev[name], full.dev[name]), name
+    assert plan_new.scalars == full.scalars
+    kept = plan_new.stable_prefix['chunk_ent'] / full.sizes['chunk_ent']
+    print(f'appended plan: {kept:.3f} of the MFMA entries kept', flush=True)
+
+    pts3d = torch.empty_like(p.pts3d)
+    pts3d[torch.from_numpy(rank)] = p.pts3d
+    o = p.options
+    inp = dict(rigs=inf_new, pids=merged.pids, pix2d=merged.pix2d, pix2d_std=merged.pix2d_std,
+               pix2d_dep=merged.pix2d_dep, K=p.K.to(DEV), P_rig2cam=p.P_rig2cam.to(DEV), P_w2rig=p.P_w2rig.to(DEV),
+               z_coefs=p.z_coefs.to(DEV), pts3d=pts3d.to(DEV))
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+              optim_P=o['optim_P'])
+    up_a, st_a = engine.lm_step(**inp, **kw)
+    bplan._cache.clear()
+    up_f, st_f = engine.lm_step(**inp, **kw)
+    assert float(st_a.new_loss) == float(st_f.new_loss)
+    for k in up_a:
+        assert torch.equal(up_a[k], up_f[k]), k
