@@ -550,7 +550,7 @@ class GaussNewtonSolver:
         if mode == 0:
             self.last['direct_A'] = ws('chol_A', (lda, lda), torch.float64)   # S_u's lower triangle, then L
             ca.A = ptr(self.last['direct_A'])
-            ca.Linv = ptr(ws('chol_Linv', (lda // 64, 64, 64), torch.float64))
+            ca.Linv = ptr(ws('chol_Linv', (lda // 128, 128, 128), torch.float64))
         check(L.ba_reduced_solve(pa, ca, st))
         self.last['direct_call'] = (pa, ca)    # kept for re-timing the bare launch sequence
         bad = int(info.cpu())                  # one read per solve

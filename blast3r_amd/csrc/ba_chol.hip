@@ -8,10 +8,11 @@
 // back-substitution that follows is unchanged.
 //
 // Two layouts:
-//   dense   S_u assembled as a full lower triangle (n_u padded to 64), factored by right-looking
-//           64-column panels: the diagonal tile and its inverse in LDS (one workgroup), the panel
-//           below as A_ik L_kk^-T and the trailing update A_ij -= L_ik L_jk^T as 64 x 64 tiles of
-//           v_mfma_f64_16x16x4f64; the triangular sweeps go block by block.  Any structure.
+//   dense   S_u assembled as a full lower triangle (n_u padded to 128), factored by right-looking
+//           128-column panels: the diagonal block's inverse in LDS (one workgroup, as the cyclic
+//           reduction's super-blocks), the panel below as A_ik L_kk^-T and the trailing update
+//           A_ij -= L_ik L_jk^T as 128 x 128 blocks of v_mfma_f64_16x16x4f64 tiles; the triangular
+//           sweeps go block by block.  Any structure.
 //   banded  the image-level blocks of a block-banded structure (every image pair within w images)
 //           with the unknowns shared by several images (a mono camera's focal pair) as a dense
 //           border.  When s >= w images fit a super-block of 128 unknowns, the super-blocks form a
@@ -32,8 +33,6 @@ namespace ba {
 int unknown_setup(const ba_pcg_args& a, hipStream_t st);   // ba_pcg.hip
 
 #define CH_T 256
-#define CH_NB 64
-#define CH_LD (CH_NB + 1)
 
 typedef double dbl4 __attribute__((ext_vector_type(4)));
 
@@ -183,189 +182,6 @@ __global__ void __launch_bounds__(CH_T) k_shared_sum(ba_pcg_args a, ChArgs c, in
         c.Cb[b1 * ns + b2] = t;
         c.Cb[b2 * ns + b1] = t;
     }
-}
-
-// ------------------------------------------------------------------ dense panel factor
-// Diagonal tile k: L_kk = chol(A_kk) in place and Linv_k = L_kk^-1 (64 x 64, row-major, compact).
-// A pivot that is not positive (S_u not positive definite in fp64) is recorded in info (the first
-// such global column + 1, by atomicMin) and replaced by 1 so that the sweep stays finite.
-__global__ void __launch_bounds__(CH_T) k_potrf_tile(double* __restrict__ A, int64_t lda, int k,
-                                                     double* __restrict__ Linv, int32_t* __restrict__ info) {
-    __shared__ double T[CH_NB][CH_LD];
-    __shared__ double X[CH_NB][CH_LD];
-    const int t = threadIdx.x;
-    const int64_t o = (int64_t)k * CH_NB;
-    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
-        const int r = e / CH_NB, q = e - r * CH_NB;
-        T[r][q] = q <= r ? A[(o + r) * lda + o + q] : 0.0;
-        X[r][q] = r == q ? 1.0 : 0.0;
-    }
-    __syncthreads();
-    for (int j = 0; j < CH_NB; ++j) {
-        if (t == 0) {
-            double dj = T[j][j];
-            if (!(dj > 0.0)) {
-                atomicMin(info, (int32_t)(o + j + 1));
-                dj = 1.0;
-            }
-            T[j][j] = sqrt(dj);
-        }
-        __syncthreads();
-        const double piv = T[j][j];
-        if (t > j && t < CH_NB) T[t][j] /= piv;
-        __syncthreads();
-        // trailing update of the lower triangle right of column j: thread (row r, column group g)
-        {
-            const int r = t & (CH_NB - 1), g = t >> 6;
-            if (r > j) {
-                const double lr = T[r][j];
-                for (int q = j + 1 + g; q <= r; q += CH_T / CH_NB) T[r][q] -= lr * T[q][j];
-            }
-        }
-        __syncthreads();
-    }
-    // X = L^-1 by elimination on [L | I]: normalise row j, then remove column j from the rows below
-    for (int j = 0; j < CH_NB; ++j) {
-        const double piv = T[j][j];
-        if (t <= j) X[j][t] /= piv;
-        __syncthreads();
-        {
-            const int r = t & (CH_NB - 1), g = t >> 6;
-            if (r > j) {
-                const double lr = T[r][j];
-                for (int q = g; q <= j; q += CH_T / CH_NB) X[r][q] -= lr * X[j][q];
-            }
-        }
-        __syncthreads();
-    }
-    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
-        const int r = e / CH_NB, q = e - r * CH_NB;
-        if (q <= r) A[(o + r) * lda + o + q] = T[r][q];
-        Linv[(int64_t)k * CH_NB * CH_NB + e] = q <= r ? X[r][q] : 0.0;
-    }
-}
-
-// ------------------------------------------------------------------ dense 64 x 64 tile products
-// mode 0 (panel): tile (k + 1 + blockIdx.x, k) <- A_ik Linv_k^T.
-// mode 1 (trailing update): tile (i, j), k < j <= i, from the triangular index blockIdx.x:
-//   A_ij -= L_ik L_jk^T (the diagonal tiles keep their upper part).
-// Four waves, each a 32 x 32 quadrant as 2 x 2 tiles of v_mfma_f64_16x16x4f64 over K = 64; the
-// operands are staged in LDS (rows padded to 65 doubles).  Accumulator layout: lane l, element v
-// holds D[4 v + l / 16][l % 16]; operand lane l holds row l % 16, k = l / 16 of its 16 x 4 slice.
-__global__ void __launch_bounds__(CH_T) k_tile_nt(double* __restrict__ A, int64_t lda, int k, int mode,
-                                                  const double* __restrict__ Linv) {
-    __shared__ double sa[CH_NB][CH_LD];
-    __shared__ double sb[CH_NB][CH_LD];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    int ti, tj;
-    if (mode == 0) {
-        ti = k + 1 + (int)blockIdx.x;
-        tj = k;
-    } else {
-        const int64_t q = blockIdx.x;
-        int i = (int)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
-        while ((int64_t)(i + 1) * (i + 2) / 2 <= q) ++i;
-        while ((int64_t)i * (i + 1) / 2 > q) --i;
-        const int j = (int)(q - (int64_t)i * (i + 1) / 2);
-        ti = k + 1 + i;
-        tj = k + 1 + j;
-    }
-    const int64_t ro = (int64_t)ti * CH_NB, co = (int64_t)tj * CH_NB, ko = (int64_t)k * CH_NB;
-    for (int e = t; e < CH_NB * CH_NB; e += CH_T) {
-        const int r = e / CH_NB, q = e - r * CH_NB;
-        sa[r][q] = A[(ro + r) * lda + ko + q];
-        sb[r][q] = mode == 0 ? Linv[(int64_t)k * CH_NB * CH_NB + e] : A[(co + r) * lda + ko + q];
-    }
-    __syncthreads();
-    const int qi = (wave >> 1) * 32, qj = (wave & 1) * 32;
-    const int l16 = lane & 15, lk = lane >> 4;
-    dbl4 acc[2][2];
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = (dbl4){0.0, 0.0, 0.0, 0.0};
-#pragma unroll 4
-    for (int kk = 0; kk < CH_NB / 4; ++kk) {
-        double av[2], bv[2];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) av[mi] = sa[qi + 16 * mi + l16][4 * kk + lk];
-#pragma unroll
-        for (int nj = 0; nj < 2; ++nj) bv[nj] = sb[qj + 16 * nj + l16][4 * kk + lk];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int nj = 0; nj < 2; ++nj)
-                acc[mi][nj] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mi], bv[nj], acc[mi][nj], 0, 0, 0);
-    }
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = qi + 16 * mi + 4 * v + lk, q = qj + 16 * nj + l16;
-                double* dst = A + (ro + r) * lda + co + q;
-                if (mode == 0) {
-                    *dst = acc[mi][nj][v];
-                } else if (ti != tj || q <= r) {
-                    *dst = *dst - acc[mi][nj][v];
-                }
-            }
-}
-
-// ------------------------------------------------------------------ dense triangular sweeps
-// Forward, block k (right-looking): y_k = Linv_k b_k; every workgroup forms y_k itself from b_k (read
-// only in this launch), workgroup 0 stores it, workgroup w >= 1 updates b_i -= L_ik y_k for the tile
-// i = k + w.  b is the working copy of the rhs (padded with zeros), y the result.
-__global__ void __launch_bounds__(CH_NB) k_fwd_block(const double* __restrict__ A, int64_t lda, int k,
-                                                     const double* __restrict__ Linv, double* __restrict__ b,
-                                                     double* __restrict__ y) {
-    __shared__ double sy[CH_NB];
-    __shared__ double sbk[CH_NB];
-    const int t = threadIdx.x;
-    const int64_t ko = (int64_t)k * CH_NB;
-    sbk[t] = b[ko + t];
-    __syncthreads();
-    const double* Li = Linv + (int64_t)k * CH_NB * CH_NB + t * CH_NB;
-    double s = 0.0;
-    for (int q = 0; q <= t; ++q) s += Li[q] * sbk[q];
-    sy[t] = s;
-    __syncthreads();
-    if (blockIdx.x == 0) {
-        y[ko + t] = s;
-        return;
-    }
-    const int64_t ro = ko + (int64_t)blockIdx.x * CH_NB;
-    const double* Lr = A + (ro + t) * lda + ko;
-    double acc = 0.0;
-    for (int q = 0; q < CH_NB; ++q) acc += Lr[q] * sy[q];
-    b[ro + t] -= acc;
-}
-
-// Backward, block k (right-looking on L^T): x_k = Linv_k^T y_k; workgroup 0 stores it, workgroup
-// w >= 1 updates y_i -= L_ki^T x_k for the tile i = w - 1 < k.
-__global__ void __launch_bounds__(CH_NB) k_bwd_block(const double* __restrict__ A, int64_t lda, int k,
-                                                     const double* __restrict__ Linv, double* __restrict__ y,
-                                                     double* __restrict__ x) {
-    __shared__ double sx[CH_NB];
-    __shared__ double syk[CH_NB];
-    const int t = threadIdx.x;
-    const int64_t ko = (int64_t)k * CH_NB;
-    syk[t] = y[ko + t];
-    __syncthreads();
-    const double* Lb = Linv + (int64_t)k * CH_NB * CH_NB;
-    double s = 0.0;
-    for (int r = t; r < CH_NB; ++r) s += Lb[r * CH_NB + t] * syk[r];
-    sx[t] = s;
-    __syncthreads();
-    if (blockIdx.x == 0) {
-        x[ko + t] = s;
-        return;
-    }
-    const int64_t io = (int64_t)(blockIdx.x - 1) * CH_NB;
-    double acc = 0.0;
-    for (int r = 0; r < CH_NB; ++r) acc += A[(ko + r) * lda + io + t] * sx[r];
-    y[io + t] -= acc;
 }
 
 __global__ void __launch_bounds__(CH_T) k_copy_pad(const double* __restrict__ src, int64_t n, int64_t N,
@@ -861,6 +677,12 @@ __device__ __forceinline__ void cr_mma(dbl4& acc, int kb, int ke, FA fa, FB fb, 
     }
 }
 
+// sum over the 64 lanes of a wave (butterfly; every lane gets the same bits)
+__device__ __forceinline__ double wave_sum64(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
 // lane src's v in every lane (src uniform)
 __device__ __forceinline__ double lane_bcast(double v, int src) {
     const int2 b = __builtin_bit_cast(int2, v);
@@ -928,25 +750,25 @@ __device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __
     }
 }
 
-// One workgroup per eliminated super-block I = (2 blockIdx.x + 1) h - 1: D_I = L L^T in LDS by 16-column
-// panels (wave 0 factors and inverts the 16 x 16 diagonal block; the panel below and the trailing blocks
-// are MFMA products; wave 0 takes the next diagonal block's trailing update first and factors it while
-// the other waves finish the trailing blocks), then L^-1 in place by block columns from the right
-// (L^-1_ij = - sum_{k = j+1..i} L^-1_ik L_kj L_jj^-1), written to crL[I] (lower; zero above).
-__global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
-    extern __shared__ double lds[];
+// D = L L^T in LDS by 16-column panels (wave 0 factors and inverts the 16 x 16 diagonal block; the panel
+// below and the trailing blocks are MFMA products; wave 0 takes the next diagonal block's trailing update
+// first and factors it while the other waves finish the trailing blocks), then L^-1 in place by block
+// columns from the right (L^-1_ij = - sum_{k = j+1..i} L^-1_ik L_kj L_jj^-1).
+// The factor of one 128 x 128 SPD block by a workgroup of CR_T threads: the lower triangle of D (row pitch
+// ld) in, L^-1 (row pitch CR_MP, zero above the diagonal) out; lds holds CR_LDS_DOUBLES.  A pivot that is
+// not positive goes to info as pos0 + its column + 1.
+__device__ __forceinline__ void factor128(const double* __restrict__ D, int64_t ld, double* __restrict__ Lo,
+                                          int32_t* __restrict__ info, int32_t pos0, double* lds) {
     double* S = lds;                          // [CR_MP][CR_LD]
     double* Inv = lds + CR_MP * CR_LD;        // [8][16][16] inverses of the diagonal blocks
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int l16 = lane & 15, lk = lane >> 4;
-    const int I = (2 * (int)blockIdx.x + 1) * h - 1;
-    const double* D = c.crD + (int64_t)I * CR_MP2;
     for (int e = t; e < CR_MP2; e += CR_T) {
         const int r = e / CR_MP, q = e - r * CR_MP;
-        S[r * CR_LD + q] = q <= r ? D[e] : 0.0;
+        S[r * CR_LD + q] = q <= r ? D[r * ld + q] : 0.0;
     }
     __syncthreads();
-    if (wave == 0) cr_diag_block(S, Inv, 0, lane, c.info, I * CR_MP);
+    if (wave == 0) cr_diag_block(S, Inv, 0, lane, info, pos0);
     __syncthreads();
     for (int p = 0; p < 7; ++p) {
         // panel: L_ip = A_ip L_pp^-T for the block rows below
@@ -980,7 +802,7 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) C[(4 * v + lk) * CR_LD + l16] -= acc[v];
             }
-        if (wave == 0) cr_diag_block(S, Inv, p + 1, lane, c.info, I * CR_MP + 16 * (p + 1));
+        if (wave == 0) cr_diag_block(S, Inv, p + 1, lane, info, pos0 + 16 * (p + 1));
         __syncthreads();
     }
     // L^-1 in place, block columns from the right
@@ -1022,11 +844,16 @@ __global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
         if (t < 256) S[(16 * j + (t >> 4)) * CR_LD + 16 * j + (t & 15)] = Ij[t];
         __syncthreads();
     }
-    double* Lo = c.crL + (int64_t)I * CR_MP2;
     for (int e = t; e < CR_MP2; e += CR_T) {
         const int r = e / CR_MP, q = e - r * CR_MP;
         Lo[e] = q <= r ? S[r * CR_LD + q] : 0.0;
     }
+}
+
+__global__ void __launch_bounds__(CR_T) k_cr_factor(ChArgs c, int h) {
+    extern __shared__ double lds[];
+    const int I = (2 * (int)blockIdx.x + 1) * h - 1;
+    factor128(c.crD + (int64_t)I * CR_MP2, CR_MP, c.crL + (int64_t)I * CR_MP2, c.info, I * CR_MP, lds);
 }
 
 // Ga = L^-1 E_I, Gb = L^-1 E_b^T and Y_I = L^-1 R_I for the eliminated super-block I = (2 blockIdx.x + 1) h - 1,
@@ -1224,20 +1051,204 @@ __global__ void __launch_bounds__(CH_T) k_cr_local(ba_pcg_args a, ChArgs c) {
     c.xl[u] = v;
 }
 
+// ------------------------------------------------------------------ dense layout, 128-column panels
+// Right-looking L L^T of S_u (lower triangle, row pitch lda = n_u rounded up to 128) by block columns of 128:
+// the diagonal block's L^-1 by factor128 (one workgroup), the panel below as L_ik = A_ik L_kk^-T (in place,
+// and into the panel copy P), the trailing blocks as A_ij -= L_ik L_jk^T from P.  Triangular sweeps by
+// block with the diagonal blocks' inverses.
+#define DN_NB CR_MP
+#define DN_KC 16                     // K columns of P staged in LDS at a time by the trailing update
+
+__global__ void __launch_bounds__(CR_T) k_dn_factor(const double* __restrict__ A, int64_t lda, int k,
+                                                    double* __restrict__ Linv, int32_t* __restrict__ info) {
+    extern __shared__ double lds[];
+    const int64_t o = (int64_t)k * DN_NB;
+    factor128(A + o * lda + o, lda, Linv + (int64_t)k * CR_MP2, info, (int32_t)o, lds);
+}
+
+// the 16-row strip blockIdx.x below block k: L = A_strip L_kk^-T, wave w the columns 16 w ..; the strip is in
+// LDS before anything is written.  L goes to A and to P (rows below block k, row pitch DN_NB).
+__global__ void __launch_bounds__(512) k_dn_panel(double* __restrict__ A, int64_t lda, int k,
+                                                  const double* __restrict__ Linv, double* __restrict__ P) {
+    __shared__ double sA[16][DN_NB + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l16 = lane & 15, lk = lane >> 4;
+    const int64_t o = (int64_t)k * DN_NB, rp = 16 * (int64_t)blockIdx.x, r0 = o + DN_NB + rp;
+    for (int e = t; e < 16 * DN_NB; e += 512) {
+        const int r = e / DN_NB, q = e - r * DN_NB;
+        sA[r][q] = A[(r0 + r) * lda + o + q];
+    }
+    __syncthreads();
+    const double* Li = Linv + (int64_t)k * CR_MP2;
+    const int c0 = 16 * wave;
+    dbl4 acc = (dbl4){0.0, 0.0, 0.0, 0.0};
+    // B[q][c] = L^-1[c0 + c][q], zero for q > c0 + c
+    cr_mma(acc, 0, c0 + 16, [&](int r, int q) { return sA[r][q]; },
+           [&](int q, int cc) { return Li[(c0 + cc) * CR_MP + q]; }, l16, lk);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = 4 * v + lk, c = c0 + l16;
+        A[(r0 + r) * lda + o + c] = acc[v];
+        P[(rp + r) * DN_NB + c] = acc[v];
+    }
+}
+
+// trailing blocks (i, j), k < j <= i, from the triangular index blockIdx.x: A_ij -= P_i P_j^T.  Four waves, each
+// a 64 x 64 quadrant as 4 x 4 tiles of v_mfma_f64_16x16x4f64 over K = 128, the operands staged in LDS DN_KC
+// columns at a time (rows padded to DN_KC + 1 doubles); two workgroups fit a CU.
+__global__ void __launch_bounds__(256) k_dn_syrk(double* __restrict__ A, int64_t lda, int k,
+                                                 const double* __restrict__ P) {
+    __shared__ double sa[DN_NB][DN_KC + 1];
+    __shared__ double sb[DN_NB][DN_KC + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l16 = lane & 15, lk = lane >> 4;
+    const int64_t q = blockIdx.x;
+    int bi = (int)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
+    while ((int64_t)(bi + 1) * (bi + 2) / 2 <= q) ++bi;
+    while ((int64_t)bi * (bi + 1) / 2 > q) --bi;
+    const int bj = (int)(q - (int64_t)bi * (bi + 1) / 2);
+    const double* Pi = P + (int64_t)bi * DN_NB * DN_NB;
+    const double* Pj = P + (int64_t)bj * DN_NB * DN_NB;
+    const int qi = (wave >> 1) * 64, qj = (wave & 1) * 64;
+    dbl4 acc[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = (dbl4){0.0, 0.0, 0.0, 0.0};
+    // the next chunk's operands are loaded into registers while this one's MFMAs run
+    constexpr int PER = DN_NB * DN_KC / 256;          // operands of one matrix per thread and chunk
+    double ra[PER], rb[PER];
+    auto fetch = [&](int kc) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = t + 256 * i, r = e / DN_KC, c = e - r * DN_KC;
+            ra[i] = Pi[r * DN_NB + kc + c];
+            rb[i] = Pj[r * DN_NB + kc + c];
+        }
+    };
+    fetch(0);
+    for (int kc = 0; kc < DN_NB; kc += DN_KC) {
+        if (kc) __syncthreads();                      // the previous chunk is consumed
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = t + 256 * i, r = e / DN_KC, c = e - r * DN_KC;
+            sa[r][c] = ra[i];
+            sb[r][c] = rb[i];
+        }
+        __syncthreads();
+        if (kc + DN_KC < DN_NB) fetch(kc + DN_KC);
+#pragma unroll 2
+        for (int kk = 0; kk < DN_KC / 4; ++kk) {
+            double av[4], bv[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) av[mi] = sa[qi + 16 * mi + l16][4 * kk + lk];
+#pragma unroll
+            for (int nj = 0; nj < 4; ++nj) bv[nj] = sb[qj + 16 * nj + l16][4 * kk + lk];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int nj = 0; nj < 4; ++nj)
+                    acc[mi][nj] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mi], bv[nj], acc[mi][nj], 0, 0, 0);
+        }
+    }
+    const int64_t ro = (int64_t)(k + 1 + bi) * DN_NB, co = (int64_t)(k + 1 + bj) * DN_NB;
+    // C -= acc, sixteen elements' loads in flight at a time
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+        double cv[4][4];
+#pragma unroll
+        for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                cv[nj][v] = __builtin_nontemporal_load(A + (ro + qi + 16 * mi + 4 * v + lk) * lda + co + qj + 16 * nj + l16);
+#pragma unroll
+        for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                A[(ro + qi + 16 * mi + 4 * v + lk) * lda + co + qj + 16 * nj + l16] = cv[nj][v] - acc[mi][nj][v];
+    }
+}
+
+// Forward sweep, block k: y_k = L_kk^-1 b_k (every workgroup forms it from b_k, which this launch does not
+// write; workgroup 0 stores it), workgroup w >= 1: b_i -= L_ik y_k for i = k + w.  Row products by one wave
+// each, lanes over the columns (coalesced), summed in a fixed tree.
+__global__ void __launch_bounds__(256) k_dn_fwd(const double* __restrict__ A, int64_t lda, int k,
+                                                const double* __restrict__ Linv, double* __restrict__ b,
+                                                double* __restrict__ y) {
+    __shared__ double sb[DN_NB], sy[DN_NB];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int64_t o = (int64_t)k * DN_NB;
+    if (t < DN_NB) sb[t] = b[o + t];
+    __syncthreads();
+    const double* Li = Linv + (int64_t)k * CR_MP2;
+    // rows r = wave + 4 m of a 128 x 128 matrix M (row pitch ld) times v (LDS): eight rows' operands at a time
+    auto rows = [&](const double* M, int64_t ld, const double* v, double* out, bool sub) {
+        for (int m0 = 0; m0 < DN_NB / 4; m0 += 8) {
+            double s[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const double* Mr = M + (int64_t)(wave + 4 * (m0 + m)) * ld;
+                s[m] = Mr[lane] * v[lane] + Mr[64 + lane] * v[64 + lane];
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const double t8 = wave_sum64(s[m]);
+                if (lane == 0) {
+                    const int r = wave + 4 * (m0 + m);
+                    if (sub) out[r] -= t8; else out[r] = t8;
+                }
+            }
+        }
+    };
+    rows(Li, CR_MP, sb, sy, false);
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (t < DN_NB) y[o + t] = sy[t];
+        return;
+    }
+    const int64_t ro = o + (int64_t)blockIdx.x * DN_NB;
+    rows(A + ro * lda + o, lda, sy, b + ro, true);
+}
+
+// Backward sweep, block k: x_k = L_kk^-T y_k (workgroup 0 stores it), workgroup w >= 1: y_i -= L_ki^T x_k for
+// i = w - 1 < k; thread r forms output r, reading the rows of L_ki (coalesced across threads).
+__global__ void __launch_bounds__(DN_NB) k_dn_bwd(const double* __restrict__ A, int64_t lda, int k,
+                                                  const double* __restrict__ Linv, double* __restrict__ y,
+                                                  double* __restrict__ x) {
+    __shared__ double sy[DN_NB], sx[DN_NB];
+    const int t = threadIdx.x;
+    const int64_t o = (int64_t)k * DN_NB;
+    sy[t] = y[o + t];
+    __syncthreads();
+    const double* Li = Linv + (int64_t)k * CR_MP2;
+    double s = 0.0;                           // L^-1[q][t] is zero for q < t
+#pragma unroll 16
+    for (int q = 0; q < DN_NB; ++q) s += Li[q * CR_MP + t] * sy[q];
+    sx[t] = s;
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        x[o + t] = s;
+        return;
+    }
+    const int64_t io = (int64_t)(blockIdx.x - 1) * DN_NB;
+    double acc = 0.0;
+#pragma unroll 16
+    for (int q = 0; q < DN_NB; ++q) acc += A[(o + q) * lda + io + t] * sx[q];
+    y[io + t] -= acc;
+}
+
 }  // namespace ba
 
 using namespace ba;
 
 extern "C" int64_t ba_chol_dense_lda(int64_t n_u) {
     const int64_t m = n_u < 1 ? 1 : n_u;
-    return (m + CH_NB - 1) / CH_NB * CH_NB;
+    return (m + DN_NB - 1) / DN_NB * DN_NB;
 }
 
 extern "C" int64_t ba_chol_work_doubles(int32_t mode, int64_t n_u, int32_t n_imgs, int32_t d, int32_t w,
                                         int32_t n_shared) {
     // banded: d is the band block size db
     const int64_t ss = (int64_t)n_shared * (n_shared + 1) * SS_CHUNKS;     // also BP_CHUNKS per border product
-    if (mode == 0) return 3 * ba_chol_dense_lda(n_u) + ss;
+    if (mode == 0) return (3 + DN_NB) * ba_chol_dense_lda(n_u) + ss;
     const int64_t M = (int64_t)(w + 1) * d, nl = (int64_t)n_imgs * d;
     int64_t n = (int64_t)n_imgs * (w + 1) * d * d + (int64_t)n_shared * nl + (int64_t)n_shared * n_shared + nl +
                 (int64_t)n_imgs * M * d + (int64_t)n_imgs * n_shared * d + 2 * nl;
@@ -1366,11 +1377,12 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     BA_REQUIRE(ca.mode == 0, "ba_reduced_solve: unknown mode");
     const int64_t N = ba_chol_dense_lda(a.n_u);
     BA_REQUIRE(c.A != nullptr && c.lda >= N && c.Linv != nullptr, "ba_reduced_solve: dense workspace missing");
-    const int nt = (int)(N / CH_NB);
+    const int nt = (int)(N / DN_NB);
     double* b = ca.work;
     double* y = b + N;
     double* xs = y + N;
-    c.ss_part = xs + N;
+    double* P = xs + N;                      // panel copy: (N - DN_NB) x DN_NB
+    c.ss_part = P + N * DN_NB;
     hipLaunchKernelGGL(k_dense_assemble, dim3((unsigned)((N + CH_T - 1) / CH_T), (unsigned)N), dim3(CH_T), 0, st, a,
                        c, N);
     if (ca.n_shared > 0) {
@@ -1380,20 +1392,22 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
         hipLaunchKernelGGL(k_shared_sum, dim3((unsigned)((ca.n_shared * ca.n_shared + CH_T - 1) / CH_T)), dim3(CH_T),
                            0, st, a, c, 0);
     }
+    const size_t f_lds = (size_t)CR_LDS_DOUBLES * sizeof(double);
+    BA_HIP(hipFuncSetAttribute((const void*)k_dn_factor, hipFuncAttributeMaxDynamicSharedMemorySize, (int)f_lds));
     for (int k = 0; k < nt; ++k) {
-        hipLaunchKernelGGL(k_potrf_tile, dim3(1), dim3(CH_T), 0, st, c.A, c.lda, k, c.Linv, c.info);
+        hipLaunchKernelGGL(k_dn_factor, dim3(1), dim3(CR_T), f_lds, st, c.A, c.lda, k, c.Linv, c.info);
         const int below = nt - 1 - k;
         if (below > 0) {
-            hipLaunchKernelGGL(k_tile_nt, dim3((unsigned)below), dim3(CH_T), 0, st, c.A, c.lda, k, 0, c.Linv);
+            hipLaunchKernelGGL(k_dn_panel, dim3((unsigned)(below * (DN_NB / 16))), dim3(512), 0, st, c.A, c.lda, k, c.Linv, P);
             const int64_t tri = (int64_t)below * (below + 1) / 2;
-            hipLaunchKernelGGL(k_tile_nt, dim3((unsigned)tri), dim3(CH_T), 0, st, c.A, c.lda, k, 1, c.Linv);
+            hipLaunchKernelGGL(k_dn_syrk, dim3((unsigned)tri), dim3(256), 0, st, c.A, c.lda, k, P);
         }
     }
     hipLaunchKernelGGL(k_copy_pad, dim3((unsigned)((N + CH_T - 1) / CH_T)), dim3(CH_T), 0, st, a.rhs, a.n_u, N, b);
     for (int k = 0; k < nt; ++k)
-        hipLaunchKernelGGL(k_fwd_block, dim3((unsigned)(nt - k)), dim3(CH_NB), 0, st, c.A, c.lda, k, c.Linv, b, y);
+        hipLaunchKernelGGL(k_dn_fwd, dim3((unsigned)(nt - k)), dim3(256), 0, st, c.A, c.lda, k, c.Linv, b, y);
     for (int k = nt - 1; k >= 0; --k)
-        hipLaunchKernelGGL(k_bwd_block, dim3((unsigned)(k + 1)), dim3(CH_NB), 0, st, c.A, c.lda, k, c.Linv, y, xs);
+        hipLaunchKernelGGL(k_dn_bwd, dim3((unsigned)(k + 1)), dim3(DN_NB), 0, st, c.A, c.lda, k, c.Linv, y, xs);
     hipLaunchKernelGGL(k_isolated, dim3(nbu), dim3(CH_T), 0, st, a, xs);
     hipLaunchKernelGGL(k_chol_status, dim3(1), dim3(64), 0, st, a, c.info);
     BA_LAUNCHED();

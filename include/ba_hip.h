@@ -290,9 +290,10 @@ int64_t ba_pcg_partials_size(int64_t n_u);
 typedef struct {
     int32_t mode;                /* 0: dense (any structure); 1: banded with a dense border (cyclic reduction
                                     where it applies); 2: banded, one workgroup */
-    double* A;                   /* dense: (lda, lda) workspace; the lower triangle of S_u, then L */
-    int64_t lda;                 /* dense: ba_chol_dense_lda(n_u) (n_u rounded up to 64) */
-    double* Linv;                /* dense: (lda / 64, 64, 64) inverses of the diagonal tiles of L */
+    double* A;                   /* dense: (lda, lda) workspace; the lower triangle of S_u, then L below the
+                                    diagonal blocks */
+    int64_t lda;                 /* dense: ba_chol_dense_lda(n_u) (n_u rounded up to 128) */
+    double* Linv;                /* dense: (lda / 128, 128, 128) inverses of the diagonal blocks of L */
     const int32_t* pair_idx;     /* (n_imgs, n_imgs): the pair id of images (i, j), i <= j, or -1 */
     const int32_t* kind;         /* (n_u): 1 local (one image-level entry), 2 shared (several: a mono
                                     camera's focal pair, a rig node), 0 isolated (none) */
