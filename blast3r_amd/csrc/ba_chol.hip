@@ -1168,44 +1168,37 @@ __global__ void __launch_bounds__(256) k_dn_syrk(double* __restrict__ A, int64_t
 }
 
 // Forward sweep, block k: y_k = L_kk^-1 b_k (every workgroup forms it from b_k, which this launch does not
-// write; workgroup 0 stores it), workgroup w >= 1: b_i -= L_ik y_k for i = k + w.  Row products by one wave
-// each, lanes over the columns (coalesced), summed in a fixed tree.
+// write; workgroup 0 stores it), workgroup w >= 1: b_i -= L_ik y_k for i = k + w.  A row product by two
+// threads, each over 64 contiguous columns (16-byte loads, all in flight), the halves added by a shuffle.
 __global__ void __launch_bounds__(256) k_dn_fwd(const double* __restrict__ A, int64_t lda, int k,
                                                 const double* __restrict__ Linv, double* __restrict__ b,
                                                 double* __restrict__ y) {
     __shared__ double sb[DN_NB], sy[DN_NB];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, r = t >> 1, h = t & 1;
     const int64_t o = (int64_t)k * DN_NB;
     if (t < DN_NB) sb[t] = b[o + t];
     __syncthreads();
-    const double* Li = Linv + (int64_t)k * CR_MP2;
-    // rows r = wave + 4 m of a 128 x 128 matrix M (row pitch ld) times v (LDS): eight rows' operands at a time
-    auto rows = [&](const double* M, int64_t ld, const double* v, double* out, bool sub) {
-        for (int m0 = 0; m0 < DN_NB / 4; m0 += 8) {
-            double s[8];
+    // row r of M (row pitch ld) times v (LDS), by the thread pair (r, h)
+    auto row = [&](const double* M, int64_t ld, const double* v) {
+        const double2* Mr = reinterpret_cast<const double2*>(M + (int64_t)r * ld + 64 * h);
+        double2 m[32];
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const double* Mr = M + (int64_t)(wave + 4 * (m0 + m)) * ld;
-                s[m] = Mr[lane] * v[lane] + Mr[64 + lane] * v[64 + lane];
-            }
+        for (int q = 0; q < 32; ++q) m[q] = Mr[q];
+        double s = 0.0;
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const double t8 = wave_sum64(s[m]);
-                if (lane == 0) {
-                    const int r = wave + 4 * (m0 + m);
-                    if (sub) out[r] -= t8; else out[r] = t8;
-                }
-            }
-        }
+        for (int q = 0; q < 32; ++q) s += m[q].x * v[64 * h + 2 * q] + m[q].y * v[64 * h + 2 * q + 1];
+        return s + __shfl_xor(s, 1);
     };
-    rows(Li, CR_MP, sb, sy, false);
+    const double yr = row(Linv + (int64_t)k * CR_MP2, CR_MP, sb);
+    if (h == 0) sy[r] = yr;
     __syncthreads();
     if (blockIdx.x == 0) {
         if (t < DN_NB) y[o + t] = sy[t];
         return;
     }
     const int64_t ro = o + (int64_t)blockIdx.x * DN_NB;
-    rows(A + ro * lda + o, lda, sy, b + ro, true);
+    const double s = row(A + ro * lda + o, lda, sy);
+    if (h == 0) b[ro + r] -= s;
 }
 
 // Backward sweep, block k: x_k = L_kk^-T y_k (workgroup 0 stores it), workgroup w >= 1: y_i -= L_ki^T x_k for
