@@ -712,14 +712,15 @@ __device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __
 #pragma unroll
     for (int q = 0; q < 16; ++q) row[q] = q <= r ? B[r * CR_LD + q] : 0.0;
     double rinv = 0.0;
+    int first_bad = -1;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        if (j < 15 && lane < 16) col[16 * j + r] = row[j];      // a wave's LDS accesses complete in order
+        // every lane writes (lanes 16-63 the same values as 0-15); a wave's LDS accesses complete in order
+        if (j < 15) col[16 * j + r] = row[j];
         double pj = lane_bcast(row[j], j);
-        if (!(pj > 0.0)) {
-            if (lane == 0) atomicMin(info, pos0 + j + 1);
-            pj = 1.0;
-        }
+        const bool bad = !(pj > 0.0);
+        first_bad = (first_bad < 0 && bad) ? j : first_bad;
+        pj = bad ? 1.0 : pj;
         const double rs = rsqrt_nr(pj);
         if (j < 15) {
             const double tj = row[j] * (rs * rs);
@@ -729,12 +730,11 @@ __device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __
         row[j] = r == j ? pj * rs : row[j] * rs;
         rinv = r == j ? rs : rinv;
     }
+    if (first_bad >= 0 && lane == 0) atomicMin(info, pos0 + first_bad + 1);
     // the factored rows through LDS (B); lane c (mod 16) forms column c of L_pp^-1 by forward substitution,
     // reading the rows at uniform addresses
-    if (lane < 16) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) B[r * CR_LD + q] = row[q];
-    }
+    for (int q = 0; q < 16; ++q) B[r * CR_LD + q] = row[q];     // lanes 16-63: the same values
     double x[16];
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
@@ -744,10 +744,8 @@ __device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __
         for (int mm = 0; mm < rr; ++mm) sum = fma(B[rr * CR_LD + mm], x[mm], sum);
         x[rr] = rr == r ? ri : (rr > r ? -ri * sum : 0.0);
     }
-    if (lane < 16) {
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) col[rr * 16 + r] = x[rr];
-    }
+    for (int rr = 0; rr < 16; ++rr) col[rr * 16 + r] = x[rr];       // lanes 16-63: the same values
 }
 
 // D = L L^T in LDS by 16-column panels (wave 0 factors and inverts the 16 x 16 diagonal block; the panel
@@ -755,7 +753,8 @@ __device__ __forceinline__ void cr_diag_block(double* __restrict__ S, double* __
 // first and factors it while the other waves finish the trailing blocks), then L^-1 in place by block
 // columns from the right (L^-1_ij = - sum_{k = j+1..i} L^-1_ik L_kj L_jj^-1).
 // The factor of one 128 x 128 SPD block by a workgroup of CR_T threads: the lower triangle of D (row pitch
-// ld) in, L^-1 (row pitch CR_MP, zero above the diagonal) out; lds holds CR_LDS_DOUBLES.  A pivot that is
+// ld; the whole block is read, the part above the diagonal ignored) in, L^-1 (row pitch CR_MP, zero above
+// the diagonal) out; lds holds CR_LDS_DOUBLES.  A pivot that is
 // not positive goes to info as pos0 + its column + 1.
 __device__ __forceinline__ void factor128(const double* __restrict__ D, int64_t ld, double* __restrict__ Lo,
                                           int32_t* __restrict__ info, int32_t pos0, double* lds) {
@@ -763,9 +762,19 @@ __device__ __forceinline__ void factor128(const double* __restrict__ D, int64_t 
     double* Inv = lds + CR_MP * CR_LD;        // [8][16][16] inverses of the diagonal blocks
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int l16 = lane & 15, lk = lane >> 4;
-    for (int e = t; e < CR_MP2; e += CR_T) {
-        const int r = e / CR_MP, q = e - r * CR_MP;
-        S[r * CR_LD + q] = q <= r ? D[r * ld + q] : 0.0;
+    {
+        // the whole block (every load in flight at once), then its lower triangle into LDS
+        double v[CR_MP2 / CR_T];
+#pragma unroll
+        for (int k = 0; k < CR_MP2 / CR_T; ++k) {
+            const int e = t + k * CR_T, r = e / CR_MP, q = e - r * CR_MP;
+            v[k] = D[r * ld + q];
+        }
+#pragma unroll
+        for (int k = 0; k < CR_MP2 / CR_T; ++k) {
+            const int e = t + k * CR_T, r = e / CR_MP, q = e - r * CR_MP;
+            S[r * CR_LD + q] = q <= r ? v[k] : 0.0;
+        }
     }
     __syncthreads();
     if (wave == 0) cr_diag_block(S, Inv, 0, lane, info, pos0);
