@@ -214,7 +214,7 @@ class ObservedTracks:
         res = ObservedTracks(trks.n_imgs, self.n_tracks + trks.n_tracks, nppi, depth_mode=self.depth_mode, **out)
         # the solver's structure plan of the result can then be made from this set's (only the batches the
         # new tracks reach are planned again)
-        note_append(res.pids, self.pids, self.n_tracks, trks.nppi, trks.pids)
+        note_append(res.pids, self.pids, self.n_tracks, trks.nppi, trks.pids, res.n_tracks)
         return res
 
     def to_dense(self, n_imgs=None):

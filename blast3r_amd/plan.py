@@ -55,7 +55,7 @@ class BAPlan:
     that the structure `old | new` can be planned from this one (BAPlan.appended), until that is done once."""
 
     def __init__(self, infos, pids, n_tracks, device=None, max_local_imgs=MAX_LOCAL, max_slots=MAX_SLOTS,
-                 max_batch_obs=0, _parent=None, _added=None):
+                 max_batch_obs=0, _parent=None, _chain=None):
         device = device or pids.device
         cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
         self.node_ids = np.ascontiguousarray(infos[1].detach().cpu().numpy().astype(np.int64))
@@ -70,21 +70,41 @@ class BAPlan:
             h = L.ba_plan_create(cum.ctypes.data_as(ctypes.c_void_p), self.n_imgs, p.ctypes.data_as(ctypes.c_void_p),
                                  self.n_obs, self.n_tracks, int(max_local_imgs), int(max_slots), int(max_batch_obs))
         else:
-            add_cnt, add_pids = _added
-            h = L.ba_plan_append(ctypes.c_void_p(_parent._h), add_cnt.ctypes.data_as(ctypes.c_void_p), self.n_imgs,
-                                 add_pids.ctypes.data_as(ctypes.c_void_p), int(add_pids.shape[0]), self.n_tracks)
+            # one append per link of the chain (each consumes the previous host plan); the parent's device
+            # arrays serve the final plan: per array the shortest stable prefix, per image the summed id shift
+            if self.n_imgs != _parent.n_imgs + len(_chain) or \
+                    any(len(c) != _parent.n_imgs + q + 1 for q, (c, _, _) in enumerate(_chain)):
+                raise RuntimeError('structure plan failed: not an append (each link adds one image)')
+            h = _parent._h
+            stable = np.full(len(ARRAYS), np.iinfo(np.int64).max, dtype=np.int64)
+            shift = np.zeros(max(self.n_imgs, 1), dtype=np.int32)
+            n_im = _parent.n_imgs
+            for q, (add_cnt, add_pids, n_tr) in enumerate(_chain):
+                n_im += 1
+                h2 = L.ba_plan_append(ctypes.c_void_p(h), add_cnt.ctypes.data_as(ctypes.c_void_p), n_im,
+                                      add_pids.ctypes.data_as(ctypes.c_void_p), int(add_pids.shape[0]), int(n_tr))
+                if not h2:
+                    if q:                      # an intermediate plan was consumed already: nothing to keep
+                        L.ba_plan_destroy(ctypes.c_void_p(h))
+                        _parent._h = None
+                    raise RuntimeError('structure plan failed: ' + (L.ba_plan_last_error() or b'').decode())
+                _parent._h = None if q == 0 else _parent._h       # consumed by ba_plan_append
+                h = h2
+                st = np.zeros(len(ARRAYS), dtype=np.int64)
+                sh = np.zeros(n_im, dtype=np.int32)
+                check(L.ba_plan_stable(h, st.ctypes.data_as(ctypes.c_void_p), sh.ctypes.data_as(ctypes.c_void_p)))
+                stable = np.minimum(stable, st)
+                shift[:n_im] += sh[:n_im]
         if not h:
             raise RuntimeError('structure plan failed: ' + (L.ba_plan_last_error() or b'').decode())
-        if _parent is not None:
-            _parent._h = None                  # consumed by ba_plan_append
         self._h = h
         sc = np.zeros(len(SCALARS), dtype=np.int64)
         sz = np.zeros(len(ARRAYS), dtype=np.int64)
         check(L.ba_plan_query(h, sc.ctypes.data_as(ctypes.c_void_p), sz.ctypes.data_as(ctypes.c_void_p)))
         self.scalars = {k: int(v) for k, v in zip(SCALARS, sc)}
-        stable = np.zeros(len(ARRAYS), dtype=np.int64)
-        shift = np.zeros(max(self.n_imgs, 1), dtype=np.int32)
-        check(L.ba_plan_stable(h, stable.ctypes.data_as(ctypes.c_void_p), shift.ctypes.data_as(ctypes.c_void_p)))
+        if _parent is None:
+            stable = np.zeros(len(ARRAYS), dtype=np.int64)
+            shift = np.zeros(max(self.n_imgs, 1), dtype=np.int32)
         self.device = torch.device(device)
         self.dev = {}
         self.sizes = {name: int(sz[i]) for i, name in enumerate(ARRAYS)}
@@ -135,11 +155,17 @@ class BAPlan:
         """Plan of `parent`'s structure with one image and new tracks appended (`old | new`): add_cnt
         (n_imgs + 1,) new observations per image, add_pids their track ids, image by image.  Equal to
         BAPlan(infos, pids, n_tracks), array for array; consumes the parent's host state."""
+        return cls.appended_chain(parent, infos, pids, n_tracks, [(add_cnt, add_pids, n_tracks)])
+
+    @classmethod
+    def appended_chain(cls, parent, infos, pids, n_tracks, links):
+        """As appended, over several appends in a row (`((old | a) | b) | ...`): links lists, oldest first,
+        each append's (add_cnt, add_pids, n_tracks after it)."""
         if parent._h is None:
             raise RuntimeError('the parent plan was already appended to')
-        return cls(infos, pids, n_tracks, device=parent.device, _parent=parent,
-                   _added=(np.ascontiguousarray(add_cnt, dtype=np.int32), np.ascontiguousarray(add_pids, dtype=np.int32)),
-                   **parent.options)
+        chain = [(np.ascontiguousarray(c, dtype=np.int32), np.ascontiguousarray(p, dtype=np.int32), int(t))
+                 for c, p, t in links]
+        return cls(infos, pids, n_tracks, device=parent.device, _parent=parent, _chain=chain, **parent.options)
 
     def __del__(self):
         h, self._h = getattr(self, '_h', None), None
@@ -250,43 +276,73 @@ def _prune():
 _lineage = {}
 
 
-def note_append(pids, parent_pids, parent_n_tracks, add_nppi, add_pids):
+_MAX_CHAIN = 64
+
+
+def note_append(pids, parent_pids, parent_n_tracks, add_nppi, add_pids, n_tracks=None):
     """Records that the structure with track ids `pids` is `old | new` of the one with `parent_pids`
     (tracks.py:84-102): add_nppi (n_imgs + 1,) new observations per image, add_pids the new tracks' ids
-    (before the shift by parent_n_tracks), image by image; device tensors, read only if a plan is needed."""
+    (before the shift by parent_n_tracks), image by image, n_tracks the merged count; device tensors,
+    read only if a plan is needed.  The parent keeps a strong reference to its own lineage, so a chain of
+    merges can be planned from the last structure that has a plan."""
     with _cache_lock:
         for k in [k for k, v in _lineage.items() if v[0]() is None]:
             del _lineage[k]
+        parent_lin = _lineage.get(id(parent_pids))
+        if parent_lin is not None and parent_lin[0]() is not parent_pids:
+            parent_lin = None
         _lineage[id(pids)] = (weakref.ref(pids), pids._version, weakref.ref(parent_pids), parent_pids._version,
-                              int(parent_n_tracks), add_nppi, add_pids)
+                              int(parent_n_tracks), add_nppi, add_pids,
+                              int(n_tracks) if n_tracks is not None else None, parent_lin)
+
+
+def _cached_appendable(pids, key):
+    for ent in _cache.get(id(pids), []):
+        ref, version, k, m, iref, iversion, plan = ent
+        if ref() is pids and version == pids._version and k[2:] == key[2:] and isinstance(plan, BAPlan) and \
+                plan.appendable:
+            return plan
+    return None
 
 
 def _appended_plan(infos, pids, n_tracks, key):
-    """The batched plan of `pids` from its parent's cached plan, when the lineage says it is an append."""
+    """The batched plan of `pids` from a cached plan of an earlier structure, when the lineage says the
+    structures between are appends (`old | new`, one image each): the nearest one that has a plan."""
+    links = []
     with _cache_lock:
         lin = _lineage.get(id(pids))
         if lin is None or lin[0]() is not pids or lin[1] != pids._version:
             return None
-        parent_pids = lin[2]()
-        if parent_pids is None or lin[3] != parent_pids._version:
-            return None
         parent = None
-        for ent in _cache.get(id(parent_pids), []):
-            ref, version, k, m, iref, iversion, plan = ent
-            if ref() is parent_pids and version == parent_pids._version and k[2:] == key[2:] and \
-                    isinstance(plan, BAPlan) and plan.appendable:
-                parent = plan
+        while lin is not None and len(links) < _MAX_CHAIN:
+            links.append(lin)
+            parent_pids = lin[2]()
+            if parent_pids is None or lin[3] != parent_pids._version:
+                return None
+            parent = _cached_appendable(parent_pids, key)
+            if parent is not None:
+                break
+            lin = lin[8]
+            if lin is not None and (lin[0]() is not parent_pids or lin[1] != parent_pids._version):
+                return None
     if parent is None:
         return None
-    add_nppi = lin[5].detach().cpu().numpy().astype(np.int64)
+    links.reverse()                                    # oldest first
+    chain, counts = [], np.diff(np.concatenate([[0], parent._cum.astype(np.int64)]))
+    for q, ln in enumerate(links):
+        add_nppi = ln[5].detach().cpu().numpy().astype(np.int64)
+        if len(add_nppi) != len(counts) + 1:
+            return None
+        counts = np.concatenate([counts, [0]]) + add_nppi
+        n_after = ln[7] if ln[7] is not None else (n_tracks if q == len(links) - 1 else None)
+        if n_after is None:
+            return None
+        chain.append((add_nppi, ln[6].detach().cpu().numpy().astype(np.int64) + ln[4], n_after))
     cum = infos[0].detach().cpu().numpy().astype(np.int64)
-    old_cnt = np.diff(np.concatenate([[0], parent._cum.astype(np.int64)]))
-    if len(cum) != parent.n_imgs + 1 or len(add_nppi) != len(cum) or \
-            not np.array_equal(cum, np.cumsum(np.concatenate([old_cnt, [0]]) + add_nppi)):
+    if chain[-1][2] != int(n_tracks) or len(cum) != len(counts) or not np.array_equal(cum, np.cumsum(counts)):
         return None
-    add_pids = lin[6].detach().cpu().numpy().astype(np.int64) + lin[4]
     try:
-        return BAPlan.appended(parent, infos, pids, n_tracks, add_nppi, add_pids)
+        return BAPlan.appended_chain(parent, infos, pids, n_tracks, chain)
     except RuntimeError:
         return None
 

@@ -541,3 +541,21 @@ def test_plan_append_rejects_non_appends():
     child = BAPlan.appended(parent, infos, pk, Tk, add_cnt, add_pids)
     full = BAPlan(infos, pk, Tk, device='cpu')
     assert all(torch.equal(child.dev[n], full.dev[n]) for n in full.sizes)
+
+
+@pytest.mark.parametrize('cfg,nf,nt,steps', [(2, 40, 2500, 6), (4, 24, 1200, 5), (0, 12, 400, 4)])
+def test_plan_append_chain_equals_full_rebuild(cfg, nf, nt, steps):
+    """BAPlan.appended_chain: several `old | new` in a row planned at once from the first structure's plan
+    (as when the solver runs only every few merges) equals a full plan of the last structure, every array and
+    scalar; the device copy keeps the shortest stable prefix of the chain, ids shifted by the summed shifts."""
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    seq = list(_online_steps(p, steps))
+    parent = BAPlan(*seq[0][:3], device='cpu')
+    links = [(add[0], add[1], Tk) for _, _, Tk, add in seq[1:]]
+    infos, pk, Tk, _ = seq[-1]
+    child = BAPlan.appended_chain(parent, infos, pk, Tk, links)
+    full = BAPlan(infos, pk, Tk, device='cpu')
+    assert child.scalars == full.scalars
+    for name in full.sizes:
+        assert torch.equal(child.dev[name], full.dev[name]), name
+    assert child.stable_prefix['chunk_ent'] > 0 or cfg == 0

@@ -237,3 +237,50 @@ def test_merge_then_plan_is_an_append_equal_to_a_full_plan():
     assert float(st_a.new_loss) == float(st_f.new_loss)
     for k in up_a:
         assert torch.equal(up_a[k], up_f[k]), k
+
+
+@pytest.mark.gpu
+def test_chain_of_merges_is_planned_from_the_last_planned_structure():
+    """Three `old | new` in a row with no plan in between (the solver runs every few frames): the plan of the
+    last structure is made from the first one's cached plan through the recorded lineage, and equals a full
+    plan on every device array."""
+    import numpy as np
+    from blast3r_amd.plan import BAPlan, get_plan
+    from blast3r_amd.synthetic import make_problem
+    p = make_problem(4, n_frames=24, n_tracks=1200)
+    n = p.n_imgs
+    cum = p.infos[0].numpy().astype(np.int64)
+    obs_img = np.repeat(np.arange(n), np.diff(np.concatenate([[0], cum])))
+    pids = p.pids.numpy().astype(np.int64)
+    T = p.n_tracks
+    tmax = np.full(T, -1)
+    np.maximum.at(tmax, pids, obs_img)
+    rank = np.empty(T, dtype=np.int64)
+    rank[np.lexsort((np.arange(T), tmax))] = np.arange(T)
+
+    def part(sel, n_imgs, shift, n_tracks):
+        oi = obs_img[sel]
+        o = np.lexsort((np.arange(len(oi)), oi))
+        idx = torch.from_numpy(np.nonzero(sel)[0][o])
+        nppi = torch.from_numpy(np.bincount(oi, minlength=n_imgs).astype(np.int32))
+        return ObservedTracks(n_imgs, n_tracks, nppi.to(DEV),
+                              torch.from_numpy((rank[pids[idx.numpy()]] - shift).astype(np.int32)).to(DEV),
+                              p.pix2d[idx].to(DEV), p.pix2d_std[idx].to(DEV), p.pix2d_dep[idx].to(DEV), 'log_multidepth')
+
+    def infos_of(trk, k):
+        return torch.stack([torch.cumsum(trk.nppi.long(), 0), p.infos[1, :k].to(DEV).long(),
+                            p.infos[2, :k].to(DEV).long()]).to(torch.int32)
+    k0 = n - 4
+    T0 = int((tmax <= k0).sum())
+    cur = part(tmax[pids] <= k0, k0 + 1, 0, T0)
+    get_plan(infos_of(cur, k0 + 1), cur.pids, cur.n_tracks, device=torch.device(DEV))
+    for k in range(k0 + 1, n):
+        Tk = int((tmax <= k).sum())
+        cur = cur | part(tmax[pids] == k, k + 1, cur.n_tracks, Tk - cur.n_tracks)
+    inf = infos_of(cur, n)
+    plan = get_plan(inf, cur.pids, cur.n_tracks, device=torch.device(DEV))
+    assert plan.stable_prefix is not None, 'the chain was planned in full'
+    full = BAPlan(inf, cur.pids, cur.n_tracks, device=DEV)
+    assert plan.scalars == full.scalars
+    for name in full.sizes:
+        assert torch.equal(plan.dev[name], full.dev[name]), name
