@@ -274,77 +274,101 @@ def _prune():
 
 
 _lineage = {}
-
-
 _MAX_CHAIN = 64
 
 
-def note_append(pids, parent_pids, parent_n_tracks, add_nppi, add_pids, n_tracks=None):
-    """Records that the structure with track ids `pids` is `old | new` of the one with `parent_pids`
-    (tracks.py:84-102): add_nppi (n_imgs + 1,) new observations per image, add_pids the new tracks' ids
-    (before the shift by parent_n_tracks), image by image, n_tracks the merged count; device tensors,
-    read only if a plan is needed.  The parent keeps a strong reference to its own lineage, so a chain of
-    merges can be planned from the last structure that has a plan."""
+class _Lineage:
+    """How the structure with track ids `ref()` was made by `old | new` (tracks.py:84-102): the new
+    observations per image and the new tracks' ids (device tensors, read only if a plan is needed), the
+    track counts, the parent structure's appendable plans when it had any (held here, since the parent
+    structure itself is usually dropped right after the merge; get_plan adds a plan made after the merge),
+    a weak reference to the parent's ids, and the parent's own record if it was a merge result too (so that
+    several merges in a row can be planned from the last planned structure)."""
+    __slots__ = ('ref', 'version', 'parent_ref', 'parent_version', 'parent_n_tracks', 'add_nppi', 'add_pids',
+                 'n_tracks', 'plans', 'parent', 'depth')
+
+    def plan_for(self, key):
+        """The parent structure's appendable plan for this key (call with _cache_lock held)."""
+        for k, plan in self.plans:
+            if k == key[2:] and plan.appendable:
+                return plan
+        ppids = self.parent_ref()
+        if ppids is None or ppids._version != self.parent_version:
+            return None
+        for ref, version, k, m, iref, iversion, plan in _cache.get(id(ppids), []):
+            if ref() is ppids and version == ppids._version and k[2:] == key[2:] and isinstance(plan, BAPlan) \
+                    and plan.appendable:
+                return plan
+        return None
+
+
+def note_append(pids, parent_pids, parent_n_tracks, add_nppi, add_pids, n_tracks):
+    """Records that the structure with track ids `pids` is `old | new` of the one with `parent_pids`:
+    add_nppi (n_imgs + 1,) new observations per image, add_pids the new tracks' ids before the shift by
+    parent_n_tracks, image by image, n_tracks the merged count."""
     with _cache_lock:
-        for k in [k for k, v in _lineage.items() if v[0]() is None]:
+        for k in [k for k, v in _lineage.items() if v.ref() is None]:
             del _lineage[k]
-        parent_lin = _lineage.get(id(parent_pids))
-        if parent_lin is not None and parent_lin[0]() is not parent_pids:
-            parent_lin = None
-        _lineage[id(pids)] = (weakref.ref(pids), pids._version, weakref.ref(parent_pids), parent_pids._version,
-                              int(parent_n_tracks), add_nppi, add_pids,
-                              int(n_tracks) if n_tracks is not None else None, parent_lin)
-
-
-def _cached_appendable(pids, key):
-    for ent in _cache.get(id(pids), []):
-        ref, version, k, m, iref, iversion, plan = ent
-        if ref() is pids and version == pids._version and k[2:] == key[2:] and isinstance(plan, BAPlan) and \
-                plan.appendable:
-            return plan
-    return None
+        rec = _Lineage()
+        rec.ref, rec.version = weakref.ref(pids), pids._version
+        rec.parent_ref, rec.parent_version = weakref.ref(parent_pids), parent_pids._version
+        rec.parent_n_tracks, rec.add_nppi, rec.add_pids, rec.n_tracks = int(parent_n_tracks), add_nppi, add_pids, \
+            int(n_tracks)
+        rec.plans = [(k[2:], plan) for ent in _cache.get(id(parent_pids), [])
+                     for ref, version, k, m, iref, iversion, plan in (ent,)
+                     if ref() is parent_pids and version == parent_pids._version and isinstance(plan, BAPlan)
+                     and plan.appendable]
+        parent = _lineage.get(id(parent_pids))
+        if parent is not None and (parent.ref() is not parent_pids or parent.version != parent_pids._version
+                                   or parent.depth >= _MAX_CHAIN):
+            parent = None
+        rec.parent = parent
+        rec.depth = 1 if parent is None else parent.depth + 1
+        _lineage[id(pids)] = rec
+        while parent is not None:          # plans kept only for appends: their workspaces are made again if used
+            if parent.parent_ref() is None:
+                for _, plan in parent.plans:
+                    plan._ws, plan._slot_cache = {}, {}
+            parent = parent.parent
 
 
 def _appended_plan(infos, pids, n_tracks, key):
-    """The batched plan of `pids` from a cached plan of an earlier structure, when the lineage says the
-    structures between are appends (`old | new`, one image each): the nearest one that has a plan."""
+    """The batched plan of `pids` from the plan of an earlier structure, when the lineage says the structures
+    between are appends (`old | new`, one image each): the nearest one that had a plan."""
     links = []
     with _cache_lock:
-        lin = _lineage.get(id(pids))
-        if lin is None or lin[0]() is not pids or lin[1] != pids._version:
+        rec = _lineage.get(id(pids))
+        if rec is None or rec.ref() is not pids or rec.version != pids._version:
             return None
         parent = None
-        while lin is not None and len(links) < _MAX_CHAIN:
-            links.append(lin)
-            parent_pids = lin[2]()
-            if parent_pids is None or lin[3] != parent_pids._version:
-                return None
-            parent = _cached_appendable(parent_pids, key)
+        while rec is not None:
+            links.append(rec)
+            parent = rec.plan_for(key)
             if parent is not None:
                 break
-            lin = lin[8]
-            if lin is not None and (lin[0]() is not parent_pids or lin[1] != parent_pids._version):
-                return None
+            rec = rec.parent
     if parent is None:
         return None
     links.reverse()                                    # oldest first
     chain, counts = [], np.diff(np.concatenate([[0], parent._cum.astype(np.int64)]))
-    for q, ln in enumerate(links):
-        add_nppi = ln[5].detach().cpu().numpy().astype(np.int64)
+    for ln in links:
+        add_nppi = ln.add_nppi.detach().cpu().numpy().astype(np.int64)
         if len(add_nppi) != len(counts) + 1:
             return None
         counts = np.concatenate([counts, [0]]) + add_nppi
-        n_after = ln[7] if ln[7] is not None else (n_tracks if q == len(links) - 1 else None)
-        if n_after is None:
-            return None
-        chain.append((add_nppi, ln[6].detach().cpu().numpy().astype(np.int64) + ln[4], n_after))
+        chain.append((add_nppi, ln.add_pids.detach().cpu().numpy().astype(np.int64) + ln.parent_n_tracks,
+                      ln.n_tracks))
     cum = infos[0].detach().cpu().numpy().astype(np.int64)
     if chain[-1][2] != int(n_tracks) or len(cum) != len(counts) or not np.array_equal(cum, np.cumsum(counts)):
         return None
     try:
-        return BAPlan.appended_chain(parent, infos, pids, n_tracks, chain)
+        plan = BAPlan.appended_chain(parent, infos, pids, n_tracks, chain)
     except RuntimeError:
         return None
+    with _cache_lock:                                  # the parent's host plan is consumed: let it go
+        for ln in links:
+            ln.plans = [(k, p) for k, p in ln.plans if p is not parent]
+    return plan
 
 
 def get_plan(infos, pids, n_tracks, kind='batched', **kw):
@@ -377,4 +401,8 @@ def get_plan(infos, pids, n_tracks, kind='batched', **kw):
             _cache.clear()
         _cache.setdefault(id(pids), []).append((weakref.ref(pids), pids._version, key, meta, weakref.ref(infos),
                                                 infos._version, plan))
+        if isinstance(plan, BAPlan):     # planned after a merge: its children keep it past this structure's end
+            for rec in _lineage.values():
+                if rec.parent_ref() is pids and rec.parent_version == pids._version:
+                    rec.plans.append((key[2:], plan))
     return plan

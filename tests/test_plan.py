@@ -559,3 +559,40 @@ def test_plan_append_chain_equals_full_rebuild(cfg, nf, nt, steps):
     for name in full.sizes:
         assert torch.equal(child.dev[name], full.dev[name]), name
     assert child.stable_prefix['chunk_ent'] > 0 or cfg == 0
+
+
+@pytest.mark.parametrize('plan_first', [True, False])
+def test_lineage_plans_merges_from_a_dropped_parent(plan_first):
+    """The solver-side path of `old | new` (tracks.py:84-102): note_append records each merge, every structure
+    but the last is dropped as a pipeline does (`trk = trk | new`), and get_plan of the last one is made from the
+    plan of the first (planned before the merges, or after the first merge while it is still alive) through the
+    recorded lineage; it equals a full plan, and the consumed plan is let go."""
+    import gc
+    from blast3r_amd import plan as bp
+    p = make_problem(4, n_frames=24, n_tracks=1200)
+    seq = [(i, pk.clone(), T, a) for i, pk, T, a in _online_steps(p, 4)]
+    infos0, prev_pids, prev_T, _ = seq[0]
+    seq[0] = None
+    if plan_first:
+        bp.get_plan(infos0, prev_pids, prev_T, device=torch.device('cpu'))
+    for j in range(1, len(seq)):
+        infos, pk, Tk, add = seq[j]
+        seq[j] = None
+        bp.note_append(pk, prev_pids, prev_T, torch.from_numpy(add[0]), torch.from_numpy(add[1] - prev_T), Tk)
+        if j == 1 and not plan_first:
+            bp.get_plan(infos0, prev_pids, prev_T, device=torch.device('cpu'))
+        prev_pids, prev_T = pk, Tk
+        del pk
+        gc.collect()
+    rec = bp._lineage[id(prev_pids)]
+    assert rec.depth == len(seq) - 1
+    plan = bp.get_plan(infos, prev_pids, Tk, device=torch.device('cpu'))
+    assert plan.stable_prefix is not None, 'the chain was planned in full'
+    full = BAPlan(infos, prev_pids, Tk, device='cpu')
+    assert plan.scalars == full.scalars
+    for name in full.sizes:
+        assert torch.equal(plan.dev[name], full.dev[name]), name
+    r = rec
+    while r is not None:
+        assert not r.plans
+        r = r.parent
