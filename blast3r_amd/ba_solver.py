@@ -456,26 +456,41 @@ class GaussNewtonSolver:
             pa.long_ptr, pa.long_idx = ptr(um['long_ptr']), ptr(um['long_idx'])
             pa.src1, pa.long_rng = ptr(um['src1']), ptr(um['long_rng'])
             self.last['direct'] = None
-            if not (self.solver == 'cholesky' and self._run_direct(pa, plan, st, n_imgs, um)):
+            direct_info = self._run_direct(pa, plan, st, n_imgs, um) if self.solver == 'cholesky' else None
+            if direct_info is None:
                 self._pcg_rows(pa, plan, d, n_imgs)
                 self._run_pcg(pa, plan, st)
             self.last.update(rhs=rhs, diagA=diagA, damp=damp)
-        # back-substitution for the points
-        dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
+        else:
+            direct_info = None
         pm = ctx['path'] == 'pairmajor'
-        if en['X'][0] and (sc['n_runs'] > 0 if pm else sc['n_chunks'] > 0):
-            if 'umap_pad' not in um:                   # -1 -> the appended zero, once per structure
-                um['umap_pad'] = torch.where(um['umap'] >= 0, um['umap'], x.numel()).long().view(-1)
-            dc_img = torch.nn.functional.pad(x, (0, 1))[um['umap_pad']]
-            a.dc_img = ptr(dc_img)                     # delta_c at image level (one load fewer per obs)
-            a.dX = ptr(dX)
-            a.dX64 = None
-            if pm:
-                check(lib().ba_pm_backsubstitute(a, st))
-            else:
-                a.dc = ptr(x)
-                a.umap = ptr(um['umap'])
-                check(lib().ba_backsubstitute(a, st))
+        has_X = en['X'][0] and (sc['n_runs'] > 0 if pm else sc['n_chunks'] > 0)
+
+        def backsubstitute():
+            # back-substitution for the points
+            dX = torch.zeros((max(T, 1), 3), dtype=torch.float32, device=dev)
+            if has_X:
+                if 'umap_pad' not in um:               # -1 -> the appended zero, once per structure
+                    um['umap_pad'] = torch.where(um['umap'] >= 0, um['umap'], x.numel()).long().view(-1)
+                dc_img = torch.nn.functional.pad(x, (0, 1))[um['umap_pad']]
+                a.dc_img = ptr(dc_img)                 # delta_c at image level (one load fewer per obs)
+                a.dX = ptr(dX)
+                a.dX64 = None
+                if pm:
+                    check(lib().ba_pm_backsubstitute(a, st))
+                else:
+                    a.dc = ptr(x)
+                    a.umap = ptr(um['umap'])
+                    check(lib().ba_backsubstitute(a, st))
+                ctx['keep_dc'] = dc_img
+            return dX
+
+        dX = backsubstitute()
+        if direct_info is not None and not self._direct_status(direct_info):
+            # a pivot was not positive: the device PCG solves the same system, then the points again
+            self._pcg_rows(pa, plan, d, n_imgs)
+            self._run_pcg(pa, plan, st)
+            dX = backsubstitute()
         self.last.update(S_pairs=S_pairs, e_img=e_img, dg_img=dg_img, unknowns=um, lay=lay, plan=plan, x=x,
                          istate=istate, Hpp=Hpp, gp=gp, lam_p=lam_p, path=ctx['path'])
         dc = x[:n_u].to(torch.float32)
@@ -501,9 +516,9 @@ class GaussNewtonSolver:
         pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * gw,), torch.int32))
 
     def _run_direct(self, pa, plan, st, n_imgs, um):
-        """ba_reduced_solve (L L^T of the damped reduced system, banded or dense).  Returns False, after
-        recording it in last['direct'], when a pivot was not positive: the caller then runs the device
-        PCG."""
+        """Enqueues ba_reduced_solve (L L^T of the damped reduced system, banded or dense) and returns
+        its status word on the device, read by _direct_status once the back-substitution is enqueued too
+        (so the host's read does not stall the queue between the two)."""
         L = lib()
         ws = plan.workspace
         d = pa.d
@@ -553,9 +568,16 @@ class GaussNewtonSolver:
             ca.Linv = ptr(ws('chol_Linv', (lda // 128, 128, 128), torch.float64))
         check(L.ba_reduced_solve(pa, ca, st))
         self.last['direct_call'] = (pa, ca)    # kept for re-timing the bare launch sequence
-        bad = int(info.cpu())                  # one read per solve
         self.last['direct'] = dict(layout=layout, w=w, db=db, n_shared=ns, superblocks=nsb if mode == 1 else 0,
-                                   first_bad_pivot=None if bad == 2 ** 31 - 1 else bad)
+                                   first_bad_pivot=None)
+        return info
+
+    def _direct_status(self, info):
+        """The direct solve's status (one read per solve): True when every pivot was positive; else
+        records the first bad pivot in last['direct'] and returns False (the caller then runs the PCG)."""
+        bad = int(info.cpu())
+        if bad != 2 ** 31 - 1:
+            self.last['direct']['first_bad_pivot'] = bad
         return bad == 2 ** 31 - 1
 
     def _run_pcg(self, pa, plan, st):

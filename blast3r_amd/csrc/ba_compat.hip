@@ -25,35 +25,90 @@ static inline hipStream_t S(void* s) { return (hipStream_t)s; }
 static inline unsigned nblk(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
 // ----------------------------------------------------------------------------- residuals
-__global__ void __launch_bounds__(256) k_residuals(const int* __restrict__ infos, int n_imgs, const float* __restrict__ K,
-                                                   const float* __restrict__ Prc, int64_t prc_stride,
-                                                   const float* __restrict__ Pwr, const float* __restrict__ zc,
-                                                   const float* __restrict__ pts, const int* __restrict__ pids,
-                                                   const float* __restrict__ pix, const float* __restrict__ sd,
-                                                   const float* __restrict__ dep, int64_t n_obs, int C, HuberParams hp,
-                                                   float* __restrict__ out) {
-    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n_obs) return;
-    int img = obs_image(infos, n_imgs, (int)idx);
-    int node = infos[n_imgs + img];
-    int cam = infos[2 * n_imgs + img];
-    int pid = pids[idx];
-    CamF cp;
-    load_cam(cp, K, Prc, prc_stride, Pwr, cam, node);
-    float X[3] = {pts[3 * (int64_t)pid], pts[3 * (int64_t)pid + 1], pts[3 * (int64_t)pid + 2]};
-    float g = 0.f;
-    for (int c = 0; c < C; ++c) g += zc[(int64_t)img * C + c] * dep[idx * C + c];
-    float2 uv = reinterpret_cast<const float2*>(pix)[idx];
-    float2 sv = reinterpret_cast<const float2*>(sd)[idx];
-    ResOut o;
-    eval_residual(cp, X, uv.x, uv.y, sv.x, sv.y, g, hp, o);
+// One block per RES_T * RES_K consecutive observations (RES_K per thread, RES_T apart, so every load
+// and store is coalesced).  The observations of a block are image-sorted, so its images form the range
+// [lo, hi], found by two searches per block; the cameras and z-coefficients of the first RES_NI images
+// of that range are staged in LDS (blocks over more images read the rest from memory).  All loads of a
+// thread's RES_K observations are issued before any of them is evaluated.  The per-observation
+// arithmetic is eval_residual's, in the reference's order (.cu:129-259).
+constexpr int RES_T = 256, RES_K = 4, RES_NI = 4, RES_ZC = 32;
+
+__device__ __forceinline__ int obs_image_in(const int* __restrict__ cum, int lo, int hi, int idx) {
+    int a = lo, b = hi + 1;                  // cum[a - 1] <= idx < cum[a], a in [lo, hi]
+    while (b - a > 1) {
+        int m = (a + b) >> 1;
+        if (idx < cum[m - 1]) b = m; else a = m;
+    }
+    return a;
+}
+
+__global__ void __launch_bounds__(RES_T) k_residuals(const int* __restrict__ infos, int n_imgs, const float* __restrict__ K,
+                                                     const float* __restrict__ Prc, int64_t prc_stride,
+                                                     const float* __restrict__ Pwr, const float* __restrict__ zc,
+                                                     const float* __restrict__ pts, const int* __restrict__ pids,
+                                                     const float* __restrict__ pix, const float* __restrict__ sd,
+                                                     const float* __restrict__ dep, int64_t n_obs, int C, HuberParams hp,
+                                                     float* __restrict__ out) {
+    __shared__ int s_rng[2];
+    __shared__ CamF s_cam[RES_NI];
+    __shared__ float s_zc[RES_NI * RES_ZC];
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)blockIdx.x * (RES_T * RES_K);
+    const int64_t last = (base + RES_T * RES_K < n_obs ? base + RES_T * RES_K : n_obs) - 1;
+    if (tid == 0) s_rng[0] = obs_image(infos, n_imgs, (int)base);
+    if (tid == 64) s_rng[1] = obs_image(infos, n_imgs, (int)last);
+    __syncthreads();
+    const int lo = s_rng[0], hi = s_rng[1];
+    const int nst = hi - lo + 1 < RES_NI ? hi - lo + 1 : RES_NI;
+    const bool zc_lds = C <= RES_ZC;
+    if (tid < nst) {
+        CamF c;
+        load_cam(c, K, Prc, prc_stride, Pwr, infos[2 * n_imgs + lo + tid], infos[n_imgs + lo + tid]);
+        s_cam[tid] = c;
+    }
+    if (zc_lds && tid < nst * C) s_zc[tid] = zc[(int64_t)lo * C + tid];
+    // every load of the thread's observations (indices clamped into range; only stores are guarded)
+    int64_t idx[RES_K];
+    int pid[RES_K], img[RES_K];
+    float2 uv[RES_K], sv[RES_K];
+    float X[RES_K][3];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) out[i * n_obs + idx] = o.r[i];
-    if (hp.pnorm > 0.f) {
+    for (int k = 0; k < RES_K; ++k) {
+        const int64_t i = base + k * RES_T + tid;
+        idx[k] = i < n_obs ? i : n_obs - 1;
+        pid[k] = pids[idx[k]];
+        uv[k] = reinterpret_cast<const float2*>(pix)[idx[k]];
+        sv[k] = reinterpret_cast<const float2*>(sd)[idx[k]];
+        img[k] = lo == hi ? lo : obs_image_in(infos, lo, hi, (int)idx[k]);
+    }
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            out[(3 + i) * n_obs + idx] = o.err[i];
-            out[(6 + i) * n_obs + idx] = o.w[i];
+    for (int k = 0; k < RES_K; ++k) {
+        const float* x = pts + 3 * (int64_t)pid[k];
+        X[k][0] = x[0]; X[k][1] = x[1]; X[k][2] = x[2];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < RES_K; ++k) {
+        const int li = img[k] - lo;
+        CamF cp;
+        if (li < RES_NI) cp = s_cam[li];
+        else load_cam(cp, K, Prc, prc_stride, Pwr, infos[2 * n_imgs + img[k]], infos[n_imgs + img[k]]);
+        const float* zi = zc_lds && li < RES_NI ? s_zc + li * C : zc + (int64_t)img[k] * C;
+        float g = 0.f;
+        for (int c = 0; c < C; ++c) g += zi[c] * dep[idx[k] * C + c];
+        ResOut o;
+        eval_residual(cp, X[k], uv[k].x, uv[k].y, sv[k].x, sv[k].y, g, hp, o);
+        if (base + k * RES_T + tid < n_obs) {
+            const int64_t i = idx[k];
+#pragma unroll
+            for (int r = 0; r < 3; ++r) out[r * n_obs + i] = o.r[r];
+            if (hp.pnorm > 0.f) {
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    out[(3 + r) * n_obs + i] = o.err[r];
+                    out[(6 + r) * n_obs + i] = o.w[r];
+                }
+            }
         }
     }
 }
@@ -70,7 +125,7 @@ extern "C" int ba_residuals(const int32_t* infos, int32_t n_imgs, const float* K
     BA_REQUIRE(n_imgs > 0 && C >= 0 && n_obs >= 0, "bad sizes");
     if (n_obs == 0) return BA_OK;
     HuberParams hp{weight_z, pnorm, max_pix_err, huber_delta, w_pts_null, is_depth_log};
-    hipLaunchKernelGGL(k_residuals, dim3(nblk(n_obs, 256)), dim3(256), 0, S(stream), infos, n_imgs, K, P_rig2cam,
+    hipLaunchKernelGGL(k_residuals, dim3(nblk(n_obs, RES_T * RES_K)), dim3(RES_T), 0, S(stream), infos, n_imgs, K, P_rig2cam,
                        P_rig2cam_stride, P_w2rig, z_coefs, pts3d, pids, pix2d, pix2d_std, pix2d_dep, n_obs, C, hp, out);
     BA_LAUNCHED();
     return BA_OK;

@@ -62,6 +62,38 @@ def test_residuals_parity(cfg, nf, nt):
     assert rel_err(out3, ref[:, :3]) < 1e-5
 
 
+@pytest.mark.parametrize('case', ['wide_C', 'empty_images', 'many_small_images'])
+def test_residuals_block_image_ranges(case):
+    """k_residuals takes each block's image range from two searches and stages the cameras and
+    z-coefficients of its first four images in LDS: blocks whose range holds empty images, more than
+    four images (the rest read from memory) or more z-coefficients than the staging holds (C = 41) give
+    the oracle's residuals, errors and weights."""
+    if case == 'wide_C':
+        p = make_problem(0, n_frames=12, n_tracks=600, n_channels=40)
+    elif case == 'many_small_images':
+        p = make_problem(1, n_frames=64, n_tracks=120)
+    else:
+        p = make_problem(0, n_frames=16, n_tracks=800)
+        cum = p.infos[0].long()
+        img = torch.repeat_interleave(torch.arange(p.n_imgs), torch.diff(torch.cat([cum.new_zeros(1), cum])))
+        keep = (img != 0) & (img != 3) & (img != 4) & (img != p.n_imgs - 1)
+        p.pids, p.pix2d, p.pix2d_std, p.pix2d_dep = (t[keep] for t in (p.pids, p.pix2d, p.pix2d_std, p.pix2d_dep))
+        infos = p.infos.clone()
+        infos[0] = torch.cumsum(torch.bincount(img[keep], minlength=p.n_imgs), 0).to(infos.dtype)
+        p.infos = infos
+    print(f'residual block ranges: {case}, {p.n_imgs} images, {p.pids.numel()} obs, C={p.pix2d_dep.shape[1]}',
+          flush=True)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    ref = _oracle_res(p)
+    assert out.shape == ref.shape
+    for sl in (slice(0, 3), slice(3, 6), slice(6, 9)):
+        assert rel_err(out[:, sl], ref[:, sl]) < 1e-5
+
+
 def test_residuals_invalid_depth_rows_are_zero():
     p = tiny_problem()
     P = p.P_w2rig.clone()
@@ -890,6 +922,41 @@ def test_lm_step_full_config2_line_search():
     ls = _check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g)
     print(f'[full cfg2 lm_step] loss {float(l0):.6g} -> {float(ls["new_loss"]):.6g} at scale {ls["scale"]}',
           flush=True)
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 30, 1500)])
+def test_reduced_solve_cholesky_fallback_runs_pcg_and_points_again(cfg, nf, nt):
+    """When the direct solve reports a pivot that is not positive (forced here from the host: the status
+    read says so), solve_delta runs the device PCG on the same system and the point back-substitution
+    again, so the step equals solver='pcg''s bit for bit; the status is read once, after the first
+    back-substitution was enqueued."""
+    print(f'cholesky fallback cfg {cfg} ({nf} frames, {nt} tracks)', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    flags = _cfg_flags(p)
+    g = _gpu(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    deltas, reads = [], []
+    for solver in ('cholesky', 'pcg'):
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, solver=solver)
+        if solver == 'cholesky':
+            real = gs._direct_status
+
+            def forced(info, real=real):
+                reads.append(real(info))
+                gs.last['direct']['first_bad_pivot'] = 0
+                return False
+            gs._direct_status = forced
+        J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
+        deltas.append(gs.solve_delta(J, res, w))
+        if solver == 'cholesky':
+            assert reads == [True] and gs.last['direct']['first_bad_pivot'] == 0
+    assert torch.equal(deltas[0], deltas[1])
 
 
 _CHOL_CASES = [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800), (2, 70, 3000)]
