@@ -70,6 +70,22 @@ struct ResOut {
 
 typedef ba_huber HuberParams;
 
+// Huber errors and IRLS weights of the three residuals (.cu:240-258); PC = 1 or 2 when the exponent p is
+// 1 or 2 (r^p, r^(p-2) in closed form), else 0 (powf).
+template <int PC>
+__device__ __forceinline__ void huber_rows(const HuberParams& hp, float a, float b, const float (&wz)[3], ResOut& o) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        float r = fabsf(o.r[i]);
+        r = (r > hp.max_pix_err) ? hp.max_pix_err : r;
+        const float rp = PC == 1 ? r : (PC == 2 ? r * r : powf(r, hp.pnorm));
+        o.err[i] = wz[i] * ((r <= hp.huber_delta) ? a * r * r : rp - b);
+        r = (r < hp.huber_delta) ? hp.huber_delta : r;
+        const float rpm2 = PC == 1 ? 1.f / r : (PC == 2 ? 1.f : powf(r, hp.pnorm - 2.f));
+        o.w[i] = (r == hp.max_pix_err) ? hp.w_pts_null : wz[i] * rpm2;
+    }
+}
+
 // Same operation order as .cu:201-258 (matmul with bias, then projection, then Huber).
 __device__ __forceinline__ void eval_residual(const CamF& cp, const float X[3], float u, float v, float su, float sv,
                                               float guidance, const HuberParams& hp, ResOut& o) {
@@ -105,14 +121,12 @@ __device__ __forceinline__ void eval_residual(const CamF& cp, const float X[3], 
         float a = 0.5f * hp.pnorm * powf(hp.huber_delta, hp.pnorm - 2.f);
         float b = powf(hp.huber_delta, hp.pnorm) - a * hp.huber_delta * hp.huber_delta;
         float wz[3] = {1.f, 1.f, hp.weight_z};
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            float r = fabsf(o.r[i]);
-            r = (r > hp.max_pix_err) ? hp.max_pix_err : r;
-            o.err[i] = wz[i] * ((r <= hp.huber_delta) ? a * r * r : powf(r, hp.pnorm) - b);
-            r = (r < hp.huber_delta) ? hp.huber_delta : r;
-            o.w[i] = (r == hp.max_pix_err) ? hp.w_pts_null : wz[i] * powf(r, hp.pnorm - 2.f);
-        }
+        // r^p and r^(p-2) in closed form for the exponents 1 (the reference's default, args.py:61) and 2:
+        // r and 1/r, r*r and 1; a general powf costs some 200 instructions, three pairs per observation.
+        // The exponent is uniform, so each case is its own branch (no speculated powf).
+        if (hp.pnorm == 1.f)      huber_rows<1>(hp, a, b, wz, o);
+        else if (hp.pnorm == 2.f) huber_rows<2>(hp, a, b, wz, o);
+        else                      huber_rows<0>(hp, a, b, wz, o);
     }
 }
 

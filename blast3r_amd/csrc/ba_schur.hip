@@ -1508,20 +1508,27 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
 // per run row: y = V_r[k] . delta_c(image of r), DP lanes per row (coalesced over V)
 template <int DP>
 __global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
-    const int64_t n_el = a.n_runs * 3 * DP;
+    // one thread per (run, column): the run's image and delta_c entry are read once for its three V rows
+    // (each row's DP columns on DP neighbouring lanes, so every V load is coalesced), and the products
+    // are summed over the DP lanes by the same xor tree for each row
     const int d = a.lay.d;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e - (threadIdx.x & 63) < n_el;
-         e += (int64_t)gridDim.x * 256) {
-        const int col = (int)(e % DP);
-        const int64_t row = e / DP;
-        double v = 0.0;
-        if (e < n_el && col < d) {
-            const int64_t r = row / 3;
-            v = a.V[e] * a.dc_img[(int64_t)a.run_img[r] * d + col];
+    const int col = threadIdx.x % DP;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t - (threadIdx.x & 63) < a.n_runs * DP;
+         t += (int64_t)gridDim.x * 256) {
+        const int64_t r = t / DP;
+        const bool live = r < a.n_runs;
+        double v[3] = {0.0, 0.0, 0.0};
+        if (live && col < d) {
+            const double dc = a.dc_img[(int64_t)a.run_img[r] * d + col];
+            const double* V = a.V + r * 3 * DP + col;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) v[k] = V[k * DP] * dc;
         }
 #pragma unroll
-        for (int m = DP / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-        if (e < n_el && col == 0) a.yrun[row] = v;
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int m = DP / 2; m >= 1; m >>= 1) v[k] += __shfl_xor(v[k], m);
+        if (live && col < 3) a.yrun[3 * r + col] = col == 0 ? v[0] : (col == 1 ? v[1] : v[2]);
     }
 }
 
@@ -1646,8 +1653,8 @@ extern "C" int ba_pm_backsubstitute(const ba_pm_args* args, void* stream) {
     hipStream_t st = (hipStream_t)stream;
     if (a.n_runs > 0) {
         const int dp = a.lay.d > 15 ? 32 : 16;
-        const int64_t n_el = a.n_runs * 3 * dp;
-        const unsigned g = (unsigned)std::min<int64_t>((n_el + 255) / 256, 65536);
+        const int64_t n_th = a.n_runs * dp;      // one thread per (run, column)
+        const unsigned g = (unsigned)std::min<int64_t>((n_th + 255) / 256, 1 << 22);
         if (dp == 32) hipLaunchKernelGGL(k_pm_yrun<32>, dim3(g), dim3(256), 0, st, a);
         else          hipLaunchKernelGGL(k_pm_yrun<16>, dim3(g), dim3(256), 0, st, a);
     }

@@ -62,6 +62,25 @@ def test_residuals_parity(cfg, nf, nt):
     assert rel_err(out3, ref[:, :3]) < 1e-5
 
 
+@pytest.mark.parametrize('pnorm', [1.0, 2.0, 0.5, 1.5])
+def test_residuals_huber_exponents(pnorm):
+    """The Huber error and IRLS weight for the exponents with closed forms (p = 1: r and 1/r; p = 2: r^2 and
+    1) and for general ones (powf), with residuals beyond delta and beyond the clip value present, against
+    the oracle's torch pow (.cu:240-258)."""
+    p = make_problem(0, n_frames=12, n_tracks=800)
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], pnorm,
+                                            o['clip_pix_err'], o['huber_delta'])
+    ref = _oracle_res(p, pnorm=pnorm)
+    r = ref[:, :2].abs()
+    assert bool((r > o['huber_delta']).any()) and bool((r < o['huber_delta']).any())
+    assert bool((r >= o['clip_pix_err']).any())
+    for sl in (slice(0, 3), slice(3, 6), slice(6, 9)):
+        assert rel_err(out[:, sl], ref[:, sl]) < 1e-5
+
+
 @pytest.mark.parametrize('case', ['wide_C', 'empty_images', 'many_small_images'])
 def test_residuals_block_image_ranges(case):
     """k_residuals takes each block's image range from two searches and stages the cameras and
