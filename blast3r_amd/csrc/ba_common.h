@@ -70,19 +70,30 @@ struct ResOut {
 
 typedef ba_huber HuberParams;
 
-// Huber errors and IRLS weights of the three residuals (.cu:240-258); PC = 1 or 2 when the exponent p is
-// 1 or 2 (r^p, r^(p-2) in closed form), else 0 (powf).
+// x^p and x^(p-2) for the Huber exponent p: in closed form when PC = 1 (x, 1/x) or PC = 2 (x*x, 1), else
+// powf (a general powf costs some 150 instructions per wave, uniform input or not).
 template <int PC>
-__device__ __forceinline__ void huber_rows(const HuberParams& hp, float a, float b, const float (&wz)[3], ResOut& o) {
+__device__ __forceinline__ float hub_pow_p(float x, float p) { return PC == 1 ? x : (PC == 2 ? x * x : powf(x, p)); }
+template <int PC>
+__device__ __forceinline__ float hub_pow_pm2(float x, float p) {
+    return PC == 1 ? 1.f / x : (PC == 2 ? 1.f : powf(x, p - 2.f));
+}
+
+// Huber errors and IRLS weights of the three residuals (.cu:240-258), with the constants
+// a = p delta^(p-2) / 2 and b = delta^p - a delta^2 of the reference's formula.
+template <int PC>
+__device__ __forceinline__ void huber_rows(const HuberParams& hp, ResOut& o) {
+    const float p = hp.pnorm, dl = hp.huber_delta;
+    const float a = 0.5f * p * hub_pow_pm2<PC>(dl, p);
+    const float b = hub_pow_p<PC>(dl, p) - a * dl * dl;
+    const float wz[3] = {1.f, 1.f, hp.weight_z};
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         float r = fabsf(o.r[i]);
         r = (r > hp.max_pix_err) ? hp.max_pix_err : r;
-        const float rp = PC == 1 ? r : (PC == 2 ? r * r : powf(r, hp.pnorm));
-        o.err[i] = wz[i] * ((r <= hp.huber_delta) ? a * r * r : rp - b);
-        r = (r < hp.huber_delta) ? hp.huber_delta : r;
-        const float rpm2 = PC == 1 ? 1.f / r : (PC == 2 ? 1.f : powf(r, hp.pnorm - 2.f));
-        o.w[i] = (r == hp.max_pix_err) ? hp.w_pts_null : wz[i] * rpm2;
+        o.err[i] = wz[i] * ((r <= dl) ? a * r * r : hub_pow_p<PC>(r, p) - b);
+        r = (r < dl) ? dl : r;
+        o.w[i] = (r == hp.max_pix_err) ? hp.w_pts_null : wz[i] * hub_pow_pm2<PC>(r, p);
     }
 }
 
@@ -118,15 +129,11 @@ __device__ __forceinline__ void eval_residual(const CamF& cp, const float X[3], 
     if (hp.is_depth_log) o.r[2] = avg_focal * (guidance - logf(z));
     else                 o.r[2] = avg_focal * logf(guidance / z);
     if (hp.pnorm > 0.f) {
-        float a = 0.5f * hp.pnorm * powf(hp.huber_delta, hp.pnorm - 2.f);
-        float b = powf(hp.huber_delta, hp.pnorm) - a * hp.huber_delta * hp.huber_delta;
-        float wz[3] = {1.f, 1.f, hp.weight_z};
-        // r^p and r^(p-2) in closed form for the exponents 1 (the reference's default, args.py:61) and 2:
-        // r and 1/r, r*r and 1; a general powf costs some 200 instructions, three pairs per observation.
-        // The exponent is uniform, so each case is its own branch (no speculated powf).
-        if (hp.pnorm == 1.f)      huber_rows<1>(hp, a, b, wz, o);
-        else if (hp.pnorm == 2.f) huber_rows<2>(hp, a, b, wz, o);
-        else                      huber_rows<0>(hp, a, b, wz, o);
+        // exponent 1 is the reference's default (args.py:61); the exponent is uniform, so each case is its
+        // own branch (no speculated powf)
+        if (hp.pnorm == 1.f)      huber_rows<1>(hp, o);
+        else if (hp.pnorm == 2.f) huber_rows<2>(hp, o);
+        else                      huber_rows<0>(hp, o);
     }
 }
 
