@@ -25,6 +25,7 @@ SCALARS = ['n_chunks', 'n_batches', 'n_slots', 'n_pairs', 'n_ctracks', 'L', 'chu
            'max_chunks_per_batch', 'n_pair_terms']
 CHUNK = 128
 MAX_LOCAL = 16
+_append_lock = threading.Lock()
 MAX_SLOTS = 96
 
 
@@ -161,11 +162,12 @@ class BAPlan:
     def appended_chain(cls, parent, infos, pids, n_tracks, links):
         """As appended, over several appends in a row (`((old | a) | b) | ...`): links lists, oldest first,
         each append's (add_cnt, add_pids, n_tracks after it)."""
-        if parent._h is None:
-            raise RuntimeError('the parent plan was already appended to')
         chain = [(np.ascontiguousarray(c, dtype=np.int32), np.ascontiguousarray(p, dtype=np.int32), int(t))
                  for c, p, t in links]
-        return cls(infos, pids, n_tracks, device=parent.device, _parent=parent, _chain=chain, **parent.options)
+        with _append_lock:             # ba_plan_append consumes the parent's host plan: one append at a time
+            if parent._h is None:
+                raise RuntimeError('the parent plan was already appended to')
+            return cls(infos, pids, n_tracks, device=parent.device, _parent=parent, _chain=chain, **parent.options)
 
     def __del__(self):
         h, self._h = getattr(self, '_h', None), None

@@ -596,3 +596,31 @@ def test_lineage_plans_merges_from_a_dropped_parent(plan_first):
     while r is not None:
         assert not r.plans
         r = r.parent
+
+
+def test_plan_append_from_two_threads_consumes_the_parent_once():
+    """Two threads appending to one parent plan at once: one append consumes the parent's host plan and
+    equals a full rebuild, the other is refused with a RuntimeError (it never touches the consumed plan)."""
+    import threading
+    p = make_problem(2, n_frames=30, n_tracks=1500)
+    seq = list(_online_steps(p, 2))
+    parent = BAPlan(*seq[0][:3], device='cpu')
+    infos, pk, Tk, add = seq[1]
+    out, errs = [], []
+    gate = threading.Barrier(2)
+
+    def run():
+        gate.wait()
+        try:
+            out.append(BAPlan.appended(parent, infos, pk, Tk, add[0], add[1]))
+        except RuntimeError as e:
+            errs.append(str(e))
+    ts = [threading.Thread(target=run) for _ in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert len(out) == 1 and len(errs) == 1 and 'already appended' in errs[0]
+    full = BAPlan(infos, pk, Tk, device='cpu')
+    for name in full.sizes:
+        assert torch.equal(out[0].dev[name], full.dev[name]), name
