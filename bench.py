@@ -53,7 +53,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one MI355X: multi-GPU runs are not part of this build '
-              '(the path would shard by track with one all-reduce of the reduced system; see DESIGN.md)',
+              '(the path would shard by track, with one all-reduce of the reduced system)',
               file=sys.stderr)
         sys.exit(2)
 
