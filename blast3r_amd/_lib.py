@@ -156,6 +156,9 @@ _SIGS = {
     'ba_linearize_stage': (c_int, [ctypes.POINTER(BaLinArgs), c_int, c_p]),
     'ba_backsubstitute': (c_int, [ctypes.POINTER(BaLinArgs), c_p]),
     'ba_pcg_solve': (c_int, [ctypes.POINTER(BaPcgArgs), c_p]),
+    'ba_pcg_solve_range': (c_int, [ctypes.POINTER(BaPcgArgs), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_p,
+                                   c_p]),
+    'ba_host_mapped_ptr': (c_p, [c_p]),
     'ba_pcg_partials_size': (c_i64, [c_i64]),
     'ba_apply_update': (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_f, c_f, c_int, c_int, c_int, c_int, c_i64,
                                 c_p, c_p, c_p, c_p, c_p]),

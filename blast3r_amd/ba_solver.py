@@ -13,6 +13,8 @@ fp64 Jacobian blocks, and ``solve_delta`` runs the fused HIP path
 
 with no host synchronisation between them.
 """
+import ctypes
+
 import numpy as np
 import torch
 
@@ -68,6 +70,9 @@ def _flag(status, name, count, device):
                                f'tensor (mask on {status.device}, observations on {device})')
         return True, status.to(torch.uint8).contiguous(), idxs
     raise ValueError(f'bad {name}={status}')
+
+
+PCG_CHUNK = 25          # PCG iterations per graph when the host stops launching after the loop stops
 
 
 class GaussNewtonSolver:
@@ -581,23 +586,75 @@ class GaussNewtonSolver:
         return bad == 2 ** 31 - 1
 
     def _run_pcg(self, pa, plan, st):
-        """ba_pcg_solve, replayed from a HIP graph (captured once per argument set and kept with the
-        plan) so that its ~4 x maxiter launches cost one graph launch."""
+        """ba_pcg_solve, replayed from HIP graphs captured once per argument set and kept with the plan.  The
+        iterations go in chunks of PCG_CHUNK, one graph each, whose last kernel stores the loop's stopped flag
+        to pinned host memory; the host reads chunk k's flag (after chunk k's event) while chunk k + 1 runs,
+        and once the loop has stopped launches only the final decisions and the result (the reference checks
+        its stopping rule after every iteration, bs:1216-1236).  The kernels skipped would have returned at
+        once, so the result is the one of the whole sequence.  Where the loop ran to its cap the last time
+        on this argument set, the whole sequence is replayed from one graph instead (chunks are tried again
+        every eighth solve); so it is without a device-reachable flag, and launched directly with use_graph
+        off."""
+        L = lib()
+        self.last['pcg_launched'] = int(pa.maxiter)    # iterations launched (those after a stop return at once)
         if not self.use_graph:
-            check(lib().ba_pcg_solve(pa, st))
+            check(L.ba_pcg_solve(pa, st))
             return
         graphs = plan.__dict__.setdefault('_pcg_graphs', {})
         key = bytes(pa)
-        g = graphs.get(key)
-        if g is None:
+        ent = graphs.get(key)
+        if ent is None:
             if len(graphs) > 4:
                 graphs.clear()
+            ent = self._capture_pcg(pa)
+            graphs[key] = ent
+        ent['solves'] += 1
+        if ent['chunks'] is None or not (ent['early'] or ent['solves'] % 8 == 1):
+            # the loop ran to its cap on this argument set last time: the whole sequence, one graph (chunks
+            # cost a graph launch and a flag store each); chunks are tried again every eighth solve
+            ent['whole'].replay()
+            return
+        flags, bounds, chunks, fin = ent['flags'], ent['bounds'], ent['chunks'], ent['fin']
+        events = []
+        end = bounds[-1]
+        for k, g in enumerate(chunks):
+            g.replay()
+            ev = torch.cuda.Event()
+            ev.record()
+            events.append(ev)
+            if k >= 1:                                 # chunk k runs while chunk k - 1's flag is read
+                events[k - 1].synchronize()
+                if int(flags[k - 1]):                  # stopped before update bounds[k]: chunk k returns at once
+                    end = bounds[k + 1]
+                    break
+        fin[end].replay()
+        self.last['pcg_launched'] = end
+        ent['early'] = end < bounds[-1]
+
+    def _capture_pcg(self, pa):
+        """The graphs of _run_pcg for one argument set: the whole sequence in one graph, and the iteration
+        chunks (each storing its stopped flag) with the final decisions and result after each chunk."""
+        L = lib()
+        dev = self.device
+        maxit = int(pa.maxiter)
+        bounds = list(range(0, maxit, PCG_CHUNK)) + [maxit]
+        flags = torch.zeros(max(len(bounds) - 1, 1), dtype=torch.int32, pin_memory=True)
+        dptr = L.ba_host_mapped_ptr(ctypes.c_void_p(flags.data_ptr())) if maxit > PCG_CHUNK else None
+        torch.cuda.synchronize(dev)
+
+        def capture(fn):
             g = torch.cuda.CUDAGraph()
-            torch.cuda.synchronize(self.device)
             with torch.cuda.graph(g):
-                check(lib().ba_pcg_solve(pa, stream_ptr(self.device)))
-            graphs[key] = g
-        g.replay()
+                check(fn(stream_ptr(dev)))
+            return g
+        whole = capture(lambda s: L.ba_pcg_solve(pa, s))
+        if not dptr:
+            return dict(whole=whole, chunks=None, solves=0, early=False)
+        chunks = [capture(lambda s, k=k: L.ba_pcg_solve_range(pa, bounds[k], bounds[k + 1], 0,
+                                                               ctypes.c_void_p(dptr + 4 * k), s))
+                  for k in range(len(bounds) - 1)]
+        fin = {e: capture(lambda s, e=e: L.ba_pcg_solve_range(pa, e, e, 1, None, s)) for e in bounds[1:]}
+        return dict(whole=whole, flags=flags, bounds=bounds, chunks=chunks, fin=fin, solves=0, early=False)
 
     def _add_z_prior(self, z_prior, lay, plan, S_pairs, e_img, dg_img):
         """Tangent-prior terms on the z-coefficient blocks before damping (bs:141-173)."""

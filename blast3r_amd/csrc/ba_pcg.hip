@@ -445,6 +445,12 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
     if (threadIdx.x < PCG_NP) a.partials[PCG_NP * blockIdx.x + threadIdx.x] = threadIdx.x == 0 ? t[0] : t[1];
 }
 
+// the flag "stopped before update n" (read once the launches before it have run) to memory the host reads
+// (pinned host memory: a system-scope store)
+__global__ void k_pcg_stopped(const int32_t* __restrict__ flag, int32_t* out) {
+    if (threadIdx.x == 0) __hip_atomic_store(out, *flag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // result: x if converged else the best iterate
 __global__ void __launch_bounds__(PCG_T) k_pcg_result(ba_pcg_args a) {
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
@@ -478,7 +484,8 @@ int unknown_setup(const ba_pcg_args& a, hipStream_t st) {
 }
 }  // namespace ba
 
-extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
+extern "C" int ba_pcg_solve_range(const ba_pcg_args* args, int32_t it0, int32_t it1, int32_t finish,
+                                  int32_t* stopped_out, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
     const ba_pcg_args& a = *args;
@@ -487,6 +494,7 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(a.n_long >= 0 && a.n_long <= a.n_u && a.long_ptr != nullptr && a.long_idx != nullptr &&
                    (a.n_long == 0 || a.long_u != nullptr) && a.img_part != nullptr,
                "bad long-list unknowns or image partials");
+    BA_REQUIRE(0 <= it0 && it0 <= it1 && it1 <= a.maxiter, "iteration range outside [0, maxiter]");
     if (a.n_u == 0) return BA_OK;
     {
         const void* need[] = {a.umap, a.inv_ptr, a.inv_src, a.leaf, a.row_ptr, a.row_ent, a.pair_i1, a.pair_i2,
@@ -501,26 +509,50 @@ extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
     BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
     const int gw = a.d <= 16 ? 16 : 32;               // lanes per block row group of the SpMV (row_u stride)
     const int per = a.d * a.d > gw ? a.d * a.d : gw;
-    if (n_ent > 0)
-        hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
-                           n_ent, per, gw);
-    hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
+    if (it0 == 0) {                                  // the setup precedes iteration 0
+        if (n_ent > 0)
+            hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
+                               n_ent, per, gw);
+        hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
+    }
     BA_LAUNCHED();
     auto spmv = [&](int it) {
         if (gw == 16) hipLaunchKernelGGL(k_pcg_spmv<16>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
         else          hipLaunchKernelGGL(k_pcg_spmv<32>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
     };
-    for (int it = 0; it < a.maxiter; ++it) {
+    for (int it = it0; it < it1; ++it) {
         spmv(it);
         hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, it);
     }
-    // the decisions after the last update (no SpMV follows them)
-    spmv(a.maxiter);
-    hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);
+    if (finish) {
+        // the decisions after update it1 - 1 (after the last update, or a launch that returns at once once
+        // the loop has stopped), then the result
+        spmv(it1);
+        hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);
+    } else if (stopped_out != nullptr) {
+        hipLaunchKernelGGL(k_pcg_stopped, dim3(1), dim3(64), 0, st, a.istate + IS_DONE0 + (it1 & 1), stopped_out);
+    }
     BA_LAUNCHED();
     return BA_OK;
+}
+
+extern "C" int ba_pcg_solve(const ba_pcg_args* args, void* stream) {
+    return ba_pcg_solve_range(args, 0, args != nullptr ? args->maxiter : 0, 1, nullptr, stream);
+}
+
+// The device address of host memory that the device can reach (pinned, mapped), or NULL: the target that
+// ba_pcg_solve_range's stopped_out needs, checked before any kernel is handed it.
+extern "C" void* ba_host_mapped_ptr(const void* host_ptr) {
+    if (host_ptr == nullptr) return nullptr;
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, host_ptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (at.type != hipMemoryTypeHost || at.devicePointer == nullptr) return nullptr;
+    return at.devicePointer;
 }

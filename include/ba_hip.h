@@ -276,6 +276,18 @@ typedef struct {
  * synchronisation).  The result (the converged iterate, else the best one) is left in x;
  * istate holds the loop's outcome. */
 int ba_pcg_solve(const ba_pcg_args* args, void* stream);
+/* ba_pcg_solve in parts, for a caller that stops launching once the loop has stopped (the reference's loop
+ * checks its stopping rule on the host after every iteration, ba_solver.py:1216-1236; launched in full, the
+ * iterations after the stop return at once but still cost a launch each): the setup when it0 == 0, then
+ * iterations [it0, it1) (0 <= it0 <= it1 <= maxiter); with finish, the decisions after update it1 - 1 and the
+ * result (valid when it1 == maxiter or when the loop has stopped before update it1); else, when stopped_out
+ * is not NULL, a last kernel stores the flag "stopped before update it1" (0 or 1) to *stopped_out with a
+ * system-scope store (pinned host memory).  ba_pcg_solve(a) = ba_pcg_solve_range(a, 0, maxiter, 1, NULL). */
+int ba_pcg_solve_range(const ba_pcg_args* args, int32_t it0, int32_t it1, int32_t finish, int32_t* stopped_out,
+                       void* stream);
+/* The device address of pinned, mapped host memory (hipPointerGetAttributes), or NULL when the device cannot
+ * reach it: the stopped_out target of ba_pcg_solve_range (no counterpart in the reference). */
+void* ba_host_mapped_ptr(const void* host_ptr);
 int64_t ba_pcg_partials_size(int64_t n_u);
 
 /* ------------------------------------------------------------------ reduced system (direct solve) */

@@ -978,6 +978,46 @@ def test_reduced_solve_cholesky_fallback_runs_pcg_and_points_again(cfg, nf, nt):
     assert torch.equal(deltas[0], deltas[1])
 
 
+@pytest.mark.parametrize('cfg,nf,nt,maxiter', [(0, None, None, 300), (2, 30, 1500, 300), (0, 16, 600, 60),
+                                                (0, 8, 300, 20)])
+def test_pcg_chunked_graphs_equal_the_whole_sequence(cfg, nf, nt, maxiter):
+    """The PCG replayed from chunk graphs, where the host stops launching chunks once the loop has stopped
+    (ba_pcg_solve_range, the flag read from pinned memory), gives the bits of the whole launch sequence
+    (ba_pcg_solve, use_graph off): delta and the loop's outcome equal, also on a second solve that replays the
+    captured graphs; where the loop converges early (full config 0) fewer iterations are launched, at most two
+    chunks past the stop."""
+    from blast3r_amd.ba_solver import PCG_CHUNK
+    print(f'pcg chunks cfg {cfg} ({nf} frames, {nt} tracks), maxiter {maxiter}', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    flags = _cfg_flags(p)
+    g = _gpu(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            o['clip_pix_err'], o['huber_delta'])
+    res, err, w = out.view(-1, 3, 3).unbind(dim=1)
+    hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
+    runs = {}
+    for use_graph in (True, False):
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, use_graph=use_graph,
+                               pcg_maxiter=maxiter)
+        J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
+        d1 = gs.solve_delta(J, res, w)
+        d2 = gs.solve_delta(J, res, w)
+        runs[use_graph] = (d1, d2, gs.last['istate'].cpu(), gs.last['pcg_launched'])
+    (c1, c2, c_ist, launched), (w1, w2, w_ist, _) = runs[True], runs[False]
+    k, conv = int(w_ist[2]), int(w_ist[3])
+    print(f'  stopped after {k} iterations (converged {conv}), launched {launched} of {maxiter}', flush=True)
+    assert torch.equal(c1, w1) and torch.equal(c2, w1) and torch.equal(w2, w1)
+    assert torch.equal(c_ist, w_ist)
+    assert k <= launched <= maxiter
+    if conv and k + 2 * PCG_CHUNK < maxiter and maxiter > PCG_CHUNK:
+        assert launched <= k + 2 * PCG_CHUNK
+    if cfg == 0 and nf is None:
+        assert conv == 1 and launched < maxiter
+
+
 _CHOL_CASES = [(0, 8, 300), (1, 32, 400), (2, 30, 1500), (3, 24, 600), (4, 20, 800), (2, 70, 3000)]
 
 
