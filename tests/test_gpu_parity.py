@@ -255,6 +255,26 @@ def test_reduced_system_parity_pairmajor(cfg, nf, nt, kw):
     _check_reduced_system(make_problem(cfg, n_frames=nf, n_tracks=nt, **kw), 'pairmajor')
 
 
+@pytest.mark.parametrize('cfg,path', [(0, 'auto'), (2, 'auto'), (0, 'pairmajor'), (2, 'pairmajor')])
+def test_reduced_system_with_empty_images_and_a_bare_track(cfg, path):
+    """Images with no observations (the first, two inner ones and the last: no image pair, no diagonal block)
+    and a track with none (its point block only the damping): S, rhs and the point blocks against the oracle
+    on both fused paths, and a finite step."""
+    p = make_problem(cfg, n_frames=16, n_tracks=800)
+    cum = p.infos[0].long()
+    img = torch.repeat_interleave(torch.arange(p.n_imgs), torch.diff(torch.cat([cum.new_zeros(1), cum])))
+    keep = (img != 0) & (img != 3) & (img != 4) & (img != p.n_imgs - 1) & (p.pids.long() != 7)
+    p.pids, p.pix2d, p.pix2d_std, p.pix2d_dep = (t[keep] for t in (p.pids, p.pix2d, p.pix2d_std, p.pix2d_dep))
+    infos = p.infos.clone()
+    infos[0] = torch.cumsum(torch.bincount(img[keep], minlength=p.n_imgs), 0).to(infos.dtype)
+    p.infos = infos
+    assert int((torch.bincount(p.pids.long(), minlength=p.n_tracks) == 0).sum()) >= 1
+    print(f'empty images cfg {cfg} {path}: {p.n_obs} obs', flush=True)
+    _check_reduced_system(p, path)
+    _, delta, _ = _gpu_solver(p, path=path, **_cfg_flags(p))
+    assert bool(torch.isfinite(delta).all())
+
+
 def _check_reduced_system(p, path):
     ne, gvec, params, _, _, _ = _oracle_ne(p, **_cfg_flags(p))
     S_ref = osol.dense_schur(ne)
