@@ -215,7 +215,7 @@ def _cfg_flags(p):
     return {k: p.options[k] for k in ('optim_K', 'optim_P') if not p.options.get(k, True)}
 
 
-def _gpu_solver(p, path='auto', **flags):
+def _gpu_solver(p, path='auto', solver='pcg', **flags):
     g = _gpu(p)
     o = opts(p)
     out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
@@ -223,7 +223,7 @@ def _gpu_solver(p, path='auto', **flags):
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
     gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
-                           no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False), path=path)
+                           no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False), path=path, solver=solver)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     fl = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in flags.items()
           if k in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'optim_Z0')}
@@ -259,7 +259,8 @@ def test_reduced_system_parity_pairmajor(cfg, nf, nt, kw):
 def test_reduced_system_with_empty_images_and_a_bare_track(cfg, path):
     """Images with no observations (the first, two inner ones and the last: no image pair, no diagonal block)
     and a track with none (its point block only the damping): S, rhs and the point blocks against the oracle
-    on both fused paths, and a finite step."""
+    on both fused paths, a finite PCG step, and the direct solve (the empty images' blocks hold only their
+    damping) with every pivot positive and the device's system solved to 1e-10."""
     p = make_problem(cfg, n_frames=16, n_tracks=800)
     cum = p.infos[0].long()
     img = torch.repeat_interleave(torch.arange(p.n_imgs), torch.diff(torch.cat([cum.new_zeros(1), cum])))
@@ -272,6 +273,14 @@ def test_reduced_system_with_empty_images_and_a_bare_track(cfg, path):
     print(f'empty images cfg {cfg} {path}: {p.n_obs} obs', flush=True)
     _check_reduced_system(p, path)
     _, delta, _ = _gpu_solver(p, path=path, **_cfg_flags(p))
+    assert bool(torch.isfinite(delta).all())
+    # the direct solve on the same system: the empty images' blocks hold only their damping
+    from tests.step_checks import device_system
+    gs, delta, _ = _gpu_solver(p, path=path, solver='cholesky', **_cfg_flags(p))
+    assert gs.last['direct'] is not None and gs.last['direct']['first_bad_pivot'] is None
+    S_dev, rhs_dev, _ = device_system(gs)
+    x = gs.last['x'][:S_dev.shape[0]].cpu()
+    assert float((S_dev @ x - rhs_dev).norm() / rhs_dev.norm()) <= 1e-10
     assert bool(torch.isfinite(delta).all())
 
 
