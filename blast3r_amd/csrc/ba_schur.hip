@@ -113,7 +113,8 @@ __device__ __forceinline__ void obs_core(const CamF& cp, const float* __restrict
 //   0-2 X_rig | 3-11 Jpr | 12 d r0/d fx | 13 d r1/d fy | 14 zscale | 15-17 W r / sqrt(W)
 //   18 (J_k_f, sqrt(W_0)) | 19 (sqrt(W_1), sqrt(W_2))  as fp32 pairs (both are fp32 values)
 __device__ __forceinline__ void core_store(double* __restrict__ rec, int t, const ObsCore& o) {
-    auto put = [&](int f, double v) { rec[f * BA_CHUNK + t] = v; };
+    // streamed out (the records of a pass exceed every cache; k_schur reads them back after the point pass)
+    auto put = [&](int f, double v) { __builtin_nontemporal_store(v, rec + f * BA_CHUNK + t); };
 #pragma unroll
     for (int k = 0; k < 3; ++k) put(k, o.J.Xr[k]);
 #pragma unroll
@@ -124,12 +125,15 @@ __device__ __forceinline__ void core_store(double* __restrict__ rec, int t, cons
 #pragma unroll
     for (int k = 0; k < 3; ++k) put(15 + k, o.Rs[k]);
     float2* p = reinterpret_cast<float2*>(rec);
-    p[18 * BA_CHUNK + t] = make_float2((float)o.J.jkf, (float)o.sW[0]);
-    p[19 * BA_CHUNK + t] = make_float2((float)o.sW[1], (float)o.sW[2]);
+    const float2 a = make_float2((float)o.J.jkf, (float)o.sW[0]), b = make_float2((float)o.sW[1], (float)o.sW[2]);
+    __builtin_nontemporal_store(__builtin_bit_cast(double, a), reinterpret_cast<double*>(p + 18 * BA_CHUNK + t));
+    __builtin_nontemporal_store(__builtin_bit_cast(double, b), reinterpret_cast<double*>(p + 19 * BA_CHUNK + t));
 }
 
+// NT: non-temporal loads (a record read once from memory, by the back-substitution)
+template <bool NT = false>
 __device__ __forceinline__ void core_load(const double* __restrict__ rec, int t, ObsCore& o) {
-    auto get = [&](int f) { return rec[f * BA_CHUNK + t]; };
+    auto get = [&](int f) { return NT ? __builtin_nontemporal_load(rec + f * BA_CHUNK + t) : rec[f * BA_CHUNK + t]; };
 #pragma unroll
     for (int k = 0; k < 3; ++k) o.J.Xr[k] = get(k);
 #pragma unroll
@@ -139,8 +143,9 @@ __device__ __forceinline__ void core_load(const double* __restrict__ rec, int t,
     o.J.zscale = get(14);
 #pragma unroll
     for (int k = 0; k < 3; ++k) o.Rs[k] = get(15 + k);
-    const float2* p = reinterpret_cast<const float2*>(rec);
-    const float2 a = p[18 * BA_CHUNK + t], b = p[19 * BA_CHUNK + t];
+    const double* p2 = reinterpret_cast<const double*>(reinterpret_cast<const float2*>(rec));
+    const float2 a = __builtin_bit_cast(float2, NT ? __builtin_nontemporal_load(p2 + 18 * BA_CHUNK + t) : p2[18 * BA_CHUNK + t]);
+    const float2 b = __builtin_bit_cast(float2, NT ? __builtin_nontemporal_load(p2 + 19 * BA_CHUNK + t) : p2[19 * BA_CHUNK + t]);
     o.J.jkf = a.x;
     o.sW[0] = a.y; o.sW[1] = b.x; o.sW[2] = b.y;
 }
@@ -887,7 +892,7 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
         ObsCore o;
-        core_load(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
+        core_load<true>(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
         double xs[16];
         if (a.dc_img != nullptr) {                     // image-level copy: one load fewer
@@ -1240,14 +1245,18 @@ __global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
             double Jp[3][3], gP[3];
             point_rows<true>(oc, c.cp, xon, Jp, gP);
             const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
-            double* q = a.pobs + 9 * o;
+            double* q = a.pobs + 9 * o;                // streamed out, as wobs (read by later passes)
 #pragma unroll
             for (int k = 0; k < 6; ++k) {
                 const int i = pr[k][0], j = pr[k][1];
-                q[k] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
+                __builtin_nontemporal_store(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j], q + k);
             }
-            q[6] = gP[0]; q[7] = gP[1]; q[8] = gP[2];
-            reinterpret_cast<float4*>(a.wobs)[o] = make_float4((float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f);
+            __builtin_nontemporal_store(gP[0], q + 6);
+            __builtin_nontemporal_store(gP[1], q + 7);
+            __builtin_nontemporal_store(gP[2], q + 8);
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 wv = {(float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f};
+            __builtin_nontemporal_store(wv, reinterpret_cast<f4*>(a.wobs) + o);
             const bool first = o == 0;
             emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
                                           [&](int j, double v) { X[3 * lane][j] = v; });
@@ -1371,7 +1380,8 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
         T.add_round(X, simg, -1.0, a.vslots, w, lane);
         const int nr = (int)min((int64_t)64, r_end - base);
         double* dst = a.V + base * 3 * DP;
-        for (int e = lane; e < nr * 3 * DP; e += 64) dst[e] = X[e / DP][e % DP];
+        // streamed out (V of a pass exceeds every cache)
+        for (int e = lane; e < nr * 3 * DP; e += 64) __builtin_nontemporal_store(X[e / DP][e % DP], dst + e);
         __syncthreads();
     }
     if (T.img >= 0) T.flush(a.vslots, w, lane);
