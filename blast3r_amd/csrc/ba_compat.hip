@@ -101,12 +101,12 @@ __global__ void __launch_bounds__(RES_T) k_residuals(const int* __restrict__ inf
         if (base + k * RES_T + tid < n_obs) {
             const int64_t i = idx[k];
 #pragma unroll
-            for (int r = 0; r < 3; ++r) out[r * n_obs + i] = o.r[r];
+            for (int r = 0; r < 3; ++r) __builtin_nontemporal_store(o.r[r], out + r * n_obs + i);
             if (hp.pnorm > 0.f) {
 #pragma unroll
                 for (int r = 0; r < 3; ++r) {
-                    out[(3 + r) * n_obs + i] = o.err[r];
-                    out[(6 + r) * n_obs + i] = o.w[r];
+                    __builtin_nontemporal_store(o.err[r], out + (3 + r) * n_obs + i);
+                    __builtin_nontemporal_store(o.w[r], out + (6 + r) * n_obs + i);
                 }
             }
         }
