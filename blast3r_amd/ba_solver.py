@@ -107,8 +107,9 @@ class GaussNewtonSolver:
         self.pcg_maxiter = pcg_maxiter
         self.plan_options = dict(plan_options or {})
         # linearize + Schur: 'batched' (chunk batches, d <= 15, tracks within 13 images and 128
-        # observations, fastest on banded structures), 'pairmajor' (any track length, d <= 32, any
-        # co-visibility), 'auto' (batched where it applies and pays, else pair-major)
+        # observations, fastest on banded structures), 'pairmajor' (any track length, d <= 31, any
+        # co-visibility), 'auto' (batched where it applies and pays, else pair-major); an explicit
+        # 'batched' outside its limits raises instead of switching paths
         if path not in ('auto', 'batched', 'pairmajor'):
             raise ValueError(f'unknown path {path!r}')
         self.path = path
@@ -257,6 +258,9 @@ class GaussNewtonSolver:
         d = 2 * hasK + 6 * hasP + C * hasZ
         lay = dict(d=d, hasK=hasK, hasP=hasP, hasZ=hasZ)
         plan = None
+        if self.path == 'batched' and d > 15:
+            raise ValueError(f"path='batched' takes at most 15 reduced parameters per image (here {d}); "
+                             "use path='pairmajor' or 'auto'")
         if self.path == 'pairmajor' or d > 15:
             return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         try:

@@ -695,7 +695,10 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
 // tracks keep their (first image, last image, id) order, so the batches that close before the first new
 // track's place are the same and only the later ones are planned again; the earlier chunks keep their
 // arrays with observation ids shifted by the new observations inserted before them (shift, per image).
-// On success prev is consumed (destroyed); on failure it is left as it was.
+// On success prev is consumed: the returned plan is prev's object, edited in place.  On failure (nullptr)
+// prev is left exactly as it was and stays appendable: every limit the re-planning can hit is checked
+// before prev is touched (per-track slot need) or before its arrays are written (MFMA entry-list
+// capacity, which emit checks first), and the planning state edited before that point is restored.
 extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_imgs_new, const int32_t* add_pids,
                                 int64_t n_add, int32_t n_tracks_new) {
     g_plan_err.clear();
@@ -752,17 +755,27 @@ extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_im
                      std::to_string(Q->L) + ")";
         return nullptr;
     }
+    // greedy() fails only when one track alone needs more pair slots (all pairs of its images, diagonal
+    // included) than max_slots; the old tracks passed that test when prev was planned
+    if ((int64_t)worst_d * (worst_d + 1) / 2 > Q->max_slots) {
+        g_plan_err = "a single track needs more pair slots than max_slots";
+        return nullptr;
+    }
     // new tracks in (first image, last image, id) order, merged into the old order
     std::vector<int32_t> nord;
     for (int t = 0; t < T_add; ++t) if (nptr[t + 1] > nptr[t]) nord.push_back(T_old + t);
     auto key_new = [&](int32_t t) { return std::make_tuple(mn[t - T_old], mx[t - T_old], t); };
     std::stable_sort(nord.begin(), nord.end(), [&](int32_t x, int32_t y) { return key_new(x) < key_new(y); });
 
-    // ---- from here on prev is consumed
+    // ---- from here on prev's planning state is edited; the undo record below restores it on failure
     Plan* P = Q;
     PlanState& S = P->st;
     const int64_t n_obs_new = P->n_obs + n_add;
     std::vector<int64_t> base_old = S.base;
+    const int64_t n_obs_old = P->n_obs, ncov_old = S.ncov;
+    const std::vector<int32_t> shift_old = P->shift;
+    int64_t stable_old[BA_PLAN_NARRAYS];
+    std::copy(P->stable, P->stable + BA_PLAN_NARRAYS, stable_old);
     S.base.resize(n_imgs_new + 1);
     {
         int64_t acc = 0;
@@ -794,6 +807,31 @@ extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_im
         while (b_star < nb && S.batches[b_star].k1 < kstar) ++b_star;
     }
     const int64_t k_re = b_star < (int)S.batches.size() ? S.batches[b_star].k0 : (int64_t)S.order.size();
+    // undo record: the tails of the planning state that the re-planning from k_re / b_star rewrites
+    const std::vector<int32_t> order_tail(S.order.begin() + kstar, S.order.end());
+    const std::vector<int64_t> oimg_ptr_tail(S.oimg_ptr.begin() + k_re + 1, S.oimg_ptr.end());
+    const std::vector<int32_t> oimg_tail(S.oimg.begin() + S.oimg_ptr[k_re], S.oimg.end());
+    const std::vector<BatchDesc> batch_tail(S.batches.begin() + b_star, S.batches.end());
+    const std::vector<int64_t> o_ch_old = S.o_ch, o_ct_old = S.o_ct, o_sl_old = S.o_sl, o_en_old = S.o_en;
+    auto restore = [&]() {
+        S.base = base_old;
+        S.tptr.resize(T_old + 1);
+        S.tob_img.resize(n_obs_old); S.tob_pos.resize(n_obs_old);
+        S.tmin.resize(T_old); S.tmax.resize(T_old); S.tdist.resize(T_old);
+        S.ncov = ncov_old;
+        S.order.resize(kstar);
+        S.order.insert(S.order.end(), order_tail.begin(), order_tail.end());
+        S.oimg_ptr.resize(k_re + 1);
+        S.oimg_ptr.insert(S.oimg_ptr.end(), oimg_ptr_tail.begin(), oimg_ptr_tail.end());
+        S.oimg.resize(S.oimg_ptr[k_re]);
+        S.oimg.insert(S.oimg.end(), oimg_tail.begin(), oimg_tail.end());
+        S.batches.resize(b_star);
+        S.batches.insert(S.batches.end(), batch_tail.begin(), batch_tail.end());
+        S.o_ch = o_ch_old; S.o_ct = o_ct_old; S.o_sl = o_sl_old; S.o_en = o_en_old;
+        P->n_imgs = n_old; P->n_obs = n_obs_old; P->n_tracks = T_old;
+        P->shift = shift_old;
+        std::copy(stable_old, stable_old + BA_PLAN_NARRAYS, P->stable);
+    };
     {
         std::vector<int32_t> tail;
         tail.reserve(S.order.size() - kstar + nord.size());
@@ -821,7 +859,15 @@ extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_im
     P->stable[BA_PA_B_IMGS] = (int64_t)b_star * P->L;
     P->stable[BA_PA_B_NIMGS] = b_star;
     P->stable[BA_PA_B_POS_SLOT] = (int64_t)b_star * BA_MAX_SLOTS;
+    // emit() writes prev's arrays only once every new batch's entry lists fit; nothing before that
+    // point has touched them
+    if (!greedy(S, k_re, n_imgs_new, P->L, P->max_slots, P->max_batch_obs) || !emit(P, b_star)) {
+        restore();
+        return nullptr;
+    }
     {
+        // the kept chunks' observation ids, in the merged structure's numbering (emit wrote only from
+        // chunk o_ch[b_star] on, so the kept prefix still holds prev's ids)
         auto& co = P->v[BA_PA_CHUNK_OBS];
         auto& ss = P->v[BA_PA_SLOT_SRC];
         const auto& si = P->v[BA_PA_S_IMG];
@@ -833,10 +879,6 @@ extern "C" void* ba_plan_append(void* prev, const int32_t* add_cnt, int32_t n_im
                 if (co[q] >= 0) co[q] += d;
             }
         });
-    }
-    if (!greedy(S, k_re, n_imgs_new, P->L, P->max_slots, P->max_batch_obs) || !emit(P, b_star)) {
-        delete P;        // prev was consumed
-        return nullptr;
     }
     return P;
 }

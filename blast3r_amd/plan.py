@@ -41,7 +41,13 @@ class _HostArrays:
         if name not in self._d:
             pl = self._plan()
             n = pl.sizes[name]
-            self._d[name] = pl._host_view(ARRAYS.index(name), n).copy() if pl._h else pl.dev[name][:n].cpu().numpy()
+            # an append (another thread) edits the host plan in place and then takes it from this plan:
+            # read it under the same lock, or from the device once it is gone
+            arr = None
+            with _append_lock:
+                if pl._h:
+                    arr = pl._host_view(ARRAYS.index(name), n).copy()
+            self._d[name] = arr if arr is not None else pl.dev[name][:n].cpu().numpy()
         return self._d[name]
 
     def __contains__(self, name):
@@ -85,9 +91,10 @@ class BAPlan:
                 h2 = L.ba_plan_append(ctypes.c_void_p(h), add_cnt.ctypes.data_as(ctypes.c_void_p), n_im,
                                       add_pids.ctypes.data_as(ctypes.c_void_p), int(add_pids.shape[0]), int(n_tr))
                 if not h2:
-                    if q:                      # an intermediate plan was consumed already: nothing to keep
+                    # a failed append leaves its input as it was: at q == 0 that is the parent's host plan,
+                    # which stays appendable; later, an intermediate plan that only this chain holds
+                    if q:
                         L.ba_plan_destroy(ctypes.c_void_p(h))
-                        _parent._h = None
                     raise RuntimeError('structure plan failed: ' + (L.ba_plan_last_error() or b'').decode())
                 _parent._h = None if q == 0 else _parent._h       # consumed by ba_plan_append
                 h = h2

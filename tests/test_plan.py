@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from blast3r_amd.plan import BAPlan
+from blast3r_amd.plan import ARRAYS, BAPlan
 from blast3r_amd.synthetic import make_problem
 from oracle import kernels as ok
 from oracle import solver as osol
@@ -624,3 +624,94 @@ def test_plan_append_from_two_threads_consumes_the_parent_once():
     full = BAPlan(infos, pk, Tk, device='cpu')
     for name in full.sizes:
         assert torch.equal(out[0].dev[name], full.dev[name]), name
+
+
+def _append_one_track(infos, pids, T, imgs):
+    """The structure `old | new` where new holds one track (id T) seen once in each of `imgs` (image ids of
+    the merged structure, which has one image more than `infos`): merged infos and pids, add_cnt, add_pids."""
+    cum = infos[0].numpy().astype(np.int64)
+    n = len(cum)
+    cnt_old = np.diff(np.concatenate([[0], cum]))
+    add_cnt = np.zeros(n + 1, dtype=np.int32)
+    add_cnt[list(imgs)] = 1
+    rows, start = [], 0
+    p = pids.numpy()
+    for i in range(n + 1):
+        c = int(cnt_old[i]) if i < n else 0
+        rows.append(p[start:start + c])
+        start += c
+        rows.append(np.full(add_cnt[i], T, dtype=np.int32))
+    nppi = np.concatenate([cnt_old, [0]]) + add_cnt
+    new_infos = torch.stack([torch.from_numpy(np.cumsum(nppi)), torch.arange(n + 1), torch.zeros(n + 1, dtype=torch.long)])
+    new_pids = torch.from_numpy(np.concatenate(rows).astype(np.int32))
+    return new_infos.to(torch.int32), new_pids, T + 1, add_cnt, np.full(len(imgs), T, dtype=np.int32)
+
+
+@pytest.mark.parametrize('cfg,span,kw', [(0, 10, dict(max_slots=40)), (2, 14, {})])
+def test_failing_append_leaves_the_parent_plan_as_it_was(cfg, span, kw):
+    """An append whose new track needs more pair slots than max_slots (10 images: 55 > 40; 14 images at the
+    defaults: 105 > 96) is refused before the parent's host plan is touched: the parent stays appendable, its
+    arrays equal a fresh plan of its structure, a valid append from it afterwards equals a full rebuild, and
+    dropping every plan frees each host plan once."""
+    import gc
+    p = make_problem(cfg, n_frames=20, n_tracks=800)
+    steps = list(_online_steps(p, 2))
+    infos0, pk0, T0 = steps[0][:3]
+    parent = BAPlan(infos0, pk0, T0, device='cpu', **kw)
+    n0 = parent.n_imgs
+    imgs = list(range(n0 + 1 - span, n0 + 1))
+    infos_b, pids_b, T_b, add_cnt, add_pids = _append_one_track(infos0, pk0, T0, imgs)
+    with pytest.raises(RuntimeError, match='pair slots'):
+        BAPlan.appended(parent, infos_b, pids_b, T_b, add_cnt, add_pids)
+    assert parent.appendable
+    fresh = BAPlan(infos0, pk0, T0, device='cpu', **kw)
+    assert parent.scalars == fresh.scalars
+    for name in fresh.sizes:
+        assert np.array_equal(parent._host_view(ARRAYS.index(name), fresh.sizes[name]), fresh.host[name]), name
+    infos, pk, Tk, add = steps[1]
+    child = BAPlan.appended(parent, infos, pk, Tk, add[0], add[1])
+    full = BAPlan(infos, pk, Tk, device='cpu', **kw)
+    assert child.scalars == full.scalars
+    for name in full.sizes:
+        assert torch.equal(child.dev[name], full.dev[name]), name
+        assert np.array_equal(child.host[name], full.host[name]), name
+    del parent, child, full, fresh
+    gc.collect()
+
+
+def test_host_arrays_read_during_an_append_of_the_plan():
+    """A reader of a plan's host arrays (plan.host[...], as the solver's PCG and direct-solve set-up do)
+    while another thread appends to that plan: every read equals the plan's own arrays, whether it runs
+    before the append took the host plan (read from it under the append lock) or after (read from the
+    device arrays, which an append leaves alone)."""
+    import threading
+    from blast3r_amd import plan as bp
+    p = make_problem(2, n_frames=30, n_tracks=1500)
+    seq = list(_online_steps(p, 2))
+    parent = BAPlan(*seq[0][:3], device='cpu')
+    ref = {name: parent.dev[name][:parent.sizes[name]].numpy().copy() for name in ARRAYS}
+    infos, pk, Tk, add = seq[1]
+    stop = threading.Event()
+    bad, reads = [], [0]
+
+    def reader():
+        while not stop.is_set():
+            h = bp._HostArrays(parent)
+            for name in ARRAYS:
+                if not np.array_equal(h[name], ref[name]):
+                    bad.append(name)
+            reads[0] += 1
+
+    t = threading.Thread(target=reader)
+    t.start()
+    child = BAPlan.appended(parent, infos, pk, Tk, add[0], add[1])
+    for _ in range(3):           # a few reads after the parent's host plan is gone
+        n = reads[0]
+        while reads[0] == n:
+            pass
+    stop.set()
+    t.join()
+    assert not bad, bad
+    full = BAPlan(infos, pk, Tk, device='cpu')
+    for name in full.sizes:
+        assert torch.equal(child.dev[name], full.dev[name]), name
