@@ -138,8 +138,9 @@ _SIGS = {
     'ba_jacobians': (c_int, [c_p, c_int, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_int,
                              c_p, c_p, c_p, c_p]),
     'ba_chol3x3_solve': (c_int, [c_p, c_p, c_p, c_i64, c_d, c_int, c_p]),
+    'ba_blockcoo_workspace_size': (c_i64, [c_i64, c_i64]),
     'ba_blockcoo_matvec': (c_int, [c_p, c_int, c_int, c_p, c_p, c_int, c_i64, c_p, c_p, c_i64, c_i64, c_int, c_int,
-                                   c_p]),
+                                   c_p, c_i64, c_p]),
     'ba_einsum_bki_bkj': (c_int, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_int, c_int, c_int, c_int, c_p]),
     'ba_exp_se3': (c_int, [c_p, c_p, c_i64, c_p]),
     'ba_plan_create': (c_p, [c_p, c_int, c_p, c_i64, c_int, c_int, c_int, c_i64]),

@@ -4,6 +4,7 @@
 // These let the reference's own solver run on MI355X unchanged; the fused
 // linearize + Schur path lives in ba_schur.hip.
 #include <hip/hip_runtime.h>
+#include <rocprim/device/device_radix_sort.hpp>
 #include <cmath>
 #include <string>
 
@@ -237,43 +238,147 @@ extern "C" int ba_chol3x3_solve(const void* blocks, const void* rhs, void* out, 
 }
 
 // ----------------------------------------------------------------------------- block-COO matvec
-template <typename T, typename I>
-__global__ void __launch_bounds__(256) k_bcoo(const T* __restrict__ blocks, int bh, int bw, const I* __restrict__ rows,
-                                              const I* __restrict__ cols, int64_t n, const T* __restrict__ x,
-                                              T* __restrict__ y, int transpose) {
-    int per = transpose ? bw : bh;
-    int64_t total = n * per;
-    for (int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tid < total;
-         tid += (int64_t)blockDim.x * gridDim.x) {
-        int64_t bi = tid / per;
-        int lo = (int)(tid - bi * per);
-        int64_t rb = (int64_t)rows[bi], cb = (int64_t)cols[bi];
-        const T* A = blocks + bi * (int64_t)bh * bw;
-        T acc = T(0);
-        if (!transpose) {
-            for (int c = 0; c < bw; ++c) acc += A[lo * bw + c] * x[cb * bw + c];
-            atomicAdd(y + rb * bh + lo, acc);
-        } else {
-            for (int r = 0; r < bh; ++r) acc += A[r * bw + lo] * x[rb * bh + r];
-            atomicAdd(y + cb * bw + lo, acc);
-        }
-    }
+// y = A x (or A^T x) for A given as n (bh x bw) blocks at block positions (row_idx, col_idx), in any order
+// and with repeats.  Output-driven, deterministic and free of atomics:
+//   1. each block's output block index becomes a sort key (an index outside [0, n_out) becomes the
+//      sentinel n_out, which no output reads);
+//   2. the block ids are sorted by key with a stable radix sort over the bits of [0, n_out];
+//   3. seg[k] = first sorted position with key >= k (one thread per sorted position writes the keys
+//      between its predecessor's and its own), so output block k owns the sorted range [seg[k], seg[k+1]);
+//   4. one thread per output element sums its blocks' contributions in ascending block id, then stores y
+//      (every element is written, so no clearing pass).
+// The sum order is fixed by the input, so repeated calls give bit-identical results.
+struct BcooWs {
+    uint32_t *keys_in, *keys_out, *ids_in, *ids_out;
+    int32_t* seg;
+    void* sort_tmp;
+    size_t sort_bytes;
+    int64_t total;
+};
+
+static inline size_t bcoo_align(size_t b) { return (b + 255) & ~(size_t)255; }
+
+static inline unsigned bcoo_bits(int64_t n_out) {
+    unsigned b = 1;
+    while (b < 32 && ((int64_t)1 << b) <= n_out) ++b;      // keys are in [0, n_out]
+    return b;
 }
 
-// Replaces blockcoo_matvec (.cu:1171-1219) for any block shape.  y (out_len) is zero-filled here.
+// layout of the caller's workspace; base == nullptr only sizes it
+static hipError_t bcoo_layout(void* base, int64_t n, int64_t n_out, hipStream_t st, BcooWs& w) {
+    size_t tmp = 0;
+    hipError_t e = rocprim::radix_sort_pairs((void*)nullptr, tmp, (uint32_t*)nullptr, (uint32_t*)nullptr,
+                                             (uint32_t*)nullptr, (uint32_t*)nullptr, (unsigned)n, 0u,
+                                             bcoo_bits(n_out), st);
+    if (e != hipSuccess) return e;
+    const size_t v = bcoo_align((size_t)n * 4);
+    char* p = (char*)base;
+    w.keys_in = (uint32_t*)p; w.keys_out = (uint32_t*)(p + v);
+    w.ids_in = (uint32_t*)(p + 2 * v); w.ids_out = (uint32_t*)(p + 3 * v);
+    w.seg = (int32_t*)(p + 4 * v);
+    const size_t segb = bcoo_align((size_t)(n_out + 1) * 4);
+    w.sort_tmp = p + 4 * v + segb;
+    w.sort_bytes = tmp;
+    w.total = (int64_t)(4 * v + segb + bcoo_align(tmp));
+    return hipSuccess;
+}
+
+template <typename I>
+__global__ void __launch_bounds__(256) k_bcoo_keys(const I* __restrict__ out_idx, int64_t n, int64_t n_out,
+                                                   uint32_t* __restrict__ keys, uint32_t* __restrict__ ids) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t k = (int64_t)out_idx[i];
+    keys[i] = (uint32_t)(k >= 0 && k < n_out ? k : n_out);
+    ids[i] = (uint32_t)i;
+}
+
+__global__ void __launch_bounds__(256) k_bcoo_bounds(const uint32_t* __restrict__ skeys, int64_t n, int64_t n_out,
+                                                     int32_t* __restrict__ seg) {
+    const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s > n) return;
+    const int64_t lo = s ? (int64_t)skeys[s - 1] + 1 : 0;
+    const int64_t hi = s < n ? (int64_t)skeys[s] : n_out;
+    for (int64_t k = lo; k <= hi; ++k) seg[k] = (int32_t)s;
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) k_bcoo_rows(const T* __restrict__ blocks, int bh, int bw,
+                                                   const I* __restrict__ in_idx, int64_t n_in,
+                                                   const uint32_t* __restrict__ sid, const int32_t* __restrict__ seg,
+                                                   int64_t n_out, const T* __restrict__ x, T* __restrict__ y,
+                                                   int transpose) {
+    const int per = transpose ? bw : bh;             // outputs per output block
+    const int len = transpose ? bh : bw;             // inputs per input block
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= n_out * per) return;
+    const int64_t k = o / per;
+    const int e = (int)(o - k * per);
+    // element (e, j) of the block as seen from the output side: A[e][j] or A[j][e]
+    const int es = transpose ? 1 : bw, js = transpose ? bw : 1;
+    T acc = T(0);
+    for (int32_t s = seg[k], s1 = seg[k + 1]; s < s1; ++s) {
+        const int64_t b = sid[s];
+        const int64_t c = (int64_t)in_idx[b];
+        if (c < 0 || c >= n_in) continue;            // the reference reads out of bounds here; skip instead
+        const T* A = blocks + b * (int64_t)bh * bw + (int64_t)e * es;
+        const T* xs = x + c * len;
+        for (int j = 0; j < len; ++j) acc = fma(A[(int64_t)j * js], xs[j], acc);
+    }
+    y[o] = acc;
+}
+
+extern "C" int64_t ba_blockcoo_workspace_size(int64_t n_blocks, int64_t n_out_blocks) {
+    clear_error();
+    if (n_blocks < 0 || n_blocks >= ((int64_t)1 << 31) || n_out_blocks < 0 || n_out_blocks >= ((int64_t)1 << 31)) {
+        set_error("blockcoo_matvec: block counts must be in [0, 2^31)");
+        return -1;
+    }
+    BcooWs w;
+    if (bcoo_layout(nullptr, n_blocks, n_out_blocks, nullptr, w) != hipSuccess) {
+        set_error("blockcoo_matvec: sort workspace query failed");
+        return -1;
+    }
+    return w.total;
+}
+
+// Replaces blockcoo_matvec (.cu:1171-1219) for any block shape; every element of y is written.
 extern "C" int ba_blockcoo_matvec(const void* blocks, int32_t bh, int32_t bw, const void* row_idx, const void* col_idx,
                                   int32_t index_int64, int64_t n_blocks, const void* x, void* y, int64_t HB1,
-                                  int64_t WB1, int32_t transpose, int32_t dtype, void* stream) {
+                                  int64_t WB1, int32_t transpose, int32_t dtype, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
     clear_error();
-    BA_REQUIRE(bh > 0 && bw > 0 && n_blocks >= 0, "bad block shape");
-    int64_t out_len = transpose ? WB1 * bw : HB1 * bh;
-    BA_HIP(hipMemsetAsync(y, 0, out_len * (dtype == 1 ? 8 : 4), S(stream)));
-    if (n_blocks == 0) return BA_OK;
-    int64_t total = n_blocks * (transpose ? bw : bh);
-    unsigned g = nblk(total, 256);
-#define BA_BCOO(T, I) \
-    hipLaunchKernelGGL((k_bcoo<T, I>), dim3(g), dim3(256), 0, S(stream), (const T*)blocks, bh, bw, (const I*)row_idx, \
-                       (const I*)col_idx, n_blocks, (const T*)x, (T*)y, transpose)
+    BA_REQUIRE(bh > 0 && bw > 0 && n_blocks >= 0 && HB1 >= 0 && WB1 >= 0, "bad block shape");
+    BA_REQUIRE(n_blocks < ((int64_t)1 << 31) && HB1 < ((int64_t)1 << 31) && WB1 < ((int64_t)1 << 31),
+               "block counts must be below 2^31");
+    const int64_t n_out = transpose ? WB1 : HB1, n_in = transpose ? HB1 : WB1;
+    const int per = transpose ? bw : bh;
+    if (n_out == 0) return BA_OK;
+    hipStream_t st = S(stream);
+    BcooWs w;
+    BA_HIP(bcoo_layout(workspace, n_blocks, n_out, st, w));
+    BA_REQUIRE(workspace != nullptr && workspace_bytes >= w.total, "workspace too small (ba_blockcoo_workspace_size)");
+    const void* out_idx = transpose ? col_idx : row_idx;
+    const void* in_idx = transpose ? row_idx : col_idx;
+    if (n_blocks > 0) {
+        if (index_int64)
+            hipLaunchKernelGGL(k_bcoo_keys<int64_t>, dim3(nblk(n_blocks, 256)), dim3(256), 0, st,
+                               (const int64_t*)out_idx, n_blocks, n_out, w.keys_in, w.ids_in);
+        else
+            hipLaunchKernelGGL(k_bcoo_keys<int32_t>, dim3(nblk(n_blocks, 256)), dim3(256), 0, st,
+                               (const int32_t*)out_idx, n_blocks, n_out, w.keys_in, w.ids_in);
+        BA_LAUNCHED();
+        size_t tb = w.sort_bytes;
+        BA_HIP(rocprim::radix_sort_pairs(w.sort_tmp, tb, w.keys_in, w.keys_out, w.ids_in, w.ids_out,
+                                         (unsigned)n_blocks, 0u, bcoo_bits(n_out), st));
+    }
+    hipLaunchKernelGGL(k_bcoo_bounds, dim3(nblk(n_blocks + 1, 256)), dim3(256), 0, st, w.keys_out, n_blocks, n_out,
+                       w.seg);
+    BA_LAUNCHED();
+    const unsigned g = nblk(n_out * per, 256);
+#define BA_BCOO(T, I)                                                                                          \
+    hipLaunchKernelGGL((k_bcoo_rows<T, I>), dim3(g), dim3(256), 0, st, (const T*)blocks, bh, bw, (const I*)in_idx, \
+                       n_in, w.ids_out, w.seg, n_out, (const T*)x, (T*)y, transpose)
     if (dtype == 1) { if (index_int64) BA_BCOO(double, int64_t); else BA_BCOO(double, int32_t); }
     else            { if (index_int64) BA_BCOO(float, int64_t);  else BA_BCOO(float, int32_t); }
 #undef BA_BCOO

@@ -127,10 +127,15 @@ def blockcoo_matvec(blocks, row_indices, col_indices, x, HB1, WB1, transpose_blo
     out_len = WB1 * bw if transpose_blocks else HB1 * bh
     _req(x.numel() == in_len, 'x has wrong length for the provided shapes')
     y = torch.empty(out_len, dtype=blocks.dtype, device=blocks.device)
-    check(lib().ba_blockcoo_matvec(ptr(blocks), bh, bw, ptr(row_indices.contiguous()),
-                                   ptr(col_indices.contiguous()), int(row_indices.dtype == torch.int64), N, ptr(x),
-                                   ptr(y), int(HB1), int(WB1), int(bool(transpose_blocks)),
-                                   int(blocks.dtype == torch.float64), stream_ptr(blocks.device)))
+    L = lib()
+    nbytes = L.ba_blockcoo_workspace_size(N, int(WB1 if transpose_blocks else HB1))
+    if nbytes < 0:
+        raise RuntimeError(L.ba_last_error().decode())
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=blocks.device)
+    check(L.ba_blockcoo_matvec(ptr(blocks), bh, bw, ptr(row_indices.contiguous()),
+                               ptr(col_indices.contiguous()), int(row_indices.dtype == torch.int64), N, ptr(x),
+                               ptr(y), int(HB1), int(WB1), int(bool(transpose_blocks)),
+                               int(blocks.dtype == torch.float64), ptr(ws), int(nbytes), stream_ptr(blocks.device)))
     return y
 
 

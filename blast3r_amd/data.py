@@ -64,6 +64,31 @@ class RigsData:
     def update(self, **updates):
         return RigsData(**dict(vars(self), **updates))
 
+    def __getitem__(self, idx):
+        """rigs.py:96-107 (int index): frame idx alone, one camera and one node, every tensor a view of
+        this object's rows (camera cam_ids[idx], image idx, node nod_ids[idx]), so that writing the result
+        of a one-frame bundle adjustment into it (rigs[:] = ..., __setitem__) updates this object."""
+        if not isinstance(idx, int):
+            raise TypeError('RigsData takes an int index here (one frame)')
+        c, n = int(self.cam_ids[idx]), int(self.nod_ids[idx])
+        zero = torch.zeros_like(self.cam_ids[:1])
+        zc = self.z_coefs[idx:idx + 1] if self.z_coefs is not None and idx < len(self.z_coefs) else None
+        return RigsData(1, zero, self.K[c:c + 1], self.P_rig2cam[c:c + 1], self.scale[idx:idx + 1], zc,
+                        self.depth_mode, 1, zero.clone(), self.P_w2rig[n:n + 1])
+
+    def __setitem__(self, idx, rigs):
+        """rigs.py:121-129 (full slice): every tensor field of `rigs` copied into this object's own; z_coefs
+        into its leading columns (a bundle adjustment may have narrowed them)."""
+        if idx != slice(None):
+            raise TypeError('RigsData assignment takes rigs[:] = other here')
+        for key, new in vars(rigs).items():
+            if isinstance(new, torch.Tensor):
+                dst = getattr(self, key)
+                if key == 'z_coefs':
+                    dst[:, :new.shape[1]] = new
+                else:
+                    dst[:] = new
+
     def z_coefs_from_scale(self, tracks):
         """rigs.py:69-94."""
         if self.z_coefs is None:

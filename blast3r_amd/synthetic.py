@@ -299,10 +299,14 @@ def _sample_tracks(rng, cfg, P, f_img, T, mmin, mmax, neigh=None):
 
 
 def make_problem(cfg=0, n_frames=None, n_tracks=None, seed=None, huber_delta=2.0, dtype=torch.float32,
-                 n_channels=None, track_len=None):
+                 n_channels=None, track_len=None, depth_mode='log'):
     """Build one benchmark configuration (optionally scaled down in frames/tracks).  n_channels (K_F,
     giving C = K_F + 1 z-coefficients) and track_len (min, max images per track) override the
-    configuration's own values, for the wide and long-track cases of the tests."""
+    configuration's own values, for the wide and long-track cases of the tests.  depth_mode='lin'
+    gives linear depth channels (the reference's 'lin' mode, r2 = fbar log(g / z), which has no ones
+    channel, multidepth.py:53-54): channel 0 the depth (for config 4 with the per-frame error applied
+    in log space), the others the random fields, with the same C columns."""
+    assert depth_mode in ('log', 'lin')
     spec = dict(_SPEC[cfg])
     if n_channels is not None:
         spec['KF'] = int(n_channels)
@@ -343,16 +347,21 @@ def make_problem(cfg=0, n_frames=None, n_tracks=None, seed=None, huber_delta=2.0
 
     KF = spec['KF']
     C = KF + 1
-    fields = _FieldBank(rng, F, KF - 1)
+    fields = _FieldBank(rng, F, KF - 1 + (depth_mode == 'lin'))     # lin: no ones channel, one more field
     dep = np.zeros((N, C), dtype=np.float32)
     logz = np.log(np.maximum(z, 1e-6))
     if cfg == 4:
         a = rng.normal(1.0, 0.1, F)
         b = rng.normal(0.0, 0.2, F)
         logz = a[frames] * logz + b[frames]
-    dep[:, 0] = logz
-    dep[:, 1] = 1.0
-    dep[:, 2:] = fields.sample(frames, np.clip(pix, 0, [W_IMG - 1e-3, H_IMG - 1e-3]))
+    smp = fields.sample(frames, np.clip(pix, 0, [W_IMG - 1e-3, H_IMG - 1e-3]))
+    if depth_mode == 'log':
+        dep[:, 0] = logz
+        dep[:, 1] = 1.0
+        dep[:, 2:] = smp
+    else:
+        dep[:, 0] = np.exp(logz)
+        dep[:, 1:] = smp
 
     nppi = np.bincount(frames, minlength=F)
     n_cams = 1 if spec['mono'] else F
@@ -383,7 +392,7 @@ def make_problem(cfg=0, n_frames=None, n_tracks=None, seed=None, huber_delta=2.0
     t32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
     options = dict(weight_z=(1.0 if cfg == 4 else 1e-4), huber_delta=huber_delta, pnorm=1.0,
                    clip_pix_err=100.0, optim_K=not fixed_cams, optim_P=not fixed_cams, optim_Z=True,
-                   optim_X=True, depth_mode='log')
+                   optim_X=True, depth_mode=depth_mode)
     truth = dict(P_w2rig=t32(P), pts3d=t32(X), f=t32(f_cam), frames=torch.from_numpy(frames.astype(np.int64)))
     return BAProblem(cfg=cfg,
                      infos=torch.from_numpy(infos),

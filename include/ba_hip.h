@@ -54,10 +54,15 @@ int ba_jacobians(const int32_t* infos, int32_t n_imgs, const float* K, const flo
 int ba_chol3x3_solve(const void* blocks, const void* rhs, void* out, int64_t n, double jitter, int32_t dtype,
                      void* stream);
 
-/* blockcoo_matvec (sfm_jacobian_rigs.cu:1171-1219); any (bh, bw); y is zero-filled by the call. */
+/* blockcoo_matvec (sfm_jacobian_rigs.cu:1171-1219); any (bh, bw); every element of y is written.  Blocks may
+ * come in any order and repeat; each output element sums its blocks in ascending block order (stable radix
+ * sort of the block ids by output block, then one thread per output element), so the result is
+ * deterministic.  Block indices outside [0, HB1) / [0, WB1) are ignored.  workspace: at least
+ * ba_blockcoo_workspace_size(n_blocks, transpose ? WB1 : HB1) bytes of device memory, 256-byte aligned. */
+int64_t ba_blockcoo_workspace_size(int64_t n_blocks, int64_t n_out_blocks);
 int ba_blockcoo_matvec(const void* blocks, int32_t bh, int32_t bw, const void* row_idx, const void* col_idx,
                        int32_t index_int64, int64_t n_blocks, const void* x, void* y, int64_t HB1, int64_t WB1,
-                       int32_t transpose, int32_t dtype, void* stream);
+                       int32_t transpose, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* fused_einsum_bki_bkj (sfm_jacobian_rigs.cu:1222-1250); any (I, J, K), strides in elements. */
 int ba_einsum_bki_bkj(const void* left, int64_t l_bs, int64_t l_ks, const void* right, int64_t r_bs, int64_t r_ks,

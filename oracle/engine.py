@@ -34,6 +34,13 @@ def update_K(K0, delta_focal, min_f=100):
     return K
 
 
+def apply_update(K, P_w2rig, z_coefs, pts3d, dK, dP, dZ, dX, scale=1.0):
+    """en:310-313: the parameters after a step of `scale` times delta: f -= dK (clipped, en:347-354),
+    P <- exp(-dP^) P (cujac/__init__.py:56-58, a left update), z -= dZ, X -= dX."""
+    return dict(K=update_K(K, dK * scale), P_w2rig=K_.exp_se3(-(dP * scale)) @ P_w2rig,
+                z_coefs=z_coefs - dZ * scale, pts3d=pts3d - dX * scale)
+
+
 def reproj_score(res):
     """Mean of the lowest 80% of ||r[:, :2]|| (en:357-361)."""
     e = res[:, :2].norm(dim=-1).sort().values
@@ -145,8 +152,7 @@ def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_co
                                                solver=solver, pcg_tol=pcg_tol, pcg_maxiter=pcg_maxiter,
                                                z_prior=z_prior)
     def trial(scale):
-        update = dict(K=update_K(K, dK * scale), P_w2rig=K_.exp_se3(-(dP * scale)) @ P_w2rig,
-                      z_coefs=z_coefs - dZ * scale, pts3d=pts3d - dX * scale)
+        update = apply_update(K, P_w2rig, z_coefs, pts3d, dK, dP, dZ, dX, scale)
         new_loss, new_residuals, _ = obj(**update)
         return new_loss, reproj_score(new_residuals), (update, new_residuals)
 

@@ -21,11 +21,12 @@ def oracle_system(inp, hp, flags, z_prior=None, extra_loss=None):
     """The oracle's objective and damped normal equations at one LM step's inputs (CPU tensors).
     z_prior (H_z, g_z) is added to the z-coefficient blocks (bs:141-173); extra_loss(z_coefs), when
     given, is added to the objective (the tangent prior's loss, en:270-277)."""
+    lg = hp.get('is_depth_log', True)
     loss, res, w = oeng.objective(inp['rigs'], inp['K'], inp['P_rig2cam'], inp['P_w2rig'], inp['z_coefs'],
-                                  inp['pts3d'], inp['pids'], inp['pix2d'], inp['pix2d_std'], inp['pix2d_dep'], True,
+                                  inp['pts3d'], inp['pids'], inp['pix2d'], inp['pix2d_std'], inp['pix2d_dep'], lg,
                                   hp['weight_z'], hp['pnorm'], hp['clip_pix_err'], hp['huber_delta'])
     Jc, Jz, Jp = ok.jacobians_with_rigs(inp['rigs'], inp['K'], inp['P_rig2cam'], inp['P_w2rig'], inp['z_coefs'],
-                                        inp['pts3d'], inp['pids'], inp['pix2d_std'], inp['pix2d_dep'], True,
+                                        inp['pts3d'], inp['pids'], inp['pix2d_std'], inp['pix2d_dep'], lg,
                                         float64=True)
     if not flags.get('optim_Z0', True):
         Jz[:, 0, 0] = 0
@@ -163,11 +164,11 @@ def check_line_search(inp, hp, sysd, delta, dev_info, st_g, up_g, min_reproj=0.0
     K, P, Z, X = inp['K'], inp['P_w2rig'], inp['z_coefs'], inp['pts3d']
 
     def trial(scale):
-        up = dict(K=oeng.update_K(K, dK * scale), P_w2rig=ok.exp_se3(-(dP * scale)) @ P, z_coefs=Z - dZ * scale,
-                  pts3d=X - dX * scale)
+        up = oeng.apply_update(K, P, Z, X, dK, dP, dZ, dX, scale)
         loss, res, _ = oeng.objective(inp['rigs'], up['K'], inp['P_rig2cam'], up['P_w2rig'], up['z_coefs'],
-                                      up['pts3d'], inp['pids'], inp['pix2d'], inp['pix2d_std'], inp['pix2d_dep'], True,
-                                      hp['weight_z'], hp['pnorm'], hp['clip_pix_err'], hp['huber_delta'])
+                                      up['pts3d'], inp['pids'], inp['pix2d'], inp['pix2d_std'], inp['pix2d_dep'],
+                                      hp.get('is_depth_log', True), hp['weight_z'], hp['pnorm'], hp['clip_pix_err'],
+                                      hp['huber_delta'])
         if extra_loss is not None:
             loss = loss + extra_loss(up['z_coefs'])
         return loss, oeng.reproj_score(res), up

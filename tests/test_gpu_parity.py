@@ -165,6 +165,48 @@ def test_jacobians_parity(float64):
         assert rel_err(a, b) < tol
 
 
+def test_lin_depth_mode_residuals_and_jacobians():
+    """depth_mode='lin' (r2 = fbar log(g / z), .cu:238; its Jacobian rows .cu:497-499): residuals, Huber
+    errors and weights (fp32, 1e-5) and the Jacobian blocks in fp64 (1e-9) and fp32 (1e-5) against the
+    oracle, on linear depth channels with no ones channel."""
+    p = make_problem(0, n_frames=10, n_tracks=500, depth_mode='lin')
+    g = _gpu(p)
+    o = opts(p)
+    out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d,
+                                            g.pix2d_std, g.pix2d_dep, False, o['weight_z'], 1.0, o['clip_pix_err'],
+                                            o['huber_delta'])
+    ref = ok.residuals_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                 p.pix2d_std, p.pix2d_dep, False, o['weight_z'], 1.0, o['clip_pix_err'],
+                                 o['huber_delta'])
+    assert bool(ref[:, 2].abs().gt(0).any())
+    for k in range(3):
+        assert rel_err(out[:, 3 * k:3 * k + 3].cpu(), ref[:, 3 * k:3 * k + 3]) < 1e-5, k
+    for f64, tol in ((True, 1e-9), (False, 1e-5)):
+        Jg = cujac.compute_jacobians_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
+                                               g.pix2d_std, g.pix2d_dep, False, float64=f64)
+        Jr = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d_std,
+                                    p.pix2d_dep, False, float64=f64)
+        for a, b in zip(Jg, Jr):
+            assert a.dtype == b.dtype and a.shape == b.shape
+            assert rel_err(a.cpu(), b) < tol, f64
+
+
+@pytest.mark.parametrize('cfg,nf,nt,path', [(0, 8, 200, 'auto'), (2, 24, 800, 'auto'), (2, 24, 800, 'pairmajor'),
+                                            (4, 12, 300, 'auto'), (3, 24, 600, 'pairmajor')])
+def test_reduced_system_parity_lin(cfg, nf, nt, path):
+    """The fused linearize + Schur pass in depth_mode='lin' (both paths) against the oracle's damped
+    reduced system, rhs and point blocks (1e-5)."""
+    print(f'lin reduced system cfg {cfg} {path}', flush=True)
+    _check_reduced_system(make_problem(cfg, n_frames=nf, n_tracks=nt, depth_mode='lin'), path)
+
+
+@pytest.mark.parametrize('cfg,nf,nt,path', [(0, 8, 300, 'auto'), (2, 30, 1500, 'auto'), (3, 24, 600, 'auto')])
+def test_lm_step_parity_lin(cfg, nf, nt, path):
+    """lm_step(depth_mode='lin') against the oracle with the bars of test_lm_step_parity."""
+    print(f'lin lm_step parity cfg {cfg}', flush=True)
+    _check_lm_step(make_problem(cfg, n_frames=nf, n_tracks=nt, depth_mode='lin'), cfg + 40, dict(path=path))
+
+
 def test_compat_ops():
     torch.manual_seed(0)
     # chol3x3_solve
@@ -194,14 +236,59 @@ def test_compat_ops():
     xi[:4, :3] *= 1e-6
     assert rel_err(cujac.exp_se3(xi.to(DEV)), ok.exp_se3(xi)) < 1e-6
 
+@pytest.mark.parametrize('bh,bw', [(3, 6), (3, 5), (6, 6), (17, 2)])
+def test_blockcoo_matvec_sorted_segments(bh, bw):
+    """ba_blockcoo_matvec (.cu:1171-1219 semantics) on 20k blocks in random order with repeats over 300 x 40
+    block positions: equal to the oracle's dense product in both orientations and index dtypes (fp64 1e-12,
+    fp32 1e-5); bit-identical over repeated calls (each output sums its blocks in ascending block order);
+    output blocks that no block touches are exactly zero; an empty block list gives a zero vector; block
+    indices outside the matrix are ignored (the reference would read or write out of bounds)."""
+    g = torch.Generator().manual_seed(bh * 100 + bw)
+    HB1, WB1, n = 300, 40, 20000
+    rows = torch.randint(0, HB1 - 7, (n,), generator=g)          # the last 7 block rows stay empty
+    cols = torch.randint(0, WB1, (n,), generator=g)
+    blocks = torch.randn(n, bh, bw, generator=g, dtype=torch.float64)
+    for dt, tol in ((torch.float64, 1e-12), (torch.float32, 1e-5)):
+        for idt in (torch.int32, torch.int64):
+            for tr in (False, True):
+                x = torch.randn(HB1 * bh if tr else WB1 * bw, generator=g, dtype=torch.float64)
+                args = (blocks.to(DEV, dt), rows.to(DEV, idt), cols.to(DEV, idt), x.to(DEV, dt), HB1, WB1, tr)
+                y = cujac.blockcoo_matvec(*args)
+                yr = ok.blockcoo_matvec(blocks, rows, cols, x, HB1, WB1, tr)
+                assert rel_err(y.double(), yr) < tol, (dt, idt, tr)
+                assert torch.equal(cujac.blockcoo_matvec(*args), y)
+                if not tr:
+                    assert not y.view(HB1, bh)[HB1 - 7:].any()
+    # empty block list
+    x = torch.randn(WB1 * bw, dtype=torch.float64)
+    y0 = cujac.blockcoo_matvec(blocks[:0].to(DEV), rows[:0].to(DEV), cols[:0].to(DEV), x.to(DEV), HB1, WB1, False)
+    assert y0.shape == (HB1 * bh,) and not y0.any()
+    # out-of-range block indices are skipped, the rest is summed as usual
+    bad_r, bad_c = rows.clone(), cols.clone()
+    bad_r[:50] = HB1 + 3
+    bad_r[50:100] = -1
+    bad_c[100:150] = WB1
+    keep = torch.ones(n, dtype=torch.bool)
+    keep[:150] = False
+    for tr in (False, True):
+        x = torch.randn(HB1 * bh if tr else WB1 * bw, generator=g, dtype=torch.float64)
+        y = cujac.blockcoo_matvec(blocks.to(DEV), bad_r.to(DEV), bad_c.to(DEV), x.to(DEV), HB1, WB1, tr)
+        yr = ok.blockcoo_matvec(blocks[keep], rows[keep], cols[keep], x, HB1, WB1, tr)
+        assert rel_err(y, yr) < 1e-12, tr
+
+
+
+def _is_log(p):
+    return p.options.get('depth_mode', 'log') == 'log'
+
 
 def _oracle_ne(p, **flags):
     o = opts(p)
     loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
-                                  p.pix2d_std, p.pix2d_dep, True, o['weight_z'], 1.0, o['clip_pix_err'],
+                                  p.pix2d_std, p.pix2d_dep, _is_log(p), o['weight_z'], 1.0, o['clip_pix_err'],
                                   o['huber_delta'])
     Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
-                                        p.pix2d_std, p.pix2d_dep, True, float64=True)
+                                        p.pix2d_std, p.pix2d_dep, _is_log(p), float64=True)
     if not flags.get('optim_Z0', True):
         Jz[:, 0, 0] = 0
     prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
@@ -219,7 +306,7 @@ def _gpu_solver(p, path='auto', solver='pcg', **flags):
     g = _gpu(p)
     o = opts(p)
     out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
-                                            g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
+                                            g.pix2d, g.pix2d_std, g.pix2d_dep, _is_log(p), o['weight_z'], 1.0,
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
     gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
@@ -228,7 +315,7 @@ def _gpu_solver(p, path='auto', solver='pcg', **flags):
     fl = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in flags.items()
           if k in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'optim_Z0')}
     J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
-                             g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **fl)
+                             g.pix2d_dep, _is_log(p), pix2d=g.pix2d, hp=hp, **fl)
     delta = gs.solve_delta(J, res, w)
     return gs, delta, g
 
@@ -602,8 +689,9 @@ def test_lm_step_direct_solve_parity(cfg, nf, nt):
 def _check_lm_step(p, cfg, solver_kw):
     o = p.options
     kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
-              optim_P=o['optim_P'], **solver_kw)
-    hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
+              optim_P=o['optim_P'], depth_mode=o['depth_mode'], **solver_kw)
+    hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100,
+              is_depth_log=_is_log(p))
     g = _gpu(p)
     info = {}
     up_g, st_g, _ = gpu_engine._lm_step(**g.lm_inputs(), **kw, info=info)
@@ -720,6 +808,71 @@ def _check_bundle_adjustment(p, cfg, n_zcfs, monkeypatch, paths=None):
     last = [s for s in steps if not bool(s[3][1].new_loss >= s[3][1].init_loss)][-1][3][0]
     for key, got in (('K', rig_out.K), ('P_w2rig', rig_out.P_w2rig), ('z_coefs', rig_out.z_coefs), ('pts3d', X_out)):
         assert torch.equal(got, last[key]), key
+
+
+@pytest.mark.parametrize('cfg,nf,nt,q', [(0, 8, 300, 5), (2, 20, 600, 12), (3, 20, 500, 7)])
+def test_frozen_single_image_bundle_adjustment(cfg, nf, nt, q, monkeypatch):
+    """The online pipeline's per-frame BA (pipeline.py:219-224): bundle_adjustment of frame q alone
+    (rigs[q], one camera and node), over the tracks seen in it restricted to that frame (tracks[q]), with
+    the points frozen (optim_X=False) and the focal frozen for a shared camera (optim_K=not mono_cam), in
+    one phase (max_n_phases=1): every lm_step it takes is replayed against the oracle (initial loss, step
+    delta, the oracle's line search on that delta), and the result written back through rigs[q][:] lands
+    in frame q's rows only."""
+    print(f'frozen single-image BA cfg {cfg} frame {q}', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    rig, trk, X = _ba_inputs(p, DEV)
+    # the pipeline's new tracks: those seen in frame q, renumbered (tracks.py:116-127), then frame q alone
+    seen = torch.zeros(p.n_tracks, dtype=torch.bool)
+    seen[trk[q].pids.long().cpu()] = True
+    new_trk, keep = trk.remove(torch.nonzero(~seen).squeeze(1).to(DEV))
+    X_new = X[keep.long()]
+    q_trk = new_trk[q]
+    assert q_trk.n_kpts == new_trk.n_tracks
+    mono = rig.n_cams == 1
+    before = {k: getattr(rig, k).clone() for k in ('K', 'P_w2rig', 'z_coefs')}
+    steps = []
+    real = gpu_engine._lm_step
+
+    def spy(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d, **k):
+        inp = _cpu_inputs(dict(rigs=rigs, pids=pids, pix2d=pix2d, pix2d_std=pix2d_std, pix2d_dep=pix2d_dep, K=K,
+                               P_rig2cam=P_rig2cam, P_w2rig=P_w2rig, z_coefs=z_coefs, pts3d=pts3d))
+        info = {}
+        out = real(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d, info=info, **k)
+        info['reduced'] = device_system(info['solver'])
+        steps.append((inp, dict(k), info, out))
+        return out
+
+    monkeypatch.setattr(gpu_engine, '_lm_step', spy)
+    q_rig = rig[q]
+    out_rig, _ = gpu_engine.bundle_adjustment(q_rig, q_trk, X_new, optim_X=False, optim_K=not mono, max_iters=4,
+                                              max_n_phases=1, pnorm=1.0, weight_z=o['weight_z'],
+                                              huber_delta=o['huber_delta'], verbose=False)
+    q_rig[:] = out_rig
+    assert len(steps) >= 1
+    accepted = 0
+    for n, (inp, k, info, (up_g, st_g, _)) in enumerate(steps):
+        assert inp['rigs'].shape == (3, 1) and not k['optim_X']
+        hp = dict(weight_z=k['weight_z'], huber_delta=k.get('huber_delta', o['huber_delta']), pnorm=k['pnorm'],
+                  clip_pix_err=k.get('clip_pix_err', 100))
+        flags = {f: k[f] for f in ('optim_K', 'optim_P', 'optim_Z', 'optim_X', 'optim_Z0')}
+        flags['no_grad_f_from_rz'] = k.get('no_grad_f_from_rz', False)
+        sysd = _oracle_system(inp, hp, flags)
+        assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-5 * abs(float(sysd['loss'])), n
+        _check_step_delta(sysd, info['delta'], info['pcg_istate'].cpu(), seed=300 + 10 * cfg + n,
+                          reduced=info['reduced'])
+        ls = _check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g)
+        stop = not bool(ls['new_loss'] < ls['init_loss'])
+        assert stop == bool(st_g.new_loss >= st_g.init_loss), n
+        accepted += not stop
+    assert accepted >= 1
+    # written back into frame q's rows of the full rig data only
+    node, cam = int(rig.nod_ids[q]), int(rig.cam_ids[q])
+    others = torch.arange(p.n_imgs) != q
+    assert torch.equal(rig.z_coefs[others.to(DEV)], before['z_coefs'][others.to(DEV)])
+    assert not torch.equal(rig.P_w2rig[node], before['P_w2rig'][node])
+    assert torch.equal(rig.P_w2rig[torch.arange(len(rig.P_w2rig)) != node], before['P_w2rig'][torch.arange(len(rig.P_w2rig)) != node])
+    assert torch.equal(rig.K[cam], before['K'][cam]) if mono else True
 
 
 def test_objective_reproj_exact():
@@ -888,21 +1041,27 @@ def test_backsubstitute_image_level_delta_matches_unknown_map():
         assert outs[0].abs().sum() > 0
 
 
-@pytest.mark.parametrize('cfg,path', [(2, 'auto'), (2, 'pairmajor'), (3, 'auto')])
+_FULL_SIZE = {1: (256, 200_000), 2: (1024, 1_000_000), 3: (4096, 3_000_000), 4: (1024, 1_000_000)}
+
+
+@pytest.mark.parametrize('cfg,path', [(2, 'auto'), (2, 'pairmajor'), (3, 'auto'), (1, 'auto'), (4, 'auto')])
 def test_reduced_system_full_size_against_oracle(cfg, path):
-    """Full benchmark sizes (config 2: 1024 frames, 1 M tracks, 8.0 M observations, on the batched
-    and the pair-major path; config 3: 4096 frames with a camera each, 3 M tracks on random
-    neighbours, 22.5 M observations, where the pair-major path is chosen): the reduced rhs, the
-    point blocks and S v for seeded v against the oracle's normal equations at the same size (the
-    oracle's pass takes seconds on the host's threads), to the 1e-5 bar."""
+    """Full benchmark sizes (config 1: 256 frames, 200 k tracks on 24-frame neighbourhoods, 1.3 M
+    observations, pair-major; config 2: 1024 frames, 1 M tracks, 8.0 M observations, on the batched and
+    the pair-major path; config 3: 4096 frames with a camera each, 3 M tracks on random neighbours,
+    22.5 M observations, pair-major; config 4: config 2's scene with 9 depth channels, focal and poses
+    fixed, 8.0 M observations, batched): the reduced rhs, the point blocks and S v for seeded v against
+    the oracle's normal equations at the same size and with the configuration's own flags (the oracle's
+    pass takes seconds on the host's threads), to the 1e-5 bar."""
     import os
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     p = make_problem(cfg)
-    assert (p.n_imgs, p.n_tracks) == ((1024, 1_000_000) if cfg == 2 else (4096, 3_000_000))
+    assert (p.n_imgs, p.n_tracks) == _FULL_SIZE[cfg]
     print(f'[full cfg{cfg} {path}] {p.n_obs} observations', flush=True)
-    gs, _, _ = _gpu_solver(p, path=path)
+    flags = _cfg_flags(p)
+    gs, _, _ = _gpu_solver(p, path=path, **flags)
     last = gs.last
-    assert last['path'] == ('batched' if (cfg, path) == (2, 'auto') else 'pairmajor')
+    assert last['path'] == ('batched' if (cfg, path) in ((2, 'auto'), (4, 'auto')) else 'pairmajor')
     um, d, plan = last['unknowns'], last['lay']['d'], last['plan']
     rhs = last['rhs'].cpu()
     H = gs.point_blocks()[0].cpu()
@@ -926,7 +1085,7 @@ def test_reduced_system_full_size_against_oracle(cfg, path):
         y.index_add_(0, umap[valid], y_img[valid])
         return (y + last['damp'] * v).cpu()
 
-    ne, gvec, _, _, _, _ = _oracle_ne(p)
+    ne, gvec, _, _, _, _ = _oracle_ne(p, **flags)
     print(f'[full cfg{cfg}] oracle normal equations built', flush=True)
     assert rel_err(rhs, osol.reduced_rhs(ne, gvec)) < 1e-5
     Hr = ne.leaves['pts'] - float(last['lam_p'].cpu()) * torch.eye(3, dtype=torch.float64)

@@ -126,6 +126,24 @@ def test_jacobians_match_autodiff():
     assert rel_err(Jc[:, 2, :2], af[:, 2]) < 1e-7                      # fp32-rounded column
 
 
+def test_jacobians_match_autodiff_lin_mode():
+    """depth_mode='lin' (.cu:481-501): r2 = fbar ln(g / z) has true derivatives fbar dep_c / g in the
+    z-coefficients and (1/2) ln(g / z) in each focal (held in fp32 by the reference, the same quirk as
+    in log mode), so every block equals torch.func derivatives of the independent fp64 residual."""
+    from blast3r_amd.synthetic import make_problem
+    p = make_problem(0, n_frames=6, n_tracks=50, depth_mode='lin')
+    Jc, Jz, Jp = ok.jacobians_with_rigs(*_jac_inputs(p), False, float64=True)
+    af, at, az, ax = od.autodiff_jacobians(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
+                                           p.pix2d_std, p.pix2d_dep, False)
+    g_pos = (p.z_coefs[ok.obs_to_img(p.infos, len(p.pids))] * p.pix2d_dep).sum(1) > 0
+    assert bool(g_pos.all())
+    assert rel_err(Jp, ax) < 1e-12
+    assert rel_err(Jc[:, :, 2:], at) < 1e-12
+    assert rel_err(Jz[:, 0], az[:, 2]) < 1e-12 and torch.count_nonzero(az[:, :2]) == 0
+    assert rel_err(Jc[:, :2, :2], af[:, :2]) < 1e-12
+    assert rel_err(Jc[:, 2, :2], af[:, 2]) < 1e-6                      # fp32-rounded column
+
+
 def test_jacobian_focal_gate_for_negative_guidance():
     """J_k_f = 0 when g <= 0 even though the true derivative is not (reference quirk, .cu:481-489)."""
     p = tiny_problem(0, n_frames=5, n_tracks=30)
@@ -312,6 +330,89 @@ def test_oracle_lm_step_decreases_loss_and_follows_schedule():
     up, st, info = oe.lm_step(**p.lm_inputs(), weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'])
     assert float(st.new_loss) < float(st.init_loss)
     assert info['scale'] in [1.0, 0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0.0]
+
+
+def _residuals_fp64(p, K, P_w2rig, z_coefs, pts3d):
+    """Every observation's three residuals in fp64 from the independent model equations
+    (oracle/dense.py residual_fp64, pinned against the oracle's fp32 residual) at the given parameters."""
+    from torch.func import vmap
+    d = torch.float64
+    n = len(p.pids)
+    img = ok.obs_to_img(p.infos, n)
+    node, cam = p.infos[1].long()[img], p.infos[2].long()[img]
+    Kc = K.to(d)[cam]
+    fxy = torch.stack([Kc[:, 0, 0], Kc[:, 1, 1]], 1)
+    f = lambda a, b, c, e, *rest: od.residual_fp64(a, b, c, e, *rest, is_depth_log=True)
+    return vmap(f)(fxy, torch.zeros((n, 6), dtype=d), z_coefs.to(d)[img], pts3d.to(d)[p.pids.long()],
+                   Kc[:, 0, 2], Kc[:, 1, 2], P_w2rig.to(d)[node], p.P_rig2cam.to(d)[cam], p.pix2d.to(d),
+                   p.pix2d_std.to(d), p.pix2d_dep.to(d))
+
+
+def _first_order_errors(p, update, group, seed=7):
+    """||r(update(x, t delta)) - r(x) + t J delta|| / ||t J delta|| for t = 1e-3 and 1e-4, with delta nonzero
+    in one parameter group only and J the autodiff derivatives of residual_fp64 under the model's own
+    parametrisation (f += df, P <- exp(xi^) P, z += dz, X += dX).  A correct update x <- x (+) (-t delta)
+    (en:310-313) gives errors of order t, shrinking tenfold from t = 1e-3 to 1e-4."""
+    d = torch.float64
+    K, P, Z, X = p.K.to(d), p.P_w2rig.to(d), p.z_coefs.to(d), p.pts3d.to(d)
+    g = torch.Generator().manual_seed(seed)
+    dK, dP = torch.zeros((len(K), 2), dtype=d), torch.zeros((len(P), 6), dtype=d)
+    dZ, dX = torch.zeros_like(Z), torch.zeros_like(X)
+    if group == 'K':
+        dK = 20.0 * torch.randn(dK.shape, generator=g, dtype=d)
+    elif group == 'P':
+        dP = torch.randn(dP.shape, generator=g, dtype=d) * torch.tensor([0.05] * 3 + [0.2] * 3, dtype=d)
+    elif group == 'Z':
+        dZ = 0.2 * torch.randn(dZ.shape, generator=g, dtype=d)
+    else:
+        dX = 0.2 * torch.randn(dX.shape, generator=g, dtype=d)
+    Jf, Jxi, Jz, Jx = od.autodiff_jacobians(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
+                                            p.pix2d, p.pix2d_std, p.pix2d_dep)
+    img = ok.obs_to_img(p.infos, len(p.pids))
+    node, cam = p.infos[1].long()[img], p.infos[2].long()[img]
+    Jd = (torch.einsum('nrc,nc->nr', Jf, dK[cam]) + torch.einsum('nrc,nc->nr', Jxi, dP[node]) +
+          torch.einsum('nrc,nc->nr', Jz, dZ[img]) + torch.einsum('nrc,nc->nr', Jx, dX[p.pids.long()]))
+    r0 = _residuals_fp64(p, K, P, Z, X)
+    errs = []
+    for t in (1e-3, 1e-4):
+        up = update(K, P, Z, X, dK, dP, dZ, dX, t)
+        rt = _residuals_fp64(p, up['K'], up['P_w2rig'], up['z_coefs'], up['pts3d'])
+        errs.append(float((rt - r0 + t * Jd).norm() / (t * Jd).norm()))
+    return errs
+
+
+def _passes_first_order(errs):
+    # the residuals are linear in the focal and the z-coefficients: there the error is rounding alone
+    return errs[0] < 2e-2 and (errs[1] < errs[0] / 5 or max(errs) < 1e-9)
+
+
+@pytest.mark.parametrize('group', ['K', 'P', 'Z', 'X'])
+def test_oracle_update_rule_is_the_first_order_step(group):
+    """The oracle's parameter update (apply_update, en:310-313 with update_K en:347-354 and exp_se3
+    cujac/__init__.py:56-58), used by its lm_step and by the GPU step checks, moves the residuals by
+    -t J delta to first order in every parameter group: the focal decrement, the left pose update
+    exp(-t dP^) P, the z-coefficient and point decrements.  The same check rejects the update with the
+    sign of any group's step flipped, and the pose update applied on the right (P exp(-t dP^)), which
+    the loss-decrease and schedule checks of the LM step do not see."""
+    p = tiny_problem(0, n_frames=6, n_tracks=80)
+    errs = _first_order_errors(p, oe.apply_update, group)
+    assert _passes_first_order(errs), (group, errs)
+
+    def flipped(K, P, Z, X, dK, dP, dZ, dX, t):
+        s = {g: (-1.0 if g == group else 1.0) for g in 'KPZX'}
+        return oe.apply_update(K, P, Z, X, dK * s['K'], dP * s['P'], dZ * s['Z'], dX * s['X'], t)
+
+    def right_pose(K, P, Z, X, dK, dP, dZ, dX, t):
+        up = oe.apply_update(K, P, Z, X, dK, dP * 0, dZ, dX, t)
+        up['P_w2rig'] = P @ ok.exp_se3(-(dP * t))
+        return up
+
+    bad = {'flipped sign': flipped}
+    if group == 'P':
+        bad['right-multiplied pose'] = right_pose
+    for name, fn in bad.items():
+        e = _first_order_errors(p, fn, group)
+        assert not _passes_first_order(e), (group, name, e)
 
 
 # Known answers for the acceptance rule of en:305-333, worked out by hand from the reference text:
