@@ -75,7 +75,7 @@ def main():
                                             g.pix2d_std, g.pix2d_dep, True, hp['weight_z'], hp['pnorm'],
                                             hp['max_pix_err'], hp['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
-    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev)
+    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, dtype=torch.float64)
     J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                              g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
     from blast3r_amd.ba_solver import _param_state
@@ -150,7 +150,8 @@ def main():
     # full LM iterations
     lm_ms = lm_ms_direct = None
     if args.lm_steps > 0:
-        kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
+        kw = dict(dtype=torch.float64,
+                  weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
                   optim_P=o['optim_P'])
         engine.lm_step(**g.lm_inputs(), **kw)          # warm (plan cached after this)
         torch.cuda.synchronize()
@@ -527,7 +528,8 @@ def bench_pairmajor(cfg, dev, steps, warmup):
                                             g.pix2d_std, g.pix2d_dep, True, hp['weight_z'], hp['pnorm'],
                                             hp['max_pix_err'], hp['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
-    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, path='pairmajor')
+    gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, dtype=torch.float64,
+                               path='pairmajor')
     J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                              g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
     res._ba_state = _param_state(J)
@@ -548,7 +550,8 @@ def bench_pairmajor(cfg, dev, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
               optim_P=o['optim_P'])
     engine.lm_step(**g.lm_inputs(), **kw)
     torch.cuda.synchronize()
@@ -613,7 +616,7 @@ def bench_reduced_solve(prob, g, dev, warmup, reps=5):
     st = stream.cuda_stream
     result = {}
     for layout in ('banded', 'banded_sequential', 'dense'):
-        gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, solver='cholesky',
+        gs = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, dtype=torch.float64, solver='cholesky',
                                cholesky_layout=layout)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                                  g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
@@ -731,7 +734,8 @@ def cpu_baseline(cfg, prob=None):
     del ne
     dt32, ne32, _ = npass(False)
     del ne32
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], clip_pix_err=o['clip_pix_err'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], clip_pix_err=o['clip_pix_err'],
               optim_K=o['optim_K'], optim_P=o['optim_P'])
     t0 = time.perf_counter()
     _, st, info = oeng.lm_step(**p.lm_inputs(), **kw, pcg_maxiter=CPU_PCG_CAP)

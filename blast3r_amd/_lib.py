@@ -71,7 +71,7 @@ class BaPcgArgs(ctypes.Structure):
                 ('p', c_p), ('y_img', c_p), ('partials', c_p), ('state', c_p), ('istate', c_p),
                 ('S_rows', c_p), ('n_row_ent', c_i64), ('row_u', c_p), ('long_u', c_p), ('n_long', c_i64),
                 ('long_ptr', c_p), ('long_idx', c_p), ('img_part', c_p), ('src1', c_p), ('long_rng', c_p),
-                ('row_cap', c_int)]
+                ('row_cap', c_int), ('real32', c_int)]
 
 class BaPmArgs(ctypes.Structure):
     _fields_ = [('infos', c_p), ('n_imgs', c_int), ('n_tracks', c_int),
@@ -85,7 +85,8 @@ class BaPmArgs(ctypes.Structure):
                 ('hp', BaHuber), ('lay', BaLayout),
                 ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
                 ('pobs', c_p), ('wobs', c_p), ('jslots', c_p), ('vslots', c_p), ('yrun', c_p), ('Hpp', c_p), ('gp', c_p), ('tmax', c_p), ('lam_p', c_p), ('pfac', c_p), ('V', c_p),
-                ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dc_img', c_p), ('dX', c_p), ('dX64', c_p)]
+                ('S_pairs', c_p), ('e_img', c_p), ('dg_img', c_p), ('dc_img', c_p), ('dX', c_p), ('dX64', c_p),
+                ('real32', c_int)]
 
 
 class BaCholArgs(ctypes.Structure):
@@ -190,7 +191,7 @@ _SIGS = {
     'ba_tangent_prior': (c_int, [ctypes.POINTER(BaTangentArgs), c_p]),
     'ba_tangent_workspace_bytes': (c_i64, [c_i64, c_int, c_int, c_int, c_int, c_int, c_int]),
     'ba_planar_confidence': (c_int, [c_p, c_int, c_int, c_f, c_p, c_p]),
-    'ba_add_z_prior': (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_p]),
+    'ba_add_z_prior': (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_int, c_p]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -86,14 +86,21 @@ class GaussNewtonSolver:
         self.imgs = Param(n_imgs)
         self.tracks = Param(n_tracks)
         self.device = torch.device(device)
-        # the fused path always linearises and reduces in fp64 (the reference's solver dtype,
-        # engine.py:490); `dtype` is accepted for signature compatibility.
+        # dtype is the precision of the linearisation's products and sums, the reduced system, the PCG and
+        # the back-substitution, as in the reference (bs:22, :37, :128): torch.float64 (bundle_adjustment's
+        # choice, en:490) on either path; torch.float32 (its default) on the pair-major path, which has a
+        # fp32 variant of every kernel (the Jacobian core is evaluated in fp64 and rounded to fp32)
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError(f'dtype must be torch.float32 or torch.float64, not {dtype}')
         self.dtype = dtype
+        self.real32 = dtype == torch.float32
         self.dampen = dampen
         self.adaptive_dampen = adaptive_dampen
         self.no_grad_f_from_rz = no_grad_f_from_rz
         if solver not in ('pcg', 'cholesky'):
             raise ValueError(f'unknown reduced solver {solver!r} (supported: "pcg", "cholesky")')
+        if solver == 'cholesky' and self.real32:
+            raise ValueError("solver='cholesky' factors the reduced system in fp64: pass dtype=torch.float64")
         self.solver = solver
         # solver='cholesky': 'banded' when every image pair lies within w images and few unknowns are shared
         # by several images: block cyclic reduction over super-blocks of 128 unknowns when w d <= 128 and
@@ -112,6 +119,9 @@ class GaussNewtonSolver:
         # 'batched' outside its limits raises instead of switching paths
         if path not in ('auto', 'batched', 'pairmajor'):
             raise ValueError(f'unknown path {path!r}')
+        if path == 'batched' and self.real32:
+            raise ValueError("path='batched' runs in fp64: pass dtype=torch.float64, or use path='pairmajor' / "
+                             "'auto' for the fp32 solver")
         self.path = path
         self.use_graph = bool(use_graph)        # replay the PCG launches from a captured graph
         self.last = {}
@@ -261,7 +271,7 @@ class GaussNewtonSolver:
         if self.path == 'batched' and d > 15:
             raise ValueError(f"path='batched' takes at most 15 reduced parameters per image (here {d}); "
                              "use path='pairmajor' or 'auto'")
-        if self.path == 'pairmajor' or d > 15:
+        if self.path == 'pairmajor' or d > 15 or self.real32:
             return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         try:
             plan = get_plan(J.rigs, J.pids, self.tracks.true_n, device=dev, **self.plan_options)
@@ -397,22 +407,24 @@ class GaussNewtonSolver:
         a.enK, a.enP, a.enZ, a.enX = (ptr(en[k][1]) for k in ('K', 'P', 'Z', 'X'))
         self._huber_args(a.hp, J)
         self._layout_args(a.lay, J, lay, clamp_w)
-        Hpp = ws('Hpp', (max(T, 1), 6), torch.float64)
-        gp = ws('gp', (max(T, 1), 3), torch.float64)
-        lam_p = ws('lam_p', (1,), torch.float64)
-        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), torch.float64)
-        e_img = ws('e_img', (n_imgs, dd), torch.float64)
-        dg_img = ws('dg_img', (n_imgs, dd), torch.float64)
-        a.pobs = ptr(ws('pobs', (max(n_obs, 1), 9), torch.float64))
+        R = self.dtype                         # the working precision of every array below but wobs
+        a.real32 = int(self.real32)
+        Hpp = ws('Hpp', (max(T, 1), 6), R)
+        gp = ws('gp', (max(T, 1), 3), R)
+        lam_p = ws('lam_p', (1,), R)
+        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), R)
+        e_img = ws('e_img', (n_imgs, dd), R)
+        dg_img = ws('dg_img', (n_imgs, dd), R)
+        a.pobs = ptr(ws('pobs', (max(n_obs, 1), 9), R))
         a.wobs = ptr(ws('wobs', (max(n_obs, 1), 4), torch.float32))
         nsl = lambda n: int(lib().ba_pm_slot_doubles(n, n_imgs, d))
-        a.jslots = ptr(ws('jslots', (max(nsl(n_obs), 1),), torch.float64))
-        a.vslots = ptr(ws('vslots', (max(nsl(sc['n_runs']), 1),), torch.float64))
-        a.yrun = ptr(ws('yrun', (max(sc['n_runs'], 1), 3), torch.float64))
+        a.jslots = ptr(ws('jslots', (max(nsl(n_obs), 1),), R))
+        a.vslots = ptr(ws('vslots', (max(nsl(sc['n_runs']), 1),), R))
+        a.yrun = ptr(ws('yrun', (max(sc['n_runs'], 1), 3), R))
         a.Hpp, a.gp, a.lam_p = ptr(Hpp), ptr(gp), ptr(lam_p)
-        a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), torch.float64))
-        a.pfac = ptr(ws('pfac', (max(T, 1), 12), torch.float64))
-        a.V = ptr(ws('V', (max(sc['n_runs'], 1), 3, dp), torch.float64))
+        a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), R))
+        a.pfac = ptr(ws('pfac', (max(T, 1), 12), R))
+        a.V = ptr(ws('V', (max(sc['n_runs'], 1), 3, dp), R))
         a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
         W = w_pts.expand(-1, 3)
         own = getattr(residuals, '_ba_state', None)
@@ -434,11 +446,12 @@ class GaussNewtonSolver:
         n_imgs = self.imgs.true_n
         um = self._unknown_maps(J, lay, plan)
         n_u = um['n_u']
+        R = S_pairs.dtype                      # the working precision (fp32 only on the pair-major path)
         if n_u > 0 and d > 0:
-            x = ws('pcg_x', (n_u,), torch.float64)
+            x = ws('pcg_x', (n_u,), R)
             istate = ws('pcg_istate', (8,), torch.int32)
         else:
-            x = torch.zeros(max(n_u, 1), dtype=torch.float64, device=dev)
+            x = torch.zeros(max(n_u, 1), dtype=R, device=dev)
             istate = torch.zeros(8, dtype=torch.int32, device=dev)
         if n_u > 0 and d > 0:
             pa = BaPcgArgs()
@@ -450,16 +463,17 @@ class GaussNewtonSolver:
             pa.S_pairs, pa.e_img, pa.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
             pa.dampen, pa.adaptive = float(self.dampen), int(bool(self.adaptive_dampen))
             pa.maxiter, pa.tol = int(self.pcg_maxiter), float(self.pcg_tol)
-            vec = lambda name: ws('pcg_' + name, (n_u,), torch.float64)
+            pa.real32 = int(R == torch.float32)
+            vec = lambda name: ws('pcg_' + name, (n_u,), R)
             rhs, diagA, damp = vec('rhs'), vec('diagA'), vec('damp')
             xbest, r, z = vec('xbest'), vec('r'), vec('z')
-            p = ws('pcg_p2', (2 * n_u,), torch.float64)
-            y_img = ws('pcg_y', (n_imgs * d,), torch.float64)
-            part = ws('pcg_part', (int(lib().ba_pcg_partials_size(n_u)),), torch.float64)
-            state = ws('pcg_state', (16,), torch.float64)
+            p = ws('pcg_p2', (2 * n_u,), R)
+            y_img = ws('pcg_y', (n_imgs * d,), R)
+            part = ws('pcg_part', (int(lib().ba_pcg_partials_size(n_u)),), R)
+            state = ws('pcg_state', (16,), R)
             pa.rhs, pa.diagA, pa.damp, pa.x, pa.xbest = ptr(rhs), ptr(diagA), ptr(damp), ptr(x), ptr(xbest)
             pa.r, pa.z, pa.p, pa.y_img = ptr(r), ptr(z), ptr(p), ptr(y_img)
-            pa.img_part = ptr(ws('pcg_img_part', (n_imgs,), torch.float64))
+            pa.img_part = ptr(ws('pcg_img_part', (n_imgs,), R))
             pa.partials, pa.state, pa.istate = ptr(part), ptr(state), ptr(istate)
             pa.long_u, pa.n_long = ptr(um['long_u']), um['n_long']
             pa.long_ptr, pa.long_idx = ptr(um['long_ptr']), ptr(um['long_idx'])
@@ -510,7 +524,8 @@ class GaussNewtonSolver:
 
     @staticmethod
     def _pcg_rows(pa, plan, d, n_imgs):
-        """The PCG's image-row copies of the pair blocks (workspace fields of ba_pcg_args)."""
+        """The PCG's image-row copies of the pair blocks (workspace fields of ba_pcg_args), in the working
+        precision pa.real32 names."""
         ws = plan.workspace
         rp = plan.host['row_ptr']
         n_ent = int(rp[-1]) if len(rp) else 0
@@ -519,7 +534,7 @@ class GaussNewtonSolver:
         cap = -(-longest // 8) * 8
         row_cap = cap if 0 < cap and n_imgs * cap <= 1.25 * n_ent else 0
         n_blk = n_imgs * row_cap if row_cap else n_ent
-        S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float64)
+        S_rows = ws('pcg_S_rows', (max(n_blk, 1), d, d), torch.float32 if pa.real32 else torch.float64)
         pa.S_rows, pa.n_row_ent, pa.row_cap = ptr(S_rows), n_ent, row_cap
         gw = 16 if d <= 16 else 32                     # row_u entries per block (the SpMV's lanes per group)
         pa.row_u = ptr(ws('pcg_row_u', (max(n_blk, 1) * gw,), torch.int32))
@@ -669,13 +684,14 @@ class GaussNewtonSolver:
             raise TypeError('Unsupported JTJ.A type for z_prior: z-coefficients are not optimised')
         C = self.n_zcf
         o = lay['d'] - C
-        H_z = H_z.to(device=S_pairs.device, dtype=torch.float64).contiguous()
-        g_z = g_z.to(device=S_pairs.device, dtype=torch.float64).contiguous()
+        R = S_pairs.dtype
+        H_z = H_z.to(device=S_pairs.device, dtype=R).contiguous()
+        g_z = g_z.to(device=S_pairs.device, dtype=R).contiguous()
         assert g_z.shape == (self.imgs.n, C) and H_z.shape == (self.imgs.n, C, C)
         if len(e_img) != self.imgs.n:          # compacted images: the rows of the optimised ones
             idx = torch.as_tensor(self.imgs.true_idxs, device=S_pairs.device).long()
-            gf = torch.zeros((len(e_img), C), dtype=torch.float64, device=S_pairs.device)
-            Hf = torch.zeros((len(e_img), C, C), dtype=torch.float64, device=S_pairs.device)
+            gf = torch.zeros((len(e_img), C), dtype=R, device=S_pairs.device)
+            Hf = torch.zeros((len(e_img), C, C), dtype=R, device=S_pairs.device)
             gf[idx], Hf[idx] = g_z, H_z
             g_z, H_z = gf, Hf
         diag = plan.workspace_cache.get('diag_pair')
@@ -689,7 +705,7 @@ class GaussNewtonSolver:
                 raise ValueError('z_prior: an image without observations has no block in the reduced system')
             plan.workspace_cache['diag_pair'] = diag
         check(lib().ba_add_z_prior(ptr(S_pairs), ptr(diag), ptr(e_img), ptr(dg_img), ptr(H_z), ptr(g_z), len(e_img),
-                                   lay['d'], C, stream_ptr(S_pairs.device)))
+                                   lay['d'], C, int(R == torch.float32), stream_ptr(S_pairs.device)))
 
     # ------------------------------------------------------------------ bs:228-248
     def unpack_delta_inplace(self, delta):
@@ -712,12 +728,12 @@ class GaussNewtonSolver:
     # ------------------------------------------------------------------ inspection helpers
     def point_blocks(self):
         """H_pp upper (n_tracks,6) and g_p (n_tracks,3) of the last solve_delta in track-id order
-        (the device keeps them in chunk-track order); tracks without observations hold zeros."""
+        (the device keeps them in chunk-track order), as fp64; tracks without observations hold zeros."""
         last = self.last
         plan = last['plan']
         T = self.tracks.true_n
         if last.get('path') == 'pairmajor':         # kept in track order
-            return last['Hpp'][:T].clone(), last['gp'][:T].clone()
+            return last['Hpp'][:T].to(torch.float64), last['gp'][:T].to(torch.float64)
         n_ct = plan.scalars['n_ctracks']
         pid = plan.dev['ct_pid'][:n_ct].long()
         H = torch.zeros((T, 6), dtype=torch.float64, device=self.device)
@@ -727,7 +743,7 @@ class GaussNewtonSolver:
         return H, g
 
     def reduced_system_dense(self):
-        """Dense S (reference unknown order, damped) and rhs of the last solve_delta (for tests)."""
+        """Dense S (reference unknown order, damped) and rhs of the last solve_delta, as fp64 (for tests)."""
         last = self.last
         um, lay, plan = last['unknowns'], last['lay'], last['plan']
         n_u, d = um['n_u'], lay['d']
@@ -739,7 +755,7 @@ class GaussNewtonSolver:
         for p in range(len(i1)):
             r = umap[i1[p]]
             c = umap[i2[p]]
-            blk = S_img_pairs[p]
+            blk = S_img_pairs[p].to(torch.float64)
             mr, mc = r >= 0, c >= 0
             sub = blk[mr][:, mc]
             S.index_put_((r[mr][:, None].expand(-1, int(mc.sum())), c[mc][None, :].expand(int(mr.sum()), -1)), sub,
@@ -747,8 +763,8 @@ class GaussNewtonSolver:
             if i1[p] != i2[p]:
                 S.index_put_((c[mc][:, None].expand(-1, int(mr.sum())), r[mr][None, :].expand(int(mc.sum()), -1)),
                              sub.T, accumulate=True)
-        S += torch.diag(last['damp'])
-        return S, last['rhs']
+        S += torch.diag(last['damp'].to(torch.float64))
+        return S, last['rhs'].to(torch.float64)
 
 
 def _param_state(J):

@@ -32,6 +32,34 @@
 namespace ba {
 int unknown_setup(const ba_pcg_args& a, hipStream_t st);   // ba_pcg.hip
 
+// ba_pcg_args with its working-precision arrays typed as fp64: the direct solve runs in fp64 only
+// (ba_reduced_solve refuses real32), so its kernels read the fields through this same-layout view.
+struct PcgArgs64 {
+    int64_t n_u;
+    int32_t n_imgs, d;
+    const int32_t *umap, *inv_ptr, *inv_src, *leaf, *row_ptr, *row_ent, *pair_i1, *pair_i2;
+    const double *S_pairs, *e_img, *dg_img;
+    double dampen; int32_t adaptive;
+    int32_t maxiter; double tol;
+    double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img, *partials, *state;
+    int32_t* istate;
+    double* S_rows;
+    int64_t n_row_ent;
+    int32_t* row_u;
+    const int32_t* long_u;
+    int64_t n_long;
+    const int32_t *long_ptr, *long_idx;
+    double* img_part;
+    const int32_t *src1, *long_rng;
+    int32_t row_cap;
+    int32_t real32;
+};
+static_assert(sizeof(PcgArgs64) == sizeof(ba_pcg_args) && offsetof(PcgArgs64, real32) == offsetof(ba_pcg_args, real32) &&
+                  offsetof(PcgArgs64, S_pairs) == offsetof(ba_pcg_args, S_pairs) &&
+                  offsetof(PcgArgs64, img_part) == offsetof(ba_pcg_args, img_part) &&
+                  offsetof(PcgArgs64, S_rows) == offsetof(ba_pcg_args, S_rows),
+              "PcgArgs64 mirrors ba_pcg_args");
+
 #define CH_T 256
 
 typedef double dbl4 __attribute__((ext_vector_type(4)));
@@ -65,7 +93,7 @@ struct ChArgs {
 // 0 = isolated (none: a group switched off, a zero leaf damped by dampen * I).
 //
 // S_img(a, b) for image-level entries a = (i, r), b = (j, c): the pair block of images (i, j).
-__device__ __forceinline__ double s_img(const ba_pcg_args& a, const int32_t* __restrict__ pair_idx, int i, int r,
+__device__ __forceinline__ double s_img(const PcgArgs64& a, const int32_t* __restrict__ pair_idx, int i, int r,
                                         int j, int c) {
     const int d = a.d;
     if (i <= j) {
@@ -78,7 +106,7 @@ __device__ __forceinline__ double s_img(const ba_pcg_args& a, const int32_t* __r
 
 // dense: S_u[u][v] for v <= u where neither is shared (the identity on the padding rows n_u .. N, the
 // damping alone on an isolated unknown), one thread per (u, v)
-__global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c, int64_t N) {
+__global__ void __launch_bounds__(CH_T) k_dense_assemble(PcgArgs64 a, ChArgs c, int64_t N) {
     const int64_t u = blockIdx.y;
     const int64_t v = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     if (v > u || u >= N) return;
@@ -101,7 +129,7 @@ __global__ void __launch_bounds__(CH_T) k_dense_assemble(ba_pcg_args a, ChArgs c
 // S_u(s, v) for every shared s (blockIdx.y) and every local v (one wave each; lane l sums the pairs l, l + 64, ..
 // of v's image row, the lanes are summed in a fixed tree): written to the dense matrix (mode 0) or to the
 // border rows Bfull[s][entry of v] (mode 1)
-__global__ void __launch_bounds__(CH_T) k_shared_local(ba_pcg_args a, ChArgs c, int mode) {
+__global__ void __launch_bounds__(CH_T) k_shared_local(PcgArgs64 a, ChArgs c, int mode) {
     const int lane = threadIdx.x & 63;
     const int64_t v = (int64_t)blockIdx.x * (CH_T / 64) + (threadIdx.x >> 6);
     const int sb = blockIdx.y;
@@ -133,7 +161,7 @@ __global__ void __launch_bounds__(CH_T) k_shared_local(ba_pcg_args a, ChArgs c, 
 // summed by block (b1 n_s + b2, chunk) over a fixed slice of the image pairs (pair p goes to chunk
 // (p / CH_T) mod SS_CHUNKS), then over the chunks in order by k_shared_sum, with the damping on the diagonal
 #define SS_CHUNKS 64
-__global__ void __launch_bounds__(CH_T) k_shared_part(ba_pcg_args a, ChArgs c, int64_t n_pairs) {
+__global__ void __launch_bounds__(CH_T) k_shared_part(PcgArgs64 a, ChArgs c, int64_t n_pairs) {
     __shared__ double sh[CH_T / 64];
     const int ns = c.n_shared;
     const int b1 = (int)blockIdx.x / ns, b2 = (int)blockIdx.x - b1 * ns;
@@ -165,7 +193,7 @@ __global__ void __launch_bounds__(CH_T) k_shared_part(ba_pcg_args a, ChArgs c, i
 }
 
 // written to the dense matrix (mode 0) or to the corner Cb (mode 1)
-__global__ void __launch_bounds__(CH_T) k_shared_sum(ba_pcg_args a, ChArgs c, int mode) {
+__global__ void __launch_bounds__(CH_T) k_shared_sum(PcgArgs64 a, ChArgs c, int mode) {
     const int ns = c.n_shared;
     const int e = (int)(blockIdx.x * CH_T + threadIdx.x);
     if (e >= ns * ns) return;
@@ -192,13 +220,13 @@ __global__ void __launch_bounds__(CH_T) k_copy_pad(const double* __restrict__ sr
 
 // unknowns that no image-level entry carries (a parameter group switched off: a zero leaf damped by
 // dampen * I, ba_solver.py:510-517) are decoupled: x_u = rhs_u / damp_u (the rhs is zero there)
-__global__ void __launch_bounds__(CH_T) k_isolated(ba_pcg_args a, const double* __restrict__ xs) {
+__global__ void __launch_bounds__(CH_T) k_isolated(PcgArgs64 a, const double* __restrict__ xs) {
     const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     if (u >= a.n_u) return;
     a.x[u] = a.inv_ptr[u + 1] > a.inv_ptr[u] ? xs[u] : a.rhs[u] / a.damp[u];
 }
 
-__global__ void k_chol_status(ba_pcg_args a, const int32_t* __restrict__ info) {
+__global__ void k_chol_status(PcgArgs64 a, const int32_t* __restrict__ info) {
     if (threadIdx.x == 0 && a.istate) {
         a.istate[0] = 1; a.istate[1] = 1;
         a.istate[2] = 0;                     // no iterations
@@ -229,7 +257,7 @@ __global__ void k_info_init(int32_t* info) {
 // band columns (the image-level columns that carry a local unknown in some image: a mono camera's focal
 // columns, shared by every image, are left out), the damping on a local diagonal entry, 1 on a
 // non-local one; bl[i db + r] = the local rhs entries; the border rows Bfull cleared.
-__global__ void __launch_bounds__(CH_T) k_band_assemble(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CH_T) k_band_assemble(PcgArgs64 a, ChArgs c) {
     const int d = a.d, db = c.db, w1 = c.w + 1;
     const int64_t e = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     const int64_t per = (int64_t)w1 * db * db;
@@ -282,7 +310,7 @@ __host__ __device__ inline int64_t band_lds_doubles(int M, int ns) {
 //      registers at the start of the step) fill the last rows of the other copy.
 // Then thread 0 factors the corner, and the backward sweep walks the images in reverse, reading each
 // column panel of L (prefetched one step ahead) against the solved x of the following images.
-__global__ void __launch_bounds__(CB_T) k_band_solve(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CB_T) k_band_solve(PcgArgs64 a, ChArgs c) {
     extern __shared__ double lds[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int d = c.db, w1 = c.w + 1, M = w1 * d, Md = M - d, ns = c.n_shared, n_imgs = a.n_imgs;
@@ -582,7 +610,7 @@ __global__ void __launch_bounds__(CB_T) k_band_solve(ba_pcg_args a, ChArgs c) {
 
 // x of the local unknowns from the banded solution (shared ones were written by k_band_solve);
 // isolated unknowns: rhs / damp
-__global__ void __launch_bounds__(CH_T) k_band_scatter(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CH_T) k_band_scatter(PcgArgs64 a, ChArgs c) {
     const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     if (u >= a.n_u) return;
     const int k = c.kind[u];
@@ -621,7 +649,7 @@ __host__ __device__ inline int cr_images(int db, int w, int ns) {
     return s > w ? s : w;
 }
 
-__global__ void __launch_bounds__(CH_T) k_cr_assemble(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CH_T) k_cr_assemble(PcgArgs64 a, ChArgs c) {
     const int64_t e = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     if (e >= (int64_t)c.nsb * CR_MP2) return;
     const int I = (int)(e / CR_MP2);
@@ -992,7 +1020,7 @@ __device__ __forceinline__ double cr_x(const ChArgs& c, int64_t u, int col) {
 // waves in a fixed tree; k_cr_border adds the chunks in order, factors the corner and solves (thread 0).
 #define BP_CHUNKS 64
 static_assert(BP_CHUNKS <= SS_CHUNKS, "the border products share the shared-shared partial-sum buffer");
-__global__ void __launch_bounds__(CH_T) k_cr_bpart(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CH_T) k_cr_bpart(PcgArgs64 a, ChArgs c) {
     __shared__ double sh[CH_T / 64];
     const int ns = c.n_shared, combo = blockIdx.y, b1 = combo / (ns + 1), col = combo - b1 * (ns + 1);
     const int64_t nl = (int64_t)a.n_imgs * c.db;
@@ -1009,7 +1037,7 @@ __global__ void __launch_bounds__(CH_T) k_cr_bpart(ba_pcg_args a, ChArgs c) {
     }
 }
 
-__global__ void k_cr_border(ba_pcg_args a, ChArgs c) {
+__global__ void k_cr_border(PcgArgs64 a, ChArgs c) {
     double Cc[(CR_NR - 1) * (CR_NR - 1)], rb[CR_NR - 1], xb[CR_NR - 1];
     if (threadIdx.x != 0) return;
     const int ns = c.n_shared;
@@ -1052,7 +1080,7 @@ __global__ void k_cr_border(ba_pcg_args a, ChArgs c) {
 }
 
 // the local solution: x_loc = S_loc^-1 b_loc - S_loc^-1 B x_s
-__global__ void __launch_bounds__(CH_T) k_cr_local(ba_pcg_args a, ChArgs c) {
+__global__ void __launch_bounds__(CH_T) k_cr_local(PcgArgs64 a, ChArgs c) {
     const int64_t u = (int64_t)blockIdx.x * CH_T + threadIdx.x;
     if (u >= (int64_t)a.n_imgs * c.db) return;
     double v = cr_x(c, u, 0);
@@ -1272,7 +1300,8 @@ extern "C" int64_t ba_chol_band_lds_bytes(int32_t d, int32_t w, int32_t n_shared
 extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* cargs, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr && cargs != nullptr, "ba_reduced_solve: null args");
-    const ba_pcg_args& a = *args;
+    BA_REQUIRE(!args->real32, "ba_reduced_solve: the direct solve runs in fp64 only (real32 must be 0)");
+    const PcgArgs64& a = *reinterpret_cast<const PcgArgs64*>(args);
     const ba_chol_args& ca = *cargs;
     hipStream_t st = (hipStream_t)stream;
     BA_REQUIRE(a.n_u >= 0 && a.d >= 1 && a.d <= 32, "ba_reduced_solve: bad sizes (1 <= d <= 32)");
@@ -1290,7 +1319,7 @@ extern "C" int ba_reduced_solve(const ba_pcg_args* args, const ba_chol_args* car
     c.shared_u = ca.shared_u; c.n_shared = ca.n_shared; c.w = ca.w; c.info = ca.info;
     c.db = ca.db; c.bcol = ca.bcol; c.bpos = ca.bpos;
     const int64_t n_pairs = ca.n_pairs;
-    int rc = unknown_setup(a, st);
+    int rc = unknown_setup(*args, st);
     if (rc != BA_OK) return rc;
     hipLaunchKernelGGL(k_info_init, dim3(1), dim3(64), 0, st, c.info);
     const unsigned nbu = (unsigned)((a.n_u + CH_T - 1) / CH_T);

@@ -268,4 +268,13 @@ __device__ __forceinline__ void eval_jacobian(const CamF& cp, const float Xf[3],
     O.valid = J.valid;
 }
 
+// Running maximum of non-negative floating-point values: their bit patterns order as the values, so
+// an integer atomic max combines them in any order with the same result.
+__device__ __forceinline__ void atomic_max_nonneg(double* p, double v) {
+    atomicMax(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v));
+}
+__device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
+    atomicMax(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
+}
+
 }  // namespace ba

@@ -26,7 +26,7 @@ namespace ba {
 #define PCG_IPF 4           // image partials of p.Ap each update thread requests at launch
 enum { PT_RR = 0, PT_RZ = 1 };
 
-// state (fp64): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
+// state (working precision): ST_RZ0/1 r.z after n updates and ST_BEST0/1 the best residual norm after n updates,
 // both in slot n & 1; ST_BETA the beta of the current direction; ST_LEAF.. the camera-leaf damping.
 // ST_LEAFMAX.. (3 words): the per-leaf maxima of |diag(A)| as bit patterns, accumulated by k_leaf_max.
 enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_BETA = 5, ST_LEAF = 8, ST_LEAFMAX = 11 };
@@ -34,26 +34,40 @@ enum { ST_BNORM = 0, ST_RZ0 = 1, ST_RZ1 = 2, ST_BEST0 = 3, ST_BEST1 = 4, ST_BETA
 // IS_CONV converged, IS_BESTK best iterate, IS_USEBEST the best iterate is returned.
 enum { IS_DONE0 = 0, IS_DONE1 = 1, IS_K = 2, IS_CONV = 3, IS_BESTK = 4, IS_USEBEST = 5 };
 
+// The arrays of ba_pcg_args in the working precision Real (double, or float when real32 is set).
+template <typename Real>
+struct PcgV {
+    const Real *S_pairs, *e_img, *dg_img;
+    Real *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img, *partials, *state, *S_rows, *img_part;
+    __device__ __forceinline__ explicit PcgV(const ba_pcg_args& a)
+        : S_pairs((const Real*)a.S_pairs), e_img((const Real*)a.e_img), dg_img((const Real*)a.dg_img),
+          rhs((Real*)a.rhs), diagA((Real*)a.diagA), damp((Real*)a.damp), x((Real*)a.x), xbest((Real*)a.xbest),
+          r((Real*)a.r), z((Real*)a.z), p((Real*)a.p), y_img((Real*)a.y_img), partials((Real*)a.partials),
+          state((Real*)a.state), S_rows((Real*)a.S_rows), img_part((Real*)a.img_part) {}
+};
+
 // search direction of update n: p_n = z_n + beta_n p_{n-1} (ba_solver.py:1235), written as one
 // fused multiply-add so that every kernel that forms it gets the same bits
-__device__ __forceinline__ double pdir(double z, double pold, double beta) { return fma(beta, pold, z); }
+template <typename Real>
+__device__ __forceinline__ Real pdir(Real z, Real pold, Real beta) { return fma(beta, pold, z); }
 
 // Sum over the 64 lanes of a wave; every lane gets the same bits (each butterfly step adds the
 // same two values in either lane, and fp addition commutes).
-__device__ __forceinline__ double wave_sum(double v) {
+template <typename Real>
+__device__ __forceinline__ Real wave_sum(Real v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
     return v;
 }
 
 // Sum over a block of NT threads in a fixed order (waves by butterfly, then the wave sums in wave
 // order); every thread gets the result.  sh holds at least NT / 64 doubles.
-template <int NT>
-__device__ __forceinline__ double block_sum(double v, double* sh) {
+template <int NT, typename Real>
+__device__ __forceinline__ Real block_sum(Real v, Real* sh) {
     v = wave_sum(v);
     __syncthreads();                                  // sh may still be read by a previous call
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
-    double t = 0.0;
+    Real t = Real(0);
 #pragma unroll
     for (int k = 0; k < NT / 64; ++k) t += sh[k];
     return t;
@@ -61,8 +75,8 @@ __device__ __forceinline__ double block_sum(double v, double* sh) {
 
 // K block sums at once with two barriers; v[k] becomes the sum of every thread's v[k], in the
 // same order as block_sum.  sh holds at least K * NT / 64 doubles.
-template <int NT, int K>
-__device__ __forceinline__ void block_sums(double (&v)[K], double* sh) {
+template <int NT, int K, typename Real>
+__device__ __forceinline__ void block_sums(Real (&v)[K], Real* sh) {
 #pragma unroll
     for (int k = 0; k < K; ++k) v[k] = wave_sum(v[k]);
     __syncthreads();
@@ -72,7 +86,7 @@ __device__ __forceinline__ void block_sums(double (&v)[K], double* sh) {
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        double t = 0.0;
+        Real t = Real(0);
 #pragma unroll
         for (int w = 0; w < NT / 64; ++w) t += sh[k * (NT / 64) + w];
         v[k] = t;
@@ -81,32 +95,34 @@ __device__ __forceinline__ void block_sums(double (&v)[K], double* sh) {
 
 // Sums of r.r and r.z over the nb block partials (deterministic, identical in every block of NT
 // threads); sh holds at least 2 * NT / 64 doubles.
-template <int NT>
-__device__ __forceinline__ void sum_partials(const double* __restrict__ part, int nb, double (&rs)[2], double* sh) {
-    rs[0] = 0.0; rs[1] = 0.0;
+template <int NT, typename Real>
+__device__ __forceinline__ void sum_partials(const Real* __restrict__ part, int nb, Real (&rs)[2], Real* sh) {
+    rs[0] = Real(0); rs[1] = Real(0);
     for (int b = threadIdx.x; b < nb; b += NT) { rs[0] += part[PCG_NP * b + PT_RR]; rs[1] += part[PCG_NP * b + PT_RZ]; }
     block_sums<NT, 2>(rs, sh);
 }
 
 // unknown-level rhs and diag(H_cc) from the image-level vectors; one wave per unknown so that
 // shared unknowns (one focal pair for every image of a camera) reduce in parallel
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_unk_setup(ba_pcg_args a) {
+    const PcgV<Real> av(a);
     const int lane = threadIdx.x & 63;
     if (blockIdx.x == 0 && threadIdx.x < 3)                  // k_leaf_max's accumulators
-        reinterpret_cast<unsigned long long*>(a.state)[ST_LEAFMAX + threadIdx.x] = 0ull;
+        av.state[ST_LEAFMAX + threadIdx.x] = Real(0);
     int64_t u = (int64_t)blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);
     if (u >= a.n_u) return;
-    double e = 0.0, g = 0.0;
+    Real e = Real(0), g = Real(0);
     for (int q = a.inv_ptr[u] + lane; q < a.inv_ptr[u + 1]; q += 64) {
         int src = a.inv_src[q];
-        e += a.e_img[src];
-        g += a.dg_img[src];
+        e += av.e_img[src];
+        g += av.dg_img[src];
     }
     for (int off = 32; off > 0; off >>= 1) {
         e += __shfl_down(e, off);
         g += __shfl_down(g, off);
     }
-    if (lane == 0) { a.rhs[u] = e; a.diagA[u] = g; }
+    if (lane == 0) { av.rhs[u] = e; av.diagA[u] = g; }
 }
 
 // per-leaf damping (BlockDiagMat.dampen_, ba_solver.py:575-582) and the Jacobi preconditioner.
@@ -116,12 +132,14 @@ __global__ void __launch_bounds__(PCG_T) k_unk_setup(ba_pcg_args a) {
 // an integer max of the bit patterns, which orders non-negative doubles as their values, so the
 // result does not depend on the order; a block whose maximum is NaN contributes nothing, as fmax
 // ignores NaN), then the damping and the clamped preconditioner diagonal per unknown.
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_leaf_max(ba_pcg_args a) {
-    __shared__ double sh[3][PCG_T];
-    double m[3] = {0.0, 0.0, 0.0};
+    const PcgV<Real> av(a);
+    __shared__ Real sh[3][PCG_T];
+    Real m[3] = {Real(0), Real(0), Real(0)};
     for (int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x; u < a.n_u; u += (int64_t)gridDim.x * PCG_T) {
         const int l = a.leaf[u];
-        if (l < 3) m[l] = fmax(m[l], fabs(a.diagA[u]));
+        if (l < 3) m[l] = fmax(m[l], fabs(av.diagA[u]));
     }
 #pragma unroll
     for (int l = 0; l < 3; ++l) sh[l][threadIdx.x] = m[l];
@@ -133,58 +151,62 @@ __global__ void __launch_bounds__(PCG_T) k_leaf_max(ba_pcg_args a) {
         __syncthreads();
     }
     if (threadIdx.x < 3) {
-        const double v = sh[threadIdx.x][0];
-        if (!isnan(v))
-            atomicMax(reinterpret_cast<unsigned long long*>(a.state) + ST_LEAFMAX + threadIdx.x,
-                      (unsigned long long)__double_as_longlong(v));
+        const Real mv = sh[threadIdx.x][0];
+        if (!isnan(mv)) atomic_max_nonneg(av.state + ST_LEAFMAX + threadIdx.x, mv);
     }
 }
 
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_leaf_damp(ba_pcg_args a) {
-    double lam[6];
+    const PcgV<Real> av(a);
+    Real lam[6];
 #pragma unroll
     for (int l = 0; l < 3; ++l) {
-        const double mx = __longlong_as_double(reinterpret_cast<const long long*>(a.state)[ST_LEAFMAX + l]);
-        lam[l] = a.adaptive ? a.dampen * mx : a.dampen;
-        lam[l + 3] = a.dampen;
+        const Real mx = av.state[ST_LEAFMAX + l];        // the bits k_leaf_max combined are the value's
+        lam[l] = a.adaptive ? Real(a.dampen) * mx : Real(a.dampen);
+        lam[l + 3] = Real(a.dampen);
     }
     for (int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x; u < a.n_u; u += (int64_t)gridDim.x * PCG_T) {
-        double dmp = lam[a.leaf[u]];
-        a.damp[u] = dmp;
-        double dA = a.diagA[u] + dmp;
-        a.diagA[u] = dA > 1e-12 ? dA : 1e-12;          // diagA.clamp(min=1e-12) (ba_solver.py:191-192)
+        Real dmp = lam[a.leaf[u]];
+        av.damp[u] = dmp;
+        Real dA = av.diagA[u] + dmp;
+        av.diagA[u] = dA > Real(1e-12) ? dA : Real(1e-12);          // diagA.clamp(min=1e-12) (ba_solver.py:191-192)
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
-        for (int l = 0; l < 3; ++l) a.state[ST_LEAF + l] = lam[l];
+        for (int l = 0; l < 3; ++l) av.state[ST_LEAF + l] = lam[l];
     }
 }
 
 // x = 0, r = b, z = M^-1 r, p_{-1} = 0 (so that p_0 = z_0); partials of b.b and r.z
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_pcg_init(ba_pcg_args a) {
-    __shared__ double sh[PCG_T];
+    const PcgV<Real> av(a);
+    __shared__ Real sh[PCG_T];
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    double t[2] = {0.0, 0.0};
+    Real t[2] = {Real(0), Real(0)};
     if (u < a.n_u) {
-        double b = a.rhs[u];
-        double z = b / a.diagA[u];
-        a.x[u] = 0.0; a.xbest[u] = 0.0; a.r[u] = b; a.z[u] = z; a.p[a.n_u + u] = 0.0;
+        Real b = av.rhs[u];
+        Real z = b / av.diagA[u];
+        av.x[u] = Real(0); av.xbest[u] = Real(0); av.r[u] = b; av.z[u] = z; av.p[a.n_u + u] = Real(0);
         t[0] = b * b; t[1] = b * z;
     }
     block_sums<PCG_T, 2>(t, sh);
-    if (threadIdx.x == 0) { a.partials[PCG_NP * blockIdx.x + PT_RR] = t[0]; a.partials[PCG_NP * blockIdx.x + PT_RZ] = t[1]; }
+    if (threadIdx.x == 0) { av.partials[PCG_NP * blockIdx.x + PT_RR] = t[0]; av.partials[PCG_NP * blockIdx.x + PT_RZ] = t[1]; }
 }
 
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
-    __shared__ double sh[PCG_T];
-    double rs[2];
-    sum_partials<PCG_T>(a.partials, nb, rs, sh);
-    const double bb = rs[0], rz = rs[1];
+    const PcgV<Real> av(a);
+    __shared__ Real sh[PCG_T];
+    Real rs[2];
+    sum_partials<PCG_T>(av.partials, nb, rs, sh);
+    const Real bb = rs[0], rz = rs[1];
     if (threadIdx.x == 0) {
-        double bn = sqrt(bb);
-        a.state[ST_BNORM] = bn > 1e-12 ? bn : 1e-12;    // torch.norm(b).clamp(min=1e-12)
-        a.state[ST_RZ0] = rz;
-        a.state[ST_BEST0] = INFINITY; a.state[ST_BEST1] = INFINITY;
-        a.state[ST_BETA] = 0.0;
+        Real bn = sqrt(bb);
+        av.state[ST_BNORM] = bn > Real(1e-12) ? bn : Real(1e-12);    // torch.norm(b).clamp(min=1e-12)
+        av.state[ST_RZ0] = rz;
+        av.state[ST_BEST0] = INFINITY; av.state[ST_BEST1] = INFINITY;
+        av.state[ST_BETA] = Real(0);
         a.istate[IS_DONE0] = a.maxiter <= 0; a.istate[IS_DONE1] = 0; a.istate[IS_K] = 0; a.istate[IS_CONV] = 0;
         a.istate[IS_BESTK] = 0;
         a.istate[IS_USEBEST] = 1;
@@ -196,7 +218,9 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
 // row j) read each column of a block contiguously.  S(i, i2) is S_p for tr = 0 and S_p^T for tr = 1.
 // row_u[q][j2] = umap[i2][j2] (-1 past d, gw entries per block: 16 for d <= 16, else 32): the unknowns
 // the block multiplies.  One thread per (entry, element), max(d^2, gw) elements per entry.
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int per, int gw) {
+    const PcgV<Real> av(a);
     const int d = a.d, dd = d * d;
     const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
     if (tid >= n_ent * per) return;
@@ -207,7 +231,7 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
         const int64_t i = q / a.row_cap, k = q - i * a.row_cap;
         qs = a.row_ptr[i] + k;
         if (qs >= a.row_ptr[i + 1]) {                  // past the row's end: a zero block, no unknowns
-            if (e < dd) a.S_rows[q * dd + e] = 0.0;
+            if (e < dd) av.S_rows[q * dd + e] = Real(0);
             if (e < gw) a.row_u[q * gw + e] = -1;
             return;
         }
@@ -216,8 +240,8 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
     const int64_t p = ent >> 1;
     if (e < dd) {
         const int j2 = e / d, j = e - (e / d) * d;
-        const double* S = a.S_pairs + p * dd;
-        a.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
+        const Real* S = av.S_pairs + p * dd;
+        av.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
     }
     if (e < gw) {
         const int i2 = (ent & 1) ? a.pair_i1[p] : a.pair_i2[p];
@@ -237,7 +261,7 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 //   k_pcg_update(n)  alpha, A p of the block's unknowns (one thread per short inverse list, one
 //                    wave per long one), x, r, z, the stored p_n, and the block partials of r.r
 //                    and r.z.
-// p is double-buffered (p_n in slot n & 1).  A launch after the stopping point returns at once: the
+// p is Real-buffered (p_n in slot n & 1).  A launch after the stopping point returns at once: the
 // flag "stopped before update n" lives in IS_DONE0 + (n & 1) and is written by k_pcg_spmv(n - 1).
 
 // y_img[i][j] = sum over the blocks of image row i of S(i, i2)[j, :] . p(i2): one workgroup of
@@ -245,78 +269,79 @@ __global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_e
 // (PCG_ST / 16)-th block of the row.  Lane j2 of a group forms p_n at the block's column unknown j2 and the group shares the
 // 16 values by shuffles; the group sums are added in LDS in a fixed order.  The operands of the
 // first pass, the row's own unknowns and the partial sums are requested before any of them is used.
-template <int GW>
+template <int GW, typename Real>
 __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int nb) {
-    __shared__ double sh[PCG_ST];
-    __shared__ double sDamp[PCG_ST / 64];
+    const PcgV<Real> av(a);
+    __shared__ Real sh[PCG_ST];
+    __shared__ Real sDamp[PCG_ST / 64];
     const int i = blockIdx.x;
     const int grp = threadIdx.x / GW, j = threadIdx.x % GW;
     const int d = a.d, dd = d * d;
-    const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
+    const Real* __restrict__ pold = av.p + (int64_t)((n + 1) & 1) * a.n_u;
     // operands that depend on nothing are requested first: each thread's first block partials of
     // update n - 1, the scalar state, and (threads 0..d-1) the row's own unknowns with z and p_{n-1}
-    double pr0 = 0.0, pr1 = 0.0;
-    if (threadIdx.x < nb) { pr0 = a.partials[PCG_NP * threadIdx.x + PT_RR]; pr1 = a.partials[PCG_NP * threadIdx.x + PT_RZ]; }
-    const double best = a.state[ST_BEST0 + ((n - 1) & 1)], rz_old = a.state[ST_RZ0 + ((n - 1) & 1)];
-    const double bnorm = a.state[ST_BNORM];
+    Real pr0 = Real(0), pr1 = Real(0);
+    if (threadIdx.x < nb) { pr0 = av.partials[PCG_NP * threadIdx.x + PT_RR]; pr1 = av.partials[PCG_NP * threadIdx.x + PT_RZ]; }
+    const Real best = av.state[ST_BEST0 + ((n - 1) & 1)], rz_old = av.state[ST_RZ0 + ((n - 1) & 1)];
+    const Real bnorm = av.state[ST_BNORM];
     int uo = -1;
-    double zo = 0.0, po = 0.0;
+    Real zo = Real(0), po = Real(0);
     if (threadIdx.x < GW && j < d) {
         uo = a.umap[(int64_t)i * d + j];
-        if (uo >= 0) { zo = a.z[uo]; po = pold[uo]; }
+        if (uo >= 0) { zo = av.z[uo]; po = pold[uo]; }
     }
     // the row's blocks: from the fixed capacity when set (no load on this chain), else from row_ptr
     const int q0 = a.row_cap > 0 ? i * a.row_cap : a.row_ptr[i];
     const int q1 = a.row_cap > 0 ? q0 + a.row_cap : a.row_ptr[i + 1];
-    auto load = [&](int q, int& u, double& zv, double& pv, double (&bcol)[GW]) {
+    auto load = [&](int q, int& u, Real& zv, Real& pv, Real (&bcol)[GW]) {
         const bool live = q < q1;
         u = live ? a.row_u[(int64_t)q * GW + j] : -1;
-        zv = 0.0; pv = 0.0;
-        if (u >= 0) { zv = a.z[u]; pv = pold[u]; }
-        const double* B = a.S_rows + (int64_t)q * dd;
+        zv = Real(0); pv = Real(0);
+        if (u >= 0) { zv = av.z[u]; pv = pold[u]; }
+        const Real* B = av.S_rows + (int64_t)q * dd;
 #pragma unroll
-        for (int j2 = 0; j2 < GW; ++j2) bcol[j2] = (live && j < d && j2 < d) ? B[j2 * d + j] : 0.0;
+        for (int j2 = 0; j2 < GW; ++j2) bcol[j2] = (live && j < d && j2 < d) ? B[j2 * d + j] : Real(0);
     };
-    auto mac = [&](int u, double zv, double pv, double beta, const double (&bcol)[GW], double acc) {
-        const double xj = u >= 0 ? pdir(zv, pv, beta) : 0.0;
+    auto mac = [&](int u, Real zv, Real pv, Real beta, const Real (&bcol)[GW], Real acc) {
+        const Real xj = u >= 0 ? pdir(zv, pv, beta) : Real(0);
 #pragma unroll
         for (int j2 = 0; j2 < GW; ++j2) acc += bcol[j2] * __shfl(xj, j2, GW);
         return acc;
     };
     int u;
-    double zv, pv, bcol[GW];
+    Real zv, pv, bcol[GW];
     load(q0 + grp, u, zv, pv, bcol);                 // requested before the done flag is known
     // damping term of the unknowns v = i + k n_imgs (thread k): its first operands are requested now
     const int64_t v0 = i + (int64_t)threadIdx.x * a.n_imgs;
-    double dz = 0.0, dpo = 0.0, dd0 = 0.0;
-    if (v0 < a.n_u) { dz = a.z[v0]; dpo = pold[v0]; dd0 = a.damp[v0]; }
+    Real dz = Real(0), dpo = Real(0), dd0 = Real(0);
+    if (v0 < a.n_u) { dz = av.z[v0]; dpo = pold[v0]; dd0 = av.damp[v0]; }
     if (a.istate[IS_DONE0 + (n & 1)]) {
         if (blockIdx.x == 0 && threadIdx.x == 0) a.istate[IS_DONE0 + ((n + 1) & 1)] = 1;
         return;
     }
 
-    double beta = 0.0;
+    Real beta = Real(0);
     if (n >= 1) {
         // end of update n - 1 (ba_solver.py:1222-1236)
-        double rs[2] = {0.0, 0.0};
+        Real rs[2] = {Real(0), Real(0)};
         if (threadIdx.x < nb) { rs[0] += pr0; rs[1] += pr1; }     // the order of sum_partials
-        for (int b = threadIdx.x + PCG_ST; b < nb; b += PCG_ST) { rs[0] += a.partials[PCG_NP * b + PT_RR]; rs[1] += a.partials[PCG_NP * b + PT_RZ]; }
+        for (int b = threadIdx.x + PCG_ST; b < nb; b += PCG_ST) { rs[0] += av.partials[PCG_NP * b + PT_RR]; rs[1] += av.partials[PCG_NP * b + PT_RZ]; }
         block_sums<PCG_ST, 2>(rs, sh);
-        const double rr = rs[0], rz_new = rs[1];
-        const double rnorm = sqrt(rr);
+        const Real rr = rs[0], rz_new = rs[1];
+        const Real rnorm = sqrt(rr);
         const bool improved = rnorm < best;
-        const bool conv = rnorm <= a.tol * bnorm;
+        const bool conv = rnorm <= Real(a.tol) * bnorm;
         const bool bad = !isfinite(rz_new);
         const bool stop = conv || bad || n >= a.maxiter;
-        beta = rz_new / (rz_old > 1e-32 ? rz_old : 1e-32);
+        beta = rz_new / (rz_old > Real(1e-32) ? rz_old : Real(1e-32));
         if (improved)                                    // best_so_far = r_norm, x, k
             for (int64_t v = (int64_t)blockIdx.x * PCG_ST + threadIdx.x; v < a.n_u; v += (int64_t)gridDim.x * PCG_ST)
-                a.xbest[v] = a.x[v];
+                av.xbest[v] = av.x[v];
         if (blockIdx.x == 0 && threadIdx.x == 0) {
-            a.state[ST_BEST0 + (n & 1)] = improved ? rnorm : best;
+            av.state[ST_BEST0 + (n & 1)] = improved ? rnorm : best;
             if (improved) a.istate[IS_BESTK] = n;
-            a.state[ST_RZ0 + (n & 1)] = rz_new;
-            a.state[ST_BETA] = beta;
+            av.state[ST_RZ0 + (n & 1)] = rz_new;
+            av.state[ST_BETA] = beta;
             a.istate[IS_K] = n;
             if (conv) { a.istate[IS_CONV] = 1; a.istate[IS_USEBEST] = 0; }
             a.istate[IS_DONE0 + ((n + 1) & 1)] = stop;
@@ -325,17 +350,17 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     } else if (blockIdx.x == 0 && threadIdx.x == 0) {
         a.istate[IS_DONE0 + 1] = 0;
     }
-    double dsum = 0.0;
+    Real dsum = Real(0);
     {
-        const double pv0 = pdir(dz, dpo, beta);
+        const Real pv0 = pdir(dz, dpo, beta);
         dsum = dd0 * pv0 * pv0;
         for (int64_t v = v0 + (int64_t)PCG_ST * a.n_imgs; v < a.n_u; v += (int64_t)PCG_ST * a.n_imgs) {
-            const double pv2 = pdir(a.z[v], pold[v], beta);
-            dsum += a.damp[v] * pv2 * pv2;
+            const Real pv2 = pdir(av.z[v], pold[v], beta);
+            dsum += av.damp[v] * pv2 * pv2;
         }
         dsum = wave_sum(dsum);
     }
-    double acc = mac(u, zv, pv, beta, bcol, 0.0);
+    Real acc = mac(u, zv, pv, beta, bcol, Real(0));
     for (int qb = q0 + PCG_ST / GW; qb < q1; qb += PCG_ST / GW) {     // the row's further blocks
         load(qb + grp, u, zv, pv, bcol);
         acc = mac(u, zv, pv, beta, bcol, acc);
@@ -347,19 +372,19 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
     // y of this image row; the row's share of p.Ap: sum_e p_u(e) y_e over its entries (one wave,
     // 16 rows at most) plus the damping sum of its unknowns
     if (threadIdx.x < 64) {
-        double part = 0.0;
+        Real part = Real(0);
         if (j < d && threadIdx.x < GW) {
-            double t = 0.0;
+            Real t = Real(0);
             for (int g = 0; g < PCG_ST / GW; ++g) t += sh[GW * g + j];
-            a.y_img[(int64_t)i * d + j] = t;
+            av.y_img[(int64_t)i * d + j] = t;
             if (uo >= 0) part = pdir(zo, po, beta) * t;
         }
         part = wave_sum(part);
         if (threadIdx.x == 0) {
-            double dt = 0.0;
+            Real dt = Real(0);
 #pragma unroll
             for (int w = 0; w < PCG_ST / 64; ++w) dt += sDamp[w];
-            a.img_part[i] = part + dt;
+            av.img_part[i] = part + dt;
         }
     }
 }
@@ -369,29 +394,31 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
 // unknown u is the sum of the image-level rows mapping to u plus damp[u] p_n[u]: one thread sums a
 // list of at most BA_PCG_LONG_LIST entries; the block's long lists (a focal pair shared by every
 // image of a camera) are summed first, one wave each, 8 entries per lane in flight, into LDS.
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
-    __shared__ double sh[2 * (PCG_T / 64)];
-    __shared__ double sLong[PCG_T];
+    const PcgV<Real> av(a);
+    __shared__ Real sh[2 * (PCG_T / 64)];
+    __shared__ Real sLong[PCG_T];
     // requested first: the image partials of p.Ap (the first PCG_IPF of each thread) and the scalars
-    double ipf[PCG_IPF];
+    Real ipf[PCG_IPF];
 #pragma unroll
     for (int k = 0; k < PCG_IPF; ++k) {
         const int b = threadIdx.x + k * PCG_T;
-        ipf[k] = b < a.n_imgs ? a.img_part[b] : 0.0;
+        ipf[k] = b < a.n_imgs ? av.img_part[b] : Real(0);
     }
-    const double beta = a.state[ST_BETA], rz = a.state[ST_RZ0 + (n & 1)];
+    const Real beta = av.state[ST_BETA], rz = av.state[ST_RZ0 + (n & 1)];
     if (a.istate[IS_DONE0 + ((n + 1) & 1)]) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    const double* __restrict__ pold = a.p + (int64_t)((n + 1) & 1) * a.n_u;
-    double zu = 0.0, pu = 0.0, xu = 0.0, ru = 0.0, du = 1.0, dmp = 0.0, y1 = 0.0;
+    const Real* __restrict__ pold = av.p + (int64_t)((n + 1) & 1) * a.n_u;
+    Real zu = Real(0), pu = Real(0), xu = Real(0), ru = Real(0), du = Real(1), dmp = Real(0), y1 = Real(0);
     int q0 = 0, q1 = 0, li = -1, s1 = -1;
     if (u < a.n_u) {                                   // operands first, then the reductions
-        zu = a.z[u]; pu = pold[u]; xu = a.x[u]; ru = a.r[u]; du = a.diagA[u]; dmp = a.damp[u];
+        zu = av.z[u]; pu = pold[u]; xu = av.x[u]; ru = av.r[u]; du = av.diagA[u]; dmp = av.damp[u];
         li = a.long_idx[u];
         if (a.src1 != nullptr) {                       // a one-entry list resolved ahead
             s1 = a.src1[u];
-            if (s1 >= 0) y1 = a.y_img[s1];
+            if (s1 >= 0) y1 = av.y_img[s1];
         }
         if (s1 < 0) { q0 = a.inv_ptr[u]; q1 = a.inv_ptr[u + 1]; }
     }
@@ -404,45 +431,45 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_update(ba_pcg_args a, int n) {
             const int v = a.long_u[k];
             b0 = a.inv_ptr[v]; b1 = a.inv_ptr[v + 1];
         }
-        double s = 0.0;
+        Real s = Real(0);
         for (int q = b0 + lane; q < b1; q += 64 * PCG_LF) {
             int src[PCG_LF];
 #pragma unroll
             for (int t = 0; t < PCG_LF; ++t) src[t] = q + 64 * t < b1 ? a.inv_src[q + 64 * t] : -1;
 #pragma unroll
-            for (int t = 0; t < PCG_LF; ++t) s += src[t] >= 0 ? a.y_img[src[t]] : 0.0;
+            for (int t = 0; t < PCG_LF; ++t) s += src[t] >= 0 ? av.y_img[src[t]] : Real(0);
         }
         s = wave_sum(s);
         if (lane == 0) sLong[k - lk0] = s;
     }
     // the short lists: y_img is complete at launch, so these sums need nothing from the reductions
-    double ys = 0.0;
+    Real ys = Real(0);
     if (s1 >= 0)
-        ys = 0.0 + y1;                                 // the same sum as the one-entry loop below
+        ys = Real(0) + y1;                                 // the same sum as the one-entry loop below
     else if (li < 0)
-        for (int q = q0; q < q1; ++q) ys += a.y_img[a.inv_src[q]];
-    double sums[1] = {0.0};
+        for (int q = q0; q < q1; ++q) ys += av.y_img[a.inv_src[q]];
+    Real sums[1] = {Real(0)};
 #pragma unroll
     for (int k = 0; k < PCG_IPF; ++k)
         if (threadIdx.x + k * PCG_T < a.n_imgs) sums[0] += ipf[k];
-    for (int b = threadIdx.x + PCG_IPF * PCG_T; b < a.n_imgs; b += PCG_T) sums[0] += a.img_part[b];
+    for (int b = threadIdx.x + PCG_IPF * PCG_T; b < a.n_imgs; b += PCG_T) sums[0] += av.img_part[b];
     block_sums<PCG_T, 1>(sums, sh);                    // p.Ap (its barriers also publish sLong)
-    const double pap = sums[0];
-    const double denom = pap > 1e-32 ? pap : 1e-32;
-    const double alpha = rz / denom;
-    double t[PCG_NP] = {0.0, 0.0};
+    const Real pap = sums[0];
+    const Real denom = pap > Real(1e-32) ? pap : Real(1e-32);
+    const Real alpha = rz / denom;
+    Real t[PCG_NP] = {Real(0), Real(0)};
     if (u < a.n_u) {
-        const double pn = pdir(zu, pu, beta);
-        const double apu = (li >= 0 ? sLong[li] : ys) + dmp * pn;
-        a.p[(int64_t)(n & 1) * a.n_u + u] = pn;
-        const double x = xu + alpha * pn;
-        const double r = ru - alpha * apu;
-        const double z = r / du;
-        a.x[u] = x; a.r[u] = r; a.z[u] = z;
+        const Real pn = pdir(zu, pu, beta);
+        const Real apu = (li >= 0 ? sLong[li] : ys) + dmp * pn;
+        av.p[(int64_t)(n & 1) * a.n_u + u] = pn;
+        const Real x = xu + alpha * pn;
+        const Real r = ru - alpha * apu;
+        const Real z = r / du;
+        av.x[u] = x; av.r[u] = r; av.z[u] = z;
         t[PT_RR] = r * r; t[PT_RZ] = r * z;
     }
     block_sums<PCG_T, PCG_NP>(t, sh);
-    if (threadIdx.x < PCG_NP) a.partials[PCG_NP * blockIdx.x + threadIdx.x] = threadIdx.x == 0 ? t[0] : t[1];
+    if (threadIdx.x < PCG_NP) av.partials[PCG_NP * blockIdx.x + threadIdx.x] = threadIdx.x == 0 ? t[0] : t[1];
 }
 
 // the flag "stopped before update n" (read once the launches before it have run) to memory the host reads
@@ -452,9 +479,11 @@ __global__ void k_pcg_stopped(const int32_t* __restrict__ flag, int32_t* out) {
 }
 
 // result: x if converged else the best iterate
+template <typename Real>
 __global__ void __launch_bounds__(PCG_T) k_pcg_result(ba_pcg_args a) {
+    const PcgV<Real> av(a);
     int64_t u = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    if (u < a.n_u && a.istate[IS_USEBEST]) a.x[u] = a.xbest[u];
+    if (u < a.n_u && a.istate[IS_USEBEST]) av.x[u] = av.xbest[u];
 }
 
 }  // namespace ba
@@ -474,15 +503,52 @@ namespace ba {
 // the direct solve that shares them: rhs = P^T e_img, damp per leaf, diagA = clamp(P^T dg_img + damp).
 int unknown_setup(const ba_pcg_args& a, hipStream_t st) {
     if (a.n_u == 0) return BA_OK;
+    BA_REQUIRE(!a.real32, "the direct reduced solve runs in fp64 only (real32 = 0)");
     const unsigned nb = nb_of(a.n_u);
     const unsigned nbw = (unsigned)((a.n_u + PCG_T / 64 - 1) / (PCG_T / 64));
-    hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
-    hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_unk_setup<double>, dim3(nbw), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_max<double>, dim3(nb), dim3(PCG_T), 0, st, a);
+    hipLaunchKernelGGL(k_leaf_damp<double>, dim3(nb), dim3(PCG_T), 0, st, a);
     BA_LAUNCHED();
     return BA_OK;
 }
 }  // namespace ba
+
+// the launches of ba_pcg_solve_range in the working precision Real
+template <typename Real>
+static void pcg_launch(const ba_pcg_args& a, int32_t it0, int32_t it1, int32_t finish, int32_t* stopped_out,
+                       int64_t n_ent, unsigned nb, unsigned nbw, hipStream_t st) {
+    const int gw = a.d <= 16 ? 16 : 32;               // lanes per block row group of the SpMV (row_u stride)
+    const int per = a.d * a.d > gw ? a.d * a.d : gw;
+    if (it0 == 0) {                                  // the setup precedes iteration 0
+        if (n_ent > 0)
+            hipLaunchKernelGGL(k_rows_build<Real>, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0,
+                               st, a, n_ent, per, gw);
+        hipLaunchKernelGGL(k_unk_setup<Real>, dim3(nbw), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_leaf_max<Real>, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_leaf_damp<Real>, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_pcg_init<Real>, dim3(nb), dim3(PCG_T), 0, st, a);
+        hipLaunchKernelGGL(k_pcg_init2<Real>, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
+    }
+    auto spmv = [&](int it) {
+        if (gw == 16)
+            hipLaunchKernelGGL((k_pcg_spmv<16, Real>), dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+        else
+            hipLaunchKernelGGL((k_pcg_spmv<32, Real>), dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
+    };
+    for (int it = it0; it < it1; ++it) {
+        spmv(it);
+        hipLaunchKernelGGL(k_pcg_update<Real>, dim3(nb), dim3(PCG_T), 0, st, a, it);
+    }
+    if (finish) {
+        // the decisions after update it1 - 1 (after the last update, or a launch that returns at once once
+        // the loop has stopped), then the result
+        spmv(it1);
+        hipLaunchKernelGGL(k_pcg_result<Real>, dim3(nb), dim3(PCG_T), 0, st, a);
+    } else if (stopped_out != nullptr) {
+        hipLaunchKernelGGL(k_pcg_stopped, dim3(1), dim3(64), 0, st, a.istate + IS_DONE0 + (it1 & 1), stopped_out);
+    }
+}
 
 extern "C" int ba_pcg_solve_range(const ba_pcg_args* args, int32_t it0, int32_t it1, int32_t finish,
                                   int32_t* stopped_out, void* stream) {
@@ -507,35 +573,8 @@ extern "C" int ba_pcg_solve_range(const ba_pcg_args* args, int32_t it0, int32_t 
     BA_REQUIRE(a.row_cap >= 0 && a.row_cap % (PCG_ST / 16) == 0, "row_cap must be a multiple of 8");
     const int64_t n_ent = a.row_cap > 0 ? (int64_t)a.n_imgs * a.row_cap : a.n_row_ent;
     BA_REQUIRE(n_ent >= 0 && a.S_rows != nullptr && a.row_u != nullptr, "image-row block workspace missing");
-    const int gw = a.d <= 16 ? 16 : 32;               // lanes per block row group of the SpMV (row_u stride)
-    const int per = a.d * a.d > gw ? a.d * a.d : gw;
-    if (it0 == 0) {                                  // the setup precedes iteration 0
-        if (n_ent > 0)
-            hipLaunchKernelGGL(k_rows_build, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0, st, a,
-                               n_ent, per, gw);
-        hipLaunchKernelGGL(k_unk_setup, dim3(nbw), dim3(PCG_T), 0, st, a);
-        hipLaunchKernelGGL(k_leaf_max, dim3(nb), dim3(PCG_T), 0, st, a);
-        hipLaunchKernelGGL(k_leaf_damp, dim3(nb), dim3(PCG_T), 0, st, a);
-        hipLaunchKernelGGL(k_pcg_init, dim3(nb), dim3(PCG_T), 0, st, a);
-        hipLaunchKernelGGL(k_pcg_init2, dim3(1), dim3(PCG_T), 0, st, a, (int)nb);
-    }
-    BA_LAUNCHED();
-    auto spmv = [&](int it) {
-        if (gw == 16) hipLaunchKernelGGL(k_pcg_spmv<16>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
-        else          hipLaunchKernelGGL(k_pcg_spmv<32>, dim3((unsigned)a.n_imgs), dim3(PCG_ST), 0, st, a, it, (int)nb);
-    };
-    for (int it = it0; it < it1; ++it) {
-        spmv(it);
-        hipLaunchKernelGGL(k_pcg_update, dim3(nb), dim3(PCG_T), 0, st, a, it);
-    }
-    if (finish) {
-        // the decisions after update it1 - 1 (after the last update, or a launch that returns at once once
-        // the loop has stopped), then the result
-        spmv(it1);
-        hipLaunchKernelGGL(k_pcg_result, dim3(nb), dim3(PCG_T), 0, st, a);
-    } else if (stopped_out != nullptr) {
-        hipLaunchKernelGGL(k_pcg_stopped, dim3(1), dim3(64), 0, st, a.istate + IS_DONE0 + (it1 & 1), stopped_out);
-    }
+    if (a.real32) pcg_launch<float>(a, it0, it1, finish, stopped_out, n_ent, nb, nbw, st);
+    else          pcg_launch<double>(a, it0, it1, finish, stopped_out, n_ent, nb, nbw, st);
     BA_LAUNCHED();
     return BA_OK;
 }

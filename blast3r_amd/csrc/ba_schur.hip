@@ -22,6 +22,7 @@
 namespace ba {
 
 typedef double dbl4 __attribute__((ext_vector_type(4)));
+typedef float flt4 __attribute__((ext_vector_type(4)));
 
 typedef ba_layout LinLayout;
 typedef ba_lin_args LinArgs;
@@ -210,21 +211,23 @@ __device__ __forceinline__ void point_rows(const ObsCore& o, const CamF& cp, boo
 }
 
 // Damped point block -> Cholesky factor with the chol3x3_solve rules (.cu:560-634):
-// + jitter on the diagonal, averaged off-diagonals, non-positive pivots + jitter.
-__device__ __forceinline__ void chol3_factor(const double H[6], double lam, double L[6]) {
-    const double jit = 1e-12;
-    double a00 = (H[0] + lam) + jit, a11 = (H[3] + lam) + jit, a22 = (H[5] + lam) + jit;
-    double a01 = H[1], a02 = H[2], a12 = H[4];
-    a00 = a00 > 0.0 ? a00 : a00 + jit;
-    double l00 = sqrt(a00);
-    double l10 = a01 / l00, l20 = a02 / l00;
-    double t11 = a11 - l10 * l10;
-    t11 = t11 > 0.0 ? t11 : t11 + jit;
-    double l11 = sqrt(t11);
-    double l21 = (a12 - l10 * l20) / l11;
-    double t22 = a22 - l20 * l20 - l21 * l21;
-    t22 = t22 > 0.0 ? t22 : t22 + jit;
-    double l22 = sqrt(t22);
+// + jitter on the diagonal, averaged off-diagonals, non-positive pivots + jitter; in the working
+// precision R (the reference's fp32 solver factors its fp32 blocks in fp32).
+template <typename R>
+__device__ __forceinline__ void chol3_factor(const R H[6], R lam, R L[6]) {
+    const R jit = R(1e-12);
+    R a00 = (H[0] + lam) + jit, a11 = (H[3] + lam) + jit, a22 = (H[5] + lam) + jit;
+    R a01 = H[1], a02 = H[2], a12 = H[4];
+    a00 = a00 > R(0) ? a00 : a00 + jit;
+    R l00 = sqrt(a00);
+    R l10 = a01 / l00, l20 = a02 / l00;
+    R t11 = a11 - l10 * l10;
+    t11 = t11 > R(0) ? t11 : t11 + jit;
+    R l11 = sqrt(t11);
+    R l21 = (a12 - l10 * l20) / l11;
+    R t22 = a22 - l20 * l20 - l21 * l21;
+    t22 = t22 > R(0) ? t22 : t22 + jit;
+    R l22 = sqrt(t22);
     L[0] = l00; L[1] = l10; L[2] = l20; L[3] = l11; L[4] = l21; L[5] = l22;
 }
 
@@ -359,13 +362,16 @@ __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 wa
 }
 
 // lam_p = dampen * max diag over all tracks (BlockDiagMat.dampen_, ba_solver.py:575-582).
-// The maximum of non-negative doubles is the maximum of their bit patterns, so blocks combine with
-// an integer atomic max into word n of cmax (cleared by k_lam_clear); the result is order-free.
-__global__ void k_lam_clear(double* __restrict__ cmax, int64_t n) { cmax[n] = 0.0; }
+// The maximum of non-negative floating-point values is the maximum of their bit patterns, so blocks
+// combine with an integer atomic max into word n of cmax (cleared by k_lam_clear); the result is
+// order-free.
+template <typename R>
+__global__ void k_lam_clear(R* __restrict__ cmax, int64_t n) { cmax[n] = R(0); }
 
-__global__ void __launch_bounds__(256) k_lam_reduce(double* __restrict__ cmax, int64_t n) {
-    __shared__ double s[256];
-    double m = 0.0;
+template <typename R>
+__global__ void __launch_bounds__(256) k_lam_reduce(R* __restrict__ cmax, int64_t n) {
+    __shared__ R s[256];
+    R m = R(0);
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) m = fmax(m, cmax[i]);
     s[threadIdx.x] = m;
     __syncthreads();
@@ -373,36 +379,38 @@ __global__ void __launch_bounds__(256) k_lam_reduce(double* __restrict__ cmax, i
         if ((int)threadIdx.x < w) s[threadIdx.x] = fmax(s[threadIdx.x], s[threadIdx.x + w]);
         __syncthreads();
     }
-    if (threadIdx.x == 0)
-        atomicMax(reinterpret_cast<unsigned long long*>(cmax + n), (unsigned long long)__double_as_longlong(s[0]));
+    if (threadIdx.x == 0) atomic_max_nonneg(cmax + n, s[0]);
 }
 
-__global__ void k_lam_final(const double* __restrict__ cmax, int64_t n, double dampen, int adaptive, int x_off,
-                            double* __restrict__ out) {
-    out[0] = (adaptive && !x_off) ? dampen * cmax[n] : dampen;
+template <typename R>
+__global__ void k_lam_final(const R* __restrict__ cmax, int64_t n, double dampen, int adaptive, int x_off,
+                            R* __restrict__ out) {
+    out[0] = (adaptive && !x_off) ? R(dampen) * cmax[n] : R(dampen);
 }
 
 // Point factors of every chunk track once the damping value is known: L = chol(H_pp + lam_p I) with
-// the chol3x3_solve rules, w = L^-1 g_p and the reciprocal pivots, 12 doubles per chunk track
-// (L0..L5 | w0 w1 w2 | 1/L0 1/L3 1/L5), read by the camera-pair kernel two doubles per copy.
-__global__ void __launch_bounds__(256) k_point_factor(const double* __restrict__ Hpp, const double* __restrict__ gp,
-                                                      const double* __restrict__ lam_p, int64_t n_ct,
-                                                      double* __restrict__ pf) {
+// the chol3x3_solve rules, w = L^-1 g_p and the reciprocal pivots, 12 values per chunk track
+// (L0..L5 | w0 w1 w2 | 1/L0 1/L3 1/L5), read by the camera-pair kernel two values per copy; in the
+// working precision R.
+template <typename R>
+__global__ void __launch_bounds__(256) k_point_factor(const R* __restrict__ Hpp, const R* __restrict__ gp,
+                                                      const R* __restrict__ lam_p, int64_t n_ct, R* __restrict__ pf) {
+    typedef R R2 __attribute__((ext_vector_type(2)));
     const int64_t ct = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (ct >= n_ct) return;
-    double H[6], Lf[6];
-    const double2* h2 = reinterpret_cast<const double2*>(Hpp + 6 * ct);      // 16-byte aligned rows
+    R H[6], Lf[6];
+    const R2* h2 = reinterpret_cast<const R2*>(Hpp + 6 * ct);                // 16-byte aligned rows (fp64)
 #pragma unroll
-    for (int k = 0; k < 3; ++k) { const double2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
+    for (int k = 0; k < 3; ++k) { const R2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
     chol3_factor(H, lam_p[0], Lf);
-    const double r0 = 1.0 / Lf[0], r1 = 1.0 / Lf[3], r2 = 1.0 / Lf[5];
-    const double g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
-    const double w0 = g0 * r0;
-    const double w1 = (g1 - Lf[1] * w0) * r1;
-    const double w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
-    double2* o = reinterpret_cast<double2*>(pf + 12 * ct);
-    o[0] = make_double2(Lf[0], Lf[1]); o[1] = make_double2(Lf[2], Lf[3]); o[2] = make_double2(Lf[4], Lf[5]);
-    o[3] = make_double2(w0, w1); o[4] = make_double2(w2, r0); o[5] = make_double2(r1, r2);
+    const R r0 = R(1) / Lf[0], r1 = R(1) / Lf[3], r2 = R(1) / Lf[5];
+    const R g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
+    const R w0 = g0 * r0;
+    const R w1 = (g1 - Lf[1] * w0) * r1;
+    const R w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
+    R2* o = reinterpret_cast<R2*>(pf + 12 * ct);
+    o[0] = (R2){Lf[0], Lf[1]}; o[1] = (R2){Lf[2], Lf[3]}; o[2] = (R2){Lf[4], Lf[5]};
+    o[3] = (R2){w0, w1}; o[4] = (R2){w2, r0}; o[5] = (R2){r1, r2};
 }
 
 // ----------------------------------------------------------------------------- camera-pair blocks
@@ -1011,21 +1019,21 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
         BA_REQUIRE(miss == nullptr, miss);
     }
     if (stage == 0) {
-        hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks);
+        hipLaunchKernelGGL(k_lam_clear<double>, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks);
         if (a.n_chunks > 0) {
             BA_REQUIRE(a.n_ctracks >= 1 && a.ct_pt != nullptr, "chunk-track state missing");
             BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0,
                                                      st, a));
             const int64_t nb = a.n_chunks < 256 * 256 ? (a.n_chunks + 255) / 256 : 256;
-            hipLaunchKernelGGL(k_lam_reduce, dim3((unsigned)nb), dim3(256), 0, st, a.chunk_max, a.n_chunks);
+            hipLaunchKernelGGL(k_lam_reduce<double>, dim3((unsigned)nb), dim3(256), 0, st, a.chunk_max, a.n_chunks);
         }
-        hipLaunchKernelGGL(k_lam_final, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen, a.lay.adaptive,
-                           a.lay.x_off, a.lam_p);
+        hipLaunchKernelGGL(k_lam_final<double>, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen,
+                           a.lay.adaptive, a.lay.x_off, a.lam_p);
         if (a.n_chunks > 0) {
             BA_REQUIRE(a.pfac != nullptr, "point-factor scratch missing");
             BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
-            hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
-                               a.n_ctracks, a.pfac);
+            hipLaunchKernelGGL(k_point_factor<double>, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, a.Hpp, a.gp,
+                               a.lam_p, a.n_ctracks, a.pfac);
         }
         BA_LAUNCHED();
         return BA_OK;
@@ -1152,37 +1160,60 @@ __device__ __forceinline__ double jc_elem(const ObsCore& o, const LinLayout& lay
     return u * o.sW[R];
 }
 
+// The 16 x 16 x 4 MFMA of the working precision: A[i][k] from lane i + 16 k, B[k][j] from lane
+// j + 16 k (both kinds); the four accumulator values of a lane are column lane & 15 of rows
+// row(lane, v), which the two kinds lay out differently.
+template <typename Real>
+struct PmMfma;
+template <>
+struct PmMfma<double> {
+    typedef dbl4 V4;
+    static __device__ __forceinline__ V4 mac(double a, double b, V4 c) {
+        return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int row(int lane, int v) { return 4 * v + (lane >> 4); }
+};
+template <>
+struct PmMfma<float> {
+    typedef flt4 V4;
+    static __device__ __forceinline__ V4 mac(float a, float b, V4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int row(int lane, int v) { return 4 * (lane >> 4) + v; }
+};
+
 // One wave's running sum of X^T X (or -X^T X) over the rows it staged for one image: the lower
-// DP/16 x DP/16 tiles of v_mfma_f64_16x16x4f64, flushed to the slot (wave + image) when the image
-// changes.  Column d of every staged row holds its right-hand-side value, so row d of the sum is
-// the image's rhs part.  A slot (w, i) is unique: obs (runs) are image-sorted, so waves w and w + 1
-// cannot hold images i + 1 and i respectively.
-template <int DP>
+// DP/16 x DP/16 tiles of the working precision's 16 x 16 x 4 MFMA, flushed to the slot (wave +
+// image) when the image changes.  Column d of every staged row holds its right-hand-side value, so
+// row d of the sum is the image's rhs part.  A slot (w, i) is unique: obs (runs) are image-sorted,
+// so waves w and w + 1 cannot hold images i + 1 and i respectively.
+template <int DP, typename Real>
 struct PmTileAcc {
+    typedef PmMfma<Real> M;
     static constexpr int NT = DP / 16, NTL = NT * (NT + 1) / 2;
-    dbl4 acc[NTL];
+    typename M::V4 acc[NTL];
     int img;
     __device__ __forceinline__ void zero() {
 #pragma unroll
-        for (int q = 0; q < NTL; ++q) acc[q] = (dbl4){0.0, 0.0, 0.0, 0.0};
+        for (int q = 0; q < NTL; ++q) acc[q] = (typename M::V4){Real(0), Real(0), Real(0), Real(0)};
     }
-    __device__ __forceinline__ void flush(double* __restrict__ slots, int64_t wave, int lane) const {
-        double* dst = slots + (wave + img) * (int64_t)(NTL * 256);
+    __device__ __forceinline__ void flush(Real* __restrict__ slots, int64_t wave, int lane) const {
+        Real* dst = slots + (wave + img) * (int64_t)(NTL * 256);
 #pragma unroll
         for (int q = 0; q < NTL; ++q)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dst[q * 256 + (4 * v + (lane >> 4)) * 16 + (lane & 15)] = acc[q][v];
+            for (int v = 0; v < 4; ++v) dst[q * 256 + M::row(lane, v) * 16 + (lane & 15)] = acc[q][v];
     }
     // rows [row_lo, row_hi) of X (LDS, row stride DP + 1) into the sum, A operand scaled by sg
-    __device__ __forceinline__ void add_rows(const double (*X)[DP + 1], int row_lo, int row_hi, double sg, int lane) {
+    __device__ __forceinline__ void add_rows(const Real (*X)[DP + 1], int row_lo, int row_hi, Real sg, int lane) {
         const int c = lane & 15, k = lane >> 4;
         for (int g = row_lo >> 2; 4 * g < row_hi; ++g) {
             const int row = 4 * g + k;
             const bool ok = row >= row_lo && row < row_hi;
-            double av[NT], bw[NT];
+            Real av[NT], bw[NT];
 #pragma unroll
             for (int h = 0; h < NT; ++h) {
-                const double x = ok ? X[row][16 * h + c] : 0.0;
+                const Real x = ok ? X[row][16 * h + c] : Real(0);
                 av[h] = sg * x;
                 bw[h] = x;
             }
@@ -1191,14 +1222,14 @@ struct PmTileAcc {
             for (int hi = 0; hi < NT; ++hi)
 #pragma unroll
                 for (int hj = 0; hj <= hi; ++hj) {
-                    acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[hi], bw[hj], acc[q], 0, 0, 0);
+                    acc[q] = M::mac(av[hi], bw[hj], acc[q]);
                     ++q;
                 }
         }
     }
     // the 64 staged entities of one round (3 rows each), image ids simg[0..64) (-1 = none, only at
     // the end; the others non-decreasing): every image segment into the sum
-    __device__ __forceinline__ void add_round(const double (*X)[DP + 1], const int* simg, double sg, double* slots,
+    __device__ __forceinline__ void add_round(const Real (*X)[DP + 1], const int* simg, Real sg, Real* slots,
                                               int64_t wave, int lane) {
         const int my = simg[lane];
         int lo = 0;
@@ -1220,15 +1251,15 @@ struct PmTileAcc {
 // Per observation (one wave per PM_SPAN observations, 64 at a time): J_p^T J_p (upper 6) and
 // J_p^T W r (3) to pobs, sqrt(W) to wobs; the weighted camera rows, with sqrt(W) r in column d,
 // staged in LDS and summed per image (X^T X) into the J slots.
-template <int HK, int HP, int DP>
+template <int HK, int HP, int DP, typename Real>
 __global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
-    __shared__ double X[192][DP + 1];
+    __shared__ Real X[192][DP + 1];
     __shared__ int simg[64];
     const int lane = threadIdx.x;
     const int64_t w = blockIdx.x;
     const int64_t o_begin = w * PM_SPAN, o_end = min(o_begin + PM_SPAN, a.n_obs);
     const int d = a.lay.d;
-    PmTileAcc<DP> T;
+    PmTileAcc<DP, Real> T;
     T.img = -1;
     T.zero();
     for (int64_t base = o_begin; base < o_end; base += 64) {
@@ -1245,54 +1276,56 @@ __global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
             double Jp[3][3], gP[3];
             point_rows<true>(oc, c.cp, xon, Jp, gP);
             const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
-            double* q = a.pobs + 9 * o;                // streamed out, as wobs (read by later passes)
+            Real* q = (Real*)a.pobs + 9 * o;           // streamed out, as wobs (read by later passes)
 #pragma unroll
             for (int k = 0; k < 6; ++k) {
                 const int i = pr[k][0], j = pr[k][1];
-                __builtin_nontemporal_store(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j], q + k);
+                __builtin_nontemporal_store((Real)(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j]),
+                                            q + k);
             }
-            __builtin_nontemporal_store(gP[0], q + 6);
-            __builtin_nontemporal_store(gP[1], q + 7);
-            __builtin_nontemporal_store(gP[2], q + 8);
+            __builtin_nontemporal_store((Real)gP[0], q + 6);
+            __builtin_nontemporal_store((Real)gP[1], q + 7);
+            __builtin_nontemporal_store((Real)gP[2], q + 8);
             typedef float f4 __attribute__((ext_vector_type(4)));
             const f4 wv = {(float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f};
             __builtin_nontemporal_store(wv, reinterpret_cast<f4*>(a.wobs) + o);
             const bool first = o == 0;
             emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane][j] = v; });
+                                          [&](int j, double v) { X[3 * lane][j] = (Real)v; });
             emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane + 1][j] = v; });
+                                          [&](int j, double v) { X[3 * lane + 1][j] = (Real)v; });
             emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane + 2][j] = v; });
+                                          [&](int j, double v) { X[3 * lane + 2][j] = (Real)v; });
 #pragma unroll
-            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = oc.Rs[k];
+            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = (Real)oc.Rs[k];
         }
         simg[lane] = img;
         __syncthreads();
-        T.add_round(X, simg, 1.0, a.jslots, w, lane);
+        T.add_round(X, simg, Real(1), (Real*)a.jslots, w, lane);
         __syncthreads();
     }
-    if (T.img >= 0) T.flush(a.jslots, w, lane);
+    if (T.img >= 0) T.flush((Real*)a.jslots, w, lane);
 }
 
 // per track: H_pp and g_p summed over its observations in image order; the block's largest diagonal
+template <typename Real>
 __global__ void __launch_bounds__(PM_T) k_pm_track(PmArgs a) {
-    __shared__ double sm[PM_T];
+    __shared__ Real sm[PM_T];
     const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
-    double m = 0.0;
+    Real m = Real(0);
     if (t < a.n_tracks) {
-        double h[9];
+        Real h[9];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) h[k] = 0.0;
+        for (int k = 0; k < 9; ++k) h[k] = Real(0);
         for (int q = a.trk_obs_ptr[t]; q < a.trk_obs_ptr[t + 1]; ++q) {
-            const double* s = a.pobs + 9 * (int64_t)a.trk_obs[q];
+            const Real* s = (const Real*)a.pobs + 9 * (int64_t)a.trk_obs[q];
 #pragma unroll
             for (int k = 0; k < 9; ++k) h[k] += s[k];
         }
 #pragma unroll
-        for (int k = 0; k < 6; ++k) a.Hpp[6 * t + k] = h[k];
+        for (int k = 0; k < 6; ++k) ((Real*)a.Hpp)[6 * t + k] = h[k];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) a.gp[3 * t + k] = h[6 + k];
+        for (int k = 0; k < 3; ++k) ((Real*)a.gp)[3 * t + k] = h[6 + k];
         m = fmax(fabs(h[0]), fmax(fabs(h[3]), fabs(h[5])));
     }
     sm[threadIdx.x] = m;
@@ -1301,21 +1334,21 @@ __global__ void __launch_bounds__(PM_T) k_pm_track(PmArgs a) {
         if ((int)threadIdx.x < w) sm[threadIdx.x] = fmax(sm[threadIdx.x], sm[threadIdx.x + w]);
         __syncthreads();
     }
-    if (threadIdx.x == 0) a.tmax[blockIdx.x] = sm[0];
+    if (threadIdx.x == 0) ((Real*)a.tmax)[blockIdx.x] = sm[0];
 }
 
 // Per run (one wave per PM_SPAN runs, 64 at a time): V = sum over the run's observations of
 // sum_R jc_R (L^-1 jp_R)^T (= (sum J_c^T J_p) L^-T), staged in LDS with L^-1 g_p in column d,
 // summed per image (-X^T X) into the V slots and copied to V (run-major, 3 x DP per run).
-template <int HK, int HP, int DP>
+template <int HK, int HP, int DP, typename Real>
 __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
-    __shared__ double X[192][DP + 1];
+    __shared__ Real X[192][DP + 1];
     __shared__ int simg[64];
     const int lane = threadIdx.x;
     const int64_t w = blockIdx.x;
     const int64_t r_begin = w * PM_SPAN, r_end = min(r_begin + PM_SPAN, a.n_runs);
     const int d = a.lay.d;
-    PmTileAcc<DP> T;
+    PmTileAcc<DP, Real> T;
     T.img = -1;
     T.zero();
     for (int64_t base = r_begin; base < r_end; base += 64) {
@@ -1328,8 +1361,8 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
             pm_ctx(a, img, c);
             const double mK = c.enK ? 1.0 : 0.0, mP = c.enP ? 1.0 : 0.0;
             const bool zon = a.lay.hasZ && c.enZ;
-            const double* pf = a.pfac + 12 * (int64_t)t;
-            const double L1 = pf[1], L2 = pf[2], L4 = pf[4], i0 = pf[9], i1 = pf[10], i2 = pf[11];
+            const Real* pf = (const Real*)a.pfac + 12 * (int64_t)t;
+            const Real L1 = pf[1], L2 = pf[2], L4 = pf[4], i0 = pf[9], i1 = pf[10], i2 = pf[11];
             const int q0 = a.run_ptr[r], q1 = a.run_ptr[r + 1];
             for (int q = q0; q < q1; ++q) {
                 const int o = a.run_obs[q];
@@ -1339,25 +1372,25 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
                 pm_jcore(a, o, c, oc, dep, xon);
                 double Jp[3][3], gP[3];
                 point_rows<false>(oc, c.cp, xon, Jp, gP);
-                double wv[3][3];                     // L^-1 jp_R, R = 0..2
+                Real wv[3][3];                       // L^-1 jp_R, R = 0..2
 #pragma unroll
                 for (int R = 0; R < 3; ++R) {
-                    wv[R][0] = Jp[R][0] * i0;
-                    wv[R][1] = (Jp[R][1] - L1 * wv[R][0]) * i1;
-                    wv[R][2] = (Jp[R][2] - L2 * wv[R][0] - L4 * wv[R][1]) * i2;
+                    wv[R][0] = (Real)Jp[R][0] * i0;
+                    wv[R][1] = ((Real)Jp[R][1] - L1 * wv[R][0]) * i1;
+                    wv[R][2] = ((Real)Jp[R][2] - L2 * wv[R][0] - L4 * wv[R][1]) * i2;
                 }
                 const bool z0off = !a.lay.optim_Z0 || (o == 0 && !a.lay.optim_Z_1st_cam);
-                auto col = [&](int j, double v[3]) {
-                    const double e0 = jc_elem<HK, HP, 0>(oc, a.lay, mK, mP, zon, z0off, dep, j);
-                    const double e1 = jc_elem<HK, HP, 1>(oc, a.lay, mK, mP, zon, z0off, dep, j);
-                    const double e2 = jc_elem<HK, HP, 2>(oc, a.lay, mK, mP, zon, z0off, dep, j);
+                auto col = [&](int j, Real v[3]) {
+                    const Real e0 = (Real)jc_elem<HK, HP, 0>(oc, a.lay, mK, mP, zon, z0off, dep, j);
+                    const Real e1 = (Real)jc_elem<HK, HP, 1>(oc, a.lay, mK, mP, zon, z0off, dep, j);
+                    const Real e2 = (Real)jc_elem<HK, HP, 2>(oc, a.lay, mK, mP, zon, z0off, dep, j);
 #pragma unroll
                     for (int k = 0; k < 3; ++k) v[k] = e0 * wv[0][k] + e1 * wv[1][k] + e2 * wv[2][k];
                 };
                 if (q == q0) {
 #pragma unroll
                     for (int j = 0; j < DP; ++j) {
-                        double v[3];
+                        Real v[3];
                         col(j, v);
 #pragma unroll
                         for (int k = 0; k < 3; ++k) X[3 * lane + k][j] = v[k];
@@ -1365,7 +1398,7 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
                 } else {                             // several observations of the track in this image
 #pragma unroll
                     for (int j = 0; j < DP; ++j) {
-                        double v[3];
+                        Real v[3];
                         col(j, v);
 #pragma unroll
                         for (int k = 0; k < 3; ++k) X[3 * lane + k][j] += v[k];
@@ -1377,35 +1410,39 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
         }
         simg[lane] = img;
         __syncthreads();
-        T.add_round(X, simg, -1.0, a.vslots, w, lane);
+        T.add_round(X, simg, Real(-1), (Real*)a.vslots, w, lane);
         const int nr = (int)min((int64_t)64, r_end - base);
-        double* dst = a.V + base * 3 * DP;
+        Real* dst = (Real*)a.V + base * 3 * DP;
         // streamed out (V of a pass exceeds every cache)
         for (int e = lane; e < nr * 3 * DP; e += 64) __builtin_nontemporal_store(X[e / DP][e % DP], dst + e);
         __syncthreads();
     }
-    if (T.img >= 0) T.flush(a.vslots, w, lane);
+    if (T.img >= 0) T.flush((Real*)a.vslots, w, lane);
 }
 
 // Per image i: the J and V slots of the waves that held its observations and runs, summed in wave
 // order: S_ii (lower tiles, mirrored), rhs_i (row d) and diag(H_cc)_i (the J part's diagonal).
-template <int DP>
+template <int DP, typename Real>
 __global__ void __launch_bounds__(256) k_pm_diag(PmArgs a) {
     constexpr int NT = DP / 16, NTL = NT * (NT + 1) / 2;
     const int i = blockIdx.x, t = threadIdx.x, d = a.lay.d;
     const int pd = a.diag_pair[i];
+    Real* const e_img = (Real*)a.e_img;
+    Real* const dg_img = (Real*)a.dg_img;
     if (pd < 0) {
-        if (t < d) { a.e_img[(int64_t)i * d + t] = 0.0; a.dg_img[(int64_t)i * d + t] = 0.0; }
+        if (t < d) { e_img[(int64_t)i * d + t] = Real(0); dg_img[(int64_t)i * d + t] = Real(0); }
         return;
     }
     const int64_t o0 = i ? a.infos[i - 1] : 0, o1 = a.infos[i];
     const int64_t r0 = a.img_run_ptr[i], r1 = a.img_run_ptr[i + 1];
     const int64_t wj0 = o0 / PM_SPAN, wj1 = (o1 - 1) / PM_SPAN, wv0 = r0 / PM_SPAN, wv1 = (r1 - 1) / PM_SPAN;
-    double* S = a.S_pairs + (int64_t)pd * d * d;
+    Real* S = (Real*)a.S_pairs + (int64_t)pd * d * d;
+    const Real* jslots = (const Real*)a.jslots;
+    const Real* vslots = (const Real*)a.vslots;
     for (int e = t; e < NTL * 256; e += 256) {
-        double sj = 0.0, sv = 0.0;
-        for (int64_t w = wj0; w <= wj1; ++w) sj += a.jslots[(w + i) * (NTL * 256) + e];
-        for (int64_t w = wv0; w <= wv1; ++w) sv += a.vslots[(w + i) * (NTL * 256) + e];
+        Real sj = Real(0), sv = Real(0);
+        for (int64_t w = wj0; w <= wj1; ++w) sj += jslots[(w + i) * (NTL * 256) + e];
+        for (int64_t w = wv0; w <= wv1; ++w) sv += vslots[(w + i) * (NTL * 256) + e];
         const int q = e >> 8, ri = (e >> 4) & 15, cj = e & 15;
         int hi = 0, hj = 0, qq = 0;
 #pragma unroll
@@ -1414,12 +1451,12 @@ __global__ void __launch_bounds__(256) k_pm_diag(PmArgs a) {
             for (int y = 0; y <= x; ++y) { if (qq == q) { hi = x; hj = y; } ++qq; }
         const int rr = 16 * hi + ri, cc = 16 * hj + cj;
         if (rr < d && cc < d && (hi != hj || cc <= rr)) {
-            const double s = sj + sv;
+            const Real s = sj + sv;
             S[rr * d + cc] = s;
             S[cc * d + rr] = s;
-            if (rr == cc) a.dg_img[(int64_t)i * d + rr] = sj;
+            if (rr == cc) dg_img[(int64_t)i * d + rr] = sj;
         } else if (rr == d && cc < d) {
-            a.e_img[(int64_t)i * d + cc] = sj + sv;
+            e_img[(int64_t)i * d + cc] = sj + sv;
         }
     }
 }
@@ -1432,12 +1469,14 @@ __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
 }
 
 // per off-diagonal image pair (one wave): S_ij = - sum over the pair's terms of V_ti V_tj^T, four
-// terms (twelve rows) per three v_mfma_f64_16x16x4f64 per tile; the term indices of 64 terms are
-// read at once and handed to the row lanes by shuffles, the rows of the next 8 terms are requested
-// before the MFMAs of the current 8
-template <int DP>
+// terms (twelve rows) per three 16 x 16 x 4 MFMAs per tile; the term indices of 64 terms are read at
+// once and handed to the row lanes by shuffles, the rows of the next 8 terms are requested before
+// the MFMAs of the current 8
+template <int DP, typename Real>
 __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
+    typedef PmMfma<Real> M;
     constexpr int NT = DP / 16;
+    const Real* const Vg = (const Real*)a.V;
     const int lane = threadIdx.x & 63;
     const int64_t p = xcd_block(blockIdx.x, gridDim.x) * (PM_T / 64) + (threadIdx.x >> 6);
     if (p >= a.n_pairs) return;
@@ -1445,11 +1484,11 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
     if (i1 == i2) return;
     const int d = a.lay.d;
     const int k = lane >> 4, c = lane & 15;
-    dbl4 acc[NT][NT];
+    typename M::V4 acc[NT][NT];
 #pragma unroll
     for (int x = 0; x < NT; ++x)
 #pragma unroll
-        for (int y = 0; y < NT; ++y) acc[x][y] = (dbl4){0.0, 0.0, 0.0, 0.0};
+        for (int y = 0; y < NT; ++y) acc[x][y] = (typename M::V4){Real(0), Real(0), Real(0), Real(0)};
     const int q0 = a.term_ptr[p], q1 = a.term_ptr[p + 1];
     const int n = q1 - q0, nbat = (n + 7) >> 3;
     // The loop body has no branches (indices clamped, out-of-range rows zeroed by a factor), so the
@@ -1463,24 +1502,24 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
         if (q >= q1) { ra = -1; rb = -1; }
     };
     // rows of batch b (8 terms, 24 rows = 6 groups of 4): group g, lane (c, k) holds row 4 g + k
-    auto fetch = [&](int b, int ra_w, int rb_w, double (&A)[6][NT], double (&B)[6][NT]) {
+    auto fetch = [&](int b, int ra_w, int rb_w, Real (&A)[6][NT], Real (&B)[6][NT]) {
 #pragma unroll
         for (int g = 0; g < 6; ++g) {
             const int row = 4 * g + k, tj = 8 * (b & 7) + row / 3, kk = row % 3;
             const int ra = __shfl(ra_w, tj), rb = __shfl(rb_w, tj);
-            const double ma = ra >= 0 ? 1.0 : 0.0, mb = rb >= 0 ? 1.0 : 0.0;
+            const Real ma = ra >= 0 ? Real(1) : Real(0), mb = rb >= 0 ? Real(1) : Real(0);
             const int64_t oa = (int64_t)max(ra, 0) * 3 * DP + kk * DP + c, ob = (int64_t)max(rb, 0) * 3 * DP + kk * DP + c;
 #pragma unroll
             for (int h = 0; h < NT; ++h) {
-                A[g][h] = ma * a.V[oa + 16 * h];
-                B[g][h] = mb * __builtin_nontemporal_load(a.V + ob + 16 * h);
+                A[g][h] = ma * Vg[oa + 16 * h];
+                B[g][h] = mb * __builtin_nontemporal_load(Vg + ob + 16 * h);
             }
         }
     };
     int ra_c, rb_c, ra_n, rb_n;
     window(0, ra_c, rb_c);
     window(1, ra_n, rb_n);
-    double A[6][NT], B[6][NT], An[6][NT], Bn[6][NT];
+    Real A[6][NT], B[6][NT], An[6][NT], Bn[6][NT];
     fetch(0, ra_c, rb_c, A, B);
     for (int b = 0; b < nbat; ++b) {
         const int nb = b + 1;
@@ -1492,7 +1531,7 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
 #pragma unroll
             for (int x = 0; x < NT; ++x)
 #pragma unroll
-                for (int y = 0; y < NT; ++y) acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[g][x], B[g][y], acc[x][y], 0, 0, 0);
+                for (int y = 0; y < NT; ++y) acc[x][y] = M::mac(A[g][x], B[g][y], acc[x][y]);
 #pragma unroll
         for (int g = 0; g < 6; ++g)
 #pragma unroll
@@ -1503,20 +1542,20 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
         ra_c = wrap ? ra_n : ra_c; rb_c = wrap ? rb_n : rb_c;
         ra_n = wrap ? ra_f : ra_n; rb_n = wrap ? rb_f : rb_n;
     }
-    double* S = a.S_pairs + p * d * d;
+    Real* S = (Real*)a.S_pairs + p * d * d;
 #pragma unroll
     for (int x = 0; x < NT; ++x)
 #pragma unroll
         for (int y = 0; y < NT; ++y)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int rr = 16 * x + 4 * v + (lane >> 4), cc = 16 * y + (lane & 15);
+                const int rr = 16 * x + M::row(lane, v), cc = 16 * y + (lane & 15);
                 if (rr < d && cc < d) S[rr * d + cc] = -acc[x][y][v];
             }
 }
 
 // per run row: y = V_r[k] . delta_c(image of r), DP lanes per row (coalesced over V)
-template <int DP>
+template <int DP, typename Real>
 __global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
     // one thread per (run, column): the run's image and delta_c entry are read once for its three V rows
     // (each row's DP columns on DP neighbouring lanes, so every V load is coalesced), and the products
@@ -1527,10 +1566,10 @@ __global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
          t += (int64_t)gridDim.x * 256) {
         const int64_t r = t / DP;
         const bool live = r < a.n_runs;
-        double v[3] = {0.0, 0.0, 0.0};
+        Real v[3] = {Real(0), Real(0), Real(0)};
         if (live && col < d) {
-            const double dc = a.dc_img[(int64_t)a.run_img[r] * d + col];
-            const double* V = a.V + r * 3 * DP + col;
+            const Real dc = ((const Real*)a.dc_img)[(int64_t)a.run_img[r] * d + col];
+            const Real* V = (const Real*)a.V + r * 3 * DP + col;
 #pragma unroll
             for (int k = 0; k < 3; ++k) v[k] = V[k * DP] * dc;
         }
@@ -1538,26 +1577,30 @@ __global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
         for (int k = 0; k < 3; ++k)
 #pragma unroll
             for (int m = DP / 2; m >= 1; m >>= 1) v[k] += __shfl_xor(v[k], m);
-        if (live && col < 3) a.yrun[3 * r + col] = col == 0 ? v[0] : (col == 1 ? v[1] : v[2]);
+        if (live && col < 3) ((Real*)a.yrun)[3 * r + col] = col == 0 ? v[0] : (col == 1 ? v[1] : v[2]);
     }
 }
 
 // per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i))
+template <typename Real>
 __global__ void __launch_bounds__(PM_T) k_pm_backsub(PmArgs a) {
     const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
     if (t >= a.n_tracks) return;
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0;
+    Real s0 = Real(0), s1 = Real(0), s2 = Real(0);
     for (int q = a.trk_run_ptr[t]; q < a.trk_run_ptr[t + 1]; ++q) {
-        const double* y = a.yrun + 3 * (int64_t)a.trk_run[q];
+        const Real* y = (const Real*)a.yrun + 3 * (int64_t)a.trk_run[q];
         s0 += y[0]; s1 += y[1]; s2 += y[2];
     }
-    const double* pf = a.pfac + 12 * t;
-    const double z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
-    const double x2 = z2 * pf[11];
-    const double x1 = (z1 - pf[4] * x2) * pf[10];
-    const double x0 = (z0 - pf[1] * x1 - pf[2] * x2) * pf[9];
+    const Real* pf = (const Real*)a.pfac + 12 * t;
+    const Real z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
+    const Real x2 = z2 * pf[11];
+    const Real x1 = (z1 - pf[4] * x2) * pf[10];
+    const Real x0 = (z0 - pf[1] * x1 - pf[2] * x2) * pf[9];
     a.dX[3 * t] = (float)x0; a.dX[3 * t + 1] = (float)x1; a.dX[3 * t + 2] = (float)x2;
-    if (a.dX64) { a.dX64[3 * t] = x0; a.dX64[3 * t + 1] = x1; a.dX64[3 * t + 2] = x2; }
+    if (a.dX64) {
+        Real* o = (Real*)a.dX64;
+        o[3 * t] = x0; o[3 * t + 1] = x1; o[3 * t + 2] = x2;
+    }
 }
 
 static const char* pm_missing(const ba_pm_args& a, bool backsub) {
@@ -1582,6 +1625,63 @@ static const char* pm_missing(const ba_pm_args& a, bool backsub) {
 
 }  // namespace ba
 
+// the launches of one stage of ba_pm_linearize_stage in the working precision Real
+template <typename Real>
+static void pm_stage(const ba_pm_args& a, int stage, hipStream_t st) {
+    const int64_t nbt = (a.n_tracks + PM_T - 1) / PM_T;
+    const bool wide = a.lay.d > 15;
+    if (stage == 1) {
+        if (a.n_pairs > 0) {
+            const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
+            if (wide) hipLaunchKernelGGL((k_pm_pairs<32, Real>), dim3(g), dim3(PM_T), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_pairs<16, Real>), dim3(g), dim3(PM_T), 0, st, a);
+        }
+        return;
+    }
+    Real* const tmax = (Real*)a.tmax;
+    Real* const lam_p = (Real*)a.lam_p;
+    hipLaunchKernelGGL(k_lam_clear<Real>, dim3(1), dim3(1), 0, st, tmax, nbt);
+    if (a.n_obs > 0) {
+        const unsigned g = (unsigned)((a.n_obs + PM_SPAN - 1) / PM_SPAN);
+        BA_DISPATCH_KP(a.lay, {
+            if (wide) hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 32, Real>), dim3(g), dim3(64), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 16, Real>), dim3(g), dim3(64), 0, st, a);
+        });
+    }
+    if (a.n_tracks > 0) {
+        hipLaunchKernelGGL(k_pm_track<Real>, dim3((unsigned)nbt), dim3(PM_T), 0, st, a);
+        const int64_t nb = nbt < 256 * 256 ? (nbt + 255) / 256 : 256;
+        hipLaunchKernelGGL(k_lam_reduce<Real>, dim3((unsigned)nb), dim3(256), 0, st, tmax, nbt);
+    }
+    hipLaunchKernelGGL(k_lam_final<Real>, dim3(1), dim3(1), 0, st, tmax, nbt, a.lay.dampen, a.lay.adaptive,
+                       a.lay.x_off, lam_p);
+    if (a.n_tracks > 0)
+        hipLaunchKernelGGL(k_point_factor<Real>, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, (const Real*)a.Hpp,
+                           (const Real*)a.gp, (const Real*)lam_p, (int64_t)a.n_tracks, (Real*)a.pfac);
+    if (a.n_runs > 0) {
+        const unsigned g = (unsigned)((a.n_runs + PM_SPAN - 1) / PM_SPAN);
+        BA_DISPATCH_KP(a.lay, {
+            if (wide) hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 32, Real>), dim3(g), dim3(64), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 16, Real>), dim3(g), dim3(64), 0, st, a);
+        });
+    }
+    if (wide) hipLaunchKernelGGL((k_pm_diag<32, Real>), dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
+    else      hipLaunchKernelGGL((k_pm_diag<16, Real>), dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
+}
+
+template <typename Real>
+static void pm_backsub(const ba_pm_args& a, hipStream_t st) {
+    if (a.n_runs > 0) {
+        const int dp = a.lay.d > 15 ? 32 : 16;
+        const int64_t n_th = a.n_runs * dp;      // one thread per (run, column)
+        const unsigned g = (unsigned)std::min<int64_t>((n_th + 255) / 256, 1 << 22);
+        if (dp == 32) hipLaunchKernelGGL((k_pm_yrun<32, Real>), dim3(g), dim3(256), 0, st, a);
+        else          hipLaunchKernelGGL((k_pm_yrun<16, Real>), dim3(g), dim3(256), 0, st, a);
+    }
+    hipLaunchKernelGGL(k_pm_backsub<Real>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+}
+
+// elements (of the working precision) of one slot array
 extern "C" int64_t ba_pm_slot_doubles(int64_t n_items, int32_t n_imgs, int32_t d) {
     if (n_items < 0 || n_imgs < 0 || d < 1 || d > 31) return -1;
     const int64_t ntl = d < 16 ? 1 : 3;
@@ -1605,44 +1705,8 @@ extern "C" int ba_pm_linearize_stage(const ba_pm_args* args, int stage, void* st
     BA_REQUIRE(miss == nullptr, miss);
     BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp | (uintptr_t)a.wobs) & 15) == 0,
                "Hpp, pfac and wobs must be 16-byte aligned");
-    const int64_t nbt = (a.n_tracks + PM_T - 1) / PM_T;
-    const bool wide = a.lay.d > 15;
-    if (stage == 1) {
-        if (a.n_pairs > 0) {
-            const unsigned g = (unsigned)((a.n_pairs + PM_T / 64 - 1) / (PM_T / 64));
-            if (wide) hipLaunchKernelGGL(k_pm_pairs<32>, dim3(g), dim3(PM_T), 0, st, a);
-            else      hipLaunchKernelGGL(k_pm_pairs<16>, dim3(g), dim3(PM_T), 0, st, a);
-        }
-        BA_LAUNCHED();
-        return BA_OK;
-    }
-    hipLaunchKernelGGL(k_lam_clear, dim3(1), dim3(1), 0, st, a.tmax, nbt);
-    if (a.n_obs > 0) {
-        const unsigned g = (unsigned)((a.n_obs + PM_SPAN - 1) / PM_SPAN);
-        BA_DISPATCH_KP(a.lay, {
-            if (wide) hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 32>), dim3(g), dim3(64), 0, st, a);
-            else      hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 16>), dim3(g), dim3(64), 0, st, a);
-        });
-    }
-    if (a.n_tracks > 0) {
-        hipLaunchKernelGGL(k_pm_track, dim3((unsigned)nbt), dim3(PM_T), 0, st, a);
-        const int64_t nb = nbt < 256 * 256 ? (nbt + 255) / 256 : 256;
-        hipLaunchKernelGGL(k_lam_reduce, dim3((unsigned)nb), dim3(256), 0, st, a.tmax, nbt);
-    }
-    hipLaunchKernelGGL(k_lam_final, dim3(1), dim3(1), 0, st, a.tmax, nbt, a.lay.dampen, a.lay.adaptive, a.lay.x_off,
-                       a.lam_p);
-    if (a.n_tracks > 0)
-        hipLaunchKernelGGL(k_point_factor, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, a.Hpp, a.gp, a.lam_p,
-                           (int64_t)a.n_tracks, a.pfac);
-    if (a.n_runs > 0) {
-        const unsigned g = (unsigned)((a.n_runs + PM_SPAN - 1) / PM_SPAN);
-        BA_DISPATCH_KP(a.lay, {
-            if (wide) hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 32>), dim3(g), dim3(64), 0, st, a);
-            else      hipLaunchKernelGGL((k_pm_runs<HK_, HP_, 16>), dim3(g), dim3(64), 0, st, a);
-        });
-    }
-    if (wide) hipLaunchKernelGGL(k_pm_diag<32>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
-    else      hipLaunchKernelGGL(k_pm_diag<16>, dim3((unsigned)a.n_imgs), dim3(256), 0, st, a);
+    if (a.real32) pm_stage<float>(a, stage, st);
+    else          pm_stage<double>(a, stage, st);
     BA_LAUNCHED();
     return BA_OK;
 }
@@ -1661,14 +1725,8 @@ extern "C" int ba_pm_backsubstitute(const ba_pm_args* args, void* stream) {
     const char* miss = pm_missing(a, true);
     BA_REQUIRE(miss == nullptr, miss);
     hipStream_t st = (hipStream_t)stream;
-    if (a.n_runs > 0) {
-        const int dp = a.lay.d > 15 ? 32 : 16;
-        const int64_t n_th = a.n_runs * dp;      // one thread per (run, column)
-        const unsigned g = (unsigned)std::min<int64_t>((n_th + 255) / 256, 1 << 22);
-        if (dp == 32) hipLaunchKernelGGL(k_pm_yrun<32>, dim3(g), dim3(256), 0, st, a);
-        else          hipLaunchKernelGGL(k_pm_yrun<16>, dim3(g), dim3(256), 0, st, a);
-    }
-    hipLaunchKernelGGL(k_pm_backsub, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+    if (a.real32) pm_backsub<float>(a, st);
+    else          pm_backsub<double>(a, st);
     BA_LAUNCHED();
     return BA_OK;
 }

@@ -560,9 +560,10 @@ extern "C" int ba_planar_confidence(const float* D0, int32_t H, int32_t W, float
 }
 
 namespace ba {
-__global__ void __launch_bounds__(TG_T) k_add_z_prior(double* __restrict__ S, const int32_t* __restrict__ diag_pair,
-                                                       double* __restrict__ e_img, double* __restrict__ dg_img,
-                                                       const double* __restrict__ Hz, const double* __restrict__ gz,
+template <typename Real>
+__global__ void __launch_bounds__(TG_T) k_add_z_prior(Real* __restrict__ S, const int32_t* __restrict__ diag_pair,
+                                                       Real* __restrict__ e_img, Real* __restrict__ dg_img,
+                                                       const Real* __restrict__ Hz, const Real* __restrict__ gz,
                                                        int64_t n_imgs, int d, int C) {
     const int64_t t = (int64_t)blockIdx.x * TG_T + threadIdx.x;
     const int per = C * C + C;
@@ -572,7 +573,7 @@ __global__ void __launch_bounds__(TG_T) k_add_z_prior(double* __restrict__ S, co
     const int o = d - C;
     if (e < C * C) {
         const int c = e / C, dd = e - c * C;
-        const double h = Hz[i * C * C + e];
+        const Real h = Hz[i * C * C + e];
         S[(int64_t)diag_pair[i] * d * d + (o + c) * d + (o + dd)] += h;
         if (c == dd) dg_img[i * d + o + c] += h;
     } else {
@@ -582,16 +583,20 @@ __global__ void __launch_bounds__(TG_T) k_add_z_prior(double* __restrict__ S, co
 }
 }  // namespace ba
 
-extern "C" int ba_add_z_prior(double* S_pairs, const int32_t* diag_pair, double* e_img, double* dg_img,
-                              const double* H_z, const double* g_z, int64_t n_imgs, int32_t d, int32_t C,
-                              void* stream) {
+extern "C" int ba_add_z_prior(void* S_pairs, const int32_t* diag_pair, void* e_img, void* dg_img, const void* H_z,
+                              const void* g_z, int64_t n_imgs, int32_t d, int32_t C, int32_t real32, void* stream) {
     clear_error();
     BA_REQUIRE(S_pairs && diag_pair && e_img && dg_img && H_z && g_z, "missing arrays");
     BA_REQUIRE(n_imgs >= 0 && C >= 1 && d >= C, "bad sizes");
     const int64_t n = n_imgs * (C * C + C);
     if (n == 0) return BA_OK;
-    hipLaunchKernelGGL(k_add_z_prior, dim3((unsigned)tg_div_up(n, TG_T)), dim3(TG_T), 0, (hipStream_t)stream, S_pairs,
-                       diag_pair, e_img, dg_img, H_z, g_z, n_imgs, d, C);
+    const dim3 g((unsigned)tg_div_up(n, TG_T));
+    if (real32)
+        hipLaunchKernelGGL(k_add_z_prior<float>, g, dim3(TG_T), 0, (hipStream_t)stream, (float*)S_pairs, diag_pair,
+                           (float*)e_img, (float*)dg_img, (const float*)H_z, (const float*)g_z, n_imgs, d, C);
+    else
+        hipLaunchKernelGGL(k_add_z_prior<double>, g, dim3(TG_T), 0, (hipStream_t)stream, (double*)S_pairs, diag_pair,
+                           (double*)e_img, (double*)dg_img, (const double*)H_z, (const double*)g_z, n_imgs, d, C);
     BA_LAUNCHED();
     return BA_OK;
 }

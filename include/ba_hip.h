@@ -208,20 +208,25 @@ typedef struct {
     ba_layout lay;                           /* d <= 31 */
     const float *r_in, *w_in;                /* optional given residuals / weights, as in ba_lin_args */
     int64_t r_s0, r_s1, w_s0, w_s1;
-    /* workspace */
-    double* pobs;                            /* (n_obs, 9) */
+    /* workspace; (R) = elements of the working precision: double, or float when real32 is set */
+    void* pobs;                              /* (R) (n_obs, 9) */
     float* wobs;                             /* (n_obs, 4) 16-byte aligned: sqrt(W) per residual row */
-    double *jslots, *vslots;                 /* per-wave image sums: ba_pm_slot_doubles(n_obs | n_runs, n_imgs, d) */
-    double* yrun;                            /* (n_runs, 3) back-substitution: V_r^T delta_c per run */
-    double *Hpp, *gp;                        /* (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
-    double* tmax;                            /* (ceil(n_tracks / 256) + 1) */
-    double* lam_p;                           /* (1) point-leaf damping value */
-    double* pfac;                            /* (n_tracks, 12) 16-byte aligned: L, L^-1 g_p, reciprocal pivots */
-    double* V;                               /* (n_runs, 3, dp), dp = 16 for d <= 15 else 32 */
-    /* outputs: (n_pairs, d, d), (n_imgs, d), (n_imgs, d) */
-    double *S_pairs, *e_img, *dg_img;
-    /* back-substitution: delta_c at image level (n_imgs, d), point steps (n_tracks, 3) */
-    const double* dc_img; float* dX; double* dX64;
+    void *jslots, *vslots;                   /* (R) per-wave image sums: ba_pm_slot_doubles(n_obs | n_runs, n_imgs, d) */
+    void* yrun;                              /* (R) (n_runs, 3) back-substitution: V_r^T delta_c per run */
+    void *Hpp, *gp;                          /* (R) (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
+    void* tmax;                              /* (R) (ceil(n_tracks / 256) + 1) */
+    void* lam_p;                             /* (R) (1) point-leaf damping value */
+    void* pfac;                              /* (R) (n_tracks, 12) 16-byte aligned: L, L^-1 g_p, reciprocal pivots */
+    void* V;                                 /* (R) (n_runs, 3, dp), dp = 16 for d <= 15 else 32 */
+    /* outputs (R): (n_pairs, d, d), (n_imgs, d), (n_imgs, d) */
+    void *S_pairs, *e_img, *dg_img;
+    /* back-substitution: delta_c at image level (R) (n_imgs, d), point steps (n_tracks, 3) in fp32 and,
+     * optionally, in the working precision (R) */
+    const void* dc_img; float* dX; void* dX64;
+    /* 0: every (R) array is fp64 (the reference's dtype=torch.float64 solver, engine.py:490); 1: fp32
+     * throughout (its dtype=torch.float32 default, ba_solver.py:22, :37, :128): the Jacobian core is
+     * evaluated in fp64 and rounded, every product, sum and factor after it is fp32 */
+    int32_t real32;
 } ba_pm_args;
 
 int ba_pm_linearize_schur(const ba_pm_args* args, void* stream);
@@ -243,16 +248,17 @@ typedef struct {
     const int32_t *leaf;               /* (n_u) 0 foc, 1 tau, 2 zcf */
     const int32_t *row_ptr, *row_ent;  /* image rows of the pair structure: (pair << 1) | transposed */
     const int32_t *pair_i1, *pair_i2;
-    const double *S_pairs, *e_img, *dg_img;
+    const void *S_pairs, *e_img, *dg_img; /* (R) */
     double dampen; int32_t adaptive;
     int32_t maxiter; double tol;
-    /* workspace (fp64 unless noted); p holds 2 * n_u (the search direction, double-buffered) */
-    double *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img;
-    double *partials;                  /* ba_pcg_partials_size(n_u) doubles */
-    double *state;                     /* 16 doubles */
+    /* workspace, (R) = the working precision (double, or float when real32 is set); p holds 2 * n_u
+     * (the search direction, double-buffered) */
+    void *rhs, *diagA, *damp, *x, *xbest, *r, *z, *p, *y_img;   /* (R) */
+    void *partials;                    /* (R) ba_pcg_partials_size(n_u) elements */
+    void *state;                       /* (R) 16 elements */
     int32_t *istate;                   /* 8 ints: [0], [1] done flags, [2] iterations, [3] converged,
                                           [4] best iteration, [5] best iterate returned */
-    double *S_rows;                    /* (n_row_ent, d, d): the pair blocks copied per image row */
+    void *S_rows;                      /* (R) (n_row_ent, d, d): the pair blocks copied per image row */
     int64_t n_row_ent;                 /* row_ptr[n_imgs] */
     int32_t *row_u;                    /* (n_row_ent, 16 if d <= 16 else 32) workspace: the unknowns each image-row
                                           block multiplies */
@@ -262,7 +268,7 @@ typedef struct {
     const int32_t *long_ptr;           /* (ceil(n_u / 256) + 1): long_u[long_ptr[b] .. long_ptr[b + 1]) lie in
                                           [256 b, 256 b + 256) */
     const int32_t *long_idx;           /* (n_u): k - long_ptr[u / 256] for u = long_u[k], else -1 */
-    double *img_part;                  /* (n_imgs) workspace: per image row partial of p.Ap */
+    void *img_part;                    /* (R) (n_imgs) workspace: per image row partial of p.Ap */
     /* optional (NULL = follow inv_ptr / inv_src): the lists pre-resolved, one dependent load fewer */
     const int32_t *src1;               /* (n_u): the only entry of u's inv list when it has exactly one,
                                           else -1 */
@@ -271,6 +277,9 @@ typedef struct {
                                           > 0 (a multiple of 8, at least every row's length): at
                                           [i row_cap, (i+1) row_cap), the rest zero blocks with unknown -1,
                                           and S_rows / row_u sized for n_imgs * row_cap blocks */
+    int32_t real32;                    /* 0: (R) = double; 1: (R) = float, the reference's fp32 _pcg
+                                          (ba_solver.py:1197-1238 on its dtype=torch.float32 operator);
+                                          ba_reduced_solve takes 0 only */
 } ba_pcg_args;
 
 #define BA_PCG_LONG_LIST 32
@@ -543,9 +552,10 @@ int ba_planar_confidence(const float* D0, int32_t H, int32_t W, float alpha, flo
 
 /* z_prior injection (ba_solver.py:141-173) into the image-level reduced system before damping:
  * S_pairs[diag_pair[i]][o + c][o + d] += H_z[i][c][d], e_img[i][o + c] += g_z[i][c],
- * dg_img[i][o + c] += H_z[i][c][c], for the n_imgs images (fp64 arrays, d x d blocks, o = d - C). */
-int ba_add_z_prior(double* S_pairs, const int32_t* diag_pair, double* e_img, double* dg_img, const double* H_z,
-                   const double* g_z, int64_t n_imgs, int32_t d, int32_t C, void* stream);
+ * dg_img[i][o + c] += H_z[i][c][c], for the n_imgs images (d x d blocks, o = d - C); every array fp64, or
+ * fp32 when real32 is set (the reduced system of the pair-major path's fp32 solver). */
+int ba_add_z_prior(void* S_pairs, const int32_t* diag_pair, void* e_img, void* dg_img, const void* H_z,
+                   const void* g_z, int64_t n_imgs, int32_t d, int32_t C, int32_t real32, void* stream);
 
 #ifdef __cplusplus
 }

@@ -120,10 +120,12 @@ def linearize_and_solve(rigs, pids, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig,
 def lm_step(rigs, pids, pix2d, pix2d_std, pix2d_dep, K, P_rig2cam, P_w2rig, z_coefs, pts3d, depth_mode='log',
             pnorm=1, clip_pix_err=100, huber_delta=0.5, min_reproj=0.01, dampen=1e-12, min_loss_delta=1e-4,
             weight_z=1, optim_K=True, optim_Z=True, optim_P=True, optim_X=True, optim_Z0=True,
-            no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float64, solver='pcg', verbose=False,
+            no_grad_f_from_rz=False, adaptive_dampen=True, dtype=torch.float32, solver='pcg', verbose=False,
             pcg_tol=1e-6, pcg_maxiter=300, log_depth_maps=None, conf=None, pts3d_ref=None, weight_tan=0.0,
             tan_stride=4, normalize_tangents=True):
-    """en:206-334 on CPU. Returns (update dict, BA_Status, info)."""
+    """en:206-334 on CPU. Returns (update dict, BA_Status, info).  dtype defaults to torch.float32, the
+    reference's GaussNewtonSolver default that lm_step uses when the caller passes none (bs:22, en:284);
+    bundle_adjustment passes torch.float64 (en:490)."""
     assert depth_mode in ('lin', 'log')
     is_depth_log = depth_mode == 'log'
     K_tan = K.detach()
@@ -218,7 +220,8 @@ def bundle_adjustment(rigs_data, track_data, pts3d, z_coefs=None, max_iters=1000
             up, st, _ = lm_step(infos, trk.pids, trk.pix2d, trk.pix2d_std, dep, var['K'], rig.P_rig2cam,
                                 var['P_w2rig'], var['z_coefs'], var['pts3d'], depth_mode=rig.depth_mode,
                                 pnorm=pnorm, weight_z=weight_z, optim_K=optim_K, optim_Z=optim_Z, optim_P=optim_P,
-                                optim_X=optim_X, optim_Z0=optim_Z0, no_grad_f_from_rz=no_Jfz, **lm_kwargs)
+                                optim_X=optim_X, optim_Z0=optim_Z0, no_grad_f_from_rz=no_Jfz, dtype=torch.float64,
+                                **lm_kwargs)
             if st.new_loss >= st.init_loss:
                 break
             var.update(up)

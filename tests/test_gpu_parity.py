@@ -282,13 +282,13 @@ def _is_log(p):
     return p.options.get('depth_mode', 'log') == 'log'
 
 
-def _oracle_ne(p, **flags):
+def _oracle_ne(p, dtype=torch.float64, **flags):
     o = opts(p)
     loss, res, w = oeng.objective(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids, p.pix2d,
                                   p.pix2d_std, p.pix2d_dep, _is_log(p), o['weight_z'], 1.0, o['clip_pix_err'],
                                   o['huber_delta'])
     Jc, Jz, Jp = ok.jacobians_with_rigs(p.infos, p.K, p.P_rig2cam, p.P_w2rig, p.z_coefs, p.pts3d, p.pids,
-                                        p.pix2d_std, p.pix2d_dep, _is_log(p), float64=True)
+                                        p.pix2d_std, p.pix2d_dep, _is_log(p), float64=dtype == torch.float64)
     if not flags.get('optim_Z0', True):
         Jz[:, 0, 0] = 0
     prob = osol.Problem(p.infos, p.pids, len(p.K), len(p.P_w2rig), p.n_tracks, p.C)
@@ -302,14 +302,14 @@ def _cfg_flags(p):
     return {k: p.options[k] for k in ('optim_K', 'optim_P') if not p.options.get(k, True)}
 
 
-def _gpu_solver(p, path='auto', solver='pcg', **flags):
+def _gpu_solver(p, path='auto', solver='pcg', dtype=torch.float64, **flags):
     g = _gpu(p)
     o = opts(p)
     out = cujac.compute_residuals_with_rigs(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids,
                                             g.pix2d, g.pix2d_std, g.pix2d_dep, _is_log(p), o['weight_z'], 1.0,
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
-    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=dtype,
                            no_grad_f_from_rz=flags.get('no_grad_f_from_rz', False), path=path, solver=solver)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     fl = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in flags.items()
@@ -560,7 +560,7 @@ def test_pcg_graph_replay_matches_eager():
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
 
     def solve(use_graph):
-        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, use_graph=use_graph)
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64, use_graph=use_graph)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                                  g.pix2d_dep, True, pix2d=g.pix2d, hp=hp)
         d = gs.solve_delta(J, res, w)
@@ -619,13 +619,113 @@ def test_two_masks_of_equal_size_on_one_plan():
     for mask in (torch.tensor(T_ + F_), torch.tensor(F_ + T_), torch.tensor(T_ + F_)):
         ne, gvec, params, _, _, _ = _oracle_ne(p, optim_P=mask)
         d_ref, _, _ = osol.solve_reduced_pcg(ne, gvec)
-        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV)
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                                  g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, optim_P=mask.to(DEV))
         delta = gs.solve_delta(J, res, w)
         plans.add(id(gs.last['plan']))
         assert rel_err(delta, d_ref.to(torch.float32)) < 1e-4, mask
     assert len(plans) == 1
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 8, 300, {}), (2, 24, 800, {}), (3, 24, 600, {}), (4, 12, 300, {}),
+                                           (2, 16, 300, dict(n_channels=16))], ids=['cfg0', 'cfg2', 'cfg3', 'cfg4', 'd25'])
+def test_reduced_system_fp32(cfg, nf, nt, kw):
+    """dtype=torch.float32, the reference's GaussNewtonSolver default (bs:22: fp32 Jacobian, fp32 normal
+    equations and Schur algebra, bs:37, :128): the pair-major pass in fp32 (fp32 sums, point factors and
+    16x16x4 fp32 MFMA tiles) gives S, the rhs and the point blocks within 5x (at least 1e-5) of the distance
+    of the oracle's own fp32 algebra from the fp64 result, i.e. no less accurate than the reference's
+    fp32 path."""
+    print(f'fp32 reduced system cfg {cfg} {kw}', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt, **kw)
+    flags = _cfg_flags(p)
+    ne64, g64, _, _, _, _ = _oracle_ne(p, **flags)
+    ne32, g32, _, _, _, _ = _oracle_ne(p, dtype=torch.float32, **flags)
+    S64, rhs64 = osol.dense_schur(ne64), osol.reduced_rhs(ne64, g64)
+    S32, rhs32 = osol.dense_schur(ne32).double(), osol.reduced_rhs(ne32, g32).double()
+    gs, delta, _ = _gpu_solver(p, dtype=torch.float32, **flags)
+    assert gs.last['path'] == 'pairmajor' and gs.last['S_pairs'].dtype == torch.float32
+    assert delta.dtype == torch.float32 and bool(torch.isfinite(delta).all())
+    S, rhs = gs.reduced_system_dense()
+    for name, dev, ref, orc in (('S', S.cpu(), S64, S32), ('rhs', rhs.cpu(), rhs64, rhs32)):
+        e_dev, e_or = rel_err(dev, ref), rel_err(orc, ref)
+        print(f'  {name}: device fp32 {e_dev:.2e}, oracle fp32 {e_or:.2e} from fp64', flush=True)
+        assert e_dev <= max(1e-5, 5 * e_or), (name, e_dev, e_or)
+    iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
+    H = gs.point_blocks()[0].cpu()
+    H64 = torch.stack([ne64.leaves['pts'][:, i, j] for i, j in iu], 1)
+    H32 = torch.stack([ne32.leaves['pts'][:, i, j] for i, j in iu], 1).double()
+    assert rel_err(H, H64) <= max(1e-5, 5 * rel_err(H32, H64))
+
+
+@pytest.mark.parametrize('cfg,nf,nt', [(0, 8, 300), (2, 30, 1500), (3, 24, 600), (4, 20, 800)])
+def test_lm_step_default_dtype_is_the_fp32_solver(cfg, nf, nt):
+    """lm_step called without dtype runs the reference's fp32 solver (GaussNewtonSolver's default,
+    bs:22, which lm_step uses unless told otherwise, en:284): the step is checked against the oracle's
+    lm_step with its own default (fp32 throughout):
+      * the same initial loss (1e-5);
+      * the device's fp32 PCG against the oracle's fp32 _pcg (bs:1197-1238) on the device's own reduced
+        system, after the device's number of updates, to 1e-4 widened only by 5x the move of that iterate
+        when S is applied transposed or b moves by one fp32 ulp;
+      * sqrt(W) J delta, the residual change the step predicts, within 5x (at least 1e-4) of the distance
+        of the oracle's fp32 step from the exact (fp64, direct) solution of the same system;
+      * the oracle's line search (en:305-333) run on the device's step: the same scales and accepted
+        one, loss and parameters within 1e-5."""
+    from tests.step_checks import weighted_jdelta
+    print(f'lm_step default dtype (fp32) cfg {cfg}', flush=True)
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    o = p.options
+    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+              optim_P=o['optim_P'])
+    hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
+    info = {}
+    up_g, st_g, _ = gpu_engine._lm_step(**_gpu(p).lm_inputs(), **kw, info=info)
+    gs = info['solver']
+    assert gs.dtype == torch.float32 and gs.last['path'] == 'pairmajor'
+    inp = p.lm_inputs()
+    _, st_o, info_o = oeng.lm_step(**inp, **kw)
+    assert info_o['delta'].dtype == torch.float32 and info_o['ne'].leaves['foc'].dtype == torch.float32
+    sysd = _oracle_system(inp, hp, dict(optim_K=o['optim_K'], optim_P=o['optim_P']))
+    assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-5 * abs(float(sysd['loss']))
+    # the device's fp32 PCG against the oracle's fp32 _pcg on the device's own system
+    S_dev, rhs_dev, dA_dev = device_system(gs)
+    S32, b32, d32 = S_dev.float(), rhs_dev.float(), dA_dev.clamp(min=1e-12).float()
+    ist = info['pcg_istate'].cpu()
+    k = int(ist[2]) if int(ist[3]) else int(ist[4])
+    assert k >= 1
+
+    def kth(A_mv, b):
+        hist = []
+        osol.pcg(A_mv, b, M_mv=lambda v: v / d32, tol=0.0, maxiter=k, history=hist)
+        return hist[k - 1]
+    gen = torch.Generator().manual_seed(cfg)
+    same = kth(lambda v: S32 @ v, b32)
+    alts = [kth(lambda v: S32.T @ v, b32),
+            kth(lambda v: S32 @ v, b32 * (1 + 2.0 ** -23 * torch.randn(b32.shape, generator=gen)))]
+    n_c = b32.shape[0]
+    tol_d = max([1e-4] + [5 * rel_err(a, same) for a in alts])
+    e_d = rel_err(info['delta'][:n_c].cpu(), same)
+    # sqrt(W) J delta against the exact solution, beside the oracle's own fp32 step
+    jd_true = weighted_jdelta(sysd, osol.solve_reduced_direct(sysd['ne'], sysd['g']))
+    e_dev = rel_err(weighted_jdelta(sysd, info['delta']), jd_true)
+    e_or = rel_err(weighted_jdelta(sysd, info_o['delta']), jd_true)
+    print(f'  k={k}: device PCG vs oracle fp32 _pcg {e_d:.2e} (bar {tol_d:.2e}); sqrt(W) J delta from the exact '
+          f'step: device {e_dev:.2e}, oracle fp32 {e_or:.2e}', flush=True)
+    assert e_d <= tol_d, (e_d, tol_d)
+    assert e_dev <= max(1e-4, 5 * e_or), (e_dev, e_or)
+    _check_line_search(inp, hp, sysd, info['delta'], info, st_g, up_g)
+
+
+def test_fp32_solver_limits():
+    """The fp32 solver runs on the pair-major path only: the batched path and the direct (fp64) Cholesky
+    refuse dtype=torch.float32 with an error instead of running in another precision; other dtypes are
+    refused too."""
+    for kw in (dict(path='batched'), dict(solver='cholesky')):
+        with pytest.raises(ValueError, match='float64'):
+            GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float32, **kw)
+    with pytest.raises(ValueError, match='dtype'):
+        GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float16)
+    assert GaussNewtonSolver(1, 4, 4, 10, DEV).dtype == torch.float32
 
 
 def _cpu_inputs(d):
@@ -661,7 +761,8 @@ def test_lm_step_direct_solve_parity(cfg, nf, nt):
     print(f'lm_step (direct solve) parity cfg {cfg} ({nf} frames, {nt} tracks)', flush=True)
     p = make_problem(cfg, n_frames=nf, n_tracks=nt)
     o = p.options
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
               optim_P=o['optim_P'], solver='cholesky')
     hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
     g = _gpu(p)
@@ -688,7 +789,8 @@ def test_lm_step_direct_solve_parity(cfg, nf, nt):
 
 def _check_lm_step(p, cfg, solver_kw):
     o = p.options
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
               optim_P=o['optim_P'], depth_mode=o['depth_mode'], **solver_kw)
     hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100,
               is_depth_log=_is_log(p))
@@ -929,7 +1031,7 @@ def test_lm_step_rejects_nonfinite_inputs():
     step and read with the first line-search trial, before any decision is taken."""
     p = make_problem(0, n_frames=6, n_tracks=60)
     o = p.options
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0)
+    kw = dict(dtype=torch.float64, weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0)
     g = _gpu(p)
     gpu_engine.lm_step(**g.lm_inputs(), **kw)                  # finite inputs pass
     for name, idx, v in [('pix2d_dep', (3, 1), float('nan')), ('K', (0, 0, 0), float('inf')),
@@ -957,7 +1059,7 @@ def test_schur_work_queue_is_deterministic():
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
-    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV,
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64,
                            plan_options=dict(max_batch_obs=400))
     J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                              g.pix2d_dep, True, pix2d=g.pix2d, hp=hp)
@@ -1019,7 +1121,7 @@ def test_backsubstitute_image_level_delta_matches_unknown_map():
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     for flags in ({}, dict(optim_P=False)):
-        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV)
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                                  g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
         gs.solve_delta(J, res, w)
@@ -1110,7 +1212,8 @@ def test_lm_step_full_config2_line_search():
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     p = make_problem(2)
     o = p.options
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
               optim_P=o['optim_P'])
     hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
     print(f'[full cfg2 lm_step] {p.n_obs} observations', flush=True)
@@ -1149,7 +1252,7 @@ def test_reduced_solve_cholesky_fallback_runs_pcg_and_points_again(cfg, nf, nt):
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     deltas, reads = [], []
     for solver in ('cholesky', 'pcg'):
-        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, solver=solver)
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64, solver=solver)
         if solver == 'cholesky':
             real = gs._direct_status
 
@@ -1187,7 +1290,7 @@ def test_pcg_chunked_graphs_equal_the_whole_sequence(cfg, nf, nt, maxiter):
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     runs = {}
     for use_graph in (True, False):
-        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, use_graph=use_graph,
+        gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64, use_graph=use_graph,
                                pcg_maxiter=maxiter)
         J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
                                  g.pix2d_dep, True, pix2d=g.pix2d, hp=hp, **flags)
@@ -1231,7 +1334,7 @@ def test_reduced_solve_cholesky_parity(cfg, nf, nt, layout):
                                             g.pix2d, g.pix2d_std, g.pix2d_dep, True, o['weight_z'], 1.0,
                                             o['clip_pix_err'], o['huber_delta'])
     res, err, w = out.view(-1, 3, 3).unbind(dim=1)
-    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, solver='cholesky',
+    gs = GaussNewtonSolver(len(p.K), len(p.P_w2rig), p.n_imgs, p.n_tracks, DEV, dtype=torch.float64, solver='cholesky',
                            cholesky_layout=layout)
     hp = dict(weight_z=o['weight_z'], pnorm=1.0, max_pix_err=o['clip_pix_err'], huber_delta=o['huber_delta'])
     J = gs.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,

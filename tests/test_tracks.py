@@ -229,7 +229,8 @@ def test_merge_then_plan_is_an_append_equal_to_a_full_plan():
     inp = dict(rigs=inf_new, pids=merged.pids, pix2d=merged.pix2d, pix2d_std=merged.pix2d_std,
                pix2d_dep=merged.pix2d_dep, K=p.K.to(DEV), P_rig2cam=p.P_rig2cam.to(DEV), P_w2rig=p.P_w2rig.to(DEV),
                z_coefs=p.z_coefs.to(DEV), pts3d=pts3d.to(DEV))
-    kw = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
+    kw = dict(dtype=torch.float64,
+              weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, optim_K=o['optim_K'],
               optim_P=o['optim_P'])
     up_a, st_a = engine.lm_step(**inp, **kw)
     bplan._cache.clear()
