@@ -90,22 +90,26 @@ class RigsData:
                     dst[:] = new
 
     def z_coefs_from_scale(self, tracks):
-        """rigs.py:69-94."""
+        """The z-coefficients with one row per image (rigs.py:69-94): rows that already exist are kept;
+        new rows (all of them when there are none, one per image of `tracks`; else up to one per scale)
+        start from the image's depth scale: [scale, 0, ...] in lin mode, [1, log scale, 0, ...] in log
+        mode (the main channel, then the additive log-depth shift).  A depth mode other than these two
+        is an error once a row has to be made."""
         if self.z_coefs is None:
+            first_new = 0
             self.z_coefs = torch.zeros((tracks.n_imgs, tracks.pix2d_dep.shape[-1]), device=self.scale.device)
-            start = 0
-        elif len(self.z_coefs) < len(self.scale):
-            start = len(self.z_coefs)
-            self.z_coefs = torch.cat((self.z_coefs, self.z_coefs.new_zeros((len(self.scale) - len(self.z_coefs),
-                                                                            self.z_coefs.shape[1]))))
         else:
-            start = len(self.z_coefs)
-        for i in range(start, len(self.z_coefs)):
+            first_new = len(self.z_coefs)
+            missing = len(self.scale) - first_new
+            if missing > 0:
+                self.z_coefs = torch.cat((self.z_coefs, self.z_coefs.new_zeros((missing, self.z_coefs.shape[1]))))
+        rows = slice(first_new, len(self.z_coefs))
+        if rows.stop > rows.start:
             if self.depth_mode == 'lin':
-                self.z_coefs[i, 0] = self.scale[i]
+                self.z_coefs[rows, 0] = self.scale[rows]
             elif self.depth_mode == 'log':
-                self.z_coefs[i, 0] = 1
-                self.z_coefs[i, 1] = self.scale[i].log()
+                self.z_coefs[rows, 0] = 1
+                self.z_coefs[rows, 1] = self.scale[rows].log()
             else:
                 raise ValueError(f'bad {self.depth_mode=}')
         return self.z_coefs

@@ -25,11 +25,10 @@ STEP_SCHEDULE = [0.5, 0.25, 0.125, 1 / 64, 1 / 512, 1 / 4096, 0]     # en:309
 
 
 def shape_of(tensor, is_contiguous=True, check_finite=True):
-    """en:340-344.  check_finite=False leaves the isfinite assertion to a later batched
-    _assert_finite over all inputs (lm_step)."""
-    assert tensor.dtype in (torch.float32, torch.int32)
-    if is_contiguous:
-        assert tensor.is_contiguous()
+    """The shape of an lm_step input once it has passed the input checks of en:340-344: fp32 or int32,
+    contiguous unless is_contiguous is False, and finite (check_finite=False leaves that check to one
+    batched device check of all inputs, _nonfinite_flag)."""
+    assert tensor.dtype in (torch.float32, torch.int32) and (not is_contiguous or tensor.is_contiguous())
     if check_finite:
         _assert_finite(tensor)
     return tensor.shape
@@ -66,13 +65,11 @@ def _assert_finite(*tensors):
 
 
 def update_K(K0, delta_focal, min_f=100):
-    """en:347-354."""
-    dfx, dfy = delta_focal.T
+    """Intrinsics after a focal step (en:347-354): (fx, fy) <- max((fx, fy) - delta_focal, min_f), the
+    rest of K0 unchanged (a NaN focal stays NaN)."""
     K = K0.clone()
-    K[:, 0, 0] -= dfx
-    K[:, 1, 1] -= dfy
-    K[:, 0, 0].clip_(min=min_f)
-    K[:, 1, 1].clip_(min=min_f)
+    diag = torch.arange(2, device=K0.device)
+    K[:, diag, diag] = torch.clamp(K0[:, diag, diag] - delta_focal, min=min_f)
     return K
 
 
@@ -95,35 +92,32 @@ def _objective(res_kn, n, has_err):
     return out[0], out[1]
 
 
-def iter_on(*iterators):
-    """en:364-383."""
-    iterable = lambda it: isinstance(it, (tuple, list))
-    max_len = 1
-    for it in iterators:
-        if iterable(it):
-            max_len = max(max_len, len(it))
-    new_iterators = []
-    for it in iterators:
-        if iterable(it):
-            assert len(it) in (1, max_len), f'missing {max_len - len(it)} values for parameter={it}'
-            new_iterators.append(it[0] if len(it) == 1 else it)
-        else:
-            new_iterators.append(it)
-    for step in range(max_len):
-        yield tuple(it[step] if iterable(it) else it for it in new_iterators)
+def iter_on(*params):
+    """The per-phase values of bundle_adjustment's phase-wise arguments (en:364-383): as many phases as
+    the longest list or tuple (at least one); a list or tuple gives its k-th value in phase k, or its
+    only value in every phase; anything else is the same in every phase.  A list of another length
+    fails the assertion the reference makes, when the first phase is asked for."""
+    is_seq = lambda v: isinstance(v, (tuple, list))
+    n_phases = max([1] + [len(v) for v in params if is_seq(v)])
+    for v in params:
+        if is_seq(v):
+            assert len(v) in (1, n_phases), f'missing {n_phases - len(v)} values for parameter={v}'
+    per_phase = [(lambda k, v=v: v[0]) if is_seq(v) and len(v) == 1 else
+                 (lambda k, v=v: v[k]) if is_seq(v) else (lambda k, v=v: v) for v in params]
+    for k in range(n_phases):
+        yield tuple(f(k) for f in per_phase)
 
 
 def used_depth_channels(n_zcfs, n_channels, depth_mode):
-    """en:386-402."""
-    phases = n_zcfs if isinstance(n_zcfs, (list, tuple)) else [n_zcfs]
-    used = 0
-    for n in phases:
-        if n is None:
-            return n_channels
-        if depth_mode[:3] == 'log' and not (n == 2 or n == n_channels):
-            n += 1
-        used = max(used, n)
-    return min(used, n_channels)
+    """The leading depth channels bundle_adjustment reads for the phases' n_zcfs (en:386-402): a phase
+    of n coefficients reads n channels, plus the frozen main channel in a log mode unless n is 2 or
+    every channel; a phase with n_zcfs None reads all of them.  At most n_channels."""
+    phases = list(n_zcfs) if isinstance(n_zcfs, (list, tuple)) else [n_zcfs]
+    if any(n is None for n in phases):
+        return n_channels
+    frozen_main = depth_mode.startswith('log')
+    reads = [n + int(frozen_main and n not in (2, n_channels)) for n in phases]
+    return min(max(reads, default=0), n_channels)
 
 
 def line_search(trial, init_loss, min_loss_delta, min_reproj, nonfinite=None):

@@ -549,3 +549,42 @@ def test_entry_points_reject_null_pointers_without_a_gpu():
     pa.long_ptr, pa.long_idx, pa.img_part = ctypes.addressof(n), ctypes.addressof(n), ctypes.addressof(n)
     assert L.ba_pcg_solve(ctypes.byref(pa), None) != 0
     assert b'null pointer' in L.ba_last_error()
+
+
+def test_boundary_helpers_known_answers():
+    """The device engine's host helpers against outcomes worked out by hand from the reference text:
+    iter_on (en:364-383: phases = the longest list, one-value lists repeat, scalars repeat, a list of
+    another length fails), used_depth_channels (en:386-402: n channels per phase, + the frozen main
+    channel in log mode unless n is 2 or all; None reads all), update_K (en:347-354: focal minus the
+    step, clipped at 100, NaN kept) and RigsData.z_coefs_from_scale (rigs.py:69-94: new rows from the
+    scale, [s, 0..] lin / [1, log s, 0..] log, existing rows kept)."""
+    from blast3r_amd import engine as de
+    from blast3r_amd.data import RigsData
+    assert list(de.iter_on(1.0, [1, 2], [3])) == [(1.0, 1, 3), (1.0, 2, 3)]
+    assert list(de.iter_on(0.5)) == [(0.5,)]
+    assert list(de.iter_on([None, 3], 'x')) == [(None, 'x'), (3, 'x')]
+    for bad in (([1, 2], [1, 2, 3]), ([],)):
+        with pytest.raises(AssertionError):
+            list(de.iter_on(*bad))
+    uc = de.used_depth_channels
+    assert uc(None, 5, 'log') == 5 and uc([1, None], 5, 'log') == 5
+    assert uc(3, 5, 'log') == 4 and uc(3, 5, 'lin') == 3 and uc(2, 5, 'log') == 2 and uc(5, 5, 'log') == 5
+    assert uc([1, 17], 17, 'log_multidepth') == 17 and uc([1, 4], 17, 'log') == 5 and uc(9, 5, 'lin') == 5
+    K = torch.tensor([[[500., 0, 256], [0, 510, 192], [0, 0, 1]], [[120., 0, 1], [0, 99, 2], [0, 0, 1]]])
+    K2 = de.update_K(K, torch.tensor([[10., -5.], [30., float('nan')]]))
+    assert K2[0, 0, 0] == 490 and K2[0, 1, 1] == 515 and K2[1, 0, 0] == 100 and torch.isnan(K2[1, 1, 1])
+    assert torch.equal(K2[:, :, 2], K[:, :, 2]) and K[1, 1, 1] == 99            # the input is left alone
+    scale = torch.tensor([2.0, 0.5, 4.0])
+    trk = type('T', (), {'n_imgs': 3, 'pix2d_dep': torch.zeros((7, 4))})()
+    for mode, row in (('lin', [4.0, 0, 0, 0]), ('log', [1.0, math.log(4.0), 0, 0])):
+        r = RigsData(1, torch.zeros(3, dtype=torch.int32), K[:1], K[:1], scale, None, mode, 3,
+                     torch.arange(3, dtype=torch.int32), K[:1])
+        z = r.z_coefs_from_scale(trk)
+        assert z.shape == (3, 4) and torch.allclose(z[2], torch.tensor(row))
+        r.z_coefs = z[:2] * 0 + 7                                    # two rows exist: only the third is made
+        z = r.z_coefs_from_scale(trk)
+        assert torch.equal(z[:2], torch.full((2, 4), 7.0)) and torch.allclose(z[2], torch.tensor(row))
+    bad = RigsData(1, torch.zeros(3, dtype=torch.int32), K[:1], K[:1], scale, None, 'cube', 3,
+                   torch.arange(3, dtype=torch.int32), K[:1])
+    with pytest.raises(ValueError):
+        bad.z_coefs_from_scale(trk)
