@@ -149,6 +149,12 @@ _SIGS = {
     'ba_plan_export': (c_int, [c_p, c_int, c_p]),
     'ba_plan_destroy': (None, [c_p]),
     'ba_plan_last_error': (ctypes.c_char_p, []),
+    'ba_pm_dplan_create': (c_p, [c_p, c_int, c_p, c_i64, c_int, c_p]),
+    'ba_pm_dplan_query': (c_int, [c_p, c_p, c_p]),
+    'ba_pm_dplan_array': (c_p, [c_p, c_int]),
+    'ba_pm_dplan_copy': (c_int, [c_p, c_int, c_p, c_p]),
+    'ba_pm_dplan_destroy': (None, [c_p]),
+    'ba_pm_dplan_last_error': (ctypes.c_char_p, []),
     'ba_plan_append': (c_p, [c_p, c_p, c_int, c_p, c_i64, c_int]),
     'ba_plan_array': (c_p, [c_p, c_int]),
     'ba_plan_stable': (c_int, [c_p, c_p, c_p]),

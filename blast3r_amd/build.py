@@ -11,7 +11,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libba_hip.so')
 SOURCES = ['ba_compat.hip', 'ba_schur.hip', 'ba_pcg.hip', 'ba_chol.hip', 'ba_update.hip', 'ba_sample.hip', 'ba_tracks.hip', 'ba_tangent.hip',
-           'ba_plan.cpp']
+           'ba_pmplan.hip', 'ba_plan.cpp']
 ARCH = os.environ.get('BA_OFFLOAD_ARCH', 'gfx950')
 
 HIPCC_FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',

@@ -223,21 +223,49 @@ PM_ARRAYS = ['run_ptr', 'run_obs', 'run_trk', 'run_img', 'img_run_ptr', 'trk_run
 PM_SCALARS = ['n_runs', 'n_pairs', 'n_terms', 'max_terms', 'max_track_runs']
 
 
+class _DeviceArrays:
+    """A plan's arrays on the host, copied from its device arrays on first use."""
+
+    def __init__(self, plan):
+        self._plan = weakref.ref(plan)
+        self._d = {}
+
+    def __getitem__(self, name):
+        if name not in self._d:
+            pl = self._plan()
+            self._d[name] = pl.dev[name][:pl.sizes[name]].cpu().numpy()
+        return self._d[name]
+
+    def __contains__(self, name):
+        return name in PM_ARRAYS
+
+    def keys(self):
+        return list(PM_ARRAYS)
+
+
 class PMPlan:
-    """Device-resident pair-major plan for one (infos, pids) structure (ba_pm_plan_create): runs (the
-    observations of one track in one image), the tracks' runs and observations in image order, and
-    the image pairs with their (run, run) terms.  No limit on track length or co-visibility."""
+    """Device-resident pair-major plan for one (infos, pids) structure: runs (the observations of one track
+    in one image), the tracks' runs and observations in image order, and the image pairs with their (run,
+    run) terms.  No limit on track length or co-visibility.  Built on the GPU for CUDA inputs
+    (ba_pm_dplan_create), on the host otherwise (ba_pm_plan_create, host_planner=True forces it); the two
+    give the same arrays."""
     kind = 'pairmajor'
 
-    def __init__(self, infos, pids, n_tracks, device=None):
-        device = device or pids.device
-        cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
+    def __init__(self, infos, pids, n_tracks, device=None, host_planner=False):
+        device = torch.device(device or pids.device)
         self.node_ids = np.ascontiguousarray(infos[1].detach().cpu().numpy().astype(np.int64))
         self.cam_ids = np.ascontiguousarray(infos[2].detach().cpu().numpy().astype(np.int64))
-        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
-        self.n_imgs = int(cum.shape[0])
-        self.n_obs = int(p.shape[0])
+        self.n_imgs = int(infos.shape[1])
+        self.n_obs = int(pids.shape[0])
         self.n_tracks = int(n_tracks)
+        self.device = device
+        self._ws = {}
+        self.workspace_cache = {}
+        if device.type == 'cuda' and not host_planner:
+            self._build_on_device(infos, pids)
+            return
+        cum = np.ascontiguousarray(infos[0].detach().cpu().numpy().astype(np.int32, copy=False))
+        p = np.ascontiguousarray(pids.detach().cpu().numpy().astype(np.int32, copy=False))
         L = lib()
         h = L.ba_pm_plan_create(cum.ctypes.data_as(ctypes.c_void_p), self.n_imgs, p.ctypes.data_as(ctypes.c_void_p),
                                 self.n_obs, self.n_tracks)
@@ -255,13 +283,39 @@ class PMPlan:
                 self.host[name] = arr
         finally:
             L.ba_pm_plan_destroy(h)
-        self.device = torch.device(device)
+        self.sizes = {k: int(v.shape[0]) for k, v in self.host.items()}
         self.dev = {k: torch.from_numpy(v).to(self.device) for k, v in self.host.items()}
         for k in PM_ARRAYS:     # never hand a null pointer to a kernel for an empty array
             if self.dev[k].numel() == 0:
                 self.dev[k] = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self._ws = {}
-        self.workspace_cache = {}
+
+    def _build_on_device(self, infos, pids):
+        """ba_pm_dplan_create on the device's current stream; its arrays are copied into torch tensors (the
+        plan is then released), and the host copies are made on first use."""
+        L = lib()
+        dev = self.device
+        cum = infos[0].to(device=dev, dtype=torch.int32).contiguous()
+        p = pids.to(device=dev, dtype=torch.int32).contiguous()
+        st = stream_ptr(dev)
+        h = L.ba_pm_dplan_create(ctypes.c_void_p(cum.data_ptr()), self.n_imgs, ctypes.c_void_p(p.data_ptr()),
+                                 self.n_obs, self.n_tracks, st)
+        if not h:
+            raise RuntimeError('pair-major structure plan failed: ' + (L.ba_pm_dplan_last_error() or b'').decode())
+        try:
+            sc = np.zeros(len(PM_SCALARS), dtype=np.int64)
+            sz = np.zeros(len(PM_ARRAYS), dtype=np.int64)
+            check(L.ba_pm_dplan_query(h, sc.ctypes.data_as(ctypes.c_void_p), sz.ctypes.data_as(ctypes.c_void_p)))
+            self.scalars = {k: int(v) for k, v in zip(PM_SCALARS, sc)}
+            self.sizes = {k: int(sz[i]) for i, k in enumerate(PM_ARRAYS)}
+            self.dev = {}
+            for i, name in enumerate(PM_ARRAYS):
+                t = torch.zeros(max(int(sz[i]), 1), dtype=torch.int32, device=dev)
+                check(L.ba_pm_dplan_copy(h, i, ctypes.c_void_p(t.data_ptr()), st))
+                self.dev[name] = t
+            torch.cuda.current_stream(dev).synchronize()
+        finally:
+            L.ba_pm_dplan_destroy(h)
+        self.host = _DeviceArrays(self)
 
     workspace = BAPlan.workspace
 

@@ -191,6 +191,19 @@ void* ba_pm_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t*
 int ba_pm_plan_query(const void* plan, int64_t* scalars, int64_t* array_sizes);
 int ba_pm_plan_export(const void* plan, int32_t which, int32_t* host_dst);
 void ba_pm_plan_destroy(void* plan);
+/* The same plan built on the device, array for array equal to ba_pm_plan_create's (the reference derives
+ * this structure with torch.unique / index_add_ on every solve, ba_solver.py:877-909): cum_nkpts (n_imgs)
+ * and pids (n_obs) are device arrays; the plan owns its device arrays (hipMalloc) until
+ * ba_pm_dplan_destroy.  Runs on `stream` and synchronises it while it sizes its arrays (once per
+ * structure, never inside a solve).  NULL on error: ba_pm_dplan_last_error() says why. */
+void* ba_pm_dplan_create(const int32_t* cum_nkpts, int32_t n_imgs, const int32_t* pids, int64_t n_obs,
+                         int32_t n_tracks, void* stream);
+int ba_pm_dplan_query(const void* plan, int64_t* scalars, int64_t* array_sizes);
+const int32_t* ba_pm_dplan_array(const void* plan, int32_t which);
+/* array `which` (BA_PM_* order) into a device buffer of at least its length, on `stream` */
+int ba_pm_dplan_copy(const void* plan, int32_t which, int32_t* dst, void* stream);
+void ba_pm_dplan_destroy(void* plan);
+const char* ba_pm_dplan_last_error(void);
 
 typedef struct {
     /* structure: the pair-major plan's arrays (device) */
