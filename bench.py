@@ -550,6 +550,13 @@ def bench_pairmajor(cfg, dev, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # the dominant kernel alone (stage 1 of the pass: k_pm_pairs, the off-diagonal pair blocks)
+    e0.record(stream)
+    for _ in range(steps):
+        check(L.ba_pm_linearize_stage(a, 1, st))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pairs_ms = e0.elapsed_time(e1) / steps
     kw = dict(dtype=torch.float64,
               weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=o['pnorm'], optim_K=o['optim_K'],
               optim_P=o['optim_P'])
@@ -561,6 +568,40 @@ def bench_pairmajor(cfg, dev, steps, warmup):
         engine.lm_step(**g.lm_inputs(), **kw)
     torch.cuda.synchronize()
     lm_ms = (time.perf_counter() - t0) * 1e3 / n_lm
+    # the structure plan built on the device (a structure change), after the build above warmed it
+    from blast3r_amd.plan import PMPlan
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    PMPlan(g.infos, g.pids, prob.n_tracks, device=dev)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    # the reference's default solver precision (GaussNewtonSolver dtype=torch.float32): the same pass in
+    # fp32, and lm_step called without dtype
+    gs32 = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, dtype=torch.float32)
+    J32 = gs32.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                 g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d, hp=hp)
+    ctx32 = gs32.prepare(J32, res, w)
+    a32 = ctx32['args']
+    for _ in range(warmup):
+        check(L.ba_pm_linearize_schur(a32, st))
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        check(L.ba_pm_linearize_schur(a32, st))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms32 = e0.elapsed_time(e1) / steps
+    kw32 = {k: v for k, v in kw.items() if k != 'dtype'}
+    engine.lm_step(**g.lm_inputs(), **kw32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n_lm):
+        engine.lm_step(**g.lm_inputs(), **kw32)
+    torch.cuda.synchronize()
+    lm32_ms = (time.perf_counter() - t0) * 1e3 / n_lm
+    del gs32, J32, ctx32
+    log(f'[bench] pair-major cfg {cfg}: device plan {plan_ms:.1f} ms; fp32 pass {ms32:.3f} ms, fp32 lm_step '
+        f'{lm32_ms:.2f} ms')
     alg = algorithmic_counts(prob, ctx['lay'], sc['n_terms'] + prob.n_obs, sc['n_pairs'])
     v_bytes = sc['n_terms'] * 2 * 3 * (16 if ctx['lay']['d'] <= 15 else 32) * 8
     pairs_traffic, src = measured_traffic(cfg, 'k_pm_pairs')
@@ -570,12 +611,25 @@ def bench_pairmajor(cfg, dev, steps, warmup):
                      f'd={ctx["lay"]["d"]}',
            'ms_per_step': ms, 'obs_per_s': prob.n_obs / (ms * 1e-3), 'lm_ms_per_iter': lm_ms,
            'lm_iters_per_s': 1e3 / lm_ms, 'runs': sc['n_runs'], 'pairs': sc['n_pairs'], 'pair_terms': sc['n_terms'],
+           'plan_device_ms': plan_ms,
+           'fp32_solver': {'note': 'GaussNewtonSolver(dtype=torch.float32), the reference default lm_step uses',
+                           'ms_per_step': ms32, 'obs_per_s': prob.n_obs / (ms32 * 1e-3), 'lm_ms_per_iter': lm32_ms,
+                           'lm_iters_per_s': 1e3 / lm32_ms},
            'hbm_roofline': {'achieved': alg['bytes'] / (ms * 1e-3) / 1e9, 'peak': 8000.0, 'unit': 'GB/s',
                             'frac': alg['bytes'] / (ms * 1e-3) / 1e9 / 8000.0, 'bytes_per_step': alg['bytes'],
                             'bytes_rule': alg['bytes_rule']},
            'k_pm_pairs': {'bound': 'hbm', 'v_bytes_per_launch': v_bytes,
-                          'v_rule': 'two V rows (3 x dp fp64) read per pair term',
-                          'traffic': pairs_traffic, 'traffic_source': src}}
+                          'v_rule': 'two V rows (3 x dp fp64, dp = 16 for d <= 15) read per pair term',
+                          'traffic': pairs_traffic, 'traffic_source': src, 'kernel_ms': pairs_ms},
+           'roofline': {'kernel': 'k_pm_pairs', 'bound': 'hbm', 'kernel_ms': pairs_ms,
+                        'achieved': v_bytes / (pairs_ms * 1e-3) / 1e9, 'peak': 8000.0, 'unit': 'GB/s',
+                        'frac': v_bytes / (pairs_ms * 1e-3) / 1e9 / 8000.0,
+                        'fp64_tflops': alg['flops_dense'] * sc['n_terms'] / (sc['n_terms'] + prob.n_obs)
+                        / (pairs_ms * 1e-3) / 1e12,
+                        'fp64_frac': alg['flops_dense'] * sc['n_terms'] / (sc['n_terms'] + prob.n_obs)
+                        / (pairs_ms * 1e-3) / 78.6e12,
+                        'rule': 'V rows requested (two 3 x dp fp64 rows per off-diagonal term) over the kernel '
+                                'time; fp64: 6 d_alg^2 per off-diagonal term'}}
     del gs, J, ctx, g, prob
     torch.cuda.empty_cache()
     return res

@@ -177,7 +177,8 @@ int ba_backsubstitute(const ba_lin_args* args, void* stream);
  * image, point blocks per track), built without chunks or batches, so that tracks of any length, up
  * to 31 image-level parameters and any co-visibility pattern are handled (the batched path needs
  * d <= 15, tracks within 13 images and 128 observations, and is slow on random co-visibility).
- * Structure from ba_pm_plan_create (host); a run is the observations of one track in one image:
+ * Structure from ba_pm_plan_create (host) or ba_pm_dplan_create (device); a run is the observations of
+ * one track in one image:
  *   per observation       J_p^T J_p and J_p^T W r (pobs); per wave of BA_PM_SPAN observations and
  *                         image, sum J_c^T J_c and J_c^T W r (jslots, MFMA)
  *   per track             H_pp, g_p in image order; the point-leaf damping; L, L^-1 g_p
