@@ -1146,29 +1146,36 @@ def test_backsubstitute_image_level_delta_matches_unknown_map():
 _FULL_SIZE = {1: (256, 200_000), 2: (1024, 1_000_000), 3: (4096, 3_000_000), 4: (1024, 1_000_000)}
 
 
-@pytest.mark.parametrize('cfg,path', [(2, 'auto'), (2, 'pairmajor'), (3, 'auto'), (1, 'auto'), (4, 'auto')])
-def test_reduced_system_full_size_against_oracle(cfg, path):
+@pytest.mark.parametrize('cfg,path,dtype', [(2, 'auto', torch.float64), (2, 'pairmajor', torch.float64),
+                                            (3, 'auto', torch.float64), (1, 'auto', torch.float64),
+                                            (4, 'auto', torch.float64), (2, 'auto', torch.float32),
+                                            (3, 'auto', torch.float32)],
+                         ids=['cfg2', 'cfg2-pm', 'cfg3', 'cfg1', 'cfg4', 'cfg2-fp32', 'cfg3-fp32'])
+def test_reduced_system_full_size_against_oracle(cfg, path, dtype):
     """Full benchmark sizes (config 1: 256 frames, 200 k tracks on 24-frame neighbourhoods, 1.3 M
     observations, pair-major; config 2: 1024 frames, 1 M tracks, 8.0 M observations, on the batched and
     the pair-major path; config 3: 4096 frames with a camera each, 3 M tracks on random neighbours,
     22.5 M observations, pair-major; config 4: config 2's scene with 9 depth channels, focal and poses
     fixed, 8.0 M observations, batched): the reduced rhs, the point blocks and S v for seeded v against
     the oracle's normal equations at the same size and with the configuration's own flags (the oracle's
-    pass takes seconds on the host's threads), to the 1e-5 bar."""
+    pass takes seconds on the host's threads), to the 1e-5 bar; also with dtype=torch.float32 (the
+    reference's default solver precision: the pair-major pass in fp32 throughout), against the same
+    fp64 normal equations and bar (measured 3.6e-6 / 2.7e-6 on S v at configs 2 / 3)."""
     import os
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     p = make_problem(cfg)
     assert (p.n_imgs, p.n_tracks) == _FULL_SIZE[cfg]
     print(f'[full cfg{cfg} {path}] {p.n_obs} observations', flush=True)
     flags = _cfg_flags(p)
-    gs, _, _ = _gpu_solver(p, path=path, **flags)
+    gs, _, _ = _gpu_solver(p, path=path, dtype=dtype, **flags)
     last = gs.last
-    assert last['path'] == ('batched' if (cfg, path) in ((2, 'auto'), (4, 'auto')) else 'pairmajor')
+    batched = (cfg, path) in ((2, 'auto'), (4, 'auto')) and dtype == torch.float64
+    assert last['path'] == ('batched' if batched else 'pairmajor') and last['S_pairs'].dtype == dtype
     um, d, plan = last['unknowns'], last['lay']['d'], last['plan']
-    rhs = last['rhs'].cpu()
+    rhs = last['rhs'].double().cpu()
     H = gs.point_blocks()[0].cpu()
     n_pairs = plan.scalars['n_pairs']
-    B = last['S_pairs'][:n_pairs].view(n_pairs, d, d)
+    B = last['S_pairs'][:n_pairs].view(n_pairs, d, d).double()
     i1 = plan.dev['pair_i1'][:n_pairs].long()
     i2 = plan.dev['pair_i2'][:n_pairs].long()
     umap = um['umap'].long().view(p.n_imgs, d)
@@ -1185,7 +1192,7 @@ def test_reduced_system_full_size_against_oracle(cfg, path):
         y_img.index_add_(0, i2[off], torch.bmm(Bt, v_img[i1[off]].unsqueeze(2)).squeeze(2))
         y = torch.zeros(n_u, dtype=v.dtype, device=DEV)
         y.index_add_(0, umap[valid], y_img[valid])
-        return (y + last['damp'] * v).cpu()
+        return (y + last['damp'].double() * v).cpu()
 
     ne, gvec, _, _, _, _ = _oracle_ne(p, **flags)
     print(f'[full cfg{cfg}] oracle normal equations built', flush=True)
