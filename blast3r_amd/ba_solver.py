@@ -48,6 +48,17 @@ class Linearization:
         s = self.solver
         return (3 * s.n_kpts, s.cams.n * N_FOC + s.nodes.n * N_TAU + s.imgs.n * s.n_zcf + s.tracks.n * 3)
 
+    def with_z_by_prior(self):
+        """This linearisation with the z-coefficient columns of every image in the reduced system and
+        their Jacobian entries zero: the switched-off z block (a ZerosMat) that a tangent prior turns
+        into its H_z (bs:163-164), so that z moves under the prior alone."""
+        kw = dict(self.__dict__)
+        solver = kw.pop('solver')
+        en = dict(kw['en'])
+        en['Z'] = (True, torch.zeros(solver.imgs.true_n, dtype=torch.uint8, device=self.pids.device), None)
+        kw['en'] = en
+        return Linearization(solver, **kw)
+
 
 def _flag(status, name, count, device):
     """Normalise an optim_* flag: returns (enabled_group, uint8 mask or None, kept indices or None).
@@ -241,6 +252,8 @@ class GaussNewtonSolver:
     # ------------------------------------------------------------------ bs:110-182
     def solve_delta(self, J, residuals, w_pts, clamp_w=(1e-6, 1e6), z_prior=None):
         """Solve (J^T W J + damping) delta = J^T W r by Schur reduction; returns fp32 delta."""
+        if z_prior is not None and z_prior[0] is not None and z_prior[1] is not None and not J.en['Z'][0]:
+            J = J.with_z_by_prior()
         ctx = self.prepare(J, residuals, w_pts, clamp_w)
         st = ctx['stream']
         if ctx['lay']['d'] > 0:
@@ -680,8 +693,7 @@ class GaussNewtonSolver:
         H_z, g_z = z_prior
         if H_z is None or g_z is None:
             return
-        if not lay['hasZ']:
-            raise TypeError('Unsupported JTJ.A type for z_prior: z-coefficients are not optimised')
+        assert lay['hasZ'], 'the z unknowns of a prior are in the reduced system (with_z_by_prior)'
         C = self.n_zcf
         o = lay['d'] - C
         R = S_pairs.dtype

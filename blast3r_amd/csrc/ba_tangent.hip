@@ -20,6 +20,9 @@
 //   dt/da_c = L_c(q) U + L_c(p) V,  U = P X(q) / |t|,  V = -P X(p) / |t|,  P = I - t_hat t_hat^T
 // (P = I and |t0| without normalisation), so per pair five dot products and the channel values
 // give g and H.  Partials go to a workspace in tile order and are summed per image in that order.
+// Up to 16 coefficients one workgroup holds the whole upper triangle of H in registers; above that
+// (up to 24) the rows of H are split over TG_RB-row groups (grid z), each group recomputing the
+// tile and holding only its rows.
 //
 // Precision: fp32 or fp64 working type T (the reference's dtype argument), with the pointmap
 // tangents and the confidence in fp32 as the reference keeps them; sums in fp64.  The fp32 parts
@@ -40,7 +43,8 @@ namespace ba {
 #define TG_TC 64                // tile columns (pair origins)
 #define TG_RC (TG_TC + 1)
 #define TG_HC (TG_TC + 3)
-#define TG_CMAX 16
+#define TG_CMAX 24              // z-coefficients with the Gauss-Newton terms
+#define TG_RB 4                 // rows of H per workgroup above 16 coefficients
 // tile rows: 16 for the loss alone, 8 with the Gauss-Newton terms, 4 with more than 8 coefficients
 // (the channel values then fill LDS)
 template <int CMAX, bool GN> struct TgRows { static constexpr int TR = !GN ? 16 : (CMAX > 8 ? 4 : 8); };
@@ -188,10 +192,14 @@ __global__ void __launch_bounds__(TG_T) k_tan_median(ba_tangent_args a, uint64_t
 }
 
 // ---------------------------------------------------------------- tiles
-template <typename T, int CMAX, bool GN, bool NORM>
+// RB = 0: the whole upper triangle of H; RB > 0: rows c0 .. c0 + RB - 1 of H (c0 = RB blockIdx.z),
+// full rows, of which the entries on and right of the diagonal are written
+template <typename T, int CMAX, bool GN, bool NORM, int RB = 0>
 __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const double* __restrict__ scale,
                                                     double* __restrict__ part, int n_tc, int n_acc) {
-    constexpr int E = CMAX * (CMAX + 1) / 2;
+    constexpr int NR = RB > 0 ? RB : CMAX;
+    constexpr int E = RB > 0 ? RB * CMAX : CMAX * (CMAX + 1) / 2;
+    const int c0 = RB > 0 ? (int)blockIdx.z * RB : 0;
     constexpr int TG_TR = TgRows<CMAX, GN>::TR, TG_RR = TG_TR + 1, TG_HR = TG_TR + 3;
     __shared__ float sD0[TG_HR][TG_HC];
     __shared__ T sX[3][TG_RR * TG_RC];
@@ -262,11 +270,11 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
     __syncthreads();
 
     double lsum[2] = {0.0, 0.0};
-    double g[GN ? CMAX : 1];
+    double g[GN ? NR : 1];
     double Hacc[GN ? E : 1];
     if (GN) {
 #pragma unroll
-        for (int c = 0; c < CMAX; ++c) g[c] = 0.0;
+        for (int c = 0; c < NR; ++c) g[c] = 0.0;
 #pragma unroll
         for (int e = 0; e < E; ++e) Hacc[e] = 0.0;
     }
@@ -328,13 +336,28 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
                 al[c] = c < C ? (double)sL[c][q] : 0.0;
                 be[c] = c < C ? (double)sL[c][p] : 0.0;
             }
+            if (RB == 0) {
 #pragma unroll
-            for (int c = 0; c < CMAX; ++c) {
-                g[c] += ww * (al[c] * ur + be[c] * vr);
-                const double s1 = ww * (al[c] * uu + be[c] * uv);
-                const double s2 = ww * (al[c] * uv + be[c] * vv);
+                for (int c = 0; c < CMAX; ++c) {
+                    g[c] += ww * (al[c] * ur + be[c] * vr);
+                    const double s1 = ww * (al[c] * uu + be[c] * uv);
+                    const double s2 = ww * (al[c] * uv + be[c] * vv);
 #pragma unroll
-                for (int d2 = c; d2 < CMAX; ++d2) Hacc[c * CMAX - c * (c - 1) / 2 + (d2 - c)] += s1 * al[d2] + s2 * be[d2];
+                    for (int d2 = c; d2 < CMAX; ++d2) Hacc[c * CMAX - c * (c - 1) / 2 + (d2 - c)] += s1 * al[d2] + s2 * be[d2];
+                }
+            } else {
+#pragma unroll
+                for (int r2 = 0; r2 < NR; ++r2) {
+                    // the group's row c (uniform over the workgroup) read from LDS: a register array
+                    // indexed at run time would live in scratch memory
+                    const int c = c0 + r2;
+                    const double ac = c < C ? (double)sL[c][q] : 0.0, bc = c < C ? (double)sL[c][p] : 0.0;
+                    g[r2] += ww * (ac * ur + bc * vr);
+                    const double s1 = ww * (ac * uu + bc * uv);
+                    const double s2 = ww * (ac * uv + bc * vv);
+#pragma unroll
+                    for (int d2 = 0; d2 < CMAX; ++d2) Hacc[r2 * CMAX + d2] += s1 * al[d2] + s2 * be[d2];
+                }
             }
         }
     }
@@ -350,6 +373,30 @@ __global__ void __launch_bounds__(TG_T) k_tan_tile(ba_tangent_args a, const doub
         return t2;
     };
     double v;
+    if (RB > 0) {
+        // (bsum synchronises the workgroup: every condition below is uniform over it)
+        if (c0 == 0) {
+            v = bsum(lsum[0]); if (threadIdx.x == 0) out[0] = v;
+            v = bsum(lsum[1]); if (threadIdx.x == 0) out[1] = v;
+        }
+#pragma unroll
+        for (int r2 = 0; r2 < NR; ++r2) {
+            const int c = c0 + r2;
+            if (c >= C) break;
+            v = bsum(g[r2]);
+            if (threadIdx.x == 0) out[2 + c] = v;
+            // entry (c, d2) of the upper triangle, row by row: sum_{c' < c} (C - c') + (d2 - c)
+            const int row0 = 2 + C + c * C - c * (c - 1) / 2 - c;
+#pragma unroll
+            for (int d2 = 0; d2 < CMAX; ++d2) {
+                if (d2 >= c && d2 < C) {
+                    v = bsum(Hacc[r2 * CMAX + d2]);
+                    if (threadIdx.x == 0) out[row0 + d2] = v;
+                }
+            }
+        }
+        return;
+    }
     v = bsum(lsum[0]); if (threadIdx.x == 0) out[0] = v;
     v = bsum(lsum[1]); if (threadIdx.x == 0) out[1] = v;
     if (GN) {
@@ -464,7 +511,8 @@ struct TgLayout {
 
 // tile rows of the kernel instantiation chosen for C (see launch_all)
 static int tg_tile_rows(int C, int compute_gn) {
-    return !compute_gn ? TgRows<1, false>::TR : (C > 8 ? TgRows<16, true>::TR : TgRows<8, true>::TR);
+    return !compute_gn ? TgRows<1, false>::TR
+                       : (C > 16 ? TgRows<TG_CMAX, true>::TR : C > 8 ? TgRows<16, true>::TR : TgRows<8, true>::TR);
 }
 
 static TgLayout tg_layout(int64_t n_imgs, int C, int H, int W, int s, int normalize, int compute_gn) {
@@ -490,10 +538,12 @@ extern "C" int64_t ba_tangent_workspace_bytes(int64_t n_imgs, int32_t C, int32_t
     return tg_layout(n_imgs, C, H, W, tan_stride, normalize, compute_gn).total;
 }
 
-template <typename T, int CMAX, bool GN, bool NORM>
+template <typename T, int CMAX, bool GN, bool NORM, int RB = 0>
 static void launch_tiles(const ba_tangent_args& a, const TgLayout& L, char* ws, hipStream_t st) {
-    hipLaunchKernelGGL((k_tan_tile<T, CMAX, GN, NORM>), dim3((unsigned)L.n_tiles, (unsigned)a.n_imgs), dim3(TG_T), 0, st,
-                       a, (const double*)(ws + L.off_scale), (double*)(ws + L.off_part), L.n_tc, L.n_acc);
+    const unsigned groups = RB > 0 ? (unsigned)((a.C + RB - 1) / RB) : 1u;
+    hipLaunchKernelGGL((k_tan_tile<T, CMAX, GN, NORM, RB>), dim3((unsigned)L.n_tiles, (unsigned)a.n_imgs, groups),
+                       dim3(TG_T), 0, st, a, (const double*)(ws + L.off_scale), (double*)(ws + L.off_part), L.n_tc,
+                       L.n_acc);
 }
 
 template <typename T>
@@ -514,9 +564,12 @@ static void launch_all(const ba_tangent_args& a, const TgLayout& L, char* ws, hi
         } else if (a.C <= 12) {
             if (a.normalize) launch_tiles<T, 12, true, true>(a, L, ws, st);
             else launch_tiles<T, 12, true, false>(a, L, ws, st);
+        } else if (a.C <= 16) {
+            if (a.normalize) launch_tiles<T, 16, true, true>(a, L, ws, st);
+            else launch_tiles<T, 16, true, false>(a, L, ws, st);
         } else {
-            if (a.normalize) launch_tiles<T, TG_CMAX, true, true>(a, L, ws, st);
-            else launch_tiles<T, TG_CMAX, true, false>(a, L, ws, st);
+            if (a.normalize) launch_tiles<T, TG_CMAX, true, true, TG_RB>(a, L, ws, st);
+            else launch_tiles<T, TG_CMAX, true, false, TG_RB>(a, L, ws, st);
         }
     } else {
         if (a.normalize) launch_tiles<T, 1, false, true>(a, L, ws, st);
@@ -534,7 +587,7 @@ extern "C" int ba_tangent_prior(const ba_tangent_args* args, void* stream) {
     hipStream_t st = (hipStream_t)stream;
     BA_REQUIRE(a.n_imgs >= 1 && a.n_imgs <= 65535, "n_imgs must be in [1, 65535]");
     BA_REQUIRE(a.C >= 1 && a.tan_stride >= 1 && a.H >= 0 && a.W >= 0, "bad sizes");
-    BA_REQUIRE(!a.compute_gn || a.C <= TG_CMAX, "the Gauss-Newton terms support at most 16 z-coefficients");
+    BA_REQUIRE(!a.compute_gn || a.C <= TG_CMAX, "the Gauss-Newton terms support at most 24 z-coefficients");
     BA_REQUIRE(a.depth_pix_stride >= a.C && a.ref_pix_stride >= 3, "pixel strides below the channel counts");
     BA_REQUIRE(a.depth_addr && a.ref_addr && a.K && a.cam_ids && a.z_coefs && a.loss && a.workspace, "missing arrays");
     BA_REQUIRE(!a.compute_gn || (a.g_z && a.H_z), "g_z / H_z missing");

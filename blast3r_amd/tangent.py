@@ -5,7 +5,7 @@ Same arguments, defaults and results (tan_loss as a 0-d tensor of ``dtype``; g_z
 H_z (n_imgs, C, C), or None when ``compute_gn`` is False).  Every image is handled by one launch
 sequence of ``ba_tangent_prior`` in libba_hip.so, which reads each image's maps where they lie
 (a list of per-image tensors, channel slices of wider maps, or one stacked tensor).  With
-compute_gn, up to 16 z-coefficients are supported.
+compute_gn, up to 24 z-coefficients are supported (the solver's own limit).
 """
 import ctypes
 

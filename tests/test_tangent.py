@@ -165,11 +165,71 @@ def _rel(a, b):
     return float((a - b).norm()) / n if n > 0 else float((a - b).norm())
 
 
+def _oracle_reduced(p, z_prior, optim_Z, dampen):
+    """The oracle's reduced system (S, rhs) and z offset for problem p with the prior z_prior."""
+    from oracle import kernels as ok
+    from oracle import solver as osol
+    from oracle import engine as oeng
+    inp, o = p.lm_inputs(), p.options
+    _, res, w = oeng.objective(inp['rigs'], inp['K'], inp['P_rig2cam'], inp['P_w2rig'], inp['z_coefs'], inp['pts3d'],
+                               inp['pids'], inp['pix2d'], inp['pix2d_std'], inp['pix2d_dep'], True, o['weight_z'],
+                               1.0, 100.0, o['huber_delta'])
+    Jc, Jz, Jp = ok.jacobians_with_rigs(inp['rigs'], inp['K'], inp['P_rig2cam'], inp['P_w2rig'], inp['z_coefs'],
+                                        inp['pts3d'], inp['pids'], inp['pix2d_std'], inp['pix2d_dep'], True,
+                                        float64=True)
+    prob = osol.Problem(inp['rigs'], inp['pids'], len(inp['K']), len(inp['P_w2rig']), len(inp['pts3d']),
+                        inp['z_coefs'].shape[1])
+    ne, g, _ = osol.build_normal_equations(prob, Jc, Jz, Jp, res, w, optim_Z=optim_Z, dampen=dampen,
+                                           z_prior=z_prior)
+    return osol.dense_schur(ne), osol.reduced_rhs(ne, g), ne.leaf_offsets['zcf']
+
+
+def test_oracle_prior_enters_the_normal_equations_before_damping():
+    """What bs:141-173 fixes, on the oracle's reduced system (dampen 1e-3 so that the damping's
+    dependence on the prior shows): with optim_Z the prior adds H_z to each image's z block, g_z to
+    the z rhs and nothing elsewhere, and the z leaf's damping is recomputed from the diagonal that
+    includes H_z; with optim_Z=False the z block is exactly H_z + dampen max(diag H_z) I, decoupled
+    from every other unknown, and the z rhs is g_z."""
+    from blast3r_amd.synthetic import make_problem
+    p = make_problem(0, n_frames=4, n_tracks=60)
+    n_imgs, C = p.z_coefs.shape
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn((n_imgs, C, C), generator=g, dtype=torch.float64)
+    H_z = A @ A.transpose(1, 2) + 0.1 * torch.eye(C, dtype=torch.float64)
+    g_z = torch.randn((n_imgs, C), generator=g, dtype=torch.float64)
+    dampen = 1e-3
+    S0, r0, oz = _oracle_reduced(p, None, True, dampen)
+    S1, r1, oz1 = _oracle_reduced(p, (H_z, g_z), True, dampen)
+    assert oz == oz1
+    nz = n_imgs * C
+    z = slice(oz, oz + nz)
+    dS = S1 - S0
+    Hb = torch.block_diag(*H_z)
+    off = dS.clone()
+    off[z, z] = 0
+    assert float(off.abs().max()) == 0.0                              # nothing outside the z block moves
+    lam_diff = torch.diagonal(dS[z, z] - Hb)                           # (lam1 - lam0) on every z unknown
+    assert float((lam_diff - lam_diff[0]).abs().max()) <= 1e-12 * float(Hb.abs().max())
+    assert float((dS[z, z] - Hb - torch.diag(lam_diff)).abs().max()) <= 1e-12 * float(Hb.abs().max())
+    assert float(lam_diff[0]) > 0                                      # the damping grew with the diagonal
+    dr = r1 - r0
+    assert oz + nz == len(dr) and float(dr[:oz].abs().max()) == 0.0     # z comes last in the reduced system
+    assert float((dr[z] - g_z.reshape(-1)).abs().max()) <= 1e-12 * float(g_z.abs().max())
+    # optim_Z=False: the z block under the prior alone
+    S2, r2, oz2 = _oracle_reduced(p, (H_z, g_z), False, dampen)
+    lam = dampen * float(torch.diagonal(H_z, dim1=1, dim2=2).max())
+    assert float((S2[z, z] - Hb - lam * torch.eye(nz, dtype=torch.float64)).abs().max()) <= 1e-12 * float(Hb.abs().max())
+    assert float(S2[z, :oz].abs().max()) == 0.0 and float(S2[:oz, z].abs().max()) == 0.0
+    assert torch.equal(r2[z], g_z.reshape(-1))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize('normalize', [True, False])
 @pytest.mark.parametrize('dtype', [torch.float64, torch.float32])
-@pytest.mark.parametrize('C,stride,n_cams,wide', [(5, 4, 1, None), (9, 3, 3, 12), (14, 4, 2, None), (3, 1, 1, None)])
+@pytest.mark.parametrize('C,stride,n_cams,wide', [(5, 4, 1, None), (9, 3, 3, 12), (14, 4, 2, None), (3, 1, 1, None),
+                                                  (17, 4, 1, None), (23, 3, 2, 30)])
 def test_device_tangent_prior_matches_oracle(normalize, dtype, C, stride, n_cams, wide):
+    """C <= 16: one workgroup per tile holds all of H; C = 17 and 23: H split over row groups."""
     cam_ids, K, z, maps, refs = _scene(7 + C, n_imgs=3, H=40, W=52, C=C, n_cams=n_cams, stride_ch=wide)
     kw = dict(weight_tan=0.8, tan_stride=stride, normalize_tangents=normalize, dtype=dtype)
     from blast3r_amd.tangent import dense_tangent_prior_terms
@@ -223,17 +283,19 @@ def test_device_planar_confidence_matches_oracle():
 
 
 @pytest.mark.gpu
-def test_lm_step_with_tangent_prior_parity():
+@pytest.mark.parametrize('optim_Z,n_channels', [(True, None), (False, None), (True, 16)])
+def test_lm_step_with_tangent_prior_parity(optim_Z, n_channels):
     """lm_step with weight_tan > 0 (prior loss in every objective, GN terms added to the z blocks)
     against the oracle with the same prior, checked as test_lm_step_parity checks a step: the step
     delta against the oracle's PCG iterate after the same number of updates (1e-4), the oracle's
     line search on the device's delta (same scales, loss and parameters within 1e-5); the
-    start-of-step loss (Huber mean + prior) to 1e-4."""
+    start-of-step loss (Huber mean + prior) to 1e-4.  optim_Z=False: the z-coefficients move under the
+    prior alone (their zero Jacobian block becomes H_z, bs:163-164); 16 channels: C = 17, d = 25."""
     from blast3r_amd.synthetic import make_problem
     from blast3r_amd import engine as gpu_engine
     import oracle.engine as oeng
     from helpers import rel_err
-    p = make_problem(0, n_frames=6, n_tracks=150)
+    p = make_problem(0, n_frames=6, n_tracks=150, n_channels=n_channels)
     o = p.options
     n_imgs, C = p.z_coefs.shape
     H, W = 96, 128
@@ -261,10 +323,11 @@ def test_lm_step_with_tangent_prior_parity():
     gp = p.to(DEV)
     info = {}
     up_g, st_g, _ = gpu_engine._lm_step(**gp.lm_inputs(), log_depth_maps=[m.to(DEV) for m in maps], conf=conf,
-                                        pts3d_ref=[r.to(DEV) for r in refs], dtype=torch.float64, info=info, **kw)
+                                        pts3d_ref=[r.to(DEV) for r in refs], dtype=torch.float64, info=info,
+                                        optim_Z=optim_Z, **kw)
     inp = p.lm_inputs()
     hp = dict(weight_z=o['weight_z'], huber_delta=o['huber_delta'], pnorm=1.0, clip_pix_err=100)
-    sysd = oracle_system(inp, hp, {}, z_prior=(H_z, g_z), extra_loss=extra)
+    sysd = oracle_system(inp, hp, dict(optim_Z=optim_Z), z_prior=(H_z, g_z), extra_loss=extra)
     assert abs(float(st_g.init_loss) - float(sysd['loss'])) <= 1e-4 * abs(float(sysd['loss']))
     check_step_delta(sysd, info['delta'], info['pcg_istate'].cpu(), seed=9,
                      reduced=device_system(info['solver']))
