@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 from ._lib import PCG_BLOCK, PCG_LONG_LIST, BaLinArgs, BaPcgArgs, check, lib, ptr, stream_ptr
-from .plan import get_plan
+from .plan import MAX_LOCAL, get_plan
 
 N_FOC = 2   # focal columns (bs:11)
 N_TAU = 6   # pose columns (bs:12)
@@ -285,6 +285,11 @@ class GaussNewtonSolver:
             raise ValueError(f"path='batched' takes at most 15 reduced parameters per image (here {d}); "
                              "use path='pairmajor' or 'auto'")
         if self.path == 'pairmajor' or d > 15 or self.real32:
+            return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
+        L_img = int(self.plan_options.get('max_local_imgs', MAX_LOCAL))
+        if self.path == 'auto' and get_plan(J.rigs, J.pids, self.tracks.true_n, kind='span').median_span > 2 * L_img:
+            # tracks on far-apart images (random co-visibility): batches would hardly share image pairs, which
+            # the rule below finds only after building the batched plan (seconds at 20M observations)
             return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         try:
             plan = get_plan(J.rigs, J.pids, self.tracks.true_n, device=dev, **self.plan_options)

@@ -60,6 +60,7 @@ class _HostArrays:
 class BAPlan:
     """Device-resident plan for one (infos, pids) structure.  The host planner's state is kept (`_h`) so
     that the structure `old | new` can be planned from this one (BAPlan.appended), until that is done once."""
+    kind = 'batched'
 
     def __init__(self, infos, pids, n_tracks, device=None, max_local_imgs=MAX_LOCAL, max_slots=MAX_SLOTS,
                  max_batch_obs=0, _parent=None, _chain=None):
@@ -320,6 +321,28 @@ class PMPlan:
     workspace = BAPlan.workspace
 
 
+class SpanProfile:
+    """How far apart the images of one track lie, for the path choice of GaussNewtonSolver(path='auto'):
+    the median over the observed tracks of (last image - first image + 1).  The batched plan packs tracks
+    in (first image, last image) order into batches of at most MAX_LOCAL images, which holds many tracks
+    per batch only where tracks are windows of nearby images; where the median span is several batches
+    wide (tracks on random neighbours of a large collection), the batched plan is not built at all.
+    Computed on the device for device inputs (a scatter min / max per track); holds no arrays."""
+    kind = 'span'
+
+    def __init__(self, infos, pids, n_tracks):
+        dev = pids.device
+        cum = infos[0].to(device=dev, dtype=torch.int64)
+        counts = torch.diff(cum, prepend=cum.new_zeros(1))
+        img = torch.repeat_interleave(torch.arange(len(cum), device=dev), counts)
+        T = max(int(n_tracks), 1)
+        p = pids.to(torch.int64)
+        lo = torch.full((T,), len(cum), dtype=torch.int64, device=dev).scatter_reduce_(0, p, img, 'amin')
+        hi = torch.full((T,), -1, dtype=torch.int64, device=dev).scatter_reduce_(0, p, img, 'amax')
+        span = (hi - lo + 1)[hi >= 0]
+        self.median_span = int(span.median()) if span.numel() else 0
+
+
 # ---------------------------------------------------------------------- cache
 _cache_lock = threading.Lock()
 _cache = {}
@@ -435,7 +458,7 @@ def _appended_plan(infos, pids, n_tracks, key):
 
 
 def get_plan(infos, pids, n_tracks, kind='batched', **kw):
-    """Plan for this structure (kind 'batched': BAPlan, 'pairmajor': PMPlan): reused while the same
+    """Plan for this structure (kind 'batched': BAPlan, 'pairmajor': PMPlan, 'span': SpanProfile): reused while the same
     pids tensor (unmodified) and the same per-image counts / node / cam ids come back, rebuilt otherwise
     (a batched plan from its parent's, when note_append recorded the structure as `old | new` of a cached one).  The ids are compared by
     content unless the very infos tensor of the cached plan comes back unmodified (torch's version
@@ -458,9 +481,10 @@ def get_plan(infos, pids, n_tracks, kind='batched', **kw):
     if kind == 'batched':
         plan = _appended_plan(infos, pids, n_tracks, key)
     if plan is None:
-        plan = PMPlan(infos, pids, n_tracks, **kw) if kind == 'pairmajor' else BAPlan(infos, pids, n_tracks, **kw)
+        make = {'pairmajor': PMPlan, 'batched': BAPlan, 'span': SpanProfile}[kind]
+        plan = make(infos, pids, n_tracks, **kw)
     with _cache_lock:
-        if sum(len(v) for v in _cache.values()) > 8:
+        if sum(1 for v in _cache.values() for ent in v if not isinstance(ent[6], SpanProfile)) > 8:
             _cache.clear()
         _cache.setdefault(id(pids), []).append((weakref.ref(pids), pids._version, key, meta, weakref.ref(infos),
                                                 infos._version, plan))

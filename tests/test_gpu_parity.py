@@ -392,6 +392,19 @@ def _check_reduced_system(p, path):
     assert rel_err(H, Hr6) < 1e-5
 
 
+def test_auto_path_on_far_apart_track_images_builds_no_batched_plan():
+    """path='auto' where tracks lie on far-apart images (config 3's random neighbours in a 96-frame
+    collection, median span 77 images): the pair-major pass, decided from the structure's track spans
+    without building the batched plan, with the reduced system against the oracle."""
+    from blast3r_amd import plan as P
+    p = make_problem(3, n_frames=96, n_tracks=1200)
+    _check_reduced_system(p, 'auto')
+    gs, _, g = _gpu_solver(p, 'auto')
+    assert gs.last['path'] == 'pairmajor'
+    kinds = [ent[6].kind for ent in P._cache.get(id(g.pids), []) if ent[0]() is g.pids]
+    assert 'span' in kinds and 'pairmajor' in kinds and 'batched' not in kinds, kinds
+
+
 @pytest.mark.parametrize('cfg,nf,nt', [(0, 6, 60), (0, 12, 600), (1, 32, 400), (2, 24, 800), (3, 24, 600),
                                         (4, 12, 300)])
 def test_pcg_step_parity(cfg, nf, nt):

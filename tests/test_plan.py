@@ -386,6 +386,30 @@ def test_pm_plan_errors():
         PMPlan(inf, p.pids, p.n_tracks, device='cpu')
 
 
+@pytest.mark.parametrize('cfg,nf,nt,wide', [(2, 60, 800, False), (1, 64, 800, False), (3, 512, 3000, True)])
+def test_span_profile_median_track_span(cfg, nf, nt, wide):
+    """SpanProfile (the path choice of path='auto' before any batched plan is built): the lower median over
+    the observed tracks of last - first + 1 image, against a brute-force count; banded and retrieval
+    neighbourhoods stay within two batches (32 images), random neighbours of a 512-frame collection do not."""
+    from blast3r_amd.plan import SpanProfile, get_plan
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    cum = p.infos[0].numpy().astype(np.int64)
+    img = np.repeat(np.arange(len(cum)), np.diff(np.concatenate([[0], cum])))
+    pids = p.pids.numpy()
+    spans = []
+    for t in range(p.n_tracks):
+        im = img[pids == t]
+        if len(im):
+            spans.append(int(im.max() - im.min() + 1))
+    spans.sort()
+    expect = spans[(len(spans) - 1) // 2]
+    sp = SpanProfile(p.infos, p.pids, p.n_tracks)
+    assert sp.median_span == expect
+    assert (sp.median_span > 32) == wide
+    # cached per structure like the plans, and not counted against the plan cache's size
+    assert get_plan(p.infos, p.pids, p.n_tracks, kind='span') is get_plan(p.infos, p.pids, p.n_tracks, kind='span')
+
+
 @pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 6, 60, {}), (2, 30, 200, dict(track_len=(20, 30))),
                                           (4, 12, 150, dict(n_channels=16))])
 def test_pm_schur_emulation_matches_oracle(cfg, nf, nt, kw):
