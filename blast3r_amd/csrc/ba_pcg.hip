@@ -360,9 +360,20 @@ __global__ void __launch_bounds__(PCG_ST) k_pcg_spmv(ba_pcg_args a, int n, int n
         }
         dsum = wave_sum(dsum);
     }
+    // the row's further blocks: each block's unknown index is requested one block ahead, so that its z,
+    // p and values are requested together (the sum keeps the block order)
+    auto index_of = [&](int q) { return q < q1 ? a.row_u[(int64_t)q * GW + j] : -1; };
+    int un = index_of(q0 + PCG_ST / GW + grp);
     Real acc = mac(u, zv, pv, beta, bcol, Real(0));
-    for (int qb = q0 + PCG_ST / GW; qb < q1; qb += PCG_ST / GW) {     // the row's further blocks
-        load(qb + grp, u, zv, pv, bcol);
+    for (int qb = q0 + PCG_ST / GW; qb < q1; qb += PCG_ST / GW) {
+        const int q = qb + grp;
+        u = un;
+        zv = Real(0); pv = Real(0);
+        if (u >= 0) { zv = av.z[u]; pv = pold[u]; }
+        const Real* B = av.S_rows + (int64_t)q * dd;
+#pragma unroll
+        for (int j2 = 0; j2 < GW; ++j2) bcol[j2] = (q < q1 && j < d && j2 < d) ? B[j2 * d + j] : Real(0);
+        un = index_of(q + PCG_ST / GW);
         acc = mac(u, zv, pv, beta, bcol, acc);
     }
     __syncthreads();
