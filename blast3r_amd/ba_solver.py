@@ -750,7 +750,7 @@ class GaussNewtonSolver:
         plan = last['plan']
         T = self.tracks.true_n
         if last.get('path') == 'pairmajor':         # kept in track order
-            return last['Hpp'][:T].to(torch.float64), last['gp'][:T].to(torch.float64)
+            return last['Hpp'][:T].to(torch.float64, copy=True), last['gp'][:T].to(torch.float64, copy=True)
         n_ct = plan.scalars['n_ctracks']
         pid = plan.dev['ct_pid'][:n_ct].long()
         H = torch.zeros((T, 6), dtype=torch.float64, device=self.device)
