@@ -1092,6 +1092,11 @@ namespace ba {
 
 #define PM_T 256
 #define PM_SPAN BA_PM_SPAN  // observations (runs) per wave of k_pm_obs (k_pm_runs)
+// waves of k_pm_obs sharing one staging buffer: two in fp64 (the buffer, not the registers, limited
+// the CU to 1.5 waves per SIMD; measured at config 3: 17.33 -> 17.05 ms per pass), one in fp32 (the
+// registers already allow no more waves than buffers; two waves there cost 3.5% in their turns)
+template <typename Real> struct PmObsWaves { static constexpr int N = sizeof(Real) == 8 ? 2 : 1; };
+static_assert(PM_SPAN % 64 == 0, "a span is whole rounds of 64 observations");
 
 typedef ba_pm_args PmArgs;
 
@@ -1250,26 +1255,32 @@ struct PmTileAcc {
 
 // Per observation (one wave per PM_SPAN observations, 64 at a time): J_p^T J_p (upper 6) and
 // J_p^T W r (3) to pobs, sqrt(W) to wobs; the weighted camera rows, with sqrt(W) r in column d,
-// staged in LDS and summed per image (X^T X) into the J slots.
+// staged in LDS and summed per image (X^T X) into the J slots.  PmObsWaves waves share one staging
+// buffer and take turns with it: each wave linearises its observations of a round in registers (the
+// loads that bound this kernel), then stages and sums them in its turn, so the buffer (26 KB in fp64)
+// limits the CU to half as many buffers as waves.  Every wave sums its own rows in the same order as
+// alone.
 template <int HK, int HP, int DP, typename Real>
-__global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
+__global__ void __launch_bounds__(64 * PmObsWaves<Real>::N, 3) k_pm_obs(PmArgs a) {
+    constexpr int NW = PmObsWaves<Real>::N;
     __shared__ Real X[192][DP + 1];
     __shared__ int simg[64];
-    const int lane = threadIdx.x;
-    const int64_t w = blockIdx.x;
-    const int64_t o_begin = w * PM_SPAN, o_end = min(o_begin + PM_SPAN, a.n_obs);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t w = (int64_t)blockIdx.x * NW + wv;
+    const int64_t o_begin = w * PM_SPAN, o_end = min(o_begin + PM_SPAN, a.n_obs);   // empty past the end
     const int d = a.lay.d;
     PmTileAcc<DP, Real> T;
     T.img = -1;
     T.zero();
-    for (int64_t base = o_begin; base < o_end; base += 64) {
-        const int64_t o = base + lane;
+#pragma unroll 1
+    for (int rnd = 0; rnd < PM_SPAN / 64; ++rnd) {     // the same rounds in every wave (barriers below)
+        const int64_t o = o_begin + 64 * rnd + lane;
         int img = -1;
+        ObsCtx c;
+        ObsCore oc;
+        DepSrc dep;
         if (o < o_end) {
             img = a.obs_img[o];
-            ObsCtx c;
-            ObsCore oc;
-            DepSrc dep;
             bool xon;
             pm_ctx(a, img, c);
             pm_core(a, (int)o, c, oc, dep, xon);
@@ -1287,22 +1298,29 @@ __global__ void __launch_bounds__(64) k_pm_obs(PmArgs a) {
             __builtin_nontemporal_store((Real)gP[1], q + 7);
             __builtin_nontemporal_store((Real)gP[2], q + 8);
             typedef float f4 __attribute__((ext_vector_type(4)));
-            const f4 wv = {(float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f};
-            __builtin_nontemporal_store(wv, reinterpret_cast<f4*>(a.wobs) + o);
-            const bool first = o == 0;
-            emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane][j] = (Real)v; });
-            emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane + 1][j] = (Real)v; });
-            emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
-                                          [&](int j, double v) { X[3 * lane + 2][j] = (Real)v; });
-#pragma unroll
-            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = (Real)oc.Rs[k];
+            const f4 wv4 = {(float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f};
+            __builtin_nontemporal_store(wv4, reinterpret_cast<f4*>(a.wobs) + o);
         }
-        simg[lane] = img;
-        __syncthreads();
-        T.add_round(X, simg, Real(1), (Real*)a.jslots, w, lane);
-        __syncthreads();
+#pragma unroll 1
+        for (int turn = 0; turn < NW; ++turn) {
+            if (wv == turn) {
+                if (img >= 0) {
+                    const bool first = o == 0;
+                    emit_jc_row<HK, HP, 0, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * lane][j] = (Real)v; });
+                    emit_jc_row<HK, HP, 1, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * lane + 1][j] = (Real)v; });
+                    emit_jc_row<HK, HP, 2, 0, DP>(oc, a.lay, c.enK, c.enP, c.enZ, first, dep,
+                                                  [&](int j, double v) { X[3 * lane + 2][j] = (Real)v; });
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = (Real)oc.Rs[k];
+                }
+                simg[lane] = img;
+            }
+            __syncthreads();
+            if (wv == turn) T.add_round(X, simg, Real(1), (Real*)a.jslots, w, lane);
+            __syncthreads();
+        }
     }
     if (T.img >= 0) T.flush((Real*)a.jslots, w, lane);
 }
@@ -1642,10 +1660,12 @@ static void pm_stage(const ba_pm_args& a, int stage, hipStream_t st) {
     Real* const lam_p = (Real*)a.lam_p;
     hipLaunchKernelGGL(k_lam_clear<Real>, dim3(1), dim3(1), 0, st, tmax, nbt);
     if (a.n_obs > 0) {
-        const unsigned g = (unsigned)((a.n_obs + PM_SPAN - 1) / PM_SPAN);
+        const int64_t nw = (a.n_obs + PM_SPAN - 1) / PM_SPAN;          // waves (spans of PM_SPAN observations)
+        constexpr int NW = PmObsWaves<Real>::N;
+        const unsigned g = (unsigned)((nw + NW - 1) / NW);
         BA_DISPATCH_KP(a.lay, {
-            if (wide) hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 32, Real>), dim3(g), dim3(64), 0, st, a);
-            else      hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 16, Real>), dim3(g), dim3(64), 0, st, a);
+            if (wide) hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 32, Real>), dim3(g), dim3(64 * NW), 0, st, a);
+            else      hipLaunchKernelGGL((k_pm_obs<HK_, HP_, 16, Real>), dim3(g), dim3(64 * NW), 0, st, a);
         });
     }
     if (a.n_tracks > 0) {
