@@ -17,22 +17,52 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <numeric>
 #include <string>
 #include <thread>
 #include <vector>
 
+#include <sys/mman.h>
+
 #include "ba_plan.h"
 #include "ba_hip.h"
 
 namespace ba {
 
-// An allocator whose construct without a value leaves the element uninitialised, so that resize does
-// not first zero-fill the plan arrays that emit then writes element by element (about 420 MB at
-// 8 M observations: the zero fill and its page faults were a third of a full plan build).
+// Allocator of the planner's large arrays: blocks of 2 MB and more are 2 MB aligned and advised onto
+// transparent huge pages, since the page faults of first touch on fresh memory were a large share of a
+// plan build (hundreds of MB of plan and planning state at 8 M observations).
 template <class T>
-struct NoInitAlloc : std::allocator<T> {
+struct HugeAlloc : std::allocator<T> {
+    static constexpr size_t kHuge = (size_t)2 << 20;
+    template <class U> struct rebind { using other = HugeAlloc<U>; };
+    HugeAlloc() = default;
+    template <class U> HugeAlloc(const HugeAlloc<U>&) noexcept {}
+    T* allocate(size_t n) {
+        const size_t bytes = n * sizeof(T);
+        if (bytes < kHuge) return std::allocator<T>::allocate(n);
+        const size_t sz = (bytes + kHuge - 1) / kHuge * kHuge;
+        void* p = std::aligned_alloc(kHuge, sz);
+        if (!p) throw std::bad_alloc();
+        madvise(p, sz, MADV_HUGEPAGE);       // advice only: without huge pages the memory is the same
+        return static_cast<T*>(p);
+    }
+    void deallocate(T* p, size_t n) {
+        if (n * sizeof(T) < kHuge) std::allocator<T>::deallocate(p, n);
+        else std::free(p);
+    }
+};
+template <class T, class U> bool operator==(const HugeAlloc<T>&, const HugeAlloc<U>&) { return true; }
+template <class T, class U> bool operator!=(const HugeAlloc<T>&, const HugeAlloc<U>&) { return false; }
+template <class T> using HugeVec = std::vector<T, HugeAlloc<T>>;
+
+// The same, with a construct without a value that leaves the element uninitialised, so that resize does
+// not first zero-fill the plan arrays that emit then writes element by element (about 420 MB at
+// 8 M observations).
+template <class T>
+struct NoInitAlloc : HugeAlloc<T> {
     template <class U> struct rebind { using other = NoInitAlloc<U>; };
     NoInitAlloc() = default;
     template <class U> NoInitAlloc(const NoInitAlloc<U>&) noexcept {}
@@ -55,12 +85,12 @@ struct BatchDesc {
 // Observations are kept as (image, position in the image's block), which an append does not move.
 struct PlanState {
     std::vector<int64_t> base;                 // n_imgs + 1: first observation of each image, then n_obs
-    std::vector<int64_t> tptr;                 // n_tracks + 1
-    std::vector<int32_t> tob_img, tob_pos;     // each track's observations, in observation order
-    std::vector<int32_t> tmin, tmax, tdist;    // per track: first and last image, distinct images
-    std::vector<int32_t> order;                // observed tracks by (first image, last image, track id)
-    std::vector<int64_t> oimg_ptr;             // per position of `order`: its distinct images in oimg
-    std::vector<int32_t> oimg;
+    HugeVec<int64_t> tptr;                     // n_tracks + 1
+    HugeVec<int32_t> tob_img, tob_pos;         // each track's observations, in observation order
+    HugeVec<int32_t> tmin, tmax, tdist;        // per track: first and last image, distinct images
+    HugeVec<int32_t> order;                    // observed tracks by (first image, last image, track id)
+    HugeVec<int64_t> oimg_ptr;                 // per position of `order`: its distinct images in oimg
+    HugeVec<int32_t> oimg;
     std::vector<BatchDesc> batches;
     std::vector<int64_t> o_ch, o_ct, o_sl, o_en;   // per batch (and one past the last): first chunk,
                                                    // chunk track, slot and MFMA entry
@@ -161,69 +191,146 @@ static void order_images(PlanState& S, int64_t k_begin) {
     });
 }
 
-// Greedy batching from order position k_begin (with an empty batch there): tracks are taken in order and a
-// batch is closed when the next track would exceed L images, max_slots pairs or max_batch_obs observations,
-// so every batch is a contiguous range of `order`.  Appends to S.batches.
-static bool greedy(PlanState& S, int64_t k_begin, int n_imgs, int L, int max_slots, int64_t max_batch_obs) {
+// The batch that opens at order position k: tracks are taken in order until the next one would exceed
+// L images, max_slots pairs or max_batch_obs observations.  Returns the batch's end (> k) and fills
+// *out, or -1 when the track at k alone needs more pair slots than max_slots.  limg_of (n_imgs, all -1)
+// is returned all -1.
+static int64_t one_batch(const PlanState& S, int64_t k, int L, int max_slots, int64_t max_batch_obs,
+                         std::vector<int32_t>& limg_of, BatchDesc* out) {
     std::vector<int32_t> cur_imgs;
     std::vector<uint32_t> rows(L, 0);
-    std::vector<int32_t> limg_of(n_imgs, -1);
     int cur_nslots = 0, n_cur = 0;
-    int64_t k_open = k_begin, cur_obs = 0;
-    auto close = [&](int64_t k_end) {
-        if (n_cur == 0) return;
-        S.batches.push_back(BatchDesc{(int32_t)k_open, (int32_t)k_end, cur_imgs, rows});
-        for (int i : cur_imgs) limg_of[i] = -1;
-        cur_imgs.clear();
-        std::fill(rows.begin(), rows.end(), 0u);
-        cur_nslots = 0; cur_obs = 0; n_cur = 0; k_open = k_end;
-    };
+    int64_t cur_obs = 0, kk = k;
     const int64_t n = (int64_t)S.order.size();
-    for (int64_t kk = k_begin; kk < n; ++kk) {
+    for (; kk < n; ++kk) {
+        if (kk + 8 < n) __builtin_prefetch(&S.tptr[S.order[kk + 8]]);   // reached through the track id
         const int t = S.order[kk];
         const int32_t* timgs = S.oimg.data() + S.oimg_ptr[kk];
         const int nti = (int)(S.oimg_ptr[kk + 1] - S.oimg_ptr[kk]);
         const int m = (int)(S.tptr[t + 1] - S.tptr[t]);
-        for (int attempt = 0; attempt < 2; ++attempt) {
-            // local ids of the track's images (images not yet local get provisional ids)
-            const int n_loc = (int)cur_imgs.size();
-            int prov = n_loc;
-            uint32_t M = 0;
-            for (int q = 0; q < nti; ++q) {
-                const int l = limg_of[timgs[q]];
-                M |= 1u << (l >= 0 ? l : prov++);
-            }
-            bool ok = prov <= L && (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || n_cur == 0);
-            int add_slots = 0;
-            if (ok) {
-                // local pairs (x <= y) within M that no earlier track of the batch touched
-                for (uint32_t r = M; r; r &= r - 1) {
-                    const int x = __builtin_ctz(r);
-                    add_slots += __builtin_popcount(M & ~((1u << x) - 1u) & ~rows[x]);
-                }
-                ok = cur_nslots + add_slots <= max_slots;
-            }
-            if (!ok) {
-                if (n_cur == 0) {
-                    g_plan_err = "a single track needs more pair slots than max_slots";
-                    return false;
-                }
-                close(kk);
-                continue;
-            }
-            for (int q = 0; q < nti; ++q)
-                if (limg_of[timgs[q]] < 0) { limg_of[timgs[q]] = (int)cur_imgs.size(); cur_imgs.push_back(timgs[q]); }
+        // local ids of the track's images (images not yet local get provisional ids)
+        int prov = (int)cur_imgs.size();
+        uint32_t M = 0;
+        for (int q = 0; q < nti; ++q) {
+            const int l = limg_of[timgs[q]];
+            M |= 1u << (l >= 0 ? l : prov++);
+        }
+        bool ok = prov <= L && (max_batch_obs <= 0 || cur_obs + m <= max_batch_obs || n_cur == 0);
+        int add_slots = 0;
+        if (ok) {
+            // local pairs (x <= y) within M that no earlier track of the batch touched
             for (uint32_t r = M; r; r &= r - 1) {
                 const int x = __builtin_ctz(r);
-                rows[x] |= M & ~((1u << x) - 1u);
+                add_slots += __builtin_popcount(M & ~((1u << x) - 1u) & ~rows[x]);
             }
-            cur_nslots += add_slots;
-            cur_obs += m;
-            n_cur++;
-            break;
+            ok = cur_nslots + add_slots <= max_slots;
         }
+        if (!ok) break;
+        for (int q = 0; q < nti; ++q)
+            if (limg_of[timgs[q]] < 0) { limg_of[timgs[q]] = (int)cur_imgs.size(); cur_imgs.push_back(timgs[q]); }
+        for (uint32_t r = M; r; r &= r - 1) {
+            const int x = __builtin_ctz(r);
+            rows[x] |= M & ~((1u << x) - 1u);
+        }
+        cur_nslots += add_slots;
+        cur_obs += m;
+        n_cur++;
     }
-    close(n);
+    for (int i : cur_imgs) limg_of[i] = -1;
+    if (n_cur == 0) return -1;
+    *out = BatchDesc{(int32_t)k, (int32_t)kk, std::move(cur_imgs), std::move(rows)};
+    return kk;
+}
+
+// Greedy batching from order position k_begin (a batch opens there): each batch is the longest run of
+// tracks, in order, that fits the limits (one_batch), and the next one opens where it ends.  Appends to
+// S.batches.  A batch depends only on where it opens, so the order is cut into segments and, for each
+// segment, threads run the greedy as if a batch opened at its start, and again from a few positions
+// inside its first batch (a second run stops where it meets the first), until past the next segment's
+// start.  The exact chain is then followed from k_begin: wherever it reaches a position at which one of
+// its segment's runs opens a batch, it takes that run's batches from there on (they are the ones the
+// chain would compute); elsewhere it computes its batches itself.  The result does not depend on the
+// segmentation.  Several start positions matter where batches advance in a period: on config 2 each
+// batch takes the rest of one first image, the next image and part of the one after, so a run started
+// one image off the chain's phase never meets it.
+static bool greedy(PlanState& S, int64_t k_begin, int n_imgs, int L, int max_slots, int64_t max_batch_obs) {
+    struct Run {
+        std::vector<BatchDesc> b;       // b[j] opens at b[j].k0; the run stops at the end of the last one
+        bool fail = false;              // the run stopped at a track that alone exceeds max_slots (at its end)
+    };
+    constexpr int kRuns = 4;            // runs per segment
+    const int64_t n = (int64_t)S.order.size();
+    const int64_t span = n - k_begin;
+    unsigned hw = std::thread::hardware_concurrency();
+    const int64_t nth = std::max(1u, std::min(hw == 0 ? 1u : hw, 16u));
+    const int64_t nseg = std::max<int64_t>(1, std::min<int64_t>(nth, span / 32768));
+    std::vector<int64_t> seg(nseg + 1);
+    for (int64_t w = 0; w <= nseg; ++w) seg[w] = k_begin + span * w / nseg;
+    std::vector<Run> runs(nseg * kRuns);
+    // run r of segment w: r = 0 from the segment's start; r > 0 from r / kRuns of the way into run 0's
+    // first batch, until it opens a batch where run 0 does (from there on it is run 0)
+    auto one_run = [&](int64_t w, int r, std::vector<int32_t>& limg_of) {
+        Run& R = runs[w * kRuns + r];
+        const Run& R0 = runs[w * kRuns];
+        int64_t p = seg[w];
+        if (r > 0) {
+            if (R0.b.empty() || R0.fail) return;
+            p += (R0.b[0].k1 - R0.b[0].k0) * r / kRuns;
+            if (p == seg[w]) return;
+        }
+        size_t j0 = 0;                                      // run 0's batches opening before p
+        while (p < seg[w + 1]) {                            // seg[nseg] = n
+            if (r > 0) {
+                while (j0 < R0.b.size() && R0.b[j0].k0 < p) ++j0;
+                if (j0 < R0.b.size() && R0.b[j0].k0 == p) return;   // met run 0
+            }
+            BatchDesc bd;
+            const int64_t e = one_batch(S, p, L, max_slots, max_batch_obs, limg_of, &bd);
+            if (e < 0) { R.fail = true; R.b.push_back(BatchDesc{(int32_t)p, (int32_t)p, {}, {}}); return; }
+            R.b.push_back(std::move(bd));
+            p = e;
+        }
+    };
+    if (nseg > 1) {
+        std::vector<std::thread> pool;
+        auto seg_runs = [&](int64_t w) {
+            std::vector<int32_t> limg_of(n_imgs, -1);
+            for (int r = 0; r < kRuns; ++r) one_run(w, r, limg_of);
+        };
+        for (int64_t w = 1; w < nseg; ++w) pool.emplace_back(seg_runs, w);
+        seg_runs(0);
+        for (auto& th : pool) th.join();
+    }
+    std::vector<int32_t> limg_of(n_imgs, -1);
+    int64_t p = k_begin;
+    int64_t w = 0;
+    while (p < n) {
+        while (w + 1 < nseg && seg[w + 1] <= p) ++w;
+        // does one of segment w's runs open a batch at p?
+        bool taken = false;
+        for (int r = 0; r < kRuns && nseg > 1 && !taken; ++r) {
+            std::vector<BatchDesc>& rb = runs[w * kRuns + r].b;
+            auto it = std::lower_bound(rb.begin(), rb.end(), p, [](const BatchDesc& x, int64_t v) { return x.k0 < v; });
+            if (it == rb.end() || it->k0 != p) continue;
+            const bool fail = runs[w * kRuns + r].fail;
+            const auto stop = fail ? rb.end() - 1 : rb.end();
+            for (auto jt = it; jt != stop; ++jt) { p = jt->k1; S.batches.push_back(std::move(*jt)); }
+            if (fail) {                // the chain has reached the track the run stopped at
+                g_plan_err = "a single track needs more pair slots than max_slots";
+                return false;
+            }
+            taken = true;
+        }
+        if (taken) continue;
+        BatchDesc bd;
+        const int64_t e = one_batch(S, p, L, max_slots, max_batch_obs, limg_of, &bd);
+        if (e < 0) {
+            g_plan_err = "a single track needs more pair slots than max_slots";
+            return false;
+        }
+        S.batches.push_back(std::move(bd));
+        p = e;
+    }
     return true;
 }
 
@@ -236,7 +343,6 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
         for (int a = 0; a <= b; ++a)
             if ((bd.rows[a] >> b) & 1u) R.slot_pair.push_back(a | (b << 8));
     const int nsl = (int)R.slot_pair.size();
-    std::vector<int16_t> lead;
     int k = bd.k0;
     while (k < bd.k1) {                                   // chunks: tracks packed whole, in order
         int used = 0, ntr = 0;
@@ -246,7 +352,16 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
         R.s_pid.resize(base + BA_CHUNK, 0);
         R.s_img.resize(base + BA_CHUNK, 0);
         const int first_ct = (int)R.ct_pid.size();
+        int16_t lead[BA_MAX_CT][BA_MAX_LOCAL];            // per chunk track and local image: its run's first slot
+        uint64_t img_trk[BA_MAX_LOCAL] = {0};             // per local image: the chunk tracks seen in it
         while (k < bd.k1) {
+            // the track lists are reached through the track id: request them a few tracks ahead
+            if (k + 8 < bd.k1) __builtin_prefetch(&S.tptr[S.order[k + 8]]);
+            if (k + 4 < bd.k1) {
+                const int64_t q = S.tptr[S.order[k + 4]];
+                __builtin_prefetch(&S.tob_img[q]);
+                __builtin_prefetch(&S.tob_pos[q]);
+            }
             const int t = S.order[k];
             const int m = (int)(S.tptr[t + 1] - S.tptr[t]);
             if (used + m > BA_CHUNK || ntr == BA_MAX_CT) break;
@@ -255,13 +370,18 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
             for (int j = 0; j < m; ++j) {
                 const int i = S.tob_img[S.tptr[t] + j];
                 const int lim = limg_of[i];
-                if (i != last_img) { leader = used + j; last_img = i; }
+                if (i != last_img) {
+                    leader = used + j;
+                    last_img = i;
+                    lead[ntr][lim] = (int16_t)leader;
+                }
                 mask |= 1u << lim;
                 R.chunk_obs[base + used + j] = (int32_t)(S.base[i] + S.tob_pos[S.tptr[t] + j]);
                 R.slot_info[base + used + j] = lim | (ntr << 8) | (leader << 16);
                 R.s_pid[base + used + j] = t;
                 R.s_img[base + used + j] = i;
             }
+            for (uint32_t r = mask; r; r &= r - 1) img_trk[__builtin_ctz(r)] |= (uint64_t)1 << ntr;
             R.ct_pid.push_back(t);
             R.ct_first.push_back(used);
             R.ct_m.push_back(m);
@@ -280,10 +400,14 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
         // a diagonal slot (a, a) lists the J rows of every observation in a (slot order, padded
         // to whole groups), then the V rows of the first observation of each (track, image) run
         // in a (slot order)
-        lead.assign((size_t)ntr * BA_MAX_LOCAL, -1);
-        for (int sidx = 0; sidx < used; ++sidx) {
-            const int inf = R.slot_info[base + sidx];
-            lead[(size_t)((inf >> 8) & 0xff) * BA_MAX_LOCAL + (inf & 0xff)] = (int16_t)(inf >> 16);
+        int16_t by_img[BA_CHUNK];                          // the chunk's slots grouped by local image
+        int img_ptr[BA_MAX_LOCAL + 1] = {0};
+        for (int sidx = 0; sidx < used; ++sidx) img_ptr[(R.slot_info[base + sidx] & 0xff) + 1]++;
+        for (int a = 0; a < BA_MAX_LOCAL; ++a) img_ptr[a + 1] += img_ptr[a];
+        {
+            int fill[BA_MAX_LOCAL];
+            std::copy(img_ptr, img_ptr + BA_MAX_LOCAL, fill);
+            for (int sidx = 0; sidx < used; ++sidx) by_img[fill[R.slot_info[base + sidx] & 0xff]++] = (int16_t)sidx;
         }
         const size_t e0 = R.ents.size();
         R.chunk_eptr.push_back((int32_t)(e0 / 4));
@@ -295,18 +419,17 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
             const size_t off = R.ents.size() - e0;
             int njg = 0;
             if (a != bq) {
-                for (int tt = 0; tt < ntr; ++tt) {
-                    const int la_ = lead[(size_t)tt * BA_MAX_LOCAL + a], lb_ = lead[(size_t)tt * BA_MAX_LOCAL + bq];
-                    if (la_ >= 0 && lb_ >= 0) ent(la_ * BA_BLK, lb_ * BA_BLK);
+                for (uint64_t r = img_trk[a] & img_trk[bq]; r; r &= r - 1) {
+                    const int tt = __builtin_ctzll(r);
+                    ent(lead[tt][a] * BA_BLK, lead[tt][bq] * BA_BLK);
                 }
             } else {
-                for (int sidx = 0; sidx < used; ++sidx)
-                    if ((R.slot_info[base + sidx] & 0xff) == a) ent(sidx * BA_BLK + BA_JROW, sidx * BA_BLK + BA_JROW);
+                for (int x = img_ptr[a]; x < img_ptr[a + 1]; ++x) ent(by_img[x] * BA_BLK + BA_JROW, by_img[x] * BA_BLK + BA_JROW);
                 pad(e0 + off);
                 njg = (int)((R.ents.size() - e0 - off) / 4);
-                for (int sidx = 0; sidx < used; ++sidx) {
-                    const int inf = R.slot_info[base + sidx];
-                    if ((inf & 0xff) == a && (inf >> 16) == sidx) ent(sidx * BA_BLK, sidx * BA_BLK);
+                for (int x = img_ptr[a]; x < img_ptr[a + 1]; ++x) {
+                    const int sidx = by_img[x];
+                    if ((R.slot_info[base + sidx] >> 16) == sidx) ent(sidx * BA_BLK, sidx * BA_BLK);
                 }
             }
             pad(e0 + off);
@@ -319,16 +442,27 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
     // place the batch's slots on the Schur kernel's waves (place wave + BA_WAVES * k, at most
     // BA_SLOTS_PER_WAVE per wave).  The MFMA phase of a chunk lasts as long as its busiest SIMD
     // (BA_WAVES / 4 waves share one MFMA pipe) and its busiest wave, so slots are taken by
-    // decreasing total work and each goes where the summed per-chunk maxima grow least.
+    // decreasing total work and each goes where the summed per-chunk maxima grow least.  A chunk in
+    // which the slot has no entries adds the same to every wave's cost (each maximum stays), so only
+    // the chunks where it has entries are summed.
     {
         const int nc = (int)(R.chunk_meta.size() / 4);
-        std::vector<int32_t> wk((size_t)nc * nsl);                  // MFMAs of (chunk, slot)
+        std::vector<int32_t> sptr(nsl + 1, 0), sc, sx;   // per slot: its chunks with entries, and their MFMAs
         std::vector<int64_t> tot(nsl, 0);
         for (int c = 0; c < nc; ++c)
-            for (int q = 0; q < nsl; ++q) {
-                wk[(size_t)c * nsl + q] = 3 * BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]);
-                tot[q] += wk[(size_t)c * nsl + q];
-            }
+            for (int q = 0; q < nsl; ++q)
+                if (BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]) > 0) sptr[q + 1]++;
+        for (int q = 0; q < nsl; ++q) sptr[q + 1] += sptr[q];
+        sc.resize(sptr[nsl]);
+        sx.resize(sptr[nsl]);
+        {
+            std::vector<int32_t> fill(sptr.begin(), sptr.end() - 1);
+            for (int c = 0; c < nc; ++c)
+                for (int q = 0; q < nsl; ++q) {
+                    const int x = 3 * BA_TAB_NG(R.chunk_slots[(size_t)c * BA_MAX_SLOTS + q]);
+                    if (x > 0) { sc[fill[q]] = c; sx[fill[q]++] = x; tot[q] += x; }
+                }
+        }
         std::vector<int> sorder(nsl);
         std::iota(sorder.begin(), sorder.end(), 0);
         std::stable_sort(sorder.begin(), sorder.end(), [&](int x, int y) { return tot[x] > tot[y]; });
@@ -337,25 +471,33 @@ static void build_batch(const PlanState& S, int batch, std::vector<int32_t>& lim
         int cnt[BA_WAVES] = {0};
         R.pos_slot.assign(BA_MAX_SLOTS, -1);
         for (int q : sorder) {
+            int64_t simd_cost[NS];
+            for (int sd = 0; sd < NS; ++sd) {
+                int64_t cost = 0;
+                for (int e = sptr[q]; e < sptr[q + 1]; ++e) {
+                    const int c = sc[e];
+                    cost += NS * std::max(ls[(size_t)c * NS + sd] + sx[e], ms[c]);
+                }
+                simd_cost[sd] = cost;
+            }
             int best = -1;
             int64_t best_cost = 0;
             for (int w = 0; w < BA_WAVES; ++w) {
                 if (cnt[w] >= BA_SLOTS_PER_WAVE) continue;
-                const int sd = w % NS;
-                int64_t cost = 0;
-                for (int c = 0; c < nc; ++c) {
-                    const int64_t x = wk[(size_t)c * nsl + q];
-                    cost += NS * std::max(ls[(size_t)c * NS + sd] + x, ms[c]) + std::max(lw[(size_t)c * BA_WAVES + w] + x, mw[c]);
+                int64_t cost = simd_cost[w % NS];
+                for (int e = sptr[q]; e < sptr[q + 1]; ++e) {
+                    const int c = sc[e];
+                    cost += std::max(lw[(size_t)c * BA_WAVES + w] + sx[e], mw[c]);
                 }
                 if (best < 0 || cost < best_cost) { best = w; best_cost = cost; }
             }
             R.pos_slot[best + BA_WAVES * cnt[best]] = q;
             cnt[best]++;
             const int sd = best % NS;
-            for (int c = 0; c < nc; ++c) {
-                const int64_t x = wk[(size_t)c * nsl + q];
-                ls[(size_t)c * NS + sd] += x;
-                lw[(size_t)c * BA_WAVES + best] += x;
+            for (int e = sptr[q]; e < sptr[q + 1]; ++e) {
+                const int c = sc[e];
+                ls[(size_t)c * NS + sd] += sx[e];
+                lw[(size_t)c * BA_WAVES + best] += sx[e];
                 ms[c] = std::max(ms[c], ls[(size_t)c * NS + sd]);
                 mw[c] = std::max(mw[c], lw[(size_t)c * BA_WAVES + best]);
             }
@@ -629,42 +771,75 @@ extern "C" void* ba_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, const 
     S.base[0] = 0;
     for (int i = 0; i < n_imgs; ++i) S.base[i + 1] = cum_nkpts[i];
 
-    // observation -> image, and per-track observation lists in observation (= image) order
-    std::vector<int32_t> img(n_obs);
-    parallel_for(n_imgs, [&](int64_t i0, int64_t i1) {
-        for (int64_t i = i0; i < i1; ++i)
-            for (int64_t o = S.base[i]; o < S.base[i + 1]; ++o) img[o] = (int32_t)i;
-    }, 1);
-    std::vector<int32_t> tcnt(n_tracks, 0);
-    std::atomic<bool> bad_pid(false);
-    parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
-        for (int64_t o = o0; o < o1; ++o) {
-            const int32_t t = pids[o];
-            if (t < 0 || t >= n_tracks) { bad_pid = true; continue; }
-            __atomic_fetch_add(&tcnt[t], 1, __ATOMIC_RELAXED);
-        }
-    });
-    if (bad_pid) { g_plan_err = "pid out of range"; delete P; return nullptr; }
-    S.tptr.assign(n_tracks + 1, 0);
-    for (int t = 0; t < n_tracks; ++t) S.tptr[t + 1] = S.tptr[t] + tcnt[t];
+    // Per-track observation lists in observation (= image) order: a counting sort over contiguous
+    // observation ranges, one per thread.  Each thread counts its range's observations per track (one
+    // byte per track: a track holds at most BA_CHUNK observations), the counts become per-thread
+    // offsets inside each track's list, and each thread then writes its range in order, so every list
+    // comes out in observation order without atomics or a sort.
     {
-        std::vector<int32_t> tobs(n_obs);
-        std::vector<int64_t> fill(S.tptr.begin(), S.tptr.end() - 1);
-        parallel_for(n_obs, [&](int64_t o0, int64_t o1) {
-            for (int64_t o = o0; o < o1; ++o) tobs[__atomic_fetch_add(&fill[pids[o]], 1, __ATOMIC_RELAXED)] = (int32_t)o;
+        unsigned hw = std::thread::hardware_concurrency();
+        int64_t nth = std::max(1u, std::min(hw == 0 ? 1u : hw, 16u));
+        nth = std::max<int64_t>(1, std::min<int64_t>(nth, n_obs / 65536));
+        nth = std::max<int64_t>(1, std::min<int64_t>(nth, ((int64_t)256 << 20) / std::max(1, n_tracks)));
+        const int64_t step = (n_obs + nth - 1) / nth;
+        std::vector<std::vector<uint8_t>> cnt((size_t)nth);
+        std::atomic<bool> bad_pid(false), too_long(false);
+        auto over_ranges = [&](auto fn) {
+            std::vector<std::thread> pool;
+            for (int64_t w = 1; w < nth; ++w) pool.emplace_back(fn, w, std::min(n_obs, w * step), std::min(n_obs, (w + 1) * step));
+            fn((int64_t)0, (int64_t)0, std::min(n_obs, step));
+            for (auto& th : pool) th.join();
+        };
+        over_ranges([&](int64_t w, int64_t o0, int64_t o1) {
+            std::vector<uint8_t>& c = cnt[w];
+            c.assign(n_tracks, 0);
+            bool bad = false, lng = false;
+            for (int64_t o = o0; o < o1; ++o) {
+                const int32_t t = pids[o];
+                if (t < 0 || t >= n_tracks) { bad = true; continue; }
+                if (c[t] == 255) lng = true; else c[t]++;
+            }
+            if (bad) bad_pid = true;
+            if (lng) too_long = true;
         });
+        if (bad_pid) { g_plan_err = "pid out of range"; delete P; return nullptr; }
+        // per track: the threads' counts -> their first positions in the list (exclusive prefix)
+        S.tptr.assign(n_tracks + 1, 0);
+        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {
+            bool lng = false;
+            for (int64_t t = t0; t < t1; ++t) {
+                int run = 0;
+                for (int64_t w = 0; w < nth; ++w) {
+                    const int x = cnt[w][t];
+                    cnt[w][t] = (uint8_t)run;
+                    run += x;
+                }
+                if (run > BA_CHUNK) lng = true;
+                S.tptr[t + 1] = run;
+            }
+            if (lng) too_long = true;
+        });
+        if (too_long) {       // the first check tracks_ok makes, before any list is needed
+            g_plan_err = "a track has more observations than one chunk holds (" + std::to_string(BA_CHUNK) + ")";
+            delete P;
+            return nullptr;
+        }
+        for (int t = 0; t < n_tracks; ++t) S.tptr[t + 1] += S.tptr[t];
         S.tob_img.reserve((size_t)(n_obs + n_obs / 8 + 4096));
         S.tob_pos.reserve((size_t)(n_obs + n_obs / 8 + 4096));
         S.tob_img.resize(n_obs);
         S.tob_pos.resize(n_obs);
-        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {        // each list back in observation order
-            for (int64_t t = t0; t < t1; ++t) {
-                std::sort(tobs.begin() + S.tptr[t], tobs.begin() + S.tptr[t + 1]);
-                for (int64_t k = S.tptr[t]; k < S.tptr[t + 1]; ++k) {
-                    const int32_t o = tobs[k], i = img[o];
-                    S.tob_img[k] = i;
-                    S.tob_pos[k] = (int32_t)(o - S.base[i]);
-                }
+        over_ranges([&](int64_t w, int64_t o0, int64_t o1) {
+            if (o0 >= o1) return;
+            std::vector<uint8_t>& c = cnt[w];
+            // image of the range's first observation: the last image whose block starts at or before it
+            int i = (int)(std::upper_bound(S.base.begin(), S.base.end() - 1, o0) - S.base.begin()) - 1;
+            for (int64_t o = o0; o < o1; ++o) {
+                while (o >= S.base[i + 1]) ++i;
+                const int32_t t = pids[o];
+                const int64_t k = S.tptr[t] + c[t]++;
+                S.tob_img[k] = i;
+                S.tob_pos[k] = (int32_t)(o - S.base[i]);
             }
         });
     }

@@ -188,6 +188,75 @@ def test_plan_errors():
         BAPlan(p.infos, bad, p.n_tracks, device='cpu')
 
 
+def _batch_tracks(pl):
+    """Per batch, its tracks in plan order (the chunks of a batch pack a contiguous run of the track order)."""
+    h = pl.host
+    meta = h['chunk_meta'].reshape(-1, 4)
+    bcp = h['b_chunk_ptr']
+    out = []
+    for b in range(pl.scalars['n_batches']):
+        c0, c1 = bcp[b], bcp[b + 1]
+        out.append(h['ct_pid'][meta[c0, 1]:meta[c1 - 1, 1] + meta[c1 - 1, 2]])
+    return out
+
+
+@pytest.mark.parametrize('cfg,nf,nt,kw', [(2, 150, 120000, {}), (1, 120, 100000, {}),
+                                          (2, 150, 120000, dict(max_batch_obs=3000)),
+                                          (2, 150, 120000, dict(max_local_imgs=13, max_slots=80))])
+def test_plan_batches_follow_the_greedy_rule(cfg, nf, nt, kw):
+    """Each batch is the longest run of the track order, from where the previous one ended, within the
+    limits (images, pair slots, observations): checked against the rule itself, at sizes where the planner
+    cuts the order into segments planned in parallel and then joins them."""
+    p = make_problem(cfg, n_frames=nf, n_tracks=nt)
+    pl = _plan(p, **kw)
+    L, max_slots, mbo = kw.get('max_local_imgs', 16), kw.get('max_slots', 96), kw.get('max_batch_obs', 0)
+    pids = p.pids.numpy()
+    img = pl.obs_img
+    srt = np.lexsort((img, pids))
+    bounds = np.searchsorted(pids[srt], np.arange(p.n_tracks + 1))
+    timgs = [np.unique(img[srt[bounds[t]:bounds[t + 1]]]) for t in range(p.n_tracks)]
+    m = np.diff(bounds)
+    batches = _batch_tracks(pl)
+    assert sum(len(b) for b in batches) == int((m > 0).sum())
+    assert pl.scalars['n_batches'] > 40
+    for b, tr in enumerate(batches):
+        imgs, pairs, nobs = set(), set(), 0
+        for t in tr:
+            imgs.update(timgs[t].tolist())
+            ti = timgs[t]
+            pairs.update(zip(*[a.ravel().tolist() for a in np.meshgrid(ti, ti)]))
+            nobs += m[t]
+        pairs = {(x, y) for x, y in pairs if x <= y}
+        assert len(imgs) <= L and len(pairs) <= max_slots and (mbo <= 0 or nobs <= mbo or len(tr) == 1)
+        if b + 1 < len(batches):            # the next track would break a limit
+            t = batches[b + 1][0]
+            ti = timgs[t]
+            imgs2 = imgs | set(ti.tolist())
+            pairs2 = pairs | {(x, y) for x in ti.tolist() for y in ti.tolist() if x <= y}
+            assert len(imgs2) > L or len(pairs2) > max_slots or (mbo > 0 and nobs + m[t] > mbo)
+
+
+def test_plan_errors_at_size():
+    """The limits' errors at a size where the greedy runs in segments: a track whose pairs exceed
+    max_slots (every segment meets one), and a track longer than a chunk."""
+    p = make_problem(2, n_frames=150, n_tracks=120000)
+    with pytest.raises(RuntimeError, match='a single track needs more pair slots than max_slots'):
+        BAPlan(p.infos, p.pids, p.n_tracks, device='cpu', max_slots=60)
+    pids = p.pids.clone()
+    cnt = torch.diff(torch.cat([torch.zeros(1, dtype=torch.long), p.infos[0].long()]))
+    # one track observed 4 times in each of the first 40 images: 160 observations
+    long_track = torch.arange(40).repeat_interleave(4)
+    keep_img = torch.repeat_interleave(torch.arange(len(cnt)), cnt)
+    new_pids = torch.cat([torch.full((160,), p.n_tracks, dtype=pids.dtype), pids])
+    new_img = torch.cat([long_track, keep_img])
+    o = torch.argsort(new_img, stable=True)
+    cnt2 = torch.bincount(new_img, minlength=len(cnt))
+    infos = p.infos.clone()
+    infos[0] = torch.cumsum(cnt2, 0).to(infos.dtype)
+    with pytest.raises(RuntimeError, match='more observations than one chunk holds'):
+        BAPlan(infos, new_pids[o].contiguous(), p.n_tracks + 1, device='cpu')
+
+
 def _chol3(H, lam, jit=1e-12):
     """chol3x3 rules (.cu:560-634) on a (T,3,3) batch, returns lower factors."""
     A = H + (lam + jit) * torch.eye(3, dtype=H.dtype)
