@@ -78,7 +78,7 @@ class BaPmArgs(ctypes.Structure):
                 ('run_ptr', c_p), ('run_obs', c_p), ('run_trk', c_p), ('run_img', c_p), ('img_run_ptr', c_p),
                 ('trk_run_ptr', c_p), ('trk_run', c_p), ('trk_obs_ptr', c_p), ('trk_obs', c_p), ('obs_img', c_p),
                 ('pair_i1', c_p), ('pair_i2', c_p), ('diag_pair', c_p), ('term_ptr', c_p), ('term', c_p),
-                ('n_obs', c_i64), ('n_runs', c_i64), ('n_pairs', c_i64),
+                ('pair_sched', c_p), ('n_obs', c_i64), ('n_runs', c_i64), ('n_pairs', c_i64),
                 ('pids', c_p), ('pix2d', c_p), ('pix2d_std', c_p), ('pix2d_dep', c_p),
                 ('K', c_p), ('P_rig2cam', c_p), ('P_rig2cam_stride', c_i64), ('P_w2rig', c_p), ('z_coefs', c_p),
                 ('pts3d', c_p), ('enK', c_p), ('enP', c_p), ('enZ', c_p), ('enX', c_p),

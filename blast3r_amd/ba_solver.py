@@ -414,7 +414,8 @@ class GaussNewtonSolver:
         a.infos = ptr(J.rigs.contiguous())
         a.n_imgs, a.n_tracks = n_imgs, T
         for name in ('run_ptr', 'run_obs', 'run_trk', 'run_img', 'img_run_ptr', 'trk_run_ptr', 'trk_run',
-                     'trk_obs_ptr', 'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'diag_pair', 'term_ptr', 'term'):
+                     'trk_obs_ptr', 'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'diag_pair', 'term_ptr', 'term',
+                     'pair_sched'):
             setattr(a, name, ptr(pd[name]))
         a.n_obs, a.n_runs, a.n_pairs = n_obs, sc['n_runs'], sc['n_pairs']
         pix = J.pix2d if J.pix2d is not None else J.pix2d_std

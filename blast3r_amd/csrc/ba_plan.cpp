@@ -1278,6 +1278,48 @@ extern "C" void* ba_pm_plan_create(const int32_t* cum_nkpts, int32_t n_imgs, con
     }, 1);
     int64_t max_terms = 0;
     for (int64_t p = 0; p < n_pairs; ++p) max_terms = std::max<int64_t>(max_terms, tcnt[p + 1] - tcnt[p]);
+    // the order k_pm_pairs takes the pairs in: by the co-visibility window of each pair's terms (the smallest
+    // first image and the largest last image of their tracks), then pair id; pairs without terms last.
+    // Pairs whose terms come from tracks of one neighbourhood then run close together and share their V
+    // rows in the L2 (random co-visibility, config 3: 9.0 -> 7.4 ms against the (i1, i2) order).
+    {
+        std::vector<int32_t> tlo(n_tracks, 0), thi(n_tracks, 0), klo(n_pairs), khi(n_pairs);
+        parallel_for(n_tracks, [&](int64_t t0, int64_t t1) {
+            for (int64_t t = t0; t < t1; ++t)
+                if (trk_run_ptr[t + 1] > trk_run_ptr[t]) {
+                    tlo[t] = run_img[trk_run[trk_run_ptr[t]]];
+                    thi[t] = run_img[trk_run[trk_run_ptr[t + 1] - 1]];
+                }
+        });
+        parallel_for(n_pairs, [&](int64_t p0, int64_t p1) {
+            for (int64_t p = p0; p < p1; ++p) {
+                int32_t lo = n_imgs, hi = n_imgs;
+                if (tcnt[p + 1] > tcnt[p]) { lo = INT32_MAX; hi = -1; }
+                for (int64_t q = tcnt[p]; q < tcnt[p + 1]; ++q) {
+                    const int t = run_trk[term[2 * q]];
+                    lo = std::min(lo, tlo[t]);
+                    hi = std::max(hi, thi[t]);
+                }
+                klo[p] = lo; khi[p] = hi;
+            }
+        });
+        // two stable counting sorts over the keys 0 .. n_imgs: by the last image, then by the first
+        std::vector<int32_t> tmp(n_pairs);
+        std::vector<int64_t> cnt(n_imgs + 2);
+        auto by = [&](const std::vector<int32_t>& key, const int32_t* in, int32_t* out) {
+            std::fill(cnt.begin(), cnt.end(), 0);
+            for (int64_t q = 0; q < n_pairs; ++q) cnt[key[in ? in[q] : q] + 1]++;
+            for (int i = 0; i <= n_imgs; ++i) cnt[i + 1] += cnt[i];
+            for (int64_t q = 0; q < n_pairs; ++q) {
+                const int32_t p = in ? in[q] : (int32_t)q;
+                out[cnt[key[p]]++] = p;
+            }
+        };
+        auto& pair_sched = P->v[BA_PM_PAIR_SCHED];
+        pair_sched.assign(n_pairs, 0);
+        by(khi, nullptr, tmp.data());
+        by(klo, tmp.data(), pair_sched.data());
+    }
     // image rows of the symmetric pair structure, as in the batched plan
     auto& row_ptr = P->v[BA_PM_ROW_PTR];
     auto& row_ent = P->v[BA_PM_ROW_ENT];

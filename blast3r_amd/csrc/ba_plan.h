@@ -100,6 +100,9 @@ enum {
     BA_PM_DIAG_PAIR,        // (n_imgs): pair id of (i, i), or -1
     BA_PM_TERM_PTR,         // (n_pairs + 1): terms of off-diagonal pair p (none for a diagonal pair)
     BA_PM_TERM,             // (2 n_terms): (run in i1, run in i2) of one track, per term
+    BA_PM_PAIR_SCHED,       // (n_pairs): the order in which k_pm_pairs takes the pairs: by the smallest first
+                            //   image and the largest last image of their terms' tracks, then pair id; pairs
+                            //   without terms last
     BA_PM_NARRAYS
 };
 #define BA_PM_SPAN 512        // observations (runs) per wave of the pair-major per-image sums

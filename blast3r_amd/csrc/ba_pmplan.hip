@@ -242,6 +242,44 @@ __global__ void __launch_bounds__(PT) k_row_items(const int32_t* __restrict__ pa
     }
 }
 
+// per track: the images of its first and last run (0 for a track without runs, which no term names)
+__global__ void __launch_bounds__(PT) k_track_span(const int32_t* __restrict__ trk_run_ptr,
+                                                   const int32_t* __restrict__ trk_run, const int32_t* __restrict__ run_img,
+                                                   int64_t T, int32_t* __restrict__ tlo, int32_t* __restrict__ thi) {
+    const int64_t t = (int64_t)blockIdx.x * PT + threadIdx.x;
+    if (t >= T) return;
+    const int32_t r0 = trk_run_ptr[t], r1 = trk_run_ptr[t + 1];
+    tlo[t] = r1 > r0 ? run_img[trk_run[r0]] : 0;
+    thi[t] = r1 > r0 ? run_img[trk_run[r1 - 1]] : 0;
+}
+
+// per pair (one wave each): the sort key of the pair schedule, lo * (F + 1) + hi with lo / hi the smallest
+// first / largest last image of its terms' tracks (F, F without terms), and the pair id as its value
+__global__ void __launch_bounds__(PT) k_pair_keys(const int32_t* __restrict__ term_ptr, const int32_t* __restrict__ term,
+                                                  const int32_t* __restrict__ run_trk, const int32_t* __restrict__ tlo,
+                                                  const int32_t* __restrict__ thi, int64_t NP, int32_t F,
+                                                  uint64_t* __restrict__ key, int32_t* __restrict__ val) {
+    const int64_t p = (int64_t)blockIdx.x * (PT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (p >= NP) return;                                // p is the same for the whole wave
+    const int32_t q0 = term_ptr[p], q1 = term_ptr[p + 1];
+    int32_t lo = INT32_MAX, hi = -1;
+    for (int32_t q = q0 + lane; q < q1; q += 64) {
+        const int32_t t = run_trk[term[2 * (int64_t)q]];
+        lo = min(lo, tlo[t]);
+        hi = max(hi, thi[t]);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        lo = min(lo, __shfl_xor(lo, off));
+        hi = max(hi, __shfl_xor(hi, off));
+    }
+    if (lane == 0) {
+        if (q1 == q0) { lo = F; hi = F; }
+        key[p] = (uint64_t)lo * (uint64_t)(F + 1) + (uint64_t)hi;
+        val[p] = (int32_t)p;
+    }
+}
+
 // ---------------------------------------------------------------------------- the plan object
 struct DevPmPlan {
     int32_t* v[BA_PM_NARRAYS] = {nullptr};
@@ -473,6 +511,26 @@ extern "C" void* ba_pm_dplan_create(const int32_t* cum, int32_t F, const int32_t
         PM_TRY(hipStreamSynchronize(st));
     }
     if (M > 0) hipLaunchKernelGGL(k_term_out, dim3(grid_of(M)), dim3(PT), 0, st, tk2, tv2, M, rbits, term);
+    // ---- the order k_pm_pairs takes the pairs in (BA_PM_PAIR_SCHED): a stable sort of the pairs by the
+    // co-visibility window of their terms' tracks, as the host planner's two counting sorts
+    {
+        int32_t* pair_sched = alloc_out(BA_PM_PAIR_SCHED, NP);
+        int32_t* tlo = tmp.get<int32_t>(T, e);
+        int32_t* thi = tmp.get<int32_t>(T, e);
+        uint64_t* sk1 = tmp.get<uint64_t>(NP, e);
+        uint64_t* sk2 = tmp.get<uint64_t>(NP, e);
+        int32_t* sv1 = tmp.get<int32_t>(NP, e);
+        PM_TRY(e);
+        if (NP > 0) {
+            if (T > 0)
+                hipLaunchKernelGGL(k_track_span, dim3(grid_of(T)), dim3(PT), 0, st, trk_run_ptr, trk_run, run_img,
+                                   (int64_t)T, tlo, thi);
+            hipLaunchKernelGGL(k_pair_keys, dim3(grid_of(NP * 64)), dim3(PT), 0, st, term_ptr, term, run_trk, tlo, thi,
+                               NP, F, sk1, sv1);
+            PM_TRY(sort_pairs<uint64_t>(tmp, sk1, sk2, sv1, pair_sched, NP,
+                                        bits_for((uint64_t)F * (uint64_t)(F + 1) + (uint64_t)F), st));
+        }
+    }
     // ---- image rows: (pair, role) items in pair order, stably by row image
     int32_t* offf = tmp.get<int32_t>(NP + 1, e);
     int32_t* ipos = tmp.get<int32_t>(NP + 1, e);

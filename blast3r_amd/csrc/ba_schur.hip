@@ -1489,15 +1489,17 @@ __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
 // per off-diagonal image pair (one wave): S_ij = - sum over the pair's terms of V_ti V_tj^T, four
 // terms (twelve rows) per three 16 x 16 x 4 MFMAs per tile; the term indices of 64 terms are read at
 // once and handed to the row lanes by shuffles, the rows of the next 8 terms are requested before
-// the MFMAs of the current 8
+// the MFMAs of the current 8.  The pairs are taken in the plan's schedule (pairs whose
+// terms come from the same neighbourhood of images run together and find each other's V rows in the L2)
 template <int DP, typename Real>
 __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
     typedef PmMfma<Real> M;
     constexpr int NT = DP / 16;
     const Real* const Vg = (const Real*)a.V;
     const int lane = threadIdx.x & 63;
-    const int64_t p = xcd_block(blockIdx.x, gridDim.x) * (PM_T / 64) + (threadIdx.x >> 6);
-    if (p >= a.n_pairs) return;
+    const int64_t q = xcd_block(blockIdx.x, gridDim.x) * (PM_T / 64) + (threadIdx.x >> 6);
+    if (q >= a.n_pairs) return;
+    const int64_t p = a.pair_sched != nullptr ? a.pair_sched[q] : q;     // the plan's processing order
     const int i1 = a.pair_i1[p], i2 = a.pair_i2[p];
     if (i1 == i2) return;
     const int d = a.lay.d;

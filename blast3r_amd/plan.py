@@ -220,7 +220,8 @@ class BAPlan:
 
 
 PM_ARRAYS = ['run_ptr', 'run_obs', 'run_trk', 'run_img', 'img_run_ptr', 'trk_run_ptr', 'trk_run', 'trk_obs_ptr',
-             'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'row_ptr', 'row_ent', 'diag_pair', 'term_ptr', 'term']
+             'trk_obs', 'obs_img', 'pair_i1', 'pair_i2', 'row_ptr', 'row_ent', 'diag_pair', 'term_ptr', 'term',
+             'pair_sched']
 PM_SCALARS = ['n_runs', 'n_pairs', 'n_terms', 'max_terms', 'max_track_runs']
 
 

@@ -211,6 +211,7 @@ typedef struct {
     const int32_t* infos; int32_t n_imgs; int32_t n_tracks;
     const int32_t *run_ptr, *run_obs, *run_trk, *run_img, *img_run_ptr, *trk_run_ptr, *trk_run, *trk_obs_ptr,
         *trk_obs, *obs_img, *pair_i1, *pair_i2, *diag_pair, *term_ptr, *term;
+    const int32_t* pair_sched;               /* optional: the order k_pm_pairs takes the pairs in (NULL = pair order) */
     int64_t n_obs, n_runs, n_pairs;
     /* observations in their own (image-major) order */
     const int32_t* pids; const float *pix2d, *pix2d_std, *pix2d_dep;

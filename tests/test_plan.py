@@ -440,6 +440,17 @@ def test_pm_plan_matches_brute_force(case):
         ent = h['row_ent'][h['row_ptr'][i]:h['row_ptr'][i + 1]]
         want = [(q << 1) | int(pr[0] != i) for q, pr in enumerate(pairs) if i in pr]
         assert ent.tolist() == want
+    # schedule: pairs by (smallest first image, largest last image) over the tracks of their terms, then
+    # pair id; pairs without terms (every diagonal pair) last, in pair order
+    F = len(cum)
+    t_imgs = {t: [keys[r][0] for r in rs] for t, rs in trk_runs.items() if rs}
+    sched_key = []
+    for q, pr in enumerate(pairs):
+        tr = [keys[ra][1] for ra, _ in terms.get(pr, [])] if pr[0] != pr[1] else []
+        lo = min((min(t_imgs[t]) for t in tr), default=F)
+        hi = max((max(t_imgs[t]) for t in tr), default=F)
+        sched_key.append((lo, hi, q))
+    assert h['pair_sched'].tolist() == [q for _, _, q in sorted(sched_key)]
 
 
 def test_pm_plan_errors():
