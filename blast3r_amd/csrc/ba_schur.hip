@@ -758,6 +758,23 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             }
             return acc_l;
         };
+        // the V groups of a diagonal slot: each entry's A and B rows are the same rows (one run with
+        // itself), read once
+        auto run_vd = [&](uint32_t Lb, int g0, int g1, dbl4 acc_l) -> dbl4 {
+            if (g0 >= g1) return acc_l;
+            uint32_t e = lds_rd_u32(Lb + 16u * (uint32_t)g0);
+            lds_wait(e);
+            for (int g = g0; g < g1; ++g) {
+                double A[3];
+                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
+                uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, g1 - 1));
+                lds_wait(A, en);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], A[c], acc_l, 0, 0, 0);
+                e = en;
+            }
+            return acc_l;
+        };
         auto run_j = [&](uint32_t Lb, int ng, dbl4 acc_l, double& dsq) -> dbl4 {
             if (ng <= 0) return acc_l;
             uint32_t e = lds_rd_u32(Lb);
@@ -793,7 +810,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 const int njg = BA_TAB_NJG(tab);
                 double dsq = 0.0;
                 acc[q] = run_j(Lb, njg, acc[q], dsq);
-                acc[q] = run_v(Lb, njg, ng, acc[q]);
+                acc[q] = run_vd(Lb, njg, ng, acc[q]);
                 dsq += __shfl_xor(dsq, 16);
                 dsq += __shfl_xor(dsq, 32);
                 if (lane < 16) lds_add_f64(lds_addr(&sDv[la][lane]), dsq);
