@@ -172,6 +172,58 @@ def main():
         lm_ms_direct = (time.perf_counter() - t0) * 1e3 / args.lm_steps
         log(f'[bench] lm_step with the direct reduced solve {lm_ms_direct:.2f} ms')
 
+    # the reference's default solver precision (GaussNewtonSolver dtype=torch.float32, what lm_step uses
+    # without dtype): the same pass in fp32 on the path the solver picks, its dominant kernel against the
+    # fp32 MFMA peak, and lm_step called without dtype
+    fp32 = None
+    if args.lm_steps > 0:
+        gs32 = GaussNewtonSolver(len(g.K), len(g.P_w2rig), prob.n_imgs, prob.n_tracks, dev, dtype=torch.float32)
+        J32 = gs32.compute_jacobians(g.infos, g.K, g.P_rig2cam, g.P_w2rig, g.z_coefs, g.pts3d, g.pids, g.pix2d_std,
+                                     g.pix2d_dep, True, optim_K=o['optim_K'], optim_P=o['optim_P'], pix2d=g.pix2d,
+                                     hp=hp)
+        res._ba_state = _param_state(J32)
+        ctx32 = gs32.prepare(J32, res, w)
+        a32, pm32 = ctx32['args'], ctx32['path'] == 'pairmajor'
+        stage = L.ba_pm_linearize_stage if pm32 else L.ba_linearize_stage
+
+        def step32(ev=None):
+            check(stage(a32, 0, st))
+            if ev is not None:
+                ev[0].record()
+            check(stage(a32, 1, st))
+            if ev is not None:
+                ev[1].record()
+            if not pm32:
+                check(stage(a32, 2, st))
+        for _ in range(args.warmup):
+            step32()
+        ev32 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(args.steps):
+            step32(ev32[k])
+        torch.cuda.synchronize()
+        ms32 = (time.perf_counter() - t0) * 1e3 / args.steps
+        k32_ms = sum(e0.elapsed_time(e1) for e0, e1 in ev32) / args.steps
+        k32_tf = kalg['flops_dense'] / (k32_ms * 1e-3) / 1e12 if not pm32 else None
+        del gs32, J32, ctx32
+        kw32 = {k: v for k, v in kw.items() if k != 'dtype'}
+        engine.lm_step(**g.lm_inputs(), **kw32)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.lm_steps):
+            engine.lm_step(**g.lm_inputs(), **kw32)
+        torch.cuda.synchronize()
+        lm32_ms = (time.perf_counter() - t0) * 1e3 / args.lm_steps
+        kn32 = 'k_pm_pairs' if pm32 else 'k_schur'
+        log(f'[bench] fp32 solver ({"pairmajor" if pm32 else "batched"} path): linearize+Schur {ms32:.3f} ms, {kn32} '
+            f'{k32_ms:.3f} ms; lm_step without dtype {lm32_ms:.2f} ms')
+        fp32 = {'note': 'GaussNewtonSolver(dtype=torch.float32), what lm_step uses without dtype (the reference default)',
+                'path': 'pairmajor' if pm32 else 'batched', 'ms_per_step': ms32, 'obs_per_s': n_obs / (ms32 * 1e-3),
+                'kernel': kn32, 'kernel_ms': k32_ms,
+                'kernel_fp32_tflops': k32_tf, 'kernel_fp32_frac': (k32_tf / 157.3) if k32_tf else None,
+                'lm_ms_per_iter': lm32_ms, 'lm_iters_per_s': 1e3 / lm32_ms}
+
     red = bench_reduced_solve(prob, g, dev, args.warmup) if args.reduced_solve else None
     smp = bench_sampling(prob, g, dev, args.steps, args.warmup, args.config) if args.sampling else None
     lay = bench_layout(prob, g, dev, args.steps, args.warmup) if args.layout else None
@@ -197,6 +249,7 @@ def main():
         'lm_iters_per_s': (1e3 / lm_ms) if lm_ms else None,
         'lm_iters_per_s_direct_solve': (1e3 / lm_ms_direct) if lm_ms_direct else None,
         'lm_ms_per_iter': lm_ms,
+        'fp32_solver': fp32,
         'roofline': {'bound': 'mfma', 'achieved': achieved_tf, 'peak': 78.6, 'unit': 'TFLOP/s',
                      'frac': achieved_tf / 78.6, 'traffic': traffic, 'kernel': kname,
                      'kernel_ms': schur_ms, 'flops_per_launch': kalg['flops_dense'], 'd_alg': kalg['d_alg'],

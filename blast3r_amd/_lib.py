@@ -54,7 +54,7 @@ _LIN_FIELDS = [
     ('r_in', c_p), ('w_in', c_p), ('r_s0', c_i64), ('r_s1', c_i64), ('w_s0', c_i64), ('w_s1', c_i64),
     ('ct_pt', c_p), ('n_ctracks', c_i64), ('core', c_p),
     ('chunk_slots', c_p), ('chunk_ent', c_p), ('chunk_eptr', c_p), ('b_pos_slot', c_p), ('pfac', c_p),
-    ('b_order', c_p), ('work_ctr', c_p), ('dc_img', c_p),
+    ('b_order', c_p), ('work_ctr', c_p), ('dc_img', c_p), ('real32', c_int),
 ]
 
 

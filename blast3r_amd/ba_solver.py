@@ -99,8 +99,8 @@ class GaussNewtonSolver:
         self.device = torch.device(device)
         # dtype is the precision of the linearisation's products and sums, the reduced system, the PCG and
         # the back-substitution, as in the reference (bs:22, :37, :128): torch.float64 (bundle_adjustment's
-        # choice, en:490) on either path; torch.float32 (its default) on the pair-major path, which has a
-        # fp32 variant of every kernel (the Jacobian core is evaluated in fp64 and rounded to fp32)
+        # choice, en:490) or torch.float32 (its default), on either path: every kernel has a fp32 variant
+        # (the Jacobian core is evaluated in fp64 and rounded to fp32)
         if dtype not in (torch.float32, torch.float64):
             raise ValueError(f'dtype must be torch.float32 or torch.float64, not {dtype}')
         self.dtype = dtype
@@ -130,9 +130,6 @@ class GaussNewtonSolver:
         # 'batched' outside its limits raises instead of switching paths
         if path not in ('auto', 'batched', 'pairmajor'):
             raise ValueError(f'unknown path {path!r}')
-        if path == 'batched' and self.real32:
-            raise ValueError("path='batched' runs in fp64: pass dtype=torch.float64, or use path='pairmajor' / "
-                             "'auto' for the fp32 solver")
         self.path = path
         self.use_graph = bool(use_graph)        # replay the PCG launches from a captured graph
         self.last = {}
@@ -284,7 +281,7 @@ class GaussNewtonSolver:
         if self.path == 'batched' and d > 15:
             raise ValueError(f"path='batched' takes at most 15 reduced parameters per image (here {d}); "
                              "use path='pairmajor' or 'auto'")
-        if self.path == 'pairmajor' or d > 15 or self.real32:
+        if self.path == 'pairmajor' or d > 15:
             return self._prepare_pm(J, residuals, w_pts, clamp_w, lay)
         L_img = int(self.plan_options.get('max_local_imgs', MAX_LOCAL))
         if self.path == 'auto' and get_plan(J.rigs, J.pids, self.tracks.true_n, kind='span').median_span > 2 * L_img:
@@ -310,24 +307,27 @@ class GaussNewtonSolver:
         ws = plan.workspace
         n_imgs = self.imgs.true_n
         n_ct = sc['n_ctracks']
-        Hpp = ws('Hpp', (max(n_ct, 1), 6), torch.float64)          # chunk-track order
-        gp = ws('gp', (max(n_ct, 1), 3), torch.float64)
+        R = self.dtype                         # the working precision of every array below but ct_pt and core
+        Hpp = ws('Hpp', (max(n_ct, 1), 6), R)  # chunk-track order
+        gp = ws('gp', (max(n_ct, 1), 3), R)
         ct_pt = ws('ct_pt', (max(n_ct, 1), 4), torch.float32)
-        pfac = ws('pfac', (max(n_ct, 1), 12), torch.float64)
+        pfac = ws('pfac', (max(n_ct, 1), 12), R)
         work_ctr = ws('work_ctr', (1,), torch.int32)
-        core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)   # linearisation records
-        chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), torch.float64)
-        lam_p = ws('lam_p', (1,), torch.float64)
+        # linearisation records: the Jacobian core, fp64 in both precisions
+        core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)
+        chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), R)
+        lam_p = ws('lam_p', (1,), R)
         dd = max(d, 1)
-        partials = ws('partials', (max(sc['n_slots'], 1), dd, dd), torch.float64)
-        img_partials = ws('img_partials', (max(sc['n_batches'], 1), plan.L, 2, dd), torch.float64)
+        partials = ws('partials', (max(sc['n_slots'], 1), dd, dd), R)
+        img_partials = ws('img_partials', (max(sc['n_batches'], 1), plan.L, 2, dd), R)
         # outputs live in the plan's workspace: fixed addresses across LM steps (graph replay)
-        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), torch.float64)
-        e_img = ws('e_img', (n_imgs, dd), torch.float64)
-        dg_img = ws('dg_img', (n_imgs, dd), torch.float64)
+        S_pairs = ws('S_pairs', (max(sc['n_pairs'], 1), dd, dd), R)
+        e_img = ws('e_img', (n_imgs, dd), R)
+        dg_img = ws('dg_img', (n_imgs, dd), R)
 
         a = BaLinArgs()
         pd = plan.dev
+        a.real32 = int(self.real32)
         a.infos = ptr(J.rigs.contiguous())
         a.n_imgs = n_imgs
         for name in ('chunk_obs', 'chunk_meta', 'slot_info', 'ct_pid', 'ct_first', 'ct_m', 'ct_mask', 'b_chunk_ptr',
@@ -465,7 +465,7 @@ class GaussNewtonSolver:
         n_imgs = self.imgs.true_n
         um = self._unknown_maps(J, lay, plan)
         n_u = um['n_u']
-        R = S_pairs.dtype                      # the working precision (fp32 only on the pair-major path)
+        R = S_pairs.dtype                      # the working precision
         if n_u > 0 and d > 0:
             x = ws('pcg_x', (n_u,), R)
             istate = ws('pcg_istate', (8,), torch.int32)
@@ -756,8 +756,8 @@ class GaussNewtonSolver:
         pid = plan.dev['ct_pid'][:n_ct].long()
         H = torch.zeros((T, 6), dtype=torch.float64, device=self.device)
         g = torch.zeros((T, 3), dtype=torch.float64, device=self.device)
-        H[pid] = last['Hpp'][:n_ct]
-        g[pid] = last['gp'][:n_ct]
+        H[pid] = last['Hpp'][:n_ct].to(torch.float64)
+        g[pid] = last['gp'][:n_ct].to(torch.float64)
         return H, g
 
     def reduced_system_dense(self):

@@ -7,7 +7,8 @@
 // with four kernels over a precomputed structure plan (ba_plan.cpp):
 //   k_track_pp     per chunk: point blocks H_pp, g_p per track (+ max diag for the damping)
 //   k_schur        per batch: camera-pair blocks of S = H_cc - H_cp H_pp^-1 H_pc, accumulated
-//                  in fp64 MFMA tiles held in registers, plus rhs and diag(H_cc) per image
+//                  in MFMA tiles of the working precision (fp64, or fp32 for the fp32 solver) held in
+//                  registers, plus rhs and diag(H_cc) per image
 //   k_pair_reduce  per image pair: deterministic sum of the batch partials
 //   k_backsub      per chunk: delta_p = H_pp^-1 (g_p - H_pc delta_c)
 // The expensive per-observation work (residual, IRLS weight, Jacobian core) is done once, in
@@ -231,13 +232,15 @@ __device__ __forceinline__ void chol3_factor(const R H[6], R lam, R L[6]) {
     L[0] = l00; L[1] = l10; L[2] = l20; L[3] = l11; L[4] = l21; L[5] = l22;
 }
 
-__device__ __forceinline__ void chol3_fwd(const double L[6], const double b[3], double y[3]) {
+template <typename R>
+__device__ __forceinline__ void chol3_fwd(const R L[6], const R b[3], R y[3]) {
     y[0] = b[0] / L[0];
     y[1] = (b[1] - L[1] * y[0]) / L[3];
     y[2] = (b[2] - L[2] * y[0] - L[4] * y[1]) / L[5];
 }
 
-__device__ __forceinline__ void chol3_bwd(const double L[6], const double z[3], double x[3]) {
+template <typename R>
+__device__ __forceinline__ void chol3_bwd(const R L[6], const R z[3], R x[3]) {
     x[2] = z[2] / L[5];
     x[1] = (z[1] - L[4] * x[2]) / L[3];
     x[0] = (z[0] - L[1] * x[1] - L[2] * x[2]) / L[0];
@@ -281,10 +284,10 @@ __device__ __forceinline__ void obs_core_slot(const LinArgs& a, int64_t slot, in
 // iteration and writes its linearisation record; writes, per chunk track (index first_ct + t),
 // H_pp upper, g_p, the point with its enable flag, and the chunk's largest point-block diagonal
 // (for the damping value).
-template <int HK, int HP>
+template <int HK, int HP, typename Real>
 __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 waves per SIMD: 96 VGPRs, no spills
-    __shared__ double sh[BA_CHUNK][9];
-    __shared__ double smax[BA_CHUNK];
+    __shared__ Real sh[BA_CHUNK][9];
+    __shared__ Real smax[BA_CHUNK];
     const int chunk = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = (int64_t)chunk * BA_CHUNK + tid;
     // Everything that depends only on the slot or the chunk is requested at once (an empty slot
@@ -301,9 +304,9 @@ __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 wa
     ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
     const int ct_f = a.ct_first[ct], ct_m = a.ct_m[ct], ct_pid = a.ct_pid[ct];
     const float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
-    double c[9];
+    Real c[9];
 #pragma unroll
-    for (int k = 0; k < 9; ++k) c[k] = 0.0;
+    for (int k = 0; k < 9; ++k) c[k] = Real(0);
     if (obs >= 0) {
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
@@ -327,28 +330,28 @@ __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 wa
 #pragma unroll
         for (int q = 0; q < 6; ++q) {
             int i = pr[q][0], j = pr[q][1];
-            c[q] = Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j];
+            c[q] = (Real)(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j]);
         }
-        c[6] = gP[0]; c[7] = gP[1]; c[8] = gP[2];
+        c[6] = (Real)gP[0]; c[7] = (Real)gP[1]; c[8] = (Real)gP[2];
     }
 #pragma unroll
     for (int k = 0; k < 9; ++k) sh[tid][k] = c[k];
     const float* Xc = a.pts3d + 3 * (int64_t)ct_pid;
     const float4 cpt = make_float4(Xc[0], Xc[1], Xc[2], (a.enX ? a.enX[ct_pid] != 0 : true) ? 1.f : 0.f);
     __syncthreads();
-    double mx = 0.0;
+    Real mx = Real(0);
     if (tid < n_ct) {
         const int f = ct_f, m = ct_m;
-        double s[9];
+        Real s[9];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) s[k] = 0.0;
+        for (int k = 0; k < 9; ++k) s[k] = Real(0);
         for (int q = 0; q < m; ++q)
 #pragma unroll
             for (int k = 0; k < 9; ++k) s[k] += sh[f + q][k];
 #pragma unroll
-        for (int k = 0; k < 6; ++k) a.Hpp[6 * ct + k] = s[k];
+        for (int k = 0; k < 6; ++k) ((Real*)a.Hpp)[6 * ct + k] = s[k];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) a.gp[3 * ct + k] = s[6 + k];
+        for (int k = 0; k < 3; ++k) ((Real*)a.gp)[3 * ct + k] = s[6 + k];
         reinterpret_cast<float4*>(a.ct_pt)[ct] = cpt;
         mx = fmax(fmax(fabs(s[0]), fabs(s[3])), fabs(s[5]));
     }
@@ -358,7 +361,7 @@ __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 wa
         if (tid < w) smax[tid] = fmax(smax[tid], smax[tid + w]);
         __syncthreads();
     }
-    if (tid == 0) a.chunk_max[chunk] = smax[0];
+    if (tid == 0) ((Real*)a.chunk_max)[chunk] = smax[0];
 }
 
 // lam_p = dampen * max diag over all tracks (BlockDiagMat.dampen_, ba_solver.py:575-582).
@@ -432,7 +435,7 @@ __global__ void __launch_bounds__(256) k_point_factor(const R* __restrict__ Hpp,
 //         diagonal (a,a):      acc += V_ta^T V_ta        per covering track
 //                              acc -= J_o^T J_o          per observation o in image a
 //       The entries of a slot are taken four at a time along the MFMA's K dimension: lane group k
-//       of a 16x16x4 fp64 MFMA reads row c of entry k's blocks, and one MFMA per row c = 0..2
+//       of a 16x16x4 MFMA reads row c of entry k's blocks, and one MFMA per row c = 0..2
 //       sums c over four entries.  The partial block is -acc; column 15 of a diagonal tile then
 //       holds sum J_c^T W r - V w = the image's rhs term, and diag(J_c^T J_c) is summed from the
 //       squared B operands of the J entries.
@@ -482,34 +485,79 @@ __device__ __forceinline__ void lds_rd3(uint32_t addr, double (&v)[3]) {
     asm volatile("ds_read_b64 %0, %1 offset:128 ; ba_pf" : "=v"(v[1]) : "v"(addr));
     asm volatile("ds_read_b64 %0, %1 offset:256 ; ba_pf" : "=v"(v[2]) : "v"(addr));
 }
+// fp32 blocks: rows 16 floats (64 bytes) apart
+__device__ __forceinline__ void lds_rd3(uint32_t addr, float (&v)[3]) {
+    asm volatile("ds_read_b32 %0, %1 ; ba_pf" : "=v"(v[0]) : "v"(addr));
+    asm volatile("ds_read_b32 %0, %1 offset:64 ; ba_pf" : "=v"(v[1]) : "v"(addr));
+    asm volatile("ds_read_b32 %0, %1 offset:128 ; ba_pf" : "=v"(v[2]) : "v"(addr));
+}
 __device__ __forceinline__ void lds_wait(uint32_t& a) {
     asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw" : "+v"(a));
 }
-__device__ __forceinline__ void lds_wait(double (&A)[3], uint32_t& d) {
+template <typename Real>
+__device__ __forceinline__ void lds_wait(Real (&A)[3], uint32_t& d) {
     asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(d));
 }
-__device__ __forceinline__ void lds_wait(double (&A)[3], double (&B)[3], uint32_t& d) {
+template <typename Real>
+__device__ __forceinline__ void lds_wait(Real (&A)[3], Real (&B)[3], uint32_t& d) {
     asm volatile("s_waitcnt lgkmcnt(0) ; ba_pw"
                  : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(d));
 }
-// LDS f64 atomic add (no return) at a byte address, also outside the compiler's view of LDS.
-__device__ __forceinline__ void lds_add_f64(uint32_t addr, double v) {
+// LDS atomic add (no return) at a byte address, also outside the compiler's view of LDS.
+__device__ __forceinline__ void lds_add(uint32_t addr, double v) {
     asm volatile("ds_add_f64 %0, %1 ; ba_pa" : : "v"(addr), "v"(v) : "memory");
 }
+__device__ __forceinline__ void lds_add(uint32_t addr, float v) {
+    asm volatile("ds_add_f32 %0, %1 ; ba_pa" : : "v"(addr), "v"(v) : "memory");
+}
 
-struct Staging {                // one chunk's inputs, laid out as the copies write them
+// The camera-pair tiles in the working precision: a 16 x 16 x 4 MFMA, the J groups with A negated
+// (fp64: the MFMA's neg modifier; fp32: the operand's sign, an exact flip), and the accumulator
+// layout (lane l, element v holds D[row(l, v)][l % 16]).
+template <typename Real> struct SchurMfma;
+template <>
+struct SchurMfma<double> {
+    typedef dbl4 V4;
+    static __device__ __forceinline__ V4 mac(double a, double b, V4 c) {
+        return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ V4 mac_neg(double a, V4 c) {
+        return __builtin_amdgcn_mfma_f64_16x16x4f64(a, a, c, 0, 0, 1);      // neg:[1,0,0]
+    }
+    static __device__ __forceinline__ int row(int lane, int v) { return 4 * v + (lane >> 4); }
+};
+template <>
+struct SchurMfma<float> {
+    typedef flt4 V4;
+    static __device__ __forceinline__ V4 mac(float a, float b, V4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ V4 mac_neg(float a, V4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(-a, a, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int row(int lane, int v) { return 4 * (lane >> 4) + v; }
+};
+
+// One chunk's inputs, laid out as the copies write them.  The point factors of a chunk track (12 values
+// in the working precision) arrive in 16-byte copies: element i of track ct at pf[i / PF][ct][i % PF].
+template <typename Real>
+struct Staging {
+    static constexpr int PF = 16 / sizeof(Real);            // values per 16-byte copy
     double rec[BA_CORE * BA_CHUNK];         // the chunk's linearisation records (field-major, as in memory)
     int info[BA_CHUNK];                     // slot_info per slot
     int obs[BA_CHUNK];                      // chunk_obs per slot
     float dep[BA_PRE_C][BA_CHUNK];          // depth guidance channels c < min(C, BA_PRE_C)
-    double pf[6][BA_MAX_CT][2];             // point factors of each chunk track (L | w | 1/pivots), 16 bytes per copy
+    Real pf[12 / PF][BA_MAX_CT][PF];        // point factors of each chunk track (L | w | 1/pivots)
     float4 X[BA_MAX_CT];                    // point, enable flag
+    __device__ __forceinline__ Real f(int i, int ct) const { return pf[i / PF][ct][i % PF]; }
 };
 
 // waves 0-1: the slots of chunk ck; wave 2: its chunk tracks (first_ct ..), n_ct; wave 3: its entry list
-__device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* sNct,
+template <typename Real>
+__device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging<Real>& S, int* sNct,
                                             uint32_t (*lists)[BA_LIST_CAP], int (*tabs)[BA_MAX_SLOTS], int ck,
                                             int first_ct, int C, int wave, int lane) {
+    constexpr int PF = Staging<Real>::PF;
     if (wave < 2) {
         const int w = __builtin_amdgcn_readfirstlane(wave);
         const int64_t slot = (int64_t)ck * BA_CHUNK + 64 * w + lane;
@@ -526,8 +574,9 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
     } else if (wave == 2) {
         int64_t ct = (int64_t)first_ct + lane;
         ct = ct < a.n_ctracks ? ct : a.n_ctracks - 1;
+        const Real* pfac = (const Real*)a.pfac;
 #pragma unroll
-        for (int k = 0; k < 6; ++k) dma16_to_lds(a.pfac + 12 * ct + 2 * k, &S.pf[k][0][0]);
+        for (int k = 0; k < 12 / PF; ++k) dma16_to_lds(pfac + 12 * ct + PF * k, &S.pf[k][0][0]);
         dma16_to_lds(a.ct_pt + 4 * ct, S.X);
         if (lane == 0) *sNct = a.chunk_meta[4 * ck + 2];
     } else if (wave == 3) {
@@ -545,12 +594,15 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging& S, int* s
     }
 }
 
-template <int HK, int HP>
+template <int HK, int HP, typename Real>
 __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
-    extern __shared__ double sBlk[];                     // [BA_CHUNK][BA_BLK] observation blocks + zero block
-    __shared__ Staging sSt;                              // this chunk's inputs (the next chunk's, in phase B)
-    __shared__ double sJp[BA_CHUNK][9];                  // weighted point rows J_p of each slot
-    __shared__ double sDv[BA_MAX_LOCAL][16];             // per local image: diag(J_c^T J_c)
+    typedef SchurMfma<Real> M;
+    typedef typename M::V4 V4;
+    extern __shared__ __align__(16) char sBlkRaw[];     // [BA_CHUNK][BA_BLK] observation blocks + zero block
+    Real* const sBlk = reinterpret_cast<Real*>(sBlkRaw);
+    __shared__ Staging<Real> sSt;                        // this chunk's inputs (the next chunk's, in phase B)
+    __shared__ Real sJp[BA_CHUNK][9];                    // weighted point rows J_p of each slot
+    __shared__ Real sDv[BA_MAX_LOCAL][16];               // per local image: diag(J_c^T J_c)
     __shared__ int sInfo[BA_CHUNK];
     __shared__ CamF sCam[BA_MAX_LOCAL];
     __shared__ unsigned char sEn[BA_MAX_LOCAL * 3];
@@ -608,16 +660,16 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             sQ[p] = q;
             sPair[p] = q >= 0 && q < ns ? a.slot_pair[s0 + q] : -1;
         }
-        for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = 0.0;
-        for (int q = tid; q < 48; q += BA_WAVES * 64) sBlk[BA_ZERO + q] = 0.0;
+        for (int q = tid; q < BA_MAX_LOCAL * 16; q += BA_WAVES * 64) sDv[q >> 4][q & 15] = Real(0);
+        for (int q = tid; q < 48; q += BA_WAVES * 64) sBlk[BA_ZERO + q] = Real(0);
     }
     __syncthreads();
 
-    dbl4 acc[BA_SLOTS_PER_WAVE];
+    V4 acc[BA_SLOTS_PER_WAVE];
     int my_pq[BA_SLOTS_PER_WAVE], my_q[BA_SLOTS_PER_WAVE];       // this wave's slots: pair, batch slot
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
-        acc[q] = dbl4{0.0, 0.0, 0.0, 0.0};
+        acc[q] = V4{Real(0), Real(0), Real(0), Real(0)};
         my_pq[q] = __builtin_amdgcn_readfirstlane(sPair[wave + BA_WAVES * q]);
         my_q[q] = __builtin_amdgcn_readfirstlane(sQ[wave + BA_WAVES * q]);
     }
@@ -639,8 +691,8 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 o.J.zscale = sSt.rec[14 * BA_CHUNK + t];
                 o.sW[2] = reinterpret_cast<const float2*>(sSt.rec)[19 * BA_CHUNK + t].y;
                 const bool eZ = sEn[3 * li + 2] != 0, first = sSt.obs[t] == 0;
-                double* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
-                auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? v : 0.0; };
+                Real* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
+                auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? (Real)v : Real(0); };
                 DepSrc dep;
 #pragma unroll
                 for (int c = 0; c < BA_PRE_C; ++c) dep.r[c] = c < C ? sSt.dep[c][t] : 0.f;
@@ -651,25 +703,25 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 core_load(sSt.rec, t, o);
                 const bool eK = sEn[3 * li] != 0, eP = sEn[3 * li + 1] != 0, eZ = sEn[3 * li + 2] != 0;
                 const bool first = sSt.obs[t] == 0, xon = sSt.X[ct].w != 0.f && !a.lay.x_off;
-                double* blk = sBlk + t * BA_BLK + BA_JROW + 16 * rr;
-                auto sink = [&](int j, double v) { if (j < 15) blk[j] = j < d ? v : 0.0; };
+                Real* blk = sBlk + t * BA_BLK + BA_JROW + 16 * rr;
+                auto sink = [&](int j, double v) { if (j < 15) blk[j] = j < d ? (Real)v : Real(0); };
                 double jp[3];
                 DepSrc dep;
                 if (rr == 0) {
                     emit_jc_row<HK, HP, 0>(o, a.lay, eK, eP, eZ, first, dep, sink);
-                    blk[15] = o.Rs[0];
+                    blk[15] = (Real)o.Rs[0];
                     point_row<0>(o, sCam[li], xon, jp);
                 } else if (rr == 1) {
                     emit_jc_row<HK, HP, 1>(o, a.lay, eK, eP, eZ, first, dep, sink);
-                    blk[15] = o.Rs[1];
+                    blk[15] = (Real)o.Rs[1];
                     point_row<1>(o, sCam[li], xon, jp);
                 } else {
                     emit_jc_row<HK, HP, 2, 0, 2 * HK + 6 * HP>(o, a.lay, eK, eP, eZ, first, dep, sink);
-                    blk[15] = o.Rs[2];
+                    blk[15] = (Real)o.Rs[2];
                     point_row<2>(o, sCam[li], xon, jp);
                 }
 #pragma unroll
-                for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = jp[k];
+                for (int k = 0; k < 3; ++k) sJp[t][3 * rr + k] = (Real)jp[k];
             }
             if (rr == 0) {
                 const uint64_t dup = __ballot(valid && leader != t);
@@ -686,29 +738,29 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             if (info2 >= 0) {
                 const int q = tid >> 7, c = q % 3, h = q / 3;
                 const int ct2 = (info2 >> 8) & 0xff, leader2 = info2 >> 16;
-                const double (*F)[BA_MAX_CT][2] = sSt.pf;      // element i of track ct at F[i / 2][ct][i % 2]
-                const double l10 = F[0][ct2][1], l20 = F[1][ct2][0], l21 = F[2][ct2][0];
-                const double r0 = F[4][ct2][1], r1 = F[5][ct2][0], r2 = F[5][ct2][1];
-                double Pc[3];
+                // the chunk track's factor: L (0-5), w = L^-1 g_p (6-8), reciprocal pivots (9-11)
+                const Real l10 = sSt.f(1, ct2), l20 = sSt.f(2, ct2), l21 = sSt.f(4, ct2);
+                const Real r0 = sSt.f(9, ct2), r1 = sSt.f(10, ct2), r2 = sSt.f(11, ct2);
+                Real Pc[3];
 #pragma unroll
                 for (int r = 0; r < 3; ++r) {
-                    const double p0 = sJp[t][3 * r] * r0;
-                    const double p1 = (sJp[t][3 * r + 1] - l10 * p0) * r1;
-                    const double p2 = (sJp[t][3 * r + 2] - l20 * p0 - l21 * p1) * r2;
+                    const Real p0 = sJp[t][3 * r] * r0;
+                    const Real p1 = (sJp[t][3 * r + 1] - l10 * p0) * r1;
+                    const Real p2 = (sJp[t][3 * r + 2] - l20 * p0 - l21 * p1) * r2;
                     Pc[r] = c == 0 ? p0 : (c == 1 ? p1 : p2);
                 }
-                double* blk = sBlk + t * BA_BLK;
+                Real* blk = sBlk + t * BA_BLK;
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
                     const int j = 8 * h + jj;
                     if (j < 15) {
-                        const double j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
-                        blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : 0.0;
+                        const Real j0 = blk[BA_JROW + j], j1 = blk[BA_JROW + 16 + j], j2 = blk[BA_JROW + 32 + j];
+                        blk[16 * c + j] = j < d ? j0 * Pc[0] + j1 * Pc[1] + j2 * Pc[2] : Real(0);
                     }
                 }
                 if (h == 1) {
-                    const double wc = c == 0 ? F[3][ct2][0] : (c == 1 ? F[3][ct2][1] : F[4][ct2][0]);
-                    blk[16 * c + 15] = leader2 == t ? wc : 0.0;
+                    const Real wc = c == 0 ? sSt.f(6, ct2) : (c == 1 ? sSt.f(7, ct2) : sSt.f(8, ct2));
+                    blk[16 * c + 15] = leader2 == t ? wc : Real(0);
                 }
             }
         }
@@ -716,11 +768,11 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         if (sDup[0] | sDup[1]) {
             // several observations of one track in one image: V of the run is summed into its first slot
             if (row_lane && rr < 3 && valid && leader == t) {   // lane (slot, rr): V row rr
-                double* dst = sBlk + t * BA_BLK + 16 * rr;
+                Real* dst = sBlk + t * BA_BLK + 16 * rr;
                 for (int f = t + 1; f < BA_CHUNK; ++f) {
                     const int fi = sInfo[f];
                     if (fi < 0 || (fi >> 16) != t) break;
-                    const double* src = sBlk + f * BA_BLK + 16 * rr;
+                    const Real* src = sBlk + f * BA_BLK + 16 * rr;
 #pragma unroll
                     for (int j = 0; j < 15; ++j) dst[j] += src[j];
                 }
@@ -741,53 +793,54 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
         // with this group's operands.  A diagonal slot starts with its J groups (A = B = the J rows
         // of one observation each, A negated by the MFMA's modifier, and their squares summed into
         // diag(J_c^T J_c)), then its V groups.  Every LDS read here goes through lds_rd* (above).
-        const uint32_t lane_base = lds_addr(sBlk) + 8u * (uint32_t)l15;
-        auto run_v = [&](uint32_t Lb, int g0, int g1, dbl4 acc_l) -> dbl4 {
+        constexpr uint32_t RB = sizeof(Real);            // bytes per value
+        const uint32_t lane_base = lds_addr(sBlk) + RB * (uint32_t)l15;
+        auto run_v = [&](uint32_t Lb, int g0, int g1, V4 acc_l) -> V4 {
             if (g0 >= g1) return acc_l;
             uint32_t e = lds_rd_u32(Lb + 16u * (uint32_t)g0);
             lds_wait(e);
             for (int g = g0; g < g1; ++g) {
-                double A[3], B[3];
-                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
-                lds_rd3(lane_base + 8u * (e >> 16), B);
+                Real A[3], B[3];
+                lds_rd3(lane_base + RB * (e & 0xffffu), A);
+                lds_rd3(lane_base + RB * (e >> 16), B);
                 uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, g1 - 1));
                 lds_wait(A, B, en);
 #pragma unroll
-                for (int c = 0; c < 3; ++c) acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], B[c], acc_l, 0, 0, 0);
+                for (int c = 0; c < 3; ++c) acc_l = M::mac(A[c], B[c], acc_l);
                 e = en;
             }
             return acc_l;
         };
         // the V groups of a diagonal slot: each entry's A and B rows are the same rows (one run with
         // itself), read once
-        auto run_vd = [&](uint32_t Lb, int g0, int g1, dbl4 acc_l) -> dbl4 {
+        auto run_vd = [&](uint32_t Lb, int g0, int g1, V4 acc_l) -> V4 {
             if (g0 >= g1) return acc_l;
             uint32_t e = lds_rd_u32(Lb + 16u * (uint32_t)g0);
             lds_wait(e);
             for (int g = g0; g < g1; ++g) {
-                double A[3];
-                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
+                Real A[3];
+                lds_rd3(lane_base + RB * (e & 0xffffu), A);
                 uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, g1 - 1));
                 lds_wait(A, en);
 #pragma unroll
-                for (int c = 0; c < 3; ++c) acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], A[c], acc_l, 0, 0, 0);
+                for (int c = 0; c < 3; ++c) acc_l = M::mac(A[c], A[c], acc_l);
                 e = en;
             }
             return acc_l;
         };
-        auto run_j = [&](uint32_t Lb, int ng, dbl4 acc_l, double& dsq) -> dbl4 {
+        auto run_j = [&](uint32_t Lb, int ng, V4 acc_l, Real& dsq) -> V4 {
             if (ng <= 0) return acc_l;
             uint32_t e = lds_rd_u32(Lb);
             lds_wait(e);
             for (int g = 0; g < ng; ++g) {
-                double A[3];
-                lds_rd3(lane_base + 8u * (e & 0xffffu), A);
+                Real A[3];
+                lds_rd3(lane_base + RB * (e & 0xffffu), A);
                 uint32_t en = lds_rd_u32(Lb + 16u * (uint32_t)min(g + 1, ng - 1));
                 lds_wait(A, en);
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
                     dsq += A[c] * A[c];
-                    acc_l = __builtin_amdgcn_mfma_f64_16x16x4f64(A[c], A[c], acc_l, 0, 0, 1);   // neg:[1,0,0]
+                    acc_l = M::mac_neg(A[c], acc_l);
                 }
                 e = en;
             }
@@ -808,36 +861,36 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
                 acc[q] = run_v(Lb, 0, ng, acc[q]);
             } else {
                 const int njg = BA_TAB_NJG(tab);
-                double dsq = 0.0;
+                Real dsq = Real(0);
                 acc[q] = run_j(Lb, njg, acc[q], dsq);
                 acc[q] = run_vd(Lb, njg, ng, acc[q]);
                 dsq += __shfl_xor(dsq, 16);
                 dsq += __shfl_xor(dsq, 32);
-                if (lane < 16) lds_add_f64(lds_addr(&sDv[la][lane]), dsq);
+                if (lane < 16) lds_add(lds_addr(&sDv[la][lane]), dsq);
             }
         }
     }
 
-    // flush this batch's partial blocks (-acc, row-major d x d, local orientation);
-    // v_mfma_f64_16x16x4f64 accumulator layout: lane l, element v holds D[4v + l/16][l%16]
+    // flush this batch's partial blocks (-acc, row-major d x d, local orientation); accumulator
+    // layout: lane l, element v holds D[M::row(l, v)][l % 16]
     const int jc = lane & 15;
 #pragma unroll
     for (int q = 0; q < BA_SLOTS_PER_WAVE; ++q) {
         const int pq = my_pq[q];
         if (pq >= 0) {
             const int sl = my_q[q];
-            double* P = a.partials + (int64_t)(s0 + sl) * d * d;
+            Real* P = (Real*)a.partials + (int64_t)(s0 + sl) * d * d;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int i = 4 * v + (lane >> 4);
+                const int i = M::row(lane, v);
                 if (i < d && jc < d) P[i * d + jc] = -acc[q][v];
             }
             const int la = pq & 0xff, lb = (pq >> 8) & 0xff;
             if (la == lb && jc == 15) {
-                double* o = a.img_partials + ((int64_t)batch * a.L + la) * 2 * d;
+                Real* o = (Real*)a.img_partials + ((int64_t)batch * a.L + la) * 2 * d;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int i = 4 * v + (lane >> 4);
+                    const int i = M::row(lane, v);
                     if (i < d) o[i] = -acc[q][v];
                 }
             }
@@ -846,7 +899,7 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
     __syncthreads();
     {
         const int va = tid >> 4, vj = tid & 15;
-        if (va < nimg && vj < d) a.img_partials[((int64_t)batch * a.L + va) * 2 * d + d + vj] = sDv[va][vj];
+        if (va < nimg && vj < d) ((Real*)a.img_partials)[((int64_t)batch * a.L + va) * 2 * d + d + vj] = sDv[va][vj];
     }
     if (a.work_ctr == nullptr) break;
     __syncthreads();                     // this batch's LDS fully read before the next one is staged
@@ -856,16 +909,17 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
 __global__ void k_ctr_clear(int* ctr) { *ctr = 0; }
 
 // ----------------------------------------------------------------------------- reductions
+template <typename Real>
 __global__ void __launch_bounds__(256) k_pair_reduce(const int* __restrict__ pair_ptr, const int* __restrict__ pair_src,
-                                                     const double* __restrict__ partials, int64_t n_pairs, int d,
-                                                     double* __restrict__ out) {
+                                                     const Real* __restrict__ partials, int64_t n_pairs, int d,
+                                                     Real* __restrict__ out) {
     int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int dd = d * d;
     if (tid >= n_pairs * dd) return;
     int64_t p = tid / dd;
     int e = (int)(tid - p * dd);
     int i = e / d, j = e - (e / d) * d;
-    double acc = 0.0;
+    Real acc = Real(0);
     for (int q = pair_ptr[p]; q < pair_ptr[p + 1]; ++q) {
         int src = pair_src[q];
         int64_t s = src >> 1;
@@ -874,15 +928,16 @@ __global__ void __launch_bounds__(256) k_pair_reduce(const int* __restrict__ pai
     out[tid] = acc;
 }
 
+template <typename Real>
 __global__ void __launch_bounds__(256) k_img_reduce(const int* __restrict__ img_ptr, const int* __restrict__ img_src,
-                                                    const double* __restrict__ ip, int n_imgs, int d,
-                                                    double* __restrict__ e_out, double* __restrict__ dg_out) {
+                                                    const Real* __restrict__ ip, int n_imgs, int d,
+                                                    Real* __restrict__ e_out, Real* __restrict__ dg_out) {
     int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (tid >= (int64_t)n_imgs * d) return;
     int i = (int)(tid / d), j = (int)(tid - (tid / d) * d);
-    double e = 0.0, g = 0.0;
+    Real e = Real(0), g = Real(0);
     for (int q = img_ptr[i]; q < img_ptr[i + 1]; ++q) {
-        const double* s = ip + (int64_t)img_src[q] * 2 * d;
+        const Real* s = ip + (int64_t)img_src[q] * 2 * d;
         e += s[j];
         g += s[d + j];
     }
@@ -891,9 +946,11 @@ __global__ void __launch_bounds__(256) k_img_reduce(const int* __restrict__ img_
 }
 
 // ----------------------------------------------------------------------------- back-substitution
-template <int HK, int HP>
+// In fp32 (Real = float) the weighted rows and point rows are rounded from the fp64 core and every
+// product and sum after them is fp32, as on the pair-major path.
+template <int HK, int HP, typename Real>
 __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
-    __shared__ double sh[BA_CHUNK][3];
+    __shared__ Real sh[BA_CHUNK][3];
     const int chunk = blockIdx.x, tid = threadIdx.x;
     const int64_t slot = (int64_t)chunk * BA_CHUNK + tid;
     // slot- and chunk-only inputs first (as in k_track_pp): the observation's slot data, and this
@@ -907,54 +964,55 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
     int64_t ctk = first_ct + (tid < n_ct ? tid : 0);
     ctk = ctk < a.n_ctracks ? ctk : a.n_ctracks - 1;
     const int ct_f = a.ct_first[ctk], ct_m = a.ct_m[ctk], ct_pid = a.ct_pid[ctk];
-    double H[6], gpt[3];
+    Real H[6], gpt[3];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) H[k] = a.Hpp[6 * ctk + k];
+    for (int k = 0; k < 6; ++k) H[k] = ((const Real*)a.Hpp)[6 * ctk + k];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) gpt[k] = a.gp[3 * ctk + k];
-    double y[3] = {0.0, 0.0, 0.0};
+    for (int k = 0; k < 3; ++k) gpt[k] = ((const Real*)a.gp)[3 * ctk + k];
+    Real y[3] = {Real(0), Real(0), Real(0)};
     if (obs >= 0) {
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
         ObsCore o;
         core_load<true>(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
-        double xs[16];
+        Real xs[16];
         if (a.dc_img != nullptr) {                     // image-level copy: one load fewer
 #pragma unroll
-            for (int j = 0; j < 16; ++j) xs[j] = j < d ? a.dc_img[(int64_t)img * d + j] : 0.0;
+            for (int j = 0; j < 16; ++j) xs[j] = j < d ? ((const Real*)a.dc_img)[(int64_t)img * d + j] : Real(0);
         } else {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int u = j < d ? a.umap[(int64_t)img * d + j] : -1;
-                xs[j] = u >= 0 ? a.dc[u] : 0.0;
+                xs[j] = u >= 0 ? ((const Real*)a.dc)[u] : Real(0);
             }
         }
-        double t[3] = {0.0, 0.0, 0.0};
+        Real t[3] = {Real(0), Real(0), Real(0)};
         emit_jc<HK, HP>(o, a.lay, ctx.enK, ctx.enP, ctx.enZ, obs == 0, dep,
-                        [&](int r, int j, double v) { t[r] += v * xs[j]; });
+                        [&](int r, int j, double v) { t[r] += (Real)v * xs[j]; });
         const bool xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
         double Jp[3][3], gP[3];
         point_rows<false>(o, ctx.cp, xon, Jp, gP);
 #pragma unroll
-        for (int k = 0; k < 3; ++k) y[k] = Jp[0][k] * t[0] + Jp[1][k] * t[1] + Jp[2][k] * t[2];
+        for (int k = 0; k < 3; ++k)
+            y[k] = (Real)Jp[0][k] * t[0] + (Real)Jp[1][k] * t[1] + (Real)Jp[2][k] * t[2];
     }
     sh[tid][0] = y[0]; sh[tid][1] = y[1]; sh[tid][2] = y[2];
     __syncthreads();
     if (tid < n_ct) {
         const int f = ct_f, m = ct_m, pid = ct_pid;
-        double s[3] = {0.0, 0.0, 0.0};
+        Real s[3] = {Real(0), Real(0), Real(0)};
         for (int q = 0; q < m; ++q) { s[0] += sh[f + q][0]; s[1] += sh[f + q][1]; s[2] += sh[f + q][2]; }
-        double Lf[6], b[3], z[3], x[3];
+        Real Lf[6], b[3], z[3], x[3];
 #pragma unroll
         for (int k = 0; k < 3; ++k) b[k] = gpt[k] - s[k];
-        chol3_factor(H, a.lam_p[0], Lf);
+        chol3_factor(H, ((const Real*)a.lam_p)[0], Lf);
         chol3_fwd(Lf, b, z);
         chol3_bwd(Lf, z, x);
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
             a.dX[3 * (int64_t)pid + k] = (float)x[k];
-            if (a.dX64) a.dX64[3 * (int64_t)pid + k] = x[k];
+            if (a.dX64) ((Real*)a.dX64)[3 * (int64_t)pid + k] = x[k];
         }
     }
 }
@@ -1019,6 +1077,62 @@ static const char* missing_pointer(const ba_lin_args& a, int stage) {
 }
 
 // stage 0: point blocks + damping value; 1: camera-pair batches; 2: deterministic reductions
+// stages of the batched pass in the working precision Real (the checks are made by the caller)
+template <typename Real>
+static int lin_stage(const ba_lin_args& a, int32_t stage, hipStream_t st) {
+    Real* const chunk_max = (Real*)a.chunk_max;
+    Real* const lam_p = (Real*)a.lam_p;
+    if (stage == 0) {
+        hipLaunchKernelGGL(k_lam_clear<Real>, dim3(1), dim3(1), 0, st, chunk_max, a.n_chunks);
+        if (a.n_chunks > 0) {
+            BA_REQUIRE(a.n_ctracks >= 1 && a.ct_pt != nullptr, "chunk-track state missing");
+            BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_, Real>), dim3((unsigned)a.n_chunks),
+                                                     dim3(BA_CHUNK), 0, st, a));
+            const int64_t nb = a.n_chunks < 256 * 256 ? (a.n_chunks + 255) / 256 : 256;
+            hipLaunchKernelGGL(k_lam_reduce<Real>, dim3((unsigned)nb), dim3(256), 0, st, chunk_max, a.n_chunks);
+        }
+        hipLaunchKernelGGL(k_lam_final<Real>, dim3(1), dim3(1), 0, st, chunk_max, a.n_chunks, a.lay.dampen,
+                           a.lay.adaptive, a.lay.x_off, lam_p);
+        if (a.n_chunks > 0) {
+            BA_REQUIRE(a.pfac != nullptr, "point-factor scratch missing");
+            BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
+            hipLaunchKernelGGL(k_point_factor<Real>, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, (const Real*)a.Hpp,
+                               (const Real*)a.gp, (const Real*)lam_p, a.n_ctracks, (Real*)a.pfac);
+        }
+        BA_LAUNCHED();
+        return BA_OK;
+    }
+    if (stage == 1 && a.n_batches > 0) {
+        size_t lds = ((size_t)BA_CHUNK * BA_BLK + 48) * sizeof(Real);
+        // one workgroup per CU (the kernel's LDS allows one) pulling batches from the work queue
+        unsigned grid = (unsigned)a.n_batches;
+        if (a.work_ctr != nullptr) {
+            int dev = 0, n_cu = 0;
+            BA_HIP(hipGetDevice(&dev));
+            BA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+            if (n_cu > 0 && (int64_t)n_cu < a.n_batches) grid = (unsigned)n_cu;
+            hipLaunchKernelGGL(k_ctr_clear, dim3(1), dim3(1), 0, st, a.work_ctr);
+        }
+        BA_DISPATCH_KP(a.lay, {
+            BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_, Real>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds));
+            hipLaunchKernelGGL((k_schur<HK_, HP_, Real>), dim3(grid), dim3(BA_WAVES * 64), lds, st, a);
+        });
+        BA_LAUNCHED();
+    }
+    if (stage == 1) return BA_OK;
+    int d = a.lay.d;
+    if (a.n_pairs > 0) {
+        hipLaunchKernelGGL(k_pair_reduce<Real>, dim3(nblk(a.n_pairs * d * d, 256)), dim3(256), 0, st, a.pair_ptr,
+                           a.pair_src, (const Real*)a.partials, a.n_pairs, d, (Real*)a.S_pairs);
+        BA_LAUNCHED();
+    }
+    hipLaunchKernelGGL(k_img_reduce<Real>, dim3(nblk((int64_t)a.n_imgs * d, 256)), dim3(256), 0, st, a.img_ptr,
+                       a.img_src, (const Real*)a.img_partials, a.n_imgs, d, (Real*)a.e_img, (Real*)a.dg_img);
+    BA_LAUNCHED();
+    return BA_OK;
+}
+
 extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* stream) {
     clear_error();
     BA_REQUIRE(args != nullptr, "null args");
@@ -1031,59 +1145,12 @@ extern "C" int ba_linearize_stage(const ba_lin_args* args, int32_t stage, void* 
     BA_REQUIRE(a.lay.C >= 0 && a.lay.C <= BA_MAX_C, "fused path supports at most 24 z-coefficient columns");
     BA_REQUIRE(a.L >= 1 && a.L <= BA_MAX_LOCAL, "bad plan L");
     BA_REQUIRE(stage >= 0 && stage <= 2, "stage must be 0, 1 or 2");
+    BA_REQUIRE(a.real32 == 0 || a.real32 == 1, "real32 must be 0 or 1");
     if (a.n_chunks > 0) {
         const char* miss = missing_pointer(a, stage);
         BA_REQUIRE(miss == nullptr, miss);
     }
-    if (stage == 0) {
-        hipLaunchKernelGGL(k_lam_clear<double>, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks);
-        if (a.n_chunks > 0) {
-            BA_REQUIRE(a.n_ctracks >= 1 && a.ct_pt != nullptr, "chunk-track state missing");
-            BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_track_pp<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0,
-                                                     st, a));
-            const int64_t nb = a.n_chunks < 256 * 256 ? (a.n_chunks + 255) / 256 : 256;
-            hipLaunchKernelGGL(k_lam_reduce<double>, dim3((unsigned)nb), dim3(256), 0, st, a.chunk_max, a.n_chunks);
-        }
-        hipLaunchKernelGGL(k_lam_final<double>, dim3(1), dim3(1), 0, st, a.chunk_max, a.n_chunks, a.lay.dampen,
-                           a.lay.adaptive, a.lay.x_off, a.lam_p);
-        if (a.n_chunks > 0) {
-            BA_REQUIRE(a.pfac != nullptr, "point-factor scratch missing");
-            BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp) & 15) == 0, "Hpp and pfac must be 16-byte aligned");
-            hipLaunchKernelGGL(k_point_factor<double>, dim3(nblk(a.n_ctracks, 256)), dim3(256), 0, st, a.Hpp, a.gp,
-                               a.lam_p, a.n_ctracks, a.pfac);
-        }
-        BA_LAUNCHED();
-        return BA_OK;
-    }
-    if (stage == 1 && a.n_batches > 0) {
-        size_t lds = ((size_t)BA_CHUNK * BA_BLK + 48) * sizeof(double);
-        // one workgroup per CU (the kernel's LDS allows one) pulling batches from the work queue
-        unsigned grid = (unsigned)a.n_batches;
-        if (a.work_ctr != nullptr) {
-            int dev = 0, n_cu = 0;
-            BA_HIP(hipGetDevice(&dev));
-            BA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-            if (n_cu > 0 && (int64_t)n_cu < a.n_batches) grid = (unsigned)n_cu;
-            hipLaunchKernelGGL(k_ctr_clear, dim3(1), dim3(1), 0, st, a.work_ctr);
-        }
-        BA_DISPATCH_KP(a.lay, {
-            BA_HIP(hipFuncSetAttribute((const void*)k_schur<HK_, HP_>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds));
-            hipLaunchKernelGGL((k_schur<HK_, HP_>), dim3(grid), dim3(BA_WAVES * 64), lds, st, a);
-        });
-        BA_LAUNCHED();
-    }
-    if (stage == 1) return BA_OK;
-    int d = a.lay.d;
-    if (a.n_pairs > 0) {
-        hipLaunchKernelGGL(k_pair_reduce, dim3(nblk(a.n_pairs * d * d, 256)), dim3(256), 0, st, a.pair_ptr, a.pair_src,
-                           a.partials, a.n_pairs, d, a.S_pairs);
-        BA_LAUNCHED();
-    }
-    hipLaunchKernelGGL(k_img_reduce, dim3(nblk((int64_t)a.n_imgs * d, 256)), dim3(256), 0, st, a.img_ptr, a.img_src,
-                       a.img_partials, a.n_imgs, d, a.e_img, a.dg_img);
-    BA_LAUNCHED();
-    return BA_OK;
+    return a.real32 ? lin_stage<float>(a, stage, st) : lin_stage<double>(a, stage, st);
 }
 
 extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
@@ -1091,12 +1158,18 @@ extern "C" int ba_backsubstitute(const ba_lin_args* args, void* stream) {
     BA_REQUIRE(args != nullptr, "null args");
     const ba_lin_args& a = *args;
     BA_REQUIRE(a.lay.d >= 1 && a.lay.d <= 15, "fused path supports 1 <= d <= 15 image-level parameters");
+    BA_REQUIRE(a.real32 == 0 || a.real32 == 1, "real32 must be 0 or 1");
     if (a.n_chunks == 0) return BA_OK;
     BA_REQUIRE(a.n_ctracks >= 1, "chunk-track state missing");
     const char* miss = missing_pointer(a, 3);
     BA_REQUIRE(miss == nullptr, miss);
     hipStream_t st = (hipStream_t)stream;
-    BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_backsub<HK_, HP_>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0, st, a));
+    if (a.real32)
+        BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_backsub<HK_, HP_, float>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK), 0,
+                                                 st, a));
+    else
+        BA_DISPATCH_KP(a.lay, hipLaunchKernelGGL((k_backsub<HK_, HP_, double>), dim3((unsigned)a.n_chunks), dim3(BA_CHUNK),
+                                                 0, st, a));
     BA_LAUNCHED();
     return BA_OK;
 }

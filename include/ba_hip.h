@@ -127,36 +127,42 @@ typedef struct {
     const uint8_t *enK, *enP, *enZ, *enX;
     ba_huber hp;
     ba_layout lay;
+    /* (R) = elements of the working precision: double, or float when real32 is set */
     /* per-track state in chunk-track order (the plan's ct_* arrays): H_pp upper (n_ctracks,6) and
-     * g_p (n_ctracks,3) in fp64, the point and its enable flag (n_ctracks,4) in fp32 */
-    double *Hpp, *gp;    /* Hpp 16-byte aligned */
-    double *chunk_max;   /* (n_chunks + 1) scratch */
-    double *lam_p;       /* (1) point-leaf damping value, written by ba_linearize_schur */
-    /* partial blocks: (n_slots, d, d) and (n_batches, L, 2, d) scratch */
-    double *partials, *img_partials;
-    /* back-substitution inputs/outputs */
-    const double* dc; const int32_t* umap; float* dX; double* dX64;
+     * g_p (n_ctracks,3) (R), the point and its enable flag (n_ctracks,4) in fp32 */
+    void *Hpp, *gp;      /* (R) Hpp 16-byte aligned */
+    void *chunk_max;     /* (R) (n_chunks + 1) scratch */
+    void *lam_p;         /* (R) (1) point-leaf damping value, written by ba_linearize_schur */
+    /* partial blocks: (n_slots, d, d) and (n_batches, L, 2, d) scratch (R) */
+    void *partials, *img_partials;
+    /* back-substitution inputs/outputs: dc (R), dX fp32, dX64 (R) */
+    const void* dc; const int32_t* umap; float* dX; void* dX64;
     /* sizes and reductions */
     int64_t n_chunks, n_batches, n_pairs;
     const int32_t *pair_ptr, *pair_src, *img_ptr, *img_src;
-    /* outputs: image-pair blocks of S (n_pairs,d,d), rhs (n_imgs,d), diag(H_cc) (n_imgs,d) */
-    double *S_pairs, *e_img, *dg_img;
+    /* outputs (R): image-pair blocks of S (n_pairs,d,d), rhs (n_imgs,d), diag(H_cc) (n_imgs,d) */
+    void *S_pairs, *e_img, *dg_img;
     /* optional given residuals / IRLS weights, element (obs, k) at r_in[obs*r_s0 + k*r_s1]
      * (the `residuals`, `w_pts` arguments of solve_delta, ba_solver.py:110); NULL = recompute */
     const float *r_in, *w_in;
     int64_t r_s0, r_s1, w_s0, w_s1;
     float* ct_pt;         /* (n_ctracks,4) scratch written by stage 0: x, y, z, enable */
     int64_t n_ctracks;
-    double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0) */
+    double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0), fp64 in
+                             both precisions (the Jacobian core is evaluated in fp64) */
     const int32_t *chunk_slots, *chunk_ent, *chunk_eptr;   /* plan: MFMA entry lists of every chunk */
     const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
-    double* pfac;         /* (n_ctracks,12) 16-byte aligned scratch written by stage 0: Cholesky factor L of H_pp + lam_p I
-                             (upper storage), w = L^-1 g_p, reciprocal pivots */
+    void* pfac;           /* (R) (n_ctracks,12) 16-byte aligned scratch written by stage 0: Cholesky factor L of H_pp +
+                             lam_p I (upper storage), w = L^-1 g_p, reciprocal pivots */
     const int32_t* b_order;  /* plan: batches in dispatch order (most expensive first); NULL = 0, 1, ... */
     int32_t* work_ctr;       /* 1 int of device scratch: the camera-pair kernel's batch queue (one
                                 workgroup per CU); NULL = one workgroup per batch */
-    const double* dc_img;    /* optional (n_imgs, d): delta_c at image level (dc[umap], 0 where umap is
+    const void* dc_img;      /* optional (R) (n_imgs, d): delta_c at image level (dc[umap], 0 where umap is
                                 -1), read by the back-substitution instead of dc through umap */
+    /* 0: every (R) array is fp64 (the reference's dtype=torch.float64 solver, engine.py:490); 1: fp32 (its
+     * dtype=torch.float32 default, ba_solver.py:22, :37, :128): the Jacobian core and the weighted rows of
+     * an observation are evaluated in fp64 and rounded, every product, sum and factor after them is fp32 */
+    int32_t real32;
 } ba_lin_args;
 
 /* Stages 1-3: point blocks, camera-pair Schur blocks, rhs and diag(H_cc) at image level.

@@ -641,23 +641,27 @@ def test_two_masks_of_equal_size_on_one_plan():
     assert len(plans) == 1
 
 
-@pytest.mark.parametrize('cfg,nf,nt,kw', [(0, 8, 300, {}), (2, 24, 800, {}), (3, 24, 600, {}), (4, 12, 300, {}),
-                                           (2, 16, 300, dict(n_channels=16))], ids=['cfg0', 'cfg2', 'cfg3', 'cfg4', 'd25'])
-def test_reduced_system_fp32(cfg, nf, nt, kw):
+@pytest.mark.parametrize('cfg,nf,nt,kw,path', [(0, 8, 300, {}, 'pairmajor'), (0, 8, 300, {}, 'batched'),
+                                                (2, 24, 800, {}, 'pairmajor'), (2, 24, 800, {}, 'batched'),
+                                                (3, 24, 600, {}, 'pairmajor'), (4, 12, 300, {}, 'pairmajor'),
+                                                (4, 12, 300, {}, 'batched'), (2, 16, 300, dict(n_channels=16), 'pairmajor')],
+                         ids=['cfg0-pm', 'cfg0-batched', 'cfg2-pm', 'cfg2-batched', 'cfg3-pm', 'cfg4-pm', 'cfg4-batched',
+                              'd25-pm'])
+def test_reduced_system_fp32(cfg, nf, nt, kw, path):
     """dtype=torch.float32, the reference's GaussNewtonSolver default (bs:22: fp32 Jacobian, fp32 normal
-    equations and Schur algebra, bs:37, :128): the pair-major pass in fp32 (fp32 sums, point factors and
+    equations and Schur algebra, bs:37, :128): the pass in fp32 on either path (fp32 sums, point factors and
     16x16x4 fp32 MFMA tiles) gives S, the rhs and the point blocks within 5x (at least 1e-5) of the distance
     of the oracle's own fp32 algebra from the fp64 result, i.e. no less accurate than the reference's
     fp32 path."""
-    print(f'fp32 reduced system cfg {cfg} {kw}', flush=True)
+    print(f'fp32 reduced system cfg {cfg} {kw} {path}', flush=True)
     p = make_problem(cfg, n_frames=nf, n_tracks=nt, **kw)
     flags = _cfg_flags(p)
     ne64, g64, _, _, _, _ = _oracle_ne(p, **flags)
     ne32, g32, _, _, _, _ = _oracle_ne(p, dtype=torch.float32, **flags)
     S64, rhs64 = osol.dense_schur(ne64), osol.reduced_rhs(ne64, g64)
     S32, rhs32 = osol.dense_schur(ne32).double(), osol.reduced_rhs(ne32, g32).double()
-    gs, delta, _ = _gpu_solver(p, dtype=torch.float32, **flags)
-    assert gs.last['path'] == 'pairmajor' and gs.last['S_pairs'].dtype == torch.float32
+    gs, delta, _ = _gpu_solver(p, path=path, dtype=torch.float32, **flags)
+    assert gs.last['path'] == path and gs.last['S_pairs'].dtype == torch.float32
     assert delta.dtype == torch.float32 and bool(torch.isfinite(delta).all())
     S, rhs = gs.reduced_system_dense()
     for name, dev, ref, orc in (('S', S.cpu(), S64, S32), ('rhs', rhs.cpu(), rhs64, rhs32)):
@@ -694,7 +698,8 @@ def test_lm_step_default_dtype_is_the_fp32_solver(cfg, nf, nt):
     info = {}
     up_g, st_g, _ = gpu_engine._lm_step(**_gpu(p).lm_inputs(), **kw, info=info)
     gs = info['solver']
-    assert gs.dtype == torch.float32 and gs.last['path'] == 'pairmajor'
+    assert gs.dtype == torch.float32 and gs.last['S_pairs'].dtype == torch.float32
+    print(f"  path {gs.last['path']}", flush=True)
     inp = p.lm_inputs()
     _, st_o, info_o = oeng.lm_step(**inp, **kw)
     assert info_o['delta'].dtype == torch.float32 and info_o['ne'].leaves['foc'].dtype == torch.float32
@@ -730,12 +735,12 @@ def test_lm_step_default_dtype_is_the_fp32_solver(cfg, nf, nt):
 
 
 def test_fp32_solver_limits():
-    """The fp32 solver runs on the pair-major path only: the batched path and the direct (fp64) Cholesky
-    refuse dtype=torch.float32 with an error instead of running in another precision; other dtypes are
-    refused too."""
-    for kw in (dict(path='batched'), dict(solver='cholesky')):
-        with pytest.raises(ValueError, match='float64'):
-            GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float32, **kw)
+    """The direct (fp64) Cholesky refuses dtype=torch.float32 with an error instead of running in another
+    precision; other dtypes are refused too; both passes take fp32."""
+    with pytest.raises(ValueError, match='float64'):
+        GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float32, solver='cholesky')
+    for path in ('batched', 'pairmajor', 'auto'):
+        assert GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float32, path=path).real32
     with pytest.raises(ValueError, match='dtype'):
         GaussNewtonSolver(1, 4, 4, 10, DEV, dtype=torch.float16)
     assert GaussNewtonSolver(1, 4, 4, 10, DEV).dtype == torch.float32
@@ -1172,8 +1177,8 @@ def test_reduced_system_full_size_against_oracle(cfg, path, dtype):
     fixed, 8.0 M observations, batched): the reduced rhs, the point blocks and S v for seeded v against
     the oracle's normal equations at the same size and with the configuration's own flags (the oracle's
     pass takes seconds on the host's threads), to the 1e-5 bar; also with dtype=torch.float32 (the
-    reference's default solver precision: the pair-major pass in fp32 throughout), against the same
-    fp64 normal equations and bar (measured 3.6e-6 / 2.7e-6 on S v at configs 2 / 3)."""
+    reference's default solver precision: the pass in fp32 throughout, batched at config 2 and pair-major
+    at config 3), against the same fp64 normal equations and bar."""
     import os
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     p = make_problem(cfg)
@@ -1182,7 +1187,7 @@ def test_reduced_system_full_size_against_oracle(cfg, path, dtype):
     flags = _cfg_flags(p)
     gs, _, _ = _gpu_solver(p, path=path, dtype=dtype, **flags)
     last = gs.last
-    batched = (cfg, path) in ((2, 'auto'), (4, 'auto')) and dtype == torch.float64
+    batched = (cfg, path) in ((2, 'auto'), (4, 'auto'))
     assert last['path'] == ('batched' if batched else 'pairmajor') and last['S_pairs'].dtype == dtype
     um, d, plan = last['unknowns'], last['lay']['d'], last['plan']
     rhs = last['rhs'].double().cpu()
