@@ -442,7 +442,7 @@ class GaussNewtonSolver:
         a.yrun = ptr(ws('yrun', (max(sc['n_runs'], 1), 3), R))
         a.Hpp, a.gp, a.lam_p = ptr(Hpp), ptr(gp), ptr(lam_p)
         a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), R))
-        a.pfac = ptr(ws('pfac', (max(T, 1), 12), R))
+        a.pfac = ptr(ws('pfac', (max(T, 1), 16), R))     # the pair-major factor record, point included
         a.V = ptr(ws('V', (max(sc['n_runs'], 1), 3, dp), R))
         a.S_pairs, a.e_img, a.dg_img = ptr(S_pairs), ptr(e_img), ptr(dg_img)
         W = w_pts.expand(-1, 3)

@@ -1220,12 +1220,10 @@ __device__ __forceinline__ void pm_core(const PmArgs& a, int o, const ObsCtx& c,
     xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
 }
 
-// The Jacobian core of observation o with the sqrt(W) k_pm_obs stored for it (no residual, no
-// IRLS weights: the run pass needs neither).
-__device__ __forceinline__ void pm_jcore(const PmArgs& a, int o, const ObsCtx& c, ObsCore& oc, DepSrc& dep,
-                                         bool& xon) {
-    const int pid = a.pids[o];
-    const float X[3] = {a.pts3d[3 * (int64_t)pid], a.pts3d[3 * (int64_t)pid + 1], a.pts3d[3 * (int64_t)pid + 2]};
+// The Jacobian core of observation o of track t (point X, from the track's factor record) with the
+// sqrt(W) k_pm_obs stored for it (no residual, no IRLS weights: the run pass needs neither).
+__device__ __forceinline__ void pm_jcore(const PmArgs& a, int o, int t, const float X[3], const ObsCtx& c, ObsCore& oc,
+                                         DepSrc& dep, bool& xon) {
     const float2 sv = reinterpret_cast<const float2*>(a.pix2d_std)[o];
     load_dep(dep, a.pix2d_dep + (int64_t)o * a.lay.C, a.lay.C);
     double gd = 0.0;
@@ -1235,7 +1233,7 @@ __device__ __forceinline__ void pm_jcore(const PmArgs& a, int o, const ObsCtx& c
     eval_jac_core(c.cp, X, sv.x, sv.y, gd, a.hp.is_depth_log, oc.J);
     const float4 w = reinterpret_cast<const float4*>(a.wobs)[o];
     oc.sW[0] = w.x; oc.sW[1] = w.y; oc.sW[2] = w.z;
-    xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
+    xon = (a.enX ? a.enX[t] != 0 : true) && !a.lay.x_off;
 }
 
 // Weighted camera-row element (R, j) of an observation (the element emit_jc_row hands its sink).
@@ -1377,16 +1375,17 @@ __global__ void __launch_bounds__(64 * PmObsWaves<Real>::N, 3) k_pm_obs(PmArgs a
             double Jp[3][3], gP[3];
             point_rows<true>(oc, c.cp, xon, Jp, gP);
             const int pr[6][2] = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 2}};
-            Real* q = (Real*)a.pobs + 9 * o;           // streamed out, as wobs (read by later passes)
+            // plain stores: a store instruction covers only part of each line of these 9-value rows,
+            // which the L2 then completes (non-temporal, the kernel took 5% longer at config 3 in fp64)
+            Real* q = (Real*)a.pobs + 9 * o;
 #pragma unroll
             for (int k = 0; k < 6; ++k) {
                 const int i = pr[k][0], j = pr[k][1];
-                __builtin_nontemporal_store((Real)(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j]),
-                                            q + k);
+                q[k] = (Real)(Jp[0][i] * Jp[0][j] + Jp[1][i] * Jp[1][j] + Jp[2][i] * Jp[2][j]);
             }
-            __builtin_nontemporal_store((Real)gP[0], q + 6);
-            __builtin_nontemporal_store((Real)gP[1], q + 7);
-            __builtin_nontemporal_store((Real)gP[2], q + 8);
+            q[6] = (Real)gP[0];
+            q[7] = (Real)gP[1];
+            q[8] = (Real)gP[2];
             typedef float f4 __attribute__((ext_vector_type(4)));
             const f4 wv4 = {(float)oc.sW[0], (float)oc.sW[1], (float)oc.sW[2], 0.f};
             __builtin_nontemporal_store(wv4, reinterpret_cast<f4*>(a.wobs) + o);
@@ -1445,11 +1444,47 @@ __global__ void __launch_bounds__(PM_T) k_pm_track(PmArgs a) {
     if (threadIdx.x == 0) ((Real*)a.tmax)[blockIdx.x] = sm[0];
 }
 
+// Per track: the point block's factor record of the pair-major passes, PM_PF values per track in the
+// working precision, so that one aligned line (fp64) or half line (fp32) holds all a run reads:
+//   0-2 L1 L2 L4 | 3-5 1/L0 1/L3 1/L5 | 6-8 w = L^-1 g_p | 9-11 the point X | 12-14 L0 L3 L5 | 15 zero
+// (L the chol3x3_solve factor of H_pp + lam_p I).  The runs gather it by track, once each; with the
+// point inside, they do not gather pts3d as well.
+#define PM_PF 16
+template <typename Real>
+__global__ void __launch_bounds__(256) k_pm_factor(PmArgs a, const Real* __restrict__ lam_p) {
+    typedef Real R2 __attribute__((ext_vector_type(2)));
+    constexpr int NV = PM_PF / 2, STR = NV + 1;         // 16-byte vectors per record; LDS row stride
+    __shared__ R2 rec[256 * STR];
+    const int64_t t0 = (int64_t)blockIdx.x * 256, t = t0 + threadIdx.x;
+    const int nt = (int)min((int64_t)256, a.n_tracks - t0);
+    if (t < a.n_tracks) {
+        const R2* h2 = reinterpret_cast<const R2*>((const Real*)a.Hpp + 6 * t);     // 16-byte aligned rows (fp64)
+        Real H[6], Lf[6];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) { const R2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
+        chol3_factor(H, lam_p[0], Lf);
+        const Real* gp = (const Real*)a.gp + 3 * t;
+        const Real r0 = Real(1) / Lf[0], r1 = Real(1) / Lf[3], r2 = Real(1) / Lf[5];
+        const Real w0 = gp[0] * r0;
+        const Real w1 = (gp[1] - Lf[1] * w0) * r1;
+        const Real w2 = (gp[2] - Lf[2] * w0 - Lf[4] * w1) * r2;
+        const float* X = a.pts3d + 3 * t;
+        R2* o = rec + threadIdx.x * STR;
+        o[0] = (R2){Lf[1], Lf[2]}; o[1] = (R2){Lf[4], r0}; o[2] = (R2){r1, r2}; o[3] = (R2){w0, w1};
+        o[4] = (R2){w2, (Real)X[0]}; o[5] = (R2){(Real)X[1], (Real)X[2]};
+        o[6] = (R2){Lf[0], Lf[3]}; o[7] = (R2){Lf[5], Real(0)};
+    }
+    __syncthreads();
+    // the block's records leave as one contiguous range, 16 bytes per lane and store
+    R2* dst = reinterpret_cast<R2*>((Real*)a.pfac + PM_PF * t0);
+    for (int e = threadIdx.x; e < nt * NV; e += 256) dst[e] = rec[(e / NV) * STR + e % NV];
+}
+
 // Per run (one wave per PM_SPAN runs, 64 at a time): V = sum over the run's observations of
 // sum_R jc_R (L^-1 jp_R)^T (= (sum J_c^T J_p) L^-T), staged in LDS with L^-1 g_p in column d,
 // summed per image (-X^T X) into the V slots and copied to V (run-major, 3 x DP per run).
 template <int HK, int HP, int DP, typename Real>
-__global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
+__global__ void __launch_bounds__(64, 2) k_pm_runs(PmArgs a) {
     __shared__ Real X[192][DP + 1];
     __shared__ int simg[64];
     const int lane = threadIdx.x;
@@ -1459,25 +1494,39 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
     PmTileAcc<DP, Real> T;
     T.img = -1;
     T.zero();
+    // a round's run indices are requested one round ahead (its first observation's index at the end of
+    // the round before), so a round starts with its factor and observation loads
+    int n_img = -1, n_t = 0, n_q0 = 0, n_q1 = 0, n_o0 = 0;
+    auto fetch_idx = [&](int64_t r) {
+        n_img = -1;
+        if (r < r_end) { n_img = a.run_img[r]; n_t = a.run_trk[r]; n_q0 = a.run_ptr[r]; n_q1 = a.run_ptr[r + 1]; }
+    };
+    fetch_idx(r_begin + lane);
+    if (n_img >= 0) n_o0 = a.run_obs[n_q0];
     for (int64_t base = r_begin; base < r_end; base += 64) {
-        const int64_t r = base + lane;
-        int img = -1;
-        if (r < r_end) {
-            img = a.run_img[r];
-            const int t = a.run_trk[r];
+        const int img = n_img, t = n_t, q0 = n_q0, q1 = n_q1, o0 = n_o0;
+        fetch_idx(base + 64 + lane);
+        if (img >= 0) {
             ObsCtx c;
             pm_ctx(a, img, c);
             const double mK = c.enK ? 1.0 : 0.0, mP = c.enP ? 1.0 : 0.0;
             const bool zon = a.lay.hasZ && c.enZ;
-            const Real* pf = (const Real*)a.pfac + 12 * (int64_t)t;
-            const Real L1 = pf[1], L2 = pf[2], L4 = pf[4], i0 = pf[9], i1 = pf[10], i2 = pf[11];
-            const int q0 = a.run_ptr[r], q1 = a.run_ptr[r + 1];
+            typedef Real R4 __attribute__((ext_vector_type(4)));
+            const R4* pf = reinterpret_cast<const R4*>((const Real*)a.pfac + PM_PF * (int64_t)t);
+            const R4 f0 = pf[0], f1 = pf[1], f2 = pf[2];
+            const Real L1 = f0.x, L2 = f0.y, L4 = f0.z, i0 = f0.w, i1 = f1.x, i2 = f1.y;
+            const float Xp[3] = {(float)f2.y, (float)f2.z, (float)f2.w};
+            // column d: L^-1 g_p, stored first (the column loops skip it), so that its registers are free
+            // during the loops (the fp64 kernel stays within 256 VGPRs without spills)
+            X[3 * lane][d] = f1.z;
+            X[3 * lane + 1][d] = f1.w;
+            X[3 * lane + 2][d] = f2.x;
             for (int q = q0; q < q1; ++q) {
-                const int o = a.run_obs[q];
+                const int o = q == q0 ? o0 : a.run_obs[q];
                 ObsCore oc;
                 DepSrc dep;
                 bool xon;
-                pm_jcore(a, o, c, oc, dep, xon);
+                pm_jcore(a, o, t, Xp, c, oc, dep, xon);
                 double Jp[3][3], gP[3];
                 point_rows<false>(oc, c.cp, xon, Jp, gP);
                 Real wv[3][3];                       // L^-1 jp_R, R = 0..2
@@ -1498,6 +1547,7 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
                 if (q == q0) {
 #pragma unroll
                     for (int j = 0; j < DP; ++j) {
+                        if (j == d) continue;
                         Real v[3];
                         col(j, v);
 #pragma unroll
@@ -1506,6 +1556,7 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
                 } else {                             // several observations of the track in this image
 #pragma unroll
                     for (int j = 0; j < DP; ++j) {
+                        if (j == d) continue;
                         Real v[3];
                         col(j, v);
 #pragma unroll
@@ -1513,9 +1564,8 @@ __global__ void __launch_bounds__(64) k_pm_runs(PmArgs a) {
                     }
                 }
             }
-#pragma unroll
-            for (int k = 0; k < 3; ++k) X[3 * lane + k][d] = pf[6 + k];
         }
+        if (n_img >= 0) n_o0 = a.run_obs[n_q0];
         simg[lane] = img;
         __syncthreads();
         T.add_round(X, simg, Real(-1), (Real*)a.vslots, w, lane);
@@ -1701,11 +1751,11 @@ __global__ void __launch_bounds__(PM_T) k_pm_backsub(PmArgs a) {
         const Real* y = (const Real*)a.yrun + 3 * (int64_t)a.trk_run[q];
         s0 += y[0]; s1 += y[1]; s2 += y[2];
     }
-    const Real* pf = (const Real*)a.pfac + 12 * t;
+    const Real* pf = (const Real*)a.pfac + PM_PF * t;       // the k_pm_factor record
     const Real z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
-    const Real x2 = z2 * pf[11];
-    const Real x1 = (z1 - pf[4] * x2) * pf[10];
-    const Real x0 = (z0 - pf[1] * x1 - pf[2] * x2) * pf[9];
+    const Real x2 = z2 * pf[5];
+    const Real x1 = (z1 - pf[2] * x2) * pf[4];
+    const Real x0 = (z0 - pf[0] * x1 - pf[1] * x2) * pf[3];
     a.dX[3 * t] = (float)x0; a.dX[3 * t + 1] = (float)x1; a.dX[3 * t + 2] = (float)x2;
     if (a.dX64) {
         Real* o = (Real*)a.dX64;
@@ -1768,8 +1818,7 @@ static void pm_stage(const ba_pm_args& a, int stage, hipStream_t st) {
     hipLaunchKernelGGL(k_lam_final<Real>, dim3(1), dim3(1), 0, st, tmax, nbt, a.lay.dampen, a.lay.adaptive,
                        a.lay.x_off, lam_p);
     if (a.n_tracks > 0)
-        hipLaunchKernelGGL(k_point_factor<Real>, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, (const Real*)a.Hpp,
-                           (const Real*)a.gp, (const Real*)lam_p, (int64_t)a.n_tracks, (Real*)a.pfac);
+        hipLaunchKernelGGL(k_pm_factor<Real>, dim3(nblk(a.n_tracks, 256)), dim3(256), 0, st, a, (const Real*)lam_p);
     if (a.n_runs > 0) {
         const unsigned g = (unsigned)((a.n_runs + PM_SPAN - 1) / PM_SPAN);
         BA_DISPATCH_KP(a.lay, {
@@ -1815,8 +1864,8 @@ extern "C" int ba_pm_linearize_stage(const ba_pm_args* args, int stage, void* st
     BA_REQUIRE(a.n_obs < ((int64_t)1 << 31) && a.n_runs <= a.n_obs, "bad observation / run counts");
     const char* miss = pm_missing(a, false);
     BA_REQUIRE(miss == nullptr, miss);
-    BA_REQUIRE((((uintptr_t)a.pfac | (uintptr_t)a.Hpp | (uintptr_t)a.wobs) & 15) == 0,
-               "Hpp, pfac and wobs must be 16-byte aligned");
+    BA_REQUIRE((((uintptr_t)a.Hpp | (uintptr_t)a.wobs) & 15) == 0, "Hpp and wobs must be 16-byte aligned");
+    BA_REQUIRE(((uintptr_t)a.pfac & (a.real32 ? 15 : 31)) == 0, "pfac must be 32-byte aligned (16 in fp32)");
     if (a.real32) pm_stage<float>(a, stage, st);
     else          pm_stage<double>(a, stage, st);
     BA_LAUNCHED();

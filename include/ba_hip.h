@@ -237,7 +237,8 @@ typedef struct {
     void *Hpp, *gp;                          /* (R) (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
     void* tmax;                              /* (R) (ceil(n_tracks / 256) + 1) */
     void* lam_p;                             /* (R) (1) point-leaf damping value */
-    void* pfac;                              /* (R) (n_tracks, 12) 16-byte aligned: L, L^-1 g_p, reciprocal pivots */
+    void* pfac;                              /* (R) (n_tracks, 16) 32-byte aligned (16 in fp32): L, L^-1 g_p, reciprocal
+                                              * pivots and the point, per track */
     void* V;                                 /* (R) (n_runs, 3, dp), dp = 16 for d <= 15 else 32 */
     /* outputs (R): (n_pairs, d, d), (n_imgs, d), (n_imgs, d) */
     void *S_pairs, *e_img, *dg_img;
