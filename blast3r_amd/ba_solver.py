@@ -439,7 +439,6 @@ class GaussNewtonSolver:
         nsl = lambda n: int(lib().ba_pm_slot_doubles(n, n_imgs, d))
         a.jslots = ptr(ws('jslots', (max(nsl(n_obs), 1),), R))
         a.vslots = ptr(ws('vslots', (max(nsl(sc['n_runs']), 1),), R))
-        a.yrun = ptr(ws('yrun', (max(sc['n_runs'], 1), 3), R))
         a.Hpp, a.gp, a.lam_p = ptr(Hpp), ptr(gp), ptr(lam_p)
         a.tmax = ptr(ws('tmax', ((T + 255) // 256 + 1,), R))
         a.pfac = ptr(ws('pfac', (max(T, 1), 16), R))     # the pair-major factor record, point included

@@ -217,35 +217,35 @@ __global__ void __launch_bounds__(PCG_T) k_pcg_init2(ba_pcg_args a, int nb) {
 // B = S(i, i2) with B[j][j2] at S_rows[q][j2 * d + j], so that the SpMV's lanes (one per output
 // row j) read each column of a block contiguously.  S(i, i2) is S_p for tr = 0 and S_p^T for tr = 1.
 // row_u[q][j2] = umap[i2][j2] (-1 past d, gw entries per block: 16 for d <= 16, else 32): the unknowns
-// the block multiplies.  One thread per (entry, element), max(d^2, gw) elements per entry.
+// the block multiplies.  One wave per destination entry (its d^2 elements and gw unknowns over the
+// lanes), so that the entry's indices are resolved once per wave.
 template <typename Real>
-__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int per, int gw) {
+__global__ void __launch_bounds__(PCG_T) k_rows_build(ba_pcg_args a, int64_t n_ent, int gw) {
     const PcgV<Real> av(a);
     const int d = a.d, dd = d * d;
-    const int64_t tid = (int64_t)blockIdx.x * PCG_T + threadIdx.x;
-    if (tid >= n_ent * per) return;
-    const int64_t q = tid / per;                       // destination block
-    const int e = (int)(tid - q * per);
+    const int64_t q = (int64_t)blockIdx.x * (PCG_T / 64) + (threadIdx.x >> 6);      // destination block
+    if (q >= n_ent) return;
+    const int lane = threadIdx.x & 63;
     int64_t qs = q;                                    // its source entry of row_ent
     if (a.row_cap > 0) {                               // fixed capacity: row i at [i cap, (i + 1) cap)
         const int64_t i = q / a.row_cap, k = q - i * a.row_cap;
         qs = a.row_ptr[i] + k;
         if (qs >= a.row_ptr[i + 1]) {                  // past the row's end: a zero block, no unknowns
-            if (e < dd) av.S_rows[q * dd + e] = Real(0);
-            if (e < gw) a.row_u[q * gw + e] = -1;
+            for (int e = lane; e < dd; e += 64) av.S_rows[q * dd + e] = Real(0);
+            if (lane < gw) a.row_u[q * gw + lane] = -1;
             return;
         }
     }
     const int ent = a.row_ent[qs];
     const int64_t p = ent >> 1;
-    if (e < dd) {
-        const int j2 = e / d, j = e - (e / d) * d;
-        const Real* S = av.S_pairs + p * dd;
+    const Real* S = av.S_pairs + p * dd;
+    for (int e = lane; e < dd; e += 64) {
+        const int j2 = e / d, j = e - j2 * d;
         av.S_rows[q * dd + e] = (ent & 1) ? S[j2 * d + j] : S[j * d + j2];
     }
-    if (e < gw) {
+    if (lane < gw) {
         const int i2 = (ent & 1) ? a.pair_i1[p] : a.pair_i2[p];
-        a.row_u[q * gw + e] = e < d ? a.umap[(int64_t)i2 * d + e] : -1;
+        a.row_u[q * gw + lane] = lane < d ? a.umap[(int64_t)i2 * d + lane] : -1;
     }
 }
 
@@ -530,11 +530,10 @@ template <typename Real>
 static void pcg_launch(const ba_pcg_args& a, int32_t it0, int32_t it1, int32_t finish, int32_t* stopped_out,
                        int64_t n_ent, unsigned nb, unsigned nbw, hipStream_t st) {
     const int gw = a.d <= 16 ? 16 : 32;               // lanes per block row group of the SpMV (row_u stride)
-    const int per = a.d * a.d > gw ? a.d * a.d : gw;
     if (it0 == 0) {                                  // the setup precedes iteration 0
         if (n_ent > 0)
-            hipLaunchKernelGGL(k_rows_build<Real>, dim3((unsigned)((n_ent * per + PCG_T - 1) / PCG_T)), dim3(PCG_T), 0,
-                               st, a, n_ent, per, gw);
+            hipLaunchKernelGGL(k_rows_build<Real>, dim3((unsigned)((n_ent + PCG_T / 64 - 1) / (PCG_T / 64))),
+                               dim3(PCG_T), 0, st, a, n_ent, gw);
         hipLaunchKernelGGL(k_unk_setup<Real>, dim3(nbw), dim3(PCG_T), 0, st, a);
         hipLaunchKernelGGL(k_leaf_max<Real>, dim3(nb), dim3(PCG_T), 0, st, a);
         hipLaunchKernelGGL(k_leaf_damp<Real>, dim3(nb), dim3(PCG_T), 0, st, a);

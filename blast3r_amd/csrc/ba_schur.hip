@@ -1714,45 +1714,55 @@ __global__ void __launch_bounds__(PM_T) k_pm_pairs(PmArgs a) {
             }
 }
 
-// per run row: y = V_r[k] . delta_c(image of r), DP lanes per row (coalesced over V)
+// per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i)), DP lanes per track
+// (lane c holds column c of the run's three V rows, so every V load is coalesced over the group): per
+// run, the three products summed over the DP lanes by an xor tree, then added over the track's runs in
+// trk_run order; lane 0 then solves with the k_pm_factor record.  Two runs per step: the run ids two
+// steps ahead and their images one step ahead are requested early, so that a step's V rows and delta_c
+// are requested together.
 template <int DP, typename Real>
-__global__ void __launch_bounds__(256) k_pm_yrun(PmArgs a) {
-    // one thread per (run, column): the run's image and delta_c entry are read once for its three V rows
-    // (each row's DP columns on DP neighbouring lanes, so every V load is coalesced), and the products
-    // are summed over the DP lanes by the same xor tree for each row
+__global__ void __launch_bounds__(256) k_pm_backsub(PmArgs a) {
     const int d = a.lay.d;
-    const int col = threadIdx.x % DP;
-    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t - (threadIdx.x & 63) < a.n_runs * DP;
-         t += (int64_t)gridDim.x * 256) {
-        const int64_t r = t / DP;
-        const bool live = r < a.n_runs;
-        Real v[3] = {Real(0), Real(0), Real(0)};
-        if (live && col < d) {
-            const Real dc = ((const Real*)a.dc_img)[(int64_t)a.run_img[r] * d + col];
-            const Real* V = (const Real*)a.V + r * 3 * DP + col;
+    const int c = threadIdx.x % DP;
+    const int64_t t = (int64_t)blockIdx.x * (256 / DP) + threadIdx.x / DP;
+    const bool live = t < a.n_tracks;
+    const int q0 = live ? a.trk_run_ptr[t] : 0, q1 = live ? a.trk_run_ptr[t + 1] : 0;
+    Real s[3] = {Real(0), Real(0), Real(0)};
+    auto run_at = [&](int q) { return q < q1 ? a.trk_run[q] : -1; };
+    auto img_of = [&](int r) { return r >= 0 ? a.run_img[r] : 0; };
+    int ra = run_at(q0), rb = run_at(q0 + 1);
+    int ia = img_of(ra), ib = img_of(rb);
+    int rc = run_at(q0 + 2), rd = run_at(q0 + 3);
+    auto prod = [&](int r, int img, Real (&v)[3]) {
+        v[0] = v[1] = v[2] = Real(0);
+        if (r >= 0 && c < d) {
+            const Real dc = ((const Real*)a.dc_img)[(int64_t)img * d + c];
+            const Real* V = (const Real*)a.V + (int64_t)r * 3 * DP + c;
 #pragma unroll
             for (int k = 0; k < 3; ++k) v[k] = V[k * DP] * dc;
         }
+    };
+    for (int q = q0; q < q1; q += 2) {
+        Real va[3], vb[3];
+        prod(ra, ia, va);
+        prod(rb, ib, vb);
+        ra = rc; rb = rd;
+        ia = img_of(ra); ib = img_of(rb);
+        rc = run_at(q + 4); rd = run_at(q + 5);
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
+        for (int k = 0; k < 3; ++k) {
 #pragma unroll
-            for (int m = DP / 2; m >= 1; m >>= 1) v[k] += __shfl_xor(v[k], m);
-        if (live && col < 3) ((Real*)a.yrun)[3 * r + col] = col == 0 ? v[0] : (col == 1 ? v[1] : v[2]);
+            for (int m = DP / 2; m >= 1; m >>= 1) {
+                va[k] += __shfl_xor(va[k], m);
+                vb[k] += __shfl_xor(vb[k], m);
+            }
+            s[k] += va[k];
+            if (q + 1 < q1) s[k] += vb[k];
+        }
     }
-}
-
-// per track: delta_p = L^-T (L^-1 g_p - sum over its runs of V_ti^T delta_c(i))
-template <typename Real>
-__global__ void __launch_bounds__(PM_T) k_pm_backsub(PmArgs a) {
-    const int64_t t = (int64_t)blockIdx.x * PM_T + threadIdx.x;
-    if (t >= a.n_tracks) return;
-    Real s0 = Real(0), s1 = Real(0), s2 = Real(0);
-    for (int q = a.trk_run_ptr[t]; q < a.trk_run_ptr[t + 1]; ++q) {
-        const Real* y = (const Real*)a.yrun + 3 * (int64_t)a.trk_run[q];
-        s0 += y[0]; s1 += y[1]; s2 += y[2];
-    }
+    if (!live || c != 0) return;
     const Real* pf = (const Real*)a.pfac + PM_PF * t;       // the k_pm_factor record
-    const Real z0 = pf[6] - s0, z1 = pf[7] - s1, z2 = pf[8] - s2;
+    const Real z0 = pf[6] - s[0], z1 = pf[7] - s[1], z2 = pf[8] - s[2];
     const Real x2 = z2 * pf[5];
     const Real x1 = (z1 - pf[2] * x2) * pf[4];
     const Real x0 = (z0 - pf[0] * x1 - pf[1] * x2) * pf[3];
@@ -1768,7 +1778,7 @@ static const char* pm_missing(const ba_pm_args& a, bool backsub) {
     const bool C = a.lay.C > 0;
     BA_NEED(true, a.trk_run_ptr); BA_NEED(true, a.trk_run); BA_NEED(true, a.run_img); BA_NEED(true, a.V);
     BA_NEED(true, a.pfac);
-    BA_NEED(backsub, a.dc_img); BA_NEED(backsub, a.dX); BA_NEED(backsub, a.yrun);
+    BA_NEED(backsub, a.dc_img); BA_NEED(backsub, a.dX);
     if (backsub) return nullptr;
     BA_NEED(true, a.jslots); BA_NEED(true, a.vslots); BA_NEED(true, a.wobs);
     BA_NEED(true, a.infos); BA_NEED(true, a.run_ptr); BA_NEED(true, a.run_obs); BA_NEED(true, a.run_trk);
@@ -1832,14 +1842,10 @@ static void pm_stage(const ba_pm_args& a, int stage, hipStream_t st) {
 
 template <typename Real>
 static void pm_backsub(const ba_pm_args& a, hipStream_t st) {
-    if (a.n_runs > 0) {
-        const int dp = a.lay.d > 15 ? 32 : 16;
-        const int64_t n_th = a.n_runs * dp;      // one thread per (run, column)
-        const unsigned g = (unsigned)std::min<int64_t>((n_th + 255) / 256, 1 << 22);
-        if (dp == 32) hipLaunchKernelGGL((k_pm_yrun<32, Real>), dim3(g), dim3(256), 0, st, a);
-        else          hipLaunchKernelGGL((k_pm_yrun<16, Real>), dim3(g), dim3(256), 0, st, a);
-    }
-    hipLaunchKernelGGL(k_pm_backsub<Real>, dim3(nblk(a.n_tracks, PM_T)), dim3(PM_T), 0, st, a);
+    if (a.lay.d > 15)
+        hipLaunchKernelGGL((k_pm_backsub<32, Real>), dim3(nblk(a.n_tracks, 256 / 32)), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_pm_backsub<16, Real>), dim3(nblk(a.n_tracks, 256 / 16)), dim3(256), 0, st, a);
 }
 
 // elements (of the working precision) of one slot array

@@ -233,7 +233,7 @@ typedef struct {
     void* pobs;                              /* (R) (n_obs, 9) */
     float* wobs;                             /* (n_obs, 4) 16-byte aligned: sqrt(W) per residual row */
     void *jslots, *vslots;                   /* (R) per-wave image sums: ba_pm_slot_doubles(n_obs | n_runs, n_imgs, d) */
-    void* yrun;                              /* (R) (n_runs, 3) back-substitution: V_r^T delta_c per run */
+    void* yrun;                              /* unused (may be NULL): kept so that the layout stays the same */
     void *Hpp, *gp;                          /* (R) (n_tracks, 6) 16-byte aligned, (n_tracks, 3) */
     void* tmax;                              /* (R) (ceil(n_tracks / 256) + 1) */
     void* lam_p;                             /* (R) (1) point-leaf damping value */
