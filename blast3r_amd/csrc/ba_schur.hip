@@ -399,21 +399,28 @@ template <typename R>
 __global__ void __launch_bounds__(256) k_point_factor(const R* __restrict__ Hpp, const R* __restrict__ gp,
                                                       const R* __restrict__ lam_p, int64_t n_ct, R* __restrict__ pf) {
     typedef R R2 __attribute__((ext_vector_type(2)));
-    const int64_t ct = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (ct >= n_ct) return;
-    R H[6], Lf[6];
-    const R2* h2 = reinterpret_cast<const R2*>(Hpp + 6 * ct);                // 16-byte aligned rows (fp64)
+    __shared__ R2 rec[256 * 7];                        // the block's records, 6 vectors each (+1: row stride)
+    const int64_t ct0 = (int64_t)blockIdx.x * 256, ct = ct0 + threadIdx.x;
+    const int nt = (int)min((int64_t)256, n_ct - ct0);
+    if (ct < n_ct) {
+        R H[6], Lf[6];
+        const R2* h2 = reinterpret_cast<const R2*>(Hpp + 6 * ct);            // 16-byte aligned rows (fp64)
 #pragma unroll
-    for (int k = 0; k < 3; ++k) { const R2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
-    chol3_factor(H, lam_p[0], Lf);
-    const R r0 = R(1) / Lf[0], r1 = R(1) / Lf[3], r2 = R(1) / Lf[5];
-    const R g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
-    const R w0 = g0 * r0;
-    const R w1 = (g1 - Lf[1] * w0) * r1;
-    const R w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
-    R2* o = reinterpret_cast<R2*>(pf + 12 * ct);
-    o[0] = (R2){Lf[0], Lf[1]}; o[1] = (R2){Lf[2], Lf[3]}; o[2] = (R2){Lf[4], Lf[5]};
-    o[3] = (R2){w0, w1}; o[4] = (R2){w2, r0}; o[5] = (R2){r1, r2};
+        for (int k = 0; k < 3; ++k) { const R2 v = h2[k]; H[2 * k] = v.x; H[2 * k + 1] = v.y; }
+        chol3_factor(H, lam_p[0], Lf);
+        const R r0 = R(1) / Lf[0], r1 = R(1) / Lf[3], r2 = R(1) / Lf[5];
+        const R g0 = gp[3 * ct], g1 = gp[3 * ct + 1], g2 = gp[3 * ct + 2];
+        const R w0 = g0 * r0;
+        const R w1 = (g1 - Lf[1] * w0) * r1;
+        const R w2 = (g2 - Lf[2] * w0 - Lf[4] * w1) * r2;
+        R2* o = rec + threadIdx.x * 7;
+        o[0] = (R2){Lf[0], Lf[1]}; o[1] = (R2){Lf[2], Lf[3]}; o[2] = (R2){Lf[4], Lf[5]};
+        o[3] = (R2){w0, w1}; o[4] = (R2){w2, r0}; o[5] = (R2){r1, r2};
+    }
+    __syncthreads();
+    // the block's records leave as one contiguous range, 16 bytes per lane and store
+    R2* dst = reinterpret_cast<R2*>(pf + 12 * ct0);
+    for (int e = threadIdx.x; e < nt * 6; e += 256) dst[e] = rec[(e / 6) * 7 + e % 6];
 }
 
 // ----------------------------------------------------------------------------- camera-pair blocks
