@@ -11,6 +11,7 @@ Tolerances (norm-wise relative, ||gpu - oracle|| / ||oracle||):
     under 1e-15 perturbations of b; the line search then run by the oracle on the device's step:
     the same scales, loss and updated parameters within 1e-5
 """
+import numpy as np
 import pytest
 import torch
 
@@ -390,6 +391,46 @@ def _check_reduced_system(p, path):
     iu = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 2)]
     Hr6 = torch.stack([Hr[:, i, j] for i, j in iu], 1)
     assert rel_err(H, Hr6) < 1e-5
+
+
+def _with_repeats(p, frac=0.15, seed=3):
+    """p with about frac of its observations repeated in their own image (the copy right after the
+    original, so pids stay ascending inside each image), its pixel moved by (0.7, -0.4): runs of two
+    observations of one track in one image, which both fused paths sum into one V per run."""
+    import dataclasses
+    rng = np.random.default_rng(seed)
+    n = p.n_obs
+    rep = rng.random(n) < frac
+    idx = torch.from_numpy(np.repeat(np.arange(n), np.where(rep, 2, 1)))
+    second = torch.zeros(len(idx), dtype=torch.bool)
+    second[1:] = idx[1:] == idx[:-1]
+    cum = p.infos[0].long()
+    start = torch.cat([cum.new_zeros(1), cum[:-1]])
+    img = torch.repeat_interleave(torch.arange(p.n_imgs), cum - start)
+    cnt = torch.bincount(img[idx], minlength=p.n_imgs)
+    infos = p.infos.clone()
+    infos[0] = torch.cumsum(cnt, 0).to(torch.int32)
+    pix = p.pix2d[idx].clone()
+    pix[second] += torch.tensor([0.7, -0.4])
+    return dataclasses.replace(p, infos=infos.contiguous(), pids=p.pids[idx].contiguous(), pix2d=pix.contiguous(),
+                               pix2d_std=p.pix2d_std[idx].contiguous(), pix2d_dep=p.pix2d_dep[idx].contiguous())
+
+
+@pytest.mark.parametrize('cfg,nf,nt,path', [(0, 8, 200, 'batched'), (0, 8, 200, 'pairmajor'), (2, 24, 800, 'batched'),
+                                            (2, 24, 800, 'pairmajor'), (3, 24, 600, 'pairmajor')])
+def test_repeated_observations_in_one_image(cfg, nf, nt, path):
+    """A track observed twice in one image (about 15% of the observations repeated): S, rhs and the point
+    blocks, then the PCG step with its back-substitution, against the oracle on both fused paths (the
+    batched pass sums the run's V into its first slot, the pair-major runs sum their observations in
+    k_pm_runs and k_pm_backsub reads one V per run)."""
+    print(f'repeated observations cfg {cfg} ({nf} frames, {nt} tracks), {path}', flush=True)
+    p = _with_repeats(make_problem(cfg, n_frames=nf, n_tracks=nt))
+    cum = p.infos[0].long()
+    img = torch.repeat_interleave(torch.arange(p.n_imgs), torch.diff(torch.cat([cum.new_zeros(1), cum])))
+    key = img * p.n_tracks + p.pids.long()
+    assert (torch.diff(key) == 0).sum() > 0.1 * p.n_obs     # the repeats are there, next to each other
+    _check_reduced_system(p, path)
+    _check_pcg_step(p, path, cfg)
 
 
 def test_auto_path_on_far_apart_track_images_builds_no_batched_plan():
