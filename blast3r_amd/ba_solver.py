@@ -307,14 +307,18 @@ class GaussNewtonSolver:
         ws = plan.workspace
         n_imgs = self.imgs.true_n
         n_ct = sc['n_ctracks']
-        R = self.dtype                         # the working precision of every array below but ct_pt and core
+        R = self.dtype                         # the working precision of every array below but ct_pt
         Hpp = ws('Hpp', (max(n_ct, 1), 6), R)  # chunk-track order
         gp = ws('gp', (max(n_ct, 1), 3), R)
         ct_pt = ws('ct_pt', (max(n_ct, 1), 4), torch.float32)
         pfac = ws('pfac', (max(n_ct, 1), 12), R)
         work_ctr = ws('work_ctr', (1,), torch.int32)
-        # linearisation records: the Jacobian core, fp64 in both precisions
-        core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)
+        # linearisation records: the Jacobian core, 20 fp64 fields per slot; the fp32 solver's rounded to
+        # fp32, 24 fields (22 used)
+        if self.real32:
+            core = ws('core', (max(sc['n_chunks'], 1), 24, sc['chunk']), torch.float32)
+        else:
+            core = ws('core', (max(sc['n_chunks'], 1), 20, sc['chunk']), torch.float64)
         chunk_max = ws('chunk_max', (sc['n_chunks'] + 1,), R)
         lam_p = ws('lam_p', (1,), R)
         dd = max(d, 1)

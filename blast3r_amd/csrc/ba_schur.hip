@@ -37,6 +37,7 @@ typedef ba_lin_args LinArgs;
 static_assert(BA_LIST_CAP * 4 % 1024 == 0 && BA_MAX_SLOTS % 4 == 0, "list copies are whole 16-byte lanes");
 static_assert(BA_ZERO + 48 < 65536 && BA_LIST_CAP < 4096, "entry offsets fit their fields");
 #define BA_CORE 20          // doubles per observation in the linearisation record
+#define BA_CORE32 24        // floats per observation in the fp32 solver's record (22 used)
 static_assert(BA_CORE * BA_CHUNK % 256 == 0, "a chunk's record block is copied 256 doubles at a time");
 
 // Depth-guidance channels of one observation: the first BA_PRE_C in registers, the rest in memory.
@@ -151,6 +152,47 @@ __device__ __forceinline__ void core_load(const double* __restrict__ rec, int t,
     o.J.jkf = a.x;
     o.sW[0] = a.y; o.sW[1] = b.x; o.sW[2] = b.y;
 }
+
+// The fp32 solver's record (real32): the same fields rounded to fp32, one float each,
+//   0-2 X_rig | 3-11 Jpr | 12, 13 focal columns | 14 zscale | 15-17 W r / sqrt(W) | 18 J_k_f | 19-21 sqrt(W)
+// (22, 23 unused: a chunk's block stays a whole number of 2 KB copies), 96 bytes per slot against 160.
+__device__ __forceinline__ void core_store(float* __restrict__ rec, int t, const ObsCore& o) {
+    auto put = [&](int f, double v) { __builtin_nontemporal_store((float)v, rec + f * BA_CHUNK + t); };
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put(k, o.J.Xr[k]);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) put(3 + k, o.J.Jpr[k]);
+    put(12, o.J.fx_col);
+    put(13, o.J.fy_col);
+    put(14, o.J.zscale);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put(15 + k, o.Rs[k]);
+    put(18, o.J.jkf);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put(19 + k, o.sW[k]);
+}
+
+template <bool NT = false>
+__device__ __forceinline__ void core_load(const float* __restrict__ rec, int t, ObsCore& o) {
+    auto get = [&](int f) { return (double)(NT ? __builtin_nontemporal_load(rec + f * BA_CHUNK + t) : rec[f * BA_CHUNK + t]); };
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o.J.Xr[k] = get(k);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) o.J.Jpr[k] = get(3 + k);
+    o.J.fx_col = get(12);
+    o.J.fy_col = get(13);
+    o.J.zscale = get(14);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o.Rs[k] = get(15 + k);
+    o.J.jkf = get(18);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o.sW[k] = get(19 + k);
+}
+
+// the record type and its fields per slot, by working precision
+template <typename Real> struct CoreRec;
+template <> struct CoreRec<double> { typedef double T; static constexpr int NF = BA_CORE; };
+template <> struct CoreRec<float> { typedef float T; static constexpr int NF = BA_CORE32; };
 
 // Weighted camera row R, element by element, from the core (.cu:444-501, ba_solver.py:38-39, :59-60);
 // only the columns j in [JLO, JHI) are formed.
@@ -321,7 +363,8 @@ __global__ void __launch_bounds__(BA_CHUNK, 5) k_track_pp(LinArgs a) {   // 5 wa
         ObsCore o;
         float Xo[3] = {X[0], X[1], X[2]};
         obs_core(ctx.cp, ctx.zc, Xo, uv, sv, dep, a.hp, a.lay, a.r_in != nullptr, grw, o);
-        core_store(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
+        typedef CoreRec<Real> CR;
+        core_store(reinterpret_cast<typename CR::T*>(a.core) + (int64_t)chunk * CR::NF * BA_CHUNK, tid, o);
         const bool xon = (a.enX ? a.enX[pid] != 0 : true) && !a.lay.x_off;
         double Jp[3][3], gP[3];
         point_rows<true>(o, ctx.cp, xon, Jp, gP);
@@ -550,7 +593,8 @@ struct SchurMfma<float> {
 template <typename Real>
 struct Staging {
     static constexpr int PF = 16 / sizeof(Real);            // values per 16-byte copy
-    double rec[BA_CORE * BA_CHUNK];         // the chunk's linearisation records (field-major, as in memory)
+    typename CoreRec<Real>::T rec[CoreRec<Real>::NF * BA_CHUNK];   // the chunk's linearisation records (field-major,
+                                                                    // as in memory)
     int info[BA_CHUNK];                     // slot_info per slot
     int obs[BA_CHUNK];                      // chunk_obs per slot
     float dep[BA_PRE_C][BA_CHUNK];          // depth guidance channels c < min(C, BA_PRE_C)
@@ -568,11 +612,21 @@ __device__ __forceinline__ void stage_chunk(const LinArgs& a, Staging<Real>& S, 
     if (wave < 2) {
         const int w = __builtin_amdgcn_readfirstlane(wave);
         const int64_t slot = (int64_t)ck * BA_CHUNK + 64 * w + lane;
-        // the record block: BA_CORE * BA_CHUNK doubles, 16 bytes per lane per copy
-        const double* rec = a.core + (int64_t)ck * BA_CORE * BA_CHUNK;
+        // the record block, 16 bytes per lane per copy (2 KB per copy of the two waves)
+        if constexpr (sizeof(Real) == 8) {
+            const double* rec = a.core + (int64_t)ck * BA_CORE * BA_CHUNK;
 #pragma unroll
-        for (int i = 0; i < BA_CORE * BA_CHUNK / 256; ++i)
-            dma16_to_lds(rec + 256 * i + 128 * w + 2 * lane, S.rec + 256 * i + 128 * w);
+            for (int i = 0; i < BA_CORE * BA_CHUNK / 256; ++i)
+                dma16_to_lds(rec + 256 * i + 128 * w + 2 * lane, S.rec + 256 * i + 128 * w);
+        } else {
+            constexpr int RB = (int)sizeof(S.rec);
+            static_assert(RB % 2048 == 0, "a chunk's record block is a whole number of 2 KB copies");
+            const char* rec = reinterpret_cast<const char*>(a.core) + (int64_t)ck * RB;
+            char* dst = reinterpret_cast<char*>(S.rec);
+#pragma unroll
+            for (int i = 0; i < RB / 2048; ++i)
+                dma16_to_lds(rec + 2048 * i + 1024 * w + 16 * lane, dst + 2048 * i + 1024 * w);
+        }
         dma4_to_lds(a.slot_info + slot, S.info + 64 * w);
         dma4_to_lds(a.chunk_obs + slot, S.obs + 64 * w);
 #pragma unroll
@@ -696,7 +750,10 @@ __global__ void __launch_bounds__(BA_WAVES * 64) k_schur(LinArgs a) {
             if (valid && rr == 3) {                        // row 2's z-coefficient columns: zscale, sqrt(W_2)
                 ObsCore o;
                 o.J.zscale = sSt.rec[14 * BA_CHUNK + t];
-                o.sW[2] = reinterpret_cast<const float2*>(sSt.rec)[19 * BA_CHUNK + t].y;
+                if constexpr (sizeof(Real) == 8)
+                    o.sW[2] = reinterpret_cast<const float2*>(sSt.rec)[19 * BA_CHUNK + t].y;
+                else
+                    o.sW[2] = sSt.rec[21 * BA_CHUNK + t];
                 const bool eZ = sEn[3 * li + 2] != 0, first = sSt.obs[t] == 0;
                 Real* blk2 = sBlk + t * BA_BLK + BA_JROW + 32;
                 auto sink2 = [&](int j, double v) { if (j < 15) blk2[j] = j < d ? (Real)v : Real(0); };
@@ -981,7 +1038,8 @@ __global__ void __launch_bounds__(BA_CHUNK) k_backsub(LinArgs a) {
         ObsCtx ctx;
         load_obs_ctx(a, img, ctx);
         ObsCore o;
-        core_load<true>(a.core + (int64_t)chunk * BA_CORE * BA_CHUNK, tid, o);
+        typedef CoreRec<Real> CR;
+        core_load<true>(reinterpret_cast<const typename CR::T*>(a.core) + (int64_t)chunk * CR::NF * BA_CHUNK, tid, o);
         // t = J_c delta_c, with delta_c of this image gathered through the unknown map
         Real xs[16];
         if (a.dc_img != nullptr) {                     // image-level copy: one load fewer

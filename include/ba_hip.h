@@ -148,8 +148,9 @@ typedef struct {
     int64_t r_s0, r_s1, w_s0, w_s1;
     float* ct_pt;         /* (n_ctracks,4) scratch written by stage 0: x, y, z, enable */
     int64_t n_ctracks;
-    double* core;         /* (n_chunks,20,128) scratch: per-observation linearisation record (stage 0), fp64 in
-                             both precisions (the Jacobian core is evaluated in fp64) */
+    double* core;         /* scratch: per-observation linearisation record (stage 0), the Jacobian core evaluated
+                             in fp64: (n_chunks,20,128) doubles, or with real32 (n_chunks,24,128) floats (the
+                             same fields rounded to fp32; the pointer is then read as float*) */
     const int32_t *chunk_slots, *chunk_ent, *chunk_eptr;   /* plan: MFMA entry lists of every chunk */
     const int32_t *b_pos_slot;                             /* plan: batch slot at each Schur-kernel place */
     void* pfac;           /* (R) (n_ctracks,12) 16-byte aligned scratch written by stage 0: Cholesky factor L of H_pp +
